@@ -1,0 +1,242 @@
+/* migemm — MI355X (gfx950) matrix-multiply operators for onnx_runtime_dart.
+ *
+ * C ABI of libmigemm.so.  Every entry point takes plain pointers and sizes,
+ * returns an mg_status, and leaves a human-readable message for the calling
+ * thread in mg_last_error() when it fails.  The Dart graph interpreter binds
+ * these through dart:ffi and keeps its own op functions' signatures; the
+ * citation on each declaration names the reference routine it replaces
+ * (paths are relative to the onnx_runtime_dart checkout).
+ *
+ * Conventions
+ *   - Host-pointer ops (no _dev suffix) are synchronous: inputs are borrowed
+ *     for the call, outputs are written into caller-allocated host memory
+ *     before the call returns (the reference's ops return fresh tensors
+ *     synchronously, lib/src/onnx_qlinear_ops.dart:174).
+ *   - _dev ops take device pointers (from mg_buffer_alloc or any HIP
+ *     allocation on the context's device) and are asynchronous on the
+ *     context's stream; mg_ctx_synchronize waits for them.
+ *   - Weights are uploaded once into an mg_weight handle (repacked for the
+ *     kernels on upload, resident in HBM until mg_weight_release); the caller
+ *     may drop its host copy after create returns.  This is the device form of
+ *     the graph's lazily built prepacked Gemm weight
+ *     (lib/src/onnx_graph.dart:102-105, :2159-2161).
+ *   - One mg_ctx per isolate / thread.  Calls on one context are serialised
+ *     by the caller; contexts share nothing but the device.
+ *   - Integer outputs are int32 (ONNX's MatMulInteger type); the Dart shim
+ *     widens them to Tensor.int64 (lib/src/onnx_qlinear_ops.dart:77-80).
+ */
+#ifndef MIGEMM_H
+#define MIGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; the Dart shim maps them to the exceptions the reference
+ * throws (lib/src/onnx_qlinear_ops.dart:39-40,127,135,152,162,165;
+ * lib/src/execution_control.dart:43-57; lib/src/onnx_graph.dart:1274-1281). */
+typedef enum mg_status {
+  MG_OK = 0,
+  MG_INVALID_ARGUMENT = 1, /* ArgumentError */
+  MG_UNSUPPORTED = 2,      /* UnsupportedError */
+  MG_OUT_OF_MEMORY = 3,    /* OnnxMemoryLimitException (budget) or HBM OOM */
+  MG_CANCELLED = 4,        /* OnnxCancelledException */
+  MG_DEVICE_ERROR = 5      /* StateError: HIP runtime failure */
+} mg_status;
+
+typedef struct mg_ctx mg_ctx;
+typedef struct mg_weight mg_weight;
+
+/* Message of the last failing call on this thread ("" if none).  The pointer
+ * stays valid until the next migemm call on the same thread.  Plays the role
+ * of the ORT status message (lib/src/ort/ort_backend.dart:774-782). */
+const char *mg_last_error(void);
+
+/* Library version as "major.minor.patch". */
+const char *mg_version(void);
+
+/* ----------------------------------------------------------------- context */
+
+/* Creates a context on HIP device `device` with its own stream.
+ * Replaces the process-wide kernel state of lib/src/gemm_kernel_simd.dart:26-28
+ * (isolate-local scratch) with a per-caller device context. */
+mg_status mg_ctx_create(int32_t device, mg_ctx **out);
+mg_status mg_ctx_destroy(mg_ctx *ctx);
+
+/* Uses `hip_stream` (a hipStream_t, may be NULL for the null stream) for all
+ * later work of the context instead of its own stream.  The caller keeps
+ * ownership of the stream. */
+mg_status mg_ctx_set_stream(mg_ctx *ctx, void *hip_stream);
+/* The hipStream_t the context launches on. */
+mg_status mg_ctx_get_stream(mg_ctx *ctx, void **hip_stream);
+mg_status mg_ctx_synchronize(mg_ctx *ctx);
+
+/* Cooperative cancellation and byte budget, checked before every launch
+ * (lib/src/execution_control.dart:43-57: checkpoint / checkAdditionalBytes).
+ * `cancel_flag` (may be NULL) is polled: non-zero => MG_CANCELLED.
+ * `max_bytes` < 0 disables the budget; otherwise an op whose device
+ * workspace plus staging would exceed it fails with MG_OUT_OF_MEMORY. */
+mg_status mg_ctx_set_control(mg_ctx *ctx, const volatile int32_t *cancel_flag,
+                             int64_t max_bytes);
+
+/* ----------------------------------------------------------- device memory */
+
+mg_status mg_buffer_alloc(mg_ctx *ctx, size_t bytes, void **dev_ptr);
+mg_status mg_buffer_free(mg_ctx *ctx, void *dev_ptr);
+mg_status mg_buffer_upload(mg_ctx *ctx, void *dev_dst, const void *host_src,
+                           size_t bytes);
+mg_status mg_buffer_download(mg_ctx *ctx, void *host_dst, const void *dev_src,
+                             size_t bytes);
+
+/* ------------------------------------------------------------- MatMulNBits */
+
+/* Zero-point forms of MatMulNBits (lib/src/onnx_qlinear_ops.dart:178-188). */
+typedef enum mg_zp_kind {
+  MG_ZP_NONE = 0,   /* default zero point 8 */
+  MG_ZP_UINT4 = 1,  /* packed uint8, [N * ceil(nb/2)] or [N, ceil(nb/2)] */
+  MG_ZP_FLOAT = 2   /* float32, [N * nb] or [N, nb] */
+} mg_zp_kind;
+
+/* Uploads an int4 block-quantized weight: validation of
+ * opMatMulNBits (lib/src/onnx_qlinear_ops.dart:126-166) plus the dispatch's
+ * g_idx rejection (lib/src/onnx_graph.dart:2919-2921, pass has_g_idx).
+ *   b      uint8 [N, nb, block_size/2], low nibble = even k  (b_shape, rank 3)
+ *   scales float32 [N*nb] or [N, nb]                          (scales_shape)
+ *   zp     per zp_kind, NULL for MG_ZP_NONE                   (zp_shape)
+ *   bias   float32 [N] or NULL                                (bias_shape)
+ * nb = ceil(K / block_size). */
+mg_status mg_weight_nbits_create(
+    mg_ctx *ctx, int64_t K, int64_t N, int64_t bits, int64_t block_size,
+    const uint8_t *b, const int64_t *b_shape, int32_t b_rank,
+    const float *scales, const int64_t *scales_shape, int32_t scales_rank,
+    int32_t zp_kind, const void *zp, const int64_t *zp_shape, int32_t zp_rank,
+    const float *bias, const int64_t *bias_shape, int32_t bias_rank,
+    int32_t has_g_idx, mg_weight **out);
+
+/* y[M, N] = a[M, K] . dequant(B)^T (+ bias): opMatMulNBits
+ * (lib/src/onnx_qlinear_ops.dart:115-228).  `a` holds M rows of K floats
+ * (the caller flattens leading dims, a.shape.last == K); y holds M*N floats.
+ * M == 0 is a no-op, as in the reference (:169-171). */
+mg_status mg_matmul_nbits(mg_ctx *ctx, const mg_weight *w, const float *a,
+                          int64_t M, float *y);
+mg_status mg_matmul_nbits_dev(mg_ctx *ctx, const mg_weight *w,
+                              const float *a_dev, int64_t M, float *y_dev);
+
+/* ------------------------------------------- MatMulInteger / QLinearMatMul */
+
+/* Uploads an 8-bit B [K, N] (`b_signed`: int8 else uint8) with its zero
+ * point (scalar when b_zp_len == 1, per-column [N], or none when NULL);
+ * column sums are computed once here.  Mirrors the operand checks of
+ * opMatMulInteger (lib/src/onnx_qlinear_ops.dart:36-45). */
+mg_status mg_weight_int8_create(mg_ctx *ctx, const void *b, int32_t b_signed,
+                                int64_t K, int64_t N, const int32_t *b_zp,
+                                int64_t b_zp_len, mg_weight **out);
+
+/* y_int32[batch, M, N] = (A - aZp) . (B - bZp): opMatMulInteger
+ * (lib/src/onnx_qlinear_ops.dart:32-81).  A and B are given with their full
+ * shapes (rank >= 2); batches must be equal or 1 (:46-54).  Zero points are
+ * int32 arrays: scalar (len 1), per-row A [M], per-column B [N], or NULL. */
+mg_status mg_matmul_integer(mg_ctx *ctx, const void *a, int32_t a_signed,
+                            const int64_t *a_shape, int32_t a_rank,
+                            const void *b, int32_t b_signed,
+                            const int64_t *b_shape, int32_t b_rank,
+                            const int32_t *a_zp, int64_t a_zp_len,
+                            const int32_t *b_zp, int64_t b_zp_len, int32_t *y);
+/* Same with an uploaded B; a is [rows = batch*M, K]. */
+mg_status mg_matmul_integer_w(mg_ctx *ctx, const void *a, int32_t a_signed,
+                              int64_t rows, int64_t K, const int32_t *a_zp,
+                              int64_t a_zp_len, const mg_weight *w, int32_t *y);
+mg_status mg_matmul_integer_w_dev(mg_ctx *ctx, const void *a_dev,
+                                  int32_t a_signed, int64_t rows, int64_t K,
+                                  const int32_t *a_zp, int64_t a_zp_len,
+                                  const mg_weight *w, int32_t *y_dev);
+
+/* QLinearMatMul (lib/src/onnx_qlinear_ops.dart:85-108): MatMulInteger, then
+ * q = roundHalfEven(fl32(acc * fl32(fl32(aS*bS)/yS))) + yZp clamped to
+ * [lo, hi].  lo/hi are -128/127 when the y zero point is int8, else 0/255
+ * (lib/src/onnx_graph.dart:2903,2914-2915); y holds uint8 when lo >= 0 and
+ * int8 otherwise.  Scales are per-tensor (:88-90). */
+mg_status mg_qlinear_matmul(mg_ctx *ctx, const void *a, int32_t a_signed,
+                            const int64_t *a_shape, int32_t a_rank,
+                            float a_scale, const int32_t *a_zp,
+                            int64_t a_zp_len, const void *b, int32_t b_signed,
+                            const int64_t *b_shape, int32_t b_rank,
+                            float b_scale, const int32_t *b_zp,
+                            int64_t b_zp_len, float y_scale, int32_t y_zp,
+                            int32_t lo, int32_t hi, void *y);
+mg_status mg_qlinear_matmul_w(mg_ctx *ctx, const void *a, int32_t a_signed,
+                              int64_t rows, int64_t K, float a_scale,
+                              const int32_t *a_zp, int64_t a_zp_len,
+                              const mg_weight *w, float b_scale, float y_scale,
+                              int32_t y_zp, int32_t lo, int32_t hi, void *y);
+mg_status mg_qlinear_matmul_w_dev(mg_ctx *ctx, const void *a_dev,
+                                  int32_t a_signed, int64_t rows, int64_t K,
+                                  float a_scale, const int32_t *a_zp,
+                                  int64_t a_zp_len, const mg_weight *w,
+                                  float b_scale, float y_scale, int32_t y_zp,
+                                  int32_t lo, int32_t hi, void *y_dev);
+
+/* DynamicQuantizeLinear (lib/src/onnx_ops.dart:3556-3583): y uint8[n],
+ * scale and zero point as the reference computes them (f64 arithmetic,
+ * rounded to f32; round-half-even).  Non-finite input => MG_UNSUPPORTED
+ * (the reference's toInt on NaN throws UnsupportedError). */
+mg_status mg_dynamic_quantize_linear(mg_ctx *ctx, const float *x, int64_t n,
+                                     uint8_t *y, float *scale, int32_t *zp);
+/* Device form: scale/zp are written to device memory (scale_zp_dev holds one
+ * float then one int32), so a following integer matmul can stay on device. */
+mg_status mg_dynamic_quantize_linear_dev(mg_ctx *ctx, const float *x_dev,
+                                         int64_t n, uint8_t *y_dev,
+                                         void *scale_zp_dev);
+
+/* ---------------------------------------------------------- fp32 MatMul/Gemm */
+
+/* numpy-broadcast batched MatMul (lib/src/onnx_ops.dart:1710-1766);
+ * y has the broadcast shape [..., M, N]. */
+mg_status mg_matmul_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape,
+                        int32_t a_rank, const float *b, const int64_t *b_shape,
+                        int32_t b_rank, float *y);
+mg_status mg_matmul_f32_dev(mg_ctx *ctx, const float *a_dev,
+                            const int64_t *a_shape, int32_t a_rank,
+                            const float *b_dev, const int64_t *b_shape,
+                            int32_t b_rank, float *y_dev);
+
+/* Gemm: y = alpha * op(A) . op(B) + beta * C (lib/src/onnx_ops.dart:2152-2172).
+ * a, b rank 2; c NULL or rank <= 2 broadcasting to [M, N]. */
+mg_status mg_gemm_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape,
+                      const float *b, const int64_t *b_shape, int32_t trans_a,
+                      int32_t trans_b, float alpha, float beta, const float *c,
+                      const int64_t *c_shape, int32_t c_rank, float *y);
+
+/* Uploads an fp32 B given as stored ([rows, cols]); with trans_b the operand
+ * is B^T, i.e. K = cols, N = rows (the transB prepack of
+ * lib/src/onnx_graph.dart:2159-2161 done once on upload). */
+mg_status mg_weight_f32_create(mg_ctx *ctx, const float *b, int64_t rows,
+                               int64_t cols, int32_t trans_b, mg_weight **out);
+/* y[rows, N] = alpha * a[rows, K] . W + beta * C, C as in mg_gemm_f32 (may be
+ * NULL).  With alpha = 1, beta = 0, C = NULL this is MatMul against an
+ * initializer, including the shared-weight batch collapse
+ * (lib/src/onnx_ops.dart:1728-1735). */
+mg_status mg_gemm_f32_w(mg_ctx *ctx, const float *a, int64_t rows, int64_t K,
+                        const mg_weight *w, float alpha, float beta,
+                        const float *c, const int64_t *c_shape, int32_t c_rank,
+                        float *y);
+mg_status mg_gemm_f32_w_dev(mg_ctx *ctx, const float *a_dev, int64_t rows,
+                            int64_t K, const mg_weight *w, float alpha,
+                            float beta, const float *c_dev,
+                            const int64_t *c_shape, int32_t c_rank,
+                            float *y_dev);
+
+/* ----------------------------------------------------------------- weights */
+
+mg_status mg_weight_release(mg_weight *w);
+/* K, N of an uploaded weight, and its resident device bytes. */
+mg_status mg_weight_info(const mg_weight *w, int64_t *K, int64_t *N,
+                         int64_t *device_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MIGEMM_H */

@@ -1,0 +1,884 @@
+// C-ABI of libmigemm.so: contexts, device buffers, weight upload, operator
+// validation (mirroring the reference's checks and their error classes) and
+// dispatch to the HIP kernels.  Declarations and reference citations are in
+// include/migemm.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "mg_internal.h"
+
+// Defined in int8.hip.
+mg_status mg_int8_run_batched(mg_ctx *ctx, const void *a_dev, int32_t a_signed,
+                              int64_t a_batch, const void *b_dev,
+                              int32_t b_signed, int64_t b_batch, int64_t M,
+                              int64_t K, int64_t N, const int32_t *a_zp,
+                              int64_t a_zp_len, const int32_t *b_zp,
+                              int64_t b_zp_len, const mg_requant *rq,
+                              void *y_dev, void *ws);
+size_t mg_int8_batched_ws_bytes(int64_t a_batch, int64_t b_batch, int64_t M,
+                                int64_t K, int64_t N);
+
+namespace {
+thread_local std::string g_last_error;
+
+int64_t prod(const int64_t *s, int32_t from, int32_t to) {
+  int64_t p = 1;
+  for (int32_t i = from; i < to; i++) p *= s[i];
+  return p;
+}
+
+bool shape_ok(const int64_t *s, int32_t r) {
+  if (r < 0 || r > 16 || (r > 0 && !s)) return false;
+  for (int32_t i = 0; i < r; i++)
+    if (s[i] < 0) return false;
+  return true;
+}
+
+// Stages host buffers through the context workspace around a device call.
+struct Staging {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t o = off;
+    off += mg_align(bytes ? bytes : 1);
+    return o;
+  }
+};
+}  // namespace
+
+mg_status mg_fail(mg_status st, const std::string &msg) {
+  g_last_error = msg;
+  return st;
+}
+
+mg_status mg_launch_check(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return mg_fail(MG_DEVICE_ERROR, std::string(what) + " launch: " + hipGetErrorString(e));
+  return MG_OK;
+}
+
+mg_status mg_use_device(mg_ctx *ctx) {
+  MG_HIP(hipSetDevice(ctx->device));
+  return MG_OK;
+}
+
+mg_status mg_check_control(mg_ctx *ctx, int64_t additional_bytes) {
+  if (ctx->cancel_flag && *ctx->cancel_flag)
+    return mg_fail(MG_CANCELLED, "operation cancelled");
+  if (ctx->max_bytes >= 0 && additional_bytes > ctx->max_bytes)
+    return mg_fail(MG_OUT_OF_MEMORY,
+                   "device memory limit exceeded: " + std::to_string(additional_bytes) +
+                       " bytes required, limit " + std::to_string(ctx->max_bytes));
+  return MG_OK;
+}
+
+mg_status mg_ws_reserve(mg_ctx *ctx, size_t bytes) {
+  if (bytes <= ctx->ws_bytes) return MG_OK;
+  if (ctx->ws) {
+    MG_HIP(hipStreamSynchronize(ctx->stream));
+    MG_HIP(hipFree(ctx->ws));
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+  }
+  const size_t want = mg_align(bytes, 1 << 20);
+  MG_HIP(hipMalloc(&ctx->ws, want));
+  ctx->ws_bytes = want;
+  return MG_OK;
+}
+
+extern "C" {
+
+const char *mg_last_error(void) { return g_last_error.c_str(); }
+const char *mg_version(void) { return "0.1.0"; }
+
+// ------------------------------------------------------------------ context
+
+mg_status mg_ctx_create(int32_t device, mg_ctx **out) {
+  g_last_error.clear();
+  if (!out) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_create: out is null");
+  *out = nullptr;
+  int n = 0;
+  MG_HIP(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_create: no HIP device " + std::to_string(device));
+  MG_HIP(hipSetDevice(device));
+  mg_ctx *c = new mg_ctx();
+  c->device = device;
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return mg_fail(MG_DEVICE_ERROR, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+  }
+  c->own_stream = true;
+  *out = c;
+  return MG_OK;
+}
+
+mg_status mg_ctx_destroy(mg_ctx *ctx) {
+  if (!ctx) return MG_OK;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return MG_OK;
+}
+
+mg_status mg_ctx_set_stream(mg_ctx *ctx, void *hip_stream) {
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_set_stream: null context");
+  MG_TRY(mg_use_device(ctx));
+  if (ctx->stream) MG_HIP(hipStreamSynchronize(ctx->stream));
+  if (ctx->own_stream && ctx->stream) MG_HIP(hipStreamDestroy(ctx->stream));
+  ctx->stream = static_cast<hipStream_t>(hip_stream);
+  ctx->own_stream = false;
+  return MG_OK;
+}
+
+mg_status mg_ctx_get_stream(mg_ctx *ctx, void **hip_stream) {
+  if (!ctx || !hip_stream) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_get_stream: null argument");
+  *hip_stream = ctx->stream;
+  return MG_OK;
+}
+
+mg_status mg_ctx_synchronize(mg_ctx *ctx) {
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_synchronize: null context");
+  MG_TRY(mg_use_device(ctx));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  return MG_OK;
+}
+
+mg_status mg_ctx_set_control(mg_ctx *ctx, const volatile int32_t *cancel_flag,
+                             int64_t max_bytes) {
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_set_control: null context");
+  ctx->cancel_flag = cancel_flag;
+  ctx->max_bytes = max_bytes;
+  return MG_OK;
+}
+
+// ---------------------------------------------------------------- buffers
+
+mg_status mg_buffer_alloc(mg_ctx *ctx, size_t bytes, void **dev_ptr) {
+  if (!ctx || !dev_ptr) return mg_fail(MG_INVALID_ARGUMENT, "mg_buffer_alloc: null argument");
+  *dev_ptr = nullptr;
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, (int64_t)bytes));
+  MG_HIP(hipMalloc(dev_ptr, bytes ? bytes : 1));
+  return MG_OK;
+}
+
+mg_status mg_buffer_free(mg_ctx *ctx, void *dev_ptr) {
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_buffer_free: null context");
+  if (!dev_ptr) return MG_OK;
+  MG_TRY(mg_use_device(ctx));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  MG_HIP(hipFree(dev_ptr));
+  return MG_OK;
+}
+
+mg_status mg_buffer_upload(mg_ctx *ctx, void *dev_dst, const void *host_src, size_t bytes) {
+  if (!ctx || (bytes && (!dev_dst || !host_src)))
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_buffer_upload: null argument");
+  MG_TRY(mg_use_device(ctx));
+  MG_HIP(hipMemcpyAsync(dev_dst, host_src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  return MG_OK;
+}
+
+mg_status mg_buffer_download(mg_ctx *ctx, void *host_dst, const void *dev_src, size_t bytes) {
+  if (!ctx || (bytes && (!host_dst || !dev_src)))
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_buffer_download: null argument");
+  MG_TRY(mg_use_device(ctx));
+  MG_HIP(hipMemcpyAsync(host_dst, dev_src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  return MG_OK;
+}
+
+// ---------------------------------------------------------------- weights
+
+mg_status mg_weight_release(mg_weight *w) {
+  if (!w) return MG_OK;
+  (void)hipSetDevice(w->device);
+  (void)hipDeviceSynchronize();
+  if (w->kind == MG_W_NBITS) mg_nbits_free(w);
+  if (w->kind == MG_W_INT8) mg_int8_free(w);
+  if (w->kind == MG_W_F32 && w->f32.b) (void)hipFree(w->f32.b);
+  delete w;
+  return MG_OK;
+}
+
+mg_status mg_weight_info(const mg_weight *w, int64_t *K, int64_t *N, int64_t *device_bytes) {
+  if (!w) return mg_fail(MG_INVALID_ARGUMENT, "mg_weight_info: null weight");
+  if (K) *K = w->K;
+  if (N) *N = w->N;
+  if (device_bytes) *device_bytes = w->device_bytes;
+  return MG_OK;
+}
+
+mg_status mg_weight_nbits_create(
+    mg_ctx *ctx, int64_t K, int64_t N, int64_t bits, int64_t block_size,
+    const uint8_t *b, const int64_t *b_shape, int32_t b_rank,
+    const float *scales, const int64_t *scales_shape, int32_t scales_rank,
+    int32_t zp_kind, const void *zp, const int64_t *zp_shape, int32_t zp_rank,
+    const float *bias, const int64_t *bias_shape, int32_t bias_rank,
+    int32_t has_g_idx, mg_weight **out) {
+  g_last_error.clear();
+  if (!ctx || !out) return mg_fail(MG_INVALID_ARGUMENT, "mg_weight_nbits_create: null argument");
+  *out = nullptr;
+  // lib/src/onnx_graph.dart:2919-2921
+  if (has_g_idx) return mg_fail(MG_UNSUPPORTED, "MatMulNBits: g_idx input not supported");
+  // lib/src/onnx_qlinear_ops.dart:126-128
+  if (bits != 4)
+    return mg_fail(MG_UNSUPPORTED,
+                   "MatMulNBits: only bits=4 supported, got " + std::to_string(bits));
+  // :129-136 (the activation-shape half of this check is made per call)
+  if (K <= 0 || N <= 0 || block_size < 16 || (block_size & (block_size - 1)) != 0)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid K, N, block_size or input shape");
+  const int64_t nb = (K + block_size - 1) / block_size;
+  const int64_t blob = block_size / 2;
+  const int64_t zp_stride = (nb + 1) / 2;
+  // :140-152
+  if (!b || !scales || !shape_ok(b_shape, b_rank) || !shape_ok(scales_shape, scales_rank) ||
+      b_rank != 3 || b_shape[0] != N || b_shape[1] != nb || b_shape[2] != blob ||
+      prod(scales_shape, 0, scales_rank) != N * nb || (scales_rank != 1 && scales_rank != 2) ||
+      (scales_rank == 2 && (scales_shape[0] != N || scales_shape[1] != nb)))
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid packed weights or scales");
+  // :155-163
+  if (zp_kind != MG_ZP_NONE) {
+    if (!zp || !shape_ok(zp_shape, zp_rank) || (zp_kind != MG_ZP_UINT4 && zp_kind != MG_ZP_FLOAT) ||
+        (zp_rank != 1 && zp_rank != 2) || (zp_rank == 2 && zp_shape[0] != N) ||
+        (zp_kind == MG_ZP_UINT4 ? prod(zp_shape, 0, zp_rank) != N * zp_stride
+                                : prod(zp_shape, 0, zp_rank) != N * nb))
+      return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid zero_points");
+  }
+  // :164-166
+  if (bias && (!shape_ok(bias_shape, bias_rank) || bias_rank != 1 || bias_shape[0] != N))
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: bias must be floating point [N]");
+  MG_TRY(mg_use_device(ctx));
+  mg_weight *w = new mg_weight();
+  w->kind = MG_W_NBITS;
+  w->device = ctx->device;
+  w->K = K;
+  w->N = N;
+  w->nbits.bs = block_size;
+  mg_status st = mg_nbits_upload(ctx, w, b, scales, zp_kind, zp, bias);
+  if (st != MG_OK) {
+    mg_nbits_free(w);
+    delete w;
+    return st;
+  }
+  *out = w;
+  return MG_OK;
+}
+
+mg_status mg_weight_int8_create(mg_ctx *ctx, const void *b, int32_t b_signed, int64_t K,
+                                int64_t N, const int32_t *b_zp, int64_t b_zp_len,
+                                mg_weight **out) {
+  g_last_error.clear();
+  if (!ctx || !out || (!b && K * N > 0))
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_weight_int8_create: null argument");
+  *out = nullptr;
+  if (K < 0 || N < 0) return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger: invalid B shape");
+  if (b_zp && b_zp_len != 1 && b_zp_len != N)
+    return mg_fail(MG_UNSUPPORTED,
+                   "MatMulInteger: zero points must be scalar, per-row [M] for A or "
+                   "per-column [N] for B");
+  MG_TRY(mg_use_device(ctx));
+  mg_weight *w = new mg_weight();
+  w->kind = MG_W_INT8;
+  w->device = ctx->device;
+  w->K = K;
+  w->N = N;
+  mg_status st = mg_int8_upload(ctx, w, b, b_signed, b_zp, b_zp ? b_zp_len : 0);
+  if (st != MG_OK) {
+    delete w;
+    return st;
+  }
+  *out = w;
+  return MG_OK;
+}
+
+mg_status mg_weight_f32_create(mg_ctx *ctx, const float *b, int64_t rows, int64_t cols,
+                               int32_t trans_b, mg_weight **out) {
+  g_last_error.clear();
+  if (!ctx || !out || (!b && rows * cols > 0))
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_weight_f32_create: null argument");
+  *out = nullptr;
+  if (rows < 0 || cols < 0) return mg_fail(MG_INVALID_ARGUMENT, "Gemm: invalid B shape");
+  MG_TRY(mg_use_device(ctx));
+  const int64_t K = trans_b ? cols : rows, N = trans_b ? rows : cols;
+  std::vector<float> t;
+  const float *src = b;
+  if (trans_b) {
+    t.resize((size_t)(K * N));
+    for (int64_t n = 0; n < N; n++)
+      for (int64_t k = 0; k < K; k++) t[(size_t)(k * N + n)] = b[n * K + k];
+    src = t.data();
+  }
+  mg_weight *w = new mg_weight();
+  w->kind = MG_W_F32;
+  w->device = ctx->device;
+  w->K = K;
+  w->N = N;
+  const size_t bytes = (size_t)(K * N) * 4;
+  hipError_t e = hipMalloc((void **)&w->f32.b, bytes ? bytes : 4);
+  if (e != hipSuccess) {
+    delete w;
+    return mg_fail(MG_OUT_OF_MEMORY, "mg_weight_f32_create: allocation failed");
+  }
+  w->device_bytes = (int64_t)bytes;
+  if (bytes && hipMemcpy(w->f32.b, src, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(w->f32.b);
+    delete w;
+    return mg_fail(MG_DEVICE_ERROR, "mg_weight_f32_create: upload failed");
+  }
+  *out = w;
+  return MG_OK;
+}
+
+// ------------------------------------------------------------ MatMulNBits
+
+mg_status mg_matmul_nbits_dev(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
+                              float *y_dev) {
+  g_last_error.clear();
+  if (!ctx || !w || w->kind != MG_W_NBITS)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits: not a MatMulNBits weight");
+  if (M < 0) return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid K, N, block_size or input shape");
+  if (M == 0) return MG_OK;
+  if (!a_dev || !y_dev) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  const size_t ws = mg_nbits_ws_bytes(w, M);
+  MG_TRY(mg_check_control(ctx, (int64_t)ws));
+  MG_TRY(mg_ws_reserve(ctx, ws));
+  return mg_nbits_run(ctx, w, a_dev, M, y_dev, ctx->ws);
+}
+
+mg_status mg_matmul_nbits(mg_ctx *ctx, const mg_weight *w, const float *a, int64_t M, float *y) {
+  g_last_error.clear();
+  if (!ctx || !w || w->kind != MG_W_NBITS)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits: not a MatMulNBits weight");
+  if (M < 0) return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid K, N, block_size or input shape");
+  if (M == 0) return MG_OK;
+  if (!a || !y) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t oa = s.take((size_t)(M * w->K) * 4);
+  const size_t oy = s.take((size_t)(M * w->N) * 4);
+  const size_t ow = s.take(mg_nbits_ws_bytes(w, M));
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  MG_HIP(hipMemcpyAsync(base + oa, a, (size_t)(M * w->K) * 4, hipMemcpyHostToDevice, ctx->stream));
+  MG_TRY(mg_nbits_run(ctx, w, reinterpret_cast<float *>(base + oa), M,
+                      reinterpret_cast<float *>(base + oy), base + ow));
+  MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)(M * w->N) * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  return MG_OK;
+}
+
+// ------------------------------------------------ MatMulInteger / QLinear
+
+namespace {
+
+struct IntProblem {
+  int64_t M = 0, K = 0, N = 0, a_batch = 1, b_batch = 1, batch = 1;
+};
+
+mg_status check_integer(const int64_t *a_shape, int32_t a_rank, const int64_t *b_shape,
+                        int32_t b_rank, int64_t a_zp_len, bool has_azp, int64_t b_zp_len,
+                        bool has_bzp, IntProblem *p) {
+  if (!shape_ok(a_shape, a_rank) || !shape_ok(b_shape, b_rank) || a_rank < 2 || b_rank < 2)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger: operands must have rank >= 2");
+  p->M = a_shape[a_rank - 2];
+  p->K = a_shape[a_rank - 1];
+  p->N = b_shape[b_rank - 1];
+  if (b_shape[b_rank - 2] != p->K)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger inner dim mismatch");
+  // lib/src/onnx_qlinear_ops.dart:37-45
+  if ((has_azp && a_zp_len != 1 && a_zp_len != p->M) ||
+      (has_bzp && b_zp_len != 1 && b_zp_len != p->N))
+    return mg_fail(MG_UNSUPPORTED,
+                   "MatMulInteger: zero points must be scalar, per-row [M] for A or "
+                   "per-column [N] for B");
+  p->a_batch = prod(a_shape, 0, a_rank - 2);
+  p->b_batch = prod(b_shape, 0, b_rank - 2);
+  p->batch = std::max(p->a_batch, p->b_batch);
+  // :46-54
+  if ((p->a_batch != p->batch && p->a_batch != 1) || (p->b_batch != p->batch && p->b_batch != 1))
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger batch mismatch");
+  if (p->K > 33025)
+    return mg_fail(MG_UNSUPPORTED,
+                   "MatMulInteger: K > 33025 may exceed the int32 accumulator");
+  return MG_OK;
+}
+
+mg_status integer_host(mg_ctx *ctx, const void *a, int32_t a_signed, const int64_t *a_shape,
+                       int32_t a_rank, const int32_t *a_zp, int64_t a_zp_len, const void *b,
+                       int32_t b_signed, const int64_t *b_shape, int32_t b_rank,
+                       const int32_t *b_zp, int64_t b_zp_len, const mg_requant *rq, void *y) {
+  IntProblem p;
+  MG_TRY(check_integer(a_shape, a_rank, b_shape, b_rank, a_zp_len, a_zp != nullptr, b_zp_len,
+                       b_zp != nullptr, &p));
+  const int64_t ysz = p.batch * p.M * p.N * (rq ? 1 : 4);
+  if (p.batch * p.M * p.N == 0) return MG_OK;
+  if ((!a && p.a_batch * p.M * p.K) || (!b && p.b_batch * p.K * p.N) || !y)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t abytes = (size_t)(p.a_batch * p.M * p.K), bbytes = (size_t)(p.b_batch * p.K * p.N);
+  const size_t oa = s.take(abytes), ob = s.take(bbytes), oy = s.take((size_t)ysz);
+  const size_t ow = s.take(mg_int8_batched_ws_bytes(p.a_batch, p.b_batch, p.M, p.K, p.N));
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  if (abytes) MG_HIP(hipMemcpyAsync(base + oa, a, abytes, hipMemcpyHostToDevice, ctx->stream));
+  if (bbytes) MG_HIP(hipMemcpyAsync(base + ob, b, bbytes, hipMemcpyHostToDevice, ctx->stream));
+  MG_TRY(mg_int8_run_batched(ctx, base + oa, a_signed, p.a_batch, base + ob, b_signed, p.b_batch,
+                             p.M, p.K, p.N, a_zp, a_zp ? a_zp_len : 0, b_zp,
+                             b_zp ? b_zp_len : 0, rq, base + oy, base + ow));
+  MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)ysz, hipMemcpyDeviceToHost, ctx->stream));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  return MG_OK;
+}
+
+mg_status requant_params(float a_scale, float b_scale, float y_scale, int32_t y_zp, int32_t lo,
+                         int32_t hi, mg_requant *rq) {
+  if (!(lo == 0 && hi == 255) && !(lo == -128 && hi == 127))
+    return mg_fail(MG_INVALID_ARGUMENT, "QLinearMatMul: [lo, hi] must be [0, 255] or [-128, 127]");
+  // lib/src/onnx_qlinear_ops.dart:95-98: each step rounded to f32.
+  const float ab = (float)((double)a_scale * (double)b_scale);
+  rq->mult = (float)((double)ab / (double)y_scale);
+  rq->y_zp = y_zp;
+  rq->lo = lo;
+  rq->hi = hi;
+  return MG_OK;
+}
+
+mg_status check_weight_rows(const mg_weight *w, int64_t rows, int64_t K, const int32_t *a_zp,
+                            int64_t a_zp_len) {
+  if (!w || w->kind != MG_W_INT8)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger: not an 8-bit weight");
+  if (rows < 0 || K != w->K) return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger inner dim mismatch");
+  if (a_zp && (a_zp_len < 1 || (a_zp_len > 1 && rows % a_zp_len != 0)))
+    return mg_fail(MG_UNSUPPORTED,
+                   "MatMulInteger: zero points must be scalar, per-row [M] for A or "
+                   "per-column [N] for B");
+  if (K > 33025)
+    return mg_fail(MG_UNSUPPORTED, "MatMulInteger: K > 33025 may exceed the int32 accumulator");
+  return MG_OK;
+}
+
+mg_status integer_w(mg_ctx *ctx, const void *a, bool a_on_device, int32_t a_signed, int64_t rows,
+                    int64_t K, const int32_t *a_zp, int64_t a_zp_len, const mg_weight *w,
+                    const mg_requant *rq, void *y, bool y_on_device) {
+  MG_TRY(check_weight_rows(w, rows, K, a_zp, a_zp_len));
+  if (rows == 0 || w->N == 0) return MG_OK;
+  if (!a || !y) return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  const size_t ysz = (size_t)(rows * w->N) * (rq ? 1 : 4);
+  Staging s;
+  const size_t oa = a_on_device ? 0 : s.take((size_t)(rows * K));
+  const size_t oy = y_on_device ? 0 : s.take(ysz);
+  const size_t ow = s.take(mg_int8_ws_bytes(w, rows) + mg_align((size_t)rows * 4 + 4));
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  const void *ad = a;
+  void *yd = y;
+  if (!a_on_device) {
+    MG_HIP(hipMemcpyAsync(base + oa, a, (size_t)(rows * K), hipMemcpyHostToDevice, ctx->stream));
+    ad = base + oa;
+  }
+  if (!y_on_device) yd = base + oy;
+  MG_TRY(mg_int8_run(ctx, w, ad, a_signed, rows, a_zp, a_zp ? a_zp_len : 0, rq, yd, base + ow));
+  if (!y_on_device) {
+    MG_HIP(hipMemcpyAsync(y, yd, ysz, hipMemcpyDeviceToHost, ctx->stream));
+    MG_HIP(hipStreamSynchronize(ctx->stream));
+  }
+  return MG_OK;
+}
+
+}  // namespace
+
+mg_status mg_matmul_integer(mg_ctx *ctx, const void *a, int32_t a_signed, const int64_t *a_shape,
+                            int32_t a_rank, const void *b, int32_t b_signed,
+                            const int64_t *b_shape, int32_t b_rank, const int32_t *a_zp,
+                            int64_t a_zp_len, const int32_t *b_zp, int64_t b_zp_len,
+                            int32_t *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer: null context");
+  return integer_host(ctx, a, a_signed, a_shape, a_rank, a_zp, a_zp_len, b, b_signed, b_shape,
+                      b_rank, b_zp, b_zp_len, nullptr, y);
+}
+
+mg_status mg_matmul_integer_w(mg_ctx *ctx, const void *a, int32_t a_signed, int64_t rows,
+                              int64_t K, const int32_t *a_zp, int64_t a_zp_len,
+                              const mg_weight *w, int32_t *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer_w: null context");
+  return integer_w(ctx, a, false, a_signed, rows, K, a_zp, a_zp_len, w, nullptr, y, false);
+}
+
+mg_status mg_matmul_integer_w_dev(mg_ctx *ctx, const void *a_dev, int32_t a_signed, int64_t rows,
+                                  int64_t K, const int32_t *a_zp, int64_t a_zp_len,
+                                  const mg_weight *w, int32_t *y_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer_w_dev: null context");
+  return integer_w(ctx, a_dev, true, a_signed, rows, K, a_zp, a_zp_len, w, nullptr, y_dev, true);
+}
+
+mg_status mg_qlinear_matmul(mg_ctx *ctx, const void *a, int32_t a_signed, const int64_t *a_shape,
+                            int32_t a_rank, float a_scale, const int32_t *a_zp, int64_t a_zp_len,
+                            const void *b, int32_t b_signed, const int64_t *b_shape,
+                            int32_t b_rank, float b_scale, const int32_t *b_zp,
+                            int64_t b_zp_len, float y_scale, int32_t y_zp, int32_t lo,
+                            int32_t hi, void *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_matmul: null context");
+  mg_requant rq;
+  MG_TRY(requant_params(a_scale, b_scale, y_scale, y_zp, lo, hi, &rq));
+  return integer_host(ctx, a, a_signed, a_shape, a_rank, a_zp, a_zp_len, b, b_signed, b_shape,
+                      b_rank, b_zp, b_zp_len, &rq, y);
+}
+
+mg_status mg_qlinear_matmul_w(mg_ctx *ctx, const void *a, int32_t a_signed, int64_t rows,
+                              int64_t K, float a_scale, const int32_t *a_zp, int64_t a_zp_len,
+                              const mg_weight *w, float b_scale, float y_scale, int32_t y_zp,
+                              int32_t lo, int32_t hi, void *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_matmul_w: null context");
+  mg_requant rq;
+  MG_TRY(requant_params(a_scale, b_scale, y_scale, y_zp, lo, hi, &rq));
+  return integer_w(ctx, a, false, a_signed, rows, K, a_zp, a_zp_len, w, &rq, y, false);
+}
+
+mg_status mg_qlinear_matmul_w_dev(mg_ctx *ctx, const void *a_dev, int32_t a_signed, int64_t rows,
+                                  int64_t K, float a_scale, const int32_t *a_zp,
+                                  int64_t a_zp_len, const mg_weight *w, float b_scale,
+                                  float y_scale, int32_t y_zp, int32_t lo, int32_t hi,
+                                  void *y_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_matmul_w_dev: null context");
+  mg_requant rq;
+  MG_TRY(requant_params(a_scale, b_scale, y_scale, y_zp, lo, hi, &rq));
+  return integer_w(ctx, a_dev, true, a_signed, rows, K, a_zp, a_zp_len, w, &rq, y_dev, true);
+}
+
+// ------------------------------------------------------------------ DQL
+
+mg_status mg_dynamic_quantize_linear_dev(mg_ctx *ctx, const float *x_dev, int64_t n,
+                                         uint8_t *y_dev, void *scale_zp_dev) {
+  g_last_error.clear();
+  if (!ctx || n < 0 || (n > 0 && (!x_dev || !y_dev)) || !scale_zp_dev)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_dynamic_quantize_linear: invalid argument");
+  MG_TRY(mg_use_device(ctx));
+  const size_t ws = mg_dql_ws_bytes(n);
+  MG_TRY(mg_check_control(ctx, (int64_t)ws));
+  MG_TRY(mg_ws_reserve(ctx, ws));
+  return mg_dql_run(ctx, x_dev, n, y_dev, scale_zp_dev, ctx->ws);
+}
+
+mg_status mg_dynamic_quantize_linear(mg_ctx *ctx, const float *x, int64_t n, uint8_t *y,
+                                     float *scale, int32_t *zp) {
+  g_last_error.clear();
+  if (!ctx || n < 0 || (n > 0 && (!x || !y)) || !scale || !zp)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_dynamic_quantize_linear: invalid argument");
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t ox = s.take((size_t)n * 4), oy = s.take((size_t)n), osz = s.take(16);
+  const size_t ow = s.take(mg_dql_ws_bytes(n));
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  if (n) MG_HIP(hipMemcpyAsync(base + ox, x, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+  MG_TRY(mg_dql_run(ctx, reinterpret_cast<float *>(base + ox), n,
+                    reinterpret_cast<uint8_t *>(base + oy), base + osz, base + ow));
+  int32_t szp[3];
+  MG_HIP(hipMemcpyAsync(szp, base + osz, 12, hipMemcpyDeviceToHost, ctx->stream));
+  if (n) MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)n, hipMemcpyDeviceToHost, ctx->stream));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  if (szp[2])
+    return mg_fail(MG_UNSUPPORTED, "DynamicQuantizeLinear: non-finite input (Infinity or NaN toInt)");
+  std::memcpy(scale, &szp[0], 4);
+  *zp = szp[1];
+  return MG_OK;
+}
+
+// ------------------------------------------------------------ fp32 ops
+
+namespace {
+
+struct F32Batch {
+  int64_t M, K, N, batch;
+  std::vector<int64_t> out_shape, a_off, b_off;
+};
+
+mg_status plan_matmul_f32(const int64_t *a_shape, int32_t a_rank, const int64_t *b_shape,
+                          int32_t b_rank, F32Batch *p) {
+  if (!shape_ok(a_shape, a_rank) || !shape_ok(b_shape, b_rank) || a_rank < 2 || b_rank < 2)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMul: operands must have rank >= 2");
+  p->M = a_shape[a_rank - 2];
+  p->K = a_shape[a_rank - 1];
+  p->N = b_shape[b_rank - 1];
+  if (b_shape[b_rank - 2] != p->K)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMul inner dims mismatch: " + std::to_string(p->K) +
+                                            " vs " + std::to_string(b_shape[b_rank - 2]));
+  const int32_t ar = a_rank - 2, br = b_rank - 2, r = std::max(ar, br);
+  std::vector<int64_t> ob(r);
+  for (int32_t d = 0; d < r; d++) {
+    const int64_t x = d < r - ar ? 1 : a_shape[d - (r - ar)];
+    const int64_t y = d < r - br ? 1 : b_shape[d - (r - br)];
+    if (x != y && x != 1 && y != 1)
+      return mg_fail(MG_INVALID_ARGUMENT, "MatMul: batch dims do not broadcast");
+    ob[d] = x == 1 ? y : x;
+  }
+  p->batch = 1;
+  for (auto v : ob) p->batch *= v;
+  p->out_shape = ob;
+  p->out_shape.push_back(p->M);
+  p->out_shape.push_back(p->N);
+  const int64_t bbatch = prod(b_shape, 0, br);
+  p->a_off.clear();
+  p->b_off.clear();
+  if (p->batch > 1 && bbatch == 1) {
+    // Shared-weight collapse (lib/src/onnx_ops.dart:1728-1735).
+    p->M *= p->batch;
+    p->batch = 1;
+    return MG_OK;
+  }
+  std::vector<int64_t> coords(r, 0);
+  for (int64_t bi = 0; bi < p->batch; bi++) {
+    int64_t rem = bi;
+    for (int32_t d = r - 1; d >= 0; d--) {
+      coords[d] = rem % ob[d];
+      rem /= ob[d];
+    }
+    int64_t ai = 0, bj = 0;
+    for (int32_t d = 0; d < ar; d++) {
+      const int64_t s = a_shape[d];
+      ai = ai * s + (s == 1 ? 0 : coords[d + (r - ar)]);
+    }
+    for (int32_t d = 0; d < br; d++) {
+      const int64_t s = b_shape[d];
+      bj = bj * s + (s == 1 ? 0 : coords[d + (r - br)]);
+    }
+    p->a_off.push_back(ai * p->M * p->K);
+    p->b_off.push_back(bj * p->K * p->N);
+  }
+  return MG_OK;
+}
+
+mg_status c_strides(const int64_t *c_shape, int32_t c_rank, int64_t M, int64_t N, int64_t *rs,
+                    int64_t *cs) {
+  if (c_rank > 2 || !shape_ok(c_shape, c_rank))
+    return mg_fail(MG_INVALID_ARGUMENT, "Gemm: C must broadcast to [M, N]");
+  int64_t s0 = 1, s1 = 1;
+  if (c_rank == 2) {
+    s0 = c_shape[0];
+    s1 = c_shape[1];
+  } else if (c_rank == 1) {
+    s1 = c_shape[0];
+  }
+  if ((s0 != 1 && s0 != M) || (s1 != 1 && s1 != N))
+    return mg_fail(MG_INVALID_ARGUMENT, "Gemm: C must broadcast to [M, N]");
+  *cs = s1 == 1 ? 0 : 1;
+  *rs = s0 == 1 ? 0 : s1;
+  return MG_OK;
+}
+
+// Runs p on device buffers; offsets go through the workspace at ws_off.
+mg_status run_f32_batched(mg_ctx *ctx, const F32Batch &p, const float *a, const float *b,
+                          float *y, char *ws) {
+  mg_f32_problem q{};
+  q.M = p.M;
+  q.N = p.N;
+  q.K = p.K;
+  q.batch = p.batch;
+  q.lda = p.K;
+  q.ldb = p.N;
+  q.alpha = 1.f;
+  q.beta = 1.f;
+  if (!p.a_off.empty()) {
+    int64_t *off = reinterpret_cast<int64_t *>(ws);
+    std::vector<int64_t> both(p.a_off);
+    both.insert(both.end(), p.b_off.begin(), p.b_off.end());
+    MG_HIP(hipMemcpyAsync(off, both.data(), both.size() * 8, hipMemcpyHostToDevice, ctx->stream));
+    q.a_off = off;
+    q.b_off = off + p.batch;
+  }
+  return mg_f32_run(ctx, q, a, b, y);
+}
+
+}  // namespace
+
+mg_status mg_matmul_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape, int32_t a_rank,
+                        const float *b, const int64_t *b_shape, int32_t b_rank, float *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_f32: null context");
+  F32Batch p;
+  MG_TRY(plan_matmul_f32(a_shape, a_rank, b_shape, b_rank, &p));
+  const int64_t ny = p.batch * p.M * p.N;
+  if (ny == 0) return MG_OK;
+  const int64_t na = prod(a_shape, 0, a_rank), nb = prod(b_shape, 0, b_rank);
+  if ((!a && na) || (!b && nb) || !y) return mg_fail(MG_INVALID_ARGUMENT, "MatMul: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t oa = s.take((size_t)na * 4), ob = s.take((size_t)nb * 4), oy = s.take((size_t)ny * 4);
+  const size_t oo = s.take((size_t)p.batch * 16 + 16);
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  if (na) MG_HIP(hipMemcpyAsync(base + oa, a, (size_t)na * 4, hipMemcpyHostToDevice, ctx->stream));
+  if (nb) MG_HIP(hipMemcpyAsync(base + ob, b, (size_t)nb * 4, hipMemcpyHostToDevice, ctx->stream));
+  MG_TRY(run_f32_batched(ctx, p, reinterpret_cast<float *>(base + oa),
+                         reinterpret_cast<float *>(base + ob), reinterpret_cast<float *>(base + oy),
+                         base + oo));
+  MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)ny * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  return MG_OK;
+}
+
+mg_status mg_matmul_f32_dev(mg_ctx *ctx, const float *a_dev, const int64_t *a_shape,
+                            int32_t a_rank, const float *b_dev, const int64_t *b_shape,
+                            int32_t b_rank, float *y_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_f32_dev: null context");
+  F32Batch p;
+  MG_TRY(plan_matmul_f32(a_shape, a_rank, b_shape, b_rank, &p));
+  if (p.batch * p.M * p.N == 0) return MG_OK;
+  MG_TRY(mg_use_device(ctx));
+  const size_t ws = (size_t)p.batch * 16 + 16;
+  MG_TRY(mg_check_control(ctx, (int64_t)ws));
+  MG_TRY(mg_ws_reserve(ctx, ws));
+  return run_f32_batched(ctx, p, a_dev, b_dev, y_dev, static_cast<char *>(ctx->ws));
+}
+
+mg_status mg_gemm_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape, const float *b,
+                      const int64_t *b_shape, int32_t trans_a, int32_t trans_b, float alpha,
+                      float beta, const float *c, const int64_t *c_shape, int32_t c_rank,
+                      float *y) {
+  g_last_error.clear();
+  if (!ctx || !a_shape || !b_shape) return mg_fail(MG_INVALID_ARGUMENT, "mg_gemm_f32: null argument");
+  if (!shape_ok(a_shape, 2) || !shape_ok(b_shape, 2))
+    return mg_fail(MG_INVALID_ARGUMENT, "Gemm: invalid operand shape");
+  const int64_t M = trans_a ? a_shape[1] : a_shape[0], K = trans_a ? a_shape[0] : a_shape[1];
+  const int64_t Kb = trans_b ? b_shape[1] : b_shape[0], N = trans_b ? b_shape[0] : b_shape[1];
+  if (K != Kb)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMul inner dims mismatch: " + std::to_string(K) +
+                                            " vs " + std::to_string(Kb));
+  mg_f32_problem q{};
+  q.M = M;
+  q.N = N;
+  q.K = K;
+  q.batch = 1;
+  q.lda = a_shape[1];
+  q.ldb = b_shape[1];
+  q.trans_a = trans_a;
+  q.trans_b = trans_b;
+  q.alpha = alpha;
+  q.beta = beta;
+  int64_t nc = 0;
+  if (c) {
+    MG_TRY(c_strides(c_shape, c_rank, M, N, &q.c_rs, &q.c_cs));
+    nc = prod(c_shape, 0, c_rank);
+  }
+  if (M * N == 0) return MG_OK;
+  if (!a || !b || !y) return mg_fail(MG_INVALID_ARGUMENT, "Gemm: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t oa = s.take((size_t)(M * K) * 4), ob = s.take((size_t)(K * N) * 4);
+  const size_t oc = s.take((size_t)nc * 4), oy = s.take((size_t)(M * N) * 4);
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  MG_HIP(hipMemcpyAsync(base + oa, a, (size_t)(M * K) * 4, hipMemcpyHostToDevice, ctx->stream));
+  MG_HIP(hipMemcpyAsync(base + ob, b, (size_t)(K * N) * 4, hipMemcpyHostToDevice, ctx->stream));
+  if (c) {
+    MG_HIP(hipMemcpyAsync(base + oc, c, (size_t)nc * 4, hipMemcpyHostToDevice, ctx->stream));
+    q.c = reinterpret_cast<const float *>(base + oc);
+  }
+  MG_TRY(mg_f32_run(ctx, q, reinterpret_cast<float *>(base + oa),
+                    reinterpret_cast<float *>(base + ob), reinterpret_cast<float *>(base + oy)));
+  MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)(M * N) * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  return MG_OK;
+}
+
+namespace {
+mg_status gemm_w(mg_ctx *ctx, const float *a, bool a_dev_ptr, int64_t rows, int64_t K,
+                 const mg_weight *w, float alpha, float beta, const float *c, bool c_dev_ptr,
+                 const int64_t *c_shape, int32_t c_rank, float *y, bool y_dev_ptr) {
+  if (!w || w->kind != MG_W_F32) return mg_fail(MG_INVALID_ARGUMENT, "Gemm: not an fp32 weight");
+  if (rows < 0 || K != w->K)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMul inner dims mismatch: " + std::to_string(K) +
+                                            " vs " + std::to_string(w->K));
+  mg_f32_problem q{};
+  q.M = rows;
+  q.N = w->N;
+  q.K = K;
+  q.batch = 1;
+  q.lda = K;
+  q.ldb = w->N;
+  q.alpha = alpha;
+  q.beta = beta;
+  int64_t nc = 0;
+  if (c) {
+    MG_TRY(c_strides(c_shape, c_rank, rows, w->N, &q.c_rs, &q.c_cs));
+    nc = prod(c_shape, 0, c_rank);
+  }
+  if (rows * w->N == 0) return MG_OK;
+  if (!a || !y) return mg_fail(MG_INVALID_ARGUMENT, "Gemm: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t oa = a_dev_ptr ? 0 : s.take((size_t)(rows * K) * 4);
+  const size_t oc = (c && !c_dev_ptr) ? s.take((size_t)nc * 4) : 0;
+  const size_t oy = y_dev_ptr ? 0 : s.take((size_t)(rows * w->N) * 4);
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  const float *ad = a;
+  float *yd = y;
+  if (!a_dev_ptr) {
+    MG_HIP(hipMemcpyAsync(base + oa, a, (size_t)(rows * K) * 4, hipMemcpyHostToDevice, ctx->stream));
+    ad = reinterpret_cast<const float *>(base + oa);
+  }
+  if (c) {
+    if (!c_dev_ptr) {
+      MG_HIP(hipMemcpyAsync(base + oc, c, (size_t)nc * 4, hipMemcpyHostToDevice, ctx->stream));
+      q.c = reinterpret_cast<const float *>(base + oc);
+    } else {
+      q.c = c;
+    }
+  }
+  if (!y_dev_ptr) yd = reinterpret_cast<float *>(base + oy);
+  MG_TRY(mg_f32_run(ctx, q, ad, w->f32.b, yd));
+  if (!y_dev_ptr) {
+    MG_HIP(hipMemcpyAsync(y, yd, (size_t)(rows * w->N) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    MG_HIP(hipStreamSynchronize(ctx->stream));
+  }
+  return MG_OK;
+}
+}  // namespace
+
+mg_status mg_gemm_f32_w(mg_ctx *ctx, const float *a, int64_t rows, int64_t K, const mg_weight *w,
+                        float alpha, float beta, const float *c, const int64_t *c_shape,
+                        int32_t c_rank, float *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_gemm_f32_w: null context");
+  return gemm_w(ctx, a, false, rows, K, w, alpha, beta, c, false, c_shape, c_rank, y, false);
+}
+
+mg_status mg_gemm_f32_w_dev(mg_ctx *ctx, const float *a_dev, int64_t rows, int64_t K,
+                            const mg_weight *w, float alpha, float beta, const float *c_dev,
+                            const int64_t *c_shape, int32_t c_rank, float *y_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_gemm_f32_w_dev: null context");
+  return gemm_w(ctx, a_dev, true, rows, K, w, alpha, beta, c_dev, true, c_shape, c_rank, y_dev,
+                true);
+}
+
+}  // extern "C"

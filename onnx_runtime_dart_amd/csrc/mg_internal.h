@@ -1,0 +1,161 @@
+// Internal declarations shared by the migemm C-ABI and its HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/migemm.h"
+
+// ---------------------------------------------------------------- errors
+
+// Records `msg` as this thread's last error and returns `st`.
+mg_status mg_fail(mg_status st, const std::string &msg);
+
+#define MG_HIP(call)                                                         \
+  do {                                                                       \
+    hipError_t e_ = (call);                                                  \
+    if (e_ != hipSuccess)                                                    \
+      return mg_fail(e_ == hipErrorOutOfMemory ? MG_OUT_OF_MEMORY            \
+                                               : MG_DEVICE_ERROR,            \
+                     std::string(#call) + ": " + hipGetErrorString(e_));     \
+  } while (0)
+
+#define MG_TRY(expr)                    \
+  do {                                  \
+    mg_status s_ = (expr);              \
+    if (s_ != MG_OK) return s_;         \
+  } while (0)
+
+// ------------------------------------------------------------ structures
+
+struct mg_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  const volatile int32_t *cancel_flag = nullptr;
+  int64_t max_bytes = -1;
+  // Grow-only device workspace for prepasses, partial sums and staging of
+  // host-pointer calls.  Reused across calls of this context only.
+  void *ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
+enum mg_weight_kind { MG_W_NBITS = 1, MG_W_INT8 = 2, MG_W_F32 = 3 };
+
+// Device form of an int4 MatMulNBits weight.  Column group = 64 columns,
+// k group = 128 k.  See nbits.hip for the layouts.
+struct mg_nbits_dev {
+  int64_t bs = 0;     // block_size
+  int64_t nb = 0;     // ceil(K / bs)
+  int64_t nbh = 0;    // ceil(nb / 2) (bytes of packed zero points per column)
+  int64_t kpad = 0;   // K padded to a multiple of 128 (and >= nb*bs)
+  int64_t c4 = 0;     // kpad / 128
+  int64_t ng = 0;     // ceil(N / 64)
+  int32_t zp_kind = 0;
+  uint32_t *wq = nullptr;     // [ng][c4][4 g][64 col][4 j] nibble dwords
+  float *scales = nullptr;    // [ng][nb][64]
+  uint8_t *zp4 = nullptr;     // [ng][nbh][64]  (MG_ZP_UINT4)
+  float *zpf = nullptr;       // [ng][nb][64]   (MG_ZP_FLOAT)
+  float *bias = nullptr;      // [N] or null
+};
+
+// Device form of an 8-bit MatMulInteger weight B [K, N].
+struct mg_int8_dev {
+  int32_t b_signed = 0;
+  int64_t kpad = 0;        // K padded to a multiple of 64
+  int64_t npad = 0;        // N padded to a multiple of 16
+  int8_t *bq = nullptr;    // B - (b_signed ? 0 : 128) as int8, fragment layout
+  int32_t *colsum = nullptr;  // [npad] column sums of the stored int8 B'
+  int32_t *cb = nullptr;      // [npad] (b_signed ? 0 : 128) - bZp[col]
+};
+
+struct mg_f32_dev {
+  float *b = nullptr;  // [K][N] row-major (transposed at upload if transB)
+};
+
+struct mg_weight {
+  mg_weight_kind kind;
+  int device = 0;
+  int64_t K = 0, N = 0;
+  int64_t device_bytes = 0;
+  mg_nbits_dev nbits;
+  mg_int8_dev i8;
+  mg_f32_dev f32;
+};
+
+// ------------------------------------------------------- context helpers
+
+// Cancellation flag and byte budget check before a launch.
+mg_status mg_check_control(mg_ctx *ctx, int64_t additional_bytes);
+// Ensures ctx->ws holds at least `bytes` (grow-only).
+mg_status mg_ws_reserve(mg_ctx *ctx, size_t bytes);
+// Sets the context's device current on this thread.
+mg_status mg_use_device(mg_ctx *ctx);
+mg_status mg_launch_check(const char *what);
+
+static inline size_t mg_align(size_t x, size_t a = 256) {
+  return (x + a - 1) / a * a;
+}
+
+// ----------------------------------------------------------- NBits entry
+
+mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const uint8_t *b,
+                          const float *scales, int32_t zp_kind, const void *zp,
+                          const float *bias);
+void mg_nbits_free(mg_weight *w);
+// Workspace bytes mg_nbits_run needs for M rows.
+size_t mg_nbits_ws_bytes(const mg_weight *w, int64_t M);
+// a_dev [M, K] f32, y_dev [M, N] f32; ws holds mg_nbits_ws_bytes bytes.
+mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
+                       int64_t M, float *y_dev, void *ws);
+
+// ------------------------------------------------------------ int8 entry
+
+mg_status mg_int8_upload(mg_ctx *ctx, mg_weight *w, const void *b,
+                         int32_t b_signed, const int32_t *b_zp,
+                         int64_t b_zp_len);
+void mg_int8_free(mg_weight *w);
+size_t mg_int8_ws_bytes(const mg_weight *w, int64_t rows);
+// Requant parameters for QLinearMatMul; null => plain int32 output.
+struct mg_requant {
+  float mult;
+  int32_t y_zp, lo, hi;
+};
+// a_dev [rows, K] (u8 or i8), a zero point array on host (len 0, 1 or rows),
+// y_dev int32 [rows, N] or (with rq) uint8/int8 [rows, N].
+mg_status mg_int8_run(mg_ctx *ctx, const mg_weight *w, const void *a_dev,
+                      int32_t a_signed, int64_t rows, const int32_t *a_zp,
+                      int64_t a_zp_len, const mg_requant *rq, void *y_dev,
+                      void *ws);
+// Device-side prepack of a runtime B [K, N] into a temporary weight whose
+// arrays live in `ws_weight` (mg_int8_weight_ws_bytes bytes).
+size_t mg_int8_weight_ws_bytes(int64_t K, int64_t N);
+mg_status mg_int8_prepack_dev(mg_ctx *ctx, mg_weight *w, const void *b_dev,
+                              int32_t b_signed, const int32_t *b_zp,
+                              int64_t b_zp_len, void *ws_weight);
+
+// ------------------------------------------------------------- fp32 entry
+
+// y[batch][M][N] = alpha * A . B + beta * C with per-batch element offsets.
+struct mg_f32_problem {
+  int64_t M, N, K;
+  int64_t batch;
+  const int64_t *a_off;  // device [batch] element offsets (null => 0)
+  const int64_t *b_off;  // device [batch]
+  int64_t lda, ldb;      // row strides of the (non-transposed views)
+  int32_t trans_a, trans_b;
+  float alpha, beta;
+  const float *c;        // null or device C
+  int64_t c_rs, c_cs;    // element strides of C over rows / cols (0 = bcast)
+};
+mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
+                     const float *b_dev, float *y_dev);
+
+// --------------------------------------------------------------- DQL entry
+
+mg_status mg_dql_run(mg_ctx *ctx, const float *x_dev, int64_t n,
+                     uint8_t *y_dev, void *scale_zp_dev, void *ws);
+size_t mg_dql_ws_bytes(int64_t n);

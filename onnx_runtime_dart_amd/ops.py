@@ -1,0 +1,364 @@
+"""Host-side operator interface over libmigemm, mirroring the reference ops.
+
+Same names (snake_case of the Dart functions), argument meaning, attribute
+defaults and error classes as the reference:
+
+    op_matmul_nbits        <- opMatMulNBits   lib/src/onnx_qlinear_ops.dart:115
+    op_matmul_integer      <- opMatMulInteger lib/src/onnx_qlinear_ops.dart:32
+    op_qlinear_matmul      <- opQLinearMatMul lib/src/onnx_qlinear_ops.dart:85
+    op_dynamic_quantize_linear <- opDynamicQuantizeLinear lib/src/onnx_ops.dart:3556
+    op_matmul              <- opMatMul        lib/src/onnx_ops.dart:1710
+    op_gemm                <- opGemm          lib/src/onnx_ops.dart:2152
+
+Tensors are numpy arrays on the host; every op runs on the GPU through the
+C ABI (there is no CPU path).  Weight handles (NBitsWeight, Int8Weight,
+F32Weight) keep prepacked weights resident in HBM across calls, like the
+graph's prepacked-weight cache (lib/src/onnx_graph.dart:102-105).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+from .errors import ArgumentError, UnsupportedError
+
+MG_ZP_NONE, MG_ZP_UINT4, MG_ZP_FLOAT = 0, 1, 2
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _shape_arr(a):
+    return np.ascontiguousarray(np.array(a.shape, dtype=np.int64))
+
+
+class Context:
+    """One mg_ctx: a device, a stream, a grow-only workspace."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check(lib.mg_ctx_create(device, C.byref(h)), "mg_ctx_create")
+        self.handle = h
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            lib.mg_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, hip_stream: int):
+        check(lib.mg_ctx_set_stream(self.handle, C.c_void_p(hip_stream)))
+
+    def stream(self) -> int:
+        s = C.c_void_p()
+        check(lib.mg_ctx_get_stream(self.handle, C.byref(s)))
+        return s.value or 0
+
+    def synchronize(self):
+        check(lib.mg_ctx_synchronize(self.handle))
+
+    def set_control(self, cancel_flag=None, max_bytes: int = -1):
+        """cancel_flag: a numpy int32 array of size 1 (polled before launches)."""
+        self._cancel = cancel_flag
+        check(lib.mg_ctx_set_control(self.handle, _ptr(cancel_flag), int(max_bytes)))
+
+
+_tls = threading.local()
+
+
+def default_context() -> Context:
+    ctx = getattr(_tls, "ctx", None)
+    if ctx is None:
+        ctx = Context(0)
+        _tls.ctx = ctx
+    return ctx
+
+
+# ------------------------------------------------------------------ weights
+
+
+class _Weight:
+    handle = None
+
+    def release(self):
+        if self.handle:
+            lib.mg_weight_release(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    def info(self):
+        k, n, b = C.c_int64(), C.c_int64(), C.c_int64()
+        check(lib.mg_weight_info(self.handle, C.byref(k), C.byref(n), C.byref(b)))
+        return k.value, n.value, b.value
+
+
+class NBitsWeight(_Weight):
+    """MatMulNBits B/scales/zero_points/bias uploaded and prepacked."""
+
+    def __init__(self, b_q, scales, zero_points=None, *, k, n, bits=4, block_size,
+                 bias=None, has_g_idx=False, ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        self.k, self.n = int(k), int(n)
+        if b_q is None or np.asarray(b_q).dtype != np.uint8:
+            raise ArgumentError("MatMulNBits: invalid packed weights or scales")
+        b_q = np.ascontiguousarray(b_q, dtype=np.uint8)
+        sc = np.asarray(scales)
+        if sc.dtype.kind != "f":
+            raise ArgumentError("MatMulNBits: invalid packed weights or scales")
+        sc = np.ascontiguousarray(sc, dtype=np.float32)
+        kind, zp = MG_ZP_NONE, None
+        if zero_points is not None:
+            zp = np.asarray(zero_points)
+            if zp.dtype == np.uint8:
+                kind = MG_ZP_UINT4
+            elif zp.dtype.kind == "f":
+                kind, zp = MG_ZP_FLOAT, zp.astype(np.float32)
+            else:
+                raise ArgumentError("MatMulNBits: invalid zero_points")
+            zp = np.ascontiguousarray(zp)
+        if bias is not None:
+            bias = np.asarray(bias)
+            if bias.dtype.kind != "f":
+                raise ArgumentError("MatMulNBits: bias must be floating point [N]")
+            bias = np.ascontiguousarray(bias, dtype=np.float32)
+        h = C.c_void_p()
+        check(lib.mg_weight_nbits_create(
+            self.ctx.handle, int(k), int(n), int(bits), int(block_size),
+            _ptr(b_q), _ptr(_shape_arr(b_q)), b_q.ndim,
+            _ptr(sc), _ptr(_shape_arr(sc)), sc.ndim,
+            kind, _ptr(zp), _ptr(_shape_arr(zp)) if zp is not None else None,
+            zp.ndim if zp is not None else 0,
+            _ptr(bias), _ptr(_shape_arr(bias)) if bias is not None else None,
+            bias.ndim if bias is not None else 0, int(bool(has_g_idx)), C.byref(h)))
+        self.handle = h
+
+    def __call__(self, a) -> np.ndarray:
+        a = np.asarray(a)
+        if a.ndim < 1 or a.shape[-1] != self.k or a.dtype.kind != "f":
+            raise ArgumentError("MatMulNBits: invalid K, N, block_size or input shape")
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        m = a.size // self.k
+        y = np.empty(a.shape[:-1] + (self.n,), dtype=np.float32)
+        if m == 0:
+            return y
+        check(lib.mg_matmul_nbits(self.ctx.handle, self.handle, _ptr(a), m, _ptr(y)))
+        return y
+
+    def run_dev(self, a_ptr: int, m: int, y_ptr: int):
+        check(lib.mg_matmul_nbits_dev(self.ctx.handle, self.handle, C.c_void_p(a_ptr), m,
+                                      C.c_void_p(y_ptr)))
+
+
+def _zp_arg(z):
+    if z is None:
+        return None, 0
+    z = np.ascontiguousarray(np.asarray(z).astype(np.int32).ravel())
+    return z, z.size
+
+
+def _q_operand(x, what):
+    x = np.asarray(x)
+    if x.dtype not in (np.uint8, np.int8):
+        raise ArgumentError(f"{what}: 8-bit integer operand expected, got {x.dtype}")
+    return np.ascontiguousarray(x), int(x.dtype == np.int8)
+
+
+class Int8Weight(_Weight):
+    """MatMulInteger B [K, N] uploaded with its zero point and column sums."""
+
+    def __init__(self, b, b_zp=None, ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        b, self.b_signed = _q_operand(b, "MatMulInteger")
+        if b.ndim != 2:
+            raise ArgumentError("MatMulInteger: weight must be [K, N]")
+        self.k, self.n = b.shape
+        zb, lb = _zp_arg(b_zp)
+        h = C.c_void_p()
+        check(lib.mg_weight_int8_create(self.ctx.handle, _ptr(b), self.b_signed, self.k,
+                                        self.n, _ptr(zb), lb, C.byref(h)))
+        self.handle = h
+
+    def matmul_integer(self, a, a_zp=None) -> np.ndarray:
+        a, sa = _q_operand(a, "MatMulInteger")
+        rows = a.size // self.k if self.k else 0
+        za, la = _zp_arg(a_zp)
+        y = np.empty(a.shape[:-1] + (self.n,), dtype=np.int32)
+        check(lib.mg_matmul_integer_w(self.ctx.handle, _ptr(a), sa, rows, a.shape[-1],
+                                      _ptr(za), la, self.handle, _ptr(y)))
+        return y.astype(np.int64)
+
+    def qlinear_matmul(self, a, a_scale, a_zp, b_scale, y_scale, y_zp, *, lo, hi):
+        a, sa = _q_operand(a, "QLinearMatMul")
+        rows = a.size // self.k if self.k else 0
+        za, la = _zp_arg(a_zp)
+        y = np.empty(a.shape[:-1] + (self.n,), dtype=np.int8 if lo < 0 else np.uint8)
+        check(lib.mg_qlinear_matmul_w(self.ctx.handle, _ptr(a), sa, rows, a.shape[-1],
+                                      float(a_scale), _ptr(za), la, self.handle,
+                                      float(b_scale), float(y_scale), int(y_zp), lo, hi,
+                                      _ptr(y)))
+        return y.astype(np.int64)
+
+
+class F32Weight(_Weight):
+    """fp32 Gemm/MatMul B uploaded once; trans_b transposes on upload."""
+
+    def __init__(self, b, trans_b=False, ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        if b.ndim != 2:
+            raise ArgumentError("Gemm: weight must be rank 2")
+        rows, cols = b.shape
+        self.k, self.n = (cols, rows) if trans_b else (rows, cols)
+        h = C.c_void_p()
+        check(lib.mg_weight_f32_create(self.ctx.handle, _ptr(b), rows, cols,
+                                       int(bool(trans_b)), C.byref(h)))
+        self.handle = h
+
+    def gemm(self, a, c=None, *, alpha=1.0, beta=1.0) -> np.ndarray:
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        rows = a.size // a.shape[-1] if a.size else 0
+        y = np.empty(a.shape[:-1] + (self.n,), dtype=np.float32)
+        if c is not None:
+            c = np.ascontiguousarray(c, dtype=np.float32)
+        check(lib.mg_gemm_f32_w(self.ctx.handle, _ptr(a), rows, a.shape[-1], self.handle,
+                                float(alpha), float(beta), _ptr(c),
+                                _ptr(_shape_arr(c)) if c is not None else None,
+                                c.ndim if c is not None else 0, _ptr(y)))
+        return y
+
+
+# ---------------------------------------------------------------------- ops
+
+
+def op_matmul_nbits(a, b_q, scales, zero_points=None, *, k, n, bits=4, block_size,
+                    bias=None, ctx: Context | None = None) -> np.ndarray:
+    """opMatMulNBits (lib/src/onnx_qlinear_ops.dart:115-228)."""
+    if bits != 4:
+        raise UnsupportedError(f"MatMulNBits: only bits=4 supported, got {bits}")
+    a = np.asarray(a)
+    if (k <= 0 or n <= 0 or block_size < 16 or block_size & (block_size - 1)
+            or a.ndim < 1 or a.shape[-1] != k):
+        raise ArgumentError("MatMulNBits: invalid K, N, block_size or input shape")
+    w = NBitsWeight(b_q, scales, zero_points, k=k, n=n, bits=bits, block_size=block_size,
+                    bias=bias, ctx=ctx)
+    try:
+        return w(a)
+    finally:
+        w.release()
+
+
+def op_matmul_integer(a, b, a_zp=None, b_zp=None, ctx: Context | None = None) -> np.ndarray:
+    """opMatMulInteger (lib/src/onnx_qlinear_ops.dart:32-81); int64 result."""
+    a, sa = _q_operand(a, "MatMulInteger")
+    b, sb = _q_operand(b, "MatMulInteger")
+    if a.ndim < 2 or b.ndim < 2:
+        raise ArgumentError("MatMulInteger: operands must have rank >= 2")
+    za, la = _zp_arg(a_zp)
+    zb, lb = _zp_arg(b_zp)
+    m, n = a.shape[-2], b.shape[-1]
+    ab = int(np.prod(a.shape[:-2])) if a.ndim > 2 else 1
+    bb = int(np.prod(b.shape[:-2])) if b.ndim > 2 else 1
+    out_batch = a.shape[:-2] if ab >= bb else b.shape[:-2]
+    y = np.empty(tuple(out_batch) + (m, n), dtype=np.int32)
+    ctx = ctx or default_context()
+    check(lib.mg_matmul_integer(ctx.handle, _ptr(a), sa, _ptr(_shape_arr(a)), a.ndim,
+                                _ptr(b), sb, _ptr(_shape_arr(b)), b.ndim, _ptr(za), la,
+                                _ptr(zb), lb, _ptr(y)))
+    return y.astype(np.int64)
+
+
+def op_qlinear_matmul(a, a_s, a_zp, b, b_s, b_zp, y_s, y_zp, *, lo, hi,
+                      ctx: Context | None = None) -> np.ndarray:
+    """opQLinearMatMul (lib/src/onnx_qlinear_ops.dart:85-108); int64 result."""
+    if np.size(a_s) != 1 or np.size(b_s) != 1 or np.size(y_s) != 1:
+        raise UnsupportedError("QLinearMatMul: only per-tensor scales supported")
+    a, sa = _q_operand(a, "QLinearMatMul")
+    b, sb = _q_operand(b, "QLinearMatMul")
+    if a.ndim < 2 or b.ndim < 2:
+        raise ArgumentError("MatMulInteger: operands must have rank >= 2")
+    za, la = _zp_arg(a_zp)
+    zb, lb = _zp_arg(b_zp)
+    yz = 0 if y_zp is None else int(np.asarray(y_zp).ravel()[0])
+    m, n = a.shape[-2], b.shape[-1]
+    ab = int(np.prod(a.shape[:-2])) if a.ndim > 2 else 1
+    bb = int(np.prod(b.shape[:-2])) if b.ndim > 2 else 1
+    out_batch = a.shape[:-2] if ab >= bb else b.shape[:-2]
+    y = np.empty(tuple(out_batch) + (m, n), dtype=np.int8 if lo < 0 else np.uint8)
+    ctx = ctx or default_context()
+    check(lib.mg_qlinear_matmul(
+        ctx.handle, _ptr(a), sa, _ptr(_shape_arr(a)), a.ndim,
+        float(np.float32(np.asarray(a_s).ravel()[0])), _ptr(za), la, _ptr(b), sb,
+        _ptr(_shape_arr(b)), b.ndim, float(np.float32(np.asarray(b_s).ravel()[0])), _ptr(zb),
+        lb, float(np.float32(np.asarray(y_s).ravel()[0])), yz, int(lo), int(hi), _ptr(y)))
+    return y.astype(np.int64)
+
+
+def op_dynamic_quantize_linear(x, ctx: Context | None = None):
+    """opDynamicQuantizeLinear (lib/src/onnx_ops.dart:3556-3583) ->
+    (y uint8, scale float32, zero point int)."""
+    ctx = ctx or default_context()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint8)
+    scale = C.c_float()
+    zp = C.c_int32()
+    check(lib.mg_dynamic_quantize_linear(ctx.handle, _ptr(x), x.size, _ptr(y),
+                                         C.byref(scale), C.byref(zp)))
+    return y, np.float32(scale.value), int(zp.value)
+
+
+def op_matmul(a, b, ctx: Context | None = None) -> np.ndarray:
+    """opMatMul (lib/src/onnx_ops.dart:1710-1766), numpy broadcasting."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    if a.ndim < 2 or b.ndim < 2:
+        raise ArgumentError("MatMul: operands must have rank >= 2")
+    try:
+        batch = np.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    except ValueError:
+        raise ArgumentError("MatMul: batch dims do not broadcast") from None
+    y = np.empty(tuple(batch) + (a.shape[-2], b.shape[-1]), dtype=np.float32)
+    ctx = ctx or default_context()
+    check(lib.mg_matmul_f32(ctx.handle, _ptr(a), _ptr(_shape_arr(a)), a.ndim, _ptr(b),
+                            _ptr(_shape_arr(b)), b.ndim, _ptr(y)))
+    return y
+
+
+def op_gemm(a, b, c=None, *, alpha=1.0, beta=1.0, trans_a=False, trans_b=False,
+            ctx: Context | None = None) -> np.ndarray:
+    """opGemm (lib/src/onnx_ops.dart:2152-2172)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    if a.ndim != 2 or b.ndim != 2:
+        raise ArgumentError("Gemm: A and B must be rank 2")
+    m = a.shape[1] if trans_a else a.shape[0]
+    n = b.shape[0] if trans_b else b.shape[1]
+    y = np.empty((m, n), dtype=np.float32)
+    if c is not None:
+        c = np.ascontiguousarray(c, dtype=np.float32)
+    ctx = ctx or default_context()
+    check(lib.mg_gemm_f32(ctx.handle, _ptr(a), _ptr(_shape_arr(a)), _ptr(b),
+                          _ptr(_shape_arr(b)), int(bool(trans_a)), int(bool(trans_b)),
+                          float(alpha), float(beta), _ptr(c),
+                          _ptr(_shape_arr(c)) if c is not None else None,
+                          c.ndim if c is not None else 0, _ptr(y)))
+    return y
+
+
+def library_path() -> str:
+    return str(_lib.LIB_PATH)

@@ -1,0 +1,398 @@
+/* CPU oracle for the matrix-multiply operator family (TEST INFRASTRUCTURE).
+ * See oracle.h for the contract; every routine cites the reference routine it
+ * restates.  Built with -ffp-contract=off so that each f32 multiply and add is
+ * rounded separately, as the reference's Float32x4 lanes do. */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------- helpers */
+
+int64_t orc_round_even(double v, int *err) {
+  /* _roundEven: floor, compare the fraction against one half, ties to even. */
+  if (!isfinite(v)) {
+    if (err) *err = ORC_UNSUPPORTED;
+    return 0;
+  }
+  double f = floor(v);
+  double frac = v - f;
+  int64_t i = (int64_t)f;
+  if (frac > 0.5) return i + 1;
+  if (frac < 0.5) return i;
+  return (i % 2 == 0) ? i : i + 1;
+}
+
+/* ------------------------------------------------------------ fp32 kernel */
+
+/* Panel width of _matmul4x16Direct (gemm_kernel_simd.dart:258-261): as many
+ * columns as keep k*panel*4 bytes under 192 KiB, a multiple of 4, >= 4, <= n.
+ * The panel loop never changes an element's k order, so it only shapes the
+ * memory traffic of the CPU baseline. */
+static int64_t panel_width(int64_t k, int64_t n) {
+  int64_t panel = (192 * 1024) / (k > 0 ? k * 4 : 4);
+  panel = (panel >> 2) << 2;
+  if (panel < 4) panel = 4;
+  if (panel > n) panel = n;
+  return panel;
+}
+
+void orc_matmul_kernel(const float *a, const float *b, float *out, int64_t m,
+                       int64_t k, int64_t n) {
+  /* Columns computed in f32 lanes.  Only the m<4 paths (_gemvScalar,
+   * _matmulSmallM) leave a scalar double tail beyond the last full lane; for
+   * m==1 with n%4==0 the aligned GEMV covers every column (:459-475). */
+  const int64_t f32_cols = (m < 4) ? (n & ~(int64_t)3) : n;
+  if (k == 0) {
+    memset(out, 0, sizeof(float) * (size_t)(m * n));
+    return;
+  }
+  const int64_t panel = panel_width(k, n > 0 ? n : 1);
+  for (int64_t p0 = 0; p0 < f32_cols; p0 += panel) {
+    const int64_t pw = (p0 + panel <= f32_cols) ? panel : f32_cols - p0;
+    int64_t i = 0;
+    /* 4-row x 16-column register tiles (:264-340). */
+    for (; i + 4 <= m; i += 4) {
+      int64_t j = 0;
+      for (; j + 16 <= pw; j += 16) {
+        float c[4][16];
+        memset(c, 0, sizeof c);
+        const float *bp = b + p0 + j;
+        for (int64_t kk = 0; kk < k; kk++, bp += n) {
+          for (int r = 0; r < 4; r++) {
+            const float v = a[(i + r) * k + kk];
+            for (int q = 0; q < 16; q++) {
+              const float prod = v * bp[q];
+              c[r][q] = c[r][q] + prod;
+            }
+          }
+        }
+        for (int r = 0; r < 4; r++)
+          memcpy(out + (i + r) * n + p0 + j, c[r], sizeof(float) * 16);
+      }
+      for (; j < pw; j++) {
+        float c[4] = {0, 0, 0, 0};
+        const float *bp = b + p0 + j;
+        for (int64_t kk = 0; kk < k; kk++, bp += n) {
+          for (int r = 0; r < 4; r++) {
+            const float prod = a[(i + r) * k + kk] * bp[0];
+            c[r] = c[r] + prod;
+          }
+        }
+        for (int r = 0; r < 4; r++) out[(i + r) * n + p0 + j] = c[r];
+      }
+    }
+    /* Remainder rows one at a time (:342-388). */
+    for (; i < m; i++) {
+      int64_t j = 0;
+      for (; j + 16 <= pw; j += 16) {
+        float c[16];
+        memset(c, 0, sizeof c);
+        const float *bp = b + p0 + j;
+        const float *ar = a + i * k;
+        for (int64_t kk = 0; kk < k; kk++, bp += n) {
+          const float v = ar[kk];
+          for (int q = 0; q < 16; q++) {
+            const float prod = v * bp[q];
+            c[q] = c[q] + prod;
+          }
+        }
+        memcpy(out + i * n + p0 + j, c, sizeof(float) * 16);
+      }
+      for (; j < pw; j++) {
+        float c = 0;
+        for (int64_t kk = 0; kk < k; kk++) {
+          const float prod = a[i * k + kk] * b[kk * n + p0 + j];
+          c = c + prod;
+        }
+        out[i * n + p0 + j] = c;
+      }
+    }
+  }
+  /* Scalar double tails (:601-609, :665-673). */
+  for (int64_t i = 0; i < m; i++) {
+    for (int64_t j = f32_cols; j < n; j++) {
+      double s = 0;
+      for (int64_t kk = 0; kk < k; kk++)
+        s += (double)a[i * k + kk] * (double)b[kk * n + j];
+      out[i * n + j] = (float)s;
+    }
+  }
+}
+
+/* ------------------------------------------------------------- MatMul f32 */
+
+static int broadcast_shape(const int64_t *x, int xr, const int64_t *y, int yr,
+                           int64_t *out, int *outr) {
+  int r = xr > yr ? xr : yr;
+  for (int d = 0; d < r; d++) {
+    int64_t xd = (d < r - xr) ? 1 : x[d - (r - xr)];
+    int64_t yd = (d < r - yr) ? 1 : y[d - (r - yr)];
+    if (xd != yd && xd != 1 && yd != 1) return ORC_INVALID_ARGUMENT;
+    out[d] = (xd == 1) ? yd : xd;
+  }
+  *outr = r;
+  return ORC_OK;
+}
+
+/* _flattenBroadcast: flat index into `shape` of the output coordinate
+ * `coords` (right-aligned; size-1 dims read index 0). */
+static int64_t flatten_broadcast(const int64_t *coords, int cr,
+                                 const int64_t *shape, int sr) {
+  int64_t idx = 0;
+  for (int d = 0; d < sr; d++) {
+    int64_t c = coords[d + (cr - sr)];
+    idx = idx * shape[d] + (shape[d] == 1 ? 0 : c);
+  }
+  return idx;
+}
+
+int orc_matmul_f32(const float *a, const int64_t *a_shape, int a_rank,
+                   const float *b, const int64_t *b_shape, int b_rank,
+                   float *y) {
+  if (a_rank < 2 || b_rank < 2 || a_rank > 8 || b_rank > 8)
+    return ORC_INVALID_ARGUMENT;
+  const int64_t m = a_shape[a_rank - 2], k = a_shape[a_rank - 1];
+  const int64_t k2 = b_shape[b_rank - 2], n = b_shape[b_rank - 1];
+  if (k != k2) return ORC_INVALID_ARGUMENT;
+  int64_t ob[8];
+  int obr = 0;
+  if (broadcast_shape(a_shape, a_rank - 2, b_shape, b_rank - 2, ob, &obr))
+    return ORC_INVALID_ARGUMENT;
+  int64_t batch = 1, bbatch = 1;
+  for (int d = 0; d < obr; d++) batch *= ob[d];
+  for (int d = 0; d < b_rank - 2; d++) bbatch *= b_shape[d];
+  /* Shared-weight collapse (onnx_ops.dart:1728-1735). */
+  if (batch > 1 && bbatch == 1) {
+    orc_matmul_kernel(a, b, y, batch * m, k, n);
+    return ORC_OK;
+  }
+  int64_t coords[8] = {0};
+  for (int64_t bi = 0; bi < batch; bi++) {
+    int64_t rem = bi;
+    for (int d = obr - 1; d >= 0; d--) {
+      coords[d] = rem % ob[d];
+      rem /= ob[d];
+    }
+    int64_t ai = flatten_broadcast(coords, obr, a_shape, a_rank - 2);
+    int64_t bj = flatten_broadcast(coords, obr, b_shape, b_rank - 2);
+    orc_matmul_kernel(a + ai * m * k, b + bj * k * n, y + bi * m * n, m, k, n);
+  }
+  return ORC_OK;
+}
+
+int orc_gemm_f32(const float *a, const int64_t *a_shape, const float *b,
+                 const int64_t *b_shape, const float *c, const int64_t *c_shape,
+                 int c_rank, double alpha, double beta, int trans_a,
+                 int trans_b, float *y) {
+  const int64_t m = trans_a ? a_shape[1] : a_shape[0];
+  const int64_t k = trans_a ? a_shape[0] : a_shape[1];
+  const int64_t kb = trans_b ? b_shape[1] : b_shape[0];
+  const int64_t n = trans_b ? b_shape[0] : b_shape[1];
+  if (k != kb) return ORC_INVALID_ARGUMENT;
+  /* opTranspose copies (onnx_ops.dart:2161-2162; the graph caches the
+   * transB copy of an initializer, onnx_graph.dart:2159-2161). */
+  float *at = NULL, *bt = NULL;
+  const float *ap = a, *bp = b;
+  if (trans_a) {
+    at = (float *)malloc(sizeof(float) * (size_t)(m * k + 1));
+    for (int64_t i = 0; i < m; i++)
+      for (int64_t kk = 0; kk < k; kk++) at[i * k + kk] = a[kk * m + i];
+    ap = at;
+  }
+  if (trans_b) {
+    bt = (float *)malloc(sizeof(float) * (size_t)(k * n + 1));
+    for (int64_t kk = 0; kk < k; kk++)
+      for (int64_t j = 0; j < n; j++) bt[kk * n + j] = b[j * k + kk];
+    bp = bt;
+  }
+  orc_matmul_kernel(ap, bp, y, m, k, n);
+  free(at);
+  free(bt);
+  /* alpha in place: f32 element times a double, stored back as f32. */
+  if (alpha != 1.0)
+    for (int64_t i = 0; i < m * n; i++) y[i] = (float)((double)y[i] * alpha);
+  if (c != NULL) {
+    if (c_rank > 2) return ORC_INVALID_ARGUMENT;
+    int64_t cs[2] = {1, 1};
+    for (int d = 0; d < c_rank; d++) cs[2 - c_rank + d] = c_shape[d];
+    if ((cs[0] != 1 && cs[0] != m) || (cs[1] != 1 && cs[1] != n))
+      return ORC_INVALID_ARGUMENT;
+    for (int64_t i = 0; i < m; i++)
+      for (int64_t j = 0; j < n; j++) {
+        float cv = c[(cs[0] == 1 ? 0 : i) * cs[1] + (cs[1] == 1 ? 0 : j)];
+        if (beta != 1.0) cv = (float)((double)cv * beta);
+        y[i * n + j] = y[i * n + j] + cv;
+      }
+  }
+  return ORC_OK;
+}
+
+/* ------------------------------------------------------------ MatMulNBits */
+
+float orc_nbits_weight(int64_t col, int64_t kk, int64_t k, int64_t block_size,
+                       const uint8_t *b, const float *scales, int zp_kind,
+                       const void *zp) {
+  const int64_t nb = (k + block_size - 1) / block_size;
+  const int64_t blob = block_size / 2;
+  const int64_t zp_stride = (nb + 1) / 2;
+  const int64_t blk = kk / block_size;
+  const uint8_t byte = b[(col * nb + blk) * blob + (kk % block_size) / 2];
+  const int q = (kk & 1) == 0 ? (byte & 15) : (byte >> 4);
+  double z = 8;
+  if (zp_kind == 1) {
+    const uint8_t zb = ((const uint8_t *)zp)[col * zp_stride + blk / 2];
+    z = (double)((blk & 1) == 0 ? (zb & 15) : (zb >> 4));
+  } else if (zp_kind == 2) {
+    z = (double)((const float *)zp)[col * nb + blk];
+  }
+  /* (q - zp) in double times the f32 scale, one rounding to f32. */
+  return (float)(((double)q - z) * (double)scales[col * nb + blk]);
+}
+
+int orc_matmul_nbits(const float *a, int64_t m, int64_t k, int64_t n,
+                     int64_t bits, int64_t block_size, const uint8_t *b,
+                     const float *scales, int zp_kind, const void *zp,
+                     const float *bias, float *y) {
+  if (bits != 4) return ORC_UNSUPPORTED;
+  if (k <= 0 || n <= 0 || block_size < 16 ||
+      (block_size & (block_size - 1)) != 0)
+    return ORC_INVALID_ARGUMENT;
+  if (m == 0) return ORC_OK;
+  if (m == 1) {
+    /* Token decode: f64 accumulation in k order, + bias, one f32 rounding
+     * (onnx_qlinear_ops.dart:194-205). */
+    for (int64_t col = 0; col < n; col++) {
+      double sum = 0;
+      for (int64_t kk = 0; kk < k; kk++)
+        sum += (double)a[kk] *
+               (double)orc_nbits_weight(col, kk, k, block_size, b, scales,
+                                        zp_kind, zp);
+      y[col] = (float)(sum + (bias ? (double)bias[col] : 0.0));
+    }
+    return ORC_OK;
+  }
+  /* Multi-row: 32-column dequantized tiles through matmulKernel, then + bias
+   * (onnx_qlinear_ops.dart:208-226). */
+  const int64_t tile_cols = 32;
+  float *bt = (float *)malloc(sizeof(float) * (size_t)(k * tile_cols));
+  float *tile = (float *)malloc(sizeof(float) * (size_t)(m * tile_cols));
+  for (int64_t start = 0; start < n; start += tile_cols) {
+    const int64_t cols = (n - start < tile_cols) ? n - start : tile_cols;
+    for (int64_t col = 0; col < cols; col++)
+      for (int64_t kk = 0; kk < k; kk++)
+        bt[kk * cols + col] = orc_nbits_weight(start + col, kk, k, block_size,
+                                               b, scales, zp_kind, zp);
+    orc_matmul_kernel(a, bt, tile, m, k, cols);
+    for (int64_t row = 0; row < m; row++)
+      for (int64_t col = 0; col < cols; col++)
+        y[row * n + start + col] =
+            (float)((double)tile[row * cols + col] +
+                    (bias ? (double)bias[start + col] : 0.0));
+  }
+  free(bt);
+  free(tile);
+  return ORC_OK;
+}
+
+/* ----------------------------------------------- MatMulInteger / QLinear */
+
+static inline int32_t load_q(const void *p, int is_signed, int64_t i) {
+  return is_signed ? (int32_t)((const int8_t *)p)[i]
+                   : (int32_t)((const uint8_t *)p)[i];
+}
+
+int orc_matmul_integer(const void *a, int a_signed, int64_t a_batch,
+                       const void *b, int b_signed, int64_t b_batch, int64_t m,
+                       int64_t k, int64_t n, const int32_t *a_zp,
+                       int64_t a_zp_len, const int32_t *b_zp, int64_t b_zp_len,
+                       int64_t *y) {
+  if ((a_zp && a_zp_len != 1 && a_zp_len != m) ||
+      (b_zp && b_zp_len != 1 && b_zp_len != n))
+    return ORC_UNSUPPORTED;
+  const int64_t az = (a_zp == NULL || a_zp_len != 1) ? 0 : a_zp[0];
+  const int32_t *az_row = (a_zp && a_zp_len == m && m != 1) ? a_zp : NULL;
+  const int64_t bz = (b_zp == NULL || b_zp_len != 1) ? 0 : b_zp[0];
+  const int32_t *bz_col = (b_zp && b_zp_len == n && n != 1) ? b_zp : NULL;
+  const int64_t batch = a_batch > b_batch ? a_batch : b_batch;
+  if ((a_batch != batch && a_batch != 1) || (b_batch != batch && b_batch != 1))
+    return ORC_INVALID_ARGUMENT;
+  memset(y, 0, sizeof(int64_t) * (size_t)(batch * m * n));
+  for (int64_t bb = 0; bb < batch; bb++) {
+    const int64_t a_off = (a_batch == 1 ? 0 : bb) * m * k;
+    const int64_t b_off = (b_batch == 1 ? 0 : bb) * k * n;
+    int64_t *o = y + bb * m * n;
+    for (int64_t i = 0; i < m; i++) {
+      const int64_t azi = az_row ? az_row[i] : az;
+      for (int64_t kk = 0; kk < k; kk++) {
+        const int64_t av = load_q(a, a_signed, a_off + i * k + kk) - azi;
+        if (av == 0) continue; /* zero contributions skipped (:61-62) */
+        for (int64_t j = 0; j < n; j++) {
+          const int64_t bv = load_q(b, b_signed, b_off + kk * n + j) -
+                             (bz_col ? bz_col[j] : bz);
+          o[i * n + j] += av * bv;
+        }
+      }
+    }
+  }
+  return ORC_OK;
+}
+
+int orc_qlinear_matmul(const void *a, int a_signed, int64_t a_batch,
+                       const void *b, int b_signed, int64_t b_batch, int64_t m,
+                       int64_t k, int64_t n, float a_scale,
+                       const int32_t *a_zp, int64_t a_zp_len, float b_scale,
+                       const int32_t *b_zp, int64_t b_zp_len, float y_scale,
+                       int32_t y_zp, int32_t lo, int32_t hi, int64_t *y) {
+  int st = orc_matmul_integer(a, a_signed, a_batch, b, b_signed, b_batch, m, k,
+                              n, a_zp, a_zp_len, b_zp, b_zp_len, y);
+  if (st) return st;
+  /* mult = fl32(fl32(aS*bS) / yS): each step rounded to f32 (:95-98). */
+  const float ab = (float)((double)a_scale * (double)b_scale);
+  const float mult = (float)((double)ab / (double)y_scale);
+  const int64_t total = (a_batch > b_batch ? a_batch : b_batch) * m * n;
+  for (int64_t i = 0; i < total; i++) {
+    const float p = (float)((double)y[i] * (double)mult);
+    int err = 0;
+    int64_t q = orc_round_even((double)p, &err) + y_zp;
+    if (err) return err;
+    y[i] = q < lo ? lo : (q > hi ? hi : q);
+  }
+  return ORC_OK;
+}
+
+/* ------------------------------------------------ DynamicQuantizeLinear */
+
+int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y,
+                                float *scale_out, int32_t *zp_out) {
+  double mn = 0, mx = 0; /* the range always spans 0 */
+  for (int64_t i = 0; i < n; i++) {
+    const double v = x[i];
+    if (v < mn) mn = v;
+    if (v > mx) mx = v;
+  }
+  const float scale_f = (float)((mx - mn) / 255.0);
+  const double scale = scale_f;
+  const float zpf = scale == 0 ? 0.0f : (float)(-mn / scale);
+  double zc = zpf;
+  if (zc < 0) zc = 0;
+  if (zc > 255) zc = 255;
+  int err = 0;
+  const int64_t zp = orc_round_even(zc, &err);
+  if (err) return err;
+  for (int64_t i = 0; i < n; i++) {
+    int64_t q;
+    if (scale == 0) {
+      q = zp;
+    } else {
+      const float r = (float)((double)x[i] / scale);
+      q = orc_round_even((double)r, &err) + zp;
+      if (err) return err;
+    }
+    y[i] = (uint8_t)(q < 0 ? 0 : (q > 255 ? 255 : q));
+  }
+  *scale_out = scale_f;
+  *zp_out = (int32_t)zp;
+  return ORC_OK;
+}

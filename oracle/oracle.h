@@ -1,0 +1,91 @@
+/* CPU oracle for the matrix-multiply operator family of onnx_runtime_dart.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the checker the parity tests compare the
+ * HIP kernels against, and the CPU baseline bench.py times beside them.  It is
+ * never linked into, loaded by, or called from the product library
+ * (onnx_runtime_dart_amd/), which fails loudly when its HIP build is missing.
+ *
+ * Each function restates one reference routine; the citation on each names
+ * the file:line it follows (paths relative to the reference checkout).
+ * Status codes mirror the product ABI: 0 ok, 1 invalid argument (Dart
+ * ArgumentError), 2 unsupported (Dart UnsupportedError).
+ */
+#ifndef MIGEMM_ORACLE_H
+#define MIGEMM_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_OK = 0, ORC_INVALID_ARGUMENT = 1, ORC_UNSUPPORTED = 2 };
+
+/* matmulKernel: out[m x n] = a[m x k] . b[k x n], row-major, out overwritten.
+ * lib/src/gemm_kernel_simd.dart:32-239 (routing), :244-389 (4x16 direct),
+ * :480-538 / :543-610 (GEMV), :616-675 (small M).  f32 lanes multiply then add
+ * with one rounding each, in k order; the scalar column tails of the m<4
+ * paths accumulate in double (:601-609, :665-673). */
+void orc_matmul_kernel(const float *a, const float *b, float *out, int64_t m,
+                       int64_t k, int64_t n);
+
+/* opMatMul: numpy-broadcast batched matmul, lib/src/onnx_ops.dart:1710-1766.
+ * Shapes have rank >= 2.  y is sized by the broadcast output shape. */
+int orc_matmul_f32(const float *a, const int64_t *a_shape, int a_rank,
+                   const float *b, const int64_t *b_shape, int b_rank,
+                   float *y);
+
+/* opGemm (+ the graph's transB prepack): lib/src/onnx_ops.dart:2152-2172,
+ * lib/src/onnx_graph.dart:2156-2173.  a, b rank 2; c may be NULL or any shape
+ * that broadcasts to [M, N]. */
+int orc_gemm_f32(const float *a, const int64_t *a_shape, const float *b,
+                 const int64_t *b_shape, const float *c, const int64_t *c_shape,
+                 int c_rank, double alpha, double beta, int trans_a,
+                 int trans_b, float *y);
+
+/* opMatMulNBits, lib/src/onnx_qlinear_ops.dart:115-228.
+ * zp_kind: 0 none (default 8), 1 packed uint4 [N * ceil(nb/2)], 2 float
+ * [N * nb].  bias may be NULL.  Shapes are assumed validated by the caller
+ * except for the checks on k, n, bits and block_size. */
+int orc_matmul_nbits(const float *a, int64_t m, int64_t k, int64_t n,
+                     int64_t bits, int64_t block_size, const uint8_t *b,
+                     const float *scales, int zp_kind, const void *zp,
+                     const float *bias, float *y);
+
+/* Dequantized weight element w(col, kk) of opMatMulNBits (the `weight`
+ * closure at lib/src/onnx_qlinear_ops.dart:177-191). */
+float orc_nbits_weight(int64_t col, int64_t kk, int64_t k, int64_t block_size,
+                       const uint8_t *b, const float *scales, int zp_kind,
+                       const void *zp);
+
+/* opMatMulInteger, lib/src/onnx_qlinear_ops.dart:32-81.  a/b are uint8 or
+ * int8 (per *_signed) with a_batch*m*k and b_batch*k*n elements; zero-point
+ * arrays are already widened to int32 (NULL = absent).  y: int64, batch*m*n
+ * elements with batch = max(a_batch, b_batch). */
+int orc_matmul_integer(const void *a, int a_signed, int64_t a_batch,
+                       const void *b, int b_signed, int64_t b_batch, int64_t m,
+                       int64_t k, int64_t n, const int32_t *a_zp,
+                       int64_t a_zp_len, const int32_t *b_zp, int64_t b_zp_len,
+                       int64_t *y);
+
+/* opQLinearMatMul, lib/src/onnx_qlinear_ops.dart:85-108 (lo/hi from the
+ * output zero point's dtype, lib/src/onnx_graph.dart:2902-2917). */
+int orc_qlinear_matmul(const void *a, int a_signed, int64_t a_batch,
+                       const void *b, int b_signed, int64_t b_batch, int64_t m,
+                       int64_t k, int64_t n, float a_scale,
+                       const int32_t *a_zp, int64_t a_zp_len, float b_scale,
+                       const int32_t *b_zp, int64_t b_zp_len, float y_scale,
+                       int32_t y_zp, int32_t lo, int32_t hi, int64_t *y);
+
+/* opDynamicQuantizeLinear, lib/src/onnx_ops.dart:3556-3583. */
+int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y,
+                                float *scale, int32_t *zp);
+
+/* _roundEven, lib/src/onnx_qlinear_ops.dart:19-26 / onnx_ops.dart:3480-3487.
+ * Returns ORC_UNSUPPORTED through *err for non-finite input (Dart's toInt
+ * throws UnsupportedError there). */
+int64_t orc_round_even(double v, int *err);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,74 @@
+"""CPU-side checks of the drop-in boundary: the built library loads, exports
+every entry point include/migemm.h declares, and the host-side operator layer
+raises the reference's error classes before touching a device."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "migemm.h"
+LIB = ROOT / "onnx_runtime_dart_amd" / "lib" / "libmigemm.so"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_operator_family():
+    syms = declared_symbols()
+    for s in ["mg_matmul_nbits", "mg_matmul_integer", "mg_qlinear_matmul",
+              "mg_dynamic_quantize_linear", "mg_matmul_f32", "mg_gemm_f32",
+              "mg_weight_nbits_create", "mg_ctx_create", "mg_last_error"]:
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    assert LIB.exists(), "run onnx_runtime_dart_amd/csrc/build.py first"
+    lib = ctypes.CDLL(str(LIB))
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_every_symbol():
+    from onnx_runtime_dart_amd import _lib
+    assert set(declared_symbols()) == set(_lib.SIGNATURES)
+
+
+def test_version_and_last_error_without_device():
+    from onnx_runtime_dart_amd import _lib
+    assert _lib.lib.mg_version() == b"0.1.0"
+    assert isinstance(_lib.lib.mg_last_error(), bytes)
+
+
+def test_status_codes_map_to_reference_exceptions():
+    from onnx_runtime_dart_amd import errors as E
+    for st, cls in [(1, E.ArgumentError), (2, E.UnsupportedError),
+                    (3, E.OnnxMemoryLimitException), (4, E.OnnxCancelledException),
+                    (5, E.StateError)]:
+        with pytest.raises(cls):
+            E.raise_for_status(st, "x")
+
+
+def test_host_validation_precedes_device_work():
+    # Errors the reference raises before any arithmetic are raised here
+    # before a context is created (no GPU in this container).
+    from onnx_runtime_dart_amd import ops
+    from onnx_runtime_dart_amd.errors import ArgumentError, UnsupportedError
+    a = np.zeros((2, 64), np.float32)
+    b = np.zeros((4, 2, 16), np.uint8)
+    s = np.zeros(8, np.float32)
+    with pytest.raises(UnsupportedError):  # onnx_qlinear_ops.dart:126-128
+        ops.op_matmul_nbits(a, b, s, k=64, n=4, bits=8, block_size=32)
+    with pytest.raises(ArgumentError):  # :129-136 block_size not a power of two
+        ops.op_matmul_nbits(a, b, s, k=64, n=4, block_size=24)
+    with pytest.raises(ArgumentError):  # a.shape.last != K
+        ops.op_matmul_nbits(a, b, s, k=32, n=4, block_size=32)
+    with pytest.raises(UnsupportedError):  # onnx_qlinear_ops.dart:88-90
+        ops.op_qlinear_matmul(np.zeros((2, 2), np.uint8), np.ones(2), None,
+                              np.zeros((2, 2), np.uint8), 1.0, None, 1.0, None,
+                              lo=0, hi=255)

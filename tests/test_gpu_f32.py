@@ -1,0 +1,104 @@
+"""fp32 MatMul / Gemm on the GPU against the oracle and the reference's
+fixtures.  Bar: max|gpu - ref| <= 1e-3 * rms(ref); the reference's own fixture
+rule (2e-5 relative to max |ref|) is also checked on its fixtures."""
+import numpy as np
+import pytest
+
+import golden_io as G
+import oracle
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from onnx_runtime_dart_amd import ops as _ops
+    return _ops
+
+
+@pytest.mark.parametrize("name", ["matmul_batched", "gemm_transB_bias", "einsum_matmul"])
+def test_fixture(ops, name):
+    d = G.load(name)
+    x, at = d["arrays"], d["attrs"]
+    if d["op_type"] == "Gemm":
+        y = ops.op_gemm(x[0], x[1], x[2] if len(x) > 2 else None, alpha=at.get("alpha", 1.0),
+                        beta=at.get("beta", 1.0), trans_a=bool(at.get("transA", 0)),
+                        trans_b=bool(at.get("transB", 0)))
+    else:
+        y = ops.op_matmul(x[0], x[1])
+    G.assert_reference_parity(y, d["want"][d["outputs"][0]], name)
+
+
+def test_known_answers(ops):
+    w = np.arange(1, 13, dtype=np.float32).reshape(4, 3)
+    c = np.array([10, 20, 30, 40], dtype=np.float32)
+    x = np.array([[1, 2, 3], [4, 5, 6]], dtype=np.float32)
+    want = [24, 52, 80, 108, 42, 97, 152, 207]  # test/gemm_prepack_test.dart:48
+    assert ops.op_gemm(x, w, c, trans_b=True).ravel().tolist() == want
+    fw = ops.F32Weight(w, trans_b=True)  # prepacked once, stable on reuse
+    assert fw.gemm(x, c).ravel().tolist() == want
+    assert fw.gemm(x, c).ravel().tolist() == want
+    fw.release()
+    xi = np.array([[5, 6], [7, 8]], dtype=np.float32)  # onnx_runtime_dart_test.dart:48-70
+    assert ops.op_matmul(xi, np.eye(2, dtype=np.float32)).ravel().tolist() == [5, 6, 7, 8]
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 384, 384), (33, 65, 17), (7, 128, 5), (128, 64, 128),
+                                   (5, 1, 9), (64, 384, 1), (1, 40, 151), (1, 896, 512),
+                                   (300, 200, 100)])
+def test_kernel_shapes(ops, m, k, n):
+    # Shape list of test/gemm_kernel_test.dart:62-80.
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    y = ops.op_matmul(a, b)
+    assert G.rms_error(y, oracle.matmul_f32(a, b)) <= TOL
+    assert np.abs(y - a.astype(np.float64) @ b).max() < 1e-3
+
+
+@pytest.mark.parametrize("sa,sb", [((2, 3, 5, 7), (2, 3, 7, 4)), ((3, 1, 4, 6), (2, 6, 5)),
+                                   ((4, 2, 8), (8, 3)), ((2, 8), (5, 8, 3)),
+                                   ((1, 3, 2), (4, 1, 2, 5))])
+def test_broadcast(ops, sa, sb):
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    y = ops.op_matmul(a, b)
+    ref = oracle.matmul_f32(a, b)
+    assert y.shape == ref.shape
+    assert G.rms_error(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("c_shape", [None, (7,), (1, 7), (5, 1), (5, 7), ()])
+def test_gemm_attributes(ops, ta, tb, c_shape):
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((6, 5) if ta else (5, 6)).astype(np.float32)
+    b = rng.standard_normal((7, 6) if tb else (6, 7)).astype(np.float32)
+    c = None if c_shape is None else rng.standard_normal(c_shape).astype(np.float32)
+    y = ops.op_gemm(a, b, c, alpha=0.5, beta=2.0, trans_a=ta, trans_b=tb)
+    ref = oracle.gemm_f32(a, b, c, alpha=0.5, beta=2.0, trans_a=ta, trans_b=tb)
+    assert G.rms_error(y, ref) <= TOL
+
+
+def test_bert_layer_shapes(ops):
+    # Config C3 (MiniLM-L6): Gemm transB=1 + bias at hidden 384 / FFN 1536,
+    # checked on 512 of the 4096 token rows; batched attention products.
+    rng = np.random.default_rng(0x5EED0002)
+    for n, k in [(384, 384), (1536, 384), (384, 1536)]:
+        x = rng.standard_normal((512, k)).astype(np.float32)
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        c = (rng.standard_normal(n) * 0.02).astype(np.float32)
+        fw = ops.F32Weight(w, trans_b=True)
+        y = fw.gemm(x, c)
+        fw.release()
+        ref = oracle.gemm_f32(x, w, c, trans_b=True)
+        assert G.rms_error(y, ref) <= TOL
+    q = rng.standard_normal((4, 12, 128, 32)).astype(np.float32)
+    kt = rng.standard_normal((4, 12, 32, 128)).astype(np.float32)
+    s = ops.op_matmul(q, kt)
+    assert G.rms_error(s, oracle.matmul_f32(q, kt)) <= TOL
+    p = rng.random((4, 12, 128, 128)).astype(np.float32)
+    v = rng.standard_normal((4, 12, 128, 32)).astype(np.float32)
+    assert G.rms_error(ops.op_matmul(p, v), oracle.matmul_f32(p, v)) <= TOL

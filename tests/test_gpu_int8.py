@@ -1,0 +1,148 @@
+"""MatMulInteger / QLinearMatMul / DynamicQuantizeLinear on the GPU: bit-exact
+against the oracle, the reference's fixtures and its known answers."""
+import numpy as np
+import pytest
+
+import golden_io as G
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from onnx_runtime_dart_amd import ops as _ops
+    return _ops
+
+
+@pytest.mark.parametrize("name", G.names("matmulinteger") + ["qlinearmatmul",
+                                                              "dynamicquantizelinear"])
+def test_fixture(ops, name):
+    d = G.load(name)
+    x = d["arrays"]
+    if d["op_type"] == "MatMulInteger":
+        y = ops.op_matmul_integer(x[0], x[1], x[2] if len(x) > 2 else None,
+                                  x[3] if len(x) > 3 else None)
+        G.assert_reference_parity(y, d["want"][d["outputs"][0]], name)
+    elif d["op_type"] == "QLinearMatMul":
+        a, as_, az, b, bs, bz, ys, yz = x
+        lo, hi = (-128, 127) if yz is not None and yz.dtype == np.int8 else (0, 255)
+        y = ops.op_qlinear_matmul(a, as_, az, b, bs, bz, ys, yz, lo=lo, hi=hi)
+        G.assert_reference_parity(y, d["want"][d["outputs"][0]], name)
+    else:
+        y, s, z = ops.op_dynamic_quantize_linear(x[0])
+        o = d["outputs"]
+        G.assert_reference_parity(y.astype(np.int64), d["want"][o[0]], name)
+        G.assert_reference_parity(np.array(s, np.float32), d["want"][o[1]], name)
+        assert z == int(d["want"][o[2]])
+
+
+def test_known_answer(ops):
+    # test/compact_tensor_test.dart:48-57
+    a = np.array([[10, 130, 250]], dtype=np.uint8)
+    b = np.array([[-1, 2], [3, -4], [5, 6]], dtype=np.int8)
+    assert ops.op_matmul_integer(a, b, np.array(10), np.array(1)).ravel().tolist() == [1200, 600]
+
+
+SHAPES = [(1, 1, 1), (4, 6, 5), (17, 65, 33), (64, 128, 64), (33, 200, 47), (128, 1024, 1024)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+@pytest.mark.parametrize("signs", [(False, True), (False, False), (True, True), (True, False)])
+@pytest.mark.parametrize("zp_mode", ["none", "scalar", "vector"])
+def test_matmul_integer_exact(ops, m, k, n, signs, zp_mode):
+    rng = np.random.default_rng(m * 131 + k * 7 + n)
+    sa, sb = signs
+    a = rng.integers(-128 if sa else 0, 128 if sa else 256, (m, k)).astype(np.int8 if sa else np.uint8)
+    b = rng.integers(-128 if sb else 0, 128 if sb else 256, (k, n)).astype(np.int8 if sb else np.uint8)
+    if zp_mode == "none":
+        az = bz = None
+    elif zp_mode == "scalar":
+        az, bz = np.array(rng.integers(0, 200)), np.array(rng.integers(-20, 20))
+    else:
+        az = rng.integers(0, 255, m) if m > 1 else np.array(rng.integers(0, 255))
+        bz = rng.integers(-100, 100, n) if n > 1 else np.array(3)
+    y = ops.op_matmul_integer(a, b, az, bz)
+    np.testing.assert_array_equal(y, oracle.matmul_integer(a, b, az, bz))
+    w = ops.Int8Weight(b, bz)
+    np.testing.assert_array_equal(w.matmul_integer(a, az), oracle.matmul_integer(a, b, az, bz))
+    w.release()
+
+
+@pytest.mark.parametrize("ab,bb", [(3, 3), (3, 1), (1, 2)])
+def test_matmul_integer_batched(ops, ab, bb):
+    rng = np.random.default_rng(ab * 10 + bb)
+    a = rng.integers(0, 256, (ab, 9, 70)).astype(np.uint8)
+    b = rng.integers(-128, 128, (bb, 70, 21)).astype(np.int8)
+    az = rng.integers(0, 255, 9)
+    y = ops.op_matmul_integer(a, b, az, np.array(-3))
+    np.testing.assert_array_equal(y, oracle.matmul_integer(a, b, az, np.array(-3)))
+
+
+@pytest.mark.parametrize("signed_out", [False, True])
+@pytest.mark.parametrize("y_scale", [0.05, 0.5, 8.0])
+def test_qlinear_exact(ops, signed_out, y_scale):
+    rng = np.random.default_rng(11)
+    a = rng.integers(0, 256, (37, 300)).astype(np.uint8)
+    b = rng.integers(-127, 128, (300, 45)).astype(np.int8)
+    lo, hi = (-128, 127) if signed_out else (0, 255)
+    yz = 5 if signed_out else 128
+    args = (a, np.float32(0.0123), np.array(118), b, np.float32(2 ** -10), np.array(0),
+            np.float32(y_scale), np.array(yz))
+    y = ops.op_qlinear_matmul(*args, lo=lo, hi=hi)
+    ref = oracle.qlinear_matmul(*args, lo=lo, hi=hi)
+    np.testing.assert_array_equal(y, ref)
+    w = ops.Int8Weight(b, np.array(0))
+    y2 = w.qlinear_matmul(a, 0.0123, np.array(118), 2 ** -10, y_scale, yz, lo=lo, hi=hi)
+    np.testing.assert_array_equal(y2, ref)
+    w.release()
+
+
+def test_config_dql_matmulinteger_qlinear_chain(ops):
+    # Config C2: fp32 [128,1024] -> DQL -> MatMulInteger / QLinearMatMul with
+    # B int8 [1024,1024] U[-127,127], zp 0; requant scale 0.05, zp 128.
+    rng = np.random.default_rng(0x5EED0001)
+    x = rng.standard_normal((128, 1024)).astype(np.float32)
+    b = rng.integers(-127, 128, (1024, 1024)).astype(np.int8)
+    q, s, z = ops.op_dynamic_quantize_linear(x)
+    q2, s2, z2 = oracle.dynamic_quantize_linear(x)
+    assert s == s2 and z == z2
+    np.testing.assert_array_equal(q, q2)
+    acc = ops.op_matmul_integer(q, b, np.array(z), np.array(0))
+    np.testing.assert_array_equal(acc, oracle.matmul_integer(q2, b, np.array(z2), np.array(0)))
+    for b_scale in (2.0 ** -10, 2.0 ** -6):  # unsaturated and saturating
+        args = (q, s, np.array(z), b, np.float32(b_scale), np.array(0), np.float32(0.05),
+                np.array(128, np.uint8))
+        y = ops.op_qlinear_matmul(*args, lo=0, hi=255)
+        np.testing.assert_array_equal(y, oracle.qlinear_matmul(*args, lo=0, hi=255))
+
+
+@pytest.mark.parametrize("shape,shift", [((7,), 0.0), ((128, 1024), 0.0), ((33, 5), -3.0),
+                                         ((100000,), 2.0), ((3, 4), 0.5)])
+def test_dql_exact(ops, shape, shift):
+    rng = np.random.default_rng(17)
+    x = (rng.standard_normal(shape) + shift).astype(np.float32)
+    y, s, z = ops.op_dynamic_quantize_linear(x)
+    y2, s2, z2 = oracle.dynamic_quantize_linear(x)
+    assert s == s2 and z == z2
+    np.testing.assert_array_equal(y, y2)
+
+
+def test_dql_edge_cases(ops):
+    from onnx_runtime_dart_amd.errors import UnsupportedError
+    y, s, z = ops.op_dynamic_quantize_linear(np.zeros(10, np.float32))
+    assert s == 0 and z == 0 and not y.any()
+    with pytest.raises(UnsupportedError):
+        ops.op_dynamic_quantize_linear(np.array([1.0, np.inf], np.float32))
+
+
+def test_errors(ops):
+    from onnx_runtime_dart_amd.errors import ArgumentError, UnsupportedError
+    a = np.zeros((4, 3), np.uint8)
+    b = np.zeros((3, 2), np.int8)
+    with pytest.raises(UnsupportedError):
+        ops.op_matmul_integer(a, b, np.zeros(3, np.int32), None)
+    with pytest.raises(ArgumentError):
+        ops.op_matmul_integer(a, np.zeros((4, 2), np.int8))
+    with pytest.raises(ArgumentError):
+        ops.op_matmul_integer(np.zeros((2, 4, 3), np.uint8), np.zeros((3, 3, 2), np.int8))

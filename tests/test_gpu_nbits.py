@@ -1,0 +1,209 @@
+"""MatMulNBits on the GPU against the oracle and the reference's fixtures.
+
+Bar (stated by the task for the int4 path): max|gpu - ref| <= 1e-3 * rms(ref).
+Full-size shapes are checked on column subsets: each output column depends
+only on its own packed weights, so slicing B/scales/zero points/bias by
+columns gives a smaller weight whose outputs must equal those columns of the
+full run.
+"""
+import numpy as np
+import pytest
+
+import golden_io as G
+import oracle
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from onnx_runtime_dart_amd import ops as _ops
+    return _ops
+
+
+def make_nbits(rng, n, k, bs, zp_mode, scale_lo=0.005, scale_hi=0.05):
+    nb = (k + bs - 1) // bs
+    b = rng.integers(0, 256, (n, nb, bs // 2), dtype=np.uint8)
+    s = rng.uniform(scale_lo, scale_hi, (n, nb)).astype(np.float32)
+    if zp_mode == "packed":
+        zp = rng.integers(0, 256, (n, (nb + 1) // 2), dtype=np.uint8)
+    elif zp_mode == "float":
+        zp = (rng.standard_normal((n, nb)) + 8).astype(np.float32)
+    else:
+        zp = None
+    return b, s, zp
+
+
+def slice_cols(b, s, zp, bias, cols):
+    return (b[cols], s[cols], None if zp is None else zp[cols],
+            None if bias is None else bias[cols])
+
+
+@pytest.mark.parametrize("name", G.names("matmulnbits"))
+def test_fixture(ops, name):
+    d = G.load(name)
+    x, at = d["arrays"], d["attrs"]
+    zp = x[3] if len(x) > 3 else None
+    bias = x[5] if len(x) > 5 else None
+    y = ops.op_matmul_nbits(x[0], x[1], x[2], zp, k=at["K"], n=at["N"],
+                            bits=at.get("bits", 4), block_size=at["block_size"], bias=bias)
+    want = d["want"][d["outputs"][0]]
+    assert y.shape == want.shape
+    assert G.rms_error(y, want) <= TOL, G.rms_error(y, want)
+
+
+CASES = [
+    # (M, K, N, bs, zp, bias)
+    (1, 64, 8, 32, "none", False),
+    (1, 1024, 3072, 32, "packed", True),
+    (2, 300, 130, 64, "packed", True),
+    (3, 35, 5, 16, "float", True),
+    (4, 2048, 512, 32, "packed", False),
+    (4, 1000, 70, 128, "float", False),
+    (5, 256, 64, 32, "none", True),
+    (8, 1024, 3072, 32, "packed", False),   # config C1
+    (16, 2048, 640, 32, "packed", True),
+    (33, 1024, 200, 128, "packed", True),
+    (64, 512, 128, 256, "none", False),
+    (65, 384, 96, 64, "packed", False),
+    (128, 1024, 1000, 128, "packed", True),
+    (9, 35, 5, 16, "packed", True),          # generic path (bs 16)
+    (12, 100, 33, 32, "float", False),       # generic path (float zp)
+]
+
+
+@pytest.mark.parametrize("m,k,n,bs,zp_mode,with_bias", CASES)
+def test_against_oracle(ops, m, k, n, bs, zp_mode, with_bias):
+    rng = np.random.default_rng(0x5EED0000 + m * 7919 + k * 31 + n)
+    b, s, zp = make_nbits(rng, n, k, bs, zp_mode)
+    bias = rng.standard_normal(n).astype(np.float32) if with_bias else None
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    y = w(a)
+    ref = oracle.matmul_nbits(a, b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    assert G.rms_error(y, ref) <= TOL, G.rms_error(y, ref)
+    # Deterministic: a second call gives identical bits.
+    np.testing.assert_array_equal(w(a), y)
+    w.release()
+
+
+def test_leading_dims_and_empty(ops):
+    rng = np.random.default_rng(3)
+    k, n, bs = 128, 40, 32
+    b, s, zp = make_nbits(rng, n, k, bs, "packed")
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs)
+    a = rng.standard_normal((2, 3, k)).astype(np.float32)
+    y = w(a)
+    assert y.shape == (2, 3, n)
+    ref = oracle.matmul_nbits(a.reshape(6, k), b, s, zp, k=k, n=n, block_size=bs)
+    assert G.rms_error(y.reshape(6, n), ref) <= TOL
+    assert w(np.zeros((0, k), np.float32)).shape == (0, n)
+    w.release()
+
+
+def test_outlier_rows_and_zero_rows(ops):
+    # Per-row scaling must keep tiny, huge and all-zero rows accurate.
+    rng = np.random.default_rng(4)
+    k, n, bs = 512, 96, 128
+    b, s, zp = make_nbits(rng, n, k, bs, "packed")
+    for m in (3, 40):
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        a[0] *= 1e-30
+        a[1] *= 1e4
+        a[2] = 0
+        a[-1, 7] = 3e3  # one outlier element in a row
+        w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs)
+        y = w(a)
+        ref = oracle.matmul_nbits(a, b, s, zp, k=k, n=n, block_size=bs)
+        for r in range(m):
+            if np.any(ref[r]):
+                assert G.rms_error(y[r], ref[r]) <= TOL, (m, r)
+            else:
+                assert not np.any(y[r])
+        w.release()
+
+
+QWEN = [  # (name, K, N): Qwen3-0.6B projections, block 128 with zero points
+    ("q", 1024, 2048), ("k", 1024, 1024), ("o", 2048, 1024), ("gate", 1024, 3072),
+    ("down", 3072, 1024), ("lm_head", 1024, 151936)]
+
+
+@pytest.mark.parametrize("proj,k,n", QWEN)
+@pytest.mark.parametrize("m", [1, 512])
+def test_qwen_shapes_column_subset(ops, proj, k, n, m):
+    rng = np.random.default_rng(0x5EED0003)
+    bs = 128
+    b, s, zp = make_nbits(rng, n, k, bs, "packed", 0.002, 0.02)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs)
+    y = w(a)
+    w.release()
+    cols = np.unique(np.concatenate([np.arange(min(n, 64)), np.arange(n - 64, n),
+                                     rng.integers(0, n, 128)]))
+    bb, ss, zz, _ = slice_cols(b, s, zp, None, cols)
+    rows = np.arange(m) if m <= 64 else np.unique(np.concatenate(
+        [np.arange(16), np.arange(m - 16, m), rng.integers(0, m, 32)]))
+    ref = oracle.matmul_nbits(a[rows], bb, ss, zz, k=k, n=len(cols), block_size=bs)
+    got = y[np.ix_(rows, cols)]
+    assert G.rms_error(got, ref) <= TOL, G.rms_error(got, ref)
+
+
+LLAMA = [("q", 2048, 2048), ("k", 2048, 512), ("up", 2048, 8192), ("down", 8192, 2048),
+         ("lm_head", 2048, 128256)]
+
+
+@pytest.mark.parametrize("proj,k,n", LLAMA)
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_llama_decode_column_subset(ops, proj, k, n, m):
+    rng = np.random.default_rng(0x5EED0004)
+    bs = 32
+    b, s, zp = make_nbits(rng, n, k, bs, "packed", 0.002, 0.02)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs)
+    y = w(a)
+    w.release()
+    cols = np.unique(np.concatenate([np.arange(64), np.arange(n - 64, n),
+                                     rng.integers(0, n, 128)]))
+    bb, ss, zz, _ = slice_cols(b, s, zp, None, cols)
+    ref = oracle.matmul_nbits(a, bb, ss, zz, k=k, n=len(cols), block_size=bs)
+    assert G.rms_error(y[:, cols], ref) <= TOL
+
+
+def test_weight_validation_errors(ops):
+    from onnx_runtime_dart_amd.errors import ArgumentError, UnsupportedError
+    b = np.zeros((4, 2, 16), np.uint8)
+    s = np.zeros(8, np.float32)
+    with pytest.raises(ArgumentError):  # wrong packed shape
+        ops.NBitsWeight(np.zeros((4, 3, 16), np.uint8), s, k=64, n=4, block_size=32)
+    with pytest.raises(ArgumentError):  # scales length
+        ops.NBitsWeight(b, np.zeros(7, np.float32), k=64, n=4, block_size=32)
+    with pytest.raises(ArgumentError):  # zero points length (ceil(nb/2) per column)
+        ops.NBitsWeight(b, s, np.zeros(5, np.uint8), k=64, n=4, block_size=32)
+    with pytest.raises(ArgumentError):  # bias shape
+        ops.NBitsWeight(b, s, k=64, n=4, block_size=32, bias=np.zeros(3, np.float32))
+    with pytest.raises(UnsupportedError):  # g_idx (onnx_graph.dart:2919-2921)
+        ops.NBitsWeight(b, s, k=64, n=4, block_size=32, has_g_idx=True)
+
+
+def test_control_cancel_and_budget(ops):
+    from onnx_runtime_dart_amd.errors import OnnxCancelledException, OnnxMemoryLimitException
+    ctx = ops.Context(0)
+    rng = np.random.default_rng(5)
+    b, s, zp = make_nbits(rng, 64, 256, 32, "packed")
+    w = ops.NBitsWeight(b, s, zp, k=256, n=64, block_size=32, ctx=ctx)
+    a = rng.standard_normal((40, 256)).astype(np.float32)
+    flag = np.zeros(1, np.int32)
+    ctx.set_control(flag, max_bytes=-1)
+    w(a)
+    flag[0] = 1
+    with pytest.raises(OnnxCancelledException):
+        w(a)
+    ctx.set_control(None, max_bytes=16)
+    with pytest.raises(OnnxMemoryLimitException):
+        w(a)
+    ctx.set_control(None, max_bytes=-1)
+    ref = oracle.matmul_nbits(a, b, s, zp, k=256, n=64, block_size=32)
+    assert G.rms_error(w(a), ref) <= TOL
+    w.release()
+    ctx.close()

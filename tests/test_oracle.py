@@ -1,0 +1,343 @@
+"""Pins the CPU oracle before anything is compared against it.
+
+Three independent anchors, per op:
+  * the reference's ORT golden fixtures (test/fixtures/*, re-encoded under
+    tests/golden/fixtures) with the reference's own comparison rule;
+  * the reference's known-answer tests (gemm_prepack_test.dart:48,
+    compact_tensor_test.dart:48-57, onnx_runtime_dart_test.dart:48-70);
+  * closed forms written independently here in numpy (f64 products, integer
+    brute force, the f32 rounding chains), on seeded random inputs that hit
+    the edge cases the reference handles (partial blocks, odd block counts,
+    float zero points, bias, per-row/per-column zero points, batching,
+    saturation, m<4 scalar tails).
+"""
+import numpy as np
+import pytest
+
+import golden_io as G
+import oracle
+
+# ----------------------------------------------------------------- fixtures
+
+
+def _run_fixture(d):
+    op = d["op_type"]
+    x = d["arrays"]
+    at = d["attrs"]
+    if op == "MatMulNBits":
+        a, b, s = x[0], x[1], x[2]
+        zp = x[3] if len(x) > 3 else None
+        bias = x[5] if len(x) > 5 else None
+        return {d["outputs"][0]: oracle.matmul_nbits(
+            a, b, s, zp, k=at["K"], n=at["N"], bits=at.get("bits", 4),
+            block_size=at["block_size"], bias=bias)}
+    if op == "MatMulInteger":
+        a, b = x[0], x[1]
+        az = x[2] if len(x) > 2 else None
+        bz = x[3] if len(x) > 3 else None
+        return {d["outputs"][0]: oracle.matmul_integer(a, b, az, bz)}
+    if op == "QLinearMatMul":
+        a, as_, az, b, bs, bz, ys, yz = x
+        signed = yz is not None and yz.dtype == np.int8
+        lo, hi = (-128, 127) if signed else (0, 255)
+        return {d["outputs"][0]: oracle.qlinear_matmul(
+            a, as_, az, b, bs, bz, ys, yz, lo=lo, hi=hi)}
+    if op == "DynamicQuantizeLinear":
+        y, s, z = oracle.dynamic_quantize_linear(x[0])
+        o = d["outputs"]
+        return {o[0]: y, o[1]: np.array(s, dtype=np.float32),
+                o[2]: np.array(z, dtype=np.int64)}
+    if op == "MatMul" or (op == "Einsum" and at["equation"] == "ij,jk->ik"):
+        return {d["outputs"][0]: oracle.matmul_f32(x[0], x[1])}
+    if op == "Gemm":
+        return {d["outputs"][0]: oracle.gemm_f32(
+            x[0], x[1], x[2] if len(x) > 2 else None,
+            alpha=at.get("alpha", 1.0), beta=at.get("beta", 1.0),
+            trans_a=bool(at.get("transA", 0)), trans_b=bool(at.get("transB", 0)))}
+    raise AssertionError(op)
+
+
+@pytest.mark.parametrize("name", G.names())
+def test_oracle_matches_reference_fixture(name):
+    d = G.load(name)
+    got = _run_fixture(d)
+    for out, want in d["want"].items():
+        G.assert_reference_parity(got[out], want, f"{name}/{out}")
+
+
+# ------------------------------------------------------------ known answers
+
+
+def test_gemm_transb_known_answer():
+    # test/gemm_prepack_test.dart:14-57
+    w = np.arange(1, 13, dtype=np.float32).reshape(4, 3)
+    c = np.array([10, 20, 30, 40], dtype=np.float32)
+    x = np.array([[1, 2, 3], [4, 5, 6]], dtype=np.float32)
+    y = oracle.gemm_f32(x, w, c, trans_b=True)
+    assert y.ravel().tolist() == [24, 52, 80, 108, 42, 97, 152, 207]
+
+
+def test_matmul_integer_known_answer():
+    # test/compact_tensor_test.dart:48-57
+    a = np.array([[10, 130, 250]], dtype=np.uint8)
+    b = np.array([[-1, 2], [3, -4], [5, 6]], dtype=np.int8)
+    y = oracle.matmul_integer(a, b, np.array(10), np.array(1))
+    assert y.ravel().tolist() == [1200, 600]
+
+
+def test_matmul_identity_known_answer():
+    # test/onnx_runtime_dart_test.dart:48-70
+    x = np.array([[5, 6], [7, 8]], dtype=np.float32)
+    y = oracle.matmul_f32(x, np.eye(2, dtype=np.float32))
+    assert y.ravel().tolist() == [5, 6, 7, 8]
+
+
+def test_round_even_ties():
+    assert [oracle.round_even(v) for v in (0.5, 1.5, 2.5, -0.5, -1.5, 2.4, 2.6)] \
+        == [0, 2, 2, 0, -2, 2, 3]
+    with pytest.raises(oracle.OracleError):
+        oracle.round_even(float("nan"))
+
+
+# --------------------------------------------------------------- fp32 GEMM
+
+
+def _seq_f32(a, b):
+    """Sequential k-order f32 mul-then-add per element (the Float32x4 lane
+    arithmetic), vectorised over outputs with numpy float32."""
+    m, k = a.shape
+    out = np.zeros((m, b.shape[1]), dtype=np.float32)
+    for kk in range(k):
+        prod = (a[:, kk:kk + 1] * b[kk:kk + 1, :]).astype(np.float32)
+        out = (out + prod).astype(np.float32)
+    return out
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 384, 384), (33, 65, 17), (7, 128, 5),
+                                   (128, 64, 128), (5, 1, 9), (64, 384, 1),
+                                   (1, 40, 151), (1, 128, 19), (1, 896, 512),
+                                   (3, 50, 7), (2, 9, 4)])
+def test_kernel_matches_naive_and_rounding_chain(m, k, n):
+    # Shape list of test/gemm_kernel_test.dart:62-80 (+ m<4 tails).
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    y = oracle.matmul_kernel(a, b)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.abs(y - ref).max() < 1e-4
+    # Bitwise: f32 lanes are sequential mul-then-add; m<4 tail columns are
+    # double sums rounded once.
+    seq = _seq_f32(a, b)
+    f32_cols = n if m >= 4 else n & ~3
+    np.testing.assert_array_equal(y[:, :f32_cols], seq[:, :f32_cols])
+    np.testing.assert_array_equal(y[:, f32_cols:], ref[:, f32_cols:].astype(np.float32))
+
+
+def test_kernel_exhaustive_small():
+    # test/gemm_kernel_test.dart:45-60
+    rng = np.random.default_rng(3)
+    for m in range(1, 7):
+        for k in range(1, 7):
+            for n in range(1, 7):
+                a = rng.standard_normal((m, k)).astype(np.float32)
+                b = rng.standard_normal((k, n)).astype(np.float32)
+                y = oracle.matmul_kernel(a, b)
+                assert np.abs(y - a.astype(np.float64) @ b).max() < 1e-5
+
+
+def test_matmul_broadcast_batches():
+    rng = np.random.default_rng(5)
+    for sa, sb in [((2, 3, 5, 7), (2, 3, 7, 4)), ((3, 1, 4, 6), (2, 6, 5)),
+                   ((4, 2, 8), (8, 3)), ((2, 8), (5, 8, 3)), ((1, 3, 2), (4, 1, 2, 5))]:
+        a = rng.standard_normal(sa).astype(np.float32)
+        b = rng.standard_normal(sb).astype(np.float32)
+        y = oracle.matmul_f32(a, b)
+        ref = np.matmul(a.astype(np.float64), b.astype(np.float64))
+        assert y.shape == ref.shape
+        assert np.abs(y - ref).max() < 1e-4
+
+
+def test_gemm_attributes():
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((6, 5)).astype(np.float32)
+    b = rng.standard_normal((7, 6)).astype(np.float32)
+    for c_shape in [None, (7,), (1, 7), (5, 1), (5, 7), ()]:
+        c = None if c_shape is None else rng.standard_normal(c_shape).astype(np.float32)
+        y = oracle.gemm_f32(a, b, c, alpha=0.5, beta=2.0, trans_a=True, trans_b=True)
+        ref = 0.5 * (a.T.astype(np.float64) @ b.T.astype(np.float64))
+        if c is not None:
+            ref = ref + 2.0 * c.astype(np.float64)
+        assert np.abs(y - ref).max() < 1e-4
+
+
+# ------------------------------------------------------------- MatMulNBits
+
+
+def make_nbits(rng, n, k, bs, zp_mode):
+    nb = (k + bs - 1) // bs
+    b = rng.integers(0, 256, (n, nb, bs // 2), dtype=np.uint8)
+    s = rng.uniform(0.005, 0.05, (n, nb)).astype(np.float32)
+    if zp_mode == "packed":
+        zp = rng.integers(0, 256, (n, (nb + 1) // 2), dtype=np.uint8)
+    elif zp_mode == "float":
+        zp = (rng.standard_normal((n, nb)) + 8).astype(np.float32)
+    else:
+        zp = None
+    return b, s, zp
+
+
+def nbits_dequant_numpy(b, s, zp, n, k, bs):
+    """Independent closed form of the dequantised weight [N, K]."""
+    nb = (k + bs - 1) // bs
+    q = np.empty((n, nb, bs), dtype=np.int64)
+    q[:, :, 0::2] = b & 15
+    q[:, :, 1::2] = b >> 4
+    if zp is None:
+        z = np.full((n, nb), 8.0)
+    elif zp.dtype == np.uint8:
+        zz = np.empty((n, 2 * zp.shape[1]), dtype=np.int64)
+        zz[:, 0::2] = zp & 15
+        zz[:, 1::2] = zp >> 4
+        z = zz[:, :nb].astype(np.float64)
+    else:
+        z = zp.astype(np.float64).reshape(n, nb)
+    w = ((q - z[:, :, None]) * s.astype(np.float64).reshape(n, nb)[:, :, None])
+    return w.astype(np.float32).reshape(n, nb * bs)[:, :k]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 9])
+@pytest.mark.parametrize("k,bs", [(64, 32), (35, 16), (40, 32), (300, 64), (256, 128)])
+@pytest.mark.parametrize("zp_mode", ["none", "packed", "float"])
+def test_nbits_closed_form(m, k, bs, zp_mode):
+    rng = np.random.default_rng(1000 * m + k)
+    n = 37
+    b, s, zp = make_nbits(rng, n, k, bs, zp_mode)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    y = oracle.matmul_nbits(a, b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    w = nbits_dequant_numpy(b, s, zp, n, k, bs)
+    ref = a.astype(np.float64) @ w.T.astype(np.float64) + bias
+    assert G.rms_error(y, ref) < 1e-5
+    if m == 1:  # f64 accumulation, one rounding: matches to f32 rounding
+        np.testing.assert_allclose(y, ref.astype(np.float32), rtol=1e-6, atol=1e-6)
+
+
+def test_nbits_default_zero_point_is_eight():
+    # q == 8 everywhere with no zero points dequantises to exactly zero.
+    n, k, bs = 4, 64, 32
+    b = np.full((n, 2, 16), 0x88, dtype=np.uint8)
+    s = np.ones((n, 2), dtype=np.float32)
+    a = np.ones((2, k), dtype=np.float32)
+    y = oracle.matmul_nbits(a, b, s, None, k=k, n=n, block_size=bs)
+    assert not y.any()
+
+
+def test_nbits_rejects_bad_attributes():
+    a = np.zeros((1, 64), dtype=np.float32)
+    b = np.zeros((2, 2, 16), dtype=np.uint8)
+    s = np.zeros(4, dtype=np.float32)
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.matmul_nbits(a, b, s, None, k=64, n=2, bits=8, block_size=32)
+    assert e.value.status == oracle.UNSUPPORTED
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.matmul_nbits(a, b, s, None, k=64, n=2, block_size=24)
+    assert e.value.status == oracle.INVALID_ARGUMENT
+
+
+# ------------------------------------------------- MatMulInteger / QLinear
+
+
+@pytest.mark.parametrize("a_signed,b_signed", [(False, True), (False, False),
+                                               (True, True), (True, False)])
+def test_matmul_integer_brute_force(a_signed, b_signed):
+    rng = np.random.default_rng(7)
+    ta = np.int8 if a_signed else np.uint8
+    tb = np.int8 if b_signed else np.uint8
+    lo_a, hi_a = (-128, 128) if a_signed else (0, 256)
+    lo_b, hi_b = (-128, 128) if b_signed else (0, 256)
+    for batch_a, batch_b in [(1, 1), (3, 3), (3, 1), (1, 2)]:
+        m, k, n = 5, 17, 6
+        a = rng.integers(lo_a, hi_a, (batch_a, m, k)).astype(ta)
+        b = rng.integers(lo_b, hi_b, (batch_b, k, n)).astype(tb)
+        for az, bz in [(None, None), (np.array(3), np.array(-2)),
+                       (rng.integers(0, 20, m), rng.integers(-5, 5, n))]:
+            y = oracle.matmul_integer(a, b, az, bz)
+            A = a.astype(np.int64) - (0 if az is None else az.astype(np.int64).reshape(-1, 1))
+            B = b.astype(np.int64) - (0 if bz is None else bz.astype(np.int64).reshape(1, -1))
+            np.testing.assert_array_equal(y.reshape(-1, m, n), np.matmul(A, B).reshape(-1, m, n))
+
+
+def test_matmul_integer_rejects_bad_zero_point():
+    a = np.zeros((4, 3), dtype=np.uint8)
+    b = np.zeros((3, 2), dtype=np.int8)
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.matmul_integer(a, b, np.zeros(3, dtype=np.int32), None)
+    assert e.value.status == oracle.UNSUPPORTED
+
+
+def _qlinear_numpy(acc, a_s, b_s, y_s, yz, lo, hi):
+    ab = np.float32(np.float64(np.float32(a_s)) * np.float64(np.float32(b_s)))
+    mult = np.float32(np.float64(ab) / np.float64(np.float32(y_s)))
+    p = (acc.astype(np.float64) * np.float64(mult)).astype(np.float32)
+    q = np.rint(p.astype(np.float64)).astype(np.int64) + yz  # rint: ties to even
+    return np.clip(q, lo, hi)
+
+
+@pytest.mark.parametrize("signed_out", [False, True])
+def test_qlinear_closed_form(signed_out):
+    rng = np.random.default_rng(9)
+    a = rng.integers(0, 256, (2, 8, 40)).astype(np.uint8)
+    b = rng.integers(-127, 128, (40, 9)).astype(np.int8)
+    az, bz = np.array(118), np.array(0)
+    lo, hi = (-128, 127) if signed_out else (0, 255)
+    yz = 3 if signed_out else 128
+    for ys in (0.05, 0.5, 5.0):  # saturating and unsaturated
+        y = oracle.qlinear_matmul(a, 0.0123, az, b, 2.0 ** -10, bz, ys, np.array(yz),
+                                  lo=lo, hi=hi)
+        acc = oracle.matmul_integer(a, b, az, bz)
+        np.testing.assert_array_equal(y, _qlinear_numpy(acc, 0.0123, 2.0 ** -10, ys,
+                                                        yz, lo, hi))
+
+
+def test_qlinear_tie_rounds_to_even():
+    # acc * mult lands exactly on .5: 3 * 0.5 = 1.5 -> 2, 5 * 0.5 = 2.5 -> 2.
+    a = np.array([[3, 5]], dtype=np.uint8)
+    b = np.array([[1, 0], [0, 1]], dtype=np.uint8)
+    y = oracle.qlinear_matmul(a, 1.0, None, b, 0.5, None, 1.0, np.array(0),
+                              lo=0, hi=255)
+    assert y.ravel().tolist() == [2, 2]
+
+
+# ----------------------------------------------------- DynamicQuantizeLinear
+
+
+def _dql_numpy(x):
+    x64 = x.astype(np.float64)
+    mn = min(0.0, float(x64.min()))
+    mx = max(0.0, float(x64.max()))
+    scale = np.float32((mx - mn) / 255.0)
+    if scale == 0:
+        return np.full(x.shape, 0, np.uint8), scale, 0
+    zpf = np.float32(-mn / np.float64(scale))
+    zp = int(np.rint(np.clip(np.float64(zpf), 0, 255)))
+    r = (x64 / np.float64(scale)).astype(np.float32)
+    q = np.rint(r.astype(np.float64)).astype(np.int64) + zp
+    return np.clip(q, 0, 255).astype(np.uint8), scale, zp
+
+
+@pytest.mark.parametrize("shape,shift", [((128, 1024), 0.0), ((7,), 3.0),
+                                         ((33, 5), -2.0), ((1000,), 0.5)])
+def test_dql_closed_form(shape, shift):
+    rng = np.random.default_rng(13)
+    x = (rng.standard_normal(shape) + shift).astype(np.float32)
+    y, s, z = oracle.dynamic_quantize_linear(x)
+    y2, s2, z2 = _dql_numpy(x)
+    assert s == s2 and z == z2
+    np.testing.assert_array_equal(y, y2)
+
+
+def test_dql_zero_input_and_nonfinite():
+    y, s, z = oracle.dynamic_quantize_linear(np.zeros(5, np.float32))
+    assert s == 0 and z == 0 and not y.any()
+    with pytest.raises(oracle.OracleError):
+        oracle.dynamic_quantize_linear(np.array([1.0, np.nan], np.float32))
