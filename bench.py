@@ -52,7 +52,7 @@ def make_weight(rng, k, n, bs=BLOCK):
     return b, s, zp
 
 
-def cpu_baseline(weights, rng, budget_s=20.0):
+def cpu_baseline(weights, rng, budget_s=30.0):
     """Times the oracle (reference algorithm: 32-column dequantised tiles +
     4x16 f32 GEMM, one thread) at M = 512 on a bounded sample: projections in
     order, the lm_head on its first columns, until ~budget_s of CPU work."""
@@ -63,7 +63,7 @@ def cpu_baseline(weights, rng, budget_s=20.0):
     t_total = 0.0
     parts = []
     for (name, k, n), (b, s, zp) in zip(QWEN3_PROJ, weights):
-        cols = n if name != "lm_head" else 4096
+        cols = n if name != "lm_head" else 65536
         a = rng.standard_normal((M_PREFILL, k)).astype(np.float32)
         bb, ss, zz = b[:cols], s[:cols], zp[:cols]
         t0 = time.perf_counter()
@@ -85,6 +85,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["lm512", "lm1", "copy"], default=None,
+                    help="profiling mode: launch one workload --steps times and exit "
+                         "(lm512: lm_head M=512, lm1: lm_head M=1, copy: 256 MiB device "
+                         "copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -102,8 +106,31 @@ def main():
     ctx = ops.Context(0)
     ctx.set_stream(stream.cuda_stream)
 
+    if args.only == "copy":
+        src = torch.empty(64 << 20, device=dev, dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        with torch.cuda.stream(stream):
+            for _ in range(args.steps):
+                dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy: {args.steps} x {src.numel() * 4} bytes read and written", flush=True)
+        return
     rng = np.random.default_rng(0x5EED0003)
     t0 = time.perf_counter()
+    if args.only in ("lm512", "lm1"):
+        m = M_PREFILL if args.only == "lm512" else 1
+        _, k, n = QWEN3_PROJ[-1]
+        b, s, zp = make_weight(rng, k, n)
+        w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=BLOCK, ctx=ctx)
+        a = torch.randn((m, k), device=dev, dtype=torch.float32)
+        y = torch.empty((m, n), device=dev, dtype=torch.float32)
+        with torch.cuda.stream(stream):
+            for _ in range(args.steps):
+                w.run_dev(a.data_ptr(), m, y.data_ptr())
+        torch.cuda.synchronize()
+        print(f"{args.only}: {args.steps} launches of lm_head M={m} K={k} N={n}", flush=True)
+        w.release()
+        return
     host_w = [make_weight(rng, k, n) for _, k, n in QWEN3_PROJ]
     weights = [ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=BLOCK, ctx=ctx)
                for (_, k, n), (b, s, zp) in zip(QWEN3_PROJ, host_w)]
