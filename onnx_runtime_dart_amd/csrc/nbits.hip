@@ -20,11 +20,11 @@
 //     lane owns one column and streams 16-byte weight loads, multiplying with
 //     v_dot8_i32_i4 against the digit planes (wave-uniform, scalar-loaded).
 //     Zero point and scale are applied once per block in fp32.
-//   * M > 4 ("prefill"): activations become an fp16 pair hi + lo (per-row
-//     power-of-two scaled, so hi + lo carries ~22 bits); weights are unpacked
-//     in registers to exact fp16 (q - zp); v_mfma_f32_16x16x32_f16 accumulates
-//     hi*W and lo*W per block in fp32, then the block scale is applied on the
-//     fp32 accumulator.
+//   * M > 4 ("prefill"): activations become an fp16 pair hi + lo (scaled by a
+//     power of two per row and 128-k slice, so hi + lo carries ~22 bits of each
+//     element); each workgroup unpacks its weight tile once into LDS as exact
+//     fp16 (q - zp); v_mfma_f32_16x16x32_f16 accumulates hi*W and lo*W in fp32
+//     and the block scale is applied on the fp32 accumulator.
 // Rare forms (float zero points or block_size 16 with M > 4) take a simple
 // per-output kernel.
 #include <hip/hip_runtime.h>
@@ -118,56 +118,59 @@ __global__ __launch_bounds__(256) void k_adigits(
 }
 
 // Activations -> fp16 hi/lo fragments for the MFMA path.  One workgroup per
-// 16-row subtile.  ahl[m16][kg][j][hl][lane] (uint4 = 8 fp16): lane
-// (r = lane%16, g = lane/16) holds rows r, k = kg*128 + 32*j + 8*g + 0..7.
-// Each row is scaled by 2^e so that its max magnitude lies in [2^13, 2^14);
-// rowexp[row] = e is undone on the fp32 result.
+// (16-row subtile, k group): 256 threads, thread t owns row t/16 and the 8
+// consecutive k at 8*(t%16) of the group.  Output ahl[m16][kg][j][hl][lane]
+// (uint4 = 8 fp16): MFMA lane (r = lane%16, g = lane/16) holds row r,
+// k = kg*128 + 32*j + 8*g + 0..7.  Each row's 128-k slice is scaled by 2^e so
+// that its max magnitude lies in [2^13, 2^14): far from fp16 overflow, and
+// hi = fp16(x), lo = fp16(x - hi) keeps ~22 bits of every element.
+// texp[m16][kg][row] = e is undone with the block scale on the fp32
+// accumulator.
 __global__ __launch_bounds__(256) void k_af16split(
-    const float *__restrict__ a, int64_t M, int64_t K, int c4n,
-    uint4 *__restrict__ ahl, int *__restrict__ rowexp) {
-  __shared__ int sexp[16];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t row0 = (int64_t)blockIdx.x * 16;
-  for (int rr = 0; rr < 4; rr++) {
-    const int r = wave * 4 + rr;
-    const int64_t row = row0 + r;
-    float mx = 0.f;
-    if (row < M)
-      for (int64_t k = lane; k < K; k += 64) mx = fmaxf(mx, fabsf(a[row * K + k]));
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) {
-      int e = 0;
-      if (mx > 0.f && isfinite(mx)) {
-        int ex;
-        frexpf(mx, &ex);
-        e = 14 - ex;
-      }
-      sexp[r] = e;
-      if (row < M) rowexp[row] = e;
-    }
+    const float *__restrict__ a, int64_t M, int64_t K, int c4n, int vec,
+    uint4 *__restrict__ ahl, int *__restrict__ texp) {
+  const int t = threadIdx.x;
+  const int kg = blockIdx.x;
+  const int64_t m16 = blockIdx.y;
+  const int r = t >> 4, c8 = t & 15;
+  const int64_t row = m16 * 16 + r;
+  const int64_t k0 = (int64_t)kg * KGRP + 8 * c8;
+  float v[8];
+  if (row < M && vec && k0 + 8 <= K) {
+    const float4 *src = reinterpret_cast<const float4 *>(a + row * K + k0);
+    const float4 x0 = src[0], x1 = src[1];
+    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (row < M && k0 + i < K) ? a[row * K + k0 + i] : 0.f;
   }
-  __syncthreads();
-  const int total = c4n * 4 * 64;
-  for (int idx = threadIdx.x; idx < total; idx += 256) {
-    const int ln = idx & 63, j = (idx >> 6) & 3, kg = idx >> 8;
-    const int r = ln & 15, g = ln >> 4;
-    const int64_t row = row0 + r;
-    const int64_t kb = (int64_t)kg * KGRP + 32 * j + 8 * g;
-    const int e = sexp[r];
-    half8 hi, lo;
-    for (int t = 0; t < 8; t++) {
-      const int64_t k = kb + t;
-      const float v = (row < M && k < K) ? ldexpf(a[row * K + k], e) : 0.f;
-      const _Float16 h = (_Float16)v;
-      float res = v - (float)h;
-      if (!isfinite(res)) res = 0.f;
-      hi[t] = h;
-      lo[t] = (_Float16)res;
-    }
-    uint4 *o = ahl + ((((int64_t)blockIdx.x * c4n + kg) * 4 + j) * 2) * 64 + ln;
-    o[0] = *reinterpret_cast<uint4 *>(&hi);
-    o[64] = *reinterpret_cast<uint4 *>(&lo);
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[i]));
+  // The 16 threads of a row are 16 consecutive lanes of one wave.
+  for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  int e = 0;
+  if (mx > 0.f && isfinite(mx)) {
+    int ex;
+    frexpf(mx, &ex);
+    e = 14 - ex;
   }
+  half8 hi, lo;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float x = ldexpf(v[i], e);
+    const _Float16 h = (_Float16)x;
+    float res = x - (float)h;
+    if (!isfinite(res)) res = 0.f;
+    hi[i] = h;
+    lo[i] = (_Float16)res;
+  }
+  const int j = c8 >> 2, g = c8 & 3, lane = g * 16 + r;
+  uint4 *o = ahl + (((m16 * c4n + kg) * 4 + j) * 2) * 64 + lane;
+  o[0] = __builtin_bit_cast(uint4, hi);
+  o[64] = __builtin_bit_cast(uint4, lo);
+  if (c8 == 0) texp[(m16 * c4n + kg) * 16 + r] = e;
 }
 
 // ---------------------------------------------------------- decode GEMV
@@ -284,123 +287,235 @@ __global__ void k_gemv_reduce(const float *__restrict__ part,
 
 // --------------------------------------------------------- prefill GEMM
 
-// Workgroup tile: (32*WMS) rows x 128 columns; 4 waves as 2 (rows) x 2
-// (column groups); each wave WMS x 4 subtiles of 16x16.  The activation
-// fragments of one k group are staged in LDS; weights go global -> VGPR and
-// are unpacked there.
-template <int WMS>
+// Dequantises one weight dword (8 codes, nibble order of wq) to 8 exact fp16
+// values q - zp: the half-word (1024 + q) is built by masking into the fp16
+// pattern 0x6400 and zz = -(1024 + zp) is added in packed fp16.
+__device__ inline uint4 deq8(uint32_t x, half2v zz) {
+  uint32_t r[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t h = ((x >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+    r[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, h) + zz);
+  }
+  return make_uint4(r[0], r[1], r[2], r[3]);
+}
+
+// Workgroup tile: (64*WM) rows x 128 columns (two column groups), 4 waves;
+// wave w owns rows [16*WM*w, +16*WM) of the tile and all 128 columns
+// (WM x 8 MFMA subtiles of 16x16).  Per k group (128 k):
+//   * the workgroup dequantises the 128x128 weight tile once into LDS, in
+//     MFMA B-fragment order (double-buffered; the packed codes of the next k
+//     group are loaded while the current one computes);
+//   * each wave streams its activation fragments (hi and lo) from global,
+//     two 32-k steps ahead of use, and issues the hi MFMAs of a step for all
+//     subtiles before the lo MFMAs, into a per-segment fp32 accumulator D;
+//   * at the end of each scale segment (SEGJ steps = min(block_size, 128) k)
+//     the block scale times the row's 2^-e is applied: acc += s * 2^-e * D.
+// Grid: x = tiles in XCD-aware order (workgroup L runs on XCD L % 8; all row
+// tiles of one column tile get the same L % 8, so its weights are read from
+// HBM once into that XCD's L2); y = k splits, each over kps k groups, whose
+// partial sums go to `part` and are added by k_gemm_reduce (ksplit > 1).
+template <int WM, int SEGJ>
 __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
-    const uint4 *__restrict__ ahl, const int *__restrict__ rowexp,
+    const uint4 *__restrict__ ahl, const int *__restrict__ texp,
     const uint4 *__restrict__ wq, const float *__restrict__ scales,
     const uint8_t *__restrict__ zp4, const float *__restrict__ bias,
-    float *__restrict__ y, int M, int N, int c4n, int nb, int nbh, int bs,
-    int has_zp) {
-  constexpr int SUB = 2 * WMS;
-  __shared__ uint4 lds[SUB * 512];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int cgi = blockIdx.x * 2 + wn;
-  const int m16_0 = blockIdx.y * SUB;
+    float *__restrict__ y, float *__restrict__ part, int M, int N, int c4n,
+    int nb, int nbh, int bs, int has_zp, int mtiles, int ntiles, int kps) {
+  __shared__ uint4 bl[2][8 * 4 * 64];
+  __shared__ float scl[2][4][16][8];  // [buf][segment][col % 16][subtile]
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int L = blockIdx.x;
+  const int xcd = L & 7, q = L >> 3;
+  const int mt = q % mtiles;
+  const int nt = (q / mtiles) * 8 + xcd;
+  if (nt >= ntiles) return;
+  const int ks = blockIdx.y;
+  const int kg0 = ks * kps;
+  const int kg1 = min(c4n, kg0 + kps);
+  const int m16w = (mt * 4 + wave) * WM;
   const int cl = lane & 15, lg = lane >> 4;
 
-  float4v acc[WMS][4], D[WMS][4];
+  // Cooperative dequantisation: thread t handles packed uint4 u = t, t + 256
+  // -> (column group 2*nt + (u >> 8), g = (u >> 6) & 3, col = u & 63).  The
+  // thread with g = s also stages the column's scale of segment s (threads
+  // with g >= segments per k group write an unused slot).
+  const int dq_g = wave;  // (t >> 6) & 3
+  int dq_cgi[2], dq_col[2], dq_dst[2], dq_ns[2];
 #pragma unroll
-  for (int i = 0; i < WMS; i++)
+  for (int h = 0; h < 2; h++) {
+    const int u = t + 256 * h;
+    dq_cgi[h] = 2 * nt + (u >> 8);
+    dq_col[h] = u & 63;
+    dq_ns[h] = (u >> 8) * 4 + (dq_col[h] >> 4);
+    dq_dst[h] = dq_ns[h] * 4 * 64 + dq_g * 16 + (dq_col[h] & 15);
+  }
+  const int nbm1 = nb - 1, nbhm1 = nbh - 1;
+  struct Meta {
+    uint4 pk[2];
+    uint32_t zb[2];  // zero-point byte(s) of the k group, first block's byte low
+    float sc[2];
+  };
+  // Branch-free: indices are clamped, out-of-range blocks (k padding) give a
+  // zero scale.
+  auto load_meta = [&](int kg, Meta &m) {
+    const int blk0 = (kg * KGRP) / bs;
+    const int blks = (kg * KGRP + 32 * SEGJ * dq_g) / bs;
+    const int zbyte0 = min(blk0 / 2, nbhm1), zbyte1 = min(blk0 / 2 + 1, nbhm1);
 #pragma unroll
-    for (int n = 0; n < 4; n++) {
-      acc[i][n] = (float4v){0.f, 0.f, 0.f, 0.f};
-      D[i][n] = (float4v){0.f, 0.f, 0.f, 0.f};
+    for (int h = 0; h < 2; h++) {
+      const int64_t cgi = dq_cgi[h];
+      m.pk[h] = wq[((cgi * c4n + kg) * 4 + dq_g) * 64 + dq_col[h]];
+      uint32_t zb = zp4[(cgi * nbh + zbyte0) * 64 + dq_col[h]];
+      if (SEGJ == 1) zb |= (uint32_t)zp4[(cgi * nbh + zbyte1) * 64 + dq_col[h]] << 8;
+      m.zb[h] = zb;
+      const float sv = scales[(cgi * nb + min(blks, nbm1)) * 64 + dq_col[h]];
+      m.sc[h] = blks < nb ? sv : 0.f;
     }
-  float sc[4] = {0.f, 0.f, 0.f, 0.f};
-  half2v zz[4];
+  };
+  // Dequantises step j of both packed uint4 into LDS buffer `buf`.
+  auto dequant_step = [&](int kg, const Meta &m, int buf, int j) {
+    const int blk0 = (kg * KGRP) / bs;
+    const int blk = (kg * KGRP + 32 * j) / bs;
+    const int sh = ((blk & 1) + 2 * (blk / 2 - blk0 / 2)) * 4;
 #pragma unroll
-  for (int n = 0; n < 4; n++) zz[n] = (half2v){(_Float16)-1032.f, (_Float16)-1032.f};
+    for (int h = 0; h < 2; h++) {
+      const uint32_t w = j == 0 ? m.pk[h].x : j == 1 ? m.pk[h].y : j == 2 ? m.pk[h].z : m.pk[h].w;
+      const int z = has_zp ? (int)((m.zb[h] >> sh) & 15u) : 8;
+      const _Float16 zh = (_Float16)(-(1024.f + (float)z));
+      bl[buf][dq_dst[h] + j * 64] = deq8(w, (half2v){zh, zh});
+    }
+    if (j == 0) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) scl[buf][dq_g][dq_col[h] & 15][dq_ns[h]] = m.sc[h];
+    }
+  };
+  // Activation fragment of step (kg, j) for row subtile i: hi at +0, lo at +64.
+  const uint4 *abase = ahl + (int64_t)m16w * c4n * 512 + lane;
+  auto a_ptr = [&](int kg, int j, int i) { return abase + ((int64_t)i * c4n + kg) * 512 + j * 128; };
 
-  for (int kg = 0; kg < c4n; kg++) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < SUB * 512; i += 256) {
-      const int s = i >> 9, off = i & 511;
-      lds[i] = ahl[((int64_t)(m16_0 + s) * c4n + kg) * 512 + off];
-    }
-    uint4 braw[4];
-    const uint4 *wp = wq + (((int64_t)cgi * c4n + kg) * 4 + lg) * 64 + cl;
+  float4v acc[WM][8], D[WM][8];
 #pragma unroll
-    for (int n = 0; n < 4; n++) braw[n] = wp[n * 16];
-    __syncthreads();
+  for (int i = 0; i < WM; i++)
+#pragma unroll
+    for (int n = 0; n < 8; n++) acc[i][n] = (float4v){0.f, 0.f, 0.f, 0.f};
+  const float4v zero4 = (float4v){0.f, 0.f, 0.f, 0.f};
+
+  // Ring of activation fragments (slot = j), loaded PD steps ahead of use:
+  // two steps for one row subtile per wave, one step for two (registers).
+  // Loads past the last k group re-read it (results unused).
+  constexpr int PD = WM == 1 ? 2 : 1;
+  uint4 ah[4][WM], al[4][WM];
+#pragma unroll
+  for (int jj = 0; jj < PD; jj++)
+#pragma unroll
+    for (int i = 0; i < WM; i++) {
+      ah[jj][i] = a_ptr(kg0, jj, i)[0];
+      al[jj][i] = a_ptr(kg0, jj, i)[64];
+    }
+  {
+    Meta m0;
+    load_meta(kg0, m0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) dequant_step(kg0, m0, 0, j);
+  }
+  __syncthreads();
+
+  for (int kg = kg0; kg < kg1; kg++) {
+    const int buf = (kg - kg0) & 1;
+    const int kgn = min(kg + 1, kg1 - 1);  // next k group (clamped)
+    Meta mnext;
+    load_meta(kgn, mnext);
+    int4 ex[WM];  // row exponents of the lane's four output rows
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+      ex[i] = reinterpret_cast<const int4 *>(texp)[((int64_t)(m16w + i) * c4n + kg) * 4 + lg];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int kk = kg * KGRP + 32 * j;
-      if (kk % bs == 0) {
-        const int blk = kk / bs;
+      {
+        const int jn = (j + PD) & 3;
+        const int kn = min(kg + ((j + PD) >> 2), kg1 - 1);
 #pragma unroll
-        for (int n = 0; n < 4; n++) {
-          const int cg = n * 16 + cl;
-          if (blk < nb) {
-            sc[n] = scales[((int64_t)cgi * nb + blk) * 64 + cg];
-            int z = 8;
-            if (has_zp) {
-              const uint8_t zb = zp4[((int64_t)cgi * nbh + blk / 2) * 64 + cg];
-              z = (blk & 1) ? (zb >> 4) : (zb & 15);
-            }
-            const _Float16 zh = (_Float16)(-(1024.f + (float)z));
-            zz[n] = (half2v){zh, zh};
-          } else {
-            sc[n] = 0.f;
-          }
+        for (int i = 0; i < WM; i++) {
+          ah[jn][i] = a_ptr(kn, jn, i)[0];
+          al[jn][i] = a_ptr(kn, jn, i)[64];
         }
       }
-      half8 bf[4];
+      // Column subtiles in pairs: the hi MFMAs of a pair, then its lo MFMAs
+      // (each lo depends on the hi issued 2*WM MFMAs earlier).
 #pragma unroll
-      for (int n = 0; n < 4; n++) {
-        const uint32_t x = j == 0 ? braw[n].x : j == 1 ? braw[n].y : j == 2 ? braw[n].z : braw[n].w;
+      for (int p2 = 0; p2 < 4; p2++) {
+        const half8 b0 = __builtin_bit_cast(half8, bl[buf][((2 * p2) * 4 + j) * 64 + lane]);
+        const half8 b1 = __builtin_bit_cast(half8, bl[buf][((2 * p2 + 1) * 4 + j) * 64 + lane]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const uint32_t h = ((x >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
-          half2v hv = __builtin_bit_cast(half2v, h) + zz[n];
-          bf[n][2 * i] = hv[0];
-          bf[n][2 * i + 1] = hv[1];
+        for (int i = 0; i < WM; i++) {
+          const half8 a_h = __builtin_bit_cast(half8, ah[j][i]);
+          D[i][2 * p2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              a_h, b0, (j % SEGJ == 0) ? zero4 : D[i][2 * p2], 0, 0, 0);
+          D[i][2 * p2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              a_h, b1, (j % SEGJ == 0) ? zero4 : D[i][2 * p2 + 1], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < WM; i++) {
+          const half8 a_l = __builtin_bit_cast(half8, al[j][i]);
+          D[i][2 * p2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, b0, D[i][2 * p2], 0, 0, 0);
+          D[i][2 * p2 + 1] =
+              __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, b1, D[i][2 * p2 + 1], 0, 0, 0);
         }
       }
+      // The next k group's weights, one step's worth per step (VALU work the
+      // scheduler interleaves with this step's MFMAs).
+      dequant_step(kgn, mnext, buf ^ 1, j);
+      if ((j + 1) % SEGJ == 0) {
+        const float4 s0 = *reinterpret_cast<const float4 *>(&scl[buf][j / SEGJ][cl][0]);
+        const float4 s1 = *reinterpret_cast<const float4 *>(&scl[buf][j / SEGJ][cl][4]);
+        const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-      for (int i = 0; i < WMS; i++) {
-        const int s = wm * WMS + i;
-        const uint4 hu = lds[((s * 4 + j) * 2 + 0) * 64 + lane];
-        const uint4 lu = lds[((s * 4 + j) * 2 + 1) * 64 + lane];
-        const half8 ah = __builtin_bit_cast(half8, hu);
-        const half8 al = __builtin_bit_cast(half8, lu);
+        for (int i = 0; i < WM; i++) {
+          const float rf[4] = {ldexpf(1.f, -ex[i].x), ldexpf(1.f, -ex[i].y),
+                               ldexpf(1.f, -ex[i].z), ldexpf(1.f, -ex[i].w)};
 #pragma unroll
-        for (int n = 0; n < 4; n++) {
-          D[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bf[n], D[i][n], 0, 0, 0);
-          D[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[n], D[i][n], 0, 0, 0);
+          for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int n = 0; n < 8; n++) acc[i][n][r] += (sc[n] * rf[r]) * D[i][n][r];
         }
-      }
-      if ((kk + 32) % bs == 0) {
-#pragma unroll
-        for (int i = 0; i < WMS; i++)
-#pragma unroll
-          for (int n = 0; n < 4; n++) {
-            acc[i][n] += sc[n] * D[i][n];
-            D[i][n] = (float4v){0.f, 0.f, 0.f, 0.f};
-          }
       }
     }
+    __syncthreads();
   }
+
+  const bool split = gridDim.y > 1;
 #pragma unroll
-  for (int i = 0; i < WMS; i++) {
-    const int rbase = (m16_0 + wm * WMS + i) * 16 + 4 * lg;
+  for (int i = 0; i < WM; i++) {
+    const int rbase = (m16w + i) * 16 + 4 * lg;
 #pragma unroll
-    for (int n = 0; n < 4; n++) {
-      const int col = cgi * 64 + n * 16 + cl;
+    for (int n = 0; n < 8; n++) {
+      const int col = nt * 128 + n * 16 + cl;
       if (col >= N) continue;
-      const float bv = bias ? bias[col] : 0.f;
+      const float bv = (!split && bias) ? bias[col] : 0.f;
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int row = rbase + r;
-        if (row < M) y[(int64_t)row * N + col] = ldexpf(acc[i][n][r], -rowexp[row]) + bv;
+        if (row >= M) continue;
+        if (split)
+          part[((int64_t)ks * M + row) * N + col] = acc[i][n][r];
+        else
+          y[(int64_t)row * N + col] = acc[i][n][r] + bv;
       }
     }
   }
+}
+
+// y = sum over k splits of part + bias (deterministic split-K reduction).
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part,
+                                                     const float *__restrict__ bias,
+                                                     float *__restrict__ y, int64_t MN, int N,
+                                                     int ksplit) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  float s = 0.f;
+  for (int k = 0; k < ksplit; k++) s += part[(int64_t)k * MN + i];
+  y[i] = s + (bias ? bias[i % N] : 0.f);
 }
 
 // ---------------------------------------------------------- generic path
@@ -443,7 +558,7 @@ struct NbitsPlan {
   int path;  // 0 gemv, 1 mfma, 2 generic
   int64_t M;
   // gemv
-  int qpg = 1, qb = 128, nqb = 0, ksplit = 1;
+  int qpg = 1, qb = 128, nqb = 0, ksplit = 1, kps = 0;
   // mfma
   int wms = 2;
   int64_t mpad = 0;
@@ -471,12 +586,20 @@ NbitsPlan plan_nbits(const mg_weight *w, int64_t M) {
     p.total = mg_align(p.off_d + (p.ksplit > 1 ? (size_t)p.ksplit * M * d.ng * 64 * 4 : 0));
   } else if (d.bs >= 32 && d.zp_kind != MG_ZP_FLOAT) {
     p.path = 1;
-    p.wms = M <= 64 ? 1 : 2;
-    const int64_t rows = 32 * p.wms;
+    p.wms = (M <= 64 || d.bs < KGRP) ? 1 : 2;
+    const int64_t rows = 64 * p.wms;
     p.mpad = (M + rows - 1) / rows * rows;
+    // Split K until the grid covers the chip (~2 workgroups per CU), keeping
+    // at least 2 k groups per split.
+    const int64_t tiles = (p.mpad / rows) * (d.ng / 2);
+    int64_t ks = 1;
+    while (tiles * ks * 2 <= 512 && d.c4 / (ks * 2) >= 2) ks *= 2;
+    p.kps = (int)((d.c4 + ks - 1) / ks);
+    p.ksplit = (int)((d.c4 + p.kps - 1) / p.kps);
     p.off_a = 0;  // ahl: mpad * kpad * 2 fp16
-    p.off_b = mg_align(p.off_a + (size_t)p.mpad * d.kpad * 4);  // rowexp
-    p.total = mg_align(p.off_b + (size_t)p.mpad * 4);
+    p.off_b = mg_align(p.off_a + (size_t)p.mpad * d.kpad * 4);  // texp
+    p.off_c = mg_align(p.off_b + (size_t)p.mpad * d.c4 * 4);    // split-K partials
+    p.total = mg_align(p.off_c + (p.ksplit > 1 ? (size_t)p.ksplit * M * w->N * 4 : 0));
   } else {
     p.path = 2;
     p.total = 0;
@@ -660,24 +783,43 @@ mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
   }
   if (p.path == 1) {
     uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
-    int *rowexp = reinterpret_cast<int *>(base + p.off_b);
-    hipLaunchKernelGGL(k_af16split, dim3((unsigned)(p.mpad / 16)), dim3(256), 0, st,
-                       a_dev, M, w->K, (int)d.c4, ahl, rowexp);
+    int *texp = reinterpret_cast<int *>(base + p.off_b);
+    float *part = p.ksplit > 1 ? reinterpret_cast<float *>(base + p.off_c) : nullptr;
+    const int vec = (w->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
+    hipLaunchKernelGGL(k_af16split, dim3((unsigned)d.c4, (unsigned)(p.mpad / 16)), dim3(256), 0,
+                       st, a_dev, M, w->K, (int)d.c4, vec, ahl, texp);
     MG_TRY(mg_launch_check("k_af16split"));
-    const int rows = 32 * p.wms;
-    const dim3 grid((unsigned)(d.ng / 2), (unsigned)(p.mpad / rows));
+    const int rows = 64 * p.wms;
+    const int mtiles = (int)(p.mpad / rows), ntiles = (int)(d.ng / 2);
+    const dim3 grid((unsigned)(8 * mtiles * ((ntiles + 7) / 8)), (unsigned)p.ksplit);
     const int has_zp = zpk == MG_ZP_UINT4;
-    if (p.wms == 1)
-      hipLaunchKernelGGL((k_gemm_f16split<1>), grid, dim3(256), 0, st, ahl, rowexp,
-                         reinterpret_cast<const uint4 *>(d.wq), d.scales, d.zp4, d.bias,
-                         y_dev, (int)M, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh,
-                         (int)d.bs, has_zp);
-    else
-      hipLaunchKernelGGL((k_gemm_f16split<2>), grid, dim3(256), 0, st, ahl, rowexp,
-                         reinterpret_cast<const uint4 *>(d.wq), d.scales, d.zp4, d.bias,
-                         y_dev, (int)M, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh,
-                         (int)d.bs, has_zp);
-    return mg_launch_check("k_gemm_f16split");
+    // The kernel reads zero-point bytes unconditionally (branch-free); without
+    // zero points it is pointed at the scales, which are at least as large.
+    const uint8_t *zp_arg = has_zp ? d.zp4 : reinterpret_cast<const uint8_t *>(d.scales);
+    const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
+#define MG_GEMM_ARGS                                                                   \
+  ahl, texp, reinterpret_cast<const uint4 *>(d.wq), d.scales, zp_arg, d.bias, y_dev, part,   \
+      (int)M, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh, (int)d.bs, has_zp, mtiles, ntiles, \
+      p.kps
+#define MG_GEMM_LAUNCH(WM_, SJ_) \
+  hipLaunchKernelGGL((k_gemm_f16split<WM_, SJ_>), grid, dim3(256), 0, st, MG_GEMM_ARGS)
+    if (p.wms == 1) {
+      if (segj == 1) MG_GEMM_LAUNCH(1, 1);
+      else if (segj == 2) MG_GEMM_LAUNCH(1, 2);
+      else MG_GEMM_LAUNCH(1, 4);
+    } else {
+      MG_GEMM_LAUNCH(2, 4);
+    }
+#undef MG_GEMM_LAUNCH
+#undef MG_GEMM_ARGS
+    MG_TRY(mg_launch_check("k_gemm_f16split"));
+    if (p.ksplit > 1) {
+      const int64_t mn = M * w->N;
+      hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st,
+                         part, d.bias, y_dev, mn, (int)w->N, p.ksplit);
+      MG_TRY(mg_launch_check("k_gemm_reduce"));
+    }
+    return MG_OK;
   }
   const int64_t tot = M * w->N;
   hipLaunchKernelGGL(k_nbits_generic, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
