@@ -21,10 +21,11 @@
 //     v_dot8_i32_i4 against the digit planes (wave-uniform, scalar-loaded).
 //     Zero point and scale are applied once per block in fp32.
 //   * M > 4 ("prefill"): activations become an fp16 pair hi + lo (scaled by a
-//     power of two per row and 128-k slice, so hi + lo carries ~22 bits of each
-//     element); each workgroup unpacks its weight tile once into LDS as exact
-//     fp16 (q - zp); v_mfma_f32_16x16x32_f16 accumulates hi*W and lo*W in fp32
-//     and the block scale is applied on the fp32 accumulator.
+//     power of two per row, so hi + lo carries ~22 bits of each element); each
+//     workgroup unpacks its weight tile once into LDS as exact fp16 (q - zp)
+//     (times 16 for half of the k, matched by a 2^-4 on those activations);
+//     v_mfma_f32_32x32x16_f16 accumulates hi*W and lo*W in fp32 and the block
+//     scale is applied on the fp32 accumulator.
 // Rare forms (float zero points or block_size 16 with M > 4) take a simple
 // per-output kernel.
 #include <hip/hip_runtime.h>
@@ -42,6 +43,7 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int KGRP = 128;  // k per k group
 constexpr int CGRP = 64;   // columns per column group
@@ -117,60 +119,77 @@ __global__ __launch_bounds__(256) void k_adigits(
   }
 }
 
-// Activations -> fp16 hi/lo fragments for the MFMA path.  One workgroup per
-// (16-row subtile, k group): 256 threads, thread t owns row t/16 and the 8
-// consecutive k at 8*(t%16) of the group.  Output ahl[m16][kg][j][hl][lane]
-// (uint4 = 8 fp16): MFMA lane (r = lane%16, g = lane/16) holds row r,
-// k = kg*128 + 32*j + 8*g + 0..7.  Each row's 128-k slice is scaled by 2^e so
-// that its max magnitude lies in [2^13, 2^14): far from fp16 overflow, and
-// hi = fp16(x), lo = fp16(x - hi) keeps ~22 bits of every element.
-// texp[m16][kg][row] = e is undone with the block scale on the fp32
-// accumulator.
+// Activation prepass of the MFMA path.  Per row: an exponent e that puts the
+// row's largest finite |a| in [2^13, 2^14), and the fp16 hi/lo split of
+// a * 2^e (hi = fp16(x), lo = fp16(x - hi)); k offsets 2, 3, 6, 7 of every 8
+// take a further 2^-4 to meet weights carried as 16 (q - zp).  Output order is
+// the GEMM's fragment order: for 32-row tile m32, k group kg, 16-k step st,
+// ahl[((m32 * c4n + kg) * 8 + st) * 128 + 32 h + r] holds the hi fp16 x 8 of
+// row r, k = 128 kg + 16 st + 8 h .. +7, and +64 the lo part; texp[row] = e.
+// Rows past M and k past K are zeros.  Non-finite values pass through in hi.
+// Workgroup: 8 rows, each row on 32 consecutive lanes (half a wave).
 __global__ __launch_bounds__(256) void k_af16split(
     const float *__restrict__ a, int64_t M, int64_t K, int c4n, int vec,
     uint4 *__restrict__ ahl, int *__restrict__ texp) {
   const int t = threadIdx.x;
-  const int kg = blockIdx.x;
-  const int64_t m16 = blockIdx.y;
-  const int r = t >> 4, c8 = t & 15;
-  const int64_t row = m16 * 16 + r;
-  const int64_t k0 = (int64_t)kg * KGRP + 8 * c8;
-  float v[8];
-  if (row < M && vec && k0 + 8 <= K) {
-    const float4 *src = reinterpret_cast<const float4 *>(a + row * K + k0);
-    const float4 x0 = src[0], x1 = src[1];
-    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-  } else {
+  const int u0 = t & 31;
+  const int64_t row = (int64_t)blockIdx.x * 8 + (t >> 5);
+  const int64_t m32 = row >> 5;
+  const int r = (int)(row & 31);
+  const int units = c4n * 8;  // 16-k pieces of the row
+  const float *arow = a + row * K;
+  auto load16 = [&](int u, float v[16]) {
+    const int64_t k0 = (int64_t)u * 16;
+    if (row < M && vec && k0 + 16 <= K) {
+      const float4 *src = reinterpret_cast<const float4 *>(arow + k0);
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = (row < M && k0 + i < K) ? a[row * K + k0 + i] : 0.f;
-  }
+      for (int q4 = 0; q4 < 4; q4++) {
+        const float4 x = src[q4];
+        v[4 * q4] = x.x; v[4 * q4 + 1] = x.y; v[4 * q4 + 2] = x.z; v[4 * q4 + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; i++) v[i] = (row < M && k0 + i < K) ? arow[k0 + i] : 0.f;
+    }
+  };
   float mx = 0.f;
+  for (int u = u0; u < units; u += 32) {
+    float v[16];
+    load16(u, v);
 #pragma unroll
-  for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[i]));
-  // The 16 threads of a row are 16 consecutive lanes of one wave.
-  for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    for (int i = 0; i < 16; i++) {
+      const float x = fabsf(v[i]);
+      mx = x < INFINITY ? fmaxf(mx, x) : mx;  // finite values only
+    }
+  }
+  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   int e = 0;
-  if (mx > 0.f && isfinite(mx)) {
+  if (mx > 0.f) {
     int ex;
     frexpf(mx, &ex);
     e = 14 - ex;
   }
-  half8 hi, lo;
+  if (u0 == 0) texp[row] = e;
+  for (int u = u0; u < units; u += 32) {
+    float v[16];
+    load16(u, v);
+    uint4 *o = ahl + ((m32 * c4n + (u >> 3)) * 8 + (u & 7)) * 128;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const float x = ldexpf(v[i], e);
-    const _Float16 h = (_Float16)x;
-    float res = x - (float)h;
-    if (!isfinite(res)) res = 0.f;
-    hi[i] = h;
-    lo[i] = (_Float16)res;
+    for (int h = 0; h < 2; h++) {
+      half8 hi, lo;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float x = ldexpf(v[8 * h + i], (i & 2) ? e - 4 : e);
+        const _Float16 hh = (_Float16)x;
+        float res = x - (float)hh;
+        if (!isfinite(res)) res = 0.f;
+        hi[i] = hh;
+        lo[i] = (_Float16)res;
+      }
+      o[r + 32 * h] = __builtin_bit_cast(uint4, hi);
+      o[64 + r + 32 * h] = __builtin_bit_cast(uint4, lo);
+    }
   }
-  const int j = c8 >> 2, g = c8 & 3, lane = g * 16 + r;
-  uint4 *o = ahl + (((m16 * c4n + kg) * 4 + j) * 2) * 64 + lane;
-  o[0] = __builtin_bit_cast(uint4, hi);
-  o[64] = __builtin_bit_cast(uint4, lo);
-  if (c8 == 0) texp[(m16 * c4n + kg) * 16 + r] = e;
 }
 
 // ---------------------------------------------------------- decode GEMV
@@ -288,43 +307,52 @@ __global__ void k_gemv_reduce(const float *__restrict__ part,
 // --------------------------------------------------------- prefill GEMM
 
 // Dequantises one weight dword (8 codes, nibble order of wq) to 8 exact fp16
-// values q - zp: the half-word (1024 + q) is built by masking into the fp16
-// pattern 0x6400 and zz = -(1024 + zp) is added in packed fp16.
-__device__ inline uint4 deq8(uint32_t x, half2v zz) {
-  uint32_t r[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const uint32_t h = ((x >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
-    r[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, h) + zz);
-  }
-  return make_uint4(r[0], r[1], r[2], r[3]);
+// values for the MFMA path.  Masking a nibble into the fp16 pattern 0x6400
+// (1024.0) gives 1024 + q for a nibble at bits 0-3 of a half-word and
+// 1024 + 16q for one at bits 4-7, so the pairs (t0,t1), (t4,t5) come out as
+// q - zp and (t2,t3), (t6,t7) as 16(q - zp) with a single shift for all
+// eight; the activation prepass scales k offsets 2,3,6,7 of every 8 by 1/16
+// to match.  `mask`/`magic` are register operands (one v_and_or_b32 each).
+__device__ inline uint4 deq8(uint32_t x, uint32_t mlo, uint32_t mhi, uint32_t magic,
+                             half2v zz1, half2v zz16) {
+  const uint32_t y = x >> 8;
+  const uint32_t d0 = (x & mlo) | magic, d1 = (x & mhi) | magic;
+  const uint32_t d2 = (y & mlo) | magic, d3 = (y & mhi) | magic;
+  return make_uint4(__builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d0) + zz1),
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d1) + zz16),
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d2) + zz1),
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d3) + zz16));
 }
 
-// Workgroup tile: (64*WM) rows x 128 columns (two column groups), 4 waves;
-// wave w owns rows [16*WM*w, +16*WM) of the tile and all 128 columns
-// (WM x 8 MFMA subtiles of 16x16).  Per k group (128 k):
+// Workgroup tile: 128 rows x 128 columns (two column groups), 4 waves; wave w
+// owns rows [32*w, +32) of the tile and all 128 columns (4 MFMA tiles of
+// 32x32, v_mfma_f32_32x32x16_f16).  Per k group (128 k = 8 steps of 16 k):
 //   * the workgroup dequantises the 128x128 weight tile once into LDS, in
-//     MFMA B-fragment order (double-buffered; the packed codes of the next k
-//     group are loaded while the current one computes);
-//   * each wave streams its activation fragments (hi and lo) from global,
-//     two 32-k steps ahead of use, and issues the hi MFMAs of a step for all
-//     subtiles before the lo MFMAs, into a per-segment fp32 accumulator D;
-//   * at the end of each scale segment (SEGJ steps = min(block_size, 128) k)
-//     the block scale times the row's 2^-e is applied: acc += s * 2^-e * D.
+//     MFMA B-fragment order (double-buffered; the next k group's packed codes
+//     are loaded at the start of the current one and unpacked step by step
+//     between its MFMAs);
+//   * each wave streams its activation fragments (hi and lo) from global, two
+//     steps ahead of use, into a per-segment fp32 accumulator D;
+//   * at the end of each scale segment (SEGJ 32-k quarters = min(block_size,
+//     128) k) the block scale times the row's 2^-e is applied:
+//     acc += s * 2^-e * D.
+// The epilogue restages each wave's 32x128 fp32 tile through LDS and writes
+// Y (or the split-K partials) as 16-byte, row-contiguous, non-temporal stores.
 // Grid: x = tiles in XCD-aware order (workgroup L runs on XCD L % 8; all row
 // tiles of one column tile get the same L % 8, so its weights are read from
 // HBM once into that XCD's L2); y = k splits, each over kps k groups, whose
 // partial sums go to `part` and are added by k_gemm_reduce (ksplit > 1).
-template <int WM, int SEGJ>
+template <int SEGJ>
 __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
     const uint4 *__restrict__ ahl, const int *__restrict__ texp,
     const uint4 *__restrict__ wq, const float *__restrict__ scales,
     const uint8_t *__restrict__ zp4, const float *__restrict__ bias,
     float *__restrict__ y, float *__restrict__ part, int M, int N, int c4n,
-    int nb, int nbh, int bs, int has_zp, int mtiles, int ntiles, int kps) {
-  __shared__ uint4 bl[2][8 * 4 * 64];
-  __shared__ float scl[2][4][16][8];  // [buf][segment][col % 16][subtile]
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    int nb, int nbh, int lbs, int has_zp, int mtiles, int ntiles, int kps, int y_vec) {
+  __shared__ uint4 bl[2][4 * 8 * 64];      // [buf][n32][step][lane] fp16 x 8
+  __shared__ float scl[2][4][32][4];       // [buf][segment][col % 32][n32]
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int L = blockIdx.x;
   const int xcd = L & 7, q = L >> 3;
   const int mt = q % mtiles;
@@ -333,91 +361,107 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
   const int ks = blockIdx.y;
   const int kg0 = ks * kps;
   const int kg1 = min(c4n, kg0 + kps);
-  const int m16w = (mt * 4 + wave) * WM;
-  const int cl = lane & 15, lg = lane >> 4;
+  const int m32 = mt * 4 + wave;  // this wave's 32-row subtile
+  const int lc = lane & 31, lh = lane >> 5;
 
-  // Cooperative dequantisation: thread t handles packed uint4 u = t, t + 256
-  // -> (column group 2*nt + (u >> 8), g = (u >> 6) & 3, col = u & 63).  The
-  // thread with g = s also stages the column's scale of segment s (threads
-  // with g >= segments per k group write an unused slot).
-  const int dq_g = wave;  // (t >> 6) & 3
-  int dq_cgi[2], dq_col[2], dq_dst[2], dq_ns[2];
+  // Cooperative dequantisation of the 512 packed uint4 of a k group: thread t
+  // handles u = t + 256 h, h < 2 -> (column group 2*nt + h, g = wave,
+  // col = lane); its dword j (k = 32j + 8g .. +7) is MFMA step 2j + g/2, half
+  // g%2.  The thread with g = s also stages the column's scale of segment s
+  // (threads with g >= segments per k group write an unused slot).
+  constexpr int PH = 2;
+  const int dq_g = wave;
+  int dq_cgi[PH], dq_col[PH], dq_dst[PH], dq_c[PH];
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
+  for (int h = 0; h < PH; h++) {
     const int u = t + 256 * h;
     dq_cgi[h] = 2 * nt + (u >> 8);
     dq_col[h] = u & 63;
-    dq_ns[h] = (u >> 8) * 4 + (dq_col[h] >> 4);
-    dq_dst[h] = dq_ns[h] * 4 * 64 + dq_g * 16 + (dq_col[h] & 15);
+    dq_c[h] = (u >> 8) * 64 + dq_col[h];  // column within the 128-column tile
+    const int n32 = dq_c[h] >> 5;
+    dq_dst[h] = (n32 * 8 + (dq_g >> 1)) * 64 + (dq_c[h] & 31) + 32 * (dq_g & 1);
   }
   const int nbm1 = nb - 1, nbhm1 = nbh - 1;
+  // Dequantisation masks held in VGPRs so that each pair is one v_and_or_b32
+  // (VOP3 takes no literal operands here).
+  uint32_t v_mlo, v_mhi, v_magic;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v_mlo) : "s"(0x000F000Fu));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v_mhi) : "s"(0x00F000F0u));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v_magic) : "s"(0x64006400u));
   struct Meta {
-    uint4 pk[2];
-    uint32_t zb[2];  // zero-point byte(s) of the k group, first block's byte low
-    float sc[2];
+    uint4 pk[PH];
+    uint32_t zb[PH], zb2[PH];  // zero-point bytes of the k group's first two byte slots
+    float sc[PH];
   };
-  // Branch-free: indices are clamped, out-of-range blocks (k padding) give a
-  // zero scale.
+  // Branch-free: indices are clamped; blocks past the last (k padding) get a
+  // zero scale when the scale is staged.
   auto load_meta = [&](int kg, Meta &m) {
-    const int blk0 = (kg * KGRP) / bs;
-    const int blks = (kg * KGRP + 32 * SEGJ * dq_g) / bs;
+    const int blk0 = (kg * KGRP) >> lbs;
+    const int blks = (kg * KGRP + 32 * SEGJ * dq_g) >> lbs;
     const int zbyte0 = min(blk0 / 2, nbhm1), zbyte1 = min(blk0 / 2 + 1, nbhm1);
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
+    for (int h = 0; h < PH; h++) {
       const int64_t cgi = dq_cgi[h];
       m.pk[h] = wq[((cgi * c4n + kg) * 4 + dq_g) * 64 + dq_col[h]];
-      uint32_t zb = zp4[(cgi * nbh + zbyte0) * 64 + dq_col[h]];
-      if (SEGJ == 1) zb |= (uint32_t)zp4[(cgi * nbh + zbyte1) * 64 + dq_col[h]] << 8;
-      m.zb[h] = zb;
-      const float sv = scales[(cgi * nb + min(blks, nbm1)) * 64 + dq_col[h]];
-      m.sc[h] = blks < nb ? sv : 0.f;
+      m.zb[h] = zp4[(cgi * nbh + zbyte0) * 64 + dq_col[h]];
+      m.zb2[h] = SEGJ == 1 ? zp4[(cgi * nbh + zbyte1) * 64 + dq_col[h]] : 0u;
+      m.sc[h] = scales[(cgi * nb + min(blks, nbm1)) * 64 + dq_col[h]];
     }
   };
-  // Dequantises step j of both packed uint4 into LDS buffer `buf`.
-  auto dequant_step = [&](int kg, const Meta &m, int buf, int j) {
-    const int blk0 = (kg * KGRP) / bs;
-    const int blk = (kg * KGRP + 32 * j) / bs;
+  // Dequantises dword j (32-k quarter j) of both packed uint4 into buffer buf.
+  auto dequant_quarter = [&](int kg, const Meta &m, int buf, int j) {
+    const int blk0 = (kg * KGRP) >> lbs;
+    const int blk = (kg * KGRP + 32 * j) >> lbs;
     const int sh = ((blk & 1) + 2 * (blk / 2 - blk0 / 2)) * 4;
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const uint32_t w = j == 0 ? m.pk[h].x : j == 1 ? m.pk[h].y : j == 2 ? m.pk[h].z : m.pk[h].w;
-      const int z = has_zp ? (int)((m.zb[h] >> sh) & 15u) : 8;
-      const _Float16 zh = (_Float16)(-(1024.f + (float)z));
-      bl[buf][dq_dst[h] + j * 64] = deq8(w, (half2v){zh, zh});
+    for (int h = 0; h < PH; h++) {
+      // Loaded values are first touched here (empty asm): arithmetic on them
+      // would otherwise be hoisted next to the loads and wait on them there.
+      uint32_t w = j == 0 ? m.pk[h].x : j == 1 ? m.pk[h].y : j == 2 ? m.pk[h].z : m.pk[h].w;
+      uint32_t zb = m.zb[h], zb2 = m.zb2[h];
+      asm volatile("" : "+v"(w), "+v"(zb), "+v"(zb2));
+      zb |= zb2 << 8;
+      const int z = has_zp ? (int)((zb >> sh) & 15u) : 8;
+      const _Float16 z1 = (_Float16)(-(1024.f + (float)z));
+      const _Float16 z16 = (_Float16)(-(1024.f + 16.f * (float)z));
+      bl[buf][dq_dst[h] + 2 * j * 64] =
+          deq8(w, v_mlo, v_mhi, v_magic, (half2v){z1, z1}, (half2v){z16, z16});
     }
     if (j == 0) {
+      const bool in_range = ((kg * KGRP + 32 * SEGJ * dq_g) >> lbs) < nb;
 #pragma unroll
-      for (int h = 0; h < 2; h++) scl[buf][dq_g][dq_col[h] & 15][dq_ns[h]] = m.sc[h];
+      for (int h = 0; h < PH; h++) {
+        float sc = m.sc[h];
+        asm volatile("" : "+v"(sc));
+        scl[buf][dq_g][dq_c[h] & 31][dq_c[h] >> 5] = in_range ? sc : 0.f;
+      }
     }
   };
-  // Activation fragment of step (kg, j) for row subtile i: hi at +0, lo at +64.
-  const uint4 *abase = ahl + (int64_t)m16w * c4n * 512 + lane;
-  auto a_ptr = [&](int kg, int j, int i) { return abase + ((int64_t)i * c4n + kg) * 512 + j * 128; };
+  // Activation fragment of step s of k group kg: hi at +0, lo at +64.
+  const uint4 *abase = ahl + (int64_t)m32 * c4n * 1024 + lane;
+  auto a_ptr = [&](int kg, int st) { return abase + ((int64_t)kg * 8 + st) * 128; };
 
-  float4v acc[WM][8], D[WM][8];
+  float16v acc[4], D[4];
 #pragma unroll
-  for (int i = 0; i < WM; i++)
-#pragma unroll
-    for (int n = 0; n < 8; n++) acc[i][n] = (float4v){0.f, 0.f, 0.f, 0.f};
-  const float4v zero4 = (float4v){0.f, 0.f, 0.f, 0.f};
+  for (int n = 0; n < 4; n++) acc[n] = (float16v){};
+  const float16v zero16 = (float16v){};
 
-  // Ring of activation fragments (slot = j), loaded PD steps ahead of use:
-  // two steps for one row subtile per wave, one step for two (registers).
-  // Loads past the last k group re-read it (results unused).
-  constexpr int PD = WM == 1 ? 2 : 1;
-  uint4 ah[4][WM], al[4][WM];
+  // Ring of activation fragments (slot = step), loaded PD steps ahead.  Loads
+  // past the last k group re-read it (results unused).  Memory loads complete
+  // in issue order, so the next k group's weights, loaded at step 0, are
+  // first needed at step PD, together with the activations issued after them.
+  constexpr int PD = 4;
+  uint4 ah[8], al[8];
 #pragma unroll
-  for (int jj = 0; jj < PD; jj++)
-#pragma unroll
-    for (int i = 0; i < WM; i++) {
-      ah[jj][i] = a_ptr(kg0, jj, i)[0];
-      al[jj][i] = a_ptr(kg0, jj, i)[64];
-    }
+  for (int ss = 0; ss < PD; ss++) {
+    ah[ss] = a_ptr(kg0, ss)[0];
+    al[ss] = a_ptr(kg0, ss)[64];
+  }
   {
     Meta m0;
     load_meta(kg0, m0);
 #pragma unroll
-    for (int j = 0; j < 4; j++) dequant_step(kg0, m0, 0, j);
+    for (int j = 0; j < 4; j++) dequant_quarter(kg0, m0, 0, j);
   }
   __syncthreads();
 
@@ -426,81 +470,93 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
     const int kgn = min(kg + 1, kg1 - 1);  // next k group (clamped)
     Meta mnext;
     load_meta(kgn, mnext);
-    int4 ex[WM];  // row exponents of the lane's four output rows
+    // Keep the scheduler from sinking these loads towards their use.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < WM; i++)
-      ex[i] = reinterpret_cast<const int4 *>(texp)[((int64_t)(m16w + i) * c4n + kg) * 4 + lg];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int st = 0; st < 8; st++) {
       {
-        const int jn = (j + PD) & 3;
-        const int kn = min(kg + ((j + PD) >> 2), kg1 - 1);
-#pragma unroll
-        for (int i = 0; i < WM; i++) {
-          ah[jn][i] = a_ptr(kn, jn, i)[0];
-          al[jn][i] = a_ptr(kn, jn, i)[64];
-        }
+        const int sn = (st + PD) & 7;
+        const int kn = min(kg + ((st + PD) >> 3), kg1 - 1);
+        ah[sn] = a_ptr(kn, sn)[0];
+        al[sn] = a_ptr(kn, sn)[64];
       }
-      // Column subtiles in pairs: the hi MFMAs of a pair, then its lo MFMAs
-      // (each lo depends on the hi issued 2*WM MFMAs earlier).
+      __builtin_amdgcn_sched_barrier(0);
+      const bool seg_start = (st % (2 * SEGJ)) == 0;
+      const half8 a_h = __builtin_bit_cast(half8, ah[st]);
+      const half8 a_l = __builtin_bit_cast(half8, al[st]);
 #pragma unroll
-      for (int p2 = 0; p2 < 4; p2++) {
-        const half8 b0 = __builtin_bit_cast(half8, bl[buf][((2 * p2) * 4 + j) * 64 + lane]);
-        const half8 b1 = __builtin_bit_cast(half8, bl[buf][((2 * p2 + 1) * 4 + j) * 64 + lane]);
-#pragma unroll
-        for (int i = 0; i < WM; i++) {
-          const half8 a_h = __builtin_bit_cast(half8, ah[j][i]);
-          D[i][2 * p2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              a_h, b0, (j % SEGJ == 0) ? zero4 : D[i][2 * p2], 0, 0, 0);
-          D[i][2 * p2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              a_h, b1, (j % SEGJ == 0) ? zero4 : D[i][2 * p2 + 1], 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < WM; i++) {
-          const half8 a_l = __builtin_bit_cast(half8, al[j][i]);
-          D[i][2 * p2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, b0, D[i][2 * p2], 0, 0, 0);
-          D[i][2 * p2 + 1] =
-              __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, b1, D[i][2 * p2 + 1], 0, 0, 0);
-        }
+      for (int n = 0; n < 4; n++) {
+        const half8 b = __builtin_bit_cast(half8, bl[buf][(n * 8 + st) * 64 + lane]);
+        D[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, b, seg_start ? zero16 : D[n], 0, 0, 0);
+        D[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, b, D[n], 0, 0, 0);
       }
-      // The next k group's weights, one step's worth per step (VALU work the
-      // scheduler interleaves with this step's MFMAs).
-      dequant_step(kgn, mnext, buf ^ 1, j);
-      if ((j + 1) % SEGJ == 0) {
-        const float4 s0 = *reinterpret_cast<const float4 *>(&scl[buf][j / SEGJ][cl][0]);
-        const float4 s1 = *reinterpret_cast<const float4 *>(&scl[buf][j / SEGJ][cl][4]);
-        const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+      // The next k group's weights, a quarter per step in steps PD..7 (VALU
+      // work the scheduler interleaves with these MFMAs).
+      if (st >= PD) dequant_quarter(kgn, mnext, buf ^ 1, st - PD);
+      if ((st + 1) % (2 * SEGJ) == 0) {
+        const float4 s4 = *reinterpret_cast<const float4 *>(&scl[buf][st / (2 * SEGJ)][lc][0]);
+        const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-        for (int i = 0; i < WM; i++) {
-          const float rf[4] = {ldexpf(1.f, -ex[i].x), ldexpf(1.f, -ex[i].y),
-                               ldexpf(1.f, -ex[i].z), ldexpf(1.f, -ex[i].w)};
+        for (int n = 0; n < 4; n++)
 #pragma unroll
-          for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int n = 0; n < 8; n++) acc[i][n][r] += (sc[n] * rf[r]) * D[i][n][r];
-        }
+          for (int v = 0; v < 16; v++) acc[n][v] = fmaf(sc[n], D[n][v], acc[n][v]);
       }
     }
     __syncthreads();
   }
 
+  // Epilogue: stage the wave's 32x128 tile row-major in LDS (the weight
+  // buffers are free now; every wave passed the last barrier), then write
+  // 16-byte row pieces.
+  float *stage = reinterpret_cast<float *>(&bl[0][0]) + wave * (32 * 128);
+  // Row exponents of the lane's 16 output rows 8*(v/4) + 4*lh + v%4; the row
+  // factor 2^-e is applied with ldexp (exact, and graded into subnormals).
+  int4 ex[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    ex[i] = reinterpret_cast<const int4 *>(texp)[(int64_t)m32 * 8 + 2 * i + lh];
+#pragma unroll
+  for (int n = 0; n < 4; n++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int r = 8 * (v >> 2) + 4 * lh + (v & 3);
+      const int4 e4 = ex[v >> 2];
+      const int e = (v & 3) == 0 ? e4.x : (v & 3) == 1 ? e4.y : (v & 3) == 2 ? e4.z : e4.w;
+      stage[r * 128 + n * 32 + lc] = ldexpf(acc[n][v], -e);
+    }
+  __syncthreads();
   const bool split = gridDim.y > 1;
-#pragma unroll
-  for (int i = 0; i < WM; i++) {
-    const int rbase = (m16w + i) * 16 + 4 * lg;
-#pragma unroll
-    for (int n = 0; n < 8; n++) {
-      const int col = nt * 128 + n * 16 + cl;
-      if (col >= N) continue;
-      const float bv = (!split && bias) ? bias[col] : 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int row = rbase + r;
-        if (row >= M) continue;
-        if (split)
-          part[((int64_t)ks * M + row) * N + col] = acc[i][n][r];
-        else
-          y[(int64_t)row * N + col] = acc[i][n][r] + bv;
+  float *dst = split ? part + (int64_t)ks * M * N : y;
+  const int c4 = lane & 31;
+  const int col = nt * 128 + 4 * c4;
+  float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!split && bias) {
+    if (col + 3 < N) {
+      bv = make_float4(bias[col], bias[col + 1], bias[col + 2], bias[col + 3]);
+    } else {
+      if (col < N) bv.x = bias[col];
+      if (col + 1 < N) bv.y = bias[col + 1];
+      if (col + 2 < N) bv.z = bias[col + 2];
+    }
+  }
+  // 16-byte stores need N % 4 == 0 and a 16-byte aligned destination (the
+  // partials buffer always is; y is checked by the host).
+  const bool vec_ok = (N % 4) == 0 && (split || y_vec);
+#pragma unroll 4
+  for (int it = 0; it < 16; it++) {
+    const int r = 2 * it + lh;
+    const int row = m32 * 32 + r;
+    float4v v = *reinterpret_cast<const float4v *>(&stage[r * 128 + 4 * c4]);
+    v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
+    if (row < M) {
+      float *p = dst + (int64_t)row * N + col;
+      if (vec_ok && col + 3 < N) {
+        __builtin_nontemporal_store(v, reinterpret_cast<float4v *>(p));
+      } else {
+        if (col < N) p[0] = v[0];
+        if (col + 1 < N) p[1] = v[1];
+        if (col + 2 < N) p[2] = v[2];
+        if (col + 3 < N) p[3] = v[3];
       }
     }
   }
@@ -560,7 +616,6 @@ struct NbitsPlan {
   // gemv
   int qpg = 1, qb = 128, nqb = 0, ksplit = 1, kps = 0;
   // mfma
-  int wms = 2;
   int64_t mpad = 0;
   size_t off_a = 0, off_b = 0, off_c = 0, off_d = 0, total = 0;
 };
@@ -586,8 +641,7 @@ NbitsPlan plan_nbits(const mg_weight *w, int64_t M) {
     p.total = mg_align(p.off_d + (p.ksplit > 1 ? (size_t)p.ksplit * M * d.ng * 64 * 4 : 0));
   } else if (d.bs >= 32 && d.zp_kind != MG_ZP_FLOAT) {
     p.path = 1;
-    p.wms = (M <= 64 || d.bs < KGRP) ? 1 : 2;
-    const int64_t rows = 64 * p.wms;
+    const int64_t rows = 128;  // workgroup tile rows
     p.mpad = (M + rows - 1) / rows * rows;
     // Split K until the grid covers the chip (~2 workgroups per CU), keeping
     // at least 2 k groups per split.
@@ -597,8 +651,8 @@ NbitsPlan plan_nbits(const mg_weight *w, int64_t M) {
     p.kps = (int)((d.c4 + ks - 1) / ks);
     p.ksplit = (int)((d.c4 + p.kps - 1) / p.kps);
     p.off_a = 0;  // ahl: mpad * kpad * 2 fp16
-    p.off_b = mg_align(p.off_a + (size_t)p.mpad * d.kpad * 4);  // texp
-    p.off_c = mg_align(p.off_b + (size_t)p.mpad * d.c4 * 4);    // split-K partials
+    p.off_b = mg_align(p.off_a + (size_t)p.mpad * d.kpad * 4);  // texp [row]
+    p.off_c = mg_align(p.off_b + (size_t)p.mpad * 4);           // split-K partials
     p.total = mg_align(p.off_c + (p.ksplit > 1 ? (size_t)p.ksplit * M * w->N * 4 : 0));
   } else {
     p.path = 2;
@@ -786,10 +840,10 @@ mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
     int *texp = reinterpret_cast<int *>(base + p.off_b);
     float *part = p.ksplit > 1 ? reinterpret_cast<float *>(base + p.off_c) : nullptr;
     const int vec = (w->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
-    hipLaunchKernelGGL(k_af16split, dim3((unsigned)d.c4, (unsigned)(p.mpad / 16)), dim3(256), 0,
+    hipLaunchKernelGGL(k_af16split, dim3((unsigned)(p.mpad / 8)), dim3(256), 0,
                        st, a_dev, M, w->K, (int)d.c4, vec, ahl, texp);
     MG_TRY(mg_launch_check("k_af16split"));
-    const int rows = 64 * p.wms;
+    const int rows = 128;
     const int mtiles = (int)(p.mpad / rows), ntiles = (int)(d.ng / 2);
     const dim3 grid((unsigned)(8 * mtiles * ((ntiles + 7) / 8)), (unsigned)p.ksplit);
     const int has_zp = zpk == MG_ZP_UINT4;
@@ -797,19 +851,17 @@ mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
     // zero points it is pointed at the scales, which are at least as large.
     const uint8_t *zp_arg = has_zp ? d.zp4 : reinterpret_cast<const uint8_t *>(d.scales);
     const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
+    const int y_vec = (reinterpret_cast<uintptr_t>(y_dev) % 16) == 0;
 #define MG_GEMM_ARGS                                                                   \
   ahl, texp, reinterpret_cast<const uint4 *>(d.wq), d.scales, zp_arg, d.bias, y_dev, part,   \
-      (int)M, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh, (int)d.bs, has_zp, mtiles, ntiles, \
-      p.kps
-#define MG_GEMM_LAUNCH(WM_, SJ_) \
-  hipLaunchKernelGGL((k_gemm_f16split<WM_, SJ_>), grid, dim3(256), 0, st, MG_GEMM_ARGS)
-    if (p.wms == 1) {
-      if (segj == 1) MG_GEMM_LAUNCH(1, 1);
-      else if (segj == 2) MG_GEMM_LAUNCH(1, 2);
-      else MG_GEMM_LAUNCH(1, 4);
-    } else {
-      MG_GEMM_LAUNCH(2, 4);
-    }
+      (int)M, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), has_zp,     \
+      mtiles, ntiles, \
+      p.kps, y_vec
+#define MG_GEMM_LAUNCH(SJ_) \
+  hipLaunchKernelGGL((k_gemm_f16split<SJ_>), grid, dim3(256), 0, st, MG_GEMM_ARGS)
+    if (segj == 1) MG_GEMM_LAUNCH(1);
+    else if (segj == 2) MG_GEMM_LAUNCH(2);
+    else MG_GEMM_LAUNCH(4);
 #undef MG_GEMM_LAUNCH
 #undef MG_GEMM_ARGS
     MG_TRY(mg_launch_check("k_gemm_f16split"));

@@ -129,6 +129,32 @@ QWEN = [  # (name, K, N): Qwen3-0.6B projections, block 128 with zero points
     ("down", 3072, 1024), ("lm_head", 1024, 151936)]
 
 
+def test_nonfinite_and_ragged_rows_prefill(ops):
+    # MFMA path: inf / nan activations give the reference's inf / nan pattern
+    # (inf * w = +-inf, inf * 0 = nan); a row whose magnitude varies by 1e12
+    # along k and a row near the fp32 range stay within the bar.
+    rng = np.random.default_rng(5)
+    m, k, n, bs = 40, 512, 96, 128
+    b, s, zp = make_nbits(rng, n, k, bs, "packed")
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a[0, 5] = np.inf
+    a[1, 9] = -np.inf
+    a[2, 3] = np.nan
+    a[3] *= 1e30
+    a[4, :256] *= 1e-6
+    a[4, 256:] *= 1e6
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs)
+    y = w(a)
+    w.release()
+    ref = oracle.matmul_nbits(a, b, s, zp, k=k, n=n, block_size=bs)
+    np.testing.assert_array_equal(np.isnan(y), np.isnan(ref))
+    np.testing.assert_array_equal(np.isposinf(y), np.isposinf(ref))
+    np.testing.assert_array_equal(np.isneginf(y), np.isneginf(ref))
+    assert np.isinf(ref[0]).any() and np.isnan(ref[2]).all()
+    for r in range(3, m):
+        assert G.rms_error(y[r], ref[r]) <= TOL, r
+
+
 @pytest.mark.parametrize("proj,k,n", QWEN)
 @pytest.mark.parametrize("m", [1, 512])
 def test_qwen_shapes_column_subset(ops, proj, k, n, m):
