@@ -55,70 +55,6 @@ __host__ __device__ inline int nib_pos(int t) {
 
 // ------------------------------------------------------------- prepasses
 
-// Activations -> int4 digit planes for the decode path.  One wave per
-// (row, qblock); qblock = min(block_size, 128) consecutive k.
-//   dig[row][kg][g][j][d]: digit plane d of the 8 k of dword (g, j), nibble
-//   order as in wq; alpha[row][qb] = dequant step; rsum[row][qb] = sum of the
-//   fixed-point values (for the zero-point term).
-__global__ __launch_bounds__(256) void k_adigits(
-    const float *__restrict__ a, int64_t M, int64_t K, int qb, int nqb,
-    int c4n, uint32_t *__restrict__ dig, float *__restrict__ alpha,
-    int *__restrict__ rsum) {
-  const int64_t widx = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (widx >= M * nqb) return;
-  const int64_t row = widx / nqb;
-  const int qbi = (int)(widx % nqb);
-  const int64_t k0 = (int64_t)qbi * qb;
-  const float *ar = a + row * K;
-  float mx = 0.f;
-  int bad = 0;
-  for (int i = lane; i < qb; i += 64) {
-    const int64_t k = k0 + i;
-    const float v = k < K ? ar[k] : 0.f;
-    if (!isfinite(v)) bad = 1;
-    mx = fmaxf(mx, fabsf(v));
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    mx = fmaxf(mx, __shfl_xor(mx, o));
-    bad |= __shfl_xor(bad, o);
-  }
-  const float inv = (mx > 0.f && !bad) ? (float)FIX_MAX / mx : 0.f;
-  int rs = 0;
-  for (int d = lane; d < qb / 8; d += 64) {
-    const int64_t kb = k0 + 8 * d;
-    uint32_t dg[4] = {0u, 0u, 0u, 0u};
-    for (int t = 0; t < 8; t++) {
-      const int64_t k = kb + t;
-      const float v = k < K ? ar[k] : 0.f;
-      int fix = (int)rintf(v * inv);
-      fix = min(max(fix, -FIX_MAX), FIX_MAX);
-      rs += fix;
-      const int p = nib_pos(t);
-      int x = fix;
-      for (int dd = 0; dd < 4; dd++) {
-        const int di = ((x + 8) & 15) - 8;
-        x = (x - di) >> 4;
-        dg[dd] |= (uint32_t)(di & 15) << (4 * p);
-      }
-    }
-    const int kg = (int)(kb / KGRP);
-    const int rem = (int)(kb % KGRP);
-    const int j = rem / 32, g = (rem % 32) / 8;
-    uint32_t *o = dig + (((row * c4n + kg) * 4 + g) * 16 + j * 4);
-    o[0] = dg[0];
-    o[1] = dg[1];
-    o[2] = dg[2];
-    o[3] = dg[3];
-  }
-  for (int o = 32; o > 0; o >>= 1) rs += __shfl_xor(rs, o);
-  if (lane == 0) {
-    alpha[row * nqb + qbi] =
-        bad ? __builtin_nanf("") : (mx > 0.f ? mx / (float)FIX_MAX : 0.f);
-    rsum[row * nqb + qbi] = rs;
-  }
-}
-
 // Activation prepass of the MFMA path.  Per row: an exponent e that puts the
 // row's largest finite |a| in [2^13, 2^14), and the fp16 hi/lo split of
 // a * 2^e (hi = fp16(x), lo = fp16(x - hi)); k offsets 2, 3, 6, 7 of every 8
@@ -194,59 +130,143 @@ __global__ __launch_bounds__(256) void k_af16split(
 
 // ---------------------------------------------------------- decode GEMV
 
-// MR activation rows; QPG = qblocks per k group (128 / min(bs, 128));
-// ZPK = zero-point kind.  Grid (column groups, k slices); 4 waves per
-// workgroup, each wave a different k slice of the same 64 columns.
+// MR activation rows (M <= 4); QPG = quantisation blocks per k group
+// (128 / min(bs, 128)); ZPK = zero-point kind.  Grid (column groups, k
+// splits); 4 waves per workgroup; wave w of split y takes the k groups
+// kg = 4y + w (mod nslices = 4 * ksplit), local index l = 4 * (kg / nslices) + w.
+//
+// Phase 1: the workgroup quantises the activations of its k groups into LDS:
+// per (row, qblock of qb = min(bs, 128) k) the step alpha = max|a| / FIX_MAX
+// (NaN when the block holds a non-finite value), fix = rint(a / alpha)
+// clamped to +-FIX_MAX and split into four balanced signed int4 digits
+// (fix = sum_d 16^d dig_d, dig_d in [-8, 7]) packed 8 per dword in the nibble
+// order of wq: sdig[r][l][g][j][d]; srsum = sum of fix over the qblock.
+// Thread per (row, k group, 8-k octet o = 4j + g); a qblock is 16 / QPG
+// consecutive lanes.
+// Phase 2: each lane owns one column and streams its packed codes with
+// 16-byte loads; v_dot8_i32_i4 multiplies (q - 8) with each digit plane and
+//   y += alpha * s * (sum_d 16^d D_d + (8 - zp) * rsum).
 template <int MR, int QPG, int ZPK>
 __global__ __launch_bounds__(256) void k_gemv_dot8(
-    const uint4 *__restrict__ wq, const float *__restrict__ scales,
-    const uint8_t *__restrict__ zp4, const float *__restrict__ zpf,
-    const uint32_t *__restrict__ dig, const float *__restrict__ alpha,
-    const int *__restrict__ rsum, const float *__restrict__ bias,
+    const float *__restrict__ a, int64_t K, int vec, const uint4 *__restrict__ wq,
+    const float *__restrict__ scales, const uint8_t *__restrict__ zp4,
+    const float *__restrict__ zpf, const float *__restrict__ bias,
     float *__restrict__ y, float *__restrict__ part, int N, int c4n, int nb,
-    int nbh, int bs, int nqb, int ncolp) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int nbh, int lbs, int nloc, int ncolp) {
+  extern __shared__ uint32_t smem[];
+  uint32_t *sdig = smem;                                            // [MR][nloc][64]
+  float *salpha = reinterpret_cast<float *>(smem + MR * nloc * 64);  // [MR][nloc][QPG]
+  int *srsum = reinterpret_cast<int *>(salpha + MR * nloc * QPG);   // [MR][nloc][QPG]
+  __shared__ float red[4][MR][64];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int cgi = blockIdx.x;
   const int nslices = gridDim.y * 4;
-  const int slice = blockIdx.y * 4 + wave;
-  const int qb = KGRP / QPG;
-  float yacc[MR];
-#pragma unroll
-  for (int r = 0; r < MR; r++) yacc[r] = 0.f;
+  constexpr int G = 16 / QPG;  // octets per qblock
 
-  for (int kg = slice; kg < c4n; kg += nslices) {
-    int acc[MR][QPG][4];
+  // Phase 1.
+  const int ntask = MR * nloc * 16;
+  for (int task = t; task < ntask; task += 256) {
+    const int o = task & 15, rl = task >> 4;
+    const int l = rl % nloc, r = rl / nloc;
+    const int kg = (l >> 2) * nslices + blockIdx.y * 4 + (l & 3);
+    const int64_t k0 = (int64_t)kg * KGRP + 8 * o;
+    const float *ar = a + (int64_t)r * K;
+    float v[8];
+    if (vec && k0 + 8 <= K) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(ar + k0);
+      const float4 x1 = *reinterpret_cast<const float4 *>(ar + k0 + 4);
+      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+      v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    } else {
 #pragma unroll
-    for (int r = 0; r < MR; r++)
+      for (int i = 0; i < 8; i++) v[i] = (kg < c4n && k0 + i < K) ? ar[k0 + i] : 0.f;
+    }
+    float mx = 0.f;
+    int bad = 0;
 #pragma unroll
-      for (int s = 0; s < QPG; s++)
+    for (int i = 0; i < 8; i++) {
+      if (!isfinite(v[i])) bad = 1;
+      mx = fmaxf(mx, fabsf(v[i]));
+    }
 #pragma unroll
-        for (int d = 0; d < 4; d++) acc[r][s][d] = 0;
-    const uint4 *wp = wq + (((int64_t)cgi * c4n + kg) * 4) * 64 + lane;
+    for (int off = 1; off < G; off <<= 1) {
+      mx = fmaxf(mx, __shfl_xor(mx, off));
+      bad |= __shfl_xor(bad, off);
+    }
+    const float inv = (mx > 0.f && !bad) ? (float)FIX_MAX / mx : 0.f;
+    int rs = 0;
+    uint32_t dg[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const uint4 w = wp[g * 64];
-      const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    for (int i = 0; i < 8; i++) {
+      int fix = (int)rintf(v[i] * inv);
+      fix = min(max(fix, -FIX_MAX), FIX_MAX);
+      rs += fix;
+      const int pos = nib_pos(i);
+      int x = fix;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int x = (int)(wv[j] ^ 0x88888888u);
-        const int slot = QPG == 1 ? 0 : (QPG == 2 ? j / 2 : (QPG == 4 ? j : 2 * j + g / 2));
-#pragma unroll
-        for (int r = 0; r < MR; r++) {
-          const uint32_t *dr =
-              dig + ((((int64_t)r * c4n + kg) * 4 + g) * 16 + j * 4);
-#pragma unroll
-          for (int d = 0; d < 4; d++)
-            acc[r][slot][d] =
-                __builtin_amdgcn_sdot8((int)dr[d], x, acc[r][slot][d], false);
-        }
+      for (int d = 0; d < 4; d++) {
+        const int di = ((x + 8) & 15) - 8;
+        x = (x - di) >> 4;
+        dg[d] |= (uint32_t)(di & 15) << (4 * pos);
       }
     }
 #pragma unroll
+    for (int off = 1; off < G; off <<= 1) rs += __shfl_xor(rs, off);
+    const int j = o >> 2, g = o & 3;
+    *reinterpret_cast<uint4 *>(&sdig[((r * nloc + l) * 4 + g) * 16 + j * 4]) =
+        make_uint4(dg[0], dg[1], dg[2], dg[3]);
+    if (o % G == 0) {
+      const int q = (r * nloc + l) * QPG + o / G;
+      salpha[q] = bad ? __builtin_nanf("") : (mx > 0.f ? mx / (float)FIX_MAX : 0.f);
+      srsum[q] = rs;
+    }
+  }
+  __syncthreads();
+
+  // Phase 2.
+  float yacc[MR];
+#pragma unroll
+  for (int r = 0; r < MR; r++) yacc[r] = 0.f;
+  const int slice = blockIdx.y * 4 + wave;
+  for (int kg = slice, l = wave; kg < c4n; kg += nslices, l += 4) {
+    const uint4 *wp = wq + (((int64_t)cgi * c4n + kg) * 4) * 64 + lane;
+    uint32_t wv[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const uint4 w4 = wp[g * 64];
+      wv[g][0] = w4.x ^ 0x88888888u; wv[g][1] = w4.y ^ 0x88888888u;
+      wv[g][2] = w4.z ^ 0x88888888u; wv[g][3] = w4.w ^ 0x88888888u;
+    }
+    // One quantisation block at a time: dword (g, j) holds k = 32j + 8g + t,
+    // so block s covers j in [4s/QPG, 4(s+1)/QPG) for QPG <= 4 and, for
+    // QPG = 8, j = s/2 with g in {2(s%2), 2(s%2) + 1}.
+#pragma unroll
     for (int s = 0; s < QPG; s++) {
-      const int qbi = kg * QPG + s;
-      const int b = (int)(((int64_t)qbi * qb) / bs);
+      int acc[MR][4];
+#pragma unroll
+      for (int r = 0; r < MR; r++)
+#pragma unroll
+        for (int d = 0; d < 4; d++) acc[r][d] = 0;
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const bool mine = QPG == 8 ? (j == s / 2 && g / 2 == s % 2) : (j * QPG / 4 == s);
+          if (!mine) continue;
+          const int x = (int)wv[g][j];
+#pragma unroll
+          for (int r = 0; r < MR; r++) {
+            const uint4 dd =
+                *reinterpret_cast<const uint4 *>(&sdig[((r * nloc + l) * 4 + g) * 16 + j * 4]);
+            acc[r][0] = __builtin_amdgcn_sdot8((int)dd.x, x, acc[r][0], false);
+            acc[r][1] = __builtin_amdgcn_sdot8((int)dd.y, x, acc[r][1], false);
+            acc[r][2] = __builtin_amdgcn_sdot8((int)dd.z, x, acc[r][2], false);
+            acc[r][3] = __builtin_amdgcn_sdot8((int)dd.w, x, acc[r][3], false);
+          }
+        }
+      const int b = (kg * KGRP + s * (KGRP / QPG)) >> lbs;
       if (b >= nb) continue;  // k padding beyond the last block
       const float sc = scales[((int64_t)cgi * nb + b) * 64 + lane];
       int zc = 0;
@@ -259,11 +279,10 @@ __global__ __launch_bounds__(256) void k_gemv_dot8(
       }
 #pragma unroll
       for (int r = 0; r < MR; r++) {
-        const int comb =
-            ((acc[r][s][3] * 16 + acc[r][s][2]) * 16 + acc[r][s][1]) * 16 +
-            acc[r][s][0];
-        const float al = alpha[(int64_t)r * nqb + qbi];
-        const int R = rsum[(int64_t)r * nqb + qbi];
+        const int comb = ((acc[r][3] * 16 + acc[r][2]) * 16 + acc[r][1]) * 16 + acc[r][0];
+        const int q = (r * nloc + l) * QPG + s;
+        const float al = salpha[q];
+        const int R = srsum[q];
         float v;
         if (ZPK == 2)
           v = (float)comb + (8.f - zf) * (float)R;
@@ -273,7 +292,6 @@ __global__ __launch_bounds__(256) void k_gemv_dot8(
       }
     }
   }
-  __shared__ float red[4][MR][64];
 #pragma unroll
   for (int r = 0; r < MR; r++) red[wave][r][lane] = yacc[r];
   __syncthreads();
@@ -614,7 +632,8 @@ struct NbitsPlan {
   int path;  // 0 gemv, 1 mfma, 2 generic
   int64_t M;
   // gemv
-  int qpg = 1, qb = 128, nqb = 0, ksplit = 1, kps = 0;
+  int qpg = 1, qb = 128, nloc = 0, ksplit = 1, kps = 0;
+  size_t lds = 0;
   // mfma
   int64_t mpad = 0;
   size_t off_a = 0, off_b = 0, off_c = 0, off_d = 0, total = 0;
@@ -628,17 +647,19 @@ NbitsPlan plan_nbits(const mg_weight *w, int64_t M) {
     p.path = 0;
     p.qb = (int)std::min<int64_t>(d.bs, KGRP);
     p.qpg = KGRP / p.qb;
-    p.nqb = (int)(d.kpad / p.qb);
+    // Split K until ~2048 waves stream weights, then further until the
+    // workgroup's quantised activations fit LDS (M * nloc <= 64 k groups).
     const int64_t waves_per_slice = d.ng * 4;
     int64_t ks = (2048 + waves_per_slice - 1) / waves_per_slice;
     ks = std::min<int64_t>(ks, std::max<int64_t>(1, d.c4 / 4));
     ks = std::max<int64_t>(ks, 1);
+    auto nloc_of = [&](int64_t k) { return 4 * ((d.c4 + 4 * k - 1) / (4 * k)); };
+    while (M * nloc_of(ks) > 64) ks++;
     p.ksplit = (int)ks;
-    p.off_a = 0;  // digits: M * c4 * 64 dwords
-    p.off_b = mg_align(p.off_a + (size_t)M * d.c4 * 64 * 4);  // alpha
-    p.off_c = mg_align(p.off_b + (size_t)M * p.nqb * 4);      // rsum
-    p.off_d = mg_align(p.off_c + (size_t)M * p.nqb * 4);      // partials
-    p.total = mg_align(p.off_d + (p.ksplit > 1 ? (size_t)p.ksplit * M * d.ng * 64 * 4 : 0));
+    p.nloc = (int)nloc_of(ks);
+    p.lds = (size_t)M * p.nloc * (64 + 2 * p.qpg) * 4;
+    p.off_d = 0;  // partials
+    p.total = p.ksplit > 1 ? mg_align((size_t)p.ksplit * M * d.ng * 64 * 4) : 0;
   } else if (d.bs >= 32 && d.zp_kind != MG_ZP_FLOAT) {
     p.path = 1;
     const int64_t rows = 128;  // workgroup tile rows
@@ -662,33 +683,31 @@ NbitsPlan plan_nbits(const mg_weight *w, int64_t M) {
 }
 
 template <int MR, int QPG>
-void launch_gemv_zp(const mg_weight *w, int zpk, dim3 grid, hipStream_t st,
-                    const uint32_t *dig, const float *alpha, const int *rsum,
-                    float *y, float *part, int nqb) {
+void launch_gemv_zp(const mg_weight *w, const NbitsPlan &p, hipStream_t st, const float *a,
+                    int vec, float *y, float *part) {
   const mg_nbits_dev &d = w->nbits;
-  const int ncolp = (int)(d.ng * 64);
-#define MG_GEMV_ARGS                                                           \
-  reinterpret_cast<const uint4 *>(d.wq), d.scales, d.zp4, d.zpf, dig, alpha,   \
-      rsum, d.bias, y, part, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh,      \
-      (int)d.bs, nqb, ncolp
-  if (zpk == 0)
-    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, 0>), grid, dim3(256), 0, st, MG_GEMV_ARGS);
-  else if (zpk == 1)
-    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, 1>), grid, dim3(256), 0, st, MG_GEMV_ARGS);
+  const dim3 grid((unsigned)d.ng, (unsigned)p.ksplit);
+#define MG_GEMV_ARGS                                                                    \
+  a, w->K, vec, reinterpret_cast<const uint4 *>(d.wq), d.scales, d.zp4, d.zpf, d.bias, y, \
+      part, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), p.nloc,     \
+      (int)(d.ng * 64)
+  if (d.zp_kind == 0)
+    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, 0>), grid, dim3(256), p.lds, st, MG_GEMV_ARGS);
+  else if (d.zp_kind == 1)
+    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, 1>), grid, dim3(256), p.lds, st, MG_GEMV_ARGS);
   else
-    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, 2>), grid, dim3(256), 0, st, MG_GEMV_ARGS);
+    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, 2>), grid, dim3(256), p.lds, st, MG_GEMV_ARGS);
 #undef MG_GEMV_ARGS
 }
 
 template <int MR>
-void launch_gemv_q(const mg_weight *w, int qpg, int zpk, dim3 grid,
-                   hipStream_t st, const uint32_t *dig, const float *alpha,
-                   const int *rsum, float *y, float *part, int nqb) {
-  switch (qpg) {
-    case 1: launch_gemv_zp<MR, 1>(w, zpk, grid, st, dig, alpha, rsum, y, part, nqb); break;
-    case 2: launch_gemv_zp<MR, 2>(w, zpk, grid, st, dig, alpha, rsum, y, part, nqb); break;
-    case 4: launch_gemv_zp<MR, 4>(w, zpk, grid, st, dig, alpha, rsum, y, part, nqb); break;
-    default: launch_gemv_zp<MR, 8>(w, zpk, grid, st, dig, alpha, rsum, y, part, nqb); break;
+void launch_gemv_q(const mg_weight *w, const NbitsPlan &p, hipStream_t st, const float *a,
+                   int vec, float *y, float *part) {
+  switch (p.qpg) {
+    case 1: launch_gemv_zp<MR, 1>(w, p, st, a, vec, y, part); break;
+    case 2: launch_gemv_zp<MR, 2>(w, p, st, a, vec, y, part); break;
+    case 4: launch_gemv_zp<MR, 4>(w, p, st, a, vec, y, part); break;
+    default: launch_gemv_zp<MR, 8>(w, p, st, a, vec, y, part); break;
   }
 }
 
@@ -811,20 +830,13 @@ mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
   char *base = static_cast<char *>(ws);
   const int zpk = d.zp_kind;
   if (p.path == 0) {
-    uint32_t *dig = reinterpret_cast<uint32_t *>(base + p.off_a);
-    float *alpha = reinterpret_cast<float *>(base + p.off_b);
-    int *rsum = reinterpret_cast<int *>(base + p.off_c);
     float *part = p.ksplit > 1 ? reinterpret_cast<float *>(base + p.off_d) : nullptr;
-    const int64_t pairs = M * p.nqb;
-    hipLaunchKernelGGL(k_adigits, dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, st,
-                       a_dev, M, w->K, p.qb, p.nqb, (int)d.c4, dig, alpha, rsum);
-    MG_TRY(mg_launch_check("k_adigits"));
-    const dim3 grid((unsigned)d.ng, (unsigned)p.ksplit);
+    const int vec = (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 && w->K % 4 == 0) ? 1 : 0;
     switch (M) {
-      case 1: launch_gemv_q<1>(w, p.qpg, zpk, grid, st, dig, alpha, rsum, y_dev, part, p.nqb); break;
-      case 2: launch_gemv_q<2>(w, p.qpg, zpk, grid, st, dig, alpha, rsum, y_dev, part, p.nqb); break;
-      case 3: launch_gemv_q<3>(w, p.qpg, zpk, grid, st, dig, alpha, rsum, y_dev, part, p.nqb); break;
-      default: launch_gemv_q<4>(w, p.qpg, zpk, grid, st, dig, alpha, rsum, y_dev, part, p.nqb); break;
+      case 1: launch_gemv_q<1>(w, p, st, a_dev, vec, y_dev, part); break;
+      case 2: launch_gemv_q<2>(w, p, st, a_dev, vec, y_dev, part); break;
+      case 3: launch_gemv_q<3>(w, p, st, a_dev, vec, y_dev, part); break;
+      default: launch_gemv_q<4>(w, p, st, a_dev, vec, y_dev, part); break;
     }
     MG_TRY(mg_launch_check("k_gemv_dot8"));
     if (p.ksplit > 1) {
