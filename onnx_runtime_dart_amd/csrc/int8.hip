@@ -12,10 +12,26 @@
 // Every term is int32 arithmetic; wrap-around cancels, so the result is exact
 // whenever the true value fits int32 (always for K <= 33025).
 //
-// Fragment layouts (v_mfma_i32_16x16x64_i8; lane = 16*g + i):
-//   A: [batch][m16][k64][lane][16 B]  lane holds row i, k = 64*k64 + 16*g + 0..15
-//   B: [batch][n16][k64][lane][16 B]  lane holds col i, same k
-// Both come from small prepack kernels (B once on upload for weights).
+// v_mfma_i32_32x32x32_i8 operands: lane l holds row (A) or column (B) l % 32
+// and 16 bytes along k; the 32x32 int32 result has lane l at column l % 32
+// and rows 8 (v / 4) + 4 (l / 32) + v % 4, v < 16.  The sum over k does not
+// care which 32 k a step covers as long as A and B agree, so within each
+// 128-k stage step q gives lane l the k = 64 (l / 32) + 16 q + 0..15: a lane
+// reads 64 contiguous bytes of its A row per stage (whole cache lines per
+// workgroup) instead of four scattered 16-byte pieces.
+//   B is prepacked once per weight in that order: bfrag[n32][4 stage + q]
+//     [lane] (uint4), re-centred, zero outside [K, N]; N padded to 128 and
+//     K to 256 (one LDS stage).
+//   A is read in place from row-major [rows, K] when K % 256 == 0 and the
+//     base is 16-byte aligned, else first copied into a padded [rows, kpad]
+//     buffer whose pad bytes re-centre to zero.
+// Workgroup tile: 128*WM rows x 128 columns, 4 waves, wave w owning rows
+// [32*WM*w, +32*WM).  B moves global -> LDS directly (global_load_lds) in
+// stages of 256 k, double buffered, one barrier per stage; its fragments are
+// read from LDS a step ahead.  A goes straight to registers, each register
+// reloaded four steps ahead right after its step; rowsum(A') is accumulated
+// alongside with v_dot4_i32_i8.  The epilogue restages each 32-row tile in
+// LDS and writes whole 16-byte row pieces.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -25,70 +41,32 @@
 namespace {
 
 typedef int int4v __attribute__((ext_vector_type(4)));
+typedef int int16v __attribute__((ext_vector_type(16)));
 
-// A (u8 or i8, [rows, K] per batch with rows = M) -> fragments, ca, rowsum.
-// One workgroup per (batch, 16-row subtile).
-__global__ __launch_bounds__(256) void k_i8_prep_a(
-    const uint8_t *__restrict__ a, int a_signed, int64_t M, int64_t K,
-    int m16n, int kq, int za_scalar, const int32_t *__restrict__ za,
-    int za_len, int4v *__restrict__ frag, int32_t *__restrict__ ca,
-    int32_t *__restrict__ rowsum) {
-  const int64_t bi = blockIdx.y;
-  const int sub = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 15, g = lane >> 4;
-  const int64_t row = (int64_t)sub * 16 + r;
-  const uint8_t *arow = a + (bi * M + row) * K;
-  const int flip = a_signed ? 0 : 0x80;
-  int s = 0;
-  for (int q = wave; q < kq; q += 4) {
-    union { int4v v; int8_t b[16]; } u;
-    for (int e = 0; e < 16; e++) {
-      const int64_t k = (int64_t)q * 64 + 16 * g + e;
-      int8_t v = 0;
-      if (row < M && k < K) v = (int8_t)(arow[k] ^ flip);
-      u.b[e] = v;
-      s += v;
-    }
-    frag[(((bi * m16n + sub) * kq + q) * 64) + lane] = u.v;
-  }
-  __shared__ int red[4][64];
-  red[wave][lane] = s;
-  __syncthreads();
-  if (threadIdx.x < 16) {
-    int t = 0;
-    for (int w = 0; w < 4; w++)
-      for (int gg = 0; gg < 4; gg++) t += red[w][gg * 16 + threadIdx.x];
-    const int64_t rr = (int64_t)sub * 16 + threadIdx.x;
-    const int64_t slot = bi * m16n * 16 + rr;
-    const int oa = a_signed ? 0 : 128;
-    int z = za_scalar;
-    if (za && za_len > 0) z = za[rr % za_len];
-    ca[slot] = oa - z;
-    rowsum[slot] = t;
-  }
-}
+constexpr int TN = 128;  // workgroup tile columns
+constexpr int QS = 8;    // 32-k MFMA steps per LDS stage (256 k)
+constexpr int RA = 4;    // A register ring: steps loaded ahead of use
 
-// B (u8 or i8, [K, N] per batch) -> fragments; one thread per 16-byte
-// fragment slot.
+// B (u8 or i8, [K, N] per batch) -> fragments bfrag[batch][n32][q][lane].
 __global__ __launch_bounds__(256) void k_i8_prep_b(
     const uint8_t *__restrict__ b, int b_signed, int64_t K, int64_t N,
-    int n16n, int kq, int4v *__restrict__ frag) {
+    int n32n, int kqp, int4v *__restrict__ frag) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t per_batch = (int64_t)n16n * kq * 64;
+  const int64_t per_batch = (int64_t)n32n * kqp * 64;
   const int64_t bi = blockIdx.y;
   if (idx >= per_batch) return;
   const int lane = (int)(idx & 63);
   const int64_t t = idx >> 6;
-  const int q = (int)(t % kq);
-  const int64_t sub = t / kq;
-  const int c = lane & 15, g = lane >> 4;
-  const int64_t col = sub * 16 + c;
+  const int q = (int)(t % kqp);
+  const int64_t n32 = t / kqp;
+  const int64_t col = n32 * 32 + (lane & 31);
+  const int64_t kb = (int64_t)(q >> 2) * 128 + 64 * (lane >> 5) + 16 * (q & 3);
   const uint8_t *bb = b + bi * K * N;
   const int flip = b_signed ? 0 : 0x80;
   union { int4v v; int8_t x[16]; } u;
+#pragma unroll
   for (int e = 0; e < 16; e++) {
-    const int64_t k = (int64_t)q * 64 + 16 * g + e;
+    const int64_t k = kb + e;
     u.x[e] = (col < N && k < K) ? (int8_t)(bb[k * N + col] ^ flip) : (int8_t)0;
   }
   frag[bi * per_batch + idx] = u.v;
@@ -112,95 +90,347 @@ __global__ __launch_bounds__(256) void k_i8_colsum(
   cb[bi * npad + col] = (b_signed ? 0 : 128) - z;
 }
 
-// y = sum A'B' + cb*rowsum + ca*colsum + K*ca*cb; REQ: requantise to bytes.
-// Workgroup: 4 waves as 2 x 2; wave tile (16*WMS) x 64.
-template <int WMS, int REQ>
-__global__ __launch_bounds__(256) void k_i8_gemm(
-    const int4v *__restrict__ afrag, const int32_t *__restrict__ ca,
-    const int32_t *__restrict__ rowsum, const int4v *__restrict__ bfrag,
-    const int32_t *__restrict__ colsum, const int32_t *__restrict__ cb,
-    void *__restrict__ y, int64_t M, int64_t N, int64_t K, int m16n, int n16n,
-    int kq, int64_t a_bstride, int64_t b_bstride, int64_t npad_b, float mult,
-    int y_zp, int lo, int hi) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int64_t bz = blockIdx.z;
-  const int sub0 = (blockIdx.y * 2 + wm) * WMS;
-  const int nsub0 = (blockIdx.x * 2 + wn) * 4;
-  const int4v *ab = afrag + bz * a_bstride;
-  const int4v *bb = bfrag + bz * b_bstride;
-  int4v acc[WMS][4];
+// 16 bytes per lane global -> LDS (gfx950 global_load_lds_dwordx4): lane i's
+// data lands at LDS byte address lds + 16 i (lds wave-uniform).  Issued as
+// asm so that the compiler's own waits do not treat it as a write to every
+// LDS location (it would otherwise wait for it before any LDS read); callers
+// wait for it themselves (vmcnt) before the barrier that publishes the data.
+__device__ inline void lds_copy16(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(g)
+               : "memory", "m0");
+}
+
+// A (u8 or i8, [M, K] per batch, row pitch lda) -> fragments
+// afrag[batch][m32][q][lane] (the order the GEMM loads them: 1 KB per wave
+// load), re-centred to signed, zero outside [M, K]; plus rowsum(A') and
+// ca = oa - aZp per row.  One workgroup per (32-row tile, batch).
+__global__ __launch_bounds__(256) void k_i8_prep_a(
+    const uint8_t *__restrict__ a, int64_t lda, int64_t a_bs, int a_signed, int vec,
+    int64_t M, int64_t K, int kqp, int m32n, int za_scalar, const int32_t *__restrict__ za,
+    int za_len, int4v *__restrict__ afrag, int32_t *__restrict__ rowsum,
+    int32_t *__restrict__ ca) {
+  const int m32 = blockIdx.x;
+  const int64_t bz = blockIdx.y;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t row = (int64_t)m32 * 32 + r;
+  const uint8_t *ar = a + bz * a_bs + row * lda;
+  const uint32_t flip = a_signed ? 0u : 0x80808080u;
+  int4v *out = afrag + ((bz * m32n + m32) * (int64_t)kqp) * 64 + lane;
+  int s = 0;
+  for (int q = wave; q < kqp; q += 4) {
+    const int64_t k0 = (int64_t)(q >> 2) * 128 + 64 * h + 16 * (q & 3);
+    int4v v;
+    if (row < M && vec && k0 + 16 <= K) {
+      v = *reinterpret_cast<const int4v *>(ar + k0);
+      v.x ^= flip; v.y ^= flip; v.z ^= flip; v.w ^= flip;
+    } else {
+      union { int4v v; uint8_t x[16]; } u;
 #pragma unroll
-  for (int i = 0; i < WMS; i++)
-#pragma unroll
-    for (int n = 0; n < 4; n++) acc[i][n] = (int4v){0, 0, 0, 0};
-  for (int q = 0; q < kq; q++) {
-    int4v bf[4];
-#pragma unroll
-    for (int n = 0; n < 4; n++) {
-      const int ns = nsub0 + n;
-      bf[n] = ns < n16n ? bb[((int64_t)ns * kq + q) * 64 + lane] : (int4v){0, 0, 0, 0};
+      for (int e = 0; e < 16; e++)
+        u.x[e] = (row < M && k0 + e < K) ? (uint8_t)(ar[k0 + e] ^ (flip & 0xff)) : (uint8_t)0;
+      v = u.v;
     }
-#pragma unroll
-    for (int i = 0; i < WMS; i++) {
-      const int ms = sub0 + i;
-      const int4v af = ms < m16n ? ab[((int64_t)ms * kq + q) * 64 + lane] : (int4v){0, 0, 0, 0};
-#pragma unroll
-      for (int n = 0; n < 4; n++)
-        acc[i][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[n], acc[i][n], 0, 0, 0);
-    }
+    s = __builtin_amdgcn_sdot4(v.x, 0x01010101, s, false);
+    s = __builtin_amdgcn_sdot4(v.y, 0x01010101, s, false);
+    s = __builtin_amdgcn_sdot4(v.z, 0x01010101, s, false);
+    s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
+    out[(int64_t)q * 64] = v;
   }
-  const int cl = lane & 15, lg = lane >> 4;
-  const int64_t arow_base = bz * (a_bstride / ((int64_t)kq * 64)) * 16;  // rows of this batch's A
+  __shared__ int red[4][64];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (t < 32) {
+    int tot = 0;
 #pragma unroll
-  for (int i = 0; i < WMS; i++) {
+    for (int w = 0; w < 4; w++) tot += red[w][t] + red[w][t + 32];
+    const int64_t rr = (int64_t)m32 * 32 + t;
+    const int64_t slot = bz * m32n * 32 + rr;
+    rowsum[slot] = tot;
+    const int z = (za && za_len > 0) ? za[rr % za_len] : za_scalar;
+    ca[slot] = (a_signed ? 0 : 128) - z;
+  }
+}
+
+struct I8Epi {
+  const int32_t *colsum, *cb;  // [b batch?][npad]
+  int64_t cs_bs;               // colsum/cb batch stride (0 = shared)
+  const int32_t *rowsum, *ca;  // [a batch?][mpad]
+  int64_t rs_bs;               // rowsum/ca batch stride (0 = shared)
+  int K;
+  int y_vec;  // output base 16-byte aligned (always for the partials)
+  float mult;
+  int y_zp, lo, hi;
+};
+
+// Final value of one output element and its store.
+template <int REQ>
+__device__ inline void i8_finish(void *y, int64_t o, int32_t acc, int32_t rs, int32_t cav,
+                                 int32_t cs, int32_t cbv, const I8Epi &e) {
+  const uint32_t v = (uint32_t)acc + (uint32_t)cbv * (uint32_t)rs + (uint32_t)cav * (uint32_t)cs +
+                     (uint32_t)e.K * (uint32_t)cav * (uint32_t)cbv;
+  const int32_t vi = (int32_t)v;
+  if (REQ) {
+    const float p = (float)((double)vi * (double)e.mult);
+    int qv = (int)rintf(p) + e.y_zp;
+    qv = qv < e.lo ? e.lo : (qv > e.hi ? e.hi : qv);
+    static_cast<uint8_t *>(y)[o] = (uint8_t)qv;
+  } else {
+    static_cast<int32_t *>(y)[o] = vi;
+  }
+}
+
+// MODE 0: int32 output, 1: requantised bytes, 2: raw partial sums (split K,
+// k_i8_reduce finishes).
+// Grid: x = tiles in XCD-aware order (workgroup L runs on XCD L % 8; all row
+// tiles of a column tile share L % 8, so its B stays in one L2), y = k
+// splits of sps stages each, z = batch.
+template <int WM, int MODE>
+__global__ __launch_bounds__(256, 2) void k_i8_gemm(
+    const int4v *__restrict__ afrag, int64_t a_bs, const int4v *__restrict__ bfrag,
+    int64_t b_bs, void *__restrict__ y, I8Epi e, int M, int N, int kqp, int mtiles,
+    int ntiles, int sps) {
+  // B double buffer [2][n32][q][lane] (64 KB); afterwards the int32
+  // epilogue stages, [32 rows][128 + 4 pad] per wave.
+  constexpr int SROW = TN + 4;
+  __shared__ int4v smem[4 * 32 * SROW / 4];
+  int4v *bl0 = smem, *bl1 = smem + 4 * QS * 64;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int L = blockIdx.x;
+  const int xcd = L & 7, qq = L >> 3;
+  const int mt = qq % mtiles;
+  const int nt = (qq / mtiles) * 8 + xcd;
+  if (nt >= ntiles) return;
+  const int64_t bz = blockIdx.z;
+  const int nstage = kqp / QS;
+  const int s0 = blockIdx.y * sps, s1 = min(nstage, s0 + sps);
+  const int lc = lane & 31, lh = lane >> 5;
+
+  const int4v *ap[WM];
+#pragma unroll
+  for (int mi = 0; mi < WM; mi++)
+    ap[mi] = afrag + bz * a_bs + ((int64_t)(mt * 4 * WM + wave * WM + mi) * kqp) * 64 + lane;
+  // B stage s -> LDS: 32 fragment blocks of 1 KB, 8 per wave.
+  const int4v *bbase = bfrag + bz * b_bs + ((int64_t)nt * 4 * kqp) * 64 + lane;
+  auto stage_b = [&](int s, int4v *dst) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int u = wave + 4 * i;  // block = (n32 = u / QS, q = u % QS)
+      lds_copy16(bbase + ((int64_t)(u / QS) * kqp + s * QS + (u % QS)) * 64,
+                 (uint32_t)reinterpret_cast<uintptr_t>(&dst[u * 64]));
+    }
+  };
+
+  int16v acc[WM][4];
+#pragma unroll
+  for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+    for (int n = 0; n < 4; n++) acc[mi][n] = (int16v){};
+
+  // ar[j % RA]: A of step j, reloaded with step j + RA right after use
+  // (clamped to the split's last step; unused there).
+  const int jlast = s1 * QS - 1;
+  int4v ar[RA][WM];
+  stage_b(s0, bl0);
+#pragma unroll
+  for (int j = 0; j < RA; j++)
+#pragma unroll
+    for (int mi = 0; mi < WM; mi++) ar[j][mi] = ap[mi][(int64_t)(s0 * QS + j) * 64];
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // One stage: MFMAs on `cur` while the next stage's B is copied into `nxt`.
+  auto run_stage = [&](int s, const int4v *cur, int4v *nxt) {
+    if (s + 1 < s1) stage_b(s + 1, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    int4v b[4];
+#pragma unroll
+    for (int n = 0; n < 4; n++) b[n] = cur[(n * QS) * 64 + lane];
+#pragma unroll
+    for (int q = 0; q < QS; q++) {
+      int4v bnx[4];
+      if (q + 1 < QS) {
+#pragma unroll
+        for (int n = 0; n < 4; n++) bnx[n] = cur[(n * QS + q + 1) * 64 + lane];
+      }
+#pragma unroll
+      for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+        for (int n = 0; n < 4; n++)
+          acc[mi][n] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[n], ar[q % RA][mi], acc[mi][n], 0, 0, 0);
+      const int jn = min(s * QS + q + RA, jlast);
+#pragma unroll
+      for (int mi = 0; mi < WM; mi++) ar[q % RA][mi] = ap[mi][(int64_t)jn * 64];
+      if (q + 1 < QS) {
+#pragma unroll
+        for (int n = 0; n < 4; n++) b[n] = bnx[n];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // The next stage's B (issued before this stage's 8 * WM A loads) has
+    // landed in LDS once at most 8 * WM loads remain; then all waves meet.
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(8 * WM) : "memory");
+  };
+  for (int s = s0; s < s1; s += 2) {
+    run_stage(s, bl0, bl1);
+    if (s + 1 < s1) run_stage(s + 1, bl1, bl0);
+  }
+
+  // Epilogue.  With B as the MFMA's first operand each accumulator tile is
+  // Y^T: lane l holds row l % 32 of the tile and, for g = 0..3, the four
+  // consecutive columns 8 g + 4 (l / 32) + 0..3 (acc[..][4 g + i]).  Per
+  // element v = acc + cb*(rowsum + K*ca) + ca*colsum in int32 wrap-around
+  // (MODE 2: acc alone).  Requantised bytes (MODE 1) are stored from there;
+  // int32 values go through the wave's LDS stage (rows padded by 16 bytes
+  // against bank conflicts) and leave as whole 16-byte row pieces.
+  const int64_t yb = (int64_t)bz * M;  // first output row of this batch
+  const bool vec_ok = (N % 4) == 0 && e.y_vec;
+  int32_t *stage = reinterpret_cast<int32_t *>(smem) + wave * (32 * SROW);
+#pragma unroll
+  for (int mi = 0; mi < WM; mi++) {
+    const int rbase = (mt * 4 * WM + wave * WM + mi) * 32;
+    const int row = rbase + lc;
+    uint32_t rk = 0, cav = 0;
+    if (MODE != 2) {
+      const int32_t rs = e.rowsum[bz * e.rs_bs + row];
+      cav = (uint32_t)e.ca[bz * e.rs_bs + row];
+      rk = (uint32_t)rs + (uint32_t)e.K * cav;
+    }
 #pragma unroll
     for (int n = 0; n < 4; n++) {
-      const int64_t col = (int64_t)(nsub0 + n) * 16 + cl;
-      if (col >= N) continue;
-      const int32_t cs = colsum[bz * npad_b * (b_bstride ? 1 : 0) + col];
-      const int32_t cbv = cb[bz * npad_b * (b_bstride ? 1 : 0) + col];
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int64_t row = (int64_t)(sub0 + i) * 16 + 4 * lg + r;
-        if (row >= M) continue;
-        const int64_t slot = arow_base + row;
-        const int32_t cav = ca[slot];
-        const uint32_t v = (uint32_t)acc[i][n][r] + (uint32_t)cbv * (uint32_t)rowsum[slot] +
-                           (uint32_t)cav * (uint32_t)cs +
-                           (uint32_t)K * (uint32_t)cav * (uint32_t)cbv;
-        const int32_t vi = (int32_t)v;
-        const int64_t o = (bz * M + row) * N + col;
-        if (REQ) {
-          const float p = (float)((double)vi * (double)mult);
-          int qv = (int)rintf(p) + y_zp;
-          qv = qv < lo ? lo : (qv > hi ? hi : qv);
-          static_cast<uint8_t *>(y)[o] = (uint8_t)qv;
+      for (int g = 0; g < 4; g++) {
+        const int cl = n * 32 + 8 * g + 4 * lh;  // column within the tile
+        const int col = nt * TN + cl;           // < npad: arrays in bounds
+        int4v v;
+        if (MODE == 2) {
+          v = (int4v){acc[mi][n][4 * g], acc[mi][n][4 * g + 1], acc[mi][n][4 * g + 2],
+                      acc[mi][n][4 * g + 3]};
         } else {
-          static_cast<int32_t *>(y)[o] = vi;
+          const int4v cbv = *reinterpret_cast<const int4v *>(&e.cb[bz * e.cs_bs + col]);
+          const int4v csv = *reinterpret_cast<const int4v *>(&e.colsum[bz * e.cs_bs + col]);
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            v[i] = (int32_t)((uint32_t)acc[mi][n][4 * g + i] + (uint32_t)cbv[i] * rk +
+                             cav * (uint32_t)csv[i]);
+        }
+        if (MODE == 1) {
+          if (row >= M || col >= N) continue;
+          uint32_t pk = 0;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float pf = (float)((double)v[i] * (double)e.mult);
+            int qv = (int)rintf(pf) + e.y_zp;
+            qv = qv < e.lo ? e.lo : (qv > e.hi ? e.hi : qv);
+            pk |= (uint32_t)(qv & 255) << (8 * i);
+          }
+          uint8_t *yp = static_cast<uint8_t *>(y) + (yb + row) * N + col;
+          if (vec_ok && col + 3 < N) {
+            *reinterpret_cast<uint32_t *>(yp) = pk;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              if (col + i < N) yp[i] = (uint8_t)(pk >> (8 * i));
+          }
+        } else {
+          *reinterpret_cast<int4v *>(&stage[lc * SROW + cl]) = v;
+        }
+      }
+    }
+    if (MODE != 1) {
+      // Same-wave LDS traffic completes in order: no barrier between this
+      // wave's stage writes and its reads.
+      const int c4 = lane & 31;  // 4-column piece of the 128-column row
+      const int col = nt * TN + 4 * c4;
+      const bool full = vec_ok && col + 3 < N;
+#pragma unroll 4
+      for (int it = 0; it < 16; it++) {
+        const int r = 2 * it + lh;
+        const int rr = rbase + r;
+        if (rr >= M) continue;
+        const int4v v4 = *reinterpret_cast<const int4v *>(&stage[r * SROW + 4 * c4]);
+        int32_t *yp = static_cast<int32_t *>(y) +
+                      (MODE == 2 ? (int64_t)blockIdx.y * gridDim.z * M * N : 0) +
+                      (yb + rr) * N + col;
+        if (full) {
+          __builtin_nontemporal_store(v4, reinterpret_cast<int4v *>(yp));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            if (col + i < N) yp[i] = v4[i];
         }
       }
     }
   }
 }
 
+// Split-K finish (and the K = 0 case, ks = 0): sums the partials of every
+// split and applies the epilogue; one thread per output element.
+template <int REQ>
+__global__ __launch_bounds__(256) void k_i8_reduce(const int32_t *__restrict__ part,
+                                                   void *__restrict__ y, I8Epi e, int64_t batch,
+                                                   int64_t M, int64_t N, int ks) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t tot = batch * M * N;
+  if (idx >= tot) return;
+  const int64_t col = idx % N, brow = idx / N, bz = brow / M, row = brow % M;
+  uint32_t s = 0;
+  for (int k = 0; k < ks; k++) s += (uint32_t)part[(int64_t)k * tot + idx];
+  const int64_t rslot = bz * e.rs_bs + row;
+  i8_finish<REQ>(y, idx, (int32_t)s, e.rowsum[rslot], e.ca[rslot], e.colsum[bz * e.cs_bs + col],
+                 e.cb[bz * e.cs_bs + col], e);
+}
+
+struct I8Plan {
+  int wm, mtiles, m32n, ntiles, ks, sps, nstage;
+  int64_t kpad, mpad;
+  size_t off_a, off_rs, off_ca, off_za, off_part, total;
+};
+
+// a_batch: batches of A; batch: output batches (grid z).
+I8Plan plan_i8(int64_t a_batch, int64_t batch, int64_t M, int64_t K, int64_t N) {
+  I8Plan p;
+  p.kpad = (K + 255) / 256 * 256;
+  p.nstage = (int)(p.kpad / 256);
+  p.wm = M > 128 ? 2 : 1;
+  p.mtiles = (int)((M + 128 * p.wm - 1) / (128 * p.wm));
+  p.m32n = p.mtiles * 4 * p.wm;
+  p.mpad = (int64_t)p.m32n * 32;
+  p.ntiles = (int)((N + TN - 1) / TN);
+  // Split K until ~2 workgroups per CU, keeping >= 2 stages per split.
+  const int64_t tiles = (int64_t)p.mtiles * p.ntiles * batch;
+  int ks = 1;
+  while (tiles * ks * 2 <= 512 && p.nstage / (ks * 2) >= 2) ks *= 2;
+  p.sps = (p.nstage + ks - 1) / ks;
+  p.ks = (p.nstage + p.sps - 1) / p.sps;
+  p.off_a = 0;
+  p.off_rs = mg_align(p.off_a + (size_t)a_batch * p.mpad * p.kpad);
+  p.off_ca = mg_align(p.off_rs + (size_t)a_batch * p.mpad * 4);
+  p.off_za = mg_align(p.off_ca + (size_t)a_batch * p.mpad * 4);
+  p.off_part = mg_align(p.off_za + (size_t)(M + 1) * 4);
+  p.total = mg_align(p.off_part + (p.ks > 1 ? (size_t)p.ks * batch * M * N * 4 : 0));
+  return p;
+}
+
 }  // namespace
 
 // Weight arrays (bq fragments, colsum, cb) laid out in one allocation.
 size_t mg_int8_weight_ws_bytes(int64_t K, int64_t N) {
-  const int64_t kq = (K + 63) / 64, n16 = (N + 15) / 16;
-  return mg_align((size_t)n16 * kq * 64 * 16) + 2 * mg_align((size_t)n16 * 16 * 4);
+  const int64_t kqp = (K + 255) / 256 * 8, n32 = (N + 127) / 128 * 4;
+  return mg_align((size_t)n32 * kqp * 64 * 16) + 2 * mg_align((size_t)n32 * 32 * 4);
 }
 
 static void int8_carve(mg_weight *w, void *base) {
-  const int64_t kq = (w->K + 63) / 64, n16 = (w->N + 15) / 16;
+  const int64_t kqp = (w->K + 255) / 256 * 8, n32 = (w->N + 127) / 128 * 4;
   char *p = static_cast<char *>(base);
-  w->i8.kpad = kq * 64;
-  w->i8.npad = n16 * 16;
+  w->i8.kpad = kqp * 32;
+  w->i8.npad = n32 * 32;
   w->i8.bq = reinterpret_cast<int8_t *>(p);
-  p += mg_align((size_t)n16 * kq * 64 * 16);
+  p += mg_align((size_t)n32 * kqp * 64 * 16);
   w->i8.colsum = reinterpret_cast<int32_t *>(p);
-  p += mg_align((size_t)n16 * 16 * 4);
+  p += mg_align((size_t)n32 * 32 * 4);
   w->i8.cb = reinterpret_cast<int32_t *>(p);
 }
 
@@ -211,7 +441,7 @@ mg_status mg_int8_prepack_dev(mg_ctx *ctx, mg_weight *w, const void *b_dev,
   int8_carve(w, ws_weight);
   w->i8.b_signed = b_signed;
   const int64_t K = w->K, N = w->N;
-  const int kq = (int)(w->i8.kpad / 64), n16 = (int)(w->i8.npad / 16);
+  const int kqp = (int)(w->i8.kpad / 32), n32 = (int)(w->i8.npad / 32);
   hipStream_t st = ctx->stream;
   int zb_scalar = 0;
   const int32_t *zb_dev = nullptr;
@@ -219,15 +449,15 @@ mg_status mg_int8_prepack_dev(mg_ctx *ctx, mg_weight *w, const void *b_dev,
   if (b_zp && b_zp_len == 1) {
     zb_scalar = b_zp[0];
   } else if (b_zp && b_zp_len > 1) {
-    // Per-column zero points travel through the tail of the cb array region:
-    // write them into cb first, then the colsum kernel reads them back.
+    // Per-column zero points travel through the cb array: written there
+    // first, then read back by the colsum kernel (one thread per column).
     MG_HIP(hipMemcpyAsync(w->i8.cb, b_zp, (size_t)b_zp_len * 4, hipMemcpyHostToDevice, st));
     zb_dev = w->i8.cb;
     zb_len = (int)b_zp_len;
   }
-  const int64_t slots = (int64_t)n16 * kq * 64;
+  const int64_t slots = (int64_t)n32 * kqp * 64;
   hipLaunchKernelGGL(k_i8_prep_b, dim3((unsigned)((slots + 255) / 256), 1), dim3(256), 0, st,
-                     static_cast<const uint8_t *>(b_dev), b_signed, K, N, n16, kq,
+                     static_cast<const uint8_t *>(b_dev), b_signed, K, N, n32, kqp,
                      reinterpret_cast<int4v *>(w->i8.bq));
   MG_TRY(mg_launch_check("k_i8_prep_b"));
   hipLaunchKernelGGL(k_i8_colsum, dim3((unsigned)((w->i8.npad + 255) / 256), 1), dim3(256), 0,
@@ -267,59 +497,95 @@ void mg_int8_free(mg_weight *w) {
 }
 
 size_t mg_int8_ws_bytes(const mg_weight *w, int64_t rows) {
-  const int64_t kq = w->i8.kpad / 64;
-  const int64_t m16 = (rows + 15) / 16;
-  return mg_align((size_t)m16 * kq * 64 * 16) + 2 * mg_align((size_t)m16 * 16 * 4) + 256;
+  return plan_i8(1, 1, rows, w->K, w->N).total;
 }
 
-// Shared launcher.  a_batch/b_batch: 1 or batch; rows per batch = M.
+// Shared launcher.  a_batch/b_batch: 1 or batch; rows per batch = M.  bq,
+// colsum, cb: prepacked B (b_batch copies, npad columns each).
 static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsum,
                              const int32_t *cb, int64_t npad, int64_t b_batch,
                              const void *a_dev, int32_t a_signed, int64_t a_batch,
                              int64_t M, int64_t N, int64_t K, const int32_t *a_zp,
                              int64_t a_zp_len, const mg_requant *rq, void *y_dev,
                              void *ws) {
-  const int64_t kq = (K + 63) / 64, m16 = (M + 15) / 16, n16 = npad / 16;
+  if (M == 0 || N == 0) return MG_OK;
+  const int64_t batch = a_batch > b_batch ? a_batch : b_batch;
+  const I8Plan p = plan_i8(a_batch, batch, M, K, N);
   hipStream_t st = ctx->stream;
-  char *p = static_cast<char *>(ws);
-  int4v *afrag = reinterpret_cast<int4v *>(p);
-  p += mg_align((size_t)a_batch * m16 * kq * 64 * 16);
-  int32_t *ca = reinterpret_cast<int32_t *>(p);
-  p += mg_align((size_t)a_batch * m16 * 16 * 4);
-  int32_t *rowsum = reinterpret_cast<int32_t *>(p);
-  p += mg_align((size_t)a_batch * m16 * 16 * 4);
-  int32_t *za_dev = reinterpret_cast<int32_t *>(p);
+  char *base = static_cast<char *>(ws);
+  int4v *afrag = reinterpret_cast<int4v *>(base + p.off_a);
+  int32_t *rowsum = reinterpret_cast<int32_t *>(base + p.off_rs);
+  int32_t *ca = reinterpret_cast<int32_t *>(base + p.off_ca);
   int za_scalar = 0, za_len = 0;
+  const int32_t *za = nullptr;
   if (a_zp && a_zp_len == 1) {
     za_scalar = a_zp[0];
   } else if (a_zp && a_zp_len > 1) {
-    MG_HIP(hipMemcpyAsync(za_dev, a_zp, (size_t)a_zp_len * 4, hipMemcpyHostToDevice, st));
+    int32_t *zd = reinterpret_cast<int32_t *>(base + p.off_za);
+    MG_HIP(hipMemcpyAsync(zd, a_zp, (size_t)a_zp_len * 4, hipMemcpyHostToDevice, st));
+    za = zd;
     za_len = (int)a_zp_len;
   }
-  hipLaunchKernelGGL(k_i8_prep_a, dim3((unsigned)m16, (unsigned)a_batch), dim3(256), 0, st,
-                     static_cast<const uint8_t *>(a_dev), a_signed, M, K, (int)m16, (int)kq,
-                     za_scalar, za_len ? za_dev : nullptr, za_len, afrag, ca, rowsum);
+  const int kqp = p.nstage * QS;
+  const int vec = (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 && K % 16 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(k_i8_prep_a, dim3((unsigned)p.m32n, (unsigned)a_batch), dim3(256), 0, st,
+                     static_cast<const uint8_t *>(a_dev), K, M * K, a_signed, vec, M, K, kqp,
+                     p.m32n, za_scalar, za, za_len, afrag, rowsum, ca);
   MG_TRY(mg_launch_check("k_i8_prep_a"));
-  const int64_t batch = a_batch > b_batch ? a_batch : b_batch;
-  const int wms = M <= 16 ? 1 : 2;
-  const dim3 grid((unsigned)((n16 + 7) / 8), (unsigned)((m16 + 2 * wms - 1) / (2 * wms)),
-                  (unsigned)batch);
-  const int64_t a_bs = a_batch > 1 ? m16 * kq * 64 : 0;
-  const int64_t b_bs = b_batch > 1 ? n16 * kq * 64 : 0;
-  const float mult = rq ? rq->mult : 0.f;
-  const int yz = rq ? rq->y_zp : 0, lo = rq ? rq->lo : 0, hi = rq ? rq->hi : 0;
-#define MG_I8_ARGS                                                                  \
-  afrag, ca, rowsum, reinterpret_cast<const int4v *>(bq), colsum, cb, y_dev, M, N, K, \
-      (int)m16, (int)n16, (int)kq, a_bs, b_bs, npad, mult, yz, lo, hi
-  if (wms == 1) {
-    if (rq) hipLaunchKernelGGL((k_i8_gemm<1, 1>), grid, dim3(256), 0, st, MG_I8_ARGS);
-    else hipLaunchKernelGGL((k_i8_gemm<1, 0>), grid, dim3(256), 0, st, MG_I8_ARGS);
-  } else {
-    if (rq) hipLaunchKernelGGL((k_i8_gemm<2, 1>), grid, dim3(256), 0, st, MG_I8_ARGS);
-    else hipLaunchKernelGGL((k_i8_gemm<2, 0>), grid, dim3(256), 0, st, MG_I8_ARGS);
+  I8Epi e{};
+  e.colsum = colsum;
+  e.cb = cb;
+  e.cs_bs = b_batch > 1 ? npad : 0;
+  e.rowsum = rowsum;
+  e.ca = ca;
+  e.rs_bs = a_batch > 1 ? p.mpad : 0;
+  e.K = (int)K;
+  if (rq) {
+    e.mult = rq->mult;
+    e.y_zp = rq->y_zp;
+    e.lo = rq->lo;
+    e.hi = rq->hi;
   }
+  int32_t *part = reinterpret_cast<int32_t *>(base + p.off_part);
+  const int mode = K == 0 ? 3 : (p.ks > 1 ? 2 : (rq ? 1 : 0));
+  e.y_vec = (mode == 2 || reinterpret_cast<uintptr_t>(y_dev) % 16 == 0) ? 1 : 0;
+  if (mode != 3) {
+    const int64_t a_bs = a_batch > 1 ? (int64_t)p.m32n * kqp * 64 : 0;
+    const int64_t b_bs = b_batch > 1 ? (npad / 32) * kqp * 64 : 0;
+    const unsigned gx = (unsigned)(((p.ntiles + 7) / 8) * 8 * p.mtiles);
+    const dim3 grid(gx, (unsigned)p.ks, (unsigned)batch);
+    void *yk = mode == 2 ? static_cast<void *>(part) : y_dev;
+#define MG_I8_ARGS                                                                         \
+  afrag, a_bs, reinterpret_cast<const int4v *>(bq), b_bs, yk, e, (int)M, (int)N, kqp, p.mtiles, \
+      p.ntiles, p.sps
+#define MG_I8_LAUNCH(WM_, MODE_) \
+  hipLaunchKernelGGL((k_i8_gemm<WM_, MODE_>), grid, dim3(256), 0, st, MG_I8_ARGS)
+    if (p.wm == 2) {
+      if (mode == 0) MG_I8_LAUNCH(2, 0);
+      else if (mode == 1) MG_I8_LAUNCH(2, 1);
+      else MG_I8_LAUNCH(2, 2);
+    } else {
+      if (mode == 0) MG_I8_LAUNCH(1, 0);
+      else if (mode == 1) MG_I8_LAUNCH(1, 1);
+      else MG_I8_LAUNCH(1, 2);
+    }
+#undef MG_I8_LAUNCH
 #undef MG_I8_ARGS
-  return mg_launch_check("k_i8_gemm");
+    MG_TRY(mg_launch_check("k_i8_gemm"));
+  }
+  if (mode >= 2) {  // split-K partials, or K == 0 (empty sums: the epilogue alone)
+    const int64_t tot = batch * M * N;
+    const unsigned blocks = (unsigned)((tot + 255) / 256);
+    const int ks = mode == 3 ? 0 : p.ks;
+    if (rq)
+      hipLaunchKernelGGL(k_i8_reduce<1>, dim3(blocks), dim3(256), 0, st, part, y_dev, e, batch,
+                         M, N, ks);
+    else
+      hipLaunchKernelGGL(k_i8_reduce<0>, dim3(blocks), dim3(256), 0, st, part, y_dev, e, batch,
+                         M, N, ks);
+    MG_TRY(mg_launch_check("k_i8_reduce"));
+  }
+  return MG_OK;
 }
 
 mg_status mg_int8_run(mg_ctx *ctx, const mg_weight *w, const void *a_dev,
@@ -330,8 +596,8 @@ mg_status mg_int8_run(mg_ctx *ctx, const mg_weight *w, const void *a_dev,
                      rows, w->N, w->K, a_zp, a_zp_len, rq, y_dev, ws);
 }
 
-// Runtime (non-weight) batched form: B already prepacked per batch into
-// `bw` by mg_int8_prepack_batched.
+// Runtime (non-weight) batched form: B is prepacked per batch into the
+// workspace first.
 mg_status mg_int8_run_batched(mg_ctx *ctx, const void *a_dev, int32_t a_signed,
                               int64_t a_batch, const void *b_dev,
                               int32_t b_signed, int64_t b_batch, int64_t M,
@@ -347,11 +613,11 @@ mg_status mg_int8_run_batched(mg_ctx *ctx, const void *a_dev, int32_t a_signed,
                               int64_t a_zp_len, const int32_t *b_zp,
                               int64_t b_zp_len, const mg_requant *rq,
                               void *y_dev, void *ws) {
-  const int64_t kq = (K + 63) / 64, n16 = (N + 15) / 16, npad = n16 * 16;
+  const int64_t kqp = (K + 255) / 256 * 8, n32 = (N + 127) / 128 * 4, npad = n32 * 32;
   hipStream_t st = ctx->stream;
   char *p = static_cast<char *>(ws);
   int8_t *bq = reinterpret_cast<int8_t *>(p);
-  p += mg_align((size_t)b_batch * n16 * kq * 64 * 16);
+  p += mg_align((size_t)b_batch * n32 * kqp * 64 * 16);
   int32_t *colsum = reinterpret_cast<int32_t *>(p);
   p += mg_align((size_t)b_batch * npad * 4);
   int32_t *cb = reinterpret_cast<int32_t *>(p);
@@ -365,10 +631,10 @@ mg_status mg_int8_run_batched(mg_ctx *ctx, const void *a_dev, int32_t a_signed,
     MG_HIP(hipMemcpyAsync(zb_dev, b_zp, (size_t)b_zp_len * 4, hipMemcpyHostToDevice, st));
     zb_len = (int)b_zp_len;
   }
-  const int64_t slots = n16 * kq * 64;
+  const int64_t slots = n32 * kqp * 64;
   hipLaunchKernelGGL(k_i8_prep_b, dim3((unsigned)((slots + 255) / 256), (unsigned)b_batch),
                      dim3(256), 0, st, static_cast<const uint8_t *>(b_dev), b_signed, K, N,
-                     (int)n16, (int)kq, reinterpret_cast<int4v *>(bq));
+                     (int)n32, (int)kqp, reinterpret_cast<int4v *>(bq));
   MG_TRY(mg_launch_check("k_i8_prep_b"));
   hipLaunchKernelGGL(k_i8_colsum, dim3((unsigned)((npad + 255) / 256), (unsigned)b_batch),
                      dim3(256), 0, st, static_cast<const uint8_t *>(b_dev), b_signed, K, N,
@@ -382,11 +648,8 @@ size_t mg_int8_batched_ws_bytes(int64_t a_batch, int64_t b_batch, int64_t M,
                                 int64_t K, int64_t N);
 size_t mg_int8_batched_ws_bytes(int64_t a_batch, int64_t b_batch, int64_t M,
                                 int64_t K, int64_t N) {
-  const int64_t kq = (K + 63) / 64, n16 = (N + 15) / 16, npad = n16 * 16;
-  const int64_t m16 = (M + 15) / 16;
-  size_t b = mg_align((size_t)b_batch * n16 * kq * 64 * 16) + 2 * mg_align((size_t)b_batch * npad * 4) +
-             mg_align((size_t)(N + 1) * 4);
-  size_t a = mg_align((size_t)a_batch * m16 * kq * 64 * 16) + 2 * mg_align((size_t)a_batch * m16 * 16 * 4) +
-             mg_align((size_t)(a_batch * M + 1) * 4);
-  return b + a + 256;
+  const int64_t kqp = (K + 255) / 256 * 8, n32 = (N + 127) / 128 * 4, npad = n32 * 32;
+  const size_t b = mg_align((size_t)b_batch * n32 * kqp * 64 * 16) +
+                   2 * mg_align((size_t)b_batch * npad * 4) + mg_align((size_t)(N + 1) * 4);
+  return b + plan_i8(a_batch, a_batch > b_batch ? a_batch : b_batch, M, K, N).total;
 }

@@ -65,8 +65,8 @@ struct mg_nbits_dev {
 // Device form of an 8-bit MatMulInteger weight B [K, N].
 struct mg_int8_dev {
   int32_t b_signed = 0;
-  int64_t kpad = 0;        // K padded to a multiple of 64
-  int64_t npad = 0;        // N padded to a multiple of 16
+  int64_t kpad = 0;        // K padded to a multiple of 256
+  int64_t npad = 0;        // N padded to a multiple of 128
   int8_t *bq = nullptr;    // B - (b_signed ? 0 : 128) as int8, fragment layout
   int32_t *colsum = nullptr;  // [npad] column sums of the stored int8 B'
   int32_t *cb = nullptr;      // [npad] (b_signed ? 0 : 128) - bZp[col]
