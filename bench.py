@@ -1,15 +1,35 @@
-"""Benchmark: int4 MatMulNBits on Qwen3-0.6B projection shapes.
+"""Benchmark of the matrix-multiply operator family on one MI355X.
 
-One step = one pass of the q, k, v, o, gate, up, down and lm_head
-MatMulNBits projections (block_size 128, packed uint4 zero points) at M = 512
-tokens (prefill).  `value` is the whole pass's algorithmic TFLOP/s
-(2*M*N*K per projection) with weights and activations resident in HBM.  The
-same run times the M = 1 decode pass over the same weights (algorithmic HBM
-GB/s), the dominant kernels' roofline fractions, and the CPU oracle (the
-reference's algorithm restated in C, one thread, as the reference never pools
-MatMulNBits) on a bounded sample.
+Headline (`value`): int4 MatMulNBits on the Qwen3-0.6B projection shapes.  One
+step = one pass of the q, k, v, o, gate, up, down and lm_head MatMulNBits
+projections (block_size 128, packed uint4 zero points) at M = 512 tokens;
+`value` is the pass's algorithmic TFLOP/s (2*M*N*K per projection) with
+weights and activations resident in HBM.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+The same run also measures, each with HIP events on the stream the library
+launches on:
+  roofline       the lm_head call at M = 512 (MFMA-bound), against fp16 peak;
+  gemv_m1        the same eight projections at M = 1, algorithmic HBM GB/s;
+                 four distinct weight sets are rotated so that the working set
+                 (~370 MB) exceeds the 256 MB last-level cache and the weights
+                 really stream from HBM;
+  roofline_gemv  the lm_head launches at M = 1 inside those passes;
+  decode_sweep   a Llama-style 1B decode step (16 layers of q/k/v/o/gate/up/
+                 down + lm_head, block_size 32 with zero points, 0.79 GB of
+                 distinct packed weights) at M = 1, 4 and 16;
+  int8_prefill   the Qwen3 projections as MatMulInteger (u8 x i8 -> int32) at
+                 M = 512, and the DynamicQuantizeLinear -> MatMulInteger ->
+                 QLinearMatMul chain at M = 128, K = N = 1024;
+  f32_encoder    one MiniLM-L6 encoder layer's Gemm/MatMul set (batch 32,
+                 seq 128, hidden 384, 12 heads, FFN 1536) in fp32;
+  cpu_baseline   the oracle (the reference's algorithm restated in C, one
+                 thread, as the reference never pools MatMulNBits) on a
+                 bounded M = 512 sample.
+`traffic` (HBM bytes per launch of the dominant kernels) comes from
+profiles/traffic.json, written from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+runs of `bench.py --only ...` (commands and calibration in that file).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--quick]
 """
 from __future__ import annotations
 
@@ -27,6 +47,8 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
+INT8_MFMA_PEAK_TOPS = 5000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
 
 # (name, K, N) — Qwen3-0.6B: hidden 1024, 16 q heads x 128, 8 kv heads x 128,
 # intermediate 3072, vocab 151936.
@@ -35,6 +57,18 @@ QWEN3_PROJ = [("q", 1024, 2048), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 204
               ("lm_head", 1024, 151936)]
 BLOCK = 128
 M_PREFILL = 512
+GEMV_ROTATE = 4
+
+# Llama-style 1B decoder: hidden 2048, 32 q heads and 8 kv heads of 64,
+# intermediate 8192, 16 layers, vocab 128256; int4 block 32 with zero points.
+LLAMA_LAYER = [("q", 2048, 2048), ("k", 2048, 512), ("v", 2048, 512), ("o", 2048, 2048),
+               ("gate", 2048, 8192), ("up", 2048, 8192), ("down", 8192, 2048)]
+LLAMA_LAYERS = 16
+LLAMA_HEAD = ("lm_head", 2048, 128256)
+LLAMA_BLOCK = 32
+
+# MiniLM-L6 encoder layer: tokens = 32 x 128, hidden 384, 12 heads x 32, FFN 1536.
+MINILM_B, MINILM_S, MINILM_H, MINILM_HEADS, MINILM_FFN = 32, 128, 384, 12, 1536
 
 
 def nbits_bytes(m, k, n, bs=BLOCK, a_bytes=4):
@@ -44,11 +78,11 @@ def nbits_bytes(m, k, n, bs=BLOCK, a_bytes=4):
     return m * k * a_bytes + n * nb * bs // 2 + n * nb * 4 + n * ((nb + 1) // 2) + m * n * 4
 
 
-def make_weight(rng, k, n, bs=BLOCK):
+def make_weight(rng, k, n, bs=BLOCK, s_lo=0.002, s_hi=0.02):
     nb = (k + bs - 1) // bs
-    b = rng.integers(0, 256, (n, nb, bs // 2), dtype=np.uint8)
-    s = rng.uniform(0.002, 0.02, (n, nb)).astype(np.float32)
-    zp = rng.integers(0, 256, (n, (nb + 1) // 2), dtype=np.uint8)
+    b = np.frombuffer(rng.bytes(n * nb * (bs // 2)), dtype=np.uint8).reshape(n, nb, bs // 2)
+    s = rng.uniform(s_lo, s_hi, (n, nb)).astype(np.float32)
+    zp = np.frombuffer(rng.bytes(n * ((nb + 1) // 2)), dtype=np.uint8).reshape(n, (nb + 1) // 2)
     return b, s, zp
 
 
@@ -79,15 +113,52 @@ def cpu_baseline(weights, rng, budget_s=30.0):
                       f"({flops / 1e9:.1f} GFLOP in {t_total:.1f} s, 1 thread)"}
 
 
+def load_traffic():
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return {}
+    return json.loads(p.read_text()).get("kernels", {})
+
+
+class Timer:
+    """HIP-event timing on one stream."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+
+    def event(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record(self.stream)
+        return e
+
+    def loop(self, fn, steps, warmup):
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0 = self.event()
+            for _ in range(steps):
+                fn()
+            e1 = self.event()
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["lm512", "lm1", "copy"], default=None,
+    ap.add_argument("--quick", action="store_true",
+                    help="headline and lm_head measurements only")
+    ap.add_argument("--only", default=None,
+                    choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1"],
                     help="profiling mode: launch one workload --steps times and exit "
-                         "(lm512: lm_head M=512, lm1: lm_head M=1, copy: 256 MiB device "
+                         "(lm512 / lm1: Qwen3 lm_head MatMulNBits at M=512 / M=1; i8lm512: "
+                         "the lm_head as MatMulInteger at M=512; f32ffn: the MiniLM FFN1 "
+                         "Gemm; llama1: the Llama lm_head at M=1; copy: 256 MiB device "
                          "copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -105,86 +176,51 @@ def main():
     stream = torch.cuda.Stream(device=dev)
     ctx = ops.Context(0)
     ctx.set_stream(stream.cuda_stream)
+    T = Timer(torch, stream)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x5EED0003)
 
-    if args.only == "copy":
-        src = torch.empty(64 << 20, device=dev, dtype=torch.float32).fill_(1.0)
-        dst = torch.empty_like(src)
-        with torch.cuda.stream(stream):
-            for _ in range(args.steps):
-                dst.copy_(src)
-        torch.cuda.synchronize()
-        print(f"copy: {args.steps} x {src.numel() * 4} bytes read and written", flush=True)
+    def randn(*shape):
+        return torch.randn(shape, device=dev, dtype=torch.float32, generator=g)
+
+    if args.only:
+        run_only(args, torch, ops, ctx, stream, dev, randn)
         return
+
     rng = np.random.default_rng(0x5EED0003)
     t0 = time.perf_counter()
-    if args.only in ("lm512", "lm1"):
-        m = M_PREFILL if args.only == "lm512" else 1
-        _, k, n = QWEN3_PROJ[-1]
-        b, s, zp = make_weight(rng, k, n)
-        w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=BLOCK, ctx=ctx)
-        a = torch.randn((m, k), device=dev, dtype=torch.float32)
-        y = torch.empty((m, n), device=dev, dtype=torch.float32)
-        with torch.cuda.stream(stream):
-            for _ in range(args.steps):
-                w.run_dev(a.data_ptr(), m, y.data_ptr())
-        torch.cuda.synchronize()
-        print(f"{args.only}: {args.steps} launches of lm_head M={m} K={k} N={n}", flush=True)
-        w.release()
-        return
     host_w = [make_weight(rng, k, n) for _, k, n in QWEN3_PROJ]
     weights = [ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=BLOCK, ctx=ctx)
                for (_, k, n), (b, s, zp) in zip(QWEN3_PROJ, host_w)]
     print(f"# weights uploaded in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
 
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x5EED0003)
-    acts = {}
-    outs = {}
+    acts, outs = {}, {}
     for m in (M_PREFILL, 1):
         for _, k, n in QWEN3_PROJ:
-            acts.setdefault((m, k), torch.randn((m, k), device=dev, dtype=torch.float32,
-                                                generator=g))
-            outs.setdefault((m, n), torch.empty((m, n), device=dev, dtype=torch.float32))
+            if (m, k) not in acts:
+                acts[(m, k)] = randn(m, k)
+            if (m, n) not in outs:
+                outs[(m, n)] = torch.empty((m, n), device=dev, dtype=torch.float32)
 
-    def run_pass(m):
-        for (_, k, n), w in zip(QWEN3_PROJ, weights):
+    def run_pass(ws, m):
+        for (_, k, n), w in zip(QWEN3_PROJ, ws):
             w.run_dev(acts[(m, k)].data_ptr(), m, outs[(m, n)].data_ptr())
 
-    def timed(fn, steps, warmup):
-        with torch.cuda.stream(stream):
-            for _ in range(warmup):
-                fn()
-            torch.cuda.synchronize()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(steps):
-                fn()
-            e1.record(stream)
-            torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / steps
-
+    # ---- headline: M = 512 prefill pass
     flops_step = sum(2.0 * M_PREFILL * n * k for _, k, n in QWEN3_PROJ)
-    ms_step = timed(lambda: run_pass(M_PREFILL), args.steps, args.warmup)
+    ms_step = T.loop(lambda: run_pass(weights, M_PREFILL), args.steps, args.warmup)
     value = flops_step / (ms_step / 1e3) / 1e12
+    print(f"# prefill pass {ms_step:.4f} ms, {value:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
-    bytes_m1 = sum(nbits_bytes(1, k, n) for _, k, n in QWEN3_PROJ)
-    ms_m1 = timed(lambda: run_pass(1), args.steps, args.warmup)
-    gbs_m1 = bytes_m1 / (ms_m1 / 1e3) / 1e9
-
-    # Dominant kernels: lm_head at M=512 (MFMA) and at M=1 (HBM stream).
-    k_lm, n_lm = QWEN3_PROJ[-1][1], QWEN3_PROJ[-1][2]
+    # ---- dominant MFMA kernel: lm_head at M = 512
+    traffic = load_traffic()
+    _, k_lm, n_lm = QWEN3_PROJ[-1]
     w_lm = weights[-1]
     reps = max(args.steps, 10)
-    ms_lm = timed(lambda: w_lm.run_dev(acts[(M_PREFILL, k_lm)].data_ptr(), M_PREFILL,
-                                       outs[(M_PREFILL, n_lm)].data_ptr()), reps, 2)
-    lm_flops = 2.0 * M_PREFILL * n_lm * k_lm
-    lm_tflops = lm_flops / (ms_lm / 1e3) / 1e12
-    ms_lm1 = timed(lambda: w_lm.run_dev(acts[(1, k_lm)].data_ptr(), 1,
-                                        outs[(1, n_lm)].data_ptr()), reps * 5, 5)
-    lm1_bytes = nbits_bytes(1, k_lm, n_lm)
-    lm1_gbs = lm1_bytes / (ms_lm1 / 1e3) / 1e9
-
+    ms_lm = T.loop(lambda: w_lm.run_dev(acts[(M_PREFILL, k_lm)].data_ptr(), M_PREFILL,
+                                        outs[(M_PREFILL, n_lm)].data_ptr()), reps, 2)
+    lm_tflops = 2.0 * M_PREFILL * n_lm * k_lm / (ms_lm / 1e3) / 1e12
+    tr = traffic.get("lm512", {})
     result = {
         "metric": "int4 MatMulNBits TFLOP/s (M=512) + M=1 GEMV HBM GB/s, Qwen3-0.6B shapes",
         "value": round(value, 2),
@@ -202,20 +238,65 @@ def main():
                                "down,lm_head; block_size 128 with uint4 zero points",
                    "M": M_PREFILL, "block_size": BLOCK,
                    "gflop_per_step": round(flops_step / 1e9, 2)},
-        "gemv_m1": {"value": round(gbs_m1, 1), "unit": "GB/s", "ms_per_pass": round(ms_m1, 4),
-                    "bytes_per_pass": bytes_m1, "frac_hbm_peak": round(gbs_m1 / HBM_PEAK_GBS, 4)},
-        "roofline": {"kernel": "k_gemm_f16split (lm_head 512x1024x151936, incl. activation "
-                               "prepass)",
+        "roofline": {"kernel": tr.get("kernel", "k_gemm_f16split") +
+                     " (lm_head 512x1024x151936; op time incl. activation prepass)",
                      "bound": "mfma", "achieved": round(lm_tflops, 2),
                      "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(lm_tflops / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(lm_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": tr.get("bytes"),
+                     "algorithmic_bytes": nbits_bytes(M_PREFILL, k_lm, n_lm),
                      "ms": round(ms_lm, 4)},
-        "roofline_gemv": {"kernel": "k_gemv_dot8 (lm_head M=1, incl. activation prepass)",
-                          "bound": "hbm", "achieved": round(lm1_gbs, 1), "peak": HBM_PEAK_GBS,
-                          "unit": "GB/s", "frac": round(lm1_gbs / HBM_PEAK_GBS, 4),
-                          "traffic": None, "bytes": lm1_bytes, "ms": round(ms_lm1, 4)},
     }
-    if not args.no_cpu and os.environ.get("MIGEMM_BENCH_NO_CPU") != "1":
+
+    # ---- M = 1 decode pass over rotated weight sets
+    rot = [weights]
+    for r in range(1, GEMV_ROTATE):
+        rng_r = np.random.default_rng(0x5EED0003 + r)
+        rot.append([ops.NBitsWeight(*make_weight(rng_r, k, n), k=k, n=n, block_size=BLOCK,
+                                    ctx=ctx) for _, k, n in QWEN3_PROJ])
+    lm_events = []
+    state = {"i": 0}
+
+    def gemv_pass():
+        ws = rot[state["i"] % GEMV_ROTATE]
+        state["i"] += 1
+        for (_, k, n), w in zip(QWEN3_PROJ[:-1], ws[:-1]):
+            w.run_dev(acts[(1, k)].data_ptr(), 1, outs[(1, n)].data_ptr())
+        e0 = T.event()
+        ws[-1].run_dev(acts[(1, k_lm)].data_ptr(), 1, outs[(1, n_lm)].data_ptr())
+        lm_events.append((e0, T.event()))
+
+    bytes_m1 = sum(nbits_bytes(1, k, n) for _, k, n in QWEN3_PROJ)
+    gsteps = max(4 * args.steps, 40)
+    ms_m1 = T.loop(gemv_pass, gsteps, 8)
+    lm_events = lm_events[-gsteps:]
+    ms_lm1 = float(np.mean([a.elapsed_time(b) for a, b in lm_events]))
+    lm1_bytes = nbits_bytes(1, k_lm, n_lm)
+    lm1_gbs = lm1_bytes / (ms_lm1 / 1e3) / 1e9
+    tr1 = traffic.get("lm1", {})
+    result["gemv_m1"] = {"value": round(bytes_m1 / (ms_m1 / 1e3) / 1e9, 1), "unit": "GB/s",
+                         "ms_per_pass": round(ms_m1, 4), "bytes_per_pass": bytes_m1,
+                         "weight_sets_rotated": GEMV_ROTATE,
+                         "frac_hbm_peak": round(bytes_m1 / (ms_m1 / 1e3) / 1e9 / HBM_PEAK_GBS,
+                                                4)}
+    result["roofline_gemv"] = {
+        "kernel": tr1.get("kernel", "k_gemv_dot8") + " (lm_head M=1, 1024x151936, one launch)",
+        "bound": "hbm", "achieved": round(lm1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(lm1_gbs / HBM_PEAK_GBS, 4), "traffic": tr1.get("bytes"),
+        "algorithmic_bytes": lm1_bytes, "ms": round(ms_lm1, 4)}
+    print(f"# gemv M=1 pass {ms_m1:.4f} ms; lm_head {ms_lm1 * 1e3:.2f} us {lm1_gbs:.0f} GB/s",
+          file=sys.stderr, flush=True)
+    for ws in rot[1:]:
+        for w in ws:
+            w.release()
+    del rot
+
+    if not args.quick:
+        result["decode_sweep"] = decode_sweep(torch, ops, ctx, T, randn, dev, args)
+        result["int8_prefill"] = int8_prefill(torch, ops, ctx, T, dev, args)
+        result["f32_encoder"] = f32_encoder(torch, ops, ctx, T, randn, dev, args)
+
+    if not args.no_cpu and not args.quick and os.environ.get("MIGEMM_BENCH_NO_CPU") != "1":
         result["cpu_baseline"] = cpu_baseline(host_w, np.random.default_rng(0x5EED0003))
     else:
         result["cpu_baseline"] = None
@@ -223,6 +304,210 @@ def main():
         w.release()
     ctx.close()
     print(json.dumps(result), flush=True)
+
+
+def decode_sweep(torch, ops, ctx, T, randn, dev, args):
+    """Llama-style 1B decode step at M in {1, 4, 16}: 16 layers x 7 projections
+    + lm_head, all distinct weights (0.79 GB packed), algorithmic HBM GB/s."""
+    t0 = time.perf_counter()
+    rng = np.random.default_rng(0x5EED0004)
+    shapes = [s for _ in range(LLAMA_LAYERS) for s in LLAMA_LAYER] + [LLAMA_HEAD]
+    ws = [ops.NBitsWeight(*make_weight(rng, k, n, LLAMA_BLOCK, 0.005, 0.02), k=k, n=n,
+                          block_size=LLAMA_BLOCK, ctx=ctx) for _, k, n in shapes]
+    print(f"# llama weights uploaded in {time.perf_counter() - t0:.1f} s", file=sys.stderr,
+          flush=True)
+    out = {"workload": "Llama-style 1B int4 decode step: 16 x (q 2048x2048, k/v 2048x512, "
+                       "o 2048x2048, gate/up 2048x8192, down 8192x2048) + lm_head "
+                       "2048x128256; block_size 32 with uint4 zero points"}
+    for m in (1, 4, 16):
+        a = {k: randn(m, k) for k in {k for _, k, _ in shapes}}
+        y = {n: torch.empty((m, n), device=dev, dtype=torch.float32)
+             for n in {n for _, _, n in shapes}}
+        head_ev = []
+
+        def step():
+            for (_, k, n), w in zip(shapes[:-1], ws[:-1]):
+                w.run_dev(a[k].data_ptr(), m, y[n].data_ptr())
+            e0 = T.event()
+            ws[-1].run_dev(a[LLAMA_HEAD[1]].data_ptr(), m, y[LLAMA_HEAD[2]].data_ptr())
+            head_ev.append((e0, T.event()))
+
+        steps = max(args.steps // 2, 5)
+        ms = T.loop(step, steps, 2)
+        nbytes = sum(nbits_bytes(m, k, n, LLAMA_BLOCK) for _, k, n in shapes)
+        ms_head = float(np.mean([e0.elapsed_time(e1) for e0, e1 in head_ev[-steps:]]))
+        hb = nbits_bytes(m, LLAMA_HEAD[1], LLAMA_HEAD[2], LLAMA_BLOCK)
+        out[f"M{m}"] = {"ms_per_step": round(ms, 4), "bytes_per_step": nbytes,
+                        "GB/s": round(nbytes / (ms / 1e3) / 1e9, 1),
+                        "frac_hbm_peak": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "lm_head_us": round(ms_head * 1e3, 2),
+                        "lm_head_GB/s": round(hb / (ms_head / 1e3) / 1e9, 1)}
+        print(f"# decode M={m}: {out[f'M{m}']}", file=sys.stderr, flush=True)
+    for w in ws:
+        w.release()
+    return out
+
+
+def int8_prefill(torch, ops, ctx, T, dev, args):
+    """Qwen3 projections as MatMulInteger (u8 activations x i8 weights, zero
+    points 128 / 0) at M = 512, and the DQL -> MatMulInteger -> QLinearMatMul
+    chain at M = 128, K = N = 1024."""
+    rng = np.random.default_rng(0x5EED0002)
+    ws = []
+    for _, k, n in QWEN3_PROJ:
+        b = np.frombuffer(rng.bytes(k * n), dtype=np.int8).reshape(k, n).copy()
+        b[b == -128] = -127
+        ws.append(ops.Int8Weight(b, np.zeros(1, np.int32), ctx=ctx))
+    a = {k: torch.randint(0, 256, (M_PREFILL, k), device=dev, dtype=torch.uint8)
+         for k in {k for _, k, _ in QWEN3_PROJ}}
+    y = {n: torch.empty((M_PREFILL, n), device=dev, dtype=torch.int32)
+         for n in {n for _, _, n in QWEN3_PROJ}}
+
+    def run():
+        for (_, k, n), w in zip(QWEN3_PROJ, ws):
+            w.matmul_integer_dev(a[k].data_ptr(), False, M_PREFILL, y[n].data_ptr(),
+                                 np.array([128], np.int32))
+
+    ops_step = sum(2.0 * M_PREFILL * n * k for _, k, n in QWEN3_PROJ)
+    ms = T.loop(run, max(args.steps // 2, 5), 2)
+    _, k_lm, n_lm = QWEN3_PROJ[-1]
+    ms_lm = T.loop(lambda: ws[-1].matmul_integer_dev(a[k_lm].data_ptr(), False, M_PREFILL,
+                                                     y[n_lm].data_ptr(),
+                                                     np.array([128], np.int32)), 10, 2)
+    lm_tops = 2.0 * M_PREFILL * n_lm * k_lm / (ms_lm / 1e3) / 1e12
+    out = {"workload": "Qwen3-0.6B projections as MatMulInteger u8 x i8 -> int32, M=512",
+           "TOP/s": round(ops_step / (ms / 1e3) / 1e12, 1), "ms_per_pass": round(ms, 4),
+           "lm_head": {"TOP/s": round(lm_tops, 1), "frac_int8_peak":
+                       round(lm_tops / INT8_MFMA_PEAK_TOPS, 4), "ms": round(ms_lm, 4)}}
+    for w in ws:
+        w.release()
+    # C2 chain: x f32 [128, 1024] -> DQL -> MatMulInteger (int32) and QLinearMatMul (u8).
+    m, k, n = 128, 1024, 1024
+    b = np.clip(rng.integers(-127, 128, (k, n)), -127, 127).astype(np.int8)
+    w = ops.Int8Weight(b, np.zeros(1, np.int32), ctx=ctx)
+    x = torch.randn((m, k), device=dev, dtype=torch.float32)
+    xq = torch.empty((m, k), device=dev, dtype=torch.uint8)
+    sz = torch.zeros(2, device=dev, dtype=torch.int32)
+    ops.dynamic_quantize_linear_dev(x.data_ptr(), m * k, xq.data_ptr(), sz.data_ptr(), ctx=ctx)
+    torch.cuda.synchronize()
+    a_scale = float(sz[:1].view(torch.float32).item())
+    a_zp = int(sz[1].item())
+    y32 = torch.empty((m, n), device=dev, dtype=torch.int32)
+    y8 = torch.empty((m, n), device=dev, dtype=torch.uint8)
+
+    def chain():
+        ops.dynamic_quantize_linear_dev(x.data_ptr(), m * k, xq.data_ptr(), sz.data_ptr(),
+                                        ctx=ctx)
+        w.matmul_integer_dev(xq.data_ptr(), False, m, y32.data_ptr(), np.array([a_zp], np.int32))
+        w.qlinear_matmul_dev(xq.data_ptr(), False, m, a_scale, np.array([a_zp], np.int32),
+                             2.0 ** -10, 0.05, 128, y8.data_ptr(), lo=0, hi=255)
+
+    ms_c = T.loop(chain, max(args.steps, 10), 3)
+    out["dql_chain_M128_K1024_N1024"] = {"us_per_chain": round(ms_c * 1e3, 2),
+                                        "ops": "DQL + MatMulInteger + QLinearMatMul"}
+    w.release()
+    print(f"# int8: {out}", file=sys.stderr, flush=True)
+    return out
+
+
+def f32_encoder(torch, ops, ctx, T, randn, dev, args):
+    """One MiniLM-L6 encoder layer's matmuls in fp32: q/k/v/out Gemm (transB,
+    bias) [4096,384]x[384,384]^T, FFN1 [4096,384]x[1536,384]^T, FFN2
+    [4096,1536]x[384,1536]^T, and the batched attention MatMuls
+    [384 x 128x32]x[32x128] and [384 x 128x128]x[128x32]."""
+    rng = np.random.default_rng(0x5EED0001)
+    tok = MINILM_B * MINILM_S
+    H, F = MINILM_H, MINILM_FFN
+    gemms = [("q", H, H), ("k", H, H), ("v", H, H), ("out", H, H), ("ffn1", H, F),
+             ("ffn2", F, H)]
+    ws, bias = [], []
+    for _, k, n in gemms:
+        wt = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        ws.append(ops.F32Weight(wt, trans_b=True, ctx=ctx))
+        bias.append(torch.from_numpy((rng.standard_normal(n) * 0.02).astype(np.float32)).to(dev))
+    x = {k: randn(tok, k) for k in (H, F)}
+    y = {n: torch.empty((tok, n), device=dev, dtype=torch.float32) for n in (H, F)}
+    bh = MINILM_B * MINILM_HEADS
+    dh = H // MINILM_HEADS
+    q = randn(MINILM_B, MINILM_HEADS, MINILM_S, dh)
+    kt = randn(MINILM_B, MINILM_HEADS, dh, MINILM_S)
+    p = randn(MINILM_B, MINILM_HEADS, MINILM_S, MINILM_S)
+    v = randn(MINILM_B, MINILM_HEADS, MINILM_S, dh)
+    sc = torch.empty((MINILM_B, MINILM_HEADS, MINILM_S, MINILM_S), device=dev)
+    ctxo = torch.empty((MINILM_B, MINILM_HEADS, MINILM_S, dh), device=dev)
+
+    def run():
+        for (_, k, n), w, bb in zip(gemms, ws, bias):
+            w.gemm_dev(x[k].data_ptr(), tok, y[n].data_ptr(), bb.data_ptr(), [n])
+        ops.matmul_f32_dev(q.data_ptr(), q.shape, kt.data_ptr(), kt.shape, sc.data_ptr(),
+                           ctx=ctx)
+        ops.matmul_f32_dev(p.data_ptr(), p.shape, v.data_ptr(), v.shape, ctxo.data_ptr(),
+                           ctx=ctx)
+
+    flops = sum(2.0 * tok * k * n for _, k, n in gemms) + 2 * (2.0 * bh * MINILM_S *
+                                                              MINILM_S * dh)
+    ms = T.loop(run, max(args.steps // 2, 5), 2)
+    ffn_ms = T.loop(lambda: ws[4].gemm_dev(x[H].data_ptr(), tok, y[F].data_ptr(),
+                                           bias[4].data_ptr(), [F]), 10, 2)
+    ffn_tf = 2.0 * tok * H * F / (ffn_ms / 1e3) / 1e12
+    out = {"workload": "MiniLM-L6 layer matmuls fp32 (batch 32, seq 128, hidden 384, "
+                       "12x32 heads, FFN 1536)",
+           "TFLOP/s": round(flops / (ms / 1e3) / 1e12, 2), "ms_per_layer": round(ms, 4),
+           "gflop_per_layer": round(flops / 1e9, 2),
+           "ffn1": {"TFLOP/s": round(ffn_tf, 2),
+                    "frac_fp32_mfma_peak": round(ffn_tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                    "ms": round(ffn_ms, 4)}}
+    for w in ws:
+        w.release()
+    print(f"# f32: {out}", file=sys.stderr, flush=True)
+    return out
+
+
+def run_only(args, torch, ops, ctx, stream, dev, randn):
+    """Profiling mode: one workload launched --steps times on the library's
+    stream."""
+    if args.only == "copy":
+        src = torch.empty(64 << 20, device=dev, dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        with torch.cuda.stream(stream):
+            for _ in range(args.steps):
+                dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy: {args.steps} x {src.numel() * 4} bytes read and written", flush=True)
+        return
+    rng = np.random.default_rng(0x5EED0003)
+    with torch.cuda.stream(stream):
+        if args.only in ("lm512", "lm1", "llama1"):
+            if args.only == "llama1":
+                m, (_, k, n), bs = 1, LLAMA_HEAD, LLAMA_BLOCK
+            else:
+                m, (_, k, n), bs = (M_PREFILL if args.only == "lm512" else 1), QWEN3_PROJ[-1], BLOCK
+            w = ops.NBitsWeight(*make_weight(rng, k, n, bs), k=k, n=n, block_size=bs, ctx=ctx)
+            a = randn(m, k)
+            y = torch.empty((m, n), device=dev, dtype=torch.float32)
+            for _ in range(args.steps):
+                w.run_dev(a.data_ptr(), m, y.data_ptr())
+        elif args.only == "i8lm512":
+            m, (_, k, n) = M_PREFILL, QWEN3_PROJ[-1]
+            b = np.frombuffer(rng.bytes(k * n), dtype=np.int8).reshape(k, n)
+            w = ops.Int8Weight(b, np.zeros(1, np.int32), ctx=ctx)
+            a = torch.randint(0, 256, (m, k), device=dev, dtype=torch.uint8)
+            y = torch.empty((m, n), device=dev, dtype=torch.int32)
+            for _ in range(args.steps):
+                w.matmul_integer_dev(a.data_ptr(), False, m, y.data_ptr(),
+                                     np.array([128], np.int32))
+        elif args.only == "f32ffn":
+            tok, k, n = MINILM_B * MINILM_S, MINILM_H, MINILM_FFN
+            w = ops.F32Weight((rng.standard_normal((n, k)) * 0.02).astype(np.float32),
+                              trans_b=True, ctx=ctx)
+            bias = torch.zeros(n, device=dev)
+            a = randn(tok, k)
+            y = torch.empty((tok, n), device=dev, dtype=torch.float32)
+            for _ in range(args.steps):
+                w.gemm_dev(a.data_ptr(), tok, y.data_ptr(), bias.data_ptr(), [n])
+    torch.cuda.synchronize()
+    print(f"{args.only}: {args.steps} launches", flush=True)
+    w.release()
 
 
 if __name__ == "__main__":

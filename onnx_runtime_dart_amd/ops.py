@@ -214,6 +214,24 @@ class Int8Weight(_Weight):
                                       _ptr(y)))
         return y.astype(np.int64)
 
+    def matmul_integer_dev(self, a_ptr: int, a_signed: bool, rows: int, y_ptr: int,
+                           a_zp=None):
+        """Device form: a [rows, K] 8-bit and y int32 [rows, N] in HBM; asynchronous
+        on the context's stream."""
+        za, la = _zp_arg(a_zp)
+        check(lib.mg_matmul_integer_w_dev(self.ctx.handle, C.c_void_p(a_ptr), int(a_signed),
+                                          rows, self.k, _ptr(za), la, self.handle,
+                                          C.c_void_p(y_ptr)))
+
+    def qlinear_matmul_dev(self, a_ptr: int, a_signed: bool, rows: int, a_scale, a_zp,
+                           b_scale, y_scale, y_zp, y_ptr: int, *, lo, hi):
+        """Device form of qlinear_matmul (y 8-bit [rows, N] in HBM)."""
+        za, la = _zp_arg(a_zp)
+        check(lib.mg_qlinear_matmul_w_dev(self.ctx.handle, C.c_void_p(a_ptr), int(a_signed),
+                                          rows, self.k, float(a_scale), _ptr(za), la,
+                                          self.handle, float(b_scale), float(y_scale),
+                                          int(y_zp), int(lo), int(hi), C.c_void_p(y_ptr)))
+
 
 class F32Weight(_Weight):
     """fp32 Gemm/MatMul B uploaded once; trans_b transposes on upload."""
@@ -241,6 +259,35 @@ class F32Weight(_Weight):
                                 _ptr(_shape_arr(c)) if c is not None else None,
                                 c.ndim if c is not None else 0, _ptr(y)))
         return y
+
+    def gemm_dev(self, a_ptr: int, rows: int, y_ptr: int, c_ptr: int | None = None,
+                 c_shape=None, *, alpha=1.0, beta=1.0):
+        """Device form: a [rows, K], y [rows, N] (and C of shape c_shape) in HBM."""
+        cs = None if c_shape is None else np.ascontiguousarray(np.array(c_shape, np.int64))
+        check(lib.mg_gemm_f32_w_dev(self.ctx.handle, C.c_void_p(a_ptr), rows, self.k,
+                                    self.handle, float(alpha), float(beta),
+                                    None if c_ptr is None else C.c_void_p(c_ptr),
+                                    _ptr(cs), 0 if cs is None else cs.size,
+                                    C.c_void_p(y_ptr)))
+
+
+def matmul_f32_dev(a_ptr: int, a_shape, b_ptr: int, b_shape, y_ptr: int,
+                   ctx: Context | None = None):
+    """opMatMul on device buffers (numpy broadcasting over leading dims)."""
+    ctx = ctx or default_context()
+    sa = np.ascontiguousarray(np.array(a_shape, np.int64))
+    sb = np.ascontiguousarray(np.array(b_shape, np.int64))
+    check(lib.mg_matmul_f32_dev(ctx.handle, C.c_void_p(a_ptr), _ptr(sa), sa.size,
+                                C.c_void_p(b_ptr), _ptr(sb), sb.size, C.c_void_p(y_ptr)))
+
+
+def dynamic_quantize_linear_dev(x_ptr: int, n: int, y_ptr: int, scale_zp_ptr: int,
+                                ctx: Context | None = None):
+    """DynamicQuantizeLinear on device: y uint8 [n]; scale (f32) then zp (i32) at
+    scale_zp_ptr."""
+    ctx = ctx or default_context()
+    check(lib.mg_dynamic_quantize_linear_dev(ctx.handle, C.c_void_p(x_ptr), int(n),
+                                             C.c_void_p(y_ptr), C.c_void_p(scale_zp_ptr)))
 
 
 # ---------------------------------------------------------------------- ops
