@@ -109,6 +109,10 @@ mg_status mg_ctx_create(int32_t device, mg_ctx **out) {
   MG_HIP(hipSetDevice(device));
   mg_ctx *c = new mg_ctx();
   c->device = device;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+      cus > 0)
+    c->num_cus = cus;
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete c;
@@ -351,7 +355,7 @@ mg_status mg_matmul_nbits_dev(mg_ctx *ctx, const mg_weight *w, const float *a_de
   if (M == 0) return MG_OK;
   if (!a_dev || !y_dev) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits: null buffer");
   MG_TRY(mg_use_device(ctx));
-  const size_t ws = mg_nbits_ws_bytes(w, M);
+  const size_t ws = mg_nbits_ws_bytes(ctx, w, M);
   MG_TRY(mg_check_control(ctx, (int64_t)ws));
   MG_TRY(mg_ws_reserve(ctx, ws));
   return mg_nbits_run(ctx, w, a_dev, M, y_dev, ctx->ws);
@@ -368,7 +372,7 @@ mg_status mg_matmul_nbits(mg_ctx *ctx, const mg_weight *w, const float *a, int64
   Staging s;
   const size_t oa = s.take((size_t)(M * w->K) * 4);
   const size_t oy = s.take((size_t)(M * w->N) * 4);
-  const size_t ow = s.take(mg_nbits_ws_bytes(w, M));
+  const size_t ow = s.take(mg_nbits_ws_bytes(ctx, w, M));
   MG_TRY(mg_check_control(ctx, (int64_t)s.off));
   MG_TRY(mg_ws_reserve(ctx, s.off));
   char *base = static_cast<char *>(ctx->ws);

@@ -41,6 +41,8 @@ struct mg_ctx {
   // host-pointer calls.  Reused across calls of this context only.
   void *ws = nullptr;
   size_t ws_bytes = 0;
+  // Compute units of the device (grid sizing).
+  int num_cus = 256;
 };
 
 enum mg_weight_kind { MG_W_NBITS = 1, MG_W_INT8 = 2, MG_W_F32 = 3 };
@@ -107,7 +109,7 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const uint8_t *b,
                           const float *bias);
 void mg_nbits_free(mg_weight *w);
 // Workspace bytes mg_nbits_run needs for M rows.
-size_t mg_nbits_ws_bytes(const mg_weight *w, int64_t M);
+size_t mg_nbits_ws_bytes(const mg_ctx *ctx, const mg_weight *w, int64_t M);
 // a_dev [M, K] f32, y_dev [M, N] f32; ws holds mg_nbits_ws_bytes bytes.
 mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
                        int64_t M, float *y_dev, void *ws);

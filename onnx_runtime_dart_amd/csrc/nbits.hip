@@ -44,6 +44,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int KGRP = 128;  // k per k group
 constexpr int CGRP = 64;   // columns per column group
@@ -131,11 +132,16 @@ __global__ __launch_bounds__(256) void k_af16split(
 // ---------------------------------------------------------- decode GEMV
 
 // MR activation rows (M <= 4); QPG = quantisation blocks per k group
-// (128 / min(bs, 128)); ZPK = zero-point kind.  Grid (column groups, k
-// splits); 4 waves per workgroup; wave w of split y takes the k groups
-// kg = 4y + w (mod nslices = 4 * ksplit), local index l = 4 * (kg / nslices) + w.
+// (128 / min(bs, 128)); ZPK = zero-point kind; PF = k groups of loads each
+// wave keeps in flight (4 with 4 waves per workgroup, 2 with up to 16).  One
+// workgroup per column group (64 columns, one per lane); its NW = blockDim /
+// 64 waves split K, wave w taking k groups w, w + NW, ...  Packed codes are
+// read once, with non-temporal loads (they stream past the caches).  The activations are handled in chunks of kc
+// k groups (one chunk unless M * K is large):
 //
-// Phase 1: the workgroup quantises the activations of its k groups into LDS:
+// Phase 0: each wave issues the loads of its first PF k groups of packed
+// codes, scales and zero points, so HBM is busy while phase 1 runs.
+// Phase 1: the workgroup quantises the chunk of the activations into LDS:
 // per (row, qblock of qb = min(bs, 128) k) the step alpha = max|a| / FIX_MAX
 // (NaN when the block holds a non-finite value), fix = rint(a / alpha)
 // clamped to +-FIX_MAX and split into four balanced signed int4 digits
@@ -143,183 +149,230 @@ __global__ __launch_bounds__(256) void k_af16split(
 // order of wq: sdig[r][l][g][j][d]; srsum = sum of fix over the qblock.
 // Thread per (row, k group, 8-k octet o = 4j + g); a qblock is 16 / QPG
 // consecutive lanes.
-// Phase 2: each lane owns one column and streams its packed codes with
-// 16-byte loads; v_dot8_i32_i4 multiplies (q - 8) with each digit plane and
-//   y += alpha * s * (sum_d 16^d D_d + (8 - zp) * rsum).
-template <int MR, int QPG, int ZPK>
-__global__ __launch_bounds__(256) void k_gemv_dot8(
+// Phase 2: v_dot8_i32_i4 multiplies (q - 8) with each digit plane (digits are
+// wave-uniform LDS broadcasts) and per block
+//   y += alpha * s * (sum_d 16^d D_d + (8 - zp) * rsum),
+// keeping PF k groups of loads in flight ahead of the arithmetic.
+// Phase 3: the NW per-wave sums are added in wave order through LDS
+// (deterministic), plus the bias, and written to y.
+template <int MR, int QPG, int ZPK, int PF>
+__global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
     const float *__restrict__ a, int64_t K, int vec, const uint4 *__restrict__ wq,
     const float *__restrict__ scales, const uint8_t *__restrict__ zp4,
     const float *__restrict__ zpf, const float *__restrict__ bias,
-    float *__restrict__ y, float *__restrict__ part, int N, int c4n, int nb,
-    int nbh, int lbs, int nloc, int ncolp) {
+    float *__restrict__ y, int N, int c4, int nb, int nbh, int lbs, int kc) {
   extern __shared__ uint32_t smem[];
-  uint32_t *sdig = smem;                                            // [MR][nloc][64]
-  float *salpha = reinterpret_cast<float *>(smem + MR * nloc * 64);  // [MR][nloc][QPG]
-  int *srsum = reinterpret_cast<int *>(salpha + MR * nloc * QPG);   // [MR][nloc][QPG]
-  __shared__ float red[4][MR][64];
+  uint32_t *sdig = smem;                                            // [MR][kc][64]
+  float *salpha = reinterpret_cast<float *>(smem + MR * kc * 64);   // [MR][kc][QPG]
+  int *srsum = reinterpret_cast<int *>(salpha + MR * kc * QPG);     // [MR][kc][QPG]
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int cgi = blockIdx.x;
-  const int nslices = gridDim.y * 4;
-  constexpr int G = 16 / QPG;  // octets per qblock
+  const int NW = blockDim.x >> 6;
+  const int nthr = blockDim.x;
+  const int cg = blockIdx.x;
+  constexpr int G = 16 / QPG;        // octets per qblock
+  constexpr int ZB = (QPG + 1) / 2;  // zero-point bytes per k group
 
-  // Phase 1.
-  const int ntask = MR * nloc * 16;
-  for (int task = t; task < ntask; task += 256) {
-    const int o = task & 15, rl = task >> 4;
-    const int l = rl % nloc, r = rl / nloc;
-    const int kg = (l >> 2) * nslices + blockIdx.y * 4 + (l & 3);
-    const int64_t k0 = (int64_t)kg * KGRP + 8 * o;
-    const float *ar = a + (int64_t)r * K;
-    float v[8];
-    if (vec && k0 + 8 <= K) {
-      const float4 x0 = *reinterpret_cast<const float4 *>(ar + k0);
-      const float4 x1 = *reinterpret_cast<const float4 *>(ar + k0 + 4);
-      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-      v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-    } else {
+  const uint4 *wp = wq + (int64_t)cg * c4 * 256 + lane;
+  const float *sp = scales + (int64_t)cg * nb * 64 + lane;
+  const uint8_t *zq = zp4 + (int64_t)cg * nbh * 64 + lane;
+  const float *zfp = zpf + (int64_t)cg * nb * 64 + lane;
+  uint4 wr[PF][4];
+  float sr[PF][QPG];
+  uint32_t zr[PF][ZB];
+  float zfr[PF][QPG];
+  // Loads of k group kg into ring slot i.
+  auto issue = [&](int i, int kg) {
 #pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = (kg < c4n && k0 + i < K) ? ar[k0 + i] : 0.f;
+    for (int g = 0; g < 4; g++)
+      wr[i][g] = __builtin_bit_cast(
+          uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wp + kg * 256 + g * 64)));
+#pragma unroll
+    for (int s = 0; s < QPG; s++) {
+      const int b = min((kg * KGRP + s * (KGRP / QPG)) >> lbs, nb - 1);
+      sr[i][s] = sp[(int64_t)b * 64];
+      if (ZPK == 2) zfr[i][s] = zfp[(int64_t)b * 64];
     }
-    float mx = 0.f;
-    int bad = 0;
+    if (ZPK == 1) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      if (!isfinite(v[i])) bad = 1;
-      mx = fmaxf(mx, fabsf(v[i]));
-    }
-#pragma unroll
-    for (int off = 1; off < G; off <<= 1) {
-      mx = fmaxf(mx, __shfl_xor(mx, off));
-      bad |= __shfl_xor(bad, off);
-    }
-    const float inv = (mx > 0.f && !bad) ? (float)FIX_MAX / mx : 0.f;
-    int rs = 0;
-    uint32_t dg[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      int fix = (int)rintf(v[i] * inv);
-      fix = min(max(fix, -FIX_MAX), FIX_MAX);
-      rs += fix;
-      const int pos = nib_pos(i);
-      int x = fix;
-#pragma unroll
-      for (int d = 0; d < 4; d++) {
-        const int di = ((x + 8) & 15) - 8;
-        x = (x - di) >> 4;
-        dg[d] |= (uint32_t)(di & 15) << (4 * pos);
+      for (int h = 0; h < ZB; h++) {
+        const int b = min((kg * KGRP + 2 * h * (KGRP / QPG)) >> lbs, nb - 1);
+        zr[i][h] = zq[(int64_t)(b >> 1) * 64];
       }
     }
-#pragma unroll
-    for (int off = 1; off < G; off <<= 1) rs += __shfl_xor(rs, off);
-    const int j = o >> 2, g = o & 3;
-    *reinterpret_cast<uint4 *>(&sdig[((r * nloc + l) * 4 + g) * 16 + j * 4]) =
-        make_uint4(dg[0], dg[1], dg[2], dg[3]);
-    if (o % G == 0) {
-      const int q = (r * nloc + l) * QPG + o / G;
-      salpha[q] = bad ? __builtin_nanf("") : (mx > 0.f ? mx / (float)FIX_MAX : 0.f);
-      srsum[q] = rs;
-    }
-  }
-  __syncthreads();
+  };
+  // This wave's k groups: wave, wave + NW, ...; the n-th is wave + n * NW.
+  const int nmine = wave < c4 ? (c4 - wave + NW - 1) / NW : 0;
 
-  // Phase 2.
+  // Phase 0.
+#pragma unroll
+  for (int i = 0; i < PF; i++)
+    if (i < nmine) issue(i, wave + i * NW);
+
   float yacc[MR];
 #pragma unroll
   for (int r = 0; r < MR; r++) yacc[r] = 0.f;
-  const int slice = blockIdx.y * 4 + wave;
-  for (int kg = slice, l = wave; kg < c4n; kg += nslices, l += 4) {
-    const uint4 *wp = wq + (((int64_t)cgi * c4n + kg) * 4) * 64 + lane;
-    uint32_t wv[4][4];
+  // kc is c4 (one chunk) or a multiple of PF * NW, so every chunk starts at a
+  // multiple of PF of this wave's k groups and ring slots stay static.
+  for (int c0 = 0; c0 < c4; c0 += kc) {
+    const int nk = min(c4, c0 + kc) - c0;
+    if (c0 > 0) __syncthreads();  // previous chunk's digits fully consumed
+    // Phase 1.
+    const int ntask = MR * nk * 16;
+    for (int task = t; task < ntask; task += nthr) {
+      const int o = task & 15, rl = task >> 4;
+      const int l = rl % nk, r = rl / nk;
+      const int64_t k0 = (int64_t)(c0 + l) * KGRP + 8 * o;
+      const float *ar = a + (int64_t)r * K;
+      float v[8];
+      if (vec && k0 + 8 <= K) {
+        const float4 x0 = *reinterpret_cast<const float4 *>(ar + k0);
+        const float4 x1 = *reinterpret_cast<const float4 *>(ar + k0 + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+      } else {
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const uint4 w4 = wp[g * 64];
-      wv[g][0] = w4.x ^ 0x88888888u; wv[g][1] = w4.y ^ 0x88888888u;
-      wv[g][2] = w4.z ^ 0x88888888u; wv[g][3] = w4.w ^ 0x88888888u;
+        for (int i = 0; i < 8; i++) v[i] = (k0 + i < K) ? ar[k0 + i] : 0.f;
+      }
+      float mx = 0.f;
+      int bad = 0;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        if (!isfinite(v[i])) bad = 1;
+        mx = fmaxf(mx, fabsf(v[i]));
+      }
+#pragma unroll
+      for (int off = 1; off < G; off <<= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+        bad |= __shfl_xor(bad, off);
+      }
+      const float inv = (mx > 0.f && !bad) ? (float)FIX_MAX / mx : 0.f;
+      int rs = 0;
+      uint32_t dg[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        int fix = (int)rintf(v[i] * inv);
+        fix = min(max(fix, -FIX_MAX), FIX_MAX);
+        rs += fix;
+        const int pos = nib_pos(i);
+        int x = fix;
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          const int di = ((x + 8) & 15) - 8;
+          x = (x - di) >> 4;
+          dg[d] |= (uint32_t)(di & 15) << (4 * pos);
+        }
+      }
+#pragma unroll
+      for (int off = 1; off < G; off <<= 1) rs += __shfl_xor(rs, off);
+      const int j = o >> 2, g = o & 3;
+      *reinterpret_cast<uint4 *>(&sdig[((r * kc + l) * 4 + g) * 16 + j * 4]) =
+          make_uint4(dg[0], dg[1], dg[2], dg[3]);
+      if (o % G == 0) {
+        const int q = (r * kc + l) * QPG + o / G;
+        salpha[q] = bad ? __builtin_nanf("") : (mx > 0.f ? mx / (float)FIX_MAX : 0.f);
+        srsum[q] = rs;
+      }
     }
-    // One quantisation block at a time: dword (g, j) holds k = 32j + 8g + t,
-    // so block s covers j in [4s/QPG, 4(s+1)/QPG) for QPG <= 4 and, for
-    // QPG = 8, j = s/2 with g in {2(s%2), 2(s%2) + 1}.
+    __syncthreads();
+
+    // Phase 2: this wave's k groups inside the chunk.  The ring slot of the
+    // n-th k group is n % PF; the loop is unrolled by PF so slots are static.
+    const int nend = min(nmine, (c0 + nk - wave + NW - 1) / NW);
+    for (int n = c0 / NW; n < nend; n += PF) {
 #pragma unroll
-    for (int s = 0; s < QPG; s++) {
-      int acc[MR][4];
+      for (int i = 0; i < PF; i++) {
+        const int nn = n + i;
+        if (nn >= nend) break;
+        const int kg = wave + nn * NW;
+        const int l = kg - c0;
+        uint32_t wv[4][4];
 #pragma unroll
-      for (int r = 0; r < MR; r++)
+        for (int g = 0; g < 4; g++) {
+          wv[g][0] = wr[i][g].x ^ 0x88888888u; wv[g][1] = wr[i][g].y ^ 0x88888888u;
+          wv[g][2] = wr[i][g].z ^ 0x88888888u; wv[g][3] = wr[i][g].w ^ 0x88888888u;
+        }
+        float scv[QPG], zfv[QPG];
+        uint32_t zbv[ZB];
 #pragma unroll
-        for (int d = 0; d < 4; d++) acc[r][d] = 0;
+        for (int s = 0; s < QPG; s++) {
+          scv[s] = sr[i][s];
+          if (ZPK == 2) zfv[s] = zfr[i][s];
+        }
+        if (ZPK == 1) {
 #pragma unroll
-      for (int g = 0; g < 4; g++)
+          for (int h = 0; h < ZB; h++) zbv[h] = zr[i][h];
+        }
+        if (nn + PF < nmine) issue(i, wave + (nn + PF) * NW);
+        // One quantisation block at a time: dword (g, j) holds k = 32j + 8g + t,
+        // so block s covers j in [4s/QPG, 4(s+1)/QPG) for QPG <= 4 and, for
+        // QPG = 8, j = s/2 with g in {2(s%2), 2(s%2) + 1}.
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const bool mine = QPG == 8 ? (j == s / 2 && g / 2 == s % 2) : (j * QPG / 4 == s);
-          if (!mine) continue;
-          const int x = (int)wv[g][j];
+        for (int s = 0; s < QPG; s++) {
+          int acc[MR][4];
+#pragma unroll
+          for (int r = 0; r < MR; r++)
+#pragma unroll
+            for (int d = 0; d < 4; d++) acc[r][d] = 0;
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const bool mine = QPG == 8 ? (j == s / 2 && g / 2 == s % 2) : (j * QPG / 4 == s);
+              if (!mine) continue;
+              const int x = (int)wv[g][j];
+#pragma unroll
+              for (int r = 0; r < MR; r++) {
+                const uint4 dd = *reinterpret_cast<const uint4 *>(
+                    &sdig[((r * kc + l) * 4 + g) * 16 + j * 4]);
+                acc[r][0] = __builtin_amdgcn_sdot8((int)dd.x, x, acc[r][0], false);
+                acc[r][1] = __builtin_amdgcn_sdot8((int)dd.y, x, acc[r][1], false);
+                acc[r][2] = __builtin_amdgcn_sdot8((int)dd.z, x, acc[r][2], false);
+                acc[r][3] = __builtin_amdgcn_sdot8((int)dd.w, x, acc[r][3], false);
+              }
+            }
+          const int b = (kg * KGRP + s * (KGRP / QPG)) >> lbs;
+          if (b >= nb) continue;  // k padding beyond the last block
+          int zc = 0;
+          if (ZPK == 1) {
+            // Zero-point byte h of this k group holds blocks 2h (low) and 2h+1.
+            const uint32_t zb = zbv[QPG == 1 ? 0 : s / 2];
+            zc = 8 - (int)((b & 1) ? (zb >> 4) : (zb & 15));
+          }
 #pragma unroll
           for (int r = 0; r < MR; r++) {
-            const uint4 dd =
-                *reinterpret_cast<const uint4 *>(&sdig[((r * nloc + l) * 4 + g) * 16 + j * 4]);
-            acc[r][0] = __builtin_amdgcn_sdot8((int)dd.x, x, acc[r][0], false);
-            acc[r][1] = __builtin_amdgcn_sdot8((int)dd.y, x, acc[r][1], false);
-            acc[r][2] = __builtin_amdgcn_sdot8((int)dd.z, x, acc[r][2], false);
-            acc[r][3] = __builtin_amdgcn_sdot8((int)dd.w, x, acc[r][3], false);
+            const int comb = ((acc[r][3] * 16 + acc[r][2]) * 16 + acc[r][1]) * 16 + acc[r][0];
+            const int q = (r * kc + l) * QPG + s;
+            const float al = salpha[q];
+            const int R = srsum[q];
+            float v;
+            if (ZPK == 2)
+              v = (float)comb + (8.f - zfv[s]) * (float)R;
+            else
+              v = (float)(comb + zc * R);
+            yacc[r] += (al * scv[s]) * v;
           }
         }
-      const int b = (kg * KGRP + s * (KGRP / QPG)) >> lbs;
-      if (b >= nb) continue;  // k padding beyond the last block
-      const float sc = scales[((int64_t)cgi * nb + b) * 64 + lane];
-      int zc = 0;
-      float zf = 8.f;
-      if (ZPK == 1) {
-        const uint8_t zb = zp4[((int64_t)cgi * nbh + b / 2) * 64 + lane];
-        zc = 8 - ((b & 1) ? (zb >> 4) : (zb & 15));
-      } else if (ZPK == 2) {
-        zf = zpf[((int64_t)cgi * nb + b) * 64 + lane];
-      }
-#pragma unroll
-      for (int r = 0; r < MR; r++) {
-        const int comb = ((acc[r][3] * 16 + acc[r][2]) * 16 + acc[r][1]) * 16 + acc[r][0];
-        const int q = (r * nloc + l) * QPG + s;
-        const float al = salpha[q];
-        const int R = srsum[q];
-        float v;
-        if (ZPK == 2)
-          v = (float)comb + (8.f - zf) * (float)R;
-        else
-          v = (float)(comb + zc * R);
-        yacc[r] += (al * sc) * v;
       }
     }
   }
+
+  // Phase 3.
+  __syncthreads();  // all waves are done with the digits; reuse LDS
+  float *red = reinterpret_cast<float *>(smem);  // [NW][MR][64]
 #pragma unroll
-  for (int r = 0; r < MR; r++) red[wave][r][lane] = yacc[r];
+  for (int r = 0; r < MR; r++) red[(wave * MR + r) * 64 + lane] = yacc[r];
   __syncthreads();
   if (wave == 0) {
-    const int col = cgi * 64 + lane;
+    const int col = cg * 64 + lane;
 #pragma unroll
     for (int r = 0; r < MR; r++) {
-      const float s = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] +
-                      red[3][r][lane];
-      if (gridDim.y == 1) {
-        if (col < N) y[(int64_t)r * N + col] = s + (bias ? bias[col] : 0.f);
-      } else {
-        part[((int64_t)blockIdx.y * MR + r) * ncolp + col] = s;
-      }
+      float s = red[r * 64 + lane];
+      for (int w = 1; w < NW; w++) s += red[(w * MR + r) * 64 + lane];
+      if (col < N) y[(int64_t)r * N + col] = s + (bias ? bias[col] : 0.f);
     }
   }
-}
-
-__global__ void k_gemv_reduce(const float *__restrict__ part,
-                              const float *__restrict__ bias,
-                              float *__restrict__ y, int M, int N, int ncolp,
-                              int ksplit) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)M * N) return;
-  const int r = (int)(idx / N), c = (int)(idx % N);
-  float s = 0.f;
-  for (int ks = 0; ks < ksplit; ks++) s += part[((int64_t)ks * M + r) * ncolp + c];
-  y[idx] = s + (bias ? bias[c] : 0.f);
 }
 
 // --------------------------------------------------------- prefill GEMM
@@ -632,14 +685,14 @@ struct NbitsPlan {
   int path;  // 0 gemv, 1 mfma, 2 generic
   int64_t M;
   // gemv
-  int qpg = 1, qb = 128, nloc = 0, ksplit = 1, kps = 0;
+  int qpg = 1, qb = 128, ksplit = 1, kps = 0, nw = 4, kc = 0;
   size_t lds = 0;
   // mfma
   int64_t mpad = 0;
   size_t off_a = 0, off_b = 0, off_c = 0, off_d = 0, total = 0;
 };
 
-NbitsPlan plan_nbits(const mg_weight *w, int64_t M) {
+NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
   const mg_nbits_dev &d = w->nbits;
   NbitsPlan p;
   p.M = M;
@@ -647,19 +700,26 @@ NbitsPlan plan_nbits(const mg_weight *w, int64_t M) {
     p.path = 0;
     p.qb = (int)std::min<int64_t>(d.bs, KGRP);
     p.qpg = KGRP / p.qb;
-    // Split K until ~2048 waves stream weights, then further until the
-    // workgroup's quantised activations fit LDS (M * nloc <= 64 k groups).
-    const int64_t waves_per_slice = d.ng * 4;
-    int64_t ks = (2048 + waves_per_slice - 1) / waves_per_slice;
-    ks = std::min<int64_t>(ks, std::max<int64_t>(1, d.c4 / 4));
-    ks = std::max<int64_t>(ks, 1);
-    auto nloc_of = [&](int64_t k) { return 4 * ((d.c4 + 4 * k - 1) / (4 * k)); };
-    while (M * nloc_of(ks) > 64) ks++;
-    p.ksplit = (int)ks;
-    p.nloc = (int)nloc_of(ks);
-    p.lds = (size_t)M * p.nloc * (64 + 2 * p.qpg) * 4;
-    p.off_d = 0;  // partials
-    p.total = p.ksplit > 1 ? mg_align((size_t)p.ksplit * M * d.ng * 64 * 4) : 0;
+    // One workgroup per column group; its waves split K.  Wide weights use
+    // 4 waves (4 k groups of loads in flight each); narrow ones use up to 16
+    // (2 in flight each) so that their few workgroups still keep enough bytes
+    // in flight per CU.
+    // (The 16-wave form is register-limited to one row and blocks <= 64.)
+    int64_t nw = 4;
+    if (M == 1 && p.qpg >= 2 && d.ng * 4 < 8 * (int64_t)std::max(ctx->num_cus, 1)) nw = 16;
+    nw = std::min<int64_t>(nw, std::max<int64_t>(d.c4, 4));
+    if (nw > 4) nw = nw > 8 ? 16 : 8;
+    const int pf = nw == 4 ? 4 : 2;
+    // Activation digits of a chunk of kc k groups live in LDS (<= 64 KiB); a
+    // partial chunk size is a multiple of pf * nw.
+    const int64_t per_kg = M * (64 + 2 * p.qpg) * 4;
+    const int64_t kc_max = 65536 / per_kg;
+    int64_t kc = d.c4;
+    if (kc > kc_max) kc = kc_max / (pf * nw) * (pf * nw);
+    p.nw = (int)nw;
+    p.kc = (int)kc;
+    p.lds = (size_t)std::max<int64_t>(kc * per_kg, nw * M * 64 * 4);
+    p.total = 0;
   } else if (d.bs >= 32 && d.zp_kind != MG_ZP_FLOAT) {
     p.path = 1;
     const int64_t rows = 128;  // workgroup tile rows
@@ -684,30 +744,37 @@ NbitsPlan plan_nbits(const mg_weight *w, int64_t M) {
 
 template <int MR, int QPG>
 void launch_gemv_zp(const mg_weight *w, const NbitsPlan &p, hipStream_t st, const float *a,
-                    int vec, float *y, float *part) {
+                    int vec, float *y) {
   const mg_nbits_dev &d = w->nbits;
-  const dim3 grid((unsigned)d.ng, (unsigned)p.ksplit);
+  const dim3 grid((unsigned)d.ng), block((unsigned)(64 * p.nw));
+  // Unused zero-point arrays are pointed at the scales (never dereferenced).
+  const uint8_t *zp4 = d.zp4 ? d.zp4 : reinterpret_cast<const uint8_t *>(d.scales);
+  const float *zpf = d.zpf ? d.zpf : d.scales;
 #define MG_GEMV_ARGS                                                                    \
-  a, w->K, vec, reinterpret_cast<const uint4 *>(d.wq), d.scales, d.zp4, d.zpf, d.bias, y, \
-      part, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), p.nloc,     \
-      (int)(d.ng * 64)
-  if (d.zp_kind == 0)
-    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, 0>), grid, dim3(256), p.lds, st, MG_GEMV_ARGS);
-  else if (d.zp_kind == 1)
-    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, 1>), grid, dim3(256), p.lds, st, MG_GEMV_ARGS);
-  else
-    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, 2>), grid, dim3(256), p.lds, st, MG_GEMV_ARGS);
+  a, w->K, vec, reinterpret_cast<const uint4 *>(d.wq), d.scales, zp4, zpf, d.bias, y,        \
+      (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), p.kc
+#define MG_GEMV_LAUNCH(Z_)                                                                   \
+  do {                                                                                       \
+    if (p.nw == 4)                                                                           \
+      hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, Z_, 4>), grid, block, p.lds, st, MG_GEMV_ARGS); \
+    else                                                                                     \
+      hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, Z_, 2>), grid, block, p.lds, st, MG_GEMV_ARGS); \
+  } while (0)
+  if (d.zp_kind == 0) MG_GEMV_LAUNCH(0);
+  else if (d.zp_kind == 1) MG_GEMV_LAUNCH(1);
+  else MG_GEMV_LAUNCH(2);
+#undef MG_GEMV_LAUNCH
 #undef MG_GEMV_ARGS
 }
 
 template <int MR>
 void launch_gemv_q(const mg_weight *w, const NbitsPlan &p, hipStream_t st, const float *a,
-                   int vec, float *y, float *part) {
+                   int vec, float *y) {
   switch (p.qpg) {
-    case 1: launch_gemv_zp<MR, 1>(w, p, st, a, vec, y, part); break;
-    case 2: launch_gemv_zp<MR, 2>(w, p, st, a, vec, y, part); break;
-    case 4: launch_gemv_zp<MR, 4>(w, p, st, a, vec, y, part); break;
-    default: launch_gemv_zp<MR, 8>(w, p, st, a, vec, y, part); break;
+    case 1: launch_gemv_zp<MR, 1>(w, p, st, a, vec, y); break;
+    case 2: launch_gemv_zp<MR, 2>(w, p, st, a, vec, y); break;
+    case 4: launch_gemv_zp<MR, 4>(w, p, st, a, vec, y); break;
+    default: launch_gemv_zp<MR, 8>(w, p, st, a, vec, y); break;
   }
 }
 
@@ -817,35 +884,27 @@ void mg_nbits_free(mg_weight *w) {
   d = mg_nbits_dev{};
 }
 
-size_t mg_nbits_ws_bytes(const mg_weight *w, int64_t M) {
-  return plan_nbits(w, M).total;
+size_t mg_nbits_ws_bytes(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
+  return plan_nbits(ctx, w, M).total;
 }
 
 mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
                        int64_t M, float *y_dev, void *ws) {
   const mg_nbits_dev &d = w->nbits;
   if (M == 0) return MG_OK;
-  const NbitsPlan p = plan_nbits(w, M);
+  const NbitsPlan p = plan_nbits(ctx, w, M);
   hipStream_t st = ctx->stream;
   char *base = static_cast<char *>(ws);
   const int zpk = d.zp_kind;
   if (p.path == 0) {
-    float *part = p.ksplit > 1 ? reinterpret_cast<float *>(base + p.off_d) : nullptr;
     const int vec = (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 && w->K % 4 == 0) ? 1 : 0;
     switch (M) {
-      case 1: launch_gemv_q<1>(w, p, st, a_dev, vec, y_dev, part); break;
-      case 2: launch_gemv_q<2>(w, p, st, a_dev, vec, y_dev, part); break;
-      case 3: launch_gemv_q<3>(w, p, st, a_dev, vec, y_dev, part); break;
-      default: launch_gemv_q<4>(w, p, st, a_dev, vec, y_dev, part); break;
+      case 1: launch_gemv_q<1>(w, p, st, a_dev, vec, y_dev); break;
+      case 2: launch_gemv_q<2>(w, p, st, a_dev, vec, y_dev); break;
+      case 3: launch_gemv_q<3>(w, p, st, a_dev, vec, y_dev); break;
+      default: launch_gemv_q<4>(w, p, st, a_dev, vec, y_dev); break;
     }
-    MG_TRY(mg_launch_check("k_gemv_dot8"));
-    if (p.ksplit > 1) {
-      const int64_t tot = M * w->N;
-      hipLaunchKernelGGL(k_gemv_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
-                         part, d.bias, y_dev, (int)M, (int)w->N, (int)(d.ng * 64), p.ksplit);
-      MG_TRY(mg_launch_check("k_gemv_reduce"));
-    }
-    return MG_OK;
+    return mg_launch_check("k_gemv_dot8");
   }
   if (p.path == 1) {
     uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
