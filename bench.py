@@ -154,11 +154,11 @@ def main():
     ap.add_argument("--quick", action="store_true",
                     help="headline and lm_head measurements only")
     ap.add_argument("--only", default=None,
-                    choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1"],
+                    choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1", "llama16"],
                     help="profiling mode: launch one workload --steps times and exit "
                          "(lm512 / lm1: Qwen3 lm_head MatMulNBits at M=512 / M=1; i8lm512: "
                          "the lm_head as MatMulInteger at M=512; f32ffn: the MiniLM FFN1 "
-                         "Gemm; llama1: the Llama lm_head at M=1; copy: 256 MiB device "
+                         "Gemm; llama1 / llama16: the Llama lm_head at M=1 / M=16; copy: 256 MiB device "
                          "copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -477,9 +477,9 @@ def run_only(args, torch, ops, ctx, stream, dev, randn):
         return
     rng = np.random.default_rng(0x5EED0003)
     with torch.cuda.stream(stream):
-        if args.only in ("lm512", "lm1", "llama1"):
-            if args.only == "llama1":
-                m, (_, k, n), bs = 1, LLAMA_HEAD, LLAMA_BLOCK
+        if args.only in ("lm512", "lm1", "llama1", "llama16"):
+            if args.only.startswith("llama"):
+                m, (_, k, n), bs = int(args.only[5:]), LLAMA_HEAD, LLAMA_BLOCK
             else:
                 m, (_, k, n), bs = (M_PREFILL if args.only == "lm512" else 1), QWEN3_PROJ[-1], BLOCK
             w = ops.NBitsWeight(*make_weight(rng, k, n, bs), k=k, n=n, block_size=bs, ctx=ctx)

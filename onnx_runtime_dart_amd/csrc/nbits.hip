@@ -54,6 +54,12 @@ __host__ __device__ inline int nib_pos(int t) {
   return (t & 1) ? 4 + (t >> 1) : (t >> 1);
 }
 
+// Position of column c (0..63) of a column group in the per-block scale and
+// zero-point rows: the four 16-column tiles of one column residue are
+// adjacent, so a lane that owns columns c, c + 16, c + 32, c + 48 (the
+// 16-row MFMA GEMV) reads their four values with one load.
+__host__ __device__ inline int sz_pos(int c) { return (c & 15) * 4 + (c >> 4); }
+
 // ------------------------------------------------------------- prepasses
 
 // Activation prepass of the MFMA path.  Per row: an exponent e that puts the
@@ -175,9 +181,9 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
   constexpr int ZB = (QPG + 1) / 2;  // zero-point bytes per k group
 
   const uint4 *wp = wq + (int64_t)cg * c4 * 256 + lane;
-  const float *sp = scales + (int64_t)cg * nb * 64 + lane;
-  const uint8_t *zq = zp4 + (int64_t)cg * nbh * 64 + lane;
-  const float *zfp = zpf + (int64_t)cg * nb * 64 + lane;
+  const float *sp = scales + (int64_t)cg * nb * 64 + sz_pos(lane);
+  const uint8_t *zq = zp4 + (int64_t)cg * nbh * 64 + sz_pos(lane);
+  const float *zfp = zpf + (int64_t)cg * nb * 64 + sz_pos(lane);
   uint4 wr[PF][4];
   float sr[PF][QPG];
   uint32_t zr[PF][ZB];
@@ -474,9 +480,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
     for (int h = 0; h < PH; h++) {
       const int64_t cgi = dq_cgi[h];
       m.pk[h] = wq[((cgi * c4n + kg) * 4 + dq_g) * 64 + dq_col[h]];
-      m.zb[h] = zp4[(cgi * nbh + zbyte0) * 64 + dq_col[h]];
-      m.zb2[h] = SEGJ == 1 ? zp4[(cgi * nbh + zbyte1) * 64 + dq_col[h]] : 0u;
-      m.sc[h] = scales[(cgi * nb + min(blks, nbm1)) * 64 + dq_col[h]];
+      const int sc_col = sz_pos(dq_col[h]);
+      m.zb[h] = zp4[(cgi * nbh + zbyte0) * 64 + sc_col];
+      m.zb2[h] = SEGJ == 1 ? zp4[(cgi * nbh + zbyte1) * 64 + sc_col] : 0u;
+      m.sc[h] = scales[(cgi * nb + min(blks, nbm1)) * 64 + sc_col];
     }
   };
   // Dequantises dword j (32-k quarter j) of both packed uint4 into buffer buf.
@@ -645,6 +652,246 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
   y[i] = s + (bias ? bias[i % N] : 0.f);
 }
 
+// ------------------------------------------------------ decode MFMA GEMV
+
+// Activation prepass of the 16-row MFMA path (3 <= M <= 16): as k_af16split
+// (per-row power-of-two exponent e, hi = fp16(x), lo = fp16(x - hi), k offsets
+// 2, 3, 6, 7 of every 8 scaled by a further 2^-4) but in the operand order of
+// v_mfma_f32_16x16x32_f16: for k group kg and 32-k step j,
+// ahl16[((kg * 4 + j) * 2 + h) * 64 + 16 g + r] holds the 8 fp16 (hi for
+// h = 0, lo for h = 1) of row r at k = 128 kg + 32 j + 8 g .. +7.  Rows >= M
+// and k >= K are zeros.  One workgroup per row (16 rows).
+__global__ __launch_bounds__(256) void k_af16split16(const float *__restrict__ a, int64_t M,
+                                                     int64_t K, int c4n, int vec,
+                                                     uint4 *__restrict__ ahl,
+                                                     int *__restrict__ texp) {
+  __shared__ float red[4];
+  const int t = threadIdx.x, r = blockIdx.x;
+  const bool live = r < M;
+  const float *ar = a + (int64_t)r * K;
+  float mx = 0.f;
+  if (live) {
+    if (vec) {
+      for (int64_t k = 4 * (int64_t)t; k + 3 < K; k += 1024) {
+        const float4 x = *reinterpret_cast<const float4 *>(ar + k);
+        const float v[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float f = fabsf(v[i]);
+          mx = f < INFINITY ? fmaxf(mx, f) : mx;  // finite values only
+        }
+      }
+      for (int64_t k = (K & ~(int64_t)3) + t; k < K; k += 256) {
+        const float f = fabsf(ar[k]);
+        mx = f < INFINITY ? fmaxf(mx, f) : mx;
+      }
+    } else {
+      for (int64_t k = t; k < K; k += 256) {
+        const float f = fabsf(ar[k]);
+        mx = f < INFINITY ? fmaxf(mx, f) : mx;
+      }
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((t & 63) == 0) red[t >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (mx > 0.f) {
+    int ex;
+    frexpf(mx, &ex);
+    e = 14 - ex;
+  }
+  if (t == 0) texp[r] = e;
+  const int octets = c4n * 16;
+  for (int o = t; o < octets; o += 256) {
+    const int64_t k0 = (int64_t)o * 8;
+    float v[8];
+    if (live && vec && k0 + 8 <= K) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(ar + k0);
+      const float4 x1 = *reinterpret_cast<const float4 *>(ar + k0 + 4);
+      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+      v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = (live && k0 + i < K) ? ar[k0 + i] : 0.f;
+    }
+    half8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float x = ldexpf(v[i], (i & 2) ? e - 4 : e);
+      const _Float16 hh = (_Float16)x;
+      float res = x - (float)hh;
+      if (!isfinite(res)) res = 0.f;
+      hi[i] = hh;
+      lo[i] = (_Float16)res;
+    }
+    const int kg = o >> 4, j = (o >> 2) & 3, g = o & 3;
+    uint4 *dst = ahl + ((int64_t)(kg * 4 + j) * 2) * 64 + 16 * g + r;
+    dst[0] = __builtin_bit_cast(uint4, hi);
+    dst[64] = __builtin_bit_cast(uint4, lo);
+  }
+}
+
+// 16-row MFMA GEMV for 3 <= M <= 16 rows (decode with a few tokens).  One
+// workgroup per column group (64 columns = four 16-column tiles); its 4 waves
+// split K, wave w taking k groups w, w + 4, ...  Lane l works on column
+// 16 tile + l % 16 and k octet g = l / 16 of every 32-k step j: the 16 bytes
+// of packed codes at (g, column) hold exactly that lane's B operand for
+// steps j = 0..3 (wq's nibble order), so each lane dequantises only its own
+// operands (deq8, exact fp16 (q - zp) and 16 (q - zp)) and no LDS is needed
+// for B.  The activations come from k_af16split16 (hi and lo fp16, two
+// v_mfma_f32_16x16x32_f16 per step and tile); block scales are applied to the
+// fp32 per-segment sum D once per block: acc += s * D.  The four waves' sums
+// are added in wave order through LDS; the row exponents come off at the end.
+// Packed codes, scales, zero points and activation fragments of the next k
+// group are loaded while the current one is computed.
+template <int SEGJ>
+__global__ __launch_bounds__(256) void k_gemv_mfma(
+    const uint4 *__restrict__ ahl, const int *__restrict__ texp,
+    const uint4 *__restrict__ wq, const float *__restrict__ scales,
+    const uint8_t *__restrict__ zp4, const float *__restrict__ bias, float *__restrict__ y,
+    int M, int N, int c4n, int nb, int nbh, int lbs, int has_zp) {
+  __shared__ float4 red[4][4][64];  // [wave][tile][lane]
+  constexpr int NBK = 4 / SEGJ;     // blocks (scale segments) per k group
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int cg = blockIdx.x;
+  const int c16 = lane & 15, g = lane >> 4;
+  const uint4 *wp = wq + (int64_t)cg * c4n * 256 + g * 64 + c16;
+  // Scales and zero-point bytes of the lane's four columns are adjacent
+  // (sz_pos): one 16-byte and one 4-byte load per block.
+  const float4 *sp = reinterpret_cast<const float4 *>(scales + (int64_t)cg * nb * 64) + c16;
+  const uint32_t *zq = reinterpret_cast<const uint32_t *>(zp4 + (int64_t)cg * nbh * 64) + c16;
+
+  // Raw loads of one k group; they are first touched in compute(), so the
+  // wait for them does not also wait for the next k group's loads.
+  struct Ring {
+    uint4 ah[4], al[4];  // activation fragments (hi, lo) per 32-k step
+    uint4 w[4];          // packed codes per tile
+    float4 s[NBK];       // scales of the four tiles per block
+    uint32_t zw[NBK];    // zero-point bytes of the four tiles per block
+  };
+  auto fetch = [&](int kg, Ring &R) {
+#pragma unroll
+    for (int tl = 0; tl < 4; tl++) R.w[tl] = wp[(int64_t)kg * 256 + tl * 16];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint4 *ap = ahl + ((int64_t)(kg * 4 + j) * 2) * 64 + lane;
+      R.ah[j] = ap[0];
+      R.al[j] = ap[64];
+    }
+#pragma unroll
+    for (int q = 0; q < NBK; q++) {
+      const int bc = min((kg * KGRP + q * 32 * SEGJ) >> lbs, nb - 1);
+      R.s[q] = sp[(int64_t)bc * 16];
+      R.zw[q] = has_zp ? zq[(int64_t)(bc >> 1) * 16] : 0x88888888u;
+    }
+  };
+  uint32_t v_mlo, v_mhi, v_magic;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v_mlo) : "s"(0x000F000Fu));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v_mhi) : "s"(0x00F000F0u));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v_magic) : "s"(0x64006400u));
+
+  float4v acc[4], D[4];
+#pragma unroll
+  for (int tl = 0; tl < 4; tl++) acc[tl] = (float4v){0.f, 0.f, 0.f, 0.f};
+  const float4v zero4 = (float4v){0.f, 0.f, 0.f, 0.f};
+
+  // At the start of each block: its scales (zero past the last block, i.e.
+  // k padding) and the dequantisation constants -(1024 + z), -(1024 + 16 z)
+  // as fp16 pairs; -(1024 + z) in fp16 is 0xE400 + z (exact), so they are
+  // built with integer arithmetic.
+  auto compute = [&](int kg, const Ring &R) {
+    float sq[4];
+    uint32_t z1[4], z16[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int q = j / SEGJ;
+      const bool seg_start = (j % SEGJ) == 0;
+      if (seg_start) {
+        const int b = (kg * KGRP + q * 32 * SEGJ) >> lbs;
+        const bool live = b < nb;
+        const uint32_t sh = (min(b, nb - 1) & 1) * 4;
+        sq[0] = live ? R.s[q].x : 0.f;
+        sq[1] = live ? R.s[q].y : 0.f;
+        sq[2] = live ? R.s[q].z : 0.f;
+        sq[3] = live ? R.s[q].w : 0.f;
+#pragma unroll
+        for (int tl = 0; tl < 4; tl++) {
+          const uint32_t zv = (R.zw[q] >> (8 * tl + sh)) & 15u;
+          z1[tl] = 0xE400E400u + zv * 0x00010001u;
+          z16[tl] = 0xE400E400u + zv * 0x00100010u;
+        }
+      }
+      const half8 a_h = __builtin_bit_cast(half8, R.ah[j]);
+      const half8 a_l = __builtin_bit_cast(half8, R.al[j]);
+      half8 bt[4];
+#pragma unroll
+      for (int tl = 0; tl < 4; tl++) {
+        const uint32_t x = j == 0 ? R.w[tl].x : j == 1 ? R.w[tl].y : j == 2 ? R.w[tl].z : R.w[tl].w;
+        bt[tl] = __builtin_bit_cast(
+            half8, deq8(x, v_mlo, v_mhi, v_magic, __builtin_bit_cast(half2v, z1[tl]),
+                        __builtin_bit_cast(half2v, z16[tl])));
+      }
+      // All hi products first, then all lo: each lo MFMA then follows its
+      // tile's hi MFMA by three others instead of waiting on it.
+#pragma unroll
+      for (int tl = 0; tl < 4; tl++)
+        D[tl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, bt[tl], seg_start ? zero4 : D[tl], 0,
+                                                       0, 0);
+#pragma unroll
+      for (int tl = 0; tl < 4; tl++)
+        D[tl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, bt[tl], D[tl], 0, 0, 0);
+      if ((j + 1) % SEGJ == 0) {
+#pragma unroll
+        for (int tl = 0; tl < 4; tl++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[tl][i] = fmaf(sq[tl], D[tl][i], acc[tl][i]);
+      }
+    }
+  };
+
+  // Two-slot ring over this wave's k groups (unrolled by two so slots are
+  // static).
+  Ring ra, rb;
+  int kg = wave;
+  if (kg < c4n) fetch(kg, ra);
+  for (; kg < c4n; kg += 8) {
+    if (kg + 4 < c4n) fetch(kg + 4, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(kg, ra);
+    if (kg + 4 >= c4n) break;
+    if (kg + 8 < c4n) fetch(kg + 8, ra);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(kg + 4, rb);
+  }
+
+#pragma unroll
+  for (int tl = 0; tl < 4; tl++)
+    red[wave][tl][lane] = make_float4(acc[tl][0], acc[tl][1], acc[tl][2], acc[tl][3]);
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int tl = 0; tl < 4; tl++) {
+      float4 s = red[0][tl][lane];
+#pragma unroll
+      for (int w = 1; w < 4; w++) {
+        const float4 o = red[w][tl][lane];
+        s.x += o.x; s.y += o.y; s.z += o.z; s.w += o.w;
+      }
+      const int col = cg * 64 + tl * 16 + c16;
+      const float bv = (bias && col < N) ? bias[col] : 0.f;
+      const float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = 4 * g + i;
+        if (row < M && col < N) y[(int64_t)row * N + col] = ldexpf(sv[i], -texp[row]) + bv;
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------- generic path
 
 // One thread per output; dequantises exactly as the reference (q - zp in
@@ -668,12 +915,13 @@ __global__ __launch_bounds__(256) void k_nbits_generic(
     const int blk = k / bs;
     double z = 8.0;
     if (zpk == 1) {
-      const uint8_t zb = zp4[((int64_t)cgi * nbh + blk / 2) * 64 + cg];
+      const uint8_t zb = zp4[((int64_t)cgi * nbh + blk / 2) * 64 + sz_pos(cg)];
       z = (double)((blk & 1) ? (zb >> 4) : (zb & 15));
     } else if (zpk == 2) {
-      z = (double)zpf[((int64_t)cgi * nb + blk) * 64 + cg];
+      z = (double)zpf[((int64_t)cgi * nb + blk) * 64 + sz_pos(cg)];
     }
-    const float w = (float)(((double)q - z) * (double)scales[((int64_t)cgi * nb + blk) * 64 + cg]);
+    const float w =
+        (float)(((double)q - z) * (double)scales[((int64_t)cgi * nb + blk) * 64 + sz_pos(cg)]);
     acc += (double)a[(int64_t)row * K + k] * (double)w;
   }
   y[idx] = (float)(acc + (bias ? (double)bias[col] : 0.0));
@@ -682,7 +930,7 @@ __global__ __launch_bounds__(256) void k_nbits_generic(
 // ------------------------------------------------------------ host side
 
 struct NbitsPlan {
-  int path;  // 0 gemv, 1 mfma, 2 generic
+  int path;  // 0 gemv (dot8), 1 prefill mfma, 2 generic, 3 decode mfma
   int64_t M;
   // gemv
   int qpg = 1, qb = 128, ksplit = 1, kps = 0, nw = 4, kc = 0;
@@ -696,7 +944,13 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
   const mg_nbits_dev &d = w->nbits;
   NbitsPlan p;
   p.M = M;
-  if (M <= 4 && d.bs <= 4096) {
+  const bool int_zp = d.zp_kind != MG_ZP_FLOAT;
+  if (M >= 3 && M <= 16 && d.bs >= 32 && int_zp) {
+    p.path = 3;
+    p.off_a = 0;  // ahl16: 16 rows x kpad x (hi, lo) fp16
+    p.off_b = mg_align((size_t)16 * d.kpad * 4);  // texp[16]
+    p.total = mg_align(p.off_b + 16 * 4);
+  } else if (M <= 4 && d.bs <= 4096) {
     p.path = 0;
     p.qb = (int)std::min<int64_t>(d.bs, KGRP);
     p.qpg = KGRP / p.qb;
@@ -720,7 +974,7 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
     p.kc = (int)kc;
     p.lds = (size_t)std::max<int64_t>(kc * per_kg, nw * M * 64 * 4);
     p.total = 0;
-  } else if (d.bs >= 32 && d.zp_kind != MG_ZP_FLOAT) {
+  } else if (d.bs >= 32 && int_zp) {
     p.path = 1;
     const int64_t rows = 128;  // workgroup tile rows
     p.mpad = (M + rows - 1) / rows * rows;
@@ -823,7 +1077,7 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const uint8_t *b,
       for (int64_t blk = 0; blk < nb; blk++)
         for (int col = 0; col < 64; col++) {
           const int64_t n = cg * 64 + col;
-          if (n < N) sp[(size_t)((cg * nb + blk) * 64 + col)] = scales[n * nb + blk];
+          if (n < N) sp[(size_t)((cg * nb + blk) * 64 + sz_pos(col))] = scales[n * nb + blk];
         }
     }
   };
@@ -845,7 +1099,7 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const uint8_t *b,
       for (int64_t h = 0; h < nbh; h++)
         for (int col = 0; col < 64; col++) {
           const int64_t n = cg * 64 + col;
-          if (n < N) zp4[(size_t)((cg * nbh + h) * 64 + col)] = z[n * nbh + h];
+          if (n < N) zp4[(size_t)((cg * nbh + h) * 64 + sz_pos(col))] = z[n * nbh + h];
         }
   } else if (zp_kind == MG_ZP_FLOAT) {
     zpf.assign((size_t)(ng * nb * 64), 8.f);
@@ -854,7 +1108,7 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const uint8_t *b,
       for (int64_t blk = 0; blk < nb; blk++)
         for (int col = 0; col < 64; col++) {
           const int64_t n = cg * 64 + col;
-          if (n < N) zpf[(size_t)((cg * nb + blk) * 64 + col)] = z[n * nb + blk];
+          if (n < N) zpf[(size_t)((cg * nb + blk) * 64 + sz_pos(col))] = z[n * nb + blk];
         }
   }
 
@@ -905,6 +1159,27 @@ mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
       default: launch_gemv_q<4>(w, p, st, a_dev, vec, y_dev); break;
     }
     return mg_launch_check("k_gemv_dot8");
+  }
+  if (p.path == 3) {
+    uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
+    int *texp = reinterpret_cast<int *>(base + p.off_b);
+    const int vec = (w->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
+    hipLaunchKernelGGL(k_af16split16, dim3(16), dim3(256), 0, st, a_dev, M, w->K, (int)d.c4,
+                       vec, ahl, texp);
+    MG_TRY(mg_launch_check("k_af16split16"));
+    const int has_zp = zpk == MG_ZP_UINT4;
+    const uint8_t *zp_arg = has_zp ? d.zp4 : reinterpret_cast<const uint8_t *>(d.scales);
+    const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
+#define MG_DEC_LAUNCH(SJ_)                                                                    \
+  hipLaunchKernelGGL((k_gemv_mfma<SJ_>), dim3((unsigned)d.ng), dim3(256), 0, st, ahl, texp,    \
+                     reinterpret_cast<const uint4 *>(d.wq), d.scales, zp_arg, d.bias, y_dev,    \
+                     (int)M, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh,                       \
+                     __builtin_ctzll(d.bs), has_zp)
+    if (segj == 1) MG_DEC_LAUNCH(1);
+    else if (segj == 2) MG_DEC_LAUNCH(2);
+    else MG_DEC_LAUNCH(4);
+#undef MG_DEC_LAUNCH
+    return mg_launch_check("k_gemv_mfma");
   }
   if (p.path == 1) {
     uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
