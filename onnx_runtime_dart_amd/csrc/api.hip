@@ -315,12 +315,15 @@ mg_status mg_weight_f32_create(mg_ctx *ctx, const float *b, int64_t rows, int64_
   if (rows < 0 || cols < 0) return mg_fail(MG_INVALID_ARGUMENT, "Gemm: invalid B shape");
   MG_TRY(mg_use_device(ctx));
   const int64_t K = trans_b ? cols : rows, N = trans_b ? rows : cols;
+  // Device layout [N][K] (k contiguous, the GEMM's operand order): a
+  // transB weight is stored as given, a plain [K][N] one is transposed once
+  // here (the prepack of lib/src/onnx_graph.dart:2159-2161, reversed).
   std::vector<float> t;
   const float *src = b;
-  if (trans_b) {
+  if (!trans_b) {
     t.resize((size_t)(K * N));
-    for (int64_t n = 0; n < N; n++)
-      for (int64_t k = 0; k < K; k++) t[(size_t)(k * N + n)] = b[n * K + k];
+    for (int64_t k = 0; k < K; k++)
+      for (int64_t n = 0; n < N; n++) t[(size_t)(n * K + k)] = b[k * N + n];
     src = t.data();
   }
   mg_weight *w = new mg_weight();
@@ -826,7 +829,8 @@ mg_status gemm_w(mg_ctx *ctx, const float *a, bool a_dev_ptr, int64_t rows, int6
   q.K = K;
   q.batch = 1;
   q.lda = K;
-  q.ldb = w->N;
+  q.ldb = K;
+  q.trans_b = 1;  // the weight is stored [N][K]
   q.alpha = alpha;
   q.beta = beta;
   int64_t nc = 0;

@@ -1,4 +1,4 @@
-// fp32 MatMul / Gemm on gfx950 fp32 MFMA (v_mfma_f32_16x16x4_f32).
+// fp32 MatMul / Gemm on gfx950 fp32 MFMA (v_mfma_f32_32x32x2_f32).
 //
 // Reference semantics: opMatMul (numpy broadcast, lib/src/onnx_ops.dart:
 // 1710-1766) and opGemm (alpha * op(A) op(B) + beta * C,
@@ -6,9 +6,17 @@
 // and accumulates in fp32, so results differ from the reference's sequential
 // k-order sums only by accumulation order.
 //
-// Workgroup tile 64 x 64, four waves as 2 x 2 of 32 x 32 (2 x 2 MFMA
-// subtiles).  Each k step of 16 is staged in LDS k-major, so the MFMA operand
-// of lane (i = lane%16, g = lane/16) is As[k0 + g][row i] and Bs[k0 + g][col i].
+// Workgroup tile 128 x 128 (four waves as 2 x 2 of 64 x 64, i.e. 2 x 2 MFMA
+// tiles of 32 x 32 each) with stages of 16 k or, when that grid would not
+// fill the chip, 64 x 64 (one MFMA tile per wave) with stages of 32 k.  Each
+// stage is double-buffered in LDS as Xs[row][k] (k contiguous, rows padded by
+// 4 floats so 16-byte reads do not collide on banks) for both operands.
+// Within a stage of KS k, MFMA step s gives lane l the k = (KS / 2)(l / 32) + s
+// (not 2 s + l / 32): the sum over the stage is the same, and each lane reads
+// its KS / 2 k of a row with 16-byte LDS loads.
+// Operands may be stored k-contiguous ("RK": A [M][K], B^T [N][K]) or
+// row-contiguous ("KR": A^T [K][M], B [K][N]); the stage loader reads 32
+// bytes per thread either way and transposes KR tiles on their way into LDS.
 // Batches run on grid.z with per-batch element offsets computed on the host
 // (numpy broadcasting, lib/src/onnx_ops.dart:1742-1764).
 #include <hip/hip_runtime.h>
@@ -17,105 +25,175 @@
 
 namespace {
 
-typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
 
-constexpr int TM = 64, TN = 64, TK = 16;
 
+// One operand's stage for a workgroup tile of T = 64 WT rows: rows
+// [r0, r0 + T) x k [k0, k0 + KS) of X, E = KS T / 256 floats per thread,
+// zero outside [R, K).  KR: X stored [K][R] (element (r, k) at k * ld + r),
+// else [R][K] (r * ld + k).  In LDS a row holds KS floats padded to LDX.
+template <int WT, int KS, bool KR>
+struct Stage {
+  static constexpr int T = 64 * WT, E = KS * T / 256, LDX = KS + 4;
+  float v[E];
+
+  // fast: the stage lies inside X and 16-byte loads are aligned (decided per
+  // workgroup and stage, so the branch is uniform).
+  __device__ inline void load(const float *__restrict__ X, bool fast, int64_t ld, int64_t R,
+                              int64_t K, int64_t r0, int64_t k0, int t) {
+    const int64_t r = KR ? r0 + (t % (T / E)) * E : r0 + t / (KS / E);
+    const int64_t k = KR ? k0 + t / (T / E) : k0 + (t % (KS / E)) * E;
+    const float *p = KR ? X + k * ld + r : X + r * ld + k;
+    if (fast) {
+#pragma unroll
+      for (int q = 0; q < E / 4; q++) {
+        const float4 x = *reinterpret_cast<const float4 *>(p + 4 * q);
+        v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; e++)
+        v[e] = (KR ? (k < K && r + e < R) : (r < R && k + e < K)) ? p[e] : 0.f;
+    }
+  }
+
+  __device__ inline void store(float *__restrict__ xs, int t) const {
+    if (!KR) {
+      float *d = xs + (t / (KS / E)) * LDX + (t % (KS / E)) * E;
+#pragma unroll
+      for (int q = 0; q < E / 4; q++)
+        *reinterpret_cast<float4 *>(d + 4 * q) =
+            make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else {
+      float *d = xs + (t % (T / E)) * E * LDX + t / (T / E);
+#pragma unroll
+      for (int e = 0; e < E; e++) d[e * LDX] = v[e];
+    }
+  }
+};
+
+// WT = 2: 128 x 128 workgroup tile, each wave 64 x 64 (2 x 2 MFMA tiles);
+// WT = 1: 64 x 64, each wave one 32 x 32 tile (for grids too small to fill
+// the chip with the larger tile).  KS = k per LDS stage; a stage is
+// KS / 2 MFMA steps per tile.  AKR / BKR: operand layouts (A transposed, B
+// not transposed).
+template <int WT, int KS, bool AKR, bool BKR>
 __global__ __launch_bounds__(256) void k_f32_gemm(
     const float *__restrict__ A, const float *__restrict__ B,
     float *__restrict__ Y, int64_t M, int64_t N, int64_t K, int64_t lda,
-    int64_t ldb, int trans_a, int trans_b, const int64_t *__restrict__ a_off,
-    const int64_t *__restrict__ b_off, float alpha, float beta,
-    const float *__restrict__ C, int64_t c_rs, int64_t c_cs) {
-  __shared__ float As[TK][TM + 4];
-  __shared__ float Bs[TK][TN + 4];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+    int64_t ldb, int vec_a, int vec_b,
+    const int64_t *__restrict__ a_off, const int64_t *__restrict__ b_off, float alpha,
+    float beta, const float *__restrict__ C, int64_t c_rs, int64_t c_cs) {
+  constexpr int T = 64 * WT, LDX = KS + 4, NS = KS / 2;
+  __shared__ float As[2][T * LDX];
+  __shared__ float Bs[2][T * LDX];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
   const int wm = wave & 1, wn = wave >> 1;
+  const int l32 = lane & 31, h = lane >> 5;
   const int64_t bz = blockIdx.z;
   const float *Ab = A + (a_off ? a_off[bz] : 0);
   const float *Bb = B + (b_off ? b_off[bz] : 0);
-  const int64_t r0 = (int64_t)blockIdx.y * TM, c0 = (int64_t)blockIdx.x * TN;
-  const int li = lane & 15, lg = lane >> 4;
+  const int64_t r0 = (int64_t)blockIdx.y * T, c0 = (int64_t)blockIdx.x * T;
+  const bool a_in = vec_a && r0 + T <= M, b_in = vec_b && c0 + T <= N;
 
-  float4v acc[2][2];
+  float16v acc[WT][WT];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < WT; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < WT; j++) acc[i][j] = (float16v){};
 
-  for (int64_t k0 = 0; k0 < K; k0 += TK) {
-    // Stage A: 64 rows x 16 k.
+  const int nst = (int)((K + KS - 1) / KS);
+  Stage<WT, KS, AKR> sa;
+  Stage<WT, KS, BKR> sb;
+  auto load = [&](int st) {
+    const int64_t k0 = (int64_t)st * KS;
+    const bool kin = k0 + KS <= K;
+    sa.load(Ab, a_in && kin, lda, M, K, r0, k0, t);
+    sb.load(Bb, b_in && kin, ldb, N, K, c0, k0, t);
+  };
+  load(0);
+  sa.store(As[0], t);
+  sb.store(Bs[0], t);
+  __syncthreads();
+  for (int st = 0; st < nst; st++) {
+    const int buf = st & 1;
+    const bool more = st + 1 < nst;
+    if (more) load(st + 1);
+    float a[WT][NS], b[WT][NS];
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int idx = tid + e * 256;
-      int rr, kk;
-      if (!trans_a) {
-        rr = idx >> 4;
-        kk = idx & 15;
-      } else {
-        kk = idx >> 6;
-        rr = idx & 63;
+    for (int i = 0; i < WT; i++) {
+      const float *p = &As[buf][(wm * 32 * WT + i * 32 + l32) * LDX + NS * h];
+#pragma unroll
+      for (int q = 0; q < NS / 4; q++) {
+        const float4 x = *reinterpret_cast<const float4 *>(p + 4 * q);
+        a[i][4 * q] = x.x; a[i][4 * q + 1] = x.y; a[i][4 * q + 2] = x.z; a[i][4 * q + 3] = x.w;
       }
-      const int64_t row = r0 + rr, k = k0 + kk;
-      float v = 0.f;
-      if (row < M && k < K) v = trans_a ? Ab[k * lda + row] : Ab[row * lda + k];
-      As[kk][rr] = v;
     }
-    // Stage B: 16 k x 64 cols.
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int idx = tid + e * 256;
-      int kk, cc;
-      if (!trans_b) {
-        kk = idx >> 6;
-        cc = idx & 63;
-      } else {
-        cc = idx >> 4;
-        kk = idx & 15;
+    for (int j = 0; j < WT; j++) {
+      const float *p = &Bs[buf][(wn * 32 * WT + j * 32 + l32) * LDX + NS * h];
+#pragma unroll
+      for (int q = 0; q < NS / 4; q++) {
+        const float4 x = *reinterpret_cast<const float4 *>(p + 4 * q);
+        b[j][4 * q] = x.x; b[j][4 * q + 1] = x.y; b[j][4 * q + 2] = x.z; b[j][4 * q + 3] = x.w;
       }
-      const int64_t col = c0 + cc, k = k0 + kk;
-      float v = 0.f;
-      if (col < N && k < K) v = trans_b ? Bb[col * ldb + k] : Bb[k * ldb + col];
-      Bs[kk][cc] = v;
     }
-    __syncthreads();
 #pragma unroll
-    for (int kk = 0; kk < TK; kk += 4) {
-      float a[2], b[2];
+    for (int s = 0; s < NS; s++)
 #pragma unroll
-      for (int i = 0; i < 2; i++) a[i] = As[kk + lg][wm * 32 + i * 16 + li];
+      for (int i = 0; i < WT; i++)
 #pragma unroll
-      for (int j = 0; j < 2; j++) b[j] = Bs[kk + lg][wn * 32 + j * 16 + li];
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < WT; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+    if (more) {
+      sa.store(As[buf ^ 1], t);
+      sb.store(Bs[buf ^ 1], t);
     }
     __syncthreads();
   }
+
+  // Lane l holds column l % 32 and rows 8 (v / 4) + 4 (l / 32) + v % 4 of
+  // each 32 x 32 tile; 32 lanes write 128 contiguous bytes per store.
   float *Yb = Y + bz * M * N;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < WT; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int64_t col = c0 + wn * 32 + j * 16 + li;
+    for (int j = 0; j < WT; j++) {
+      const int64_t col = c0 + wn * 32 * WT + j * 32 + l32;
       if (col >= N) continue;
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int64_t row = r0 + wm * 32 + i * 16 + 4 * lg + r;
+      for (int v = 0; v < 16; v++) {
+        const int64_t row = r0 + wm * 32 * WT + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
         if (row >= M) continue;
-        float v = acc[i][j][r];
-        if (alpha != 1.f) v = alpha * v;
+        float y = acc[i][j][v];
+        if (alpha != 1.f) y = alpha * y;
         if (C) {
           float cv = C[row * c_rs + col * c_cs];
           if (beta != 1.f) cv = beta * cv;
-          v = v + cv;
+          y = y + cv;
         }
-        Yb[row * N + col] = v;
+        Yb[row * N + col] = y;
       }
     }
+}
+
+template <int WT, int KS>
+void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float *a,
+                const float *b, float *y, int vec_a, int vec_b) {
+#define MG_F32_ARGS                                                                           \
+  a, b, y, p.M, p.N, p.K, p.lda, p.ldb, vec_a, vec_b, p.a_off, p.b_off, p.alpha, p.beta, p.c, \
+      p.c_rs, p.c_cs
+  const bool akr = p.trans_a != 0, bkr = p.trans_b == 0;
+  if (!akr && !bkr)
+    hipLaunchKernelGGL((k_f32_gemm<WT, KS, false, false>), grid, dim3(256), 0, st, MG_F32_ARGS);
+  else if (!akr && bkr)
+    hipLaunchKernelGGL((k_f32_gemm<WT, KS, false, true>), grid, dim3(256), 0, st, MG_F32_ARGS);
+  else if (akr && !bkr)
+    hipLaunchKernelGGL((k_f32_gemm<WT, KS, true, false>), grid, dim3(256), 0, st, MG_F32_ARGS);
+  else
+    hipLaunchKernelGGL((k_f32_gemm<WT, KS, true, true>), grid, dim3(256), 0, st, MG_F32_ARGS);
+#undef MG_F32_ARGS
 }
 
 }  // namespace
@@ -123,10 +201,31 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
 mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
                      const float *b_dev, float *y_dev) {
   if (p.M == 0 || p.N == 0 || p.batch == 0) return MG_OK;
-  const dim3 grid((unsigned)((p.N + TN - 1) / TN), (unsigned)((p.M + TM - 1) / TM),
+  // 16-byte operand loads need 16-byte aligned rows: the base pointers and,
+  // for batches, every per-batch offset (offsets are multiples of M*K resp.
+  // K*N elements, so checking the leading dimension and one batch stride
+  // suffices).
+  auto aligned = [](const float *ptr, int64_t ld, int64_t batch_stride) {
+    return reinterpret_cast<uintptr_t>(ptr) % 16 == 0 && ld % 4 == 0 && batch_stride % 4 == 0;
+  };
+  const int vec_a = aligned(a_dev, p.lda, p.M * p.K) ? 1 : 0;
+  const int vec_b = aligned(b_dev, p.ldb, p.K * p.N) ? 1 : 0;
+  // The 128 x 128 tile when it still gives about two workgroups per CU,
+  // else 64 x 64.
+  const int64_t big = ((p.N + 127) / 128) * ((p.M + 127) / 128) * p.batch;
+  const bool use_big = big >= 2 * (int64_t)ctx->num_cus;
+  const int T = use_big ? 128 : 64;
+  const dim3 grid((unsigned)((p.N + T - 1) / T), (unsigned)((p.M + T - 1) / T),
                   (unsigned)p.batch);
-  hipLaunchKernelGGL(k_f32_gemm, grid, dim3(256), 0, ctx->stream, a_dev, b_dev, y_dev, p.M,
-                     p.N, p.K, p.lda, p.ldb, p.trans_a, p.trans_b, p.a_off, p.b_off, p.alpha,
-                     p.beta, p.c, p.c_rs, p.c_cs);
+#ifndef MG_F32_KS_BIG
+#define MG_F32_KS_BIG 16
+#endif
+#ifndef MG_F32_KS_SMALL
+#define MG_F32_KS_SMALL 32
+#endif
+  if (use_big)
+    launch_f32<2, MG_F32_KS_BIG>(p, grid, ctx->stream, a_dev, b_dev, y_dev, vec_a, vec_b);
+  else
+    launch_f32<1, MG_F32_KS_SMALL>(p, grid, ctx->stream, a_dev, b_dev, y_dev, vec_a, vec_b);
   return mg_launch_check("k_f32_gemm");
 }

@@ -75,7 +75,7 @@ struct mg_int8_dev {
 };
 
 struct mg_f32_dev {
-  float *b = nullptr;  // [K][N] row-major (transposed at upload if transB)
+  float *b = nullptr;  // [N][K] row-major (B^T; transposed at upload unless transB)
 };
 
 struct mg_weight {
