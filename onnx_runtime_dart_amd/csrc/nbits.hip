@@ -70,13 +70,13 @@ __host__ __device__ inline int sz_pos(int c) { return (c & 15) * 4 + (c >> 4); }
 // ahl[((m32 * c4n + kg) * 8 + st) * 128 + 32 h + r] holds the hi fp16 x 8 of
 // row r, k = 128 kg + 16 st + 8 h .. +7, and +64 the lo part; texp[row] = e.
 // Rows past M and k past K are zeros.  Non-finite values pass through in hi.
-// Workgroup: 8 rows, each row on 32 consecutive lanes (half a wave).
+// Workgroup: 4 rows, each row on one wave.
 __global__ __launch_bounds__(256) void k_af16split(
     const float *__restrict__ a, int64_t M, int64_t K, int c4n, int vec,
     uint4 *__restrict__ ahl, int *__restrict__ texp) {
   const int t = threadIdx.x;
-  const int u0 = t & 31;
-  const int64_t row = (int64_t)blockIdx.x * 8 + (t >> 5);
+  const int u0 = t & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (t >> 6);
   const int64_t m32 = row >> 5;
   const int r = (int)(row & 31);
   const int units = c4n * 8;  // 16-k pieces of the row
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void k_af16split(
     }
   };
   float mx = 0.f;
-  for (int u = u0; u < units; u += 32) {
+  for (int u = u0; u < units; u += 64) {
     float v[16];
     load16(u, v);
 #pragma unroll
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void k_af16split(
       mx = x < INFINITY ? fmaxf(mx, x) : mx;  // finite values only
     }
   }
-  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   int e = 0;
   if (mx > 0.f) {
     int ex;
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void k_af16split(
     e = 14 - ex;
   }
   if (u0 == 0) texp[row] = e;
-  for (int u = u0; u < units; u += 32) {
+  for (int u = u0; u < units; u += 64) {
     float v[16];
     load16(u, v);
     uint4 *o = ahl + ((m32 * c4n + (u >> 3)) * 8 + (u & 7)) * 128;
@@ -1186,7 +1186,7 @@ mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
     int *texp = reinterpret_cast<int *>(base + p.off_b);
     float *part = p.ksplit > 1 ? reinterpret_cast<float *>(base + p.off_c) : nullptr;
     const int vec = (w->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
-    hipLaunchKernelGGL(k_af16split, dim3((unsigned)(p.mpad / 8)), dim3(256), 0,
+    hipLaunchKernelGGL(k_af16split, dim3((unsigned)(p.mpad / 4)), dim3(256), 0,
                        st, a_dev, M, w->K, (int)d.c4, vec, ahl, texp);
     MG_TRY(mg_launch_check("k_af16split"));
     const int rows = 128;
