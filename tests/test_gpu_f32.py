@@ -102,3 +102,33 @@ def test_bert_layer_shapes(ops):
     p = rng.random((4, 12, 128, 128)).astype(np.float32)
     v = rng.standard_normal((4, 12, 128, 32)).astype(np.float32)
     assert G.rms_error(ops.op_matmul(p, v), oracle.matmul_f32(p, v)) <= TOL
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_layouts_multi_tile(ops, ta, tb):
+    # Every operand layout through several tiles and k stages, with ragged
+    # edges in M, N and K (partial tiles and a partial last stage).
+    rng = np.random.default_rng(12)
+    m, k, n = 257, 129, 383
+    a = rng.standard_normal((k, m) if ta else (m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k) if tb else (k, n)).astype(np.float32)
+    c = rng.standard_normal(n).astype(np.float32)
+    y = ops.op_gemm(a, b, c, alpha=1.5, beta=0.5, trans_a=ta, trans_b=tb)
+    ref = oracle.gemm_f32(a, b, c, alpha=1.5, beta=0.5, trans_a=ta, trans_b=tb)
+    assert G.rms_error(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("k", [40, 256])
+def test_large_tile_path(ops, k):
+    # Enough 128 x 128 tiles to take the large-tile kernel; N not a multiple
+    # of the tile; a weight uploaded without transB (transposed on upload).
+    rng = np.random.default_rng(13)
+    m, n = 2176, 4160
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((k, n)).astype(np.float32)
+    fw = ops.F32Weight(w, trans_b=False)
+    y = fw.gemm(a)
+    fw.release()
+    rows = np.concatenate([np.arange(64), np.arange(m - 64, m)])
+    ref = oracle.matmul_f32(a[rows], w)
+    assert G.rms_error(y[rows], ref) <= TOL

@@ -70,6 +70,14 @@ CASES = [
     (128, 1024, 1000, 128, "packed", True),
     (9, 35, 5, 16, "packed", True),          # generic path (bs 16)
     (12, 100, 33, 32, "float", False),       # generic path (float zp)
+    # 16-row MFMA decode path (3 <= M <= 16): partial k groups and blocks,
+    # ragged N, every block size it takes, with and without zero points.
+    (3, 200, 70, 32, "packed", True),
+    (7, 300, 130, 64, "packed", False),
+    (9, 96, 64, 32, "packed", False),
+    (12, 1000, 200, 256, "none", True),
+    (16, 4100, 96, 128, "packed", True),
+    (14, 640, 1000, 128, "none", False),
 ]
 
 
@@ -152,6 +160,24 @@ def test_nonfinite_and_ragged_rows_prefill(ops):
     np.testing.assert_array_equal(np.isneginf(y), np.isneginf(ref))
     assert np.isinf(ref[0]).any() and np.isnan(ref[2]).all()
     for r in range(3, m):
+        assert G.rms_error(y[r], ref[r]) <= TOL, r
+
+
+@pytest.mark.parametrize("m", [2, 6])
+def test_nonfinite_decode(ops, m):
+    # Decode paths (dot8 for M <= 2, 16-row MFMA above): inf / nan in one row
+    # give the reference's inf / nan columns there and leave other rows exact.
+    rng = np.random.default_rng(7)
+    k, n, bs = 256, 80, 32
+    b, s, zp = make_nbits(rng, n, k, bs, "packed")
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a[0, 3] = np.inf
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs)
+    y = w(a)
+    w.release()
+    ref = oracle.matmul_nbits(a, b, s, zp, k=k, n=n, block_size=bs)
+    np.testing.assert_array_equal(np.isfinite(y), np.isfinite(ref))
+    for r in range(1, m):
         assert G.rms_error(y[r], ref[r]) <= TOL, r
 
 
