@@ -318,7 +318,9 @@ def decode_sweep(torch, ops, ctx, T, randn, dev, args):
           flush=True)
     out = {"workload": "Llama-style 1B int4 decode step: 16 x (q 2048x2048, k/v 2048x512, "
                        "o 2048x2048, gate/up 2048x8192, down 8192x2048) + lm_head "
-                       "2048x128256; block_size 32 with uint4 zero points"}
+                       "2048x128256; block_size 32 with uint4 zero points",
+           "grouped": "q/k/v and gate/up of each layer as one mg_matmul_nbits_group_dev "
+                      "call each (the same products; 4 launches per layer instead of 7)"}
     for m in (1, 4, 16):
         a = {k: randn(m, k) for k in {k for _, k, _ in shapes}}
         y = {n: torch.empty((m, n), device=dev, dtype=torch.float32)
@@ -332,7 +334,22 @@ def decode_sweep(torch, ops, ctx, T, randn, dev, args):
             ws[-1].run_dev(a[LLAMA_HEAD[1]].data_ptr(), m, y[LLAMA_HEAD[2]].data_ptr())
             head_ev.append((e0, T.event()))
 
+        nl = len(LLAMA_LAYER)
+
+        def step_grouped():
+            for li in range(LLAMA_LAYERS):
+                lw = ws[li * nl:(li + 1) * nl]
+                ops.matmul_nbits_group_dev(lw[0:3], a[2048].data_ptr(), m,
+                                           [y[2048].data_ptr(), y[512].data_ptr(),
+                                            y[512].data_ptr()], ctx=ctx)
+                lw[3].run_dev(a[2048].data_ptr(), m, y[2048].data_ptr())
+                ops.matmul_nbits_group_dev(lw[4:6], a[2048].data_ptr(), m,
+                                           [y[8192].data_ptr(), y[8192].data_ptr()], ctx=ctx)
+                lw[6].run_dev(a[8192].data_ptr(), m, y[2048].data_ptr())
+            ws[-1].run_dev(a[LLAMA_HEAD[1]].data_ptr(), m, y[LLAMA_HEAD[2]].data_ptr())
+
         steps = max(args.steps // 2, 5)
+        ms_g = T.loop(step_grouped, steps, 2)
         ms = T.loop(step, steps, 2)
         nbytes = sum(nbits_bytes(m, k, n, LLAMA_BLOCK) for _, k, n in shapes)
         ms_head = float(np.mean([e0.elapsed_time(e1) for e0, e1 in head_ev[-steps:]]))
@@ -340,6 +357,8 @@ def decode_sweep(torch, ops, ctx, T, randn, dev, args):
         out[f"M{m}"] = {"ms_per_step": round(ms, 4), "bytes_per_step": nbytes,
                         "GB/s": round(nbytes / (ms / 1e3) / 1e9, 1),
                         "frac_hbm_peak": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "grouped_ms_per_step": round(ms_g, 4),
+                        "grouped_GB/s": round(nbytes / (ms_g / 1e3) / 1e9, 1),
                         "lm_head_us": round(ms_head * 1e3, 2),
                         "lm_head_GB/s": round(hb / (ms_head / 1e3) / 1e9, 1)}
         print(f"# decode M={m}: {out[f'M{m}']}", file=sys.stderr, flush=True)

@@ -125,6 +125,18 @@ mg_status mg_matmul_nbits(mg_ctx *ctx, const mg_weight *w, const float *a,
 mg_status mg_matmul_nbits_dev(mg_ctx *ctx, const mg_weight *w,
                               const float *a_dev, int64_t M, float *y_dev);
 
+/* Several MatMulNBits nodes that read the same activations (a decoder layer's
+ * q/k/v or gate/up projections): y_dev[i] = opMatMulNBits(a, W_i) for
+ * 1 <= n <= 4 weights sharing K, block_size, zero-point form and device, each
+ * result identical to a separate mg_matmul_nbits_dev call
+ * (lib/src/onnx_qlinear_ops.dart:115-228).  Decode shapes (M <= 16) run as
+ * one launch over all the weights' columns, which halves or thirds the
+ * per-token launch count of a layer. */
+mg_status mg_matmul_nbits_group_dev(mg_ctx *ctx, int32_t n,
+                                    const mg_weight *const *w,
+                                    const float *a_dev, int64_t M,
+                                    float *const *y_dev);
+
 /* ------------------------------------------- MatMulInteger / QLinearMatMul */
 
 /* Uploads an 8-bit B [K, N] (`b_signed`: int8 else uint8) with its zero

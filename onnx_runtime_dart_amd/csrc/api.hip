@@ -364,6 +364,31 @@ mg_status mg_matmul_nbits_dev(mg_ctx *ctx, const mg_weight *w, const float *a_de
   return mg_nbits_run(ctx, w, a_dev, M, y_dev, ctx->ws);
 }
 
+mg_status mg_matmul_nbits_group_dev(mg_ctx *ctx, int32_t n, const mg_weight *const *w,
+                                    const float *a_dev, int64_t M, float *const *y_dev) {
+  g_last_error.clear();
+  if (!ctx || !w || !y_dev || n < 1 || n > 4)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits_group_dev: 1 to 4 weights expected");
+  for (int32_t i = 0; i < n; i++) {
+    if (!w[i] || w[i]->kind != MG_W_NBITS)
+      return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits_group_dev: not a MatMulNBits weight");
+    if (w[i]->K != w[0]->K || w[i]->nbits.bs != w[0]->nbits.bs ||
+        w[i]->nbits.zp_kind != w[0]->nbits.zp_kind || w[i]->device != w[0]->device)
+      return mg_fail(MG_INVALID_ARGUMENT,
+                     "mg_matmul_nbits_group_dev: weights must share K, block_size, zero-point "
+                     "form and device");
+    if (!y_dev[i]) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits_group_dev: null output");
+  }
+  if (M < 0) return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid K, N, block_size or input shape");
+  if (M == 0) return MG_OK;
+  if (!a_dev) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits_group_dev: null input");
+  MG_TRY(mg_use_device(ctx));
+  const size_t ws = mg_nbits_group_ws_bytes(ctx, n, w, M);
+  MG_TRY(mg_check_control(ctx, (int64_t)ws));
+  MG_TRY(mg_ws_reserve(ctx, ws));
+  return mg_nbits_run_group(ctx, n, w, a_dev, M, y_dev, ctx->ws);
+}
+
 mg_status mg_matmul_nbits(mg_ctx *ctx, const mg_weight *w, const float *a, int64_t M, float *y) {
   g_last_error.clear();
   if (!ctx || !w || w->kind != MG_W_NBITS)

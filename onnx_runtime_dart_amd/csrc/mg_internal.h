@@ -113,6 +113,13 @@ size_t mg_nbits_ws_bytes(const mg_ctx *ctx, const mg_weight *w, int64_t M);
 // a_dev [M, K] f32, y_dev [M, N] f32; ws holds mg_nbits_ws_bytes bytes.
 mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
                        int64_t M, float *y_dev, void *ws);
+// n <= 4 weights with the same K, block size and zero-point kind applied to
+// one activation a_dev: y_dev[i] = a . W_i^T.  Decode shapes run as one
+// launch; ws holds mg_nbits_group_ws_bytes bytes.
+size_t mg_nbits_group_ws_bytes(const mg_ctx *ctx, int n, const mg_weight *const *w,
+                               int64_t M);
+mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
+                             const float *a_dev, int64_t M, float *const *y_dev, void *ws);
 
 // ------------------------------------------------------------ int8 entry
 

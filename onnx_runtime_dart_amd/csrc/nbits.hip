@@ -137,6 +137,32 @@ __global__ __launch_bounds__(256) void k_af16split(
 
 // ---------------------------------------------------------- decode GEMV
 
+// Up to GMAX weights that share K, block size, zero-point kind and the input
+// activations, launched together (q/k/v or gate/up of a decoder layer): the
+// grid's column groups are the concatenation of the members' column groups,
+// and each workgroup picks its member from the running totals cg_end.
+constexpr int GMAX = 4;
+struct GemvSet {
+  const uint4 *wq[GMAX];
+  const float *scales[GMAX];
+  const uint8_t *zp4[GMAX];
+  const float *zpf[GMAX];
+  const float *bias[GMAX];
+  float *y[GMAX];
+  int N[GMAX];
+  int cg_end[GMAX];
+  int n;
+};
+
+// Member of workgroup x and its local column group (workgroup-uniform).
+__device__ inline int gemv_member(const GemvSet &gs, int x, int *cg) {
+  int m = 0;
+  while (m + 1 < gs.n && x >= gs.cg_end[m]) m++;
+  *cg = x - (m ? gs.cg_end[m - 1] : 0);
+  return m;
+}
+
+
 // MR activation rows (M <= 4); QPG = quantisation blocks per k group
 // (128 / min(bs, 128)); ZPK = zero-point kind; PF = k groups of loads each
 // wave keeps in flight (4 with 4 waves per workgroup, 2 with up to 16).  One
@@ -163,10 +189,8 @@ __global__ __launch_bounds__(256) void k_af16split(
 // (deterministic), plus the bias, and written to y.
 template <int MR, int QPG, int ZPK, int PF>
 __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
-    const float *__restrict__ a, int64_t K, int vec, const uint4 *__restrict__ wq,
-    const float *__restrict__ scales, const uint8_t *__restrict__ zp4,
-    const float *__restrict__ zpf, const float *__restrict__ bias,
-    float *__restrict__ y, int N, int c4, int nb, int nbh, int lbs, int kc) {
+    const float *__restrict__ a, int64_t K, int vec, const GemvSet gs, int c4, int nb,
+    int nbh, int lbs, int kc) {
   extern __shared__ uint32_t smem[];
   uint32_t *sdig = smem;                                            // [MR][kc][64]
   float *salpha = reinterpret_cast<float *>(smem + MR * kc * 64);   // [MR][kc][QPG]
@@ -176,7 +200,15 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int NW = blockDim.x >> 6;
   const int nthr = blockDim.x;
-  const int cg = blockIdx.x;
+  int cg;
+  const int gm = gemv_member(gs, blockIdx.x, &cg);
+  const uint4 *__restrict__ wq = gs.wq[gm];
+  const float *__restrict__ scales = gs.scales[gm];
+  const uint8_t *__restrict__ zp4 = gs.zp4[gm];
+  const float *__restrict__ zpf = gs.zpf[gm];
+  const float *__restrict__ bias = gs.bias[gm];
+  float *__restrict__ y = gs.y[gm];
+  const int N = gs.N[gm];
   constexpr int G = 16 / QPG;        // octets per qblock
   constexpr int ZB = (QPG + 1) / 2;  // zero-point bytes per k group
 
@@ -748,15 +780,20 @@ __global__ __launch_bounds__(256) void k_af16split16(const float *__restrict__ a
 // group are loaded while the current one is computed.
 template <int SEGJ>
 __global__ __launch_bounds__(256) void k_gemv_mfma(
-    const uint4 *__restrict__ ahl, const int *__restrict__ texp,
-    const uint4 *__restrict__ wq, const float *__restrict__ scales,
-    const uint8_t *__restrict__ zp4, const float *__restrict__ bias, float *__restrict__ y,
-    int M, int N, int c4n, int nb, int nbh, int lbs, int has_zp) {
+    const uint4 *__restrict__ ahl, const int *__restrict__ texp, const GemvSet gs, int M,
+    int c4n, int nb, int nbh, int lbs, int has_zp) {
   __shared__ float4 red[4][4][64];  // [wave][tile][lane]
   constexpr int NBK = 4 / SEGJ;     // blocks (scale segments) per k group
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int cg = blockIdx.x;
+  int cg;
+  const int gm = gemv_member(gs, blockIdx.x, &cg);
+  const uint4 *__restrict__ wq = gs.wq[gm];
+  const float *__restrict__ scales = gs.scales[gm];
+  const uint8_t *__restrict__ zp4 = gs.zp4[gm];
+  const float *__restrict__ bias = gs.bias[gm];
+  float *__restrict__ y = gs.y[gm];
+  const int N = gs.N[gm];
   const int c16 = lane & 15, g = lane >> 4;
   const uint4 *wp = wq + (int64_t)cg * c4n * 256 + g * 64 + c16;
   // Scales and zero-point bytes of the lane's four columns are adjacent
@@ -940,7 +977,8 @@ struct NbitsPlan {
   size_t off_a = 0, off_b = 0, off_c = 0, off_d = 0, total = 0;
 };
 
-NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
+// ng_total: column groups of all weights launched together (grouped decode).
+NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t ng_total) {
   const mg_nbits_dev &d = w->nbits;
   NbitsPlan p;
   p.M = M;
@@ -960,7 +998,7 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
     // in flight per CU.
     // (The 16-wave form is register-limited to one row and blocks <= 64.)
     int64_t nw = 4;
-    if (M == 1 && p.qpg >= 2 && d.ng * 4 < 8 * (int64_t)std::max(ctx->num_cus, 1)) nw = 16;
+    if (M == 1 && p.qpg >= 2 && ng_total * 4 < 8 * (int64_t)std::max(ctx->num_cus, 1)) nw = 16;
     nw = std::min<int64_t>(nw, std::max<int64_t>(d.c4, 4));
     if (nw > 4) nw = nw > 8 ? 16 : 8;
     const int pf = nw == 4 ? 4 : 2;
@@ -996,17 +1034,33 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
   return p;
 }
 
+GemvSet make_set(int n, const mg_weight *const *w, float *const *y) {
+  GemvSet gs{};
+  gs.n = n;
+  int acc = 0;
+  for (int i = 0; i < n; i++) {
+    const mg_nbits_dev &d = w[i]->nbits;
+    gs.wq[i] = reinterpret_cast<const uint4 *>(d.wq);
+    gs.scales[i] = d.scales;
+    // Unused zero-point arrays point at the scales (never dereferenced).
+    gs.zp4[i] = d.zp4 ? d.zp4 : reinterpret_cast<const uint8_t *>(d.scales);
+    gs.zpf[i] = d.zpf ? d.zpf : d.scales;
+    gs.bias[i] = d.bias;
+    gs.y[i] = y[i];
+    gs.N[i] = (int)w[i]->N;
+    acc += (int)d.ng;
+    gs.cg_end[i] = acc;
+  }
+  return gs;
+}
+
 template <int MR, int QPG>
-void launch_gemv_zp(const mg_weight *w, const NbitsPlan &p, hipStream_t st, const float *a,
-                    int vec, float *y) {
+void launch_gemv_zp(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p,
+                    hipStream_t st, const float *a, int vec) {
   const mg_nbits_dev &d = w->nbits;
-  const dim3 grid((unsigned)d.ng), block((unsigned)(64 * p.nw));
-  // Unused zero-point arrays are pointed at the scales (never dereferenced).
-  const uint8_t *zp4 = d.zp4 ? d.zp4 : reinterpret_cast<const uint8_t *>(d.scales);
-  const float *zpf = d.zpf ? d.zpf : d.scales;
-#define MG_GEMV_ARGS                                                                    \
-  a, w->K, vec, reinterpret_cast<const uint4 *>(d.wq), d.scales, zp4, zpf, d.bias, y,        \
-      (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), p.kc
+  const dim3 grid((unsigned)gs.cg_end[gs.n - 1]), block((unsigned)(64 * p.nw));
+#define MG_GEMV_ARGS \
+  a, w->K, vec, gs, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), p.kc
 #define MG_GEMV_LAUNCH(Z_)                                                                   \
   do {                                                                                       \
     if (p.nw == 4)                                                                           \
@@ -1022,13 +1076,13 @@ void launch_gemv_zp(const mg_weight *w, const NbitsPlan &p, hipStream_t st, cons
 }
 
 template <int MR>
-void launch_gemv_q(const mg_weight *w, const NbitsPlan &p, hipStream_t st, const float *a,
-                   int vec, float *y) {
+void launch_gemv_q(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, hipStream_t st,
+                   const float *a, int vec) {
   switch (p.qpg) {
-    case 1: launch_gemv_zp<MR, 1>(w, p, st, a, vec, y); break;
-    case 2: launch_gemv_zp<MR, 2>(w, p, st, a, vec, y); break;
-    case 4: launch_gemv_zp<MR, 4>(w, p, st, a, vec, y); break;
-    default: launch_gemv_zp<MR, 8>(w, p, st, a, vec, y); break;
+    case 1: launch_gemv_zp<MR, 1>(w, gs, p, st, a, vec); break;
+    case 2: launch_gemv_zp<MR, 2>(w, gs, p, st, a, vec); break;
+    case 4: launch_gemv_zp<MR, 4>(w, gs, p, st, a, vec); break;
+    default: launch_gemv_zp<MR, 8>(w, gs, p, st, a, vec); break;
   }
 }
 
@@ -1139,48 +1193,83 @@ void mg_nbits_free(mg_weight *w) {
 }
 
 size_t mg_nbits_ws_bytes(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
-  return plan_nbits(ctx, w, M).total;
+  return plan_nbits(ctx, w, M, w->nbits.ng).total;
 }
 
-mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
-                       int64_t M, float *y_dev, void *ws) {
-  const mg_nbits_dev &d = w->nbits;
-  if (M == 0) return MG_OK;
-  const NbitsPlan p = plan_nbits(ctx, w, M);
+size_t mg_nbits_group_ws_bytes(const mg_ctx *ctx, int n, const mg_weight *const *w,
+                               int64_t M) {
+  int64_t ng = 0;
+  size_t most = 0;
+  for (int i = 0; i < n; i++) ng += w[i]->nbits.ng;
+  for (int i = 0; i < n; i++) most = std::max(most, plan_nbits(ctx, w[i], M, ng).total);
+  return most;
+}
+
+namespace {
+mg_status nbits_run_one(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
+                        float *y_dev, void *ws, const NbitsPlan &p);
+}  // namespace
+
+mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
+                             const float *a_dev, int64_t M, float *const *y_dev, void *ws) {
+  if (M == 0 || n == 0) return MG_OK;
+  int64_t ng = 0;
+  for (int i = 0; i < n; i++) ng += w[i]->nbits.ng;
+  const mg_weight *w0 = w[0];
+  const mg_nbits_dev &d = w0->nbits;
+  const NbitsPlan p = plan_nbits(ctx, w0, M, ng);
   hipStream_t st = ctx->stream;
   char *base = static_cast<char *>(ws);
-  const int zpk = d.zp_kind;
   if (p.path == 0) {
-    const int vec = (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 && w->K % 4 == 0) ? 1 : 0;
+    const GemvSet gs = make_set(n, w, y_dev);
+    const int vec = (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 && w0->K % 4 == 0) ? 1 : 0;
     switch (M) {
-      case 1: launch_gemv_q<1>(w, p, st, a_dev, vec, y_dev); break;
-      case 2: launch_gemv_q<2>(w, p, st, a_dev, vec, y_dev); break;
-      case 3: launch_gemv_q<3>(w, p, st, a_dev, vec, y_dev); break;
-      default: launch_gemv_q<4>(w, p, st, a_dev, vec, y_dev); break;
+      case 1: launch_gemv_q<1>(w0, gs, p, st, a_dev, vec); break;
+      case 2: launch_gemv_q<2>(w0, gs, p, st, a_dev, vec); break;
+      case 3: launch_gemv_q<3>(w0, gs, p, st, a_dev, vec); break;
+      default: launch_gemv_q<4>(w0, gs, p, st, a_dev, vec); break;
     }
     return mg_launch_check("k_gemv_dot8");
   }
   if (p.path == 3) {
+    const GemvSet gs = make_set(n, w, y_dev);
     uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
     int *texp = reinterpret_cast<int *>(base + p.off_b);
-    const int vec = (w->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
-    hipLaunchKernelGGL(k_af16split16, dim3(16), dim3(256), 0, st, a_dev, M, w->K, (int)d.c4,
+    const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
+    hipLaunchKernelGGL(k_af16split16, dim3(16), dim3(256), 0, st, a_dev, M, w0->K, (int)d.c4,
                        vec, ahl, texp);
     MG_TRY(mg_launch_check("k_af16split16"));
-    const int has_zp = zpk == MG_ZP_UINT4;
-    const uint8_t *zp_arg = has_zp ? d.zp4 : reinterpret_cast<const uint8_t *>(d.scales);
+    const int has_zp = d.zp_kind == MG_ZP_UINT4;
     const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
-#define MG_DEC_LAUNCH(SJ_)                                                                    \
-  hipLaunchKernelGGL((k_gemv_mfma<SJ_>), dim3((unsigned)d.ng), dim3(256), 0, st, ahl, texp,    \
-                     reinterpret_cast<const uint4 *>(d.wq), d.scales, zp_arg, d.bias, y_dev,    \
-                     (int)M, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh,                       \
-                     __builtin_ctzll(d.bs), has_zp)
+#define MG_DEC_LAUNCH(SJ_)                                                                \
+  hipLaunchKernelGGL((k_gemv_mfma<SJ_>), dim3((unsigned)ng), dim3(256), 0, st, ahl, texp,  \
+                     gs, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs),   \
+                     has_zp)
     if (segj == 1) MG_DEC_LAUNCH(1);
     else if (segj == 2) MG_DEC_LAUNCH(2);
     else MG_DEC_LAUNCH(4);
 #undef MG_DEC_LAUNCH
     return mg_launch_check("k_gemv_mfma");
   }
+  // Prefill and generic forms: one call per weight on the same stream (they
+  // reuse the workspace in stream order).
+  for (int i = 0; i < n; i++)
+    MG_TRY(nbits_run_one(ctx, w[i], a_dev, M, y_dev[i], ws, plan_nbits(ctx, w[i], M, ng)));
+  return MG_OK;
+}
+
+mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
+                       int64_t M, float *y_dev, void *ws) {
+  return mg_nbits_run_group(ctx, 1, &w, a_dev, M, &y_dev, ws);
+}
+
+namespace {
+mg_status nbits_run_one(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
+                        float *y_dev, void *ws, const NbitsPlan &p) {
+  const mg_nbits_dev &d = w->nbits;
+  hipStream_t st = ctx->stream;
+  char *base = static_cast<char *>(ws);
+  const int zpk = d.zp_kind;
   if (p.path == 1) {
     uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
     int *texp = reinterpret_cast<int *>(base + p.off_b);
@@ -1225,3 +1314,4 @@ mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
                      (int)w->N, (int)w->K, (int)d.c4, (int)d.nb, (int)d.nbh, (int)d.bs);
   return mg_launch_check("k_nbits_generic");
 }
+}  // namespace

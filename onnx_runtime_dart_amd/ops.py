@@ -77,6 +77,42 @@ class Context:
 _tls = threading.local()
 
 
+class DeviceBuffer:
+    """HBM buffer of the context's device (mg_buffer_alloc), for the _dev ops."""
+
+    def __init__(self, nbytes: int, ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(lib.mg_buffer_alloc(self.ctx.handle, max(self.nbytes, 1), C.byref(p)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray, ctx: Context | None = None) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes, ctx)
+        check(lib.mg_buffer_upload(buf.ctx.handle, C.c_void_p(buf.ptr), _ptr(arr), arr.nbytes))
+        return buf
+
+    def to_array(self, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        self.ctx.synchronize()
+        check(lib.mg_buffer_download(self.ctx.handle, _ptr(out), C.c_void_p(self.ptr),
+                                     out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib.mg_buffer_free(self.ctx.handle, C.c_void_p(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 def default_context() -> Context:
     ctx = getattr(_tls, "ctx", None)
     if ctx is None:
@@ -163,6 +199,18 @@ class NBitsWeight(_Weight):
     def run_dev(self, a_ptr: int, m: int, y_ptr: int):
         check(lib.mg_matmul_nbits_dev(self.ctx.handle, self.handle, C.c_void_p(a_ptr), m,
                                       C.c_void_p(y_ptr)))
+
+
+def matmul_nbits_group_dev(weights, a_ptr: int, m: int, y_ptrs, ctx: Context | None = None):
+    """Several NBitsWeight sharing K, block size and zero-point form applied to
+    one device activation a [m, K]: y_ptrs[i] receives a . W_i^T (one launch
+    for decode shapes)."""
+    ctx = ctx or weights[0].ctx
+    n = len(weights)
+    ws = (C.c_void_p * n)(*[w.handle.value if isinstance(w.handle, C.c_void_p) else w.handle
+                            for w in weights])
+    ys = (C.c_void_p * n)(*[C.c_void_p(p).value for p in y_ptrs])
+    check(lib.mg_matmul_nbits_group_dev(ctx.handle, n, ws, C.c_void_p(a_ptr), m, ys))
 
 
 def _zp_arg(z):

@@ -259,3 +259,46 @@ def test_control_cancel_and_budget(ops):
     assert G.rms_error(w(a), ref) <= TOL
     w.release()
     ctx.close()
+
+
+@pytest.mark.parametrize("m,bs,zp_mode", [(1, 32, "packed"), (1, 128, "none"), (2, 64, "packed"),
+                                          (5, 32, "packed"), (16, 128, "packed"),
+                                          (40, 128, "packed"), (3, 32, "float")])
+def test_group_matches_single_calls(ops, m, bs, zp_mode):
+    # q/k/v-like group: one activation, three weights of different N (one not
+    # a multiple of 64), one with a bias.  Each output must equal the oracle
+    # and the separate single-weight call.
+    rng = np.random.default_rng(0x5EED0005 + m)
+    k = 1000
+    ns = [200, 64, 330]
+    hw = [make_nbits(rng, n, k, bs, zp_mode) for n in ns]
+    bias = [None, rng.standard_normal(ns[1]).astype(np.float32), None]
+    ws = [ops.NBitsWeight(b, s, z, k=k, n=n, block_size=bs, bias=bb)
+          for (b, s, z), n, bb in zip(hw, ns, bias)]
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    ad = ops.DeviceBuffer.from_array(a)
+    ys = [ops.DeviceBuffer.from_array(np.full((m, n), np.nan, np.float32)) for n in ns]
+    ops.matmul_nbits_group_dev(ws, ad.ptr, m, [y.ptr for y in ys])
+    for (b, s, z), n, bb, w, y in zip(hw, ns, bias, ws, ys):
+        got = y.to_array((m, n), np.float32)
+        ref = oracle.matmul_nbits(a, b, s, z, k=k, n=n, block_size=bs, bias=bb)
+        assert G.rms_error(got, ref) <= TOL
+        single = w(a)
+        assert np.abs(got - single).max() <= 1e-5 * max(1.0, float(np.abs(single).max()))
+    for w in ws:
+        w.release()
+
+
+def test_group_validation(ops):
+    from onnx_runtime_dart_amd.errors import ArgumentError
+    rng = np.random.default_rng(8)
+    b, s, z = make_nbits(rng, 64, 256, 32, "packed")
+    b2, s2, z2 = make_nbits(rng, 64, 512, 32, "packed")
+    w1 = ops.NBitsWeight(b, s, z, k=256, n=64, block_size=32)
+    w2 = ops.NBitsWeight(b2, s2, z2, k=512, n=64, block_size=32)
+    with pytest.raises(ArgumentError):  # different K
+        ops.matmul_nbits_group_dev([w1, w2], 0, 1, [0, 0])
+    with pytest.raises(ArgumentError):  # more than 4 weights
+        ops.matmul_nbits_group_dev([w1] * 5, 0, 1, [0] * 5)
+    w1.release()
+    w2.release()
