@@ -531,11 +531,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
       uint32_t zb = m.zb[h], zb2 = m.zb2[h];
       asm volatile("" : "+v"(w), "+v"(zb), "+v"(zb2));
       zb |= zb2 << 8;
-      const int z = has_zp ? (int)((zb >> sh) & 15u) : 8;
-      const _Float16 z1 = (_Float16)(-(1024.f + (float)z));
-      const _Float16 z16 = (_Float16)(-(1024.f + 16.f * (float)z));
-      bl[buf][dq_dst[h] + 2 * j * 64] =
-          deq8(w, v_mlo, v_mhi, v_magic, (half2v){z1, z1}, (half2v){z16, z16});
+      const uint32_t z = has_zp ? (zb >> sh) & 15u : 8u;
+      // -(1024 + z) and -(1024 + 16 z) in fp16 are 0xE400 + z and + 16 z.
+      const uint32_t z1 = 0xE400E400u + z * 0x00010001u;
+      const uint32_t z16 = 0xE400E400u + z * 0x00100010u;
+      bl[buf][dq_dst[h] + 2 * j * 64] = deq8(w, v_mlo, v_mhi, v_magic,
+                                             __builtin_bit_cast(half2v, z1),
+                                             __builtin_bit_cast(half2v, z16));
     }
     if (j == 0) {
       const bool in_range = ((kg * KGRP + 32 * SEGJ * dq_g) >> lbs) < nb;
