@@ -197,11 +197,33 @@ mg_status mg_qlinear_matmul_w_dev(mg_ctx *ctx, const void *a_dev,
  * (the reference's toInt on NaN throws UnsupportedError). */
 mg_status mg_dynamic_quantize_linear(mg_ctx *ctx, const float *x, int64_t n,
                                      uint8_t *y, float *scale, int32_t *zp);
-/* Device form: scale/zp are written to device memory (scale_zp_dev holds one
- * float then one int32), so a following integer matmul can stay on device. */
+/* Device form: scale/zp are written to device memory, so a following integer
+ * matmul can stay on device.  scale_zp_dev receives 12 bytes: the float
+ * scale, the int32 zero point, then an int32 that is 1 when the input held
+ * Infinity or NaN (where the host form fails with MG_UNSUPPORTED; y, scale
+ * and zp are then unspecified) and 0 otherwise. */
 mg_status mg_dynamic_quantize_linear_dev(mg_ctx *ctx, const float *x_dev,
                                          int64_t n, uint8_t *y_dev,
                                          void *scale_zp_dev);
+
+/* DynamicQuantizeLinear -> MatMulInteger / QLinearMatMul with the quantized
+ * activation consumed where DQL left it: a_dev is DQL's uint8 [rows, K] and
+ * a_scale_zp_dev its scale/zp words, read on the device, so the chain needs
+ * no host synchronisation.  This is the dynamic-quantisation subgraph as the
+ * graph runs it (lib/src/onnx_graph.dart:2878-2917: DQL's y_scale and
+ * y_zero_point outputs feed QLinearMatMul's a_scale / a_zero_point inputs,
+ * or MatMulInteger's a_zero_point); results equal mg_matmul_integer_w_dev /
+ * mg_qlinear_matmul_w_dev called with the same scale and zero point. */
+mg_status mg_matmul_integer_w_dq_dev(mg_ctx *ctx, const uint8_t *a_dev,
+                                     int64_t rows, int64_t K,
+                                     const void *a_scale_zp_dev,
+                                     const mg_weight *w, int32_t *y_dev);
+mg_status mg_qlinear_matmul_w_dq_dev(mg_ctx *ctx, const uint8_t *a_dev,
+                                     int64_t rows, int64_t K,
+                                     const void *a_scale_zp_dev,
+                                     const mg_weight *w, float b_scale,
+                                     float y_scale, int32_t y_zp, int32_t lo,
+                                     int32_t hi, void *y_dev);
 
 /* ---------------------------------------------------------- fp32 MatMul/Gemm */
 

@@ -455,7 +455,7 @@ mg_status integer_host(mg_ctx *ctx, const void *a, int32_t a_signed, const int64
   IntProblem p;
   MG_TRY(check_integer(a_shape, a_rank, b_shape, b_rank, a_zp_len, a_zp != nullptr, b_zp_len,
                        b_zp != nullptr, &p));
-  const int64_t ysz = p.batch * p.M * p.N * (rq ? 1 : 4);
+  const int64_t ysz = p.batch * p.M * p.N * (mg_requant_out(rq) ? 1 : 4);
   if (p.batch * p.M * p.N == 0) return MG_OK;
   if ((!a && p.a_batch * p.M * p.K) || (!b && p.b_batch * p.K * p.N) || !y)
     return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger: null buffer");
@@ -511,7 +511,7 @@ mg_status integer_w(mg_ctx *ctx, const void *a, bool a_on_device, int32_t a_sign
   if (rows == 0 || w->N == 0) return MG_OK;
   if (!a || !y) return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger: null buffer");
   MG_TRY(mg_use_device(ctx));
-  const size_t ysz = (size_t)(rows * w->N) * (rq ? 1 : 4);
+  const size_t ysz = (size_t)(rows * w->N) * (mg_requant_out(rq) ? 1 : 4);
   Staging s;
   const size_t oa = a_on_device ? 0 : s.take((size_t)(rows * K));
   const size_t oy = y_on_device ? 0 : s.take(ysz);
@@ -598,6 +598,37 @@ mg_status mg_qlinear_matmul_w_dev(mg_ctx *ctx, const void *a_dev, int32_t a_sign
   mg_requant rq;
   MG_TRY(requant_params(a_scale, b_scale, y_scale, y_zp, lo, hi, &rq));
   return integer_w(ctx, a_dev, true, a_signed, rows, K, a_zp, a_zp_len, w, &rq, y_dev, true);
+}
+
+// DynamicQuantizeLinear output consumed in place: A is uint8 and its scale
+// and zero point are the words at a_scale_zp_dev (float scale, int32 zp), so
+// DQL -> MatMulInteger / QLinearMatMul needs no host round trip.
+mg_status mg_matmul_integer_w_dq_dev(mg_ctx *ctx, const uint8_t *a_dev, int64_t rows, int64_t K,
+                                     const void *a_scale_zp_dev, const mg_weight *w,
+                                     int32_t *y_dev) {
+  g_last_error.clear();
+  if (!ctx || !a_scale_zp_dev)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer_w_dq_dev: null context or scale/zp");
+  mg_requant rq;
+  rq.quantized_out = 0;
+  rq.a_zp_dev = static_cast<const int32_t *>(a_scale_zp_dev) + 1;
+  return integer_w(ctx, a_dev, true, 0, rows, K, nullptr, 0, w, &rq, y_dev, true);
+}
+
+mg_status mg_qlinear_matmul_w_dq_dev(mg_ctx *ctx, const uint8_t *a_dev, int64_t rows, int64_t K,
+                                     const void *a_scale_zp_dev, const mg_weight *w,
+                                     float b_scale, float y_scale, int32_t y_zp, int32_t lo,
+                                     int32_t hi, void *y_dev) {
+  g_last_error.clear();
+  if (!ctx || !a_scale_zp_dev)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_matmul_w_dq_dev: null context or scale/zp");
+  mg_requant rq;
+  MG_TRY(requant_params(1.f, b_scale, y_scale, y_zp, lo, hi, &rq));
+  rq.a_scale_dev = static_cast<const float *>(a_scale_zp_dev);
+  rq.a_zp_dev = static_cast<const int32_t *>(a_scale_zp_dev) + 1;
+  rq.b_scale = b_scale;
+  rq.y_scale = y_scale;
+  return integer_w(ctx, a_dev, true, 0, rows, K, nullptr, 0, w, &rq, y_dev, true);
 }
 
 // ------------------------------------------------------------------ DQL

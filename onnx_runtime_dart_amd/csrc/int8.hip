@@ -163,7 +163,19 @@ struct I8Epi {
   int y_vec;  // output base 16-byte aligned (always for the partials)
   float mult;
   int y_zp, lo, hi;
+  // Device-resident A scale (DynamicQuantizeLinear output): when set, the
+  // multiplier is formed on the device from it, b_scale and y_scale.
+  const float *a_scale_dev;
+  float b_scale, y_scale;
 };
+
+// Requant multiplier fl32(fl32(aS * bS) / yS) with each step rounded to f32
+// from a double product / quotient (lib/src/onnx_qlinear_ops.dart:95-98).
+__device__ inline float i8_mult(const I8Epi &e) {
+  if (!e.a_scale_dev) return e.mult;
+  const float ab = (float)((double)e.a_scale_dev[0] * (double)e.b_scale);
+  return (float)((double)ab / (double)e.y_scale);
+}
 
 // Final value of one output element and its store.
 template <int REQ>
@@ -173,7 +185,7 @@ __device__ inline void i8_finish(void *y, int64_t o, int32_t acc, int32_t rs, in
                      (uint32_t)e.K * (uint32_t)cav * (uint32_t)cbv;
   const int32_t vi = (int32_t)v;
   if (REQ) {
-    const float p = (float)((double)vi * (double)e.mult);
+    const float p = (float)((double)vi * (double)i8_mult(e));
     int qv = (int)rintf(p) + e.y_zp;
     qv = qv < e.lo ? e.lo : (qv > e.hi ? e.hi : qv);
     static_cast<uint8_t *>(y)[o] = (uint8_t)qv;
@@ -286,6 +298,7 @@ __global__ __launch_bounds__(256, 2) void k_i8_gemm(
   // int32 values go through the wave's LDS stage (rows padded by 16 bytes
   // against bank conflicts) and leave as whole 16-byte row pieces.
   const int64_t yb = (int64_t)bz * M;  // first output row of this batch
+  const float mult = MODE == 1 ? i8_mult(e) : 0.f;
   const bool vec_ok = (N % 4) == 0 && e.y_vec;
   int32_t *stage = reinterpret_cast<int32_t *>(smem) + wave * (32 * SROW);
 #pragma unroll
@@ -321,7 +334,7 @@ __global__ __launch_bounds__(256, 2) void k_i8_gemm(
           uint32_t pk = 0;
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            const float pf = (float)((double)v[i] * (double)e.mult);
+            const float pf = (float)((double)v[i] * (double)mult);
             int qv = (int)rintf(pf) + e.y_zp;
             qv = qv < e.lo ? e.lo : (qv > e.hi ? e.hi : qv);
             pk |= (uint32_t)(qv & 255) << (8 * i);
@@ -518,7 +531,10 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
   int32_t *ca = reinterpret_cast<int32_t *>(base + p.off_ca);
   int za_scalar = 0, za_len = 0;
   const int32_t *za = nullptr;
-  if (a_zp && a_zp_len == 1) {
+  if (rq && rq->a_zp_dev) {
+    za = rq->a_zp_dev;  // one int32 in device memory
+    za_len = 1;
+  } else if (a_zp && a_zp_len == 1) {
     za_scalar = a_zp[0];
   } else if (a_zp && a_zp_len > 1) {
     int32_t *zd = reinterpret_cast<int32_t *>(base + p.off_za);
@@ -540,14 +556,18 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
   e.ca = ca;
   e.rs_bs = a_batch > 1 ? p.mpad : 0;
   e.K = (int)K;
-  if (rq) {
+  const bool req = mg_requant_out(rq);
+  if (req) {
     e.mult = rq->mult;
     e.y_zp = rq->y_zp;
     e.lo = rq->lo;
     e.hi = rq->hi;
+    e.a_scale_dev = rq->a_scale_dev;
+    e.b_scale = rq->b_scale;
+    e.y_scale = rq->y_scale;
   }
   int32_t *part = reinterpret_cast<int32_t *>(base + p.off_part);
-  const int mode = K == 0 ? 3 : (p.ks > 1 ? 2 : (rq ? 1 : 0));
+  const int mode = K == 0 ? 3 : (p.ks > 1 ? 2 : (req ? 1 : 0));
   e.y_vec = (mode == 2 || reinterpret_cast<uintptr_t>(y_dev) % 16 == 0) ? 1 : 0;
   if (mode != 3) {
     const int64_t a_bs = a_batch > 1 ? (int64_t)p.m32n * kqp * 64 : 0;
@@ -577,7 +597,7 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
     const int64_t tot = batch * M * N;
     const unsigned blocks = (unsigned)((tot + 255) / 256);
     const int ks = mode == 3 ? 0 : p.ks;
-    if (rq)
+    if (req)
       hipLaunchKernelGGL(k_i8_reduce<1>, dim3(blocks), dim3(256), 0, st, part, y_dev, e, batch,
                          M, N, ks);
     else

@@ -129,10 +129,20 @@ mg_status mg_int8_upload(mg_ctx *ctx, mg_weight *w, const void *b,
 void mg_int8_free(mg_weight *w);
 size_t mg_int8_ws_bytes(const mg_weight *w, int64_t rows);
 // Requant parameters for QLinearMatMul; null => plain int32 output.
+// a_zp_dev, when set, is the A zero point (one int32) in device memory and
+// replaces the host one; quantized_out = 0 then keeps the int32 output of
+// MatMulInteger.  a_scale_dev, when set, is the A scale (one float) in device
+// memory: the multiplier is then formed on the device from it, b_scale and
+// y_scale instead of taken from mult.
 struct mg_requant {
-  float mult;
-  int32_t y_zp, lo, hi;
+  float mult = 0.f;
+  int32_t y_zp = 0, lo = 0, hi = 255;
+  int quantized_out = 1;
+  const float *a_scale_dev = nullptr;
+  const int32_t *a_zp_dev = nullptr;
+  float b_scale = 0.f, y_scale = 1.f;
 };
+inline bool mg_requant_out(const mg_requant *rq) { return rq && rq->quantized_out; }
 // a_dev [rows, K] (u8 or i8), a zero point array on host (len 0, 1 or rows),
 // y_dev int32 [rows, N] or (with rq) uint8/int8 [rows, N].
 mg_status mg_int8_run(mg_ctx *ctx, const mg_weight *w, const void *a_dev,

@@ -280,6 +280,22 @@ class Int8Weight(_Weight):
                                           self.handle, float(b_scale), float(y_scale),
                                           int(y_zp), int(lo), int(hi), C.c_void_p(y_ptr)))
 
+    def matmul_integer_dq_dev(self, a_ptr: int, rows: int, scale_zp_ptr: int, y_ptr: int):
+        """MatMulInteger on DynamicQuantizeLinear's device outputs: a uint8
+        [rows, K] and the zero point read from scale_zp_ptr on the device."""
+        check(lib.mg_matmul_integer_w_dq_dev(self.ctx.handle, C.c_void_p(a_ptr), rows, self.k,
+                                             C.c_void_p(scale_zp_ptr), self.handle,
+                                             C.c_void_p(y_ptr)))
+
+    def qlinear_matmul_dq_dev(self, a_ptr: int, rows: int, scale_zp_ptr: int, b_scale,
+                              y_scale, y_zp, y_ptr: int, *, lo, hi):
+        """QLinearMatMul on DynamicQuantizeLinear's device outputs: a_scale and
+        a_zp are read from scale_zp_ptr on the device."""
+        check(lib.mg_qlinear_matmul_w_dq_dev(self.ctx.handle, C.c_void_p(a_ptr), rows, self.k,
+                                             C.c_void_p(scale_zp_ptr), self.handle,
+                                             float(b_scale), float(y_scale), int(y_zp),
+                                             int(lo), int(hi), C.c_void_p(y_ptr)))
+
 
 class F32Weight(_Weight):
     """fp32 Gemm/MatMul B uploaded once; trans_b transposes on upload."""
@@ -331,8 +347,8 @@ def matmul_f32_dev(a_ptr: int, a_shape, b_ptr: int, b_shape, y_ptr: int,
 
 def dynamic_quantize_linear_dev(x_ptr: int, n: int, y_ptr: int, scale_zp_ptr: int,
                                 ctx: Context | None = None):
-    """DynamicQuantizeLinear on device: y uint8 [n]; scale (f32) then zp (i32) at
-    scale_zp_ptr."""
+    """DynamicQuantizeLinear on device: y uint8 [n]; at scale_zp_ptr 12 bytes:
+    scale (f32), zp (i32), and an i32 that is 1 when x held Infinity or NaN."""
     ctx = ctx or default_context()
     check(lib.mg_dynamic_quantize_linear_dev(ctx.handle, C.c_void_p(x_ptr), int(n),
                                              C.c_void_p(y_ptr), C.c_void_p(scale_zp_ptr)))

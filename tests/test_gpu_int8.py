@@ -146,3 +146,85 @@ def test_errors(ops):
         ops.op_matmul_integer(a, np.zeros((4, 2), np.int8))
     with pytest.raises(ArgumentError):
         ops.op_matmul_integer(np.zeros((2, 4, 3), np.uint8), np.zeros((3, 3, 2), np.int8))
+
+
+# DQL -> MatMulInteger / QLinearMatMul with the scale and zero point left in
+# device memory (mg_*_w_dq_dev).  Shapes cover the fused requant epilogue
+# (one K split), the split-K reduce, ragged edges and one row.
+DQ_SHAPES = [(128, 1024, 1024), (300, 256, 1024), (4, 2048, 256), (17, 65, 33), (1, 1, 1)]
+
+
+@pytest.mark.parametrize("m,k,n", DQ_SHAPES)
+@pytest.mark.parametrize("shift", [0.0, 1.5, -4.0])
+def test_dq_dev_chain(ops, m, k, n, shift):
+    rng = np.random.default_rng(m * 7 + k * 3 + n + int(shift * 10) + 100)
+    x = (rng.standard_normal((m, k)) + shift).astype(np.float32)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    bz = rng.integers(-3, 4, n).astype(np.int32)
+    w = ops.Int8Weight(b, bz)
+    xd = ops.DeviceBuffer.from_array(x)
+    qd = ops.DeviceBuffer(m * k)
+    szd = ops.DeviceBuffer.from_array(np.full(4, -1, np.int32))
+    y32 = ops.DeviceBuffer(m * n * 4)
+    y8 = ops.DeviceBuffer(m * n)
+    ops.dynamic_quantize_linear_dev(xd.ptr, m * k, qd.ptr, szd.ptr)
+    w.matmul_integer_dq_dev(qd.ptr, m, szd.ptr, y32.ptr)
+    q2, s2, z2 = oracle.dynamic_quantize_linear(x)
+    sz = szd.to_array(4, np.int32)
+    assert sz[:1].view(np.float32)[0] == s2 and sz[1] == z2 and sz[2] == 0
+    np.testing.assert_array_equal(qd.to_array((m, k), np.uint8), q2)
+    np.testing.assert_array_equal(y32.to_array((m, n), np.int32),
+                                  oracle.matmul_integer(q2, b, np.array(z2), bz))
+    for b_scale, y_scale, y_zp, lo, hi in ((2.0 ** -10, 0.05, 128, 0, 255),
+                                           (2.0 ** -6, 0.05, 128, 0, 255),
+                                           (0.003, 0.37, -5, -128, 127)):
+        w.qlinear_matmul_dq_dev(qd.ptr, m, szd.ptr, b_scale, y_scale, y_zp, y8.ptr, lo=lo, hi=hi)
+        yz = np.array(y_zp, np.int8 if lo < 0 else np.uint8)
+        want = oracle.qlinear_matmul(q2, np.float32(s2), np.array(z2), b, np.float32(b_scale),
+                                     bz, np.float32(y_scale), yz, lo=lo, hi=hi)
+        got = y8.to_array((m, n), np.int8 if lo < 0 else np.uint8)
+        np.testing.assert_array_equal(got, want, err_msg=f"b_scale={b_scale} y_zp={y_zp}")
+    for buf in (xd, qd, szd, y32, y8):
+        buf.free()
+    w.release()
+
+
+def test_dq_dev_degenerate_inputs(ops):
+    # All-zero activations: scale 0, zp 0 (lib/src/onnx_ops.dart:3556-3583),
+    # so every QLinearMatMul output is y_zp.  Non-finite input sets the flag.
+    m, k, n = 8, 64, 40
+    b = np.random.default_rng(5).integers(-127, 128, (k, n)).astype(np.int8)
+    w = ops.Int8Weight(b, None)
+    xd = ops.DeviceBuffer.from_array(np.zeros((m, k), np.float32))
+    qd = ops.DeviceBuffer(m * k)
+    szd = ops.DeviceBuffer.from_array(np.full(4, -1, np.int32))
+    y32 = ops.DeviceBuffer(m * n * 4)
+    y8 = ops.DeviceBuffer(m * n)
+    ops.dynamic_quantize_linear_dev(xd.ptr, m * k, qd.ptr, szd.ptr)
+    w.matmul_integer_dq_dev(qd.ptr, m, szd.ptr, y32.ptr)
+    w.qlinear_matmul_dq_dev(qd.ptr, m, szd.ptr, 0.01, 0.05, 77, y8.ptr, lo=0, hi=255)
+    assert szd.to_array(4, np.int32)[:3].tolist() == [0, 0, 0]
+    assert not y32.to_array((m, n), np.int32).any()
+    assert (y8.to_array((m, n), np.uint8) == 77).all()
+    x = np.ones((m, k), np.float32)
+    x[3, 5] = np.inf
+    xi = ops.DeviceBuffer.from_array(x)
+    ops.dynamic_quantize_linear_dev(xi.ptr, m * k, qd.ptr, szd.ptr)
+    assert szd.to_array(4, np.int32)[2] == 1
+    for buf in (xd, xi, qd, szd, y32, y8):
+        buf.free()
+    w.release()
+
+
+def test_dq_dev_errors(ops):
+    from onnx_runtime_dart_amd.errors import ArgumentError
+    w = ops.Int8Weight(np.zeros((4, 4), np.int8), None)
+    buf = ops.DeviceBuffer(64)
+    with pytest.raises(ArgumentError):
+        w.matmul_integer_dq_dev(buf.ptr, 2, 0, buf.ptr)
+    with pytest.raises(ArgumentError):
+        w.qlinear_matmul_dq_dev(buf.ptr, 2, 0, 1.0, 1.0, 0, buf.ptr, lo=0, hi=255)
+    with pytest.raises(ArgumentError):
+        w.qlinear_matmul_dq_dev(buf.ptr, 2, buf.ptr, 1.0, 1.0, 0, buf.ptr, lo=0, hi=127)
+    buf.free()
+    w.release()
