@@ -433,60 +433,97 @@ __device__ inline uint4 deq8(uint32_t x, uint32_t mlo, uint32_t mhi, uint32_t ma
                     __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d3) + zz16));
 }
 
-// Workgroup tile: 128 rows x 128 columns (two column groups), 4 waves; wave w
-// owns rows [32*w, +32) of the tile and all 128 columns (4 MFMA tiles of
-// 32x32, v_mfma_f32_32x32x16_f16).  Per k group (128 k = 8 steps of 16 k):
-//   * the workgroup dequantises the 128x128 weight tile once into LDS, in
+// Up to GMAX weights that share K, block size, zero-point kind and the input
+// activations, run as one prefill launch: the grid's column tiles are the
+// concatenation of the members' column tiles (ct_end holds the running
+// totals), and each workgroup picks its member from them.  Split-K partials of
+// member i start at part + part_off[i] ([ksplit][M][N_i]).
+struct PrefillSet {
+  const uint4 *wq[GMAX];
+  const float *scales[GMAX];
+  const uint8_t *zp4[GMAX];
+  const float *bias[GMAX];
+  float *y[GMAX];
+  int64_t part_off[GMAX];
+  int N[GMAX];
+  int ct_end[GMAX];
+  int y_vec[GMAX];  // y base 16-byte aligned
+  int n;
+};
+
+// Member of global column tile x and its local tile index (workgroup-uniform).
+__device__ inline int prefill_member(const PrefillSet &ps, int x, int *nt) {
+  int m = 0;
+#pragma unroll
+  for (int i = 0; i < GMAX - 1; i++)
+    if (i + 1 < ps.n && x >= ps.ct_end[i]) m = i + 1;
+  *nt = x - (m ? ps.ct_end[m - 1] : 0);
+  return m;
+}
+
+// Workgroup tile: 128 rows x 32*NT columns (NT/2 column groups), 4 waves;
+// wave w owns rows [32*w, +32) of the tile and all its columns (NT MFMA tiles
+// of 32x32, v_mfma_f32_32x32x16_f16).  NT = 4 for wide weights; NT = 2 halves
+// the tile so that narrow weights still give enough workgroups without
+// splitting K.  Per k group (128 k = 8 steps of 16 k):
+//   * the workgroup dequantises the 128 x 32*NT weight tile once into LDS, in
 //     MFMA B-fragment order (double-buffered; the next k group's packed codes
 //     are loaded at the start of the current one and unpacked step by step
 //     between its MFMAs);
-//   * each wave streams its activation fragments (hi and lo) from global, two
+//   * each wave streams its activation fragments (hi and lo) from global, PD
 //     steps ahead of use, into a per-segment fp32 accumulator D;
 //   * at the end of each scale segment (SEGJ 32-k quarters = min(block_size,
-//     128) k) the block scale times the row's 2^-e is applied:
-//     acc += s * 2^-e * D.
-// The epilogue restages each wave's 32x128 fp32 tile through LDS and writes
-// Y (or the split-K partials) as 16-byte, row-contiguous, non-temporal stores.
+//     128) k) the block scale is applied: acc += s * D.
+// The epilogue applies the row factor 2^-e, restages each wave's 32-row tile
+// through LDS and writes Y (or the split-K partials) as 16-byte,
+// row-contiguous, non-temporal stores.
 // Grid: x = tiles in XCD-aware order (workgroup L runs on XCD L % 8; all row
 // tiles of one column tile get the same L % 8, so its weights are read from
 // HBM once into that XCD's L2); y = k splits, each over kps k groups, whose
-// partial sums go to `part` and are added by k_gemm_reduce (ksplit > 1).
-template <int SEGJ>
-__global__ __launch_bounds__(256, 2) void k_gemm_f16split(
-    const uint4 *__restrict__ ahl, const int *__restrict__ texp,
-    const uint4 *__restrict__ wq, const float *__restrict__ scales,
-    const uint8_t *__restrict__ zp4, const float *__restrict__ bias,
-    float *__restrict__ y, float *__restrict__ part, int M, int N, int c4n,
-    int nb, int nbh, int lbs, int has_zp, int mtiles, int ntiles, int kps, int y_vec) {
-  __shared__ uint4 bl[2][4 * 8 * 64];      // [buf][n32][step][lane] fp16 x 8
-  __shared__ float scl[2][4][32][4];       // [buf][segment][col % 32][n32]
+// partial sums go to the partials and are added by k_gemm_reduce (ksplit > 1).
+template <int SEGJ, int NT>
+__global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
+    const uint4 *__restrict__ ahl, const int *__restrict__ texp, const PrefillSet ps,
+    float *__restrict__ part, int M, int c4n, int nb, int nbh, int lbs, int has_zp,
+    int mtiles, int ntiles, int kps) {
+  constexpr int PH = NT / 2;                 // column groups per tile
+  constexpr int TC = 32 * NT;                // tile columns
+  __shared__ uint4 bl[2][NT * 8 * 64];       // [buf][n32][step][lane] fp16 x 8
+  __shared__ float scl[2][4][32][4];         // [buf][segment][col % 32][n32]
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int L = blockIdx.x;
   const int xcd = L & 7, q = L >> 3;
   const int mt = q % mtiles;
-  const int nt = (q / mtiles) * 8 + xcd;
-  if (nt >= ntiles) return;
+  const int ntg = (q / mtiles) * 8 + xcd;
+  if (ntg >= ntiles) return;
+  int nt;
+  const int mem = prefill_member(ps, ntg, &nt);
+  const uint4 *__restrict__ wq = ps.wq[mem];
+  const float *__restrict__ scales = ps.scales[mem];
+  const uint8_t *__restrict__ zp4 = ps.zp4[mem];
+  const float *__restrict__ bias = ps.bias[mem];
+  const int N = ps.N[mem];
   const int ks = blockIdx.y;
   const int kg0 = ks * kps;
   const int kg1 = min(c4n, kg0 + kps);
   const int m32 = mt * 4 + wave;  // this wave's 32-row subtile
   const int lc = lane & 31, lh = lane >> 5;
 
-  // Cooperative dequantisation of the 512 packed uint4 of a k group: thread t
-  // handles u = t + 256 h, h < 2 -> (column group 2*nt + h, g = wave,
-  // col = lane); its dword j (k = 32j + 8g .. +7) is MFMA step 2j + g/2, half
-  // g%2.  The thread with g = s also stages the column's scale of segment s
-  // (threads with g >= segments per k group write an unused slot).
-  constexpr int PH = 2;
+  // Cooperative dequantisation of the 256*PH packed uint4 of a k group:
+  // thread t handles u = t + 256 h, h < PH -> (column group PH*nt + h,
+  // g = wave, col = lane); its dword j (k = 32j + 8g .. +7) is MFMA step
+  // 2j + g/2, half g%2.  The thread with g = s also stages the column's scale
+  // of segment s (threads with g >= segments per k group write an unused
+  // slot).
   const int dq_g = wave;
   int dq_cgi[PH], dq_col[PH], dq_dst[PH], dq_c[PH];
 #pragma unroll
   for (int h = 0; h < PH; h++) {
     const int u = t + 256 * h;
-    dq_cgi[h] = 2 * nt + (u >> 8);
+    dq_cgi[h] = PH * nt + (u >> 8);
     dq_col[h] = u & 63;
-    dq_c[h] = (u >> 8) * 64 + dq_col[h];  // column within the 128-column tile
+    dq_c[h] = (u >> 8) * 64 + dq_col[h];  // column within the tile
     const int n32 = dq_c[h] >> 5;
     dq_dst[h] = (n32 * 8 + (dq_g >> 1)) * 64 + (dq_c[h] & 31) + 32 * (dq_g & 1);
   }
@@ -518,7 +555,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
       m.sc[h] = scales[(cgi * nb + min(blks, nbm1)) * 64 + sc_col];
     }
   };
-  // Dequantises dword j (32-k quarter j) of both packed uint4 into buffer buf.
+  // Dequantises dword j (32-k quarter j) of the packed uint4 into buffer buf.
   auto dequant_quarter = [&](int kg, const Meta &m, int buf, int j) {
     const int blk0 = (kg * KGRP) >> lbs;
     const int blk = (kg * KGRP + 32 * j) >> lbs;
@@ -553,15 +590,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
   const uint4 *abase = ahl + (int64_t)m32 * c4n * 1024 + lane;
   auto a_ptr = [&](int kg, int st) { return abase + ((int64_t)kg * 8 + st) * 128; };
 
-  float16v acc[4], D[4];
+  float16v acc[NT], D[NT];
 #pragma unroll
-  for (int n = 0; n < 4; n++) acc[n] = (float16v){};
+  for (int n = 0; n < NT; n++) acc[n] = (float16v){};
   const float16v zero16 = (float16v){};
 
   // Ring of activation fragments (slot = step), loaded PD steps ahead.  Loads
-  // past the last k group re-read it (results unused).  Memory loads complete
-  // in issue order, so the next k group's weights, loaded at step 0, are
-  // first needed at step PD, together with the activations issued after them.
+  // past the last k group re-read it (results unused).  The next k group's
+  // weights, loaded at step 0, are dequantised in steps PD..7.
   constexpr int PD = 4;
   uint4 ah[8], al[8];
 #pragma unroll
@@ -597,7 +633,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
       const half8 a_h = __builtin_bit_cast(half8, ah[st]);
       const half8 a_l = __builtin_bit_cast(half8, al[st]);
 #pragma unroll
-      for (int n = 0; n < 4; n++) {
+      for (int n = 0; n < NT; n++) {
         const half8 b = __builtin_bit_cast(half8, bl[buf][(n * 8 + st) * 64 + lane]);
         D[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, b, seg_start ? zero16 : D[n], 0, 0, 0);
         D[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, b, D[n], 0, 0, 0);
@@ -609,7 +645,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
         const float4 s4 = *reinterpret_cast<const float4 *>(&scl[buf][st / (2 * SEGJ)][lc][0]);
         const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-        for (int n = 0; n < 4; n++)
+        for (int n = 0; n < NT; n++)
 #pragma unroll
           for (int v = 0; v < 16; v++) acc[n][v] = fmaf(sc[n], D[n][v], acc[n][v]);
       }
@@ -617,10 +653,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
     __syncthreads();
   }
 
-  // Epilogue: stage the wave's 32x128 tile row-major in LDS (the weight
+  // Epilogue: stage the wave's 32 x TC tile row-major in LDS (the weight
   // buffers are free now; every wave passed the last barrier), then write
   // 16-byte row pieces.
-  float *stage = reinterpret_cast<float *>(&bl[0][0]) + wave * (32 * 128);
+  float *stage = reinterpret_cast<float *>(&bl[0][0]) + wave * (32 * TC);
   // Row exponents of the lane's 16 output rows 8*(v/4) + 4*lh + v%4; the row
   // factor 2^-e is applied with ldexp (exact, and graded into subnormals).
   int4 ex[4];
@@ -628,19 +664,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
   for (int i = 0; i < 4; i++)
     ex[i] = reinterpret_cast<const int4 *>(texp)[(int64_t)m32 * 8 + 2 * i + lh];
 #pragma unroll
-  for (int n = 0; n < 4; n++)
+  for (int n = 0; n < NT; n++)
 #pragma unroll
     for (int v = 0; v < 16; v++) {
       const int r = 8 * (v >> 2) + 4 * lh + (v & 3);
       const int4 e4 = ex[v >> 2];
       const int e = (v & 3) == 0 ? e4.x : (v & 3) == 1 ? e4.y : (v & 3) == 2 ? e4.z : e4.w;
-      stage[r * 128 + n * 32 + lc] = ldexpf(acc[n][v], -e);
+      stage[r * TC + n * 32 + lc] = ldexpf(acc[n][v], -e);
     }
   __syncthreads();
   const bool split = gridDim.y > 1;
-  float *dst = split ? part + (int64_t)ks * M * N : y;
-  const int c4 = lane & 31;
-  const int col = nt * 128 + 4 * c4;
+  float *dst = split ? part + ps.part_off[mem] + (int64_t)ks * M * N : ps.y[mem];
+  // Lane -> (row offset, 4-column piece): a row is 8*NT pieces.
+  constexpr int PPR = 8 * NT, RPI = 64 / PPR;  // pieces per row, rows per iteration
+  const int c4 = lane % PPR, ro = lane / PPR;
+  const int col = nt * TC + 4 * c4;
   float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
   if (!split && bias) {
     if (col + 3 < N) {
@@ -653,12 +691,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
   }
   // 16-byte stores need N % 4 == 0 and a 16-byte aligned destination (the
   // partials buffer always is; y is checked by the host).
-  const bool vec_ok = (N % 4) == 0 && (split || y_vec);
+  const bool vec_ok = (N % 4) == 0 && (split || ps.y_vec[mem]);
 #pragma unroll 4
-  for (int it = 0; it < 16; it++) {
-    const int r = 2 * it + lh;
+  for (int it = 0; it < 32 / RPI; it++) {
+    const int r = RPI * it + ro;
     const int row = m32 * 32 + r;
-    float4v v = *reinterpret_cast<const float4v *>(&stage[r * 128 + 4 * c4]);
+    float4v v = *reinterpret_cast<const float4v *>(&stage[r * TC + 4 * c4]);
     v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
     if (row < M) {
       float *p = dst + (int64_t)row * N + col;
@@ -674,16 +712,32 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f16split(
   }
 }
 
-// y = sum over k splits of part + bias (deterministic split-K reduction).
+// y_i = sum over k splits of the partials of member i + bias_i
+// (deterministic split-K reduction); elements of the members concatenated,
+// member i starting at element e_end[i - 1] (M * N_i elements each).
+struct ReduceSet {
+  const float *bias[GMAX];
+  float *y[GMAX];
+  int64_t part_off[GMAX];
+  int64_t e_end[GMAX];
+  int N[GMAX];
+  int n;
+};
 __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part,
-                                                     const float *__restrict__ bias,
-                                                     float *__restrict__ y, int64_t MN, int N,
-                                                     int ksplit) {
+                                                     const ReduceSet rs, int ksplit) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= MN) return;
+  if (i >= rs.e_end[rs.n - 1]) return;
+  int m = 0;
+#pragma unroll
+  for (int j = 0; j < GMAX - 1; j++)
+    if (j + 1 < rs.n && i >= rs.e_end[j]) m = j + 1;
+  const int64_t li = i - (m ? rs.e_end[m - 1] : 0);
+  const int64_t mn = rs.e_end[m] - (m ? rs.e_end[m - 1] : 0);
+  const float *p = part + rs.part_off[m] + li;
   float s = 0.f;
-  for (int k = 0; k < ksplit; k++) s += part[(int64_t)k * MN + i];
-  y[i] = s + (bias ? bias[i % N] : 0.f);
+  for (int k = 0; k < ksplit; k++) s += p[(int64_t)k * mn];
+  const float *b = rs.bias[m];
+  rs.y[m][li] = s + (b ? b[li % rs.N[m]] : 0.f);
 }
 
 // ------------------------------------------------------ decode MFMA GEMV
@@ -976,11 +1030,14 @@ struct NbitsPlan {
   size_t lds = 0;
   // mfma
   int64_t mpad = 0;
+  int nt = 4;  // prefill tile width in 32-column MFMA tiles (4 or 2)
   size_t off_a = 0, off_b = 0, off_c = 0, off_d = 0, total = 0;
 };
 
-// ng_total: column groups of all weights launched together (grouped decode).
-NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t ng_total) {
+// ng_total / n_total: column groups / columns of all weights launched together
+// (sibling weights sharing one input).
+NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t ng_total,
+                     int64_t n_total) {
   const mg_nbits_dev &d = w->nbits;
   NbitsPlan p;
   p.M = M;
@@ -1016,19 +1073,29 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
     p.total = 0;
   } else if (d.bs >= 32 && int_zp) {
     p.path = 1;
+    // Workgroups per CU to aim for, and k groups per split to keep.
+#ifndef MG_PREFILL_WG_PER_CU
+#define MG_PREFILL_WG_PER_CU 1
+#endif
+#ifndef MG_PREFILL_MIN_KG
+#define MG_PREFILL_MIN_KG 2
+#endif
+    const int64_t target = MG_PREFILL_WG_PER_CU * (int64_t)std::max(ctx->num_cus, 1);
     const int64_t rows = 128;  // workgroup tile rows
     p.mpad = (M + rows - 1) / rows * rows;
-    // Split K until the grid covers the chip (~2 workgroups per CU), keeping
-    // at least 2 k groups per split.
-    const int64_t tiles = (p.mpad / rows) * (d.ng / 2);
+    const int64_t mt = p.mpad / rows;
+    // 128-column tiles when they alone cover the chip, else 64-column tiles;
+    // then split K until the grid covers it.
+    p.nt = mt * (ng_total / 2) >= target ? 4 : 2;
+    const int64_t tiles = mt * (p.nt == 4 ? ng_total / 2 : ng_total);
     int64_t ks = 1;
-    while (tiles * ks * 2 <= 512 && d.c4 / (ks * 2) >= 2) ks *= 2;
+    while (tiles * ks * 2 <= target && d.c4 / (ks * 2) >= MG_PREFILL_MIN_KG) ks *= 2;
     p.kps = (int)((d.c4 + ks - 1) / ks);
     p.ksplit = (int)((d.c4 + p.kps - 1) / p.kps);
     p.off_a = 0;  // ahl: mpad * kpad * 2 fp16
     p.off_b = mg_align(p.off_a + (size_t)p.mpad * d.kpad * 4);  // texp [row]
     p.off_c = mg_align(p.off_b + (size_t)p.mpad * 4);           // split-K partials
-    p.total = mg_align(p.off_c + (p.ksplit > 1 ? (size_t)p.ksplit * M * w->N * 4 : 0));
+    p.total = mg_align(p.off_c + (p.ksplit > 1 ? (size_t)p.ksplit * M * n_total * 4 : 0));
   } else {
     p.path = 2;
     p.total = 0;
@@ -1195,21 +1262,32 @@ void mg_nbits_free(mg_weight *w) {
 }
 
 size_t mg_nbits_ws_bytes(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
-  return plan_nbits(ctx, w, M, w->nbits.ng).total;
-}
-
-size_t mg_nbits_group_ws_bytes(const mg_ctx *ctx, int n, const mg_weight *const *w,
-                               int64_t M) {
-  int64_t ng = 0;
-  size_t most = 0;
-  for (int i = 0; i < n; i++) ng += w[i]->nbits.ng;
-  for (int i = 0; i < n; i++) most = std::max(most, plan_nbits(ctx, w[i], M, ng).total);
-  return most;
+  return plan_nbits(ctx, w, M, w->nbits.ng, w->N).total;
 }
 
 namespace {
-mg_status nbits_run_one(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
-                        float *y_dev, void *ws, const NbitsPlan &p);
+// The plan of a group of weights launched together: member 0's kind of path,
+// sized for all members.
+NbitsPlan plan_group(const mg_ctx *ctx, int n, const mg_weight *const *w, int64_t M) {
+  int64_t ng = 0, nn = 0;
+  for (int i = 0; i < n; i++) {
+    ng += w[i]->nbits.ng;
+    nn += w[i]->N;
+  }
+  return plan_nbits(ctx, w[0], M, ng, nn);
+}
+}  // namespace
+
+size_t mg_nbits_group_ws_bytes(const mg_ctx *ctx, int n, const mg_weight *const *w,
+                               int64_t M) {
+  return plan_group(ctx, n, w, M).total;
+}
+
+namespace {
+mg_status nbits_run_generic(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
+                            float *y_dev);
+mg_status prefill_run(mg_ctx *ctx, int n, const mg_weight *const *w, const float *a_dev,
+                      int64_t M, float *const *y_dev, void *ws, const NbitsPlan &p);
 }  // namespace
 
 mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
@@ -1219,7 +1297,7 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
   for (int i = 0; i < n; i++) ng += w[i]->nbits.ng;
   const mg_weight *w0 = w[0];
   const mg_nbits_dev &d = w0->nbits;
-  const NbitsPlan p = plan_nbits(ctx, w0, M, ng);
+  const NbitsPlan p = plan_group(ctx, n, w, M);
   hipStream_t st = ctx->stream;
   char *base = static_cast<char *>(ws);
   if (p.path == 0) {
@@ -1253,10 +1331,9 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
 #undef MG_DEC_LAUNCH
     return mg_launch_check("k_gemv_mfma");
   }
-  // Prefill and generic forms: one call per weight on the same stream (they
-  // reuse the workspace in stream order).
-  for (int i = 0; i < n; i++)
-    MG_TRY(nbits_run_one(ctx, w[i], a_dev, M, y_dev[i], ws, plan_nbits(ctx, w[i], M, ng)));
+  if (p.path == 1) return prefill_run(ctx, n, w, a_dev, M, y_dev, ws, p);
+  // Generic form: one launch per weight.
+  for (int i = 0; i < n; i++) MG_TRY(nbits_run_generic(ctx, w[i], a_dev, M, y_dev[i]));
   return MG_OK;
 }
 
@@ -1266,54 +1343,79 @@ mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
 }
 
 namespace {
-mg_status nbits_run_one(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
-                        float *y_dev, void *ws, const NbitsPlan &p) {
-  const mg_nbits_dev &d = w->nbits;
+// Prefill: one activation prepass shared by the n weights, one GEMM launch
+// over their concatenated column tiles, and (split K) one reduction launch.
+mg_status prefill_run(mg_ctx *ctx, int n, const mg_weight *const *w, const float *a_dev,
+                      int64_t M, float *const *y_dev, void *ws, const NbitsPlan &p) {
+  const mg_weight *w0 = w[0];
+  const mg_nbits_dev &d = w0->nbits;
   hipStream_t st = ctx->stream;
   char *base = static_cast<char *>(ws);
-  const int zpk = d.zp_kind;
-  if (p.path == 1) {
-    uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
-    int *texp = reinterpret_cast<int *>(base + p.off_b);
-    float *part = p.ksplit > 1 ? reinterpret_cast<float *>(base + p.off_c) : nullptr;
-    const int vec = (w->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
-    hipLaunchKernelGGL(k_af16split, dim3((unsigned)(p.mpad / 4)), dim3(256), 0,
-                       st, a_dev, M, w->K, (int)d.c4, vec, ahl, texp);
-    MG_TRY(mg_launch_check("k_af16split"));
-    const int rows = 128;
-    const int mtiles = (int)(p.mpad / rows), ntiles = (int)(d.ng / 2);
-    const dim3 grid((unsigned)(8 * mtiles * ((ntiles + 7) / 8)), (unsigned)p.ksplit);
-    const int has_zp = zpk == MG_ZP_UINT4;
+  uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
+  int *texp = reinterpret_cast<int *>(base + p.off_b);
+  float *part = p.ksplit > 1 ? reinterpret_cast<float *>(base + p.off_c) : nullptr;
+  const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
+  hipLaunchKernelGGL(k_af16split, dim3((unsigned)(p.mpad / 4)), dim3(256), 0, st, a_dev, M,
+                     w0->K, (int)d.c4, vec, ahl, texp);
+  MG_TRY(mg_launch_check("k_af16split"));
+  const int has_zp = d.zp_kind == MG_ZP_UINT4;
+  PrefillSet ps{};
+  ReduceSet rs{};
+  ps.n = rs.n = n;
+  int ct = 0;
+  int64_t poff = 0, eend = 0;
+  for (int i = 0; i < n; i++) {
+    const mg_nbits_dev &di = w[i]->nbits;
+    ps.wq[i] = reinterpret_cast<const uint4 *>(di.wq);
+    ps.scales[i] = di.scales;
     // The kernel reads zero-point bytes unconditionally (branch-free); without
     // zero points it is pointed at the scales, which are at least as large.
-    const uint8_t *zp_arg = has_zp ? d.zp4 : reinterpret_cast<const uint8_t *>(d.scales);
-    const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
-    const int y_vec = (reinterpret_cast<uintptr_t>(y_dev) % 16) == 0;
-#define MG_GEMM_ARGS                                                                   \
-  ahl, texp, reinterpret_cast<const uint4 *>(d.wq), d.scales, zp_arg, d.bias, y_dev, part,   \
-      (int)M, (int)w->N, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), has_zp,     \
-      mtiles, ntiles, \
-      p.kps, y_vec
-#define MG_GEMM_LAUNCH(SJ_) \
-  hipLaunchKernelGGL((k_gemm_f16split<SJ_>), grid, dim3(256), 0, st, MG_GEMM_ARGS)
-    if (segj == 1) MG_GEMM_LAUNCH(1);
-    else if (segj == 2) MG_GEMM_LAUNCH(2);
-    else MG_GEMM_LAUNCH(4);
-#undef MG_GEMM_LAUNCH
-#undef MG_GEMM_ARGS
-    MG_TRY(mg_launch_check("k_gemm_f16split"));
-    if (p.ksplit > 1) {
-      const int64_t mn = M * w->N;
-      hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st,
-                         part, d.bias, y_dev, mn, (int)w->N, p.ksplit);
-      MG_TRY(mg_launch_check("k_gemm_reduce"));
-    }
-    return MG_OK;
+    ps.zp4[i] = has_zp ? di.zp4 : reinterpret_cast<const uint8_t *>(di.scales);
+    ps.bias[i] = rs.bias[i] = di.bias;
+    ps.y[i] = rs.y[i] = y_dev[i];
+    ps.N[i] = rs.N[i] = (int)w[i]->N;
+    ps.y_vec[i] = (reinterpret_cast<uintptr_t>(y_dev[i]) % 16) == 0;
+    ps.part_off[i] = rs.part_off[i] = poff;
+    poff += (int64_t)p.ksplit * M * w[i]->N;
+    eend += M * w[i]->N;
+    rs.e_end[i] = eend;
+    ct += (int)(p.nt == 4 ? di.ng / 2 : di.ng);
+    ps.ct_end[i] = ct;
   }
+  const int mtiles = (int)(p.mpad / 128);
+  const dim3 grid((unsigned)(8 * mtiles * ((ct + 7) / 8)), (unsigned)p.ksplit);
+  const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
+#define MG_GEMM_LAUNCH(SJ_, NT_)                                                           \
+  hipLaunchKernelGGL((k_gemm_f16split<SJ_, NT_>), grid, dim3(256), 0, st, ahl, texp, ps, part, \
+                     (int)M, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), has_zp, \
+                     mtiles, ct, p.kps)
+  if (p.nt == 4) {
+    if (segj == 1) MG_GEMM_LAUNCH(1, 4);
+    else if (segj == 2) MG_GEMM_LAUNCH(2, 4);
+    else MG_GEMM_LAUNCH(4, 4);
+  } else {
+    if (segj == 1) MG_GEMM_LAUNCH(1, 2);
+    else if (segj == 2) MG_GEMM_LAUNCH(2, 2);
+    else MG_GEMM_LAUNCH(4, 2);
+  }
+#undef MG_GEMM_LAUNCH
+  MG_TRY(mg_launch_check("k_gemm_f16split"));
+  if (p.ksplit > 1) {
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((eend + 255) / 256)), dim3(256), 0, st,
+                       part, rs, p.ksplit);
+    MG_TRY(mg_launch_check("k_gemm_reduce"));
+  }
+  return MG_OK;
+}
+
+mg_status nbits_run_generic(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
+                            float *y_dev) {
+  const mg_nbits_dev &d = w->nbits;
   const int64_t tot = M * w->N;
-  hipLaunchKernelGGL(k_nbits_generic, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
-                     a_dev, d.wq, d.scales, d.zp4, d.zpf, zpk, d.bias, y_dev, (int)M,
-                     (int)w->N, (int)w->K, (int)d.c4, (int)d.nb, (int)d.nbh, (int)d.bs);
+  hipLaunchKernelGGL(k_nbits_generic, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
+                     ctx->stream, a_dev, d.wq, d.scales, d.zp4, d.zpf, (int)d.zp_kind, d.bias,
+                     y_dev, (int)M, (int)w->N, (int)w->K, (int)d.c4, (int)d.nb, (int)d.nbh,
+                     (int)d.bs);
   return mg_launch_check("k_nbits_generic");
 }
 }  // namespace

@@ -302,3 +302,80 @@ def test_group_validation(ops):
         ops.matmul_nbits_group_dev([w1] * 5, 0, 1, [0] * 5)
     w1.release()
     w2.release()
+
+
+# Prefill at large N (the 128-column tiles alone cover the chip, no K split):
+# k padding past the last block, zero-scale blocks (all-zero, leading and
+# trailing), negative, widely spread and non-finite scales; checked on column
+# subsets.
+WIDE = [
+    # (M, K, N, bs, zp_mode, special)
+    (256, 256, 33000, 128, "packed", None),
+    (512, 320, 32832, 64, "packed", None),        # k padding past the last block
+    (512, 640, 32768, 64, "none", "zero_blocks"),
+    (256, 384, 33024, 256, "packed", "neg_scales"),
+    (256, 256, 33000, 128, "packed", "huge_ratio"),  # scales 1e-30 .. 2e-2 in one column
+    (256, 256, 33000, 128, "packed", "nonfinite"),   # inf / nan scales
+]
+
+
+@pytest.mark.parametrize("m,k,n,bs,zp_mode,special", WIDE)
+def test_wide_prefill_column_subset(ops, m, k, n, bs, zp_mode, special):
+    rng = np.random.default_rng(0x5EED0006 + m + k + n + bs)
+    b, s, zp = make_nbits(rng, n, k, bs, zp_mode, 0.002, 0.02)
+    nb = s.shape[1]
+    if special == "zero_blocks":
+        s[rng.integers(0, n, 400), rng.integers(0, nb, 400)] = 0.0
+        s[7, :] = 0.0           # all-zero column
+        s[9, : nb - 1] = 0.0    # leading zero blocks
+        s[11, 1:] = 0.0         # trailing zero blocks
+    elif special == "neg_scales":
+        s *= rng.choice([-1.0, 1.0], s.shape).astype(np.float32)
+    elif special == "huge_ratio":
+        s[5, 0] = 1e-30
+    elif special == "nonfinite":
+        s[5, 0] = np.inf
+        s[6, nb - 1] = np.nan
+    bias = rng.standard_normal(n).astype(np.float32)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    y = w(a)
+    np.testing.assert_array_equal(w(a), y)  # deterministic
+    w.release()
+    cols = np.unique(np.concatenate([np.arange(16), np.arange(n - 48, n),
+                                     rng.integers(0, n, 160)]))
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(m - 8, m), rng.integers(0, m, 48)]))
+    bb, ss, zz, bi = slice_cols(b, s, zp, bias, cols)
+    ref = oracle.matmul_nbits(a[rows], bb, ss, zz, k=k, n=len(cols), block_size=bs, bias=bi)
+    got = y[np.ix_(rows, cols)]
+    np.testing.assert_array_equal(np.isfinite(got), np.isfinite(ref))
+    fin = np.isfinite(ref).all(axis=0)
+    assert G.rms_error(got[:, fin], ref[:, fin]) <= TOL, G.rms_error(got[:, fin], ref[:, fin])
+
+
+def test_wide_prefill_group_matches_single_calls(ops):
+    # Three sibling weights launched as one prefill GEMM: together their
+    # column tiles take 128-column tiles without a K split; alone each takes
+    # 64-column tiles.
+    rng = np.random.default_rng(0x5EED0007)
+    m, k, bs = 256, 256, 128
+    ns = [12000, 11000, 10050]
+    hw = [make_nbits(rng, n, k, bs, "packed", 0.002, 0.02) for n in ns]
+    ws = [ops.NBitsWeight(bq, s, z, k=k, n=n, block_size=bs) for (bq, s, z), n in zip(hw, ns)]
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    ad = ops.DeviceBuffer.from_array(a)
+    ys = [ops.DeviceBuffer(m * n * 4) for n in ns]
+    ops.matmul_nbits_group_dev(ws, ad.ptr, m, [y.ptr for y in ys])
+    for (bq, s, z), n, w, y in zip(hw, ns, ws, ys):
+        got = y.to_array((m, n), np.float32)
+        single = w(a)
+        assert np.abs(got - single).max() <= 1e-5 * max(1.0, float(np.abs(single).max()))
+        cols = np.unique(np.concatenate([np.arange(8), np.arange(n - 8, n),
+                                         rng.integers(0, n, 64)]))
+        bb, ss, zz, _ = slice_cols(bq, s, z, None, cols)
+        ref = oracle.matmul_nbits(a, bb, ss, zz, k=k, n=len(cols), block_size=bs)
+        assert G.rms_error(got[:, cols], ref) <= TOL
+        y.free()
+    ad.free()
+    for w in ws:
+        w.release()
