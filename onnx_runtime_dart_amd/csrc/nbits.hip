@@ -168,8 +168,9 @@ __device__ inline int gemv_member(const GemvSet &gs, int x, int *cg) {
 // wave keeps in flight (4 with 4 waves per workgroup, 2 with up to 16).  One
 // workgroup per column group (64 columns, one per lane); its NW = blockDim /
 // 64 waves split K, wave w taking k groups w, w + NW, ...  Packed codes are
-// read once, with non-temporal loads (they stream past the caches).  The activations are handled in chunks of kc
-// k groups (one chunk unless M * K is large):
+// read once, with non-temporal loads (they stream past the caches).  The
+// activations are handled in chunks of kc k groups (one chunk unless M * K is
+// large):
 //
 // Phase 0: each wave issues the loads of its first PF k groups of packed
 // codes, scales and zero points, so HBM is busy while phase 1 runs.
@@ -187,6 +188,168 @@ __device__ inline int gemv_member(const GemvSet &gs, int x, int *cg) {
 // keeping PF k groups of loads in flight ahead of the arithmetic.
 // Phase 3: the NW per-wave sums are added in wave order through LDS
 // (deterministic), plus the bias, and written to y.
+
+// Packed codes, scales and zero points of one k group of one column group.
+template <int QPG, int ZPK>
+struct GemvSlot {
+  uint4 w[4];
+  float s[QPG];
+  uint32_t z[(QPG + 1) / 2];
+  float zf[QPG];
+};
+
+// Loads of k group kg of the column group whose packed codes start at wp and
+// whose scale / zero-point columns start at sp / zq / zfp (lane's column).
+template <int QPG, int ZPK>
+__device__ inline void gemv_issue(GemvSlot<QPG, ZPK> &sl, const uint4 *wp, const float *sp,
+                                  const uint8_t *zq, const float *zfp, int kg, int nb,
+                                  int lbs) {
+#pragma unroll
+  for (int g = 0; g < 4; g++)
+    sl.w[g] = __builtin_bit_cast(
+        uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wp + kg * 256 + g * 64)));
+#pragma unroll
+  for (int s = 0; s < QPG; s++) {
+    const int b = min((kg * KGRP + s * (KGRP / QPG)) >> lbs, nb - 1);
+    sl.s[s] = sp[(int64_t)b * 64];
+    if (ZPK == 2) sl.zf[s] = zfp[(int64_t)b * 64];
+  }
+  if (ZPK == 1) {
+#pragma unroll
+    for (int h = 0; h < (QPG + 1) / 2; h++) {
+      const int b = min((kg * KGRP + 2 * h * (KGRP / QPG)) >> lbs, nb - 1);
+      sl.z[h] = zq[(int64_t)(b >> 1) * 64];
+    }
+  }
+}
+
+// Phase 1 for k groups [c0, c0 + nk) into LDS slots l = 0 .. nk - 1 (kc slots
+// per row), by nthr threads.
+template <int MR, int QPG>
+__device__ inline void gemv_digits(const float *__restrict__ a, int64_t K, int vec, int c0,
+                                   int nk, int kc, uint32_t *sdig, float *salpha, int *srsum,
+                                   int t, int nthr) {
+  constexpr int G = 16 / QPG;  // octets per qblock
+  const int ntask = MR * nk * 16;
+  for (int task = t; task < ntask; task += nthr) {
+    const int o = task & 15, rl = task >> 4;
+    const int l = rl % nk, r = rl / nk;
+    const int64_t k0 = (int64_t)(c0 + l) * KGRP + 8 * o;
+    const float *ar = a + (int64_t)r * K;
+    float v[8];
+    if (vec && k0 + 8 <= K) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(ar + k0);
+      const float4 x1 = *reinterpret_cast<const float4 *>(ar + k0 + 4);
+      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+      v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = (k0 + i < K) ? ar[k0 + i] : 0.f;
+    }
+    float mx = 0.f;
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      if (!isfinite(v[i])) bad = 1;
+      mx = fmaxf(mx, fabsf(v[i]));
+    }
+#pragma unroll
+    for (int off = 1; off < G; off <<= 1) {
+      mx = fmaxf(mx, __shfl_xor(mx, off));
+      bad |= __shfl_xor(bad, off);
+    }
+    const float inv = (mx > 0.f && !bad) ? (float)FIX_MAX / mx : 0.f;
+    int rs = 0;
+    uint32_t dg[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      int fix = (int)rintf(v[i] * inv);
+      fix = min(max(fix, -FIX_MAX), FIX_MAX);
+      rs += fix;
+      const int pos = nib_pos(i);
+      int x = fix;
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        const int di = ((x + 8) & 15) - 8;
+        x = (x - di) >> 4;
+        dg[d] |= (uint32_t)(di & 15) << (4 * pos);
+      }
+    }
+#pragma unroll
+    for (int off = 1; off < G; off <<= 1) rs += __shfl_xor(rs, off);
+    const int j = o >> 2, g = o & 3;
+    *reinterpret_cast<uint4 *>(&sdig[((r * kc + l) * 4 + g) * 16 + j * 4]) =
+        make_uint4(dg[0], dg[1], dg[2], dg[3]);
+    if (o % G == 0) {
+      const int q = (r * kc + l) * QPG + o / G;
+      salpha[q] = bad ? __builtin_nanf("") : (mx > 0.f ? mx / (float)FIX_MAX : 0.f);
+      srsum[q] = rs;
+    }
+  }
+}
+
+// Phase 2 for one k group kg (LDS slot l) held in sl: yacc[r] += its share.
+template <int MR, int QPG, int ZPK>
+__device__ inline void gemv_kgroup(const GemvSlot<QPG, ZPK> &sl, int kg, int l, int kc, int nb,
+                                   int lbs, const uint32_t *sdig, const float *salpha,
+                                   const int *srsum, float (&yacc)[MR]) {
+  uint32_t wv[4][4];
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    wv[g][0] = sl.w[g].x ^ 0x88888888u; wv[g][1] = sl.w[g].y ^ 0x88888888u;
+    wv[g][2] = sl.w[g].z ^ 0x88888888u; wv[g][3] = sl.w[g].w ^ 0x88888888u;
+  }
+  // One quantisation block at a time: dword (g, j) holds k = 32j + 8g + t,
+  // so block s covers j in [4s/QPG, 4(s+1)/QPG) for QPG <= 4 and, for
+  // QPG = 8, j = s/2 with g in {2(s%2), 2(s%2) + 1}.
+#pragma unroll
+  for (int s = 0; s < QPG; s++) {
+    int acc[MR][4];
+#pragma unroll
+    for (int r = 0; r < MR; r++)
+#pragma unroll
+      for (int d = 0; d < 4; d++) acc[r][d] = 0;
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const bool mine = QPG == 8 ? (j == s / 2 && g / 2 == s % 2) : (j * QPG / 4 == s);
+        if (!mine) continue;
+        const int x = (int)wv[g][j];
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+          const uint4 dd =
+              *reinterpret_cast<const uint4 *>(&sdig[((r * kc + l) * 4 + g) * 16 + j * 4]);
+          acc[r][0] = __builtin_amdgcn_sdot8((int)dd.x, x, acc[r][0], false);
+          acc[r][1] = __builtin_amdgcn_sdot8((int)dd.y, x, acc[r][1], false);
+          acc[r][2] = __builtin_amdgcn_sdot8((int)dd.z, x, acc[r][2], false);
+          acc[r][3] = __builtin_amdgcn_sdot8((int)dd.w, x, acc[r][3], false);
+        }
+      }
+    const int b = (kg * KGRP + s * (KGRP / QPG)) >> lbs;
+    if (b >= nb) continue;  // k padding beyond the last block
+    int zc = 0;
+    if (ZPK == 1) {
+      // Zero-point byte h of this k group holds blocks 2h (low) and 2h+1.
+      const uint32_t zb = sl.z[QPG == 1 ? 0 : s / 2];
+      zc = 8 - (int)((b & 1) ? (zb >> 4) : (zb & 15));
+    }
+#pragma unroll
+    for (int r = 0; r < MR; r++) {
+      const int comb = ((acc[r][3] * 16 + acc[r][2]) * 16 + acc[r][1]) * 16 + acc[r][0];
+      const int q = (r * kc + l) * QPG + s;
+      const float al = salpha[q];
+      const int R = srsum[q];
+      float v;
+      if (ZPK == 2)
+        v = (float)comb + (8.f - sl.zf[s]) * (float)R;
+      else
+        v = (float)(comb + zc * R);
+      yacc[r] += (al * sl.s[s]) * v;
+    }
+  }
+}
+
 template <int MR, int QPG, int ZPK, int PF>
 __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
     const float *__restrict__ a, int64_t K, int vec, const GemvSet gs, int c4, int nb,
@@ -202,51 +365,22 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
   const int nthr = blockDim.x;
   int cg;
   const int gm = gemv_member(gs, blockIdx.x, &cg);
-  const uint4 *__restrict__ wq = gs.wq[gm];
-  const float *__restrict__ scales = gs.scales[gm];
-  const uint8_t *__restrict__ zp4 = gs.zp4[gm];
-  const float *__restrict__ zpf = gs.zpf[gm];
-  const float *__restrict__ bias = gs.bias[gm];
   float *__restrict__ y = gs.y[gm];
+  const float *__restrict__ bias = gs.bias[gm];
   const int N = gs.N[gm];
-  constexpr int G = 16 / QPG;        // octets per qblock
-  constexpr int ZB = (QPG + 1) / 2;  // zero-point bytes per k group
 
-  const uint4 *wp = wq + (int64_t)cg * c4 * 256 + lane;
-  const float *sp = scales + (int64_t)cg * nb * 64 + sz_pos(lane);
-  const uint8_t *zq = zp4 + (int64_t)cg * nbh * 64 + sz_pos(lane);
-  const float *zfp = zpf + (int64_t)cg * nb * 64 + sz_pos(lane);
-  uint4 wr[PF][4];
-  float sr[PF][QPG];
-  uint32_t zr[PF][ZB];
-  float zfr[PF][QPG];
-  // Loads of k group kg into ring slot i.
-  auto issue = [&](int i, int kg) {
-#pragma unroll
-    for (int g = 0; g < 4; g++)
-      wr[i][g] = __builtin_bit_cast(
-          uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wp + kg * 256 + g * 64)));
-#pragma unroll
-    for (int s = 0; s < QPG; s++) {
-      const int b = min((kg * KGRP + s * (KGRP / QPG)) >> lbs, nb - 1);
-      sr[i][s] = sp[(int64_t)b * 64];
-      if (ZPK == 2) zfr[i][s] = zfp[(int64_t)b * 64];
-    }
-    if (ZPK == 1) {
-#pragma unroll
-      for (int h = 0; h < ZB; h++) {
-        const int b = min((kg * KGRP + 2 * h * (KGRP / QPG)) >> lbs, nb - 1);
-        zr[i][h] = zq[(int64_t)(b >> 1) * 64];
-      }
-    }
-  };
+  const uint4 *wp = gs.wq[gm] + (int64_t)cg * c4 * 256 + lane;
+  const float *sp = gs.scales[gm] + (int64_t)cg * nb * 64 + sz_pos(lane);
+  const uint8_t *zq = gs.zp4[gm] + (int64_t)cg * nbh * 64 + sz_pos(lane);
+  const float *zfp = gs.zpf[gm] + (int64_t)cg * nb * 64 + sz_pos(lane);
+  GemvSlot<QPG, ZPK> ring[PF];
   // This wave's k groups: wave, wave + NW, ...; the n-th is wave + n * NW.
   const int nmine = wave < c4 ? (c4 - wave + NW - 1) / NW : 0;
 
   // Phase 0.
 #pragma unroll
   for (int i = 0; i < PF; i++)
-    if (i < nmine) issue(i, wave + i * NW);
+    if (i < nmine) gemv_issue(ring[i], wp, sp, zq, zfp, wave + i * NW, nb, lbs);
 
   float yacc[MR];
 #pragma unroll
@@ -257,62 +391,7 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
     const int nk = min(c4, c0 + kc) - c0;
     if (c0 > 0) __syncthreads();  // previous chunk's digits fully consumed
     // Phase 1.
-    const int ntask = MR * nk * 16;
-    for (int task = t; task < ntask; task += nthr) {
-      const int o = task & 15, rl = task >> 4;
-      const int l = rl % nk, r = rl / nk;
-      const int64_t k0 = (int64_t)(c0 + l) * KGRP + 8 * o;
-      const float *ar = a + (int64_t)r * K;
-      float v[8];
-      if (vec && k0 + 8 <= K) {
-        const float4 x0 = *reinterpret_cast<const float4 *>(ar + k0);
-        const float4 x1 = *reinterpret_cast<const float4 *>(ar + k0 + 4);
-        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = (k0 + i < K) ? ar[k0 + i] : 0.f;
-      }
-      float mx = 0.f;
-      int bad = 0;
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        if (!isfinite(v[i])) bad = 1;
-        mx = fmaxf(mx, fabsf(v[i]));
-      }
-#pragma unroll
-      for (int off = 1; off < G; off <<= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, off));
-        bad |= __shfl_xor(bad, off);
-      }
-      const float inv = (mx > 0.f && !bad) ? (float)FIX_MAX / mx : 0.f;
-      int rs = 0;
-      uint32_t dg[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        int fix = (int)rintf(v[i] * inv);
-        fix = min(max(fix, -FIX_MAX), FIX_MAX);
-        rs += fix;
-        const int pos = nib_pos(i);
-        int x = fix;
-#pragma unroll
-        for (int d = 0; d < 4; d++) {
-          const int di = ((x + 8) & 15) - 8;
-          x = (x - di) >> 4;
-          dg[d] |= (uint32_t)(di & 15) << (4 * pos);
-        }
-      }
-#pragma unroll
-      for (int off = 1; off < G; off <<= 1) rs += __shfl_xor(rs, off);
-      const int j = o >> 2, g = o & 3;
-      *reinterpret_cast<uint4 *>(&sdig[((r * kc + l) * 4 + g) * 16 + j * 4]) =
-          make_uint4(dg[0], dg[1], dg[2], dg[3]);
-      if (o % G == 0) {
-        const int q = (r * kc + l) * QPG + o / G;
-        salpha[q] = bad ? __builtin_nanf("") : (mx > 0.f ? mx / (float)FIX_MAX : 0.f);
-        srsum[q] = rs;
-      }
-    }
+    gemv_digits<MR, QPG>(a, K, vec, c0, nk, kc, sdig, salpha, srsum, t, nthr);
     __syncthreads();
 
     // Phase 2: this wave's k groups inside the chunk.  The ring slot of the
@@ -324,74 +403,9 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
         const int nn = n + i;
         if (nn >= nend) break;
         const int kg = wave + nn * NW;
-        const int l = kg - c0;
-        uint32_t wv[4][4];
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-          wv[g][0] = wr[i][g].x ^ 0x88888888u; wv[g][1] = wr[i][g].y ^ 0x88888888u;
-          wv[g][2] = wr[i][g].z ^ 0x88888888u; wv[g][3] = wr[i][g].w ^ 0x88888888u;
-        }
-        float scv[QPG], zfv[QPG];
-        uint32_t zbv[ZB];
-#pragma unroll
-        for (int s = 0; s < QPG; s++) {
-          scv[s] = sr[i][s];
-          if (ZPK == 2) zfv[s] = zfr[i][s];
-        }
-        if (ZPK == 1) {
-#pragma unroll
-          for (int h = 0; h < ZB; h++) zbv[h] = zr[i][h];
-        }
-        if (nn + PF < nmine) issue(i, wave + (nn + PF) * NW);
-        // One quantisation block at a time: dword (g, j) holds k = 32j + 8g + t,
-        // so block s covers j in [4s/QPG, 4(s+1)/QPG) for QPG <= 4 and, for
-        // QPG = 8, j = s/2 with g in {2(s%2), 2(s%2) + 1}.
-#pragma unroll
-        for (int s = 0; s < QPG; s++) {
-          int acc[MR][4];
-#pragma unroll
-          for (int r = 0; r < MR; r++)
-#pragma unroll
-            for (int d = 0; d < 4; d++) acc[r][d] = 0;
-#pragma unroll
-          for (int g = 0; g < 4; g++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-              const bool mine = QPG == 8 ? (j == s / 2 && g / 2 == s % 2) : (j * QPG / 4 == s);
-              if (!mine) continue;
-              const int x = (int)wv[g][j];
-#pragma unroll
-              for (int r = 0; r < MR; r++) {
-                const uint4 dd = *reinterpret_cast<const uint4 *>(
-                    &sdig[((r * kc + l) * 4 + g) * 16 + j * 4]);
-                acc[r][0] = __builtin_amdgcn_sdot8((int)dd.x, x, acc[r][0], false);
-                acc[r][1] = __builtin_amdgcn_sdot8((int)dd.y, x, acc[r][1], false);
-                acc[r][2] = __builtin_amdgcn_sdot8((int)dd.z, x, acc[r][2], false);
-                acc[r][3] = __builtin_amdgcn_sdot8((int)dd.w, x, acc[r][3], false);
-              }
-            }
-          const int b = (kg * KGRP + s * (KGRP / QPG)) >> lbs;
-          if (b >= nb) continue;  // k padding beyond the last block
-          int zc = 0;
-          if (ZPK == 1) {
-            // Zero-point byte h of this k group holds blocks 2h (low) and 2h+1.
-            const uint32_t zb = zbv[QPG == 1 ? 0 : s / 2];
-            zc = 8 - (int)((b & 1) ? (zb >> 4) : (zb & 15));
-          }
-#pragma unroll
-          for (int r = 0; r < MR; r++) {
-            const int comb = ((acc[r][3] * 16 + acc[r][2]) * 16 + acc[r][1]) * 16 + acc[r][0];
-            const int q = (r * kc + l) * QPG + s;
-            const float al = salpha[q];
-            const int R = srsum[q];
-            float v;
-            if (ZPK == 2)
-              v = (float)comb + (8.f - zfv[s]) * (float)R;
-            else
-              v = (float)(comb + zc * R);
-            yacc[r] += (al * scv[s]) * v;
-          }
-        }
+        const GemvSlot<QPG, ZPK> cur = ring[i];
+        if (nn + PF < nmine) gemv_issue(ring[i], wp, sp, zq, zfp, wave + (nn + PF) * NW, nb, lbs);
+        gemv_kgroup<MR, QPG, ZPK>(cur, kg, kg - c0, kc, nb, lbs, sdig, salpha, srsum, yacc);
       }
     }
   }
@@ -409,6 +423,76 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
       float s = red[r * 64 + lane];
       for (int w = 1; w < NW; w++) s += red[(w * MR + r) * 64 + lane];
       if (col < N) y[(int64_t)r * N + col] = s + (bias ? bias[col] : 0.f);
+    }
+  }
+}
+
+// Persistent form for wide weights whose k groups split evenly over 4 waves
+// (c4 = 4 * PF, PF = 1 or 2): the activation digits of all k groups are made once per
+// workgroup, which then takes column groups blockIdx.x, + gridDim.x, ...;
+// wave w owns k groups w + 4i, i < PF, of each, and refills ring slot i with
+// the next column group's k group as soon as it has copied the current one,
+// so the stream of packed codes continues across column groups.  Per column
+// group the four wave sums meet in LDS (double-buffered, one barrier) and
+// wave 0 adds them in wave order and stores: results are bitwise those of
+// k_gemv_dot8.
+template <int MR, int QPG, int ZPK, int PF>
+__global__ __launch_bounds__(256) void k_gemv_dot8p(
+    const float *__restrict__ a, int64_t K, int vec, const GemvSet gs, int c4, int nb,
+    int nbh, int lbs) {
+  extern __shared__ uint32_t smem[];
+  uint32_t *sdig = smem;                                            // [MR][c4][64]
+  float *salpha = reinterpret_cast<float *>(smem + MR * c4 * 64);   // [MR][c4][QPG]
+  int *srsum = reinterpret_cast<int *>(salpha + MR * c4 * QPG);     // [MR][c4][QPG]
+  float *red = reinterpret_cast<float *>(srsum + MR * c4 * QPG);    // [2][4][MR][64]
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int ncg = gs.cg_end[gs.n - 1];
+  GemvSlot<QPG, ZPK> ring[PF];
+  auto issue_cg = [&](int x) {
+    int cg;
+    const int gm = gemv_member(gs, x, &cg);
+    const uint4 *wp = gs.wq[gm] + (int64_t)cg * c4 * 256 + lane;
+    const float *sp = gs.scales[gm] + (int64_t)cg * nb * 64 + sz_pos(lane);
+    const uint8_t *zq = gs.zp4[gm] + (int64_t)cg * nbh * 64 + sz_pos(lane);
+    const float *zfp = gs.zpf[gm] + (int64_t)cg * nb * 64 + sz_pos(lane);
+#pragma unroll
+    for (int i = 0; i < PF; i++) gemv_issue(ring[i], wp, sp, zq, zfp, wave + 4 * i, nb, lbs);
+  };
+  if ((int)blockIdx.x < ncg) issue_cg(blockIdx.x);
+  gemv_digits<MR, QPG>(a, K, vec, 0, c4, c4, sdig, salpha, srsum, t, 256);
+  __syncthreads();
+  int it = 0;
+  for (int x = blockIdx.x; x < ncg; x += gridDim.x, it++) {
+    float yacc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; r++) yacc[r] = 0.f;
+    const int nx = x + gridDim.x;
+    GemvSlot<QPG, ZPK> cur[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) cur[i] = ring[i];
+    if (nx < ncg) issue_cg(nx);
+#pragma unroll
+    for (int i = 0; i < PF; i++) {
+      const int kg = wave + 4 * i;
+      gemv_kgroup<MR, QPG, ZPK>(cur[i], kg, kg, c4, nb, lbs, sdig, salpha, srsum, yacc);
+    }
+    float *rb = red + (it & 1) * (4 * MR * 64);
+#pragma unroll
+    for (int r = 0; r < MR; r++) rb[(wave * MR + r) * 64 + lane] = yacc[r];
+    __syncthreads();
+    if (wave == 0) {
+      int cg;
+      const int gm = gemv_member(gs, x, &cg);
+      const int col = cg * 64 + lane;
+      const float *bias = gs.bias[gm];
+#pragma unroll
+      for (int r = 0; r < MR; r++) {
+        float s = rb[r * 64 + lane];
+        for (int w = 1; w < 4; w++) s += rb[(w * MR + r) * 64 + lane];
+        if (col < gs.N[gm]) gs.y[gm][(int64_t)r * gs.N[gm] + col] = s + (bias ? bias[col] : 0.f);
+      }
     }
   }
 }
@@ -1031,6 +1115,8 @@ struct NbitsPlan {
   // mfma
   int64_t mpad = 0;
   int nt = 4;  // prefill tile width in 32-column MFMA tiles (4 or 2)
+  int pers = 0;       // GEMV on the persistent kernel (k_gemv_dot8p)
+  int pers_grid = 0;  // its workgroups
   size_t off_a = 0, off_b = 0, off_c = 0, off_d = 0, total = 0;
 };
 
@@ -1071,6 +1157,25 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
     p.kc = (int)kc;
     p.lds = (size_t)std::max<int64_t>(kc * per_kg, nw * M * 64 * 4);
     p.total = 0;
+    // One row, k groups that split evenly over 4 waves (1 or 2 each) and
+    // enough column groups for several per workgroup: the persistent kernel,
+    // with the column groups dealt evenly over about MG_GEMV_WG_PER_CU
+    // workgroups per CU.  (With 4 k groups per wave its per-column-group work
+    // is long enough that the one-workgroup-per-column-group form, with more
+    // waves resident per SIMD, streams as fast.)
+#ifndef MG_GEMV_WG_PER_CU
+#define MG_GEMV_WG_PER_CU 2
+#endif
+    const int64_t slots = MG_GEMV_WG_PER_CU * (int64_t)std::max(ctx->num_cus, 1);
+    const int64_t per_wave = d.c4 / 4;
+    if (M == 1 && nw == 4 && kc == d.c4 && d.c4 % 4 == 0 &&
+        (per_wave == 1 || per_wave == 2) &&
+        ng_total >= 2 * slots) {
+      const int64_t per = (ng_total + slots - 1) / slots;
+      p.pers = 1;
+      p.pers_grid = (int)((ng_total + per - 1) / per);
+      p.lds = (size_t)(d.c4 * per_kg + 2 * 4 * M * 64 * 4);
+    }
   } else if (d.bs >= 32 && int_zp) {
     p.path = 1;
     // Workgroups per CU to aim for, and k groups per split to keep.
@@ -1130,12 +1235,17 @@ void launch_gemv_zp(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p,
   const dim3 grid((unsigned)gs.cg_end[gs.n - 1]), block((unsigned)(64 * p.nw));
 #define MG_GEMV_ARGS \
   a, w->K, vec, gs, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), p.kc
+  // The 8/16-wave form (PF 2) is planned only for one row and QPG >= 2.
 #define MG_GEMV_LAUNCH(Z_)                                                                   \
   do {                                                                                       \
-    if (p.nw == 4)                                                                           \
-      hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, Z_, 4>), grid, block, p.lds, st, MG_GEMV_ARGS); \
-    else                                                                                     \
-      hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, Z_, 2>), grid, block, p.lds, st, MG_GEMV_ARGS); \
+    if constexpr (MR == 1 && QPG >= 2) {                                                     \
+      if (p.nw != 4) {                                                                       \
+        hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, Z_, 2>), grid, block, p.lds, st,            \
+                           MG_GEMV_ARGS);                                                    \
+        break;                                                                               \
+      }                                                                                      \
+    }                                                                                        \
+    hipLaunchKernelGGL((k_gemv_dot8<MR, QPG, Z_, 4>), grid, block, p.lds, st, MG_GEMV_ARGS); \
   } while (0)
   if (d.zp_kind == 0) MG_GEMV_LAUNCH(0);
   else if (d.zp_kind == 1) MG_GEMV_LAUNCH(1);
@@ -1144,9 +1254,39 @@ void launch_gemv_zp(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p,
 #undef MG_GEMV_ARGS
 }
 
+template <int QPG, int ZPK>
+void launch_gemv_pers_pf(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p,
+                         hipStream_t st, const float *a, int vec) {
+  const mg_nbits_dev &d = w->nbits;
+  const dim3 grid((unsigned)p.pers_grid), block(256);
+#define MG_PERS_LAUNCH(PF_)                                                                  \
+  hipLaunchKernelGGL((k_gemv_dot8p<1, QPG, ZPK, PF_>), grid, block, p.lds, st, a, w->K, vec, gs, \
+                     (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs))
+  if (d.c4 == 4) MG_PERS_LAUNCH(1);
+  else MG_PERS_LAUNCH(2);
+#undef MG_PERS_LAUNCH
+}
+
+template <int QPG>
+void launch_gemv_pers(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, hipStream_t st,
+                      const float *a, int vec) {
+  if (w->nbits.zp_kind == 0) launch_gemv_pers_pf<QPG, 0>(w, gs, p, st, a, vec);
+  else if (w->nbits.zp_kind == 1) launch_gemv_pers_pf<QPG, 1>(w, gs, p, st, a, vec);
+  else launch_gemv_pers_pf<QPG, 2>(w, gs, p, st, a, vec);
+}
+
 template <int MR>
 void launch_gemv_q(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, hipStream_t st,
                    const float *a, int vec) {
+  if (MR == 1 && p.pers) {
+    switch (p.qpg) {
+      case 1: launch_gemv_pers<1>(w, gs, p, st, a, vec); break;
+      case 2: launch_gemv_pers<2>(w, gs, p, st, a, vec); break;
+      case 4: launch_gemv_pers<4>(w, gs, p, st, a, vec); break;
+      default: launch_gemv_pers<8>(w, gs, p, st, a, vec); break;
+    }
+    return;
+  }
   switch (p.qpg) {
     case 1: launch_gemv_zp<MR, 1>(w, gs, p, st, a, vec); break;
     case 2: launch_gemv_zp<MR, 2>(w, gs, p, st, a, vec); break;

@@ -379,3 +379,60 @@ def test_wide_prefill_group_matches_single_calls(ops):
     ad.free()
     for w in ws:
         w.release()
+
+
+# Persistent GEMV (one row, 4 or 8 k groups, >= 1024 column groups): each
+# workgroup streams many column groups; checked on column subsets, with a
+# ragged last column group and every zero-point kind (16 k groups take the
+# one-workgroup-per-column-group form).
+PERSISTENT = [
+    # (K, N, bs, zp_mode)
+    (512, 70001, 128, "none"),
+    (1024, 66000, 64, "float"),
+    (2048, 65600, 32, "packed"),
+    (1000, 66500, 16, "packed"),   # K % 128 != 0: padded last k group
+]
+
+
+@pytest.mark.parametrize("k,n,bs,zp_mode", PERSISTENT)
+def test_persistent_gemv_column_subset(ops, k, n, bs, zp_mode):
+    rng = np.random.default_rng(0x5EED0008 + k + n + bs)
+    b, s, zp = make_nbits(rng, n, k, bs, zp_mode, 0.002, 0.02)
+    bias = rng.standard_normal(n).astype(np.float32)
+    a = rng.standard_normal((1, k)).astype(np.float32)
+    a[0, 3] = 40.0  # an outlier in one quantisation block
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    y = w(a)
+    np.testing.assert_array_equal(w(a), y)
+    w.release()
+    cols = np.unique(np.concatenate([np.arange(70), np.arange(n - 70, n),
+                                     rng.integers(0, n, 300)]))
+    bb, ss, zz, bi = slice_cols(b, s, zp, bias, cols)
+    ref = oracle.matmul_nbits(a, bb, ss, zz, k=k, n=len(cols), block_size=bs, bias=bi)
+    assert G.rms_error(y[:, cols], ref) <= TOL, G.rms_error(y[:, cols], ref)
+
+
+def test_persistent_gemv_group(ops):
+    # Siblings whose column groups together take the persistent kernel.
+    rng = np.random.default_rng(0x5EED0009)
+    k, bs = 1024, 128
+    ns = [40000, 30001, 2000]
+    hw = [make_nbits(rng, n, k, bs, "packed", 0.002, 0.02) for n in ns]
+    ws = [ops.NBitsWeight(bq, s, z, k=k, n=n, block_size=bs) for (bq, s, z), n in zip(hw, ns)]
+    a = rng.standard_normal((1, k)).astype(np.float32)
+    ad = ops.DeviceBuffer.from_array(a)
+    ys = [ops.DeviceBuffer(n * 4) for n in ns]
+    ops.matmul_nbits_group_dev(ws, ad.ptr, 1, [y.ptr for y in ys])
+    for (bq, s, z), n, w, y in zip(hw, ns, ws, ys):
+        got = y.to_array((1, n), np.float32)
+        cols = np.unique(np.concatenate([np.arange(64), np.arange(n - 64, n),
+                                         rng.integers(0, n, 200)]))
+        bb, ss, zz, _ = slice_cols(bq, s, z, None, cols)
+        ref = oracle.matmul_nbits(a, bb, ss, zz, k=k, n=len(cols), block_size=bs)
+        assert G.rms_error(got[:, cols], ref) <= TOL
+        single = w(a)
+        assert np.abs(got - single).max() <= 1e-5 * max(1.0, float(np.abs(single).max()))
+        y.free()
+    ad.free()
+    for w in ws:
+        w.release()
