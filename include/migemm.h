@@ -263,6 +263,51 @@ mg_status mg_gemm_f32_w_dev(mg_ctx *ctx, const float *a_dev, int64_t rows,
                             const int64_t *c_shape, int32_t c_rank,
                             float *y_dev);
 
+/* --------------------------------------------------------------- attention */
+
+/* _FusedSDPA (lib/src/onnx_ops.dart:2100-2149, the graph fusion of
+ * MatMul(Softmax(MatMul(A, B) * scale + mask), V) at
+ * lib/src/onnx_graph.dart:560-620, dispatched at :1812-1821):
+ * y = MatMul(softmax_row(MatMul(a, b) * scale + mask), v) in fp32.  a is
+ * [..., S, D], b [..., D, T] (K^T), v [..., T, DV]; batch dims broadcast as
+ * in MatMul (a with b, then the scores with v); the mask (any rank up to the
+ * score rank) broadcasts right-aligned into the scores [..., S, T].  y is the
+ * broadcast [..., S, DV].  A row whose scores are all -inf is NaN, as in the
+ * reference.  D and DV <= 128; at most 4 batch dims (else MG_UNSUPPORTED). */
+mg_status mg_fused_sdpa(mg_ctx *ctx, const float *a, const int64_t *a_shape,
+                        int32_t a_rank, const float *b, const int64_t *b_shape,
+                        int32_t b_rank, const float *v, const int64_t *v_shape,
+                        int32_t v_rank, const float *mask,
+                        const int64_t *mask_shape, int32_t mask_rank,
+                        float scale, float *y);
+mg_status mg_fused_sdpa_dev(mg_ctx *ctx, const float *a_dev,
+                            const int64_t *a_shape, int32_t a_rank,
+                            const float *b_dev, const int64_t *b_shape,
+                            int32_t b_rank, const float *v_dev,
+                            const int64_t *v_shape, int32_t v_rank,
+                            const float *mask_dev, const int64_t *mask_shape,
+                            int32_t mask_rank, float scale, float *y_dev);
+
+/* MultiHeadAttention (com.microsoft; lib/src/onnx_ops.dart:2014-2098,
+ * dispatched at lib/src/onnx_graph.dart:1670-1680): q [batch, seq, hidden],
+ * k and v [batch, kv_seq, hidden], num_heads heads of hidden / num_heads;
+ * bias (optional) [batch, bias_heads, seq, kv_seq] with bias_heads 1 or
+ * num_heads, added to the scaled scores; scale = 1 / sqrt(head size) unless
+ * has_scale.  y [batch, seq, hidden]. */
+mg_status mg_multi_head_attention(mg_ctx *ctx, const float *q, const float *k,
+                                  const float *v, int64_t batch, int64_t seq,
+                                  int64_t kv_seq, int64_t hidden,
+                                  int32_t num_heads, const float *bias,
+                                  int32_t bias_heads, int32_t has_scale,
+                                  float scale, float *y);
+mg_status mg_multi_head_attention_dev(mg_ctx *ctx, const float *q_dev,
+                                      const float *k_dev, const float *v_dev,
+                                      int64_t batch, int64_t seq,
+                                      int64_t kv_seq, int64_t hidden,
+                                      int32_t num_heads, const float *bias_dev,
+                                      int32_t bias_heads, int32_t has_scale,
+                                      float scale, float *y_dev);
+
 /* ----------------------------------------------------------------- weights */
 
 mg_status mg_weight_release(mg_weight *w);

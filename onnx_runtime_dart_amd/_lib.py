@@ -54,6 +54,12 @@ SIGNATURES = {
     "mg_dynamic_quantize_linear_dev": [_P, _P, _I64, _P, _P],
     "mg_matmul_integer_w_dq_dev": [_P, _P, _I64, _I64, _P, _P, _P],
     "mg_qlinear_matmul_w_dq_dev": [_P, _P, _I64, _I64, _P, _P, _F, _F, _I32, _I32, _I32, _P],
+    "mg_fused_sdpa": [_P, _P, _P, _I32, _P, _P, _I32, _P, _P, _I32, _P, _P, _I32, _F, _P],
+    "mg_fused_sdpa_dev": [_P, _P, _P, _I32, _P, _P, _I32, _P, _P, _I32, _P, _P, _I32, _F, _P],
+    "mg_multi_head_attention": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P, _I32, _I32,
+                                _F, _P],
+    "mg_multi_head_attention_dev": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P, _I32,
+                                    _I32, _F, _P],
     "mg_matmul_f32": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_matmul_f32_dev": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_gemm_f32": [_P, _P, _P, _P, _P, _I32, _I32, _F, _F, _P, _P, _I32, _P],

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstring>
 #include <string>
@@ -946,3 +947,260 @@ mg_status mg_gemm_f32_w_dev(mg_ctx *ctx, const float *a_dev, int64_t rows, int64
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------ attention
+
+namespace {
+
+// Right-aligned broadcast of two shapes; false if they do not broadcast.
+bool bcast(const std::vector<int64_t> &x, const std::vector<int64_t> &y,
+           std::vector<int64_t> *out) {
+  const size_t r = std::max(x.size(), y.size());
+  out->assign(r, 1);
+  for (size_t d = 0; d < r; d++) {
+    const int64_t xd = d < r - x.size() ? 1 : x[d - (r - x.size())];
+    const int64_t yd = d < r - y.size() ? 1 : y[d - (r - y.size())];
+    if (xd != yd && xd != 1 && yd != 1) return false;
+    (*out)[d] = xd == 1 ? yd : xd;
+  }
+  return true;
+}
+
+// Element strides, over the output batch dims `ob`, of an operand whose
+// leading dims `xb` (right-aligned to `ab`, itself right-aligned to `ob`)
+// are laid out contiguously with `inner` elements per batch entry: 0 where
+// either shape has size 1 or the dim is absent.
+void batch_strides(const std::vector<int64_t> &ob, const std::vector<int64_t> &ab,
+                   const std::vector<int64_t> &xb, int64_t inner, int64_t *out) {
+  std::vector<int64_t> xs(xb.size());
+  int64_t s = inner;
+  for (size_t d = xb.size(); d-- > 0;) {
+    xs[d] = xb[d] == 1 ? 0 : s;
+    s *= xb[d];
+  }
+  for (size_t d = 0; d < ob.size(); d++) {
+    out[d] = 0;
+    const int64_t da = (int64_t)d - (int64_t)(ob.size() - ab.size());
+    if (da < 0 || ab[(size_t)da] == 1) continue;
+    const int64_t dx = da - (int64_t)(ab.size() - xb.size());
+    if (dx >= 0) out[d] = xs[(size_t)dx];
+  }
+}
+
+bool fits_lane_offsets(const mg_attn_problem &p) {
+  // Lane parts of the kernel's offsets: 32 rows/keys and 128 dims per stride.
+  const int64_t lim = (int64_t)1 << 30;
+  for (int64_t s : {p.k_ts, p.k_ds, p.v_ts, p.v_ds, p.m_ts, p.q_cs})
+    if (s < 0 || s * 160 >= lim) return false;
+  return true;
+}
+
+// _FusedSDPA shapes -> kernel problem (y contiguous [out batch..., S, DV]).
+mg_status plan_sdpa(const int64_t *as, int32_t ar, const int64_t *bs, int32_t br,
+                    const int64_t *vs, int32_t vr, const int64_t *ms, int32_t mr, float scale,
+                    mg_attn_problem *p, int64_t *ny) {
+  if (!shape_ok(as, ar) || !shape_ok(bs, br) || !shape_ok(vs, vr) || !shape_ok(ms, mr) ||
+      ar < 2 || br < 2 || vr < 2)
+    return mg_fail(MG_INVALID_ARGUMENT, "_FusedSDPA: operands need rank >= 2");
+  const int64_t S = as[ar - 2], D = as[ar - 1], D2 = bs[br - 2], T = bs[br - 1];
+  const int64_t T2 = vs[vr - 2], DV = vs[vr - 1];
+  if (D != D2)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMul inner dims mismatch: " + std::to_string(D) +
+                                            " vs " + std::to_string(D2));
+  if (T != T2)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMul inner dims mismatch: " + std::to_string(T) +
+                                            " vs " + std::to_string(T2));
+  std::vector<int64_t> ab(as, as + ar - 2), bb(bs, bs + br - 2), vb(vs, vs + vr - 2), sb, ob;
+  if (!bcast(ab, bb, &sb) || !bcast(sb, vb, &ob))
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMul: batch dims do not broadcast");
+  // The mask broadcasts (right-aligned) into the score shape [sb..., S, T].
+  std::vector<int64_t> sc(sb);
+  sc.push_back(S);
+  sc.push_back(T);
+  if ((size_t)mr > sc.size())
+    return mg_fail(MG_INVALID_ARGUMENT, "_FusedSDPA: mask rank exceeds the score rank");
+  for (int32_t d = 0; d < mr; d++) {
+    const int64_t md = ms[d], sd = sc[sc.size() - mr + d];
+    if (md != 1 && md != sd)
+      return mg_fail(MG_INVALID_ARGUMENT, "_FusedSDPA: mask does not broadcast to the scores");
+  }
+  if (ob.size() > (size_t)MG_ATTN_MAX_BATCH_DIMS)
+    return mg_fail(MG_UNSUPPORTED, "_FusedSDPA: more than 4 batch dimensions");
+  *p = mg_attn_problem{};
+  p->nbd = (int)ob.size();
+  for (size_t d = 0; d < ob.size(); d++) p->bdim[d] = ob[d];
+  batch_strides(ob, sb, ab, S * D, p->q_bs);
+  batch_strides(ob, sb, bb, D * T, p->k_bs);
+  batch_strides(ob, ob, vb, T * DV, p->v_bs);
+  std::vector<int64_t> mb(ms, ms + std::max<int32_t>(mr - 2, 0));
+  const int64_t m_last = mr >= 1 ? ms[mr - 1] : 1, m_row = mr >= 2 ? ms[mr - 2] : 1;
+  batch_strides(ob, sb, mb, m_last * m_row, p->m_bs);
+  {
+    int64_t s = S * DV;
+    for (size_t d = ob.size(); d-- > 0;) {
+      p->y_bs[d] = s;
+      s *= ob[d];
+    }
+    *ny = s;
+  }
+  p->q_rs = D;
+  p->q_cs = 1;
+  p->k_ts = 1;  // b holds K^T: element (t, d) at d * T + t
+  p->k_ds = T;
+  p->v_ts = DV;
+  p->v_ds = 1;
+  p->m_qs = m_row == 1 ? 0 : m_last;
+  p->m_ts = m_last == 1 ? 0 : 1;
+  p->y_rs = DV;
+  p->S = (int)S;
+  p->T = (int)T;
+  p->D = (int)D;
+  p->DV = (int)DV;
+  p->scale = scale;
+  if (S > 0x7fffffff || T > 0x7fffffff || !fits_lane_offsets(*p))
+    return mg_fail(MG_UNSUPPORTED, "_FusedSDPA: dimensions too large");
+  return MG_OK;
+}
+
+// MultiHeadAttention [batch, seq, hidden] views -> kernel problem.
+mg_status plan_mha(int64_t batch, int64_t seq, int64_t kv_seq, int64_t hidden, int32_t heads,
+                   int32_t bias_heads, int32_t has_bias, int32_t has_scale, float scale,
+                   mg_attn_problem *p) {
+  if (batch < 0 || seq < 0 || kv_seq < 0 || hidden < 0 || heads <= 0 || hidden % heads != 0)
+    return mg_fail(MG_INVALID_ARGUMENT,
+                   "MultiHeadAttention: hidden must be a multiple of num_heads");
+  if (has_bias && bias_heads != 1 && bias_heads != heads)
+    return mg_fail(MG_UNSUPPORTED, "MultiHeadAttention: bias heads must be 1 or num_heads");
+  const int64_t hs = hidden / heads;
+  *p = mg_attn_problem{};
+  p->nbd = 2;
+  p->bdim[0] = batch;
+  p->bdim[1] = heads;
+  p->q_bs[0] = seq * hidden;
+  p->q_bs[1] = hs;
+  p->k_bs[0] = p->v_bs[0] = kv_seq * hidden;
+  p->k_bs[1] = p->v_bs[1] = hs;
+  p->y_bs[0] = seq * hidden;
+  p->y_bs[1] = hs;
+  if (has_bias) {
+    p->m_bs[0] = (int64_t)bias_heads * seq * kv_seq;
+    p->m_bs[1] = bias_heads == 1 ? 0 : seq * kv_seq;
+    p->m_qs = kv_seq;
+    p->m_ts = 1;
+  }
+  p->q_rs = p->k_ts = p->v_ts = p->y_rs = hidden;
+  p->q_cs = p->k_ds = p->v_ds = 1;
+  p->S = (int)seq;
+  p->T = (int)kv_seq;
+  p->D = p->DV = (int)hs;
+  // lib/src/onnx_ops.dart:2030: scale ?? 1 / sqrt(headSize).
+  p->scale = has_scale ? scale : (float)(1.0 / std::sqrt((double)hs));
+  if (seq > 0x7fffffff || kv_seq > 0x7fffffff || !fits_lane_offsets(*p))
+    return mg_fail(MG_UNSUPPORTED, "MultiHeadAttention: dimensions too large");
+  return MG_OK;
+}
+
+mg_status run_attn_host(mg_ctx *ctx, mg_attn_problem p, const float *q, int64_t nq,
+                        const float *k, int64_t nk, const float *v, int64_t nv,
+                        const float *mask, int64_t nm, float *y, int64_t ny) {
+  if (ny == 0) return MG_OK;
+  if ((!q && nq) || (!k && nk) || (!v && nv) || !y)
+    return mg_fail(MG_INVALID_ARGUMENT, "attention: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t oq = s.take((size_t)nq * 4), ok = s.take((size_t)nk * 4),
+               ov = s.take((size_t)nv * 4), om = s.take((size_t)nm * 4),
+               oy = s.take((size_t)ny * 4);
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  hipStream_t st = ctx->stream;
+  if (nq) MG_HIP(hipMemcpyAsync(base + oq, q, (size_t)nq * 4, hipMemcpyHostToDevice, st));
+  if (nk) MG_HIP(hipMemcpyAsync(base + ok, k, (size_t)nk * 4, hipMemcpyHostToDevice, st));
+  if (nv) MG_HIP(hipMemcpyAsync(base + ov, v, (size_t)nv * 4, hipMemcpyHostToDevice, st));
+  if (mask && nm) MG_HIP(hipMemcpyAsync(base + om, mask, (size_t)nm * 4, hipMemcpyHostToDevice, st));
+  p.q = reinterpret_cast<float *>(base + oq);
+  p.k = reinterpret_cast<float *>(base + ok);
+  p.v = reinterpret_cast<float *>(base + ov);
+  p.mask = mask ? reinterpret_cast<float *>(base + om) : nullptr;
+  p.y = reinterpret_cast<float *>(base + oy);
+  MG_TRY(mg_attn_run(ctx, p));
+  MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)ny * 4, hipMemcpyDeviceToHost, st));
+  MG_HIP(hipStreamSynchronize(st));
+  return MG_OK;
+}
+
+}  // namespace
+
+mg_status mg_fused_sdpa(mg_ctx *ctx, const float *a, const int64_t *a_shape, int32_t a_rank,
+                        const float *b, const int64_t *b_shape, int32_t b_rank, const float *v,
+                        const int64_t *v_shape, int32_t v_rank, const float *mask,
+                        const int64_t *mask_shape, int32_t mask_rank, float scale, float *y) {
+  g_last_error.clear();
+  if (!ctx || !mask) return mg_fail(MG_INVALID_ARGUMENT, "mg_fused_sdpa: null context or mask");
+  mg_attn_problem p;
+  int64_t ny = 0;
+  MG_TRY(plan_sdpa(a_shape, a_rank, b_shape, b_rank, v_shape, v_rank, mask_shape, mask_rank,
+                   scale, &p, &ny));
+  return run_attn_host(ctx, p, a, prod(a_shape, 0, a_rank), b, prod(b_shape, 0, b_rank), v,
+                       prod(v_shape, 0, v_rank), mask, prod(mask_shape, 0, mask_rank), y, ny);
+}
+
+mg_status mg_fused_sdpa_dev(mg_ctx *ctx, const float *a_dev, const int64_t *a_shape,
+                            int32_t a_rank, const float *b_dev, const int64_t *b_shape,
+                            int32_t b_rank, const float *v_dev, const int64_t *v_shape,
+                            int32_t v_rank, const float *mask_dev, const int64_t *mask_shape,
+                            int32_t mask_rank, float scale, float *y_dev) {
+  g_last_error.clear();
+  if (!ctx || !mask_dev)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_fused_sdpa_dev: null context or mask");
+  mg_attn_problem p;
+  int64_t ny = 0;
+  MG_TRY(plan_sdpa(a_shape, a_rank, b_shape, b_rank, v_shape, v_rank, mask_shape, mask_rank,
+                   scale, &p, &ny));
+  if (ny == 0) return MG_OK;
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, 0));
+  p.q = a_dev;
+  p.k = b_dev;
+  p.v = v_dev;
+  p.mask = mask_dev;
+  p.y = y_dev;
+  return mg_attn_run(ctx, p);
+}
+
+mg_status mg_multi_head_attention(mg_ctx *ctx, const float *q, const float *k, const float *v,
+                                  int64_t batch, int64_t seq, int64_t kv_seq, int64_t hidden,
+                                  int32_t num_heads, const float *bias, int32_t bias_heads,
+                                  int32_t has_scale, float scale, float *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_multi_head_attention: null context");
+  mg_attn_problem p;
+  MG_TRY(plan_mha(batch, seq, kv_seq, hidden, num_heads, bias_heads, bias != nullptr, has_scale,
+                  scale, &p));
+  return run_attn_host(ctx, p, q, batch * seq * hidden, k, batch * kv_seq * hidden, v,
+                       batch * kv_seq * hidden, bias,
+                       bias ? batch * (int64_t)bias_heads * seq * kv_seq : 0, y,
+                       batch * seq * hidden);
+}
+
+mg_status mg_multi_head_attention_dev(mg_ctx *ctx, const float *q_dev, const float *k_dev,
+                                      const float *v_dev, int64_t batch, int64_t seq,
+                                      int64_t kv_seq, int64_t hidden, int32_t num_heads,
+                                      const float *bias_dev, int32_t bias_heads,
+                                      int32_t has_scale, float scale, float *y_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_multi_head_attention_dev: null context");
+  mg_attn_problem p;
+  MG_TRY(plan_mha(batch, seq, kv_seq, hidden, num_heads, bias_heads, bias_dev != nullptr,
+                  has_scale, scale, &p));
+  if (batch * seq * hidden == 0) return MG_OK;
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, 0));
+  p.q = q_dev;
+  p.k = k_dev;
+  p.v = v_dev;
+  p.mask = bias_dev;
+  p.y = y_dev;
+  return mg_attn_run(ctx, p);
+}

@@ -173,6 +173,29 @@ struct mg_f32_problem {
 mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
                      const float *b_dev, float *y_dev);
 
+// ---------------------------------------------------------- attention entry
+
+// y[b][q][:DV] = softmax_t(scale * sum_d Q[b][q][d] K[b][t][d] + mask[b][q][t])
+//                . V[b][t][:DV] over strided views; b runs over up to
+// MG_ATTN_MAX_BATCH_DIMS batch dims bdim with per-operand element strides
+// (0 = broadcast).  Element (q, d) of Q is at q_rs * q + q_cs * d past the
+// batch offset, and likewise (t, d) of K, (t, dv) of V and (q, t) of the
+// mask; output rows are contiguous (row stride y_rs).  mask may be null.
+constexpr int MG_ATTN_MAX_BATCH_DIMS = 4;
+struct mg_attn_problem {
+  const float *q, *k, *v, *mask;
+  float *y;
+  int nbd;
+  int64_t bdim[MG_ATTN_MAX_BATCH_DIMS];
+  int64_t q_bs[MG_ATTN_MAX_BATCH_DIMS], k_bs[MG_ATTN_MAX_BATCH_DIMS],
+      v_bs[MG_ATTN_MAX_BATCH_DIMS], m_bs[MG_ATTN_MAX_BATCH_DIMS],
+      y_bs[MG_ATTN_MAX_BATCH_DIMS];
+  int64_t q_rs, q_cs, k_ts, k_ds, v_ts, v_ds, m_qs, m_ts, y_rs;
+  int S, T, D, DV;
+  float scale;
+};
+mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p);
+
 // --------------------------------------------------------------- DQL entry
 
 mg_status mg_dql_run(mg_ctx *ctx, const float *x_dev, int64_t n,

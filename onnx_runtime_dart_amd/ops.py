@@ -9,6 +9,8 @@ defaults and error classes as the reference:
     op_dynamic_quantize_linear <- opDynamicQuantizeLinear lib/src/onnx_ops.dart:3556
     op_matmul              <- opMatMul        lib/src/onnx_ops.dart:1710
     op_gemm                <- opGemm          lib/src/onnx_ops.dart:2152
+    op_fused_sdpa          <- opFusedSDPA     lib/src/onnx_ops.dart:2106
+    op_multi_head_attention <- opMultiHeadAttention lib/src/onnx_ops.dart:2019
 
 Tensors are numpy arrays on the host; every op runs on the GPU through the
 C ABI (there is no CPU path).  Weight handles (NBitsWeight, Int8Weight,
@@ -469,6 +471,82 @@ def op_gemm(a, b, c=None, *, alpha=1.0, beta=1.0, trans_a=False, trans_b=False,
                           _ptr(_shape_arr(c)) if c is not None else None,
                           c.ndim if c is not None else 0, _ptr(y)))
     return y
+
+
+def op_fused_sdpa(a, b, v, mask, scale: float, ctx: Context | None = None) -> np.ndarray:
+    """opFusedSDPA (lib/src/onnx_ops.dart:2106-2149):
+    MatMul(Softmax(MatMul(a, b) * scale + mask), v); b is K^T [..., D, T]."""
+    a, b, v, mask = (np.ascontiguousarray(x, dtype=np.float32) for x in (a, b, v, mask))
+    if a.ndim < 2 or b.ndim < 2 or v.ndim < 2:
+        raise ArgumentError("_FusedSDPA: operands need rank >= 2")
+    try:
+        sb = np.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+        ob = np.broadcast_shapes(sb, v.shape[:-2])
+    except ValueError:
+        raise ArgumentError("MatMul: batch dims do not broadcast") from None
+    y = np.empty(tuple(ob) + (a.shape[-2], v.shape[-1]), dtype=np.float32)
+    ctx = ctx or default_context()
+    check(lib.mg_fused_sdpa(ctx.handle, _ptr(a), _ptr(_shape_arr(a)), a.ndim, _ptr(b),
+                            _ptr(_shape_arr(b)), b.ndim, _ptr(v), _ptr(_shape_arr(v)), v.ndim,
+                            _ptr(mask), _ptr(_shape_arr(mask)), mask.ndim, float(scale),
+                            _ptr(y)))
+    return y
+
+
+def op_multi_head_attention(q, k, v, attention_bias=None, *, num_heads: int,
+                            scale: float | None = None,
+                            ctx: Context | None = None) -> np.ndarray:
+    """opMultiHeadAttention (lib/src/onnx_ops.dart:2019-2098): q [batch, seq,
+    hidden], k / v [batch, kv_seq, hidden], attention_bias [batch, bias_heads,
+    seq, kv_seq] or None; scale defaults to 1 / sqrt(hidden / num_heads)."""
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape or \
+            k.shape[0] != q.shape[0] or k.shape[2] != q.shape[2]:
+        raise ArgumentError("MultiHeadAttention: q, k, v must be [batch, seq, hidden]")
+    batch, seq, hidden = q.shape
+    kv_seq = k.shape[1]
+    bias_heads = 0
+    if attention_bias is not None:
+        attention_bias = np.ascontiguousarray(attention_bias, dtype=np.float32)
+        if attention_bias.ndim != 4 or attention_bias.shape[0] != batch or \
+                attention_bias.shape[2:] != (seq, kv_seq):
+            raise ArgumentError("MultiHeadAttention: bias must be [batch, heads, seq, kv_seq]")
+        bias_heads = attention_bias.shape[1]
+    y = np.empty_like(q)
+    ctx = ctx or default_context()
+    check(lib.mg_multi_head_attention(ctx.handle, _ptr(q), _ptr(k), _ptr(v), batch, seq, kv_seq,
+                                      hidden, int(num_heads), _ptr(attention_bias), bias_heads,
+                                      int(scale is not None),
+                                      float(scale if scale is not None else 0.0), _ptr(y)))
+    return y
+
+
+def fused_sdpa_dev(a_ptr: int, a_shape, b_ptr: int, b_shape, v_ptr: int, v_shape,
+                   mask_ptr: int, mask_shape, scale: float, y_ptr: int,
+                   ctx: Context | None = None):
+    """op_fused_sdpa on device buffers (asynchronous on the context's stream)."""
+    ctx = ctx or default_context()
+    sh = [np.ascontiguousarray(np.array(x, np.int64)) for x in (a_shape, b_shape, v_shape,
+                                                                 mask_shape)]
+    check(lib.mg_fused_sdpa_dev(ctx.handle, C.c_void_p(a_ptr), _ptr(sh[0]), sh[0].size,
+                                C.c_void_p(b_ptr), _ptr(sh[1]), sh[1].size, C.c_void_p(v_ptr),
+                                _ptr(sh[2]), sh[2].size, C.c_void_p(mask_ptr), _ptr(sh[3]),
+                                sh[3].size, float(scale), C.c_void_p(y_ptr)))
+
+
+def multi_head_attention_dev(q_ptr: int, k_ptr: int, v_ptr: int, batch: int, seq: int,
+                             kv_seq: int, hidden: int, num_heads: int, y_ptr: int,
+                             bias_ptr: int = 0, bias_heads: int = 0,
+                             scale: float | None = None, ctx: Context | None = None):
+    """op_multi_head_attention on device buffers."""
+    ctx = ctx or default_context()
+    check(lib.mg_multi_head_attention_dev(ctx.handle, C.c_void_p(q_ptr), C.c_void_p(k_ptr),
+                                          C.c_void_p(v_ptr), batch, seq, kv_seq, hidden,
+                                          int(num_heads),
+                                          C.c_void_p(bias_ptr) if bias_ptr else None,
+                                          int(bias_heads), int(scale is not None),
+                                          float(scale if scale is not None else 0.0),
+                                          C.c_void_p(y_ptr)))
 
 
 def library_path() -> str:

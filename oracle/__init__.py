@@ -14,6 +14,8 @@ Thin numpy wrappers over ``oracle/lib/liboracle.so`` (built from oracle.c by
 * ``matmul_f32``           — lib/src/onnx_ops.dart:1710-1766
 * ``gemm_f32``             — lib/src/onnx_ops.dart:2152-2172
 * ``matmul_kernel``        — lib/src/gemm_kernel_simd.dart:32-239
+* ``fused_sdpa``           — lib/src/onnx_ops.dart:2106-2149
+* ``multi_head_attention`` — lib/src/onnx_ops.dart:2019-2098
 """
 from __future__ import annotations
 
@@ -76,6 +78,10 @@ def _declare(L):
                                      _I64, C.c_float, C.c_int32, C.c_int32,
                                      C.c_int32, _P]
     L.orc_dynamic_quantize_linear.argtypes = [_P, _I64, _P, _P, _P]
+    L.orc_fused_sdpa.argtypes = [_P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, C.c_double,
+                                 _P]
+    L.orc_multi_head_attention.argtypes = [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64,
+                                           _I, C.c_double, _P]
     L.orc_round_even.argtypes = [C.c_double, _P]
     L.orc_round_even.restype = _I64
 
@@ -245,3 +251,31 @@ def dynamic_quantize_linear(x):
 
 __all__ = [n for n in dir() if not n.startswith("_")]
 _ = os  # keep import for callers that inspect LIB_PATH via os.path
+
+
+def fused_sdpa(a, b, v, mask, scale: float) -> np.ndarray:
+    a, b, v, mask = (np.ascontiguousarray(x, dtype=np.float32) for x in (a, b, v, mask))
+    sb = _broadcast(a.shape[:-2], b.shape[:-2])
+    ob = _broadcast(sb, v.shape[:-2])
+    y = np.empty(ob + [a.shape[-2], v.shape[-1]], dtype=np.float32)
+    _check(lib().orc_fused_sdpa(_ptr(a), _ptr(_shape(a)), a.ndim, _ptr(b), _ptr(_shape(b)),
+                                b.ndim, _ptr(v), _ptr(_shape(v)), v.ndim, _ptr(mask),
+                                _ptr(_shape(mask)), mask.ndim, float(scale), _ptr(y)),
+           "fused_sdpa")
+    return y
+
+
+def multi_head_attention(q, k, v, bias=None, *, num_heads: int, scale=None) -> np.ndarray:
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
+    batch, seq, hidden = q.shape
+    kv_seq = k.shape[1]
+    bh = 0
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=np.float32)
+        bh = bias.shape[1]
+    out = np.empty_like(q)
+    _check(lib().orc_multi_head_attention(_ptr(q), _ptr(k), _ptr(v), batch, seq, kv_seq, hidden,
+                                          num_heads, _ptr(bias), bh, int(scale is not None),
+                                          float(scale or 0.0), _ptr(out)),
+           "multi_head_attention")
+    return out

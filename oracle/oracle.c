@@ -396,3 +396,125 @@ int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y,
   *zp_out = (int32_t)zp;
   return ORC_OK;
 }
+
+/* ------------------------------------------------------------ attention */
+
+/* Scale, mask and row softmax of one score row in place, as opFusedSDPA
+ * (lib/src/onnx_ops.dart:2123-2141) and opMultiHeadAttention (:2072-2089) do
+ * it: val = s * scale + mask in double, stored rounded to f32, the max over
+ * the unrounded doubles; e = exp(stored - max) in double, stored rounded,
+ * summed in double; then divide by the sum (div = 1) or multiply by its
+ * inverse (div = 0). */
+static void softmax_row(float *row, int64_t t, double scale, const float *mask,
+                        int64_t mask_stride, int div) {
+  double mx = -INFINITY;
+  for (int64_t j = 0; j < t; j++) {
+    const double val = (double)row[j] * scale + (mask ? (double)mask[j * mask_stride] : 0.0);
+    row[j] = (float)val;
+    if (val > mx) mx = val;
+  }
+  double sum = 0;
+  for (int64_t j = 0; j < t; j++) {
+    const double e = exp((double)row[j] - mx);
+    row[j] = (float)e;
+    sum += e;
+  }
+  if (div) {
+    for (int64_t j = 0; j < t; j++) row[j] = (float)((double)row[j] / sum);
+  } else {
+    const double inv = 1.0 / sum;
+    for (int64_t j = 0; j < t; j++) row[j] = (float)((double)row[j] * inv);
+  }
+}
+
+int orc_fused_sdpa(const float *a, const int64_t *a_shape, int a_rank,
+                   const float *b, const int64_t *b_shape, int b_rank,
+                   const float *v, const int64_t *v_shape, int v_rank,
+                   const float *mask, const int64_t *mask_shape, int mask_rank,
+                   double scale, float *y) {
+  if (a_rank < 2 || b_rank < 2 || v_rank < 2 || a_rank > 8 || b_rank > 8 || v_rank > 8 ||
+      mask_rank > 8)
+    return ORC_INVALID_ARGUMENT;
+  /* s = opMatMul(a, b) (:2107). */
+  int64_t sb[8];
+  int sbr = 0;
+  if (broadcast_shape(a_shape, a_rank - 2, b_shape, b_rank - 2, sb, &sbr))
+    return ORC_INVALID_ARGUMENT;
+  const int64_t m = a_shape[a_rank - 2], t = b_shape[b_rank - 1];
+  int64_t srows = m;
+  for (int d = 0; d < sbr; d++) srows *= sb[d];
+  float *s = (float *)malloc((size_t)(srows * t > 0 ? srows * t : 1) * sizeof(float));
+  if (!s) return ORC_INVALID_ARGUMENT;
+  int st = orc_matmul_f32(a, a_shape, a_rank, b, b_shape, b_rank, s);
+  if (st) {
+    free(s);
+    return st;
+  }
+  /* Row loop with the mask broadcast (:2113-2146). */
+  int64_t sshape[8];
+  for (int d = 0; d < sbr; d++) sshape[d] = sb[d];
+  sshape[sbr] = m;
+  sshape[sbr + 1] = t;
+  const int srank = sbr + 2;
+  const int64_t mlast_stride = (mask_rank > 0 && mask_shape[mask_rank - 1] == t) ? 1 : 0;
+  const int mrow_rank = mask_rank > 0 ? mask_rank - 1 : 0;
+  int64_t coords[8] = {0};
+  for (int64_t r = 0; r < srows; r++) {
+    int64_t rem = r;
+    for (int d = srank - 2; d >= 0; d--) {
+      coords[d] = rem % sshape[d];
+      rem /= sshape[d];
+    }
+    const int64_t mbase =
+        mask_rank == 0 ? 0
+                       : flatten_broadcast(coords, srank - 1, mask_shape, mrow_rank) *
+                             mask_shape[mask_rank - 1];
+    softmax_row(s + r * t, t, scale, mask + mbase, mlast_stride, 1);
+  }
+  /* opMatMul(s, v) (:2148). */
+  sshape[sbr] = m;
+  st = orc_matmul_f32(s, sshape, srank, v, v_shape, v_rank, y);
+  free(s);
+  return st;
+}
+
+int orc_multi_head_attention(const float *q, const float *k, const float *v,
+                             int64_t batch, int64_t seq, int64_t kv_seq,
+                             int64_t hidden, int64_t num_heads, const float *bias,
+                             int64_t bias_heads, int has_scale, double scale, float *out) {
+  if (num_heads <= 0 || hidden % num_heads) return ORC_INVALID_ARGUMENT;
+  const int64_t hs = hidden / num_heads;
+  const double s = has_scale ? scale : 1.0 / sqrt((double)hs); /* :2030 */
+  float *qh = (float *)malloc((size_t)(seq * hs + 1) * sizeof(float));
+  float *kt = (float *)malloc((size_t)(hs * kv_seq + 1) * sizeof(float));
+  float *vh = (float *)malloc((size_t)(kv_seq * hs + 1) * sizeof(float));
+  float *sc = (float *)malloc((size_t)(seq * kv_seq + 1) * sizeof(float));
+  float *cx = (float *)malloc((size_t)(seq * hs + 1) * sizeof(float));
+  if (!qh || !kt || !vh || !sc || !cx) {
+    free(qh); free(kt); free(vh); free(sc); free(cx);
+    return ORC_INVALID_ARGUMENT;
+  }
+  for (int64_t b = 0; b < batch; b++) {
+    for (int64_t h = 0; h < num_heads; h++) {
+      /* Gather Q [seq, hs], K^T [hs, kv_seq], V [kv_seq, hs] (:2047-2061). */
+      for (int64_t i = 0; i < seq; i++)
+        for (int64_t d = 0; d < hs; d++)
+          qh[i * hs + d] = q[(b * seq + i) * hidden + h * hs + d];
+      for (int64_t j = 0; j < kv_seq; j++)
+        for (int64_t d = 0; d < hs; d++) {
+          kt[d * kv_seq + j] = k[(b * kv_seq + j) * hidden + h * hs + d];
+          vh[j * hs + d] = v[(b * kv_seq + j) * hidden + h * hs + d];
+        }
+      orc_matmul_kernel(qh, kt, sc, seq, hs, kv_seq); /* :2063-2064 */
+      const int64_t bbase = bias ? (b * bias_heads + (h % bias_heads)) * seq * kv_seq : 0;
+      for (int64_t i = 0; i < seq; i++)
+        softmax_row(sc + i * kv_seq, kv_seq, s, bias ? bias + bbase + i * kv_seq : NULL, 1, 0);
+      orc_matmul_kernel(sc, vh, cx, seq, kv_seq, hs); /* :2090-2091 */
+      for (int64_t i = 0; i < seq; i++)
+        for (int64_t d = 0; d < hs; d++)
+          out[(b * seq + i) * hidden + h * hs + d] = cx[i * hs + d];
+    }
+  }
+  free(qh); free(kt); free(vh); free(sc); free(cx);
+  return ORC_OK;
+}

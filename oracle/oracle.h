@@ -80,6 +80,26 @@ int orc_qlinear_matmul(const void *a, int a_signed, int64_t a_batch,
 int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y,
                                 float *scale, int32_t *zp);
 
+/* opFusedSDPA, lib/src/onnx_ops.dart:2106-2149: s = opMatMul(a, b); per score
+ * row val = s * scale + mask (double, stored as f32; mask broadcast
+ * right-aligned, a last dim != T read with stride 0), e = exp(val - max),
+ * val = e / sum; y = opMatMul(s, v).  y sized by the broadcast output shape. */
+int orc_fused_sdpa(const float *a, const int64_t *a_shape, int a_rank,
+                   const float *b, const int64_t *b_shape, int b_rank,
+                   const float *v, const int64_t *v_shape, int v_rank,
+                   const float *mask, const int64_t *mask_shape, int mask_rank,
+                   double scale, float *y);
+
+/* opMultiHeadAttention, lib/src/onnx_ops.dart:2019-2098: per (batch, head)
+ * the gathered Q.K^T (matmulKernel), scale + bias [batch, bias_heads, seq,
+ * kv_seq] (head h reads bias head h % bias_heads), row softmax multiplied by
+ * the inverse sum, then . V; out [batch, seq, hidden]. */
+int orc_multi_head_attention(const float *q, const float *k, const float *v,
+                             int64_t batch, int64_t seq, int64_t kv_seq,
+                             int64_t hidden, int64_t num_heads, const float *bias,
+                             int64_t bias_heads, int has_scale, double scale,
+                             float *out);
+
 /* _roundEven, lib/src/onnx_qlinear_ops.dart:19-26 / onnx_ops.dart:3480-3487.
  * Returns ORC_UNSUPPORTED through *err for non-finite input (Dart's toInt
  * throws UnsupportedError there). */

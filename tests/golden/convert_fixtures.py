@@ -2,7 +2,7 @@
 
 Provenance: the inputs are `test/fixtures/<name>/{model.onnx,case.json}` of
 PieroSoria/onnx_runtime_dart (MIT; expected outputs were produced there by
-ONNX Runtime, see tool/gen_fixtures.py:891-925, :713-760 and
+ONNX Runtime, see tool/gen_fixtures.py:891-925, :713-760, :789-799 and
 tool/gen_transformer_fixtures.py:55-63).  Each fixture becomes one JSON file
 holding the node's op type, its attributes, every operand in node-input order
 (initializers merged with the case's feeds) and the expected outputs.  The
@@ -43,6 +43,8 @@ HOT_PATH = [
     "matmul_batched",
     "gemm_transB_bias",
     "einsum_matmul",
+    "mha_with_bias",
+    "mha_no_bias",
 ]
 
 # ONNX TensorProto.DataType -> (numpy dtype, json dtype name)

@@ -54,6 +54,10 @@ def _run_fixture(d):
             x[0], x[1], x[2] if len(x) > 2 else None,
             alpha=at.get("alpha", 1.0), beta=at.get("beta", 1.0),
             trans_a=bool(at.get("transA", 0)), trans_b=bool(at.get("transB", 0)))}
+    if op == "MultiHeadAttention":
+        bias = x[5] if len(x) > 5 else None
+        return {d["outputs"][0]: oracle.multi_head_attention(
+            x[0], x[1], x[2], bias, num_heads=at["num_heads"], scale=at.get("scale"))}
     raise AssertionError(op)
 
 
@@ -341,3 +345,72 @@ def test_dql_zero_input_and_nonfinite():
     assert s == 0 and z == 0 and not y.any()
     with pytest.raises(oracle.OracleError):
         oracle.dynamic_quantize_linear(np.array([1.0, np.nan], np.float32))
+
+
+# ------------------------------------------------------------- attention
+
+
+def _sdpa_closed_form(a, b, v, mask, scale):
+    s = np.matmul(a.astype(np.float64), b.astype(np.float64)) * scale + mask
+    mx = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - mx)
+    p = e / e.sum(axis=-1, keepdims=True)
+    return np.matmul(p, v.astype(np.float64))
+
+
+@pytest.mark.parametrize("shapes", [
+    # a, b, v, mask
+    ((2, 3, 5, 8), (2, 3, 8, 7), (2, 3, 7, 4), (2, 1, 1, 7)),   # BERT-style padding mask
+    ((4, 6, 3), (4, 3, 6), (4, 6, 5), (6, 6)),                  # causal-style [S, T] mask
+    ((2, 1, 5, 8), (1, 3, 8, 9), (2, 3, 9, 4), ()),             # broadcast batches, scalar mask
+    ((3, 7, 16), (16, 7), (7, 16), (7,)),                        # shared K / V, per-key mask
+    ((1, 1, 4), (1, 4, 2), (3, 1, 2, 5), (1, 2)),                # v broadcasts the scores
+])
+def test_fused_sdpa_closed_form(shapes):
+    rng = np.random.default_rng(sum(len(x) for x in shapes))
+    a, b, v, m = (rng.standard_normal(sh).astype(np.float32) for sh in shapes)
+    got = oracle.fused_sdpa(a, b, v, m, 0.37)
+    want = _sdpa_closed_form(a, b, v, m, 0.37)
+    assert got.shape == want.shape
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-6)
+
+
+def test_fused_sdpa_masked_rows_and_equivalence_to_mha():
+    rng = np.random.default_rng(3)
+    b_, h, s_, t, d = 2, 4, 5, 6, 8
+    q = rng.standard_normal((b_, s_, h * d)).astype(np.float32)
+    k = rng.standard_normal((b_, t, h * d)).astype(np.float32)
+    v = rng.standard_normal((b_, t, h * d)).astype(np.float32)
+    bias = rng.standard_normal((b_, h, s_, t)).astype(np.float32)
+    mha = oracle.multi_head_attention(q, k, v, bias, num_heads=h, scale=0.25)
+    # The same attention as _FusedSDPA over per-head views.
+    qh = q.reshape(b_, s_, h, d).transpose(0, 2, 1, 3)
+    kt = k.reshape(b_, t, h, d).transpose(0, 2, 3, 1)
+    vh = v.reshape(b_, t, h, d).transpose(0, 2, 1, 3)
+    sd = oracle.fused_sdpa(qh, kt, vh, bias, 0.25).transpose(0, 2, 1, 3).reshape(b_, s_, h * d)
+    np.testing.assert_allclose(mha, sd, rtol=1e-5, atol=1e-6)
+    # A fully masked row is NaN (exp(-inf - -inf)); a partly masked one ignores
+    # the masked keys exactly.
+    m = np.zeros((s_, t), np.float32)
+    m[1, :] = -np.inf
+    m[2, 3:] = -np.inf
+    y = oracle.fused_sdpa(qh, kt, vh, m, 0.25)
+    assert np.isnan(y[:, :, 1]).all() and np.isfinite(np.delete(y, 1, axis=2)).all()
+    y2 = oracle.fused_sdpa(qh[:, :, 2:3], kt[..., :3], vh[:, :, :3], np.zeros((1, 3), np.float32),
+                           0.25)
+    np.testing.assert_allclose(y[:, :, 2:3], y2, rtol=1e-6, atol=1e-7)
+
+
+def test_mha_default_scale_and_shared_bias_head():
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((1, 3, 12)).astype(np.float32)
+    k = rng.standard_normal((1, 5, 12)).astype(np.float32)
+    v = rng.standard_normal((1, 5, 12)).astype(np.float32)
+    bias = rng.standard_normal((1, 1, 3, 5)).astype(np.float32)
+    got = oracle.multi_head_attention(q, k, v, bias, num_heads=3)
+    want = np.empty((1, 3, 12))
+    for hh in range(3):
+        sl = slice(4 * hh, 4 * hh + 4)
+        want[0, :, sl] = _sdpa_closed_form(q[0, :, sl], k[0, :, sl].T, v[0, :, sl], bias[0, 0],
+                                           1 / np.sqrt(4))
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-6)
