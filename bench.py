@@ -154,12 +154,14 @@ def main():
     ap.add_argument("--quick", action="store_true",
                     help="headline and lm_head measurements only")
     ap.add_argument("--only", default=None,
-                    choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1", "llama16"],
+                    choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1", "llama16",
+                             "attn"],
                     help="profiling mode: launch one workload --steps times and exit "
                          "(lm512 / lm1: Qwen3 lm_head MatMulNBits at M=512 / M=1; i8lm512: "
                          "the lm_head as MatMulInteger at M=512; f32ffn: the MiniLM FFN1 "
-                         "Gemm; llama1 / llama16: the Llama lm_head at M=1 / M=16; copy: 256 MiB device "
-                         "copy used to calibrate the HBM byte counters)")
+                         "Gemm; llama1 / llama16: the Llama lm_head at M=1 / M=16; attn: the MiniLM "
+                         "fused attention; copy: 256 MiB device copy used to calibrate the HBM "
+                         "byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -443,8 +445,10 @@ def int8_prefill(torch, ops, ctx, T, dev, args):
 def f32_encoder(torch, ops, ctx, T, randn, dev, args):
     """One MiniLM-L6 encoder layer's matmuls in fp32: q/k/v/out Gemm (transB,
     bias) [4096,384]x[384,384]^T, FFN1 [4096,384]x[1536,384]^T, FFN2
-    [4096,1536]x[384,1536]^T, and the batched attention MatMuls
-    [384 x 128x32]x[32x128] and [384 x 128x128]x[128x32]."""
+    [4096,1536]x[384,1536]^T, and the attention as the graph runs it after its
+    _FusedSDPA rewrite: softmax([384 x 128x32]x[32x128] * 1/sqrt(32) + padding
+    mask [32,1,1,128]) x [128x32] in one fused launch.  The two attention
+    MatMuls alone (no softmax) are timed beside it."""
     rng = np.random.default_rng(0x5EED0001)
     tok = MINILM_B * MINILM_S
     H, F = MINILM_H, MINILM_FFN
@@ -465,18 +469,33 @@ def f32_encoder(torch, ops, ctx, T, randn, dev, args):
     v = randn(MINILM_B, MINILM_HEADS, MINILM_S, dh)
     sc = torch.empty((MINILM_B, MINILM_HEADS, MINILM_S, MINILM_S), device=dev)
     ctxo = torch.empty((MINILM_B, MINILM_HEADS, MINILM_S, dh), device=dev)
+    # BERT extended attention mask: 0 for tokens, -10000 for padding (the last
+    # 16 positions of every other sequence).
+    mask = torch.zeros((MINILM_B, 1, 1, MINILM_S), device=dev)
+    mask[1::2, :, :, -16:] = -10000.0
+    scale = 1.0 / float(np.sqrt(dh))
 
-    def run():
-        for (_, k, n), w, bb in zip(gemms, ws, bias):
-            w.gemm_dev(x[k].data_ptr(), tok, y[n].data_ptr(), bb.data_ptr(), [n])
+    def attention():
+        ops.fused_sdpa_dev(q.data_ptr(), q.shape, kt.data_ptr(), kt.shape, v.data_ptr(),
+                           v.shape, mask.data_ptr(), mask.shape, scale, ctxo.data_ptr(), ctx=ctx)
+
+    def attention_unfused_matmuls():
         ops.matmul_f32_dev(q.data_ptr(), q.shape, kt.data_ptr(), kt.shape, sc.data_ptr(),
                            ctx=ctx)
         ops.matmul_f32_dev(p.data_ptr(), p.shape, v.data_ptr(), v.shape, ctxo.data_ptr(),
                            ctx=ctx)
 
-    flops = sum(2.0 * tok * k * n for _, k, n in gemms) + 2 * (2.0 * bh * MINILM_S *
-                                                              MINILM_S * dh)
+    def run():
+        for (_, k, n), w, bb in zip(gemms, ws, bias):
+            w.gemm_dev(x[k].data_ptr(), tok, y[n].data_ptr(), bb.data_ptr(), [n])
+        attention()
+
+    attn_flops = 2 * (2.0 * bh * MINILM_S * MINILM_S * dh)
+    flops = sum(2.0 * tok * k * n for _, k, n in gemms) + attn_flops
     ms = T.loop(run, max(args.steps // 2, 5), 2)
+    attn_ms = T.loop(attention, 20, 3)
+    unfused_ms = T.loop(attention_unfused_matmuls, 10, 2)
+    attn_bytes = 4 * (3 * bh * MINILM_S * dh + MINILM_B * MINILM_S + bh * MINILM_S * dh)
     ffn_ms = T.loop(lambda: ws[4].gemm_dev(x[H].data_ptr(), tok, y[F].data_ptr(),
                                            bias[4].data_ptr(), [F]), 10, 2)
     ffn_tf = 2.0 * tok * H * F / (ffn_ms / 1e3) / 1e12
@@ -486,7 +505,15 @@ def f32_encoder(torch, ops, ctx, T, randn, dev, args):
            "gflop_per_layer": round(flops / 1e9, 2),
            "ffn1": {"TFLOP/s": round(ffn_tf, 2),
                     "frac_fp32_mfma_peak": round(ffn_tf / FP32_MFMA_PEAK_TFLOPS, 4),
-                    "ms": round(ffn_ms, 4)}}
+                    "ms": round(ffn_ms, 4)},
+           "attention_fused": {
+               "kernel": "k_attn (_FusedSDPA, 384 heads x 128x128, head 32, padding mask)",
+               "us": round(attn_ms * 1e3, 2),
+               "TFLOP/s": round(attn_flops / (attn_ms / 1e3) / 1e12, 2),
+               "frac_fp32_mfma_peak": round(attn_flops / (attn_ms / 1e3) / 1e12 /
+                                            FP32_MFMA_PEAK_TFLOPS, 4),
+               "GB/s": round(attn_bytes / (attn_ms / 1e3) / 1e9, 1),
+               "unfused_two_matmuls_us": round(unfused_ms * 1e3, 2)}}
     for w in ws:
         w.release()
     print(f"# f32: {out}", file=sys.stderr, flush=True)
@@ -535,9 +562,22 @@ def run_only(args, torch, ops, ctx, stream, dev, randn):
             y = torch.empty((tok, n), device=dev, dtype=torch.float32)
             for _ in range(args.steps):
                 w.gemm_dev(a.data_ptr(), tok, y.data_ptr(), bias.data_ptr(), [n])
+        elif args.only == "attn":
+            dh = MINILM_H // MINILM_HEADS
+            q = randn(MINILM_B, MINILM_HEADS, MINILM_S, dh)
+            kt = randn(MINILM_B, MINILM_HEADS, dh, MINILM_S)
+            v = randn(MINILM_B, MINILM_HEADS, MINILM_S, dh)
+            mask = torch.zeros((MINILM_B, 1, 1, MINILM_S), device=dev)
+            y = torch.empty_like(v)
+            w = None
+            for _ in range(args.steps):
+                ops.fused_sdpa_dev(q.data_ptr(), q.shape, kt.data_ptr(), kt.shape, v.data_ptr(),
+                                   v.shape, mask.data_ptr(), mask.shape, 1.0 / np.sqrt(dh),
+                                   y.data_ptr(), ctx=ctx)
     torch.cuda.synchronize()
     print(f"{args.only}: {args.steps} launches", flush=True)
-    w.release()
+    if w is not None:
+        w.release()
 
 
 if __name__ == "__main__":

@@ -4,9 +4,12 @@
 // operands are strided views of [batch, seq, hidden] tensors.
 //
 // One wave per 32 query rows (a workgroup of 4 waves takes 128 rows of one
-// batch index), streaming the keys in tiles of 32 with an online softmax:
+// batch index), streaming the keys in tiles of 32 with an online softmax.
+// The workgroup stages each K and V tile once in LDS (double-buffered; the
+// next tile's loads are in flight while the current one is computed, one
+// barrier per tile):
 //   * S^T tile (32 keys x 32 queries) = K . Q^T on v_mfma_f32_32x32x2_f32:
-//     A operand lane l = key l % 32, dim 2s + l / 32 (read from K); B operand
+//     A operand lane l = key l % 32, dim 2s + l / 32 (from the K tile); B operand
 //     lane l = query l % 32, dim 2s + l / 32 (the wave's Q, held in
 //     registers for all tiles).  The result gives each lane one query and 16
 //     keys t = 8 (v / 4) + 4 (l / 32) + v % 4 (the other 16 in lane l ^ 32).
@@ -17,7 +20,7 @@
 //     step s pairs k slot l / 32 with key t(s, l / 32) = 8 (s / 4) +
 //     4 (l / 32) + s % 4, so the B operand of step s is exactly the lane's
 //     p[s] from the score layout (no data movement); the A operand lane l
-//     reads V[t(s, l / 32)][32 j + l % 32].
+//     reads V[t(s, l / 32)][32 j + l % 32] from the V tile.
 //   * At the end y = O / l per query; a row whose every score is -inf is NaN
 //     (the reference's exp(-inf - -inf)), and T = 0 gives zeros (an empty
 //     product).
@@ -26,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "mg_internal.h"
 
@@ -35,19 +39,26 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 template <int DS, int DVT>
 __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  constexpr int DP = 2 * DS + 1;     // LDS row pitch of a K tile (odd: no bank conflicts)
+  constexpr int VP = 32 * DVT;       // LDS row pitch of a V tile
+  constexpr int KE = 32 * 2 * DS / 256, VE = 32 * VP / 256;  // staged elements per thread
+  __shared__ float ks[2][32 * DP];
+  __shared__ float vs[2][32 * VP];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int qtiles = (p.S + 127) / 128;
-  const int64_t bi = blockIdx.x / qtiles;
+  const int bi = (int)(blockIdx.x / qtiles);  // the host keeps the grid below 2^31
   const int q0 = (int)(blockIdx.x % qtiles) * 128 + wave * 32;
-  if (q0 >= p.S) return;  // no barriers below: idle waves may leave
+  const bool active = q0 < p.S;  // idle waves still stage tiles and meet the barriers
   // Batch offsets of every operand.
   int64_t oq = 0, ok = 0, ov = 0, om = 0, oy = 0;
   {
-    int64_t rem = bi;
+    int rem = bi;
     for (int d = p.nbd - 1; d >= 0; d--) {
-      const int64_t c = rem % p.bdim[d];
-      rem /= p.bdim[d];
+      const int bd = (int)p.bdim[d];
+      const int64_t c = rem % bd;
+      rem /= bd;
       oq += c * p.q_bs[d];
       ok += c * p.k_bs[d];
       ov += c * p.v_bs[d];
@@ -58,88 +69,182 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
   const int r32 = lane & 31, h = lane >> 5;
   const int q = q0 + r32;  // this lane's query (B-operand column / result column)
   const bool qok = q < p.S;
-  // Lane parts of the element offsets are 32-bit (the host checks the
-  // strides); the uniform parts ride on the per-tile base pointers.
-  const int kst = (int)p.k_ts, kds = (int)p.k_ds, vst = (int)p.v_ts, vds = (int)p.v_ds;
+
+  // Cooperative staging of key tile t0: element e of the thread's share is
+  // (key, dim) chosen so that consecutive threads read consecutive addresses
+  // of whichever index is contiguous in memory.  Out-of-range elements are 0.
+  // The element offsets inside a tile are fixed per thread and 32-bit (the
+  // host checks the strides); the tile base advances by 32 keys.
+  const bool k_tmajor = p.k_ts == 1, v_tmajor = p.v_ts == 1;
+  int kgo[KE], klo[KE], vgo[VE], vlo[VE];
+  unsigned kd_ok = 0, vd_ok = 0;  // per element: dim in range
+#pragma unroll
+  for (int e = 0; e < KE; e++) {
+    const int idx = tid + 256 * e;
+    const int t = k_tmajor ? idx & 31 : idx / (2 * DS);
+    const int d = k_tmajor ? idx >> 5 : idx % (2 * DS);
+    kgo[e] = 4 * (t * (int)p.k_ts + d * (int)p.k_ds);  // bytes
+    klo[e] = t * DP + d;
+    if (d < p.D) kd_ok |= 1u << e;
+  }
+#pragma unroll
+  for (int e = 0; e < VE; e++) {
+    const int idx = tid + 256 * e;
+    const int t = v_tmajor ? idx & 31 : idx / VP;
+    const int dv = v_tmajor ? idx >> 5 : idx % VP;
+    vgo[e] = 4 * (t * (int)p.v_ts + dv * (int)p.v_ds);  // bytes
+    vlo[e] = t * VP + dv;
+    if (dv < p.DV) vd_ok |= 1u << e;
+  }
+  // Raw loaded values: range selections happen when they are consumed (a
+  // use at the load would make the wave wait for it right there).
+  float kreg[KE], vreg[VE];
+  unsigned kin = 0, vin = 0;  // per element: inside the tensor
+  float mreg[16];  // the lane's mask values of the fetched tile (its query)
+  // Loads address a uniform base plus a per-lane 32-bit byte offset.
+  auto ldb = [](const float *base, unsigned bytes) {
+    return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(base) + bytes);
+  };
+  const float *mrow = p.mask ? p.mask + om + (int64_t)(qok ? q : 0) * p.m_qs : nullptr;
   const int mts = (int)p.m_ts;
+  const unsigned mlane = 16u * h * mts;  // bytes of key offset 4h
+  // full: the tile holds 32 keys (no clamping or range checks).
+  auto fetch = [&](int t0, auto full) {
+    constexpr bool F = decltype(full)::value;
+    const int tl = p.T - t0;  // keys left from t0
+    if (mrow && active) {
+      const float *mt = mrow + (int64_t)t0 * p.m_ts;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        // Unconditional loads (clamped in range) so that they batch; keys past
+        // the end are excluded when the scores are formed.
+        const int tu = 8 * (v >> 2) + (v & 3);
+        if (F) {
+          mreg[v] = ldb(mt + tu * mts, mlane);
+        } else {
+          const int tt = tu + 4 * h;
+          mreg[v] = mt[min(tt, tl - 1) * mts];
+        }
+      }
+    }
+    const float *kt = p.k + ok + (int64_t)t0 * p.k_ts;
+    const float *vt = p.v + ov + (int64_t)t0 * p.v_ts;
+#pragma unroll
+    for (int e = 0; e < KE; e++) {
+      const int idx = tid + 256 * e;
+      const int t = k_tmajor ? idx & 31 : idx / (2 * DS);
+      const bool in = (F || t < tl) && ((kd_ok >> e) & 1);
+      kin = in ? kin | (1u << e) : kin & ~(1u << e);
+      kreg[e] = ldb(kt, in ? (unsigned)kgo[e] : 0u);
+    }
+#pragma unroll
+    for (int e = 0; e < VE; e++) {
+      const int idx = tid + 256 * e;
+      const int t = v_tmajor ? idx & 31 : idx / VP;
+      const bool in = (F || t < tl) && ((vd_ok >> e) & 1);
+      vin = in ? vin | (1u << e) : vin & ~(1u << e);
+      vreg[e] = ldb(vt, in ? (unsigned)vgo[e] : 0u);
+    }
+  };
+  auto fetch_any = [&](int t0) {
+    if (t0 + 32 <= p.T)
+      fetch(t0, std::true_type{});
+    else
+      fetch(t0, std::false_type{});
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < KE; e++) ks[buf][klo[e]] = ((kin >> e) & 1) ? kreg[e] : 0.f;
+#pragma unroll
+    for (int e = 0; e < VE; e++) vs[buf][vlo[e]] = ((vin >> e) & 1) ? vreg[e] : 0.f;
+  };
 
   // Q^T fragments: step s holds dim 2s + h of query q.
   float qf[DS];
   {
     const float *qr = p.q + oq + (int64_t)(qok ? q : 0) * p.q_rs;
-    const int qcs = (int)p.q_cs;
 #pragma unroll
     for (int s = 0; s < DS; s++) {
       const int d = 2 * s + h;
-      qf[s] = (qok && d < p.D) ? qr[d * qcs] : 0.f;
+      const bool in = qok && d < p.D;
+      const float x = qr[in ? d * (int)p.q_cs : 0];
+      qf[s] = in ? x : 0.f;
     }
   }
   float16v o[DVT];
 #pragma unroll
   for (int j = 0; j < DVT; j++) o[j] = (float16v){};
   float m_run = -INFINITY, l_run = 0.f;
-  const float *mrow = p.mask ? p.mask + om + (int64_t)(qok ? q : 0) * p.m_qs : nullptr;
-  const int koff = r32 * kst + h * kds;  // key r32, dim h
-  const int voff = 4 * h * vst;          // key offset 4h of every step
+  float mcur[16];
 
-  for (int t0 = 0; t0 < p.T; t0 += 32) {
-    const float *kt = p.k + ok + (int64_t)t0 * p.k_ts;
-    const float *vt = p.v + ov + (int64_t)t0 * p.v_ts;
-    // Scores S^T[t][q] for keys t0 .. t0 + 31.
-    float16v sc = (float16v){};
-    const bool tkok = t0 + r32 < p.T;
+  if (p.T > 0) {
+    fetch_any(0);
+    stage(0);
+  }
+  // Scores in the log2 domain: p = 2^(s * scale * log2 e + mask * log2 e - m).
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float scale2 = p.scale * kLog2e;
+  __syncthreads();
+  for (int t0 = 0, it = 0; t0 < p.T; t0 += 32, it++) {
+    const int buf = it & 1;
+    const bool more = t0 + 32 < p.T;
 #pragma unroll
-    for (int s = 0; s < DS; s++) {
-      const bool dok = 2 * s + h < p.D;
-      const float kv = (tkok && dok) ? kt[koff + 2 * s * kds] : 0.f;
-      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv, qf[s], sc, 0, 0, 0);
-    }
-    float pv[16];
-    float tmax = -INFINITY;
+    for (int v = 0; v < 16; v++) mcur[v] = mreg[v];
+    if (more) fetch_any(t0 + 32);  // next tile's loads fly while this one is computed
+    const bool full = t0 + 32 <= p.T;
+    if (active) {
+      const float *kl = &ks[buf][0];
+      const float *vl = &vs[buf][0];
+      // Scores S^T[t][q] for keys t0 .. t0 + 31.
+      float16v sc = (float16v){};
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int tt = 8 * (v >> 2) + (v & 3);  // key of slot v in half 0
-      float x = -INFINITY;
-      if (t0 + tt + 4 * h < p.T)
-        x = fmaf(sc[v], p.scale, mrow ? mrow[(int64_t)t0 * p.m_ts + (tt + 4 * h) * mts] : 0.f);
-      pv[v] = x;
-      tmax = fmaxf(tmax, x);
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    float corr = 1.f;
-    if (m_new == -INFINITY) {
-#pragma unroll
-      for (int v = 0; v < 16; v++) pv[v] = 0.f;
-    } else {
-      corr = __expf(m_run - m_new);  // 0 while nothing has been accumulated
-      float ls = 0.f;
+      for (int s = 0; s < DS; s++)
+        sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kl[r32 * DP + 2 * s + h], qf[s], sc, 0, 0, 0);
+      float pv[16];
+      float tmax = -INFINITY;
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        pv[v] = __expf(pv[v] - m_new);
-        ls += pv[v];
+        const int tt = 8 * (v >> 2) + (v & 3) + 4 * h;  // key of slot v
+        float x = fmaf(sc[v], scale2, mrow ? mcur[v] * kLog2e : 0.f);
+        if (!full && t0 + tt >= p.T) x = -INFINITY;
+        pv[v] = x;
+        tmax = fmaxf(tmax, x);
       }
-      l_run = l_run * corr + ls;
-      m_run = m_new;
-    }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float m_new = fmaxf(m_run, tmax);
+      float corr = 1.f;
+      if (m_new == -INFINITY) {
 #pragma unroll
-    for (int j = 0; j < DVT; j++) {
+        for (int v = 0; v < 16; v++) pv[v] = 0.f;
+      } else {
+        corr = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 while nothing has been accumulated
+        float ls = 0.f;
 #pragma unroll
-      for (int v = 0; v < 16; v++) o[j][v] *= corr;
-      const int dv = 32 * j + r32;
-      const bool dvok = dv < p.DV;
-      const int vl = voff + dv * vds;
+        for (int v = 0; v < 16; v++) {
+          pv[v] = __builtin_amdgcn_exp2f(pv[v] - m_new);
+          ls += pv[v];
+        }
+        l_run = l_run * corr + ls;
+        m_run = m_new;
+      }
 #pragma unroll
-      for (int s = 0; s < 16; s++) {
-        const int tt = 8 * (s >> 2) + (s & 3);
-        const float a = (dvok && t0 + tt + 4 * h < p.T) ? vt[vl + tt * vst] : 0.f;
-        o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, pv[s], o[j], 0, 0, 0);
+      for (int j = 0; j < DVT; j++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[j][v] *= corr;
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+          const int tt = 8 * (s >> 2) + (s & 3) + 4 * h;
+          o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vl[tt * VP + 32 * j + r32], pv[s], o[j], 0,
+                                                      0, 0);
+        }
       }
     }
+    if (more) stage(buf ^ 1);  // the other buffer: its readers passed the last barrier
+    __syncthreads();
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (!qok) return;
+  if (!active || !qok) return;
   float inv;
   if (p.T == 0)
     inv = 0.f;  // empty softmax: the product is a sum over no keys
@@ -180,11 +285,17 @@ mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
   const int64_t wgs = nbatch * ((p.S + 127) / 128);
   if (wgs > 0x7fffffff) return mg_fail(MG_UNSUPPORTED, "attention: grid too large");
   const dim3 grid((unsigned)wgs);
+  mg_attn_problem pp = p;
+  if (p.D == 0) {  // no products: the kernel's (masked-off) Q and K loads read V instead
+    pp.q = pp.k = p.v;
+    pp.q_rs = pp.q_cs = pp.k_ts = pp.k_ds = 0;
+    for (int d = 0; d < MG_ATTN_MAX_BATCH_DIMS; d++) pp.q_bs[d] = pp.k_bs[d] = 0;
+  }
   if (p.D <= 32)
-    launch_dvt<16>(p, grid, ctx->stream);
+    launch_dvt<16>(pp, grid, ctx->stream);
   else if (p.D <= 64)
-    launch_dvt<32>(p, grid, ctx->stream);
+    launch_dvt<32>(pp, grid, ctx->stream);
   else
-    launch_dvt<64>(p, grid, ctx->stream);
+    launch_dvt<64>(pp, grid, ctx->stream);
   return mg_launch_check("k_attn");
 }
