@@ -988,9 +988,10 @@ void batch_strides(const std::vector<int64_t> &ob, const std::vector<int64_t> &a
 }
 
 bool fits_lane_offsets(const mg_attn_problem &p) {
-  // Lane parts of the kernel's offsets: 32 rows/keys and 128 dims per stride.
-  const int64_t lim = (int64_t)1 << 30;
-  for (int64_t s : {p.k_ts, p.k_ds, p.v_ts, p.v_ds, p.m_ts, p.q_cs})
+  // Lane parts of the kernel's byte offsets (32 rows/keys and 128 dims per
+  // stride, 4 bytes each) stay below 2^31, the kernel's out-of-range marker.
+  const int64_t lim = (int64_t)1 << 28;
+  for (int64_t s : {p.k_ts, p.k_ds, p.v_ts, p.v_ds, p.m_ts, p.m_qs, p.q_cs})
     if (s < 0 || s * 160 >= lim) return false;
   return true;
 }

@@ -5,22 +5,25 @@
 //
 // One wave per 32 query rows (a workgroup of 4 waves takes 128 rows of one
 // batch index), streaming the keys in tiles of 32 with an online softmax.
-// The workgroup stages each K and V tile once in LDS (double-buffered; the
-// next tile's loads are in flight while the current one is computed, one
-// barrier per tile):
+// The workgroup stages each K and V tile once in LDS (double-buffered, one
+// barrier per tile); its global loads are raw buffer loads issued two tiles
+// ahead of use (two register sets), with out-of-range elements read as 0 by
+// the hardware:
 //   * S^T tile (32 keys x 32 queries) = K . Q^T on v_mfma_f32_32x32x2_f32:
-//     A operand lane l = key l % 32, dim 2s + l / 32 (from the K tile); B operand
-//     lane l = query l % 32, dim 2s + l / 32 (the wave's Q, held in
-//     registers for all tiles).  The result gives each lane one query and 16
-//     keys t = 8 (v / 4) + 4 (l / 32) + v % 4 (the other 16 in lane l ^ 32).
+//     step s gives lane l key l % 32 (A) or query l % 32 (B) at dim
+//     DS (l / 32) + s, so a lane's K fragments of a tile are one contiguous
+//     LDS run (16-byte reads); the Q fragments stay in registers.  The result
+//     gives each lane one query and 16 keys t = 8 (v / 4) + 4 (l / 32) + v % 4
+//     (the other 16 in lane l ^ 32).
 //   * val = fma(S, scale, mask) (padding keys -inf); the running max m and
 //     sum l per query (lane pair), p = exp(val - m_new), and the output and
-//     sum rescaled by exp(m_old - m_new).
+//     sum rescaled by exp(m_old - m_new), all in the log2 domain.
 //   * O^T (32 dims x 32 queries, per 32-dim tile of V) += V^T . P^T: MFMA
 //     step s pairs k slot l / 32 with key t(s, l / 32) = 8 (s / 4) +
 //     4 (l / 32) + s % 4, so the B operand of step s is exactly the lane's
 //     p[s] from the score layout (no data movement); the A operand lane l
-//     reads V[t(s, l / 32)][32 j + l % 32] from the V tile.
+//     reads V[t(s, l / 32)][32 j + l % 32] from the transposed V tile, where
+//     the keys of steps 4g .. 4g + 3 are adjacent (one 16-byte read).
 //   * At the end y = O / l per query; a row whose every score is -inf is NaN
 //     (the reference's exp(-inf - -inf)), and T = 0 gives zeros (an empty
 //     product).
@@ -39,14 +42,18 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 template <int DS, int DVT>
 __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
-  constexpr int DP = 2 * DS + 1;     // LDS row pitch of a K tile (odd: no bank conflicts)
-  constexpr int VP = 32 * DVT;       // LDS row pitch of a V tile
-  constexpr int KE = 32 * 2 * DS / 256, VE = 32 * VP / 256;  // staged elements per thread
-  __shared__ float ks[2][32 * DP];
-  __shared__ float vs[2][32 * VP];
+  // LDS tiles: K as [key][dim] with row pitch DP, V transposed as [dim][key]
+  // with row pitch VT.  Both pitches are 4 (mod 64) floats: rows start on 16
+  // bytes and the 16-byte reads of 16 consecutive rows fall in distinct bank
+  // groups.
+  constexpr int DP = 2 * DS + 4;
+  constexpr int VT = 36;
+  constexpr int KE = 32 * 2 * DS / 256, VE = 32 * 32 * DVT / 256;  // staged elements per thread
+  __shared__ __attribute__((aligned(16))) float ks[2][32 * DP];
+  __shared__ __attribute__((aligned(16))) float vs[2][32 * DVT * VT];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qtiles = (p.S + 127) / 128;
   const int bi = (int)(blockIdx.x / qtiles);  // the host keeps the grid below 2^31
   const int q0 = (int)(blockIdx.x % qtiles) * 128 + wave * 32;
@@ -72,100 +79,101 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
 
   // Cooperative staging of key tile t0: element e of the thread's share is
   // (key, dim) chosen so that consecutive threads read consecutive addresses
-  // of whichever index is contiguous in memory.  Out-of-range elements are 0.
-  // The element offsets inside a tile are fixed per thread and 32-bit (the
-  // host checks the strides); the tile base advances by 32 keys.
+  // of whichever index is contiguous in memory.  Loads are raw buffer loads:
+  // a tile base in the (uniform) resource plus a fixed 32-bit byte offset per
+  // element; an element outside the tensor gets offset kOob, past the
+  // resource's range, and the hardware returns 0 for it.  The host keeps the
+  // in-range offsets below 2^31.
+  constexpr unsigned kOob = 0x80000000u;
   const bool k_tmajor = p.k_ts == 1, v_tmajor = p.v_ts == 1;
-  int kgo[KE], klo[KE], vgo[VE], vlo[VE];
-  unsigned kd_ok = 0, vd_ok = 0;  // per element: dim in range
+  unsigned kgo[KE], vgo[VE];
+  int klo[KE], vlo[VE];
 #pragma unroll
   for (int e = 0; e < KE; e++) {
     const int idx = tid + 256 * e;
     const int t = k_tmajor ? idx & 31 : idx / (2 * DS);
     const int d = k_tmajor ? idx >> 5 : idx % (2 * DS);
-    kgo[e] = 4 * (t * (int)p.k_ts + d * (int)p.k_ds);  // bytes
+    kgo[e] = d < p.D ? 4u * (unsigned)(t * (int)p.k_ts + d * (int)p.k_ds) : kOob;
     klo[e] = t * DP + d;
-    if (d < p.D) kd_ok |= 1u << e;
   }
 #pragma unroll
   for (int e = 0; e < VE; e++) {
     const int idx = tid + 256 * e;
-    const int t = v_tmajor ? idx & 31 : idx / VP;
-    const int dv = v_tmajor ? idx >> 5 : idx % VP;
-    vgo[e] = 4 * (t * (int)p.v_ts + dv * (int)p.v_ds);  // bytes
-    vlo[e] = t * VP + dv;
-    if (dv < p.DV) vd_ok |= 1u << e;
+    const int t = v_tmajor ? idx & 31 : idx / (32 * DVT);
+    const int dv = v_tmajor ? idx >> 5 : idx % (32 * DVT);
+    vgo[e] = dv < p.DV ? 4u * (unsigned)(t * (int)p.v_ts + dv * (int)p.v_ds) : kOob;
+    vlo[e] = dv * VT + t;
   }
-  // Raw loaded values: range selections happen when they are consumed (a
-  // use at the load would make the wave wait for it right there).
-  float kreg[KE], vreg[VE];
-  unsigned kin = 0, vin = 0;  // per element: inside the tensor
-  float mreg[16];  // the lane's mask values of the fetched tile (its query)
-  // Loads address a uniform base plus a per-lane 32-bit byte offset.
-  auto ldb = [](const float *base, unsigned bytes) {
-    return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(base) + bytes);
+  auto rsrc = [](const float *base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, 0x7ffffff0,
+                                             0x00020000);
   };
-  const float *mrow = p.mask ? p.mask + om + (int64_t)(qok ? q : 0) * p.m_qs : nullptr;
-  const int mts = (int)p.m_ts;
-  const unsigned mlane = 16u * h * mts;  // bytes of key offset 4h
-  // full: the tile holds 32 keys (no clamping or range checks).
-  auto fetch = [&](int t0, auto full) {
+  auto ldr = [](__amdgpu_buffer_rsrc_t r, unsigned off) __attribute__((always_inline)) {
+    asm("" : "+v"(off));  // an opaque offset: the select stays a select, not a branch
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  };
+  // Two register sets: tile i is fetched into set i % 2 two tiles ahead of
+  // its use, so each load has two tiles of compute to arrive.
+  float kreg[2][KE], vreg[2][VE];
+  float mreg[2][16];  // the lane's mask values of a fetched tile (its query)
+  // Mask rows of the wave's 32 queries: a wave-uniform base (row q0) and the
+  // lane's row offset; rows past S read nothing.
+  const float *mrow = p.mask ? p.mask + om + (int64_t)q0 * p.m_qs : nullptr;
+  const unsigned mts4 = 4u * (unsigned)p.m_ts;
+  const unsigned mq = qok ? 4u * (unsigned)(r32 * (int)p.m_qs) : kOob;
+  // full: the tile holds 32 keys (no range checks on keys).
+  auto fetch = [&](int t0, auto full, auto set) __attribute__((always_inline)) {
     constexpr bool F = decltype(full)::value;
+    constexpr int R = decltype(set)::value;
     const int tl = p.T - t0;  // keys left from t0
     if (mrow && active) {
-      const float *mt = mrow + (int64_t)t0 * p.m_ts;
+      const __amdgpu_buffer_rsrc_t rm = rsrc(mrow + (int64_t)t0 * p.m_ts);
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        // Unconditional loads (clamped in range) so that they batch; keys past
-        // the end are excluded when the scores are formed.
-        const int tu = 8 * (v >> 2) + (v & 3);
-        if (F) {
-          mreg[v] = ldb(mt + tu * mts, mlane);
-        } else {
-          const int tt = tu + 4 * h;
-          mreg[v] = mt[min(tt, tl - 1) * mts];
-        }
+        const int tt = 8 * (v >> 2) + (v & 3) + 4 * h;  // key of slot v
+        mreg[R][v] = ldr(rm, (F || tt < tl) && qok ? mq + (unsigned)tt * mts4 : kOob);
       }
     }
-    const float *kt = p.k + ok + (int64_t)t0 * p.k_ts;
-    const float *vt = p.v + ov + (int64_t)t0 * p.v_ts;
+    const __amdgpu_buffer_rsrc_t rk = rsrc(p.k + ok + (int64_t)t0 * p.k_ts);
+    const __amdgpu_buffer_rsrc_t rv = rsrc(p.v + ov + (int64_t)t0 * p.v_ts);
 #pragma unroll
     for (int e = 0; e < KE; e++) {
       const int idx = tid + 256 * e;
       const int t = k_tmajor ? idx & 31 : idx / (2 * DS);
-      const bool in = (F || t < tl) && ((kd_ok >> e) & 1);
-      kin = in ? kin | (1u << e) : kin & ~(1u << e);
-      kreg[e] = ldb(kt, in ? (unsigned)kgo[e] : 0u);
+      kreg[R][e] = ldr(rk, F || t < tl ? kgo[e] : kOob);
     }
 #pragma unroll
     for (int e = 0; e < VE; e++) {
       const int idx = tid + 256 * e;
-      const int t = v_tmajor ? idx & 31 : idx / VP;
-      const bool in = (F || t < tl) && ((vd_ok >> e) & 1);
-      vin = in ? vin | (1u << e) : vin & ~(1u << e);
-      vreg[e] = ldb(vt, in ? (unsigned)vgo[e] : 0u);
+      const int t = v_tmajor ? idx & 31 : idx / (32 * DVT);
+      vreg[R][e] = ldr(rv, F || t < tl ? vgo[e] : kOob);
     }
   };
-  auto fetch_any = [&](int t0) {
+  auto fetch_any = [&](int t0, auto set) __attribute__((always_inline)) {
     if (t0 + 32 <= p.T)
-      fetch(t0, std::true_type{});
+      fetch(t0, std::true_type{}, set);
     else
-      fetch(t0, std::false_type{});
+      fetch(t0, std::false_type{}, set);
   };
-  auto stage = [&](int buf) {
+  // Register set R -> LDS buffer R.
+  auto stage = [&](auto set) __attribute__((always_inline)) {
+    constexpr int R = decltype(set)::value;
 #pragma unroll
-    for (int e = 0; e < KE; e++) ks[buf][klo[e]] = ((kin >> e) & 1) ? kreg[e] : 0.f;
+    for (int e = 0; e < KE; e++) ks[R][klo[e]] = kreg[R][e];
 #pragma unroll
-    for (int e = 0; e < VE; e++) vs[buf][vlo[e]] = ((vin >> e) & 1) ? vreg[e] : 0.f;
+    for (int e = 0; e < VE; e++) vs[R][vlo[e]] = vreg[R][e];
   };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
 
-  // Q^T fragments: step s holds dim 2s + h of query q.
+  // Q^T fragments: step s holds dim DS h + s of query q (lane half h takes
+  // one half of the dims, so its K fragments are one contiguous LDS run).
   float qf[DS];
   {
     const float *qr = p.q + oq + (int64_t)(qok ? q : 0) * p.q_rs;
 #pragma unroll
     for (int s = 0; s < DS; s++) {
-      const int d = 2 * s + h;
+      const int d = DS * h + s;
       const bool in = qok && d < p.D;
       const float x = qr[in ? d * (int)p.q_cs : 0];
       qf[s] = in ? x : 0.f;
@@ -178,28 +186,39 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
   float mcur[16];
 
   if (p.T > 0) {
-    fetch_any(0);
-    stage(0);
+    fetch_any(0, I0{});
+    if (p.T > 32) fetch_any(32, I1{});
+    stage(I0{});
   }
   // Scores in the log2 domain: p = 2^(s * scale * log2 e + mask * log2 e - m).
   constexpr float kLog2e = 1.4426950408889634f;
   const float scale2 = p.scale * kLog2e;
   __syncthreads();
-  for (int t0 = 0, it = 0; t0 < p.T; t0 += 32, it++) {
-    const int buf = it & 1;
-    const bool more = t0 + 32 < p.T;
+  // Tile at t0 (parity B): its K/V are in LDS buffer B and its mask in set
+  // B.  Set B is then refilled with the tile at t0 + 64, and set 1 - B (the
+  // tile at t0 + 32, fetched one tile ago) is staged into buffer 1 - B.
+  auto tile = [&](int t0, auto bsel) __attribute__((always_inline)) {
+    constexpr int B = decltype(bsel)::value;
+    using NB = std::integral_constant<int, 1 - B>;
 #pragma unroll
-    for (int v = 0; v < 16; v++) mcur[v] = mreg[v];
-    if (more) fetch_any(t0 + 32);  // next tile's loads fly while this one is computed
+    for (int v = 0; v < 16; v++) mcur[v] = mreg[B][v];
+    if (t0 + 64 < p.T) fetch_any(t0 + 64, bsel);
     const bool full = t0 + 32 <= p.T;
     if (active) {
-      const float *kl = &ks[buf][0];
-      const float *vl = &vs[buf][0];
-      // Scores S^T[t][q] for keys t0 .. t0 + 31.
+      const float *kl = &ks[B][0];
+      const float *vl = &vs[B][0];
+      // Scores S^T[t][q] for keys t0 .. t0 + 31.  The lane's K fragments
+      // (key r32, dims DS h ..) are read with 16-byte loads up front.
+      float kf[DS];
+#pragma unroll
+      for (int i = 0; i < DS / 4; i++) {
+        const float4 x = *reinterpret_cast<const float4 *>(kl + r32 * DP + DS * h + 4 * i);
+        kf[4 * i] = x.x, kf[4 * i + 1] = x.y, kf[4 * i + 2] = x.z, kf[4 * i + 3] = x.w;
+      }
       float16v sc = (float16v){};
 #pragma unroll
       for (int s = 0; s < DS; s++)
-        sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kl[r32 * DP + 2 * s + h], qf[s], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[s], sc, 0, 0, 0);
       float pv[16];
       float tmax = -INFINITY;
 #pragma unroll
@@ -229,18 +248,28 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
       }
 #pragma unroll
       for (int j = 0; j < DVT; j++) {
+        // V^T fragments of dim 32 j + r32: keys t(s, h) of steps 4g .. 4g + 3
+        // are the 4 consecutive keys 8g + 4h .., one 16-byte read each.
+        float vf[16];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4 x =
+              *reinterpret_cast<const float4 *>(vl + (32 * j + r32) * VT + 8 * g + 4 * h);
+          vf[4 * g] = x.x, vf[4 * g + 1] = x.y, vf[4 * g + 2] = x.z, vf[4 * g + 3] = x.w;
+        }
 #pragma unroll
         for (int v = 0; v < 16; v++) o[j][v] *= corr;
 #pragma unroll
-        for (int s = 0; s < 16; s++) {
-          const int tt = 8 * (s >> 2) + (s & 3) + 4 * h;
-          o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vl[tt * VP + 32 * j + r32], pv[s], o[j], 0,
-                                                      0, 0);
-        }
+        for (int s = 0; s < 16; s++)
+          o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s], pv[s], o[j], 0, 0, 0);
       }
     }
-    if (more) stage(buf ^ 1);  // the other buffer: its readers passed the last barrier
+    if (t0 + 32 < p.T) stage(NB{});  // its readers passed the last barrier
     __syncthreads();
+  };
+  for (int t0 = 0; t0 < p.T; t0 += 64) {
+    tile(t0, I0{});
+    if (t0 + 32 < p.T) tile(t0 + 32, I1{});
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
