@@ -308,6 +308,106 @@ mg_status mg_multi_head_attention_dev(mg_ctx *ctx, const float *q_dev,
                                       int32_t bias_heads, int32_t has_scale,
                                       float scale, float *y_dev);
 
+/* ---------------------------------------------------------- convolution */
+
+/* Conv (lib/src/onnx_nn_ops.dart:179-817, dispatched at
+ * lib/src/onnx_graph.dart:2436-2490): x [N, C, spatial...] with 1 to 3
+ * spatial dims, w [M, C / group, kernel...], bias NULL or [M].  strides and
+ * dilations NULL (all 1) or [nd]; pads NULL (all 0) or [2 nd] (all begins,
+ * then all ends); auto_pad 0 NOTSET, 1 SAME_UPPER, 2 SAME_LOWER, 3 VALID,
+ * resolved as the reference's _resolvePads (lib/src/onnx_nn_ops.dart:38-87).
+ * y [N, M, out...] from mg_conv_output_shape (x_rank values). */
+mg_status mg_conv_output_shape(const int64_t *x_shape, int32_t x_rank,
+                               const int64_t *w_shape, const int64_t *strides,
+                               const int64_t *pads, const int64_t *dilations,
+                               int32_t group, int32_t auto_pad,
+                               int64_t *y_shape);
+mg_status mg_conv_f32(mg_ctx *ctx, const float *x, const int64_t *x_shape,
+                      int32_t x_rank, const float *w, const int64_t *w_shape,
+                      const float *bias, const int64_t *strides,
+                      const int64_t *pads, const int64_t *dilations,
+                      int32_t group, int32_t auto_pad, float *y);
+mg_status mg_conv_f32_dev(mg_ctx *ctx, const float *x_dev,
+                          const int64_t *x_shape, int32_t x_rank,
+                          const float *w_dev, const int64_t *w_shape,
+                          const float *bias_dev, const int64_t *strides,
+                          const int64_t *pads, const int64_t *dilations,
+                          int32_t group, int32_t auto_pad, float *y_dev);
+
+/* ConvTranspose (lib/src/onnx_nn_ops.dart:818-1059, dispatched at
+ * lib/src/onnx_graph.dart:2491-2513; auto_pad is not read there):
+ * w [C, M / group, kernel...]; output_padding NULL or [nd]; output_shape
+ * NULL or at least nd entries (its last nd are the spatial dims; the pads are
+ * then derived, the larger half at the beginning). */
+mg_status mg_conv_transpose_output_shape(
+    const int64_t *x_shape, int32_t x_rank, const int64_t *w_shape,
+    const int64_t *strides, const int64_t *pads, const int64_t *dilations,
+    const int64_t *output_padding, const int64_t *output_shape,
+    int32_t output_shape_len, int32_t group, int64_t *y_shape);
+mg_status mg_conv_transpose_f32(mg_ctx *ctx, const float *x,
+                                const int64_t *x_shape, int32_t x_rank,
+                                const float *w, const int64_t *w_shape,
+                                const float *bias, const int64_t *strides,
+                                const int64_t *pads, const int64_t *dilations,
+                                const int64_t *output_padding,
+                                const int64_t *output_shape,
+                                int32_t output_shape_len, int32_t group,
+                                float *y);
+mg_status mg_conv_transpose_f32_dev(
+    mg_ctx *ctx, const float *x_dev, const int64_t *x_shape, int32_t x_rank,
+    const float *w_dev, const int64_t *w_shape, const float *bias_dev,
+    const int64_t *strides, const int64_t *pads, const int64_t *dilations,
+    const int64_t *output_padding, const int64_t *output_shape,
+    int32_t output_shape_len, int32_t group, float *y_dev);
+
+/* ConvInteger (lib/src/onnx_qlinear_ops.dart:232-337, dispatched at
+ * lib/src/onnx_graph.dart:2889-2901): y = sum (x - x_zp)(w - w_zp[m]) as
+ * exact int32 (the shim widens to Tensor.int64); x and w are bytes, uint8
+ * or int8 per *_signed; w_zp NULL, scalar (len 1) or per output channel
+ * (len M), else MG_UNSUPPORTED.  Geometry as mg_conv_f32 with auto_pad
+ * NOTSET.  The _dev form takes device x / w / y; w_zp stays a host array. */
+mg_status mg_conv_integer(mg_ctx *ctx, const void *x, int32_t x_signed,
+                          const int64_t *x_shape, int32_t x_rank,
+                          const void *w, int32_t w_signed,
+                          const int64_t *w_shape, int32_t x_zp,
+                          const int32_t *w_zp, int64_t w_zp_len,
+                          const int64_t *strides, const int64_t *pads,
+                          const int64_t *dilations, int32_t group,
+                          int32_t *y);
+mg_status mg_conv_integer_dev(mg_ctx *ctx, const void *x_dev,
+                              int32_t x_signed, const int64_t *x_shape,
+                              int32_t x_rank, const void *w_dev,
+                              int32_t w_signed, const int64_t *w_shape,
+                              int32_t x_zp, const int32_t *w_zp,
+                              int64_t w_zp_len, const int64_t *strides,
+                              const int64_t *pads, const int64_t *dilations,
+                              int32_t group, int32_t *y_dev);
+
+/* QLinearConv (lib/src/onnx_qlinear_ops.dart:339-382, dispatched at
+ * lib/src/onnx_graph.dart:2935-2955): q = roundHalfEven((acc + bias[m]) *
+ * x_scale * w_scale[m] / y_scale, in double) + y_zp clamped to [lo, hi]
+ * ([-128, 127] when the y_zp initializer is int8, else [0, 255]), stored as
+ * bytes.  w_scale scalar or per output channel; bias NULL or int32 [M].  The
+ * _dev form takes device x / w / bias / y; w_scale and w_zp stay host arrays. */
+mg_status mg_qlinear_conv(mg_ctx *ctx, const void *x, int32_t x_signed,
+                          const int64_t *x_shape, int32_t x_rank,
+                          float x_scale, int32_t x_zp, const void *w,
+                          int32_t w_signed, const int64_t *w_shape,
+                          const float *w_scale, int64_t w_scale_len,
+                          const int32_t *w_zp, int64_t w_zp_len,
+                          float y_scale, int32_t y_zp, const int32_t *bias,
+                          const int64_t *strides, const int64_t *pads,
+                          const int64_t *dilations, int32_t group,
+                          int32_t lo, int32_t hi, uint8_t *y);
+mg_status mg_qlinear_conv_dev(
+    mg_ctx *ctx, const void *x_dev, int32_t x_signed, const int64_t *x_shape,
+    int32_t x_rank, float x_scale, int32_t x_zp, const void *w_dev,
+    int32_t w_signed, const int64_t *w_shape, const float *w_scale,
+    int64_t w_scale_len, const int32_t *w_zp, int64_t w_zp_len,
+    float y_scale, int32_t y_zp, const int32_t *bias_dev,
+    const int64_t *strides, const int64_t *pads, const int64_t *dilations,
+    int32_t group, int32_t lo, int32_t hi, uint8_t *y_dev);
+
 /* ----------------------------------------------------------------- weights */
 
 mg_status mg_weight_release(mg_weight *w);

@@ -60,6 +60,22 @@ SIGNATURES = {
                                 _F, _P],
     "mg_multi_head_attention_dev": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P, _I32,
                                     _I32, _F, _P],
+    "mg_conv_output_shape": [_P, _I32, _P, _P, _P, _P, _I32, _I32, _P],
+    "mg_conv_f32": [_P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _P],
+    "mg_conv_f32_dev": [_P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _P],
+    "mg_conv_transpose_output_shape": [_P, _I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _P],
+    "mg_conv_transpose_f32": [_P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32,
+                              _P],
+    "mg_conv_transpose_f32_dev": [_P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _I32,
+                                  _I32, _P],
+    "mg_conv_integer": [_P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I64, _P, _P, _P,
+                        _I32, _P],
+    "mg_conv_integer_dev": [_P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I64, _P, _P, _P,
+                            _I32, _P],
+    "mg_qlinear_conv": [_P, _P, _I32, _P, _I32, _F, _I32, _P, _I32, _P, _P, _I64, _P, _I64,
+                        _F, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P],
+    "mg_qlinear_conv_dev": [_P, _P, _I32, _P, _I32, _F, _I32, _P, _I32, _P, _P, _I64, _P,
+                            _I64, _F, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P],
     "mg_matmul_f32": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_matmul_f32_dev": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_gemm_f32": [_P, _P, _P, _P, _P, _I32, _I32, _F, _F, _P, _P, _I32, _P],

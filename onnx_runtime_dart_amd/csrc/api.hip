@@ -1205,3 +1205,434 @@ mg_status mg_multi_head_attention_dev(mg_ctx *ctx, const float *q_dev, const flo
   p.y = y_dev;
   return mg_attn_run(ctx, p);
 }
+
+// --------------------------------------------------------------------------
+// Convolution family.
+
+namespace {
+
+// Spatial axes are stored right-aligned in 3 slots (depth, height, width).
+constexpr int kConvSlots = 3;
+
+mg_status conv_common(const char *op, const int64_t *xs, int32_t xr, const int64_t *ws,
+                      int32_t wr, const int64_t *strides, const int64_t *dil, int32_t group,
+                      mg_conv_problem *p) {
+  if (xr < 3 || xr > 5 || wr != xr || !shape_ok(xs, xr) || !shape_ok(ws, wr))
+    return mg_fail(MG_INVALID_ARGUMENT,
+                   std::string(op) + ": x and w must have the same rank, 3 to 5");
+  if (group < 1) return mg_fail(MG_INVALID_ARGUMENT, std::string(op) + ": group must be >= 1");
+  const int nd = xr - 2, o = kConvSlots - nd;
+  for (int a = 0; a < nd; a++) {
+    const int64_t s = strides ? strides[a] : 1, d = dil ? dil[a] : 1;
+    if (s < 1 || d < 1)
+      return mg_fail(MG_INVALID_ARGUMENT, std::string(op) + ": strides and dilations must be >= 1");
+    if (ws[2 + a] < 1)
+      return mg_fail(MG_INVALID_ARGUMENT, std::string(op) + ": empty kernel");
+    p->in[o + a] = xs[2 + a];
+    p->ker[o + a] = ws[2 + a];
+    p->str[o + a] = s;
+    p->dil[o + a] = d;
+  }
+  p->n = xs[0];
+  p->c = xs[1];
+  p->group = group;
+  return MG_OK;
+}
+
+mg_status conv_limits(const char *op, const mg_conv_problem &p) {
+  const int64_t lim = 0x7fffffff;
+  int64_t in_sp = 1, out_sp = 1;
+  for (int a = 0; a < kConvSlots; a++) {
+    // The kernel forms o * str + kk * dil +- pad in 32 bits.
+    if (p.in[a] > lim || p.out[a] > lim || p.ker[a] > lim || p.dil[a] > lim || p.str[a] > lim ||
+        std::abs(p.pad[a]) > lim / 4 ||
+        (double)p.out[a] * (double)p.str[a] + (double)p.ker[a] * (double)p.dil[a] +
+                (double)std::abs(p.pad[a]) > (double)lim / 2)
+      return mg_fail(MG_UNSUPPORTED, std::string(op) + ": spatial size too large");
+    in_sp *= p.in[a];
+    out_sp *= p.out[a];
+  }
+  if (in_sp > lim || out_sp > lim)
+    return mg_fail(MG_UNSUPPORTED, std::string(op) + ": spatial size too large");
+  // The kernel clamps out-of-range reads to element 0 of x, which must exist.
+  if (in_sp == 0 && out_sp > 0 && p.n > 0 && p.m > 0 && p.cg > 0)
+    return mg_fail(MG_UNSUPPORTED, std::string(op) + ": empty spatial input with padding");
+  return MG_OK;
+}
+
+// Conv geometry (lib/src/onnx_nn_ops.dart:179-245 with _resolvePads :38-87):
+// w [M, C/group, kernel...]; pads [begins..., ends...]; auto_pad 0 NOTSET,
+// 1 SAME_UPPER, 2 SAME_LOWER, 3 VALID.  y_shape receives x_rank values.
+mg_status plan_conv(const int64_t *xs, int32_t xr, const int64_t *ws, int32_t wr,
+                    const int64_t *strides, const int64_t *pads, const int64_t *dil,
+                    int32_t group, int32_t auto_pad, mg_conv_problem *p, int64_t *y_shape) {
+  MG_TRY(conv_common("Conv", xs, xr, ws, wr, strides, dil, group, p));
+  if (auto_pad < 0 || auto_pad > 3)
+    return mg_fail(MG_INVALID_ARGUMENT, "Conv: auto_pad must be 0..3");
+  const int nd = xr - 2, o = kConvSlots - nd;
+  p->m = ws[0];
+  p->cg = ws[1];
+  if (p->cg * group != p->c)
+    return mg_fail(MG_INVALID_ARGUMENT, "Conv: input channels must equal w.shape[1] * group");
+  if (p->m % group != 0)
+    return mg_fail(MG_INVALID_ARGUMENT, "Conv: output channels must be a multiple of group");
+  p->mg = p->m / group;
+  for (int a = 0; a < nd; a++) {
+    const int64_t in = xs[2 + a], s = p->str[o + a];
+    const int64_t window = p->dil[o + a] * (ws[2 + a] - 1) + 1;
+    int64_t out, pb = 0;
+    if (auto_pad == 1 || auto_pad == 2) {
+      out = (in + s - 1) / s;
+      const int64_t total = std::max<int64_t>(0, (out - 1) * s + window - in);
+      const int64_t small = total / 2;
+      pb = auto_pad == 1 ? small : total - small;  // SAME_UPPER: the extra at the end
+    } else if (auto_pad == 3) {
+      out = (in - window) / s + 1;  // truncating, as Dart's ~/
+    } else {
+      pb = pads ? pads[a] : 0;
+      const int64_t pe = pads ? pads[nd + a] : 0;
+      if (pb < 0 || pe < 0) return mg_fail(MG_INVALID_ARGUMENT, "Conv: negative pads");
+      out = (in + pb + pe - window) / s + 1;
+    }
+    if (out < 0) return mg_fail(MG_INVALID_ARGUMENT, "Conv: kernel larger than padded input");
+    p->out[o + a] = out;
+    p->pad[o + a] = pb;
+  }
+  p->w_ms = p->cg * prod(ws, 2, wr);
+  p->w_cs = prod(ws, 2, wr);
+  p->w_gs = p->mg * p->w_ms;
+  y_shape[0] = p->n;
+  y_shape[1] = p->m;
+  for (int a = 0; a < nd; a++) y_shape[2 + a] = p->out[o + a];
+  return conv_limits("Conv", *p);
+}
+
+// ConvTranspose geometry (lib/src/onnx_nn_ops.dart:818-848, :976-995):
+// w [C, M/group, kernel...]; full = (in - 1) s + d (k - 1) + 1 + output_padding;
+// with output_shape (its last nd entries) the pads become total = full - out,
+// end = total / 2, begin = total - end; else out = full - begin - end.
+mg_status plan_conv_transpose(const int64_t *xs, int32_t xr, const int64_t *ws, int32_t wr,
+                              const int64_t *strides, const int64_t *pads, const int64_t *dil,
+                              const int64_t *out_pad, const int64_t *out_shape,
+                              int32_t out_shape_len, int32_t group, mg_conv_problem *p,
+                              int64_t *y_shape) {
+  MG_TRY(conv_common("ConvTranspose", xs, xr, ws, wr, strides, dil, group, p));
+  const int nd = xr - 2, o = kConvSlots - nd;
+  if (out_shape && out_shape_len < nd)
+    return mg_fail(MG_INVALID_ARGUMENT, "ConvTranspose: output_shape needs the spatial dims");
+  if (p->c % group != 0)
+    return mg_fail(MG_INVALID_ARGUMENT, "ConvTranspose: input channels must be a multiple of group");
+  if (ws[0] != p->c)
+    return mg_fail(MG_INVALID_ARGUMENT, "ConvTranspose: w.shape[0] must equal input channels");
+  p->cg = p->c / group;
+  p->mg = ws[1];
+  p->m = p->mg * group;
+  p->trans = 1;
+  for (int a = 0; a < nd; a++) {
+    const int64_t full =
+        (xs[2 + a] - 1) * p->str[o + a] + p->dil[o + a] * (ws[2 + a] - 1) + 1 +
+        (out_pad ? out_pad[a] : 0);
+    int64_t out, pb;
+    if (out_shape) {
+      out = out_shape[out_shape_len - nd + a];
+      const int64_t total = full - out;
+      const int64_t pe = total / 2;  // truncating, as Dart's ~/
+      pb = total - pe;
+    } else {
+      pb = pads ? pads[a] : 0;
+      out = full - pb - (pads ? pads[nd + a] : 0);
+    }
+    if (out < 0) return mg_fail(MG_INVALID_ARGUMENT, "ConvTranspose: negative output size");
+    p->out[o + a] = out;
+    p->pad[o + a] = pb;
+  }
+  // W[g * cg + c][m][r]
+  p->w_ms = prod(ws, 2, wr);
+  p->w_cs = p->mg * p->w_ms;
+  p->w_gs = p->cg * p->w_cs;
+  y_shape[0] = p->n;
+  y_shape[1] = p->m;
+  for (int a = 0; a < nd; a++) y_shape[2 + a] = p->out[o + a];
+  return conv_limits("ConvTranspose", *p);
+}
+
+int64_t conv_out_count(const mg_conv_problem &p) {
+  return p.n * p.m * p.out[0] * p.out[1] * p.out[2];
+}
+int64_t conv_x_count(const mg_conv_problem &p) { return p.n * p.c * p.in[0] * p.in[1] * p.in[2]; }
+int64_t conv_w_count(const mg_conv_problem &p) {
+  return p.m * p.cg * p.ker[0] * p.ker[1] * p.ker[2];
+}
+
+// Per-channel integer parameters: weight zero points (scalar or [M]) as
+// floats, and the requant multipliers x_scale * w_scale[m] / y_scale in
+// double (lib/src/onnx_qlinear_ops.dart:371).
+mg_status conv_int_params(const char *op, const mg_conv_problem &p, const int32_t *w_zp,
+                          int64_t w_zp_len, const float *w_scale, int64_t w_scale_len,
+                          float x_scale, float y_scale, bool requant, std::vector<float> *wz,
+                          std::vector<double> *mult) {
+  if (w_zp && w_zp_len != 1 && w_zp_len != p.m)
+    return mg_fail(MG_UNSUPPORTED,
+                   std::string(op) + ": weight zero point must be scalar or per-output-channel");
+  if (requant && (!w_scale || (w_scale_len != 1 && w_scale_len != p.m)))
+    return mg_fail(MG_UNSUPPORTED,
+                   std::string(op) + ": weight scale must be scalar or per-output-channel");
+  wz->assign((size_t)p.m, 0.f);
+  if (w_zp)
+    for (int64_t c = 0; c < p.m; c++) (*wz)[c] = (float)w_zp[w_zp_len == 1 ? 0 : c];
+  if (requant) {
+    mult->assign((size_t)p.m, 0.0);
+    for (int64_t c = 0; c < p.m; c++)
+      (*mult)[c] = (double)x_scale * (double)w_scale[w_scale_len == 1 ? 0 : c] / (double)y_scale;
+  }
+  return MG_OK;
+}
+
+// Runs p with operands already on the device; per-channel tables go into
+// the workspace at table_off (copied and waited for before the launch, so
+// the host tables may go away on return).
+mg_status conv_launch(mg_ctx *ctx, mg_conv_problem p, const std::vector<float> &wz,
+                      const std::vector<double> &mult, size_t wz_off, size_t mult_off) {
+  char *base = static_cast<char *>(ctx->ws);
+  hipStream_t st = ctx->stream;
+  if (!wz.empty()) {
+    MG_HIP(hipMemcpyAsync(base + wz_off, wz.data(), wz.size() * 4, hipMemcpyHostToDevice, st));
+    p.w_zp = reinterpret_cast<const float *>(base + wz_off);
+  }
+  if (!mult.empty()) {
+    MG_HIP(hipMemcpyAsync(base + mult_off, mult.data(), mult.size() * 8, hipMemcpyHostToDevice,
+                          st));
+    p.mult = reinterpret_cast<const double *>(base + mult_off);
+  }
+  if (!wz.empty() || !mult.empty()) MG_HIP(hipStreamSynchronize(st));
+  return mg_conv_run(ctx, p);
+}
+
+// Host-pointer call: stages x, w, bias and the tables, runs, copies y back.
+mg_status conv_host(mg_ctx *ctx, mg_conv_problem p, const void *x, size_t x_el, const void *w,
+                    size_t w_el, const void *bias, size_t bias_bytes, void *y, size_t y_el,
+                    const std::vector<float> &wz, const std::vector<double> &mult) {
+  const int64_t ny = conv_out_count(p);
+  if (ny == 0) return MG_OK;
+  const int64_t nx = conv_x_count(p), nw = conv_w_count(p);
+  if ((!x && nx) || (!w && nw) || !y) return mg_fail(MG_INVALID_ARGUMENT, "conv: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t ox = s.take((size_t)nx * x_el), ow = s.take((size_t)nw * w_el),
+               ob = s.take(bias ? bias_bytes : 0), oy = s.take((size_t)ny * y_el),
+               oz = s.take(wz.size() * 4), om = s.take(mult.size() * 8);
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  hipStream_t st = ctx->stream;
+  if (nx) MG_HIP(hipMemcpyAsync(base + ox, x, (size_t)nx * x_el, hipMemcpyHostToDevice, st));
+  if (nw) MG_HIP(hipMemcpyAsync(base + ow, w, (size_t)nw * w_el, hipMemcpyHostToDevice, st));
+  if (bias) MG_HIP(hipMemcpyAsync(base + ob, bias, bias_bytes, hipMemcpyHostToDevice, st));
+  p.x = base + ox;
+  p.w = base + ow;
+  p.bias = bias ? base + ob : nullptr;
+  p.y = base + oy;
+  MG_TRY(conv_launch(ctx, p, wz, mult, oz, om));
+  MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)ny * y_el, hipMemcpyDeviceToHost, st));
+  MG_HIP(hipStreamSynchronize(st));
+  return MG_OK;
+}
+
+// Device-pointer call: only the tables are staged.
+mg_status conv_dev(mg_ctx *ctx, mg_conv_problem p, const void *x, const void *w,
+                   const void *bias, void *y, const std::vector<float> &wz,
+                   const std::vector<double> &mult) {
+  if (conv_out_count(p) == 0) return MG_OK;
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t oz = s.take(wz.size() * 4), om = s.take(mult.size() * 8);
+  MG_TRY(mg_check_control(ctx, 0));
+  if (!wz.empty() || !mult.empty()) MG_TRY(mg_ws_reserve(ctx, s.off));
+  p.x = x;
+  p.w = w;
+  p.bias = bias;
+  p.y = y;
+  return conv_launch(ctx, p, wz, mult, oz, om);
+}
+
+void conv_int_kinds(mg_conv_problem *p, int32_t x_signed, int32_t w_signed) {
+  p->xk = x_signed ? MG_CONV_I8 : MG_CONV_U8;
+  p->wk = w_signed ? MG_CONV_I8 : MG_CONV_U8;
+}
+
+}  // namespace
+
+mg_status mg_conv_output_shape(const int64_t *x_shape, int32_t x_rank, const int64_t *w_shape,
+                               const int64_t *strides, const int64_t *pads,
+                               const int64_t *dilations, int32_t group, int32_t auto_pad,
+                               int64_t *y_shape) {
+  g_last_error.clear();
+  if (!y_shape) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_output_shape: null y_shape");
+  mg_conv_problem p;
+  return plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, auto_pad,
+                   &p, y_shape);
+}
+
+mg_status mg_conv_f32(mg_ctx *ctx, const float *x, const int64_t *x_shape, int32_t x_rank,
+                      const float *w, const int64_t *w_shape, const float *bias,
+                      const int64_t *strides, const int64_t *pads, const int64_t *dilations,
+                      int32_t group, int32_t auto_pad, float *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_f32: null context");
+  mg_conv_problem p;
+  int64_t ys[5];
+  MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, auto_pad,
+                   &p, ys));
+  return conv_host(ctx, p, x, 4, w, 4, bias, (size_t)p.m * 4, y, 4, {}, {});
+}
+
+mg_status mg_conv_f32_dev(mg_ctx *ctx, const float *x_dev, const int64_t *x_shape,
+                          int32_t x_rank, const float *w_dev, const int64_t *w_shape,
+                          const float *bias_dev, const int64_t *strides, const int64_t *pads,
+                          const int64_t *dilations, int32_t group, int32_t auto_pad,
+                          float *y_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_f32_dev: null context");
+  mg_conv_problem p;
+  int64_t ys[5];
+  MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, auto_pad,
+                   &p, ys));
+  return conv_dev(ctx, p, x_dev, w_dev, bias_dev, y_dev, {}, {});
+}
+
+mg_status mg_conv_transpose_output_shape(const int64_t *x_shape, int32_t x_rank,
+                                         const int64_t *w_shape, const int64_t *strides,
+                                         const int64_t *pads, const int64_t *dilations,
+                                         const int64_t *output_padding,
+                                         const int64_t *output_shape, int32_t output_shape_len,
+                                         int32_t group, int64_t *y_shape) {
+  g_last_error.clear();
+  if (!y_shape) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_transpose_output_shape: null y_shape");
+  mg_conv_problem p;
+  return plan_conv_transpose(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations,
+                             output_padding, output_shape, output_shape_len, group, &p, y_shape);
+}
+
+mg_status mg_conv_transpose_f32(mg_ctx *ctx, const float *x, const int64_t *x_shape,
+                                int32_t x_rank, const float *w, const int64_t *w_shape,
+                                const float *bias, const int64_t *strides, const int64_t *pads,
+                                const int64_t *dilations, const int64_t *output_padding,
+                                const int64_t *output_shape, int32_t output_shape_len,
+                                int32_t group, float *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_transpose_f32: null context");
+  mg_conv_problem p;
+  int64_t ys[5];
+  MG_TRY(plan_conv_transpose(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations,
+                             output_padding, output_shape, output_shape_len, group, &p, ys));
+  return conv_host(ctx, p, x, 4, w, 4, bias, (size_t)p.m * 4, y, 4, {}, {});
+}
+
+mg_status mg_conv_transpose_f32_dev(mg_ctx *ctx, const float *x_dev, const int64_t *x_shape,
+                                    int32_t x_rank, const float *w_dev, const int64_t *w_shape,
+                                    const float *bias_dev, const int64_t *strides,
+                                    const int64_t *pads, const int64_t *dilations,
+                                    const int64_t *output_padding, const int64_t *output_shape,
+                                    int32_t output_shape_len, int32_t group, float *y_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_transpose_f32_dev: null context");
+  mg_conv_problem p;
+  int64_t ys[5];
+  MG_TRY(plan_conv_transpose(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations,
+                             output_padding, output_shape, output_shape_len, group, &p, ys));
+  return conv_dev(ctx, p, x_dev, w_dev, bias_dev, y_dev, {}, {});
+}
+
+mg_status mg_conv_integer(mg_ctx *ctx, const void *x, int32_t x_signed, const int64_t *x_shape,
+                          int32_t x_rank, const void *w, int32_t w_signed,
+                          const int64_t *w_shape, int32_t x_zp, const int32_t *w_zp,
+                          int64_t w_zp_len, const int64_t *strides, const int64_t *pads,
+                          const int64_t *dilations, int32_t group, int32_t *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_integer: null context");
+  mg_conv_problem p;
+  int64_t ys[5];
+  MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, 0, &p, ys));
+  conv_int_kinds(&p, x_signed, w_signed);
+  p.mode = MG_CONV_OUT_I32;
+  p.x_zp = x_zp;
+  std::vector<float> wz;
+  std::vector<double> mult;
+  MG_TRY(conv_int_params("ConvInteger", p, w_zp, w_zp_len, nullptr, 0, 0.f, 1.f, false, &wz,
+                         &mult));
+  return conv_host(ctx, p, x, 1, w, 1, nullptr, 0, y, 4, wz, mult);
+}
+
+mg_status mg_conv_integer_dev(mg_ctx *ctx, const void *x_dev, int32_t x_signed,
+                              const int64_t *x_shape, int32_t x_rank, const void *w_dev,
+                              int32_t w_signed, const int64_t *w_shape, int32_t x_zp,
+                              const int32_t *w_zp, int64_t w_zp_len, const int64_t *strides,
+                              const int64_t *pads, const int64_t *dilations, int32_t group,
+                              int32_t *y_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_integer_dev: null context");
+  mg_conv_problem p;
+  int64_t ys[5];
+  MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, 0, &p, ys));
+  conv_int_kinds(&p, x_signed, w_signed);
+  p.mode = MG_CONV_OUT_I32;
+  p.x_zp = x_zp;
+  std::vector<float> wz;
+  std::vector<double> mult;
+  MG_TRY(conv_int_params("ConvInteger", p, w_zp, w_zp_len, nullptr, 0, 0.f, 1.f, false, &wz,
+                         &mult));
+  return conv_dev(ctx, p, x_dev, w_dev, nullptr, y_dev, wz, mult);
+}
+
+mg_status mg_qlinear_conv(mg_ctx *ctx, const void *x, int32_t x_signed, const int64_t *x_shape,
+                          int32_t x_rank, float x_scale, int32_t x_zp, const void *w,
+                          int32_t w_signed, const int64_t *w_shape, const float *w_scale,
+                          int64_t w_scale_len, const int32_t *w_zp, int64_t w_zp_len,
+                          float y_scale, int32_t y_zp, const int32_t *bias,
+                          const int64_t *strides, const int64_t *pads, const int64_t *dilations,
+                          int32_t group, int32_t lo, int32_t hi, uint8_t *y) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_conv: null context");
+  if (lo > hi) return mg_fail(MG_INVALID_ARGUMENT, "QLinearConv: lo > hi");
+  mg_conv_problem p;
+  int64_t ys[5];
+  MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, 0, &p, ys));
+  conv_int_kinds(&p, x_signed, w_signed);
+  p.mode = MG_CONV_OUT_Q8;
+  p.x_zp = x_zp;
+  p.y_zp = y_zp;
+  p.lo = lo;
+  p.hi = hi;
+  std::vector<float> wz;
+  std::vector<double> mult;
+  MG_TRY(conv_int_params("QLinearConv", p, w_zp, w_zp_len, w_scale, w_scale_len, x_scale,
+                         y_scale, true, &wz, &mult));
+  return conv_host(ctx, p, x, 1, w, 1, bias, (size_t)p.m * 4, y, 1, wz, mult);
+}
+
+mg_status mg_qlinear_conv_dev(mg_ctx *ctx, const void *x_dev, int32_t x_signed,
+                              const int64_t *x_shape, int32_t x_rank, float x_scale,
+                              int32_t x_zp, const void *w_dev, int32_t w_signed,
+                              const int64_t *w_shape, const float *w_scale, int64_t w_scale_len,
+                              const int32_t *w_zp, int64_t w_zp_len, float y_scale,
+                              int32_t y_zp, const int32_t *bias_dev, const int64_t *strides,
+                              const int64_t *pads, const int64_t *dilations, int32_t group,
+                              int32_t lo, int32_t hi, uint8_t *y_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_conv_dev: null context");
+  if (lo > hi) return mg_fail(MG_INVALID_ARGUMENT, "QLinearConv: lo > hi");
+  mg_conv_problem p;
+  int64_t ys[5];
+  MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, 0, &p, ys));
+  conv_int_kinds(&p, x_signed, w_signed);
+  p.mode = MG_CONV_OUT_Q8;
+  p.x_zp = x_zp;
+  p.y_zp = y_zp;
+  p.lo = lo;
+  p.hi = hi;
+  std::vector<float> wz;
+  std::vector<double> mult;
+  MG_TRY(conv_int_params("QLinearConv", p, w_zp, w_zp_len, w_scale, w_scale_len, x_scale,
+                         y_scale, true, &wz, &mult));
+  return conv_dev(ctx, p, x_dev, w_dev, bias_dev, y_dev, wz, mult);
+}

@@ -173,6 +173,38 @@ struct mg_f32_problem {
 mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
                      const float *b_dev, float *y_dev);
 
+// --------------------------------------------------------------- conv entry
+
+// Convolution as an implicit GEMM per (batch, group): rows = output channels
+// of the group, columns = output positions, k = (input channel, kernel tap).
+// Spatial dims are padded to 3 (depth, height, width) with size-1 leading
+// dims.  Conv reads input position i = o * str - pad + kk * dil; the
+// transposed form (ConvTranspose) reads i = (o + pad - kk * dil) / str where
+// that division is exact.  Element kinds: MG_CONV_F32, MG_CONV_U8,
+// MG_CONV_I8.  Integer kinds use (x - x_zp) and (w - w_zp[channel]); taps in
+// the padding contribute 0.
+enum { MG_CONV_F32 = 0, MG_CONV_U8 = 1, MG_CONV_I8 = 2 };
+// Output modes: fp32 (+ fp32 bias), int32 accumulators, requantised bytes.
+enum { MG_CONV_OUT_F32 = 0, MG_CONV_OUT_I32 = 1, MG_CONV_OUT_Q8 = 2 };
+struct mg_conv_problem {
+  const void *x = nullptr, *w = nullptr;
+  const void *bias = nullptr;  // f32 [M] (fp32 mode) or int32 [M] (requant mode), or null
+  void *y = nullptr;
+  int xk = MG_CONV_F32, wk = MG_CONV_F32, mode = MG_CONV_OUT_F32, trans = 0;
+  int64_t n = 0, c = 0, m = 0;  // batch, input channels, output channels
+  int64_t group = 1, cg = 0, mg = 0;
+  int64_t in[3] = {1, 1, 1}, out[3] = {1, 1, 1}, ker[3] = {1, 1, 1};
+  int64_t str[3] = {1, 1, 1}, dil[3] = {1, 1, 1}, pad[3] = {0, 0, 0};  // begin pads
+  // Weight element (group g, out channel m of the group, in channel c of the
+  // group, tap r) sits at g * w_gs + m * w_ms + c * w_cs + r.
+  int64_t w_gs = 0, w_ms = 0, w_cs = 0;
+  int32_t x_zp = 0;
+  const float *w_zp = nullptr;   // device [M] (integer kinds)
+  const double *mult = nullptr;  // device [M] requant multipliers
+  int32_t y_zp = 0, lo = 0, hi = 255;
+};
+mg_status mg_conv_run(mg_ctx *ctx, const mg_conv_problem &p);
+
 // ---------------------------------------------------------- attention entry
 
 // y[b][q][:DV] = softmax_t(scale * sum_d Q[b][q][d] K[b][t][d] + mask[b][q][t])

@@ -11,6 +11,10 @@ defaults and error classes as the reference:
     op_gemm                <- opGemm          lib/src/onnx_ops.dart:2152
     op_fused_sdpa          <- opFusedSDPA     lib/src/onnx_ops.dart:2106
     op_multi_head_attention <- opMultiHeadAttention lib/src/onnx_ops.dart:2019
+    op_conv                <- opConv          lib/src/onnx_nn_ops.dart:179
+    op_conv_transpose      <- opConvTranspose lib/src/onnx_nn_ops.dart:818
+    op_conv_integer        <- opConvInteger   lib/src/onnx_qlinear_ops.dart:299
+    op_qlinear_conv        <- opQLinearConv   lib/src/onnx_qlinear_ops.dart:339
 
 Tensors are numpy arrays on the host; every op runs on the GPU through the
 C ABI (there is no CPU path).  Weight handles (NBitsWeight, Int8Weight,
@@ -26,7 +30,7 @@ import numpy as np
 
 from . import _lib
 from ._lib import check, lib
-from .errors import ArgumentError, UnsupportedError
+from .errors import ArgumentError, StateError, UnsupportedError
 
 MG_ZP_NONE, MG_ZP_UINT4, MG_ZP_FLOAT = 0, 1, 2
 
@@ -547,6 +551,223 @@ def multi_head_attention_dev(q_ptr: int, k_ptr: int, v_ptr: int, batch: int, seq
                                           int(bias_heads), int(scale is not None),
                                           float(scale if scale is not None else 0.0),
                                           C.c_void_p(y_ptr)))
+
+
+# ------------------------------------------------------------ convolution
+
+_AUTO_PAD = {"NOTSET": 0, "SAME_UPPER": 1, "SAME_LOWER": 2, "VALID": 3}
+
+
+def _i64(v):
+    return None if v is None else np.ascontiguousarray(np.array(list(v), dtype=np.int64))
+
+
+def _check_ranks(op: str, x, w):
+    """x and w of one rank, 3 to 5 (lib/src/onnx_nn_ops.dart:196-201); the C
+    ABI takes that one rank for both."""
+    if x.ndim != w.ndim or not 3 <= x.ndim <= 5:
+        raise ArgumentError(f"{op}: x and w must have the same rank, 3 to 5")
+
+
+def _check_kernel_shape(op: str, kernel_shape, w):
+    """The dispatcher's kernel_shape check (lib/src/onnx_graph.dart:2438-2445)."""
+    if kernel_shape is not None and list(kernel_shape) != list(w.shape[2:]):
+        raise StateError(f"{op} kernel_shape {list(kernel_shape)} does not match weight "
+                         f"shape {list(w.shape[2:])}.")
+
+
+def conv_output_shape(x_shape, w_shape, *, strides=None, pads=None, dilations=None, group=1,
+                      auto_pad="NOTSET") -> tuple:
+    """Output shape of a Conv (pads resolved as lib/src/onnx_nn_ops.dart:38-87)."""
+    xs, ws = _i64(x_shape), _i64(w_shape)
+    if auto_pad not in _AUTO_PAD:
+        raise ArgumentError(f"Conv: unknown auto_pad {auto_pad}")
+    y = np.zeros(max(xs.size, 1), np.int64)
+    st, pd, dl = _i64(strides), _i64(pads), _i64(dilations)
+    check(lib.mg_conv_output_shape(_ptr(xs), xs.size, _ptr(ws), _ptr(st), _ptr(pd), _ptr(dl),
+                                   int(group), _AUTO_PAD[auto_pad], _ptr(y)))
+    return tuple(int(v) for v in y)
+
+
+def op_conv(x, w, bias=None, *, strides=None, pads=None, dilations=None, group: int = 1,
+            auto_pad: str = "NOTSET", kernel_shape=None, ctx: Context | None = None):
+    """opConv (lib/src/onnx_nn_ops.dart:179-817): x [N, C, *spatial] (1 to 3
+    spatial dims), w [M, C / group, *kernel], bias [M] or None."""
+    x, w = (np.ascontiguousarray(a, dtype=np.float32) for a in (x, w))
+    _check_ranks("Conv", x, w)
+    _check_kernel_shape("Conv", kernel_shape, w)
+    ys = conv_output_shape(x.shape, w.shape, strides=strides, pads=pads, dilations=dilations,
+                           group=group, auto_pad=auto_pad)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    if b is not None and b.size != w.shape[0]:
+        raise ArgumentError("Conv: bias must have one value per output channel")
+    y = np.empty(ys, np.float32)
+    st, pd, dl = _i64(strides), _i64(pads), _i64(dilations)
+    ctx = ctx or default_context()
+    check(lib.mg_conv_f32(ctx.handle, _ptr(x), _ptr(_shape_arr(x)), x.ndim, _ptr(w),
+                          _ptr(_shape_arr(w)), _ptr(b), _ptr(st), _ptr(pd), _ptr(dl), int(group),
+                          _AUTO_PAD[auto_pad], _ptr(y)))
+    return y
+
+
+def conv_transpose_output_shape(x_shape, w_shape, *, strides=None, pads=None, dilations=None,
+                                output_padding=None, output_shape=None, group=1) -> tuple:
+    """Output shape of a ConvTranspose (lib/src/onnx_nn_ops.dart:976-995)."""
+    xs, ws = _i64(x_shape), _i64(w_shape)
+    y = np.zeros(max(xs.size, 1), np.int64)
+    os_ = _i64(output_shape)
+    check(lib.mg_conv_transpose_output_shape(
+        _ptr(xs), xs.size, _ptr(ws), _ptr(_i64(strides)), _ptr(_i64(pads)),
+        _ptr(_i64(dilations)), _ptr(_i64(output_padding)), _ptr(os_),
+        0 if os_ is None else os_.size, int(group), _ptr(y)))
+    return tuple(int(v) for v in y)
+
+
+def op_conv_transpose(x, w, bias=None, *, strides=None, pads=None, dilations=None,
+                      output_padding=None, output_shape=None, group: int = 1,
+                      kernel_shape=None, ctx: Context | None = None):
+    """opConvTranspose (lib/src/onnx_nn_ops.dart:818-1059): w [C, M / group,
+    *kernel]; output_shape (spatial dims, or the full shape) sets the pads."""
+    x, w = (np.ascontiguousarray(a, dtype=np.float32) for a in (x, w))
+    _check_ranks("ConvTranspose", x, w)
+    _check_kernel_shape("ConvTranspose", kernel_shape, w)
+    ys = conv_transpose_output_shape(x.shape, w.shape, strides=strides, pads=pads,
+                                     dilations=dilations, output_padding=output_padding,
+                                     output_shape=output_shape, group=group)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    if b is not None and b.size != ys[1]:
+        raise ArgumentError("ConvTranspose: bias must have one value per output channel")
+    y = np.empty(ys, np.float32)
+    os_ = _i64(output_shape)
+    ctx = ctx or default_context()
+    check(lib.mg_conv_transpose_f32(
+        ctx.handle, _ptr(x), _ptr(_shape_arr(x)), x.ndim, _ptr(w), _ptr(_shape_arr(w)), _ptr(b),
+        _ptr(_i64(strides)), _ptr(_i64(pads)), _ptr(_i64(dilations)),
+        _ptr(_i64(output_padding)), _ptr(os_), 0 if os_ is None else os_.size, int(group),
+        _ptr(y)))
+    return y
+
+
+def _int_operand(a, what: str):
+    a = np.ascontiguousarray(a)
+    if a.dtype not in (np.uint8, np.int8):
+        raise ArgumentError(f"{what} must be uint8 or int8")
+    return a, int(a.dtype == np.int8)
+
+
+def _zp_list(z):
+    if z is None:
+        return None, 0
+    z = np.ascontiguousarray(np.asarray(z).astype(np.int32).ravel())
+    return z, z.size
+
+
+def _scalar_int(z) -> int:
+    return 0 if z is None else int(np.asarray(z).ravel()[0])
+
+
+def op_conv_integer(x, w, x_zero_point=None, w_zero_point=None, *, strides=None, pads=None,
+                    dilations=None, group: int = 1, ctx: Context | None = None):
+    """opConvInteger (lib/src/onnx_qlinear_ops.dart:299-337): exact
+    sum (x - x_zp)(w - w_zp[m]); returns int64 like the reference's
+    Tensor.int64 (the library computes int32)."""
+    x, xs = _int_operand(x, "ConvInteger: x")
+    w, wsg = _int_operand(w, "ConvInteger: w")
+    _check_ranks("ConvInteger", x, w)
+    wz, nwz = _zp_list(w_zero_point)
+    ys = conv_output_shape(x.shape, w.shape, strides=strides, pads=pads, dilations=dilations,
+                           group=group)
+    y = np.empty(ys, np.int32)
+    ctx = ctx or default_context()
+    check(lib.mg_conv_integer(ctx.handle, _ptr(x), xs, _ptr(_shape_arr(x)), x.ndim, _ptr(w), wsg,
+                              _ptr(_shape_arr(w)), _scalar_int(x_zero_point), _ptr(wz), nwz,
+                              _ptr(_i64(strides)), _ptr(_i64(pads)), _ptr(_i64(dilations)),
+                              int(group), _ptr(y)))
+    return y.astype(np.int64)
+
+
+def op_qlinear_conv(x, x_scale, x_zero_point, w, w_scale, w_zero_point, y_scale, y_zero_point,
+                    bias=None, *, strides=None, pads=None, dilations=None, group: int = 1,
+                    lo: int, hi: int, ctx: Context | None = None):
+    """opQLinearConv (lib/src/onnx_qlinear_ops.dart:339-382); lo / hi are
+    [-128, 127] when the y_zero_point initializer is int8, else [0, 255]
+    (lib/src/onnx_graph.dart:2936,2952-2953).  Returns int64 values."""
+    x, xs = _int_operand(x, "QLinearConv: x")
+    w, wsg = _int_operand(w, "QLinearConv: w")
+    _check_ranks("QLinearConv", x, w)
+    wz, nwz = _zp_list(w_zero_point)
+    wsc = np.ascontiguousarray(np.asarray(w_scale, dtype=np.float32).ravel())
+    b = None if bias is None else np.ascontiguousarray(np.asarray(bias).astype(np.int32).ravel())
+    ys = conv_output_shape(x.shape, w.shape, strides=strides, pads=pads, dilations=dilations,
+                           group=group)
+    y = np.empty(ys, np.uint8)
+    ctx = ctx or default_context()
+    check(lib.mg_qlinear_conv(
+        ctx.handle, _ptr(x), xs, _ptr(_shape_arr(x)), x.ndim,
+        float(np.asarray(x_scale, np.float32).ravel()[0]), _scalar_int(x_zero_point), _ptr(w),
+        wsg, _ptr(_shape_arr(w)), _ptr(wsc), wsc.size, _ptr(wz), nwz,
+        float(np.asarray(y_scale, np.float32).ravel()[0]), _scalar_int(y_zero_point), _ptr(b),
+        _ptr(_i64(strides)), _ptr(_i64(pads)), _ptr(_i64(dilations)), int(group), int(lo),
+        int(hi), _ptr(y)))
+    return (y.view(np.int8) if lo < 0 else y).astype(np.int64)
+
+
+def conv_f32_dev(x_ptr: int, x_shape, w_ptr: int, w_shape, y_ptr: int, bias_ptr: int = 0, *,
+                 strides=None, pads=None, dilations=None, group: int = 1,
+                 auto_pad: str = "NOTSET", ctx: Context | None = None):
+    """op_conv on device buffers (asynchronous on the context's stream)."""
+    ctx = ctx or default_context()
+    xs, ws = _i64(x_shape), _i64(w_shape)
+    check(lib.mg_conv_f32_dev(ctx.handle, C.c_void_p(x_ptr), _ptr(xs), xs.size,
+                              C.c_void_p(w_ptr), _ptr(ws), C.c_void_p(bias_ptr) if bias_ptr else None,
+                              _ptr(_i64(strides)), _ptr(_i64(pads)), _ptr(_i64(dilations)),
+                              int(group), _AUTO_PAD[auto_pad], C.c_void_p(y_ptr)))
+
+
+def conv_transpose_f32_dev(x_ptr: int, x_shape, w_ptr: int, w_shape, y_ptr: int,
+                           bias_ptr: int = 0, *, strides=None, pads=None, dilations=None,
+                           output_padding=None, output_shape=None, group: int = 1,
+                           ctx: Context | None = None):
+    """op_conv_transpose on device buffers."""
+    ctx = ctx or default_context()
+    xs, ws, os_ = _i64(x_shape), _i64(w_shape), _i64(output_shape)
+    check(lib.mg_conv_transpose_f32_dev(
+        ctx.handle, C.c_void_p(x_ptr), _ptr(xs), xs.size, C.c_void_p(w_ptr), _ptr(ws),
+        C.c_void_p(bias_ptr) if bias_ptr else None, _ptr(_i64(strides)), _ptr(_i64(pads)),
+        _ptr(_i64(dilations)), _ptr(_i64(output_padding)), _ptr(os_),
+        0 if os_ is None else os_.size, int(group), C.c_void_p(y_ptr)))
+
+
+def conv_integer_dev(x_ptr: int, x_signed: bool, x_shape, w_ptr: int, w_signed: bool, w_shape,
+                     y_ptr: int, x_zero_point: int = 0, w_zero_point=None, *, strides=None,
+                     pads=None, dilations=None, group: int = 1, ctx: Context | None = None):
+    """op_conv_integer on device buffers; y is int32."""
+    ctx = ctx or default_context()
+    xs, ws = _i64(x_shape), _i64(w_shape)
+    wz, nwz = _zp_list(w_zero_point)
+    check(lib.mg_conv_integer_dev(ctx.handle, C.c_void_p(x_ptr), int(x_signed), _ptr(xs),
+                                  xs.size, C.c_void_p(w_ptr), int(w_signed), _ptr(ws),
+                                  int(x_zero_point), _ptr(wz), nwz, _ptr(_i64(strides)),
+                                  _ptr(_i64(pads)), _ptr(_i64(dilations)), int(group),
+                                  C.c_void_p(y_ptr)))
+
+
+def qlinear_conv_dev(x_ptr: int, x_signed: bool, x_shape, x_scale: float, x_zero_point: int,
+                     w_ptr: int, w_signed: bool, w_shape, w_scale, w_zero_point,
+                     y_scale: float, y_zero_point: int, y_ptr: int, bias_ptr: int = 0, *,
+                     strides=None, pads=None, dilations=None, group: int = 1, lo: int, hi: int,
+                     ctx: Context | None = None):
+    """op_qlinear_conv on device buffers; y is bytes."""
+    ctx = ctx or default_context()
+    xs, ws = _i64(x_shape), _i64(w_shape)
+    wz, nwz = _zp_list(w_zero_point)
+    wsc = np.ascontiguousarray(np.asarray(w_scale, dtype=np.float32).ravel())
+    check(lib.mg_qlinear_conv_dev(
+        ctx.handle, C.c_void_p(x_ptr), int(x_signed), _ptr(xs), xs.size, float(x_scale),
+        int(x_zero_point), C.c_void_p(w_ptr), int(w_signed), _ptr(ws), _ptr(wsc), wsc.size,
+        _ptr(wz), nwz, float(y_scale), int(y_zero_point),
+        C.c_void_p(bias_ptr) if bias_ptr else None, _ptr(_i64(strides)), _ptr(_i64(pads)),
+        _ptr(_i64(dilations)), int(group), int(lo), int(hi), C.c_void_p(y_ptr)))
 
 
 def library_path() -> str:

@@ -16,6 +16,10 @@ Thin numpy wrappers over ``oracle/lib/liboracle.so`` (built from oracle.c by
 * ``matmul_kernel``        — lib/src/gemm_kernel_simd.dart:32-239
 * ``fused_sdpa``           — lib/src/onnx_ops.dart:2106-2149
 * ``multi_head_attention`` — lib/src/onnx_ops.dart:2019-2098
+* ``conv``                 — lib/src/onnx_nn_ops.dart:179-817 (+ _resolvePads :38-87)
+* ``conv_transpose``       — lib/src/onnx_nn_ops.dart:818-1059
+* ``conv_integer``         — lib/src/onnx_qlinear_ops.dart:232-337
+* ``qlinear_conv``         — lib/src/onnx_qlinear_ops.dart:339-382
 """
 from __future__ import annotations
 
@@ -82,6 +86,8 @@ def _declare(L):
                                  _P]
     L.orc_multi_head_attention.argtypes = [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64,
                                            _I, C.c_double, _P]
+    L.orc_conv.argtypes = [_P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I,
+                           C.c_int32, _P, _P]
     L.orc_round_even.argtypes = [C.c_double, _P]
     L.orc_round_even.restype = _I64
 
@@ -278,4 +284,150 @@ def multi_head_attention(q, k, v, bias=None, *, num_heads: int, scale=None) -> n
                                           num_heads, _ptr(bias), bh, int(scale is not None),
                                           float(scale or 0.0), _ptr(out)),
            "multi_head_attention")
+    return out
+
+
+# ------------------------------------------------------------------ conv
+
+def resolve_pads(in_dims, kernel, strides, dilations, auto_pad="NOTSET", pads=None):
+    """_resolvePads (lib/src/onnx_nn_ops.dart:38-87, ceil_mode off): begin /
+    end pads and output dims per spatial axis.  Integer division truncates
+    towards zero, as Dart's ``~/``."""
+    nd = len(in_dims)
+    p = [0] * (2 * nd)
+    out = [0] * nd
+    for k in range(nd):
+        window = dilations[k] * (kernel[k] - 1) + 1
+        if auto_pad in ("SAME_UPPER", "SAME_LOWER"):
+            out[k] = -(-in_dims[k] // strides[k])
+            total = max(0, (out[k] - 1) * strides[k] + window - in_dims[k])
+            small = total // 2
+            p[k] = small if auto_pad == "SAME_UPPER" else total - small
+            p[nd + k] = total - p[k]
+        elif auto_pad == "VALID":
+            out[k] = int((in_dims[k] - window) / strides[k]) + 1
+        else:
+            p[k] = 0 if pads is None else pads[k]
+            p[nd + k] = 0 if pads is None else pads[nd + k]
+            out[k] = int((in_dims[k] + p[k] + p[nd + k] - window) / strides[k]) + 1
+    return p, out
+
+
+def _conv_sums(x, x_kind, w, w_kind, n, c, m, group, in_sp, ker, out, st, dl, pb, trans,
+               x_zp=0, w_zp=None):
+    nd = len(in_sp)
+    pad3 = lambda v, fill: [fill] * (3 - nd) + list(v)  # noqa: E731
+    arr = lambda v: np.ascontiguousarray(np.array(v, dtype=np.int64))  # noqa: E731
+    acc = np.zeros((n, m) + tuple(out), dtype=np.float64)
+    wz = None if w_zp is None else np.ascontiguousarray(np.asarray(w_zp, np.int32))
+    _check(lib().orc_conv(_ptr(x), x_kind, _ptr(w), w_kind, n, c, m, group,
+                          _ptr(arr(pad3(in_sp, 1))), _ptr(arr(pad3(ker, 1))),
+                          _ptr(arr(pad3(out, 1))), _ptr(arr(pad3(st, 1))),
+                          _ptr(arr(pad3(dl, 1))), _ptr(arr(pad3(pb, 0))), int(trans),
+                          int(x_zp), _ptr(wz), _ptr(acc)), "orc_conv")
+    return acc
+
+
+def conv(x, w, bias=None, *, strides=None, pads=None, dilations=None, group=1,
+         auto_pad="NOTSET") -> np.ndarray:
+    """opConv: sums in double, bias added, one rounding to f32."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    nd = x.ndim - 2
+    st = list(strides) if strides is not None else [1] * nd
+    dl = list(dilations) if dilations is not None else [1] * nd
+    p, out = resolve_pads(list(x.shape[2:]), list(w.shape[2:]), st, dl, auto_pad, pads)
+    acc = _conv_sums(x, 0, w, 0, x.shape[0], x.shape[1], w.shape[0], group, list(x.shape[2:]),
+                     list(w.shape[2:]), out, st, dl, p[:nd], 0)
+    if bias is not None:
+        acc += np.asarray(bias, np.float64).reshape((1, -1) + (1,) * nd)
+    return acc.astype(np.float32)
+
+
+def conv_transpose_dims(in_sp, kernel, strides, dilations, output_padding=None,
+                        output_shape=None, pads=None):
+    """Output dims and begin pads of opConvTranspose
+    (lib/src/onnx_nn_ops.dart:976-995)."""
+    nd = len(in_sp)
+    op = list(output_padding) if output_padding is not None else [0] * nd
+    p = list(pads) if pads is not None else [0] * (2 * nd)
+    out = [0] * nd
+    for k in range(nd):
+        full = (in_sp[k] - 1) * strides[k] + dilations[k] * (kernel[k] - 1) + 1 + op[k]
+        if output_shape is not None:
+            out[k] = output_shape[len(output_shape) - nd + k]
+            total = full - out[k]
+            p[nd + k] = int(total / 2)
+            p[k] = total - p[nd + k]
+        else:
+            out[k] = full - p[k] - p[nd + k]
+    return p[:nd], out
+
+
+def conv_transpose(x, w, bias=None, *, strides=None, pads=None, dilations=None,
+                   output_padding=None, output_shape=None, group=1) -> np.ndarray:
+    """opConvTranspose: scatter sums in double, bias added, one rounding."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    nd = x.ndim - 2
+    st = list(strides) if strides is not None else [1] * nd
+    dl = list(dilations) if dilations is not None else [1] * nd
+    pb, out = conv_transpose_dims(list(x.shape[2:]), list(w.shape[2:]), st, dl, output_padding,
+                                  output_shape, pads)
+    m = w.shape[1] * group
+    acc = _conv_sums(x, 0, w, 0, x.shape[0], x.shape[1], m, group, list(x.shape[2:]),
+                     list(w.shape[2:]), out, st, dl, pb, 1)
+    if bias is not None:
+        acc += np.asarray(bias, np.float64).reshape((1, -1) + (1,) * nd)
+    return acc.astype(np.float32)
+
+
+def _kind(a):
+    return {np.dtype(np.float32): 0, np.dtype(np.uint8): 1, np.dtype(np.int8): 2}[a.dtype]
+
+
+def _wz_list(w_zp, m):
+    if w_zp is None:
+        return [0] * m
+    z = np.asarray(w_zp).astype(np.int64).ravel()
+    if z.size not in (1, m):
+        raise OracleError(UNSUPPORTED, "weight zero point must be scalar or per-channel")
+    return [int(z[0 if z.size == 1 else i]) for i in range(m)]
+
+
+def conv_integer(x, w, x_zp=None, w_zp=None, *, strides=None, pads=None, dilations=None,
+                 group=1) -> np.ndarray:
+    """opConvInteger: exact sum (x - x_zp)(w - w_zp[m]) as int64."""
+    x, w = np.ascontiguousarray(x), np.ascontiguousarray(w)
+    nd = x.ndim - 2
+    st = list(strides) if strides is not None else [1] * nd
+    dl = list(dilations) if dilations is not None else [1] * nd
+    p = list(pads) if pads is not None else [0] * (2 * nd)
+    _, out = resolve_pads(list(x.shape[2:]), list(w.shape[2:]), st, dl, "NOTSET", p)
+    xz = 0 if x_zp is None else int(np.asarray(x_zp).ravel()[0])
+    acc = _conv_sums(x, _kind(x), w, _kind(w), x.shape[0], x.shape[1], w.shape[0], group,
+                     list(x.shape[2:]), list(w.shape[2:]), out, st, dl, p[:nd], 0, xz,
+                     _wz_list(w_zp, w.shape[0]))
+    return acc.astype(np.int64)
+
+
+def qlinear_conv(x, x_scale, x_zp, w, w_scale, w_zp, y_scale, y_zp, bias=None, *,
+                 strides=None, pads=None, dilations=None, group=1, lo, hi) -> np.ndarray:
+    """opQLinearConv: q = roundHalfEven((acc + bias[m]) * mult[m]) + y_zp,
+    clamped; mult = x_scale * w_scale[m] / y_scale in double (the f32 scales
+    widened, as Tensor.getD does)."""
+    acc = conv_integer(x, w, x_zp, w_zp, strides=strides, pads=pads, dilations=dilations,
+                       group=group)
+    m = acc.shape[1]
+    ws = np.asarray(w_scale, np.float32).ravel()
+    xs = float(np.asarray(x_scale, np.float32).ravel()[0])
+    ys = float(np.asarray(y_scale, np.float32).ravel()[0])
+    yz = 0 if y_zp is None else int(np.asarray(y_zp).ravel()[0])
+    bi = None if bias is None else np.asarray(bias).astype(np.int64).ravel()
+    out = np.empty_like(acc)
+    for om in range(m):
+        mult = xs * float(ws[0 if ws.size == 1 else om]) / ys
+        s = acc[:, om] + (0 if bi is None else int(bi[om]))
+        q = np.rint(s.astype(np.float64) * mult).astype(np.int64) + yz
+        out[:, om] = np.clip(q, lo, hi)
     return out

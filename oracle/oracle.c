@@ -518,3 +518,88 @@ int orc_multi_head_attention(const float *q, const float *k, const float *v,
   free(qh); free(kt); free(vh); free(sc); free(cx);
   return ORC_OK;
 }
+
+/* ------------------------------------------------------------ convolution */
+
+static double conv_elem(const void *p, int kind, int64_t i) {
+  if (kind == 1) return (double)((const uint8_t *)p)[i];
+  if (kind == 2) return (double)((const int8_t *)p)[i];
+  return (double)((const float *)p)[i];
+}
+
+int orc_conv(const void *x, int x_kind, const void *w, int w_kind, int64_t n, int64_t c,
+             int64_t m, int64_t group, const int64_t *in, const int64_t *ker,
+             const int64_t *out, const int64_t *str, const int64_t *dil,
+             const int64_t *pad, int trans, int32_t x_zp, const int32_t *w_zp,
+             double *acc) {
+  if (group < 1 || c % group || m % group) return ORC_INVALID_ARGUMENT;
+  const int64_t cg = c / group, mg = m / group;
+  const int64_t in_sp = in[0] * in[1] * in[2], out_sp = out[0] * out[1] * out[2];
+  const int64_t taps = ker[0] * ker[1] * ker[2];
+  const double xz = x_kind ? (double)x_zp : 0.0;
+  for (int64_t i = 0; i < n * m * out_sp; i++) acc[i] = 0.0;
+  if (!trans) {
+    /* Gather per output element (_convIntAcc order: c, ky, kx). */
+    for (int64_t b = 0; b < n; b++)
+      for (int64_t om = 0; om < m; om++) {
+        const int64_t g = om / mg;
+        const double wz = (w_kind && w_zp) ? (double)w_zp[om] : 0.0;
+        for (int64_t oz = 0; oz < out[0]; oz++)
+          for (int64_t oy = 0; oy < out[1]; oy++)
+            for (int64_t ox = 0; ox < out[2]; ox++) {
+              double s = 0.0;
+              for (int64_t cc = 0; cc < cg; cc++) {
+                const int64_t xb = (b * c + g * cg + cc) * in_sp;
+                const int64_t wb = (om * cg + cc) * taps;
+                for (int64_t kz = 0; kz < ker[0]; kz++) {
+                  const int64_t iz = oz * str[0] - pad[0] + kz * dil[0];
+                  if (iz < 0 || iz >= in[0]) continue;
+                  for (int64_t ky = 0; ky < ker[1]; ky++) {
+                    const int64_t iy = oy * str[1] - pad[1] + ky * dil[1];
+                    if (iy < 0 || iy >= in[1]) continue;
+                    for (int64_t kx = 0; kx < ker[2]; kx++) {
+                      const int64_t ix = ox * str[2] - pad[2] + kx * dil[2];
+                      if (ix < 0 || ix >= in[2]) continue;
+                      const double xv = conv_elem(x, x_kind, xb + (iz * in[1] + iy) * in[2] + ix) - xz;
+                      const double wv = conv_elem(w, w_kind, wb + (kz * ker[1] + ky) * ker[2] + kx) - wz;
+                      s += xv * wv;
+                    }
+                  }
+                }
+              }
+              acc[((b * m + om) * out[0] + oz) * out[1] * out[2] + oy * out[2] + ox] = s;
+            }
+      }
+    return ORC_OK;
+  }
+  /* Scatter per input element (opConvTranspose's generic path). */
+  for (int64_t b = 0; b < n; b++)
+    for (int64_t ci = 0; ci < c; ci++) {
+      const int64_t g = ci / cg;
+      for (int64_t iz = 0; iz < in[0]; iz++)
+        for (int64_t iy = 0; iy < in[1]; iy++)
+          for (int64_t ix = 0; ix < in[2]; ix++) {
+            const double v = conv_elem(x, x_kind, ((b * c + ci) * in[0] + iz) * in[1] * in[2] +
+                                                      iy * in[2] + ix) - xz;
+            for (int64_t kz = 0; kz < ker[0]; kz++) {
+              const int64_t oz = iz * str[0] + kz * dil[0] - pad[0];
+              if (oz < 0 || oz >= out[0]) continue;
+              for (int64_t ky = 0; ky < ker[1]; ky++) {
+                const int64_t oy = iy * str[1] + ky * dil[1] - pad[1];
+                if (oy < 0 || oy >= out[1]) continue;
+                for (int64_t kx = 0; kx < ker[2]; kx++) {
+                  const int64_t ox = ix * str[2] + kx * dil[2] - pad[2];
+                  if (ox < 0 || ox >= out[2]) continue;
+                  const int64_t r = (kz * ker[1] + ky) * ker[2] + kx;
+                  for (int64_t mm = 0; mm < mg; mm++) {
+                    const double wv = conv_elem(w, w_kind, (ci * mg + mm) * taps + r);
+                    acc[((b * m + g * mg + mm) * out[0] + oz) * out[1] * out[2] + oy * out[2] +
+                        ox] += v * wv;
+                  }
+                }
+              }
+            }
+          }
+    }
+  return ORC_OK;
+}

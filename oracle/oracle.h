@@ -100,6 +100,21 @@ int orc_multi_head_attention(const float *q, const float *k, const float *v,
                              int64_t bias_heads, int has_scale, double scale,
                              float *out);
 
+/* Convolution sums, direct loops over (channel, tap) per output element,
+ * spatial dims right-aligned in 3 slots.  kind 0 = f32, 1 = u8, 2 = i8.
+ *   trans = 0 (opConv, lib/src/onnx_nn_ops.dart:179-817, and _convIntAcc,
+ *     lib/src/onnx_qlinear_ops.dart:232-283): w [M][C/group][taps], input
+ *     position i = o * str - pad + k * dil, out-of-range taps skipped.
+ *   trans = 1 (opConvTranspose, lib/src/onnx_nn_ops.dart:1009-1047): w
+ *     [C][M/group][taps]; input i contributes to o = i * str + k * dil - pad.
+ * Integer kinds subtract x_zp and w_zp[m] (w_zp NULL = 0).  acc receives the
+ * exact products summed in double [N][M][out]. */
+int orc_conv(const void *x, int x_kind, const void *w, int w_kind, int64_t n, int64_t c,
+             int64_t m, int64_t group, const int64_t *in, const int64_t *ker,
+             const int64_t *out, const int64_t *str, const int64_t *dil,
+             const int64_t *pad, int trans, int32_t x_zp, const int32_t *w_zp,
+             double *acc);
+
 /* _roundEven, lib/src/onnx_qlinear_ops.dart:19-26 / onnx_ops.dart:3480-3487.
  * Returns ORC_UNSUPPORTED through *err for non-finite input (Dart's toInt
  * throws UnsupportedError there). */

@@ -2,8 +2,8 @@
 
 Provenance: the inputs are `test/fixtures/<name>/{model.onnx,case.json}` of
 PieroSoria/onnx_runtime_dart (MIT; expected outputs were produced there by
-ONNX Runtime, see tool/gen_fixtures.py:891-925, :713-760, :789-799 and
-tool/gen_transformer_fixtures.py:55-63).  Each fixture becomes one JSON file
+ONNX Runtime, see tool/gen_fixtures.py:891-925, :713-760, :789-799, the
+conv recipes and tool/gen_transformer_fixtures.py:55-63).  Each fixture becomes one JSON file
 holding the node's op type, its attributes, every operand in node-input order
 (initializers merged with the case's feeds) and the expected outputs.  The
 result files are data only; they are what the tests read.
@@ -45,6 +45,30 @@ HOT_PATH = [
     "einsum_matmul",
     "mha_with_bias",
     "mha_no_bias",
+    "conv1d",
+    "conv2d_basic",
+    "conv2d_bias",
+    "conv2d_depthwise",
+    "conv2d_dilation",
+    "conv2d_groups",
+    "conv2d_pads",
+    "conv2d_pads_asym",
+    "conv2d_same_lower",
+    "conv2d_same_upper",
+    "conv2d_strides",
+    "conv3d",
+    "convinteger",
+    "convinteger_1d",
+    "convtranspose_1d",
+    "convtranspose_basic",
+    "convtranspose_bias",
+    "convtranspose_groups",
+    "convtranspose_outpad",
+    "convtranspose_output_shape",
+    "convtranspose_pads",
+    "convtranspose_stride2",
+    "qlinearconv_perchannel_bias",
+    "qlinearconv_pertensor",
 ]
 
 # ONNX TensorProto.DataType -> (numpy dtype, json dtype name)

@@ -10,6 +10,10 @@ Three independent anchors, per op:
     the edge cases the reference handles (partial blocks, odd block counts,
     float zero points, bias, per-row/per-column zero points, batching,
     saturation, m<4 scalar tails).
+The convolution family is pinned by its 24 fixtures and by identities that a
+wrong index, pad side or weight transpose breaks: a 1x1 conv is a matmul,
+a one-hot kernel shifts the input, ConvTranspose is the adjoint of Conv,
+and the integer conv equals the float conv of the centred operands.
 """
 import numpy as np
 import pytest
@@ -58,6 +62,23 @@ def _run_fixture(d):
         bias = x[5] if len(x) > 5 else None
         return {d["outputs"][0]: oracle.multi_head_attention(
             x[0], x[1], x[2], bias, num_heads=at["num_heads"], scale=at.get("scale"))}
+    geo = dict(strides=at.get("strides"), pads=at.get("pads"), dilations=at.get("dilations"),
+               group=at.get("group", 1))
+    if op == "Conv":
+        return {d["outputs"][0]: oracle.conv(x[0], x[1], x[2] if len(x) > 2 else None,
+                                             auto_pad=at.get("auto_pad", "NOTSET"), **geo)}
+    if op == "ConvTranspose":
+        return {d["outputs"][0]: oracle.conv_transpose(
+            x[0], x[1], x[2] if len(x) > 2 else None, output_padding=at.get("output_padding"),
+            output_shape=at.get("output_shape"), **geo)}
+    if op == "ConvInteger":
+        return {d["outputs"][0]: oracle.conv_integer(
+            x[0], x[1], x[2] if len(x) > 2 else None, x[3] if len(x) > 3 else None, **geo)}
+    if op == "QLinearConv":
+        yz = x[7] if len(x) > 7 else None
+        lo, hi = (-128, 127) if yz is not None and yz.dtype == np.int8 else (0, 255)
+        return {d["outputs"][0]: oracle.qlinear_conv(
+            *x[:8], x[8] if len(x) > 8 else None, lo=lo, hi=hi, **geo)}
     raise AssertionError(op)
 
 
@@ -414,3 +435,110 @@ def test_mha_default_scale_and_shared_bias_head():
         want[0, :, sl] = _sdpa_closed_form(q[0, :, sl], k[0, :, sl].T, v[0, :, sl], bias[0, 0],
                                            1 / np.sqrt(4))
     np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-6)
+
+
+# ------------------------------------------------------------ convolution
+
+
+def test_conv_1x1_is_a_matmul():
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((2, 6, 5, 7)).astype(np.float32)
+    w = rng.standard_normal((4, 6, 1, 1)).astype(np.float32)
+    b = rng.standard_normal(4).astype(np.float32)
+    want = np.einsum("mc,nchw->nmhw", w[:, :, 0, 0].astype(np.float64), x.astype(np.float64))
+    want += b.reshape(1, -1, 1, 1)
+    np.testing.assert_allclose(oracle.conv(x, w, b), want, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("nd", [1, 2, 3])
+def test_conv_one_hot_kernel_shifts_input(nd):
+    rng = np.random.default_rng(42 + nd)
+    sp = [6, 5, 4][:nd]
+    x = rng.standard_normal([1, 1] + sp).astype(np.float32)
+    ker = [3, 2, 3][:nd]
+    w = np.zeros([1, 1] + ker, np.float32)
+    tap = tuple(k - 1 for k in ker)  # last tap of every axis
+    w[(0, 0) + tap] = 1.0
+    pads = [1] * nd + [0] * nd  # pad at the beginning only
+    y = oracle.conv(x, w, pads=pads)
+    # begin pad 1: y[o] = x[o + tap - 1] per axis (tap >= 1), 0 past the end
+    want = np.zeros_like(y)
+    src = x[(0, 0) + tuple(slice(t - 1, None) for t in tap)]
+    n = tuple(min(a, b) for a, b in zip(src.shape, y.shape[2:]))
+    want[(0, 0) + tuple(slice(0, v) for v in n)] = src[tuple(slice(0, v) for v in n)]
+    np.testing.assert_array_equal(y, want)
+
+
+@pytest.mark.parametrize("case", [
+    dict(st=[1, 1], dl=[1, 1], pads=[0, 0, 0, 0], g=1),
+    dict(st=[2, 2], dl=[1, 1], pads=[1, 1, 1, 1], g=1),
+    dict(st=[2, 3], dl=[2, 1], pads=[2, 0, 1, 2], g=2),
+    dict(st=[1, 2], dl=[1, 1], pads=[0, 1, 0, 1], g=4),
+])
+def test_conv_transpose_is_the_adjoint_of_conv(case):
+    """<conv(x, w), y> == <x, conv_transpose(y, w)> with the same geometry
+    (output_padding chosen so the transposed output has x's shape)."""
+    rng = np.random.default_rng(7)
+    g = case["g"]
+    x = rng.standard_normal((2, 4, 9, 8))
+    w = rng.standard_normal((8, 4 // g, 3, 2))
+    y_shape = oracle.conv(x.astype(np.float32), w.astype(np.float32), strides=case["st"],
+                          dilations=case["dl"], pads=case["pads"], group=g).shape
+    y = rng.standard_normal(y_shape)
+    # output_padding that gives the transposed output x's spatial shape
+    op = [x.shape[2 + a] - ((y_shape[2 + a] - 1) * case["st"][a] + case["dl"][a] *
+                            (w.shape[2 + a] - 1) + 1 - case["pads"][a] - case["pads"][2 + a])
+          for a in range(2)]
+    assert all(0 <= v < s for v, s in zip(op, case["st"])) or case["st"] == [1, 1]
+    cx = oracle.conv(x, w, strides=case["st"], dilations=case["dl"], pads=case["pads"],
+                     group=g).astype(np.float64)
+    ty = oracle.conv_transpose(y, w, strides=case["st"], dilations=case["dl"],
+                               pads=case["pads"], output_padding=op,
+                               group=g).astype(np.float64)
+    assert ty.shape == x.shape
+    lhs = float(np.sum(cx * y))
+    rhs = float(np.sum(x * ty))
+    assert abs(lhs - rhs) <= 1e-4 * max(1.0, abs(lhs)), (lhs, rhs)
+
+
+def test_conv_same_pads_put_the_extra_on_the_right_side():
+    # even total padding split 1/1 is symmetric; with in 6, k 4, stride 1 the
+    # total is 3: SAME_UPPER pads (1 begin, 2 end), SAME_LOWER (2, 1).
+    assert oracle.resolve_pads([6], [4], [1], [1], "SAME_UPPER")[0] == [1, 2]
+    assert oracle.resolve_pads([6], [4], [1], [1], "SAME_LOWER")[0] == [2, 1]
+    assert oracle.resolve_pads([7], [3], [2], [1], "VALID") == ([0, 0], [3])
+    # Dart's ~/ truncates: (2 - 3) ~/ 2 + 1 == 1 - 0 == 1? (-1 ~/ 2 == 0)
+    assert oracle.resolve_pads([2], [3], [2], [1], "NOTSET", [0, 0])[1] == [1]
+
+
+@pytest.mark.parametrize("xs,ws", [(False, True), (True, True), (False, False), (True, False)])
+def test_conv_integer_equals_float_conv_of_centred_operands(xs, ws):
+    rng = np.random.default_rng(11)
+    xt = np.int8 if xs else np.uint8
+    wt = np.int8 if ws else np.uint8
+    lo_x, hi_x = (-128, 128) if xs else (0, 256)
+    lo_w, hi_w = (-128, 128) if ws else (0, 256)
+    x = rng.integers(lo_x, hi_x, (2, 6, 7, 6)).astype(xt)
+    w = rng.integers(lo_w, hi_w, (4, 3, 3, 3)).astype(wt)
+    xz = int(rng.integers(lo_x, hi_x))
+    wz = rng.integers(lo_w, hi_w, 4).astype(wt)
+    y = oracle.conv_integer(x, w, np.array(xz, xt), wz, pads=[1, 2, 0, 1], strides=[1, 2],
+                            group=2)
+    # padding contributes (x_zp - x_zp) = 0: pad the centred input with zeros
+    xc = x.astype(np.float64) - xz
+    wc = w.astype(np.float64) - wz.astype(np.float64).reshape(-1, 1, 1, 1)
+    want = oracle.conv(xc, wc, pads=[1, 2, 0, 1], strides=[1, 2], group=2)
+    np.testing.assert_array_equal(y, want.astype(np.float64).round().astype(np.int64))
+
+
+def test_qlinear_conv_requant_rounds_half_to_even():
+    # one output channel, 1x1 kernel: acc = x - x_zp; mult = 0.5 makes halves
+    x = np.array([[[[1, 2, 3, 5, 7]]]], np.uint8)
+    w = np.array([[[[1]]]], np.int8)
+    y = oracle.qlinear_conv(x, np.float32(0.5), np.uint8(0), w, np.float32(1.0), np.int8(0),
+                            np.float32(1.0), np.uint8(10), lo=0, hi=255)
+    # 0.5 -> 0, 1.0 -> 1, 1.5 -> 2, 2.5 -> 2, 3.5 -> 4
+    np.testing.assert_array_equal(y.ravel(), [10, 11, 12, 12, 14])
+    y = oracle.qlinear_conv(x, np.float32(0.5), np.uint8(0), w, np.float32(1.0), np.int8(0),
+                            np.float32(1.0), np.int8(-127), lo=-128, hi=127)
+    np.testing.assert_array_equal(y.ravel(), [-127, -126, -125, -125, -123])
