@@ -116,6 +116,33 @@ mg_status mg_weight_nbits_create(
     const float *bias, const int64_t *bias_shape, int32_t bias_rank,
     int32_t has_g_idx, mg_weight **out);
 
+/* Where one weight tensor's bytes are: host memory (host != NULL), or the
+ * byte range [offset, offset + length) of the file at path, which is how an
+ * ONNX initializer with external data is stored (location / offset / length
+ * entries, lib/src/onnx_proto_loader.dart:96-125).  length 0 means "implied
+ * by the shape", as the reference's resolver falls back to. */
+typedef struct mg_tensor_source {
+  const void *host;
+  const char *path;
+  int64_t offset;
+  int64_t length;
+} mg_tensor_source;
+
+/* The load path for big int4 models (lib/src/onnx_proto_loader.dart:96-125,
+ * :252-266; lib/src/model_source.dart:58): uploads a MatMulNBits weight with
+ * b / scales / zp taken from their sources in the raw ONNX layouts of
+ * mg_weight_nbits_create (B [N, nb, bs/2] bytes, scales f32 [N * nb], zero
+ * points packed [N * ceil(nb/2)] or f32 [N * nb]).  The bytes stream through
+ * pinned staging in column-group chunks of about chunk_bytes (0 = 32 MiB)
+ * and are repacked on the GPU, so no host copy of the whole tensor is made.
+ * bias: host float [N] or NULL.  Same validation and results as
+ * mg_weight_nbits_create. */
+mg_status mg_weight_nbits_create_streamed(
+    mg_ctx *ctx, int64_t K, int64_t N, int64_t bits, int64_t block_size,
+    const mg_tensor_source *b, const mg_tensor_source *scales, int32_t zp_kind,
+    const mg_tensor_source *zp, const float *bias, int32_t has_g_idx,
+    int64_t chunk_bytes, mg_weight **out);
+
 /* y[M, N] = a[M, K] . dequant(B)^T (+ bias): opMatMulNBits
  * (lib/src/onnx_qlinear_ops.dart:115-228).  `a` holds M rows of K floats
  * (the caller flattens leading dims, a.shape.last == K); y holds M*N floats.

@@ -76,6 +76,8 @@ SIGNATURES = {
                         _F, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P],
     "mg_qlinear_conv_dev": [_P, _P, _I32, _P, _I32, _F, _I32, _P, _I32, _P, _P, _I64, _P,
                             _I64, _F, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P],
+    "mg_weight_nbits_create_streamed": [_P, _I64, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I32,
+                                        _I64, _PP],
     "mg_matmul_f32": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_matmul_f32_dev": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_gemm_f32": [_P, _P, _P, _P, _P, _I32, _I32, _F, _F, _P, _P, _I32, _P],

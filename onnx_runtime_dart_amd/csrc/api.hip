@@ -270,7 +270,69 @@ mg_status mg_weight_nbits_create(
   w->K = K;
   w->N = N;
   w->nbits.bs = block_size;
-  mg_status st = mg_nbits_upload(ctx, w, b, scales, zp_kind, zp, bias);
+  mg_byte_source sb, ss, sz;
+  sb.host = b;
+  ss.host = reinterpret_cast<const uint8_t *>(scales);
+  sz.host = static_cast<const uint8_t *>(zp);
+  mg_status st = mg_nbits_upload(ctx, w, sb, ss, zp_kind, sz, bias, 0);
+  if (st != MG_OK) {
+    mg_nbits_free(w);
+    delete w;
+    return st;
+  }
+  *out = w;
+  return MG_OK;
+}
+
+mg_status mg_weight_nbits_create_streamed(mg_ctx *ctx, int64_t K, int64_t N, int64_t bits,
+                                          int64_t block_size, const mg_tensor_source *b,
+                                          const mg_tensor_source *scales, int32_t zp_kind,
+                                          const mg_tensor_source *zp, const float *bias,
+                                          int32_t has_g_idx, int64_t chunk_bytes,
+                                          mg_weight **out) {
+  g_last_error.clear();
+  if (!ctx || !out || !b || !scales)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_weight_nbits_create_streamed: null argument");
+  *out = nullptr;
+  if (has_g_idx) return mg_fail(MG_UNSUPPORTED, "MatMulNBits: g_idx input not supported");
+  if (bits != 4)
+    return mg_fail(MG_UNSUPPORTED,
+                   "MatMulNBits: only bits=4 supported, got " + std::to_string(bits));
+  if (K <= 0 || N <= 0 || block_size < 16 || (block_size & (block_size - 1)) != 0)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid K, N, block_size or input shape");
+  if (zp_kind != MG_ZP_NONE && zp_kind != MG_ZP_UINT4 && zp_kind != MG_ZP_FLOAT)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid zero_points");
+  if (zp_kind != MG_ZP_NONE && !zp)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid zero_points");
+  const int64_t nb = (K + block_size - 1) / block_size;
+  // Byte counts implied by the shapes; a stated length must cover them (a
+  // shorter tensor is malformed, lib/src/onnx_proto_loader.dart:96-125).
+  const int64_t need[3] = {N * nb * (block_size / 2), N * nb * 4,
+                           zp_kind == MG_ZP_UINT4 ? N * ((nb + 1) / 2)
+                                                  : zp_kind == MG_ZP_FLOAT ? N * nb * 4 : 0};
+  const mg_tensor_source *src[3] = {b, scales, zp};
+  const char *what[3] = {"B", "scales", "zero_points"};
+  mg_byte_source bsrc[3];
+  for (int i = 0; i < 3; i++) {
+    if (i == 2 && zp_kind == MG_ZP_NONE) break;
+    const mg_tensor_source &t = *src[i];
+    if ((!t.host && !t.path) || t.offset < 0 || t.length < 0 ||
+        (t.length > 0 && t.length < need[i]))
+      return mg_fail(MG_INVALID_ARGUMENT, std::string("MatMulNBits: ") + what[i] +
+                                              " source must hold " + std::to_string(need[i]) +
+                                              " bytes");
+    bsrc[i].host = static_cast<const uint8_t *>(t.host);
+    bsrc[i].path = t.host ? nullptr : t.path;
+    bsrc[i].offset = t.offset;
+  }
+  MG_TRY(mg_use_device(ctx));
+  mg_weight *w = new mg_weight();
+  w->kind = MG_W_NBITS;
+  w->device = ctx->device;
+  w->K = K;
+  w->N = N;
+  w->nbits.bs = block_size;
+  mg_status st = mg_nbits_upload(ctx, w, bsrc[0], bsrc[1], zp_kind, bsrc[2], bias, chunk_bytes);
   if (st != MG_OK) {
     mg_nbits_free(w);
     delete w;

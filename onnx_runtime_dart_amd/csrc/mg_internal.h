@@ -104,9 +104,19 @@ static inline size_t mg_align(size_t x, size_t a = 256) {
 
 // ----------------------------------------------------------- NBits entry
 
-mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const uint8_t *b,
-                          const float *scales, int32_t zp_kind, const void *zp,
-                          const float *bias);
+// Where the bytes of one weight tensor come from: host memory, or a byte
+// range of a file (ONNX external data).
+struct mg_byte_source {
+  const uint8_t *host = nullptr;
+  const char *path = nullptr;
+  int64_t offset = 0;
+};
+// Uploads a MatMulNBits weight: the raw tensors stream through pinned
+// staging in column-group chunks of about chunk_bytes (0 = default) and are
+// repacked on the device.  zp unused for MG_ZP_NONE; bias host [N] or null.
+mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const mg_byte_source &b,
+                          const mg_byte_source &scales, int32_t zp_kind,
+                          const mg_byte_source &zp, const float *bias, int64_t chunk_bytes);
 void mg_nbits_free(mg_weight *w);
 // Workspace bytes mg_nbits_run needs for M rows.
 size_t mg_nbits_ws_bytes(const mg_ctx *ctx, const mg_weight *w, int64_t M);

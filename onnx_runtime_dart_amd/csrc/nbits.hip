@@ -5,7 +5,8 @@
 // with q the 4-bit code (low nibble = even k), blk = k / block_size and the
 // zero point 8 by default, packed uint4, or float.
 //
-// Device weight layout (built once on upload, mg_nbits_upload):
+// Device weight layout (built once on upload by the repack kernels of
+// mg_nbits_upload):
 //   columns are grouped by 64 ("column group"), k by 128 ("k group").
 //   wq[cg][kg][g][col][j] is one dword holding the 8 nibbles of column
 //   (cg*64 + col) at k = kg*128 + 32*j + 8*g + t, t = 0..7, with even t in the
@@ -30,10 +31,14 @@
 // per-output kernel.
 #include <hip/hip_runtime.h>
 
+#include <errno.h>
+#include <fcntl.h>
+#include <unistd.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
-#include <thread>
+#include <string>
 #include <vector>
 
 #include "mg_internal.h"
@@ -1299,9 +1304,93 @@ void launch_gemv_q(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, hi
 
 // ------------------------------------------------------------- uploading
 
-mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const uint8_t *b,
-                          const float *scales, int32_t zp_kind, const void *zp,
-                          const float *bias) {
+namespace {
+
+// Device repack of one chunk of columns [n0, n0 + rows) (column groups
+// [cg0, cg0 + cgs)) from the raw ONNX tensors in `raw` (B [rows][nb][bs/2],
+// low nibble = even k) into the layout above.  Columns past N and k past
+// nb * bs get code 8; all eight codes of a dword share one block
+// (block_size >= 16 is a power of two and a dword spans 8 aligned k).
+__global__ __launch_bounds__(256) void k_nbits_repack_codes(
+    const uint32_t *__restrict__ raw, int64_t n0, int64_t N, int64_t nb, int64_t bs,
+    int64_t c4, int64_t cg0, int64_t cgs, uint32_t *__restrict__ wq) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= cgs * c4 * 1024) return;
+  const int j = (int)(idx & 3), col = (int)((idx >> 2) & 63), g = (int)((idx >> 8) & 3);
+  const int64_t t2 = idx >> 10;
+  const int64_t kg = t2 % c4, cg = cg0 + t2 / c4;
+  const int64_t n = cg * 64 + col;
+  const int64_t k0 = kg * KGRP + 32 * j + 8 * g;
+  uint32_t dw = 0x88888888u;
+  if (n < N && k0 < nb * bs) {
+    // 4 bytes = k0 .. k0 + 7; byte i holds k0 + 2i (low) and k0 + 2i + 1 (high)
+    const uint32_t v = raw[(((n - n0) * nb + k0 / bs) * (bs / 2) + (k0 % bs) / 2) / 4];
+    // even k -> nibbles 0..3, odd k -> nibbles 4..7 (nib_pos)
+    dw = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t by = (v >> (8 * i)) & 0xFFu;
+      dw |= (by & 15u) << (4 * i);
+      dw |= (by >> 4) << (16 + 4 * i);
+    }
+  }
+  wq[(((cg * c4 + kg) * 4 + g) * 64 + col) * 4 + j] = dw;
+}
+
+// Per-block tables of the chunk: scales [cg][blk][sz_pos(col)] (0 past N),
+// zero points as packed bytes [cg][blk/2][sz_pos(col)] (0x88 past N) or
+// floats [cg][blk][sz_pos(col)] (8 past N).
+__global__ __launch_bounds__(256) void k_nbits_repack_tables(
+    const float *__restrict__ sc_raw, const uint8_t *__restrict__ zp_raw, int zp_kind,
+    int64_t n0, int64_t N, int64_t nb, int64_t nbh, int64_t cg0, int64_t cgs,
+    float *__restrict__ sp, uint8_t *__restrict__ zp4, float *__restrict__ zpf) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= cgs * nb * 64) return;
+  const int col = (int)(idx & 63);
+  const int64_t blk = (idx >> 6) % nb, cg = cg0 + (idx >> 6) / nb;
+  const int64_t n = cg * 64 + col;
+  const bool in = n < N;
+  const int64_t o = (cg * nb + blk) * 64 + sz_pos(col);
+  sp[o] = in ? sc_raw[(n - n0) * nb + blk] : 0.f;
+  if (zp_kind == MG_ZP_FLOAT)
+    zpf[o] = in ? reinterpret_cast<const float *>(zp_raw)[(n - n0) * nb + blk] : 8.f;
+  if (zp_kind == MG_ZP_UINT4 && blk < nbh)
+    zp4[(cg * nbh + blk) * 64 + sz_pos(col)] = in ? zp_raw[(n - n0) * nbh + blk] : 0x88;
+}
+
+// Reads bytes [off, off + len) of a source into dst.
+mg_status read_source(const mg_byte_source &s, int fd, int64_t off, int64_t len, uint8_t *dst) {
+  if (len == 0) return MG_OK;
+  if (s.host) {
+    std::memcpy(dst, s.host + off, (size_t)len);
+    return MG_OK;
+  }
+  int64_t done = 0;
+  while (done < len) {
+    const ssize_t r = pread(fd, dst + done, (size_t)(len - done), (off_t)(s.offset + off + done));
+    if (r < 0 && errno == EINTR) continue;
+    if (r <= 0)
+      return mg_fail(MG_INVALID_ARGUMENT, std::string("MatMulNBits: cannot read ") +
+                                              std::to_string(len) + " bytes of " + s.path +
+                                              " at offset " + std::to_string(s.offset + off));
+    done += r;
+  }
+  return MG_OK;
+}
+
+struct OpenFiles {
+  int fd[3] = {-1, -1, -1};
+  ~OpenFiles() {
+    for (int f : fd)
+      if (f >= 0) close(f);
+  }
+};
+
+}  // namespace
+
+mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const mg_byte_source &b,
+                          const mg_byte_source &scales, int32_t zp_kind,
+                          const mg_byte_source &zp, const float *bias, int64_t chunk_bytes) {
   mg_nbits_dev &d = w->nbits;
   const int64_t N = w->N, K = w->K, bs = d.bs;
   d.nb = (K + bs - 1) / bs;
@@ -1311,84 +1400,93 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const uint8_t *b,
   d.ng = ((N + CGRP - 1) / CGRP + 1) / 2 * 2;  // even: the GEMM pairs groups
   d.zp_kind = zp_kind;
   const int64_t ng = d.ng, nb = d.nb, nbh = d.nbh, c4 = d.c4;
-  const int64_t blob = bs / 2, kstored = nb * bs;
+  const int64_t blob = bs / 2;
+  // Raw bytes per column of each tensor.
+  const int64_t col_b = nb * blob, col_s = nb * 4;
+  const int64_t col_z = zp_kind == MG_ZP_UINT4 ? nbh : zp_kind == MG_ZP_FLOAT ? nb * 4 : 0;
+  const int64_t col_all = mg_align(col_b) + col_s + col_z;  // rough per-column footprint
 
-  std::vector<uint32_t> wq((size_t)(ng * c4 * 4 * 64 * 4));
-  std::vector<float> sp((size_t)(ng * nb * 64), 0.f);
-  std::vector<uint8_t> zp4;
-  std::vector<float> zpf;
-  auto work = [&](int64_t g0, int64_t g1) {
-    for (int64_t cg = g0; cg < g1; cg++) {
-      for (int64_t kg = 0; kg < c4; kg++)
-        for (int g = 0; g < 4; g++)
-          for (int col = 0; col < 64; col++) {
-            const int64_t n = cg * 64 + col;
-            for (int j = 0; j < 4; j++) {
-              uint32_t dw = 0;
-              for (int t = 0; t < 8; t++) {
-                const int64_t k = kg * KGRP + 32 * j + 8 * g + t;
-                uint32_t q = 8;
-                if (n < N && k < kstored) {
-                  const uint8_t by = b[(n * nb + k / bs) * blob + (k % bs) / 2];
-                  q = (k & 1) ? (by >> 4) : (by & 15);
-                }
-                dw |= q << (4 * nib_pos(t));
-              }
-              wq[(size_t)((((cg * c4 + kg) * 4 + g) * 64 + col) * 4 + j)] = dw;
-            }
-          }
-      for (int64_t blk = 0; blk < nb; blk++)
-        for (int col = 0; col < 64; col++) {
-          const int64_t n = cg * 64 + col;
-          if (n < N) sp[(size_t)((cg * nb + blk) * 64 + sz_pos(col))] = scales[n * nb + blk];
-        }
+  OpenFiles files;
+  const mg_byte_source *srcs[3] = {&b, &scales, &zp};
+  for (int i = 0; i < 3; i++) {
+    if (i == 2 && zp_kind == MG_ZP_NONE) break;
+    if (!srcs[i]->host) {
+      if (!srcs[i]->path) return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: missing tensor data");
+      files.fd[i] = open(srcs[i]->path, O_RDONLY | O_CLOEXEC);
+      if (files.fd[i] < 0)
+        return mg_fail(MG_INVALID_ARGUMENT,
+                       std::string("MatMulNBits: cannot open ") + srcs[i]->path);
     }
-  };
-  {
-    const int64_t nthreads = std::max<int64_t>(
-        1, std::min<int64_t>(ng, std::thread::hardware_concurrency()));
-    std::vector<std::thread> th;
-    const int64_t per = (ng + nthreads - 1) / nthreads;
-    for (int64_t t = 0; t < nthreads; t++) {
-      const int64_t g0 = t * per, g1 = std::min(ng, g0 + per);
-      if (g0 < g1) th.emplace_back(work, g0, g1);
-    }
-    for (auto &t : th) t.join();
-  }
-  if (zp_kind == MG_ZP_UINT4) {
-    zp4.assign((size_t)(ng * nbh * 64), 0x88);
-    const uint8_t *z = static_cast<const uint8_t *>(zp);
-    for (int64_t cg = 0; cg < ng; cg++)
-      for (int64_t h = 0; h < nbh; h++)
-        for (int col = 0; col < 64; col++) {
-          const int64_t n = cg * 64 + col;
-          if (n < N) zp4[(size_t)((cg * nbh + h) * 64 + sz_pos(col))] = z[n * nbh + h];
-        }
-  } else if (zp_kind == MG_ZP_FLOAT) {
-    zpf.assign((size_t)(ng * nb * 64), 8.f);
-    const float *z = static_cast<const float *>(zp);
-    for (int64_t cg = 0; cg < ng; cg++)
-      for (int64_t blk = 0; blk < nb; blk++)
-        for (int col = 0; col < 64; col++) {
-          const int64_t n = cg * 64 + col;
-          if (n < N) zpf[(size_t)((cg * nb + blk) * 64 + sz_pos(col))] = z[n * nb + blk];
-        }
   }
 
-  auto up = [&](void **dst, const void *src, size_t bytes) -> mg_status {
-    if (bytes == 0) return MG_OK;
+  auto alloc = [&](void **dst, size_t bytes) -> mg_status {
     MG_HIP(hipMalloc(dst, bytes));
     w->device_bytes += (int64_t)bytes;
-    MG_HIP(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
     return MG_OK;
   };
-  MG_TRY(up((void **)&d.wq, wq.data(), wq.size() * 4));
-  MG_TRY(up((void **)&d.scales, sp.data(), sp.size() * 4));
-  if (!zp4.empty()) MG_TRY(up((void **)&d.zp4, zp4.data(), zp4.size()));
-  if (!zpf.empty()) MG_TRY(up((void **)&d.zpf, zpf.data(), zpf.size() * 4));
-  if (bias) MG_TRY(up((void **)&d.bias, bias, (size_t)N * 4));
-  (void)ctx;
-  return MG_OK;
+  MG_TRY(alloc((void **)&d.wq, (size_t)(ng * c4 * 1024) * 4));
+  MG_TRY(alloc((void **)&d.scales, (size_t)(ng * nb * 64) * 4));
+  if (zp_kind == MG_ZP_UINT4) MG_TRY(alloc((void **)&d.zp4, (size_t)(ng * nbh * 64)));
+  if (zp_kind == MG_ZP_FLOAT) MG_TRY(alloc((void **)&d.zpf, (size_t)(ng * nb * 64) * 4));
+  if (bias) {
+    MG_TRY(alloc((void **)&d.bias, (size_t)N * 4));
+    MG_HIP(hipMemcpy(d.bias, bias, (size_t)N * 4, hipMemcpyHostToDevice));
+  }
+
+  // Chunks of whole column groups; two staging slots (pinned host + device)
+  // so that reading chunk i + 1 overlaps the copy and repack of chunk i.
+  if (chunk_bytes <= 0) chunk_bytes = 32ll << 20;
+  const int64_t cgs_per = std::min<int64_t>(ng, std::max<int64_t>(1, chunk_bytes / (64 * col_all)));
+  const int64_t rows_per = cgs_per * 64;
+  const size_t off_s = mg_align((size_t)(rows_per * col_b));
+  const size_t off_z = off_s + mg_align((size_t)(rows_per * col_s));
+  const size_t slot = off_z + mg_align((size_t)(rows_per * col_z));
+  hipStream_t st = ctx->stream;
+  uint8_t *pinned[2] = {nullptr, nullptr};
+  uint8_t *stage[2] = {nullptr, nullptr};
+  hipEvent_t done[2] = {nullptr, nullptr};
+  mg_status status = MG_OK;
+  auto cleanup = [&]() {
+    if (st) (void)hipStreamSynchronize(st);
+    for (int i = 0; i < 2; i++) {
+      if (pinned[i]) (void)hipHostFree(pinned[i]);
+      if (stage[i]) (void)hipFree(stage[i]);
+      if (done[i]) (void)hipEventDestroy(done[i]);
+    }
+  };
+  auto run = [&]() -> mg_status {
+    for (int i = 0; i < 2; i++) {
+      MG_HIP(hipHostMalloc((void **)&pinned[i], slot, hipHostMallocDefault));
+      MG_HIP(hipMalloc((void **)&stage[i], slot));
+      MG_HIP(hipEventCreateWithFlags(&done[i], hipEventDisableTiming));
+    }
+    for (int64_t ci = 0, cg0 = 0; cg0 < ng; ci++, cg0 += cgs_per) {
+      const int sl = (int)(ci & 1);
+      const int64_t cgs = std::min(cgs_per, ng - cg0);
+      const int64_t n0 = cg0 * 64, n1 = std::min(N, (cg0 + cgs) * 64);
+      const int64_t rows = std::max<int64_t>(0, n1 - n0);
+      if (ci >= 2) MG_HIP(hipEventSynchronize(done[sl]));  // the slot's last copy and kernels
+      MG_TRY(read_source(b, files.fd[0], n0 * col_b, rows * col_b, pinned[sl]));
+      MG_TRY(read_source(scales, files.fd[1], n0 * col_s, rows * col_s, pinned[sl] + off_s));
+      if (col_z) MG_TRY(read_source(zp, files.fd[2], n0 * col_z, rows * col_z, pinned[sl] + off_z));
+      if (rows > 0) MG_HIP(hipMemcpyAsync(stage[sl], pinned[sl], slot, hipMemcpyHostToDevice, st));
+      const int64_t ncodes = cgs * c4 * 1024, ntab = cgs * nb * 64;
+      hipLaunchKernelGGL(k_nbits_repack_codes, dim3((unsigned)((ncodes + 255) / 256)), dim3(256),
+                         0, st, reinterpret_cast<const uint32_t *>(stage[sl]), n0, N, nb, bs, c4,
+                         cg0, cgs, d.wq);
+      hipLaunchKernelGGL(k_nbits_repack_tables, dim3((unsigned)((ntab + 255) / 256)), dim3(256),
+                         0, st, reinterpret_cast<const float *>(stage[sl] + off_s),
+                         stage[sl] + off_z, zp_kind, n0, N, nb, nbh, cg0, cgs, d.scales, d.zp4,
+                         d.zpf);
+      MG_TRY(mg_launch_check("k_nbits_repack"));
+      MG_HIP(hipEventRecord(done[sl], st));
+    }
+    MG_HIP(hipStreamSynchronize(st));
+    return MG_OK;
+  };
+  status = run();
+  cleanup();
+  return status;
 }
 
 void mg_nbits_free(mg_weight *w) {

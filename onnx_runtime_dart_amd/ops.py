@@ -150,8 +150,48 @@ class _Weight:
         return k.value, n.value, b.value
 
 
+class TensorSource(C.Structure):
+    """mg_tensor_source: a tensor's bytes in host memory or in a file range
+    (ONNX external data: location / offset / length)."""
+    _fields_ = [("host", C.c_void_p), ("path", C.c_char_p), ("offset", C.c_int64),
+                ("length", C.c_int64)]
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray) -> "TensorSource":
+        src = cls(arr.ctypes.data_as(C.c_void_p), None, 0, arr.nbytes)
+        src._keep = arr  # the array must outlive the upload
+        return src
+
+    @classmethod
+    def from_file(cls, path, offset: int = 0, length: int = 0) -> "TensorSource":
+        return cls(None, str(path).encode(), int(offset), int(length))
+
+
 class NBitsWeight(_Weight):
     """MatMulNBits B/scales/zero_points/bias uploaded and prepacked."""
+
+    @classmethod
+    def streamed(cls, b: TensorSource, scales: TensorSource, zero_points: TensorSource = None,
+                 *, zp_kind: int = MG_ZP_NONE, k: int, n: int, bits: int = 4,
+                 block_size: int, bias=None, has_g_idx=False, chunk_bytes: int = 0,
+                 ctx: Context | None = None) -> "NBitsWeight":
+        """The load path: B / scales / zero points streamed from host arrays or
+        file ranges (mg_weight_nbits_create_streamed), repacked on the GPU."""
+        self = cls.__new__(cls)
+        self.ctx = ctx or default_context()
+        self.k, self.n = int(k), int(n)
+        if bias is not None:
+            bias = np.asarray(bias)
+            if bias.dtype.kind != "f" or bias.shape != (self.n,):
+                raise ArgumentError("MatMulNBits: bias must be floating point [N]")
+            bias = np.ascontiguousarray(bias, dtype=np.float32)
+        h = C.c_void_p()
+        check(lib.mg_weight_nbits_create_streamed(
+            self.ctx.handle, int(k), int(n), int(bits), int(block_size), C.byref(b),
+            C.byref(scales), int(zp_kind), C.byref(zero_points) if zero_points is not None else None,
+            _ptr(bias), int(bool(has_g_idx)), int(chunk_bytes), C.byref(h)))
+        self.handle = h
+        return self
 
     def __init__(self, b_q, scales, zero_points=None, *, k, n, bits=4, block_size,
                  bias=None, has_g_idx=False, ctx: Context | None = None):
