@@ -155,13 +155,13 @@ def main():
                     help="headline and lm_head measurements only")
     ap.add_argument("--only", default=None,
                     choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1", "llama16",
-                             "attn"],
+                             "attn", "conv"],
                     help="profiling mode: launch one workload --steps times and exit "
                          "(lm512 / lm1: Qwen3 lm_head MatMulNBits at M=512 / M=1; i8lm512: "
                          "the lm_head as MatMulInteger at M=512; f32ffn: the MiniLM FFN1 "
                          "Gemm; llama1 / llama16: the Llama lm_head at M=1 / M=16; attn: the MiniLM "
-                         "fused attention; copy: 256 MiB device copy used to calibrate the HBM "
-                         "byte counters)")
+                         "fused attention; conv: the ResNet-50 3x3 conv; copy: 256 MiB device copy "
+                         "used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -311,6 +311,8 @@ def main():
         result["decode_sweep"] = decode_sweep(torch, ops, ctx, T, randn, dev, args)
         result["int8_prefill"] = int8_prefill(torch, ops, ctx, T, dev, args)
         result["f32_encoder"] = f32_encoder(torch, ops, ctx, T, randn, dev, args)
+        result["conv"] = conv_family(torch, ops, ctx, T, randn, dev, args)
+        result["load_path"] = load_path(ops, ctx, host_w[-1], QWEN3_PROJ[-1])
 
     if not args.no_cpu and not args.quick and os.environ.get("MIGEMM_BENCH_NO_CPU") != "1":
         result["cpu_baseline"] = cpu_baseline(host_w, np.random.default_rng(0x5EED0003))
@@ -520,6 +522,108 @@ def f32_encoder(torch, ops, ctx, T, randn, dev, args):
     return out
 
 
+# Convolution workloads (no BASELINE config names one; these are common CNN
+# shapes): ResNet-50 stage-3 3x3 conv, the ResNet stem, a stride-2 4x4
+# ConvTranspose upsampler (VAE decoder) and the stage-3 conv as QLinearConv.
+RESNET_3X3 = ((32, 256, 14, 14), (256, 256, 3, 3), dict(pads=[1, 1, 1, 1]))
+RESNET_STEM = ((32, 3, 224, 224), (64, 3, 7, 7), dict(strides=[2, 2], pads=[3, 3, 3, 3]))
+VAE_UP = ((8, 128, 32, 32), (128, 64, 4, 4), dict(strides=[2, 2], pads=[1, 1, 1, 1]))
+
+
+def conv_flops(xs, ws, ys):
+    """2 * N * M * out_positions * (C / group) * taps (taps in the padding
+    count, as a GEMM over im2col would)."""
+    return 2.0 * ys[0] * ys[1] * float(np.prod(ys[2:])) * ws[1] * float(np.prod(ws[2:]))
+
+
+def conv_family(torch, ops, ctx, T, randn, dev, args):
+    rng = np.random.default_rng(0x5EED0004)
+    out = {}
+
+    def f32_case(name, spec, transposed=False):
+        xs, ws, at = spec
+        x = randn(*xs)
+        w = torch.from_numpy((rng.standard_normal(ws) * 0.05).astype(np.float32)).to(dev)
+        if transposed:
+            ys = ops.conv_transpose_output_shape(xs, ws, **at)
+            flops = 2.0 * xs[0] * xs[1] * ws[1] * float(np.prod(xs[2:])) * float(np.prod(ws[2:]))
+        else:
+            ys = ops.conv_output_shape(xs, ws, **at)
+            flops = conv_flops(xs, ws, ys)
+        b = torch.zeros(ys[1], device=dev)
+        y = torch.empty(ys, device=dev, dtype=torch.float32)
+        fn = ops.conv_transpose_f32_dev if transposed else ops.conv_f32_dev
+        ms = T.loop(lambda: fn(x.data_ptr(), xs, w.data_ptr(), ws, y.data_ptr(), b.data_ptr(),
+                               ctx=ctx, **at), 20, 3)
+        tf = flops / (ms / 1e3) / 1e12
+        out[name] = {"x": list(xs), "w": list(ws), **{k: v for k, v in at.items()},
+                     "us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2),
+                     "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+
+    f32_case("resnet50_3x3_256", RESNET_3X3)
+    f32_case("resnet50_stem_7x7", RESNET_STEM)
+    f32_case("conv_transpose_4x4_s2", VAE_UP, transposed=True)
+    out["conv_transpose_4x4_s2"]["note"] = ("FLOPs count the useful taps; the gather form "
+                                            "issues all 16 taps per output, 4 of them valid")
+
+    xs, ws, at = RESNET_3X3
+    x = torch.randint(0, 256, xs, device=dev, dtype=torch.uint8)
+    w = torch.randint(-128, 128, ws, device=dev, dtype=torch.int8)
+    ys = ops.conv_output_shape(xs, ws, **at)
+    y = torch.empty(ys, device=dev, dtype=torch.uint8)
+    wsc = rng.uniform(0.002, 0.02, ws[0]).astype(np.float32)
+    wz = np.zeros(ws[0], np.int8)
+    ms = T.loop(lambda: ops.qlinear_conv_dev(x.data_ptr(), False, xs, 0.05, 128, w.data_ptr(),
+                                             True, ws, wsc, wz, 4.0, 128, y.data_ptr(),
+                                             lo=0, hi=255, ctx=ctx, **at), 20, 3)
+    tf = conv_flops(xs, ws, ys) / (ms / 1e3) / 1e12
+    out["qlinear_conv_resnet50_3x3_256"] = {
+        "us": round(ms * 1e3, 2), "TOP/s": round(tf, 2),
+        "note": "integer operands on fp32 MFMA (exact); includes the per-call upload of the "
+                "per-channel requant table and its stream wait"}
+    print(f"# conv: {out}", file=sys.stderr, flush=True)
+    return out
+
+
+def load_path(ops, ctx, hw, proj):
+    """Upload time of the Qwen lm_head's int4 tensors (B, scales, zero points)
+    through the streamed path: from host arrays, and from a file (the ONNX
+    external-data case; the file is written first, so it is read from the page
+    cache).  GB/s counts the raw ONNX bytes."""
+    import tempfile
+    b, sc, zp = hw
+    _, k, n = proj
+    raw = b.nbytes + sc.nbytes + zp.nbytes
+    out = {"workload": f"Qwen3 lm_head MatMulNBits {k}x{n} bs {BLOCK} uint4 zp, "
+                       f"{raw / 1e6:.1f} MB raw"}
+    srcs = [ops.TensorSource.from_array(np.ascontiguousarray(t)) for t in (b, sc, zp)]
+
+    def timed(sources, chunk=0):
+        best = None
+        for _ in range(3):
+            t0 = time.perf_counter()
+            w = ops.NBitsWeight.streamed(*sources, zp_kind=ops.MG_ZP_UINT4, k=k, n=n,
+                                         block_size=BLOCK, chunk_bytes=chunk, ctx=ctx)
+            dt = time.perf_counter() - t0
+            w.release()
+            best = dt if best is None else min(best, dt)
+        return best
+
+    t_host = timed(srcs)
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "lm_head.bin"
+        with open(path, "wb") as f:
+            for t in (b, sc, zp):
+                f.write(np.ascontiguousarray(t).tobytes())
+        offs = np.cumsum([0, b.nbytes, sc.nbytes])
+        fsrc = [ops.TensorSource.from_file(path, int(o)) for o in offs]
+        t_file = timed(fsrc)
+    out["host_arrays"] = {"ms": round(t_host * 1e3, 2), "GB/s": round(raw / t_host / 1e9, 2)}
+    out["file_page_cache"] = {"ms": round(t_file * 1e3, 2), "GB/s": round(raw / t_file / 1e9, 2)}
+    print(f"# load path: {out}", file=sys.stderr, flush=True)
+    return out
+
+
 def run_only(args, torch, ops, ctx, stream, dev, randn):
     """Profiling mode: one workload launched --steps times on the library's
     stream."""
@@ -562,6 +666,14 @@ def run_only(args, torch, ops, ctx, stream, dev, randn):
             y = torch.empty((tok, n), device=dev, dtype=torch.float32)
             for _ in range(args.steps):
                 w.gemm_dev(a.data_ptr(), tok, y.data_ptr(), bias.data_ptr(), [n])
+        elif args.only == "conv":
+            xs, ws, at = RESNET_3X3
+            x = randn(*xs)
+            wt = torch.from_numpy((rng.standard_normal(ws) * 0.05).astype(np.float32)).to(dev)
+            y = torch.empty(ops.conv_output_shape(xs, ws, **at), device=dev, dtype=torch.float32)
+            w = None
+            for _ in range(args.steps):
+                ops.conv_f32_dev(x.data_ptr(), xs, wt.data_ptr(), ws, y.data_ptr(), ctx=ctx, **at)
         elif args.only == "attn":
             dh = MINILM_H // MINILM_HEADS
             q = randn(MINILM_B, MINILM_HEADS, MINILM_S, dh)
