@@ -335,6 +335,40 @@ mg_status mg_multi_head_attention_dev(mg_ctx *ctx, const float *q_dev,
                                       int32_t bias_heads, int32_t has_scale,
                                       float scale, float *y_dev);
 
+/* GroupQueryAttention (com.microsoft; lib/src/onnx_ops.dart:1829-2012,
+ * dispatched at lib/src/onnx_graph.dart:1649-1668): q [batch, seq, hidden]
+ * with num_heads heads of hidden / num_heads; k and v [batch, seq,
+ * kv_num_heads * head_size]; query head h uses KV head
+ * h / (num_heads / kv_num_heads).  past_key / past_value NULL (past_len 0)
+ * or [batch, kv_num_heads, past_len, head_size].  With do_rotary, RoPE at
+ * positions past_len + s from cos_cache / sin_cache [max_pos, half_rot]
+ * (GPT-J pairs when rotary_interleaved) is applied to q and k.  Query s sees
+ * keys 0 .. past_len + s (causal), plus attention_bias [batch, bias_heads,
+ * seq, past_len + seq] (bias_heads 1 or num_heads) if given.  scale defaults
+ * to 1 / sqrt(head_size).  softcap != 0 or local_window > 0 is
+ * MG_UNSUPPORTED, as in the reference.  Outputs: y [batch, seq, hidden] and
+ * present_key / present_value [batch, kv_num_heads, past_len + seq,
+ * head_size] (the past followed by the rotated K / raw V).  Head size <= 128. */
+mg_status mg_group_query_attention(
+    mg_ctx *ctx, const float *q, const float *k, const float *v, int64_t batch,
+    int64_t seq, int64_t hidden, int32_t num_heads, int32_t kv_num_heads,
+    const float *past_key, const float *past_value, int64_t past_len,
+    const float *cos_cache, const float *sin_cache, int64_t max_pos,
+    int64_t half_rot, int32_t do_rotary, int32_t rotary_interleaved,
+    const float *attention_bias, int32_t bias_heads, int32_t has_scale,
+    float scale, float softcap, int32_t local_window, float *y,
+    float *present_key, float *present_value);
+mg_status mg_group_query_attention_dev(
+    mg_ctx *ctx, const float *q_dev, const float *k_dev, const float *v_dev,
+    int64_t batch, int64_t seq, int64_t hidden, int32_t num_heads,
+    int32_t kv_num_heads, const float *past_key_dev,
+    const float *past_value_dev, int64_t past_len, const float *cos_cache_dev,
+    const float *sin_cache_dev, int64_t max_pos, int64_t half_rot,
+    int32_t do_rotary, int32_t rotary_interleaved,
+    const float *attention_bias_dev, int32_t bias_heads, int32_t has_scale,
+    float scale, float softcap, int32_t local_window, float *y_dev,
+    float *present_key_dev, float *present_value_dev);
+
 /* ---------------------------------------------------------- convolution */
 
 /* Conv (lib/src/onnx_nn_ops.dart:179-817, dispatched at

@@ -78,6 +78,12 @@ SIGNATURES = {
                             _I64, _F, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P],
     "mg_weight_nbits_create_streamed": [_P, _I64, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I32,
                                         _I64, _PP],
+    "mg_group_query_attention": [_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P, _I64,
+                                 _P, _P, _I64, _I64, _I32, _I32, _P, _I32, _I32, _F, _F, _I32,
+                                 _P, _P, _P],
+    "mg_group_query_attention_dev": [_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P,
+                                     _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _I32, _I32, _F,
+                                     _F, _I32, _P, _P, _P],
     "mg_matmul_f32": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_matmul_f32_dev": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_gemm_f32": [_P, _P, _P, _P, _P, _I32, _I32, _F, _F, _P, _P, _I32, _P],

@@ -1698,3 +1698,197 @@ mg_status mg_qlinear_conv_dev(mg_ctx *ctx, const void *x_dev, int32_t x_signed,
                          y_scale, true, &wz, &mult));
   return conv_dev(ctx, p, x_dev, w_dev, bias_dev, y_dev, wz, mult);
 }
+
+// --------------------------------------------------------------------------
+// GroupQueryAttention (lib/src/onnx_ops.dart:1829-2012).
+
+namespace {
+
+struct GqaArgs {
+  int64_t batch, seq, hidden, heads, kv, past, max_pos, half_rot;
+  int32_t rotary, interleaved, bias_heads, has_bias, has_scale;
+  float scale, softcap;
+  int32_t local_window;
+};
+
+mg_status plan_gqa(const GqaArgs &a, mg_attn_problem *p, mg_gqa_prep *g) {
+  // lib/src/onnx_ops.dart:1862-1866
+  if (a.softcap != 0.f || a.local_window > 0)
+    return mg_fail(MG_UNSUPPORTED, "GroupQueryAttention: softcap / local_window not supported");
+  if (a.batch < 0 || a.seq < 0 || a.past < 0 || a.heads <= 0 || a.kv <= 0 ||
+      a.heads % a.kv != 0 || a.hidden < 0 || a.hidden % a.heads != 0)
+    return mg_fail(MG_INVALID_ARGUMENT,
+                   "GroupQueryAttention: hidden must be a multiple of num_heads, and num_heads "
+                   "of kv_num_heads");
+  const int64_t hs = a.hidden / a.heads, group = a.heads / a.kv, total = a.past + a.seq;
+  if (a.rotary && (a.half_rot < 1 || 2 * a.half_rot > hs || a.past + a.seq > a.max_pos))
+    return mg_fail(MG_INVALID_ARGUMENT,
+                   "GroupQueryAttention: cos/sin caches must be [>= past + seq, <= head_size / 2]");
+  if (a.has_bias && a.bias_heads != 1 && a.bias_heads != a.heads)
+    return mg_fail(MG_UNSUPPORTED, "GroupQueryAttention: bias heads must be 1 or num_heads");
+  *g = mg_gqa_prep{};
+  g->batch = a.batch;
+  g->seq = a.seq;
+  g->heads = a.heads;
+  g->kv_heads = a.kv;
+  g->hs = hs;
+  g->past = a.past;
+  g->half_rot = a.half_rot;
+  g->rotary = a.rotary;
+  g->interleaved = a.interleaved;
+  *p = mg_attn_problem{};
+  // Batch dims (batch, kv head, query head of the group): query head
+  // h = kvh * group + j shares KV head kvh (stride 0 over j).
+  p->nbd = 3;
+  p->bdim[0] = a.batch;
+  p->bdim[1] = a.kv;
+  p->bdim[2] = group;
+  p->q_bs[0] = p->y_bs[0] = a.seq * a.hidden;
+  p->q_bs[1] = p->y_bs[1] = group * hs;
+  p->q_bs[2] = p->y_bs[2] = hs;
+  p->k_bs[0] = p->v_bs[0] = a.kv * total * hs;
+  p->k_bs[1] = p->v_bs[1] = total * hs;
+  p->k_bs[2] = p->v_bs[2] = 0;
+  p->q_rs = p->y_rs = a.hidden;
+  p->q_cs = 1;
+  p->k_ts = p->v_ts = hs;
+  p->k_ds = p->v_ds = 1;
+  if (a.has_bias) {
+    const bool one = a.bias_heads == 1;
+    p->m_bs[0] = a.bias_heads * a.seq * total;
+    p->m_bs[1] = one ? 0 : group * a.seq * total;
+    p->m_bs[2] = one ? 0 : a.seq * total;
+    p->m_qs = total;
+    p->m_ts = 1;
+  }
+  p->S = (int)a.seq;
+  p->T = (int)total;
+  p->D = p->DV = (int)hs;
+  p->scale = a.has_scale ? a.scale : (float)(1.0 / std::sqrt((double)hs));  // :1898
+  p->causal = 1;
+  p->causal_off = a.past;
+  if (a.seq > 0x7fffffff || total > 0x7fffffff || !fits_lane_offsets(*p))
+    return mg_fail(MG_UNSUPPORTED, "GroupQueryAttention: dimensions too large");
+  return MG_OK;
+}
+
+mg_status gqa_run(mg_ctx *ctx, mg_attn_problem p, mg_gqa_prep g, const float *q, float *q_rot,
+                  const float *bias, float *y) {
+  g.q = q;
+  g.q_rot = q_rot;
+  MG_TRY(mg_gqa_prep_run(ctx, g));
+  p.q = g.rotary ? q_rot : q;
+  p.k = g.present_k;
+  p.v = g.present_v;
+  p.mask = bias;
+  p.y = y;
+  return mg_attn_run(ctx, p);
+}
+
+}  // namespace
+
+mg_status mg_group_query_attention(
+    mg_ctx *ctx, const float *q, const float *k, const float *v, int64_t batch, int64_t seq,
+    int64_t hidden, int32_t num_heads, int32_t kv_num_heads, const float *past_key,
+    const float *past_value, int64_t past_len, const float *cos_cache, const float *sin_cache,
+    int64_t max_pos, int64_t half_rot, int32_t do_rotary, int32_t rotary_interleaved,
+    const float *attention_bias, int32_t bias_heads, int32_t has_scale, float scale,
+    float softcap, int32_t local_window, float *y, float *present_key, float *present_value) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_group_query_attention: null context");
+  GqaArgs a{batch, seq, hidden, num_heads, kv_num_heads, past_len, max_pos, half_rot,
+            do_rotary, rotary_interleaved, bias_heads, attention_bias != nullptr, has_scale,
+            scale, softcap, local_window};
+  mg_attn_problem p;
+  mg_gqa_prep g;
+  MG_TRY(plan_gqa(a, &p, &g));
+  const int64_t hs = hidden / num_heads, total = past_len + seq;
+  const int64_t nq = batch * seq * hidden, nkv = batch * seq * kv_num_heads * hs;
+  const int64_t npast = batch * kv_num_heads * past_len * hs;
+  const int64_t npres = batch * kv_num_heads * total * hs;
+  const int64_t ncs = do_rotary ? max_pos * half_rot : 0;
+  const int64_t nb = attention_bias ? batch * (int64_t)bias_heads * seq * total : 0;
+  if ((!q && nq) || (!k && nkv) || (!v && nkv) || (past_len && (!past_key || !past_value)) ||
+      (do_rotary && (!cos_cache || !sin_cache)) || (!y && nq) ||
+      (npres && (!present_key || !present_value)))
+    return mg_fail(MG_INVALID_ARGUMENT, "GroupQueryAttention: null buffer");
+  if (nq + npres == 0) return MG_OK;
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t oq = s.take(nq * 4), ok = s.take(nkv * 4), ov = s.take(nkv * 4),
+               opk = s.take(npast * 4), opv = s.take(npast * 4), oc = s.take(ncs * 4),
+               osn = s.take(ncs * 4), ob = s.take(nb * 4), oy = s.take(nq * 4),
+               ork = s.take(npres * 4), orv = s.take(npres * 4),
+               oqr = s.take(do_rotary ? nq * 4 : 0);
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  hipStream_t st = ctx->stream;
+  auto up = [&](size_t off, const float *src, int64_t n) -> mg_status {
+    if (n) MG_HIP(hipMemcpyAsync(base + off, src, (size_t)n * 4, hipMemcpyHostToDevice, st));
+    return MG_OK;
+  };
+  MG_TRY(up(oq, q, nq));
+  MG_TRY(up(ok, k, nkv));
+  MG_TRY(up(ov, v, nkv));
+  MG_TRY(up(opk, past_key, npast));
+  MG_TRY(up(opv, past_value, npast));
+  MG_TRY(up(oc, cos_cache, ncs));
+  MG_TRY(up(osn, sin_cache, ncs));
+  MG_TRY(up(ob, attention_bias, nb));
+  auto at = [&](size_t off) { return reinterpret_cast<float *>(base + off); };
+  g.k = at(ok);
+  g.v = at(ov);
+  g.past_k = at(opk);
+  g.past_v = at(opv);
+  g.cos = at(oc);
+  g.sin = at(osn);
+  g.present_k = at(ork);
+  g.present_v = at(orv);
+  MG_TRY(gqa_run(ctx, p, g, at(oq), at(oqr), attention_bias ? at(ob) : nullptr, at(oy)));
+  if (nq) MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)nq * 4, hipMemcpyDeviceToHost, st));
+  if (npres) {
+    MG_HIP(hipMemcpyAsync(present_key, base + ork, (size_t)npres * 4, hipMemcpyDeviceToHost, st));
+    MG_HIP(hipMemcpyAsync(present_value, base + orv, (size_t)npres * 4, hipMemcpyDeviceToHost, st));
+  }
+  MG_HIP(hipStreamSynchronize(st));
+  return MG_OK;
+}
+
+mg_status mg_group_query_attention_dev(
+    mg_ctx *ctx, const float *q_dev, const float *k_dev, const float *v_dev, int64_t batch,
+    int64_t seq, int64_t hidden, int32_t num_heads, int32_t kv_num_heads,
+    const float *past_key_dev, const float *past_value_dev, int64_t past_len,
+    const float *cos_cache_dev, const float *sin_cache_dev, int64_t max_pos, int64_t half_rot,
+    int32_t do_rotary, int32_t rotary_interleaved, const float *attention_bias_dev,
+    int32_t bias_heads, int32_t has_scale, float scale, float softcap, int32_t local_window,
+    float *y_dev, float *present_key_dev, float *present_value_dev) {
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_group_query_attention_dev: null context");
+  GqaArgs a{batch, seq, hidden, num_heads, kv_num_heads, past_len, max_pos, half_rot,
+            do_rotary, rotary_interleaved, bias_heads, attention_bias_dev != nullptr, has_scale,
+            scale, softcap, local_window};
+  mg_attn_problem p;
+  mg_gqa_prep g;
+  MG_TRY(plan_gqa(a, &p, &g));
+  const int64_t nq = batch * seq * hidden;
+  const int64_t npres = batch * kv_num_heads * (past_len + seq) * (hidden / num_heads);
+  if ((past_len && (!past_key_dev || !past_value_dev)) ||
+      (do_rotary && (!cos_cache_dev || !sin_cache_dev)) ||
+      (npres && (!present_key_dev || !present_value_dev)))
+    return mg_fail(MG_INVALID_ARGUMENT, "GroupQueryAttention: null buffer");
+  if (nq + npres == 0) return MG_OK;
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, do_rotary ? nq * 4 : 0));
+  if (do_rotary) MG_TRY(mg_ws_reserve(ctx, (size_t)nq * 4));
+  g.k = k_dev;
+  g.v = v_dev;
+  g.past_k = past_key_dev;
+  g.past_v = past_value_dev;
+  g.cos = cos_cache_dev;
+  g.sin = sin_cache_dev;
+  g.present_k = present_key_dev;
+  g.present_v = present_value_dev;
+  return gqa_run(ctx, p, g, q_dev, do_rotary ? static_cast<float *>(ctx->ws) : nullptr,
+                 attention_bias_dev, y_dev);
+}

@@ -24,6 +24,9 @@
 //     p[s] from the score layout (no data movement); the A operand lane l
 //     reads V[t(s, l / 32)][32 j + l % 32] from the transposed V tile, where
 //     the keys of steps 4g .. 4g + 3 are adjacent (one 16-byte read).
+//   * With causal masking (GroupQueryAttention) key t is -inf for query q
+//     when t > q + causal_off, and a workgroup stops after the last key its
+//     last query sees.
 //   * At the end y = O / l per query; a row whose every score is -inf is NaN
 //     (the reference's exp(-inf - -inf)), and T = 0 gives zeros (an empty
 //     product).
@@ -31,6 +34,7 @@
 // softmax in f64; results agree to fp32 rounding of the different order).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 
@@ -185,9 +189,16 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
   float m_run = -INFINITY, l_run = 0.f;
   float mcur[16];
 
-  if (p.T > 0) {
+  // Keys the workgroup visits: all T, or with causal masking only up to the
+  // last key its last query sees (keys past it are -inf for every query).
+  int t_loop = p.T;
+  if (p.causal) {
+    const int64_t q_last = (int64_t)(blockIdx.x % qtiles) * 128 + 127;
+    t_loop = (int)std::min<int64_t>(p.T, std::max<int64_t>(0, q_last + p.causal_off + 1));
+  }
+  if (t_loop > 0) {
     fetch_any(0, I0{});
-    if (p.T > 32) fetch_any(32, I1{});
+    if (t_loop > 32) fetch_any(32, I1{});
     stage(I0{});
   }
   // Scores in the log2 domain: p = 2^(s * scale * log2 e + mask * log2 e - m).
@@ -202,7 +213,7 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
     using NB = std::integral_constant<int, 1 - B>;
 #pragma unroll
     for (int v = 0; v < 16; v++) mcur[v] = mreg[B][v];
-    if (t0 + 64 < p.T) fetch_any(t0 + 64, bsel);
+    if (t0 + 64 < t_loop) fetch_any(t0 + 64, bsel);
     const bool full = t0 + 32 <= p.T;
     if (active) {
       const float *kl = &ks[B][0];
@@ -225,7 +236,7 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
       for (int v = 0; v < 16; v++) {
         const int tt = 8 * (v >> 2) + (v & 3) + 4 * h;  // key of slot v
         float x = fmaf(sc[v], scale2, mrow ? mcur[v] * kLog2e : 0.f);
-        if (!full && t0 + tt >= p.T) x = -INFINITY;
+        if ((!full && t0 + tt >= p.T) || (p.causal && t0 + tt > q + p.causal_off)) x = -INFINITY;
         pv[v] = x;
         tmax = fmaxf(tmax, x);
       }
@@ -264,12 +275,12 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
           o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s], pv[s], o[j], 0, 0, 0);
       }
     }
-    if (t0 + 32 < p.T) stage(NB{});  // its readers passed the last barrier
+    if (t0 + 32 < t_loop) stage(NB{});  // its readers passed the last barrier
     __syncthreads();
   };
-  for (int t0 = 0; t0 < p.T; t0 += 64) {
+  for (int t0 = 0; t0 < t_loop; t0 += 64) {
     tile(t0, I0{});
-    if (t0 + 32 < p.T) tile(t0 + 32, I1{});
+    if (t0 + 32 < t_loop) tile(t0 + 32, I1{});
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -327,4 +338,71 @@ mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
   else
     launch_dvt<64>(pp, grid, ctx->stream);
   return mg_launch_check("k_attn");
+}
+
+// ------------------------------------------------------ GroupQueryAttention
+
+namespace {
+
+// RoPE of element d of one head row x (lib/src/onnx_ops.dart:2693-2716):
+// computed in double and rounded once to f32, as the reference's
+// Float32List stores of double expressions do.
+__device__ inline float rope(const float *x, int64_t d, int64_t half_rot, const float *c,
+                             const float *sn, int interleaved) {
+  if (d >= 2 * half_rot) return x[d];
+  if (interleaved) {
+    const int64_t i = d >> 1;
+    const double cc = c[i], ss = sn[i];
+    return (d & 1) ? (float)((double)x[d] * cc + (double)x[d - 1] * ss)
+                   : (float)((double)x[d] * cc - (double)x[d + 1] * ss);
+  }
+  if (d < half_rot) {
+    const double cc = c[d], ss = sn[d];
+    return (float)((double)x[d] * cc - (double)x[d + half_rot] * ss);
+  }
+  const int64_t i = d - half_rot;
+  const double cc = c[i], ss = sn[i];
+  return (float)((double)x[d] * cc + (double)x[i] * ss);
+}
+
+// One thread per element of present K/V (both written) and, when rotary,
+// of the rotated Q.  Elements [0, nkv) are the caches, [nkv, nkv + nq) Q.
+__global__ __launch_bounds__(256) void k_gqa_prep(const mg_gqa_prep g, int64_t nkv, int64_t nq) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= nkv + nq) return;
+  const int64_t total = g.past + g.seq;
+  if (idx < nkv) {
+    const int64_t d = idx % g.hs, j = (idx / g.hs) % total, bh = idx / (g.hs * total);
+    const int64_t kvh = bh % g.kv_heads, b = bh / g.kv_heads;
+    if (j < g.past) {
+      const int64_t src = (bh * g.past + j) * g.hs + d;
+      g.present_k[idx] = g.past_k[src];
+      g.present_v[idx] = g.past_v[src];
+    } else {
+      const int64_t s = j - g.past;
+      const int64_t row = (b * g.seq + s) * g.kv_heads * g.hs + kvh * g.hs;
+      g.present_k[idx] = g.rotary ? rope(g.k + row, d, g.half_rot, g.cos + (g.past + s) * g.half_rot,
+                                         g.sin + (g.past + s) * g.half_rot, g.interleaved)
+                                  : g.k[row + d];
+      g.present_v[idx] = g.v[row + d];
+    }
+    return;
+  }
+  const int64_t e = idx - nkv;  // rotated Q, [batch][seq][heads * hs]
+  const int64_t d = e % g.hs, row = e - d;
+  const int64_t s = (e / (g.heads * g.hs)) % g.seq;
+  g.q_rot[e] = rope(g.q + row, d, g.half_rot, g.cos + (g.past + s) * g.half_rot,
+                    g.sin + (g.past + s) * g.half_rot, g.interleaved);
+}
+
+}  // namespace
+
+mg_status mg_gqa_prep_run(mg_ctx *ctx, const mg_gqa_prep &g) {
+  const int64_t nkv = g.batch * g.kv_heads * (g.past + g.seq) * g.hs;
+  const int64_t nq = g.rotary ? g.batch * g.seq * g.heads * g.hs : 0;
+  if (nkv + nq == 0) return MG_OK;
+  const int64_t blocks = (nkv + nq + 255) / 256;
+  if (blocks > 0x7fffffff) return mg_fail(MG_UNSUPPORTED, "GroupQueryAttention: too large");
+  hipLaunchKernelGGL(k_gqa_prep, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, g, nkv, nq);
+  return mg_launch_check("k_gqa_prep");
 }

@@ -235,8 +235,25 @@ struct mg_attn_problem {
   int64_t q_rs, q_cs, k_ts, k_ds, v_ts, v_ds, m_qs, m_ts, y_rs;
   int S, T, D, DV;
   float scale;
+  // Causal masking: key t is excluded for query q when t > q + causal_off.
+  int causal = 0;
+  int64_t causal_off = 0;
 };
 mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p);
+
+// GroupQueryAttention's data movement before the attention products: the
+// present K/V caches [batch][kv_heads][past + seq][hs] (past rows copied,
+// current rows appended, K rotated when rotary) and, when rotary, the
+// rotated Q [batch][seq][heads * hs] into q_rot.  RoPE at positions
+// past + s from cos/sin [max_pos][half_rot], GPT-J pairs when interleaved,
+// else rotate-half; dims past 2 half_rot pass through.
+struct mg_gqa_prep {
+  const float *q, *k, *v, *past_k, *past_v, *cos, *sin;
+  float *q_rot, *present_k, *present_v;
+  int64_t batch, seq, heads, kv_heads, hs, past, half_rot;
+  int rotary, interleaved;
+};
+mg_status mg_gqa_prep_run(mg_ctx *ctx, const mg_gqa_prep &g);
 
 // --------------------------------------------------------------- DQL entry
 

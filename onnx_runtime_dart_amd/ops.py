@@ -11,6 +11,7 @@ defaults and error classes as the reference:
     op_gemm                <- opGemm          lib/src/onnx_ops.dart:2152
     op_fused_sdpa          <- opFusedSDPA     lib/src/onnx_ops.dart:2106
     op_multi_head_attention <- opMultiHeadAttention lib/src/onnx_ops.dart:2019
+    op_group_query_attention <- opGroupQueryAttention lib/src/onnx_ops.dart:1844
     op_conv                <- opConv          lib/src/onnx_nn_ops.dart:179
     op_conv_transpose      <- opConvTranspose lib/src/onnx_nn_ops.dart:818
     op_conv_integer        <- opConvInteger   lib/src/onnx_qlinear_ops.dart:299
@@ -591,6 +592,85 @@ def multi_head_attention_dev(q_ptr: int, k_ptr: int, v_ptr: int, batch: int, seq
                                           int(bias_heads), int(scale is not None),
                                           float(scale if scale is not None else 0.0),
                                           C.c_void_p(y_ptr)))
+
+
+def op_group_query_attention(q, k, v, *, num_heads: int, kv_num_heads: int, scale=None,
+                            do_rotary: bool = False, rotary_interleaved: bool = False,
+                            past_key=None, past_value=None, cos_cache=None, sin_cache=None,
+                            attention_bias=None, softcap: float = 0.0, local_window: int = -1,
+                            ctx: Context | None = None):
+    """opGroupQueryAttention (lib/src/onnx_ops.dart:1844-2012): returns
+    [output, present_key, present_value]."""
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape or \
+            k.shape[:2] != q.shape[:2]:
+        raise ArgumentError("GroupQueryAttention: q, k, v must be [batch, seq, hidden]")
+    batch, seq, hidden = q.shape
+    if num_heads <= 0 or hidden % num_heads:
+        raise ArgumentError("GroupQueryAttention: hidden must be a multiple of num_heads")
+    hs = hidden // num_heads
+    if kv_num_heads <= 0 or k.shape[2] != kv_num_heads * hs:
+        raise ArgumentError("GroupQueryAttention: k and v must be [batch, seq, kv_heads * head_size]")
+    past_len = 0
+    if past_key is not None:
+        past_key = np.ascontiguousarray(past_key, dtype=np.float32)
+        past_value = np.ascontiguousarray(past_value, dtype=np.float32)
+        if past_key.ndim == 4:
+            past_len = past_key.shape[2]
+            if past_key.shape != (batch, kv_num_heads, past_len, hs) or \
+                    past_value.shape != past_key.shape:
+                raise ArgumentError("GroupQueryAttention: past_key / past_value must be "
+                                    "[batch, kv_heads, past, head_size]")
+        else:
+            past_key = past_value = None
+    max_pos = half = 0
+    if do_rotary:
+        if cos_cache is None or sin_cache is None:
+            raise ArgumentError("GroupQueryAttention: do_rotary needs cos_cache and sin_cache")
+        cos_cache = np.ascontiguousarray(cos_cache, dtype=np.float32)
+        sin_cache = np.ascontiguousarray(sin_cache, dtype=np.float32)
+        max_pos, half = cos_cache.shape[0], cos_cache.shape[-1]
+    total = past_len + seq
+    bias_heads = 0
+    if attention_bias is not None:
+        attention_bias = np.ascontiguousarray(attention_bias, dtype=np.float32)
+        if attention_bias.ndim != 4 or attention_bias.shape[0] != batch or \
+                attention_bias.shape[2:] != (seq, total):
+            raise ArgumentError("GroupQueryAttention: attention_bias must be "
+                                "[batch, heads, seq, past + seq]")
+        bias_heads = attention_bias.shape[1]
+    y = np.empty_like(q)
+    pk = np.empty((batch, kv_num_heads, total, hs), np.float32)
+    pv = np.empty_like(pk)
+    ctx = ctx or default_context()
+    check(lib.mg_group_query_attention(
+        ctx.handle, _ptr(q), _ptr(k), _ptr(v), batch, seq, hidden, int(num_heads),
+        int(kv_num_heads), _ptr(past_key), _ptr(past_value), past_len, _ptr(cos_cache),
+        _ptr(sin_cache), max_pos, half, int(bool(do_rotary)), int(bool(rotary_interleaved)),
+        _ptr(attention_bias), bias_heads, int(scale is not None),
+        float(scale if scale is not None else 0.0), float(softcap), int(local_window), _ptr(y),
+        _ptr(pk), _ptr(pv)))
+    return [y, pk, pv]
+
+
+def group_query_attention_dev(q_ptr: int, k_ptr: int, v_ptr: int, batch: int, seq: int,
+                              hidden: int, num_heads: int, kv_num_heads: int, y_ptr: int,
+                              present_key_ptr: int, present_value_ptr: int, *,
+                              past_key_ptr: int = 0, past_value_ptr: int = 0, past_len: int = 0,
+                              cos_ptr: int = 0, sin_ptr: int = 0, max_pos: int = 0,
+                              half_rot: int = 0, do_rotary: bool = False,
+                              rotary_interleaved: bool = False, bias_ptr: int = 0,
+                              bias_heads: int = 0, scale=None, ctx: Context | None = None):
+    """op_group_query_attention on device buffers (asynchronous)."""
+    ctx = ctx or default_context()
+    vp = lambda x: C.c_void_p(x) if x else None  # noqa: E731
+    check(lib.mg_group_query_attention_dev(
+        ctx.handle, vp(q_ptr), vp(k_ptr), vp(v_ptr), batch, seq, hidden, int(num_heads),
+        int(kv_num_heads), vp(past_key_ptr), vp(past_value_ptr), past_len, vp(cos_ptr),
+        vp(sin_ptr), max_pos, half_rot, int(bool(do_rotary)), int(bool(rotary_interleaved)),
+        vp(bias_ptr), bias_heads, int(scale is not None),
+        float(scale if scale is not None else 0.0), 0.0, -1, vp(y_ptr), vp(present_key_ptr),
+        vp(present_value_ptr)))
 
 
 # ------------------------------------------------------------ convolution

@@ -16,6 +16,8 @@ Thin numpy wrappers over ``oracle/lib/liboracle.so`` (built from oracle.c by
 * ``matmul_kernel``        — lib/src/gemm_kernel_simd.dart:32-239
 * ``fused_sdpa``           — lib/src/onnx_ops.dart:2106-2149
 * ``multi_head_attention`` — lib/src/onnx_ops.dart:2019-2098
+* ``group_query_attention`` — lib/src/onnx_ops.dart:1844-2012
+* ``rotary_embedding``     — lib/src/onnx_ops.dart:2659-2722
 * ``conv``                 — lib/src/onnx_nn_ops.dart:179-817 (+ _resolvePads :38-87)
 * ``conv_transpose``       — lib/src/onnx_nn_ops.dart:818-1059
 * ``conv_integer``         — lib/src/onnx_qlinear_ops.dart:232-337
@@ -88,6 +90,11 @@ def _declare(L):
                                            _I, C.c_double, _P]
     L.orc_conv.argtypes = [_P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I,
                            C.c_int32, _P, _P]
+    L.orc_rotary_embedding.argtypes = [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I, _P]
+    L.orc_rotary_embedding.restype = None
+    L.orc_group_query_attention.argtypes = [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P,
+                                            _I64, _P, _P, _I64, _I, _I, _P, _I64, _I,
+                                            C.c_double, _P, _P, _P]
     L.orc_round_even.argtypes = [C.c_double, _P]
     L.orc_round_even.restype = _I64
 
@@ -431,3 +438,53 @@ def qlinear_conv(x, x_scale, x_zp, w, w_scale, w_zp, y_scale, y_zp, bias=None, *
         q = np.rint(s.astype(np.float64) * mult).astype(np.int64) + yz
         out[:, om] = np.clip(q, lo, hi)
     return out
+
+
+# ------------------------------------------------------ GroupQueryAttention
+
+def rotary_embedding(x, positions, cos_cache, sin_cache, *, num_heads, interleaved=False):
+    """opRotaryEmbedding on [batch, seq, heads * hs] with one position row."""
+    x = np.ascontiguousarray(x, np.float32)
+    cos_cache = np.ascontiguousarray(cos_cache, np.float32)
+    sin_cache = np.ascontiguousarray(sin_cache, np.float32)
+    pos = np.ascontiguousarray(np.asarray(positions, np.int64).ravel())
+    b, s, hidden = x.shape
+    out = np.empty_like(x)
+    lib().orc_rotary_embedding(_ptr(x), b, s, num_heads, hidden // num_heads, _ptr(pos),
+                               _ptr(cos_cache), _ptr(sin_cache), cos_cache.shape[-1],
+                               int(interleaved), _ptr(out))
+    return out
+
+
+def group_query_attention(q, k, v, *, num_heads, kv_num_heads, scale=None, do_rotary=False,
+                          rotary_interleaved=False, past_key=None, past_value=None,
+                          cos_cache=None, sin_cache=None, attention_bias=None):
+    """opGroupQueryAttention -> [output, present_key, present_value]."""
+    q, k, v = (np.ascontiguousarray(x, np.float32) for x in (q, k, v))
+    b, s, hidden = q.shape
+    hs = hidden // num_heads
+    past = 0
+    if past_key is not None and np.ndim(past_key) == 4:
+        past_key = np.ascontiguousarray(past_key, np.float32)
+        past_value = np.ascontiguousarray(past_value, np.float32)
+        past = past_key.shape[2]
+    else:
+        past_key = past_value = None
+    half = 0
+    if do_rotary:
+        cos_cache = np.ascontiguousarray(cos_cache, np.float32)
+        sin_cache = np.ascontiguousarray(sin_cache, np.float32)
+        half = cos_cache.shape[-1]
+    bh = 0
+    if attention_bias is not None:
+        attention_bias = np.ascontiguousarray(attention_bias, np.float32)
+        bh = attention_bias.shape[1]
+    out = np.empty_like(q)
+    pk = np.empty((b, kv_num_heads, past + s, hs), np.float32)
+    pv = np.empty_like(pk)
+    _check(lib().orc_group_query_attention(
+        _ptr(q), _ptr(k), _ptr(v), b, s, hidden, num_heads, kv_num_heads, _ptr(past_key),
+        _ptr(past_value), past, _ptr(cos_cache), _ptr(sin_cache), half, int(do_rotary),
+        int(rotary_interleaved), _ptr(attention_bias), bh, int(scale is not None),
+        float(scale or 0.0), _ptr(out), _ptr(pk), _ptr(pv)), "orc_group_query_attention")
+    return [out, pk, pv]

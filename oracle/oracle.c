@@ -603,3 +603,111 @@ int orc_conv(const void *x, int x_kind, const void *w, int w_kind, int64_t n, in
     }
   return ORC_OK;
 }
+
+/* ------------------------------------------------------ GroupQueryAttention */
+
+void orc_rotary_embedding(const float *x, int64_t batch, int64_t seq, int64_t heads,
+                          int64_t hs, const int64_t *pos, const float *cos_cache,
+                          const float *sin_cache, int64_t half_rot, int interleaved,
+                          float *out) {
+  const int64_t rot = 2 * half_rot;
+  for (int64_t b = 0; b < batch; b++)
+    for (int64_t s = 0; s < seq; s++) {
+      const int64_t cb = pos[s] * half_rot;
+      for (int64_t h = 0; h < heads; h++) {
+        const int64_t base = (b * seq + s) * heads * hs + h * hs;
+        if (interleaved) {
+          for (int64_t i = 0; i < rot / 2; i++) {
+            const double c = cos_cache[cb + i], sn = sin_cache[cb + i];
+            const double x0 = x[base + 2 * i], x1 = x[base + 2 * i + 1];
+            out[base + 2 * i] = (float)(x0 * c - x1 * sn);
+            out[base + 2 * i + 1] = (float)(x1 * c + x0 * sn);
+          }
+        } else {
+          const int64_t half = rot / 2;
+          for (int64_t i = 0; i < half; i++) {
+            const double c = cos_cache[cb + i], sn = sin_cache[cb + i];
+            const double x0 = x[base + i], x1 = x[base + i + half];
+            out[base + i] = (float)(x0 * c - x1 * sn);
+            out[base + i + half] = (float)(x1 * c + x0 * sn);
+          }
+        }
+        for (int64_t i = rot; i < hs; i++) out[base + i] = x[base + i];
+      }
+    }
+}
+
+int orc_group_query_attention(const float *q, const float *k, const float *v, int64_t batch,
+                              int64_t seq, int64_t hidden, int64_t heads, int64_t kv_heads,
+                              const float *past_k, const float *past_v, int64_t past_len,
+                              const float *cos_cache, const float *sin_cache, int64_t half_rot,
+                              int do_rotary, int interleaved, const float *bias,
+                              int64_t bias_heads, int has_scale, double scale, float *out,
+                              float *present_k, float *present_v) {
+  if (heads <= 0 || kv_heads <= 0 || heads % kv_heads || hidden % heads)
+    return ORC_INVALID_ARGUMENT;
+  const int64_t hs = hidden / heads, group = heads / kv_heads, kvh_n = kv_heads * hs;
+  const int64_t total = past_len + seq;
+  float *qq = (float *)malloc((size_t)(batch * seq * hidden + 1) * sizeof(float));
+  float *kk = (float *)malloc((size_t)(batch * seq * kvh_n + 1) * sizeof(float));
+  int64_t *pos = (int64_t *)malloc((size_t)(seq + 1) * sizeof(int64_t));
+  float *qh = (float *)malloc((size_t)(seq * hs + 1) * sizeof(float));
+  float *kt = (float *)malloc((size_t)(hs * total + 1) * sizeof(float));
+  float *sc = (float *)malloc((size_t)(seq * total + 1) * sizeof(float));
+  float *cx = (float *)malloc((size_t)(seq * hs + 1) * sizeof(float));
+  if (!qq || !kk || !pos || !qh || !kt || !sc || !cx) {
+    free(qq); free(kk); free(pos); free(qh); free(kt); free(sc); free(cx);
+    return ORC_INVALID_ARGUMENT;
+  }
+  memcpy(qq, q, sizeof(float) * (size_t)(batch * seq * hidden));
+  memcpy(kk, k, sizeof(float) * (size_t)(batch * seq * kvh_n));
+  if (do_rotary) { /* :1876-1896 */
+    for (int64_t s = 0; s < seq; s++) pos[s] = past_len + s;
+    orc_rotary_embedding(q, batch, seq, heads, hs, pos, cos_cache, sin_cache, half_rot,
+                         interleaved, qq);
+    orc_rotary_embedding(k, batch, seq, kv_heads, hs, pos, cos_cache, sin_cache, half_rot,
+                         interleaved, kk);
+  }
+  const double s = has_scale ? scale : 1.0 / sqrt((double)hs);
+  /* present K / V (:1907-1931) */
+  for (int64_t b = 0; b < batch; b++)
+    for (int64_t kvh = 0; kvh < kv_heads; kvh++) {
+      const int64_t base = (b * kv_heads + kvh) * total * hs;
+      for (int64_t j = 0; j < past_len; j++)
+        for (int64_t d = 0; d < hs; d++) {
+          const int64_t src = ((b * kv_heads + kvh) * past_len + j) * hs + d;
+          present_k[base + j * hs + d] = past_k[src];
+          present_v[base + j * hs + d] = past_v[src];
+        }
+      for (int64_t j = 0; j < seq; j++)
+        for (int64_t d = 0; d < hs; d++) {
+          const int64_t src = (b * seq + j) * kvh_n + kvh * hs + d;
+          present_k[base + (past_len + j) * hs + d] = kk[src];
+          present_v[base + (past_len + j) * hs + d] = v[src];
+        }
+    }
+  for (int64_t b = 0; b < batch; b++)
+    for (int64_t h = 0; h < heads; h++) {
+      const int64_t kvh = h / group;
+      const int64_t base = (b * kv_heads + kvh) * total * hs;
+      for (int64_t i = 0; i < seq; i++)
+        for (int64_t d = 0; d < hs; d++)
+          qh[i * hs + d] = qq[(b * seq + i) * hidden + h * hs + d];
+      for (int64_t j = 0; j < total; j++)
+        for (int64_t d = 0; d < hs; d++) kt[d * total + j] = present_k[base + j * hs + d];
+      orc_matmul_kernel(qh, kt, sc, seq, hs, total); /* :1952 */
+      const int64_t bb = bias ? (b * bias_heads + (h % bias_heads)) * seq * total : 0;
+      for (int64_t i = 0; i < seq; i++) { /* :1956-1981 */
+        float *row = sc + i * total;
+        const int64_t last = past_len + i;
+        softmax_row(row, last + 1, s, bias ? bias + bb + i * total : NULL, 1, 0);
+        for (int64_t j = last + 1; j < total; j++) row[j] = 0.f;
+      }
+      orc_matmul_kernel(sc, present_v + base, cx, seq, total, hs); /* :1985-1995 */
+      for (int64_t i = 0; i < seq; i++)
+        for (int64_t d = 0; d < hs; d++)
+          out[(b * seq + i) * hidden + h * hs + d] = cx[i * hs + d];
+    }
+  free(qq); free(kk); free(pos); free(qh); free(kt); free(sc); free(cx);
+  return ORC_OK;
+}

@@ -100,6 +100,28 @@ int orc_multi_head_attention(const float *q, const float *k, const float *v,
                              int64_t bias_heads, int has_scale, double scale,
                              float *out);
 
+/* opRotaryEmbedding, lib/src/onnx_ops.dart:2659-2722, for a [batch, seq,
+ * heads * hs] input at positions pos[seq] (one row shared by the batch):
+ * the first 2 half_rot dims of every head rotated (GPT-J pairs when
+ * interleaved, else rotate-half) in double, stored as f32; the tail copied. */
+void orc_rotary_embedding(const float *x, int64_t batch, int64_t seq, int64_t heads,
+                          int64_t hs, const int64_t *pos, const float *cos_cache,
+                          const float *sin_cache, int64_t half_rot, int interleaved,
+                          float *out);
+
+/* opGroupQueryAttention, lib/src/onnx_ops.dart:1844-2012: optional RoPE of
+ * q and k at positions past_len + s; present K/V = past followed by the
+ * current (rotated) K / raw V; per query head h (KV head h / group) the
+ * gathered Q.K^T (matmulKernel), scale + bias (head h % bias_heads), a
+ * softmax over keys 0 .. past_len + i only (the rest 0), then . V. */
+int orc_group_query_attention(const float *q, const float *k, const float *v, int64_t batch,
+                              int64_t seq, int64_t hidden, int64_t heads, int64_t kv_heads,
+                              const float *past_k, const float *past_v, int64_t past_len,
+                              const float *cos_cache, const float *sin_cache, int64_t half_rot,
+                              int do_rotary, int interleaved, const float *bias,
+                              int64_t bias_heads, int has_scale, double scale, float *out,
+                              float *present_k, float *present_v);
+
 /* Convolution sums, direct loops over (channel, tap) per output element,
  * spatial dims right-aligned in 3 slots.  kind 0 = f32, 1 = u8, 2 = i8.
  *   trans = 0 (opConv, lib/src/onnx_nn_ops.dart:179-817, and _convIntAcc,

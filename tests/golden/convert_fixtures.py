@@ -45,6 +45,10 @@ HOT_PATH = [
     "einsum_matmul",
     "mha_with_bias",
     "mha_no_bias",
+    "gqa_causal",
+    "gqa_kvcache",
+    "gqa_kvcache_bias",
+    "gqa_kvcache_rotary",
     "conv1d",
     "conv2d_basic",
     "conv2d_bias",

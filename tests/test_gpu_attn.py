@@ -131,3 +131,109 @@ def test_attention_errors(ops):
     with pytest.raises(UnsupportedError):  # bias heads neither 1 nor num_heads
         ops.op_multi_head_attention(z((1, 2, 16)), z((1, 3, 16)), z((1, 3, 16)),
                                     z((1, 2, 2, 3)), num_heads=4)
+
+
+# ------------------------------------------------------ GroupQueryAttention
+
+
+@pytest.mark.parametrize("name", G.names("gqa"))
+def test_gqa_fixture(ops, name):
+    d = G.load(name)
+    x, at = d["arrays"], d["attrs"]
+
+    def g(i):
+        return x[i] if len(x) > i else None
+    outs = ops.op_group_query_attention(
+        x[0], x[1], x[2], num_heads=at["num_heads"], kv_num_heads=at["kv_num_heads"],
+        scale=at.get("scale"), do_rotary=bool(at.get("do_rotary", 0)),
+        rotary_interleaved=bool(at.get("rotary_interleaved", 0)), past_key=g(3),
+        past_value=g(4), cos_cache=g(7), sin_cache=g(8), attention_bias=g(10))
+    for name_out, y in zip(d["outputs"], outs):
+        if name_out in d["want"]:
+            G.assert_reference_parity(y, d["want"][name_out], f"{name}/{name_out}",
+                                      tolerance=1e-4)
+
+
+GQA = [
+    # batch, seq, heads, kv heads, head size, past, rotary, interleaved, half_rot, bias heads
+    (2, 1, 32, 8, 64, 100, True, False, 32, 0),     # Llama-style decode step
+    (1, 130, 16, 4, 64, 0, True, False, 32, 0),     # causal prefill, ragged query tiles
+    (1, 37, 12, 12, 32, 20, False, False, 0, 12),   # no groups, bias per head
+    (3, 5, 8, 2, 128, 7, True, True, 32, 1),        # GPT-J pairs, partial rotary, shared bias
+    (1, 64, 14, 2, 64, 0, True, False, 32, 0),      # group of 7
+    (1, 300, 4, 1, 16, 33, False, False, 0, 0),     # long causal with past
+]
+
+
+@pytest.mark.parametrize("b,s,h,kv,hs,past,rot,inter,half,bh", GQA)
+def test_gqa_against_oracle(ops, b, s, h, kv, hs, past, rot, inter, half, bh):
+    rng = np.random.default_rng(b * 1000 + s * 10 + h + past)
+    q = rng.standard_normal((b, s, h * hs)).astype(np.float32)
+    k = rng.standard_normal((b, s, kv * hs)).astype(np.float32)
+    v = rng.standard_normal((b, s, kv * hs)).astype(np.float32)
+    pk = rng.standard_normal((b, kv, past, hs)).astype(np.float32) if past else None
+    pv = rng.standard_normal((b, kv, past, hs)).astype(np.float32) if past else None
+    kw = dict(num_heads=h, kv_num_heads=kv, past_key=pk, past_value=pv)
+    if rot:
+        theta = rng.uniform(0, 6.3, (past + s + 5, half))
+        kw.update(do_rotary=True, rotary_interleaved=inter,
+                  cos_cache=np.cos(theta).astype(np.float32),
+                  sin_cache=np.sin(theta).astype(np.float32))
+    if bh:
+        bias = rng.standard_normal((b, bh, s, past + s)).astype(np.float32)
+        bias[bias < -1.8] = -10000.0
+        kw["attention_bias"] = bias
+    y, prk, prv = ops.op_group_query_attention(q, k, v, **kw)
+    ry, rk, rv = oracle.group_query_attention(q, k, v, **kw)
+    assert G.rms_error(y, ry) <= TOL, G.rms_error(y, ry)
+    np.testing.assert_array_equal(prk, rk)  # copies and the double-then-f32 RoPE: exact
+    np.testing.assert_array_equal(prv, rv)
+
+
+def test_gqa_device_entry_point_matches_host(ops):
+    rng = np.random.default_rng(31)
+    b, s, h, kv, hs, past = 1, 9, 8, 2, 64, 4
+    q = rng.standard_normal((b, s, h * hs)).astype(np.float32)
+    k = rng.standard_normal((b, s, kv * hs)).astype(np.float32)
+    v = rng.standard_normal((b, s, kv * hs)).astype(np.float32)
+    pk = rng.standard_normal((b, kv, past, hs)).astype(np.float32)
+    pv = rng.standard_normal((b, kv, past, hs)).astype(np.float32)
+    theta = rng.uniform(0, 6.3, (32, 32))
+    cos, sin = np.cos(theta).astype(np.float32), np.sin(theta).astype(np.float32)
+    y, prk, prv = ops.op_group_query_attention(q, k, v, num_heads=h, kv_num_heads=kv,
+                                               past_key=pk, past_value=pv, do_rotary=True,
+                                               cos_cache=cos, sin_cache=sin)
+    D = ops.DeviceBuffer
+    bufs = [D.from_array(a) for a in (q, k, v, pk, pv, cos, sin)]
+    yd, kd, vd = D(y.nbytes), D(prk.nbytes), D(prv.nbytes)
+    ops.group_query_attention_dev(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, b, s, h * hs, h, kv,
+                                  yd.ptr, kd.ptr, vd.ptr, past_key_ptr=bufs[3].ptr,
+                                  past_value_ptr=bufs[4].ptr, past_len=past, cos_ptr=bufs[5].ptr,
+                                  sin_ptr=bufs[6].ptr, max_pos=32, half_rot=32, do_rotary=True)
+    np.testing.assert_array_equal(yd.to_array(y.shape, np.float32), y)
+    np.testing.assert_array_equal(kd.to_array(prk.shape, np.float32), prk)
+    np.testing.assert_array_equal(vd.to_array(prv.shape, np.float32), prv)
+    for x in bufs + [yd, kd, vd]:
+        x.free()
+
+
+def test_gqa_errors(ops):
+    from onnx_runtime_dart_amd.errors import ArgumentError, UnsupportedError
+    q = np.zeros((1, 3, 64), np.float32)
+    k = np.zeros((1, 3, 32), np.float32)
+    with pytest.raises(UnsupportedError):
+        ops.op_group_query_attention(q, k, k, num_heads=4, kv_num_heads=2, softcap=5.0)
+    with pytest.raises(UnsupportedError):
+        ops.op_group_query_attention(q, k, k, num_heads=4, kv_num_heads=2, local_window=2)
+    with pytest.raises(UnsupportedError):
+        ops.op_group_query_attention(q, k, k, num_heads=4, kv_num_heads=2,
+                                     attention_bias=np.zeros((1, 2, 3, 3), np.float32))
+    with pytest.raises(ArgumentError):  # cos cache shorter than past + seq
+        ops.op_group_query_attention(q, k, k, num_heads=4, kv_num_heads=2, do_rotary=True,
+                                     cos_cache=np.ones((2, 4), np.float32),
+                                     sin_cache=np.zeros((2, 4), np.float32))
+    with pytest.raises(UnsupportedError):  # head size 256
+        ops.op_group_query_attention(np.zeros((1, 2, 512), np.float32),
+                                     np.zeros((1, 2, 256), np.float32),
+                                     np.zeros((1, 2, 256), np.float32), num_heads=2,
+                                     kv_num_heads=1)

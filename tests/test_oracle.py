@@ -62,6 +62,15 @@ def _run_fixture(d):
         bias = x[5] if len(x) > 5 else None
         return {d["outputs"][0]: oracle.multi_head_attention(
             x[0], x[1], x[2], bias, num_heads=at["num_heads"], scale=at.get("scale"))}
+    if op == "GroupQueryAttention":
+        def g(i):
+            return x[i] if len(x) > i else None
+        outs = oracle.group_query_attention(
+            x[0], x[1], x[2], num_heads=at["num_heads"], kv_num_heads=at["kv_num_heads"],
+            scale=at.get("scale"), do_rotary=bool(at.get("do_rotary", 0)),
+            rotary_interleaved=bool(at.get("rotary_interleaved", 0)), past_key=g(3),
+            past_value=g(4), cos_cache=g(7), sin_cache=g(8), attention_bias=g(10))
+        return dict(zip(d["outputs"], outs))
     geo = dict(strides=at.get("strides"), pads=at.get("pads"), dilations=at.get("dilations"),
                group=at.get("group", 1))
     if op == "Conv":
@@ -542,3 +551,79 @@ def test_qlinear_conv_requant_rounds_half_to_even():
     y = oracle.qlinear_conv(x, np.float32(0.5), np.uint8(0), w, np.float32(1.0), np.int8(0),
                             np.float32(1.0), np.int8(-127), lo=-128, hi=127)
     np.testing.assert_array_equal(y.ravel(), [-127, -126, -125, -125, -123])
+
+
+# ------------------------------------------------------ GroupQueryAttention
+
+
+def _gqa_inputs(rng, b, s, heads, kv, hs, past=0):
+    q = rng.standard_normal((b, s, heads * hs)).astype(np.float32)
+    k = rng.standard_normal((b, s, kv * hs)).astype(np.float32)
+    v = rng.standard_normal((b, s, kv * hs)).astype(np.float32)
+    pk = rng.standard_normal((b, kv, past, hs)).astype(np.float32) if past else None
+    pv = rng.standard_normal((b, kv, past, hs)).astype(np.float32) if past else None
+    return q, k, v, pk, pv
+
+
+def test_gqa_without_groups_or_past_is_causal_mha():
+    rng = np.random.default_rng(21)
+    q, k, v, _, _ = _gqa_inputs(rng, 2, 7, 3, 3, 8)
+    y = oracle.group_query_attention(q, k, v, num_heads=3, kv_num_heads=3)[0]
+    causal = np.triu(np.full((7, 7), -np.inf, np.float32), 1)
+    bias = np.broadcast_to(causal, (2, 1, 7, 7)).copy()
+    want = oracle.multi_head_attention(q, k, v, bias, num_heads=3)
+    np.testing.assert_allclose(y, want, rtol=1e-6, atol=1e-6)
+
+
+def test_gqa_groups_equal_repeated_kv_heads():
+    rng = np.random.default_rng(22)
+    q, k, v, pk, pv = _gqa_inputs(rng, 1, 4, 8, 2, 16, past=3)
+    y, prk, prv = oracle.group_query_attention(q, k, v, num_heads=8, kv_num_heads=2,
+                                               past_key=pk, past_value=pv)
+    rep = lambda t: np.repeat(t.reshape(1, 4, 2, 16), 4, axis=2).reshape(1, 4, 128)  # noqa
+    rep_p = lambda t: np.repeat(t, 4, axis=1)  # noqa: E731
+    y2 = oracle.group_query_attention(q, rep(k), rep(v), num_heads=8, kv_num_heads=8,
+                                      past_key=rep_p(pk), past_value=rep_p(pv))[0]
+    np.testing.assert_array_equal(y, y2)
+    np.testing.assert_array_equal(prk[:, :, :3], pk)
+    np.testing.assert_array_equal(prk[:, :, 3:], k.reshape(1, 4, 2, 16).transpose(0, 2, 1, 3))
+    np.testing.assert_array_equal(prv[:, :, 3:], v.reshape(1, 4, 2, 16).transpose(0, 2, 1, 3))
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rotary_is_a_complex_rotation(interleaved):
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((2, 3, 2 * 10)).astype(np.float32)  # 2 heads of 10
+    theta = rng.uniform(-3, 3, (9, 3))  # rotary dims 6 of 10
+    cos, sin = np.cos(theta).astype(np.float32), np.sin(theta).astype(np.float32)
+    pos = [4, 0, 8]
+    y = oracle.rotary_embedding(x, pos, cos, sin, num_heads=2, interleaved=interleaved)
+    xh = x.reshape(2, 3, 2, 10).astype(np.float64)
+    want = xh.copy()
+    c = cos[pos].astype(np.float64)[None, :, None, :]
+    s_ = sin[pos].astype(np.float64)[None, :, None, :]
+    if interleaved:
+        x0, x1 = xh[..., 0:6:2], xh[..., 1:6:2]
+        want[..., 0:6:2], want[..., 1:6:2] = x0 * c - x1 * s_, x1 * c + x0 * s_
+    else:
+        x0, x1 = xh[..., 0:3], xh[..., 3:6]
+        want[..., 0:3], want[..., 3:6] = x0 * c - x1 * s_, x1 * c + x0 * s_
+    np.testing.assert_array_equal(y, want.astype(np.float32).reshape(2, 3, 20))
+
+
+def test_gqa_decode_step_continues_the_prefill():
+    """Prefill of 6 tokens == prefill of 5, then one decode step with the
+    present cache as the past (causal attention, RoPE at the absolute
+    position)."""
+    rng = np.random.default_rng(24)
+    q, k, v, _, _ = _gqa_inputs(rng, 1, 6, 4, 2, 8)
+    cos = rng.uniform(-1, 1, (16, 4)).astype(np.float32)
+    sin = rng.uniform(-1, 1, (16, 4)).astype(np.float32)
+    kw = dict(num_heads=4, kv_num_heads=2, do_rotary=True, cos_cache=cos, sin_cache=sin)
+    full = oracle.group_query_attention(q, k, v, **kw)
+    head = oracle.group_query_attention(q[:, :5], k[:, :5], v[:, :5], **kw)
+    step = oracle.group_query_attention(q[:, 5:], k[:, 5:], v[:, 5:], past_key=head[1],
+                                        past_value=head[2], **kw)
+    np.testing.assert_allclose(step[0], full[0][:, 5:], rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(step[1], full[1])
+    np.testing.assert_allclose(head[0], full[0][:, :5], rtol=1e-6, atol=1e-6)
