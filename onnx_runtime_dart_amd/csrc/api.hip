@@ -1171,12 +1171,14 @@ mg_status run_attn_host(mg_ctx *ctx, mg_attn_problem p, const float *q, int64_t 
     return mg_fail(MG_INVALID_ARGUMENT, "attention: null buffer");
   MG_TRY(mg_use_device(ctx));
   Staging s;
+  const size_t pb = mg_attn_plan_split(ctx, &p);
   const size_t oq = s.take((size_t)nq * 4), ok = s.take((size_t)nk * 4),
                ov = s.take((size_t)nv * 4), om = s.take((size_t)nm * 4),
-               oy = s.take((size_t)ny * 4);
+               oy = s.take((size_t)ny * 4), opart = s.take(pb);
   MG_TRY(mg_check_control(ctx, (int64_t)s.off));
   MG_TRY(mg_ws_reserve(ctx, s.off));
   char *base = static_cast<char *>(ctx->ws);
+  if (pb) p.part = reinterpret_cast<float *>(base + opart);
   hipStream_t st = ctx->stream;
   if (nq) MG_HIP(hipMemcpyAsync(base + oq, q, (size_t)nq * 4, hipMemcpyHostToDevice, st));
   if (nk) MG_HIP(hipMemcpyAsync(base + ok, k, (size_t)nk * 4, hipMemcpyHostToDevice, st));
@@ -1223,7 +1225,12 @@ mg_status mg_fused_sdpa_dev(mg_ctx *ctx, const float *a_dev, const int64_t *a_sh
                    scale, &p, &ny));
   if (ny == 0) return MG_OK;
   MG_TRY(mg_use_device(ctx));
-  MG_TRY(mg_check_control(ctx, 0));
+  const size_t pb = mg_attn_plan_split(ctx, &p);
+  MG_TRY(mg_check_control(ctx, (int64_t)pb));
+  if (pb) {
+    MG_TRY(mg_ws_reserve(ctx, pb));
+    p.part = static_cast<float *>(ctx->ws);
+  }
   p.q = a_dev;
   p.k = b_dev;
   p.v = v_dev;
@@ -1259,7 +1266,12 @@ mg_status mg_multi_head_attention_dev(mg_ctx *ctx, const float *q_dev, const flo
                   has_scale, scale, &p));
   if (batch * seq * hidden == 0) return MG_OK;
   MG_TRY(mg_use_device(ctx));
-  MG_TRY(mg_check_control(ctx, 0));
+  const size_t pb = mg_attn_plan_split(ctx, &p);
+  MG_TRY(mg_check_control(ctx, (int64_t)pb));
+  if (pb) {
+    MG_TRY(mg_ws_reserve(ctx, pb));
+    p.part = static_cast<float *>(ctx->ws);
+  }
   p.q = q_dev;
   p.k = k_dev;
   p.v = v_dev;
@@ -1737,6 +1749,36 @@ mg_status plan_gqa(const GqaArgs &a, mg_attn_problem *p, mg_gqa_prep *g) {
   g->rotary = a.rotary;
   g->interleaved = a.interleaved;
   *p = mg_attn_problem{};
+  if (a.seq == 1) {
+    // One query per head (a decode step): it sees every key, so the group's
+    // query heads become the rows of one problem per (batch, KV head) and
+    // read that KV head's keys once.
+    p->nbd = 2;
+    p->bdim[0] = a.batch;
+    p->bdim[1] = a.kv;
+    p->q_bs[0] = p->y_bs[0] = a.hidden;
+    p->q_bs[1] = p->y_bs[1] = group * hs;
+    p->k_bs[0] = p->v_bs[0] = a.kv * total * hs;
+    p->k_bs[1] = p->v_bs[1] = total * hs;
+    p->q_rs = p->y_rs = hs;
+    p->q_cs = 1;
+    p->k_ts = p->v_ts = hs;
+    p->k_ds = p->v_ds = 1;
+    if (a.has_bias) {
+      const bool one = a.bias_heads == 1;
+      p->m_bs[0] = a.bias_heads * total;
+      p->m_bs[1] = one ? 0 : group * total;
+      p->m_qs = one ? 0 : total;
+      p->m_ts = 1;
+    }
+    p->S = (int)group;
+    p->T = (int)total;
+    p->D = p->DV = (int)hs;
+    p->scale = a.has_scale ? a.scale : (float)(1.0 / std::sqrt((double)hs));
+    if (total > 0x7fffffff || !fits_lane_offsets(*p))
+      return mg_fail(MG_UNSUPPORTED, "GroupQueryAttention: dimensions too large");
+    return MG_OK;
+  }
   // Batch dims (batch, kv head, query head of the group): query head
   // h = kvh * group + j shares KV head kvh (stride 0 over j).
   p->nbd = 3;
@@ -1815,6 +1857,8 @@ mg_status mg_group_query_attention(
   if (nq + npres == 0) return MG_OK;
   MG_TRY(mg_use_device(ctx));
   Staging s;
+  const size_t pb = mg_attn_plan_split(ctx, &p);
+  const size_t opart = s.take(pb);
   const size_t oq = s.take(nq * 4), ok = s.take(nkv * 4), ov = s.take(nkv * 4),
                opk = s.take(npast * 4), opv = s.take(npast * 4), oc = s.take(ncs * 4),
                osn = s.take(ncs * 4), ob = s.take(nb * 4), oy = s.take(nq * 4),
@@ -1837,6 +1881,7 @@ mg_status mg_group_query_attention(
   MG_TRY(up(osn, sin_cache, ncs));
   MG_TRY(up(ob, attention_bias, nb));
   auto at = [&](size_t off) { return reinterpret_cast<float *>(base + off); };
+  if (pb) p.part = at(opart);
   g.k = at(ok);
   g.v = at(ov);
   g.past_k = at(opk);
@@ -1879,8 +1924,11 @@ mg_status mg_group_query_attention_dev(
     return mg_fail(MG_INVALID_ARGUMENT, "GroupQueryAttention: null buffer");
   if (nq + npres == 0) return MG_OK;
   MG_TRY(mg_use_device(ctx));
-  MG_TRY(mg_check_control(ctx, do_rotary ? nq * 4 : 0));
-  if (do_rotary) MG_TRY(mg_ws_reserve(ctx, (size_t)nq * 4));
+  const size_t pb = mg_attn_plan_split(ctx, &p);
+  const size_t qrot_bytes = do_rotary ? mg_align((size_t)nq * 4) : 0;
+  MG_TRY(mg_check_control(ctx, (int64_t)(qrot_bytes + pb)));
+  if (qrot_bytes + pb) MG_TRY(mg_ws_reserve(ctx, qrot_bytes + pb));
+  if (pb) p.part = reinterpret_cast<float *>(static_cast<char *>(ctx->ws) + qrot_bytes);
   g.k = k_dev;
   g.v = v_dev;
   g.past_k = past_key_dev;

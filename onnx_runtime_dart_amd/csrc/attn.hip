@@ -191,14 +191,17 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
 
   // Keys the workgroup visits: all T, or with causal masking only up to the
   // last key its last query sees (keys past it are -inf for every query).
-  int t_loop = p.T;
+  // With a key split (p.kc > 0) the workgroup takes keys [t_begin,
+  // t_begin + kc) of split blockIdx.y and writes partial results.
+  const int t_begin = p.kc > 0 ? (int)blockIdx.y * p.kc : 0;
+  int t_loop = p.kc > 0 ? std::min(p.T, t_begin + p.kc) : p.T;
   if (p.causal) {
     const int64_t q_last = (int64_t)(blockIdx.x % qtiles) * 128 + 127;
-    t_loop = (int)std::min<int64_t>(p.T, std::max<int64_t>(0, q_last + p.causal_off + 1));
+    t_loop = (int)std::min<int64_t>(t_loop, std::max<int64_t>(0, q_last + p.causal_off + 1));
   }
-  if (t_loop > 0) {
-    fetch_any(0, I0{});
-    if (t_loop > 32) fetch_any(32, I1{});
+  if (t_loop > t_begin) {
+    fetch_any(t_begin, I0{});
+    if (t_loop > t_begin + 32) fetch_any(t_begin + 32, I1{});
     stage(I0{});
   }
   // Scores in the log2 domain: p = 2^(s * scale * log2 e + mask * log2 e - m).
@@ -278,13 +281,28 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
     if (t0 + 32 < t_loop) stage(NB{});  // its readers passed the last barrier
     __syncthreads();
   };
-  for (int t0 = 0; t0 < t_loop; t0 += 64) {
+  for (int t0 = t_begin; t0 < t_loop; t0 += 64) {
     tile(t0, I0{});
     if (t0 + 32 < t_loop) tile(t0 + 32, I1{});
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   if (!active || !qok) return;
+  if (p.part) {
+    // Partial of this key split: unnormalised O, the running max (log2
+    // domain) and the sum, [split][batch index][query][DV + 2].
+    float *pr = p.part + (((int64_t)blockIdx.y * (gridDim.x / qtiles) + bi) * p.S + q) *
+                             (p.DV + 2);
+#pragma unroll
+    for (int j = 0; j < DVT; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int dv = 32 * j + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (dv < p.DV) pr[dv] = o[j][v];
+      }
+    if (h == 0) pr[p.DV] = m_run, pr[p.DV + 1] = l_tot;
+    return;
+  }
   float inv;
   if (p.T == 0)
     inv = 0.f;  // empty softmax: the product is a sum over no keys
@@ -300,6 +318,62 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
       const int dv = 32 * j + 8 * (v >> 2) + 4 * h + (v & 3);
       if (dv < p.DV) yr[dv] = p.T == 0 ? 0.f : o[j][v] * inv;
     }
+}
+
+// Merges the key splits of each (batch index, query): with M the largest
+// split max, y = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c; every score
+// -inf gives NaN, as without splits.  One thread per output element.
+__global__ __launch_bounds__(256) void k_attn_combine(const mg_attn_problem p, int nsplit,
+                                                      int64_t nbatch) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= nbatch * p.S * p.DV) return;
+  const int dv = (int)(idx % p.DV);
+  const int64_t row = idx / p.DV;  // bi * S + q
+  const int q = (int)(row % p.S);
+  const int64_t bi = row / p.S;
+  // Eight splits per step with independent loads (a loop of one load per
+  // split would wait out the memory latency once per split).
+  const float *p0 = p.part + row * (p.DV + 2);
+  const int64_t cs = nbatch * p.S * (p.DV + 2);  // stride between splits
+  float M = -INFINITY;
+  int c = 0;
+  for (; c + 8 <= nsplit; c += 8) {
+    float mm[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) mm[u] = p0[(c + u) * cs + p.DV];
+#pragma unroll
+    for (int u = 0; u < 8; u++) M = fmaxf(M, mm[u]);
+  }
+  for (; c < nsplit; c++) M = fmaxf(M, p0[c * cs + p.DV]);
+  float num = 0.f, den = 0.f;
+  if (M != -INFINITY) {
+    auto add = [&](float m, float o, float l) {
+      const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+      num = fmaf(w, o, num);
+      den = fmaf(w, l, den);
+    };
+    c = 0;
+    for (; c + 8 <= nsplit; c += 8) {
+      float mm[8], oo[8], ll[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const float *pr = p0 + (c + u) * cs;
+        mm[u] = pr[p.DV], oo[u] = pr[dv], ll[u] = pr[p.DV + 1];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) add(mm[u], oo[u], ll[u]);
+    }
+    for (; c < nsplit; c++) {
+      const float *pr = p0 + c * cs;
+      add(pr[p.DV], pr[dv], pr[p.DV + 1]);
+    }
+  }
+  int64_t oy = 0, rem = bi;
+  for (int d = p.nbd - 1; d >= 0; d--) {
+    oy += (rem % p.bdim[d]) * p.y_bs[d];
+    rem /= p.bdim[d];
+  }
+  p.y[oy + (int64_t)q * p.y_rs + dv] = M == -INFINITY ? __builtin_nanf("") : num / den;
 }
 
 template <int DS>
@@ -324,7 +398,9 @@ mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
   if (nbatch == 0 || p.S == 0 || p.DV == 0) return MG_OK;
   const int64_t wgs = nbatch * ((p.S + 127) / 128);
   if (wgs > 0x7fffffff) return mg_fail(MG_UNSUPPORTED, "attention: grid too large");
-  const dim3 grid((unsigned)wgs);
+  const int nsplit = p.kc > 0 ? (p.T + p.kc - 1) / p.kc : 1;
+  if (p.kc > 0 && !p.part) return mg_fail(MG_INVALID_ARGUMENT, "attention: no partial buffer");
+  const dim3 grid((unsigned)wgs, (unsigned)nsplit);
   mg_attn_problem pp = p;
   if (p.D == 0) {  // no products: the kernel's (masked-off) Q and K loads read V instead
     pp.q = pp.k = p.v;
@@ -337,7 +413,35 @@ mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
     launch_dvt<32>(pp, grid, ctx->stream);
   else
     launch_dvt<64>(pp, grid, ctx->stream);
-  return mg_launch_check("k_attn");
+  MG_TRY(mg_launch_check("k_attn"));
+  if (p.kc > 0) {
+    const int64_t n = nbatch * p.S * p.DV;
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       ctx->stream, pp, nsplit, nbatch);
+    MG_TRY(mg_launch_check("k_attn_combine"));
+  }
+  return MG_OK;
+}
+
+// Key split for grids that leave the CUs idle (decode-like shapes: few
+// queries, many keys): about two workgroups per CU,
+// splits of at least 64 keys (a multiple of 32).  Sets p->kc and returns the
+// bytes of the partial buffer the caller provides in p->part (0 = no split).
+size_t mg_attn_plan_split(const mg_ctx *ctx, mg_attn_problem *p) {
+  p->kc = 0;
+  int64_t nbatch = 1;
+  for (int d = 0; d < p->nbd; d++) nbatch *= p->bdim[d];
+  const int64_t wgs = nbatch * ((p->S + 127) / 128);
+  // Causal problems are not split: their early query tiles would leave most
+  // splits empty while the combine pass still reads them all.
+  if (wgs == 0 || p->T < 128 || p->DV == 0 || p->causal || wgs >= ctx->num_cus) return 0;
+  const int64_t want = std::min<int64_t>((2 * ctx->num_cus + wgs - 1) / wgs, (p->T + 63) / 64);
+  if (want < 2) return 0;
+  const int64_t kc = ((p->T + want - 1) / want + 31) / 32 * 32;
+  const int64_t nsplit = (p->T + kc - 1) / kc;
+  if (nsplit < 2) return 0;
+  p->kc = (int)kc;
+  return (size_t)(nsplit * nbatch * p->S * (p->DV + 2)) * 4;
 }
 
 // ------------------------------------------------------ GroupQueryAttention
@@ -365,44 +469,66 @@ __device__ inline float rope(const float *x, int64_t d, int64_t half_rot, const 
   return (float)((double)x[d] * cc + (double)x[i] * ss);
 }
 
-// One thread per element of present K/V (both written) and, when rotary,
-// of the rotated Q.  Elements [0, nkv) are the caches, [nkv, nkv + nq) Q.
+// One thread per VEC consecutive elements (along the head dim) of present
+// K/V (both written) and, when rotary, of the rotated Q.  Groups [0, nkv)
+// are the caches, [nkv, nkv + nq) Q.  VEC = 4 needs head_size % 4 == 0 and
+// 16-byte aligned tensors (checked by the host): the cache copies are then
+// 16-byte loads and stores.
+template <int VEC>
 __global__ __launch_bounds__(256) void k_gqa_prep(const mg_gqa_prep g, int64_t nkv, int64_t nq) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= nkv + nq) return;
   const int64_t total = g.past + g.seq;
   if (idx < nkv) {
-    const int64_t d = idx % g.hs, j = (idx / g.hs) % total, bh = idx / (g.hs * total);
+    const int64_t e = idx * VEC;
+    const int64_t d = e % g.hs, j = (e / g.hs) % total, bh = e / (g.hs * total);
     const int64_t kvh = bh % g.kv_heads, b = bh / g.kv_heads;
     if (j < g.past) {
       const int64_t src = (bh * g.past + j) * g.hs + d;
-      g.present_k[idx] = g.past_k[src];
-      g.present_v[idx] = g.past_v[src];
+      if (VEC == 4) {
+        *reinterpret_cast<float4 *>(g.present_k + e) = *reinterpret_cast<const float4 *>(g.past_k + src);
+        *reinterpret_cast<float4 *>(g.present_v + e) = *reinterpret_cast<const float4 *>(g.past_v + src);
+      } else {
+        g.present_k[e] = g.past_k[src];
+        g.present_v[e] = g.past_v[src];
+      }
     } else {
       const int64_t s = j - g.past;
       const int64_t row = (b * g.seq + s) * g.kv_heads * g.hs + kvh * g.hs;
-      g.present_k[idx] = g.rotary ? rope(g.k + row, d, g.half_rot, g.cos + (g.past + s) * g.half_rot,
-                                         g.sin + (g.past + s) * g.half_rot, g.interleaved)
-                                  : g.k[row + d];
-      g.present_v[idx] = g.v[row + d];
+      const float *c = g.cos + (g.past + s) * g.half_rot, *sn = g.sin + (g.past + s) * g.half_rot;
+#pragma unroll
+      for (int u = 0; u < VEC; u++) {
+        g.present_k[e + u] = g.rotary ? rope(g.k + row, d + u, g.half_rot, c, sn, g.interleaved)
+                                      : g.k[row + d + u];
+        g.present_v[e + u] = g.v[row + d + u];
+      }
     }
     return;
   }
-  const int64_t e = idx - nkv;  // rotated Q, [batch][seq][heads * hs]
+  const int64_t e = (idx - nkv) * VEC;  // rotated Q, [batch][seq][heads * hs]
   const int64_t d = e % g.hs, row = e - d;
   const int64_t s = (e / (g.heads * g.hs)) % g.seq;
-  g.q_rot[e] = rope(g.q + row, d, g.half_rot, g.cos + (g.past + s) * g.half_rot,
-                    g.sin + (g.past + s) * g.half_rot, g.interleaved);
+#pragma unroll
+  for (int u = 0; u < VEC; u++)
+    g.q_rot[e + u] = rope(g.q + row, d + u, g.half_rot, g.cos + (g.past + s) * g.half_rot,
+                          g.sin + (g.past + s) * g.half_rot, g.interleaved);
 }
 
 }  // namespace
 
 mg_status mg_gqa_prep_run(mg_ctx *ctx, const mg_gqa_prep &g) {
-  const int64_t nkv = g.batch * g.kv_heads * (g.past + g.seq) * g.hs;
-  const int64_t nq = g.rotary ? g.batch * g.seq * g.heads * g.hs : 0;
+  auto al = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+  const bool v4 = g.hs % 4 == 0 && al(g.present_k) && al(g.present_v) &&
+                  (g.past == 0 || (al(g.past_k) && al(g.past_v)));
+  const int vec = v4 ? 4 : 1;
+  const int64_t nkv = g.batch * g.kv_heads * (g.past + g.seq) * g.hs / vec;
+  const int64_t nq = g.rotary ? g.batch * g.seq * g.heads * g.hs / vec : 0;
   if (nkv + nq == 0) return MG_OK;
   const int64_t blocks = (nkv + nq + 255) / 256;
   if (blocks > 0x7fffffff) return mg_fail(MG_UNSUPPORTED, "GroupQueryAttention: too large");
-  hipLaunchKernelGGL(k_gqa_prep, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, g, nkv, nq);
+  if (v4)
+    hipLaunchKernelGGL(k_gqa_prep<4>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, g, nkv, nq);
+  else
+    hipLaunchKernelGGL(k_gqa_prep<1>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, g, nkv, nq);
   return mg_launch_check("k_gqa_prep");
 }

@@ -238,8 +238,13 @@ struct mg_attn_problem {
   // Causal masking: key t is excluded for query q when t > q + causal_off.
   int causal = 0;
   int64_t causal_off = 0;
+  // Key split (flash-decoding): kc keys per split, partials in part (device,
+  // mg_attn_plan_split's bytes), merged by a second kernel.  0 = no split.
+  int kc = 0;
+  float *part = nullptr;
 };
 mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p);
+size_t mg_attn_plan_split(const mg_ctx *ctx, mg_attn_problem *p);
 
 // GroupQueryAttention's data movement before the attention products: the
 // present K/V caches [batch][kv_heads][past + seq][hs] (past rows copied,

@@ -162,6 +162,9 @@ GQA = [
     (3, 5, 8, 2, 128, 7, True, True, 32, 1),        # GPT-J pairs, partial rotary, shared bias
     (1, 64, 14, 2, 64, 0, True, False, 32, 0),      # group of 7
     (1, 300, 4, 1, 16, 33, False, False, 0, 0),     # long causal with past
+    (1, 1, 32, 8, 64, 1000, True, False, 32, 0),    # decode: packed heads, key splits
+    (2, 1, 14, 2, 64, 700, False, False, 0, 14),    # decode with per-head bias, splits
+    (1, 3, 8, 8, 32, 500, True, True, 16, 1),       # short chunk over a long cache, splits
 ]
 
 
@@ -237,3 +240,22 @@ def test_gqa_errors(ops):
                                      np.zeros((1, 2, 256), np.float32),
                                      np.zeros((1, 2, 256), np.float32), num_heads=2,
                                      kv_num_heads=1)
+
+
+def test_key_splits_keep_masked_rows_and_match_unsplit(ops):
+    """Few query tiles over many keys take the key-split path (partials plus
+    a combine kernel); fully masked rows stay NaN and the rest match the
+    oracle."""
+    rng = np.random.default_rng(41)
+    a = rng.standard_normal((1, 2, 40, 64)).astype(np.float32)
+    b = rng.standard_normal((1, 2, 64, 900)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 900, 64)).astype(np.float32)
+    m = rng.standard_normal((1, 2, 40, 900)).astype(np.float32)
+    m[:, :, 5, :] = -np.inf       # a fully masked row
+    m[:, :, 7, :850] = -np.inf    # only the last split has keys
+    y = ops.op_fused_sdpa(a, b, v, m, 0.125)
+    ref = oracle.fused_sdpa(a, b, v, m, 0.125)
+    assert np.isnan(y[:, :, 5]).all() and np.isnan(ref[:, :, 5]).all()
+    keep = np.ones(40, bool)
+    keep[5] = False
+    assert G.rms_error(y[:, :, keep], ref[:, :, keep]) <= TOL
