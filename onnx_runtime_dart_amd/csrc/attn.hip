@@ -320,6 +320,152 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
     }
 }
 
+// Decode-shaped attention: at most 16 queries per batch index (a decode
+// step, or GroupQueryAttention's query heads of one KV head), where the
+// products are too thin for MFMA tiles and the work is reading K and V.
+// Workgroup = one batch index and one key split, walked in blocks of 64
+// keys: the 256 threads stage the block's K ([key][dim], padded rows) and V
+// ([key][dim]) in LDS with coalesced loads; wave w owns queries w, w + 4, ...
+// For each block a wave
+//   * scores the 64 keys against its queries, lane = key, reading its K row
+//     from LDS (odd pitch: no bank conflicts) and Q as LDS broadcasts;
+//   * runs the online softmax per query (block max across the wave; each
+//     lane keeps its share of the sum) and puts p in LDS;
+//   * accumulates O, lane = output dim (DL dims per lane), reading V rows
+//     and p from LDS.
+// It writes y, or with several key splits the partials k_attn_combine merges.
+constexpr int DEC_S = 16;
+template <int DL>
+__global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
+  constexpr int KB = 64, KP = 129;  // keys per block, K row pitch
+  __shared__ float qs[DEC_S * 128];
+  __shared__ float ks[KB * KP];
+  __shared__ float vs[KB * 128];
+  __shared__ float pls[DEC_S * KB];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t bi = blockIdx.x;
+  int64_t oq = 0, ok = 0, ov = 0, om = 0, oy = 0;
+  {
+    int64_t rem = bi;
+    for (int d = p.nbd - 1; d >= 0; d--) {
+      const int64_t c = rem % p.bdim[d];
+      rem /= p.bdim[d];
+      oq += c * p.q_bs[d];
+      ok += c * p.k_bs[d];
+      ov += c * p.v_bs[d];
+      om += c * p.m_bs[d];
+      oy += c * p.y_bs[d];
+    }
+  }
+  const int S = p.S, D = p.D, DV = p.DV;
+  const int t_begin = p.kc > 0 ? (int)blockIdx.y * p.kc : 0;
+  const int t_end = p.kc > 0 ? min(p.T, t_begin + p.kc) : p.T;
+  for (int e = tid; e < S * D; e += 256) {
+    const int q = e / D, d = e % D;
+    qs[q * 128 + d] = p.q[oq + (int64_t)q * p.q_rs + (int64_t)d * p.q_cs];
+  }
+  // Staging order: consecutive threads take consecutive addresses of
+  // whichever index is contiguous in memory.
+  const bool k_key_fast = p.k_ts == 1, v_key_fast = p.v_ts == 1;
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float scale2 = p.scale * kLog2e;
+  constexpr int QW = DEC_S / 4;  // queries per wave
+  float m[QW], l[QW], o[QW][DL];
+#pragma unroll
+  for (int i = 0; i < QW; i++) {
+    m[i] = -INFINITY, l[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < DL; j++) o[i][j] = 0.f;
+  }
+  for (int tb = t_begin; tb < t_end; tb += KB) {
+    const int nk = min(KB, t_end - tb);
+    __syncthreads();  // the previous block's readers are done
+    for (int e = tid; e < KB * D; e += 256) {
+      const int key = k_key_fast ? e % KB : e / D, d = k_key_fast ? e / KB : e % D;
+      ks[key * KP + d] =
+          key < nk ? p.k[ok + (int64_t)(tb + key) * p.k_ts + (int64_t)d * p.k_ds] : 0.f;
+    }
+    for (int e = tid; e < KB * DV; e += 256) {
+      const int key = v_key_fast ? e % KB : e / DV, d = v_key_fast ? e / KB : e % DV;
+      vs[key * 128 + d] =
+          key < nk ? p.v[ov + (int64_t)(tb + key) * p.v_ts + (int64_t)d * p.v_ds] : 0.f;
+    }
+    __syncthreads();
+    const int t = tb + lane;
+    const bool tok = lane < nk;
+    float sc[QW];
+#pragma unroll
+    for (int i = 0; i < QW; i++) sc[i] = 0.f;
+    for (int d = 0; d < D; d++) {
+      const float kv = ks[lane * KP + d];
+#pragma unroll
+      for (int i = 0; i < QW; i++) sc[i] = fmaf(qs[(wave + 4 * i) * 128 + d], kv, sc[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < QW; i++) {
+      const int q = wave + 4 * i;
+      if (q >= S) break;
+      float x = -INFINITY;
+      if (tok && !(p.causal && t > q + p.causal_off)) {
+        const float mk = p.mask ? p.mask[om + (int64_t)q * p.m_qs + (int64_t)t * p.m_ts] : 0.f;
+        x = fmaf(sc[i], scale2, mk * kLog2e);
+      }
+      float bm = x;
+#pragma unroll
+      for (int w = 32; w >= 1; w >>= 1) bm = fmaxf(bm, __shfl_xor(bm, w));
+      const float m_new = fmaxf(m[i], bm);
+      float pv = 0.f, corr = 1.f;
+      if (m_new != -INFINITY) {
+        corr = __builtin_amdgcn_exp2f(m[i] - m_new);  // 0 while nothing has been accumulated
+        pv = __builtin_amdgcn_exp2f(x - m_new);
+        m[i] = m_new;
+      }
+      l[i] = fmaf(l[i], corr, pv);  // the lane's share of the sum
+#pragma unroll
+      for (int j = 0; j < DL; j++) o[i][j] *= corr;
+      pls[q * KB + lane] = pv;
+    }
+    // p rows of this wave only: the wave's LDS writes complete in order.
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    for (int j = 0; j < nk; j++) {
+      float vv[DL];
+#pragma unroll
+      for (int k = 0; k < DL; k++) vv[k] = vs[j * 128 + lane + 64 * k];
+#pragma unroll
+      for (int i = 0; i < QW; i++) {
+        const int q = wave + 4 * i;
+        if (q >= S) break;
+        const float pj = pls[q * KB + j];
+#pragma unroll
+        for (int k = 0; k < DL; k++) o[i][k] = fmaf(pj, vv[k], o[i][k]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < QW; i++) {
+    const int q = wave + 4 * i;
+    if (q >= S) break;
+    float ls = l[i];
+#pragma unroll
+    for (int w = 32; w >= 1; w >>= 1) ls += __shfl_xor(ls, w);
+    if (p.part) {
+      float *pr = p.part + (((int64_t)blockIdx.y * gridDim.x + bi) * S + q) * (DV + 2);
+#pragma unroll
+      for (int k = 0; k < DL; k++)
+        if (lane + 64 * k < DV) pr[lane + 64 * k] = o[i][k];
+      if (lane == 0) pr[DV] = m[i], pr[DV + 1] = ls;
+    } else {
+      const float inv = p.T == 0 ? 0.f : (m[i] == -INFINITY ? __builtin_nanf("") : 1.f / ls);
+#pragma unroll
+      for (int k = 0; k < DL; k++)
+        if (lane + 64 * k < DV)
+          p.y[oy + (int64_t)q * p.y_rs + lane + 64 * k] = p.T == 0 ? 0.f : o[i][k] * inv;
+    }
+  }
+}
+
 // Merges the key splits of each (batch index, query): with M the largest
 // split max, y = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c; every score
 // -inf gives NaN, as without splits.  One thread per output element.
@@ -396,11 +542,26 @@ mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
   int64_t nbatch = 1;
   for (int d = 0; d < p.nbd; d++) nbatch *= p.bdim[d];
   if (nbatch == 0 || p.S == 0 || p.DV == 0) return MG_OK;
-  const int64_t wgs = nbatch * ((p.S + 127) / 128);
+  const bool dec = p.S <= DEC_S;
+  const int64_t wgs = dec ? nbatch : nbatch * ((p.S + 127) / 128);
   if (wgs > 0x7fffffff) return mg_fail(MG_UNSUPPORTED, "attention: grid too large");
   const int nsplit = p.kc > 0 ? (p.T + p.kc - 1) / p.kc : 1;
   if (p.kc > 0 && !p.part) return mg_fail(MG_INVALID_ARGUMENT, "attention: no partial buffer");
   const dim3 grid((unsigned)wgs, (unsigned)nsplit);
+  if (dec) {
+    if (p.DV <= 64)
+      hipLaunchKernelGGL((k_attn_dec<1>), grid, dim3(256), 0, ctx->stream, p);
+    else
+      hipLaunchKernelGGL((k_attn_dec<2>), grid, dim3(256), 0, ctx->stream, p);
+    MG_TRY(mg_launch_check("k_attn_dec"));
+    if (p.kc > 0) {
+      const int64_t n = nbatch * p.S * p.DV;
+      hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                         ctx->stream, p, nsplit, nbatch);
+      MG_TRY(mg_launch_check("k_attn_combine"));
+    }
+    return MG_OK;
+  }
   mg_attn_problem pp = p;
   if (p.D == 0) {  // no products: the kernel's (masked-off) Q and K loads read V instead
     pp.q = pp.k = p.v;
@@ -431,13 +592,19 @@ size_t mg_attn_plan_split(const mg_ctx *ctx, mg_attn_problem *p) {
   p->kc = 0;
   int64_t nbatch = 1;
   for (int d = 0; d < p->nbd; d++) nbatch *= p->bdim[d];
-  const int64_t wgs = nbatch * ((p->S + 127) / 128);
-  // Causal problems are not split: their early query tiles would leave most
-  // splits empty while the combine pass still reads them all.
-  if (wgs == 0 || p->T < 128 || p->DV == 0 || p->causal || wgs >= ctx->num_cus) return 0;
-  const int64_t want = std::min<int64_t>((2 * ctx->num_cus + wgs - 1) / wgs, (p->T + 63) / 64);
+  // Decode-shaped problems (k_attn_dec) split in multiples of its 64-key
+  // blocks, the tiled kernel in multiples of 32.
+  const bool dec = p->S <= DEC_S;
+  const int64_t gran = dec ? 64 : 32;
+  const int64_t wgs = dec ? nbatch : nbatch * ((p->S + 127) / 128);
+  // Causal problems with many queries are not split: their early query
+  // tiles would leave most splits empty while the combine pass reads them.
+  if (wgs == 0 || p->T < 128 || p->DV == 0 || (p->causal && !dec) || wgs >= ctx->num_cus)
+    return 0;
+  const int64_t want = std::min<int64_t>((2 * ctx->num_cus + wgs - 1) / wgs,
+                                         (p->T + gran - 1) / gran);
   if (want < 2) return 0;
-  const int64_t kc = ((p->T + want - 1) / want + 31) / 32 * 32;
+  const int64_t kc = ((p->T + want - 1) / want + gran - 1) / gran * gran;
   const int64_t nsplit = (p->T + kc - 1) / kc;
   if (nsplit < 2) return 0;
   p->kc = (int)kc;
