@@ -347,10 +347,11 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
   const int64_t bi = blockIdx.x;
   int64_t oq = 0, ok = 0, ov = 0, om = 0, oy = 0;
   {
-    int64_t rem = bi;
+    int rem = (int)bi;  // the host keeps the grid below 2^31
     for (int d = p.nbd - 1; d >= 0; d--) {
-      const int64_t c = rem % p.bdim[d];
-      rem /= p.bdim[d];
+      const int bd = (int)p.bdim[d];
+      const int64_t c = rem % bd;
+      rem /= bd;
       oq += c * p.q_bs[d];
       ok += c * p.k_bs[d];
       ov += c * p.v_bs[d];
@@ -368,6 +369,13 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
   // Staging order: consecutive threads take consecutive addresses of
   // whichever index is contiguous in memory.
   const bool k_key_fast = p.k_ts == 1, v_key_fast = p.v_ts == 1;
+  // Rows of 16-byte aligned, contiguous dims (the KV-cache layout): 16-byte
+  // loads, all issued before the first store (indices clamped in range,
+  // padding keys zeroed at the store).
+  const bool rows4 = p.k_ds == 1 && p.v_ds == 1 && D % 4 == 0 && DV % 4 == 0 &&
+                     p.k_ts % 4 == 0 && p.v_ts % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(p.k + ok) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(p.v + ov) % 16 == 0;
   constexpr float kLog2e = 1.4426950408889634f;
   const float scale2 = p.scale * kLog2e;
   constexpr int QW = DEC_S / 4;  // queries per wave
@@ -381,6 +389,34 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
   for (int tb = t_begin; tb < t_end; tb += KB) {
     const int nk = min(KB, t_end - tb);
     __syncthreads();  // the previous block's readers are done
+    if (rows4) {
+      constexpr int C4 = KB * 128 / 4 / 256;  // float4 per thread at 128 dims
+      const int d4 = D / 4, dv4 = DV / 4;
+      float4 kx[C4], vx[C4];
+#pragma unroll
+      for (int u = 0; u < C4; u++) {
+        const int c = tid + 256 * u;
+        const int key = min(c / d4, nk - 1), d = (c % d4) * 4;
+        kx[u] = *reinterpret_cast<const float4 *>(p.k + ok + (int64_t)(tb + key) * p.k_ts + d);
+        const int vkey = min(c / dv4, nk - 1), vd = (c % dv4) * 4;
+        vx[u] = *reinterpret_cast<const float4 *>(p.v + ov + (int64_t)(tb + vkey) * p.v_ts + vd);
+      }
+#pragma unroll
+      for (int u = 0; u < C4; u++) {
+        const int c = tid + 256 * u;
+        if (c < KB * d4) {
+          const int key = c / d4, d = (c % d4) * 4;
+          const float4 x = key < nk ? kx[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+          float *dst = ks + key * KP + d;
+          dst[0] = x.x, dst[1] = x.y, dst[2] = x.z, dst[3] = x.w;
+        }
+        if (c < KB * dv4) {
+          const int key = c / dv4, d = (c % dv4) * 4;
+          const float4 x = key < nk ? vx[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+          *reinterpret_cast<float4 *>(vs + key * 128 + d) = x;
+        }
+      }
+    } else {
     for (int e = tid; e < KB * D; e += 256) {
       const int key = k_key_fast ? e % KB : e / D, d = k_key_fast ? e / KB : e % D;
       ks[key * KP + d] =
@@ -391,12 +427,14 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
       vs[key * 128 + d] =
           key < nk ? p.v[ov + (int64_t)(tb + key) * p.v_ts + (int64_t)d * p.v_ds] : 0.f;
     }
+    }
     __syncthreads();
     const int t = tb + lane;
     const bool tok = lane < nk;
     float sc[QW];
 #pragma unroll
     for (int i = 0; i < QW; i++) sc[i] = 0.f;
+#pragma unroll 8
     for (int d = 0; d < D; d++) {
       const float kv = ks[lane * KP + d];
 #pragma unroll
@@ -429,6 +467,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
     // p rows of this wave only: the wave's LDS writes complete in order.
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
+#pragma unroll 8
     for (int j = 0; j < nk; j++) {
       float vv[DL];
 #pragma unroll
