@@ -312,6 +312,7 @@ def main():
         result["int8_prefill"] = int8_prefill(torch, ops, ctx, T, dev, args)
         result["f32_encoder"] = f32_encoder(torch, ops, ctx, T, randn, dev, args)
         result["conv"] = conv_family(torch, ops, ctx, T, randn, dev, args)
+        result["gqa"] = gqa_steps(torch, ops, ctx, T, randn, dev)
         result["load_path"] = load_path(ops, ctx, host_w[-1], QWEN3_PROJ[-1])
 
     if not args.no_cpu and not args.quick and os.environ.get("MIGEMM_BENCH_NO_CPU") != "1":
@@ -582,6 +583,42 @@ def conv_family(torch, ops, ctx, T, randn, dev, args):
         "note": "integer operands on fp32 MFMA (exact); includes the per-call upload of the "
                 "per-channel requant table and its stream wait"}
     print(f"# conv: {out}", file=sys.stderr, flush=True)
+    return out
+
+
+def gqa_steps(torch, ops, ctx, T, randn, dev):
+    """GroupQueryAttention at Llama-3.2-1B geometry (32 query heads, 8 KV heads
+    of 64, RoPE): one decode step over a 1024- and a 4096-token cache (KV
+    append, attention over the cache; algorithmic bytes = the cache read
+    twice plus written once, the op's present-KV contract) and a 512-token
+    causal prefill."""
+    out = {}
+    h, kv, hs = 32, 8, 64
+    for name, b, s, past in (("decode_past1024", 1, 1, 1024), ("decode_past4096", 1, 1, 4096),
+                             ("prefill_512", 1, 512, 0)):
+        q, k, v = randn(b, s, h * hs), randn(b, s, kv * hs), randn(b, s, kv * hs)
+        pk, pv = randn(b, kv, max(past, 1), hs), randn(b, kv, max(past, 1), hs)
+        cos, sin = randn(past + s, hs // 2), randn(past + s, hs // 2)
+        y = torch.empty_like(q)
+        prk = torch.empty((b, kv, past + s, hs), device=dev)
+        prv = torch.empty_like(prk)
+
+        def step():
+            ops.group_query_attention_dev(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), b, s, h * hs, h, kv, y.data_ptr(),
+                prk.data_ptr(), prv.data_ptr(), past_key_ptr=pk.data_ptr() if past else 0,
+                past_value_ptr=pv.data_ptr() if past else 0, past_len=past,
+                cos_ptr=cos.data_ptr(), sin_ptr=sin.data_ptr(), max_pos=past + s,
+                half_rot=hs // 2, do_rotary=True, ctx=ctx)
+
+        ms = T.loop(step, 20, 3)
+        kv_bytes = 2 * b * kv * (past + s) * hs * 4
+        out[name] = {"us": round(ms * 1e3, 2),
+                     "cache_GB/s": round(3 * kv_bytes / (ms / 1e3) / 1e9, 1)}
+        if s > 1:
+            flops = 4.0 * b * h * hs * s * (s + 1) / 2
+            out[name]["TFLOP/s"] = round(flops / (ms / 1e3) / 1e12, 2)
+    print(f"# gqa: {out}", file=sys.stderr, flush=True)
     return out
 
 

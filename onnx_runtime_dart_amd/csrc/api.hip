@@ -1328,6 +1328,14 @@ mg_status conv_limits(const char *op, const mg_conv_problem &p) {
   }
   if (in_sp > lim || out_sp > lim)
     return mg_fail(MG_UNSUPPORTED, std::string(op) + ": spatial size too large");
+  // The kernel forms a window origin's offset in an input plane plus a tap's
+  // shift in 32 bits (padding can put both outside the plane).
+  auto span = [&](int a) {
+    return (double)p.in[a] + (double)std::abs(p.pad[a]) + (double)p.str[a] +
+           (double)p.ker[a] * (double)p.dil[a];
+  };
+  if ((span(0) * (double)p.in[1] + span(1)) * (double)p.in[2] + span(2) > (double)lim)
+    return mg_fail(MG_UNSUPPORTED, std::string(op) + ": spatial size too large");
   // The kernel clamps out-of-range reads to element 0 of x, which must exist.
   if (in_sp == 0 && out_sp > 0 && p.n > 0 && p.m > 0 && p.cg > 0)
     return mg_fail(MG_UNSUPPORTED, std::string(op) + ": empty spatial input with padding");

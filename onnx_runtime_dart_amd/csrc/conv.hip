@@ -85,11 +85,51 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p, int pix_t
   // B (input window): thread k kb, output run [nb, nb + E) of the stage.
   const int kb = t / (T / E), nb = (t % (T / E)) * E;
   const int64_t xbatch = (b * p.c + g * p.cg) * in_sp;  // channel 0 of the group
+  // The thread's output positions are the same in every stage: for Conv
+  // their window origins (o * str - pad per axis) and the origin's offset in
+  // an input plane are computed once; a stage adds its tap's shift.
+  int bz[E], by[E], bx[E], spe[E];
+  bool nok[E];
+  if (!TR) {
+    const int64_t n0 = c0 + nb;
+    int oz = (int)(n0 / o12), oy = (int)((n0 % o12) / o2), ox = (int)(n0 % o2);
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+      nok[e] = n0 + e < out_sp;
+      bz[e] = oz * (int)p.str[0] - (int)p.pad[0];
+      by[e] = oy * (int)p.str[1] - (int)p.pad[1];
+      bx[e] = ox * (int)p.str[2] - (int)p.pad[2];
+      spe[e] = (bz[e] * (int)p.in[1] + by[e]) * (int)p.in[2] + bx[e];
+      if (++ox == o2) {
+        ox = 0;
+        if (++oy == (int)p.out[1]) oy = 0, oz++;
+      }
+    }
+  }
 
   float va[E], vb[E];
   auto load = [&](int st) __attribute__((always_inline)) {
     const int64_t k0 = (int64_t)st * KS;
-    {  // weights: taps of one output channel, k consecutive
+    // Conv weights: an output channel's k run is contiguous (channel stride
+    // = taps); whole aligned runs load as two 16-byte loads.
+    if (!TR && !INT && row_ok && k0 + ka + E <= K && ((wbase + k0 + ka) & 3) == 0) {
+      const float *wp = static_cast<const float *>(p.w) + wbase + k0 + ka;
+#pragma unroll
+      for (int q = 0; q < E / 4; q++) {
+        const float4 x = *reinterpret_cast<const float4 *>(wp + 4 * q);
+        va[4 * q] = x.x, va[4 * q + 1] = x.y, va[4 * q + 2] = x.z, va[4 * q + 3] = x.w;
+      }
+    } else if (!TR && INT && row_ok && k0 + ka + E <= K && ((wbase + k0 + ka) & 7) == 0) {
+      // integer weights: the 8 bytes of the run in one load
+      const uint2 x = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(p.w) + wbase +
+                                                       k0 + ka);
+#pragma unroll
+      for (int e = 0; e < E; e++) {
+        const uint32_t by = ((e < 4 ? x.x : x.y) >> (8 * (e & 3))) & 0xFFu;
+        const int wv = p.wk == MG_CONV_I8 ? (int)(int8_t)by : (int)by;
+        va[e] = (float)wv - wz;
+      }
+    } else {  // weights: taps of one output channel, k consecutive
       int64_t k = k0 + ka;
       int c = (int)(k / kk), r = (int)(k - (int64_t)c * kk);
 #pragma unroll
@@ -111,9 +151,27 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p, int pix_t
       const int c = k_ok ? (int)(k / kk) : 0;
       const int r = k_ok ? (int)(k - (int64_t)c * kk) : 0;
       const int kz = r / k12, ky = (r % k12) / kw2, kx = r % kw2;
+      const int64_t xc = xbatch + (int64_t)c * in_sp;
+      if (!TR) {
+        const int shz = kz * (int)p.dil[0], shy = ky * (int)p.dil[1], shx = kx * (int)p.dil[2];
+        const int tap = (shz * (int)p.in[1] + shy) * (int)p.in[2] + shx;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+          const int iz = bz[e] + shz, iy = by[e] + shy, ix = bx[e] + shx;
+          const bool ok = k_ok && nok[e] && (unsigned)iz < (unsigned)p.in[0] &&
+                          (unsigned)iy < (unsigned)p.in[1] && (unsigned)ix < (unsigned)p.in[2];
+          const int64_t off = ok ? xc + (spe[e] + tap) : 0;
+          float v;
+          if (INT)
+            v = (float)(load_int(static_cast<const uint8_t *>(p.x), off, p.xk) - p.x_zp);
+          else
+            v = static_cast<const float *>(p.x)[off];
+          vb[e] = ok ? v : 0.f;
+        }
+        return;
+      }
       const int64_t n0 = c0 + nb;
       int oz = (int)(n0 / o12), oy = (int)((n0 % o12) / o2), ox = (int)(n0 % o2);
-      const int64_t xc = xbatch + (int64_t)c * in_sp;
 #pragma unroll
       for (int e = 0; e < E; e++) {
         int iz, iy, ix;
