@@ -1410,6 +1410,9 @@ mg_status plan_conv_transpose(const int64_t *xs, int32_t xr, const int64_t *ws, 
   p->mg = ws[1];
   p->m = p->mg * group;
   p->trans = 1;
+  for (int a = 0; a < nd; a++)  // the kernel packs three stride remainders in 10 bits each
+    if (p->str[o + a] >= 1024)
+      return mg_fail(MG_UNSUPPORTED, "ConvTranspose: strides of 1024 or more");
   for (int a = 0; a < nd; a++) {
     const int64_t full =
         (xs[2 + a] - 1) * p->str[o + a] + p->dil[o + a] * (ws[2 + a] - 1) + 1 +

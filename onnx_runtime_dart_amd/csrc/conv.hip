@@ -88,9 +88,32 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p, int pix_t
   // The thread's output positions are the same in every stage: for Conv
   // their window origins (o * str - pad per axis) and the origin's offset in
   // an input plane are computed once; a stage adds its tap's shift.
-  int bz[E], by[E], bx[E], spe[E];
+  // ConvTranspose: (o + pad) = q * str + rem per axis; a tap kk * dil =
+  // kq * str + kr reaches input q - kq exactly when rem == kr.  q goes to
+  // bz/by/bx and spe, the three remainders (each < 2^10) packed in rem3.
+  int bz[E], by[E], bx[E], spe[E], rem3[E];
   bool nok[E];
-  if (!TR) {
+  if (TR) {
+    const int64_t n0 = c0 + nb;
+    int oz = (int)(n0 / o12), oy = (int)((n0 % o12) / o2), ox = (int)(n0 % o2);
+    const int sz = (int)p.str[0], sy = (int)p.str[1], sx = (int)p.str[2];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+      nok[e] = n0 + e < out_sp;
+      const int tz = oz + (int)p.pad[0], ty = oy + (int)p.pad[1], tx = ox + (int)p.pad[2];
+      // floor division (t may be negative with negative pads)
+      const int qz = tz >= 0 ? tz / sz : -((-tz + sz - 1) / sz);
+      const int qy = ty >= 0 ? ty / sy : -((-ty + sy - 1) / sy);
+      const int qx = tx >= 0 ? tx / sx : -((-tx + sx - 1) / sx);
+      bz[e] = qz, by[e] = qy, bx[e] = qx;
+      rem3[e] = (tz - qz * sz) | ((ty - qy * sy) << 10) | ((tx - qx * sx) << 20);
+      spe[e] = (qz * (int)p.in[1] + qy) * (int)p.in[2] + qx;
+      if (++ox == o2) {
+        ox = 0;
+        if (++oy == (int)p.out[1]) oy = 0, oz++;
+      }
+    }
+  } else {
     const int64_t n0 = c0 + nb;
     int oz = (int)(n0 / o12), oy = (int)((n0 % o12) / o2), ox = (int)(n0 % o2);
 #pragma unroll
@@ -170,38 +193,26 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p, int pix_t
         }
         return;
       }
-      const int64_t n0 = c0 + nb;
-      int oz = (int)(n0 / o12), oy = (int)((n0 % o12) / o2), ox = (int)(n0 % o2);
+      {
+        const int sz = (int)p.str[0], sy = (int)p.str[1], sx = (int)p.str[2];
+        const int dz = kz * (int)p.dil[0], dy = ky * (int)p.dil[1], dx = kx * (int)p.dil[2];
+        const int kqz = dz / sz, kqy = dy / sy, kqx = dx / sx;
+        const int kr3 = (dz - kqz * sz) | ((dy - kqy * sy) << 10) | ((dx - kqx * sx) << 20);
+        const int tap = (kqz * (int)p.in[1] + kqy) * (int)p.in[2] + kqx;
 #pragma unroll
-      for (int e = 0; e < E; e++) {
-        int iz, iy, ix;
-        bool ok = k_ok && n0 + e < out_sp;
-        if (!TR) {
-          iz = oz * (int)p.str[0] - (int)p.pad[0] + kz * (int)p.dil[0];
-          iy = oy * (int)p.str[1] - (int)p.pad[1] + ky * (int)p.dil[1];
-          ix = ox * (int)p.str[2] - (int)p.pad[2] + kx * (int)p.dil[2];
-        } else {
-          const int tz = oz + (int)p.pad[0] - kz * (int)p.dil[0];
-          const int ty = oy + (int)p.pad[1] - ky * (int)p.dil[1];
-          const int tx = ox + (int)p.pad[2] - kx * (int)p.dil[2];
-          const int sz = (int)p.str[0], sy = (int)p.str[1], sx = (int)p.str[2];
-          ok = ok && tz >= 0 && ty >= 0 && tx >= 0 && tz % sz == 0 && ty % sy == 0 &&
-               tx % sx == 0;
-          iz = tz / sz, iy = ty / sy, ix = tx / sx;
+        for (int e = 0; e < E; e++) {
+          const int iz = bz[e] - kqz, iy = by[e] - kqy, ix = bx[e] - kqx;
+          const bool ok = k_ok && nok[e] && rem3[e] == kr3 && (unsigned)iz < (unsigned)p.in[0] &&
+                          (unsigned)iy < (unsigned)p.in[1] && (unsigned)ix < (unsigned)p.in[2];
+          const int64_t off = ok ? xc + (spe[e] - tap) : 0;
+          float v;
+          if (INT)
+            v = (float)(load_int(static_cast<const uint8_t *>(p.x), off, p.xk) - p.x_zp);
+          else
+            v = static_cast<const float *>(p.x)[off];
+          vb[e] = ok ? v : 0.f;
         }
-        ok = ok && iz >= 0 && iz < (int)p.in[0] && iy >= 0 && iy < (int)p.in[1] && ix >= 0 &&
-             ix < (int)p.in[2];
-        const int64_t off = ok ? xc + ((int64_t)iz * p.in[1] + iy) * p.in[2] + ix : 0;
-        float v;
-        if (INT)
-          v = (float)(load_int(static_cast<const uint8_t *>(p.x), off, p.xk) - p.x_zp);
-        else
-          v = static_cast<const float *>(p.x)[off];
-        vb[e] = ok ? v : 0.f;
-        if (++ox == o2) {
-          ox = 0;
-          if (++oy == (int)p.out[1]) oy = 0, oz++;
-        }
+        return;
       }
     }
   };
