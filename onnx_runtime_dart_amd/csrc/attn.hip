@@ -194,7 +194,8 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
   // With a key split (p.kc > 0) the workgroup takes keys [t_begin,
   // t_begin + kc) of split blockIdx.y and writes partial results.
   const int t_begin = p.kc > 0 ? (int)blockIdx.y * p.kc : 0;
-  int t_loop = p.kc > 0 ? std::min(p.T, t_begin + p.kc) : p.T;
+  // (min() by value: a reference to a field of p would put p in scratch memory)
+  int t_loop = p.kc > 0 ? min(p.T, t_begin + p.kc) : p.T;
   if (p.causal) {
     const int64_t q_last = (int64_t)(blockIdx.x % qtiles) * 128 + 127;
     t_loop = (int)std::min<int64_t>(t_loop, std::max<int64_t>(0, q_last + p.causal_off + 1));

@@ -47,14 +47,33 @@ def hipcc() -> str:
 
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [hipcc(), *HIPFLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPFLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src),
+           "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
+    # Per-kernel resource report (registers, scratch, LDS, occupancy).
+    usage = [ln.split("remark: ", 1)[1].replace(" [-Rpass-analysis=kernel-resource-usage]", "")
+             for ln in r.stderr.splitlines() if "remark: " in ln and "kernel-resource-usage" in ln]
+    (BUILD / (Path(src).stem + ".usage.txt")).write_text("\n".join(usage) + "\n")
     warn = [ln for ln in r.stderr.splitlines() if "warning" in ln and "packed-fp32-ops" not in ln]
     if warn:
         print("\n".join(warn), file=sys.stderr)
     return obj
+
+
+def kernels_with_scratch() -> list[str]:
+    """Kernels of the last build that use scratch (per-lane stack) memory."""
+    out = []
+    for f in sorted(BUILD.glob("*.usage.txt")):
+        name = None
+        for ln in f.read_text().splitlines():
+            ln = ln.strip()
+            if ln.startswith("Function Name:"):
+                name = ln.split(":", 1)[1].strip()
+            elif ln.startswith("ScratchSize") and not ln.endswith(": 0"):
+                out.append(f"{f.stem}: {name} ({ln})")
+    return out
 
 
 def build(jobs: int | None = None) -> Path:
@@ -70,6 +89,8 @@ def build(jobs: int | None = None) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    for k in kernels_with_scratch():
+        print(f"warning: kernel uses scratch memory: {k}", file=sys.stderr)
     return LIB
 
 

@@ -72,3 +72,17 @@ def test_host_validation_precedes_device_work():
         ops.op_qlinear_matmul(np.zeros((2, 2), np.uint8), np.ones(2), None,
                               np.zeros((2, 2), np.uint8), 1.0, None, 1.0, None,
                               lo=0, hi=255)
+
+
+def test_no_kernel_uses_scratch_memory():
+    """Every kernel keeps its state in registers and LDS: a stack copy (an
+    escaped kernel argument, a non-inlined helper, a dynamically indexed
+    array) costs scratch traffic on every access."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "mg_build", ROOT / "onnx_runtime_dart_amd" / "csrc" / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    if not list(mod.BUILD.glob("*.usage.txt")):
+        pytest.skip("no resource report: run onnx_runtime_dart_amd/csrc/build.py")
+    assert mod.kernels_with_scratch() == []
