@@ -923,11 +923,11 @@ __global__ __launch_bounds__(256) void k_af16split16(const float *__restrict__ a
 // are added in wave order through LDS; the row exponents come off at the end.
 // Packed codes, scales, zero points and activation fragments of the next k
 // group are loaded while the current one is computed.
-template <int SEGJ>
-__global__ __launch_bounds__(256) void k_gemv_mfma(
+template <int SEGJ, int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
     const uint4 *__restrict__ ahl, const int *__restrict__ texp, const GemvSet gs, int M,
     int c4n, int nb, int nbh, int lbs, int has_zp) {
-  __shared__ float4 red[4][4][64];  // [wave][tile][lane]
+  __shared__ float4 red[NW][4][64];  // [wave][tile][lane]
   constexpr int NBK = 4 / SEGJ;     // blocks (scale segments) per k group
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -1036,17 +1036,18 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(
 
   // Two-slot ring over this wave's k groups (unrolled by two so slots are
   // static).
+  // Wave w takes k groups w, w + NW, ... with the next one's loads in flight.
   Ring ra, rb;
   int kg = wave;
   if (kg < c4n) fetch(kg, ra);
-  for (; kg < c4n; kg += 8) {
-    if (kg + 4 < c4n) fetch(kg + 4, rb);
+  for (; kg < c4n; kg += 2 * NW) {
+    if (kg + NW < c4n) fetch(kg + NW, rb);
     __builtin_amdgcn_sched_barrier(0);
     compute(kg, ra);
-    if (kg + 4 >= c4n) break;
-    if (kg + 8 < c4n) fetch(kg + 8, ra);
+    if (kg + NW >= c4n) break;
+    if (kg + 2 * NW < c4n) fetch(kg + 2 * NW, ra);
     __builtin_amdgcn_sched_barrier(0);
-    compute(kg + 4, rb);
+    compute(kg + NW, rb);
   }
 
 #pragma unroll
@@ -1058,7 +1059,7 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(
     for (int tl = 0; tl < 4; tl++) {
       float4 s = red[0][tl][lane];
 #pragma unroll
-      for (int w = 1; w < 4; w++) {
+      for (int w = 1; w < NW; w++) {
         const float4 o = red[w][tl][lane];
         s.x += o.x; s.y += o.y; s.z += o.z; s.w += o.w;
       }
@@ -1559,13 +1560,23 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
     MG_TRY(mg_launch_check("k_af16split16"));
     const int has_zp = d.zp_kind == MG_ZP_UINT4;
     const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
-#define MG_DEC_LAUNCH(SJ_)                                                                \
-  hipLaunchKernelGGL((k_gemv_mfma<SJ_>), dim3((unsigned)ng), dim3(256), 0, st, ahl, texp,  \
-                     gs, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs),   \
-                     has_zp)
-    if (segj == 1) MG_DEC_LAUNCH(1);
-    else if (segj == 2) MG_DEC_LAUNCH(2);
-    else MG_DEC_LAUNCH(4);
+    // Waves per workgroup: 4 for wide weights; narrow ones (fewer than two
+    // workgroups per CU) split K over 8 waves, so that their few workgroups
+    // keep more k groups' loads in flight.  (16 waves would cap the kernel
+    // at 128 registers and spill.)
+    int nw = 4;
+    if ((int64_t)ng < 2 * (int64_t)std::max(ctx->num_cus, 1) && d.c4 >= 8) nw = 8;
+#define MG_DEC_LAUNCH(SJ_, NW_)                                                             \
+  hipLaunchKernelGGL((k_gemv_mfma<SJ_, NW_>), dim3((unsigned)ng), dim3(NW_ * 64), 0, st,     \
+                     ahl, texp, gs, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,               \
+                     __builtin_ctzll(d.bs), has_zp)
+#define MG_DEC_NW(SJ_)               \
+  if (nw == 8) MG_DEC_LAUNCH(SJ_, 8); \
+  else MG_DEC_LAUNCH(SJ_, 4)
+    if (segj == 1) { MG_DEC_NW(1); }
+    else if (segj == 2) { MG_DEC_NW(2); }
+    else { MG_DEC_NW(4); }
+#undef MG_DEC_NW
 #undef MG_DEC_LAUNCH
     return mg_launch_check("k_gemv_mfma");
   }
