@@ -45,7 +45,11 @@ namespace {
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 template <int DS, int DVT>
-__global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
+__device__ __attribute__((always_inline)) void attn_tiles(const mg_attn_problem &p) {
+  // Tiles prefetched ahead in registers: two for head size <= 32, one for the
+  // larger heads (their fragments and accumulators need the registers; one
+  // set keeps them at two waves per SIMD).
+  constexpr int PD = (DS >= 32 || DVT >= 2) ? 1 : 2;
   // LDS tiles: K as [key][dim] with row pitch DP, V transposed as [dim][key]
   // with row pitch VT.  Both pitches are 4 (mod 64) floats: rows start on 16
   // bytes and the 16-byte reads of 16 consecutive rows fall in distinct bank
@@ -91,14 +95,12 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
   constexpr unsigned kOob = 0x80000000u;
   const bool k_tmajor = p.k_ts == 1, v_tmajor = p.v_ts == 1;
   unsigned kgo[KE], vgo[VE];
-  int klo[KE], vlo[VE];
 #pragma unroll
   for (int e = 0; e < KE; e++) {
     const int idx = tid + 256 * e;
     const int t = k_tmajor ? idx & 31 : idx / (2 * DS);
     const int d = k_tmajor ? idx >> 5 : idx % (2 * DS);
     kgo[e] = d < p.D ? 4u * (unsigned)(t * (int)p.k_ts + d * (int)p.k_ds) : kOob;
-    klo[e] = t * DP + d;
   }
 #pragma unroll
   for (int e = 0; e < VE; e++) {
@@ -106,7 +108,6 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
     const int t = v_tmajor ? idx & 31 : idx / (32 * DVT);
     const int dv = v_tmajor ? idx >> 5 : idx % (32 * DVT);
     vgo[e] = dv < p.DV ? 4u * (unsigned)(t * (int)p.v_ts + dv * (int)p.v_ds) : kOob;
-    vlo[e] = dv * VT + t;
   }
   auto rsrc = [](const float *base) __attribute__((always_inline)) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, 0x7ffffff0,
@@ -116,10 +117,11 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
     asm("" : "+v"(off));  // an opaque offset: the select stays a select, not a branch
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
   };
-  // Two register sets: tile i is fetched into set i % 2 two tiles ahead of
-  // its use, so each load has two tiles of compute to arrive.
-  float kreg[2][KE], vreg[2][VE];
-  float mreg[2][16];  // the lane's mask values of a fetched tile (its query)
+  // With two register sets tile i is fetched into set i % 2 two tiles ahead
+  // of its use, so each load has two tiles of compute to arrive; with one it
+  // is fetched one tile ahead.
+  float kreg[PD][KE], vreg[PD][VE];
+  float mreg[PD][16];  // the lane's mask values of a fetched tile (its query)
   // Mask rows of the wave's 32 queries: a wave-uniform base (row q0) and the
   // lane's row offset; rows past S read nothing.
   const float *mrow = p.mask ? p.mask + om + (int64_t)q0 * p.m_qs : nullptr;
@@ -159,13 +161,33 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
     else
       fetch(t0, std::false_type{}, set);
   };
-  // Register set R -> LDS buffer R.
-  auto stage = [&](auto set) __attribute__((always_inline)) {
-    constexpr int R = decltype(set)::value;
+  // Register set R -> LDS buffer L.  Element e of the thread's share sits
+  // at a fixed LDS offset from the thread's first (256 divides the tile
+  // rows), so the stores take immediate offsets and no index registers.
+  const int kt0 = k_tmajor ? tid & 31 : tid / (2 * DS);
+  const int kd0 = k_tmajor ? tid >> 5 : tid % (2 * DS);
+  const int vt0 = v_tmajor ? tid & 31 : tid / (32 * DVT);
+  const int vd0 = v_tmajor ? tid >> 5 : tid % (32 * DVT);
+  float *const ks_t = &ks[0][kt0 * DP + kd0];
+  float *const vs_t = &vs[0][vd0 * VT + vt0];
+  auto stage = [&](auto set, auto buf) __attribute__((always_inline)) {
+    constexpr int R = decltype(set)::value, L = decltype(buf)::value;
+    float *const kw = ks_t + L * 32 * DP;
+    float *const vw = vs_t + L * 32 * DVT * VT;
+    if (k_tmajor) {
 #pragma unroll
-    for (int e = 0; e < KE; e++) ks[R][klo[e]] = kreg[R][e];
+      for (int e = 0; e < KE; e++) kw[8 * e] = kreg[R][e];
+    } else {
 #pragma unroll
-    for (int e = 0; e < VE; e++) vs[R][vlo[e]] = vreg[R][e];
+      for (int e = 0; e < KE; e++) kw[e * (256 / (2 * DS)) * DP] = kreg[R][e];
+    }
+    if (v_tmajor) {
+#pragma unroll
+      for (int e = 0; e < VE; e++) vw[8 * e * VT] = vreg[R][e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VE; e++) vw[e * (8 / DVT)] = vreg[R][e];
+    }
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -202,38 +224,55 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
   }
   if (t_loop > t_begin) {
     fetch_any(t_begin, I0{});
-    if (t_loop > t_begin + 32) fetch_any(t_begin + 32, I1{});
-    stage(I0{});
+    if constexpr (PD == 2) {
+      if (t_loop > t_begin + 32) fetch_any(t_begin + 32, I1{});
+      stage(I0{}, I0{});
+    } else {
+      stage(I0{}, I0{});
+#pragma unroll
+      for (int v = 0; v < 16; v++) mcur[v] = mreg[0][v];
+      if (t_loop > t_begin + 32) fetch_any(t_begin + 32, I0{});
+    }
   }
   // Scores in the log2 domain: p = 2^(s * scale * log2 e + mask * log2 e - m).
   constexpr float kLog2e = 1.4426950408889634f;
   const float scale2 = p.scale * kLog2e;
   __syncthreads();
-  // Tile at t0 (parity B): its K/V are in LDS buffer B and its mask in set
-  // B.  Set B is then refilled with the tile at t0 + 64, and set 1 - B (the
-  // tile at t0 + 32, fetched one tile ago) is staged into buffer 1 - B.
+  // Tile at t0 (parity B): its K/V are in LDS buffer B.  Two register
+  // sets: its mask is in set B, set B is then refilled with the tile at
+  // t0 + 64, and set 1 - B (the tile at t0 + 32, fetched one tile ago) is
+  // staged into buffer 1 - B after the scores.  One set: its mask is in
+  // mcur and the set holds the tile at t0 + 32, staged after the scores;
+  // the tile at t0 + 64 is fetched next.
   auto tile = [&](int t0, auto bsel) __attribute__((always_inline)) {
     constexpr int B = decltype(bsel)::value;
     using NB = std::integral_constant<int, 1 - B>;
+    if constexpr (PD == 2) {
 #pragma unroll
-    for (int v = 0; v < 16; v++) mcur[v] = mreg[B][v];
-    if (t0 + 64 < t_loop) fetch_any(t0 + 64, bsel);
+      for (int v = 0; v < 16; v++) mcur[v] = mreg[B][v];
+      if (t0 + 64 < t_loop) fetch_any(t0 + 64, bsel);
+    }
     const bool full = t0 + 32 <= p.T;
     if (active) {
       const float *kl = &ks[B][0];
       const float *vl = &vs[B][0];
       // Scores S^T[t][q] for keys t0 .. t0 + 31.  The lane's K fragments
-      // (key r32, dims DS h ..) are read with 16-byte loads up front.
-      float kf[DS];
-#pragma unroll
-      for (int i = 0; i < DS / 4; i++) {
-        const float4 x = *reinterpret_cast<const float4 *>(kl + r32 * DP + DS * h + 4 * i);
-        kf[4 * i] = x.x, kf[4 * i + 1] = x.y, kf[4 * i + 2] = x.z, kf[4 * i + 3] = x.w;
-      }
+      // (key r32, dims DS h ..) are read with 16-byte loads, KC at a time.
+      constexpr int KC = DS < 16 ? DS : 16;
       float16v sc = (float16v){};
 #pragma unroll
-      for (int s = 0; s < DS; s++)
-        sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[s], sc, 0, 0, 0);
+      for (int c = 0; c < DS; c += KC) {
+        float kf[KC];
+#pragma unroll
+        for (int i = 0; i < KC / 4; i++) {
+          const float4 x =
+              *reinterpret_cast<const float4 *>(kl + r32 * DP + DS * h + c + 4 * i);
+          kf[4 * i] = x.x, kf[4 * i + 1] = x.y, kf[4 * i + 2] = x.z, kf[4 * i + 3] = x.w;
+        }
+#pragma unroll
+        for (int s = 0; s < KC; s++)
+          sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[c + s], sc, 0, 0, 0);
+      }
       float pv[16];
       float tmax = -INFINITY;
 #pragma unroll
@@ -279,7 +318,16 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
           o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s], pv[s], o[j], 0, 0, 0);
       }
     }
-    if (t0 + 32 < t_loop) stage(NB{});  // its readers passed the last barrier
+    if (t0 + 32 < t_loop) {  // buffer 1 - B: its readers passed the last barrier
+      if constexpr (PD == 2) {
+        stage(NB{}, NB{});
+      } else {
+        stage(I0{}, NB{});
+#pragma unroll
+        for (int v = 0; v < 16; v++) mcur[v] = mreg[0][v];
+        if (t0 + 64 < t_loop) fetch_any(t0 + 64, I0{});
+      }
+    }
     __syncthreads();
   };
   for (int t0 = t_begin; t0 < t_loop; t0 += 64) {
@@ -319,6 +367,23 @@ __global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
       const int dv = 32 * j + 8 * (v >> 2) + 4 * h + (v & 3);
       if (dv < p.DV) yr[dv] = p.T == 0 ? 0.f : o[j][v] * inv;
     }
+}
+
+// Head sizes whose fragments and accumulators fit 256 registers run at two
+// waves per SIMD (k_attn_o2); the larger ones keep one (with two, the
+// compiler would spill them to scratch memory).
+template <int DS, int DVT>
+constexpr bool attn_two_waves = DS <= 16 || (DS <= 32 && DVT <= 2);
+
+template <int DS, int DVT>
+__global__ __launch_bounds__(256) void k_attn(const mg_attn_problem p) {
+  attn_tiles<DS, DVT>(p);
+}
+
+template <int DS, int DVT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_o2(
+    const mg_attn_problem p) {
+  attn_tiles<DS, DVT>(p);
 }
 
 // Decode-shaped attention: at most 16 queries per batch index (a decode
@@ -562,14 +627,22 @@ __global__ __launch_bounds__(256) void k_attn_combine(const mg_attn_problem p, i
   p.y[oy + (int64_t)q * p.y_rs + dv] = M == -INFINITY ? __builtin_nanf("") : num / den;
 }
 
+template <int DS, int DVT>
+void launch_attn(const mg_attn_problem &p, dim3 grid, hipStream_t st) {
+  if constexpr (attn_two_waves<DS, DVT>)
+    hipLaunchKernelGGL((k_attn_o2<DS, DVT>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((k_attn<DS, DVT>), grid, dim3(256), 0, st, p);
+}
+
 template <int DS>
 void launch_dvt(const mg_attn_problem &p, dim3 grid, hipStream_t st) {
   if (p.DV <= 32)
-    hipLaunchKernelGGL((k_attn<DS, 1>), grid, dim3(256), 0, st, p);
+    launch_attn<DS, 1>(p, grid, st);
   else if (p.DV <= 64)
-    hipLaunchKernelGGL((k_attn<DS, 2>), grid, dim3(256), 0, st, p);
+    launch_attn<DS, 2>(p, grid, st);
   else
-    hipLaunchKernelGGL((k_attn<DS, 4>), grid, dim3(256), 0, st, p);
+    launch_attn<DS, 4>(p, grid, st);
 }
 
 }  // namespace
