@@ -75,7 +75,11 @@ __host__ __device__ inline int sz_pos(int c) { return (c & 15) * 4 + (c >> 4); }
 // ahl[((m32 * c4n + kg) * 8 + st) * 128 + 32 h + r] holds the hi fp16 x 8 of
 // row r, k = 128 kg + 16 st + 8 h .. +7, and +64 the lo part; texp[row] = e.
 // Rows past M and k past K are zeros.  Non-finite values pass through in hi.
-// Workgroup: 4 rows, each row on one wave.
+// Workgroup: 4 rows, each row on one wave.  UL > 0: the row's 16-k pieces are
+// at most 64 UL, and each lane reads its UL pieces once, with all loads in
+// flight together, and keeps them in registers for the split; UL = 0 (longer
+// rows) reads the row twice.
+template <int UL>
 __global__ __launch_bounds__(256) void k_af16split(
     const float *__restrict__ a, int64_t M, int64_t K, int c4n, int vec,
     uint4 *__restrict__ ahl, int *__restrict__ texp) {
@@ -100,27 +104,18 @@ __global__ __launch_bounds__(256) void k_af16split(
       for (int i = 0; i < 16; i++) v[i] = (row < M && k0 + i < K) ? arow[k0 + i] : 0.f;
     }
   };
-  float mx = 0.f;
-  for (int u = u0; u < units; u += 64) {
-    float v[16];
-    load16(u, v);
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const float x = fabsf(v[i]);
-      mx = x < INFINITY ? fmaxf(mx, x) : mx;  // finite values only
+  auto row_exponent = [&](float mx) {
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    int e = 0;
+    if (mx > 0.f) {
+      int ex;
+      frexpf(mx, &ex);
+      e = 14 - ex;
     }
-  }
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  int e = 0;
-  if (mx > 0.f) {
-    int ex;
-    frexpf(mx, &ex);
-    e = 14 - ex;
-  }
-  if (u0 == 0) texp[row] = e;
-  for (int u = u0; u < units; u += 64) {
-    float v[16];
-    load16(u, v);
+    if (u0 == 0) texp[row] = e;
+    return e;
+  };
+  auto split = [&](int u, const float v[16], int e) {
     uint4 *o = ahl + ((m32 * c4n + (u >> 3)) * 8 + (u & 7)) * 128;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
@@ -136,6 +131,46 @@ __global__ __launch_bounds__(256) void k_af16split(
       }
       o[r + 32 * h] = __builtin_bit_cast(uint4, hi);
       o[64 + r + 32 * h] = __builtin_bit_cast(uint4, lo);
+    }
+  };
+  float mx = 0.f;
+  if constexpr (UL > 0) {
+    float v[UL][16];
+#pragma unroll
+    for (int j = 0; j < UL; j++) {
+      if (u0 + 64 * j < units) {
+        load16(u0 + 64 * j, v[j]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[j][i] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < UL; j++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float x = fabsf(v[j][i]);
+        mx = x < INFINITY ? fmaxf(mx, x) : mx;  // finite values only
+      }
+    const int e = row_exponent(mx);
+#pragma unroll
+    for (int j = 0; j < UL; j++)
+      if (u0 + 64 * j < units) split(u0 + 64 * j, v[j], e);
+  } else {
+    for (int u = u0; u < units; u += 64) {
+      float v[16];
+      load16(u, v);
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float x = fabsf(v[i]);
+        mx = x < INFINITY ? fmaxf(mx, x) : mx;
+      }
+    }
+    const int e = row_exponent(mx);
+    for (int u = u0; u < units; u += 64) {
+      float v[16];
+      load16(u, v);
+      split(u, v, e);
     }
   }
 }
@@ -679,9 +714,18 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
   const uint4 *abase = ahl + (int64_t)m32 * c4n * 1024 + lane;
   auto a_ptr = [&](int kg, int st) { return abase + ((int64_t)kg * 8 + st) * 128; };
 
+  // D holds the running scale segment.  With one segment per k group
+  // (DEFER), acc += s * D of a finished segment is deferred to the first step
+  // of the next one, tile by tile just before the MFMA that restarts D[n], so
+  // those FMAs overlap the other tiles' MFMAs instead of stalling on the last
+  // ones before the barrier (s_pend: the finished segment's scales; zero
+  // before the first segment).  Shorter segments apply it at once (deferring
+  // there costs more registers than the tile has).
+  constexpr bool DEFER = SEGJ == 4;
   float16v acc[NT], D[NT];
 #pragma unroll
-  for (int n = 0; n < NT; n++) acc[n] = (float16v){};
+  for (int n = 0; n < NT; n++) acc[n] = (float16v){}, D[n] = (float16v){};
+  float s_pend[4] = {0.f, 0.f, 0.f, 0.f};
   const float16v zero16 = (float16v){};
 
   // Ring of activation fragments (slot = step), loaded PD steps ahead.  Loads
@@ -724,6 +768,10 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
 #pragma unroll
       for (int n = 0; n < NT; n++) {
         const half8 b = __builtin_bit_cast(half8, bl[buf][(n * 8 + st) * 64 + lane]);
+        if (DEFER && seg_start) {
+#pragma unroll
+          for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
+        }
         D[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, b, seg_start ? zero16 : D[n], 0, 0, 0);
         D[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, b, D[n], 0, 0, 0);
       }
@@ -732,14 +780,22 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
       if (st >= PD) dequant_quarter(kgn, mnext, buf ^ 1, st - PD);
       if ((st + 1) % (2 * SEGJ) == 0) {
         const float4 s4 = *reinterpret_cast<const float4 *>(&scl[buf][st / (2 * SEGJ)][lc][0]);
-        const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
+        s_pend[0] = s4.x, s_pend[1] = s4.y, s_pend[2] = s4.z, s_pend[3] = s4.w;
+        if constexpr (!DEFER) {
 #pragma unroll
-        for (int n = 0; n < NT; n++)
+          for (int n = 0; n < NT; n++)
 #pragma unroll
-          for (int v = 0; v < 16; v++) acc[n][v] = fmaf(sc[n], D[n][v], acc[n][v]);
+            for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
+        }
       }
     }
     __syncthreads();
+  }
+  if constexpr (DEFER) {
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
   }
 
   // Epilogue: stage the wave's 32 x TC tile row-major in LDS (the weight
@@ -812,9 +868,14 @@ struct ReduceSet {
   int N[GMAX];
   int n;
 };
+// Thread = VW consecutive elements of one member (VW = 4: every N % 4 == 0
+// and y 16-byte aligned, so a piece never straddles rows or members).  The
+// splits are added in split order, four loads in flight at a time.
+template <int VW>
 __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part,
                                                      const ReduceSet rs, int ksplit) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  typedef float fv __attribute__((ext_vector_type(VW)));
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VW;
   if (i >= rs.e_end[rs.n - 1]) return;
   int m = 0;
 #pragma unroll
@@ -822,11 +883,28 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
     if (j + 1 < rs.n && i >= rs.e_end[j]) m = j + 1;
   const int64_t li = i - (m ? rs.e_end[m - 1] : 0);
   const int64_t mn = rs.e_end[m] - (m ? rs.e_end[m - 1] : 0);
-  const float *p = part + rs.part_off[m] + li;
-  float s = 0.f;
-  for (int k = 0; k < ksplit; k++) s += p[(int64_t)k * mn];
+  const fv *p = reinterpret_cast<const fv *>(part + rs.part_off[m] + li);
+  const int64_t step = mn / VW;
+  fv s = (fv)(0.f);
+  int k = 0;
+  for (; k + 4 <= ksplit; k += 4) {
+    const fv x0 = p[k * step], x1 = p[(k + 1) * step];
+    const fv x2 = p[(k + 2) * step], x3 = p[(k + 3) * step];
+    s += x0;
+    s += x1;
+    s += x2;
+    s += x3;
+  }
+  for (; k < ksplit; k++) s += p[k * step];
   const float *b = rs.bias[m];
-  rs.y[m][li] = s + (b ? b[li % rs.N[m]] : 0.f);
+  float *y = rs.y[m] + li;
+  if constexpr (VW == 1) {
+    *y = s[0] + (b ? b[li % rs.N[m]] : 0.f);
+  } else {
+    const int64_t c = li % rs.N[m];
+    if (b) s += *reinterpret_cast<const fv *>(b + c);
+    *reinterpret_cast<fv *>(y) = s;
+  }
 }
 
 // ------------------------------------------------------ decode MFMA GEMV
@@ -1604,8 +1682,18 @@ mg_status prefill_run(mg_ctx *ctx, int n, const mg_weight *const *w, const float
   int *texp = reinterpret_cast<int *>(base + p.off_b);
   float *part = p.ksplit > 1 ? reinterpret_cast<float *>(base + p.off_c) : nullptr;
   const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
-  hipLaunchKernelGGL(k_af16split, dim3((unsigned)(p.mpad / 4)), dim3(256), 0, st, a_dev, M,
-                     w0->K, (int)d.c4, vec, ahl, texp);
+  {
+    const int ul = (int)((d.c4 * 8 + 63) / 64);  // 16-k pieces per lane
+#define MG_SPLIT_LAUNCH(UL_)                                                                   \
+  hipLaunchKernelGGL((k_af16split<UL_>), dim3((unsigned)(p.mpad / 4)), dim3(256), 0, st, a_dev, \
+                     M, w0->K, (int)d.c4, vec, ahl, texp)
+    if (ul == 1) MG_SPLIT_LAUNCH(1);
+    else if (ul == 2) MG_SPLIT_LAUNCH(2);
+    else if (ul == 3) MG_SPLIT_LAUNCH(3);
+    else if (ul == 4) MG_SPLIT_LAUNCH(4);
+    else MG_SPLIT_LAUNCH(0);
+#undef MG_SPLIT_LAUNCH
+  }
   MG_TRY(mg_launch_check("k_af16split"));
   const int has_zp = d.zp_kind == MG_ZP_UINT4;
   PrefillSet ps{};
@@ -1650,8 +1738,19 @@ mg_status prefill_run(mg_ctx *ctx, int n, const mg_weight *const *w, const float
 #undef MG_GEMM_LAUNCH
   MG_TRY(mg_launch_check("k_gemm_f16split"));
   if (p.ksplit > 1) {
-    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((eend + 255) / 256)), dim3(256), 0, st,
-                       part, rs, p.ksplit);
+    // Four elements per thread when no piece can straddle a row: every N % 4
+    // == 0, y and the bias 16-byte aligned (partial offsets are then
+    // multiples of 4 elements and the buffer is aligned).
+    bool v4 = true;
+    for (int i = 0; i < n; i++)
+      v4 = v4 && rs.N[i] % 4 == 0 && reinterpret_cast<uintptr_t>(rs.y[i]) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(rs.bias[i]) % 16 == 0;
+    if (v4)
+      hipLaunchKernelGGL(k_gemm_reduce<4>, dim3((unsigned)((eend / 4 + 255) / 256)), dim3(256),
+                         0, st, part, rs, p.ksplit);
+    else
+      hipLaunchKernelGGL(k_gemm_reduce<1>, dim3((unsigned)((eend + 255) / 256)), dim3(256), 0,
+                         st, part, rs, p.ksplit);
     MG_TRY(mg_launch_check("k_gemm_reduce"));
   }
   return MG_OK;

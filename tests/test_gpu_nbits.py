@@ -201,6 +201,25 @@ def test_qwen_shapes_column_subset(ops, proj, k, n, m):
     assert G.rms_error(got, ref) <= TOL, G.rms_error(got, ref)
 
 
+@pytest.mark.parametrize("m,k,n,bias", [
+    (48, 4096, 200, True),    # longest row kept in registers by the activation prepass
+    (48, 4100, 130, True),    # longer rows (read twice); N % 4 != 0 (scalar split-K sum)
+    (96, 2048, 64, False),    # split K, four-wide sum
+    (300, 8192, 36, True),    # many splits (sum in groups of four plus a remainder)
+])
+def test_prefill_long_rows_and_split_sums(ops, m, k, n, bias):
+    rng = np.random.default_rng(m + k + n)
+    bs = 128
+    b, s, zp = make_nbits(rng, n, k, bs, "packed", 0.002, 0.02)
+    bv = rng.standard_normal(n).astype(np.float32) if bias else None
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs, bias=bv)
+    y = w(a)
+    w.release()
+    ref = oracle.matmul_nbits(a, b, s, zp, k=k, n=n, block_size=bs, bias=bv)
+    assert G.rms_error(y, ref) <= TOL, G.rms_error(y, ref)
+
+
 LLAMA = [("q", 2048, 2048), ("k", 2048, 512), ("up", 2048, 8192), ("down", 8192, 2048),
          ("lm_head", 2048, 128256)]
 
