@@ -645,13 +645,32 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
 #pragma unroll
   for (int h = 0; h < PH; h++) {
     const int u = t + 256 * h;
-    dq_cgi[h] = PH * nt + (u >> 8);
+    dq_cgi[h] = PH * nt + h;  // u >> 8 == h (t < 256), written so it is seen as uniform
     dq_col[h] = u & 63;
     dq_c[h] = (u >> 8) * 64 + dq_col[h];  // column within the tile
     const int n32 = dq_c[h] >> 5;
     dq_dst[h] = (n32 * 8 + (dq_g >> 1)) * 64 + (dq_c[h] & 31) + 32 * (dq_g & 1);
   }
   const int nbm1 = nb - 1, nbhm1 = nbh - 1;
+  // Weight tables and activations are read with raw buffer loads: a
+  // wave-uniform resource (the column group's, or the wave's 32-row tile's,
+  // base), a fixed per-lane byte offset and a uniform offset, so no per-lane
+  // 64-bit address arithmetic is needed.  All offsets stay inside the tensors.
+  auto rsrc = [](const void *base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7ffffff0,
+                                             0x00020000);
+  };
+  __amdgpu_buffer_rsrc_t r_wq[PH], r_zp[PH], r_sc[PH];
+#pragma unroll
+  for (int h = 0; h < PH; h++) {
+    const int64_t cgi = dq_cgi[h];
+    r_wq[h] = rsrc(wq + cgi * c4n * 256);
+    r_zp[h] = rsrc(zp4 + cgi * nbh * 64);
+    r_sc[h] = rsrc(scales + cgi * nb * 64);
+  }
+  const unsigned vo16 = 16u * lane;                   // this lane's uint4
+  const unsigned vo_zp = (unsigned)sz_pos(lane);      // dq_col[h] == lane for every h
+  const unsigned vo_sc = 4u * vo_zp;
   // Dequantisation masks held in VGPRs so that each pair is one v_and_or_b32
   // (VOP3 takes no literal operands here).
   uint32_t v_mlo, v_mhi, v_magic;
@@ -662,6 +681,7 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
     uint4 pk[PH];
     uint32_t zb[PH], zb2[PH];  // zero-point bytes of the k group's first two byte slots
     float sc[PH];
+    uint32_t z1[PH], z16[PH];  // dequantisation constants (SEGJ == 4: one block per k group)
   };
   // Branch-free: indices are clamped; blocks past the last (k padding) get a
   // zero scale when the scale is staged.
@@ -671,16 +691,17 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
     const int zbyte0 = min(blk0 / 2, nbhm1), zbyte1 = min(blk0 / 2 + 1, nbhm1);
 #pragma unroll
     for (int h = 0; h < PH; h++) {
-      const int64_t cgi = dq_cgi[h];
-      m.pk[h] = wq[((cgi * c4n + kg) * 4 + dq_g) * 64 + dq_col[h]];
-      const int sc_col = sz_pos(dq_col[h]);
-      m.zb[h] = zp4[(cgi * nbh + zbyte0) * 64 + sc_col];
-      m.zb2[h] = SEGJ == 1 ? zp4[(cgi * nbh + zbyte1) * 64 + sc_col] : 0u;
-      m.sc[h] = scales[(cgi * nb + min(blks, nbm1)) * 64 + sc_col];
+      m.pk[h] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(r_wq[h], vo16, (kg * 4 + dq_g) * 1024, 0));
+      m.zb[h] = __builtin_amdgcn_raw_buffer_load_b8(r_zp[h], vo_zp, zbyte0 * 64, 0);
+      m.zb2[h] = SEGJ == 1 ? __builtin_amdgcn_raw_buffer_load_b8(r_zp[h], vo_zp, zbyte1 * 64, 0)
+                           : 0u;
+      m.sc[h] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(r_sc[h], vo_sc, min(blks, nbm1) * 256, 0));
     }
   };
   // Dequantises dword j (32-k quarter j) of the packed uint4 into buffer buf.
-  auto dequant_quarter = [&](int kg, const Meta &m, int buf, int j) {
+  auto dequant_quarter = [&](int kg, Meta &m, int buf, int j) {
     const int blk0 = (kg * KGRP) >> lbs;
     const int blk = (kg * KGRP + 32 * j) >> lbs;
     const int sh = ((blk & 1) + 2 * (blk / 2 - blk0 / 2)) * 4;
@@ -689,13 +710,20 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
       // Loaded values are first touched here (empty asm): arithmetic on them
       // would otherwise be hoisted next to the loads and wait on them there.
       uint32_t w = j == 0 ? m.pk[h].x : j == 1 ? m.pk[h].y : j == 2 ? m.pk[h].z : m.pk[h].w;
-      uint32_t zb = m.zb[h], zb2 = m.zb2[h];
-      asm volatile("" : "+v"(w), "+v"(zb), "+v"(zb2));
-      zb |= zb2 << 8;
-      const uint32_t z = has_zp ? (zb >> sh) & 15u : 8u;
-      // -(1024 + z) and -(1024 + 16 z) in fp16 are 0xE400 + z and + 16 z.
-      const uint32_t z1 = 0xE400E400u + z * 0x00010001u;
-      const uint32_t z16 = 0xE400E400u + z * 0x00100010u;
+      asm volatile("" : "+v"(w));
+      uint32_t z1, z16;
+      if (SEGJ < 4 || j == 0) {  // with SEGJ == 4 the block (and z) spans the k group
+        uint32_t zb = m.zb[h], zb2 = m.zb2[h];
+        asm volatile("" : "+v"(zb), "+v"(zb2));
+        zb |= zb2 << 8;
+        const uint32_t z = has_zp ? (zb >> sh) & 15u : 8u;
+        // -(1024 + z) and -(1024 + 16 z) in fp16 are 0xE400 + z and + 16 z.
+        z1 = 0xE400E400u + z * 0x00010001u;
+        z16 = 0xE400E400u + z * 0x00100010u;
+        m.z1[h] = z1, m.z16[h] = z16;
+      } else {
+        z1 = m.z1[h], z16 = m.z16[h];
+      }
       bl[buf][dq_dst[h] + 2 * j * 64] = deq8(w, v_mlo, v_mhi, v_magic,
                                              __builtin_bit_cast(half2v, z1),
                                              __builtin_bit_cast(half2v, z16));
@@ -710,9 +738,12 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
       }
     }
   };
-  // Activation fragment of step s of k group kg: hi at +0, lo at +64.
-  const uint4 *abase = ahl + (int64_t)m32 * c4n * 1024 + lane;
-  auto a_ptr = [&](int kg, int st) { return abase + ((int64_t)kg * 8 + st) * 128; };
+  // Activation fragment of step s of k group kg: hi at +0, lo at +64 uint4.
+  const __amdgpu_buffer_rsrc_t r_a = rsrc(ahl + (int64_t)m32 * c4n * 1024);
+  auto a_load = [&](int kg, int st, int part) __attribute__((always_inline)) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         r_a, vo16, ((kg * 8 + st) * 128 + 64 * part) * 16, 0));
+  };
 
   // D holds the running scale segment.  With one segment per k group
   // (DEFER), acc += s * D of a finished segment is deferred to the first step
@@ -735,8 +766,8 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
   uint4 ah[8], al[8];
 #pragma unroll
   for (int ss = 0; ss < PD; ss++) {
-    ah[ss] = a_ptr(kg0, ss)[0];
-    al[ss] = a_ptr(kg0, ss)[64];
+    ah[ss] = a_load(kg0, ss, 0);
+    al[ss] = a_load(kg0, ss, 1);
   }
   {
     Meta m0;
@@ -758,8 +789,8 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
       {
         const int sn = (st + PD) & 7;
         const int kn = min(kg + ((st + PD) >> 3), kg1 - 1);
-        ah[sn] = a_ptr(kn, sn)[0];
-        al[sn] = a_ptr(kn, sn)[64];
+        ah[sn] = a_load(kn, sn, 0);
+        al[sn] = a_load(kn, sn, 1);
       }
       __builtin_amdgcn_sched_barrier(0);
       const bool seg_start = (st % (2 * SEGJ)) == 0;
