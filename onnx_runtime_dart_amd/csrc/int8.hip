@@ -72,21 +72,38 @@ __global__ __launch_bounds__(256) void k_i8_prep_b(
   frag[bi * per_batch + idx] = u.v;
 }
 
-// Column sums of B' and cb per column; one thread per (batch, column).
+// Column sums of B' and cb per column.  Workgroup = 64 columns of one batch
+// (lane = column); its four waves take every fourth row k, each lane with 16
+// row loads in flight, and the four partial sums meet in LDS (integer sums:
+// exact in any order).
 __global__ __launch_bounds__(256) void k_i8_colsum(
     const uint8_t *__restrict__ b, int b_signed, int64_t K, int64_t N,
     int64_t npad, int zb_scalar, const int32_t *__restrict__ zb, int zb_len,
     int32_t *__restrict__ colsum, int32_t *__restrict__ cb) {
-  const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  __shared__ int part[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * 64 + lane;
   const int64_t bi = blockIdx.y;
-  if (col >= npad) return;
   const int flip = b_signed ? 0 : 0x80;
+  const bool live = col < N;
+  const uint8_t *bc = b + bi * K * N + (live ? col : 0);
+  constexpr int U = 16;
   int s = 0;
-  if (col < N)
-    for (int64_t k = 0; k < K; k++) s += (int8_t)(b[(bi * K + k) * N + col] ^ flip);
-  colsum[bi * npad + col] = s;
+  int64_t k = wave;
+  for (; k + 4 * (U - 1) < K; k += 4 * U) {
+    int x[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) x[u] = bc[(k + 4 * u) * N];
+#pragma unroll
+    for (int u = 0; u < U; u++) s += (int8_t)(x[u] ^ flip);
+  }
+  for (; k < K; k += 4) s += (int8_t)(bc[k * N] ^ flip);
+  part[wave][lane] = live ? s : 0;
+  __syncthreads();
+  if (wave != 0 || col >= npad) return;
+  colsum[bi * npad + col] = part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
   int z = zb_scalar;
-  if (zb && zb_len > 0 && col < N) z = zb[col % zb_len];
+  if (zb && zb_len > 0 && live) z = zb[col % zb_len];
   cb[bi * npad + col] = (b_signed ? 0 : 128) - z;
 }
 
@@ -473,7 +490,7 @@ mg_status mg_int8_prepack_dev(mg_ctx *ctx, mg_weight *w, const void *b_dev,
                      static_cast<const uint8_t *>(b_dev), b_signed, K, N, n32, kqp,
                      reinterpret_cast<int4v *>(w->i8.bq));
   MG_TRY(mg_launch_check("k_i8_prep_b"));
-  hipLaunchKernelGGL(k_i8_colsum, dim3((unsigned)((w->i8.npad + 255) / 256), 1), dim3(256), 0,
+  hipLaunchKernelGGL(k_i8_colsum, dim3((unsigned)((w->i8.npad + 63) / 64), 1), dim3(256), 0,
                      st, static_cast<const uint8_t *>(b_dev), b_signed, K, N, w->i8.npad,
                      zb_scalar, zb_dev, zb_len, w->i8.colsum, w->i8.cb);
   return mg_launch_check("k_i8_colsum");
@@ -656,7 +673,7 @@ mg_status mg_int8_run_batched(mg_ctx *ctx, const void *a_dev, int32_t a_signed,
                      dim3(256), 0, st, static_cast<const uint8_t *>(b_dev), b_signed, K, N,
                      (int)n32, (int)kqp, reinterpret_cast<int4v *>(bq));
   MG_TRY(mg_launch_check("k_i8_prep_b"));
-  hipLaunchKernelGGL(k_i8_colsum, dim3((unsigned)((npad + 255) / 256), (unsigned)b_batch),
+  hipLaunchKernelGGL(k_i8_colsum, dim3((unsigned)((npad + 63) / 64), (unsigned)b_batch),
                      dim3(256), 0, st, static_cast<const uint8_t *>(b_dev), b_signed, K, N,
                      npad, zb_scalar, zb_len ? zb_dev : nullptr, zb_len, colsum, cb);
   MG_TRY(mg_launch_check("k_i8_colsum"));
