@@ -1049,11 +1049,23 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   float *__restrict__ y = gs.y[gm];
   const int N = gs.N[gm];
   const int c16 = lane & 15, g = lane >> 4;
-  const uint4 *wp = wq + (int64_t)cg * c4n * 256 + g * 64 + c16;
+  // Raw buffer loads: wave-uniform resources (the column group's tables, the
+  // activation fragments), a fixed lane byte offset and a uniform offset.  The
+  // scale resource spans exactly the column group's nb blocks and the block
+  // offset goes in the vector offset (the range check ignores the scalar
+  // one), so blocks past the last (k padding) read as zero scales.
+  auto rsrc = [](const void *base, int bytes) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes,
+                                             0x00020000);
+  };
+  const __amdgpu_buffer_rsrc_t r_w = rsrc(wq + (int64_t)cg * c4n * 256, 0x7ffffff0);
+  const __amdgpu_buffer_rsrc_t r_a = rsrc(ahl, 0x7ffffff0);
   // Scales and zero-point bytes of the lane's four columns are adjacent
   // (sz_pos): one 16-byte and one 4-byte load per block.
-  const float4 *sp = reinterpret_cast<const float4 *>(scales + (int64_t)cg * nb * 64) + c16;
-  const uint32_t *zq = reinterpret_cast<const uint32_t *>(zp4 + (int64_t)cg * nbh * 64) + c16;
+  const __amdgpu_buffer_rsrc_t r_s = rsrc(scales + (int64_t)cg * nb * 64, nb * 256);
+  const __amdgpu_buffer_rsrc_t r_z = rsrc(zp4 + (int64_t)cg * nbh * 64, 0x7ffffff0);
+  const unsigned vo_w = 16u * (unsigned)(g * 64 + c16), vo_a = 16u * (unsigned)lane;
+  const unsigned vo_s = 16u * (unsigned)c16, vo_z = 4u * (unsigned)c16;
 
   // Raw loads of one k group; they are first touched in compute(), so the
   // wait for them does not also wait for the next k group's loads.
@@ -1063,20 +1075,24 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
     float4 s[NBK];       // scales of the four tiles per block
     uint32_t zw[NBK];    // zero-point bytes of the four tiles per block
   };
+  auto ld16 = [](__amdgpu_buffer_rsrc_t r, unsigned vo, int so) __attribute__((always_inline)) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
+  };
   auto fetch = [&](int kg, Ring &R) {
 #pragma unroll
-    for (int tl = 0; tl < 4; tl++) R.w[tl] = wp[(int64_t)kg * 256 + tl * 16];
+    for (int tl = 0; tl < 4; tl++) R.w[tl] = ld16(r_w, vo_w, (kg * 256 + tl * 16) * 16);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const uint4 *ap = ahl + ((int64_t)(kg * 4 + j) * 2) * 64 + lane;
-      R.ah[j] = ap[0];
-      R.al[j] = ap[64];
+      R.ah[j] = ld16(r_a, vo_a, (kg * 4 + j) * 2048);
+      R.al[j] = ld16(r_a, vo_a, (kg * 4 + j) * 2048 + 1024);
     }
 #pragma unroll
     for (int q = 0; q < NBK; q++) {
-      const int bc = min((kg * KGRP + q * 32 * SEGJ) >> lbs, nb - 1);
-      R.s[q] = sp[(int64_t)bc * 16];
-      R.zw[q] = has_zp ? zq[(int64_t)(bc >> 1) * 16] : 0x88888888u;
+      const int b = (kg * KGRP + q * 32 * SEGJ) >> lbs;  // past nb: k padding, zero scale
+      R.s[q] = __builtin_bit_cast(float4, ld16(r_s, vo_s + 256u * (unsigned)b, 0));
+      const int bc = min(b, nb - 1);
+      R.zw[q] = has_zp ? __builtin_amdgcn_raw_buffer_load_b32(r_z, vo_z, (bc >> 1) * 64, 0)
+                       : 0x88888888u;
     }
   };
   uint32_t v_mlo, v_mhi, v_magic;
@@ -1102,12 +1118,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
       const bool seg_start = (j % SEGJ) == 0;
       if (seg_start) {
         const int b = (kg * KGRP + q * 32 * SEGJ) >> lbs;
-        const bool live = b < nb;
         const uint32_t sh = (min(b, nb - 1) & 1) * 4;
-        sq[0] = live ? R.s[q].x : 0.f;
-        sq[1] = live ? R.s[q].y : 0.f;
-        sq[2] = live ? R.s[q].z : 0.f;
-        sq[3] = live ? R.s[q].w : 0.f;
+        sq[0] = R.s[q].x;
+        sq[1] = R.s[q].y;
+        sq[2] = R.s[q].z;
+        sq[3] = R.s[q].w;
 #pragma unroll
         for (int tl = 0; tl < 4; tl++) {
           const uint32_t zv = (R.zw[q] >> (8 * tl + sh)) & 15u;
