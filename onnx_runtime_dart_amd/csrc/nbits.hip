@@ -1032,16 +1032,20 @@ __global__ __launch_bounds__(256) void k_af16split16(const float *__restrict__ a
 // are added in wave order through LDS; the row exponents come off at the end.
 // Packed codes, scales, zero points and activation fragments of the next k
 // group are loaded while the current one is computed.
-template <int SEGJ, int NW>
+// TPW = 16-column tiles per workgroup (4: the whole column group; 2 or 1
+// give narrow weights 2 or 4 workgroups per column group, tiles t0 ..).
+template <int SEGJ, int NW, int TPW>
 __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
     const uint4 *__restrict__ ahl, const int *__restrict__ texp, const GemvSet gs, int M,
     int c4n, int nb, int nbh, int lbs, int has_zp) {
-  __shared__ float4 red[NW][4][64];  // [wave][tile][lane]
-  constexpr int NBK = 4 / SEGJ;     // blocks (scale segments) per k group
+  __shared__ float4 red[NW][TPW][64];  // [wave][tile][lane]
+  constexpr int NBK = 4 / SEGJ;       // blocks (scale segments) per k group
+  constexpr int WPG = 4 / TPW;        // workgroups per column group
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   int cg;
-  const int gm = gemv_member(gs, blockIdx.x, &cg);
+  const int gm = gemv_member(gs, (int)blockIdx.x / WPG, &cg);
+  const int t0 = ((int)blockIdx.x % WPG) * TPW;  // first tile of this workgroup
   const uint4 *__restrict__ wq = gs.wq[gm];
   const float *__restrict__ scales = gs.scales[gm];
   const uint8_t *__restrict__ zp4 = gs.zp4[gm];
@@ -1071,8 +1075,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   // wait for them does not also wait for the next k group's loads.
   struct Ring {
     uint4 ah[4], al[4];  // activation fragments (hi, lo) per 32-k step
-    uint4 w[4];          // packed codes per tile
-    float4 s[NBK];       // scales of the four tiles per block
+    uint4 w[TPW];        // packed codes per tile
+    float s[NBK][TPW];   // scales of the workgroup's tiles per block
     uint32_t zw[NBK];    // zero-point bytes of the four tiles per block
   };
   auto ld16 = [](__amdgpu_buffer_rsrc_t r, unsigned vo, int so) __attribute__((always_inline)) {
@@ -1080,7 +1084,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   };
   auto fetch = [&](int kg, Ring &R) {
 #pragma unroll
-    for (int tl = 0; tl < 4; tl++) R.w[tl] = ld16(r_w, vo_w, (kg * 256 + tl * 16) * 16);
+    for (int tl = 0; tl < TPW; tl++) R.w[tl] = ld16(r_w, vo_w, (kg * 256 + (t0 + tl) * 16) * 16);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       R.ah[j] = ld16(r_a, vo_a, (kg * 4 + j) * 2048);
@@ -1089,7 +1093,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
 #pragma unroll
     for (int q = 0; q < NBK; q++) {
       const int b = (kg * KGRP + q * 32 * SEGJ) >> lbs;  // past nb: k padding, zero scale
-      R.s[q] = __builtin_bit_cast(float4, ld16(r_s, vo_s + 256u * (unsigned)b, 0));
+      const unsigned so = vo_s + 4u * (unsigned)t0 + 256u * (unsigned)b;
+      if constexpr (TPW == 4) {
+        const float4 x = __builtin_bit_cast(float4, ld16(r_s, so, 0));
+        R.s[q][0] = x.x, R.s[q][1] = x.y, R.s[q][2] = x.z, R.s[q][3] = x.w;
+      } else if constexpr (TPW == 2) {
+        const float2 x = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r_s, so, 0, 0));
+        R.s[q][0] = x.x, R.s[q][1] = x.y;
+      } else {
+        R.s[q][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_s, so, 0, 0));
+      }
       const int bc = min(b, nb - 1);
       R.zw[q] = has_zp ? __builtin_amdgcn_raw_buffer_load_b32(r_z, vo_z, (bc >> 1) * 64, 0)
                        : 0x88888888u;
@@ -1100,9 +1113,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   asm volatile("v_mov_b32 %0, %1" : "=v"(v_mhi) : "s"(0x00F000F0u));
   asm volatile("v_mov_b32 %0, %1" : "=v"(v_magic) : "s"(0x64006400u));
 
-  float4v acc[4], D[4];
+  float4v acc[TPW], D[TPW];
 #pragma unroll
-  for (int tl = 0; tl < 4; tl++) acc[tl] = (float4v){0.f, 0.f, 0.f, 0.f};
+  for (int tl = 0; tl < TPW; tl++) acc[tl] = (float4v){0.f, 0.f, 0.f, 0.f};
   const float4v zero4 = (float4v){0.f, 0.f, 0.f, 0.f};
 
   // At the start of each block: its scales (zero past the last block, i.e.
@@ -1110,8 +1123,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   // as fp16 pairs; -(1024 + z) in fp16 is 0xE400 + z (exact), so they are
   // built with integer arithmetic.
   auto compute = [&](int kg, const Ring &R) {
-    float sq[4];
-    uint32_t z1[4], z16[4];
+    float sq[TPW];
+    uint32_t z1[TPW], z16[TPW];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int q = j / SEGJ;
@@ -1119,22 +1132,20 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
       if (seg_start) {
         const int b = (kg * KGRP + q * 32 * SEGJ) >> lbs;
         const uint32_t sh = (min(b, nb - 1) & 1) * 4;
-        sq[0] = R.s[q].x;
-        sq[1] = R.s[q].y;
-        sq[2] = R.s[q].z;
-        sq[3] = R.s[q].w;
 #pragma unroll
-        for (int tl = 0; tl < 4; tl++) {
-          const uint32_t zv = (R.zw[q] >> (8 * tl + sh)) & 15u;
+        for (int tl = 0; tl < TPW; tl++) sq[tl] = R.s[q][tl];
+#pragma unroll
+        for (int tl = 0; tl < TPW; tl++) {
+          const uint32_t zv = (R.zw[q] >> (8 * (t0 + tl) + sh)) & 15u;
           z1[tl] = 0xE400E400u + zv * 0x00010001u;
           z16[tl] = 0xE400E400u + zv * 0x00100010u;
         }
       }
       const half8 a_h = __builtin_bit_cast(half8, R.ah[j]);
       const half8 a_l = __builtin_bit_cast(half8, R.al[j]);
-      half8 bt[4];
+      half8 bt[TPW];
 #pragma unroll
-      for (int tl = 0; tl < 4; tl++) {
+      for (int tl = 0; tl < TPW; tl++) {
         const uint32_t x = j == 0 ? R.w[tl].x : j == 1 ? R.w[tl].y : j == 2 ? R.w[tl].z : R.w[tl].w;
         bt[tl] = __builtin_bit_cast(
             half8, deq8(x, v_mlo, v_mhi, v_magic, __builtin_bit_cast(half2v, z1[tl]),
@@ -1143,15 +1154,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
       // All hi products first, then all lo: each lo MFMA then follows its
       // tile's hi MFMA by three others instead of waiting on it.
 #pragma unroll
-      for (int tl = 0; tl < 4; tl++)
+      for (int tl = 0; tl < TPW; tl++)
         D[tl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, bt[tl], seg_start ? zero4 : D[tl], 0,
                                                        0, 0);
 #pragma unroll
-      for (int tl = 0; tl < 4; tl++)
+      for (int tl = 0; tl < TPW; tl++)
         D[tl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, bt[tl], D[tl], 0, 0, 0);
       if ((j + 1) % SEGJ == 0) {
 #pragma unroll
-        for (int tl = 0; tl < 4; tl++)
+        for (int tl = 0; tl < TPW; tl++)
 #pragma unroll
           for (int i = 0; i < 4; i++) acc[tl][i] = fmaf(sq[tl], D[tl][i], acc[tl][i]);
       }
@@ -1175,19 +1186,19 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   }
 
 #pragma unroll
-  for (int tl = 0; tl < 4; tl++)
+  for (int tl = 0; tl < TPW; tl++)
     red[wave][tl][lane] = make_float4(acc[tl][0], acc[tl][1], acc[tl][2], acc[tl][3]);
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
-    for (int tl = 0; tl < 4; tl++) {
+    for (int tl = 0; tl < TPW; tl++) {
       float4 s = red[0][tl][lane];
 #pragma unroll
       for (int w = 1; w < NW; w++) {
         const float4 o = red[w][tl][lane];
         s.x += o.x; s.y += o.y; s.z += o.z; s.w += o.w;
       }
-      const int col = cg * 64 + tl * 16 + c16;
+      const int col = cg * 64 + (t0 + tl) * 16 + c16;
       const float bv = (bias && col < N) ? bias[col] : 0.f;
       const float sv[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
@@ -1688,19 +1699,29 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
     // workgroups per CU) split K over 8 waves, so that their few workgroups
     // keep more k groups' loads in flight.  (16 waves would cap the kernel
     // at 128 registers and spill.)
+    // Tiles per workgroup: narrow weights (fewer column groups than CUs)
+    // take 2 or 1 of a column group's four 16-column tiles per workgroup.
+    const int64_t cus = std::max(ctx->num_cus, 1);
+    const int tpw = ng >= cus ? 4 : (2 * ng >= cus ? 2 : 1);
+    const int64_t wgs = ng * (4 / tpw);
     int nw = 4;
-    if ((int64_t)ng < 2 * (int64_t)std::max(ctx->num_cus, 1) && d.c4 >= 8) nw = 8;
-#define MG_DEC_LAUNCH(SJ_, NW_)                                                             \
-  hipLaunchKernelGGL((k_gemv_mfma<SJ_, NW_>), dim3((unsigned)ng), dim3(NW_ * 64), 0, st,     \
-                     ahl, texp, gs, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,               \
+    if (wgs < 2 * cus && d.c4 >= 8) nw = 8;
+#define MG_DEC_LAUNCH(SJ_, NW_, TPW_)                                                      \
+  hipLaunchKernelGGL((k_gemv_mfma<SJ_, NW_, TPW_>), dim3((unsigned)wgs), dim3(NW_ * 64), 0, \
+                     st, ahl, texp, gs, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,           \
                      __builtin_ctzll(d.bs), has_zp)
+#define MG_DEC_TPW(SJ_, NW_)                  \
+  if (tpw == 4) MG_DEC_LAUNCH(SJ_, NW_, 4);  \
+  else if (tpw == 2) MG_DEC_LAUNCH(SJ_, NW_, 2); \
+  else MG_DEC_LAUNCH(SJ_, NW_, 1)
 #define MG_DEC_NW(SJ_)               \
-  if (nw == 8) MG_DEC_LAUNCH(SJ_, 8); \
-  else MG_DEC_LAUNCH(SJ_, 4)
+  if (nw == 8) { MG_DEC_TPW(SJ_, 8); } \
+  else { MG_DEC_TPW(SJ_, 4); }
     if (segj == 1) { MG_DEC_NW(1); }
     else if (segj == 2) { MG_DEC_NW(2); }
     else { MG_DEC_NW(4); }
 #undef MG_DEC_NW
+#undef MG_DEC_TPW
 #undef MG_DEC_LAUNCH
     return mg_launch_check("k_gemv_mfma");
   }
