@@ -1701,7 +1701,10 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
     // at 128 registers and spill.)
     // Tiles per workgroup: narrow weights (fewer column groups than CUs)
     // take 2 or 1 of a column group's four 16-column tiles per workgroup.
-    const int64_t cus = std::max(ctx->num_cus, 1);
+#ifndef MG_GEMV16_WG_PER_CU
+#define MG_GEMV16_WG_PER_CU 1
+#endif
+    const int64_t cus = std::max(ctx->num_cus, 1) * (int64_t)MG_GEMV16_WG_PER_CU;
     const int tpw = ng >= cus ? 4 : (2 * ng >= cus ? 2 : 1);
     const int64_t wgs = ng * (4 / tpw);
     int nw = 4;
