@@ -946,7 +946,11 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
 // v_mfma_f32_16x16x32_f16: for k group kg and 32-k step j,
 // ahl16[((kg * 4 + j) * 2 + h) * 64 + 16 g + r] holds the 8 fp16 (hi for
 // h = 0, lo for h = 1) of row r at k = 128 kg + 32 j + 8 g .. +7.  Rows >= M
-// and k >= K are zeros.  One workgroup per row (16 rows).
+// and k >= K are zeros.  One workgroup per row (16 rows).  P > 0: the row has
+// at most 256 P octets (8 k each, padding included) and thread t reads octets
+// t + 256 i (i < P) once, all loads in flight, converting them from registers;
+// P = 0 (longer rows) reads the row twice.
+template <int P>
 __global__ __launch_bounds__(256) void k_af16split16(const float *__restrict__ a, int64_t M,
                                                      int64_t K, int c4n, int vec,
                                                      uint4 *__restrict__ ahl,
@@ -955,6 +959,74 @@ __global__ __launch_bounds__(256) void k_af16split16(const float *__restrict__ a
   const int t = threadIdx.x, r = blockIdx.x;
   const bool live = r < M;
   const float *ar = a + (int64_t)r * K;
+  const int octets = c4n * 16;
+  auto load8 = [&](int o, float v[8]) __attribute__((always_inline)) {
+    const int64_t k0 = (int64_t)o * 8;
+    if (live && vec && k0 + 8 <= K) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(ar + k0);
+      const float4 x1 = *reinterpret_cast<const float4 *>(ar + k0 + 4);
+      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+      v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = (live && k0 + i < K) ? ar[k0 + i] : 0.f;
+    }
+  };
+  auto row_exponent = [&](float mx) __attribute__((always_inline)) {
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (mx > 0.f) {
+      int ex;
+      frexpf(mx, &ex);
+      e = 14 - ex;
+    }
+    if (t == 0) texp[r] = e;
+    return e;
+  };
+  auto split = [&](int o, const float v[8], int e) __attribute__((always_inline)) {
+    half8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float x = ldexpf(v[i], (i & 2) ? e - 4 : e);
+      const _Float16 hh = (_Float16)x;
+      float res = x - (float)hh;
+      if (!isfinite(res)) res = 0.f;
+      hi[i] = hh;
+      lo[i] = (_Float16)res;
+    }
+    const int kg = o >> 4, j = (o >> 2) & 3, g = o & 3;
+    uint4 *dst = ahl + ((int64_t)(kg * 4 + j) * 2) * 64 + 16 * g + r;
+    dst[0] = __builtin_bit_cast(uint4, hi);
+    dst[64] = __builtin_bit_cast(uint4, lo);
+  };
+  if constexpr (P > 0) {
+    float v[P][8];
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+      if (t + 256 * i < octets) {
+        load8(t + 256 * i, v[i]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[i][q] = 0.f;
+      }
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < P; i++)
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const float f = fabsf(v[i][q]);
+        mx = f < INFINITY ? fmaxf(mx, f) : mx;  // finite values only
+      }
+    const int e = row_exponent(mx);
+#pragma unroll
+    for (int i = 0; i < P; i++)
+      if (t + 256 * i < octets) split(t + 256 * i, v[i], e);
+    return;
+  }
   float mx = 0.f;
   if (live) {
     if (vec) {
@@ -978,44 +1050,11 @@ __global__ __launch_bounds__(256) void k_af16split16(const float *__restrict__ a
       }
     }
   }
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if ((t & 63) == 0) red[t >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int e = 0;
-  if (mx > 0.f) {
-    int ex;
-    frexpf(mx, &ex);
-    e = 14 - ex;
-  }
-  if (t == 0) texp[r] = e;
-  const int octets = c4n * 16;
+  const int e = row_exponent(mx);
   for (int o = t; o < octets; o += 256) {
-    const int64_t k0 = (int64_t)o * 8;
     float v[8];
-    if (live && vec && k0 + 8 <= K) {
-      const float4 x0 = *reinterpret_cast<const float4 *>(ar + k0);
-      const float4 x1 = *reinterpret_cast<const float4 *>(ar + k0 + 4);
-      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-      v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = (live && k0 + i < K) ? ar[k0 + i] : 0.f;
-    }
-    half8 hi, lo;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float x = ldexpf(v[i], (i & 2) ? e - 4 : e);
-      const _Float16 hh = (_Float16)x;
-      float res = x - (float)hh;
-      if (!isfinite(res)) res = 0.f;
-      hi[i] = hh;
-      lo[i] = (_Float16)res;
-    }
-    const int kg = o >> 4, j = (o >> 2) & 3, g = o & 3;
-    uint4 *dst = ahl + ((int64_t)(kg * 4 + j) * 2) * 64 + 16 * g + r;
-    dst[0] = __builtin_bit_cast(uint4, hi);
-    dst[64] = __builtin_bit_cast(uint4, lo);
+    load8(o, v);
+    split(o, v, e);
   }
 }
 
@@ -1690,8 +1729,17 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
     uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
     int *texp = reinterpret_cast<int *>(base + p.off_b);
     const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
-    hipLaunchKernelGGL(k_af16split16, dim3(16), dim3(256), 0, st, a_dev, M, w0->K, (int)d.c4,
-                       vec, ahl, texp);
+    {
+      const int per = (int)((d.c4 * 16 + 255) / 256);  // octets per thread
+#define MG_SPLIT16(P_)                                                                          \
+  hipLaunchKernelGGL((k_af16split16<P_>), dim3(16), dim3(256), 0, st, a_dev, M, w0->K,        \
+                     (int)d.c4, vec, ahl, texp)
+      if (per == 1) MG_SPLIT16(1);
+      else if (per == 2) MG_SPLIT16(2);
+      else if (per <= 4) MG_SPLIT16(4);
+      else MG_SPLIT16(0);
+#undef MG_SPLIT16
+    }
     MG_TRY(mg_launch_check("k_af16split16"));
     const int has_zp = d.zp_kind == MG_ZP_UINT4;
     const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
