@@ -337,9 +337,12 @@ mg_status mg_conv_run(mg_ctx *ctx, const mg_conv_problem &p) {
   const int64_t out_sp = p.out[0] * p.out[1] * p.out[2];
   if (p.n == 0 || p.m == 0 || out_sp == 0) return MG_OK;
   const bool integer = p.xk != MG_CONV_F32;
-  // The 128 x 128 tile when it still gives about two workgroups per CU.
+  // The 128 x 128 tile when it still gives about two workgroups per CU and
+  // at most a quarter of its rows are padding (64 output channels, as in a
+  // ResNet stem, would waste half of its MFMA work).
   const int64_t big_wgs = ((out_sp + 127) / 128) * ((p.mg + 127) / 128) * p.n * p.group;
-  const bool big = !integer && big_wgs >= 2 * (int64_t)ctx->num_cus;
+  const bool big = !integer && big_wgs >= 2 * (int64_t)ctx->num_cus &&
+                   3 * ((p.mg + 127) / 128 * 128) <= 4 * (int64_t)p.mg;
   const int64_t wgs = ((out_sp + (big ? 127 : 63)) / (big ? 128 : 64)) * p.n * p.group;
   if (wgs > 0x7fffffff || (p.mg + 63) / 64 > 65535)
     return mg_fail(MG_UNSUPPORTED, "conv: grid too large");
