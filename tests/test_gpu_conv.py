@@ -55,7 +55,8 @@ CONV = [
     ((1, 7, 9, 9), (5, 7, 4, 4), dict(auto_pad="SAME_UPPER", strides=[2, 2])),
     ((1, 7, 9, 9), (5, 7, 4, 4), dict(auto_pad="SAME_LOWER", strides=[2, 2])),
     ((1, 6, 11, 10), (4, 6, 3, 5), dict(auto_pad="VALID", strides=[1, 2])),
-    ((4, 64, 28, 28), (128, 64, 3, 3), dict(pads=[1, 1, 1, 1])),                 # large tile path
+    ((4, 64, 28, 28), (128, 64, 3, 3), dict(pads=[1, 1, 1, 1])),                 # K = 576
+    ((16, 8, 64, 64), (128, 8, 3, 3), dict(pads=[1, 1, 1, 1])),    # 512 tiles of 128 x 128
     ((1, 3, 224, 224), (64, 3, 7, 7), dict(strides=[2, 2], pads=[3, 3, 3, 3])),  # ResNet stem
     ((2, 256, 14, 14), (256, 256, 1, 1), {}),                                     # pointwise
 ]
@@ -82,6 +83,7 @@ CONVT = [
     ((3, 5, 21), (5, 4, 6), dict(strides=[4], pads=[1, 2])),                    # 1-D
     ((1, 3, 4, 5, 3), (3, 2, 2, 3, 3), dict(strides=[2, 1, 2], pads=[0, 1, 0, 1, 0, 1])),
     ((2, 64, 16, 16), (64, 32, 4, 4), dict(strides=[2, 2], pads=[1, 1, 1, 1])),  # VAE-like upsample
+    ((16, 16, 32, 32), (16, 128, 2, 2), dict(strides=[2, 2])),     # 512 tiles of 128 x 128
 ]
 
 
