@@ -39,6 +39,13 @@ SDPA = [
     ((1, 2, 1, 100), (1, 2, 100, 77), (1, 2, 77, 96), (1, 1, 1, 77)),        # one query, D 100, DV 96
     ((1, 1, 33, 128), (1, 1, 128, 65), (1, 1, 65, 128), (33, 65)),           # D = DV = 128
     ((8, 12, 128, 32), (8, 12, 32, 128), (8, 12, 128, 32), (8, 1, 1, 128)),  # MiniLM-shaped
+    # every tiled-kernel head / value size class (2 query tiles, ragged keys)
+    ((1, 2, 150, 32), (1, 2, 32, 200), (1, 2, 200, 64), (1, 1, 150, 200)),   # D 32, DV 64
+    ((1, 2, 150, 24), (1, 2, 24, 200), (1, 2, 200, 128), (1, 1, 1, 200)),    # D 24, DV 128
+    ((2, 1, 70, 64), (2, 1, 64, 90), (2, 1, 90, 32), ()),                    # D 64, DV 32
+    ((1, 2, 150, 48), (1, 2, 48, 200), (1, 2, 200, 100), (1, 1, 150, 200)),  # D 48, DV 100
+    ((1, 2, 150, 128), (1, 2, 128, 200), (1, 2, 200, 20), ()),               # D 128, DV 20
+    ((1, 2, 150, 96), (1, 2, 96, 200), (1, 2, 200, 64), (1, 1, 1, 200)),     # D 96, DV 64
 ]
 
 

@@ -78,6 +78,7 @@ CASES = [
     (12, 1000, 200, 256, "none", True),
     (16, 4100, 96, 128, "packed", True),
     (14, 640, 1000, 128, "none", False),
+    (6, 8320, 72, 128, "packed", True),      # rows past 8192 k: the prepass reads them twice
 ]
 
 
