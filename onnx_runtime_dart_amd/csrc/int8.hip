@@ -47,29 +47,67 @@ constexpr int TN = 128;  // workgroup tile columns
 constexpr int QS = 8;    // 32-k MFMA steps per LDS stage (256 k)
 constexpr int RA = 4;    // A register ring: steps loaded ahead of use
 
-// B (u8 or i8, [K, N] per batch) -> fragments bfrag[batch][n32][q][lane].
+// B (u8 or i8, [K, N] per batch) -> fragments bfrag[batch][n32][q][lane]
+// (lane l of fragment q holds column 32 n32 + l % 32, k = 128 (q / 4) +
+// 64 (l / 32) + 16 (q % 4) .. +15, re-centred to signed).  Workgroup = one
+// 32-column tile and one 128-k group (its four fragments q): the 128 x 32
+// byte block is read row by row with 16-byte loads where the row piece is
+// whole and aligned, staged in LDS, and each thread gathers its fragment's 16
+// bytes of one column from there.  Bytes outside [K, N] are stored as the
+// re-centring constant, so they come out as 0.  Grid: n32n * kqp / 4 per batch
+// (kqp is a multiple of 8).
 __global__ __launch_bounds__(256) void k_i8_prep_b(
     const uint8_t *__restrict__ b, int b_signed, int64_t K, int64_t N,
     int n32n, int kqp, int4v *__restrict__ frag) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t per_batch = (int64_t)n32n * kqp * 64;
+  __shared__ uint32_t tile[128][9];  // [k][32 columns as 8 words], one word of padding
+  const int t = threadIdx.x;
   const int64_t bi = blockIdx.y;
-  if (idx >= per_batch) return;
-  const int lane = (int)(idx & 63);
-  const int64_t t = idx >> 6;
-  const int q = (int)(t % kqp);
-  const int64_t n32 = t / kqp;
-  const int64_t col = n32 * 32 + (lane & 31);
-  const int64_t kb = (int64_t)(q >> 2) * 128 + 64 * (lane >> 5) + 16 * (q & 3);
-  const uint8_t *bb = b + bi * K * N;
-  const int flip = b_signed ? 0 : 0x80;
-  union { int4v v; int8_t x[16]; } u;
+  const int qgs = kqp / 4;
+  const int n32 = (int)blockIdx.x / qgs, qg = (int)blockIdx.x % qgs;
+  const uint32_t flip = b_signed ? 0u : 0x80u;
+  {
+    const int r = t >> 1, hh = t & 1;  // row of the block, 16-column half
+    const int64_t k = (int64_t)qg * 128 + r;
+    const int64_t c0 = (int64_t)n32 * 32 + 16 * hh;
+    const uint8_t *src = b + (bi * K + (k < K ? k : 0)) * N + c0;
+    uint32_t w[4];
+    if (k < K && c0 + 16 <= N && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+      const uint4 x = *reinterpret_cast<const uint4 *>(src);
+      w[0] = x.x, w[1] = x.y, w[2] = x.z, w[3] = x.w;
+    } else {
 #pragma unroll
-  for (int e = 0; e < 16; e++) {
-    const int64_t k = kb + e;
-    u.x[e] = (col < N && k < K) ? (int8_t)(bb[k * N + col] ^ flip) : (int8_t)0;
+      for (int q = 0; q < 4; q++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int64_t c = c0 + 4 * q + e;
+          const uint32_t by = (k < K && c < N) ? src[4 * q + e] : flip;
+          word |= by << (8 * e);
+        }
+        w[q] = word;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) tile[r][4 * hh + q] = w[q];
   }
-  frag[bi * per_batch + idx] = u.v;
+  __syncthreads();
+  const int lane = t & 63, qq = t >> 6;
+  const int col = lane & 31, kl = 64 * (lane >> 5) + 16 * qq;
+  const uint32_t fl4 = flip * 0x01010101u;
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t by = (tile[kl + 4 * q + e][col >> 2] >> (8 * (col & 3))) & 0xFFu;
+      word |= by << (8 * e);
+    }
+    o[q] = word ^ fl4;
+  }
+  const int64_t per_batch = (int64_t)n32n * kqp * 64;
+  const int64_t idx = ((int64_t)n32 * kqp + qg * 4 + qq) * 64 + lane;
+  frag[bi * per_batch + idx] = (int4v){(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
 }
 
 // Column sums of B' and cb per column.  Workgroup = 64 columns of one batch
