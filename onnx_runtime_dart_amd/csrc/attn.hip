@@ -710,10 +710,7 @@ size_t mg_attn_plan_split(const mg_ctx *ctx, mg_attn_problem *p) {
   const bool dec = p->S <= DEC_S;
   const int64_t gran = dec ? 64 : 32;
   const int64_t wgs = dec ? nbatch : nbatch * ((p->S + 127) / 128);
-  // Causal problems with many queries are not split: their early query
-  // tiles would leave most splits empty while the combine pass reads them.
-  if (wgs == 0 || p->T < 128 || p->DV == 0 || (p->causal && !dec) || wgs >= ctx->num_cus)
-    return 0;
+  if (wgs == 0 || p->T < 128 || p->DV == 0 || wgs >= ctx->num_cus) return 0;
   const int64_t want = std::min<int64_t>((2 * ctx->num_cus + wgs - 1) / wgs,
                                          (p->T + gran - 1) / gran);
   if (want < 2) return 0;
