@@ -1322,8 +1322,12 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
     // (2 in flight each) so that their few workgroups still keep enough bytes
     // in flight per CU.
     // (The 16-wave form is register-limited to one row and blocks <= 64.)
+#ifndef MG_GEMV_MAX_NW
+#define MG_GEMV_MAX_NW 16
+#endif
     int64_t nw = 4;
-    if (M == 1 && p.qpg >= 2 && ng_total * 4 < 8 * (int64_t)std::max(ctx->num_cus, 1)) nw = 16;
+    if (M == 1 && p.qpg >= 2 && ng_total * 4 < 8 * (int64_t)std::max(ctx->num_cus, 1))
+      nw = MG_GEMV_MAX_NW;
     nw = std::min<int64_t>(nw, std::max<int64_t>(d.c4, 4));
     if (nw > 4) nw = nw > 8 ? 16 : 8;
     const int pf = nw == 4 ? 4 : 2;
