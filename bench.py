@@ -256,27 +256,54 @@ def main():
         rng_r = np.random.default_rng(0x5EED0003 + r)
         rot.append([ops.NBitsWeight(*make_weight(rng_r, k, n), k=k, n=n, block_size=BLOCK,
                                     ctx=ctx) for _, k, n in QWEN3_PROJ])
-    lm_events = []
     state = {"i": 0}
 
-    def gemv_pass():
-        ws = rot[state["i"] % GEMV_ROTATE]
-        state["i"] += 1
-        for (_, k, n), w in zip(QWEN3_PROJ[:-1], ws[:-1]):
+    def gemv_pass_on(ws):
+        for (_, k, n), w in zip(QWEN3_PROJ, ws):
             w.run_dev(acts[(1, k)].data_ptr(), 1, outs[(1, n)].data_ptr())
-        e0 = T.event()
-        ws[-1].run_dev(acts[(1, k_lm)].data_ptr(), 1, outs[(1, n_lm)].data_ptr())
-        lm_events.append((e0, T.event()))
+
+    def gemv_pass():
+        gemv_pass_on(rot[state["i"] % GEMV_ROTATE])
+        state["i"] += 1
 
     bytes_m1 = sum(nbits_bytes(1, k, n) for _, k, n in QWEN3_PROJ)
     gsteps = max(4 * args.steps, 40)
-    ms_m1 = T.loop(gemv_pass, gsteps, 8)
-    lm_events = lm_events[-gsteps:]
-    ms_lm1 = float(np.mean([a.elapsed_time(b) for a, b in lm_events]))
+    # Host-issued passes (8 ctypes calls each; on a slow host the launch
+    # rate, not the GPU, can bound this figure).
+    ms_m1_eager = T.loop(gemv_pass, gsteps, 8)
+    # The same passes replayed from a HIP graph (one pass per rotated weight
+    # set captured once): the GPU time of the pass without host launch gaps.
+    ms_m1_graph = None
+    graph = None
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for ws in rot:
+                gemv_pass_on(ws)
+        ms_m1_graph = T.loop(graph.replay, max(gsteps // GEMV_ROTATE, 10), 3) / GEMV_ROTATE
+    except Exception as e:  # capture unsupported: report the host-issued figure only
+        print(f"# gemv M=1 graph capture failed: {e}", file=sys.stderr, flush=True)
+    ms_m1 = ms_m1_graph if ms_m1_graph is not None else ms_m1_eager
+    # Per-launch kernel times: each of the 8 launches between its own pair of
+    # events (pre-created), averaged over the rotated sets.
+    nsum = 4 * GEMV_ROTATE
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in QWEN3_PROJ] for _ in range(nsum)]
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        for it in range(nsum):
+            ws = rot[it % GEMV_ROTATE]
+            for j, ((_, k, n), w) in enumerate(zip(QWEN3_PROJ, ws)):
+                evs[it][j][0].record(stream)
+                w.run_dev(acts[(1, k)].data_ptr(), 1, outs[(1, n)].data_ptr())
+                evs[it][j][1].record(stream)
+        torch.cuda.synchronize()
+    per_launch = [float(np.mean([evs[it][j][0].elapsed_time(evs[it][j][1])
+                                 for it in range(nsum)])) for j in range(len(QWEN3_PROJ))]
+    ms_lm1_pass = per_launch[-1]
     lm1_bytes = nbits_bytes(1, k_lm, n_lm)
     # Average launch duration of the lm_head GEMV alone: back-to-back launches
-    # over the rotated weight sets (each launch streams its weights from HBM;
-    # the per-launch event pair inside the pass above adds event overhead).
+    # over the rotated weight sets (each launch streams its weights from HBM).
     state["j"] = 0
 
     def lm1_launch():
@@ -284,12 +311,18 @@ def main():
         state["j"] += 1
         ws[-1].run_dev(acts[(1, k_lm)].data_ptr(), 1, outs[(1, n_lm)].data_ptr())
 
-    ms_lm1_pass = ms_lm1
     ms_lm1 = T.loop(lm1_launch, gsteps, 8)
     lm1_gbs = lm1_bytes / (ms_lm1 / 1e3) / 1e9
     tr1 = traffic.get("lm1", {})
     result["gemv_m1"] = {"value": round(bytes_m1 / (ms_m1 / 1e3) / 1e9, 1), "unit": "GB/s",
-                         "ms_per_pass": round(ms_m1, 4), "bytes_per_pass": bytes_m1,
+                         "ms_per_pass": round(ms_m1, 4),
+                         "timing": "HIP graph replay" if ms_m1_graph is not None
+                                   else "host-issued launches",
+                         "ms_per_pass_host_issued": round(ms_m1_eager, 4),
+                         "kernel_us": {name: round(t * 1e3, 2)
+                                       for (name, _, _), t in zip(QWEN3_PROJ, per_launch)},
+                         "kernel_sum_ms": round(sum(per_launch), 4),
+                         "bytes_per_pass": bytes_m1,
                          "weight_sets_rotated": GEMV_ROTATE,
                          "frac_hbm_peak": round(bytes_m1 / (ms_m1 / 1e3) / 1e9 / HBM_PEAK_GBS,
                                                 4)}
@@ -300,15 +333,17 @@ def main():
         "frac": round(lm1_gbs / HBM_PEAK_GBS, 4), "traffic": tr1.get("bytes"),
         "algorithmic_bytes": lm1_bytes, "ms": round(ms_lm1, 4),
         "ms_in_pass_events": round(ms_lm1_pass, 4)}
-    print(f"# gemv M=1 pass {ms_m1:.4f} ms; lm_head {ms_lm1 * 1e3:.2f} us {lm1_gbs:.0f} GB/s",
+    print(f"# gemv M=1 pass {ms_m1:.4f} ms (host-issued {ms_m1_eager:.4f} ms, kernel sum "
+          f"{sum(per_launch):.4f} ms); lm_head {ms_lm1 * 1e3:.2f} us {lm1_gbs:.0f} GB/s",
           file=sys.stderr, flush=True)
+    graph = None
     for ws in rot[1:]:
         for w in ws:
             w.release()
     del rot
 
     if not args.quick:
-        result["decode_sweep"] = decode_sweep(torch, ops, ctx, T, randn, dev, args)
+        result["decode_sweep"] = decode_sweep(torch, ops, ctx, T, randn, dev, args, stream)
         result["int8_prefill"] = int8_prefill(torch, ops, ctx, T, dev, args)
         result["f32_encoder"] = f32_encoder(torch, ops, ctx, T, randn, dev, args)
         result["conv"] = conv_family(torch, ops, ctx, T, randn, dev, args)
@@ -325,7 +360,7 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def decode_sweep(torch, ops, ctx, T, randn, dev, args):
+def decode_sweep(torch, ops, ctx, T, randn, dev, args, stream):
     """Llama-style 1B decode step at M in {1, 4, 16}: 16 layers x 7 projections
     + lm_head, all distinct weights (0.79 GB packed), algorithmic HBM GB/s."""
     t0 = time.perf_counter()
@@ -344,14 +379,10 @@ def decode_sweep(torch, ops, ctx, T, randn, dev, args):
         a = {k: randn(m, k) for k in {k for _, k, _ in shapes}}
         y = {n: torch.empty((m, n), device=dev, dtype=torch.float32)
              for n in {n for _, _, n in shapes}}
-        head_ev = []
 
         def step():
-            for (_, k, n), w in zip(shapes[:-1], ws[:-1]):
+            for (_, k, n), w in zip(shapes, ws):
                 w.run_dev(a[k].data_ptr(), m, y[n].data_ptr())
-            e0 = T.event()
-            ws[-1].run_dev(a[LLAMA_HEAD[1]].data_ptr(), m, y[LLAMA_HEAD[2]].data_ptr())
-            head_ev.append((e0, T.event()))
 
         nl = len(LLAMA_LAYER)
 
@@ -368,16 +399,35 @@ def decode_sweep(torch, ops, ctx, T, randn, dev, args):
             ws[-1].run_dev(a[LLAMA_HEAD[1]].data_ptr(), m, y[LLAMA_HEAD[2]].data_ptr())
 
         steps = max(args.steps // 2, 5)
-        ms_g = T.loop(step_grouped, steps, 2)
-        ms = T.loop(step, steps, 2)
+        ms_g_eager = T.loop(step_grouped, steps, 2)
+        ms_eager = T.loop(step, steps, 2)
+        # The steps replayed from HIP graphs: GPU time without host launch gaps.
+        ms, ms_g = ms_eager, ms_g_eager
+        timing = "host-issued launches"
+        try:
+            g1, g2 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g1, stream=stream):
+                step()
+            with torch.cuda.graph(g2, stream=stream):
+                step_grouped()
+            ms = T.loop(g1.replay, steps, 2)
+            ms_g = T.loop(g2.replay, steps, 2)
+            timing = "HIP graph replay"
+            del g1, g2
+        except Exception as e:
+            print(f"# decode M={m} graph capture failed: {e}", file=sys.stderr, flush=True)
+        ms_head = T.loop(lambda: ws[-1].run_dev(a[LLAMA_HEAD[1]].data_ptr(), m,
+                                                y[LLAMA_HEAD[2]].data_ptr()), steps, 2)
         nbytes = sum(nbits_bytes(m, k, n, LLAMA_BLOCK) for _, k, n in shapes)
-        ms_head = float(np.mean([e0.elapsed_time(e1) for e0, e1 in head_ev[-steps:]]))
         hb = nbits_bytes(m, LLAMA_HEAD[1], LLAMA_HEAD[2], LLAMA_BLOCK)
         out[f"M{m}"] = {"ms_per_step": round(ms, 4), "bytes_per_step": nbytes,
                         "GB/s": round(nbytes / (ms / 1e3) / 1e9, 1),
                         "frac_hbm_peak": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                         "grouped_ms_per_step": round(ms_g, 4),
                         "grouped_GB/s": round(nbytes / (ms_g / 1e3) / 1e9, 1),
+                        "timing": timing,
+                        "host_issued_ms_per_step": round(ms_eager, 4),
+                        "host_issued_grouped_ms_per_step": round(ms_g_eager, 4),
                         "lm_head_us": round(ms_head * 1e3, 2),
                         "lm_head_GB/s": round(hb / (ms_head / 1e3) / 1e9, 1)}
         print(f"# decode M={m}: {out[f'M{m}']}", file=sys.stderr, flush=True)

@@ -55,6 +55,14 @@ typedef struct mg_weight mg_weight;
  * of the ORT status message (lib/src/ort/ort_backend.dart:774-782). */
 const char *mg_last_error(void);
 
+/* When the last failing call on this thread failed on the byte budget of
+ * mg_ctx_set_control, returns 1 and stores the bytes the op needed and the
+ * limit: the fields of OnnxMemoryLimitException
+ * (lib/src/execution_control.dart:12-19).  Returns 0 otherwise (an
+ * MG_OUT_OF_MEMORY from the device allocator maps to StateError).  Either
+ * pointer may be NULL. */
+int32_t mg_last_error_budget(int64_t *required_bytes, int64_t *limit_bytes);
+
 /* Library version as "major.minor.patch". */
 const char *mg_version(void);
 
@@ -263,6 +271,24 @@ mg_status mg_matmul_f32_dev(mg_ctx *ctx, const float *a_dev,
                             const int64_t *a_shape, int32_t a_rank,
                             const float *b_dev, const int64_t *b_shape,
                             int32_t b_rank, float *y_dev);
+/* Output shape of MatMul over these operand shapes (the broadcast of
+ * lib/src/onnx_ops.dart:1717-1722 plus [M, N]); y_shape holds up to 16
+ * entries.  Lets the caller allocate y before mg_matmul_f32(_dev).  No
+ * device is touched. */
+mg_status mg_matmul_f32_output_shape(const int64_t *a_shape, int32_t a_rank,
+                                     const int64_t *b_shape, int32_t b_rank,
+                                     int64_t *y_shape, int32_t *y_rank);
+/* Element offsets into A and B of kernel batches [first, first + count) as
+ * the kernels compute them (the per-batch broadcast offsets of
+ * lib/src/onnx_ops.dart:1742-1764); *batches (if not NULL) receives the
+ * number of kernel batches.  Host-only; for checking the batch planner
+ * without a device.  With the shared-weight collapse
+ * (lib/src/onnx_ops.dart:1728-1735) there is one batch at offsets 0. */
+mg_status mg_matmul_f32_batch_offsets(const int64_t *a_shape, int32_t a_rank,
+                                      const int64_t *b_shape, int32_t b_rank,
+                                      int64_t first, int64_t count,
+                                      int64_t *a_off, int64_t *b_off,
+                                      int64_t *batches);
 
 /* Gemm: y = alpha * op(A) . op(B) + beta * C (lib/src/onnx_ops.dart:2152-2172).
  * a, b rank 2; c NULL or rank <= 2 broadcasting to [M, N]. */

@@ -24,6 +24,7 @@ _PP = C.POINTER(C.c_void_p)
 # name -> argtypes (all return mg_status = int32 unless listed in _RESTYPE)
 SIGNATURES = {
     "mg_last_error": [],
+    "mg_last_error_budget": [_P, _P],
     "mg_version": [],
     "mg_ctx_create": [_I32, _PP],
     "mg_ctx_destroy": [_P],
@@ -86,6 +87,8 @@ SIGNATURES = {
                                      _F, _I32, _P, _P, _P],
     "mg_matmul_f32": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_matmul_f32_dev": [_P, _P, _P, _I32, _P, _P, _I32, _P],
+    "mg_matmul_f32_output_shape": [_P, _I32, _P, _I32, _P, _P],
+    "mg_matmul_f32_batch_offsets": [_P, _I32, _P, _I32, _I64, _I64, _P, _P, _P],
     "mg_gemm_f32": [_P, _P, _P, _P, _P, _I32, _I32, _F, _F, _P, _P, _I32, _P],
     "mg_weight_f32_create": [_P, _P, _I64, _I64, _I32, _PP],
     "mg_gemm_f32_w": [_P, _P, _I64, _I64, _P, _F, _F, _P, _P, _I32, _P],
@@ -115,4 +118,9 @@ lib = _load()
 def check(status: int, what: str = "") -> None:
     if status != 0:
         msg = lib.mg_last_error().decode(errors="replace")
-        raise_for_status(status, msg or what)
+        budget = None
+        if status == 3:
+            req, lim = C.c_int64(0), C.c_int64(0)
+            if lib.mg_last_error_budget(C.byref(req), C.byref(lim)):
+                budget = (req.value, lim.value)
+        raise_for_status(status, msg or what, budget)

@@ -26,6 +26,9 @@ size_t mg_int8_batched_ws_bytes(int64_t a_batch, int64_t b_batch, int64_t M,
 
 namespace {
 thread_local std::string g_last_error;
+// Set when the last failure was the byte budget (mg_last_error_budget).
+thread_local bool g_budget_failed = false;
+thread_local int64_t g_budget_required = 0, g_budget_limit = 0;
 
 int64_t prod(const int64_t *s, int32_t from, int32_t to) {
   int64_t p = 1;
@@ -53,6 +56,7 @@ struct Staging {
 
 mg_status mg_fail(mg_status st, const std::string &msg) {
   g_last_error = msg;
+  g_budget_failed = false;
   return st;
 }
 
@@ -71,10 +75,15 @@ mg_status mg_use_device(mg_ctx *ctx) {
 mg_status mg_check_control(mg_ctx *ctx, int64_t additional_bytes) {
   if (ctx->cancel_flag && *ctx->cancel_flag)
     return mg_fail(MG_CANCELLED, "operation cancelled");
-  if (ctx->max_bytes >= 0 && additional_bytes > ctx->max_bytes)
-    return mg_fail(MG_OUT_OF_MEMORY,
-                   "device memory limit exceeded: " + std::to_string(additional_bytes) +
-                       " bytes required, limit " + std::to_string(ctx->max_bytes));
+  if (ctx->max_bytes >= 0 && additional_bytes > ctx->max_bytes) {
+    mg_fail(MG_OUT_OF_MEMORY, "device memory limit exceeded: " +
+                                  std::to_string(additional_bytes) + " bytes required, limit " +
+                                  std::to_string(ctx->max_bytes));
+    g_budget_failed = true;
+    g_budget_required = additional_bytes;
+    g_budget_limit = ctx->max_bytes;
+    return MG_OUT_OF_MEMORY;
+  }
   return MG_OK;
 }
 
@@ -92,9 +101,41 @@ mg_status mg_ws_reserve(mg_ctx *ctx, size_t bytes) {
   return MG_OK;
 }
 
+mg_status mg_h2d_table(mg_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes) {
+  if (bytes == 0) return MG_OK;
+  if (bytes > MG_PIN_SLOT_BYTES) {
+    MG_HIP(hipMemcpyAsync(dst_dev, src_host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    MG_HIP(hipStreamSynchronize(ctx->stream));
+    return MG_OK;
+  }
+  if (!ctx->pin) {
+    MG_HIP(hipHostMalloc(&ctx->pin, (size_t)MG_PIN_SLOTS * MG_PIN_SLOT_BYTES,
+                         hipHostMallocDefault));
+    for (int i = 0; i < MG_PIN_SLOTS; i++)
+      MG_HIP(hipEventCreateWithFlags(&ctx->pin_ev[i], hipEventDisableTiming));
+  }
+  const int slot = ctx->pin_next;
+  ctx->pin_next = (slot + 1) % MG_PIN_SLOTS;
+  // The slot's previous copy must have run before its bytes are replaced
+  // (an event never recorded counts as complete).
+  MG_HIP(hipEventSynchronize(ctx->pin_ev[slot]));
+  char *stage = static_cast<char *>(ctx->pin) + (size_t)slot * MG_PIN_SLOT_BYTES;
+  std::memcpy(stage, src_host, bytes);
+  MG_HIP(hipMemcpyAsync(dst_dev, stage, bytes, hipMemcpyHostToDevice, ctx->stream));
+  MG_HIP(hipEventRecord(ctx->pin_ev[slot], ctx->stream));
+  return MG_OK;
+}
+
 extern "C" {
 
 const char *mg_last_error(void) { return g_last_error.c_str(); }
+
+int32_t mg_last_error_budget(int64_t *required_bytes, int64_t *limit_bytes) {
+  if (!g_budget_failed || g_last_error.empty()) return 0;
+  if (required_bytes) *required_bytes = g_budget_required;
+  if (limit_bytes) *limit_bytes = g_budget_limit;
+  return 1;
+}
 const char *mg_version(void) { return "0.1.0"; }
 
 // ------------------------------------------------------------------ context
@@ -129,6 +170,9 @@ mg_status mg_ctx_destroy(mg_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->ws) (void)hipFree(ctx->ws);
+  for (int i = 0; i < MG_PIN_SLOTS; i++)
+    if (ctx->pin_ev[i]) (void)hipEventDestroy(ctx->pin_ev[i]);
+  if (ctx->pin) (void)hipHostFree(ctx->pin);
   if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return MG_OK;
@@ -740,9 +784,18 @@ namespace {
 
 struct F32Batch {
   int64_t M, K, N, batch;
-  std::vector<int64_t> out_shape, a_off, b_off;
+  std::vector<int64_t> out_shape;
+  // Inner merged batch dims run in one launch (bc); merged dims beyond
+  // MG_F32_MAX_BATCH_DIMS become host loops over launches (outer_*,
+  // innermost first), each launch offsetting A, B and Y by its coordinates.
+  mg_f32_bcast bc;
+  int64_t inner_batch = 1;
+  std::vector<int64_t> outer_dim, outer_a, outer_b;
 };
 
+// numpy broadcasting of the batch dims (lib/src/onnx_ops.dart:1717-1722,
+// per-batch offsets :1742-1764) as strides: output dim d steps A by
+// a_bs[d] elements (0 where A's dim is 1) and B by b_bs[d].
 mg_status plan_matmul_f32(const int64_t *a_shape, int32_t a_rank, const int64_t *b_shape,
                           int32_t b_rank, F32Batch *p) {
   if (!shape_ok(a_shape, a_rank) || !shape_ok(b_shape, b_rank) || a_rank < 2 || b_rank < 2)
@@ -767,35 +820,66 @@ mg_status plan_matmul_f32(const int64_t *a_shape, int32_t a_rank, const int64_t 
   p->out_shape = ob;
   p->out_shape.push_back(p->M);
   p->out_shape.push_back(p->N);
-  const int64_t bbatch = prod(b_shape, 0, br);
-  p->a_off.clear();
-  p->b_off.clear();
-  if (p->batch > 1 && bbatch == 1) {
+  p->bc = mg_f32_bcast{};
+  p->inner_batch = p->batch;
+  p->outer_dim.clear();
+  p->outer_a.clear();
+  p->outer_b.clear();
+  if (p->batch > 1 && prod(b_shape, 0, br) == 1) {
     // Shared-weight collapse (lib/src/onnx_ops.dart:1728-1735).
     p->M *= p->batch;
-    p->batch = 1;
+    p->batch = p->inner_batch = 1;
     return MG_OK;
   }
-  std::vector<int64_t> coords(r, 0);
-  for (int64_t bi = 0; bi < p->batch; bi++) {
-    int64_t rem = bi;
-    for (int32_t d = r - 1; d >= 0; d--) {
-      coords[d] = rem % ob[d];
-      rem /= ob[d];
+  if (p->batch <= 1) return MG_OK;
+  // Strides from the innermost batch dim out; size-1 output dims dropped,
+  // neighbours that step both operands contiguously merged.
+  std::vector<int64_t> dim, as, bs;
+  int64_t sa = p->M * p->K, sb = p->K * p->N;
+  for (int32_t d = r - 1; d >= 0; d--) {
+    const int64_t x = d < r - ar ? 1 : a_shape[d - (r - ar)];
+    const int64_t y = d < r - br ? 1 : b_shape[d - (r - br)];
+    const int64_t da = x == 1 ? 0 : sa, db = y == 1 ? 0 : sb;
+    sa *= x;
+    sb *= y;
+    if (ob[d] == 1) continue;
+    if (!dim.empty() && da == as.back() * dim.back() && db == bs.back() * dim.back()) {
+      dim.back() *= ob[d];
+      continue;
     }
-    int64_t ai = 0, bj = 0;
-    for (int32_t d = 0; d < ar; d++) {
-      const int64_t s = a_shape[d];
-      ai = ai * s + (s == 1 ? 0 : coords[d + (r - ar)]);
-    }
-    for (int32_t d = 0; d < br; d++) {
-      const int64_t s = b_shape[d];
-      bj = bj * s + (s == 1 ? 0 : coords[d + (r - br)]);
-    }
-    p->a_off.push_back(ai * p->M * p->K);
-    p->b_off.push_back(bj * p->K * p->N);
+    dim.push_back(ob[d]);
+    as.push_back(da);
+    bs.push_back(db);
+  }
+  const size_t nin = std::min<size_t>(dim.size(), MG_F32_MAX_BATCH_DIMS);
+  p->bc.nbd = (int32_t)nin;
+  p->inner_batch = 1;
+  for (size_t d = 0; d < nin; d++) {
+    p->bc.dim[d] = (uint32_t)dim[d];
+    p->bc.a_bs[d] = as[d];
+    p->bc.b_bs[d] = bs[d];
+    p->inner_batch *= dim[d];
+  }
+  for (size_t d = nin; d < dim.size(); d++) {
+    p->outer_dim.push_back(dim[d]);
+    p->outer_a.push_back(as[d]);
+    p->outer_b.push_back(bs[d]);
   }
   return MG_OK;
+}
+
+// Launch-level offsets of outer launch `o` (coordinates over outer_dim,
+// innermost first).
+void outer_offsets(const F32Batch &p, int64_t o, int64_t *ao, int64_t *bo) {
+  int64_t a = 0, b = 0;
+  for (size_t d = 0; d < p.outer_dim.size(); d++) {
+    const int64_t c = o % p.outer_dim[d];
+    o /= p.outer_dim[d];
+    a += c * p.outer_a[d];
+    b += c * p.outer_b[d];
+  }
+  *ao = a;
+  *bo = b;
 }
 
 mg_status c_strides(const int64_t *c_shape, int32_t c_rank, int64_t M, int64_t N, int64_t *rs,
@@ -816,30 +900,67 @@ mg_status c_strides(const int64_t *c_shape, int32_t c_rank, int64_t M, int64_t N
   return MG_OK;
 }
 
-// Runs p on device buffers; offsets go through the workspace at ws_off.
+// Runs p on device buffers: one launch per outer coordinate (a single one
+// unless more than MG_F32_MAX_BATCH_DIMS merged batch dims remain); the
+// batch offsets are kernel arguments, so nothing is staged.
 mg_status run_f32_batched(mg_ctx *ctx, const F32Batch &p, const float *a, const float *b,
-                          float *y, char *ws) {
+                          float *y) {
   mg_f32_problem q{};
   q.M = p.M;
   q.N = p.N;
   q.K = p.K;
-  q.batch = p.batch;
+  q.batch = p.inner_batch;
+  q.bc = p.bc;
   q.lda = p.K;
   q.ldb = p.N;
   q.alpha = 1.f;
   q.beta = 1.f;
-  if (!p.a_off.empty()) {
-    int64_t *off = reinterpret_cast<int64_t *>(ws);
-    std::vector<int64_t> both(p.a_off);
-    both.insert(both.end(), p.b_off.begin(), p.b_off.end());
-    MG_HIP(hipMemcpyAsync(off, both.data(), both.size() * 8, hipMemcpyHostToDevice, ctx->stream));
-    q.a_off = off;
-    q.b_off = off + p.batch;
+  const int64_t outer = p.batch / std::max<int64_t>(p.inner_batch, 1);
+  for (int64_t o = 0; o < outer; o++) {
+    int64_t ao = 0, bo = 0;
+    outer_offsets(p, o, &ao, &bo);
+    MG_TRY(mg_f32_run(ctx, q, a + ao, b + bo, y + o * p.inner_batch * p.M * p.N));
   }
-  return mg_f32_run(ctx, q, a, b, y);
+  return MG_OK;
 }
 
 }  // namespace
+
+mg_status mg_matmul_f32_output_shape(const int64_t *a_shape, int32_t a_rank,
+                                     const int64_t *b_shape, int32_t b_rank, int64_t *y_shape,
+                                     int32_t *y_rank) {
+  g_last_error.clear();
+  if (!y_shape || !y_rank)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_f32_output_shape: null output");
+  F32Batch p;
+  MG_TRY(plan_matmul_f32(a_shape, a_rank, b_shape, b_rank, &p));
+  *y_rank = (int32_t)p.out_shape.size();
+  for (size_t i = 0; i < p.out_shape.size(); i++) y_shape[i] = p.out_shape[i];
+  return MG_OK;
+}
+
+mg_status mg_matmul_f32_batch_offsets(const int64_t *a_shape, int32_t a_rank,
+                                      const int64_t *b_shape, int32_t b_rank, int64_t first,
+                                      int64_t count, int64_t *a_off, int64_t *b_off,
+                                      int64_t *batches) {
+  g_last_error.clear();
+  F32Batch p;
+  MG_TRY(plan_matmul_f32(a_shape, a_rank, b_shape, b_rank, &p));
+  if (batches) *batches = p.batch;
+  if (first < 0 || count < 0 || first + count > p.batch)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_f32_batch_offsets: batch range out of bounds");
+  if (count && (!a_off || !b_off))
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_f32_batch_offsets: null output");
+  const int64_t ib = std::max<int64_t>(p.inner_batch, 1);
+  for (int64_t z = first; z < first + count; z++) {
+    int64_t ao = 0, bo = 0, ai = 0, bi = 0;
+    outer_offsets(p, z / ib, &ao, &bo);
+    mg_f32_batch_offsets(p.bc, (uint32_t)(z % ib), &ai, &bi);
+    a_off[z - first] = ao + ai;
+    b_off[z - first] = bo + bi;
+  }
+  return MG_OK;
+}
 
 mg_status mg_matmul_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape, int32_t a_rank,
                         const float *b, const int64_t *b_shape, int32_t b_rank, float *y) {
@@ -854,15 +975,13 @@ mg_status mg_matmul_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape, int
   MG_TRY(mg_use_device(ctx));
   Staging s;
   const size_t oa = s.take((size_t)na * 4), ob = s.take((size_t)nb * 4), oy = s.take((size_t)ny * 4);
-  const size_t oo = s.take((size_t)p.batch * 16 + 16);
   MG_TRY(mg_check_control(ctx, (int64_t)s.off));
   MG_TRY(mg_ws_reserve(ctx, s.off));
   char *base = static_cast<char *>(ctx->ws);
   if (na) MG_HIP(hipMemcpyAsync(base + oa, a, (size_t)na * 4, hipMemcpyHostToDevice, ctx->stream));
   if (nb) MG_HIP(hipMemcpyAsync(base + ob, b, (size_t)nb * 4, hipMemcpyHostToDevice, ctx->stream));
   MG_TRY(run_f32_batched(ctx, p, reinterpret_cast<float *>(base + oa),
-                         reinterpret_cast<float *>(base + ob), reinterpret_cast<float *>(base + oy),
-                         base + oo));
+                         reinterpret_cast<float *>(base + ob), reinterpret_cast<float *>(base + oy)));
   MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)ny * 4, hipMemcpyDeviceToHost, ctx->stream));
   MG_HIP(hipStreamSynchronize(ctx->stream));
   return MG_OK;
@@ -876,11 +995,12 @@ mg_status mg_matmul_f32_dev(mg_ctx *ctx, const float *a_dev, const int64_t *a_sh
   F32Batch p;
   MG_TRY(plan_matmul_f32(a_shape, a_rank, b_shape, b_rank, &p));
   if (p.batch * p.M * p.N == 0) return MG_OK;
+  const int64_t na = prod(a_shape, 0, a_rank), nb = prod(b_shape, 0, b_rank);
+  if ((!a_dev && na) || (!b_dev && nb) || !y_dev)
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMul: null buffer");
   MG_TRY(mg_use_device(ctx));
-  const size_t ws = (size_t)p.batch * 16 + 16;
-  MG_TRY(mg_check_control(ctx, (int64_t)ws));
-  MG_TRY(mg_ws_reserve(ctx, ws));
-  return run_f32_batched(ctx, p, a_dev, b_dev, y_dev, static_cast<char *>(ctx->ws));
+  MG_TRY(mg_check_control(ctx, 0));
+  return run_f32_batched(ctx, p, a_dev, b_dev, y_dev);
 }
 
 mg_status mg_gemm_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape, const float *b,
@@ -1474,22 +1594,19 @@ mg_status conv_int_params(const char *op, const mg_conv_problem &p, const int32_
 }
 
 // Runs p with operands already on the device; per-channel tables go into
-// the workspace at table_off (copied and waited for before the launch, so
-// the host tables may go away on return).
+// the workspace at wz_off / mult_off through the pinned staging, so the host
+// tables may go away on return without a wait.
 mg_status conv_launch(mg_ctx *ctx, mg_conv_problem p, const std::vector<float> &wz,
                       const std::vector<double> &mult, size_t wz_off, size_t mult_off) {
   char *base = static_cast<char *>(ctx->ws);
-  hipStream_t st = ctx->stream;
   if (!wz.empty()) {
-    MG_HIP(hipMemcpyAsync(base + wz_off, wz.data(), wz.size() * 4, hipMemcpyHostToDevice, st));
+    MG_TRY(mg_h2d_table(ctx, base + wz_off, wz.data(), wz.size() * 4));
     p.w_zp = reinterpret_cast<const float *>(base + wz_off);
   }
   if (!mult.empty()) {
-    MG_HIP(hipMemcpyAsync(base + mult_off, mult.data(), mult.size() * 8, hipMemcpyHostToDevice,
-                          st));
+    MG_TRY(mg_h2d_table(ctx, base + mult_off, mult.data(), mult.size() * 8));
     p.mult = reinterpret_cast<const double *>(base + mult_off);
   }
-  if (!wz.empty() || !mult.empty()) MG_HIP(hipStreamSynchronize(st));
   return mg_conv_run(ctx, p);
 }
 

@@ -17,9 +17,19 @@
 // Operands may be stored k-contiguous ("RK": A [M][K], B^T [N][K]) or
 // row-contiguous ("KR": A^T [K][M], B [K][N]); the stage loader reads 32
 // bytes per thread either way and transposes KR tiles on their way into LDS.
-// Batches run on grid.z with per-batch element offsets computed on the host
-// (numpy broadcasting, lib/src/onnx_ops.dart:1742-1764).
+// Batches run on grid.z; each workgroup decodes its batch's operand offsets
+// from the broadcast strides it receives as an argument (numpy broadcasting,
+// lib/src/onnx_ops.dart:1742-1764).
+//
+// Tile order.  Workgroups are dealt to the chip's 8 XCDs round-robin
+// (workgroup L runs on XCD L % 8) and each XCD has its own L2.  When the
+// tile grid is large enough, it is cut into pr row bands x pc column bands
+// (pr * pc = 8) and XCD j takes the tiles of rectangle j, so a row tile of A
+// is fetched by pc XCDs and a column tile of B by pr, instead of both by
+// all 8.  The host picks the cut that fetches the fewest bytes.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "mg_internal.h"
 
@@ -82,8 +92,8 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
     const float *__restrict__ A, const float *__restrict__ B,
     float *__restrict__ Y, int64_t M, int64_t N, int64_t K, int64_t lda,
     int64_t ldb, int vec_a, int vec_b,
-    const int64_t *__restrict__ a_off, const int64_t *__restrict__ b_off, float alpha,
-    float beta, const float *__restrict__ C, int64_t c_rs, int64_t c_cs) {
+    const mg_f32_bcast bc, uint32_t z0, int nx, int pr, int pc, float alpha, float beta,
+    const float *__restrict__ C, int64_t c_rs, int64_t c_cs) {
   constexpr int T = 64 * WT, LDX = KS + 4, NS = KS / 2;
   __shared__ float As[2][T * LDX];
   __shared__ float Bs[2][T * LDX];
@@ -91,10 +101,30 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int l32 = lane & 31, h = lane >> 5;
-  const int64_t bz = blockIdx.z;
-  const float *Ab = A + (a_off ? a_off[bz] : 0);
-  const float *Bb = B + (b_off ? b_off[bz] : 0);
-  const int64_t r0 = (int64_t)blockIdx.y * T, c0 = (int64_t)blockIdx.x * T;
+  // Tile of this workgroup (see the tile order above).  pr = 0: row-major.
+  int tr, tc;
+  {
+    const int L = (int)blockIdx.x;
+    if (pr == 0) {
+      tr = L / nx;
+      tc = L % nx;
+    } else {
+      const int ny = (int)((M + T - 1) / T);
+      const int x = L & 7, i = L >> 3, br = x / pc, bcol = x % pc;
+      const int rlo = br * ny / pr, rhi = (br + 1) * ny / pr;
+      const int clo = bcol * nx / pc, chi = (bcol + 1) * nx / pc;
+      const int w = chi - clo;
+      if (i >= (rhi - rlo) * w) return;  // uniform: the whole workgroup leaves
+      tr = rlo + i / w;
+      tc = clo + i % w;
+    }
+  }
+  const uint32_t bz = z0 + blockIdx.z;
+  int64_t a_off, b_off;
+  mg_f32_batch_offsets(bc, bz, &a_off, &b_off);
+  const float *Ab = A + a_off;
+  const float *Bb = B + b_off;
+  const int64_t r0 = (int64_t)tr * T, c0 = (int64_t)tc * T;
   const bool a_in = vec_a && r0 + T <= M, b_in = vec_b && c0 + T <= N;
 
   float16v acc[WT][WT];
@@ -155,7 +185,7 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
 
   // Lane l holds column l % 32 and rows 8 (v / 4) + 4 (l / 32) + v % 4 of
   // each 32 x 32 tile; 32 lanes write 128 contiguous bytes per store.
-  float *Yb = Y + bz * M * N;
+  float *Yb = Y + (int64_t)bz * M * N;
 #pragma unroll
   for (int i = 0; i < WT; i++)
 #pragma unroll
@@ -180,10 +210,11 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
 
 template <int WT, int KS>
 void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float *a,
-                const float *b, float *y, int vec_a, int vec_b) {
-#define MG_F32_ARGS                                                                           \
-  a, b, y, p.M, p.N, p.K, p.lda, p.ldb, vec_a, vec_b, p.a_off, p.b_off, p.alpha, p.beta, p.c, \
-      p.c_rs, p.c_cs
+                const float *b, float *y, int vec_a, int vec_b, uint32_t z0, int nx, int pr,
+                int pc) {
+#define MG_F32_ARGS                                                                         \
+  a, b, y, p.M, p.N, p.K, p.lda, p.ldb, vec_a, vec_b, p.bc, z0, nx, pr, pc, p.alpha, p.beta, \
+      p.c, p.c_rs, p.c_cs
   const bool akr = p.trans_a != 0, bkr = p.trans_b == 0;
   if (!akr && !bkr)
     hipLaunchKernelGGL((k_f32_gemm<WT, KS, false, false>), grid, dim3(256), 0, st, MG_F32_ARGS);
@@ -198,13 +229,38 @@ void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float 
 
 }  // namespace
 
+// The XCD cut of an ny x nx tile grid: pr row bands x pc column bands with
+// pr * pc = 8, at least one tile per band, minimising the tiles fetched
+// (ny * pc row tiles of A + nx * pr column tiles of B, equal sizes), then the
+// largest rectangle.  Returns false (row-major order) for grids of fewer than
+// 64 tiles or that no cut fits.
+static bool mg_f32_xcd_cut(int64_t ny, int64_t nx, int *pr, int *pc, int64_t *per) {
+  if (ny * nx < 64) return false;
+  int64_t best = -1, best_per = 0;
+  for (int r = 1; r <= 8; r *= 2) {
+    const int c = 8 / r;
+    if (r > ny || c > nx) continue;
+    const int64_t cost = ny * c + nx * r;
+    const int64_t rect = ((ny + r - 1) / r) * ((nx + c - 1) / c);
+    if (best < 0 || cost < best || (cost == best && rect < best_per)) {
+      best = cost;
+      best_per = rect;
+      *pr = r;
+      *pc = c;
+    }
+  }
+  if (best < 0) return false;
+  *per = best_per;
+  return true;
+}
+
 mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
                      const float *b_dev, float *y_dev) {
   if (p.M == 0 || p.N == 0 || p.batch == 0) return MG_OK;
   // 16-byte operand loads need 16-byte aligned rows: the base pointers and,
-  // for batches, every per-batch offset (offsets are multiples of M*K resp.
-  // K*N elements, so checking the leading dimension and one batch stride
-  // suffices).
+  // for batches, every batch offset (the broadcast strides are multiples of
+  // M*K resp. K*N elements, so checking the leading dimension and one batch
+  // stride suffices).
   auto aligned = [](const float *ptr, int64_t ld, int64_t batch_stride) {
     return reinterpret_cast<uintptr_t>(ptr) % 16 == 0 && ld % 4 == 0 && batch_stride % 4 == 0;
   };
@@ -215,17 +271,28 @@ mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
   const int64_t big = ((p.N + 127) / 128) * ((p.M + 127) / 128) * p.batch;
   const bool use_big = big >= 2 * (int64_t)ctx->num_cus;
   const int T = use_big ? 128 : 64;
-  const dim3 grid((unsigned)((p.N + T - 1) / T), (unsigned)((p.M + T - 1) / T),
-                  (unsigned)p.batch);
+  const int64_t nx = (p.N + T - 1) / T, ny = (p.M + T - 1) / T;
+  int pr = 0, pc = 0;
+  int64_t per = 0;
+  const bool cut = mg_f32_xcd_cut(ny, nx, &pr, &pc, &per);
+  if (!cut) pr = pc = 0;
+  const unsigned gx = (unsigned)(cut ? 8 * per : nx * ny);
 #ifndef MG_F32_KS_BIG
 #define MG_F32_KS_BIG 16
 #endif
 #ifndef MG_F32_KS_SMALL
 #define MG_F32_KS_SMALL 32
 #endif
-  if (use_big)
-    launch_f32<2, MG_F32_KS_BIG>(p, grid, ctx->stream, a_dev, b_dev, y_dev, vec_a, vec_b);
-  else
-    launch_f32<1, MG_F32_KS_SMALL>(p, grid, ctx->stream, a_dev, b_dev, y_dev, vec_a, vec_b);
-  return mg_launch_check("k_f32_gemm");
+  // Batches in chunks of at most 65535 per launch (grid z).
+  for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
+    const dim3 grid(gx, 1, (unsigned)std::min<int64_t>(65535, p.batch - z0));
+    if (use_big)
+      launch_f32<2, MG_F32_KS_BIG>(p, grid, ctx->stream, a_dev, b_dev, y_dev, vec_a, vec_b,
+                                   (uint32_t)z0, (int)nx, pr, pc);
+    else
+      launch_f32<1, MG_F32_KS_SMALL>(p, grid, ctx->stream, a_dev, b_dev, y_dev, vec_a, vec_b,
+                                     (uint32_t)z0, (int)nx, pr, pc);
+    MG_TRY(mg_launch_check("k_f32_gemm"));
+  }
+  return MG_OK;
 }

@@ -519,7 +519,7 @@ mg_status mg_int8_prepack_dev(mg_ctx *ctx, mg_weight *w, const void *b_dev,
   } else if (b_zp && b_zp_len > 1) {
     // Per-column zero points travel through the cb array: written there
     // first, then read back by the colsum kernel (one thread per column).
-    MG_HIP(hipMemcpyAsync(w->i8.cb, b_zp, (size_t)b_zp_len * 4, hipMemcpyHostToDevice, st));
+    MG_TRY(mg_h2d_table(ctx, w->i8.cb, b_zp, (size_t)b_zp_len * 4));
     zb_dev = w->i8.cb;
     zb_len = (int)b_zp_len;
   }
@@ -593,7 +593,7 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
     za_scalar = a_zp[0];
   } else if (a_zp && a_zp_len > 1) {
     int32_t *zd = reinterpret_cast<int32_t *>(base + p.off_za);
-    MG_HIP(hipMemcpyAsync(zd, a_zp, (size_t)a_zp_len * 4, hipMemcpyHostToDevice, st));
+    MG_TRY(mg_h2d_table(ctx, zd, a_zp, (size_t)a_zp_len * 4));
     za = zd;
     za_len = (int)a_zp_len;
   }
@@ -703,7 +703,7 @@ mg_status mg_int8_run_batched(mg_ctx *ctx, const void *a_dev, int32_t a_signed,
   if (b_zp && b_zp_len == 1) {
     zb_scalar = b_zp[0];
   } else if (b_zp && b_zp_len > 1) {
-    MG_HIP(hipMemcpyAsync(zb_dev, b_zp, (size_t)b_zp_len * 4, hipMemcpyHostToDevice, st));
+    MG_TRY(mg_h2d_table(ctx, zb_dev, b_zp, (size_t)b_zp_len * 4));
     zb_len = (int)b_zp_len;
   }
   const int64_t slots = n32 * kqp * 64;

@@ -31,6 +31,13 @@ mg_status mg_fail(mg_status st, const std::string &msg);
 
 // ------------------------------------------------------------ structures
 
+// Pinned staging of small host tables (zero points, requant multipliers)
+// that _dev calls copy on the stream: MG_PIN_SLOTS slots of MG_PIN_SLOT_BYTES
+// used round-robin, each reused only after the event recorded behind its
+// last copy has completed.
+constexpr int MG_PIN_SLOTS = 16;
+constexpr size_t MG_PIN_SLOT_BYTES = 256 << 10;
+
 struct mg_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -43,6 +50,9 @@ struct mg_ctx {
   size_t ws_bytes = 0;
   // Compute units of the device (grid sizing).
   int num_cus = 256;
+  void *pin = nullptr;  // MG_PIN_SLOTS * MG_PIN_SLOT_BYTES pinned host bytes
+  hipEvent_t pin_ev[MG_PIN_SLOTS] = {};
+  int pin_next = 0;
 };
 
 enum mg_weight_kind { MG_W_NBITS = 1, MG_W_INT8 = 2, MG_W_F32 = 3 };
@@ -96,6 +106,11 @@ mg_status mg_check_control(mg_ctx *ctx, int64_t additional_bytes);
 mg_status mg_ws_reserve(mg_ctx *ctx, size_t bytes);
 // Sets the context's device current on this thread.
 mg_status mg_use_device(mg_ctx *ctx);
+// Copies `bytes` of host memory to device memory on the context's stream.
+// The bytes are first copied into the context's pinned staging, so the
+// caller's array may go away as soon as this returns; tables larger than a
+// staging slot are copied and waited for.
+mg_status mg_h2d_table(mg_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes);
 mg_status mg_launch_check(const char *what);
 
 static inline size_t mg_align(size_t x, size_t a = 256) {
@@ -168,12 +183,42 @@ mg_status mg_int8_prepack_dev(mg_ctx *ctx, mg_weight *w, const void *b_dev,
 
 // ------------------------------------------------------------- fp32 entry
 
-// y[batch][M][N] = alpha * A . B + beta * C with per-batch element offsets.
+// Broadcast batch dims of a batched product, innermost first, after size-1
+// dims are dropped and dims that step both operands contiguously are merged.
+// Output batch z has coordinates c[0] = z % dim[0], c[1] = (z / dim[0]) %
+// dim[1], ...; operand element offsets are sum_d c[d] * a_bs[d] (b_bs[d]), a
+// stride of 0 broadcasting that operand over the dim.
+constexpr int MG_F32_MAX_BATCH_DIMS = 4;
+struct mg_f32_bcast {
+  int32_t nbd = 0;
+  uint32_t dim[MG_F32_MAX_BATCH_DIMS] = {1, 1, 1, 1};
+  int64_t a_bs[MG_F32_MAX_BATCH_DIMS] = {0, 0, 0, 0};
+  int64_t b_bs[MG_F32_MAX_BATCH_DIMS] = {0, 0, 0, 0};
+};
+
+// Operand offsets of output batch z (host and device; fixed trip count so a
+// kernel keeps the descriptor in scalar registers).
+__host__ __device__ inline void mg_f32_batch_offsets(const mg_f32_bcast bc, uint32_t z,
+                                                     int64_t *ao, int64_t *bo) {
+  int64_t a = 0, b = 0;
+#pragma unroll
+  for (int d = 0; d < MG_F32_MAX_BATCH_DIMS; d++) {
+    if (d < bc.nbd) {
+      const uint32_t c = z % bc.dim[d];
+      z /= bc.dim[d];
+      a += (int64_t)c * bc.a_bs[d];
+      b += (int64_t)c * bc.b_bs[d];
+    }
+  }
+  *ao = a;
+  *bo = b;
+}
+
+// y[batch][M][N] = alpha * A . B + beta * C with broadcast batch offsets.
 struct mg_f32_problem {
   int64_t M, N, K;
   int64_t batch;
-  const int64_t *a_off;  // device [batch] element offsets (null => 0)
-  const int64_t *b_off;  // device [batch]
+  mg_f32_bcast bc;       // batch dims (nbd = 0: one batch, or batches laid out contiguously)
   int64_t lda, ldb;      // row strides of the (non-transposed views)
   int32_t trans_a, trans_b;
   float alpha, beta;

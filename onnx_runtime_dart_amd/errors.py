@@ -16,7 +16,14 @@ class UnsupportedError(NotImplementedError):
 
 
 class OnnxMemoryLimitException(MemoryError):
-    """MG_OUT_OF_MEMORY"""
+    """MG_OUT_OF_MEMORY from the byte budget, with the reference exception's
+    fields (lib/src/execution_control.dart:12-19).  A device allocator
+    failure is a StateError instead."""
+
+    def __init__(self, message: str = "", required_bytes: int = 0, limit_bytes: int = 0):
+        super().__init__(message)
+        self.required_bytes = required_bytes
+        self.limit_bytes = limit_bytes
 
 
 class OnnxCancelledException(Exception):
@@ -36,5 +43,11 @@ _BY_STATUS = {
 }
 
 
-def raise_for_status(status: int, message: str) -> None:
+def raise_for_status(status: int, message: str, budget=None) -> None:
+    """budget: (required, limit) when an MG_OUT_OF_MEMORY came from the byte
+    budget; None for a device allocator failure (-> StateError)."""
+    if status == 3 and budget is None:
+        raise StateError(message)
+    if status == 3:
+        raise OnnxMemoryLimitException(message, *budget)
     raise _BY_STATUS.get(status, StateError)(message)

@@ -392,6 +392,34 @@ def matmul_f32_dev(a_ptr: int, a_shape, b_ptr: int, b_shape, y_ptr: int,
                                 C.c_void_p(b_ptr), _ptr(sb), sb.size, C.c_void_p(y_ptr)))
 
 
+def matmul_f32_output_shape(a_shape, b_shape) -> tuple:
+    """Broadcast output shape of opMatMul over these operand shapes (no device)."""
+    sa = np.ascontiguousarray(np.array(a_shape, np.int64))
+    sb = np.ascontiguousarray(np.array(b_shape, np.int64))
+    out = np.zeros(16, np.int64)
+    rank = C.c_int32(0)
+    check(lib.mg_matmul_f32_output_shape(_ptr(sa), sa.size, _ptr(sb), sb.size, _ptr(out),
+                                         C.byref(rank)))
+    return tuple(int(v) for v in out[:rank.value])
+
+
+def matmul_f32_batch_offsets(a_shape, b_shape, first: int = 0, count: int | None = None):
+    """Element offsets into A and B of output batches [first, first + count) as
+    the fp32 kernels compute them (host-only)."""
+    sa = np.ascontiguousarray(np.array(a_shape, np.int64))
+    sb = np.ascontiguousarray(np.array(b_shape, np.int64))
+    if count is None:
+        nb = C.c_int64(0)
+        check(lib.mg_matmul_f32_batch_offsets(_ptr(sa), sa.size, _ptr(sb), sb.size, 0, 0,
+                                              None, None, C.byref(nb)))
+        count = nb.value - first
+    ao = np.zeros(max(count, 1), np.int64)
+    bo = np.zeros(max(count, 1), np.int64)
+    check(lib.mg_matmul_f32_batch_offsets(_ptr(sa), sa.size, _ptr(sb), sb.size, int(first),
+                                          int(count), _ptr(ao), _ptr(bo), None))
+    return ao[:count], bo[:count]
+
+
 def dynamic_quantize_linear_dev(x_ptr: int, n: int, y_ptr: int, scale_zp_ptr: int,
                                 ctx: Context | None = None):
     """DynamicQuantizeLinear on device: y uint8 [n]; at scale_zp_ptr 12 bytes:

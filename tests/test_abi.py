@@ -48,10 +48,22 @@ def test_version_and_last_error_without_device():
 def test_status_codes_map_to_reference_exceptions():
     from onnx_runtime_dart_amd import errors as E
     for st, cls in [(1, E.ArgumentError), (2, E.UnsupportedError),
-                    (3, E.OnnxMemoryLimitException), (4, E.OnnxCancelledException),
-                    (5, E.StateError)]:
+                    (4, E.OnnxCancelledException), (5, E.StateError)]:
         with pytest.raises(cls):
             E.raise_for_status(st, "x")
+    # MG_OUT_OF_MEMORY: the byte budget carries the reference exception's
+    # fields; a device allocator failure is a StateError.
+    with pytest.raises(E.OnnxMemoryLimitException) as ei:
+        E.raise_for_status(3, "x", (100, 16))
+    assert (ei.value.required_bytes, ei.value.limit_bytes) == (100, 16)
+    with pytest.raises(E.StateError):
+        E.raise_for_status(3, "hipMalloc: out of memory")
+
+
+def test_budget_query_without_a_failure():
+    from onnx_runtime_dart_amd import _lib
+    req = ctypes.c_int64(-1)
+    assert _lib.lib.mg_last_error_budget(ctypes.byref(req), None) in (0, 1)
 
 
 def test_host_validation_precedes_device_work():

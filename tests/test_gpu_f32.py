@@ -82,26 +82,68 @@ def test_gemm_attributes(ops, ta, tb, c_shape):
     assert G.rms_error(y, ref) <= TOL
 
 
-def test_bert_layer_shapes(ops):
-    # Config C3 (MiniLM-L6): Gemm transB=1 + bias at hidden 384 / FFN 1536,
-    # checked on 512 of the 4096 token rows; batched attention products.
+# Config C3 (MiniLM-L6, batch 32 x seq 128 = 4096 token rows, hidden 384,
+# 12 heads x 32, FFN 1536) at the size the bench times.  Every output row is
+# checked against a float64 product; row blocks at the start, across the
+# XCD band boundaries and at the end are checked against the oracle.
+C3_ROWS = 4096
+C3_ORACLE_ROWS = np.concatenate([np.arange(0, 256), np.arange(1984, 2240),
+                                 np.arange(C3_ROWS - 256, C3_ROWS)])
+
+
+@pytest.mark.parametrize("name,n,k", [("q", 384, 384), ("k", 384, 384), ("v", 384, 384),
+                                      ("out", 384, 384), ("ffn1", 1536, 384),
+                                      ("ffn2", 384, 1536)])
+def test_c3_gemm_full_size(ops, name, n, k):
+    rng = np.random.default_rng(0x5EED0002 + n + k)
+    x = rng.standard_normal((C3_ROWS, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    c = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    fw = ops.F32Weight(w, trans_b=True)
+    y = fw.gemm(x, c)
+    fw.release()
+    full = x.astype(np.float64) @ w.T.astype(np.float64) + c
+    assert G.rms_error(y, full) <= TOL
+    rows = C3_ORACLE_ROWS
+    ref = oracle.gemm_f32(x[rows], w, c, trans_b=True)
+    assert G.rms_error(y[rows], ref) <= TOL
+
+
+def test_c3_attention_matmuls_full_size(ops):
+    # The unfused attention products over all 32 x 12 heads.
     rng = np.random.default_rng(0x5EED0002)
-    for n, k in [(384, 384), (1536, 384), (384, 1536)]:
-        x = rng.standard_normal((512, k)).astype(np.float32)
-        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
-        c = (rng.standard_normal(n) * 0.02).astype(np.float32)
-        fw = ops.F32Weight(w, trans_b=True)
-        y = fw.gemm(x, c)
-        fw.release()
-        ref = oracle.gemm_f32(x, w, c, trans_b=True)
-        assert G.rms_error(y, ref) <= TOL
-    q = rng.standard_normal((4, 12, 128, 32)).astype(np.float32)
-    kt = rng.standard_normal((4, 12, 32, 128)).astype(np.float32)
+    q = rng.standard_normal((32, 12, 128, 32)).astype(np.float32)
+    kt = rng.standard_normal((32, 12, 32, 128)).astype(np.float32)
     s = ops.op_matmul(q, kt)
     assert G.rms_error(s, oracle.matmul_f32(q, kt)) <= TOL
-    p = rng.random((4, 12, 128, 128)).astype(np.float32)
-    v = rng.standard_normal((4, 12, 128, 32)).astype(np.float32)
+    p = rng.random((32, 12, 128, 128)).astype(np.float32)
+    v = rng.standard_normal((32, 12, 128, 32)).astype(np.float32)
     assert G.rms_error(ops.op_matmul(p, v), oracle.matmul_f32(p, v)) <= TOL
+
+
+@pytest.mark.parametrize("sa,sb", [((2, 3, 5, 7), (2, 3, 7, 4)),
+                                   ((2, 1, 40, 24), (3, 24, 36)),
+                                   ((1, 4, 3), (6, 3, 5)),
+                                   ((6, 4, 3), (3, 5)),
+                                   ((2, 1, 2, 1, 2, 1, 9, 8), (1, 2, 1, 2, 1, 2, 8, 12)),
+                                   ((32, 12, 128, 32), (32, 12, 32, 128))])
+def test_matmul_dev_broadcast_matches_host_entry(ops, sa, sb):
+    # mg_matmul_f32_dev with broadcast batch dims (offsets decoded in the
+    # kernel; more than four merged dims loop over launches) gives bitwise
+    # the host entry point's result, twice in a row on the same buffers.
+    rng = np.random.default_rng(31)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    want = ops.op_matmul(a, b)
+    ad, bd = ops.DeviceBuffer.from_array(a), ops.DeviceBuffer.from_array(b)
+    yd = ops.DeviceBuffer(want.nbytes)
+    for _ in range(2):
+        ops.matmul_f32_dev(ad.ptr, sa, bd.ptr, sb, yd.ptr)
+        got = yd.to_array(want.shape, np.float32)
+        np.testing.assert_array_equal(got, want)
+    assert G.rms_error(want, oracle.matmul_f32(a, b)) <= TOL
+    for buf in (ad, bd, yd):
+        buf.free()
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])

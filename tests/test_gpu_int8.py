@@ -228,3 +228,69 @@ def test_dq_dev_errors(ops):
         w.qlinear_matmul_dq_dev(buf.ptr, 2, buf.ptr, 1.0, 1.0, 0, buf.ptr, lo=0, hi=127)
     buf.free()
     w.release()
+
+
+# The Qwen3-0.6B projections as MatMulInteger at M = 512 (the shapes the
+# bench times, u8 activations with zero point 128, i8 weights with zero point
+# 0).  Column subsets (first, across the middle, last) are bit-exact against
+# the oracle; over the whole output, exact row and column sums pin every
+# element's contribution: sum_n Y[m, n] = (A[m] - zp) . (B 1) and
+# sum_m Y[m, n] = (1^T (A - zp)) . B[:, n], computed in int64.
+QWEN_I8 = [("q", 1024, 2048), ("k", 1024, 1024), ("o", 2048, 1024), ("gate", 1024, 3072),
+           ("down", 3072, 1024), ("lm_head", 1024, 151936)]
+
+
+def _column_subsets(n):
+    mid = n // 2 - 96
+    return np.unique(np.concatenate([np.arange(0, min(n, 160)), np.arange(mid, mid + 192),
+                                     np.arange(max(0, n - 224), n)]))
+
+
+@pytest.mark.parametrize("name,k,n", QWEN_I8)
+def test_qwen_int8_projection_full_size(ops, name, k, n):
+    rng = np.random.default_rng(0x5EED0002 + k + n)
+    m = 512
+    a = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    w = ops.Int8Weight(b, np.array(0))
+    y = w.matmul_integer(a, np.array(128))
+    assert y.shape == (m, n)
+    cols = _column_subsets(n)
+    np.testing.assert_array_equal(y[:, cols], oracle.matmul_integer(a, b[:, cols].copy(),
+                                                                    np.array(128), np.array(0)))
+    ac = a.astype(np.int64) - 128
+    np.testing.assert_array_equal(y.astype(np.int64).sum(axis=1),
+                                  ac @ b.astype(np.int64).sum(axis=1))
+    np.testing.assert_array_equal(y.astype(np.int64).sum(axis=0),
+                                  ac.sum(axis=0) @ b.astype(np.int64))
+    # QLinearMatMul through the same packed weight, bit-exact on the subsets.
+    rows = np.arange(0, m, 3)
+    yq = w.qlinear_matmul(a[rows], 0.0123, np.array(128), 2 ** -10, 0.05, 128, lo=0, hi=255)
+    ref = oracle.qlinear_matmul(a[rows], np.float32(0.0123), np.array(128), b[:, cols].copy(),
+                                np.float32(2 ** -10), np.array(0), np.float32(0.05),
+                                np.array(128), lo=0, hi=255)
+    np.testing.assert_array_equal(yq[:, cols], ref)
+    w.release()
+
+
+def test_dev_calls_with_per_row_zero_points_back_to_back(ops):
+    # Asynchronous calls whose per-row zero-point tables are host arrays that
+    # go away right after each call: the tables travel through the context's
+    # pinned staging (16 slots), so 40 calls queued without a wait wrap it
+    # and every result still uses its own table.
+    rng = np.random.default_rng(41)
+    m, k, n, calls = 33, 200, 70, 40
+    a = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    b = rng.integers(-128, 128, (k, n)).astype(np.int8)
+    w = ops.Int8Weight(b, np.array(-5))
+    ad = ops.DeviceBuffer.from_array(a)
+    ys = [ops.DeviceBuffer(m * n * 4) for _ in range(calls)]
+    zps = [rng.integers(0, 255, m) for _ in range(calls)]
+    for i in range(calls):
+        w.matmul_integer_dev(ad.ptr, False, m, ys[i].ptr, zps[i].copy())
+    for i in range(calls):
+        got = ys[i].to_array((m, n), np.int32)
+        np.testing.assert_array_equal(got, oracle.matmul_integer(a, b, zps[i], np.array(-5)))
+    for buf in ys + [ad]:
+        buf.free()
+    w.release()

@@ -272,8 +272,9 @@ def test_control_cancel_and_budget(ops):
     with pytest.raises(OnnxCancelledException):
         w(a)
     ctx.set_control(None, max_bytes=16)
-    with pytest.raises(OnnxMemoryLimitException):
+    with pytest.raises(OnnxMemoryLimitException) as ei:
         w(a)
+    assert ei.value.limit_bytes == 16 and ei.value.required_bytes > 16
     ctx.set_control(None, max_bytes=-1)
     ref = oracle.matmul_nbits(a, b, s, zp, k=256, n=64, block_size=32)
     assert G.rms_error(w(a), ref) <= TOL
@@ -307,6 +308,37 @@ def test_group_matches_single_calls(ops, m, bs, zp_mode):
         assert np.abs(got - single).max() <= 1e-5 * max(1.0, float(np.abs(single).max()))
     for w in ws:
         w.release()
+
+
+# Llama-1B decode groups the bench times (block 32, packed zero points): q/k/v
+# (K 2048 -> 2048 + 512 + 512) and gate/up (K 2048 -> 8192 + 8192) as one
+# launch each, at M = 1, 4 and 16.  Every output is checked against the
+# oracle on column subsets and must equal bitwise the separate single-weight
+# calls (at these shapes the group and the single calls split K the same way).
+@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("group", ["qkv", "gate_up"])
+def test_llama_groups_at_bench_shapes(ops, m, group):
+    rng = np.random.default_rng(0x5EED0004 + m)
+    k, bs = 2048, 32
+    ns = [2048, 512, 512] if group == "qkv" else [8192, 8192]
+    hw = [make_nbits(rng, n, k, bs, "packed") for n in ns]
+    ws = [ops.NBitsWeight(b, s, z, k=k, n=n, block_size=bs) for (b, s, z), n in zip(hw, ns)]
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    ad = ops.DeviceBuffer.from_array(a)
+    ys = [ops.DeviceBuffer.from_array(np.full((m, n), np.nan, np.float32)) for n in ns]
+    ops.matmul_nbits_group_dev(ws, ad.ptr, m, [y.ptr for y in ys])
+    for (b, s, z), n, w, y in zip(hw, ns, ws, ys):
+        got = y.to_array((m, n), np.float32)
+        cols = np.unique(np.concatenate([np.arange(0, 96), np.arange(n // 2 - 40, n // 2 + 40),
+                                         np.arange(n - 72, n)]))
+        ref = oracle.matmul_nbits(a, *slice_cols(b, s, z, None, cols)[:3], k=k, n=len(cols),
+                                  block_size=bs)
+        assert G.rms_error(got[:, cols], ref) <= TOL
+        np.testing.assert_array_equal(got, w(a))
+    for w in ws:
+        w.release()
+    for buf in ys + [ad]:
+        buf.free()
 
 
 def test_group_validation(ops):
