@@ -42,28 +42,9 @@
 #include <vector>
 
 #include "mg_internal.h"
+#include "nbits_common.h"
 
 namespace {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float float4v __attribute__((ext_vector_type(4)));
-typedef float float16v __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int KGRP = 128;  // k per k group
-constexpr int CGRP = 64;   // columns per column group
-constexpr int FIX_MAX = 30583;  // 7 * (1 + 16 + 256 + 4096): 4 balanced int4 digits
-
-__host__ __device__ inline int nib_pos(int t) {
-  return (t & 1) ? 4 + (t >> 1) : (t >> 1);
-}
-
-// Position of column c (0..63) of a column group in the per-block scale and
-// zero-point rows: the four 16-column tiles of one column residue are
-// adjacent, so a lane that owns columns c, c + 16, c + 32, c + 48 (the
-// 16-row MFMA GEMV) reads their four values with one load.
-__host__ __device__ inline int sz_pos(int c) { return (c & 15) * 4 + (c >> 4); }
 
 // ------------------------------------------------------------- prepasses
 
@@ -181,7 +162,6 @@ __global__ __launch_bounds__(256) void k_af16split(
 // activations, launched together (q/k/v or gate/up of a decoder layer): the
 // grid's column groups are the concatenation of the members' column groups,
 // and each workgroup picks its member from the running totals cg_end.
-constexpr int GMAX = 4;
 struct GemvSet {
   const uint4 *wq[GMAX];
   const float *scales[GMAX];
@@ -539,52 +519,6 @@ __global__ __launch_bounds__(256) void k_gemv_dot8p(
 
 // --------------------------------------------------------- prefill GEMM
 
-// Dequantises one weight dword (8 codes, nibble order of wq) to 8 exact fp16
-// values for the MFMA path.  Masking a nibble into the fp16 pattern 0x6400
-// (1024.0) gives 1024 + q for a nibble at bits 0-3 of a half-word and
-// 1024 + 16q for one at bits 4-7, so the pairs (t0,t1), (t4,t5) come out as
-// q - zp and (t2,t3), (t6,t7) as 16(q - zp) with a single shift for all
-// eight; the activation prepass scales k offsets 2,3,6,7 of every 8 by 1/16
-// to match.  `mask`/`magic` are register operands (one v_and_or_b32 each).
-__device__ inline uint4 deq8(uint32_t x, uint32_t mlo, uint32_t mhi, uint32_t magic,
-                             half2v zz1, half2v zz16) {
-  const uint32_t y = x >> 8;
-  const uint32_t d0 = (x & mlo) | magic, d1 = (x & mhi) | magic;
-  const uint32_t d2 = (y & mlo) | magic, d3 = (y & mhi) | magic;
-  return make_uint4(__builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d0) + zz1),
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d1) + zz16),
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d2) + zz1),
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d3) + zz16));
-}
-
-// Up to GMAX weights that share K, block size, zero-point kind and the input
-// activations, run as one prefill launch: the grid's column tiles are the
-// concatenation of the members' column tiles (ct_end holds the running
-// totals), and each workgroup picks its member from them.  Split-K partials of
-// member i start at part + part_off[i] ([ksplit][M][N_i]).
-struct PrefillSet {
-  const uint4 *wq[GMAX];
-  const float *scales[GMAX];
-  const uint8_t *zp4[GMAX];
-  const float *bias[GMAX];
-  float *y[GMAX];
-  int64_t part_off[GMAX];
-  int N[GMAX];
-  int ct_end[GMAX];
-  int y_vec[GMAX];  // y base 16-byte aligned
-  int n;
-};
-
-// Member of global column tile x and its local tile index (workgroup-uniform).
-__device__ inline int prefill_member(const PrefillSet &ps, int x, int *nt) {
-  int m = 0;
-#pragma unroll
-  for (int i = 0; i < GMAX - 1; i++)
-    if (i + 1 < ps.n && x >= ps.ct_end[i]) m = i + 1;
-  *nt = x - (m ? ps.ct_end[m - 1] : 0);
-  return m;
-}
-
 // Workgroup tile: 128 rows x 32*NT columns (NT/2 column groups), 4 waves;
 // wave w owns rows [32*w, +32) of the tile and all its columns (NT MFMA tiles
 // of 32x32, v_mfma_f32_32x32x16_f16).  NT = 4 for wide weights; NT = 2 halves
@@ -885,56 +819,6 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f16split(
         if (col + 3 < N) p[3] = v[3];
       }
     }
-  }
-}
-
-// y_i = sum over k splits of the partials of member i + bias_i
-// (deterministic split-K reduction); elements of the members concatenated,
-// member i starting at element e_end[i - 1] (M * N_i elements each).
-struct ReduceSet {
-  const float *bias[GMAX];
-  float *y[GMAX];
-  int64_t part_off[GMAX];
-  int64_t e_end[GMAX];
-  int N[GMAX];
-  int n;
-};
-// Thread = VW consecutive elements of one member (VW = 4: every N % 4 == 0
-// and y 16-byte aligned, so a piece never straddles rows or members).  The
-// splits are added in split order, four loads in flight at a time.
-template <int VW>
-__global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part,
-                                                     const ReduceSet rs, int ksplit) {
-  typedef float fv __attribute__((ext_vector_type(VW)));
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VW;
-  if (i >= rs.e_end[rs.n - 1]) return;
-  int m = 0;
-#pragma unroll
-  for (int j = 0; j < GMAX - 1; j++)
-    if (j + 1 < rs.n && i >= rs.e_end[j]) m = j + 1;
-  const int64_t li = i - (m ? rs.e_end[m - 1] : 0);
-  const int64_t mn = rs.e_end[m] - (m ? rs.e_end[m - 1] : 0);
-  const fv *p = reinterpret_cast<const fv *>(part + rs.part_off[m] + li);
-  const int64_t step = mn / VW;
-  fv s = (fv)(0.f);
-  int k = 0;
-  for (; k + 4 <= ksplit; k += 4) {
-    const fv x0 = p[k * step], x1 = p[(k + 1) * step];
-    const fv x2 = p[(k + 2) * step], x3 = p[(k + 3) * step];
-    s += x0;
-    s += x1;
-    s += x2;
-    s += x3;
-  }
-  for (; k < ksplit; k++) s += p[k * step];
-  const float *b = rs.bias[m];
-  float *y = rs.y[m] + li;
-  if constexpr (VW == 1) {
-    *y = s[0] + (b ? b[li % rs.N[m]] : 0.f);
-  } else {
-    const int64_t c = li % rs.N[m];
-    if (b) s += *reinterpret_cast<const fv *>(b + c);
-    *reinterpret_cast<fv *>(y) = s;
   }
 }
 
@@ -1286,8 +1170,19 @@ __global__ __launch_bounds__(256) void k_nbits_generic(
 
 // ------------------------------------------------------------ host side
 
+}  // namespace
+
+// The fp8 prefill GEMM (nbits_f8.hip): workspace layout for mpad rows and c4
+// k groups (returns the bytes before the split-K partials), and the launch.
+size_t mg_nbits_f8_ws(int64_t mpad, int64_t c4, size_t *off_asc, size_t *off_nf);
+mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, const float *a_dev,
+                              int64_t M, float *const *y_dev, void *ws, int64_t mpad, int nt,
+                              int ksplit, int kps, size_t off_part);
+
+namespace {
+
 struct NbitsPlan {
-  int path;  // 0 gemv (dot8), 1 prefill mfma, 2 generic, 3 decode mfma
+  int path;  // 0 gemv (dot8), 1 prefill mfma (fp16), 2 generic, 3 decode mfma, 4 prefill fp8
   int64_t M;
   // gemv
   int qpg = 1, qb = 128, ksplit = 1, kps = 0, nw = 4, kc = 0;
@@ -1361,7 +1256,10 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
       p.lds = (size_t)(d.c4 * per_kg + 2 * 4 * M * 64 * 4);
     }
   } else if (d.bs >= 32 && int_zp) {
-    p.path = 1;
+#ifndef MG_PREFILL_F8
+#define MG_PREFILL_F8 1
+#endif
+    p.path = (MG_PREFILL_F8 && d.bs >= KGRP) ? 4 : 1;
     // Workgroups per CU to aim for, and k groups per split to keep.
 #ifndef MG_PREFILL_WG_PER_CU
 #define MG_PREFILL_WG_PER_CU 1
@@ -1381,9 +1279,14 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
     while (tiles * ks * 2 <= target && d.c4 / (ks * 2) >= MG_PREFILL_MIN_KG) ks *= 2;
     p.kps = (int)((d.c4 + ks - 1) / ks);
     p.ksplit = (int)((d.c4 + p.kps - 1) / p.kps);
-    p.off_a = 0;  // ahl: mpad * kpad * 2 fp16
-    p.off_b = mg_align(p.off_a + (size_t)p.mpad * d.kpad * 4);  // texp [row]
-    p.off_c = mg_align(p.off_b + (size_t)p.mpad * 4);           // split-K partials
+    if (p.path == 4) {
+      size_t o_asc = 0, o_nf = 0;  // fp8 digits, scale words, non-finite flags
+      p.off_c = mg_nbits_f8_ws(p.mpad, d.c4, &o_asc, &o_nf);  // split-K partials after them
+    } else {
+      p.off_a = 0;  // ahl: mpad * kpad * 2 fp16
+      p.off_b = mg_align(p.off_a + (size_t)p.mpad * d.kpad * 4);  // texp [row]
+      p.off_c = mg_align(p.off_b + (size_t)p.mpad * 4);           // split-K partials
+    }
     p.total = mg_align(p.off_c + (p.ksplit > 1 ? (size_t)p.ksplit * M * n_total * 4 : 0));
   } else {
     p.path = 2;
@@ -1781,6 +1684,9 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
     return mg_launch_check("k_gemv_mfma");
   }
   if (p.path == 1) return prefill_run(ctx, n, w, a_dev, M, y_dev, ws, p);
+  if (p.path == 4)
+    return mg_nbits_prefill_f8(ctx, n, w, a_dev, M, y_dev, ws, p.mpad, p.nt, p.ksplit, p.kps,
+                               p.off_c);
   // Generic form: one launch per weight.
   for (int i = 0; i < n; i++) MG_TRY(nbits_run_generic(ctx, w[i], a_dev, M, y_dev[i]));
   return MG_OK;
@@ -1820,27 +1726,9 @@ mg_status prefill_run(mg_ctx *ctx, int n, const mg_weight *const *w, const float
   const int has_zp = d.zp_kind == MG_ZP_UINT4;
   PrefillSet ps{};
   ReduceSet rs{};
-  ps.n = rs.n = n;
   int ct = 0;
-  int64_t poff = 0, eend = 0;
-  for (int i = 0; i < n; i++) {
-    const mg_nbits_dev &di = w[i]->nbits;
-    ps.wq[i] = reinterpret_cast<const uint4 *>(di.wq);
-    ps.scales[i] = di.scales;
-    // The kernel reads zero-point bytes unconditionally (branch-free); without
-    // zero points it is pointed at the scales, which are at least as large.
-    ps.zp4[i] = has_zp ? di.zp4 : reinterpret_cast<const uint8_t *>(di.scales);
-    ps.bias[i] = rs.bias[i] = di.bias;
-    ps.y[i] = rs.y[i] = y_dev[i];
-    ps.N[i] = rs.N[i] = (int)w[i]->N;
-    ps.y_vec[i] = (reinterpret_cast<uintptr_t>(y_dev[i]) % 16) == 0;
-    ps.part_off[i] = rs.part_off[i] = poff;
-    poff += (int64_t)p.ksplit * M * w[i]->N;
-    eend += M * w[i]->N;
-    rs.e_end[i] = eend;
-    ct += (int)(p.nt == 4 ? di.ng / 2 : di.ng);
-    ps.ct_end[i] = ct;
-  }
+  int64_t eend = 0;
+  make_prefill_sets(n, w, y_dev, M, p.ksplit, p.nt, &ps, &rs, &ct, &eend);
   const int mtiles = (int)(p.mpad / 128);
   const dim3 grid((unsigned)(8 * mtiles * ((ct + 7) / 8)), (unsigned)p.ksplit);
   const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
@@ -1859,22 +1747,7 @@ mg_status prefill_run(mg_ctx *ctx, int n, const mg_weight *const *w, const float
   }
 #undef MG_GEMM_LAUNCH
   MG_TRY(mg_launch_check("k_gemm_f16split"));
-  if (p.ksplit > 1) {
-    // Four elements per thread when no piece can straddle a row: every N % 4
-    // == 0, y and the bias 16-byte aligned (partial offsets are then
-    // multiples of 4 elements and the buffer is aligned).
-    bool v4 = true;
-    for (int i = 0; i < n; i++)
-      v4 = v4 && rs.N[i] % 4 == 0 && reinterpret_cast<uintptr_t>(rs.y[i]) % 16 == 0 &&
-           reinterpret_cast<uintptr_t>(rs.bias[i]) % 16 == 0;
-    if (v4)
-      hipLaunchKernelGGL(k_gemm_reduce<4>, dim3((unsigned)((eend / 4 + 255) / 256)), dim3(256),
-                         0, st, part, rs, p.ksplit);
-    else
-      hipLaunchKernelGGL(k_gemm_reduce<1>, dim3((unsigned)((eend + 255) / 256)), dim3(256), 0,
-                         st, part, rs, p.ksplit);
-    MG_TRY(mg_launch_check("k_gemm_reduce"));
-  }
+  if (p.ksplit > 1) MG_TRY(launch_gemm_reduce(st, part, rs, eend, p.ksplit));
   return MG_OK;
 }
 

@@ -1,0 +1,530 @@
+// MatMulNBits prefill GEMM on gfx950 block-scaled fp8 MFMA
+// (v_mfma_scale_f32_32x32x64_f8f6f4), for block_size >= 128 with integer
+// zero points.
+//
+// Reference semantics: opMatMulNBits, lib/src/onnx_qlinear_ops.dart:115-228
+// (M > 1: dequantised fp32 weights times fp32 activations, :208-226).
+//
+// Numbers.  Each weight (q - zp) is an integer in [-15, 15] and each
+// 16 (q - zp) one in [-240, 240]: both are exact in fp8 e4m3.  Each fp32
+// activation is carried as the sum of three e4m3 digits, each digit of a
+// 32-element block with its own power-of-two (E8M0) scale that the MFMA
+// applies in hardware: r0 = a, d_i = e4m3(r_i / 2^E_i) rounded to nearest
+// even, r_{i+1} = r_i - d_i 2^E_i, with 2^E_i putting the block's largest
+// |r_i| in [128, 256).  Every digit keeps 4 significant bits of what is left,
+// so the residual after three digits is below 2^-12 of each element; products
+// and sums are fp32 in the MFMA.  Measured against fp64 on 512 x 1024 x 8192
+// Gaussian activations this is ~1e-4 of the output rms at the largest
+// element, against ~1.3e-3 for fp16 activations.  Three fp8 MFMAs cost 1.5
+// fp16 ones (the fp16 hi/lo split of the other prefill path costs 2), and the
+// weight tile in LDS is 1 byte per weight instead of 2.
+//
+// Non-finite activations: the digits carry the finite values only and the
+// prepass flags the 32-element blocks that held Inf or NaN; for a flagged row
+// the epilogue rebuilds the reference's Inf / NaN pattern of each output
+// column from the non-finite activations of the launch's k range and the
+// dequantised weights there (inf * w = +-inf by sign, inf * 0 and NaN give
+// NaN, opposite infinities give NaN).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "mg_internal.h"
+#include "nbits_common.h"
+
+namespace {
+
+typedef int int8v __attribute__((ext_vector_type(8)));
+typedef short short2v __attribute__((ext_vector_type(2)));
+
+// --------------------------------------------------------------- prepass
+
+// Activations -> three e4m3 digits per element in the A-operand order of
+// v_mfma_scale_f32_32x32x64_f8f6f4.  Lane l of the operand holds row l % 32
+// of 32-row tile m32; in 64-k step st of k group kg, byte i of lane half
+// h = l / 32 holds k = 128 kg + 32 j + 8 g + t with g = 2 h + i / 16,
+// j = 2 st + (i / 8) % 2, t = i % 8 (the weight fragments in LDS use the
+// same order).  The MFMA's scale blocks are bytes 0-15 of both lane halves
+// (block 0, scale from lane r) and bytes 16-31 of both (block 1, scale from
+// lane r + 32): block b holds the octets g = b and g = b + 2.  Bytes at t in
+// {2, 3, 6, 7} carry a * 2^-4: the weights there are 16 (q - zp), as deq8
+// makes them.
+// Output per (m32, kg): aq[((m32 * c4n + kg) * 2 + st) * 3 + d][lane][2]
+// (uint4: bytes 0-15, 16-31), asc[(m32 * c4n + kg) * 2 + st][r + 32 b] = the
+// three E8M0 scale bytes of block b (digit d in byte d), nf[(row * c4n + kg)
+// * 4 + 2 st + b] = 1 when the block held a non-finite value.  Rows >= M and
+// k >= K are zeros.  Thread = one scale block (r, b); wave = one (m32, kg, st).
+__global__ __launch_bounds__(256) void k_af8x3(const float *__restrict__ a, int64_t M,
+                                               int64_t K, int c4n, int vec, int64_t nwaves,
+                                               uint4 *__restrict__ aq,
+                                               uint32_t *__restrict__ asc,
+                                               uint8_t *__restrict__ nf) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int64_t wv = (int64_t)blockIdx.x * 4 + (t >> 6);
+  if (wv >= nwaves) return;  // whole wave
+  const int st = (int)(wv & 1);
+  const int64_t mk = wv >> 1;  // m32 * c4n + kg
+  const int kg = (int)(mk % c4n);
+  const int64_t m32 = mk / c4n;
+  const int r = lane & 31, b = lane >> 5;
+  const int64_t row = m32 * 32 + r;
+  const bool live = row < M;
+  const float *arow = a + (live ? row : 0) * K;
+  // v[16 hh + 8 jj + tt]: lane half hh, octet g = 2 hh + b, j = 2 st + jj.
+  float v[32];
+#pragma unroll
+  for (int o = 0; o < 4; o++) {
+    const int hh = o >> 1, jj = o & 1;
+    const int g = 2 * hh + b, j = 2 * st + jj;
+    const int64_t k0 = (int64_t)kg * KGRP + 32 * j + 8 * g;
+    if (live && vec && k0 + 8 <= K) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(arow + k0);
+      const float4 x1 = *reinterpret_cast<const float4 *>(arow + k0 + 4);
+      v[8 * o] = x0.x; v[8 * o + 1] = x0.y; v[8 * o + 2] = x0.z; v[8 * o + 3] = x0.w;
+      v[8 * o + 4] = x1.x; v[8 * o + 5] = x1.y; v[8 * o + 6] = x1.z; v[8 * o + 7] = x1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[8 * o + i] = (live && k0 + i < K) ? arow[k0 + i] : 0.f;
+    }
+  }
+  int bad = 0;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    float x = v[i];
+    if (!isfinite(x)) {
+      bad = 1;
+      x = 0.f;
+    }
+    v[i] = (i & 2) ? x * 0.0625f : x;  // exact
+  }
+  uint32_t scales = 0;
+  uint4 *out = aq + (((m32 * c4n + kg) * 2 + st) * 3) * 128 + 2 * r + b;
+#pragma unroll
+  for (int d = 0; d < 3; d++) {
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) mx = fmaxf(mx, fabsf(v[i]));
+    int E = 0;
+    if (mx > 0.f) {
+      int ex;
+      frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+      E = min(max(ex - 8, -127), 127);
+    }
+    uint32_t wd[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      int w = 0;
+      w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * q], -E), ldexpf(v[4 * q + 1], -E), w,
+                                          false);
+      w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * q + 2], -E), ldexpf(v[4 * q + 3], -E),
+                                          w, true);
+      wd[q] = (uint32_t)w;
+      v[4 * q] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 0), E);
+      v[4 * q + 1] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 1), E);
+      v[4 * q + 2] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 2), E);
+      v[4 * q + 3] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 3), E);
+    }
+    // Plane b of lane r (half 0) and of lane r + 32 (half 1).
+    out[d * 128] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    out[d * 128 + 64] = make_uint4(wd[4], wd[5], wd[6], wd[7]);
+    scales |= (uint32_t)(E + 127) << (8 * d);
+  }
+  asc[((m32 * c4n + kg) * 2 + st) * 64 + lane] = scales;
+  nf[(row * c4n + kg) * 4 + 2 * st + b] = (uint8_t)bad;
+}
+
+// ------------------------------------------------------------------ GEMM
+
+// One digit's MFMA: the op_sel byte of the A scale word is the digit.
+template <int DG>
+__device__ inline float16v mfma_digit(const int8v &a, const int8v &b, const float16v &c, int sa,
+                                      int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, DG, sa, 0, sb);
+}
+
+// Dequantised weight (q - zp) * s of column col at k, in fp32 (the
+// non-finite pattern only needs its sign and whether it is zero).
+__device__ inline float nbits_weight(const uint4 *__restrict__ wq, const float *__restrict__ sc,
+                                     const uint8_t *__restrict__ zp4, int c4n, int nb, int nbh,
+                                     int lbs, int has_zp, int col, int k) {
+  const int cg = col >> 6, cl = col & 63;
+  const int kg = k >> 7, kk = k & 127;
+  const int j = kk >> 5, g = (kk >> 3) & 3, tt = kk & 7;
+  const uint32_t *wd = reinterpret_cast<const uint32_t *>(wq) +
+                       (((int64_t)cg * c4n + kg) * 256 + g * 64 + cl) * 4 + j;
+  const int q = (int)((*wd >> (4 * nib_pos(tt))) & 15u);
+  const int blk = min(k >> lbs, nb - 1);
+  const int z = has_zp ? (int)((zp4[((int64_t)cg * nbh + blk / 2) * 64 + sz_pos(cl)] >>
+                                (4 * (blk & 1))) & 15u)
+                       : 8;
+  return (float)(q - z) * sc[((int64_t)cg * nb + blk) * 64 + sz_pos(cl)];
+}
+
+// Workgroup tile: 128 rows x 32*NT columns (NT/2 column groups), 4 waves;
+// wave w owns rows [32 w, +32) of the tile and all its columns (NT MFMA
+// tiles of 32 x 32).  Per k group (128 k = 2 steps of 64 k):
+//   * the workgroup dequantises the 128 x 32*NT weight tile once into LDS as
+//     e4m3 fragments (double-buffered: the next k group's packed codes are
+//     loaded at the start of the current one and converted a quarter at a
+//     time between its MFMAs);
+//   * per step each wave runs three MFMA rounds (digits d = 0, 1, 2) over its
+//     NT tiles into the k group's fp32 accumulator D, the digit's scales
+//     selected with op_sel; after round d the digit-d fragment of the next
+//     step is loaded into the same registers (three rounds ahead of use);
+//   * the block scale (one per k group: block_size >= 128) is applied on the
+//     fp32 accumulator, acc += s * D, deferred to the next k group's first
+//     round so those FMAs overlap MFMAs.
+// Grid, member choice, split-K partials and the epilogue's row-contiguous
+// 16-byte stores are those of the fp16 prefill kernel.
+template <int NT>
+__global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f8x3(
+    const uint4 *__restrict__ aq, const uint32_t *__restrict__ asc,
+    const uint8_t *__restrict__ nf, const float *__restrict__ a, int64_t K,
+    const PrefillSet ps, float *__restrict__ part, int M, int c4n, int nb, int nbh, int lbs,
+    int has_zp, int mtiles, int ntiles, int kps) {
+  constexpr int PH = NT / 2;          // column groups per tile
+  constexpr int TC = 32 * NT;         // tile columns
+  constexpr int BU4 = NT * 2 * 2 * 64;  // uint4 per weight buffer: [n32][st][plane][lane]
+  constexpr int STAGE_U4 = 32 * TC;     // 4 waves x 32 rows x TC floats, in uint4
+  constexpr int LDS_U4 = 2 * BU4 > STAGE_U4 ? 2 * BU4 : STAGE_U4;
+  __shared__ uint4 lds[LDS_U4];
+  __shared__ float scl[2][32][NT];  // [buf][col % 32][n32]
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int L = blockIdx.x;
+  const int xcd = L & 7, q = L >> 3;
+  const int mt = q % mtiles;
+  const int ntg = (q / mtiles) * 8 + xcd;
+  if (ntg >= ntiles) return;
+  int nt;
+  const int mem = prefill_member(ps, ntg, &nt);
+  const uint4 *__restrict__ wq = ps.wq[mem];
+  const float *__restrict__ scales = ps.scales[mem];
+  const uint8_t *__restrict__ zp4 = ps.zp4[mem];
+  const float *__restrict__ bias = ps.bias[mem];
+  const int N = ps.N[mem];
+  const int ks = blockIdx.y;
+  const int kg0 = ks * kps;
+  const int kg1 = min(c4n, kg0 + kps);
+  const int m32 = mt * 4 + wave;  // this wave's 32-row subtile
+  const int lc = lane & 31;
+
+  // Cooperative dequantisation: thread t handles the packed uint4 (column
+  // group PH*nt + h, g = wave, col = lane) for h < PH; its dword j (k = 32 j +
+  // 8 g .. +7) becomes 8 e4m3 bytes of lane (c % 32) + 32 (g / 2), step j / 2,
+  // plane g % 2, 8-byte slot j % 2, where c = 64 h + lane is the tile column.
+  const int dq_g = wave;
+  int dq_dst[PH];
+#pragma unroll
+  for (int h = 0; h < PH; h++) {
+    const int c = 64 * h + lane;
+    dq_dst[h] = ((c >> 5) * 4 + (dq_g & 1)) * 64 + (c & 31) + 32 * (dq_g >> 1);
+  }
+  const int nbm1 = nb - 1, nbhm1 = nbh - 1;
+  auto rsrc = [](const void *base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7ffffff0,
+                                             0x00020000);
+  };
+  __amdgpu_buffer_rsrc_t r_wq[PH], r_zp[PH], r_sc[PH];
+#pragma unroll
+  for (int h = 0; h < PH; h++) {
+    const int64_t cgi = PH * nt + h;
+    r_wq[h] = rsrc(wq + cgi * c4n * 256);
+    r_zp[h] = rsrc(zp4 + cgi * nbh * 64);
+    r_sc[h] = rsrc(scales + cgi * nb * 64);
+  }
+  const unsigned vo16 = 16u * lane;
+  const unsigned vo_zp = (unsigned)sz_pos(lane);
+  const unsigned vo_sc = 4u * vo_zp;
+  uint32_t v_mlo, v_mhi, v_magic;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v_mlo) : "s"(0x000F000Fu));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v_mhi) : "s"(0x00F000F0u));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v_magic) : "s"(0x64006400u));
+  struct Meta {
+    uint4 pk[PH];
+    uint32_t zb[PH];
+    float sc[PH];
+    uint32_t z1[PH], z16[PH];
+  };
+  auto load_meta = [&](int kg, Meta &m) {
+    const int blk = (kg * KGRP) >> lbs;
+    const int zbyte = min(blk / 2, nbhm1);
+#pragma unroll
+    for (int h = 0; h < PH; h++) {
+      m.pk[h] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(r_wq[h], vo16, (kg * 4 + dq_g) * 1024, 0));
+      m.zb[h] = __builtin_amdgcn_raw_buffer_load_b8(r_zp[h], vo_zp, zbyte * 64, 0);
+      m.sc[h] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(r_sc[h], vo_sc, min(blk, nbm1) * 256, 0));
+    }
+  };
+  // Converts dword j of the packed uint4 into buffer buf (and, with j == 0,
+  // stages the k group's block scale).
+  auto dequant_quarter = [&](int kg, Meta &m, int buf, int j) {
+    const int blk = (kg * KGRP) >> lbs;
+#pragma unroll
+    for (int h = 0; h < PH; h++) {
+      uint32_t w = j == 0 ? m.pk[h].x : j == 1 ? m.pk[h].y : j == 2 ? m.pk[h].z : m.pk[h].w;
+      asm volatile("" : "+v"(w));
+      if (j == 0) {
+        uint32_t zb = m.zb[h];
+        asm volatile("" : "+v"(zb));
+        const uint32_t z = has_zp ? (zb >> ((blk & 1) * 4)) & 15u : 8u;
+        m.z1[h] = 0xE400E400u + z * 0x00010001u;
+        m.z16[h] = 0xE400E400u + z * 0x00100010u;
+      }
+      const uint4 f = deq8(w, v_mlo, v_mhi, v_magic, __builtin_bit_cast(half2v, m.z1[h]),
+                           __builtin_bit_cast(half2v, m.z16[h]));
+      short2v b0 = (short2v){0, 0}, b1 = (short2v){0, 0};
+      b0 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(b0, __builtin_bit_cast(half2v, f.x), 1.0f,
+                                                    false);
+      b0 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(b0, __builtin_bit_cast(half2v, f.y), 1.0f,
+                                                    true);
+      b1 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(b1, __builtin_bit_cast(half2v, f.z), 1.0f,
+                                                    false);
+      b1 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(b1, __builtin_bit_cast(half2v, f.w), 1.0f,
+                                                    true);
+      uint2 *dst = reinterpret_cast<uint2 *>(&lds[buf * BU4 + dq_dst[h] + (j >> 1) * 128]);
+      dst[j & 1] = make_uint2(__builtin_bit_cast(uint32_t, b0), __builtin_bit_cast(uint32_t, b1));
+    }
+    if (j == 0 && dq_g == 0) {
+      const bool in_range = blk < nb;
+#pragma unroll
+      for (int h = 0; h < PH; h++) {
+        float sc = m.sc[h];
+        asm volatile("" : "+v"(sc));
+        const int c = 64 * h + lane;
+        scl[buf][c & 31][c >> 5] = in_range ? sc : 0.f;
+      }
+    }
+  };
+  // Digit d of step st of k group kg: 32 bytes (two uint4) of this lane.
+  const __amdgpu_buffer_rsrc_t r_a = rsrc(aq + (int64_t)m32 * c4n * 768);
+  const __amdgpu_buffer_rsrc_t r_s = rsrc(asc + (int64_t)m32 * c4n * 128);
+  const unsigned vo32 = 32u * lane, vo4 = 4u * lane;
+  auto a_load = [&](int kg, int st, int d) __attribute__((always_inline)) {
+    const int off = ((kg * 2 + st) * 3 + d) * 2048;
+    const uint4 x0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r_a, vo32, off, 0));
+    const uint4 x1 =
+        __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r_a, vo32, off + 16, 0));
+    return (int8v){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                   (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+  };
+  auto s_load = [&](int kg, int st) __attribute__((always_inline)) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r_s, vo4, (kg * 2 + st) * 256, 0);
+  };
+  auto b_load = [&](int buf, int n, int st) __attribute__((always_inline)) {
+    const uint4 x0 = lds[buf * BU4 + ((n * 2 + st) * 2) * 64 + lane];
+    const uint4 x1 = lds[buf * BU4 + ((n * 2 + st) * 2 + 1) * 64 + lane];
+    return (int8v){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                   (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+  };
+
+  float16v acc[NT], D[NT];
+#pragma unroll
+  for (int n = 0; n < NT; n++) acc[n] = (float16v){}, D[n] = (float16v){};
+  float s_pend[NT];
+#pragma unroll
+  for (int n = 0; n < NT; n++) s_pend[n] = 0.f;
+  const float16v zero16 = (float16v){};
+  const int sb = 127;  // weight scale 2^0
+
+  int8v A[3];
+  uint32_t sa;
+#pragma unroll
+  for (int d = 0; d < 3; d++) A[d] = a_load(kg0, 0, d);
+  sa = s_load(kg0, 0);
+  {
+    Meta m0;
+    load_meta(kg0, m0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) dequant_quarter(kg0, m0, 0, j);
+  }
+  __syncthreads();
+
+  for (int kg = kg0; kg < kg1; kg++) {
+    const int buf = (kg - kg0) & 1;
+    const int kgn = min(kg + 1, kg1 - 1);  // next k group (clamped)
+    Meta mnext;
+    load_meta(kgn, mnext);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+      int8v B[NT];
+#pragma unroll
+      for (int n = 0; n < NT; n++) B[n] = b_load(buf, n, st);
+      // The fragments of the step after this one: this k group's step 1, or
+      // the next k group's step 0 (re-read on the last k group, unused).
+      const int nkg = st == 0 ? kg : kgn, nst = st ^ 1;
+#pragma unroll
+      for (int d = 0; d < 3; d++) {
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+          if (st == 0 && d == 0) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
+          }
+          const float16v cin = (st == 0 && d == 0) ? zero16 : D[n];
+          D[n] = d == 0   ? mfma_digit<0>(A[0], B[n], cin, (int)sa, sb)
+                 : d == 1 ? mfma_digit<1>(A[1], B[n], cin, (int)sa, sb)
+                          : mfma_digit<2>(A[2], B[n], cin, (int)sa, sb);
+        }
+        A[d] = a_load(nkg, nst, d);
+        if (d == 2) sa = s_load(nkg, nst);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // The next k group's weights, two quarters per step.
+      dequant_quarter(kgn, mnext, buf ^ 1, 2 * st);
+      dequant_quarter(kgn, mnext, buf ^ 1, 2 * st + 1);
+    }
+#pragma unroll
+    for (int n = 0; n < NT; n++) s_pend[n] = scl[buf][lc][n];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int n = 0; n < NT; n++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
+
+  // Epilogue: stage the wave's 32 x TC tile row-major in LDS (free now: every
+  // wave passed the last barrier), then write 16-byte row pieces.
+  float *stage = reinterpret_cast<float *>(lds) + wave * (32 * TC);
+  const int lh = lane >> 5;
+#pragma unroll
+  for (int n = 0; n < NT; n++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int r = 8 * (v >> 2) + 4 * lh + (v & 3);
+      stage[r * TC + n * 32 + lc] = acc[n][v];
+    }
+  __syncthreads();
+  // Rows of this wave's tile with a non-finite activation in this launch's
+  // k range get the reference's Inf / NaN pattern (rare: a uniform branch).
+  {
+    int flag = 0;
+    if (lane < 32 && m32 * 32 + lane < M) {
+      const uint32_t *nfw = reinterpret_cast<const uint32_t *>(nf) + (int64_t)(m32 * 32 + lane) * c4n;
+      for (int kg = kg0; kg < kg1; kg++) flag |= nfw[kg] != 0u;
+    }
+    uint64_t rows = __ballot(flag);
+    const int klo = kg0 * KGRP;
+    const int64_t khi = min((int64_t)kg1 * KGRP, K);
+    while (rows) {
+      const int r = __builtin_ctzll(rows);
+      rows &= rows - 1;
+      const float *arow = a + (int64_t)(m32 * 32 + r) * K;
+      bool fnan[2] = {false, false}, fpos[2] = {false, false}, fneg[2] = {false, false};
+      for (int64_t k0 = klo; k0 < khi; k0 += 64) {
+        const float x = k0 + lane < khi ? arow[k0 + lane] : 0.f;
+        uint64_t m = __ballot(!isfinite(x));
+        while (m) {
+          const int b = __builtin_ctzll(m);
+          m &= m - 1;
+          const float xv = __shfl(x, b);
+#pragma unroll
+          for (int u = 0; u < 2; u++) {
+            const int c = lane + 64 * u;
+            const int col = nt * TC + c;
+            if (c >= TC || col >= N) continue;
+            const float wv = nbits_weight(wq, scales, zp4, c4n, nb, nbh, lbs, has_zp, col,
+                                          (int)(k0 + b));
+            if (isnan(xv) || !(wv != 0.f)) fnan[u] = true;
+            else if ((xv > 0.f) == (wv > 0.f)) fpos[u] = true;
+            else fneg[u] = true;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int c = lane + 64 * u;
+        if (c >= TC || !(fnan[u] || fpos[u] || fneg[u])) continue;
+        stage[r * TC + c] = (fnan[u] || (fpos[u] && fneg[u])) ? __builtin_nanf("")
+                            : fpos[u] ? INFINITY : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+  const bool split = gridDim.y > 1;
+  float *dst = split ? part + ps.part_off[mem] + (int64_t)ks * M * N : ps.y[mem];
+  constexpr int PPR = 8 * NT, RPI = 64 / PPR;  // pieces per row, rows per iteration
+  const int c4 = lane % PPR, ro = lane / PPR;
+  const int col = nt * TC + 4 * c4;
+  float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!split && bias) {
+    if (col + 3 < N) {
+      bv = make_float4(bias[col], bias[col + 1], bias[col + 2], bias[col + 3]);
+    } else {
+      if (col < N) bv.x = bias[col];
+      if (col + 1 < N) bv.y = bias[col + 1];
+      if (col + 2 < N) bv.z = bias[col + 2];
+    }
+  }
+  const bool vec_ok = (N % 4) == 0 && (split || ps.y_vec[mem]);
+#pragma unroll 4
+  for (int it = 0; it < 32 / RPI; it++) {
+    const int r = RPI * it + ro;
+    const int row = m32 * 32 + r;
+    float4v v = *reinterpret_cast<const float4v *>(&stage[r * TC + 4 * c4]);
+    v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
+    if (row < M) {
+      float *p = dst + (int64_t)row * N + col;
+      if (vec_ok && col + 3 < N) {
+        __builtin_nontemporal_store(v, reinterpret_cast<float4v *>(p));
+      } else {
+        if (col < N) p[0] = v[0];
+        if (col + 1 < N) p[1] = v[1];
+        if (col + 2 < N) p[2] = v[2];
+        if (col + 3 < N) p[3] = v[3];
+      }
+    }
+  }
+}
+
+}  // namespace
+
+size_t mg_nbits_f8_ws(int64_t mpad, int64_t c4, size_t *off_asc, size_t *off_nf) {
+  const size_t aq = (size_t)mpad * c4 * 128 * 3;  // 3 bytes per element
+  *off_asc = mg_align(aq);
+  *off_nf = mg_align(*off_asc + (size_t)mpad * c4 * 16);  // 4 scale words per 128 k per row
+  return mg_align(*off_nf + (size_t)mpad * c4 * 4);
+}
+
+mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, const float *a_dev,
+                              int64_t M, float *const *y_dev, void *ws, int64_t mpad, int nt,
+                              int ksplit, int kps, size_t off_part) {
+  const mg_weight *w0 = w[0];
+  const mg_nbits_dev &d = w0->nbits;
+  hipStream_t st = ctx->stream;
+  char *base = static_cast<char *>(ws);
+  size_t off_asc = 0, off_nf = 0;
+  (void)mg_nbits_f8_ws(mpad, d.c4, &off_asc, &off_nf);
+  uint4 *aq = reinterpret_cast<uint4 *>(base);
+  uint32_t *asc = reinterpret_cast<uint32_t *>(base + off_asc);
+  uint8_t *nf = reinterpret_cast<uint8_t *>(base + off_nf);
+  float *part = ksplit > 1 ? reinterpret_cast<float *>(base + off_part) : nullptr;
+  const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
+  const int64_t nwaves = (mpad / 32) * d.c4 * 2;
+  hipLaunchKernelGGL(k_af8x3, dim3((unsigned)((nwaves + 3) / 4)), dim3(256), 0, st, a_dev, M,
+                     w0->K, (int)d.c4, vec, nwaves, aq, asc, nf);
+  MG_TRY(mg_launch_check("k_af8x3"));
+  const int has_zp = d.zp_kind == MG_ZP_UINT4;
+  PrefillSet ps{};
+  ReduceSet rs{};
+  int ct = 0;
+  int64_t eend = 0;
+  make_prefill_sets(n, w, y_dev, M, ksplit, nt, &ps, &rs, &ct, &eend);
+  const int mtiles = (int)(mpad / 128);
+  const dim3 grid((unsigned)(8 * mtiles * ((ct + 7) / 8)), (unsigned)ksplit);
+  if (nt == 4)
+    hipLaunchKernelGGL((k_gemm_f8x3<4>), grid, dim3(256), 0, st, aq, asc, nf, a_dev, w0->K, ps,
+                       part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs),
+                       has_zp, mtiles, ct, kps);
+  else
+    hipLaunchKernelGGL((k_gemm_f8x3<2>), grid, dim3(256), 0, st, aq, asc, nf, a_dev, w0->K, ps,
+                       part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs),
+                       has_zp, mtiles, ct, kps);
+  MG_TRY(mg_launch_check("k_gemm_f8x3"));
+  if (ksplit > 1) MG_TRY(launch_gemm_reduce(st, part, rs, eend, ksplit));
+  return MG_OK;
+}
