@@ -160,6 +160,21 @@ mg_status mg_matmul_nbits(mg_ctx *ctx, const mg_weight *w, const float *a,
 mg_status mg_matmul_nbits_dev(mg_ctx *ctx, const mg_weight *w,
                               const float *a_dev, int64_t M, float *y_dev);
 
+/* mg_matmul_nbits_dev without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Results are those of mg_matmul_nbits_dev.  The kernels' workspace
+ * (activation prepasses, split-K partial sums) is a static per-device scratch
+ * array of MG_NOALLOC_SCRATCH_BYTES bytes, held by each GPU the library runs
+ * on until the process ends; a call that would need more fails with
+ * MG_INVALID_ARGUMENT before launching anything.  Every call on one GPU uses
+ * that GPU's array: calls that overlap on one GPU (several contexts or
+ * streams in flight at once) race. */
+#define MG_NOALLOC_SCRATCH_BYTES (32u << 20)
+mg_status mg_matmul_nbits_dev_noalloc(mg_ctx *ctx, const mg_weight *w,
+                                      const float *a_dev, int64_t M,
+                                      float *y_dev);
+
 /* Several MatMulNBits nodes that read the same activations (a decoder layer's
  * q/k/v or gate/up projections): y_dev[i] = opMatMulNBits(a, W_i) for
  * 1 <= n <= 4 weights sharing K, block_size, zero-point form and device, each

@@ -40,6 +40,7 @@ SIGNATURES = {
                                _I32, _P, _P, _I32, _P, _P, _I32, _I32, _PP],
     "mg_matmul_nbits": [_P, _P, _P, _I64, _P],
     "mg_matmul_nbits_dev": [_P, _P, _P, _I64, _P],
+    "mg_matmul_nbits_dev_noalloc": [_P, _P, _P, _I64, _P],
     "mg_matmul_nbits_group_dev": [_P, _I32, _P, _P, _I64, _P],
     "mg_weight_int8_create": [_P, _P, _I32, _I64, _I64, _P, _I64, _PP],
     "mg_matmul_integer": [_P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I64, _P, _I64, _P],

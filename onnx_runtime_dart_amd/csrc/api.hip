@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -23,6 +24,13 @@ mg_status mg_int8_run_batched(mg_ctx *ctx, const void *a_dev, int32_t a_signed,
                               void *y_dev, void *ws);
 size_t mg_int8_batched_ws_bytes(int64_t a_batch, int64_t b_batch, int64_t M,
                                 int64_t K, int64_t N);
+
+// Workspace of mg_matmul_nbits_dev_noalloc: one array per device, held by
+// each GPU the library runs on until the process ends.  In host code the name
+// `scratch` is a host-side stand-in, not a device address: the device address
+// is taken with hipGetSymbolAddress once per device (scratch_init, with that
+// device current) and only that address is used.
+static __device__ __align__(256) unsigned char scratch[MG_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 thread_local std::string g_last_error;
@@ -86,6 +94,32 @@ mg_status mg_check_control(mg_ctx *ctx, int64_t additional_bytes) {
   }
   return MG_OK;
 }
+
+namespace {
+constexpr int MG_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_dev[MG_MAX_DEVICES] = {};
+
+// With `device` current: records the device address of `scratch` on it.
+mg_status scratch_init(int device) {
+  if (device < 0 || device >= MG_MAX_DEVICES)
+    return mg_fail(MG_UNSUPPORTED, "device index beyond " + std::to_string(MG_MAX_DEVICES));
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_dev[device]) return MG_OK;
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return mg_fail(MG_DEVICE_ERROR,
+                   std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+  g_scratch_dev[device] = p;
+  return MG_OK;
+}
+
+void *scratch_dev(int device) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return device >= 0 && device < MG_MAX_DEVICES ? g_scratch_dev[device] : nullptr;
+}
+}  // namespace
 
 mg_status mg_ws_reserve(mg_ctx *ctx, size_t bytes) {
   if (bytes <= ctx->ws_bytes) return MG_OK;
@@ -161,6 +195,12 @@ mg_status mg_ctx_create(int32_t device, mg_ctx **out) {
     return mg_fail(MG_DEVICE_ERROR, std::string("hipStreamCreate: ") + hipGetErrorString(e));
   }
   c->own_stream = true;
+  const mg_status ss = scratch_init(device);
+  if (ss != MG_OK) {
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return ss;
+  }
   *out = c;
   return MG_OK;
 }
@@ -469,6 +509,27 @@ mg_status mg_matmul_nbits_dev(mg_ctx *ctx, const mg_weight *w, const float *a_de
   MG_TRY(mg_check_control(ctx, (int64_t)ws));
   MG_TRY(mg_ws_reserve(ctx, ws));
   return mg_nbits_run(ctx, w, a_dev, M, y_dev, ctx->ws);
+}
+
+mg_status mg_matmul_nbits_dev_noalloc(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
+                                      int64_t M, float *y_dev) {
+  g_last_error.clear();
+  if (!ctx || !w || w->kind != MG_W_NBITS)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits: not a MatMulNBits weight");
+  if (M < 0) return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid K, N, block_size or input shape");
+  if (M == 0) return MG_OK;
+  if (!a_dev || !y_dev) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits: null buffer");
+  const size_t ws = mg_nbits_ws_bytes(ctx, w, M);
+  if (ws > (size_t)MG_NOALLOC_SCRATCH_BYTES)
+    return mg_fail(MG_INVALID_ARGUMENT,
+                   "mg_matmul_nbits_dev_noalloc: " + std::to_string(M) + " rows need " +
+                       std::to_string(ws) + " bytes of workspace, the scratch holds " +
+                       std::to_string((size_t)MG_NOALLOC_SCRATCH_BYTES));
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, 0));
+  void *s = scratch_dev(ctx->device);
+  if (!s) return mg_fail(MG_DEVICE_ERROR, "mg_matmul_nbits_dev_noalloc: no scratch on this device");
+  return mg_nbits_run(ctx, w, a_dev, M, y_dev, s);
 }
 
 mg_status mg_matmul_nbits_group_dev(mg_ctx *ctx, int32_t n, const mg_weight *const *w,

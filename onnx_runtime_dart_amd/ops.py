@@ -247,6 +247,12 @@ class NBitsWeight(_Weight):
         check(lib.mg_matmul_nbits_dev(self.ctx.handle, self.handle, C.c_void_p(a_ptr), m,
                                       C.c_void_p(y_ptr)))
 
+    def run_dev_noalloc(self, a_ptr: int, m: int, y_ptr: int):
+        """run_dev without allocating: the workspace is the library's static
+        per-device scratch (calls overlapping on one GPU race)."""
+        check(lib.mg_matmul_nbits_dev_noalloc(self.ctx.handle, self.handle, C.c_void_p(a_ptr),
+                                              m, C.c_void_p(y_ptr)))
+
 
 def matmul_nbits_group_dev(weights, a_ptr: int, m: int, y_ptrs, ctx: Context | None = None):
     """Several NBitsWeight sharing K, block size and zero-point form applied to
