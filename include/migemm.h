@@ -82,6 +82,18 @@ mg_status mg_ctx_set_stream(mg_ctx *ctx, void *hip_stream);
 mg_status mg_ctx_get_stream(mg_ctx *ctx, void **hip_stream);
 mg_status mg_ctx_synchronize(mg_ctx *ctx);
 
+/* Per-op device timing, the ABI's part of ExecutionProfile
+ * (lib/src/onnx_graph.dart:27-86: per-node times by op type).  While enabled,
+ * every op entry point records HIP events on the context's stream around its
+ * work, in issue order; mg_ctx_profile_get waits for record i and returns its
+ * op type ("MatMulNBits", "Gemm", ..., "<op>.upload" for weight creation) and
+ * device milliseconds (host-pointer ops include their transfers).  Enabling or
+ * clearing discards the records (after waiting for the stream). */
+mg_status mg_ctx_set_profiling(mg_ctx *ctx, int32_t enable);
+mg_status mg_ctx_profile_count(mg_ctx *ctx, int64_t *n);
+mg_status mg_ctx_profile_get(mg_ctx *ctx, int64_t i, const char **op, float *ms);
+mg_status mg_ctx_profile_clear(mg_ctx *ctx);
+
 /* Cooperative cancellation and byte budget, checked before every launch
  * (lib/src/execution_control.dart:43-57: checkpoint / checkAdditionalBytes).
  * `cancel_flag` (may be NULL) is polled: non-zero => MG_CANCELLED.

@@ -32,6 +32,10 @@ SIGNATURES = {
     "mg_ctx_get_stream": [_P, _PP],
     "mg_ctx_synchronize": [_P],
     "mg_ctx_set_control": [_P, _P, _I64],
+    "mg_ctx_set_profiling": [_P, _I32],
+    "mg_ctx_profile_count": [_P, _P],
+    "mg_ctx_profile_get": [_P, _I64, _P, _P],
+    "mg_ctx_profile_clear": [_P],
     "mg_buffer_alloc": [_P, _SZ, _PP],
     "mg_buffer_free": [_P, _P],
     "mg_buffer_upload": [_P, _P, _P, _SZ],

@@ -121,6 +121,33 @@ void *scratch_dev(int device) {
 }
 }  // namespace
 
+ProfScope::ProfScope(mg_ctx *ctx, const char *op) : ctx_(ctx), op_(op) {
+  if (!ctx_ || !ctx_->prof) {
+    ctx_ = nullptr;
+    return;
+  }
+  e0_ = prof_event(ctx_);
+  if (!e0_ || hipEventRecord(e0_, ctx_->stream) != hipSuccess) ctx_ = nullptr;
+}
+
+ProfScope::~ProfScope() {
+  if (!ctx_) return;
+  hipEvent_t e1 = prof_event(ctx_);
+  if (e1 && hipEventRecord(e1, ctx_->stream) == hipSuccess)
+    ctx_->prof_recs.push_back({op_, e0_, e1});
+}
+
+hipEvent_t prof_event(mg_ctx *ctx) {
+  if (!ctx->prof_pool.empty()) {
+    hipEvent_t e = ctx->prof_pool.back();
+    ctx->prof_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
 mg_status mg_ws_reserve(mg_ctx *ctx, size_t bytes) {
   if (bytes <= ctx->ws_bytes) return MG_OK;
   if (ctx->ws) {
@@ -212,6 +239,11 @@ mg_status mg_ctx_destroy(mg_ctx *ctx) {
   if (ctx->ws) (void)hipFree(ctx->ws);
   for (int i = 0; i < MG_PIN_SLOTS; i++)
     if (ctx->pin_ev[i]) (void)hipEventDestroy(ctx->pin_ev[i]);
+  for (const mg_prof_rec &r : ctx->prof_recs) {
+    (void)hipEventDestroy(r.e0);
+    (void)hipEventDestroy(r.e1);
+  }
+  for (hipEvent_t e : ctx->prof_pool) (void)hipEventDestroy(e);
   if (ctx->pin) (void)hipHostFree(ctx->pin);
   if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -231,6 +263,41 @@ mg_status mg_ctx_set_stream(mg_ctx *ctx, void *hip_stream) {
 mg_status mg_ctx_get_stream(mg_ctx *ctx, void **hip_stream) {
   if (!ctx || !hip_stream) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_get_stream: null argument");
   *hip_stream = ctx->stream;
+  return MG_OK;
+}
+
+mg_status mg_ctx_set_profiling(mg_ctx *ctx, int32_t enable) {
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_set_profiling: null context");
+  MG_TRY(mg_ctx_profile_clear(ctx));
+  ctx->prof = enable != 0;
+  return MG_OK;
+}
+
+mg_status mg_ctx_profile_count(mg_ctx *ctx, int64_t *n) {
+  if (!ctx || !n) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_profile_count: null argument");
+  *n = (int64_t)ctx->prof_recs.size();
+  return MG_OK;
+}
+
+mg_status mg_ctx_profile_get(mg_ctx *ctx, int64_t i, const char **op, float *ms) {
+  if (!ctx || !op || !ms) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_profile_get: null argument");
+  if (i < 0 || i >= (int64_t)ctx->prof_recs.size())
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_profile_get: record index out of range");
+  const mg_prof_rec &r = ctx->prof_recs[(size_t)i];
+  MG_HIP(hipEventSynchronize(r.e1));
+  MG_HIP(hipEventElapsedTime(ms, r.e0, r.e1));
+  *op = r.op;
+  return MG_OK;
+}
+
+mg_status mg_ctx_profile_clear(mg_ctx *ctx) {
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_profile_clear: null context");
+  if (!ctx->prof_recs.empty()) MG_HIP(hipStreamSynchronize(ctx->stream));
+  for (const mg_prof_rec &r : ctx->prof_recs) {
+    ctx->prof_pool.push_back(r.e0);
+    ctx->prof_pool.push_back(r.e1);
+  }
+  ctx->prof_recs.clear();
   return MG_OK;
 }
 
@@ -315,6 +382,7 @@ mg_status mg_weight_nbits_create(
     int32_t zp_kind, const void *zp, const int64_t *zp_shape, int32_t zp_rank,
     const float *bias, const int64_t *bias_shape, int32_t bias_rank,
     int32_t has_g_idx, mg_weight **out) {
+  ProfScope prof_(ctx, "MatMulNBits.upload");
   g_last_error.clear();
   if (!ctx || !out) return mg_fail(MG_INVALID_ARGUMENT, "mg_weight_nbits_create: null argument");
   *out = nullptr;
@@ -374,6 +442,7 @@ mg_status mg_weight_nbits_create_streamed(mg_ctx *ctx, int64_t K, int64_t N, int
                                           const mg_tensor_source *zp, const float *bias,
                                           int32_t has_g_idx, int64_t chunk_bytes,
                                           mg_weight **out) {
+  ProfScope prof_(ctx, "MatMulNBits.upload");
   g_last_error.clear();
   if (!ctx || !out || !b || !scales)
     return mg_fail(MG_INVALID_ARGUMENT, "mg_weight_nbits_create_streamed: null argument");
@@ -429,6 +498,7 @@ mg_status mg_weight_nbits_create_streamed(mg_ctx *ctx, int64_t K, int64_t N, int
 mg_status mg_weight_int8_create(mg_ctx *ctx, const void *b, int32_t b_signed, int64_t K,
                                 int64_t N, const int32_t *b_zp, int64_t b_zp_len,
                                 mg_weight **out) {
+  ProfScope prof_(ctx, "MatMulInteger.upload");
   g_last_error.clear();
   if (!ctx || !out || (!b && K * N > 0))
     return mg_fail(MG_INVALID_ARGUMENT, "mg_weight_int8_create: null argument");
@@ -455,6 +525,7 @@ mg_status mg_weight_int8_create(mg_ctx *ctx, const void *b, int32_t b_signed, in
 
 mg_status mg_weight_f32_create(mg_ctx *ctx, const float *b, int64_t rows, int64_t cols,
                                int32_t trans_b, mg_weight **out) {
+  ProfScope prof_(ctx, "Gemm.upload");
   g_last_error.clear();
   if (!ctx || !out || (!b && rows * cols > 0))
     return mg_fail(MG_INVALID_ARGUMENT, "mg_weight_f32_create: null argument");
@@ -498,6 +569,7 @@ mg_status mg_weight_f32_create(mg_ctx *ctx, const float *b, int64_t rows, int64_
 
 mg_status mg_matmul_nbits_dev(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
                               float *y_dev) {
+  ProfScope prof_(ctx, "MatMulNBits");
   g_last_error.clear();
   if (!ctx || !w || w->kind != MG_W_NBITS)
     return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits: not a MatMulNBits weight");
@@ -534,6 +606,7 @@ mg_status mg_matmul_nbits_dev_noalloc(mg_ctx *ctx, const mg_weight *w, const flo
 
 mg_status mg_matmul_nbits_group_dev(mg_ctx *ctx, int32_t n, const mg_weight *const *w,
                                     const float *a_dev, int64_t M, float *const *y_dev) {
+  ProfScope prof_(ctx, "MatMulNBits");
   g_last_error.clear();
   if (!ctx || !w || !y_dev || n < 1 || n > 4)
     return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits_group_dev: 1 to 4 weights expected");
@@ -558,6 +631,7 @@ mg_status mg_matmul_nbits_group_dev(mg_ctx *ctx, int32_t n, const mg_weight *con
 }
 
 mg_status mg_matmul_nbits(mg_ctx *ctx, const mg_weight *w, const float *a, int64_t M, float *y) {
+  ProfScope prof_(ctx, "MatMulNBits");
   g_last_error.clear();
   if (!ctx || !w || w->kind != MG_W_NBITS)
     return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits: not a MatMulNBits weight");
@@ -709,6 +783,7 @@ mg_status mg_matmul_integer(mg_ctx *ctx, const void *a, int32_t a_signed, const 
                             const int64_t *b_shape, int32_t b_rank, const int32_t *a_zp,
                             int64_t a_zp_len, const int32_t *b_zp, int64_t b_zp_len,
                             int32_t *y) {
+  ProfScope prof_(ctx, "MatMulInteger");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer: null context");
   return integer_host(ctx, a, a_signed, a_shape, a_rank, a_zp, a_zp_len, b, b_signed, b_shape,
@@ -718,6 +793,7 @@ mg_status mg_matmul_integer(mg_ctx *ctx, const void *a, int32_t a_signed, const 
 mg_status mg_matmul_integer_w(mg_ctx *ctx, const void *a, int32_t a_signed, int64_t rows,
                               int64_t K, const int32_t *a_zp, int64_t a_zp_len,
                               const mg_weight *w, int32_t *y) {
+  ProfScope prof_(ctx, "MatMulInteger");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer_w: null context");
   return integer_w(ctx, a, false, a_signed, rows, K, a_zp, a_zp_len, w, nullptr, y, false);
@@ -726,6 +802,7 @@ mg_status mg_matmul_integer_w(mg_ctx *ctx, const void *a, int32_t a_signed, int6
 mg_status mg_matmul_integer_w_dev(mg_ctx *ctx, const void *a_dev, int32_t a_signed, int64_t rows,
                                   int64_t K, const int32_t *a_zp, int64_t a_zp_len,
                                   const mg_weight *w, int32_t *y_dev) {
+  ProfScope prof_(ctx, "MatMulInteger");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer_w_dev: null context");
   return integer_w(ctx, a_dev, true, a_signed, rows, K, a_zp, a_zp_len, w, nullptr, y_dev, true);
@@ -737,6 +814,7 @@ mg_status mg_qlinear_matmul(mg_ctx *ctx, const void *a, int32_t a_signed, const 
                             int32_t b_rank, float b_scale, const int32_t *b_zp,
                             int64_t b_zp_len, float y_scale, int32_t y_zp, int32_t lo,
                             int32_t hi, void *y) {
+  ProfScope prof_(ctx, "QLinearMatMul");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_matmul: null context");
   mg_requant rq;
@@ -749,6 +827,7 @@ mg_status mg_qlinear_matmul_w(mg_ctx *ctx, const void *a, int32_t a_signed, int6
                               int64_t K, float a_scale, const int32_t *a_zp, int64_t a_zp_len,
                               const mg_weight *w, float b_scale, float y_scale, int32_t y_zp,
                               int32_t lo, int32_t hi, void *y) {
+  ProfScope prof_(ctx, "QLinearMatMul");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_matmul_w: null context");
   mg_requant rq;
@@ -761,6 +840,7 @@ mg_status mg_qlinear_matmul_w_dev(mg_ctx *ctx, const void *a_dev, int32_t a_sign
                                   int64_t a_zp_len, const mg_weight *w, float b_scale,
                                   float y_scale, int32_t y_zp, int32_t lo, int32_t hi,
                                   void *y_dev) {
+  ProfScope prof_(ctx, "QLinearMatMul");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_matmul_w_dev: null context");
   mg_requant rq;
@@ -774,6 +854,7 @@ mg_status mg_qlinear_matmul_w_dev(mg_ctx *ctx, const void *a_dev, int32_t a_sign
 mg_status mg_matmul_integer_w_dq_dev(mg_ctx *ctx, const uint8_t *a_dev, int64_t rows, int64_t K,
                                      const void *a_scale_zp_dev, const mg_weight *w,
                                      int32_t *y_dev) {
+  ProfScope prof_(ctx, "MatMulInteger");
   g_last_error.clear();
   if (!ctx || !a_scale_zp_dev)
     return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer_w_dq_dev: null context or scale/zp");
@@ -787,6 +868,7 @@ mg_status mg_qlinear_matmul_w_dq_dev(mg_ctx *ctx, const uint8_t *a_dev, int64_t 
                                      const void *a_scale_zp_dev, const mg_weight *w,
                                      float b_scale, float y_scale, int32_t y_zp, int32_t lo,
                                      int32_t hi, void *y_dev) {
+  ProfScope prof_(ctx, "QLinearMatMul");
   g_last_error.clear();
   if (!ctx || !a_scale_zp_dev)
     return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_matmul_w_dq_dev: null context or scale/zp");
@@ -803,6 +885,7 @@ mg_status mg_qlinear_matmul_w_dq_dev(mg_ctx *ctx, const uint8_t *a_dev, int64_t 
 
 mg_status mg_dynamic_quantize_linear_dev(mg_ctx *ctx, const float *x_dev, int64_t n,
                                          uint8_t *y_dev, void *scale_zp_dev) {
+  ProfScope prof_(ctx, "DynamicQuantizeLinear");
   g_last_error.clear();
   if (!ctx || n < 0 || (n > 0 && (!x_dev || !y_dev)) || !scale_zp_dev)
     return mg_fail(MG_INVALID_ARGUMENT, "mg_dynamic_quantize_linear: invalid argument");
@@ -815,6 +898,7 @@ mg_status mg_dynamic_quantize_linear_dev(mg_ctx *ctx, const float *x_dev, int64_
 
 mg_status mg_dynamic_quantize_linear(mg_ctx *ctx, const float *x, int64_t n, uint8_t *y,
                                      float *scale, int32_t *zp) {
+  ProfScope prof_(ctx, "DynamicQuantizeLinear");
   g_last_error.clear();
   if (!ctx || n < 0 || (n > 0 && (!x || !y)) || !scale || !zp)
     return mg_fail(MG_INVALID_ARGUMENT, "mg_dynamic_quantize_linear: invalid argument");
@@ -1025,6 +1109,7 @@ mg_status mg_matmul_f32_batch_offsets(const int64_t *a_shape, int32_t a_rank,
 
 mg_status mg_matmul_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape, int32_t a_rank,
                         const float *b, const int64_t *b_shape, int32_t b_rank, float *y) {
+  ProfScope prof_(ctx, "MatMul");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_f32: null context");
   F32Batch p;
@@ -1051,6 +1136,7 @@ mg_status mg_matmul_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape, int
 mg_status mg_matmul_f32_dev(mg_ctx *ctx, const float *a_dev, const int64_t *a_shape,
                             int32_t a_rank, const float *b_dev, const int64_t *b_shape,
                             int32_t b_rank, float *y_dev) {
+  ProfScope prof_(ctx, "MatMul");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_f32_dev: null context");
   F32Batch p;
@@ -1068,6 +1154,7 @@ mg_status mg_gemm_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape, const
                       const int64_t *b_shape, int32_t trans_a, int32_t trans_b, float alpha,
                       float beta, const float *c, const int64_t *c_shape, int32_t c_rank,
                       float *y) {
+  ProfScope prof_(ctx, "Gemm");
   g_last_error.clear();
   if (!ctx || !a_shape || !b_shape) return mg_fail(MG_INVALID_ARGUMENT, "mg_gemm_f32: null argument");
   if (!shape_ok(a_shape, 2) || !shape_ok(b_shape, 2))
@@ -1175,6 +1262,7 @@ mg_status gemm_w(mg_ctx *ctx, const float *a, bool a_dev_ptr, int64_t rows, int6
 mg_status mg_gemm_f32_w(mg_ctx *ctx, const float *a, int64_t rows, int64_t K, const mg_weight *w,
                         float alpha, float beta, const float *c, const int64_t *c_shape,
                         int32_t c_rank, float *y) {
+  ProfScope prof_(ctx, "Gemm");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_gemm_f32_w: null context");
   return gemm_w(ctx, a, false, rows, K, w, alpha, beta, c, false, c_shape, c_rank, y, false);
@@ -1183,6 +1271,7 @@ mg_status mg_gemm_f32_w(mg_ctx *ctx, const float *a, int64_t rows, int64_t K, co
 mg_status mg_gemm_f32_w_dev(mg_ctx *ctx, const float *a_dev, int64_t rows, int64_t K,
                             const mg_weight *w, float alpha, float beta, const float *c_dev,
                             const int64_t *c_shape, int32_t c_rank, float *y_dev) {
+  ProfScope prof_(ctx, "Gemm");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_gemm_f32_w_dev: null context");
   return gemm_w(ctx, a_dev, true, rows, K, w, alpha, beta, c_dev, true, c_shape, c_rank, y_dev,
@@ -1382,6 +1471,7 @@ mg_status mg_fused_sdpa(mg_ctx *ctx, const float *a, const int64_t *a_shape, int
                         const float *b, const int64_t *b_shape, int32_t b_rank, const float *v,
                         const int64_t *v_shape, int32_t v_rank, const float *mask,
                         const int64_t *mask_shape, int32_t mask_rank, float scale, float *y) {
+  ProfScope prof_(ctx, "_FusedSDPA");
   g_last_error.clear();
   if (!ctx || !mask) return mg_fail(MG_INVALID_ARGUMENT, "mg_fused_sdpa: null context or mask");
   mg_attn_problem p;
@@ -1397,6 +1487,7 @@ mg_status mg_fused_sdpa_dev(mg_ctx *ctx, const float *a_dev, const int64_t *a_sh
                             int32_t b_rank, const float *v_dev, const int64_t *v_shape,
                             int32_t v_rank, const float *mask_dev, const int64_t *mask_shape,
                             int32_t mask_rank, float scale, float *y_dev) {
+  ProfScope prof_(ctx, "_FusedSDPA");
   g_last_error.clear();
   if (!ctx || !mask_dev)
     return mg_fail(MG_INVALID_ARGUMENT, "mg_fused_sdpa_dev: null context or mask");
@@ -1424,6 +1515,7 @@ mg_status mg_multi_head_attention(mg_ctx *ctx, const float *q, const float *k, c
                                   int64_t batch, int64_t seq, int64_t kv_seq, int64_t hidden,
                                   int32_t num_heads, const float *bias, int32_t bias_heads,
                                   int32_t has_scale, float scale, float *y) {
+  ProfScope prof_(ctx, "MultiHeadAttention");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_multi_head_attention: null context");
   mg_attn_problem p;
@@ -1440,6 +1532,7 @@ mg_status mg_multi_head_attention_dev(mg_ctx *ctx, const float *q_dev, const flo
                                       int64_t kv_seq, int64_t hidden, int32_t num_heads,
                                       const float *bias_dev, int32_t bias_heads,
                                       int32_t has_scale, float scale, float *y_dev) {
+  ProfScope prof_(ctx, "MultiHeadAttention");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_multi_head_attention_dev: null context");
   mg_attn_problem p;
@@ -1740,6 +1833,7 @@ mg_status mg_conv_f32(mg_ctx *ctx, const float *x, const int64_t *x_shape, int32
                       const float *w, const int64_t *w_shape, const float *bias,
                       const int64_t *strides, const int64_t *pads, const int64_t *dilations,
                       int32_t group, int32_t auto_pad, float *y) {
+  ProfScope prof_(ctx, "Conv");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_f32: null context");
   mg_conv_problem p;
@@ -1754,6 +1848,7 @@ mg_status mg_conv_f32_dev(mg_ctx *ctx, const float *x_dev, const int64_t *x_shap
                           const float *bias_dev, const int64_t *strides, const int64_t *pads,
                           const int64_t *dilations, int32_t group, int32_t auto_pad,
                           float *y_dev) {
+  ProfScope prof_(ctx, "Conv");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_f32_dev: null context");
   mg_conv_problem p;
@@ -1782,6 +1877,7 @@ mg_status mg_conv_transpose_f32(mg_ctx *ctx, const float *x, const int64_t *x_sh
                                 const int64_t *dilations, const int64_t *output_padding,
                                 const int64_t *output_shape, int32_t output_shape_len,
                                 int32_t group, float *y) {
+  ProfScope prof_(ctx, "ConvTranspose");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_transpose_f32: null context");
   mg_conv_problem p;
@@ -1797,6 +1893,7 @@ mg_status mg_conv_transpose_f32_dev(mg_ctx *ctx, const float *x_dev, const int64
                                     const int64_t *pads, const int64_t *dilations,
                                     const int64_t *output_padding, const int64_t *output_shape,
                                     int32_t output_shape_len, int32_t group, float *y_dev) {
+  ProfScope prof_(ctx, "ConvTranspose");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_transpose_f32_dev: null context");
   mg_conv_problem p;
@@ -1811,6 +1908,7 @@ mg_status mg_conv_integer(mg_ctx *ctx, const void *x, int32_t x_signed, const in
                           const int64_t *w_shape, int32_t x_zp, const int32_t *w_zp,
                           int64_t w_zp_len, const int64_t *strides, const int64_t *pads,
                           const int64_t *dilations, int32_t group, int32_t *y) {
+  ProfScope prof_(ctx, "ConvInteger");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_integer: null context");
   mg_conv_problem p;
@@ -1832,6 +1930,7 @@ mg_status mg_conv_integer_dev(mg_ctx *ctx, const void *x_dev, int32_t x_signed,
                               const int32_t *w_zp, int64_t w_zp_len, const int64_t *strides,
                               const int64_t *pads, const int64_t *dilations, int32_t group,
                               int32_t *y_dev) {
+  ProfScope prof_(ctx, "ConvInteger");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_conv_integer_dev: null context");
   mg_conv_problem p;
@@ -1854,6 +1953,7 @@ mg_status mg_qlinear_conv(mg_ctx *ctx, const void *x, int32_t x_signed, const in
                           float y_scale, int32_t y_zp, const int32_t *bias,
                           const int64_t *strides, const int64_t *pads, const int64_t *dilations,
                           int32_t group, int32_t lo, int32_t hi, uint8_t *y) {
+  ProfScope prof_(ctx, "QLinearConv");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_conv: null context");
   if (lo > hi) return mg_fail(MG_INVALID_ARGUMENT, "QLinearConv: lo > hi");
@@ -1881,6 +1981,7 @@ mg_status mg_qlinear_conv_dev(mg_ctx *ctx, const void *x_dev, int32_t x_signed,
                               int32_t y_zp, const int32_t *bias_dev, const int64_t *strides,
                               const int64_t *pads, const int64_t *dilations, int32_t group,
                               int32_t lo, int32_t hi, uint8_t *y_dev) {
+  ProfScope prof_(ctx, "QLinearConv");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_qlinear_conv_dev: null context");
   if (lo > hi) return mg_fail(MG_INVALID_ARGUMENT, "QLinearConv: lo > hi");
@@ -2025,6 +2126,7 @@ mg_status mg_group_query_attention(
     int64_t max_pos, int64_t half_rot, int32_t do_rotary, int32_t rotary_interleaved,
     const float *attention_bias, int32_t bias_heads, int32_t has_scale, float scale,
     float softcap, int32_t local_window, float *y, float *present_key, float *present_value) {
+  ProfScope prof_(ctx, "GroupQueryAttention");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_group_query_attention: null context");
   GqaArgs a{batch, seq, hidden, num_heads, kv_num_heads, past_len, max_pos, half_rot,
@@ -2097,6 +2199,7 @@ mg_status mg_group_query_attention_dev(
     int32_t do_rotary, int32_t rotary_interleaved, const float *attention_bias_dev,
     int32_t bias_heads, int32_t has_scale, float scale, float softcap, int32_t local_window,
     float *y_dev, float *present_key_dev, float *present_value_dev) {
+  ProfScope prof_(ctx, "GroupQueryAttention");
   g_last_error.clear();
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_group_query_attention_dev: null context");
   GqaArgs a{batch, seq, hidden, num_heads, kv_num_heads, past_len, max_pos, half_rot,

@@ -6,6 +6,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "../../include/migemm.h"
 
@@ -38,6 +39,12 @@ mg_status mg_fail(mg_status st, const std::string &msg);
 constexpr int MG_PIN_SLOTS = 16;
 constexpr size_t MG_PIN_SLOT_BYTES = 256 << 10;
 
+// One profiled op: its name and the events recorded around its work.
+struct mg_prof_rec {
+  const char *op;
+  hipEvent_t e0, e1;
+};
+
 struct mg_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -53,7 +60,29 @@ struct mg_ctx {
   void *pin = nullptr;  // MG_PIN_SLOTS * MG_PIN_SLOT_BYTES pinned host bytes
   hipEvent_t pin_ev[MG_PIN_SLOTS] = {};
   int pin_next = 0;
+  // Per-op device timing (mg_ctx_set_profiling): records in issue order and
+  // a pool of spare events.
+  bool prof = false;
+  std::vector<mg_prof_rec> prof_recs;
+  std::vector<hipEvent_t> prof_pool;
 };
+
+// Records events on the context's stream around one op's work when the
+// context profiles (constructed at the op's entry, destroyed at its return).
+class ProfScope {
+ public:
+  ProfScope(mg_ctx *ctx, const char *op);
+  ~ProfScope();
+  ProfScope(const ProfScope &) = delete;
+  ProfScope &operator=(const ProfScope &) = delete;
+
+ private:
+  mg_ctx *ctx_;
+  const char *op_;
+  hipEvent_t e0_ = nullptr;
+};
+// An event from the context's pool (or a new one); null on failure.
+hipEvent_t prof_event(mg_ctx *ctx);
 
 enum mg_weight_kind { MG_W_NBITS = 1, MG_W_INT8 = 2, MG_W_F32 = 3 };
 

@@ -80,6 +80,61 @@ class Context:
         self._cancel = cancel_flag
         check(lib.mg_ctx_set_control(self.handle, _ptr(cancel_flag), int(max_bytes)))
 
+    def set_profiling(self, enable: bool = True):
+        """Per-op device timing of the ops issued on this context (clears
+        the records)."""
+        check(lib.mg_ctx_set_profiling(self.handle, int(bool(enable))))
+
+    def profile_records(self) -> list:
+        """[(op type, device ms)] of the profiled ops, in issue order (waits
+        for them)."""
+        n = C.c_int64(0)
+        check(lib.mg_ctx_profile_count(self.handle, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            op, ms = C.c_char_p(), C.c_float(0.0)
+            check(lib.mg_ctx_profile_get(self.handle, i, C.byref(op), C.byref(ms)))
+            out.append((op.value.decode(), float(ms.value)))
+        return out
+
+    def profile_clear(self):
+        check(lib.mg_ctx_profile_clear(self.handle))
+
+
+class ExecutionProfile:
+    """Cumulative per-op-type device timing, as the reference's
+    ExecutionProfile keeps per-op wall time (lib/src/onnx_graph.dart:27-86):
+    calls_by_op, micros_by_op, per-record `nodes`, and the same report()."""
+
+    def __init__(self):
+        self.calls_by_op: dict = {}
+        self.micros_by_op: dict = {}
+        self.nodes: list = []
+
+    def add(self, ctx: Context, name: str = ""):
+        """Folds the context's records in and clears them."""
+        for op, ms in ctx.profile_records():
+            us = int(round(ms * 1000))
+            self.calls_by_op[op] = self.calls_by_op.get(op, 0) + 1
+            self.micros_by_op[op] = self.micros_by_op.get(op, 0) + us
+            self.nodes.append((name, op, us))
+        ctx.profile_clear()
+
+    @property
+    def total_micros(self) -> int:
+        return sum(self.micros_by_op.values())
+
+    def report(self) -> str:
+        ops = sorted(self.micros_by_op, key=lambda o: -self.micros_by_op[o])
+        total = self.total_micros
+        lines = [f"{'op':<22}{'calls':>7}{'ms':>10}{'share':>8}"]
+        for op in ops:
+            us = self.micros_by_op[op]
+            share = f"{us * 100 / total:.1f}%" if total else ""
+            lines.append(f"{op:<22}{self.calls_by_op[op]:>7}{us / 1000:>10.1f}{share:>8}")
+        lines.append(f"{'total':<29}{total / 1000:>10.1f}")
+        return "\n".join(lines)
+
 
 _tls = threading.local()
 

@@ -488,3 +488,34 @@ def test_persistent_gemv_group(ops):
     ad.free()
     for w in ws:
         w.release()
+
+
+def test_profiling_records_each_op(ops):
+    # Per-op device timing (the ABI's part of ExecutionProfile): one record
+    # per op entry, in issue order, with the reference's op-type names.
+    ctx = ops.Context(0)
+    rng = np.random.default_rng(21)
+    b, s, zp = make_nbits(rng, 256, 512, 128, "packed")
+    w = ops.NBitsWeight(b, s, zp, k=512, n=256, block_size=128, ctx=ctx)
+    a = rng.standard_normal((64, 512)).astype(np.float32)
+    y0 = w(a)  # not profiled
+    ctx.set_profiling(True)
+    y1 = w(a)
+    y2 = w(a[:1])
+    fw = ops.F32Weight(rng.standard_normal((32, 512)).astype(np.float32), trans_b=True, ctx=ctx)
+    fw.gemm(a)
+    recs = ctx.profile_records()
+    assert [op for op, _ in recs] == ["MatMulNBits", "MatMulNBits", "Gemm.upload", "Gemm"]
+    assert all(ms > 0 for _, ms in recs)
+    prof = ops.ExecutionProfile()
+    prof.add(ctx, "layer0")
+    assert prof.calls_by_op["MatMulNBits"] == 2 and ctx.profile_records() == []
+    assert "MatMulNBits" in prof.report()
+    ctx.set_profiling(False)
+    w(a)
+    assert ctx.profile_records() == []
+    np.testing.assert_array_equal(y1, y0)  # profiling changes no result
+    assert y2.shape == (1, 256)
+    fw.release()
+    w.release()
+    ctx.close()
