@@ -86,13 +86,37 @@ def make_weight(rng, k, n, bs=BLOCK, s_lo=0.002, s_hi=0.02):
     return b, s, zp
 
 
-def cpu_baseline(weights, rng, budget_s=30.0):
-    """Times the oracle (reference algorithm: 32-column dequantised tiles +
-    4x16 f32 GEMM, one thread) at M = 512 on a bounded sample: projections in
-    order, the lm_head on its first columns, until ~budget_s of CPU work."""
+def host_info():
+    """Host CPU model and the cores this process may use."""
+    model = "unknown"
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    return {"cpu_model": model, "cores_available": cores, "cpu_count": os.cpu_count()}
+
+
+def cpu_baseline(weights, rng, budget_s=12.0):
+    """The reference's CPU algorithms restated in C (the oracle), timed on
+    bounded samples of the benchmark's workloads:
+      int4 prefill  M = 512 MatMulNBits, 32-column dequantised tiles + the
+                    4x16 f32 kernel, one thread (the reference never pools
+                    MatMulNBits) -> `value`;
+      int4 GEMV     M = 1 MatMulNBits, the f64 per-column decode, one thread;
+      fp32 pool     the MiniLM-L6 Gemm set (config C3) on the GemmPool N-split
+                    over the host's cores (lib/src/parallel_pool.dart).
+    """
     import oracle
 
     oracle.lib()
+    info = host_info()
     flops = 0.0
     t_total = 0.0
     parts = []
@@ -108,9 +132,42 @@ def cpu_baseline(weights, rng, budget_s=30.0):
         parts.append(f"{name}[{cols}]")
         if t_total > budget_s:
             break
-    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"M=512 int4 MatMulNBits bs128 zp, projections {'+'.join(parts)} "
-                      f"({flops / 1e9:.1f} GFLOP in {t_total:.1f} s, 1 thread)"}
+    out = {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+           "sample": f"M=512 int4 MatMulNBits bs128 zp, projections {'+'.join(parts)} "
+                     f"({flops / 1e9:.1f} GFLOP in {t_total:.1f} s, 1 thread)",
+           "host": info}
+    # M = 1 GEMV over all eight projections (the whole lm_head).
+    nbytes, t1 = 0, 0.0
+    for (name, k, n), (b, s, zp) in zip(QWEN3_PROJ, weights):
+        a = rng.standard_normal((1, k)).astype(np.float32)
+        t0 = time.perf_counter()
+        oracle.matmul_nbits(a, b, s, zp, k=k, n=n, block_size=BLOCK)
+        t1 += time.perf_counter() - t0
+        nbytes += nbits_bytes(1, k, n)
+    out["gemv_m1"] = {"value": round(nbytes / t1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+                      "sample": f"M=1 int4 MatMulNBits, the eight Qwen3 projections "
+                                f"({nbytes / 1e6:.1f} MB in {t1:.2f} s, 1 thread)"}
+    # fp32 MiniLM Gemm set on the pool's N-split.
+    workers = max(1, min(16, info["cores_available"]))
+    H, F = MINILM_H, MINILM_FFN
+    gemms = [("q", H, H), ("k", H, H), ("v", H, H), ("out", H, H), ("ffn1", H, F),
+             ("ffn2", F, H)]
+    rows = MINILM_B * MINILM_S
+    fl, tp = 0.0, 0.0
+    for _, k, n in gemms:
+        w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)  # prepacked B [K, N]
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        pool = oracle.GemmPool(w, workers)
+        t0 = time.perf_counter()
+        pool.matmul(x)
+        tp += time.perf_counter() - t0
+        pool.close()
+        fl += 2.0 * rows * k * n
+    out["f32_pool"] = {"value": round(fl / tp / 1e12, 5), "unit": "TFLOP/s", "cores": workers,
+                       "sample": f"MiniLM-L6 layer Gemm set q/k/v/out/ffn1/ffn2 at {rows} rows "
+                                 f"on the GemmPool N-split over {workers} threads "
+                                 f"({fl / 1e9:.1f} GFLOP in {tp:.2f} s)"}
+    return out
 
 
 def load_traffic():
@@ -463,10 +520,19 @@ def int8_prefill(torch, ops, ctx, T, dev, args):
                                                      y[n_lm].data_ptr(),
                                                      np.array([128], np.int32)), 10, 2)
     lm_tops = 2.0 * M_PREFILL * n_lm * k_lm / (ms_lm / 1e3) / 1e12
+    # The lm_head shape is below the int8 ridge: its roofline is
+    # min(peak, arithmetic intensity x HBM bandwidth) (A u8, B i8, Y int32).
+    lm_bytes = M_PREFILL * k_lm + k_lm * n_lm + M_PREFILL * n_lm * 4
+    ai = 2.0 * M_PREFILL * n_lm * k_lm / lm_bytes
+    roof = min(INT8_MFMA_PEAK_TOPS, ai * HBM_PEAK_GBS / 1e3)
     out = {"workload": "Qwen3-0.6B projections as MatMulInteger u8 x i8 -> int32, M=512",
            "TOP/s": round(ops_step / (ms / 1e3) / 1e12, 1), "ms_per_pass": round(ms, 4),
-           "lm_head": {"TOP/s": round(lm_tops, 1), "frac_int8_peak":
-                       round(lm_tops / INT8_MFMA_PEAK_TOPS, 4), "ms": round(ms_lm, 4)}}
+           "lm_head": {"TOP/s": round(lm_tops, 1), "ms": round(ms_lm, 4),
+                       "arithmetic_intensity_op_per_byte": round(ai, 1),
+                       "roofline_TOP/s": round(roof, 1),
+                       "bound": "hbm" if roof < INT8_MFMA_PEAK_TOPS else "mfma",
+                       "frac_roofline": round(lm_tops / roof, 4),
+                       "frac_int8_peak": round(lm_tops / INT8_MFMA_PEAK_TOPS, 4)}}
     for w in ws:
         w.release()
     # C2 chain: x f32 [128, 1024] -> DQL -> MatMulInteger (int32) and QLinearMatMul (u8).

@@ -14,6 +14,7 @@ Thin numpy wrappers over ``oracle/lib/liboracle.so`` (built from oracle.c by
 * ``matmul_f32``           — lib/src/onnx_ops.dart:1710-1766
 * ``gemm_f32``             — lib/src/onnx_ops.dart:2152-2172
 * ``matmul_kernel``        — lib/src/gemm_kernel_simd.dart:32-239
+* ``GemmPool``             — lib/src/parallel_pool.dart:217-261, :299-329
 * ``fused_sdpa``           — lib/src/onnx_ops.dart:2106-2149
 * ``multi_head_attention`` — lib/src/onnx_ops.dart:2019-2098
 * ``group_query_attention`` — lib/src/onnx_ops.dart:1844-2012
@@ -70,6 +71,11 @@ _I = C.c_int
 def _declare(L):
     L.orc_matmul_kernel.argtypes = [_P, _P, _P, _I64, _I64, _I64]
     L.orc_matmul_kernel.restype = None
+    L.orc_pool_create.argtypes = [_P, _I64, _I64, C.c_int]
+    L.orc_pool_create.restype = C.c_void_p
+    L.orc_pool_matmul.argtypes = [C.c_void_p, _P, _I64, _P]
+    L.orc_pool_destroy.argtypes = [C.c_void_p]
+    L.orc_pool_destroy.restype = None
     L.orc_matmul_f32.argtypes = [_P, _P, _I, _P, _P, _I, _P]
     L.orc_gemm_f32.argtypes = [_P, _P, _P, _P, _P, _P, _I, C.c_double,
                                C.c_double, _I, _I, _P]
@@ -117,6 +123,33 @@ def round_even(v: float) -> int:
     r = lib().orc_round_even(float(v), C.byref(err))
     _check(err.value, "round_even")
     return int(r)
+
+
+class GemmPool:
+    """The reference's isolate pool for one f32 weight b [k, n]
+    (lib/src/parallel_pool.dart:217-261, :299-329) with threads as workers."""
+
+    def __init__(self, b: np.ndarray, workers: int):
+        self.b = np.ascontiguousarray(b, dtype=np.float32)
+        self.k, self.n = self.b.shape
+        self.handle = lib().orc_pool_create(_ptr(self.b), self.k, self.n, int(workers))
+        if not self.handle:
+            raise OracleError(INVALID_ARGUMENT, "orc_pool_create")
+
+    def matmul(self, a: np.ndarray) -> np.ndarray:
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        m = a.shape[0]
+        y = np.empty((m, self.n), dtype=np.float32)
+        _check(lib().orc_pool_matmul(self.handle, _ptr(a), m, _ptr(y)), "pool_matmul")
+        return y
+
+    def close(self):
+        if self.handle:
+            lib().orc_pool_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
 
 
 def matmul_kernel(a: np.ndarray, b: np.ndarray) -> np.ndarray:

@@ -5,6 +5,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -119,6 +120,101 @@ void orc_matmul_kernel(const float *a, const float *b, float *out, int64_t m,
       out[i * n + j] = (float)s;
     }
   }
+}
+
+/* ------------------------------------------------------- GemmPool N-split */
+
+/* The reference's isolate pool for f32 weights (lib/src/parallel_pool.dart:
+ * 217-261 partition, :299-329 matmul): W workers, worker w owns columns
+ * [start_w, start_w + count_w) with count_w = n / W + (w < n % W), as its own
+ * contiguous [k x count_w] slice; a call sends every worker a copy of A, each
+ * runs matmulKernel on its slice, and the slabs are stitched by column range.
+ * Each column's arithmetic is that of the unsplit kernel (same k order), so
+ * the result is bitwise the unsplit one.  Threads stand in for isolates. */
+struct orc_pool {
+  int workers;
+  int64_t k, n;
+  int64_t *start, *count;
+  float **slice;
+};
+
+struct orc_pool_job {
+  const struct orc_pool *p;
+  int w;
+  const float *a;
+  int64_t m;
+  float *slab;
+};
+
+static void *orc_pool_worker(void *arg) {
+  struct orc_pool_job *j = (struct orc_pool_job *)arg;
+  const struct orc_pool *p = j->p;
+  const int64_t nw = p->count[j->w];
+  /* The message copy of A (a Float32List sent to the isolate). */
+  float *a = (float *)malloc(sizeof(float) * (size_t)(j->m * p->k + 1));
+  memcpy(a, j->a, sizeof(float) * (size_t)(j->m * p->k));
+  if (nw > 0) orc_matmul_kernel(a, p->slice[j->w], j->slab, j->m, p->k, nw);
+  free(a);
+  return NULL;
+}
+
+void *orc_pool_create(const float *b, int64_t k, int64_t n, int workers) {
+  if (workers < 1 || k < 0 || n < 0) return NULL;
+  struct orc_pool *p = (struct orc_pool *)calloc(1, sizeof *p);
+  p->workers = workers;
+  p->k = k;
+  p->n = n;
+  p->start = (int64_t *)calloc((size_t)workers, sizeof(int64_t));
+  p->count = (int64_t *)calloc((size_t)workers, sizeof(int64_t));
+  p->slice = (float **)calloc((size_t)workers, sizeof(float *));
+  const int64_t base = n / workers, rem = n % workers;
+  int64_t col = 0;
+  for (int w = 0; w < workers; w++) {
+    const int64_t nw = base + (w < rem ? 1 : 0);
+    p->start[w] = col;
+    p->count[w] = nw;
+    p->slice[w] = (float *)malloc(sizeof(float) * (size_t)(k * nw + 1));
+    for (int64_t r = 0; r < k; r++)
+      memcpy(p->slice[w] + r * nw, b + r * n + col, sizeof(float) * (size_t)nw);
+    col += nw;
+  }
+  return p;
+}
+
+int orc_pool_matmul(void *pool, const float *a, int64_t m, float *y) {
+  struct orc_pool *p = (struct orc_pool *)pool;
+  if (!p || m < 0) return ORC_INVALID_ARGUMENT;
+  pthread_t *th = (pthread_t *)calloc((size_t)p->workers, sizeof(pthread_t));
+  struct orc_pool_job *jobs =
+      (struct orc_pool_job *)calloc((size_t)p->workers, sizeof(struct orc_pool_job));
+  for (int w = 0; w < p->workers; w++) {
+    jobs[w].p = p;
+    jobs[w].w = w;
+    jobs[w].a = a;
+    jobs[w].m = m;
+    jobs[w].slab = (float *)malloc(sizeof(float) * (size_t)(m * p->count[w] + 1));
+    pthread_create(&th[w], NULL, orc_pool_worker, &jobs[w]);
+  }
+  for (int w = 0; w < p->workers; w++) {
+    pthread_join(th[w], NULL);
+    const int64_t nw = p->count[w], c0 = p->start[w];
+    for (int64_t i = 0; i < m; i++)
+      memcpy(y + i * p->n + c0, jobs[w].slab + i * nw, sizeof(float) * (size_t)nw);
+    free(jobs[w].slab);
+  }
+  free(jobs);
+  free(th);
+  return ORC_OK;
+}
+
+void orc_pool_destroy(void *pool) {
+  struct orc_pool *p = (struct orc_pool *)pool;
+  if (!p) return;
+  for (int w = 0; w < p->workers; w++) free(p->slice[w]);
+  free(p->slice);
+  free(p->start);
+  free(p->count);
+  free(p);
 }
 
 /* ------------------------------------------------------------- MatMul f32 */

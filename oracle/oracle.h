@@ -28,6 +28,14 @@ enum { ORC_OK = 0, ORC_INVALID_ARGUMENT = 1, ORC_UNSUPPORTED = 2 };
 void orc_matmul_kernel(const float *a, const float *b, float *out, int64_t m,
                        int64_t k, int64_t n);
 
+/* GemmPool (lib/src/parallel_pool.dart:217-261, :299-329): b [k x n] split
+ * by columns over `workers` threads (n / W each, the first n % W one more),
+ * each running matmulKernel on its slice with its own copy of a; the result
+ * is bitwise orc_matmul_kernel's.  create returns NULL on bad arguments. */
+void *orc_pool_create(const float *b, int64_t k, int64_t n, int workers);
+int orc_pool_matmul(void *pool, const float *a, int64_t m, float *y);
+void orc_pool_destroy(void *pool);
+
 /* opMatMul: numpy-broadcast batched matmul, lib/src/onnx_ops.dart:1710-1766.
  * Shapes have rank >= 2.  y is sized by the broadcast output shape. */
 int orc_matmul_f32(const float *a, const int64_t *a_shape, int a_rank,

@@ -627,3 +627,19 @@ def test_gqa_decode_step_continues_the_prefill():
     np.testing.assert_allclose(step[0], full[0][:, 5:], rtol=1e-6, atol=1e-6)
     np.testing.assert_array_equal(step[1], full[1])
     np.testing.assert_allclose(head[0], full[0][:, :5], rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("m,k,n,workers", [(7, 33, 50, 3), (64, 128, 1000, 8), (5, 16, 3, 4),
+                                           (4, 40, 151, 2), (300, 64, 17, 16)])
+def test_pool_split_is_bitwise_the_unsplit_kernel(m, k, n, workers):
+    # parallel_pool_test.dart:27-111: an N-split over workers (the first n % W
+    # take one more column) gives bitwise the single-kernel result, including
+    # more workers than columns.  The graph pools only calls of >= 4 rows
+    # (lib/src/onnx_graph.dart:856-872), where every column takes the f32
+    # lanes; below 4 rows the kernel's double tails depend on n % 4.
+    rng = np.random.default_rng(23)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    pool = oracle.GemmPool(b, workers)
+    np.testing.assert_array_equal(pool.matmul(a), oracle.matmul_kernel(a, b))
+    pool.close()
