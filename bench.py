@@ -8,7 +8,9 @@ weights and activations resident in HBM.
 
 The same run also measures, each with HIP events on the stream the library
 launches on:
-  roofline       the lm_head call at M = 512 (MFMA-bound), against fp16 peak;
+  roofline       the lm_head call at M = 512 (MFMA-bound), against fp16 peak
+                 (the kernel issues three fp8 products per product: its
+                 share of the fp8 peak is reported beside it);
   gemv_m1        the same eight projections at M = 1, algorithmic HBM GB/s;
                  four distinct weight sets are rotated so that the working set
                  (~370 MB) exceeds the 256 MB last-level cache and the weights
@@ -22,9 +24,11 @@ launches on:
                  QLinearMatMul chain at M = 128, K = N = 1024;
   f32_encoder    one MiniLM-L6 encoder layer's Gemm/MatMul set (batch 32,
                  seq 128, hidden 384, 12 heads, FFN 1536) in fp32;
-  cpu_baseline   the oracle (the reference's algorithm restated in C, one
-                 thread, as the reference never pools MatMulNBits) on a
-                 bounded M = 512 sample.
+  cpu_baseline   the oracle (the reference's algorithms restated in C) on
+                 bounded samples: the M = 512 int4 prefill on one thread (the
+                 reference never pools MatMulNBits) as `value`, the M = 1
+                 GEMV, and the fp32 MiniLM Gemm set on the GemmPool N-split
+                 over the host's cores, with the host's CPU model.
 `traffic` (HBM bytes per launch of the dominant kernels) comes from
 profiles/traffic.json, written from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 runs of `bench.py --only ...` (commands and calibration in that file).
@@ -47,6 +51,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
+FP8_MFMA_PEAK_TFLOPS = 5000.0
 INT8_MFMA_PEAK_TOPS = 5000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
@@ -291,17 +296,20 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 weights x fp32 activations (fp16 hi/lo MFMA, fp32 accumulate)",
+        "dtype": "int4 weights x fp32 activations (activations as three fp8 e4m3 digits with "
+                 "per-32-k E8M0 scales on block-scaled fp8 MFMA, fp32 accumulate)",
         "data": "synthetic (seeded uniform nibbles, scales U(0.002,0.02), A ~ N(0,1))",
         "config": {"workload": "Qwen3-0.6B int4 MatMulNBits projections q,k,v,o,gate,up,"
                                "down,lm_head; block_size 128 with uint4 zero points",
                    "M": M_PREFILL, "block_size": BLOCK,
                    "gflop_per_step": round(flops_step / 1e9, 2)},
-        "roofline": {"kernel": tr.get("kernel", "k_gemm_f16split") +
+        "roofline": {"kernel": tr.get("kernel", "k_gemm_f8x3") +
                      " (lm_head 512x1024x151936; op time incl. activation prepass)",
                      "bound": "mfma", "achieved": round(lm_tflops, 2),
                      "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(lm_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
+                     "issued": "3 fp8 MFMA products per algorithmic product",
+                     "issued_frac_of_fp8_peak": round(3 * lm_tflops / FP8_MFMA_PEAK_TFLOPS, 4),
                      "traffic": tr.get("bytes"),
                      "algorithmic_bytes": nbits_bytes(M_PREFILL, k_lm, n_lm),
                      "ms": round(ms_lm, 4)},
