@@ -60,6 +60,10 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 QWEN3_PROJ = [("q", 1024, 2048), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 2048, 1024),
               ("gate", 1024, 3072), ("up", 1024, 3072), ("down", 3072, 1024),
               ("lm_head", 1024, 151936)]
+# Sibling projections that read the same activations and run as one grouped
+# launch (mg_matmul_nbits_group_dev), as the Dart shim issues them: q/k/v and
+# gate/up.  Indices into QWEN3_PROJ.
+QWEN3_GROUPS = [(0, 1, 2), (3,), (4, 5), (6,), (7,)]
 BLOCK = 128
 M_PREFILL = 512
 GEMV_ROTATE = 4
@@ -266,15 +270,34 @@ def main():
             if (m, n) not in outs:
                 outs[(m, n)] = torch.empty((m, n), device=dev, dtype=torch.float32)
 
-    def run_pass(ws, m):
+    # Grouped members write separate outputs (one per projection).
+    for m in (M_PREFILL, 1):
+        for name, _, n in QWEN3_PROJ:
+            outs[(m, name)] = torch.empty((m, n), device=dev, dtype=torch.float32)
+
+    def run_pass_separate(ws, m):
         for (_, k, n), w in zip(QWEN3_PROJ, ws):
             w.run_dev(acts[(m, k)].data_ptr(), m, outs[(m, n)].data_ptr())
 
-    # ---- headline: M = 512 prefill pass
+    def run_pass(ws, m):
+        for grp in QWEN3_GROUPS:
+            k = QWEN3_PROJ[grp[0]][1]
+            if len(grp) == 1:
+                ws[grp[0]].run_dev(acts[(m, k)].data_ptr(), m,
+                                   outs[(m, QWEN3_PROJ[grp[0]][0])].data_ptr())
+            else:
+                ops.matmul_nbits_group_dev([ws[i] for i in grp], acts[(m, k)].data_ptr(), m,
+                                           [outs[(m, QWEN3_PROJ[i][0])].data_ptr() for i in grp],
+                                           ctx=ctx)
+
+    # ---- headline: M = 512 prefill pass (siblings grouped), and the same
+    # eight projections launched one by one
     flops_step = sum(2.0 * M_PREFILL * n * k for _, k, n in QWEN3_PROJ)
     ms_step = T.loop(lambda: run_pass(weights, M_PREFILL), args.steps, args.warmup)
     value = flops_step / (ms_step / 1e3) / 1e12
-    print(f"# prefill pass {ms_step:.4f} ms, {value:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    ms_step_sep = T.loop(lambda: run_pass_separate(weights, M_PREFILL), args.steps, args.warmup)
+    print(f"# prefill pass {ms_step:.4f} ms, {value:.1f} TFLOP/s (separate launches "
+          f"{ms_step_sep:.4f} ms)", file=sys.stderr, flush=True)
 
     # ---- dominant MFMA kernel: lm_head at M = 512
     traffic = load_traffic()
@@ -302,7 +325,11 @@ def main():
         "config": {"workload": "Qwen3-0.6B int4 MatMulNBits projections q,k,v,o,gate,up,"
                                "down,lm_head; block_size 128 with uint4 zero points",
                    "M": M_PREFILL, "block_size": BLOCK,
-                   "gflop_per_step": round(flops_step / 1e9, 2)},
+                   "gflop_per_step": round(flops_step / 1e9, 2),
+                   "launches": "q/k/v and gate/up as sibling groups (one launch each, as the "
+                               "Dart shim issues them); o, down, lm_head alone"},
+        "separate_launches": {"ms_per_step": round(ms_step_sep, 4),
+                              "TFLOP/s": round(flops_step / (ms_step_sep / 1e3) / 1e12, 2)},
         "roofline": {"kernel": tr.get("kernel", "k_gemm_f8x3") +
                      " (lm_head 512x1024x151936; op time incl. activation prepass)",
                      "bound": "mfma", "achieved": round(lm_tflops, 2),
@@ -324,8 +351,7 @@ def main():
     state = {"i": 0}
 
     def gemv_pass_on(ws):
-        for (_, k, n), w in zip(QWEN3_PROJ, ws):
-            w.run_dev(acts[(1, k)].data_ptr(), 1, outs[(1, n)].data_ptr())
+        run_pass(ws, 1)
 
     def gemv_pass():
         gemv_pass_on(rot[state["i"] % GEMV_ROTATE])
@@ -349,8 +375,18 @@ def main():
     except Exception as e:  # capture unsupported: report the host-issued figure only
         print(f"# gemv M=1 graph capture failed: {e}", file=sys.stderr, flush=True)
     ms_m1 = ms_m1_graph if ms_m1_graph is not None else ms_m1_eager
-    # Per-launch kernel times: each of the 8 launches between its own pair of
-    # events (pre-created), averaged over the rotated sets.
+    # The eight projections launched one by one, replayed the same way.
+    ms_m1_sep = None
+    try:
+        graph_sep = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph_sep, stream=stream):
+            for ws in rot:
+                run_pass_separate(ws, 1)
+        ms_m1_sep = T.loop(graph_sep.replay, max(gsteps // GEMV_ROTATE, 10), 3) / GEMV_ROTATE
+    except Exception as e:
+        print(f"# gemv M=1 graph capture (separate) failed: {e}", file=sys.stderr, flush=True)
+    # Per-projection times, each of the 8 projections launched alone between
+    # its own pair of events (pre-created), averaged over the rotated sets.
     nsum = 4 * GEMV_ROTATE
     evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in QWEN3_PROJ] for _ in range(nsum)]
@@ -384,6 +420,9 @@ def main():
                          "timing": "HIP graph replay" if ms_m1_graph is not None
                                    else "host-issued launches",
                          "ms_per_pass_host_issued": round(ms_m1_eager, 4),
+                         "launches": "q/k/v and gate/up as sibling groups, as the headline",
+                         "ms_per_pass_separate_launches":
+                             None if ms_m1_sep is None else round(ms_m1_sep, 4),
                          "kernel_us": {name: round(t * 1e3, 2)
                                        for (name, _, _), t in zip(QWEN3_PROJ, per_launch)},
                          "kernel_sum_ms": round(sum(per_launch), 4),

@@ -243,70 +243,114 @@ __device__ inline void gemv_issue(GemvSlot<QPG, ZPK> &sl, const uint4 *wp, const
   }
 }
 
+// Phase 1, one task (row r, k group slot l, 8-k octet o): the activation
+// loads, then the digits into LDS.  The loads are branch-free (addresses
+// clamped into the row, values outside it replaced by 0 afterwards), so a
+// caller can keep several tasks' loads in flight.  VEC: K % 4 == 0 and
+// 16-byte rows (two float4 loads).
+template <bool VEC>
+__device__ inline void gemv_digits_load(const float *__restrict__ a, int64_t K, int c0, int nk,
+                                        int task, float (&v)[8]) {
+  const int o = task & 15, rl = task >> 4;
+  const int l = rl % nk, r = rl / nk;
+  const int64_t k0 = (int64_t)(c0 + l) * KGRP + 8 * o;
+  const float *ar = a + (int64_t)r * K;
+  if constexpr (VEC) {
+    const bool ok0 = k0 + 4 <= K, ok1 = k0 + 8 <= K;
+    const float4 x0 = *reinterpret_cast<const float4 *>(ar + (ok0 ? k0 : 0));
+    const float4 x1 = *reinterpret_cast<const float4 *>(ar + (ok1 ? k0 + 4 : 0));
+    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = ar[min(k0 + i, K - 1)];
+  }
+}
+
+// Zeroes the values of a task's loads that lie past the end of the row
+// (VEC: by float4; K % 4 == 0 there).
+__device__ inline void gemv_digits_mask(int64_t K, int c0, int nk, int task, float (&v)[8]) {
+  const int o = task & 15, l = (task >> 4) % nk;
+  const int64_t k0 = (int64_t)(c0 + l) * KGRP + 8 * o;
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    if (k0 + i >= K) v[i] = 0.f;
+}
+
+template <int QPG>
+__device__ inline void gemv_digits_put(const float (&v)[8], int nk, int kc, int task,
+                                       uint32_t *sdig, float *salpha, int *srsum) {
+  constexpr int G = 16 / QPG;  // octets per qblock
+  const int o = task & 15, rl = task >> 4;
+  const int l = rl % nk, r = rl / nk;
+  float mx = 0.f;
+  int bad = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    if (!isfinite(v[i])) bad = 1;
+    mx = fmaxf(mx, fabsf(v[i]));
+  }
+#pragma unroll
+  for (int off = 1; off < G; off <<= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, off));
+    bad |= __shfl_xor(bad, off);
+  }
+  const float inv = (mx > 0.f && !bad) ? (float)FIX_MAX / mx : 0.f;
+  int rs = 0;
+  uint32_t dg[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    int fix = (int)rintf(v[i] * inv);
+    fix = min(max(fix, -FIX_MAX), FIX_MAX);
+    rs += fix;
+    const int pos = nib_pos(i);
+    int x = fix;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      const int di = ((x + 8) & 15) - 8;
+      x = (x - di) >> 4;
+      dg[d] |= (uint32_t)(di & 15) << (4 * pos);
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < G; off <<= 1) rs += __shfl_xor(rs, off);
+  const int j = o >> 2, g = o & 3;
+  *reinterpret_cast<uint4 *>(&sdig[((r * kc + l) * 4 + g) * 16 + j * 4]) =
+      make_uint4(dg[0], dg[1], dg[2], dg[3]);
+  if (o % G == 0) {
+    const int q = (r * kc + l) * QPG + o / G;
+    salpha[q] = bad ? __builtin_nanf("") : (mx > 0.f ? mx / (float)FIX_MAX : 0.f);
+    srsum[q] = rs;
+  }
+}
+
 // Phase 1 for k groups [c0, c0 + nk) into LDS slots l = 0 .. nk - 1 (kc slots
-// per row), by nthr threads.
+// per row), by nthr threads.  Tasks are 16 consecutive lanes per (row, k
+// group), so the shuffles inside a qblock see only active lanes.
 template <int MR, int QPG>
 __device__ inline void gemv_digits(const float *__restrict__ a, int64_t K, int vec, int c0,
                                    int nk, int kc, uint32_t *sdig, float *salpha, int *srsum,
                                    int t, int nthr) {
-  constexpr int G = 16 / QPG;  // octets per qblock
   const int ntask = MR * nk * 16;
   for (int task = t; task < ntask; task += nthr) {
-    const int o = task & 15, rl = task >> 4;
-    const int l = rl % nk, r = rl / nk;
-    const int64_t k0 = (int64_t)(c0 + l) * KGRP + 8 * o;
-    const float *ar = a + (int64_t)r * K;
     float v[8];
-    if (vec && k0 + 8 <= K) {
-      const float4 x0 = *reinterpret_cast<const float4 *>(ar + k0);
-      const float4 x1 = *reinterpret_cast<const float4 *>(ar + k0 + 4);
-      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-      v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = (k0 + i < K) ? ar[k0 + i] : 0.f;
-    }
-    float mx = 0.f;
-    int bad = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      if (!isfinite(v[i])) bad = 1;
-      mx = fmaxf(mx, fabsf(v[i]));
-    }
-#pragma unroll
-    for (int off = 1; off < G; off <<= 1) {
-      mx = fmaxf(mx, __shfl_xor(mx, off));
-      bad |= __shfl_xor(bad, off);
-    }
-    const float inv = (mx > 0.f && !bad) ? (float)FIX_MAX / mx : 0.f;
-    int rs = 0;
-    uint32_t dg[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      int fix = (int)rintf(v[i] * inv);
-      fix = min(max(fix, -FIX_MAX), FIX_MAX);
-      rs += fix;
-      const int pos = nib_pos(i);
-      int x = fix;
-#pragma unroll
-      for (int d = 0; d < 4; d++) {
-        const int di = ((x + 8) & 15) - 8;
-        x = (x - di) >> 4;
-        dg[d] |= (uint32_t)(di & 15) << (4 * pos);
-      }
-    }
-#pragma unroll
-    for (int off = 1; off < G; off <<= 1) rs += __shfl_xor(rs, off);
-    const int j = o >> 2, g = o & 3;
-    *reinterpret_cast<uint4 *>(&sdig[((r * kc + l) * 4 + g) * 16 + j * 4]) =
-        make_uint4(dg[0], dg[1], dg[2], dg[3]);
-    if (o % G == 0) {
-      const int q = (r * kc + l) * QPG + o / G;
-      salpha[q] = bad ? __builtin_nanf("") : (mx > 0.f ? mx / (float)FIX_MAX : 0.f);
-      srsum[q] = rs;
-    }
+    if (vec) gemv_digits_load<true>(a, K, c0, nk, task, v);
+    else gemv_digits_load<false>(a, K, c0, nk, task, v);
+    gemv_digits_mask(K, c0, nk, task, v);
+    gemv_digits_put<QPG>(v, nk, kc, task, sdig, salpha, srsum);
   }
 }
+
+// The float arithmetic of one (row, block) term, shared by every M <= 4
+// GEMV kernel so that all of them round alike: the block's integer sum comb
+// (sum over its k of activation fixed point times q - 8) plus the zero-point
+// correction, then y = fma(alpha * scale, v, y) in k order.
+template <int ZPK>
+__device__ inline float gemv_block_value(int comb, int zc, int R, float zf) {
+  if (ZPK == 2) return __builtin_fmaf(8.f - zf, (float)R, (float)comb);
+  return (float)(comb + zc * R);
+}
+__device__ inline float gemv_term(float y, float p, float v) { return __builtin_fmaf(p, v, y); }
 
 // Phase 2 for one k group kg (LDS slot l) held in sl: yacc[r] += its share.
 template <int MR, int QPG, int ZPK>
@@ -360,12 +404,7 @@ __device__ inline void gemv_kgroup(const GemvSlot<QPG, ZPK> &sl, int kg, int l, 
       const int q = (r * kc + l) * QPG + s;
       const float al = salpha[q];
       const int R = srsum[q];
-      float v;
-      if (ZPK == 2)
-        v = (float)comb + (8.f - sl.zf[s]) * (float)R;
-      else
-        v = (float)(comb + zc * R);
-      yacc[r] += (al * sl.s[s]) * v;
+      yacc[r] = gemv_term(yacc[r], al * sl.s[s], gemv_block_value<ZPK>(comb, zc, R, sl.zf[s]));
     }
   }
 }
@@ -440,8 +479,15 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
     const int col = cg * 64 + lane;
 #pragma unroll
     for (int r = 0; r < MR; r++) {
-      float s = red[r * 64 + lane];
-      for (int w = 1; w < NW; w++) s += red[(w * MR + r) * 64 + lane];
+      // All NW wave sums are read before the ordered adds, so the LDS reads
+      // overlap (NW <= 16; the launch bounds allow no more).
+      float part[16];
+#pragma unroll
+      for (int w = 0; w < 16; w++) part[w] = w < NW ? red[(w * MR + r) * 64 + lane] : 0.f;
+      float s = part[0];
+#pragma unroll
+      for (int w = 1; w < 16; w++)
+        if (w < NW) s += part[w];
       if (col < N) y[(int64_t)r * N + col] = s + (bias ? bias[col] : 0.f);
     }
   }
@@ -514,6 +560,141 @@ __global__ __launch_bounds__(256) void k_gemv_dot8p(
         if (col < gs.N[gm]) gs.y[gm][(int64_t)r * gs.N[gm] + col] = s + (bias ? bias[col] : 0.f);
       }
     }
+  }
+}
+
+// Column-slice form for one row, narrow weights and block_size >= 128 (one
+// quantisation block per k group): a workgroup takes 16 columns (a quarter
+// of a column group) over all of K, so a weight spreads over four times the
+// workgroups of k_gemv_dot8 and each CU streams a quarter of the bytes.
+// Lane l works on column cl = 16 (x % 4) + l % 16 and octet g = l / 16 of
+// every k group: its packed uint4 is 16 bytes of a 256-byte run (16 columns
+// of one octet), so each wave reads whole lines.  Wave w takes k groups w,
+// w + 4, ... (those of wave w in k_gemv_dot8 with four waves), PF of them in
+// flight.  Per k group the lanes' integer sums over their octet are added
+// over the four octets with shuffles (exact), so every lane holds the
+// block's integer sum for its column and runs the same float chain over k
+// groups as k_gemv_dot8's lane for that column; the four wave sums are added
+// in wave order.  Results are bitwise those of k_gemv_dot8 (four waves) and
+// k_gemv_dot8p.  (With smaller blocks the per-block scale and zero-point
+// loads of 16 columns cost more than the wider spread gains.)
+constexpr int CS_TASKS = 4;  // digits tasks per thread: K <= 64 k groups
+
+template <int ZPK>
+struct CsSlot {
+  uint4 w;
+  float s;
+  uint32_t z;
+  float zf;
+};
+
+template <int ZPK, int PF, bool VEC>
+__global__ __launch_bounds__(256) void k_gemv_cs(const float *__restrict__ a, int64_t K,
+                                                 const GemvSet gs, int c4, int nb, int nbh,
+                                                 int lbs) {
+  extern __shared__ uint32_t smem[];
+  uint32_t *sdig = smem;                                       // [c4][64]
+  float *salpha = reinterpret_cast<float *>(smem + c4 * 64);   // [c4]
+  int *srsum = reinterpret_cast<int *>(salpha + c4);           // [c4]
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  int cg;
+  const int gm = gemv_member(gs, (int)(blockIdx.x >> 2), &cg);
+  const int cl = (int)(blockIdx.x & 3) * 16 + c;
+  const uint4 *wp = gs.wq[gm] + (int64_t)cg * c4 * 256 + g * 64 + cl;
+  const float *sp = gs.scales[gm] + (int64_t)cg * nb * 64 + sz_pos(cl);
+  const uint8_t *zq = gs.zp4[gm] + (int64_t)cg * nbh * 64 + sz_pos(cl);
+  const float *zfp = gs.zpf[gm] + (int64_t)cg * nb * 64 + sz_pos(cl);
+
+  auto issue = [&](CsSlot<ZPK> &sl, int kg) {
+    sl.w = __builtin_bit_cast(
+        uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wp + kg * 256)));
+    const int b = min((kg * KGRP) >> lbs, nb - 1);
+    sl.s = sp[(int64_t)b * 64];
+    if (ZPK == 1) sl.z = zq[(int64_t)(b >> 1) * 64];
+    if (ZPK == 2) sl.zf = zfp[(int64_t)b * 64];
+  };
+
+  // The activation loads go first: the vector memory counter retires loads
+  // in issue order, so the digits then wait for them alone.  Tasks: k group
+  // slot l, octet o (at most CS_TASKS per thread: c4 <= 16 * CS_TASKS).
+  const int ntask = c4 * 16;
+  float av[CS_TASKS][8];
+#pragma unroll
+  for (int i = 0; i < CS_TASKS; i++)
+    gemv_digits_load<VEC>(a, K, 0, c4, min(t + 256 * i, ntask - 1), av[i]);
+  __builtin_amdgcn_sched_barrier(0);  // keep the issue order: activations, weights
+  // This wave's k groups are wave + 4 n, n < nk; the loads of the n-th sit
+  // in ring slot n % PF.  Loads are issued in straight-line code (addresses
+  // clamped to the last k group where a slot has nothing left to take), so
+  // the wait before each slot's use counts exactly the loads issued after it.
+  const int nk = (c4 - wave + 3) / 4;  // 0 for waves past c4 < 4
+  const int niter = (c4 + 3) / 4;      // nk of wave 0, the largest
+  auto kg_at = [&](int n) { return min(wave + 4 * n, c4 - 1); };
+  CsSlot<ZPK> ring[PF];
+#pragma unroll
+  for (int i = 0; i < PF; i++) issue(ring[i], kg_at(i));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < CS_TASKS; i++)
+    if (t + 256 * i < ntask) {
+      gemv_digits_mask(K, 0, c4, t + 256 * i, av[i]);
+      gemv_digits_put<1>(av[i], c4, c4, t + 256 * i, sdig, salpha, srsum);
+    }
+  __syncthreads();
+
+  float y = 0.f;
+  auto kgroup = [&](const CsSlot<ZPK> &cur, int kg) {
+    // Integer sum over dword j (k = 32 j + 8 g + 0..7) and the four digit
+    // planes, then over the four octets (lanes c, c + 16, c + 32, c + 48).
+    const uint32_t wv[4] = {cur.w.x ^ 0x88888888u, cur.w.y ^ 0x88888888u,
+                            cur.w.z ^ 0x88888888u, cur.w.w ^ 0x88888888u};
+    int v = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint4 dd = *reinterpret_cast<const uint4 *>(&sdig[(kg * 4 + g) * 16 + j * 4]);
+      const int a0 = __builtin_amdgcn_sdot8((int)dd.x, (int)wv[j], 0, false);
+      const int a1 = __builtin_amdgcn_sdot8((int)dd.y, (int)wv[j], 0, false);
+      const int a2 = __builtin_amdgcn_sdot8((int)dd.z, (int)wv[j], 0, false);
+      const int a3 = __builtin_amdgcn_sdot8((int)dd.w, (int)wv[j], 0, false);
+      v += ((a3 * 16 + a2) * 16 + a1) * 16 + a0;
+    }
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    const int b = (kg * KGRP) >> lbs;
+    if (b >= nb) return;  // k padding beyond the last block
+    int zc = 0;
+    if (ZPK == 1) zc = 8 - (int)((b & 1) ? (cur.z >> 4) : (cur.z & 15));
+    y = gemv_term(y, salpha[kg] * cur.s, gemv_block_value<ZPK>(v, zc, srsum[kg], cur.zf));
+  };
+  for (int n = 0; n < niter; n += PF) {
+    if (n + PF < niter) {
+#pragma unroll
+      for (int i = 0; i < PF; i++) {
+        const CsSlot<ZPK> cur = ring[i];
+        issue(ring[i], kg_at(n + i + PF));
+        if (n + i < nk) kgroup(cur, wave + 4 * (n + i));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PF; i++)
+        if (n + i < nk) kgroup(ring[i], wave + 4 * (n + i));
+    }
+  }
+  __syncthreads();  // every wave is done with the digits; reuse LDS
+  float *red = reinterpret_cast<float *>(smem);  // [4][16]
+  if (g == 0) red[wave * 16 + c] = y;
+  __syncthreads();
+  if (wave == 0 && g == 0) {
+    float s = red[c];
+    s += red[16 + c];
+    s += red[32 + c];
+    s += red[48 + c];
+    const int col = cg * 64 + cl;
+    const float *bias = gs.bias[gm];
+    if (col < gs.N[gm]) gs.y[gm][col] = s + (bias ? bias[col] : 0.f);
   }
 }
 
@@ -1192,6 +1373,8 @@ struct NbitsPlan {
   int nt = 4;  // prefill tile width in 32-column MFMA tiles (4 or 2)
   int pers = 0;       // GEMV on the persistent kernel (k_gemv_dot8p)
   int pers_grid = 0;  // its workgroups
+  int cs = 0;         // GEMV on the column-slice kernel (k_gemv_cs)
+  int cs_pf = 4;      // its k groups in flight per wave
   size_t off_a = 0, off_b = 0, off_c = 0, off_d = 0, total = 0;
 };
 
@@ -1254,6 +1437,21 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
       p.pers = 1;
       p.pers_grid = (int)((ng_total + per - 1) / per);
       p.lds = (size_t)(d.c4 * per_kg + 2 * 4 * M * 64 * 4);
+    }
+    // One row, one quantisation block per k group and fewer column groups
+    // than MG_GEMV_CS_MAX_CG: 16-column slices (four workgroups per column
+    // group), for K up to 64 k groups (the digits of all of K in LDS).
+    // Measured on the Qwen3 shapes (graph replay, rotated weights): 16-64
+    // column groups 4.1-6.5 us against 4.5-8.0 us on k_gemv_dot8; at 96
+    // (gate/up grouped) 5.3 against 5.0 us.
+#ifndef MG_GEMV_CS_MAX_CG
+#define MG_GEMV_CS_MAX_CG 96
+#endif
+    if (M == 1 && p.qpg == 1 && !p.pers && ng_total < MG_GEMV_CS_MAX_CG && kc == d.c4 &&
+        d.c4 <= 16 * CS_TASKS) {
+      p.cs = 1;
+      p.cs_pf = d.c4 > 16 ? 8 : 4;
+      p.lds = (size_t)std::max<int64_t>(d.c4 * per_kg, 4 * 16 * 4);
     }
   } else if (d.bs >= 32 && int_zp) {
 #ifndef MG_PREFILL_F8
@@ -1362,9 +1560,38 @@ void launch_gemv_pers(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p,
   else launch_gemv_pers_pf<QPG, 2>(w, gs, p, st, a, vec);
 }
 
+template <int ZPK>
+void launch_gemv_cs_z(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, hipStream_t st,
+                      const float *a, int vec) {
+  const mg_nbits_dev &d = w->nbits;
+  const dim3 grid((unsigned)gs.cg_end[gs.n - 1] * 4), block(256);
+#define MG_CS_LAUNCH(PF_, V_)                                                            \
+  hipLaunchKernelGGL((k_gemv_cs<ZPK, PF_, V_>), grid, block, p.lds, st, a, w->K, gs,      \
+                     (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs))
+  if (p.cs_pf == 8) {
+    if (vec) MG_CS_LAUNCH(8, true);
+    else MG_CS_LAUNCH(8, false);
+  } else {
+    if (vec) MG_CS_LAUNCH(4, true);
+    else MG_CS_LAUNCH(4, false);
+  }
+#undef MG_CS_LAUNCH
+}
+
+void launch_gemv_cs(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, hipStream_t st,
+                    const float *a, int vec) {
+  if (w->nbits.zp_kind == 0) launch_gemv_cs_z<0>(w, gs, p, st, a, vec);
+  else if (w->nbits.zp_kind == 1) launch_gemv_cs_z<1>(w, gs, p, st, a, vec);
+  else launch_gemv_cs_z<2>(w, gs, p, st, a, vec);
+}
+
 template <int MR>
 void launch_gemv_q(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, hipStream_t st,
                    const float *a, int vec) {
+  if (MR == 1 && p.cs) {
+    launch_gemv_cs(w, gs, p, st, a, vec);
+    return;
+  }
   if (MR == 1 && p.pers) {
     switch (p.qpg) {
       case 1: launch_gemv_pers<1>(w, gs, p, st, a, vec); break;

@@ -490,6 +490,47 @@ def test_persistent_gemv_group(ops):
         w.release()
 
 
+PLANS_AGREE = [
+    # (K, bs, zp_mode): one row through the column-slice kernel (narrow
+    # slices of the weight, block_size >= 128) and the one-workgroup-per-
+    # column-group kernels (the whole weight, 512+ column groups).
+    (1024, 128, "packed"),
+    (3072, 128, "float"),
+    (8192, 128, "none"),
+    (200, 256, "packed"),
+    (4100, 128, "packed"),
+    (2048, 512, "packed"),
+]
+
+
+@pytest.mark.parametrize("k,bs,zp_mode", PLANS_AGREE)
+def test_m1_gemv_plans_agree_bitwise(ops, k, bs, zp_mode):
+    # At one row every plan adds the same float terms in the same order, so a
+    # column slice run as its own (narrow) weight gives bitwise the columns of
+    # the whole weight's launch, wherever the slice starts.
+    rng = np.random.default_rng(0x5EED0050 + k + bs)
+    n = 512 * 64 + 37
+    b, s, zp = make_nbits(rng, n, k, bs, zp_mode, 0.002, 0.02)
+    bias = rng.standard_normal(n).astype(np.float32)
+    a = rng.standard_normal((3, k)).astype(np.float32)
+    a[1, 5] = np.inf     # a non-finite row: the same Inf / NaN pattern on both
+    a[2, k - 1] = 60.0   # an outlier in the last block
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    full = [w(a[r:r + 1]) for r in range(3)]
+    w.release()
+    for lo, cnt in [(0, 1000), (777, 1001), (n - 70, 70)]:
+        cols = np.arange(lo, lo + cnt)
+        bb, ss, zz, bi = slice_cols(b, s, zp, bias, cols)
+        ws = ops.NBitsWeight(bb, ss, zz, k=k, n=cnt, block_size=bs, bias=bi)
+        for r in range(3):
+            np.testing.assert_array_equal(ws(a[r:r + 1]), full[r][:, cols],
+                                          err_msg=f"cols {lo}+{cnt} row {r}")
+        ws.release()
+    ref = oracle.matmul_nbits(a[2:3], *slice_cols(b, s, zp, bias, np.arange(1000))[:3], k=k,
+                              n=1000, block_size=bs, bias=bias[:1000])
+    assert G.rms_error(full[2][:, :1000], ref) <= TOL
+
+
 def test_profiling_records_each_op(ops):
     # Per-op device timing (the ABI's part of ExecutionProfile): one record
     # per op entry, in issue order, with the reference's op-type names.
