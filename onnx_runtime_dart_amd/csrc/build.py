@@ -32,6 +32,7 @@ HIPFLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Wall",
+    "-Werror=shadow",  # a local shadowing a kernel argument has written the wrong buffer
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}",

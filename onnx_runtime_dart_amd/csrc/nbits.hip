@@ -169,6 +169,7 @@ struct GemvSet {
   const float *zpf[GMAX];
   const float *bias[GMAX];
   float *y[GMAX];
+  int64_t part_off[GMAX];  // split-K partials of member m: part + part_off[m] + split * M * N
   int N[GMAX];
   int cg_end[GMAX];
   int n;
@@ -412,7 +413,7 @@ __device__ inline void gemv_kgroup(const GemvSlot<QPG, ZPK> &sl, int kg, int l, 
 template <int MR, int QPG, int ZPK, int PF>
 __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
     const float *__restrict__ a, int64_t K, int vec, const GemvSet gs, int c4, int nb,
-    int nbh, int lbs, int kc) {
+    int nbh, int lbs, int kc, int kps, float *__restrict__ part) {
   extern __shared__ uint32_t smem[];
   uint32_t *sdig = smem;                                            // [MR][kc][64]
   float *salpha = reinterpret_cast<float *>(smem + MR * kc * 64);   // [MR][kc][QPG]
@@ -433,24 +434,31 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
   const uint8_t *zq = gs.zp4[gm] + (int64_t)cg * nbh * 64 + sz_pos(lane);
   const float *zfp = gs.zpf[gm] + (int64_t)cg * nb * 64 + sz_pos(lane);
   GemvSlot<QPG, ZPK> ring[PF];
-  // This wave's k groups: wave, wave + NW, ...; the n-th is wave + n * NW.
-  const int nmine = wave < c4 ? (c4 - wave + NW - 1) / NW : 0;
+  // Split-K (gridDim.y > 1): this workgroup takes k groups [kb, kb + cs)
+  // and writes its sum, without the bias, to the split's partials.
+  const int kb = (int)blockIdx.y * kps;
+  const int cs = min(kps, c4 - kb);
+  // This wave's k groups: kb + wave, kb + wave + NW, ...; the n-th is
+  // kb + wave + n * NW.
+  const int nmine = wave < cs ? (cs - wave + NW - 1) / NW : 0;
 
-  // Phase 0.
+  // Phase 0.  (Issuing the activation loads ahead of these, so that the
+  // digits wait for them alone, measured slower here: 5.2 -> 6.1 us on a
+  // 2048 x 512 weight, 31 -> 38 us on the 2048 x 128256 lm_head.)
 #pragma unroll
   for (int i = 0; i < PF; i++)
-    if (i < nmine) gemv_issue(ring[i], wp, sp, zq, zfp, wave + i * NW, nb, lbs);
+    if (i < nmine) gemv_issue(ring[i], wp, sp, zq, zfp, kb + wave + i * NW, nb, lbs);
 
   float yacc[MR];
 #pragma unroll
   for (int r = 0; r < MR; r++) yacc[r] = 0.f;
   // kc is c4 (one chunk) or a multiple of PF * NW, so every chunk starts at a
   // multiple of PF of this wave's k groups and ring slots stay static.
-  for (int c0 = 0; c0 < c4; c0 += kc) {
-    const int nk = min(c4, c0 + kc) - c0;
+  for (int c0 = 0; c0 < cs; c0 += kc) {
+    const int nk = min(cs, c0 + kc) - c0;
     if (c0 > 0) __syncthreads();  // previous chunk's digits fully consumed
     // Phase 1.
-    gemv_digits<MR, QPG>(a, K, vec, c0, nk, kc, sdig, salpha, srsum, t, nthr);
+    gemv_digits<MR, QPG>(a, K, vec, kb + c0, nk, kc, sdig, salpha, srsum, t, nthr);
     __syncthreads();
 
     // Phase 2: this wave's k groups inside the chunk.  The ring slot of the
@@ -461,10 +469,11 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
       for (int i = 0; i < PF; i++) {
         const int nn = n + i;
         if (nn >= nend) break;
-        const int kg = wave + nn * NW;
+        const int kl = wave + nn * NW;  // within the split
         const GemvSlot<QPG, ZPK> cur = ring[i];
-        if (nn + PF < nmine) gemv_issue(ring[i], wp, sp, zq, zfp, wave + (nn + PF) * NW, nb, lbs);
-        gemv_kgroup<MR, QPG, ZPK>(cur, kg, kg - c0, kc, nb, lbs, sdig, salpha, srsum, yacc);
+        if (nn + PF < nmine)
+          gemv_issue(ring[i], wp, sp, zq, zfp, kb + wave + (nn + PF) * NW, nb, lbs);
+        gemv_kgroup<MR, QPG, ZPK>(cur, kb + kl, kl - c0, kc, nb, lbs, sdig, salpha, srsum, yacc);
       }
     }
   }
@@ -481,14 +490,18 @@ __global__ __launch_bounds__(PF == 4 ? 256 : 1024) void k_gemv_dot8(
     for (int r = 0; r < MR; r++) {
       // All NW wave sums are read before the ordered adds, so the LDS reads
       // overlap (NW <= 16; the launch bounds allow no more).
-      float part[16];
+      float wsum[16];
 #pragma unroll
-      for (int w = 0; w < 16; w++) part[w] = w < NW ? red[(w * MR + r) * 64 + lane] : 0.f;
-      float s = part[0];
+      for (int w = 0; w < 16; w++) wsum[w] = w < NW ? red[(w * MR + r) * 64 + lane] : 0.f;
+      float s = wsum[0];
 #pragma unroll
       for (int w = 1; w < 16; w++)
-        if (w < NW) s += part[w];
-      if (col < N) y[(int64_t)r * N + col] = s + (bias ? bias[col] : 0.f);
+        if (w < NW) s += wsum[w];
+      if (col >= N) continue;
+      if (part)
+        part[gs.part_off[gm] + ((int64_t)blockIdx.y * MR + r) * N + col] = s;
+      else
+        y[(int64_t)r * N + col] = s + (bias ? bias[col] : 0.f);
     }
   }
 }
@@ -1403,22 +1416,42 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
 #ifndef MG_GEMV_MAX_NW
 #define MG_GEMV_MAX_NW 16
 #endif
+    // One row, blocks <= 64, K >= 4096 and fewer than half a column group
+    // per CU: K is also split over workgroups (kps k groups each, at least
+    // 4) until the grid covers the CUs, and an ordered sum of the splits'
+    // partials adds the bias (k_gemm_reduce): a CU streams at most ~100
+    // GB/s, so a long narrow weight must spread over many CUs.  (Llama down
+    // 8192 x 2048: 14.2 -> 8.1 us with the sum; at K = 2048 the extra launch
+    // costs more than the spread gains.)
+#ifndef MG_GEMV_SPLIT
+#define MG_GEMV_SPLIT 1
+#endif
+    const int64_t cus = std::max(ctx->num_cus, 1);
+    int64_t kspan = d.c4;
+    if (MG_GEMV_SPLIT && M == 1 && p.qpg >= 2 && ng_total * 2 < cus && d.c4 >= 32) {
+      int64_t ks = 1;
+      while (ng_total * ks * 2 <= cus && d.c4 / (ks * 2) >= 4) ks *= 2;
+      if (ks > 1) {
+        p.kps = (int)((d.c4 + ks - 1) / ks);
+        p.ksplit = (int)((d.c4 + p.kps - 1) / p.kps);
+        kspan = p.kps;
+      }
+    }
     int64_t nw = 4;
-    if (M == 1 && p.qpg >= 2 && ng_total * 4 < 8 * (int64_t)std::max(ctx->num_cus, 1))
-      nw = MG_GEMV_MAX_NW;
-    nw = std::min<int64_t>(nw, std::max<int64_t>(d.c4, 4));
+    if (M == 1 && p.qpg >= 2 && ng_total * p.ksplit * 4 < 8 * cus) nw = MG_GEMV_MAX_NW;
+    nw = std::min<int64_t>(nw, std::max<int64_t>(kspan, 4));
     if (nw > 4) nw = nw > 8 ? 16 : 8;
     const int pf = nw == 4 ? 4 : 2;
     // Activation digits of a chunk of kc k groups live in LDS (<= 64 KiB); a
     // partial chunk size is a multiple of pf * nw.
     const int64_t per_kg = M * (64 + 2 * p.qpg) * 4;
     const int64_t kc_max = 65536 / per_kg;
-    int64_t kc = d.c4;
+    int64_t kc = kspan;
     if (kc > kc_max) kc = kc_max / (pf * nw) * (pf * nw);
     p.nw = (int)nw;
     p.kc = (int)kc;
     p.lds = (size_t)std::max<int64_t>(kc * per_kg, nw * M * 64 * 4);
-    p.total = 0;
+    p.total = p.ksplit > 1 ? mg_align((size_t)p.ksplit * M * n_total * 4) : 0;
     // One row, k groups that split evenly over 4 waves (1 or 2 each) and
     // enough column groups for several per workgroup: the persistent kernel,
     // with the column groups dealt evenly over about MG_GEMV_WG_PER_CU
@@ -1430,7 +1463,7 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
 #endif
     const int64_t slots = MG_GEMV_WG_PER_CU * (int64_t)std::max(ctx->num_cus, 1);
     const int64_t per_wave = d.c4 / 4;
-    if (M == 1 && nw == 4 && kc == d.c4 && d.c4 % 4 == 0 &&
+    if (M == 1 && p.ksplit == 1 && nw == 4 && kc == d.c4 && d.c4 % 4 == 0 &&
         (per_wave == 1 || per_wave == 2) &&
         ng_total >= 2 * slots) {
       const int64_t per = (ng_total + slots - 1) / slots;
@@ -1447,7 +1480,8 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
 #ifndef MG_GEMV_CS_MAX_CG
 #define MG_GEMV_CS_MAX_CG 96
 #endif
-    if (M == 1 && p.qpg == 1 && !p.pers && ng_total < MG_GEMV_CS_MAX_CG && kc == d.c4 &&
+    if (M == 1 && p.qpg == 1 && p.ksplit == 1 && !p.pers && ng_total < MG_GEMV_CS_MAX_CG &&
+        kc == d.c4 &&
         d.c4 <= 16 * CS_TASKS) {
       p.cs = 1;
       p.cs_pf = d.c4 > 16 ? 8 : 4;
@@ -1515,11 +1549,13 @@ GemvSet make_set(int n, const mg_weight *const *w, float *const *y) {
 
 template <int MR, int QPG>
 void launch_gemv_zp(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p,
-                    hipStream_t st, const float *a, int vec) {
+                    hipStream_t st, const float *a, int vec, float *part) {
   const mg_nbits_dev &d = w->nbits;
-  const dim3 grid((unsigned)gs.cg_end[gs.n - 1]), block((unsigned)(64 * p.nw));
-#define MG_GEMV_ARGS \
-  a, w->K, vec, gs, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), p.kc
+  const dim3 grid((unsigned)gs.cg_end[gs.n - 1], (unsigned)p.ksplit),
+      block((unsigned)(64 * p.nw));
+#define MG_GEMV_ARGS                                                                        \
+  a, w->K, vec, gs, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs), p.kc,       \
+      p.ksplit > 1 ? p.kps : (int)d.c4, p.ksplit > 1 ? part : nullptr
   // The 8/16-wave form (PF 2) is planned only for one row and QPG >= 2.
 #define MG_GEMV_LAUNCH(Z_)                                                                   \
   do {                                                                                       \
@@ -1587,7 +1623,7 @@ void launch_gemv_cs(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, h
 
 template <int MR>
 void launch_gemv_q(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, hipStream_t st,
-                   const float *a, int vec) {
+                   const float *a, int vec, float *part) {
   if (MR == 1 && p.cs) {
     launch_gemv_cs(w, gs, p, st, a, vec);
     return;
@@ -1602,10 +1638,10 @@ void launch_gemv_q(const mg_weight *w, const GemvSet &gs, const NbitsPlan &p, hi
     return;
   }
   switch (p.qpg) {
-    case 1: launch_gemv_zp<MR, 1>(w, gs, p, st, a, vec); break;
-    case 2: launch_gemv_zp<MR, 2>(w, gs, p, st, a, vec); break;
-    case 4: launch_gemv_zp<MR, 4>(w, gs, p, st, a, vec); break;
-    default: launch_gemv_zp<MR, 8>(w, gs, p, st, a, vec); break;
+    case 1: launch_gemv_zp<MR, 1>(w, gs, p, st, a, vec, part); break;
+    case 2: launch_gemv_zp<MR, 2>(w, gs, p, st, a, vec, part); break;
+    case 4: launch_gemv_zp<MR, 4>(w, gs, p, st, a, vec, part); break;
+    default: launch_gemv_zp<MR, 8>(w, gs, p, st, a, vec, part); break;
   }
 }
 
@@ -1848,15 +1884,33 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
   hipStream_t st = ctx->stream;
   char *base = static_cast<char *>(ws);
   if (p.path == 0) {
-    const GemvSet gs = make_set(n, w, y_dev);
+    GemvSet gs = make_set(n, w, y_dev);
     const int vec = (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 && w0->K % 4 == 0) ? 1 : 0;
-    switch (M) {
-      case 1: launch_gemv_q<1>(w0, gs, p, st, a_dev, vec); break;
-      case 2: launch_gemv_q<2>(w0, gs, p, st, a_dev, vec); break;
-      case 3: launch_gemv_q<3>(w0, gs, p, st, a_dev, vec); break;
-      default: launch_gemv_q<4>(w0, gs, p, st, a_dev, vec); break;
+    float *part = reinterpret_cast<float *>(base);
+    ReduceSet rs{};
+    int64_t eend = 0;
+    if (p.ksplit > 1) {
+      rs.n = n;
+      int64_t poff = 0;
+      for (int i = 0; i < n; i++) {
+        gs.part_off[i] = rs.part_off[i] = poff;
+        poff += (int64_t)p.ksplit * M * w[i]->N;
+        eend += M * w[i]->N;
+        rs.e_end[i] = eend;
+        rs.bias[i] = w[i]->nbits.bias;
+        rs.y[i] = y_dev[i];
+        rs.N[i] = (int)w[i]->N;
+      }
     }
-    return mg_launch_check("k_gemv_dot8");
+    switch (M) {
+      case 1: launch_gemv_q<1>(w0, gs, p, st, a_dev, vec, part); break;
+      case 2: launch_gemv_q<2>(w0, gs, p, st, a_dev, vec, part); break;
+      case 3: launch_gemv_q<3>(w0, gs, p, st, a_dev, vec, part); break;
+      default: launch_gemv_q<4>(w0, gs, p, st, a_dev, vec, part); break;
+    }
+    MG_TRY(mg_launch_check("k_gemv_dot8"));
+    if (p.ksplit > 1) return launch_gemm_reduce(st, part, rs, eend, p.ksplit);
+    return MG_OK;
   }
   if (p.path == 3) {
     const GemvSet gs = make_set(n, w, y_dev);

@@ -531,6 +531,35 @@ def test_m1_gemv_plans_agree_bitwise(ops, k, bs, zp_mode):
     assert G.rms_error(full[2][:, :1000], ref) <= TOL
 
 
+SPLIT_K = [
+    # (K, N, bs, zp_mode, bias): one row, blocks <= 64, K >= 4096 and few
+    # column groups: K split over workgroups, partials summed in split order
+    # with the bias.
+    (4100, 300, 16, "packed", True),
+    (4200, 130, 64, "float", True),
+    (8192, 100, 32, "none", False),
+    (4096, 2048, 32, "packed", True),
+    (5000, 70, 32, "packed", False),
+]
+
+
+@pytest.mark.parametrize("k,n,bs,zp_mode,with_bias", SPLIT_K)
+def test_m1_split_k_against_oracle(ops, k, n, bs, zp_mode, with_bias):
+    rng = np.random.default_rng(0x5EED0060 + k + n + bs)
+    b, s, zp = make_nbits(rng, n, k, bs, zp_mode)
+    bias = rng.standard_normal(n).astype(np.float32) if with_bias else None
+    a = rng.standard_normal((1, k)).astype(np.float32)
+    a[0, k // 2] = 50.0
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    y = w(a)
+    np.testing.assert_array_equal(w(a), y)
+    ref = oracle.matmul_nbits(a, b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    assert G.rms_error(y, ref) <= TOL, G.rms_error(y, ref)
+    a[0, 7] = np.nan  # a non-finite activation reaches every column through the sum
+    assert np.isnan(w(a)).all()
+    w.release()
+
+
 def test_profiling_records_each_op(ops):
     # Per-op device timing (the ABI's part of ExecutionProfile): one record
     # per op entry, in issue order, with the reference's op-type names.
