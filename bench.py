@@ -449,6 +449,7 @@ def main():
     if not args.quick:
         result["decode_sweep"] = decode_sweep(torch, ops, ctx, T, randn, dev, args, stream)
         result["int8_prefill"] = int8_prefill(torch, ops, ctx, T, dev, args)
+        result["nbits_float_zp_prefill"] = nbits_float_zp(torch, ops, ctx, T, randn, dev, args)
         result["f32_encoder"] = f32_encoder(torch, ops, ctx, T, randn, dev, args)
         result["conv"] = conv_family(torch, ops, ctx, T, randn, dev, args)
         result["gqa"] = gqa_steps(torch, ops, ctx, T, randn, dev)
@@ -536,6 +537,28 @@ def decode_sweep(torch, ops, ctx, T, randn, dev, args, stream):
                         "lm_head_GB/s": round(hb / (ms_head / 1e3) / 1e9, 1)}
         print(f"# decode M={m}: {out[f'M{m}']}", file=sys.stderr, flush=True)
     for w in ws:
+        w.release()
+    return out
+
+
+def nbits_float_zp(torch, ops, ctx, T, randn, dev, args):
+    """MatMulNBits with float zero points (the form some exporters write) at
+    M = 512 on the Qwen3 gate and lm_head shapes: columns dequantised to fp32
+    in chunks and run on the fp32 MFMA GEMM."""
+    rng = np.random.default_rng(0x5EED0004)
+    out = {}
+    for name, k, n in (("gate", 1024, 3072), ("lm_head", 1024, 151936)):
+        nb = k // BLOCK
+        b = np.frombuffer(rng.bytes(n * nb * BLOCK // 2), np.uint8).reshape(n, nb, BLOCK // 2)
+        s = rng.uniform(0.002, 0.02, (n, nb)).astype(np.float32)
+        zp = (rng.standard_normal((n, nb)) + 8).astype(np.float32)
+        w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=BLOCK, ctx=ctx)
+        a = randn(M_PREFILL, k)
+        y = torch.empty((M_PREFILL, n), device=dev, dtype=torch.float32)
+        ms = T.loop(lambda: w.run_dev(a.data_ptr(), M_PREFILL, y.data_ptr()),
+                    max(args.steps // 2, 5), 2)
+        out[name] = {"shape": [M_PREFILL, k, n], "ms": round(ms, 4),
+                     "TFLOP/s": round(2.0 * M_PREFILL * k * n / (ms / 1e3) / 1e12, 2)}
         w.release()
     return out
 

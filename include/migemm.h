@@ -522,6 +522,45 @@ mg_status mg_qlinear_conv_dev(
     const int64_t *strides, const int64_t *pads, const int64_t *dilations,
     int32_t group, int32_t lo, int32_t hi, uint8_t *y_dev);
 
+/* ------------------------------------------------------- elementwise ops */
+
+/* The elementwise ops between the products of a decoder layer, on device
+ * buffers (asynchronous on the context's stream), so activations stay in HBM
+ * from one product to the next.  f32 in, f32 out. */
+typedef enum mg_binary_op {
+  MG_BIN_ADD = 0, /* opAdd, lib/src/onnx_ops.dart:402-404 */
+  MG_BIN_SUB = 1, /* opSub, :444-446 */
+  MG_BIN_MUL = 2, /* opMul, :447-449 */
+  MG_BIN_DIV = 3  /* opDiv on floats, :476 */
+} mg_binary_op;
+
+/* y = a op b with broadcasting (_broadcastShape, lib/src/onnx_ops.dart:26-44;
+ * _arithFloatFast / _elementwiseBinary, :103-330): shapes right-aligned,
+ * y holds the broadcast shape (rank max(a_rank, b_rank)).  Incompatible
+ * shapes: MG_INVALID_ARGUMENT "Cannot broadcast shapes [..] and [..]"
+ * (ArgumentError); ranks up to 16.  y may be a_dev or b_dev when that
+ * operand has the output's shape (an in-place residual add). */
+mg_status mg_binary_f32_dev(mg_ctx *ctx, int32_t op, const float *a_dev,
+                            const int64_t *a_shape, int32_t a_rank, const float *b_dev,
+                            const int64_t *b_shape, int32_t b_rank, float *y_dev);
+/* opSigmoid (lib/src/onnx_ops.dart:2349-2350): 1 / (1 + exp(-x)) in double. */
+mg_status mg_sigmoid_f32_dev(mg_ctx *ctx, const float *x_dev, int64_t n, float *y_dev);
+/* opRMSNorm (lib/src/onnx_ops.dart:1771-1815), the op behind _FusedRMSNorm and
+ * SimplifiedLayerNormalization (lib/src/onnx_graph.dart:1640-1649,
+ * :1783-1792): x * rsqrt(mean(x^2, axis) + epsilon) * gamma, gamma along the
+ * last axis.  gamma_len != last dim: MG_INVALID_ARGUMENT ("RMSNorm gamma
+ * length .. != last dim .."). */
+mg_status mg_rms_norm_f32_dev(mg_ctx *ctx, const float *x_dev, const int64_t *shape,
+                              int32_t rank, const float *gamma_dev, int64_t gamma_len,
+                              int64_t axis, double epsilon, float *y_dev);
+/* SkipSimplifiedLayerNormalization (lib/src/onnx_graph.dart:1793-1813):
+ * sum = x + skip (equal shapes), y = RMSNorm(sum, gamma, last axis) (+ bias
+ * when bias_dev is not null); sum_dev (may be null) receives sum. */
+mg_status mg_skip_rms_norm_f32_dev(mg_ctx *ctx, const float *x_dev, const float *skip_dev,
+                                   const int64_t *shape, int32_t rank, const float *gamma_dev,
+                                   int64_t gamma_len, const float *bias_dev, double epsilon,
+                                   float *y_dev, float *sum_dev);
+
 /* ----------------------------------------------------------------- weights */
 
 mg_status mg_weight_release(mg_weight *w);

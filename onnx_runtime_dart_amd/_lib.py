@@ -58,6 +58,10 @@ SIGNATURES = {
                                 _I32, _I32, _P],
     "mg_dynamic_quantize_linear": [_P, _P, _I64, _P, _P, _P],
     "mg_dynamic_quantize_linear_dev": [_P, _P, _I64, _P, _P],
+    "mg_binary_f32_dev": [_P, _I32, _P, _P, _I32, _P, _P, _I32, _P],
+    "mg_sigmoid_f32_dev": [_P, _P, _I64, _P],
+    "mg_rms_norm_f32_dev": [_P, _P, _P, _I32, _P, _I64, _I64, C.c_double, _P],
+    "mg_skip_rms_norm_f32_dev": [_P, _P, _P, _P, _I32, _P, _I64, _P, C.c_double, _P, _P],
     "mg_matmul_integer_w_dq_dev": [_P, _P, _I64, _I64, _P, _P, _P],
     "mg_qlinear_matmul_w_dq_dev": [_P, _P, _I64, _I64, _P, _P, _F, _F, _I32, _I32, _I32, _P],
     "mg_fused_sdpa": [_P, _P, _P, _I32, _P, _P, _I32, _P, _P, _I32, _P, _P, _I32, _F, _P],

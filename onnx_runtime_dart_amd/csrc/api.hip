@@ -2232,3 +2232,162 @@ mg_status mg_group_query_attention_dev(
   return gqa_run(ctx, p, g, q_dev, do_rotary ? static_cast<float *>(ctx->ws) : nullptr,
                  attention_bias_dev, y_dev);
 }
+
+// ------------------------------------------------------- elementwise ops
+
+namespace {
+
+// A shape as the reference prints a Dart List<int>: "[2, 3, 4]".
+std::string dart_list(const int64_t *s, int32_t r) {
+  std::string o = "[";
+  for (int32_t i = 0; i < r; i++) o += (i ? ", " : "") + std::to_string(s[i]);
+  return o + "]";
+}
+
+}  // namespace
+
+extern "C" {
+
+mg_status mg_binary_f32_dev(mg_ctx *ctx, int32_t op, const float *a_dev,
+                            const int64_t *a_shape, int32_t a_rank, const float *b_dev,
+                            const int64_t *b_shape, int32_t b_rank, float *y_dev) {
+  static const char *names[] = {"Add", "Sub", "Mul", "Div"};
+  ProfScope prof_(ctx, op >= 0 && op <= 3 ? names[op] : "Elementwise");
+  g_last_error.clear();
+  if (!ctx || op < 0 || op > 3 || !shape_ok(a_shape, a_rank) || !shape_ok(b_shape, b_rank))
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_binary_f32_dev: invalid argument");
+  // Right-aligned broadcast (_broadcastShape).
+  const int32_t rank = std::max(a_rank, b_rank);
+  std::vector<int64_t> ad(rank), bd(rank), od(rank);
+  for (int32_t k = 0; k < rank; k++) {
+    ad[k] = k - (rank - a_rank) >= 0 ? a_shape[k - (rank - a_rank)] : 1;
+    bd[k] = k - (rank - b_rank) >= 0 ? b_shape[k - (rank - b_rank)] : 1;
+    if (ad[k] == bd[k]) od[k] = ad[k];
+    else if (ad[k] == 1) od[k] = bd[k];
+    else if (bd[k] == 1) od[k] = ad[k];
+    else
+      return mg_fail(MG_INVALID_ARGUMENT, "Cannot broadcast shapes " +
+                                              dart_list(a_shape, a_rank) + " and " +
+                                              dart_list(b_shape, b_rank));
+  }
+  int64_t n = 1;
+  for (int32_t k = 0; k < rank; k++) n *= od[k];
+  if (n == 0) return MG_OK;
+  if (!a_dev || !b_dev || !y_dev)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_binary_f32_dev: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, 0));
+  const bool same = ad == bd;
+  mg_elem_bcast s{};
+  if (!same) {
+    // Row-major strides of each operand over the output dims (0 where it
+    // broadcasts); size-1 output dims dropped, then neighbours merged while
+    // both operands stay contiguous (or both broadcast) across them.
+    std::vector<int64_t> dims, sa, sb;
+    int64_t ra = 1, rb = 1;
+    std::vector<int64_t> fa(rank), fb(rank);
+    for (int32_t k = rank - 1; k >= 0; k--) {
+      fa[k] = ad[k] == 1 ? 0 : ra;
+      fb[k] = bd[k] == 1 ? 0 : rb;
+      ra *= ad[k];
+      rb *= bd[k];
+    }
+    for (int32_t k = 0; k < rank; k++) {
+      if (od[k] == 1) continue;
+      if (!dims.empty() && sa.back() == fa[k] * od[k] && sb.back() == fb[k] * od[k]) {
+        dims.back() *= od[k];
+        sa.back() = fa[k];
+        sb.back() = fb[k];
+      } else {
+        dims.push_back(od[k]);
+        sa.push_back(fa[k]);
+        sb.push_back(fb[k]);
+      }
+    }
+    s.rank = (int)dims.size();
+    for (int k = 0; k < s.rank; k++) {
+      s.dim[k] = dims[k];
+      s.sa[k] = sa[k];
+      s.sb[k] = sb[k];
+    }
+  }
+  return mg_elem_binary(ctx, op, a_dev, b_dev, y_dev, n, same, s);
+}
+
+mg_status mg_sigmoid_f32_dev(mg_ctx *ctx, const float *x_dev, int64_t n, float *y_dev) {
+  ProfScope prof_(ctx, "Sigmoid");
+  g_last_error.clear();
+  if (!ctx || n < 0 || (n > 0 && (!x_dev || !y_dev)))
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_sigmoid_f32_dev: invalid argument");
+  if (n == 0) return MG_OK;
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, 0));
+  return mg_elem_sigmoid(ctx, x_dev, y_dev, n);
+}
+
+}  // extern "C"
+
+namespace {
+
+mg_status rms_common(mg_ctx *ctx, const char *what, const float *x_dev, const int64_t *shape,
+                     int32_t rank, const float *gamma_dev, int64_t gamma_len, int64_t axis,
+                     int64_t *outer, int64_t *dim, int64_t *inner) {
+  if (!ctx || !shape_ok(shape, rank) || rank < 1)
+    return mg_fail(MG_INVALID_ARGUMENT, std::string(what) + ": invalid argument");
+  const int64_t ax = axis < 0 ? axis + rank : axis;
+  if (ax < 0 || ax >= rank)
+    return mg_fail(MG_INVALID_ARGUMENT, std::string(what) + ": axis out of range");
+  if (gamma_len != shape[rank - 1])
+    return mg_fail(MG_INVALID_ARGUMENT, "RMSNorm gamma length " + std::to_string(gamma_len) +
+                                            " != last dim " + std::to_string(shape[rank - 1]));
+  *outer = 1;
+  *inner = 1;
+  for (int64_t k = 0; k < ax; k++) *outer *= shape[k];
+  for (int64_t k = ax + 1; k < rank; k++) *inner *= shape[k];
+  *dim = shape[ax];
+  if (*outer * *dim * *inner > 0 && (!x_dev || !gamma_dev))
+    return mg_fail(MG_INVALID_ARGUMENT, std::string(what) + ": null buffer");
+  if (*inner == 1 && *outer > INT32_MAX)
+    return mg_fail(MG_UNSUPPORTED, std::string(what) + ": more than 2^31 rows");
+  return MG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+mg_status mg_rms_norm_f32_dev(mg_ctx *ctx, const float *x_dev, const int64_t *shape,
+                              int32_t rank, const float *gamma_dev, int64_t gamma_len,
+                              int64_t axis, double epsilon, float *y_dev) {
+  ProfScope prof_(ctx, "RMSNorm");
+  g_last_error.clear();
+  int64_t outer, dim, inner;
+  MG_TRY(rms_common(ctx, "mg_rms_norm_f32_dev", x_dev, shape, rank, gamma_dev, gamma_len, axis,
+                    &outer, &dim, &inner));
+  if (outer * dim * inner == 0) return MG_OK;
+  if (!y_dev) return mg_fail(MG_INVALID_ARGUMENT, "mg_rms_norm_f32_dev: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, 0));
+  return mg_elem_rms_norm(ctx, x_dev, nullptr, gamma_dev, nullptr, epsilon, outer, dim, inner,
+                          shape[rank - 1], y_dev, nullptr);
+}
+
+mg_status mg_skip_rms_norm_f32_dev(mg_ctx *ctx, const float *x_dev, const float *skip_dev,
+                                   const int64_t *shape, int32_t rank, const float *gamma_dev,
+                                   int64_t gamma_len, const float *bias_dev, double epsilon,
+                                   float *y_dev, float *sum_dev) {
+  ProfScope prof_(ctx, "SkipSimplifiedLayerNormalization");
+  g_last_error.clear();
+  int64_t outer, dim, inner;
+  MG_TRY(rms_common(ctx, "mg_skip_rms_norm_f32_dev", x_dev, shape, rank, gamma_dev, gamma_len,
+                    -1, &outer, &dim, &inner));
+  if (outer * dim == 0) return MG_OK;
+  if (!skip_dev || !y_dev)
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_skip_rms_norm_f32_dev: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, 0));
+  return mg_elem_rms_norm(ctx, x_dev, skip_dev, gamma_dev, bias_dev, epsilon, outer, dim, 1,
+                          dim, y_dev, sum_dev);
+}
+
+}  // extern "C"

@@ -22,7 +22,8 @@ ROOT = PKG.parent
 BUILD = CSRC / "_build"
 LIB = PKG / "lib" / "libmigemm.so"
 
-SOURCES = ["api.hip", "nbits.hip", "nbits_f8.hip", "int8.hip", "f32.hip", "dql.hip", "attn.hip", "conv.hip"]
+SOURCES = ["api.hip", "nbits.hip", "nbits_f8.hip", "int8.hip", "f32.hip", "dql.hip", "attn.hip", "conv.hip",
+           "elem.hip"]
 
 # Packed fp32 VALU forms are disabled (-packed-fp32-ops); the compiler still
 # schedules plain fp32 and the MFMA units.

@@ -1,0 +1,197 @@
+// Elementwise device ops between the matrix products of a decoder layer, so
+// that its activations stay in HBM from one product to the next:
+//   * Add / Sub / Mul / Div of float tensors with broadcasting
+//     (lib/src/onnx_ops.dart:26-44, :103-330, :402, :444-448, :476);
+//   * Sigmoid (lib/src/onnx_ops.dart:2349-2350);
+//   * RMSNorm (opRMSNorm, lib/src/onnx_ops.dart:1771-1815) and the residual
+//     add + RMSNorm of SkipSimplifiedLayerNormalization
+//     (lib/src/onnx_graph.dart:1793-1813).
+//
+// Numbers.  The reference computes each op in double and stores f32; for
+// + - * / of two f32 values that equals the correctly rounded f32 op (53 >=
+// 2 * 24 + 2 bits), which is what these kernels compute.  Sigmoid and the
+// RMSNorm scale are computed in double as the reference does; the RMSNorm
+// sum of squares is a fixed-order parallel double sum (the reference adds in
+// k order: the two differ only by double rounding, far below an f32 ulp).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "mg_internal.h"
+
+namespace {
+
+template <int OP>
+__device__ inline float bin_op(float x, float y) {
+  if (OP == MG_BIN_ADD) return x + y;
+  if (OP == MG_BIN_SUB) return x - y;
+  if (OP == MG_BIN_MUL) return x * y;
+  return x / y;
+}
+
+// Equal shapes: four elements per thread (VEC: 16-byte aligned operands).
+// y may be a or b (each element is read before it is written).
+template <int OP, bool VEC>
+__global__ __launch_bounds__(256) void k_bin_same(const float *a, const float *b, float *y,
+                                                  int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  if (VEC && i + 4 <= n) {
+    const float4 x = *reinterpret_cast<const float4 *>(a + i);
+    const float4 v = *reinterpret_cast<const float4 *>(b + i);
+    *reinterpret_cast<float4 *>(y + i) = make_float4(bin_op<OP>(x.x, v.x), bin_op<OP>(x.y, v.y),
+                                                     bin_op<OP>(x.z, v.z), bin_op<OP>(x.w, v.w));
+  } else {
+    for (int64_t k = i; k < std::min<int64_t>(i + 4, n); k++) y[k] = bin_op<OP>(a[k], b[k]);
+  }
+}
+
+// Broadcast: output element -> coordinates over the merged output dims ->
+// operand offsets (stride 0 along broadcast dims).
+template <int OP>
+__global__ __launch_bounds__(256) void k_bin_bcast(const float *a, const float *b, float *y,
+                                                   int64_t n, const mg_elem_bcast s) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  int64_t rem = i, ia = 0, ib = 0;
+#pragma unroll
+  for (int k = MG_ELEM_MAXRANK - 1; k >= 0; k--) {
+    if (k >= s.rank) continue;
+    const int64_t c = rem % s.dim[k];
+    rem /= s.dim[k];
+    ia += c * s.sa[k];
+    ib += c * s.sb[k];
+  }
+  y[i] = bin_op<OP>(a[ia], b[ib]);
+}
+
+__global__ __launch_bounds__(256) void k_sigmoid(const float *__restrict__ x,
+                                                 float *__restrict__ y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  y[i] = (float)(1.0 / (1.0 + exp(-(double)x[i])));
+}
+
+// Fixed-order double sum over the 256 threads of a workgroup (shuffles within
+// each wave, then the four wave sums in wave order).  Every thread gets it.
+__device__ inline double block_sum(double v, double *red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  const int t = threadIdx.x;
+  __syncthreads();  // red may still be read from a previous call
+  if ((t & 63) == 0) red[t >> 6] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// RMSNorm over the last axis: one workgroup per row of d elements.  With a
+// skip input the row is s = x + skip (f32), written to sum when asked; with
+// a bias, out = normed + bias (f32), as the reference's Add after the norm.
+__global__ __launch_bounds__(256) void k_rms_last(const float *__restrict__ x,
+                                                  const float *__restrict__ skip,
+                                                  const float *__restrict__ gamma,
+                                                  const float *__restrict__ bias, double eps,
+                                                  int64_t d, float *__restrict__ y,
+                                                  float *__restrict__ sum) {
+  __shared__ double red[4];
+  const int64_t base = (int64_t)blockIdx.x * d;
+  const int t = threadIdx.x;
+  double ss = 0;
+  for (int64_t j = t; j < d; j += 256) {
+    float v = x[base + j];
+    if (skip) {
+      v = v + skip[base + j];
+      if (sum) sum[base + j] = v;
+    }
+    ss += (double)v * (double)v;
+  }
+  ss = block_sum(ss, red);
+  const double inv = 1.0 / sqrt(ss / (double)d + eps);
+  for (int64_t j = t; j < d; j += 256) {
+    float v = x[base + j];
+    if (skip) v = v + skip[base + j];
+    float o = (float)((double)v * inv * (double)gamma[j]);
+    if (bias) o = o + bias[j];
+    y[base + j] = o;
+  }
+}
+
+// RMSNorm over another axis: one thread per (outer, inner) slice, walking the
+// reduce axis in order as the reference does; gamma follows the last axis.
+__global__ __launch_bounds__(256) void k_rms_axis(const float *__restrict__ x,
+                                                  const float *__restrict__ gamma, double eps,
+                                                  int64_t outer, int64_t dim, int64_t inner,
+                                                  int64_t last, float *__restrict__ y) {
+  const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (s >= outer * inner) return;
+  const int64_t o = s / inner, i = s % inner;
+  const int64_t base = o * dim * inner + i;
+  double ss = 0;
+  for (int64_t j = 0; j < dim; j++) {
+    const double v = x[base + j * inner];
+    ss += v * v;
+  }
+  const double inv = 1.0 / sqrt(ss / (double)dim + eps);
+  for (int64_t j = 0; j < dim; j++) {
+    const int64_t idx = base + j * inner;
+    y[idx] = (float)((double)x[idx] * inv * (double)gamma[idx % last]);
+  }
+}
+
+inline unsigned blocks(int64_t n, int64_t per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+mg_status mg_elem_binary(mg_ctx *ctx, int op, const float *a, const float *b, float *y,
+                         int64_t n, bool same, const mg_elem_bcast &s) {
+  if (n == 0) return MG_OK;
+  hipStream_t st = ctx->stream;
+  if (same) {
+    const bool vec = (reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                      reinterpret_cast<uintptr_t>(y)) % 16 == 0;
+#define MG_SAME(OP_)                                                                        \
+  if (vec) hipLaunchKernelGGL((k_bin_same<OP_, true>), dim3(blocks(n, 1024)), dim3(256), 0, st, \
+                              a, b, y, n);                                                  \
+  else hipLaunchKernelGGL((k_bin_same<OP_, false>), dim3(blocks(n, 1024)), dim3(256), 0, st, a, \
+                          b, y, n)
+    switch (op) {
+      case MG_BIN_ADD: MG_SAME(MG_BIN_ADD); break;
+      case MG_BIN_SUB: MG_SAME(MG_BIN_SUB); break;
+      case MG_BIN_MUL: MG_SAME(MG_BIN_MUL); break;
+      default: MG_SAME(MG_BIN_DIV); break;
+    }
+#undef MG_SAME
+    return mg_launch_check("k_bin_same");
+  }
+#define MG_BC(OP_) \
+  hipLaunchKernelGGL((k_bin_bcast<OP_>), dim3(blocks(n, 256)), dim3(256), 0, st, a, b, y, n, s)
+  switch (op) {
+    case MG_BIN_ADD: MG_BC(MG_BIN_ADD); break;
+    case MG_BIN_SUB: MG_BC(MG_BIN_SUB); break;
+    case MG_BIN_MUL: MG_BC(MG_BIN_MUL); break;
+    default: MG_BC(MG_BIN_DIV); break;
+  }
+#undef MG_BC
+  return mg_launch_check("k_bin_bcast");
+}
+
+mg_status mg_elem_sigmoid(mg_ctx *ctx, const float *x, float *y, int64_t n) {
+  if (n == 0) return MG_OK;
+  hipLaunchKernelGGL(k_sigmoid, dim3(blocks(n, 256)), dim3(256), 0, ctx->stream, x, y, n);
+  return mg_launch_check("k_sigmoid");
+}
+
+mg_status mg_elem_rms_norm(mg_ctx *ctx, const float *x, const float *skip, const float *gamma,
+                           const float *bias, double eps, int64_t outer, int64_t dim,
+                           int64_t inner, int64_t last, float *y, float *sum) {
+  if (outer * dim * inner == 0) return MG_OK;
+  if (inner == 1) {  // the caller keeps rows (outer) below 2^31
+    hipLaunchKernelGGL(k_rms_last, dim3((unsigned)outer), dim3(256), 0, ctx->stream, x, skip,
+                       gamma, bias, eps, dim, y, sum);
+    return mg_launch_check("k_rms_last");
+  }
+  hipLaunchKernelGGL(k_rms_axis, dim3(blocks(outer * inner, 256)), dim3(256), 0, ctx->stream, x,
+                     gamma, eps, outer, dim, inner, last, y);
+  return mg_launch_check("k_rms_axis");
+}

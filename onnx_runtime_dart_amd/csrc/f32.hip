@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
     float *__restrict__ Y, int64_t M, int64_t N, int64_t K, int64_t lda,
     int64_t ldb, int vec_a, int vec_b,
     const mg_f32_bcast bc, uint32_t z0, int nx, int pr, int pc, float alpha, float beta,
-    const float *__restrict__ C, int64_t c_rs, int64_t c_cs) {
+    const float *__restrict__ C, int64_t c_rs, int64_t c_cs, int64_t ldy) {
   constexpr int T = 64 * WT, LDX = KS + 4, NS = KS / 2;
   __shared__ float As[2][T * LDX];
   __shared__ float Bs[2][T * LDX];
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
 
   // Lane l holds column l % 32 and rows 8 (v / 4) + 4 (l / 32) + v % 4 of
   // each 32 x 32 tile; 32 lanes write 128 contiguous bytes per store.
-  float *Yb = Y + (int64_t)bz * M * N;
+  float *Yb = Y + (int64_t)bz * M * ldy;
 #pragma unroll
   for (int i = 0; i < WT; i++)
 #pragma unroll
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
           if (beta != 1.f) cv = beta * cv;
           y = y + cv;
         }
-        Yb[row * N + col] = y;
+        Yb[row * ldy + col] = y;
       }
     }
 }
@@ -214,7 +214,7 @@ void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float 
                 int pc) {
 #define MG_F32_ARGS                                                                         \
   a, b, y, p.M, p.N, p.K, p.lda, p.ldb, vec_a, vec_b, p.bc, z0, nx, pr, pc, p.alpha, p.beta, \
-      p.c, p.c_rs, p.c_cs
+      p.c, p.c_rs, p.c_cs, p.ldy ? p.ldy : p.N
   const bool akr = p.trans_a != 0, bkr = p.trans_b == 0;
   if (!akr && !bkr)
     hipLaunchKernelGGL((k_f32_gemm<WT, KS, false, false>), grid, dim3(256), 0, st, MG_F32_ARGS);

@@ -253,9 +253,30 @@ struct mg_f32_problem {
   float alpha, beta;
   const float *c;        // null or device C
   int64_t c_rs, c_cs;    // element strides of C over rows / cols (0 = bcast)
+  int64_t ldy = 0;       // row stride of Y (0: N; batches then lie M * ldy apart)
 };
 mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
                      const float *b_dev, float *y_dev);
+
+// ------------------------------------------------------- elementwise ops
+
+// Broadcast operand strides over the merged output dims (stride 0 along a
+// broadcast dim), innermost last.
+constexpr int MG_ELEM_MAXRANK = 16;  // every rank the API takes
+struct mg_elem_bcast {
+  int rank;
+  int64_t dim[MG_ELEM_MAXRANK];
+  int64_t sa[MG_ELEM_MAXRANK], sb[MG_ELEM_MAXRANK];
+};
+// y = a op b over n output elements; same: equal shapes (s unused).
+mg_status mg_elem_binary(mg_ctx *ctx, int op, const float *a, const float *b, float *y,
+                         int64_t n, bool same, const mg_elem_bcast &s);
+mg_status mg_elem_sigmoid(mg_ctx *ctx, const float *x, float *y, int64_t n);
+// RMSNorm over the middle dim of [outer][dim][inner]; skip / bias / sum only
+// with inner == 1 (the last axis).
+mg_status mg_elem_rms_norm(mg_ctx *ctx, const float *x, const float *skip, const float *gamma,
+                           const float *bias, double eps, int64_t outer, int64_t dim,
+                           int64_t inner, int64_t last, float *y, float *sum);
 
 // --------------------------------------------------------------- conv entry
 

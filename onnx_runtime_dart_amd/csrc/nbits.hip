@@ -1327,39 +1327,54 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   }
 }
 
-// ---------------------------------------------------------- generic path
+// ------------------------------------- float zero points, 16-k blocks
 
-// One thread per output; dequantises exactly as the reference (q - zp in
-// double times the f32 scale, one rounding) and accumulates in double.
-__global__ __launch_bounds__(256) void k_nbits_generic(
-    const float *__restrict__ a, const uint32_t *__restrict__ wq,
-    const float *__restrict__ scales, const uint8_t *__restrict__ zp4,
-    const float *__restrict__ zpf, int zpk, const float *__restrict__ bias,
-    float *__restrict__ y, int M, int N, int K, int c4n, int nb, int nbh,
-    int bs) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)M * N) return;
-  const int row = (int)(idx / N), col = (int)(idx % N);
-  const int cgi = col / 64, cg = col % 64;
-  double acc = 0.0;
-  for (int k = 0; k < K; k++) {
-    const int kg = k / KGRP, rem = k % KGRP;
-    const int j = rem / 32, g = (rem % 32) / 8, t = k % 8;
-    const uint32_t dw = wq[((((int64_t)cgi * c4n + kg) * 4 + g) * 64 + cg) * 4 + j];
-    const int q = (dw >> (4 * nib_pos(t))) & 15;
-    const int blk = k / bs;
+// Columns [n0, n0 + nc) of a packed weight dequantised to fp32 as the
+// reference does before its GEMM (onnx_qlinear_ops.dart:208-226): w = (q -
+// zp) * scale in double, one rounding to fp32.  Output row cl holds column
+// n0 + cl over all K (the [N][K] operand of the fp32 GEMM).  Thread = the 8
+// consecutive k of one packed dword: k = 128 kg + 8 o, o = 4 j + g.
+__global__ __launch_bounds__(256) void k_nbits_dequant_f32(
+    const uint32_t *__restrict__ wq, const float *__restrict__ scales,
+    const uint8_t *__restrict__ zp4, const float *__restrict__ zpf, int zpk, int64_t n0,
+    int64_t nc, int64_t K, int c4, int nb, int nbh, int bs, float *__restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= nc * c4 * 16) return;
+  const int o = (int)(idx & 15);
+  const int64_t rest = idx >> 4;
+  const int kg = (int)(rest % c4);
+  const int64_t cl = rest / c4;
+  const int64_t col = n0 + cl;
+  const int64_t cgi = col >> 6;
+  const int cg = (int)(col & 63);
+  const int j = o >> 2, g = o & 3;
+  const int64_t k0 = (int64_t)kg * KGRP + 8 * o;
+  if (k0 >= K) return;
+  const uint32_t dw = wq[((((int64_t)cgi * c4 + kg) * 4 + g) * 64 + cg) * 4 + j];
+  float v[8];
+#pragma unroll
+  for (int t = 0; t < 8; t++) {
+    const int64_t k = k0 + t;
+    const int q = (int)((dw >> (4 * nib_pos(t))) & 15);
+    const int64_t blk = min(k, K - 1) / bs;
     double z = 8.0;
     if (zpk == 1) {
-      const uint8_t zb = zp4[((int64_t)cgi * nbh + blk / 2) * 64 + sz_pos(cg)];
+      const uint8_t zb = zp4[(cgi * nbh + blk / 2) * 64 + sz_pos(cg)];
       z = (double)((blk & 1) ? (zb >> 4) : (zb & 15));
     } else if (zpk == 2) {
-      z = (double)zpf[((int64_t)cgi * nb + blk) * 64 + sz_pos(cg)];
+      z = (double)zpf[(cgi * nb + blk) * 64 + sz_pos(cg)];
     }
-    const float w =
-        (float)(((double)q - z) * (double)scales[((int64_t)cgi * nb + blk) * 64 + sz_pos(cg)]);
-    acc += (double)a[(int64_t)row * K + k] * (double)w;
+    v[t] = (float)(((double)q - z) * (double)scales[(cgi * nb + blk) * 64 + sz_pos(cg)]);
   }
-  y[idx] = (float)(acc + (bias ? (double)bias[col] : 0.0));
+  float *dst = out + cl * K + k0;
+  if (K % 4 == 0 && k0 + 8 <= K) {
+    *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4 *>(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+      if (k0 + t < K) dst[t] = v[t];
+  }
 }
 
 // ------------------------------------------------------------ host side
@@ -1384,6 +1399,7 @@ struct NbitsPlan {
   // mfma
   int64_t mpad = 0;
   int nt = 4;  // prefill tile width in 32-column MFMA tiles (4 or 2)
+  int64_t chunk = 0;  // fp32 path: columns dequantised per chunk
   int pers = 0;       // GEMV on the persistent kernel (k_gemv_dot8p)
   int pers_grid = 0;  // its workgroups
   int cs = 0;         // GEMV on the column-slice kernel (k_gemv_cs)
@@ -1399,7 +1415,10 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
   NbitsPlan p;
   p.M = M;
   const bool int_zp = d.zp_kind != MG_ZP_FLOAT;
-  if (M >= 3 && M <= 16 && d.bs >= 32 && int_zp) {
+#ifndef MG_DECODE_MFMA_MIN_M
+#define MG_DECODE_MFMA_MIN_M 3
+#endif
+  if (M >= MG_DECODE_MFMA_MIN_M && M <= 16 && d.bs >= 32 && int_zp) {
     p.path = 3;
     p.off_a = 0;  // ahl16: 16 rows x kpad x (hi, lo) fp16
     p.off_b = mg_align((size_t)16 * d.kpad * 4);  // texp[16]
@@ -1521,8 +1540,14 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
     }
     p.total = mg_align(p.off_c + (p.ksplit > 1 ? (size_t)p.ksplit * M * n_total * 4 : 0));
   } else {
+    // Float zero points or 16-k blocks with more rows: the columns are
+    // dequantised to fp32 in chunks of about 64 MiB and each chunk runs
+    // through the fp32 MFMA GEMM.
     p.path = 2;
-    p.total = 0;
+    const int64_t per_col = d.c4 * KGRP;  // floats a column takes (K rounded up)
+    p.chunk = std::max<int64_t>(64, ((int64_t)(16 << 20) / per_col) / 64 * 64);
+    p.chunk = std::min<int64_t>(p.chunk, (n_total + 63) / 64 * 64);
+    p.total = mg_align((size_t)p.chunk * per_col * 4);
   }
   return p;
 }
@@ -1867,8 +1892,8 @@ size_t mg_nbits_group_ws_bytes(const mg_ctx *ctx, int n, const mg_weight *const 
 }
 
 namespace {
-mg_status nbits_run_generic(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
-                            float *y_dev);
+mg_status nbits_run_f32(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
+                        float *y_dev, float *wd, int64_t chunk);
 mg_status prefill_run(mg_ctx *ctx, int n, const mg_weight *const *w, const float *a_dev,
                       int64_t M, float *const *y_dev, void *ws, const NbitsPlan &p);
 }  // namespace
@@ -1968,8 +1993,9 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
   if (p.path == 4)
     return mg_nbits_prefill_f8(ctx, n, w, a_dev, M, y_dev, ws, p.mpad, p.nt, p.ksplit, p.kps,
                                p.off_c);
-  // Generic form: one launch per weight.
-  for (int i = 0; i < n; i++) MG_TRY(nbits_run_generic(ctx, w[i], a_dev, M, y_dev[i]));
+  // Float zero points / 16-k blocks: one weight at a time.
+  for (int i = 0; i < n; i++)
+    MG_TRY(nbits_run_f32(ctx, w[i], a_dev, M, y_dev[i], static_cast<float *>(ws), p.chunk));
   return MG_OK;
 }
 
@@ -2032,14 +2058,35 @@ mg_status prefill_run(mg_ctx *ctx, int n, const mg_weight *const *w, const float
   return MG_OK;
 }
 
-mg_status nbits_run_generic(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
-                            float *y_dev) {
+mg_status nbits_run_f32(mg_ctx *ctx, const mg_weight *w, const float *a_dev, int64_t M,
+                        float *y_dev, float *wd, int64_t chunk) {
   const mg_nbits_dev &d = w->nbits;
-  const int64_t tot = M * w->N;
-  hipLaunchKernelGGL(k_nbits_generic, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
-                     ctx->stream, a_dev, d.wq, d.scales, d.zp4, d.zpf, (int)d.zp_kind, d.bias,
-                     y_dev, (int)M, (int)w->N, (int)w->K, (int)d.c4, (int)d.nb, (int)d.nbh,
-                     (int)d.bs);
-  return mg_launch_check("k_nbits_generic");
+  const int64_t N = w->N, K = w->K;
+  for (int64_t n0 = 0; n0 < N; n0 += chunk) {
+    const int64_t nc = std::min(chunk, N - n0);
+    const int64_t threads = nc * d.c4 * 16;
+    hipLaunchKernelGGL(k_nbits_dequant_f32, dim3((unsigned)((threads + 255) / 256)), dim3(256),
+                       0, ctx->stream, reinterpret_cast<const uint32_t *>(d.wq), d.scales,
+                       d.zp4, d.zpf, (int)d.zp_kind, n0, nc, K, (int)d.c4, (int)d.nb,
+                       (int)d.nbh, (int)d.bs, wd);
+    MG_TRY(mg_launch_check("k_nbits_dequant_f32"));
+    // Y[:, n0 : n0 + nc] = A * Wd^T (+ bias): Wd is [nc][K], row stride of Y is N.
+    mg_f32_problem q{};
+    q.M = M;
+    q.N = nc;
+    q.K = K;
+    q.batch = 1;
+    q.lda = K;
+    q.ldb = K;
+    q.trans_b = 1;
+    q.alpha = 1.f;
+    q.beta = 1.f;
+    q.c = d.bias ? d.bias + n0 : nullptr;
+    q.c_rs = 0;
+    q.c_cs = 1;
+    q.ldy = N;
+    MG_TRY(mg_f32_run(ctx, q, a_dev, wd, y_dev + n0));
+  }
+  return MG_OK;
 }
 }  // namespace

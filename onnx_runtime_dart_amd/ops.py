@@ -490,7 +490,129 @@ def dynamic_quantize_linear_dev(x_ptr: int, n: int, y_ptr: int, scale_zp_ptr: in
                                              C.c_void_p(y_ptr), C.c_void_p(scale_zp_ptr)))
 
 
+BINARY_OPS = {"add": 0, "sub": 1, "mul": 2, "div": 3}
+
+
+def binary_f32_dev(op: str, a_ptr: int, a_shape, b_ptr: int, b_shape, y_ptr: int,
+                   ctx: Context | None = None):
+    """opAdd / opSub / opMul / opDiv on device buffers with broadcasting
+    (lib/src/onnx_ops.dart:26-44, :103-330); y holds the broadcast shape."""
+    ctx = ctx or default_context()
+    sa = np.ascontiguousarray(np.array(a_shape, np.int64))
+    sb = np.ascontiguousarray(np.array(b_shape, np.int64))
+    check(lib.mg_binary_f32_dev(ctx.handle, BINARY_OPS[op], C.c_void_p(a_ptr), _ptr(sa), sa.size,
+                                C.c_void_p(b_ptr), _ptr(sb), sb.size, C.c_void_p(y_ptr)))
+
+
+def sigmoid_f32_dev(x_ptr: int, n: int, y_ptr: int, ctx: Context | None = None):
+    """opSigmoid (lib/src/onnx_ops.dart:2349) on a device buffer of n floats."""
+    ctx = ctx or default_context()
+    check(lib.mg_sigmoid_f32_dev(ctx.handle, C.c_void_p(x_ptr), int(n), C.c_void_p(y_ptr)))
+
+
+def rms_norm_f32_dev(x_ptr: int, shape, gamma_ptr: int, gamma_len: int, axis: int, eps: float,
+                     y_ptr: int, ctx: Context | None = None):
+    """opRMSNorm (lib/src/onnx_ops.dart:1771-1815) on device buffers."""
+    ctx = ctx or default_context()
+    sh = np.ascontiguousarray(np.array(shape, np.int64))
+    check(lib.mg_rms_norm_f32_dev(ctx.handle, C.c_void_p(x_ptr), _ptr(sh), sh.size,
+                                  C.c_void_p(gamma_ptr), int(gamma_len), int(axis), float(eps),
+                                  C.c_void_p(y_ptr)))
+
+
+def skip_rms_norm_f32_dev(x_ptr: int, skip_ptr: int, shape, gamma_ptr: int, gamma_len: int,
+                          bias_ptr: int | None, eps: float, y_ptr: int, sum_ptr: int | None,
+                          ctx: Context | None = None):
+    """SkipSimplifiedLayerNormalization (lib/src/onnx_graph.dart:1793-1813) on
+    device buffers: sum = x + skip, y = RMSNorm(sum) (+ bias)."""
+    ctx = ctx or default_context()
+    sh = np.ascontiguousarray(np.array(shape, np.int64))
+    check(lib.mg_skip_rms_norm_f32_dev(ctx.handle, C.c_void_p(x_ptr), C.c_void_p(skip_ptr),
+                                       _ptr(sh), sh.size, C.c_void_p(gamma_ptr), int(gamma_len),
+                                       C.c_void_p(bias_ptr) if bias_ptr else None, float(eps),
+                                       C.c_void_p(y_ptr),
+                                       C.c_void_p(sum_ptr) if sum_ptr else None))
+
+
 # ---------------------------------------------------------------------- ops
+
+
+def _run_dev(arrays, out_shapes, call, ctx):
+    """Uploads arrays, runs call(device pointers..., output pointers...),
+    downloads the outputs (float32)."""
+    ctx = ctx or default_context()
+    ins = [DeviceBuffer.from_array(np.ascontiguousarray(x, np.float32), ctx) for x in arrays]
+    outs = [DeviceBuffer(max(int(np.prod(sh, dtype=np.int64)), 1) * 4, ctx) for sh in out_shapes]
+    try:
+        call(*[b.ptr for b in ins], *[b.ptr for b in outs])
+        return [o.to_array(sh, np.float32) for o, sh in zip(outs, out_shapes)]
+    finally:
+        for b in ins + outs:
+            b.free()
+
+
+def _binary(op, a, b, ctx):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    try:
+        shape = np.broadcast_shapes(a.shape, b.shape)
+    except ValueError:
+        shape = ()  # the library reports the reference's ArgumentError
+    return _run_dev([a, b], [shape], lambda pa, pb, py: binary_f32_dev(
+        op, pa, a.shape, pb, b.shape, py, ctx), ctx)[0]
+
+
+def op_add(a, b, ctx: Context | None = None) -> np.ndarray:
+    """opAdd on float tensors (lib/src/onnx_ops.dart:402-404)."""
+    return _binary("add", a, b, ctx)
+
+
+def op_sub(a, b, ctx: Context | None = None) -> np.ndarray:
+    """opSub on float tensors (lib/src/onnx_ops.dart:444-446)."""
+    return _binary("sub", a, b, ctx)
+
+
+def op_mul(a, b, ctx: Context | None = None) -> np.ndarray:
+    """opMul on float tensors (lib/src/onnx_ops.dart:447-449)."""
+    return _binary("mul", a, b, ctx)
+
+
+def op_div(a, b, ctx: Context | None = None) -> np.ndarray:
+    """opDiv on float tensors (lib/src/onnx_ops.dart:475-477)."""
+    return _binary("div", a, b, ctx)
+
+
+def op_sigmoid(x, ctx: Context | None = None) -> np.ndarray:
+    """opSigmoid (lib/src/onnx_ops.dart:2349-2350)."""
+    x = np.asarray(x, np.float32)
+    return _run_dev([x], [x.shape], lambda px, py: sigmoid_f32_dev(px, x.size, py, ctx), ctx)[0]
+
+
+def op_rms_norm(x, gamma, axis: int, eps: float, ctx: Context | None = None) -> np.ndarray:
+    """opRMSNorm (lib/src/onnx_ops.dart:1771-1815)."""
+    x = np.asarray(x, np.float32)
+    g = np.asarray(gamma, np.float32).ravel()
+    return _run_dev([x, g], [x.shape], lambda px, pg, py: rms_norm_f32_dev(
+        px, x.shape, pg, g.size, axis, eps, py, ctx), ctx)[0]
+
+
+def op_skip_simplified_layer_norm(x, skip, gamma, bias=None, eps: float = 1e-5,
+                                  ctx: Context | None = None):
+    """SkipSimplifiedLayerNormalization (lib/src/onnx_graph.dart:1793-1813):
+    returns (rmsnorm(x + skip) [+ bias], x + skip)."""
+    x = np.asarray(x, np.float32)
+    s = np.asarray(skip, np.float32)
+    g = np.asarray(gamma, np.float32).ravel()
+    ins = [x, s, g] + ([np.asarray(bias, np.float32).ravel()] if bias is not None else [])
+
+    def call(*p):
+        px, ps, pg = p[:3]
+        pb = p[3] if bias is not None else None
+        py, psum = p[-2], p[-1]
+        skip_rms_norm_f32_dev(px, ps, x.shape, pg, g.size, pb, eps, py, psum, ctx)
+
+    y, total = _run_dev(ins, [x.shape, x.shape], call, ctx)
+    return y, total
 
 
 def op_matmul_nbits(a, b_q, scales, zero_points=None, *, k, n, bits=4, block_size,

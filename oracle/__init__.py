@@ -23,6 +23,9 @@ Thin numpy wrappers over ``oracle/lib/liboracle.so`` (built from oracle.c by
 * ``conv_transpose``       — lib/src/onnx_nn_ops.dart:818-1059
 * ``conv_integer``         — lib/src/onnx_qlinear_ops.dart:232-337
 * ``qlinear_conv``         — lib/src/onnx_qlinear_ops.dart:339-382
+* ``binary_f32``           — lib/src/onnx_ops.dart:26-44, :103-330 (Add/Sub/Mul/Div)
+* ``sigmoid_f32``          — lib/src/onnx_ops.dart:2349-2350
+* ``rms_norm_f32``         — lib/src/onnx_ops.dart:1771-1815
 """
 from __future__ import annotations
 
@@ -102,6 +105,10 @@ def _declare(L):
                                             _I64, _P, _P, _I64, _I, _I, _P, _I64, _I,
                                             C.c_double, _P, _P, _P]
     L.orc_round_even.argtypes = [C.c_double, _P]
+    L.orc_binary_f32.argtypes = [_I, _P, _P, _I, _P, _P, _I, _P, _P]
+    L.orc_sigmoid_f32.argtypes = [_P, _I64, _P]
+    L.orc_sigmoid_f32.restype = None
+    L.orc_rms_norm_f32.argtypes = [_P, _P, _I, _P, _I64, _I64, C.c_double, _P]
     L.orc_round_even.restype = _I64
 
 
@@ -521,3 +528,42 @@ def group_query_attention(q, k, v, *, num_heads, kv_num_heads, scale=None, do_ro
         int(rotary_interleaved), _ptr(attention_bias), bh, int(scale is not None),
         float(scale or 0.0), _ptr(out), _ptr(pk), _ptr(pv)), "orc_group_query_attention")
     return [out, pk, pv]
+
+
+BINARY_OPS = {"add": 0, "sub": 1, "mul": 2, "div": 3}
+
+
+def binary_f32(op: str, a, b) -> np.ndarray:
+    """Add / Sub / Mul / Div of float tensors with broadcasting: op in double
+    per element, one rounding to f32."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    rank = max(a.ndim, b.ndim)
+    out_shape = np.zeros(max(rank, 1), np.int64)
+    try:
+        shape = np.broadcast_shapes(a.shape, b.shape)
+    except ValueError:
+        shape = ()
+    y = np.empty(max(int(np.prod(shape, dtype=np.int64)), 1), np.float32)
+    st = lib().orc_binary_f32(BINARY_OPS[op], _ptr(a), _ptr(np.array(a.shape, np.int64)), a.ndim,
+                              _ptr(b), _ptr(np.array(b.shape, np.int64)), b.ndim, _ptr(y),
+                              _ptr(out_shape))
+    _check(st, "binary_f32")
+    return y[:int(np.prod(shape, dtype=np.int64))].reshape(tuple(int(d) for d in out_shape[:rank]))
+
+
+def sigmoid_f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_sigmoid_f32(_ptr(x), x.size, _ptr(y))
+    return y
+
+
+def rms_norm_f32(x, gamma, axis: int, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = np.ascontiguousarray(gamma, dtype=np.float32).ravel()
+    y = np.empty_like(x)
+    st = lib().orc_rms_norm_f32(_ptr(x), _ptr(np.array(x.shape, np.int64)), x.ndim, _ptr(g),
+                                g.size, axis, eps, _ptr(y))
+    _check(st, "rms_norm_f32")
+    return y

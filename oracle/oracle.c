@@ -807,3 +807,79 @@ int orc_group_query_attention(const float *q, const float *k, const float *v, in
   free(qq); free(kk); free(pos); free(qh); free(kt); free(sc); free(cx);
   return ORC_OK;
 }
+
+/* ------------------------------------------------- elementwise (decoder) */
+
+int orc_binary_f32(int op, const float *a, const int64_t *a_shape, int a_rank, const float *b,
+                   const int64_t *b_shape, int b_rank, float *y, int64_t *out_shape) {
+  enum { R = 16 };
+  const int rank = a_rank > b_rank ? a_rank : b_rank;
+  if (op < 0 || op > 3 || rank > R || a_rank < 0 || b_rank < 0) return ORC_INVALID_ARGUMENT;
+  int64_t ad[R], bd[R], od[R];
+  for (int k = 0; k < rank; k++) {
+    const int ka = k - (rank - a_rank), kb = k - (rank - b_rank);
+    ad[k] = ka >= 0 ? a_shape[ka] : 1;
+    bd[k] = kb >= 0 ? b_shape[kb] : 1;
+    if (ad[k] == bd[k]) od[k] = ad[k];
+    else if (ad[k] == 1) od[k] = bd[k];
+    else if (bd[k] == 1) od[k] = ad[k];
+    else return ORC_INVALID_ARGUMENT;  /* "Cannot broadcast shapes" */
+    out_shape[k] = od[k];
+  }
+  int64_t n = 1;
+  for (int k = 0; k < rank; k++) n *= od[k];
+  for (int64_t i = 0; i < n; i++) {
+    /* coordinates of output element i, then the operands' row-major offsets */
+    int64_t rem = i, ia = 0, ib = 0, sa = 1, sb = 1;
+    for (int k = rank - 1; k >= 0; k--) {
+      const int64_t c = rem % od[k];
+      rem /= od[k];
+      ia += (ad[k] == 1 ? 0 : c) * sa;
+      ib += (bd[k] == 1 ? 0 : c) * sb;
+      sa *= ad[k];
+      sb *= bd[k];
+    }
+    const double x = a[ia], v = b[ib];
+    double r;
+    switch (op) {
+      case 0: r = x + v; break;
+      case 1: r = x - v; break;
+      case 2: r = x * v; break;
+      default: r = x / v; break;
+    }
+    y[i] = (float)r;
+  }
+  return ORC_OK;
+}
+
+void orc_sigmoid_f32(const float *x, int64_t n, float *y) {
+  for (int64_t i = 0; i < n; i++) y[i] = (float)(1.0 / (1.0 + exp(-(double)x[i])));
+}
+
+int orc_rms_norm_f32(const float *x, const int64_t *shape, int rank, const float *gamma,
+                     int64_t gamma_len, int64_t axis, double eps, float *y) {
+  if (rank < 1) return ORC_INVALID_ARGUMENT;
+  const int64_t ax = axis < 0 ? axis + rank : axis;
+  if (ax < 0 || ax >= rank) return ORC_INVALID_ARGUMENT;
+  const int64_t last = shape[rank - 1];
+  if (gamma_len != last) return ORC_INVALID_ARGUMENT;  /* "RMSNorm gamma length" */
+  int64_t outer = 1, inner = 1;
+  for (int64_t k = 0; k < ax; k++) outer *= shape[k];
+  for (int64_t k = ax + 1; k < rank; k++) inner *= shape[k];
+  const int64_t dim = shape[ax];
+  for (int64_t o = 0; o < outer; o++)
+    for (int64_t i = 0; i < inner; i++) {
+      const int64_t base = o * dim * inner + i;
+      double ss = 0;
+      for (int64_t j = 0; j < dim; j++) {
+        const double v = x[base + j * inner];
+        ss += v * v;
+      }
+      const double inv = 1.0 / sqrt(ss / (double)dim + eps);
+      for (int64_t j = 0; j < dim; j++) {
+        const int64_t idx = base + j * inner;
+        y[idx] = (float)((double)x[idx] * inv * (double)gamma[idx % last]);
+      }
+    }
+  return ORC_OK;
+}

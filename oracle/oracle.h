@@ -145,6 +145,24 @@ int orc_conv(const void *x, int x_kind, const void *w, int w_kind, int64_t n, in
              const int64_t *pad, int trans, int32_t x_zp, const int32_t *w_zp,
              double *acc);
 
+/* Float binary ops with broadcasting: _broadcastShape (lib/src/onnx_ops.dart:
+ * 26-44) and _elementwiseBinary / _arithFloatFast (:103-330): each output
+ * element is op(a, b) of the broadcast operands computed in double and
+ * stored to f32.  op: 0 add, 1 sub, 2 mul, 3 div.  Shapes are right-aligned;
+ * y holds the broadcast shape (out_shape receives it, rank max(ra, rb)). */
+int orc_binary_f32(int op, const float *a, const int64_t *a_shape, int a_rank, const float *b,
+                   const int64_t *b_shape, int b_rank, float *y, int64_t *out_shape);
+
+/* opSigmoid, lib/src/onnx_ops.dart:2349-2350: 1 / (1 + exp(-x)) in double. */
+void orc_sigmoid_f32(const float *x, int64_t n, float *y);
+
+/* opRMSNorm, lib/src/onnx_ops.dart:1771-1815: per slice along axis, ss =
+ * sum of v*v in double (in order), inv = 1 / sqrt(ss / dim + eps), out =
+ * x * inv * gamma[i % last_dim] (double, one rounding to f32).  gamma has
+ * the last dim's length. */
+int orc_rms_norm_f32(const float *x, const int64_t *shape, int rank, const float *gamma,
+                     int64_t gamma_len, int64_t axis, double eps, float *y);
+
 /* _roundEven, lib/src/onnx_qlinear_ops.dart:19-26 / onnx_ops.dart:3480-3487.
  * Returns ORC_UNSUPPORTED through *err for non-finite input (Dart's toInt
  * throws UnsupportedError there). */

@@ -73,7 +73,22 @@ HOT_PATH = [
     "convtranspose_stride2",
     "qlinearconv_perchannel_bias",
     "qlinearconv_pertensor",
+    # elementwise ops between the products of a decoder layer
+    "add_bias_broadcast_lastdim",
+    "add_broadcast_middle",
+    "skipsimplifiedlayernorm",
 ]
+
+# Multi-node patterns the reference's graph rewrite fuses into one op
+# (lib/src/onnx_graph.dart:466-500, :500-560): stored as the fused op with
+# the pattern's feeds, constants and attributes.
+FUSED = {
+    # Pow(2) -> ReduceMean(ax) -> Add(eps) -> Sqrt -> Reciprocal -> Mul(x) ->
+    # Mul(gamma)  =>  _FusedRMSNorm(x, gamma; axis, epsilon)
+    "rmsnorm_pattern": "_FusedRMSNorm",
+    # Split(axis, 2) -> Sigmoid(b) -> Mul(a, .)  =>  _FusedGlu(x; axis)
+    "glu_gate": "_FusedGlu",
+}
 
 # ONNX TensorProto.DataType -> (numpy dtype, json dtype name)
 _DT = {
@@ -263,6 +278,47 @@ def convert(src: Path, dst: Path) -> None:
               [(o["name"], o["dtype"], o["shape"]) if o else None for o in operands])
 
 
+def convert_fused(src: Path, dst: Path) -> None:
+    for name, fused in FUSED.items():
+        d = src / name
+        nodes, inits = parse_model((d / "model.onnx").read_bytes())
+        case = json.loads((d / "case.json").read_text())
+        by_op = {n["op_type"]: n for n in nodes}
+
+        def feed(nm):
+            return {"name": nm, "initializer": False, **case["inputs"][nm]}
+
+        def init(nm):
+            arr = inits[nm]
+            dtname = {np.dtype(t): n for t, n in _DT.values()}[arr.dtype]
+            return {"name": nm, "initializer": True, **tensor_json(arr, dtname)}
+
+        if fused == "_FusedRMSNorm":
+            x = by_op["Pow"]["input"][0]
+            gamma = [i for i in nodes[-1]["input"] if i in inits][0]
+            eps = [i for i in by_op["Add"]["input"] if i in inits][0]
+            axis = int(inits[by_op["ReduceMean"]["input"][1]].ravel()[0])
+            operands = [feed(x), init(gamma)]
+            attrs = {"axis": axis, "epsilon": float(inits[eps].ravel()[0])}
+        else:
+            split = by_op["Split"]
+            operands = [feed(split["input"][0])]
+            attrs = {"axis": int(split["attrs"]["axis"])}
+        out = {
+            "name": name,
+            "source": f"test/fixtures/{name}",
+            "op_type": fused,
+            "domain": "",
+            "attrs": attrs,
+            "inputs": operands,
+            "outputs": [nodes[-1]["output"][0]],
+            "expected": case["expected"],
+        }
+        (dst / f"{name}.json").write_text(json.dumps(out, separators=(",", ":")))
+        print(name, fused, attrs, [(o["name"], o["dtype"], o["shape"]) for o in operands])
+
+
 if __name__ == "__main__":
     src = Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference/test/fixtures")
     convert(src, Path(__file__).resolve().parent / "fixtures")
+    convert_fused(src, Path(__file__).resolve().parent / "fixtures")

@@ -560,6 +560,35 @@ def test_m1_split_k_against_oracle(ops, k, n, bs, zp_mode, with_bias):
     w.release()
 
 
+FP32_PATH = [
+    # (M, K, N, bs, zp_mode, bias): float zero points or 16-k blocks with more
+    # than four rows: columns dequantised to fp32 (the reference's weights)
+    # in chunks, each chunk on the fp32 MFMA GEMM.
+    (64, 8192, 5000, 128, "float", True),   # 2048-column chunks: three of them
+    (33, 1000, 300, 16, "packed", True),
+    (512, 1024, 4096, 32, "float", False),
+    (5, 2100, 130, 64, "float", True),
+    (17, 4096, 70, 16, "none", False),
+]
+
+
+@pytest.mark.parametrize("m,k,n,bs,zp_mode,with_bias", FP32_PATH)
+def test_fp32_path_against_oracle(ops, m, k, n, bs, zp_mode, with_bias):
+    rng = np.random.default_rng(0x5EED0070 + m + k + n + bs)
+    b, s, zp = make_nbits(rng, n, k, bs, zp_mode)
+    bias = rng.standard_normal(n).astype(np.float32) if with_bias else None
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    y = w(a)
+    np.testing.assert_array_equal(w(a), y)
+    w.release()
+    cols = np.unique(np.concatenate([np.arange(min(n, 40)), np.arange(max(0, n - 40), n),
+                                     rng.integers(0, n, 100)]))
+    bb, ss, zz, bi = slice_cols(b, s, zp, bias, cols)
+    ref = oracle.matmul_nbits(a, bb, ss, zz, k=k, n=len(cols), block_size=bs, bias=bi)
+    assert G.rms_error(y[:, cols], ref) <= TOL, G.rms_error(y[:, cols], ref)
+
+
 def test_profiling_records_each_op(ops):
     # Per-op device timing (the ABI's part of ExecutionProfile): one record
     # per op entry, in issue order, with the reference's op-type names.

@@ -71,6 +71,16 @@ def _run_fixture(d):
             rotary_interleaved=bool(at.get("rotary_interleaved", 0)), past_key=g(3),
             past_value=g(4), cos_cache=g(7), sin_cache=g(8), attention_bias=g(10))
         return dict(zip(d["outputs"], outs))
+    if op == "Add":
+        return {d["outputs"][0]: oracle.binary_f32("add", x[0], x[1])}
+    if op == "_FusedRMSNorm":
+        return {d["outputs"][0]: oracle.rms_norm_f32(x[0], x[1], at["axis"], at["epsilon"])}
+    if op == "SkipSimplifiedLayerNormalization":
+        s = oracle.binary_f32("add", x[0], x[1])
+        return {"out0": oracle.rms_norm_f32(s, x[2], -1, at.get("epsilon", 1e-5)), "out3": s}
+    if op == "_FusedGlu":
+        a, b = np.split(x[0], 2, axis=at["axis"])
+        return {d["outputs"][0]: oracle.binary_f32("mul", a, oracle.sigmoid_f32(b))}
     geo = dict(strides=at.get("strides"), pads=at.get("pads"), dilations=at.get("dilations"),
                group=at.get("group", 1))
     if op == "Conv":
