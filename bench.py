@@ -750,8 +750,8 @@ def conv_family(torch, ops, ctx, T, randn, dev, args):
     f32_case("resnet50_3x3_256", RESNET_3X3)
     f32_case("resnet50_stem_7x7", RESNET_STEM)
     f32_case("conv_transpose_4x4_s2", VAE_UP, transposed=True)
-    out["conv_transpose_4x4_s2"]["note"] = ("FLOPs count the useful taps; the gather form "
-                                            "issues all 16 taps per output, 4 of them valid")
+    out["conv_transpose_4x4_s2"]["note"] = ("FLOPs count the useful taps (4 of 16 per output); "
+                                            "the four sub-pixel phases issue only those")
 
     xs, ws, at = RESNET_3X3
     x = torch.randint(0, 256, xs, device=dev, dtype=torch.uint8)

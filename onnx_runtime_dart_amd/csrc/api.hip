@@ -1751,7 +1751,8 @@ mg_status conv_int_params(const char *op, const mg_conv_problem &p, const int32_
 // the workspace at wz_off / mult_off through the pinned staging, so the host
 // tables may go away on return without a wait.
 mg_status conv_launch(mg_ctx *ctx, mg_conv_problem p, const std::vector<float> &wz,
-                      const std::vector<double> &mult, size_t wz_off, size_t mult_off) {
+                      const std::vector<double> &mult, size_t wz_off, size_t mult_off,
+                      size_t phase_off) {
   char *base = static_cast<char *>(ctx->ws);
   if (!wz.empty()) {
     MG_TRY(mg_h2d_table(ctx, base + wz_off, wz.data(), wz.size() * 4));
@@ -1761,7 +1762,7 @@ mg_status conv_launch(mg_ctx *ctx, mg_conv_problem p, const std::vector<float> &
     MG_TRY(mg_h2d_table(ctx, base + mult_off, mult.data(), mult.size() * 8));
     p.mult = reinterpret_cast<const double *>(base + mult_off);
   }
-  return mg_conv_run(ctx, p);
+  return mg_conv_run(ctx, p, base + phase_off);
 }
 
 // Host-pointer call: stages x, w, bias and the tables, runs, copies y back.
@@ -1776,7 +1777,8 @@ mg_status conv_host(mg_ctx *ctx, mg_conv_problem p, const void *x, size_t x_el, 
   Staging s;
   const size_t ox = s.take((size_t)nx * x_el), ow = s.take((size_t)nw * w_el),
                ob = s.take(bias ? bias_bytes : 0), oy = s.take((size_t)ny * y_el),
-               oz = s.take(wz.size() * 4), om = s.take(mult.size() * 8);
+               oz = s.take(wz.size() * 4), om = s.take(mult.size() * 8),
+               oph = s.take(mg_conv_ws_bytes(p));
   MG_TRY(mg_check_control(ctx, (int64_t)s.off));
   MG_TRY(mg_ws_reserve(ctx, s.off));
   char *base = static_cast<char *>(ctx->ws);
@@ -1788,7 +1790,7 @@ mg_status conv_host(mg_ctx *ctx, mg_conv_problem p, const void *x, size_t x_el, 
   p.w = base + ow;
   p.bias = bias ? base + ob : nullptr;
   p.y = base + oy;
-  MG_TRY(conv_launch(ctx, p, wz, mult, oz, om));
+  MG_TRY(conv_launch(ctx, p, wz, mult, oz, om, oph));
   MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)ny * y_el, hipMemcpyDeviceToHost, st));
   MG_HIP(hipStreamSynchronize(st));
   return MG_OK;
@@ -1801,14 +1803,15 @@ mg_status conv_dev(mg_ctx *ctx, mg_conv_problem p, const void *x, const void *w,
   if (conv_out_count(p) == 0) return MG_OK;
   MG_TRY(mg_use_device(ctx));
   Staging s;
-  const size_t oz = s.take(wz.size() * 4), om = s.take(mult.size() * 8);
-  MG_TRY(mg_check_control(ctx, 0));
-  if (!wz.empty() || !mult.empty()) MG_TRY(mg_ws_reserve(ctx, s.off));
+  const size_t oz = s.take(wz.size() * 4), om = s.take(mult.size() * 8),
+               oph = s.take(mg_conv_ws_bytes(p));
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  if (s.off) MG_TRY(mg_ws_reserve(ctx, s.off));
   p.x = x;
   p.w = w;
   p.bias = bias;
   p.y = y;
-  return conv_launch(ctx, p, wz, mult, oz, om);
+  return conv_launch(ctx, p, wz, mult, oz, om, oph);
 }
 
 void conv_int_kinds(mg_conv_problem *p, int32_t x_signed, int32_t w_signed) {

@@ -53,8 +53,56 @@ __device__ inline int load_int(const uint8_t *p, int64_t i, int kind) {
   return kind == MG_CONV_I8 ? (int)(int8_t)b : (int)b;
 }
 
+// Sub-pixel phases of a strided ConvTranspose with unit dilation.  Output
+// position o along an axis reads input i = (o + pad - k) / str for the taps
+// k with k == (o + pad) mod str; so the outputs of one phase ph = o mod str
+// (o = ph + str * o') use only the taps k = r + str * k' with r = (ph + pad)
+// mod str, and read i = o' + base - k' with base = (ph + pad - r) / str: a
+// forward convolution of stride 1 and dilation -1 over a 1/str-sized kernel.
+// Each phase then issues only its own taps, where the gather form issues all
+// of them for every output.
+// All phases run as one launch (grid z = phase); each workgroup takes its
+// phase's geometry from this table.
+constexpr int MG_CONV_MAX_PHASES = 16;
+struct ConvPhases {
+  int n;                            // phases (str0 * str1 * str2)
+  int64_t off[MG_CONV_MAX_PHASES];  // first element of each phase's weights
+  int64_t ker[MG_CONV_MAX_PHASES][3];
+  int64_t out[MG_CONV_MAX_PHASES][3], pad[MG_CONV_MAX_PHASES][3], yb[MG_CONV_MAX_PHASES][3];
+};
+
+__host__ __device__ inline int64_t floor_mod(int64_t a, int64_t m) { return ((a % m) + m) % m; }
+
+bool use_phases(const mg_conv_problem &p) {
+  if (!p.trans || p.xk != MG_CONV_F32) return false;
+  const int64_t np = p.str[0] * p.str[1] * p.str[2];
+  return p.dil[0] == 1 && p.dil[1] == 1 && p.dil[2] == 1 && np > 1 && np <= MG_CONV_MAX_PHASES;
+}
+
+// Phase (pz, py, px) = index ((pz * s1) + py) * s2 + px: sub-kernel dims and
+// weight offsets (weights laid out [phase][group][m][c][k']).
+ConvPhases phase_table(const mg_conv_problem &p) {
+  ConvPhases t{};
+  t.n = (int)(p.str[0] * p.str[1] * p.str[2]);
+  int64_t off = 0;
+  for (int ph = 0; ph < t.n; ph++) {
+    const int64_t pv[3] = {ph / (p.str[1] * p.str[2]), (ph / p.str[2]) % p.str[1],
+                           ph % p.str[2]};
+    int64_t kk = 1;
+    for (int d = 0; d < 3; d++) {
+      const int64_t r = floor_mod(pv[d] + p.pad[d], p.str[d]);
+      t.ker[ph][d] = r < p.ker[d] ? (p.ker[d] - r + p.str[d] - 1) / p.str[d] : 0;
+      kk *= t.ker[ph][d];
+    }
+    t.off[ph] = off;
+    off += p.group * p.mg * p.cg * kk;
+  }
+  return t;
+}
+
 template <int WT, int KS, bool TR, bool INT>
-__global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p, int pix_tiles) {
+__global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p0, int pix_tiles,
+                                              const ConvPhases ph) {
   constexpr int T = 64 * WT, LDX = KS + 4, NS = KS / 2;
   constexpr int E = KS * T / 256;  // elements per thread and operand per stage
   constexpr int FLUSH = 256 / KS;  // stages per exact fp32 segment (integer kinds)
@@ -64,6 +112,23 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p, int pix_t
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int l32 = lane & 31, h = lane >> 5;
+  mg_conv_problem p = p0;
+  if (p0.phased) {  // phase blockIdx.z of a strided ConvTranspose
+    const int z3 = (int)blockIdx.z;
+    const int64_t kk3 = ph.ker[z3][0] * ph.ker[z3][1] * ph.ker[z3][2];
+    for (int d = 0; d < 3; d++) {
+      p.out[d] = ph.out[z3][d];
+      p.ker[d] = ph.ker[z3][d];
+      p.pad[d] = ph.pad[z3][d];
+      p.yb[d] = ph.yb[z3][d];
+    }
+    p.w = static_cast<const float *>(p0.w) + ph.off[z3];
+    p.w_cs = kk3;
+    p.w_ms = p.cg * kk3;
+    p.w_gs = p.mg * p.cg * kk3;
+    // The grid covers the largest phase: tiles past this one's outputs exit.
+    if ((int64_t)(blockIdx.x % pix_tiles) * 64 * WT >= p.out[0] * p.out[1] * p.out[2]) return;
+  }
   const int64_t z = blockIdx.x / pix_tiles;  // batch * group + g
   const int64_t b = z / p.group, g = z % p.group;
   const int64_t c0 = (int64_t)(blockIdx.x % pix_tiles) * T;  // first output position
@@ -286,20 +351,28 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p, int pix_t
     __syncthreads();
   }
 
-  // Lane l holds output position l % 32 and channels 8 (v / 4) + 4 (l / 32)
-  // + v % 4 of each 32 x 32 tile; 32 lanes write consecutive positions.
+    // Lane l holds output position l % 32 and channels 8 (v / 4) + 4 (l / 32)
+  // + v % 4 of each 32 x 32 tile; 32 lanes write consecutive positions.  A
+  // sub-pixel phase places its position o' at o' * ys + yb of the full
+  // output.
+  const int64_t y_sp = p.phased ? p.yo[0] * p.yo[1] * p.yo[2] : out_sp;
 #pragma unroll
   for (int i = 0; i < WT; i++)
 #pragma unroll
     for (int j = 0; j < WT; j++) {
-      const int64_t col = c0 + wn * 32 * WT + j * 32 + l32;
+      int64_t col = c0 + wn * 32 * WT + j * 32 + l32;
       if (col >= out_sp) continue;
+      if (p.phased) {
+        const int64_t oz = col / o12, oy = (col % o12) / o2, ox = col % o2;
+        col = ((oz * p.ys[0] + p.yb[0]) * p.yo[1] + (oy * p.ys[1] + p.yb[1])) * p.yo[2] +
+              (ox * p.ys[2] + p.yb[2]);
+      }
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int64_t row = r0 + wm * 32 * WT + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
         if (row >= p.mg) continue;
         const int64_t ch = g * p.mg + row;
-        const int64_t oi = (b * p.m + ch) * out_sp + col;
+        const int64_t oi = (b * p.m + ch) * y_sp + col;
         if (!INT) {
           float y = acc[i][j][v];
           if (p.bias) y += static_cast<const float *>(p.bias)[ch];
@@ -317,42 +390,131 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p, int pix_t
     }
 }
 
+// One thread per weight element (group g, out channel m, in channel c, tap
+// k): tap k belongs to the phases whose r == k mod str, i.e. ph == (k - pad)
+// mod str, at sub-kernel tap k' = k / str.
+__global__ __launch_bounds__(256) void k_conv_phase_weights(const mg_conv_problem p,
+                                                            const ConvPhases t,
+                                                            float *__restrict__ out) {
+  const int64_t taps = p.ker[0] * p.ker[1] * p.ker[2];
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= p.group * p.mg * p.cg * taps) return;
+  const int64_t tap = idx % taps, c = (idx / taps) % p.cg, m = (idx / (taps * p.cg)) % p.mg,
+                g = idx / (taps * p.cg * p.mg);
+  const int64_t k[3] = {tap / (p.ker[1] * p.ker[2]), (tap / p.ker[2]) % p.ker[1],
+                        tap % p.ker[2]};
+  int64_t ph = 0, kq[3];
+  for (int d = 0; d < 3; d++) {
+    ph = ph * p.str[d] + floor_mod(k[d] - p.pad[d], p.str[d]);
+    kq[d] = k[d] / p.str[d];
+  }
+  const int64_t *kp = t.ker[ph];
+  const int64_t kk = kp[0] * kp[1] * kp[2];
+  const int64_t kl = (kq[0] * kp[1] + kq[1]) * kp[2] + kq[2];
+  out[t.off[ph] + ((g * p.mg + m) * p.cg + c) * kk + kl] =
+      static_cast<const float *>(p.w)[g * p.w_gs + m * p.w_ms + c * p.w_cs + tap];
+}
+
 template <bool TR, bool INT>
-void launch_conv(const mg_conv_problem &p, bool big, int64_t out_sp, hipStream_t st) {
+void launch_conv(const mg_conv_problem &p, bool big, int64_t out_sp, hipStream_t st,
+                 const ConvPhases &tb) {
   const int T = big ? 128 : 64;
   const int64_t pix_tiles = (out_sp + T - 1) / T;
-  const dim3 grid((unsigned)(pix_tiles * p.n * p.group), (unsigned)((p.mg + T - 1) / T));
+  const dim3 grid((unsigned)(pix_tiles * p.n * p.group), (unsigned)((p.mg + T - 1) / T),
+                  (unsigned)(p.phased ? tb.n : 1));
   if constexpr (!INT) {
     if (big) {
-      hipLaunchKernelGGL((k_conv<2, 16, TR, INT>), grid, dim3(256), 0, st, p, (int)pix_tiles);
+      hipLaunchKernelGGL((k_conv<2, 16, TR, INT>), grid, dim3(256), 0, st, p, (int)pix_tiles,
+                         tb);
       return;
     }
   }
-  hipLaunchKernelGGL((k_conv<1, 32, TR, INT>), grid, dim3(256), 0, st, p, (int)pix_tiles);
+  hipLaunchKernelGGL((k_conv<1, 32, TR, INT>), grid, dim3(256), 0, st, p, (int)pix_tiles, tb);
 }
 
 }  // namespace
 
-mg_status mg_conv_run(mg_ctx *ctx, const mg_conv_problem &p) {
+size_t mg_conv_ws_bytes(const mg_conv_problem &p) {
+  if (!use_phases(p)) return 0;
+  return mg_align((size_t)(p.group * p.mg * p.cg * p.ker[0] * p.ker[1] * p.ker[2]) * 4);
+}
+
+mg_status mg_conv_run(mg_ctx *ctx, const mg_conv_problem &p, void *ws);
+
+namespace {
+mg_status conv_launch_all(mg_ctx *ctx, const mg_conv_problem &p, int64_t out_sp,
+                          const ConvPhases &tb);
+
+// A strided ConvTranspose as forward convolutions, one per sub-pixel phase,
+// in one launch.
+mg_status conv_run_phases(mg_ctx *ctx, const mg_conv_problem &p, float *wph) {
+  ConvPhases t = phase_table(p);
+  const int64_t nw = p.group * p.mg * p.cg * p.ker[0] * p.ker[1] * p.ker[2];
+  if (nw > 0) {
+    hipLaunchKernelGGL(k_conv_phase_weights, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0,
+                       ctx->stream, p, t, wph);
+    MG_TRY(mg_launch_check("k_conv_phase_weights"));
+  }
+  mg_conv_problem q = p;
+  q.trans = 0;
+  q.phased = 1;
+  q.w = wph;
+  int64_t max_sp = 0;
+  for (int ph = 0; ph < t.n; ph++) {
+    const int64_t pv[3] = {ph / (p.str[1] * p.str[2]), (ph / p.str[2]) % p.str[1],
+                           ph % p.str[2]};
+    int64_t sp = 1;
+    for (int d = 0; d < 3; d++) {
+      const int64_t r = floor_mod(pv[d] + p.pad[d], p.str[d]);
+      t.pad[ph][d] = -((pv[d] + p.pad[d] - r) / p.str[d]);  // exact division
+      t.out[ph][d] = p.out[d] > pv[d] ? (p.out[d] - pv[d] + p.str[d] - 1) / p.str[d] : 0;
+      t.yb[ph][d] = pv[d];
+      sp *= t.out[ph][d];
+    }
+    max_sp = std::max(max_sp, sp);
+  }
+  for (int d = 0; d < 3; d++) {
+    q.str[d] = 1;
+    q.dil[d] = -1;
+    q.yo[d] = p.out[d];
+    q.ys[d] = p.str[d];
+    // The tile plan and grid follow the largest phase.
+    q.out[d] = t.out[0][d];
+    q.ker[d] = t.ker[0][d];
+  }
+  return conv_launch_all(ctx, q, max_sp, t);
+}
+}  // namespace
+
+mg_status mg_conv_run(mg_ctx *ctx, const mg_conv_problem &p, void *ws) {
   const int64_t out_sp = p.out[0] * p.out[1] * p.out[2];
   if (p.n == 0 || p.m == 0 || out_sp == 0) return MG_OK;
+  if (use_phases(p)) return conv_run_phases(ctx, p, static_cast<float *>(ws));
+  return conv_launch_all(ctx, p, out_sp, ConvPhases{});
+}
+
+namespace {
+mg_status conv_launch_all(mg_ctx *ctx, const mg_conv_problem &p, int64_t out_sp,
+                          const ConvPhases &tb) {
   const bool integer = p.xk != MG_CONV_F32;
   // The 128 x 128 tile when it still gives about two workgroups per CU and
   // at most a quarter of its rows are padding (64 output channels, as in a
   // ResNet stem, would waste half of its MFMA work).
-  const int64_t big_wgs = ((out_sp + 127) / 128) * ((p.mg + 127) / 128) * p.n * p.group;
+  const int64_t nz = p.phased ? tb.n : 1;  // sub-pixel phases in grid z
+  const int64_t big_wgs = ((out_sp + 127) / 128) * ((p.mg + 127) / 128) * p.n * p.group * nz;
   const bool big = !integer && big_wgs >= 2 * (int64_t)ctx->num_cus &&
                    3 * ((p.mg + 127) / 128 * 128) <= 4 * (int64_t)p.mg;
   const int64_t wgs = ((out_sp + (big ? 127 : 63)) / (big ? 128 : 64)) * p.n * p.group;
   if (wgs > 0x7fffffff || (p.mg + 63) / 64 > 65535)
     return mg_fail(MG_UNSUPPORTED, "conv: grid too large");
   if (!integer && !p.trans)
-    launch_conv<false, false>(p, big, out_sp, ctx->stream);
+    launch_conv<false, false>(p, big, out_sp, ctx->stream, tb);
   else if (!integer)
-    launch_conv<true, false>(p, big, out_sp, ctx->stream);
+    launch_conv<true, false>(p, big, out_sp, ctx->stream, tb);
   else if (!p.trans)
-    launch_conv<false, true>(p, false, out_sp, ctx->stream);
+    launch_conv<false, true>(p, false, out_sp, ctx->stream, tb);
   else
     return mg_fail(MG_UNSUPPORTED, "conv: transposed integer convolution");
   return mg_launch_check("k_conv");
 }
+}  // namespace

@@ -307,8 +307,16 @@ struct mg_conv_problem {
   const float *w_zp = nullptr;   // device [M] (integer kinds)
   const double *mult = nullptr;  // device [M] requant multipliers
   int32_t y_zp = 0, lo = 0, hi = 255;
+  // Output placement of a sub-pixel phase (set by the phase split of a
+  // strided ConvTranspose): output position o' of this problem lands at
+  // o = o' * ys + yb in an output of dims yo.  phased = 0: o = o'.
+  int phased = 0;
+  int64_t yo[3] = {1, 1, 1}, ys[3] = {1, 1, 1}, yb[3] = {0, 0, 0};
 };
-mg_status mg_conv_run(mg_ctx *ctx, const mg_conv_problem &p);
+// Workspace a call needs (the sub-pixel phase weights of a strided fp32
+// ConvTranspose; 0 otherwise), and the launch.
+size_t mg_conv_ws_bytes(const mg_conv_problem &p);
+mg_status mg_conv_run(mg_ctx *ctx, const mg_conv_problem &p, void *ws);
 
 // ---------------------------------------------------------- attention entry
 

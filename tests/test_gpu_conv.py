@@ -84,6 +84,16 @@ CONVT = [
     ((1, 3, 4, 5, 3), (3, 2, 2, 3, 3), dict(strides=[2, 1, 2], pads=[0, 1, 0, 1, 0, 1])),
     ((2, 64, 16, 16), (64, 32, 4, 4), dict(strides=[2, 2], pads=[1, 1, 1, 1])),  # VAE-like upsample
     ((16, 16, 32, 32), (16, 128, 2, 2), dict(strides=[2, 2])),     # 512 tiles of 128 x 128
+    # Sub-pixel phases (unit dilation, stride > 1): kernels smaller than the
+    # stride leave phases with no taps (bias only); 8 phases in 3-D; 16 in
+    # 2-D at stride 4; groups; pads past the kernel; the bench's upsampler.
+    ((1, 3, 5, 5), (3, 2, 1, 1), dict(strides=[2, 2])),
+    ((2, 4, 6, 7), (4, 3, 5, 5), dict(strides=[3, 3], pads=[2, 1, 2, 1])),
+    ((1, 4, 3, 4, 5), (4, 2, 3, 3, 3), dict(strides=[2, 2, 2], pads=[1, 1, 1, 1, 1, 1],
+                                            output_padding=[1, 0, 1])),
+    ((2, 6, 5, 5), (6, 2, 8, 8), dict(strides=[4, 4], pads=[2, 2, 2, 2], group=3)),
+    ((1, 2, 4, 4), (2, 3, 3, 3), dict(strides=[2, 2], pads=[3, 3, 3, 3])),
+    ((8, 128, 32, 32), (128, 64, 4, 4), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
 ]
 
 
