@@ -54,43 +54,43 @@ typedef short short2v __attribute__((ext_vector_type(2)));
 // (uint4: bytes 0-15, 16-31), asc[(m32 * c4n + kg) * 2 + st][r + 32 b] = the
 // three E8M0 scale bytes of block b (digit d in byte d), nf[(row * c4n + kg)
 // * 4 + 2 st + b] = 1 when the block held a non-finite value.  Rows >= M and
-// k >= K are zeros.  Thread = one scale block (r, b); wave = one (m32, kg, st).
+// k >= K are zeros.  Four threads per scale block (r, b), eight elements each
+// (octet o of the block's four); the block maxima meet by shuffles over the
+// four lanes.  Workgroup = one (m32, kg, st): its 64 blocks are blk = t / 4,
+// r = blk % 32, b = blk / 32.
 __global__ __launch_bounds__(256) void k_af8x3(const float *__restrict__ a, int64_t M,
-                                               int64_t K, int c4n, int vec, int64_t nwaves,
+                                               int64_t K, int c4n, int vec,
                                                uint4 *__restrict__ aq,
                                                uint32_t *__restrict__ asc,
                                                uint8_t *__restrict__ nf) {
-  const int t = threadIdx.x, lane = t & 63;
-  const int64_t wv = (int64_t)blockIdx.x * 4 + (t >> 6);
-  if (wv >= nwaves) return;  // whole wave
+  const int t = threadIdx.x;
+  const int64_t wv = blockIdx.x;  // (m32 * c4n + kg) * 2 + st
   const int st = (int)(wv & 1);
   const int64_t mk = wv >> 1;  // m32 * c4n + kg
   const int kg = (int)(mk % c4n);
   const int64_t m32 = mk / c4n;
-  const int r = lane & 31, b = lane >> 5;
+  const int o = t & 3, blk = t >> 2;
+  const int r = blk & 31, b = blk >> 5;
   const int64_t row = m32 * 32 + r;
   const bool live = row < M;
   const float *arow = a + (live ? row : 0) * K;
-  // v[16 hh + 8 jj + tt]: lane half hh, octet g = 2 hh + b, j = 2 st + jj.
-  float v[32];
+  // Octet o = 2 hh + jj of the block: lane half hh, g = 2 hh + b, j = 2 st + jj.
+  const int hh = o >> 1, jj = o & 1;
+  const int g = 2 * hh + b, j = 2 * st + jj;
+  const int64_t k0 = (int64_t)kg * KGRP + 32 * j + 8 * g;
+  float v[8];
+  if (live && vec && k0 + 8 <= K) {
+    const float4 x0 = *reinterpret_cast<const float4 *>(arow + k0);
+    const float4 x1 = *reinterpret_cast<const float4 *>(arow + k0 + 4);
+    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+  } else {
 #pragma unroll
-  for (int o = 0; o < 4; o++) {
-    const int hh = o >> 1, jj = o & 1;
-    const int g = 2 * hh + b, j = 2 * st + jj;
-    const int64_t k0 = (int64_t)kg * KGRP + 32 * j + 8 * g;
-    if (live && vec && k0 + 8 <= K) {
-      const float4 x0 = *reinterpret_cast<const float4 *>(arow + k0);
-      const float4 x1 = *reinterpret_cast<const float4 *>(arow + k0 + 4);
-      v[8 * o] = x0.x; v[8 * o + 1] = x0.y; v[8 * o + 2] = x0.z; v[8 * o + 3] = x0.w;
-      v[8 * o + 4] = x1.x; v[8 * o + 5] = x1.y; v[8 * o + 6] = x1.z; v[8 * o + 7] = x1.w;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) v[8 * o + i] = (live && k0 + i < K) ? arow[k0 + i] : 0.f;
-    }
+    for (int i = 0; i < 8; i++) v[i] = (live && k0 + i < K) ? arow[k0 + i] : 0.f;
   }
   int bad = 0;
 #pragma unroll
-  for (int i = 0; i < 32; i++) {
+  for (int i = 0; i < 8; i++) {
     float x = v[i];
     if (!isfinite(x)) {
       bad = 1;
@@ -98,22 +98,26 @@ __global__ __launch_bounds__(256) void k_af8x3(const float *__restrict__ a, int6
     }
     v[i] = (i & 2) ? x * 0.0625f : x;  // exact
   }
+  bad |= __shfl_xor(bad, 1);
+  bad |= __shfl_xor(bad, 2);
   uint32_t scales = 0;
-  uint4 *out = aq + (((m32 * c4n + kg) * 2 + st) * 3) * 128 + 2 * r + b;
+  uint2 *out = reinterpret_cast<uint2 *>(aq + (wv * 3) * 128 + hh * 64 + 2 * r + b) + jj;
 #pragma unroll
   for (int d = 0; d < 3; d++) {
     float mx = 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; i++) mx = fmaxf(mx, fabsf(v[i]));
+    for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[i]));
+    mx = fmaxf(mx, __shfl_xor(mx, 1));
+    mx = fmaxf(mx, __shfl_xor(mx, 2));
     int E = 0;
     if (mx > 0.f) {
       int ex;
       frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
       E = min(max(ex - 8, -127), 127);
     }
-    uint32_t wd[8];
+    uint32_t wd[2];
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
+    for (int q = 0; q < 2; q++) {
       int w = 0;
       w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * q], -E), ldexpf(v[4 * q + 1], -E), w,
                                           false);
@@ -125,13 +129,14 @@ __global__ __launch_bounds__(256) void k_af8x3(const float *__restrict__ a, int6
       v[4 * q + 2] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 2), E);
       v[4 * q + 3] -= ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 3), E);
     }
-    // Plane b of lane r (half 0) and of lane r + 32 (half 1).
-    out[d * 128] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-    out[d * 128 + 64] = make_uint4(wd[4], wd[5], wd[6], wd[7]);
+    // Octet o's 8 bytes of plane b: lane r (half 0, o < 2) or lane r + 32.
+    out[d * 256] = make_uint2(wd[0], wd[1]);
     scales |= (uint32_t)(E + 127) << (8 * d);
   }
-  asc[((m32 * c4n + kg) * 2 + st) * 64 + lane] = scales;
-  nf[(row * c4n + kg) * 4 + 2 * st + b] = (uint8_t)bad;
+  if (o == 0) {
+    asc[wv * 64 + r + 32 * b] = scales;
+    nf[(row * c4n + kg) * 4 + 2 * st + b] = (uint8_t)bad;
+  }
 }
 
 // ------------------------------------------------------------------ GEMM
@@ -177,16 +182,18 @@ __device__ inline float nbits_weight(const uint4 *__restrict__ wq, const float *
 //     round so those FMAs overlap MFMAs.
 // Grid, member choice, split-K partials and the epilogue's row-contiguous
 // 16-byte stores are those of the fp16 prefill kernel.
-template <int NT>
-__global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f8x3(
+template <int NT, int MW>
+__global__ __launch_bounds__(64 * MW, MW == 8 ? 1 : (NT == 4 ? 2 : 3)) void k_gemm_f8x3(
     const uint4 *__restrict__ aq, const uint32_t *__restrict__ asc,
     const uint8_t *__restrict__ nf, const float *__restrict__ a, int64_t K,
     const PrefillSet ps, float *__restrict__ part, int M, int c4n, int nb, int nbh, int lbs,
     int has_zp, int mtiles, int ntiles, int kps) {
   constexpr int PH = NT / 2;          // column groups per tile
+  constexpr int HPW = PH * 4 / MW;    // column groups each thread dequantises
+  static_assert(HPW >= 1, "tile too narrow for the waves");
   constexpr int TC = 32 * NT;         // tile columns
   constexpr int BU4 = NT * 2 * 2 * 64;  // uint4 per weight buffer: [n32][st][plane][lane]
-  constexpr int STAGE_U4 = 32 * TC;     // 4 waves x 32 rows x TC floats, in uint4
+  constexpr int STAGE_U4 = 8 * MW * TC;  // MW waves x 32 rows x TC floats, in uint4
   constexpr int LDS_U4 = 2 * BU4 > STAGE_U4 ? 2 * BU4 : STAGE_U4;
   __shared__ uint4 lds[LDS_U4];
   __shared__ float scl[2][32][NT];  // [buf][col % 32][n32]
@@ -207,18 +214,20 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f8x3(
   const int ks = blockIdx.y;
   const int kg0 = ks * kps;
   const int kg1 = min(c4n, kg0 + kps);
-  const int m32 = mt * 4 + wave;  // this wave's 32-row subtile
+  const int m32 = mt * MW + wave;  // this wave's 32-row subtile
   const int lc = lane & 31;
 
   // Cooperative dequantisation: thread t handles the packed uint4 (column
-  // group PH*nt + h, g = wave, col = lane) for h < PH; its dword j (k = 32 j +
-  // 8 g .. +7) becomes 8 e4m3 bytes of lane (c % 32) + 32 (g / 2), step j / 2,
-  // plane g % 2, 8-byte slot j % 2, where c = 64 h + lane is the tile column.
-  const int dq_g = wave;
-  int dq_dst[PH];
+  // group PH*nt + hb + h, g = wave % 4, col = lane) for h < HPW, hb = HPW *
+  // (wave / 4); its dword j (k = 32 j + 8 g .. +7) becomes 8 e4m3 bytes of
+  // lane (c % 32) + 32 (g / 2), step j / 2, plane g % 2, 8-byte slot j % 2,
+  // where c = 64 (hb + h) + lane is the tile column.
+  const int dq_g = wave & 3;
+  const int hb = HPW * (wave >> 2);
+  int dq_dst[HPW];
 #pragma unroll
-  for (int h = 0; h < PH; h++) {
-    const int c = 64 * h + lane;
+  for (int h = 0; h < HPW; h++) {
+    const int c = 64 * (hb + h) + lane;
     dq_dst[h] = ((c >> 5) * 4 + (dq_g & 1)) * 64 + (c & 31) + 32 * (dq_g >> 1);
   }
   const int nbm1 = nb - 1, nbhm1 = nbh - 1;
@@ -226,10 +235,10 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f8x3(
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7ffffff0,
                                              0x00020000);
   };
-  __amdgpu_buffer_rsrc_t r_wq[PH], r_zp[PH], r_sc[PH];
+  __amdgpu_buffer_rsrc_t r_wq[HPW], r_zp[HPW], r_sc[HPW];
 #pragma unroll
-  for (int h = 0; h < PH; h++) {
-    const int64_t cgi = PH * nt + h;
+  for (int h = 0; h < HPW; h++) {
+    const int64_t cgi = PH * nt + hb + h;
     r_wq[h] = rsrc(wq + cgi * c4n * 256);
     r_zp[h] = rsrc(zp4 + cgi * nbh * 64);
     r_sc[h] = rsrc(scales + cgi * nb * 64);
@@ -242,16 +251,16 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f8x3(
   asm volatile("v_mov_b32 %0, %1" : "=v"(v_mhi) : "s"(0x00F000F0u));
   asm volatile("v_mov_b32 %0, %1" : "=v"(v_magic) : "s"(0x64006400u));
   struct Meta {
-    uint4 pk[PH];
-    uint32_t zb[PH];
-    float sc[PH];
-    uint32_t z1[PH], z16[PH];
+    uint4 pk[HPW];
+    uint32_t zb[HPW];
+    float sc[HPW];
+    uint32_t z1[HPW], z16[HPW];
   };
   auto load_meta = [&](int kg, Meta &m) {
     const int blk = (kg * KGRP) >> lbs;
     const int zbyte = min(blk / 2, nbhm1);
 #pragma unroll
-    for (int h = 0; h < PH; h++) {
+    for (int h = 0; h < HPW; h++) {
       m.pk[h] = __builtin_bit_cast(
           uint4, __builtin_amdgcn_raw_buffer_load_b128(r_wq[h], vo16, (kg * 4 + dq_g) * 1024, 0));
       m.zb[h] = __builtin_amdgcn_raw_buffer_load_b8(r_zp[h], vo_zp, zbyte * 64, 0);
@@ -264,7 +273,7 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f8x3(
   auto dequant_quarter = [&](int kg, Meta &m, int buf, int j) {
     const int blk = (kg * KGRP) >> lbs;
 #pragma unroll
-    for (int h = 0; h < PH; h++) {
+    for (int h = 0; h < HPW; h++) {
       uint32_t w = j == 0 ? m.pk[h].x : j == 1 ? m.pk[h].y : j == 2 ? m.pk[h].z : m.pk[h].w;
       asm volatile("" : "+v"(w));
       if (j == 0) {
@@ -291,10 +300,10 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f8x3(
     if (j == 0 && dq_g == 0) {
       const bool in_range = blk < nb;
 #pragma unroll
-      for (int h = 0; h < PH; h++) {
+      for (int h = 0; h < HPW; h++) {
         float sc = m.sc[h];
         asm volatile("" : "+v"(sc));
-        const int c = 64 * h + lane;
+        const int c = 64 * (hb + h) + lane;
         scl[buf][c & 31][c >> 5] = in_range ? sc : 0.f;
       }
     }
@@ -504,9 +513,9 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
   uint8_t *nf = reinterpret_cast<uint8_t *>(base + off_nf);
   float *part = ksplit > 1 ? reinterpret_cast<float *>(base + off_part) : nullptr;
   const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
-  const int64_t nwaves = (mpad / 32) * d.c4 * 2;
-  hipLaunchKernelGGL(k_af8x3, dim3((unsigned)((nwaves + 3) / 4)), dim3(256), 0, st, a_dev, M,
-                     w0->K, (int)d.c4, vec, nwaves, aq, asc, nf);
+  const int64_t groups = (mpad / 32) * d.c4 * 2;  // (m32, kg, st)
+  hipLaunchKernelGGL(k_af8x3, dim3((unsigned)groups), dim3(256), 0, st, a_dev, M, w0->K,
+                     (int)d.c4, vec, aq, asc, nf);
   MG_TRY(mg_launch_check("k_af8x3"));
   const int has_zp = d.zp_kind == MG_ZP_UINT4;
   PrefillSet ps{};
@@ -514,16 +523,19 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
   int ct = 0;
   int64_t eend = 0;
   make_prefill_sets(n, w, y_dev, M, ksplit, nt, &ps, &rs, &ct, &eend);
+  // (256-row workgroups of 8 waves, k_gemm_f8x3<4, 8>, dequantise each
+  // weight tile once for twice the rows; measured 2-4% slower on the lm_head
+  // at M = 512, so 128-row tiles are used.)
   const int mtiles = (int)(mpad / 128);
   const dim3 grid((unsigned)(8 * mtiles * ((ct + 7) / 8)), (unsigned)ksplit);
+#define MG_F8_ARGS                                                                         \
+  aq, asc, nf, a_dev, w0->K, ps, part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,          \
+      __builtin_ctzll(d.bs), has_zp, mtiles, ct, kps
   if (nt == 4)
-    hipLaunchKernelGGL((k_gemm_f8x3<4>), grid, dim3(256), 0, st, aq, asc, nf, a_dev, w0->K, ps,
-                       part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs),
-                       has_zp, mtiles, ct, kps);
+    hipLaunchKernelGGL((k_gemm_f8x3<4, 4>), grid, dim3(256), 0, st, MG_F8_ARGS);
   else
-    hipLaunchKernelGGL((k_gemm_f8x3<2>), grid, dim3(256), 0, st, aq, asc, nf, a_dev, w0->K, ps,
-                       part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs),
-                       has_zp, mtiles, ct, kps);
+    hipLaunchKernelGGL((k_gemm_f8x3<2, 4>), grid, dim3(256), 0, st, MG_F8_ARGS);
+#undef MG_F8_ARGS
   MG_TRY(mg_launch_check("k_gemm_f8x3"));
   if (ksplit > 1) MG_TRY(launch_gemm_reduce(st, part, rs, eend, ksplit));
   return MG_OK;
