@@ -9,8 +9,10 @@ weights and activations resident in HBM.
 The same run also measures, each with HIP events on the stream the library
 launches on:
   roofline       the lm_head call at M = 512 (MFMA-bound), against fp16 peak
-                 (the kernel issues three fp8 products per product: its
-                 share of the fp8 peak is reported beside it);
+                 (the kernel issues three fp6 products per product: its
+                 share of the fp6 peak is reported beside it), and the same
+                 call on a weight without prefill images (the fp8 GEMM that
+                 dequantises each tile);
   gemv_m1        the same eight projections at M = 1, algorithmic HBM GB/s;
                  four distinct weight sets are rotated so that the working set
                  (~370 MB) exceeds the 256 MB last-level cache and the weights
@@ -52,6 +54,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 FP8_MFMA_PEAK_TFLOPS = 5000.0
+FP6_MFMA_PEAK_TFLOPS = 10100.0
 INT8_MFMA_PEAK_TOPS = 5000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
@@ -308,6 +311,13 @@ def main():
                                         outs[(M_PREFILL, n_lm)].data_ptr()), reps, 2)
     lm_tflops = 2.0 * M_PREFILL * n_lm * k_lm / (ms_lm / 1e3) / 1e12
     tr = traffic.get("lm512", {})
+    # The same lm_head on a weight created without prefill images.
+    ctx.set_prefill_images(False)
+    w_lm8 = ops.NBitsWeight(*host_w[-1], k=k_lm, n=n_lm, block_size=BLOCK, ctx=ctx)
+    ctx.set_prefill_images(True)
+    ms_lm8 = T.loop(lambda: w_lm8.run_dev(acts[(M_PREFILL, k_lm)].data_ptr(), M_PREFILL,
+                                          outs[(M_PREFILL, n_lm)].data_ptr()), reps, 2)
+    w_lm8.release()
     result = {
         "metric": "int4 MatMulNBits TFLOP/s (M=512) + M=1 GEMV HBM GB/s, Qwen3-0.6B shapes",
         "value": round(value, 2),
@@ -319,8 +329,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 weights x fp32 activations (activations as three fp8 e4m3 digits with "
-                 "per-32-k E8M0 scales on block-scaled fp8 MFMA, fp32 accumulate)",
+        "dtype": "int4 weights x fp32 activations (weights' (q - zp) / 2 as fp6 e2m3 prefill "
+                 "images, activations as three e2m3 digits with per-32-k E8M0 scales, "
+                 "block-scaled fp6 MFMA, fp32 accumulate)",
+        "weight_format": "packed int4 (decode) + prefill images, 0.75 byte per weight, built "
+                         "on the device at weight upload (outside the timed region)",
         "data": "synthetic (seeded uniform nibbles, scales U(0.002,0.02), A ~ N(0,1))",
         "config": {"workload": "Qwen3-0.6B int4 MatMulNBits projections q,k,v,o,gate,up,"
                                "down,lm_head; block_size 128 with uint4 zero points",
@@ -330,13 +343,19 @@ def main():
                                "Dart shim issues them); o, down, lm_head alone"},
         "separate_launches": {"ms_per_step": round(ms_step_sep, 4),
                               "TFLOP/s": round(flops_step / (ms_step_sep / 1e3) / 1e12, 2)},
-        "roofline": {"kernel": tr.get("kernel", "k_gemm_f8x3") +
+        "roofline": {"kernel": tr.get("kernel", "k_gemm_f6x3") +
                      " (lm_head 512x1024x151936; op time incl. activation prepass)",
                      "bound": "mfma", "achieved": round(lm_tflops, 2),
                      "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(lm_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
-                     "issued": "3 fp8 MFMA products per algorithmic product",
-                     "issued_frac_of_fp8_peak": round(3 * lm_tflops / FP8_MFMA_PEAK_TFLOPS, 4),
+                     "issued": "3 fp6 MFMA products per algorithmic product",
+                     "issued_frac_of_fp6_peak": round(3 * lm_tflops / FP6_MFMA_PEAK_TFLOPS, 4),
+                     "without_images": {
+                         "kernel": "k_gemm_f8x3 (three e4m3 digits, weight tiles dequantised "
+                                   "in the GEMM)",
+                         "ms": round(ms_lm8, 4),
+                         "TFLOP/s": round(2.0 * M_PREFILL * n_lm * k_lm / (ms_lm8 / 1e3) / 1e12,
+                                          2)},
                      "traffic": tr.get("bytes"),
                      "algorithmic_bytes": nbits_bytes(M_PREFILL, k_lm, n_lm),
                      "ms": round(ms_lm, 4)},

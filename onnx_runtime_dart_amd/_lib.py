@@ -33,6 +33,7 @@ SIGNATURES = {
     "mg_ctx_synchronize": [_P],
     "mg_ctx_set_control": [_P, _P, _I64],
     "mg_ctx_set_profiling": [_P, _I32],
+    "mg_ctx_set_prefill_images": [_P, _I32],
     "mg_ctx_profile_count": [_P, _P],
     "mg_ctx_profile_get": [_P, _I64, _P, _P],
     "mg_ctx_profile_clear": [_P],

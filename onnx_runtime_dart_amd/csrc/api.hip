@@ -273,6 +273,12 @@ mg_status mg_ctx_set_profiling(mg_ctx *ctx, int32_t enable) {
   return MG_OK;
 }
 
+mg_status mg_ctx_set_prefill_images(mg_ctx *ctx, int32_t enable) {
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_set_prefill_images: null context");
+  ctx->prefill_images = enable != 0;
+  return MG_OK;
+}
+
 mg_status mg_ctx_profile_count(mg_ctx *ctx, int64_t *n) {
   if (!ctx || !n) return mg_fail(MG_INVALID_ARGUMENT, "mg_ctx_profile_count: null argument");
   *n = (int64_t)ctx->prof_recs.size();

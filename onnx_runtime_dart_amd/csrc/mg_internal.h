@@ -65,6 +65,9 @@ struct mg_ctx {
   bool prof = false;
   std::vector<mg_prof_rec> prof_recs;
   std::vector<hipEvent_t> prof_pool;
+  // MatMulNBits weights created afterwards keep their prefill images
+  // (mg_ctx_set_prefill_images).
+  bool prefill_images = true;
 };
 
 // Records events on the context's stream around one op's work when the
@@ -101,6 +104,10 @@ struct mg_nbits_dev {
   uint8_t *zp4 = nullptr;     // [ng][nbh][64]  (MG_ZP_UINT4)
   float *zpf = nullptr;       // [ng][nb][64]   (MG_ZP_FLOAT)
   float *bias = nullptr;      // [N] or null
+  // Prefill images ([2 ng][c4][256] uint4, or null): per 32-column slab and
+  // k group, the 4 KiB of e4m3 weight fragments that the fp8 prefill GEMM
+  // would otherwise dequantise into LDS (mg_nbits_f8_images).
+  void *img = nullptr;
 };
 
 // Device form of an 8-bit MatMulInteger weight B [K, N].
@@ -162,6 +169,11 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const mg_byte_source &b,
                           const mg_byte_source &scales, int32_t zp_kind,
                           const mg_byte_source &zp, const float *bias, int64_t chunk_bytes);
 void mg_nbits_free(mg_weight *w);
+// Whether a weight's prefill GEMM is the fp8 one (block_size >= 128, integer
+// zero points), and the build of its prefill images (allocates w->nbits.img;
+// synchronous).
+bool mg_nbits_f8_eligible(const mg_nbits_dev &d);
+mg_status mg_nbits_f8_images(mg_ctx *ctx, mg_weight *w);
 // Workspace bytes mg_nbits_run needs for M rows.
 size_t mg_nbits_ws_bytes(const mg_ctx *ctx, const mg_weight *w, int64_t M);
 // a_dev [M, K] f32, y_dev [M, N] f32; ws holds mg_nbits_ws_bytes bytes.

@@ -1856,12 +1856,15 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const mg_byte_source &b,
   };
   status = run();
   cleanup();
+  if (status == MG_OK && ctx->prefill_images && mg_nbits_f8_eligible(d))
+    status = mg_nbits_f8_images(ctx, w);
   return status;
 }
 
 void mg_nbits_free(mg_weight *w) {
   mg_nbits_dev &d = w->nbits;
   if (d.wq) (void)hipFree(d.wq);
+  if (d.img) (void)hipFree(d.img);
   if (d.scales) (void)hipFree(d.scales);
   if (d.zp4) (void)hipFree(d.zp4);
   if (d.zpf) (void)hipFree(d.zpf);

@@ -59,6 +59,7 @@ __device__ inline uint4 deq8(uint32_t x, uint32_t mlo, uint32_t mhi, uint32_t ma
 // member i start at part + part_off[i] ([ksplit][M][N_i]).
 struct PrefillSet {
   const uint4 *wq[GMAX];
+  const uint4 *img[GMAX];  // prefill images (mg_nbits_dev::img) or null
   const float *scales[GMAX];
   const uint8_t *zp4[GMAX];
   const float *bias[GMAX];
@@ -143,6 +144,7 @@ inline void make_prefill_sets(int n, const mg_weight *const *w, float *const *y_
   for (int i = 0; i < n; i++) {
     const mg_nbits_dev &di = w[i]->nbits;
     ps->wq[i] = reinterpret_cast<const uint4 *>(di.wq);
+    ps->img[i] = static_cast<const uint4 *>(di.img);
     ps->scales[i] = di.scales;
     // The kernels read zero-point bytes unconditionally (branch-free); without
     // zero points they are pointed at the scales, which are at least as large.

@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "mg_internal.h"
 #include "nbits_common.h"
@@ -139,6 +140,182 @@ __global__ __launch_bounds__(256) void k_af8x3(const float *__restrict__ a, int6
   }
 }
 
+// ------------------------------------------------- fp6 prefill (images)
+
+// e2m3 code (sign, 2 exponent bits, 3 mantissa bits, exponent bias 1) of y
+// rounded to nearest even, for |y| <= 4: the e2m3 magnitudes below 2 are the
+// multiples of 1/8 (code 8 |y|), those in [2, 4] the multiples of 1/4 (code
+// 8 + 4 |y|).  *val receives the code's value (signed).
+__device__ inline uint32_t e2m3_rne(float y, float *val) {
+  const float ay = fabsf(y);
+  const bool lo = ay < 2.f;
+  const float q = rintf(lo ? ay * 8.f : ay * 4.f);
+  const uint32_t c = (uint32_t)q + (lo ? 0u : 8u);
+  const float v = lo ? q * 0.125f : q * 0.25f;
+  *val = y < 0.f ? -v : v;
+  return c == 0u ? 0u : (c | (y < 0.f ? 32u : 0u));
+}
+
+// Sixteen 6-bit fields, field i at bits 6 i of three dwords.
+__device__ inline void pack6x16(const uint32_t (&c)[16], uint32_t (&w)[3]) {
+  w[0] = w[1] = w[2] = 0u;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int bit = 6 * i, wd = bit >> 5, sh = bit & 31;
+    w[wd] |= c[i] << sh;
+    if (sh > 26) w[wd + 1] |= c[i] >> (32 - sh);
+  }
+}
+
+// Activations -> three e2m3 digits per element in the A-operand order of the
+// fp6 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4, both operands e2m3): lane l
+// holds row l % 32 of 32-row tile m32; in 64-k step st of k group kg, field i
+// (bits 6 i of the lane's six dwords) holds k = 128 kg + 64 st + 32 (l / 32)
+// + i.  With fp6 operands the MFMA's scale block h is the 32 fields of lane
+// half h (unlike fp8, whose blocks take 16 bytes from each half), its scale
+// from the lane itself.
+// Digit d of a block: e_d = e2m3(r_d / 2^E_d) rounded to nearest even,
+// r_{d+1} = r_d - e_d 2^E_d (exact: Sterbenz), where 2^E_d puts the block's
+// largest |r_d| in [2, 4), so every digit leaves at most 2^-4 of the block's
+// largest residual.
+// Output per (m32, kg, st, d), at aq + (((m32 * c4n + kg) * 2 + st) * 3 + d)
+// * 1536: dwords 0-3 of lane l at byte 16 l, dwords 4-5 at 1024 + 8 l;
+// asc[(m32 * c4n + kg) * 2 + st][l] = the three E8M0 scale bytes of lane l's
+// block (digit d in byte d), nf[(row * c4n + kg) * 4 + 2 st + h] = 1 when
+// the block held a non-finite value.  Rows >= M and k >= K are zeros.
+// Thread = 16 consecutive k of one row, t = 8 r + s with s = 4 st + 2 h + e
+// (k = 128 kg + 16 s, fields 16 e .. + 15 of lane r + 32 h); the two halves
+// of a block meet by shuffles (xor 1), and the e = 1 thread hands its first
+// dword to the e = 0 thread, so that each writes one piece of the lane.
+__global__ __launch_bounds__(256) void k_af6x3(const float *__restrict__ a, int64_t M,
+                                               int64_t K, int c4n, int vec,
+                                               uint8_t *__restrict__ aq,
+                                               uint32_t *__restrict__ asc,
+                                               uint8_t *__restrict__ nf) {
+  const int t = threadIdx.x;
+  const int64_t mk = blockIdx.x;  // m32 * c4n + kg
+  const int kg = (int)(mk % c4n);
+  const int64_t m32 = mk / c4n;
+  const int r = t >> 3, sg = t & 7;
+  const int st = sg >> 2, h = (sg >> 1) & 1, e = sg & 1;
+  const int64_t row = m32 * 32 + r;
+  const bool live = row < M;
+  const float *arow = a + (live ? row : 0) * K;
+  const int64_t k0 = (int64_t)kg * KGRP + 16 * sg;
+  float v[16];
+  if (live && vec && k0 + 16 <= K) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float4 x = *reinterpret_cast<const float4 *>(arow + k0 + 4 * q);
+      v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = (live && k0 + i < K) ? arow[k0 + i] : 0.f;
+  }
+  int bad = 0;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    if (!isfinite(v[i])) {
+      bad = 1;
+      v[i] = 0.f;
+    }
+  }
+  bad |= __shfl_xor(bad, 1);
+  const int lane = r + 32 * h;
+  uint8_t *base = aq + (mk * 2 + st) * 3 * 1536;
+  uint32_t scales = 0;
+#pragma unroll
+  for (int d = 0; d < 3; d++) {
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
+    mx = fmaxf(mx, __shfl_xor(mx, 1));
+    int E = 0;
+    if (mx > 0.f) {
+      int ex;
+      frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+      E = max(ex - 2, -127);
+    }
+    uint32_t c[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float y = ldexpf(v[i], -E);  // exact
+      float val;
+      c[i] = e2m3_rne(y, &val);
+      v[i] = ldexpf(y - val, E);  // exact, no overflow
+    }
+    uint32_t w[3];
+    pack6x16(c, w);
+    const uint32_t w0p = __shfl_xor(w[0], 1);
+    if (e == 0)
+      *reinterpret_cast<uint4 *>(base + d * 1536 + 16 * lane) = make_uint4(w[0], w[1], w[2], w0p);
+    else
+      *reinterpret_cast<uint2 *>(base + d * 1536 + 1024 + 8 * lane) = make_uint2(w[1], w[2]);
+    scales |= (uint32_t)(E + 127) << (8 * d);
+  }
+  if (e == 0) {
+    asc[(mk * 2 + st) * 64 + lane] = scales;
+    nf[(row * c4n + kg) * 4 + 2 * st + h] = (uint8_t)bad;
+  }
+}
+
+// e2m3 code of the weight integer v / 2, v = q - zp in [-15, 15] (all exact:
+// magnitudes m / 2 below 2 are codes 4 m, in [2, 4) codes 8 + 2 m, in [4, 7.5]
+// codes 16 + m); the GEMM scales the weight operand by 2.
+__device__ inline uint32_t e2m3_half_int(int v) {
+  const int m = v < 0 ? -v : v;
+  const uint32_t c = (uint32_t)(m < 4 ? 4 * m : m < 8 ? 8 + 2 * m : 16 + m);
+  return v < 0 ? (c | 32u) : c;
+}
+
+// Prefill images, built once per weight at upload: for 32-column slab u
+// (columns 32 u .. + 31) and k group kg, the 3072 bytes of B operands of the
+// fp6 GEMM: per step st, lane l = column (l % 32) and fields as the A operand
+// (k = 64 st + 32 (l / 32) + i), dwords 0-3 of lane l at st * 1536 + 16 l
+// and dwords 4-5 at st * 1536 + 1024 + 8 l.  Thread = the four packed uint4
+// of wq (g = 0..3) of column group cg, k group kg, column col, i = (cg * c4n
+// + kg) * 64 + col: dword j of octet row g holds k = 32 j + 8 g + t, so dword
+// j of all four gives the 32 fields (i = 8 g + t) of step j / 2, lane half
+// j % 2.
+__global__ __launch_bounds__(256) void k_f6_images(const uint4 *__restrict__ wq,
+                                                   const uint8_t *__restrict__ zp4, int has_zp,
+                                                   int64_t n, int c4n, int nbh, int lbs,
+                                                   uint8_t *__restrict__ img) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int col = (int)(i & 63);
+  const int64_t cgk = i >> 6;  // cg * c4n + kg
+  const int kg = (int)(cgk % c4n);
+  const int64_t cg = cgk / c4n;
+  uint4 p[4];
+#pragma unroll
+  for (int g = 0; g < 4; g++) p[g] = wq[(cgk * 4 + g) * 64 + col];
+  const int blk = (kg * KGRP) >> lbs;
+  int z = 8;
+  if (has_zp)
+    z = (int)((zp4[(cg * nbh + min(blk / 2, nbh - 1)) * 64 + sz_pos(col)] >> ((blk & 1) * 4)) &
+              15u);
+  uint8_t *dst = img + ((2 * cg + (col >> 5)) * c4n + kg) * 3072;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    uint32_t c[2][16];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const uint32_t dw = j == 0 ? p[g].x : j == 1 ? p[g].y : j == 2 ? p[g].z : p[g].w;
+#pragma unroll
+      for (int tt = 0; tt < 8; tt++)
+        c[g >> 1][8 * (g & 1) + tt] = e2m3_half_int((int)((dw >> (4 * nib_pos(tt))) & 15u) - z);
+    }
+    uint32_t w0[3], w1[3];
+    pack6x16(c[0], w0);
+    pack6x16(c[1], w1);
+    const int lane = (col & 31) + 32 * (j & 1), st = j >> 1;
+    *reinterpret_cast<uint4 *>(dst + st * 1536 + 16 * lane) = make_uint4(w0[0], w0[1], w0[2], w1[0]);
+    *reinterpret_cast<uint2 *>(dst + st * 1536 + 1024 + 8 * lane) = make_uint2(w1[1], w1[2]);
+  }
+}
+
 // ------------------------------------------------------------------ GEMM
 
 // One digit's MFMA: the op_sel byte of the A scale word is the digit.
@@ -164,6 +341,113 @@ __device__ inline float nbits_weight(const uint4 *__restrict__ wq, const float *
                                 (4 * (blk & 1))) & 15u)
                        : 8;
   return (float)(q - z) * sc[((int64_t)cg * nb + blk) * 64 + sz_pos(cl)];
+}
+
+// Epilogue of the prefill GEMMs: stages each wave's 32 x 32 NT tile of
+// fp32 sums row-major in LDS (free then: every wave has passed the main
+// loop's last barrier), rebuilds the reference's Inf / NaN pattern on rows
+// with a non-finite activation, and writes 16-byte row pieces of y (with the
+// bias) or of this k split's partials.
+template <int NT>
+__device__ inline void prefill_epilogue(
+    const float16v (&acc)[NT], uint4 *lds, const PrefillSet &ps, int mem, int nt, int m32, int M,
+    int c4n, int kg0, int kg1, int64_t K, const float *__restrict__ a,
+    const uint8_t *__restrict__ nf, const uint4 *__restrict__ wq,
+    const float *__restrict__ scales, const uint8_t *__restrict__ zp4, int nb, int nbh, int lbs,
+    int has_zp, int N, const float *__restrict__ bias, float *__restrict__ part, int ks) {
+  constexpr int TC = 32 * NT;
+  const int t = threadIdx.x, lane = t & 63, lc = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  float *stage = reinterpret_cast<float *>(lds) + wave * (32 * TC);
+  const int lh = lane >> 5;
+#pragma unroll
+  for (int n = 0; n < NT; n++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int r = 8 * (v >> 2) + 4 * lh + (v & 3);
+      stage[r * TC + n * 32 + lc] = acc[n][v];
+    }
+  __syncthreads();
+  // Rows of this wave's tile with a non-finite activation in this launch's
+  // k range get the reference's Inf / NaN pattern (rare: a uniform branch).
+  {
+    int flag = 0;
+    if (lane < 32 && m32 * 32 + lane < M) {
+      const uint32_t *nfw = reinterpret_cast<const uint32_t *>(nf) + (int64_t)(m32 * 32 + lane) * c4n;
+      for (int kg = kg0; kg < kg1; kg++) flag |= nfw[kg] != 0u;
+    }
+    uint64_t rows = __ballot(flag);
+    const int klo = kg0 * KGRP;
+    const int64_t khi = min((int64_t)kg1 * KGRP, K);
+    while (rows) {
+      const int r = __builtin_ctzll(rows);
+      rows &= rows - 1;
+      const float *arow = a + (int64_t)(m32 * 32 + r) * K;
+      bool fnan[2] = {false, false}, fpos[2] = {false, false}, fneg[2] = {false, false};
+      for (int64_t k0 = klo; k0 < khi; k0 += 64) {
+        const float x = k0 + lane < khi ? arow[k0 + lane] : 0.f;
+        uint64_t m = __ballot(!isfinite(x));
+        while (m) {
+          const int b = __builtin_ctzll(m);
+          m &= m - 1;
+          const float xv = __shfl(x, b);
+#pragma unroll
+          for (int u = 0; u < 2; u++) {
+            const int c = lane + 64 * u;
+            const int col = nt * TC + c;
+            if (c >= TC || col >= N) continue;
+            const float wv = nbits_weight(wq, scales, zp4, c4n, nb, nbh, lbs, has_zp, col,
+                                          (int)(k0 + b));
+            if (isnan(xv) || !(wv != 0.f)) fnan[u] = true;
+            else if ((xv > 0.f) == (wv > 0.f)) fpos[u] = true;
+            else fneg[u] = true;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int c = lane + 64 * u;
+        if (c >= TC || !(fnan[u] || fpos[u] || fneg[u])) continue;
+        stage[r * TC + c] = (fnan[u] || (fpos[u] && fneg[u])) ? __builtin_nanf("")
+                            : fpos[u] ? INFINITY : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+  const bool split = gridDim.y > 1;
+  float *dst = split ? part + ps.part_off[mem] + (int64_t)ks * M * N : ps.y[mem];
+  constexpr int PPR = 8 * NT, RPI = 64 / PPR;  // pieces per row, rows per iteration
+  const int c4 = lane % PPR, ro = lane / PPR;
+  const int col = nt * TC + 4 * c4;
+  float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!split && bias) {
+    if (col + 3 < N) {
+      bv = make_float4(bias[col], bias[col + 1], bias[col + 2], bias[col + 3]);
+    } else {
+      if (col < N) bv.x = bias[col];
+      if (col + 1 < N) bv.y = bias[col + 1];
+      if (col + 2 < N) bv.z = bias[col + 2];
+    }
+  }
+  const bool vec_ok = (N % 4) == 0 && (split || ps.y_vec[mem]);
+#pragma unroll 4
+  for (int it = 0; it < 32 / RPI; it++) {
+    const int r = RPI * it + ro;
+    const int row = m32 * 32 + r;
+    float4v v = *reinterpret_cast<const float4v *>(&stage[r * TC + 4 * c4]);
+    v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
+    if (row < M) {
+      float *p = dst + (int64_t)row * N + col;
+      if (vec_ok && col + 3 < N) {
+        __builtin_nontemporal_store(v, reinterpret_cast<float4v *>(p));
+      } else {
+        if (col < N) p[0] = v[0];
+        if (col + 1 < N) p[1] = v[1];
+        if (col + 2 < N) p[2] = v[2];
+        if (col + 3 < N) p[3] = v[3];
+      }
+    }
+  }
 }
 
 // Workgroup tile: 128 rows x 32*NT columns (NT/2 column groups), 4 waves;
@@ -396,98 +680,191 @@ __global__ __launch_bounds__(64 * MW, MW == 8 ? 1 : (NT == 4 ? 2 : 3)) void k_ge
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
 
-  // Epilogue: stage the wave's 32 x TC tile row-major in LDS (free now: every
-  // wave passed the last barrier), then write 16-byte row pieces.
-  float *stage = reinterpret_cast<float *>(lds) + wave * (32 * TC);
-  const int lh = lane >> 5;
+  prefill_epilogue<NT>(acc, lds, ps, mem, nt, m32, M, c4n, kg0, kg1, K, a, nf, wq, scales, zp4, nb,
+                       nbh, lbs, has_zp, N, bias, part, ks);
+}
+
+
+// One digit's fp6 MFMA: A and B e2m3 (format 2), the B scale 2 (E8M0 128)
+// turning the stored (q - zp) / 2 back into q - zp.
+template <int DG>
+__device__ inline float16v mfma6_digit(const int8v &a, const int8v &b, const float16v &c,
+                                       int sa) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 2, 2, DG, sa, 0, 128);
+}
+
+// The prefill GEMM on weights with prefill images (k_f6_images), with the
+// activations as three e2m3 digits (k_af6x3): both MFMA operands fp6, which
+// gfx950 runs at twice the fp8 rate.  Tiles, grid, member choice, split-K
+// partials, the deferred block scale and the epilogue are those of
+// k_gemm_f8x3; per k group the workgroup copies its NT slab images (NT x 3
+// KiB: three pieces of NT x 4 bytes per thread, loaded at the start of the
+// previous k group) into LDS instead of dequantising, and stages the
+// columns' block scales.
+template <int NT>
+__global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
+    const uint8_t *__restrict__ aq, const uint32_t *__restrict__ asc,
+    const uint8_t *__restrict__ nf, const float *__restrict__ a, int64_t K,
+    const PrefillSet ps, float *__restrict__ part, int M, int c4n, int nb, int nbh, int lbs,
+    int has_zp, int mtiles, int ntiles, int kps) {
+  constexpr int PH = NT / 2;           // column groups per tile
+  constexpr int TC = 32 * NT;          // tile columns
+  constexpr int SLAB = 192;            // uint4 per slab image of a k group
+  constexpr int BU4 = NT * SLAB;       // uint4 per weight buffer
+  constexpr int STAGE_U4 = 8 * 4 * TC; // 4 waves x 32 rows x TC floats, in uint4
+  constexpr int LDS_U4 = 2 * BU4 > STAGE_U4 ? 2 * BU4 : STAGE_U4;
+  constexpr int PB = NT * 4;           // bytes per image piece (3 per thread)
+  typedef typename std::conditional<NT == 4, uint4, uint2>::type piece_t;
+  __shared__ uint4 lds[LDS_U4];
+  __shared__ float scl[2][32][NT];  // [buf][col % 32][n32]
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int L = blockIdx.x;
+  const int xcd = L & 7, q = L >> 3;
+  const int mt = q % mtiles;
+  const int ntg = (q / mtiles) * 8 + xcd;
+  if (ntg >= ntiles) return;
+  int nt;
+  const int mem = prefill_member(ps, ntg, &nt);
+  const uint4 *__restrict__ wq = ps.wq[mem];
+  const float *__restrict__ scales = ps.scales[mem];
+  const uint8_t *__restrict__ zp4 = ps.zp4[mem];
+  const float *__restrict__ bias = ps.bias[mem];
+  const int N = ps.N[mem];
+  const int ks = blockIdx.y;
+  const int kg0 = ks * kps;
+  const int kg1 = min(c4n, kg0 + kps);
+  const int m32 = mt * 4 + wave;  // this wave's 32-row subtile
+  const int lc = lane & 31;
+
+  auto rsrc = [](const void *base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7ffffff0,
+                                             0x00020000);
+  };
+  // Image pieces p = t + 256 j of the tile's k group (NT slabs x 3072 bytes).
+  const uint8_t *__restrict__ img = reinterpret_cast<const uint8_t *>(ps.img[mem]);
+  const __amdgpu_buffer_rsrc_t r_im = rsrc(img + (int64_t)NT * nt * c4n * 3072);
+  unsigned vo_im[3];
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    const int pb = (t + 256 * j) * PB;
+    vo_im[j] = (unsigned)((pb / 3072) * c4n * 3072 + pb % 3072);
+  }
+  // Block scale of tile column tc = t % TC (threads t < TC stage it).
+  const int tc = t % TC;
+  const __amdgpu_buffer_rsrc_t r_sc = rsrc(scales + (int64_t)(PH * nt + tc / 64) * nb * 64);
+  const unsigned vo_sc = 4u * (unsigned)sz_pos(tc & 63);
+  const int nbm1 = nb - 1;
+  struct Meta {
+    piece_t im[3];
+    float sc;
+  };
+  auto load_meta = [&](int kg, Meta &m) {
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+      if constexpr (NT == 4)
+        m.im[j] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(r_im, vo_im[j], kg * 3072, 0));
+      else
+        m.im[j] = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_raw_buffer_load_b64(r_im, vo_im[j], kg * 3072, 0));
+    }
+    const int blk = (kg * KGRP) >> lbs;
+    m.sc = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r_sc, vo_sc, min(blk, nbm1) * 256, 0));
+  };
+  // Piece j of the images into buffer buf (j < 3); with j == 0 also the
+  // block scales.
+  auto store_piece = [&](int kg, Meta &m, int buf, int j) {
+    if (j < 3) reinterpret_cast<piece_t *>(&lds[buf * BU4])[t + 256 * j] = m.im[j];
+    if (j == 0 && t < TC) {
+      const int blk = (kg * KGRP) >> lbs;
+      scl[buf][tc & 31][tc >> 5] = blk < nb ? m.sc : 0.f;
+    }
+  };
+  // Digit d of step st of k group kg: this lane's six dwords.
+  const __amdgpu_buffer_rsrc_t r_a = rsrc(aq + (int64_t)m32 * c4n * 9216);
+  const __amdgpu_buffer_rsrc_t r_s = rsrc(asc + (int64_t)m32 * c4n * 128);
+  const unsigned vo16 = 16u * lane, vo8 = 1024u + 8u * lane, vo4 = 4u * lane;
+  auto a_load = [&](int kg, int st, int d) __attribute__((always_inline)) {
+    const int off = ((kg * 2 + st) * 3 + d) * 1536;
+    const uint4 x0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r_a, vo16, off, 0));
+    const uint2 x1 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r_a, vo8, off, 0));
+    return (int8v){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, 0, 0};
+  };
+  auto s_load = [&](int kg, int st) __attribute__((always_inline)) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r_s, vo4, (kg * 2 + st) * 256, 0);
+  };
+  auto b_load = [&](int buf, int n, int st) __attribute__((always_inline)) {
+    const int base = buf * BU4 + n * SLAB + st * 96;
+    const uint4 x0 = lds[base + lane];
+    const uint2 x1 = reinterpret_cast<const uint2 *>(&lds[base + 64])[lane];
+    return (int8v){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, 0, 0};
+  };
+
+  float16v acc[NT], D[NT];
+#pragma unroll
+  for (int n = 0; n < NT; n++) acc[n] = (float16v){}, D[n] = (float16v){};
+  float s_pend[NT];
+#pragma unroll
+  for (int n = 0; n < NT; n++) s_pend[n] = 0.f;
+  const float16v zero16 = (float16v){};
+
+  int8v A[3];
+  uint32_t sa;
+#pragma unroll
+  for (int d = 0; d < 3; d++) A[d] = a_load(kg0, 0, d);
+  sa = s_load(kg0, 0);
+  {
+    Meta m0;
+    load_meta(kg0, m0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) store_piece(kg0, m0, 0, j);
+  }
+  __syncthreads();
+
+  for (int kg = kg0; kg < kg1; kg++) {
+    const int buf = (kg - kg0) & 1;
+    const int kgn = min(kg + 1, kg1 - 1);  // next k group (clamped)
+    Meta mnext;
+    load_meta(kgn, mnext);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+      int8v B[NT];
+#pragma unroll
+      for (int n = 0; n < NT; n++) B[n] = b_load(buf, n, st);
+      const int nkg = st == 0 ? kg : kgn, nst = st ^ 1;
+#pragma unroll
+      for (int d = 0; d < 3; d++) {
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+          if (st == 0 && d == 0) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
+          }
+          const float16v cin = (st == 0 && d == 0) ? zero16 : D[n];
+          D[n] = d == 0   ? mfma6_digit<0>(A[0], B[n], cin, (int)sa)
+                 : d == 1 ? mfma6_digit<1>(A[1], B[n], cin, (int)sa)
+                          : mfma6_digit<2>(A[2], B[n], cin, (int)sa);
+        }
+        A[d] = a_load(nkg, nst, d);
+        if (d == 2) sa = s_load(nkg, nst);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      store_piece(kgn, mnext, buf ^ 1, 2 * st);
+      store_piece(kgn, mnext, buf ^ 1, 2 * st + 1);
+    }
+#pragma unroll
+    for (int n = 0; n < NT; n++) s_pend[n] = scl[buf][lc][n];
+    __syncthreads();
+  }
 #pragma unroll
   for (int n = 0; n < NT; n++)
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int r = 8 * (v >> 2) + 4 * lh + (v & 3);
-      stage[r * TC + n * 32 + lc] = acc[n][v];
-    }
-  __syncthreads();
-  // Rows of this wave's tile with a non-finite activation in this launch's
-  // k range get the reference's Inf / NaN pattern (rare: a uniform branch).
-  {
-    int flag = 0;
-    if (lane < 32 && m32 * 32 + lane < M) {
-      const uint32_t *nfw = reinterpret_cast<const uint32_t *>(nf) + (int64_t)(m32 * 32 + lane) * c4n;
-      for (int kg = kg0; kg < kg1; kg++) flag |= nfw[kg] != 0u;
-    }
-    uint64_t rows = __ballot(flag);
-    const int klo = kg0 * KGRP;
-    const int64_t khi = min((int64_t)kg1 * KGRP, K);
-    while (rows) {
-      const int r = __builtin_ctzll(rows);
-      rows &= rows - 1;
-      const float *arow = a + (int64_t)(m32 * 32 + r) * K;
-      bool fnan[2] = {false, false}, fpos[2] = {false, false}, fneg[2] = {false, false};
-      for (int64_t k0 = klo; k0 < khi; k0 += 64) {
-        const float x = k0 + lane < khi ? arow[k0 + lane] : 0.f;
-        uint64_t m = __ballot(!isfinite(x));
-        while (m) {
-          const int b = __builtin_ctzll(m);
-          m &= m - 1;
-          const float xv = __shfl(x, b);
-#pragma unroll
-          for (int u = 0; u < 2; u++) {
-            const int c = lane + 64 * u;
-            const int col = nt * TC + c;
-            if (c >= TC || col >= N) continue;
-            const float wv = nbits_weight(wq, scales, zp4, c4n, nb, nbh, lbs, has_zp, col,
-                                          (int)(k0 + b));
-            if (isnan(xv) || !(wv != 0.f)) fnan[u] = true;
-            else if ((xv > 0.f) == (wv > 0.f)) fpos[u] = true;
-            else fneg[u] = true;
-          }
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const int c = lane + 64 * u;
-        if (c >= TC || !(fnan[u] || fpos[u] || fneg[u])) continue;
-        stage[r * TC + c] = (fnan[u] || (fpos[u] && fneg[u])) ? __builtin_nanf("")
-                            : fpos[u] ? INFINITY : -INFINITY;
-      }
-    }
-  }
-  __syncthreads();
-  const bool split = gridDim.y > 1;
-  float *dst = split ? part + ps.part_off[mem] + (int64_t)ks * M * N : ps.y[mem];
-  constexpr int PPR = 8 * NT, RPI = 64 / PPR;  // pieces per row, rows per iteration
-  const int c4 = lane % PPR, ro = lane / PPR;
-  const int col = nt * TC + 4 * c4;
-  float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (!split && bias) {
-    if (col + 3 < N) {
-      bv = make_float4(bias[col], bias[col + 1], bias[col + 2], bias[col + 3]);
-    } else {
-      if (col < N) bv.x = bias[col];
-      if (col + 1 < N) bv.y = bias[col + 1];
-      if (col + 2 < N) bv.z = bias[col + 2];
-    }
-  }
-  const bool vec_ok = (N % 4) == 0 && (split || ps.y_vec[mem]);
-#pragma unroll 4
-  for (int it = 0; it < 32 / RPI; it++) {
-    const int r = RPI * it + ro;
-    const int row = m32 * 32 + r;
-    float4v v = *reinterpret_cast<const float4v *>(&stage[r * TC + 4 * c4]);
-    v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
-    if (row < M) {
-      float *p = dst + (int64_t)row * N + col;
-      if (vec_ok && col + 3 < N) {
-        __builtin_nontemporal_store(v, reinterpret_cast<float4v *>(p));
-      } else {
-        if (col < N) p[0] = v[0];
-        if (col + 1 < N) p[1] = v[1];
-        if (col + 2 < N) p[2] = v[2];
-        if (col + 3 < N) p[3] = v[3];
-      }
-    }
-  }
+    for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
+  prefill_epilogue<NT>(acc, lds, ps, mem, nt, m32, M, c4n, kg0, kg1, K, a, nf, wq, scales, zp4,
+                       nb, nbh, lbs, has_zp, N, bias, part, ks);
 }
 
 }  // namespace
@@ -513,16 +890,21 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
   uint8_t *nf = reinterpret_cast<uint8_t *>(base + off_nf);
   float *part = ksplit > 1 ? reinterpret_cast<float *>(base + off_part) : nullptr;
   const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
-  const int64_t groups = (mpad / 32) * d.c4 * 2;  // (m32, kg, st)
-  hipLaunchKernelGGL(k_af8x3, dim3((unsigned)groups), dim3(256), 0, st, a_dev, M, w0->K,
-                     (int)d.c4, vec, aq, asc, nf);
-  MG_TRY(mg_launch_check("k_af8x3"));
   const int has_zp = d.zp_kind == MG_ZP_UINT4;
   PrefillSet ps{};
   ReduceSet rs{};
   int ct = 0;
   int64_t eend = 0;
   make_prefill_sets(n, w, y_dev, M, ksplit, nt, &ps, &rs, &ct, &eend);
+  bool f6 = true;  // every member has its prefill images
+  for (int i = 0; i < n; i++) f6 = f6 && ps.img[i] != nullptr;
+  if (f6)
+    hipLaunchKernelGGL(k_af6x3, dim3((unsigned)((mpad / 32) * d.c4)), dim3(256), 0, st, a_dev, M,
+                       w0->K, (int)d.c4, vec, reinterpret_cast<uint8_t *>(aq), asc, nf);
+  else
+    hipLaunchKernelGGL(k_af8x3, dim3((unsigned)((mpad / 32) * d.c4 * 2)), dim3(256), 0, st, a_dev,
+                       M, w0->K, (int)d.c4, vec, aq, asc, nf);
+  MG_TRY(mg_launch_check(f6 ? "k_af6x3" : "k_af8x3"));
   // (256-row workgroups of 8 waves, k_gemm_f8x3<4, 8>, dequantise each
   // weight tile once for twice the rows; measured 2-4% slower on the lm_head
   // at M = 512, so 128-row tiles are used.)
@@ -531,12 +913,40 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
 #define MG_F8_ARGS                                                                         \
   aq, asc, nf, a_dev, w0->K, ps, part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,          \
       __builtin_ctzll(d.bs), has_zp, mtiles, ct, kps
-  if (nt == 4)
+  const uint8_t *aq6 = reinterpret_cast<const uint8_t *>(aq);
+#define MG_F6_ARGS                                                                         \
+  aq6, asc, nf, a_dev, w0->K, ps, part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,         \
+      __builtin_ctzll(d.bs), has_zp, mtiles, ct, kps
+  if (f6 && nt == 4)
+    hipLaunchKernelGGL((k_gemm_f6x3<4>), grid, dim3(256), 0, st, MG_F6_ARGS);
+  else if (f6)
+    hipLaunchKernelGGL((k_gemm_f6x3<2>), grid, dim3(256), 0, st, MG_F6_ARGS);
+  else if (nt == 4)
     hipLaunchKernelGGL((k_gemm_f8x3<4, 4>), grid, dim3(256), 0, st, MG_F8_ARGS);
   else
     hipLaunchKernelGGL((k_gemm_f8x3<2, 4>), grid, dim3(256), 0, st, MG_F8_ARGS);
 #undef MG_F8_ARGS
-  MG_TRY(mg_launch_check("k_gemm_f8x3"));
+#undef MG_F6_ARGS
+  MG_TRY(mg_launch_check(f6 ? "k_gemm_f6x3" : "k_gemm_f8x3"));
   if (ksplit > 1) MG_TRY(launch_gemm_reduce(st, part, rs, eend, ksplit));
+  return MG_OK;
+}
+
+bool mg_nbits_f8_eligible(const mg_nbits_dev &d) {
+  return d.bs >= KGRP && d.zp_kind != MG_ZP_FLOAT;
+}
+
+mg_status mg_nbits_f8_images(mg_ctx *ctx, mg_weight *w) {
+  mg_nbits_dev &d = w->nbits;
+  const size_t bytes = (size_t)d.ng * 2 * d.c4 * 3072;  // 3/4 byte per (padded) weight
+  MG_HIP(hipMalloc(&d.img, bytes));
+  w->device_bytes += (int64_t)bytes;
+  const int64_t n = d.ng * d.c4 * 64;  // (cg, kg, col)
+  const int has_zp = d.zp_kind == MG_ZP_UINT4;
+  hipLaunchKernelGGL(k_f6_images, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream,
+                     reinterpret_cast<const uint4 *>(d.wq), d.zp4, has_zp, n, (int)d.c4,
+                     (int)d.nbh, __builtin_ctzll(d.bs), static_cast<uint8_t *>(d.img));
+  MG_TRY(mg_launch_check("k_f6_images"));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
   return MG_OK;
 }

@@ -85,6 +85,12 @@ class Context:
         the records)."""
         check(lib.mg_ctx_set_profiling(self.handle, int(bool(enable))))
 
+    def set_prefill_images(self, enable: bool = True):
+        """Whether MatMulNBits weights created on this context from now on
+        keep prefill images (e4m3 (q - zp), 1 byte per weight, for the fp8
+        prefill GEMM; default on).  Same results either way."""
+        check(lib.mg_ctx_set_prefill_images(self.handle, int(bool(enable))))
+
     def profile_records(self) -> list:
         """[(op type, device ms)] of the profiled ops, in issue order (waits
         for them)."""

@@ -1,0 +1,123 @@
+"""Prefill images of MatMulNBits weights (mg_ctx_set_prefill_images): weights
+with images run the fp6 prefill GEMM (the image holds (q - zp) / 2 as e2m3
+fragments, the activations go as three e2m3 digits); weights without them
+run the fp8 GEMM that dequantises each tile.  Both are checked against the
+oracle to the MatMulNBits bar, and the rows with a non-finite activation
+must carry the same Inf / NaN pattern.  Shapes cover 128- and 64-column
+tiles, a K split with its ordered partial sum, ragged M and N, no zero
+points, blocks of 256 and 512, and a sibling group whose members have
+images or not."""
+import numpy as np
+import pytest
+
+import golden_io as G
+import oracle
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from onnx_runtime_dart_amd import ops as _ops
+    return _ops
+
+
+def make_nbits(rng, n, k, bs, zp_mode):
+    nb = (k + bs - 1) // bs
+    b = rng.integers(0, 256, (n, nb, bs // 2), dtype=np.uint8)
+    s = rng.uniform(0.005, 0.05, (n, nb)).astype(np.float32)
+    zp = rng.integers(0, 256, (n, (nb + 1) // 2), dtype=np.uint8) if zp_mode == "packed" else None
+    return b, s, zp
+
+
+def weight(ops, images, *args, **kw):
+    ctx = ops.default_context()
+    ctx.set_prefill_images(images)
+    try:
+        return ops.NBitsWeight(*args, **kw)
+    finally:
+        ctx.set_prefill_images(True)
+
+
+CASES = [
+    # (M, K, N, bs, zp_mode, bias)
+    (512, 1024, 8192 + 64, 128, "packed", True),  # 128-column tiles
+    (130, 2048, 1000, 256, "none", False),        # ragged M and N
+    (64, 4096, 300, 128, "packed", True),         # 64-column tiles, K split
+    (17, 200, 70, 128, "packed", True),           # K not a multiple of 128
+    (300, 1024, 4096, 512, "none", True),
+]
+
+
+@pytest.mark.parametrize("m,k,n,bs,zp_mode,with_bias", CASES)
+def test_images_and_dequantising_gemm_against_oracle(ops, m, k, n, bs, zp_mode, with_bias):
+    rng = np.random.default_rng(0x5EED0090 + m + k + n + bs)
+    b, s, zp = make_nbits(rng, n, k, bs, zp_mode)
+    bias = rng.standard_normal(n).astype(np.float32) if with_bias else None
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a[m // 2, k // 3] = np.inf  # a non-finite row: the epilogue's pattern on both
+    w_img = weight(ops, True, b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    w_deq = weight(ops, False, b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    bytes_img, bytes_deq = w_img.info()[2], w_deq.info()[2]
+    kpad = -(-k // 128) * 128
+    ngp = -(-n // 128) * 2  # column groups, padded to an even count
+    assert bytes_img - bytes_deq == ngp * 48 * kpad  # 3/4 byte per padded weight
+    y_img, y_deq = w_img(a), w_deq(a)
+    np.testing.assert_array_equal(w_img(a), y_img)
+    bad = m // 2
+    for f in (np.isnan, np.isposinf, np.isneginf):
+        np.testing.assert_array_equal(f(y_img[bad]), f(y_deq[bad]))
+    assert not np.isfinite(y_img[bad]).any()
+    cols = np.unique(np.concatenate([np.arange(0, min(n, 64)), np.arange(n - min(n, 40), n)]))
+    rows = [r for r in range(m) if r != bad][:48]
+    ref = oracle.matmul_nbits(a[rows], b[cols], s[cols], None if zp is None else zp[cols], k=k,
+                              n=len(cols), block_size=bs,
+                              bias=None if bias is None else bias[cols])
+    assert G.rms_error(y_img[np.ix_(rows, cols)], ref) <= TOL
+    assert G.rms_error(y_deq[np.ix_(rows, cols)], ref) <= TOL
+    w_img.release()
+    w_deq.release()
+
+
+def test_small_blocks_have_no_images(ops):
+    # Blocks below 128 run the fp16 prefill GEMM: no images, same footprint.
+    rng = np.random.default_rng(0x5EED0091)
+    b, s, zp = make_nbits(rng, 256, 512, 64, "packed")
+    w1 = weight(ops, True, b, s, zp, k=512, n=256, block_size=64)
+    w2 = weight(ops, False, b, s, zp, k=512, n=256, block_size=64)
+    assert w1.info()[2] == w2.info()[2]
+    w1.release()
+    w2.release()
+
+
+def test_group_with_and_without_images(ops):
+    # Sibling weights in one launch: the fp6 GEMM when every member has
+    # images, else the dequantising fp8 GEMM (a mixed group gives bitwise the
+    # group without images).
+    rng = np.random.default_rng(0x5EED0092)
+    m, k, bs = 256, 1024, 128
+    ns = [3072, 1024]
+    hw = [make_nbits(rng, n, k, bs, "packed") for n in ns]
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    ad = ops.DeviceBuffer.from_array(a)
+    outs = []
+    for images in [(True, True), (True, False), (False, False)]:
+        ws = [weight(ops, img, b, s, z, k=k, n=n, block_size=bs)
+              for img, (b, s, z), n in zip(images, hw, ns)]
+        ys = [ops.DeviceBuffer.from_array(np.full((m, n), np.nan, np.float32)) for n in ns]
+        ops.matmul_nbits_group_dev(ws, ad.ptr, m, [y.ptr for y in ys])
+        outs.append([y.to_array((m, n), np.float32) for y, n in zip(ys, ns)])
+        for w in ws:
+            w.release()
+        for y in ys:
+            y.free()
+    ad.free()
+    for got, want in zip(outs[1], outs[2]):
+        np.testing.assert_array_equal(got, want)
+    for (b, s, z), n, y6, y8 in zip(hw, ns, outs[0], outs[2]):
+        cols = np.arange(n - 50, n)
+        ref = oracle.matmul_nbits(a[:40], b[cols], s[cols], z[cols], k=k, n=len(cols),
+                                  block_size=bs)
+        assert G.rms_error(y6[:40, cols], ref) <= TOL
+        assert G.rms_error(y8[:40, cols], ref) <= TOL
