@@ -10,7 +10,10 @@ import onnx_writer as W
 import oracle
 
 pytestmark = pytest.mark.gpu
-TOL = 1e-4
+# The MatMulNBits bar: max|gpu - ref| <= 1e-3 * rms(ref).  A repacking mistake
+# gives errors of order one; the 64-row launches run the fp6 prefill GEMM
+# (three e2m3 activation digits, ~1.5e-4 at these shapes).
+TOL = 1e-3
 
 
 @pytest.fixture(scope="module")
