@@ -1963,9 +1963,10 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
     // workgroups per CU) split K over 8 waves, so that their few workgroups
     // keep more k groups' loads in flight.  (16 waves would cap the kernel
     // at 128 registers and spill.)  The widest (at least four workgroups of
-    // whole column groups per CU) take 2 waves: twice the k groups per wave
-    // behind one prologue, twice the workgroups resident per CU (Llama
-    // lm_head 2048 x 128256 at M = 4 / 16: 50.5 / 51.1 -> 47.2 / 47.9 us).
+    // whole column groups per CU) take one wave: all k groups in one wave
+    // behind one prologue, no cross-wave sum, four times the workgroups
+    // resident per CU (Llama lm_head 2048 x 128256 at M = 4 / 16: 50.5 /
+    // 51.1 us with 4 waves, 47.2 / 47.9 with 2, 44.0 / 44.7 with 1).
     // Tiles per workgroup: narrow weights (fewer column groups than CUs)
     // take 2 or 1 of a column group's four 16-column tiles per workgroup.
 #ifndef MG_GEMV16_WG_PER_CU
@@ -1976,7 +1977,7 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
     const int64_t wgs = ng * (4 / tpw);
     int nw = 4;
     if (wgs < 2 * cus && d.c4 >= 8) nw = 8;
-    if (wgs >= 4 * cus && tpw == 4) nw = 2;
+    if (wgs >= 4 * cus && tpw == 4) nw = 1;
 #define MG_DEC_LAUNCH(SJ_, NW_, TPW_)                                                      \
   hipLaunchKernelGGL((k_gemv_mfma<SJ_, NW_, TPW_>), dim3((unsigned)wgs), dim3(NW_ * 64), 0, \
                      st, ahl, texp, gs, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,           \
@@ -1987,7 +1988,7 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
   else MG_DEC_LAUNCH(SJ_, NW_, 1)
 #define MG_DEC_NW(SJ_)               \
   if (nw == 8) { MG_DEC_TPW(SJ_, 8); } \
-  else if (nw == 2) { MG_DEC_LAUNCH(SJ_, 2, 4); } \
+  else if (nw == 1) { MG_DEC_LAUNCH(SJ_, 1, 4); } \
   else { MG_DEC_TPW(SJ_, 4); }
     if (segj == 1) { MG_DEC_NW(1); }
     else if (segj == 2) { MG_DEC_NW(2); }
