@@ -183,79 +183,88 @@ __device__ inline void pack6x16(const uint32_t (&c)[16], uint32_t (&w)[3]) {
 // asc[(m32 * c4n + kg) * 2 + st][l] = the three E8M0 scale bytes of lane l's
 // block (digit d in byte d), nf[(row * c4n + kg) * 4 + 2 st + h] = 1 when
 // the block held a non-finite value.  Rows >= M and k >= K are zeros.
-// Thread = 16 consecutive k of one row, t = 8 r + s with s = 4 st + 2 h + e
-// (k = 128 kg + 16 s, fields 16 e .. + 15 of lane r + 32 h); the two halves
-// of a block meet by shuffles (xor 1), and the e = 1 thread hands its first
-// dword to the e = 0 thread, so that each writes one piece of the lane.
+// Workgroup = one (m32, kg, st); thread = 8 consecutive k of one row, t = 8 r
+// + s with s = 4 h + e (k = 128 kg + 64 st + 8 s: fields 8 e .. + 7 of lane
+// r + 32 h, bits 48 e .. + 47 of its six dwords).  The four quarters of a
+// block meet by shuffles (max, and the 48-bit pieces: quarter 0 writes dwords
+// 0-3, quarter 1 dwords 4-5).
 __global__ __launch_bounds__(256) void k_af6x3(const float *__restrict__ a, int64_t M,
                                                int64_t K, int c4n, int vec,
                                                uint8_t *__restrict__ aq,
                                                uint32_t *__restrict__ asc,
                                                uint8_t *__restrict__ nf) {
   const int t = threadIdx.x;
-  const int64_t mk = blockIdx.x;  // m32 * c4n + kg
+  const int64_t bid = blockIdx.x;  // (m32 * c4n + kg) * 2 + st
+  const int st = (int)(bid & 1);
+  const int64_t mk = bid >> 1;
   const int kg = (int)(mk % c4n);
   const int64_t m32 = mk / c4n;
   const int r = t >> 3, sg = t & 7;
-  const int st = sg >> 2, h = (sg >> 1) & 1, e = sg & 1;
+  const int h = sg >> 2, e = sg & 3;
   const int64_t row = m32 * 32 + r;
   const bool live = row < M;
   const float *arow = a + (live ? row : 0) * K;
-  const int64_t k0 = (int64_t)kg * KGRP + 16 * sg;
-  float v[16];
-  if (live && vec && k0 + 16 <= K) {
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const float4 x = *reinterpret_cast<const float4 *>(arow + k0 + 4 * q);
-      v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
-    }
+  const int64_t k0 = (int64_t)kg * KGRP + 64 * st + 8 * sg;
+  float v[8];
+  if (live && vec && k0 + 8 <= K) {
+    const float4 x0 = *reinterpret_cast<const float4 *>(arow + k0);
+    const float4 x1 = *reinterpret_cast<const float4 *>(arow + k0 + 4);
+    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
   } else {
 #pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = (live && k0 + i < K) ? arow[k0 + i] : 0.f;
+    for (int i = 0; i < 8; i++) v[i] = (live && k0 + i < K) ? arow[k0 + i] : 0.f;
   }
   int bad = 0;
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
+  for (int i = 0; i < 8; i++) {
     if (!isfinite(v[i])) {
       bad = 1;
       v[i] = 0.f;
     }
   }
   bad |= __shfl_xor(bad, 1);
+  bad |= __shfl_xor(bad, 2);
   const int lane = r + 32 * h;
-  uint8_t *base = aq + (mk * 2 + st) * 3 * 1536;
+  uint8_t *base = aq + bid * 3 * 1536;
   uint32_t scales = 0;
 #pragma unroll
   for (int d = 0; d < 3; d++) {
     float mx = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
+    for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[i]));
     mx = fmaxf(mx, __shfl_xor(mx, 1));
+    mx = fmaxf(mx, __shfl_xor(mx, 2));
     int E = 0;
     if (mx > 0.f) {
       int ex;
       frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
       E = max(ex - 2, -127);
     }
-    uint32_t c[16];
+    uint32_t lo = 0, hi = 0;  // this quarter's 48 bits
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
+    for (int i = 0; i < 8; i++) {
       const float y = ldexpf(v[i], -E);  // exact
       float val;
-      c[i] = e2m3_rne(y, &val);
+      const uint32_t c = e2m3_rne(y, &val);
       v[i] = ldexpf(y - val, E);  // exact, no overflow
+      const int bit = 6 * i;
+      if (bit < 32) lo |= c << bit;
+      if (bit > 26) hi |= bit >= 32 ? c << (bit - 32) : c >> (32 - bit);
     }
-    uint32_t w[3];
-    pack6x16(c, w);
-    const uint32_t w0p = __shfl_xor(w[0], 1);
+    const uint32_t x1 = __shfl_xor(lo, 1), y1 = __shfl_xor(hi, 1);
+    const uint32_t x2 = __shfl_xor(lo, 2), y2 = __shfl_xor(hi, 2);
+    const uint32_t x3 = __shfl_xor(lo, 3), y3 = __shfl_xor(hi, 3);
     if (e == 0)
-      *reinterpret_cast<uint4 *>(base + d * 1536 + 16 * lane) = make_uint4(w[0], w[1], w[2], w0p);
-    else
-      *reinterpret_cast<uint2 *>(base + d * 1536 + 1024 + 8 * lane) = make_uint2(w[1], w[2]);
+      *reinterpret_cast<uint4 *>(base + d * 1536 + 16 * lane) =
+          make_uint4(lo, hi | (x1 << 16), (x1 >> 16) | (y1 << 16), x2);
+    else if (e == 1)  // quarter 2 is lane xor 3 here, quarter 3 lane xor 2
+      *reinterpret_cast<uint2 *>(base + d * 1536 + 1024 + 8 * lane) =
+          make_uint2(y3 | (x2 << 16), (x2 >> 16) | (y2 << 16));
     scales |= (uint32_t)(E + 127) << (8 * d);
   }
   if (e == 0) {
-    asc[(mk * 2 + st) * 64 + lane] = scales;
+    asc[bid * 64 + lane] = scales;
     nf[(row * c4n + kg) * 4 + 2 * st + h] = (uint8_t)bad;
   }
 }
@@ -899,7 +908,7 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
   bool f6 = true;  // every member has its prefill images
   for (int i = 0; i < n; i++) f6 = f6 && ps.img[i] != nullptr;
   if (f6)
-    hipLaunchKernelGGL(k_af6x3, dim3((unsigned)((mpad / 32) * d.c4)), dim3(256), 0, st, a_dev, M,
+    hipLaunchKernelGGL(k_af6x3, dim3((unsigned)((mpad / 32) * d.c4 * 2)), dim3(256), 0, st, a_dev, M,
                        w0->K, (int)d.c4, vec, reinterpret_cast<uint8_t *>(aq), asc, nf);
   else
     hipLaunchKernelGGL(k_af8x3, dim3((unsigned)((mpad / 32) * d.c4 * 2)), dim3(256), 0, st, a_dev,
