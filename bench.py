@@ -562,8 +562,9 @@ def decode_sweep(torch, ops, ctx, T, randn, dev, args, stream):
 
 def nbits_float_zp(torch, ops, ctx, T, randn, dev, args):
     """MatMulNBits with float zero points (the form some exporters write) at
-    M = 512 on the Qwen3 gate and lm_head shapes: columns dequantised to fp32
-    in chunks and run on the fp32 MFMA GEMM."""
+    M = 512 on the Qwen3 gate and lm_head shapes: the fp6 GEMM on the prefill
+    images (q / 2), the zero point taken out as z times the activations' row
+    sums."""
     rng = np.random.default_rng(0x5EED0004)
     out = {}
     for name, k, n in (("gate", 1024, 3072), ("lm_head", 1024, 151936)):

@@ -96,14 +96,16 @@ mg_status mg_ctx_profile_clear(mg_ctx *ctx);
 
 /* Whether MatMulNBits weights created on this context from now on also keep
  * prefill images (default: enabled).  An image holds the weight's integers
- * (q - zp) as e4m3 bytes in the fragment order of the fp8 prefill GEMM, one
+ * (q - zp) / 2 (q / 2 with float zero points) as fp6 e2m3 MFMA operands, 3/4
  * byte per weight on top of the packed half byte, built on the device at
- * upload; the GEMM then loads them instead of dequantising each tile for
- * every 128 rows.  Results are the same bit for bit either way.  Only block
- * sizes >= 128 with packed or default zero points have images (the weights
- * that GEMM runs).  No counterpart in the reference, which dequantises the
- * weight to fp32 on every call (lib/src/onnx_qlinear_ops.dart:208-226); for
- * callers that run only decode rows and want the smaller footprint. */
+ * upload; prefill calls (M > 16, or M > 4 with float zero points) on weights
+ * with images run the fp6 GEMM, those without run the fp8 GEMM that
+ * dequantises each tile (or, for float zero points, the fp32 path).  Both
+ * meet the MatMulNBits tolerance; their results differ in rounding.  Only
+ * block sizes >= 128 have images.  No counterpart in the reference, which
+ * dequantises the weight to fp32 on every call
+ * (lib/src/onnx_qlinear_ops.dart:208-226); for callers that run only decode
+ * rows and want the smaller footprint. */
 mg_status mg_ctx_set_prefill_images(mg_ctx *ctx, int32_t enable);
 
 /* Cooperative cancellation and byte budget, checked before every launch

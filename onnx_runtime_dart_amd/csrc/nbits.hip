@@ -1383,7 +1383,8 @@ __global__ __launch_bounds__(256) void k_nbits_dequant_f32(
 
 // The fp8 prefill GEMM (nbits_f8.hip): workspace layout for mpad rows and c4
 // k groups (returns the bytes before the split-K partials), and the launch.
-size_t mg_nbits_f8_ws(int64_t mpad, int64_t c4, size_t *off_asc, size_t *off_nf);
+size_t mg_nbits_f8_ws(int64_t mpad, int64_t c4, size_t *off_asc, size_t *off_nf,
+                      size_t *off_rs);
 mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, const float *a_dev,
                               int64_t M, float *const *y_dev, void *ws, int64_t mpad, int nt,
                               int ksplit, int kps, size_t off_part);
@@ -1410,7 +1411,7 @@ struct NbitsPlan {
 // ng_total / n_total: column groups / columns of all weights launched together
 // (sibling weights sharing one input).
 NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t ng_total,
-                     int64_t n_total) {
+                     int64_t n_total, bool imgs) {
   const mg_nbits_dev &d = w->nbits;
   NbitsPlan p;
   p.M = M;
@@ -1506,7 +1507,9 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
       p.cs_pf = d.c4 > 16 ? 8 : 4;
       p.lds = (size_t)std::max<int64_t>(d.c4 * per_kg, 4 * 16 * 4);
     }
-  } else if (d.bs >= 32 && int_zp) {
+  } else if ((d.bs >= 32 && int_zp) || (d.bs >= KGRP && imgs)) {
+    // (Float zero points at blocks >= 128 on weights with prefill images:
+    // the fp6 GEMM with the zero point taken out as a row sum.)
 #ifndef MG_PREFILL_F8
 #define MG_PREFILL_F8 1
 #endif
@@ -1531,8 +1534,8 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
     p.kps = (int)((d.c4 + ks - 1) / ks);
     p.ksplit = (int)((d.c4 + p.kps - 1) / p.kps);
     if (p.path == 4) {
-      size_t o_asc = 0, o_nf = 0;  // fp8 digits, scale words, non-finite flags
-      p.off_c = mg_nbits_f8_ws(p.mpad, d.c4, &o_asc, &o_nf);  // split-K partials after them
+      size_t o_asc = 0, o_nf = 0, o_rs = 0;  // digits, scale words, flags, row sums
+      p.off_c = mg_nbits_f8_ws(p.mpad, d.c4, &o_asc, &o_nf, &o_rs);  // split-K partials after
     } else {
       p.off_a = 0;  // ahl: mpad * kpad * 2 fp16
       p.off_b = mg_align(p.off_a + (size_t)p.mpad * d.kpad * 4);  // texp [row]
@@ -1873,7 +1876,7 @@ void mg_nbits_free(mg_weight *w) {
 }
 
 size_t mg_nbits_ws_bytes(const mg_ctx *ctx, const mg_weight *w, int64_t M) {
-  return plan_nbits(ctx, w, M, w->nbits.ng, w->N).total;
+  return plan_nbits(ctx, w, M, w->nbits.ng, w->N, w->nbits.img != nullptr).total;
 }
 
 namespace {
@@ -1881,11 +1884,13 @@ namespace {
 // sized for all members.
 NbitsPlan plan_group(const mg_ctx *ctx, int n, const mg_weight *const *w, int64_t M) {
   int64_t ng = 0, nn = 0;
+  bool imgs = true;  // every member has prefill images
   for (int i = 0; i < n; i++) {
     ng += w[i]->nbits.ng;
     nn += w[i]->N;
+    imgs = imgs && w[i]->nbits.img != nullptr;
   }
-  return plan_nbits(ctx, w[0], M, ng, nn);
+  return plan_nbits(ctx, w[0], M, ng, nn, imgs);
 }
 }  // namespace
 

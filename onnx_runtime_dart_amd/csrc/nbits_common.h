@@ -62,6 +62,7 @@ struct PrefillSet {
   const uint4 *img[GMAX];  // prefill images (mg_nbits_dev::img) or null
   const float *scales[GMAX];
   const uint8_t *zp4[GMAX];
+  const float *zpf[GMAX];  // float zero points (MG_ZP_FLOAT) or null
   const float *bias[GMAX];
   float *y[GMAX];
   int64_t part_off[GMAX];
@@ -149,6 +150,7 @@ inline void make_prefill_sets(int n, const mg_weight *const *w, float *const *y_
     // The kernels read zero-point bytes unconditionally (branch-free); without
     // zero points they are pointed at the scales, which are at least as large.
     ps->zp4[i] = has_zp ? di.zp4 : reinterpret_cast<const uint8_t *>(di.scales);
+    ps->zpf[i] = di.zpf;
     ps->bias[i] = rs->bias[i] = di.bias;
     ps->y[i] = rs->y[i] = y_dev[i];
     ps->N[i] = rs->N[i] = (int)w[i]->N;

@@ -187,12 +187,15 @@ __device__ inline void pack6x16(const uint32_t (&c)[16], uint32_t (&w)[3]) {
 // + s with s = 4 h + e (k = 128 kg + 64 st + 8 s: fields 8 e .. + 7 of lane
 // r + 32 h, bits 48 e .. + 47 of its six dwords).  The four quarters of a
 // block meet by shuffles (max, and the 48-bit pieces: quarter 0 writes dwords
-// 0-3, quarter 1 dwords 4-5).
+// 0-3, quarter 1 dwords 4-5).  With rsum (float zero points), also the
+// sum of the row's finite values over the step, rsum[(row * c4n + kg) * 2 +
+// st], added in a fixed order (shuffles over the 8 threads of the row).
 __global__ __launch_bounds__(256) void k_af6x3(const float *__restrict__ a, int64_t M,
                                                int64_t K, int c4n, int vec,
                                                uint8_t *__restrict__ aq,
                                                uint32_t *__restrict__ asc,
-                                               uint8_t *__restrict__ nf) {
+                                               uint8_t *__restrict__ nf,
+                                               float *__restrict__ rsum) {
   const int t = threadIdx.x;
   const int64_t bid = blockIdx.x;  // (m32 * c4n + kg) * 2 + st
   const int st = (int)(bid & 1);
@@ -225,6 +228,13 @@ __global__ __launch_bounds__(256) void k_af6x3(const float *__restrict__ a, int6
   }
   bad |= __shfl_xor(bad, 1);
   bad |= __shfl_xor(bad, 2);
+  if (rsum) {
+    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    if (sg == 0) rsum[(row * c4n + kg) * 2 + st] = sum;
+  }
   const int lane = r + 32 * h;
   uint8_t *base = aq + bid * 3 * 1536;
   uint32_t scales = 0;
@@ -287,10 +297,13 @@ __device__ inline uint32_t e2m3_half_int(int v) {
 // + kg) * 64 + col: dword j of octet row g holds k = 32 j + 8 g + t, so dword
 // j of all four gives the 32 fields (i = 8 g + t) of step j / 2, lane half
 // j % 2.
+// Without packed zero points the codes are of (q - zdef) / 2: zdef = 8 (the
+// default zero point), or 0 for float zero points, which the GEMM then takes
+// out as z * (sum of the activations).
 __global__ __launch_bounds__(256) void k_f6_images(const uint4 *__restrict__ wq,
                                                    const uint8_t *__restrict__ zp4, int has_zp,
-                                                   int64_t n, int c4n, int nbh, int lbs,
-                                                   uint8_t *__restrict__ img) {
+                                                   int zdef, int64_t n, int c4n, int nbh,
+                                                   int lbs, uint8_t *__restrict__ img) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   const int col = (int)(i & 63);
@@ -301,7 +314,7 @@ __global__ __launch_bounds__(256) void k_f6_images(const uint4 *__restrict__ wq,
 #pragma unroll
   for (int g = 0; g < 4; g++) p[g] = wq[(cgk * 4 + g) * 64 + col];
   const int blk = (kg * KGRP) >> lbs;
-  int z = 8;
+  int z = zdef;
   if (has_zp)
     z = (int)((zp4[(cg * nbh + min(blk / 2, nbh - 1)) * 64 + sz_pos(col)] >> ((blk & 1) * 4)) &
               15u);
@@ -335,10 +348,12 @@ __device__ inline float16v mfma_digit(const int8v &a, const int8v &b, const floa
 }
 
 // Dequantised weight (q - zp) * s of column col at k, in fp32 (the
-// non-finite pattern only needs its sign and whether it is zero).
+// non-finite pattern only needs its sign and whether it is zero); zpk is the
+// zero-point kind (MG_ZP_NONE: 8, MG_ZP_UINT4: packed zp4, MG_ZP_FLOAT: zpf).
 __device__ inline float nbits_weight(const uint4 *__restrict__ wq, const float *__restrict__ sc,
-                                     const uint8_t *__restrict__ zp4, int c4n, int nb, int nbh,
-                                     int lbs, int has_zp, int col, int k) {
+                                     const uint8_t *__restrict__ zp4,
+                                     const float *__restrict__ zpf, int c4n, int nb, int nbh,
+                                     int lbs, int zpk, int col, int k) {
   const int cg = col >> 6, cl = col & 63;
   const int kg = k >> 7, kk = k & 127;
   const int j = kk >> 5, g = (kk >> 3) & 3, tt = kk & 7;
@@ -346,10 +361,12 @@ __device__ inline float nbits_weight(const uint4 *__restrict__ wq, const float *
                        (((int64_t)cg * c4n + kg) * 256 + g * 64 + cl) * 4 + j;
   const int q = (int)((*wd >> (4 * nib_pos(tt))) & 15u);
   const int blk = min(k >> lbs, nb - 1);
-  const int z = has_zp ? (int)((zp4[((int64_t)cg * nbh + blk / 2) * 64 + sz_pos(cl)] >>
-                                (4 * (blk & 1))) & 15u)
-                       : 8;
-  return (float)(q - z) * sc[((int64_t)cg * nb + blk) * 64 + sz_pos(cl)];
+  const float s = sc[((int64_t)cg * nb + blk) * 64 + sz_pos(cl)];
+  if (zpk == MG_ZP_FLOAT) return ((float)q - zpf[((int64_t)cg * nb + blk) * 64 + sz_pos(cl)]) * s;
+  const int z = zpk == MG_ZP_UINT4 ? (int)((zp4[((int64_t)cg * nbh + blk / 2) * 64 + sz_pos(cl)] >>
+                                            (4 * (blk & 1))) & 15u)
+                                   : 8;
+  return (float)(q - z) * s;
 }
 
 // Epilogue of the prefill GEMMs: stages each wave's 32 x 32 NT tile of
@@ -362,8 +379,9 @@ __device__ inline void prefill_epilogue(
     const float16v (&acc)[NT], uint4 *lds, const PrefillSet &ps, int mem, int nt, int m32, int M,
     int c4n, int kg0, int kg1, int64_t K, const float *__restrict__ a,
     const uint8_t *__restrict__ nf, const uint4 *__restrict__ wq,
-    const float *__restrict__ scales, const uint8_t *__restrict__ zp4, int nb, int nbh, int lbs,
-    int has_zp, int N, const float *__restrict__ bias, float *__restrict__ part, int ks) {
+    const float *__restrict__ scales, const uint8_t *__restrict__ zp4,
+    const float *__restrict__ zpf, int nb, int nbh, int lbs, int zpk, int N,
+    const float *__restrict__ bias, float *__restrict__ part, int ks) {
   constexpr int TC = 32 * NT;
   const int t = threadIdx.x, lane = t & 63, lc = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -405,7 +423,7 @@ __device__ inline void prefill_epilogue(
             const int c = lane + 64 * u;
             const int col = nt * TC + c;
             if (c >= TC || col >= N) continue;
-            const float wv = nbits_weight(wq, scales, zp4, c4n, nb, nbh, lbs, has_zp, col,
+            const float wv = nbits_weight(wq, scales, zp4, zpf, c4n, nb, nbh, lbs, zpk, col,
                                           (int)(k0 + b));
             if (isnan(xv) || !(wv != 0.f)) fnan[u] = true;
             else if ((xv > 0.f) == (wv > 0.f)) fpos[u] = true;
@@ -689,8 +707,9 @@ __global__ __launch_bounds__(64 * MW, MW == 8 ? 1 : (NT == 4 ? 2 : 3)) void k_ge
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
 
-  prefill_epilogue<NT>(acc, lds, ps, mem, nt, m32, M, c4n, kg0, kg1, K, a, nf, wq, scales, zp4, nb,
-                       nbh, lbs, has_zp, N, bias, part, ks);
+  prefill_epilogue<NT>(acc, lds, ps, mem, nt, m32, M, c4n, kg0, kg1, K, a, nf, wq, scales, zp4,
+                       nullptr, nb, nbh, lbs, has_zp ? MG_ZP_UINT4 : MG_ZP_NONE, N, bias, part,
+                       ks);
 }
 
 
@@ -710,12 +729,16 @@ __device__ inline float16v mfma6_digit(const int8v &a, const int8v &b, const flo
 // KiB: three pieces of NT x 4 bytes per thread, loaded at the start of the
 // previous k group) into LDS instead of dequantising, and stages the
 // columns' block scales.
-template <int NT>
-__global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
+// FZP (float zero points, block_size >= 128): the images hold q / 2 and the
+// k group adds s (sum a q - z R) with R = sum a over its 128 k (the
+// prepass's row sums): its accumulator D starts at -z R instead of zero,
+// with z per column and R per row staged in LDS.
+template <int NT, bool FZP>
+__global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
     const uint8_t *__restrict__ aq, const uint32_t *__restrict__ asc,
-    const uint8_t *__restrict__ nf, const float *__restrict__ a, int64_t K,
-    const PrefillSet ps, float *__restrict__ part, int M, int c4n, int nb, int nbh, int lbs,
-    int has_zp, int mtiles, int ntiles, int kps) {
+    const uint8_t *__restrict__ nf, const float *__restrict__ rsum,
+    const float *__restrict__ a, int64_t K, const PrefillSet ps, float *__restrict__ part,
+    int M, int c4n, int nb, int nbh, int lbs, int zpk, int mtiles, int ntiles, int kps) {
   constexpr int PH = NT / 2;           // column groups per tile
   constexpr int TC = 32 * NT;          // tile columns
   constexpr int SLAB = 192;            // uint4 per slab image of a k group
@@ -726,6 +749,8 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
   typedef typename std::conditional<NT == 4, uint4, uint2>::type piece_t;
   __shared__ uint4 lds[LDS_U4];
   __shared__ float scl[2][32][NT];  // [buf][col % 32][n32]
+  __shared__ float czl[FZP ? 2 : 1][32][NT];  // s * z per column (FZP)
+  __shared__ __align__(16) float rl[FZP ? 2 : 1][128];  // row sums of the tile's rows (FZP)
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int L = blockIdx.x;
@@ -738,6 +763,7 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
   const uint4 *__restrict__ wq = ps.wq[mem];
   const float *__restrict__ scales = ps.scales[mem];
   const uint8_t *__restrict__ zp4 = ps.zp4[mem];
+  const float *__restrict__ zpf = ps.zpf[mem];
   const float *__restrict__ bias = ps.bias[mem];
   const int N = ps.N[mem];
   const int ks = blockIdx.y;
@@ -761,12 +787,23 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
   }
   // Block scale of tile column tc = t % TC (threads t < TC stage it).
   const int tc = t % TC;
-  const __amdgpu_buffer_rsrc_t r_sc = rsrc(scales + (int64_t)(PH * nt + tc / 64) * nb * 64);
+  // (tc / 64 is wave-uniform: one column group per wave.)
+  const int tcg = __builtin_amdgcn_readfirstlane(tc / 64);
+  const __amdgpu_buffer_rsrc_t r_sc = rsrc(scales + (int64_t)(PH * nt + tcg) * nb * 64);
   const unsigned vo_sc = 4u * (unsigned)sz_pos(tc & 63);
   const int nbm1 = nb - 1;
+  // FZP: float zero points like the scales; row sums of row mt * 128 + t % 128
+  // (a uniform resource for the tile's rows, the row in the lane offset).
+  __amdgpu_buffer_rsrc_t r_zf = r_sc, r_rs = r_sc;
+  const unsigned vo_rs = (unsigned)(t & 127) * (unsigned)c4n * 8u;
+  if constexpr (FZP) {
+    r_zf = rsrc(zpf + (int64_t)(PH * nt + tcg) * nb * 64);
+    r_rs = rsrc(rsum + (int64_t)mt * 128 * c4n * 2);
+  }
   struct Meta {
     piece_t im[3];
-    float sc;
+    float sc, zf;
+    float2 rs;
   };
   auto load_meta = [&](int kg, Meta &m) {
 #pragma unroll
@@ -781,6 +818,12 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
     const int blk = (kg * KGRP) >> lbs;
     m.sc = __builtin_bit_cast(
         float, __builtin_amdgcn_raw_buffer_load_b32(r_sc, vo_sc, min(blk, nbm1) * 256, 0));
+    if constexpr (FZP) {
+      m.zf = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(r_zf, vo_sc, min(blk, nbm1) * 256, 0));
+      m.rs = __builtin_bit_cast(float2,
+                                __builtin_amdgcn_raw_buffer_load_b64(r_rs, vo_rs, kg * 8, 0));
+    }
   };
   // Piece j of the images into buffer buf (j < 3); with j == 0 also the
   // block scales.
@@ -789,6 +832,10 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
     if (j == 0 && t < TC) {
       const int blk = (kg * KGRP) >> lbs;
       scl[buf][tc & 31][tc >> 5] = blk < nb ? m.sc : 0.f;
+      if constexpr (FZP) czl[buf][tc & 31][tc >> 5] = blk < nb ? m.zf : 0.f;
+    }
+    if constexpr (FZP) {
+      if (j == 0 && t < 128) rl[buf][t] = m.rs.x + m.rs.y;
     }
   };
   // Digit d of step st of k group kg: this lane's six dwords.
@@ -837,6 +884,17 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
     const int kgn = min(kg + 1, kg1 - 1);  // next k group (clamped)
     Meta mnext;
     load_meta(kgn, mnext);
+    // FZP: this k group's -z R (the lane's 16 rows are 8 i + 4 (lane / 32) +
+    // 0..3 of the wave's 32, i = v / 4).
+    float rr[FZP ? 16 : 1];
+    if constexpr (FZP) {
+      const int lh = lane >> 5;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float4 x = *reinterpret_cast<const float4 *>(&rl[buf][wave * 32 + 8 * i + 4 * lh]);
+        rr[4 * i] = x.x, rr[4 * i + 1] = x.y, rr[4 * i + 2] = x.z, rr[4 * i + 3] = x.w;
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int st = 0; st < 2; st++) {
@@ -852,7 +910,14 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
           }
-          const float16v cin = (st == 0 && d == 0) ? zero16 : D[n];
+          float16v cin = (st == 0 && d == 0) ? zero16 : D[n];
+          if constexpr (FZP) {
+            if (st == 0 && d == 0) {
+              const float z = czl[buf][lc][n];
+#pragma unroll
+              for (int v = 0; v < 16; v++) cin[v] = -z * rr[v];
+            }
+          }
           D[n] = d == 0   ? mfma6_digit<0>(A[0], B[n], cin, (int)sa)
                  : d == 1 ? mfma6_digit<1>(A[1], B[n], cin, (int)sa)
                           : mfma6_digit<2>(A[2], B[n], cin, (int)sa);
@@ -873,16 +938,18 @@ __global__ __launch_bounds__(256, NT == 4 ? 2 : 3) void k_gemm_f6x3(
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
   prefill_epilogue<NT>(acc, lds, ps, mem, nt, m32, M, c4n, kg0, kg1, K, a, nf, wq, scales, zp4,
-                       nb, nbh, lbs, has_zp, N, bias, part, ks);
+                       zpf, nb, nbh, lbs, zpk, N, bias, part, ks);
 }
 
 }  // namespace
 
-size_t mg_nbits_f8_ws(int64_t mpad, int64_t c4, size_t *off_asc, size_t *off_nf) {
+size_t mg_nbits_f8_ws(int64_t mpad, int64_t c4, size_t *off_asc, size_t *off_nf,
+                      size_t *off_rs) {
   const size_t aq = (size_t)mpad * c4 * 128 * 3;  // 3 bytes per element
   *off_asc = mg_align(aq);
   *off_nf = mg_align(*off_asc + (size_t)mpad * c4 * 16);  // 4 scale words per 128 k per row
-  return mg_align(*off_nf + (size_t)mpad * c4 * 4);
+  *off_rs = mg_align(*off_nf + (size_t)mpad * c4 * 4);     // row sums per 64 k
+  return mg_align(*off_rs + (size_t)mpad * c4 * 8);
 }
 
 mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, const float *a_dev,
@@ -892,14 +959,16 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
   const mg_nbits_dev &d = w0->nbits;
   hipStream_t st = ctx->stream;
   char *base = static_cast<char *>(ws);
-  size_t off_asc = 0, off_nf = 0;
-  (void)mg_nbits_f8_ws(mpad, d.c4, &off_asc, &off_nf);
+  size_t off_asc = 0, off_nf = 0, off_rs = 0;
+  (void)mg_nbits_f8_ws(mpad, d.c4, &off_asc, &off_nf, &off_rs);
   uint4 *aq = reinterpret_cast<uint4 *>(base);
   uint32_t *asc = reinterpret_cast<uint32_t *>(base + off_asc);
   uint8_t *nf = reinterpret_cast<uint8_t *>(base + off_nf);
+  float *rsum = reinterpret_cast<float *>(base + off_rs);
   float *part = ksplit > 1 ? reinterpret_cast<float *>(base + off_part) : nullptr;
   const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
   const int has_zp = d.zp_kind == MG_ZP_UINT4;
+  const bool fzp = d.zp_kind == MG_ZP_FLOAT;
   PrefillSet ps{};
   ReduceSet rs{};
   int ct = 0;
@@ -907,9 +976,12 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
   make_prefill_sets(n, w, y_dev, M, ksplit, nt, &ps, &rs, &ct, &eend);
   bool f6 = true;  // every member has its prefill images
   for (int i = 0; i < n; i++) f6 = f6 && ps.img[i] != nullptr;
+  if (fzp && !f6)  // the planner sends float zero points here only with images
+    return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: float zero points without prefill images");
   if (f6)
     hipLaunchKernelGGL(k_af6x3, dim3((unsigned)((mpad / 32) * d.c4 * 2)), dim3(256), 0, st, a_dev, M,
-                       w0->K, (int)d.c4, vec, reinterpret_cast<uint8_t *>(aq), asc, nf);
+                       w0->K, (int)d.c4, vec, reinterpret_cast<uint8_t *>(aq), asc, nf,
+                       fzp ? rsum : nullptr);
   else
     hipLaunchKernelGGL(k_af8x3, dim3((unsigned)((mpad / 32) * d.c4 * 2)), dim3(256), 0, st, a_dev,
                        M, w0->K, (int)d.c4, vec, aq, asc, nf);
@@ -923,13 +995,18 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
   aq, asc, nf, a_dev, w0->K, ps, part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,          \
       __builtin_ctzll(d.bs), has_zp, mtiles, ct, kps
   const uint8_t *aq6 = reinterpret_cast<const uint8_t *>(aq);
+  const int zpk = d.zp_kind;
 #define MG_F6_ARGS                                                                         \
-  aq6, asc, nf, a_dev, w0->K, ps, part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,         \
-      __builtin_ctzll(d.bs), has_zp, mtiles, ct, kps
-  if (f6 && nt == 4)
-    hipLaunchKernelGGL((k_gemm_f6x3<4>), grid, dim3(256), 0, st, MG_F6_ARGS);
+  aq6, asc, nf, rsum, a_dev, w0->K, ps, part, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,   \
+      __builtin_ctzll(d.bs), zpk, mtiles, ct, kps
+  if (f6 && fzp && nt == 4)
+    hipLaunchKernelGGL((k_gemm_f6x3<4, true>), grid, dim3(256), 0, st, MG_F6_ARGS);
+  else if (f6 && fzp)
+    hipLaunchKernelGGL((k_gemm_f6x3<2, true>), grid, dim3(256), 0, st, MG_F6_ARGS);
+  else if (f6 && nt == 4)
+    hipLaunchKernelGGL((k_gemm_f6x3<4, false>), grid, dim3(256), 0, st, MG_F6_ARGS);
   else if (f6)
-    hipLaunchKernelGGL((k_gemm_f6x3<2>), grid, dim3(256), 0, st, MG_F6_ARGS);
+    hipLaunchKernelGGL((k_gemm_f6x3<2, false>), grid, dim3(256), 0, st, MG_F6_ARGS);
   else if (nt == 4)
     hipLaunchKernelGGL((k_gemm_f8x3<4, 4>), grid, dim3(256), 0, st, MG_F8_ARGS);
   else
@@ -941,9 +1018,7 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
   return MG_OK;
 }
 
-bool mg_nbits_f8_eligible(const mg_nbits_dev &d) {
-  return d.bs >= KGRP && d.zp_kind != MG_ZP_FLOAT;
-}
+bool mg_nbits_f8_eligible(const mg_nbits_dev &d) { return d.bs >= KGRP; }
 
 mg_status mg_nbits_f8_images(mg_ctx *ctx, mg_weight *w) {
   mg_nbits_dev &d = w->nbits;
@@ -953,8 +1028,9 @@ mg_status mg_nbits_f8_images(mg_ctx *ctx, mg_weight *w) {
   const int64_t n = d.ng * d.c4 * 64;  // (cg, kg, col)
   const int has_zp = d.zp_kind == MG_ZP_UINT4;
   hipLaunchKernelGGL(k_f6_images, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream,
-                     reinterpret_cast<const uint4 *>(d.wq), d.zp4, has_zp, n, (int)d.c4,
-                     (int)d.nbh, __builtin_ctzll(d.bs), static_cast<uint8_t *>(d.img));
+                     reinterpret_cast<const uint4 *>(d.wq), d.zp4, has_zp,
+                     d.zp_kind == MG_ZP_FLOAT ? 0 : 8, n, (int)d.c4, (int)d.nbh,
+                     __builtin_ctzll(d.bs), static_cast<uint8_t *>(d.img));
   MG_TRY(mg_launch_check("k_f6_images"));
   MG_HIP(hipStreamSynchronize(ctx->stream));
   return MG_OK;

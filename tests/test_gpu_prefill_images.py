@@ -27,7 +27,12 @@ def make_nbits(rng, n, k, bs, zp_mode):
     nb = (k + bs - 1) // bs
     b = rng.integers(0, 256, (n, nb, bs // 2), dtype=np.uint8)
     s = rng.uniform(0.005, 0.05, (n, nb)).astype(np.float32)
-    zp = rng.integers(0, 256, (n, (nb + 1) // 2), dtype=np.uint8) if zp_mode == "packed" else None
+    if zp_mode == "packed":
+        zp = rng.integers(0, 256, (n, (nb + 1) // 2), dtype=np.uint8)
+    elif zp_mode == "float":
+        zp = (rng.standard_normal((n, nb)) * 2 + 8).astype(np.float32)
+    else:
+        zp = None
     return b, s, zp
 
 
@@ -121,3 +126,38 @@ def test_group_with_and_without_images(ops):
                                   block_size=bs)
         assert G.rms_error(y6[:40, cols], ref) <= TOL
         assert G.rms_error(y8[:40, cols], ref) <= TOL
+
+
+FZP_CASES = [
+    # (M, K, N, bs, bias): float zero points on the fp6 GEMM (the zero point
+    # taken out as z times the activations' row sums), against the oracle and
+    # the fp32 path a weight without images takes.
+    (512, 1024, 8192 + 64, 128, True),  # 128-column tiles
+    (200, 2048, 1000, 256, False),      # ragged M and N, blocks of 256
+    (64, 4096, 300, 128, True),         # 64-column tiles, K split
+    (9, 384, 130, 128, True),           # few rows
+]
+
+
+@pytest.mark.parametrize("m,k,n,bs,with_bias", FZP_CASES)
+def test_float_zero_points_on_fp6_gemm(ops, m, k, n, bs, with_bias):
+    rng = np.random.default_rng(0x5EED0093 + m + k + n + bs)
+    b, s, zp = make_nbits(rng, n, k, bs, "float")
+    bias = rng.standard_normal(n).astype(np.float32) if with_bias else None
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    bad = m // 2
+    a[bad, k // 5] = -np.inf
+    w_img = weight(ops, True, b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    w_f32 = weight(ops, False, b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    y_img, y_f32 = w_img(a), w_f32(a)
+    np.testing.assert_array_equal(w_img(a), y_img)
+    for f in (np.isnan, np.isposinf, np.isneginf):
+        np.testing.assert_array_equal(f(y_img[bad]), f(y_f32[bad]))
+    rows = [r for r in range(m) if r != bad][:48]
+    cols = np.unique(np.concatenate([np.arange(0, min(n, 64)), np.arange(n - min(n, 40), n)]))
+    ref = oracle.matmul_nbits(a[rows], b[cols], s[cols], zp[cols], k=k, n=len(cols),
+                              block_size=bs, bias=None if bias is None else bias[cols])
+    assert G.rms_error(y_img[np.ix_(rows, cols)], ref) <= TOL
+    assert G.rms_error(y_f32[np.ix_(rows, cols)], ref) <= TOL
+    w_img.release()
+    w_f32.release()
