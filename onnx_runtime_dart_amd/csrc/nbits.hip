@@ -15,20 +15,27 @@
 //   scales[cg][blk][col], zero points zp4[cg][blk/2][col] (original packed
 //   byte) or zpf[cg][blk][col].
 //
-// Two compute paths:
-//   * M <= 4 ("decode"): activations are quantised per (row, 128-or-block k
-//     slice) to 15-bit fixed point split into four signed int4 digits; each
-//     lane owns one column and streams 16-byte weight loads, multiplying with
-//     v_dot8_i32_i4 against the digit planes (wave-uniform, scalar-loaded).
-//     Zero point and scale are applied once per block in fp32.
-//   * M > 4 ("prefill"): activations become an fp16 pair hi + lo (scaled by a
-//     power of two per row, so hi + lo carries ~22 bits of each element); each
+// Compute paths (plan_nbits picks one per call):
+//   * M <= 2, and M <= 4 with float zero points ("decode"): activations are
+//     quantised per (row, 128-or-block k slice) to 15-bit fixed point split
+//     into four signed int4 digits; each lane owns one column and streams
+//     16-byte weight loads, multiplying with v_dot8_i32_i4 against the digit
+//     planes.  Zero point and scale are applied once per block in fp32.  At
+//     one row: column-slice, split-K and persistent forms of the same sums.
+//   * 3 <= M <= 16 with integer zero points: the 16-row MFMA GEMV
+//     (k_gemv_mfma: fp16 hi/lo activations, weights dequantised per lane).
+//   * Prefill, block >= 128 (nbits_f8.hip): on weights with prefill images
+//     the fp6 GEMM (three e2m3 activation digits; float zero points taken
+//     out as row sums), otherwise the fp8 GEMM that dequantises each tile.
+//   * Prefill, blocks of 32 or 64 with integer zero points: activations as an
+//     fp16 pair hi + lo (scaled by a power of two per row, ~22 bits); each
 //     workgroup unpacks its weight tile once into LDS as exact fp16 (q - zp)
 //     (times 16 for half of the k, matched by a 2^-4 on those activations);
 //     v_mfma_f32_32x32x16_f16 accumulates hi*W and lo*W in fp32 and the block
 //     scale is applied on the fp32 accumulator.
-// Rare forms (float zero points or block_size 16 with M > 4) take a simple
-// per-output kernel.
+//   * The rest with M > 4 (float zero points without images or below block
+//     128, 16-k blocks): columns dequantised to fp32 as the reference does,
+//     in chunks, each chunk on the fp32 MFMA GEMM.
 #include <hip/hip_runtime.h>
 
 #include <errno.h>
