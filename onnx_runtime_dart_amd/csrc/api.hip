@@ -245,6 +245,10 @@ mg_status mg_ctx_destroy(mg_ctx *ctx) {
   }
   for (hipEvent_t e : ctx->prof_pool) (void)hipEventDestroy(e);
   if (ctx->pin) (void)hipHostFree(ctx->pin);
+  if (ctx->up_pin) (void)hipHostFree(ctx->up_pin);
+  if (ctx->up_dev) (void)hipFree(ctx->up_dev);
+  for (hipEvent_t e : ctx->up_done)
+    if (e) (void)hipEventDestroy(e);
   if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return MG_OK;

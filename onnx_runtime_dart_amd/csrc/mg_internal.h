@@ -68,6 +68,13 @@ struct mg_ctx {
   // MatMulNBits weights created afterwards keep their prefill images
   // (mg_ctx_set_prefill_images).
   bool prefill_images = true;
+  // The two chunk slots of the MatMulNBits upload (pinned host and device,
+  // up_slot bytes each, grow-only), held until the context is destroyed so
+  // that the weights of a model pin host memory once.
+  void *up_pin = nullptr;
+  void *up_dev = nullptr;
+  size_t up_slot = 0;
+  hipEvent_t up_done[2] = {};
 };
 
 // Records events on the context's stream around one op's work when the

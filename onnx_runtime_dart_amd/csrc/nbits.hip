@@ -1768,6 +1768,27 @@ struct OpenFiles {
 
 }  // namespace
 
+namespace {
+// Grows the context's upload slots to two of at least `slot` bytes (pinned
+// host and device, 8 MiB at least, so that the smaller weights of a model
+// share the first allocation); every later upload of the context reuses them.
+mg_status upload_slots(mg_ctx *ctx, size_t slot) {
+  for (hipEvent_t &e : ctx->up_done)
+    if (!e) MG_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  if (ctx->up_slot >= slot) return MG_OK;
+  slot = std::max(slot, (size_t)8 << 20);
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  if (ctx->up_pin) MG_HIP(hipHostFree(ctx->up_pin));
+  if (ctx->up_dev) MG_HIP(hipFree(ctx->up_dev));
+  ctx->up_pin = ctx->up_dev = nullptr;
+  ctx->up_slot = 0;
+  MG_HIP(hipHostMalloc(&ctx->up_pin, 2 * slot, hipHostMallocDefault));
+  MG_HIP(hipMalloc(&ctx->up_dev, 2 * slot));
+  ctx->up_slot = slot;
+  return MG_OK;
+}
+}  // namespace
+
 mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const mg_byte_source &b,
                           const mg_byte_source &scales, int32_t zp_kind,
                           const mg_byte_source &zp, const float *bias, int64_t chunk_bytes) {
@@ -1813,8 +1834,9 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const mg_byte_source &b,
     MG_HIP(hipMemcpy(d.bias, bias, (size_t)N * 4, hipMemcpyHostToDevice));
   }
 
-  // Chunks of whole column groups; two staging slots (pinned host + device)
-  // so that reading chunk i + 1 overlaps the copy and repack of chunk i.
+  // Chunks of whole column groups; two staging slots (pinned host + device,
+  // the context's) so that reading chunk i + 1 overlaps the copy and repack
+  // of chunk i.
   if (chunk_bytes <= 0) chunk_bytes = 32ll << 20;
   const int64_t cgs_per = std::min<int64_t>(ng, std::max<int64_t>(1, chunk_bytes / (64 * col_all)));
   const int64_t rows_per = cgs_per * 64;
@@ -1822,24 +1844,14 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const mg_byte_source &b,
   const size_t off_z = off_s + mg_align((size_t)(rows_per * col_s));
   const size_t slot = off_z + mg_align((size_t)(rows_per * col_z));
   hipStream_t st = ctx->stream;
-  uint8_t *pinned[2] = {nullptr, nullptr};
-  uint8_t *stage[2] = {nullptr, nullptr};
-  hipEvent_t done[2] = {nullptr, nullptr};
-  mg_status status = MG_OK;
-  auto cleanup = [&]() {
-    if (st) (void)hipStreamSynchronize(st);
-    for (int i = 0; i < 2; i++) {
-      if (pinned[i]) (void)hipHostFree(pinned[i]);
-      if (stage[i]) (void)hipFree(stage[i]);
-      if (done[i]) (void)hipEventDestroy(done[i]);
-    }
-  };
+  uint8_t *pinned[2], *stage[2];
   auto run = [&]() -> mg_status {
+    MG_TRY(upload_slots(ctx, slot));
     for (int i = 0; i < 2; i++) {
-      MG_HIP(hipHostMalloc((void **)&pinned[i], slot, hipHostMallocDefault));
-      MG_HIP(hipMalloc((void **)&stage[i], slot));
-      MG_HIP(hipEventCreateWithFlags(&done[i], hipEventDisableTiming));
+      pinned[i] = static_cast<uint8_t *>(ctx->up_pin) + i * slot;
+      stage[i] = static_cast<uint8_t *>(ctx->up_dev) + i * slot;
     }
+    hipEvent_t *done = ctx->up_done;
     for (int64_t ci = 0, cg0 = 0; cg0 < ng; ci++, cg0 += cgs_per) {
       const int sl = (int)(ci & 1);
       const int64_t cgs = std::min(cgs_per, ng - cg0);
@@ -1864,8 +1876,8 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const mg_byte_source &b,
     MG_HIP(hipStreamSynchronize(st));
     return MG_OK;
   };
-  status = run();
-  cleanup();
+  mg_status status = run();
+  (void)hipStreamSynchronize(st);  // the slots are free for the next upload
   if (status == MG_OK && ctx->prefill_images && mg_nbits_f8_eligible(d))
     status = mg_nbits_f8_images(ctx, w);
   return status;

@@ -264,7 +264,7 @@ __global__ __launch_bounds__(256) void k_af6x3(const float *__restrict__ a, int6
     }
     const uint32_t x1 = __shfl_xor(lo, 1), y1 = __shfl_xor(hi, 1);
     const uint32_t x2 = __shfl_xor(lo, 2), y2 = __shfl_xor(hi, 2);
-    const uint32_t x3 = __shfl_xor(lo, 3), y3 = __shfl_xor(hi, 3);
+    const uint32_t y3 = __shfl_xor(hi, 3);
     if (e == 0)
       *reinterpret_cast<uint4 *>(base + d * 1536 + 16 * lane) =
           make_uint4(lo, hi | (x1 << 16), (x1 >> 16) | (y1 << 16), x2);
