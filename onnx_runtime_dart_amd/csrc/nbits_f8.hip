@@ -713,6 +713,24 @@ __global__ __launch_bounds__(64 * MW, MW == 8 ? 1 : (NT == 4 ? 2 : 3)) void k_ge
 }
 
 
+// Global -> LDS copies (gfx950 global_load_lds_dwordx4 / _dword): lane i's
+// 16 (4) bytes land at LDS byte address lds + 16 i (4 i), lds wave-uniform.
+// Issued as asm so that the compiler's waits do not treat them as writes to
+// every LDS location; the caller waits for them (vmcnt, which returns in
+// issue order) before the barrier that publishes the data.
+__device__ inline void lds_load16(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(g)
+               : "memory", "m0");
+}
+__device__ inline void lds_load4(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds), "v"(g)
+               : "memory", "m0");
+}
+
 // One digit's fp6 MFMA: A and B e2m3 (format 2), the B scale 2 (E8M0 128)
 // turning the stored (q - zp) / 2 back into q - zp.
 template <int DG>
@@ -747,8 +765,15 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
   constexpr int LDS_U4 = 2 * BU4 > STAGE_U4 ? 2 * BU4 : STAGE_U4;
   constexpr int PB = NT * 4;           // bytes per image piece (3 per thread)
   typedef typename std::conditional<NT == 4, uint4, uint2>::type piece_t;
+  // LD: the images and block scales go global -> LDS directly (no registers,
+  // no LDS stores to schedule), and the activations run in a two-step ring:
+  // every load issued in k group kg is for kg + 1, so the in-order return of
+  // vector loads never makes a step wait for the images behind its own A.
+  constexpr bool LD = NT == 4 && !FZP;
+  constexpr int AR = LD ? 2 : 1;
   __shared__ uint4 lds[LDS_U4];
-  __shared__ float scl[2][32][NT];  // [buf][col % 32][n32]
+  __shared__ float scl[2][32 * NT];  // [buf][n32][col % 32] (LD), else [buf][col % 32][n32]
+  auto si = [](int n, int c) { return LD ? n * 32 + c : c * NT + n; };
   __shared__ float czl[FZP ? 2 : 1][32][NT];  // s * z per column (FZP)
   __shared__ __align__(16) float rl[FZP ? 2 : 1][128];  // row sums of the tile's rows (FZP)
   const int t = threadIdx.x, lane = t & 63;
@@ -831,7 +856,7 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
     if (j < 3) reinterpret_cast<piece_t *>(&lds[buf * BU4])[t + 256 * j] = m.im[j];
     if (j == 0 && t < TC) {
       const int blk = (kg * KGRP) >> lbs;
-      scl[buf][tc & 31][tc >> 5] = blk < nb ? m.sc : 0.f;
+      scl[buf][si(tc >> 5, tc & 31)] = blk < nb ? m.sc : 0.f;
       if constexpr (FZP) czl[buf][tc & 31][tc >> 5] = blk < nb ? m.zf : 0.f;
     }
     if constexpr (FZP) {
@@ -866,12 +891,39 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
   for (int n = 0; n < NT; n++) s_pend[n] = 0.f;
   const float16v zero16 = (float16v){};
 
-  int8v A[3];
-  uint32_t sa;
+  // LD: the image pieces p = t + 256 j of k group kg and the block scales of
+  // tile column tc = t (threads t < TC, whole waves) straight into buffer buf.
+  auto issue_lds = [&](int kg, int buf) {
+    const uint8_t *ib = img + ((int64_t)NT * nt * c4n + kg) * 3072;
+    const uint32_t lb = (uint32_t)reinterpret_cast<uintptr_t>(&lds[buf * BU4]);
 #pragma unroll
-  for (int d = 0; d < 3; d++) A[d] = a_load(kg0, 0, d);
-  sa = s_load(kg0, 0);
-  {
+    for (int j = 0; j < 3; j++) lds_load16(ib + vo_im[j], lb + (64 * wave + 256 * j) * 16);
+    if (t < TC) {
+      const int blk = min((kg * KGRP) >> lbs, nbm1);  // < nb here: bs >= 128 and kpad = nb bs
+      lds_load4(scales + ((int64_t)(PH * nt + tcg) * nb + blk) * 64 + sz_pos(tc & 63),
+                (uint32_t)reinterpret_cast<uintptr_t>(&scl[buf][0]) + 256 * wave);
+    }
+  };
+
+  // Activation ring: AR steps of the three digits and their scale word.
+  int8v A[AR][3];
+  uint32_t sa[AR];
+  if constexpr (LD) issue_lds(kg0, 0);
+#pragma unroll
+  for (int j = 0; j < AR; j++) {
+#pragma unroll
+    for (int d = 0; d < 3; d++) A[j][d] = a_load(kg0, j, d);
+    sa[j] = s_load(kg0, j);
+  }
+  if constexpr (LD) {
+    // All of it landed (the compiler also sees the ring consumed here, so
+    // its own wait counts in the loop start from an empty queue).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < AR; j++)
+      asm volatile("" ::"v"(A[j][0][0]), "v"(A[j][0][4]), "v"(A[j][1][0]), "v"(A[j][1][4]),
+                   "v"(A[j][2][0]), "v"(A[j][2][4]), "v"(sa[j]));
+  } else {
     Meta m0;
     load_meta(kg0, m0);
 #pragma unroll
@@ -883,7 +935,21 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
     const int buf = (kg - kg0) & 1;
     const int kgn = min(kg + 1, kg1 - 1);  // next k group (clamped)
     Meta mnext;
-    load_meta(kgn, mnext);
+    // LD: four small loads of this k group's activation slices (in L2),
+    // then the copies for the next one.  The compiler counts only its own
+    // loads in its waits, so a wait for a load older than the copies
+    // would also wait for up to four copies behind it; with these four
+    // between, such waits end before the copies.  Consuming the last of
+    // them at the end of the k group waits for the copies themselves.
+    uint32_t pad[4];
+    if constexpr (LD) {
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        pad[j] = __builtin_amdgcn_raw_buffer_load_b32(r_a, vo4, (kg * 6 + j) * 1536, 0);
+      if (kg + 1 < kg1) issue_lds(kg + 1, buf ^ 1);
+    } else {
+      load_meta(kgn, mnext);
+    }
     // FZP: this k group's -z R (the lane's 16 rows are 8 i + 4 (lane / 32) +
     // 0..3 of the wave's 32, i = v / 4).
     float rr[FZP ? 16 : 1];
@@ -901,7 +967,10 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
       int8v B[NT];
 #pragma unroll
       for (int n = 0; n < NT; n++) B[n] = b_load(buf, n, st);
-      const int nkg = st == 0 ? kg : kgn, nst = st ^ 1;
+      // Ring slot of this step and the step its registers are reloaded with
+      // (AR = 2: the same step of the next k group).
+      const int sl = AR == 2 ? st : 0;
+      const int nkg = AR == 2 || st == 1 ? kgn : kg, nst = AR == 2 ? st : st ^ 1;
 #pragma unroll
       for (int d = 0; d < 3; d++) {
 #pragma unroll
@@ -918,19 +987,22 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
               for (int v = 0; v < 16; v++) cin[v] = -z * rr[v];
             }
           }
-          D[n] = d == 0   ? mfma6_digit<0>(A[0], B[n], cin, (int)sa)
-                 : d == 1 ? mfma6_digit<1>(A[1], B[n], cin, (int)sa)
-                          : mfma6_digit<2>(A[2], B[n], cin, (int)sa);
+          D[n] = d == 0   ? mfma6_digit<0>(A[sl][0], B[n], cin, (int)sa[sl])
+                 : d == 1 ? mfma6_digit<1>(A[sl][1], B[n], cin, (int)sa[sl])
+                          : mfma6_digit<2>(A[sl][2], B[n], cin, (int)sa[sl]);
         }
-        A[d] = a_load(nkg, nst, d);
-        if (d == 2) sa = s_load(nkg, nst);
+        A[sl][d] = a_load(nkg, nst, d);
+        if (d == 2) sa[sl] = s_load(nkg, nst);
         __builtin_amdgcn_sched_barrier(0);
       }
-      store_piece(kgn, mnext, buf ^ 1, 2 * st);
-      store_piece(kgn, mnext, buf ^ 1, 2 * st + 1);
+      if constexpr (!LD) {
+        store_piece(kgn, mnext, buf ^ 1, 2 * st);
+        store_piece(kgn, mnext, buf ^ 1, 2 * st + 1);
+      }
     }
+    if constexpr (LD) asm volatile("" ::"v"(pad[0]), "v"(pad[1]), "v"(pad[2]), "v"(pad[3]));
 #pragma unroll
-    for (int n = 0; n < NT; n++) s_pend[n] = scl[buf][lc][n];
+    for (int n = 0; n < NT; n++) s_pend[n] = scl[buf][si(n, lc)];
     __syncthreads();
   }
 #pragma unroll
