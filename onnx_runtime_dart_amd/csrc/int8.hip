@@ -160,8 +160,11 @@ __device__ inline void lds_copy16(const void *g, uint32_t lds) {
 // A (u8 or i8, [M, K] per batch, row pitch lda) -> fragments
 // afrag[batch][m32][q][lane] (the order the GEMM loads them: 1 KB per wave
 // load), re-centred to signed, zero outside [M, K]; plus rowsum(A') and
-// ca = oa - aZp per row.  One workgroup per (32-row tile, batch).
-__global__ __launch_bounds__(256) void k_i8_prep_a(
+// ca = oa - aZp per row.  One workgroup per (32-row tile, batch); its 16
+// waves take every 16th k step, so that few row tiles still keep many
+// loads in flight.
+constexpr int PREP_A_WAVES = 16;
+__global__ __launch_bounds__(64 * PREP_A_WAVES) void k_i8_prep_a(
     const uint8_t *__restrict__ a, int64_t lda, int64_t a_bs, int a_signed, int vec,
     int64_t M, int64_t K, int kqp, int m32n, int za_scalar, const int32_t *__restrict__ za,
     int za_len, int4v *__restrict__ afrag, int32_t *__restrict__ rowsum,
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(256) void k_i8_prep_a(
   const uint32_t flip = a_signed ? 0u : 0x80808080u;
   int4v *out = afrag + ((bz * m32n + m32) * (int64_t)kqp) * 64 + lane;
   int s = 0;
-  for (int q = wave; q < kqp; q += 4) {
+  for (int q = wave; q < kqp; q += PREP_A_WAVES) {
     const int64_t k0 = (int64_t)(q >> 2) * 128 + 64 * h + 16 * (q & 3);
     int4v v;
     if (row < M && vec && k0 + 16 <= K) {
@@ -194,13 +197,13 @@ __global__ __launch_bounds__(256) void k_i8_prep_a(
     s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
     out[(int64_t)q * 64] = v;
   }
-  __shared__ int red[4][64];
+  __shared__ int red[PREP_A_WAVES][64];
   red[wave][lane] = s;
   __syncthreads();
   if (t < 32) {
     int tot = 0;
 #pragma unroll
-    for (int w = 0; w < 4; w++) tot += red[w][t] + red[w][t + 32];
+    for (int w = 0; w < PREP_A_WAVES; w++) tot += red[w][t] + red[w][t + 32];
     const int64_t rr = (int64_t)m32 * 32 + t;
     const int64_t slot = bz * m32n * 32 + rr;
     rowsum[slot] = tot;
@@ -599,7 +602,8 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
   }
   const int kqp = p.nstage * QS;
   const int vec = (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 && K % 16 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(k_i8_prep_a, dim3((unsigned)p.m32n, (unsigned)a_batch), dim3(256), 0, st,
+  hipLaunchKernelGGL(k_i8_prep_a, dim3((unsigned)p.m32n, (unsigned)a_batch),
+                     dim3(64 * PREP_A_WAVES), 0, st,
                      static_cast<const uint8_t *>(a_dev), K, M * K, a_signed, vec, M, K, kqp,
                      p.m32n, za_scalar, za, za_len, afrag, rowsum, ca);
   MG_TRY(mg_launch_check("k_i8_prep_a"));
