@@ -401,7 +401,15 @@ __device__ inline void prefill_epilogue(
     int flag = 0;
     if (lane < 32 && m32 * 32 + lane < M) {
       const uint32_t *nfw = reinterpret_cast<const uint32_t *>(nf) + (int64_t)(m32 * 32 + lane) * c4n;
-      for (int kg = kg0; kg < kg1; kg++) flag |= nfw[kg] != 0u;
+      // Eight flag words in flight at a time (one at a time, each load's
+      // latency would add up over the k groups).
+      for (int kb = kg0; kb < kg1; kb += 8) {
+        uint32_t w[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) w[j] = nfw[min(kb + j, kg1 - 1)];  // branch-free
+#pragma unroll
+        for (int j = 0; j < 8; j++) flag |= w[j] != 0u;
+      }
     }
     uint64_t rows = __ballot(flag);
     const int klo = kg0 * KGRP;
