@@ -302,6 +302,11 @@ def main():
     print(f"# prefill pass {ms_step:.4f} ms, {value:.1f} TFLOP/s (separate launches "
           f"{ms_step_sep:.4f} ms)", file=sys.stderr, flush=True)
 
+    # Resident weight bytes of the pass, with and without the prefill images.
+    resident_img = int(sum(w.info()[2] for w in weights))
+    images_bytes = int(sum(-(-n // 128) * 2 * 48 * (-(-k // 128) * 128) for _, k, n in QWEN3_PROJ))
+    packed_bytes = int(sum(b.nbytes + s.nbytes + z.nbytes for b, s, z in host_w))
+
     # ---- dominant MFMA kernel: lm_head at M = 512
     traffic = load_traffic()
     _, k_lm, n_lm = QWEN3_PROJ[-1]
@@ -310,6 +315,10 @@ def main():
     ms_lm = T.loop(lambda: w_lm.run_dev(acts[(M_PREFILL, k_lm)].data_ptr(), M_PREFILL,
                                         outs[(M_PREFILL, n_lm)].data_ptr()), reps, 2)
     lm_tflops = 2.0 * M_PREFILL * n_lm * k_lm / (ms_lm / 1e3) / 1e12
+    lm_alg_bytes = nbits_bytes(M_PREFILL, k_lm, n_lm)
+    lm_ai = 2.0 * M_PREFILL * n_lm * k_lm / lm_alg_bytes
+    lm_roof_tflops = min(FP6_MFMA_PEAK_TFLOPS, lm_ai * HBM_PEAK_GBS / 1e3)
+    lm_gbs = lm_alg_bytes / (ms_lm / 1e3) / 1e9
     tr = traffic.get("lm512", {})
     # The same lm_head on a weight created without prefill images.
     ctx.set_prefill_images(False)
@@ -332,8 +341,13 @@ def main():
         "dtype": "int4 weights x fp32 activations (weights' (q - zp) / 2 as fp6 e2m3 prefill "
                  "images, activations as three e2m3 digits with per-32-k E8M0 scales, "
                  "block-scaled fp6 MFMA, fp32 accumulate)",
-        "weight_format": "packed int4 (decode) + prefill images, 0.75 byte per weight, built "
-                         "on the device at weight upload (outside the timed region)",
+        "weight_format": {
+            "form": "packed int4 (decode) + prefill images, 0.75 byte per weight, built on "
+                    "the device at weight upload (outside the timed region)",
+            "resident_bytes": resident_img,
+            "resident_bytes_without_images": resident_img - images_bytes,
+            "packed_onnx_bytes": packed_bytes,
+            "image_bytes": images_bytes},
         "data": "synthetic (seeded uniform nibbles, scales U(0.002,0.02), A ~ N(0,1))",
         "config": {"workload": "Qwen3-0.6B int4 MatMulNBits projections q,k,v,o,gate,up,"
                                "down,lm_head; block_size 128 with uint4 zero points",
@@ -345,11 +359,22 @@ def main():
                               "TFLOP/s": round(flops_step / (ms_step_sep / 1e3) / 1e12, 2)},
         "roofline": {"kernel": tr.get("kernel", "k_gemm_f6x3") +
                      " (lm_head 512x1024x151936; op time incl. activation prepass)",
-                     "bound": "mfma", "achieved": round(lm_tflops, 2),
-                     "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(lm_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
+                     # The kernel issues fp6 MFMAs (10.1 PFLOP/s dense); at its
+                     # arithmetic intensity (159.3 GFLOP over 396.5 MB, 402
+                     # FLOP/B) that is above min(peak, AI x 8 TB/s) = 3.21
+                     # PFLOP/s, so the bound is HBM: achieved = algorithmic
+                     # bytes / op time against 8 TB/s.
+                     "bound": "hbm" if lm_ai * HBM_PEAK_GBS / 1e3 < FP6_MFMA_PEAK_TFLOPS
+                              else "mfma",
+                     "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(lm_tflops / lm_roof_tflops, 4),
+                     "arithmetic_intensity_flop_per_byte": round(lm_ai, 1),
+                     "achieved_tflops": round(lm_tflops, 2),
+                     "roofline_tflops": round(lm_roof_tflops, 1),
+                     "frac_of_fp16_peak": round(lm_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
                      "issued": "3 fp6 MFMA products per algorithmic product",
-                     "issued_frac_of_fp6_peak": round(3 * lm_tflops / FP6_MFMA_PEAK_TFLOPS, 4),
+                     "mfma_issue_utilisation_fp6": round(3 * lm_tflops / FP6_MFMA_PEAK_TFLOPS,
+                                                         4),
                      "without_images": {
                          "kernel": "k_gemm_f8x3 (three e4m3 digits, weight tiles dequantised "
                                    "in the GEMM)",
@@ -357,7 +382,7 @@ def main():
                          "TFLOP/s": round(2.0 * M_PREFILL * n_lm * k_lm / (ms_lm8 / 1e3) / 1e12,
                                           2)},
                      "traffic": tr.get("bytes"),
-                     "algorithmic_bytes": nbits_bytes(M_PREFILL, k_lm, n_lm),
+                     "algorithmic_bytes": lm_alg_bytes,
                      "ms": round(ms_lm, 4)},
     }
 
@@ -442,9 +467,14 @@ def main():
                          "launches": "q/k/v and gate/up as sibling groups, as the headline",
                          "ms_per_pass_separate_launches":
                              None if ms_m1_sep is None else round(ms_m1_sep, 4),
-                         "kernel_us": {name: round(t * 1e3, 2)
-                                       for (name, _, _), t in zip(QWEN3_PROJ, per_launch)},
-                         "kernel_sum_ms": round(sum(per_launch), 4),
+                         # Each projection launched alone between its own
+                         # pair of events on host-issued passes: these include
+                         # the event overhead (~2-4 us each), so they are not
+                         # kernel times and their sum exceeds the pass.
+                         "launch_event_pair_us": {name: round(t * 1e3, 2)
+                                                  for (name, _, _), t in zip(QWEN3_PROJ,
+                                                                             per_launch)},
+                         "launch_event_pair_sum_ms": round(sum(per_launch), 4),
                          "bytes_per_pass": bytes_m1,
                          "weight_sets_rotated": GEMV_ROTATE,
                          "frac_hbm_peak": round(bytes_m1 / (ms_m1 / 1e3) / 1e9 / HBM_PEAK_GBS,
@@ -456,7 +486,7 @@ def main():
         "frac": round(lm1_gbs / HBM_PEAK_GBS, 4), "traffic": tr1.get("bytes"),
         "algorithmic_bytes": lm1_bytes, "ms": round(ms_lm1, 4),
         "ms_in_pass_events": round(ms_lm1_pass, 4)}
-    print(f"# gemv M=1 pass {ms_m1:.4f} ms (host-issued {ms_m1_eager:.4f} ms, kernel sum "
+    print(f"# gemv M=1 pass {ms_m1:.4f} ms (host-issued {ms_m1_eager:.4f} ms, event-pair sum "
           f"{sum(per_launch):.4f} ms); lm_head {ms_lm1 * 1e3:.2f} us {lm1_gbs:.0f} GB/s",
           file=sys.stderr, flush=True)
     graph = None
