@@ -233,7 +233,20 @@ mg_status mg_matmul_integer(mg_ctx *ctx, const void *a, int32_t a_signed,
                             const int64_t *b_shape, int32_t b_rank,
                             const int32_t *a_zp, int64_t a_zp_len,
                             const int32_t *b_zp, int64_t b_zp_len, int32_t *y);
-/* Same with an uploaded B; a is [rows = batch*M, K]. */
+/* opMatMulInteger with the reference's own output type: y_int64[batch, M,
+ * N], Tensor.int64 accumulated in 64-bit ints (lib/src/onnx_qlinear_ops.dart:
+ * 55-80), for any K.  mg_matmul_integer's int32 output is exact only for
+ * K <= 33025 (a k term is at most 255 * 255) and refuses longer rows with
+ * MG_UNSUPPORTED; this form cuts K into segments of 32768 whose int32 sums
+ * are exact and adds them in int64 on the device. */
+mg_status mg_matmul_integer_i64(mg_ctx *ctx, const void *a, int32_t a_signed,
+                                const int64_t *a_shape, int32_t a_rank,
+                                const void *b, int32_t b_signed,
+                                const int64_t *b_shape, int32_t b_rank,
+                                const int32_t *a_zp, int64_t a_zp_len,
+                                const int32_t *b_zp, int64_t b_zp_len, int64_t *y);
+/* Same with an uploaded B; a is [rows = batch*M, K].  The uploaded-weight
+ * forms (here and below) need K <= 33025 (MG_UNSUPPORTED otherwise). */
 mg_status mg_matmul_integer_w(mg_ctx *ctx, const void *a, int32_t a_signed,
                               int64_t rows, int64_t K, const int32_t *a_zp,
                               int64_t a_zp_len, const mg_weight *w, int32_t *y);
@@ -246,7 +259,9 @@ mg_status mg_matmul_integer_w_dev(mg_ctx *ctx, const void *a_dev,
  * q = roundHalfEven(fl32(acc * fl32(fl32(aS*bS)/yS))) + yZp clamped to
  * [lo, hi].  lo/hi are -128/127 when the y zero point is int8, else 0/255
  * (lib/src/onnx_graph.dart:2903,2914-2915); y holds uint8 when lo >= 0 and
- * int8 otherwise.  Scales are per-tensor (:88-90). */
+ * int8 otherwise.  Scales are per-tensor (:88-90).  Any K: rows longer than
+ * 33025 are summed in int64 (as the reference's int accumulator) before the
+ * requantisation. */
 mg_status mg_qlinear_matmul(mg_ctx *ctx, const void *a, int32_t a_signed,
                             const int64_t *a_shape, int32_t a_rank,
                             float a_scale, const int32_t *a_zp,
@@ -312,6 +327,15 @@ mg_status mg_matmul_f32_dev(mg_ctx *ctx, const float *a_dev,
                             const int64_t *a_shape, int32_t a_rank,
                             const float *b_dev, const int64_t *b_shape,
                             int32_t b_rank, float *y_dev);
+/* opMatMul on operands that are not both float tensors (integer tensors,
+ * or one float and one integer): the reference's fallback
+ * (lib/src/onnx_ops.dart:1753-1762) sums a.getD * b.getD over k in order
+ * in double and stores f32.  The operands are passed as doubles (each
+ * element's getD value); products and sums are rounded separately, so y is
+ * bitwise the reference's.  Shapes and broadcasting as mg_matmul_f32. */
+mg_status mg_matmul_f64acc(mg_ctx *ctx, const double *a, const int64_t *a_shape,
+                           int32_t a_rank, const double *b,
+                           const int64_t *b_shape, int32_t b_rank, float *y);
 /* Output shape of MatMul over these operand shapes (the broadcast of
  * lib/src/onnx_ops.dart:1717-1722 plus [M, N]); y_shape holds up to 16
  * entries.  Lets the caller allocate y before mg_matmul_f32(_dev).  No
@@ -557,19 +581,22 @@ typedef enum mg_binary_op {
 mg_status mg_binary_f32_dev(mg_ctx *ctx, int32_t op, const float *a_dev,
                             const int64_t *a_shape, int32_t a_rank, const float *b_dev,
                             const int64_t *b_shape, int32_t b_rank, float *y_dev);
-/* opSigmoid (lib/src/onnx_ops.dart:2349-2350): 1 / (1 + exp(-x)) in double. */
+/* opSigmoid (lib/src/onnx_ops.dart:2349-2350): 1 / (1 + exp(-x)) in double.
+ * y may be x. */
 mg_status mg_sigmoid_f32_dev(mg_ctx *ctx, const float *x_dev, int64_t n, float *y_dev);
 /* opRMSNorm (lib/src/onnx_ops.dart:1771-1815), the op behind _FusedRMSNorm and
  * SimplifiedLayerNormalization (lib/src/onnx_graph.dart:1640-1649,
  * :1783-1792): x * rsqrt(mean(x^2, axis) + epsilon) * gamma, gamma along the
  * last axis.  gamma_len != last dim: MG_INVALID_ARGUMENT ("RMSNorm gamma
- * length .. != last dim .."). */
+ * length .. != last dim ..").  y may be x. */
 mg_status mg_rms_norm_f32_dev(mg_ctx *ctx, const float *x_dev, const int64_t *shape,
                               int32_t rank, const float *gamma_dev, int64_t gamma_len,
                               int64_t axis, double epsilon, float *y_dev);
 /* SkipSimplifiedLayerNormalization (lib/src/onnx_graph.dart:1793-1813):
  * sum = x + skip (equal shapes), y = RMSNorm(sum, gamma, last axis) (+ bias
- * when bias_dev is not null); sum_dev (may be null) receives sum. */
+ * when bias_dev is not null); sum_dev (may be null) receives sum.  Any of
+ * x_dev, skip_dev, y_dev and sum_dev may be the same buffer (an in-place
+ * residual stream: sum written over x or skip, y over either). */
 mg_status mg_skip_rms_norm_f32_dev(mg_ctx *ctx, const float *x_dev, const float *skip_dev,
                                    const int64_t *shape, int32_t rank, const float *gamma_dev,
                                    int64_t gamma_len, const float *bias_dev, double epsilon,

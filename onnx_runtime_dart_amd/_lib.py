@@ -49,6 +49,8 @@ SIGNATURES = {
     "mg_matmul_nbits_group_dev": [_P, _I32, _P, _P, _I64, _P],
     "mg_weight_int8_create": [_P, _P, _I32, _I64, _I64, _P, _I64, _PP],
     "mg_matmul_integer": [_P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I64, _P, _I64, _P],
+    "mg_matmul_integer_i64": [_P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I64, _P, _I64,
+                              _P],
     "mg_matmul_integer_w": [_P, _P, _I32, _I64, _I64, _P, _I64, _P, _P],
     "mg_matmul_integer_w_dev": [_P, _P, _I32, _I64, _I64, _P, _I64, _P, _P],
     "mg_qlinear_matmul": [_P, _P, _I32, _P, _I32, _F, _P, _I64, _P, _I32, _P, _I32, _F, _P,
@@ -96,6 +98,7 @@ SIGNATURES = {
                                      _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _I32, _I32, _F,
                                      _F, _I32, _P, _P, _P],
     "mg_matmul_f32": [_P, _P, _P, _I32, _P, _P, _I32, _P],
+    "mg_matmul_f64acc": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_matmul_f32_dev": [_P, _P, _P, _I32, _P, _P, _I32, _P],
     "mg_matmul_f32_output_shape": [_P, _I32, _P, _I32, _P, _P],
     "mg_matmul_f32_batch_offsets": [_P, _I32, _P, _I32, _I64, _I64, _P, _P, _P],

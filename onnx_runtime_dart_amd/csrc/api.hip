@@ -22,6 +22,13 @@ mg_status mg_int8_run_batched(mg_ctx *ctx, const void *a_dev, int32_t a_signed,
                               int64_t a_zp_len, const int32_t *b_zp,
                               int64_t b_zp_len, const mg_requant *rq,
                               void *y_dev, void *ws);
+size_t mg_int8_long_k_ws_bytes(int64_t a_batch, int64_t b_batch, int64_t M, int64_t K, int64_t N,
+                               bool requant);
+mg_status mg_int8_run_long_k(mg_ctx *ctx, const void *a_dev, int32_t a_signed, int64_t a_batch,
+                             const void *b_dev, int32_t b_signed, int64_t b_batch, int64_t M,
+                             int64_t K, int64_t N, const int32_t *a_zp, int64_t a_zp_len,
+                             const int32_t *b_zp, int64_t b_zp_len, const mg_requant *rq,
+                             void *y_dev, void *ws);
 size_t mg_int8_batched_ws_bytes(int64_t a_batch, int64_t b_batch, int64_t M,
                                 int64_t K, int64_t N);
 
@@ -672,6 +679,10 @@ struct IntProblem {
   int64_t M = 0, K = 0, N = 0, a_batch = 1, b_batch = 1, batch = 1;
 };
 
+// Longest K whose int32 sum is exact for every operand: 33025 * 255 * 255 <
+// 2^31.  Longer rows take the int64 segment path (mg_int8_run_long_k).
+constexpr int64_t MG_I8_MAX_K32 = 33025;
+
 mg_status check_integer(const int64_t *a_shape, int32_t a_rank, const int64_t *b_shape,
                         int32_t b_rank, int64_t a_zp_len, bool has_azp, int64_t b_zp_len,
                         bool has_bzp, IntProblem *p) {
@@ -694,20 +705,27 @@ mg_status check_integer(const int64_t *a_shape, int32_t a_rank, const int64_t *b
   // :46-54
   if ((p->a_batch != p->batch && p->a_batch != 1) || (p->b_batch != p->batch && p->b_batch != 1))
     return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger batch mismatch");
-  if (p->K > 33025)
-    return mg_fail(MG_UNSUPPORTED,
-                   "MatMulInteger: K > 33025 may exceed the int32 accumulator");
   return MG_OK;
 }
 
+// Host-pointer MatMulInteger / QLinearMatMul on a runtime B.  y: int32
+// (out_i64 false), int64 (out_i64 true) or requantised bytes (rq).  Rows
+// longer than MG_I8_MAX_K32 k, and every int64 call, take the segment path
+// with int64 sums; int32 output is refused there (the sums may not fit).
 mg_status integer_host(mg_ctx *ctx, const void *a, int32_t a_signed, const int64_t *a_shape,
                        int32_t a_rank, const int32_t *a_zp, int64_t a_zp_len, const void *b,
                        int32_t b_signed, const int64_t *b_shape, int32_t b_rank,
-                       const int32_t *b_zp, int64_t b_zp_len, const mg_requant *rq, void *y) {
+                       const int32_t *b_zp, int64_t b_zp_len, const mg_requant *rq, void *y,
+                       bool out_i64 = false) {
   IntProblem p;
   MG_TRY(check_integer(a_shape, a_rank, b_shape, b_rank, a_zp_len, a_zp != nullptr, b_zp_len,
                        b_zp != nullptr, &p));
-  const int64_t ysz = p.batch * p.M * p.N * (mg_requant_out(rq) ? 1 : 4);
+  const bool long_k = out_i64 || p.K > MG_I8_MAX_K32;
+  if (long_k && !out_i64 && !mg_requant_out(rq))
+    return mg_fail(MG_UNSUPPORTED,
+                   "MatMulInteger: K > 33025 may exceed the int32 output; use the int64 form "
+                   "(mg_matmul_integer_i64)");
+  const int64_t ysz = p.batch * p.M * p.N * (mg_requant_out(rq) ? 1 : (out_i64 ? 8 : 4));
   if (p.batch * p.M * p.N == 0) return MG_OK;
   if ((!a && p.a_batch * p.M * p.K) || (!b && p.b_batch * p.K * p.N) || !y)
     return mg_fail(MG_INVALID_ARGUMENT, "MatMulInteger: null buffer");
@@ -715,15 +733,22 @@ mg_status integer_host(mg_ctx *ctx, const void *a, int32_t a_signed, const int64
   Staging s;
   const size_t abytes = (size_t)(p.a_batch * p.M * p.K), bbytes = (size_t)(p.b_batch * p.K * p.N);
   const size_t oa = s.take(abytes), ob = s.take(bbytes), oy = s.take((size_t)ysz);
-  const size_t ow = s.take(mg_int8_batched_ws_bytes(p.a_batch, p.b_batch, p.M, p.K, p.N));
+  const size_t ow = s.take(
+      long_k ? mg_int8_long_k_ws_bytes(p.a_batch, p.b_batch, p.M, p.K, p.N, mg_requant_out(rq))
+             : mg_int8_batched_ws_bytes(p.a_batch, p.b_batch, p.M, p.K, p.N));
   MG_TRY(mg_check_control(ctx, (int64_t)s.off));
   MG_TRY(mg_ws_reserve(ctx, s.off));
   char *base = static_cast<char *>(ctx->ws);
   if (abytes) MG_HIP(hipMemcpyAsync(base + oa, a, abytes, hipMemcpyHostToDevice, ctx->stream));
   if (bbytes) MG_HIP(hipMemcpyAsync(base + ob, b, bbytes, hipMemcpyHostToDevice, ctx->stream));
-  MG_TRY(mg_int8_run_batched(ctx, base + oa, a_signed, p.a_batch, base + ob, b_signed, p.b_batch,
-                             p.M, p.K, p.N, a_zp, a_zp ? a_zp_len : 0, b_zp,
-                             b_zp ? b_zp_len : 0, rq, base + oy, base + ow));
+  if (long_k)
+    MG_TRY(mg_int8_run_long_k(ctx, base + oa, a_signed, p.a_batch, base + ob, b_signed,
+                              p.b_batch, p.M, p.K, p.N, a_zp, a_zp ? a_zp_len : 0, b_zp,
+                              b_zp ? b_zp_len : 0, rq, base + oy, base + ow));
+  else
+    MG_TRY(mg_int8_run_batched(ctx, base + oa, a_signed, p.a_batch, base + ob, b_signed,
+                               p.b_batch, p.M, p.K, p.N, a_zp, a_zp ? a_zp_len : 0, b_zp,
+                               b_zp ? b_zp_len : 0, rq, base + oy, base + ow));
   MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)ysz, hipMemcpyDeviceToHost, ctx->stream));
   MG_HIP(hipStreamSynchronize(ctx->stream));
   return MG_OK;
@@ -751,8 +776,10 @@ mg_status check_weight_rows(const mg_weight *w, int64_t rows, int64_t K, const i
     return mg_fail(MG_UNSUPPORTED,
                    "MatMulInteger: zero points must be scalar, per-row [M] for A or "
                    "per-column [N] for B");
-  if (K > 33025)
-    return mg_fail(MG_UNSUPPORTED, "MatMulInteger: K > 33025 may exceed the int32 accumulator");
+  if (K > MG_I8_MAX_K32)
+    return mg_fail(MG_UNSUPPORTED,
+                   "MatMulInteger: K > 33025 may exceed the int32 accumulator of an uploaded "
+                   "weight; use the runtime-B forms (mg_matmul_integer_i64, mg_qlinear_matmul)");
   return MG_OK;
 }
 
@@ -798,6 +825,18 @@ mg_status mg_matmul_integer(mg_ctx *ctx, const void *a, int32_t a_signed, const 
   if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer: null context");
   return integer_host(ctx, a, a_signed, a_shape, a_rank, a_zp, a_zp_len, b, b_signed, b_shape,
                       b_rank, b_zp, b_zp_len, nullptr, y);
+}
+
+mg_status mg_matmul_integer_i64(mg_ctx *ctx, const void *a, int32_t a_signed,
+                                const int64_t *a_shape, int32_t a_rank, const void *b,
+                                int32_t b_signed, const int64_t *b_shape, int32_t b_rank,
+                                const int32_t *a_zp, int64_t a_zp_len, const int32_t *b_zp,
+                                int64_t b_zp_len, int64_t *y) {
+  ProfScope prof_(ctx, "MatMulInteger");
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_integer_i64: null context");
+  return integer_host(ctx, a, a_signed, a_shape, a_rank, a_zp, a_zp_len, b, b_signed, b_shape,
+                      b_rank, b_zp, b_zp_len, nullptr, y, true);
 }
 
 mg_status mg_matmul_integer_w(mg_ctx *ctx, const void *a, int32_t a_signed, int64_t rows,
@@ -1139,6 +1178,45 @@ mg_status mg_matmul_f32(mg_ctx *ctx, const float *a, const int64_t *a_shape, int
   MG_TRY(run_f32_batched(ctx, p, reinterpret_cast<float *>(base + oa),
                          reinterpret_cast<float *>(base + ob), reinterpret_cast<float *>(base + oy)));
   MG_HIP(hipMemcpyAsync(y, base + oy, (size_t)ny * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MG_HIP(hipStreamSynchronize(ctx->stream));
+  return MG_OK;
+}
+
+mg_status mg_matmul_f64acc(mg_ctx *ctx, const double *a, const int64_t *a_shape, int32_t a_rank,
+                           const double *b, const int64_t *b_shape, int32_t b_rank, float *y) {
+  ProfScope prof_(ctx, "MatMul");
+  g_last_error.clear();
+  if (!ctx) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_f64acc: null context");
+  F32Batch p;
+  MG_TRY(plan_matmul_f32(a_shape, a_rank, b_shape, b_rank, &p));
+  const int64_t ny = p.batch * p.M * p.N;
+  if (ny == 0) return MG_OK;
+  const int64_t na = prod(a_shape, 0, a_rank), nb = prod(b_shape, 0, b_rank);
+  if ((!a && na) || (!b && nb) || !y) return mg_fail(MG_INVALID_ARGUMENT, "MatMul: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  Staging s;
+  const size_t oa = s.take((size_t)na * 8), ob = s.take((size_t)nb * 8), oy = s.take((size_t)ny * 4);
+  MG_TRY(mg_check_control(ctx, (int64_t)s.off));
+  MG_TRY(mg_ws_reserve(ctx, s.off));
+  char *base = static_cast<char *>(ctx->ws);
+  if (na) MG_HIP(hipMemcpyAsync(base + oa, a, (size_t)na * 8, hipMemcpyHostToDevice, ctx->stream));
+  if (nb) MG_HIP(hipMemcpyAsync(base + ob, b, (size_t)nb * 8, hipMemcpyHostToDevice, ctx->stream));
+  mg_f32_problem q{};
+  q.M = p.M;
+  q.N = p.N;
+  q.K = p.K;
+  q.batch = p.inner_batch;
+  q.bc = p.bc;
+  const double *ad = reinterpret_cast<const double *>(base + oa);
+  const double *bd = reinterpret_cast<const double *>(base + ob);
+  float *yd = reinterpret_cast<float *>(base + oy);
+  const int64_t outer = p.batch / std::max<int64_t>(p.inner_batch, 1);
+  for (int64_t o = 0; o < outer; o++) {
+    int64_t ao = 0, bo = 0;
+    outer_offsets(p, o, &ao, &bo);
+    MG_TRY(mg_f64acc_run(ctx, q, ad + ao, bd + bo, yd + o * p.inner_batch * p.M * p.N));
+  }
+  MG_HIP(hipMemcpyAsync(y, yd, (size_t)ny * 4, hipMemcpyDeviceToHost, ctx->stream));
   MG_HIP(hipStreamSynchronize(ctx->stream));
   return MG_OK;
 }

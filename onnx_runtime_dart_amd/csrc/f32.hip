@@ -296,3 +296,56 @@ mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
   }
   return MG_OK;
 }
+
+// ------------------------------------------- MatMul on non-float operands
+//
+// opMatMul's fallback for operands that are not both Float32List
+// (lib/src/onnx_ops.dart:1753-1762): each output is a double sum over k in
+// order of a.getD * b.getD, rounded once to f32.  The operands arrive as
+// doubles (getD's value: an int64 element converted to the nearest double,
+// a float element exactly).  The products and sums are rounded separately
+// (contraction into fused multiply-adds is switched off in the kernel: a
+// product of two doubles is not exact, so a fused form would differ), so
+// every output equals the reference's bit for bit.  One thread per output;
+// batches decoded as the fp32 kernel decodes them.
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_matmul_f64acc(const double *__restrict__ a,
+                                                       const double *__restrict__ b,
+                                                       float *__restrict__ y, int64_t M,
+                                                       int64_t K, int64_t N,
+                                                       const mg_f32_bcast bc, uint32_t z0) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * N) return;
+  const uint32_t z = z0 + blockIdx.y;
+  int64_t ao = 0, bo = 0;
+  mg_f32_batch_offsets(bc, z, &ao, &bo);
+  const int64_t r = i / N, c = i % N;
+  const double *ar = a + ao + r * K;
+  const double *bc_ = b + bo + c;
+  double s = 0;
+  {
+#pragma clang fp contract(off)
+    for (int64_t k = 0; k < K; k++) {
+      const double p = ar[k] * bc_[k * N];
+      s = s + p;
+    }
+  }
+  y[(int64_t)z * M * N + i] = (float)s;
+}
+
+}  // namespace
+
+mg_status mg_f64acc_run(mg_ctx *ctx, const mg_f32_problem &p, const double *a_dev,
+                        const double *b_dev, float *y_dev) {
+  if (p.M * p.N == 0 || p.batch == 0) return MG_OK;
+  const unsigned gx = (unsigned)((p.M * p.N + 255) / 256);
+  for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {  // grid y holds at most 65535
+    const unsigned gy = (unsigned)std::min<int64_t>(65535, p.batch - z0);
+    hipLaunchKernelGGL(k_matmul_f64acc, dim3(gx, gy), dim3(256), 0, ctx->stream, a_dev, b_dev,
+                       y_dev, p.M, p.K, p.N, p.bc, (uint32_t)z0);
+    MG_TRY(mg_launch_check("k_matmul_f64acc"));
+  }
+  return MG_OK;
+}

@@ -244,7 +244,10 @@ __device__ inline void i8_finish(void *y, int64_t o, int32_t acc, int32_t rs, in
   const int32_t vi = (int32_t)v;
   if (REQ) {
     const float p = (float)((double)vi * (double)i8_mult(e));
-    int qv = (int)rintf(p) + e.y_zp;
+    // Rounded values beyond +-65536 saturate alike after + y_zp and the
+    // clamp (the reference's int is 64-bit; an int32 conversion of a larger
+    // value would saturate and the + y_zp could wrap).
+    int qv = (int)__builtin_amdgcn_fmed3f(rintf(p), -65536.f, 65536.f) + e.y_zp;
     qv = qv < e.lo ? e.lo : (qv > e.hi ? e.hi : qv);
     static_cast<uint8_t *>(y)[o] = (uint8_t)qv;
   } else {
@@ -393,7 +396,7 @@ __global__ __launch_bounds__(256, 2) void k_i8_gemm(
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             const float pf = (float)((double)v[i] * (double)mult);
-            int qv = (int)rintf(pf) + e.y_zp;
+            int qv = (int)__builtin_amdgcn_fmed3f(rintf(pf), -65536.f, 65536.f) + e.y_zp;
             qv = qv < e.lo ? e.lo : (qv > e.hi ? e.hi : qv);
             pk |= (uint32_t)(qv & 255) << (8 * i);
           }
@@ -731,4 +734,112 @@ size_t mg_int8_batched_ws_bytes(int64_t a_batch, int64_t b_batch, int64_t M,
   const size_t b = mg_align((size_t)b_batch * n32 * kqp * 64 * 16) +
                    2 * mg_align((size_t)b_batch * npad * 4) + mg_align((size_t)(N + 1) * 4);
   return b + plan_i8(a_batch, a_batch > b_batch ? a_batch : b_batch, M, K, N).total;
+}
+
+// ------------------------------------------------------------ long K
+//
+// MatMulInteger accumulates in Dart's 64-bit int and returns Tensor.int64
+// (lib/src/onnx_qlinear_ops.dart:55-80).  A k term is at most 255 * 255 in
+// magnitude, so the int32 GEMM above is exact for K <= 33025.  Longer rows
+// are cut into segments of MG_I8_SEG k: each segment runs the int32 GEMM
+// (exact, |sum| <= 32768 * 65025 < 2^31) on contiguous copies of its A
+// columns and B rows, and the segment sums are added in int64.  QLinearMatMul
+// then requantises the int64 sum as the reference does: (double)acc * mult
+// rounded to f32, round half to even, + y_zp, clamped (:100-106).
+
+namespace {
+
+constexpr int64_t MG_I8_SEG = 32768;
+
+__global__ __launch_bounds__(256) void k_i64_accum(const int32_t *__restrict__ part,
+                                                   int64_t *__restrict__ acc, int64_t n,
+                                                   int first) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  acc[i] = first ? (int64_t)part[i] : acc[i] + (int64_t)part[i];
+}
+
+__global__ __launch_bounds__(256) void k_i64_requant(const int64_t *__restrict__ acc,
+                                                     uint8_t *__restrict__ y, int64_t n,
+                                                     float mult, int32_t y_zp, int32_t lo,
+                                                     int32_t hi) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float p = (float)((double)acc[i] * (double)mult);
+  // Rounded values beyond +-65536 saturate alike after + y_zp and the clamp.
+  int q = (int)__builtin_amdgcn_fmed3f(rintf(p), -65536.f, 65536.f) + y_zp;
+  q = q < lo ? lo : (q > hi ? hi : q);
+  y[i] = (uint8_t)q;
+}
+
+struct LongKLayout {
+  int64_t seg, nseg;
+  size_t off_a, off_b, off_part, off_acc, off_run, total;
+};
+
+LongKLayout long_k_layout(int64_t a_batch, int64_t b_batch, int64_t M, int64_t K, int64_t N,
+                          bool requant) {
+  LongKLayout l;
+  const int64_t batch = a_batch > b_batch ? a_batch : b_batch;
+  l.nseg = K <= MG_I8_SEG ? 1 : (K + MG_I8_SEG - 1) / MG_I8_SEG;
+  l.seg = l.nseg == 1 ? K : MG_I8_SEG;
+  const bool copy = l.nseg > 1;
+  l.off_a = 0;
+  l.off_b = l.off_a + (copy ? mg_align((size_t)(a_batch * M * l.seg)) : 0);
+  l.off_part = l.off_b + (copy ? mg_align((size_t)(b_batch * l.seg * N)) : 0);
+  l.off_acc = l.off_part + mg_align((size_t)(batch * M * N) * 4);
+  l.off_run = l.off_acc + (requant ? mg_align((size_t)(batch * M * N) * 8) : 0);
+  l.total = l.off_run + mg_int8_batched_ws_bytes(a_batch, b_batch, M, l.seg, N);
+  return l;
+}
+
+}  // namespace
+
+size_t mg_int8_long_k_ws_bytes(int64_t a_batch, int64_t b_batch, int64_t M, int64_t K, int64_t N,
+                               bool requant) {
+  return long_k_layout(a_batch, b_batch, M, K, N, requant).total;
+}
+
+mg_status mg_int8_run_long_k(mg_ctx *ctx, const void *a_dev, int32_t a_signed, int64_t a_batch,
+                             const void *b_dev, int32_t b_signed, int64_t b_batch, int64_t M,
+                             int64_t K, int64_t N, const int32_t *a_zp, int64_t a_zp_len,
+                             const int32_t *b_zp, int64_t b_zp_len, const mg_requant *rq,
+                             void *y_dev, void *ws) {
+  const bool req = mg_requant_out(rq);
+  const LongKLayout l = long_k_layout(a_batch, b_batch, M, K, N, req);
+  const int64_t batch = a_batch > b_batch ? a_batch : b_batch;
+  const int64_t tot = batch * M * N;
+  if (tot == 0) return MG_OK;
+  hipStream_t st = ctx->stream;
+  char *base = static_cast<char *>(ws);
+  int32_t *part = reinterpret_cast<int32_t *>(base + l.off_part);
+  int64_t *acc = req ? reinterpret_cast<int64_t *>(base + l.off_acc)
+                     : static_cast<int64_t *>(y_dev);
+  const unsigned blocks = (unsigned)((tot + 255) / 256);
+  for (int64_t s = 0; s < l.nseg; s++) {
+    const int64_t k0 = s * l.seg, kn = std::min<int64_t>(l.seg, K - k0);
+    const void *as = a_dev, *bs = b_dev;
+    if (l.nseg > 1) {
+      // A[:, :, k0:k0+kn] and B[:, k0:k0+kn, :] as contiguous operands.
+      char *ad = base + l.off_a, *bd = base + l.off_b;
+      MG_HIP(hipMemcpy2DAsync(ad, (size_t)kn, static_cast<const char *>(a_dev) + k0, (size_t)K,
+                              (size_t)kn, (size_t)(a_batch * M), hipMemcpyDeviceToDevice, st));
+      MG_HIP(hipMemcpy2DAsync(bd, (size_t)(kn * N),
+                              static_cast<const char *>(b_dev) + k0 * N, (size_t)(K * N),
+                              (size_t)(kn * N), (size_t)b_batch, hipMemcpyDeviceToDevice, st));
+      as = ad;
+      bs = bd;
+    }
+    MG_TRY(mg_int8_run_batched(ctx, as, a_signed, a_batch, bs, b_signed, b_batch, M, kn, N, a_zp,
+                               a_zp_len, b_zp, b_zp_len, nullptr, part, base + l.off_run));
+    hipLaunchKernelGGL(k_i64_accum, dim3(blocks), dim3(256), 0, st, part, acc, tot,
+                       s == 0 ? 1 : 0);
+    MG_TRY(mg_launch_check("k_i64_accum"));
+  }
+  if (req) {
+    hipLaunchKernelGGL(k_i64_requant, dim3(blocks), dim3(256), 0, st, acc,
+                       static_cast<uint8_t *>(y_dev), tot, rq->mult, rq->y_zp, rq->lo, rq->hi);
+    MG_TRY(mg_launch_check("k_i64_requant"));
+  }
+  return MG_OK;
 }

@@ -87,8 +87,13 @@ class Context:
 
     def set_prefill_images(self, enable: bool = True):
         """Whether MatMulNBits weights created on this context from now on
-        keep prefill images (e4m3 (q - zp), 1 byte per weight, for the fp8
-        prefill GEMM; default on).  Same results either way."""
+        keep prefill images (default on): the weight's (q - zp) / 2 (q / 2
+        with float zero points) as fp6 e2m3 MFMA operands, 3/4 byte per
+        weight on top of the packed half byte, for blocks >= 128.  Prefill
+        calls on weights with images run the fp6 GEMM, those without the fp8
+        GEMM that dequantises each tile (or the fp32 path for float zero
+        points).  Both meet the MatMulNBits tolerance; the results differ in
+        rounding."""
         check(lib.mg_ctx_set_prefill_images(self.handle, int(bool(enable))))
 
     def profile_records(self) -> list:
@@ -638,6 +643,11 @@ def op_matmul_nbits(a, b_q, scales, zero_points=None, *, k, n, bits=4, block_siz
         w.release()
 
 
+# Longest K whose MatMulInteger sums fit int32 for every operand (33025 *
+# 255 * 255 < 2^31); longer rows use the int64 entry point.
+MAX_K_INT32 = 33025
+
+
 def op_matmul_integer(a, b, a_zp=None, b_zp=None, ctx: Context | None = None) -> np.ndarray:
     """opMatMulInteger (lib/src/onnx_qlinear_ops.dart:32-81); int64 result."""
     a, sa = _q_operand(a, "MatMulInteger")
@@ -650,8 +660,15 @@ def op_matmul_integer(a, b, a_zp=None, b_zp=None, ctx: Context | None = None) ->
     ab = int(np.prod(a.shape[:-2])) if a.ndim > 2 else 1
     bb = int(np.prod(b.shape[:-2])) if b.ndim > 2 else 1
     out_batch = a.shape[:-2] if ab >= bb else b.shape[:-2]
-    y = np.empty(tuple(out_batch) + (m, n), dtype=np.int32)
     ctx = ctx or default_context()
+    if a.shape[-1] > MAX_K_INT32:
+        # Sums may exceed int32: the int64 form (segments summed in int64).
+        y = np.empty(tuple(out_batch) + (m, n), dtype=np.int64)
+        check(lib.mg_matmul_integer_i64(ctx.handle, _ptr(a), sa, _ptr(_shape_arr(a)), a.ndim,
+                                        _ptr(b), sb, _ptr(_shape_arr(b)), b.ndim, _ptr(za), la,
+                                        _ptr(zb), lb, _ptr(y)))
+        return y
+    y = np.empty(tuple(out_batch) + (m, n), dtype=np.int32)
     check(lib.mg_matmul_integer(ctx.handle, _ptr(a), sa, _ptr(_shape_arr(a)), a.ndim,
                                 _ptr(b), sb, _ptr(_shape_arr(b)), b.ndim, _ptr(za), la,
                                 _ptr(zb), lb, _ptr(y)))
@@ -698,9 +715,15 @@ def op_dynamic_quantize_linear(x, ctx: Context | None = None):
 
 
 def op_matmul(a, b, ctx: Context | None = None) -> np.ndarray:
-    """opMatMul (lib/src/onnx_ops.dart:1710-1766), numpy broadcasting."""
-    a = np.ascontiguousarray(a, dtype=np.float32)
-    b = np.ascontiguousarray(b, dtype=np.float32)
+    """opMatMul (lib/src/onnx_ops.dart:1710-1766), numpy broadcasting.
+
+    Float operands (the reference's Float32List tensors; other float widths
+    are taken as f32, as the loader widens fp16) run the fp32 kernel.  When
+    either operand is an integer tensor the reference falls back to a double
+    sum of getD products per output (:1753-1762): both operands then go to
+    the device as doubles (an int64 element's nearest double, as getD) and
+    the double-accumulation kernel."""
+    a, b = np.asarray(a), np.asarray(b)
     if a.ndim < 2 or b.ndim < 2:
         raise ArgumentError("MatMul: operands must have rank >= 2")
     try:
@@ -709,6 +732,14 @@ def op_matmul(a, b, ctx: Context | None = None) -> np.ndarray:
         raise ArgumentError("MatMul: batch dims do not broadcast") from None
     y = np.empty(tuple(batch) + (a.shape[-2], b.shape[-1]), dtype=np.float32)
     ctx = ctx or default_context()
+    if a.dtype.kind in "iub" or b.dtype.kind in "iub":
+        ad = np.ascontiguousarray(a, dtype=np.float64)
+        bd = np.ascontiguousarray(b, dtype=np.float64)
+        check(lib.mg_matmul_f64acc(ctx.handle, _ptr(ad), _ptr(_shape_arr(ad)), ad.ndim,
+                                   _ptr(bd), _ptr(_shape_arr(bd)), bd.ndim, _ptr(y)))
+        return y
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
     check(lib.mg_matmul_f32(ctx.handle, _ptr(a), _ptr(_shape_arr(a)), a.ndim, _ptr(b),
                             _ptr(_shape_arr(b)), b.ndim, _ptr(y)))
     return y

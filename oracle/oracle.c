@@ -278,6 +278,46 @@ int orc_matmul_f32(const float *a, const int64_t *a_shape, int a_rank,
   return ORC_OK;
 }
 
+/* opMatMul's fallback when the operands are not both Float32List
+ * (onnx_ops.dart:1753-1762): per batch (broadcast offsets :1742-1749), each
+ * output is `double sum = 0; sum += a.getD(..) * b.getD(..)` over k in order,
+ * stored into a Float32List (one rounding).  The operands arrive as the
+ * getD doubles; this file is built with -ffp-contract=off, so each product
+ * and sum is rounded on its own, as Dart's double arithmetic does. */
+int orc_matmul_f64acc(const double *a, const int64_t *a_shape, int a_rank,
+                      const double *b, const int64_t *b_shape, int b_rank,
+                      float *y) {
+  if (a_rank < 2 || b_rank < 2 || a_rank > 8 || b_rank > 8)
+    return ORC_INVALID_ARGUMENT;
+  const int64_t m = a_shape[a_rank - 2], k = a_shape[a_rank - 1];
+  const int64_t k2 = b_shape[b_rank - 2], n = b_shape[b_rank - 1];
+  if (k != k2) return ORC_INVALID_ARGUMENT;
+  int64_t ob[8];
+  int obr = 0;
+  if (broadcast_shape(a_shape, a_rank - 2, b_shape, b_rank - 2, ob, &obr))
+    return ORC_INVALID_ARGUMENT;
+  int64_t batch = 1;
+  for (int d = 0; d < obr; d++) batch *= ob[d];
+  int64_t coords[8] = {0};
+  for (int64_t bi = 0; bi < batch; bi++) {
+    int64_t rem = bi;
+    for (int d = obr - 1; d >= 0; d--) {
+      coords[d] = rem % ob[d];
+      rem /= ob[d];
+    }
+    const double *ab = a + flatten_broadcast(coords, obr, a_shape, a_rank - 2) * m * k;
+    const double *bb = b + flatten_broadcast(coords, obr, b_shape, b_rank - 2) * k * n;
+    float *yb = y + bi * m * n;
+    for (int64_t i = 0; i < m; i++)
+      for (int64_t j = 0; j < n; j++) {
+        double sum = 0;
+        for (int64_t kk = 0; kk < k; kk++) sum += ab[i * k + kk] * bb[kk * n + j];
+        yb[i * n + j] = (float)sum;
+      }
+  }
+  return ORC_OK;
+}
+
 int orc_gemm_f32(const float *a, const int64_t *a_shape, const float *b,
                  const int64_t *b_shape, const float *c, const int64_t *c_shape,
                  int c_rank, double alpha, double beta, int trans_a,

@@ -41,6 +41,11 @@ void orc_pool_destroy(void *pool);
 int orc_matmul_f32(const float *a, const int64_t *a_shape, int a_rank,
                    const float *b, const int64_t *b_shape, int b_rank,
                    float *y);
+/* MatMul on non-float operands given as doubles (double sum over k in
+ * order, one rounding to f32). */
+int orc_matmul_f64acc(const double *a, const int64_t *a_shape, int a_rank,
+                      const double *b, const int64_t *b_shape, int b_rank,
+                      float *y);
 
 /* opGemm (+ the graph's transB prepack): lib/src/onnx_ops.dart:2152-2172,
  * lib/src/onnx_graph.dart:2156-2173.  a, b rank 2; c may be NULL or any shape

@@ -174,3 +174,46 @@ def test_large_tile_path(ops, k):
     rows = np.concatenate([np.arange(64), np.arange(m - 64, m)])
     ref = oracle.matmul_f32(a[rows], w)
     assert G.rms_error(y[rows], ref) <= TOL
+
+
+@pytest.mark.parametrize("sa,sb,kinds", [
+    ((3, 7), (7, 5), ("i64", "i64")),
+    ((2, 3, 40, 129), (2, 3, 129, 65), ("i64", "i64")),   # batched, ragged
+    ((2, 1, 4, 300), (3, 300, 17), ("u8", "i8")),         # broadcast batch dims
+    ((5, 64), (64, 33), ("f32", "i64")),                  # float x integer
+    ((70000, 2), (2, 3), ("i32", "f32")),                 # many rows
+])
+def test_matmul_non_float_operands_bitwise(ops, sa, sb, kinds):
+    # opMatMul's double fallback (lib/src/onnx_ops.dart:1753-1762): a double
+    # sum of getD products in k order, one rounding to f32.  Bitwise against
+    # the oracle, with operands large enough that the products and sums
+    # round in double.
+    rng = np.random.default_rng(0x5EED00B0 + len(sa) + sa[-1])
+
+    def make(shape, kind):
+        if kind == "i64":
+            return rng.integers(-2**52, 2**52, shape, dtype=np.int64)
+        if kind == "i32":
+            return rng.integers(-2**31, 2**31, shape, dtype=np.int64).astype(np.int32)
+        if kind == "u8":
+            return rng.integers(0, 256, shape, dtype=np.uint8)
+        if kind == "i8":
+            return rng.integers(-128, 128, shape, dtype=np.int8)
+        return (rng.standard_normal(shape) * 1e6).astype(np.float32)
+
+    a, b = make(sa, kinds[0]), make(sb, kinds[1])
+    y = ops.op_matmul(a, b)
+    ref = oracle.matmul_f64acc(a, b)
+    assert y.dtype == np.float32 and y.shape == ref.shape
+    np.testing.assert_array_equal(y, ref)
+
+
+def test_matmul_non_float_cancellations(ops):
+    # The closed-form cells of the oracle's pin: no fused multiply-add
+    # (y[0,0] = 0, not 1) and k order (y[1,1] = 0, not 1).
+    t40, t60 = 2**40, 2**60
+    a = np.array([[-t40, t40 + 1, 0], [1, t60, -t60]], np.int64)
+    b = np.array([[t40 + 2, 1], [t40 + 1, 1], [1, 1]], np.int64)
+    y = ops.op_matmul(a, b)
+    assert y[0, 0] == 0.0 and y[1, 1] == 0.0
+    np.testing.assert_array_equal(y, oracle.matmul_f64acc(a, b))

@@ -148,6 +148,85 @@ def test_errors(ops):
         ops.op_matmul_integer(np.zeros((2, 4, 3), np.uint8), np.zeros((3, 3, 2), np.int8))
 
 
+# Rows longer than 33025 k: the reference's int64 accumulator
+# (lib/src/onnx_qlinear_ops.dart:55-80) holds sums past int32.  The int64
+# entry point cuts K into 32768-k segments summed in int64 on the device.
+LONG_K = [
+    # (a batch, b batch, M, K, N, extreme): extreme operands push every sum
+    # past int32 (255 * -255 per term with these zero points).
+    (1, 1, 3, 40000, 70, True),
+    (1, 1, 5, 70000, 33, False),   # three segments, the last one short
+    (2, 1, 4, 33026, 20, True),    # one k past the int32 bound; batched A
+    (2, 2, 2, 65536, 9, False),    # two whole segments; batched B
+]
+
+
+@pytest.mark.parametrize("ab,bb,m,k,n,extreme", LONG_K)
+def test_matmul_integer_int64_long_k(ops, ab, bb, m, k, n, extreme):
+    rng = np.random.default_rng(0x5EED00A0 + k + n)
+    a = rng.integers(0, 256, (ab, m, k), dtype=np.uint8)
+    b = rng.integers(-128, 128, (bb, k, n), dtype=np.int8)
+    az, bz = np.array(3), rng.integers(-128, 128, n).astype(np.int8)
+    if extreme:
+        a[...] = 255
+        a[0, 0, : k // 3] = 0
+        b[...] = -128
+        az, bz = np.array(0), np.full(n, 127, np.int8)
+    y = ops.op_matmul_integer(a, b, az, bz)
+    ref = oracle.matmul_integer(a, b, az, bz)
+    assert y.dtype == np.int64
+    np.testing.assert_array_equal(y, ref)
+    if extreme:
+        assert ref.min() < -2**31
+    with pytest.raises(Exception, match="int64 form"):
+        ops.check(ops.lib.mg_matmul_integer(
+            ops.default_context().handle, ops._ptr(a), 0, ops._ptr(ops._shape_arr(a)), a.ndim,
+            ops._ptr(b), 1, ops._ptr(ops._shape_arr(b)), b.ndim, None, 0, None, 0,
+            ops._ptr(np.empty(ref.shape, np.int32))))
+
+
+def test_matmul_integer_int64_short_k_equals_int32_form(ops):
+    # The int64 entry point at ordinary K (one segment) gives the int32
+    # form's values.
+    rng = np.random.default_rng(0x5EED00A1)
+    a = rng.integers(-128, 128, (3, 37, 1000), dtype=np.int8)
+    b = rng.integers(0, 256, (1000, 300), dtype=np.uint8)
+    az, bz = rng.integers(-128, 128, 37).astype(np.int8), np.array(7)
+    y32 = ops.op_matmul_integer(a, b, az, bz)
+    y64 = np.empty(y32.shape, np.int64)
+    ops.check(ops.lib.mg_matmul_integer_i64(
+        ops.default_context().handle, ops._ptr(a), 1, ops._ptr(ops._shape_arr(a)), a.ndim,
+        ops._ptr(b), 0, ops._ptr(ops._shape_arr(b)), b.ndim,
+        ops._ptr(np.ascontiguousarray(az.astype(np.int32))), az.size,
+        ops._ptr(np.ascontiguousarray(bz.astype(np.int32).ravel())), 1, ops._ptr(y64)))
+    np.testing.assert_array_equal(y64, y32)
+
+
+@pytest.mark.parametrize("signed_out", [False, True])
+def test_qlinear_long_k(ops, signed_out):
+    # QLinearMatMul requantises the int64 sum: (double)acc * mult rounded to
+    # f32, half to even, + y_zp, clamped (:100-106); sums past int32 saturate
+    # and the rest round as the reference does.
+    rng = np.random.default_rng(0x5EED00A2 + signed_out)
+    m, k, n = 6, 50000, 40
+    a = rng.integers(0, 256, (m, k), dtype=np.uint8)
+    b = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    a[0] = 255
+    b[:, :5] = -128
+    bz = np.zeros(n, np.int8)
+    bz[:5] = 127  # row 0, columns 0-4: 50000 terms of 255 * -255, below -2^31
+    a_s, b_s, y_s = np.float32(0.02), np.float32(2.0**-10), np.float32(0.5)
+    az = np.array(0, np.uint8)
+    yz = np.array(3 if signed_out else 128, np.int8 if signed_out else np.uint8)
+    lo, hi = (-128, 127) if signed_out else (0, 255)
+    y = ops.op_qlinear_matmul(a, a_s, az, b, b_s, bz, y_s, yz, lo=lo, hi=hi)
+    ref = oracle.qlinear_matmul(a, a_s, az, b, b_s, bz, y_s, yz, lo=lo, hi=hi)
+    np.testing.assert_array_equal(y.astype(np.int64), ref)
+    assert oracle.matmul_integer(a[:1], b[:, :5], az, bz[:5]).max() < -2**31
+    rest = ref[1:, 5:]
+    assert ((rest > lo) & (rest < hi)).any()  # not all saturated
+
+
 # DQL -> MatMulInteger / QLinearMatMul with the scale and zero point left in
 # device memory (mg_*_w_dq_dev).  Shapes cover the fused requant epilogue
 # (one K split), the split-K reduce, ragged edges and one row.

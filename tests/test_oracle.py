@@ -201,6 +201,53 @@ def test_matmul_broadcast_batches():
         assert np.abs(y - ref).max() < 1e-4
 
 
+def test_matmul_non_float_exact_integer_sums():
+    # Integer operands whose every partial sum stays below 2^53: the double
+    # sum is the exact integer, so the f32 output is that integer rounded
+    # once (numpy's int64 -> float32 conversion).  Broadcast batches and a
+    # mixed float-by-int case (float values that are integers) included.
+    rng = np.random.default_rng(51)
+    for sa, sb in [((3, 7), (7, 5)), ((2, 3, 4, 9), (2, 3, 9, 6)), ((2, 1, 4, 6), (3, 6, 5)),
+                   ((1, 64), (64, 3))]:
+        a = rng.integers(-2**20, 2**20, sa, dtype=np.int64)
+        b = rng.integers(-2**20, 2**20, sb, dtype=np.int64)
+        exact = np.matmul(a, b)
+        assert np.abs(exact).max() < 2**53
+        np.testing.assert_array_equal(oracle.matmul_f64acc(a, b), exact.astype(np.float32))
+        af = a.astype(np.float32)  # |a| < 2^20: exact in f32
+        np.testing.assert_array_equal(oracle.matmul_f64acc(af, b), exact.astype(np.float32))
+
+
+def test_matmul_non_float_rounds_each_double_step_in_k_order():
+    # Beyond 2^53 each product and sum rounds.  Two cancellations fix the
+    # chain in closed form:
+    #   y[0,0] = -(2^40)(2^40+2) + (2^40+1)^2 = 1 exactly, but the second
+    #     product rounds to 2^80 + 2^41 in double, so the reference gets 0
+    #     (a fused multiply-add would give 1);
+    #   y[1,1] = 1 + 2^60 - 2^60: in k order 1 is absorbed (0); in reverse
+    #     order, or exactly, it is 1.
+    # Random large operands are then checked against a Python-float loop
+    # (IEEE double, one rounding per operation, k in order).
+    t40, t60 = 2**40, 2**60
+    a = np.array([[-t40, t40 + 1, 0], [1, t60, -t60]], np.int64)
+    b = np.array([[t40 + 2, 1], [t40 + 1, 1], [1, 1]], np.int64)
+    y = oracle.matmul_f64acc(a, b)
+    assert y[0, 0] == 0.0 and y[1, 1] == 0.0
+    rng = np.random.default_rng(52)
+    a = rng.integers(-2**62, 2**62, (4, 23), dtype=np.int64)
+    b = rng.integers(-2**40, 2**40, (23, 6), dtype=np.int64)
+    y = oracle.matmul_f64acc(a, b)
+    ad, bd = a.astype(np.float64), b.astype(np.float64)
+    want = np.empty((4, 6), np.float32)
+    for i in range(4):
+        for j in range(6):
+            acc = 0.0
+            for k in range(23):
+                acc += float(ad[i, k]) * float(bd[k, j])
+            want[i, j] = acc
+    np.testing.assert_array_equal(y, want)
+
+
 def test_gemm_attributes():
     rng = np.random.default_rng(6)
     a = rng.standard_normal((6, 5)).astype(np.float32)
