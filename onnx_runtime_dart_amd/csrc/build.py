@@ -1,10 +1,16 @@
 """Builds libmigemm.so (HIP kernels + C ABI) for gfx950 with hipcc.
 
-    python onnx_runtime_dart_amd/csrc/build.py [--jobs N]
+    python onnx_runtime_dart_amd/csrc/build.py [--jobs N] [--sanitize]
 
 Objects go to onnx_runtime_dart_amd/csrc/_build/, the library to
 onnx_runtime_dart_amd/lib/libmigemm.so.  Every source is recompiled on each
 call (the build is a few seconds per file).
+
+--sanitize (build_sanitized) also writes lib/libmigemm_san.so: the same
+kernels with the C ABI's host code (api.hip: validation, planners, staging)
+compiled with AddressSanitizer and UndefinedBehaviorSanitizer (host pass
+only; errors abort).  It is loaded through MIGEMM_LIBRARY with clang's ASan
+runtime preloaded, for CPU tests of the host side (tests/test_sanitizers.py).
 """
 from __future__ import annotations
 
@@ -96,7 +102,55 @@ def build(jobs: int | None = None) -> Path:
     return LIB
 
 
+SAN_LIB = PKG / "lib" / "libmigemm_san.so"
+# Sanitizers on the host pass only: each flag behind -Xarch_host.
+SAN_HOST = ["-Xarch_host", "-fsanitize=address",
+            "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-sanitize-recover=undefined",
+            "-Xarch_host", "-fno-omit-frame-pointer",
+            "-Xarch_host", "-g"]
+
+
+def asan_runtime() -> Path:
+    """clang's shared ASan runtime (preloaded before the sanitized library)."""
+    hits = sorted(Path(hipcc()).resolve().parent.parent.glob(
+        "llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not hits:
+        hits = sorted(Path("/opt/rocm/llvm/lib/clang").glob("*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not hits:
+        raise RuntimeError("clang ASan runtime not found")
+    return hits[-1]
+
+
+def build_sanitized() -> Path:
+    """api.hip with host ASan/UBSan, linked with the other objects of the last
+    build(), into SAN_LIB."""
+    objs = [BUILD / (Path(src).stem + ".o") for src in SOURCES if src != "api.hip"]
+    if not all(o.exists() for o in objs):
+        build()
+    san_obj = BUILD / "api_san.o"
+    flags = [f for f in HIPFLAGS if f != "-O3"] + ["-O1"]
+    r = subprocess.run([hipcc(), *flags, *SAN_HOST, "-c", str(CSRC / "api.hip"), "-o",
+                        str(san_obj)], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc (sanitized api.hip) failed:\n{r.stderr}")
+    tmp = SAN_LIB.with_suffix(".so.tmp")
+    link_san = ["-Xarch_host", "-fsanitize=address",
+                "-Xarch_host", "-fsanitize=undefined",
+                "-Xarch_host", "-shared-libasan"]
+    r = subprocess.run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *link_san, "-o",
+                        str(tmp), str(san_obj), *map(str, objs)], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link (sanitized) failed:\n{r.stderr}")
+    os.replace(tmp, SAN_LIB)
+    return SAN_LIB
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
-    print(build(ap.parse_args().jobs))
+    ap.add_argument("--sanitize", action="store_true")
+    a = ap.parse_args()
+    print(build(a.jobs))
+    if a.sanitize:
+        print(build_sanitized())

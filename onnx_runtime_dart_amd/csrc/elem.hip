@@ -66,8 +66,7 @@ __global__ __launch_bounds__(256) void k_bin_bcast(const float *a, const float *
   y[i] = bin_op<OP>(a[ia], b[ib]);
 }
 
-__global__ __launch_bounds__(256) void k_sigmoid(const float *__restrict__ x,
-                                                 float *__restrict__ y, int64_t n) {
+__global__ __launch_bounds__(256) void k_sigmoid(const float *x, float *y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   y[i] = (float)(1.0 / (1.0 + exp(-(double)x[i])));
@@ -88,12 +87,13 @@ __device__ inline double block_sum(double v, double *red) {
 // RMSNorm over the last axis: one workgroup per row of d elements.  With a
 // skip input the row is s = x + skip (f32), written to sum when asked; with
 // a bias, out = normed + bias (f32), as the reference's Add after the norm.
-__global__ __launch_bounds__(256) void k_rms_last(const float *__restrict__ x,
-                                                  const float *__restrict__ skip,
+// Any of x, skip, sum and y may be the same buffer (an in-place residual):
+// each element is read and written by one thread only, and once sum holds
+// s the second pass reads s back from it instead of re-adding x and skip.
+__global__ __launch_bounds__(256) void k_rms_last(const float *x, const float *skip,
                                                   const float *__restrict__ gamma,
                                                   const float *__restrict__ bias, double eps,
-                                                  int64_t d, float *__restrict__ y,
-                                                  float *__restrict__ sum) {
+                                                  int64_t d, float *y, float *sum) {
   __shared__ double red[4];
   const int64_t base = (int64_t)blockIdx.x * d;
   const int t = threadIdx.x;
@@ -109,8 +109,10 @@ __global__ __launch_bounds__(256) void k_rms_last(const float *__restrict__ x,
   ss = block_sum(ss, red);
   const double inv = 1.0 / sqrt(ss / (double)d + eps);
   for (int64_t j = t; j < d; j += 256) {
-    float v = x[base + j];
-    if (skip) v = v + skip[base + j];
+    float v;
+    if (skip && sum) v = sum[base + j];
+    else if (skip) v = x[base + j] + skip[base + j];
+    else v = x[base + j];
     float o = (float)((double)v * inv * (double)gamma[j]);
     if (bias) o = o + bias[j];
     y[base + j] = o;
@@ -119,10 +121,10 @@ __global__ __launch_bounds__(256) void k_rms_last(const float *__restrict__ x,
 
 // RMSNorm over another axis: one thread per (outer, inner) slice, walking the
 // reduce axis in order as the reference does; gamma follows the last axis.
-__global__ __launch_bounds__(256) void k_rms_axis(const float *__restrict__ x,
+__global__ __launch_bounds__(256) void k_rms_axis(const float *x,
                                                   const float *__restrict__ gamma, double eps,
                                                   int64_t outer, int64_t dim, int64_t inner,
-                                                  int64_t last, float *__restrict__ y) {
+                                                  int64_t last, float *y) {
   const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (s >= outer * inner) return;
   const int64_t o = s / inner, i = s % inner;

@@ -111,9 +111,10 @@ struct mg_nbits_dev {
   uint8_t *zp4 = nullptr;     // [ng][nbh][64]  (MG_ZP_UINT4)
   float *zpf = nullptr;       // [ng][nb][64]   (MG_ZP_FLOAT)
   float *bias = nullptr;      // [N] or null
-  // Prefill images ([2 ng][c4][256] uint4, or null): per 32-column slab and
-  // k group, the 4 KiB of e4m3 weight fragments that the fp8 prefill GEMM
-  // would otherwise dequantise into LDS (mg_nbits_f8_images).
+  // Prefill images ([2 ng][c4][3072] bytes, or null): per 32-column slab and
+  // k group, the fp6 e2m3 MFMA B operands of (q - zp) / 2 (q / 2 with float
+  // zero points), 3/4 byte per weight, that the fp6 prefill GEMM copies into
+  // LDS (mg_nbits_f8_images).
   void *img = nullptr;
 };
 
@@ -176,9 +177,9 @@ mg_status mg_nbits_upload(mg_ctx *ctx, mg_weight *w, const mg_byte_source &b,
                           const mg_byte_source &scales, int32_t zp_kind,
                           const mg_byte_source &zp, const float *bias, int64_t chunk_bytes);
 void mg_nbits_free(mg_weight *w);
-// Whether a weight's prefill GEMM is the fp8 one (block_size >= 128, integer
-// zero points), and the build of its prefill images (allocates w->nbits.img;
-// synchronous).
+// Whether a weight can have prefill images and run the block-scaled fp6 /
+// fp8 prefill GEMMs (block_size >= 128, any zero-point form), and the build
+// of its images (allocates w->nbits.img; synchronous).
 bool mg_nbits_f8_eligible(const mg_nbits_dev &d);
 mg_status mg_nbits_f8_images(mg_ctx *ctx, mg_weight *w);
 // Workspace bytes mg_nbits_run needs for M rows.
@@ -276,6 +277,11 @@ struct mg_f32_problem {
 };
 mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
                      const float *b_dev, float *y_dev);
+// MatMul on operands given as doubles (the reference's non-float fallback):
+// double products summed in k order, one rounding to f32.  Uses p.M, K, N,
+// batch and bc (row-major A [M, K] and B [K, N] per batch).
+mg_status mg_f64acc_run(mg_ctx *ctx, const mg_f32_problem &p, const double *a_dev,
+                        const double *b_dev, float *y_dev);
 
 // ------------------------------------------------------- elementwise ops
 

@@ -37,7 +37,9 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "lib" / "liboracle.so"
+# ORACLE_LIBRARY selects another build of oracle.c (the sanitizer build,
+# lib/liboracle_san.so, under tests/test_sanitizers.py).
+LIB_PATH = Path(os.environ.get("ORACLE_LIBRARY", HERE / "lib" / "liboracle.so"))
 
 OK, INVALID_ARGUMENT, UNSUPPORTED = 0, 1, 2
 
@@ -80,6 +82,7 @@ def _declare(L):
     L.orc_pool_destroy.argtypes = [C.c_void_p]
     L.orc_pool_destroy.restype = None
     L.orc_matmul_f32.argtypes = [_P, _P, _I, _P, _P, _I, _P]
+    L.orc_matmul_f64acc.argtypes = [_P, _P, _I, _P, _P, _I, _P]
     L.orc_gemm_f32.argtypes = [_P, _P, _P, _P, _P, _P, _I, C.c_double,
                                C.c_double, _I, _I, _P]
     L.orc_matmul_nbits.argtypes = [_P, _I64, _I64, _I64, _I64, _I64, _P, _P,
@@ -182,6 +185,19 @@ def matmul_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     sa, sb = _shape(a), _shape(b)
     _check(lib().orc_matmul_f32(_ptr(a), _ptr(sa), a.ndim, _ptr(b), _ptr(sb),
                                 b.ndim, _ptr(y)), "matmul_f32")
+    return y
+
+
+def matmul_f64acc(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """opMatMul on non-float operands (lib/src/onnx_ops.dart:1753-1762): the
+    operands as doubles (getD), a double sum over k per output, f32 result."""
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    b = np.ascontiguousarray(b, dtype=np.float64)
+    out_shape = _broadcast(a.shape[:-2], b.shape[:-2]) + [a.shape[-2], b.shape[-1]]
+    y = np.empty(out_shape, dtype=np.float32)
+    sa, sb = _shape(a), _shape(b)
+    _check(lib().orc_matmul_f64acc(_ptr(a), _ptr(sa), a.ndim, _ptr(b), _ptr(sb),
+                                   b.ndim, _ptr(y)), "matmul_f64acc")
     return y
 
 

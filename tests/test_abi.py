@@ -98,3 +98,23 @@ def test_no_kernel_uses_scratch_memory():
     if not list(mod.BUILD.glob("*.usage.txt")):
         pytest.skip("no resource report: run onnx_runtime_dart_amd/csrc/build.py")
     assert mod.kernels_with_scratch() == []
+
+
+def test_every_entry_point_rejects_null_arguments():
+    # Every status-returning entry point called with null pointers and zero
+    # sizes returns a status (MG_OK for the release / destroy of nothing,
+    # MG_INVALID_ARGUMENT otherwise) without touching a device or memory it
+    # was not given.  Under tests/test_sanitizers.py this runs on the host
+    # code built with AddressSanitizer and UndefinedBehaviorSanitizer.
+    import ctypes as C
+    from onnx_runtime_dart_amd import _lib
+    ok_on_null = {"mg_weight_release", "mg_ctx_destroy", "mg_last_error_budget"}
+    for name, argtypes in sorted(_lib.SIGNATURES.items()):
+        if name in _lib._RESTYPE:
+            continue
+        args = [None if (t in (C.c_void_p, _lib._PP) or
+                         (isinstance(t, type) and issubclass(t, C._Pointer))) else 0
+                for t in argtypes]
+        st = getattr(_lib.lib, name)(*args)
+        assert st == (0 if name in ok_on_null else 1) or (name == "mg_last_error_budget"
+                                                          and st in (0, 1)), (name, st)

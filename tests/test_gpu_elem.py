@@ -145,6 +145,38 @@ def test_skip_rms_norm(ops, rows, d, with_bias):
     assert ulps(y, y_ref) <= 1
 
 
+@pytest.mark.parametrize("alias", ["sum=x", "sum=skip", "y=x", "y=skip", "y=sum",
+                                   "sum=x,y=skip", "y=x,no-sum"])
+def test_skip_rms_norm_in_place(ops, alias):
+    # An in-place residual stream: the sum and the normed output written over
+    # the inputs.  Each aliasing form must give the separate-buffer results.
+    rng = np.random.default_rng(7)
+    rows, d = 5, 2100
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    skip = rng.standard_normal((rows, d)).astype(np.float32)
+    g = rng.uniform(0.5, 2.0, d).astype(np.float32)
+    s_ref = oracle.binary_f32("add", x, skip)
+    y_ref = oracle.rms_norm_f32(s_ref, g, -1, 1e-5)
+    D = ops.DeviceBuffer
+    bx, bskip, bg = D.from_array(x), D.from_array(skip), D.from_array(g)
+    by, bsum = D(x.nbytes), D(x.nbytes)
+    pairs = dict(p.split("=") for p in alias.split(",") if "=" in p)
+    ptr = {"x": bx.ptr, "skip": bskip.ptr}
+    psum = None if "no-sum" in alias else ptr.get(pairs.get("sum"), bsum.ptr)
+    ptr["sum"] = psum
+    py = ptr.get(pairs.get("y"), by.ptr)
+    ops.skip_rms_norm_f32_dev(bx.ptr, bskip.ptr, (rows, d), bg.ptr, d, None, 1e-5, py, psum)
+    out = {}
+    for name, b in (("x", bx), ("skip", bskip), ("y", by), ("sum", bsum)):
+        out[b.ptr] = b.to_array((rows, d), np.float32)
+    assert ulps(out[py], y_ref) <= 1
+    if psum is not None:
+        if psum != py:
+            np.testing.assert_array_equal(out[psum], s_ref)
+    for b in (bx, bskip, bg, by, bsum):
+        b.free()
+
+
 @pytest.mark.parametrize("m", [1, 16])
 def test_decoder_mlp_chain_on_device(ops, m):
     # The MLP half of a Qwen3-style layer with every intermediate in HBM:

@@ -562,9 +562,11 @@ def test_m1_split_k_against_oracle(ops, k, n, bs, zp_mode, with_bias):
 
 FP32_PATH = [
     # (M, K, N, bs, zp_mode, bias): float zero points or 16-k blocks with more
-    # than four rows: columns dequantised to fp32 (the reference's weights)
-    # in chunks, each chunk on the fp32 MFMA GEMM.
+    # than four rows, on weights without prefill images: columns dequantised
+    # to fp32 (the reference's weights) in chunks of 64 MiB, each chunk on the
+    # fp32 MFMA GEMM writing its columns of Y.
     (64, 8192, 5000, 128, "float", True),   # 2048-column chunks: three of them
+    (8, 2048, 8200, 32, "float", True),     # 8192-column chunks: two of them
     (33, 1000, 300, 16, "packed", True),
     (512, 1024, 4096, 32, "float", False),
     (5, 2100, 130, 64, "float", True),
@@ -578,12 +580,19 @@ def test_fp32_path_against_oracle(ops, m, k, n, bs, zp_mode, with_bias):
     b, s, zp = make_nbits(rng, n, k, bs, zp_mode)
     bias = rng.standard_normal(n).astype(np.float32) if with_bias else None
     a = rng.standard_normal((m, k)).astype(np.float32)
-    w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    ctx = ops.default_context()
+    ctx.set_prefill_images(False)  # float zero points at bs >= 128 would take the fp6 GEMM
+    try:
+        w = ops.NBitsWeight(b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    finally:
+        ctx.set_prefill_images(True)
     y = w(a)
     np.testing.assert_array_equal(w(a), y)
     w.release()
+    chunk = (16 << 20) // (-(-k // 128) * 128) // 64 * 64  # columns per dequantised chunk
+    edges = [c for c0 in range(0, n, chunk) for c in range(max(0, c0 - 3), min(n, c0 + 3))]
     cols = np.unique(np.concatenate([np.arange(min(n, 40)), np.arange(max(0, n - 40), n),
-                                     rng.integers(0, n, 100)]))
+                                     np.array(edges, np.int64), rng.integers(0, n, 100)]))
     bb, ss, zz, bi = slice_cols(b, s, zp, bias, cols)
     ref = oracle.matmul_nbits(a, bb, ss, zz, k=k, n=len(cols), block_size=bs, bias=bi)
     assert G.rms_error(y[:, cols], ref) <= TOL, G.rms_error(y[:, cols], ref)
