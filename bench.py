@@ -224,13 +224,14 @@ def main():
                     help="headline and lm_head measurements only")
     ap.add_argument("--only", default=None,
                     choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1", "llama16",
-                             "attn", "conv"],
+                             "attn", "conv", "pass512"],
                     help="profiling mode: launch one workload --steps times and exit "
                          "(lm512 / lm1: Qwen3 lm_head MatMulNBits at M=512 / M=1; i8lm512: "
                          "the lm_head as MatMulInteger at M=512; f32ffn: the MiniLM FFN1 "
                          "Gemm; llama1 / llama16: the Llama lm_head at M=1 / M=16; attn: the MiniLM "
-                         "fused attention; conv: the ResNet-50 3x3 conv; copy: 256 MiB device copy "
-                         "used to calibrate the HBM byte counters)")
+                         "fused attention; conv: the ResNet-50 3x3 conv; pass512: the headline "
+                         "M=512 pass of eight Qwen3 projections, grouped as timed; copy: 256 MiB "
+                         "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -921,6 +922,22 @@ def run_only(args, torch, ops, ctx, stream, dev, randn):
             y = torch.empty((m, n), device=dev, dtype=torch.float32)
             for _ in range(args.steps):
                 w.run_dev(a.data_ptr(), m, y.data_ptr())
+        elif args.only == "pass512":
+            ws = [ops.NBitsWeight(*make_weight(rng, k, n), k=k, n=n, block_size=BLOCK, ctx=ctx)
+                  for _, k, n in QWEN3_PROJ]
+            acts = {k: randn(M_PREFILL, k) for _, k, _ in QWEN3_PROJ}
+            outs = [torch.empty((M_PREFILL, n), device=dev, dtype=torch.float32)
+                    for _, _, n in QWEN3_PROJ]
+            for _ in range(args.steps):
+                for grp in QWEN3_GROUPS:
+                    k = QWEN3_PROJ[grp[0]][1]
+                    ops.matmul_nbits_group_dev([ws[i] for i in grp], acts[k].data_ptr(),
+                                               M_PREFILL, [outs[i].data_ptr() for i in grp],
+                                               ctx=ctx)
+            torch.cuda.synchronize()
+            for x in ws:
+                x.release()
+            w = None
         elif args.only == "i8lm512":
             m, (_, k, n) = M_PREFILL, QWEN3_PROJ[-1]
             b = np.frombuffer(rng.bytes(k * n), dtype=np.int8).reshape(k, n)

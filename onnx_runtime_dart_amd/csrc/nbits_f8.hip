@@ -38,6 +38,8 @@ namespace {
 
 typedef int int8v __attribute__((ext_vector_type(8)));
 typedef short short2v __attribute__((ext_vector_type(2)));
+typedef unsigned uint6v __attribute__((ext_vector_type(6)));
+typedef float float32v __attribute__((ext_vector_type(32)));
 
 // --------------------------------------------------------------- prepass
 
@@ -142,20 +144,6 @@ __global__ __launch_bounds__(256) void k_af8x3(const float *__restrict__ a, int6
 
 // ------------------------------------------------- fp6 prefill (images)
 
-// e2m3 code (sign, 2 exponent bits, 3 mantissa bits, exponent bias 1) of y
-// rounded to nearest even, for |y| <= 4: the e2m3 magnitudes below 2 are the
-// multiples of 1/8 (code 8 |y|), those in [2, 4] the multiples of 1/4 (code
-// 8 + 4 |y|).  *val receives the code's value (signed).
-__device__ inline uint32_t e2m3_rne(float y, float *val) {
-  const float ay = fabsf(y);
-  const bool lo = ay < 2.f;
-  const float q = rintf(lo ? ay * 8.f : ay * 4.f);
-  const uint32_t c = (uint32_t)q + (lo ? 0u : 8u);
-  const float v = lo ? q * 0.125f : q * 0.25f;
-  *val = y < 0.f ? -v : v;
-  return c == 0u ? 0u : (c | (y < 0.f ? 32u : 0u));
-}
-
 // Sixteen 6-bit fields, field i at bits 6 i of three dwords.
 __device__ inline void pack6x16(const uint32_t (&c)[16], uint32_t (&w)[3]) {
   w[0] = w[1] = w[2] = 0u;
@@ -176,106 +164,103 @@ __device__ inline void pack6x16(const uint32_t (&c)[16], uint32_t (&w)[3]) {
 // from the lane itself.
 // Digit d of a block: e_d = e2m3(r_d / 2^E_d) rounded to nearest even,
 // r_{d+1} = r_d - e_d 2^E_d (exact: Sterbenz), where 2^E_d puts the block's
-// largest |r_d| in [2, 4), so every digit leaves at most 2^-4 of the block's
-// largest residual.
+// largest |r_d| in [2, 4) (E_d >= -126, so 2^E_d is a normal float and the
+// block still fits below 4), so every digit leaves at most 2^-4 of the
+// block's largest residual.
+// One thread per 32-k scale block, i.e. per (row, lane half): it converts
+// its 32 values with gfx950's fp6 conversions.  v_cvt_scalef32_2xpk16_fp6_f32
+// (x, y, s) writes field 2 j = e2m3(x_j / s) and field 2 j + 1 = e2m3(y_j /
+// s), rounded to nearest even, and v_cvt_scalef32_pk32_f32_fp6 (w, s) gives
+// field j's value times s (a probe on the GPU matched these to a software
+// rounding bit for bit, ties and the subnormal e2m3 values included); so the
+// even k go to x, the odd k to y, and the decoded digit is subtracted
+// exactly.
 // Output per (m32, kg, st, d), at aq + (((m32 * c4n + kg) * 2 + st) * 3 + d)
 // * 1536: dwords 0-3 of lane l at byte 16 l, dwords 4-5 at 1024 + 8 l;
 // asc[(m32 * c4n + kg) * 2 + st][l] = the three E8M0 scale bytes of lane l's
 // block (digit d in byte d), nf[(row * c4n + kg) * 4 + 2 st + h] = 1 when
 // the block held a non-finite value.  Rows >= M and k >= K are zeros.
-// Workgroup = one (m32, kg, st); thread = 8 consecutive k of one row, t = 8 r
-// + s with s = 4 h + e (k = 128 kg + 64 st + 8 s: fields 8 e .. + 7 of lane
-// r + 32 h, bits 48 e .. + 47 of its six dwords).  The four quarters of a
-// block meet by shuffles (max, and the 48-bit pieces: quarter 0 writes dwords
-// 0-3, quarter 1 dwords 4-5).  With rsum (float zero points), also the
-// sum of the row's finite values over the step, rsum[(row * c4n + kg) * 2 +
-// st], added in a fixed order (shuffles over the 8 threads of the row).
-__global__ __launch_bounds__(256) void k_af6x3(const float *__restrict__ a, int64_t M,
-                                               int64_t K, int c4n, int vec,
-                                               uint8_t *__restrict__ aq,
-                                               uint32_t *__restrict__ asc,
-                                               uint8_t *__restrict__ nf,
-                                               float *__restrict__ rsum) {
-  const int t = threadIdx.x;
+// Workgroup = one wave for one (m32, kg, st); lane = the MFMA lane.
+// With rsum (float zero points), also the sum over the step's 64 k of the
+// values the three digits represent (input minus final residual), added in a
+// fixed order, rsum[(row * c4n + kg) * 2 + st]: the GEMM subtracts z times
+// it, so the zero point meets the same activations as the weights do.
+__global__ __launch_bounds__(64) void k_af6x3(const float *__restrict__ a, int64_t M, int64_t K,
+                                              int c4n, int vec, uint8_t *__restrict__ aq,
+                                              uint32_t *__restrict__ asc,
+                                              uint8_t *__restrict__ nf,
+                                              float *__restrict__ rsum) {
+  const int lane = threadIdx.x;
+  const int r = lane & 31, h = lane >> 5;
   const int64_t bid = blockIdx.x;  // (m32 * c4n + kg) * 2 + st
   const int st = (int)(bid & 1);
-  const int64_t mk = bid >> 1;
+  const int64_t mk = bid >> 1;     // m32 * c4n + kg
   const int kg = (int)(mk % c4n);
   const int64_t m32 = mk / c4n;
-  const int r = t >> 3, sg = t & 7;
-  const int h = sg >> 2, e = sg & 3;
   const int64_t row = m32 * 32 + r;
   const bool live = row < M;
   const float *arow = a + (live ? row : 0) * K;
-  const int64_t k0 = (int64_t)kg * KGRP + 64 * st + 8 * sg;
-  float v[8];
-  if (live && vec && k0 + 8 <= K) {
-    const float4 x0 = *reinterpret_cast<const float4 *>(arow + k0);
-    const float4 x1 = *reinterpret_cast<const float4 *>(arow + k0 + 4);
-    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+  const int64_t k0 = (int64_t)kg * KGRP + 64 * st + 32 * h;
+  float v[32];
+  if (live && vec && k0 + 32 <= K) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const float4 x = *reinterpret_cast<const float4 *>(arow + k0 + 4 * q);
+      v[4 * q] = x.x, v[4 * q + 1] = x.y, v[4 * q + 2] = x.z, v[4 * q + 3] = x.w;
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = (live && k0 + i < K) ? arow[k0 + i] : 0.f;
+    for (int i = 0; i < 32; i++) v[i] = (live && k0 + i < K) ? arow[k0 + i] : 0.f;
   }
   int bad = 0;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < 32; i++) {
     if (!isfinite(v[i])) {
       bad = 1;
       v[i] = 0.f;
     }
   }
-  bad |= __shfl_xor(bad, 1);
-  bad |= __shfl_xor(bad, 2);
+  float v0[32];
   if (rsum) {
-    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-    sum += __shfl_xor(sum, 1);
-    sum += __shfl_xor(sum, 2);
-    sum += __shfl_xor(sum, 4);
-    if (sg == 0) rsum[(row * c4n + kg) * 2 + st] = sum;
+#pragma unroll
+    for (int i = 0; i < 32; i++) v0[i] = v[i];
   }
-  const int lane = r + 32 * h;
   uint8_t *base = aq + bid * 3 * 1536;
   uint32_t scales = 0;
 #pragma unroll
   for (int d = 0; d < 3; d++) {
     float mx = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[i]));
-    mx = fmaxf(mx, __shfl_xor(mx, 1));
-    mx = fmaxf(mx, __shfl_xor(mx, 2));
+    for (int i = 0; i < 32; i++) mx = fmaxf(mx, fabsf(v[i]));
     int E = 0;
     if (mx > 0.f) {
       int ex;
       frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
-      E = max(ex - 2, -127);
+      E = max(ex - 2, -126);
     }
-    uint32_t lo = 0, hi = 0;  // this quarter's 48 bits
+    const float sc = __uint_as_float((uint32_t)(E + 127) << 23);  // 2^E
+    float16v xe, xo;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float y = ldexpf(v[i], -E);  // exact
-      float val;
-      const uint32_t c = e2m3_rne(y, &val);
-      v[i] = ldexpf(y - val, E);  // exact, no overflow
-      const int bit = 6 * i;
-      if (bit < 32) lo |= c << bit;
-      if (bit > 26) hi |= bit >= 32 ? c << (bit - 32) : c >> (32 - bit);
-    }
-    const uint32_t x1 = __shfl_xor(lo, 1), y1 = __shfl_xor(hi, 1);
-    const uint32_t x2 = __shfl_xor(lo, 2), y2 = __shfl_xor(hi, 2);
-    const uint32_t y3 = __shfl_xor(hi, 3);
-    if (e == 0)
-      *reinterpret_cast<uint4 *>(base + d * 1536 + 16 * lane) =
-          make_uint4(lo, hi | (x1 << 16), (x1 >> 16) | (y1 << 16), x2);
-    else if (e == 1)  // quarter 2 is lane xor 3 here, quarter 3 lane xor 2
-      *reinterpret_cast<uint2 *>(base + d * 1536 + 1024 + 8 * lane) =
-          make_uint2(y3 | (x2 << 16), (x2 >> 16) | (y2 << 16));
+    for (int j = 0; j < 16; j++) xe[j] = v[2 * j], xo[j] = v[2 * j + 1];
+    const uint6v w = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(xe, xo, sc);
+    const float32v dv = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(w, sc);
+#pragma unroll
+    for (int i = 0; i < 32; i++) v[i] -= dv[i];  // exact
+    *reinterpret_cast<uint4 *>(base + d * 1536 + 16 * lane) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint2 *>(base + d * 1536 + 1024 + 8 * lane) = make_uint2(w[4], w[5]);
     scales |= (uint32_t)(E + 127) << (8 * d);
   }
-  if (e == 0) {
-    asc[bid * 64 + lane] = scales;
-    nf[(row * c4n + kg) * 4 + 2 * st + h] = (uint8_t)bad;
+  asc[bid * 64 + lane] = scales;
+  nf[(row * c4n + kg) * 4 + 2 * st + h] = (uint8_t)bad;
+  if (rsum) {
+    float p[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+      p[q] = ((v0[4 * q] - v[4 * q]) + (v0[4 * q + 1] - v[4 * q + 1])) +
+             ((v0[4 * q + 2] - v[4 * q + 2]) + (v0[4 * q + 3] - v[4 * q + 3]));
+    float sum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    sum += __shfl_xor(sum, 32);
+    if (h == 0) rsum[(row * c4n + kg) * 2 + st] = sum;
   }
 }
 
@@ -1059,7 +1044,7 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
   if (fzp && !f6)  // the planner sends float zero points here only with images
     return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: float zero points without prefill images");
   if (f6)
-    hipLaunchKernelGGL(k_af6x3, dim3((unsigned)((mpad / 32) * d.c4 * 2)), dim3(256), 0, st, a_dev, M,
+    hipLaunchKernelGGL(k_af6x3, dim3((unsigned)((mpad / 32) * d.c4 * 2)), dim3(64), 0, st, a_dev, M,
                        w0->K, (int)d.c4, vec, reinterpret_cast<uint8_t *>(aq), asc, nf,
                        fzp ? rsum : nullptr);
   else
