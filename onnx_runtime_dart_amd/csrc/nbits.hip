@@ -1394,7 +1394,7 @@ size_t mg_nbits_f8_ws(int64_t mpad, int64_t c4, size_t *off_asc, size_t *off_nf,
                       size_t *off_rs);
 mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, const float *a_dev,
                               int64_t M, float *const *y_dev, void *ws, int64_t mpad, int nt,
-                              int ksplit, int kps, size_t off_part);
+                              int ksplit, int kps, size_t off_part, int kwave);
 
 namespace {
 
@@ -1412,6 +1412,7 @@ struct NbitsPlan {
   int pers_grid = 0;  // its workgroups
   int cs = 0;         // GEMV on the column-slice kernel (k_gemv_cs)
   int cs_pf = 4;      // its k groups in flight per wave
+  int kwave = 0;      // fp6 prefill on k_gemm_f6kw (32 x 64 tiles, waves split K)
   size_t off_a = 0, off_b = 0, off_c = 0, off_d = 0, total = 0;
 };
 
@@ -1538,6 +1539,20 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
     const int64_t tiles = mt * (p.nt == 4 ? ng_total / 2 : ng_total);
     int64_t ks = 1;
     while (tiles * ks * 2 <= target && d.c4 / (ks * 2) >= MG_PREFILL_MIN_KG) ks *= 2;
+#ifndef MG_PREFILL_KWAVE
+#define MG_PREFILL_KWAVE 1
+#endif
+    // Where even 128 x 64 tiles leave the chip short and K would be split
+    // over workgroups (fp6 images, integer zero points): 32 x 64 tiles whose
+    // four waves split K instead (k_gemm_f6kw), with the partial sums added
+    // in the same launch.  Qwen3 o / down at M = 512: 10.0 + 5.2 -> 11.4 us
+    // and 12.2 + 5.1 -> 14.9 us.  Where the grid is already full without a
+    // split it is slower (three rounds of small workgroups, each paying the
+    // load latency: q/k/v 13.8 -> 17.4 us), so it is not used there.
+    if (MG_PREFILL_KWAVE && p.path == 4 && p.nt == 2 && ks > 1 && imgs && int_zp) {
+      p.kwave = 1;
+      ks = 1;
+    }
     p.kps = (int)((d.c4 + ks - 1) / ks);
     p.ksplit = (int)((d.c4 + p.kps - 1) / p.kps);
     if (p.path == 4) {
@@ -2025,7 +2040,7 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
   if (p.path == 1) return prefill_run(ctx, n, w, a_dev, M, y_dev, ws, p);
   if (p.path == 4)
     return mg_nbits_prefill_f8(ctx, n, w, a_dev, M, y_dev, ws, p.mpad, p.nt, p.ksplit, p.kps,
-                               p.off_c);
+                               p.off_c, p.kwave);
   // Float zero points / 16-k blocks: one weight at a time.
   for (int i = 0; i < n; i++)
     MG_TRY(nbits_run_f32(ctx, w[i], a_dev, M, y_dev[i], static_cast<float *>(ws), p.chunk));

@@ -1006,6 +1006,210 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
                        zpf, nb, nbh, lbs, zpk, N, bias, part, ks);
 }
 
+// The fp6 prefill GEMM for small launches (weights with prefill images,
+// integer zero points, too few 128 x 128 tiles to fill the chip): a
+// workgroup takes 32 rows x 64 columns (one column group), and its four
+// waves take a quarter of the k groups each.  A wave streams its activation
+// digits and image fragments straight into registers, reloading each slot
+// for the next k group right after its last use (the vector-memory queue
+// then always holds one k group ahead), and applies the block scale per k
+// group (acc += s D).  No LDS holds operands and no barrier separates the
+// k groups, so the serial chain of a workgroup is a quarter of K; the four
+// partial tiles meet in LDS and are added in wave order (deterministic),
+// with no split-K launch.  Rows with a non-finite activation get the
+// reference's Inf / NaN pattern as in prefill_epilogue.
+__global__ __launch_bounds__(256, 2) void k_gemm_f6kw(
+    const uint8_t *__restrict__ aq, const uint32_t *__restrict__ asc,
+    const uint8_t *__restrict__ nf, const float *__restrict__ a, int64_t K,
+    const PrefillSet ps, int M, int c4n, int nb, int nbh, int lbs, int zpk, int mt32,
+    int ntiles) {
+  __shared__ __align__(16) float part[4][32 * 64];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int L = blockIdx.x;
+  const int xcd = L & 7, q = L >> 3;
+  const int mt = q % mt32;  // 32-row tile
+  const int ntg = (q / mt32) * 8 + xcd;
+  if (ntg >= ntiles) return;
+  int cg;
+  const int mem = prefill_member(ps, ntg, &cg);  // column group of the member
+  const int N = ps.N[mem];
+  const int lc = lane & 31;
+  auto rsrc = [](const void *base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7ffffff0,
+                                             0x00020000);
+  };
+  const __amdgpu_buffer_rsrc_t r_a = rsrc(aq + (int64_t)mt * c4n * 9216);
+  const __amdgpu_buffer_rsrc_t r_s = rsrc(asc + (int64_t)mt * c4n * 128);
+  const __amdgpu_buffer_rsrc_t r_b =
+      rsrc(reinterpret_cast<const uint8_t *>(ps.img[mem]) + (int64_t)2 * cg * c4n * 3072);
+  const __amdgpu_buffer_rsrc_t r_c = rsrc(ps.scales[mem] + (int64_t)cg * nb * 64);
+  const unsigned vo16 = 16u * lane, vo8 = 1024u + 8u * lane, vo4 = 4u * lane;
+  const unsigned vo_c0 = 4u * (unsigned)sz_pos(lc), vo_c1 = 4u * (unsigned)sz_pos(32 + lc);
+  auto frag = [&](const __amdgpu_buffer_rsrc_t &r, int off) __attribute__((always_inline)) {
+    const uint4 x0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo16, off, 0));
+    const uint2 x1 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, vo8, off, 0));
+    return (int8v){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, 0, 0};
+  };
+  auto a_load = [&](int kg, int st, int d) __attribute__((always_inline)) {
+    return frag(r_a, ((kg * 2 + st) * 3 + d) * 1536);
+  };
+  auto b_load = [&](int kg, int st, int n) __attribute__((always_inline)) {
+    return frag(r_b, (n * c4n + kg) * 3072 + st * 1536);
+  };
+  auto s_load = [&](int kg, int st) __attribute__((always_inline)) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r_s, vo4, (kg * 2 + st) * 256, 0);
+  };
+  auto c_load = [&](int kg, unsigned vo) __attribute__((always_inline)) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r_c, vo, ((kg * KGRP) >> lbs) * 256, 0));
+  };
+
+  float16v acc[2], D[2];
+#pragma unroll
+  for (int n = 0; n < 2; n++) acc[n] = (float16v){}, D[n] = (float16v){};
+  const int kpw = (c4n + 3) >> 2;
+  const int kb = min(c4n, wave * kpw), ke = min(c4n, kb + kpw);
+  if (kb < ke) {
+    int8v A[2][3], B[2][2];
+    uint32_t sa[2];
+    float sc[2];
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+#pragma unroll
+      for (int d = 0; d < 3; d++) A[st][d] = a_load(kb, st, d);
+      B[st][0] = b_load(kb, st, 0);
+      B[st][1] = b_load(kb, st, 1);
+      sa[st] = s_load(kb, st);
+    }
+    sc[0] = c_load(kb, vo_c0);
+    sc[1] = c_load(kb, vo_c1);
+    const float16v zero16 = (float16v){};
+    for (int kg = kb; kg < ke; kg++) {
+      const bool more = kg + 1 < ke;  // wave-uniform
+      const int kn = kg + 1;
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+#pragma unroll
+        for (int d = 0; d < 3; d++) {
+#pragma unroll
+          for (int n = 0; n < 2; n++) {
+            const float16v cin = (st == 0 && d == 0) ? zero16 : D[n];
+            D[n] = d == 0   ? mfma6_digit<0>(A[st][0], B[st][n], cin, (int)sa[st])
+                   : d == 1 ? mfma6_digit<1>(A[st][1], B[st][n], cin, (int)sa[st])
+                            : mfma6_digit<2>(A[st][2], B[st][n], cin, (int)sa[st]);
+          }
+          if (more) A[st][d] = a_load(kn, st, d);
+        }
+        if (more) {
+          B[st][0] = b_load(kn, st, 0);
+          B[st][1] = b_load(kn, st, 1);
+          sa[st] = s_load(kn, st);
+        }
+      }
+      const float s0 = sc[0], s1 = sc[1];
+      if (more) {
+        sc[0] = c_load(kn, vo_c0);
+        sc[1] = c_load(kn, vo_c1);
+      }
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        acc[0][v] = fmaf(s0, D[0][v], acc[0][v]);
+        acc[1][v] = fmaf(s1, D[1][v], acc[1][v]);
+      }
+    }
+  }
+  // The four partial tiles, row-major, then their sum in wave order.
+  {
+    float *pw = part[wave];
+    const int lh = lane >> 5;
+#pragma unroll
+    for (int n = 0; n < 2; n++)
+#pragma unroll
+      for (int v = 0; v < 16; v++)
+        pw[(8 * (v >> 2) + 4 * lh + (v & 3)) * 64 + n * 32 + lc] = acc[n][v];
+  }
+  __syncthreads();
+  const int r = t >> 3, c0 = 8 * (t & 7);
+  float4v y0 = *reinterpret_cast<const float4v *>(&part[0][r * 64 + c0]);
+  float4v y1 = *reinterpret_cast<const float4v *>(&part[0][r * 64 + c0 + 4]);
+#pragma unroll
+  for (int w = 1; w < 4; w++) {
+    y0 += *reinterpret_cast<const float4v *>(&part[w][r * 64 + c0]);
+    y1 += *reinterpret_cast<const float4v *>(&part[w][r * 64 + c0 + 4]);
+  }
+  // Rows of the tile with a non-finite activation (rare; every wave computes
+  // the same mask, so the branch is uniform over the workgroup).
+  int flag = 0;
+  if (lane < 32 && mt * 32 + lane < M) {
+    const uint32_t *nfw = reinterpret_cast<const uint32_t *>(nf) + (int64_t)(mt * 32 + lane) * c4n;
+    for (int kq = 0; kq < c4n; kq += 8) {
+      uint32_t fw[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) fw[j] = nfw[min(kq + j, c4n - 1)];
+#pragma unroll
+      for (int j = 0; j < 8; j++) flag |= fw[j] != 0u;
+    }
+  }
+  uint64_t rows = __ballot(flag);
+  if (rows) {
+    *reinterpret_cast<float4v *>(&part[0][r * 64 + c0]) = y0;
+    *reinterpret_cast<float4v *>(&part[0][r * 64 + c0 + 4]) = y1;
+    __syncthreads();
+    if (wave == 0) {
+      const int col = cg * 64 + lane;
+      while (rows) {
+        const int rr = __builtin_ctzll(rows);
+        rows &= rows - 1;
+        const float *arow = a + (int64_t)(mt * 32 + rr) * K;
+        bool fnan = false, fpos = false, fneg = false;
+        for (int64_t k0 = 0; k0 < K; k0 += 64) {
+          const float x = k0 + lane < K ? arow[k0 + lane] : 0.f;
+          uint64_t m = __ballot(!isfinite(x));
+          while (m) {
+            const int bi = __builtin_ctzll(m);
+            m &= m - 1;
+            const float xv = __shfl(x, bi);
+            if (col >= N) continue;
+            const float wv = nbits_weight(ps.wq[mem], ps.scales[mem], ps.zp4[mem], ps.zpf[mem],
+                                          c4n, nb, nbh, lbs, zpk, col, (int)(k0 + bi));
+            if (isnan(xv) || !(wv != 0.f)) fnan = true;
+            else if ((xv > 0.f) == (wv > 0.f)) fpos = true;
+            else fneg = true;
+          }
+        }
+        if (fnan || fpos || fneg)
+          part[0][rr * 64 + lane] = (fnan || (fpos && fneg)) ? __builtin_nanf("")
+                                    : fpos ? INFINITY : -INFINITY;
+      }
+    }
+    __syncthreads();
+    y0 = *reinterpret_cast<const float4v *>(&part[0][r * 64 + c0]);
+    y1 = *reinterpret_cast<const float4v *>(&part[0][r * 64 + c0 + 4]);
+  }
+  const int row = mt * 32 + r;
+  if (row >= M) return;
+  const int col = cg * 64 + c0;
+  const float *__restrict__ bias = ps.bias[mem];
+  float yv[8] = {y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+  if (bias) {
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (col + j < N) yv[j] += bias[col + j];
+  }
+  float *p = ps.y[mem] + (int64_t)row * N + col;
+  if (ps.y_vec[mem] && (N % 4) == 0 && col + 7 < N) {
+    __builtin_nontemporal_store((float4v){yv[0], yv[1], yv[2], yv[3]},
+                                reinterpret_cast<float4v *>(p));
+    __builtin_nontemporal_store((float4v){yv[4], yv[5], yv[6], yv[7]},
+                                reinterpret_cast<float4v *>(p + 4));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (col + j < N) p[j] = yv[j];
+  }
+}
+
 }  // namespace
 
 size_t mg_nbits_f8_ws(int64_t mpad, int64_t c4, size_t *off_asc, size_t *off_nf,
@@ -1019,7 +1223,7 @@ size_t mg_nbits_f8_ws(int64_t mpad, int64_t c4, size_t *off_asc, size_t *off_nf,
 
 mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, const float *a_dev,
                               int64_t M, float *const *y_dev, void *ws, int64_t mpad, int nt,
-                              int ksplit, int kps, size_t off_part) {
+                              int ksplit, int kps, size_t off_part, int kwave) {
   const mg_weight *w0 = w[0];
   const mg_nbits_dev &d = w0->nbits;
   hipStream_t st = ctx->stream;
@@ -1051,6 +1255,16 @@ mg_status mg_nbits_prefill_f8(mg_ctx *ctx, int n, const mg_weight *const *w, con
     hipLaunchKernelGGL(k_af8x3, dim3((unsigned)((mpad / 32) * d.c4 * 2)), dim3(256), 0, st, a_dev,
                        M, w0->K, (int)d.c4, vec, aq, asc, nf);
   MG_TRY(mg_launch_check(f6 ? "k_af6x3" : "k_af8x3"));
+  if (kwave) {  // the planner sends only fp6, integer-zero-point, 64-column plans here
+    if (!f6 || fzp || nt != 2 || ksplit != 1)
+      return mg_fail(MG_DEVICE_ERROR, "MatMulNBits: invalid wave-split prefill plan");
+    const int mt32 = (int)((M + 31) / 32);
+    hipLaunchKernelGGL(k_gemm_f6kw, dim3((unsigned)(8 * mt32 * ((ct + 7) / 8))), dim3(256), 0,
+                       st, reinterpret_cast<const uint8_t *>(aq), asc, nf, a_dev, w0->K, ps,
+                       (int)M, (int)d.c4, (int)d.nb, (int)d.nbh, __builtin_ctzll(d.bs),
+                       (int)d.zp_kind, mt32, ct);
+    return mg_launch_check("k_gemm_f6kw");
+  }
   // (256-row workgroups of 8 waves, k_gemm_f8x3<4, 8>, dequantise each
   // weight tile once for twice the rows; measured 2-4% slower on the lm_head
   // at M = 512, so 128-row tiles are used.)

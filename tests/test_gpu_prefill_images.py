@@ -52,6 +52,10 @@ CASES = [
     (64, 4096, 300, 128, "packed", True),         # 64-column tiles, K split
     (17, 200, 70, 128, "packed", True),           # K not a multiple of 128
     (300, 1024, 4096, 512, "none", True),
+    # Few tiles: 32 x 64 tiles whose waves split K (k_gemm_f6kw): five k
+    # groups over four waves, and blocks of 256 (two k groups per scale).
+    (40, 640, 200, 128, "packed", True),
+    (33, 1000, 130, 256, "none", True),
 ]
 
 
@@ -173,8 +177,9 @@ def test_headline_grouped_launches(ops, members):
     # rows of all four 128-row tiles (the first and last row of each, and
     # random ones).  gate and up alone take the same plan as their group, so
     # there the group must equal the single calls bitwise; q, k and v alone
-    # split K (fewer tiles), which reorders the fp32 sum, so there the single
-    # calls are held to the same bar against the oracle.
+    # have too few tiles for that plan and split K over the waves of smaller
+    # tiles, which reorders the fp32 sum, so there the single calls are held
+    # to the same bar against the oracle.
     widths = {"q": 2048, "k": 1024, "v": 1024, "gate": 3072, "up": 3072}
     rng = np.random.default_rng(0x5EED0094 + len(members))
     m, k, bs = 512, 1024, 128
