@@ -224,13 +224,14 @@ def main():
                     help="headline and lm_head measurements only")
     ap.add_argument("--only", default=None,
                     choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1", "llama16",
-                             "attn", "conv", "pass512"],
+                             "attn", "conv", "pass512", "dec1", "dec4", "dec16"],
                     help="profiling mode: launch one workload --steps times and exit "
                          "(lm512 / lm1: Qwen3 lm_head MatMulNBits at M=512 / M=1; i8lm512: "
                          "the lm_head as MatMulInteger at M=512; f32ffn: the MiniLM FFN1 "
                          "Gemm; llama1 / llama16: the Llama lm_head at M=1 / M=16; attn: the MiniLM "
                          "fused attention; conv: the ResNet-50 3x3 conv; pass512: the headline "
-                         "M=512 pass of eight Qwen3 projections, grouped as timed; copy: 256 MiB "
+                         "M=512 pass of eight Qwen3 projections, grouped as timed; dec1 / dec4 / "
+                         "dec16: the grouped Llama-style decode step at M=1 / 4 / 16; copy: 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -934,6 +935,31 @@ def run_only(args, torch, ops, ctx, stream, dev, randn):
                     ops.matmul_nbits_group_dev([ws[i] for i in grp], acts[k].data_ptr(),
                                                M_PREFILL, [outs[i].data_ptr() for i in grp],
                                                ctx=ctx)
+            torch.cuda.synchronize()
+            for x in ws:
+                x.release()
+            w = None
+        elif args.only in ("dec1", "dec4", "dec16"):
+            m = int(args.only[3:])
+            shapes = [x for _ in range(LLAMA_LAYERS) for x in LLAMA_LAYER] + [LLAMA_HEAD]
+            ws = [ops.NBitsWeight(*make_weight(rng, k, n, LLAMA_BLOCK, 0.005, 0.02), k=k, n=n,
+                                  block_size=LLAMA_BLOCK, ctx=ctx) for _, k, n in shapes]
+            a = {k: randn(m, k) for k in {k for _, k, _ in shapes}}
+            y = {n: torch.empty((m, n), device=dev, dtype=torch.float32)
+                 for n in {n for _, _, n in shapes}}
+            nl = len(LLAMA_LAYER)
+            for _ in range(args.steps):
+                for li in range(LLAMA_LAYERS):
+                    lw = ws[li * nl:(li + 1) * nl]
+                    ops.matmul_nbits_group_dev(lw[0:3], a[2048].data_ptr(), m,
+                                               [y[2048].data_ptr(), y[512].data_ptr(),
+                                                y[512].data_ptr()], ctx=ctx)
+                    lw[3].run_dev(a[2048].data_ptr(), m, y[2048].data_ptr())
+                    ops.matmul_nbits_group_dev(lw[4:6], a[2048].data_ptr(), m,
+                                               [y[8192].data_ptr(), y[8192].data_ptr()],
+                                               ctx=ctx)
+                    lw[6].run_dev(a[8192].data_ptr(), m, y[2048].data_ptr())
+                ws[-1].run_dev(a[LLAMA_HEAD[1]].data_ptr(), m, y[LLAMA_HEAD[2]].data_ptr())
             torch.cuda.synchronize()
             for x in ws:
                 x.release()

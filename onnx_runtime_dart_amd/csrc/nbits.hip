@@ -1158,10 +1158,16 @@ __global__ __launch_bounds__(256) void k_af16split16(const float *__restrict__ a
 // group are loaded while the current one is computed.
 // TPW = 16-column tiles per workgroup (4: the whole column group; 2 or 1
 // give narrow weights 2 or 4 workgroups per column group, tiles t0 ..).
-template <int SEGJ, int NW, int TPW>
+#ifndef MG_DEC_PD
+#define MG_DEC_PD 2
+#endif
+// Split K (gridDim.y > 1, part not null): the workgroup takes k groups
+// [kps * y, + kps) and writes its sum, the row exponent taken off, to the
+// partials; k_gemm_reduce adds the splits in order with the bias.
+template <int SEGJ, int NW, int TPW, int PD = MG_DEC_PD>
 __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
     const uint4 *__restrict__ ahl, const int *__restrict__ texp, const GemvSet gs, int M,
-    int c4n, int nb, int nbh, int lbs, int has_zp) {
+    int c4n, int nb, int nbh, int lbs, int has_zp, int kps, float *__restrict__ part) {
   __shared__ float4 red[NW][TPW][64];  // [wave][tile][lane]
   constexpr int NBK = 4 / SEGJ;       // blocks (scale segments) per k group
   constexpr int WPG = 4 / TPW;        // workgroups per column group
@@ -1192,7 +1198,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   // (sz_pos): one 16-byte and one 4-byte load per block.
   const __amdgpu_buffer_rsrc_t r_s = rsrc(scales + (int64_t)cg * nb * 64, nb * 256);
   const __amdgpu_buffer_rsrc_t r_z = rsrc(zp4 + (int64_t)cg * nbh * 64, 0x7ffffff0);
-  const unsigned vo_w = 16u * (unsigned)(g * 64 + c16), vo_a = 16u * (unsigned)lane;
+  // Lanes of activation rows >= M load nothing (an offset past the
+  // resource reads as zero without a memory access): at M = 4 that is three
+  // quarters of the activation traffic.
+  const unsigned vo_w = 16u * (unsigned)(g * 64 + c16);
+  const unsigned vo_a = c16 < M ? 16u * (unsigned)lane : 0x7ffffff0u;
   const unsigned vo_s = 16u * (unsigned)c16, vo_z = 4u * (unsigned)c16;
 
   // Raw loads of one k group; they are first touched in compute(), so the
@@ -1293,20 +1303,25 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
     }
   };
 
-  // Two-slot ring over this wave's k groups (unrolled by two so slots are
-  // static).
-  // Wave w takes k groups w, w + NW, ... with the next one's loads in flight.
-  Ring ra, rb;
-  int kg = wave;
-  if (kg < c4n) fetch(kg, ra);
-  for (; kg < c4n; kg += 2 * NW) {
-    if (kg + NW < c4n) fetch(kg + NW, rb);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(kg, ra);
-    if (kg + NW >= c4n) break;
-    if (kg + 2 * NW < c4n) fetch(kg + 2 * NW, ra);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(kg + NW, rb);
+  // PD-slot ring over this wave's k groups (unrolled by PD so slots are
+  // static registers).  Wave w takes k groups w, w + NW, ... with the loads
+  // of the next PD - 1 in flight: one k group of work is far shorter than
+  // a load's latency, so a wave with several k groups needs them in flight.
+  const int kbeg = part ? (int)blockIdx.y * kps : 0;
+  const int kend = part ? min(c4n, kbeg + kps) : c4n;
+  Ring R[PD];
+#pragma unroll
+  for (int j = 0; j < PD - 1; j++)
+    if (kbeg + wave + j * NW < kend) fetch(kbeg + wave + j * NW, R[j]);
+  for (int kb = kbeg + wave; kb < kend; kb += PD * NW) {
+#pragma unroll
+    for (int j = 0; j < PD; j++) {
+      const int kg = kb + j * NW;
+      if (kg >= kend) break;
+      if (kg + (PD - 1) * NW < kend) fetch(kg + (PD - 1) * NW, R[(j + PD - 1) % PD]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(kg, R[j]);
+    }
   }
 
 #pragma unroll
@@ -1323,12 +1338,17 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
         s.x += o.x; s.y += o.y; s.z += o.z; s.w += o.w;
       }
       const int col = cg * 64 + (t0 + tl) * 16 + c16;
-      const float bv = (bias && col < N) ? bias[col] : 0.f;
+      const float bv = (bias && col < N && !part) ? bias[col] : 0.f;
       const float sv[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int row = 4 * g + i;
-        if (row < M && col < N) y[(int64_t)row * N + col] = ldexpf(sv[i], -texp[row]) + bv;
+        if (row >= M || col >= N) continue;
+        if (part)
+          part[gs.part_off[gm] + ((int64_t)blockIdx.y * M + row) * N + col] =
+              ldexpf(sv[i], -texp[row]);
+        else
+          y[(int64_t)row * N + col] = ldexpf(sv[i], -texp[row]) + bv;
       }
     }
   }
@@ -1431,7 +1451,26 @@ NbitsPlan plan_nbits(const mg_ctx *ctx, const mg_weight *w, int64_t M, int64_t n
     p.path = 3;
     p.off_a = 0;  // ahl16: 16 rows x kpad x (hi, lo) fp16
     p.off_b = mg_align((size_t)16 * d.kpad * 4);  // texp[16]
-    p.total = mg_align(p.off_b + 16 * 4);
+    p.off_c = mg_align(p.off_b + 16 * 4);          // split-K partials
+#ifndef MG_DEC_SPLIT
+#define MG_DEC_SPLIT 1
+#endif
+    // Narrow weights (fewer column groups than CUs) with long rows: whole
+    // column groups per workgroup with K split over workgroups (at least 8
+    // k groups each), summed by k_gemm_reduce.  Each workgroup reads the
+    // 16-row activation block of its k range only, where 16-column slices
+    // over all of K read it whole per slice (Llama down 8192 x 2048: 64 MB
+    // of activation reads for 8.4 MB of weights).
+    const int64_t cus = std::max(ctx->num_cus, 1);
+    if (MG_DEC_SPLIT && ng_total < cus && d.c4 >= 32) {
+      int64_t ks = 1;
+      while (ng_total * ks * 2 <= 2 * cus && d.c4 / (ks * 2) >= 8) ks *= 2;
+      if (ks > 1) {
+        p.kps = (int)((d.c4 + ks - 1) / ks);
+        p.ksplit = (int)((d.c4 + p.kps - 1) / p.kps);
+      }
+    }
+    p.total = mg_align(p.off_c + (p.ksplit > 1 ? (size_t)p.ksplit * M * n_total * 4 : 0));
   } else if (M <= 4 && d.bs <= 4096) {
     p.path = 0;
     p.qb = (int)std::min<int64_t>(d.bs, KGRP);
@@ -1980,7 +2019,23 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
     return MG_OK;
   }
   if (p.path == 3) {
-    const GemvSet gs = make_set(n, w, y_dev);
+    GemvSet gs = make_set(n, w, y_dev);
+    float *part = p.ksplit > 1 ? reinterpret_cast<float *>(base + p.off_c) : nullptr;
+    ReduceSet rs{};
+    int64_t eend = 0;
+    if (p.ksplit > 1) {
+      rs.n = n;
+      int64_t poff = 0;
+      for (int i = 0; i < n; i++) {
+        gs.part_off[i] = rs.part_off[i] = poff;
+        poff += (int64_t)p.ksplit * M * w[i]->N;
+        eend += M * w[i]->N;
+        rs.e_end[i] = eend;
+        rs.bias[i] = w[i]->nbits.bias;
+        rs.y[i] = y_dev[i];
+        rs.N[i] = (int)w[i]->N;
+      }
+    }
     uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
     int *texp = reinterpret_cast<int *>(base + p.off_b);
     const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
@@ -2012,15 +2067,16 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
 #define MG_GEMV16_WG_PER_CU 1
 #endif
     const int64_t cus = std::max(ctx->num_cus, 1) * (int64_t)MG_GEMV16_WG_PER_CU;
-    const int tpw = ng >= cus ? 4 : (2 * ng >= cus ? 2 : 1);
+    const bool split = p.ksplit > 1;
+    const int tpw = split || ng >= cus ? 4 : (2 * ng >= cus ? 2 : 1);
     const int64_t wgs = ng * (4 / tpw);
     int nw = 4;
-    if (wgs < 2 * cus && d.c4 >= 8) nw = 8;
-    if (wgs >= 4 * cus && tpw == 4) nw = 1;
+    if (split ? p.kps >= 8 : (wgs < 2 * cus && d.c4 >= 8)) nw = 8;
+    if (!split && wgs >= 4 * cus && tpw == 4) nw = 1;
 #define MG_DEC_LAUNCH(SJ_, NW_, TPW_)                                                      \
-  hipLaunchKernelGGL((k_gemv_mfma<SJ_, NW_, TPW_>), dim3((unsigned)wgs), dim3(NW_ * 64), 0, \
-                     st, ahl, texp, gs, (int)M, (int)d.c4, (int)d.nb, (int)d.nbh,           \
-                     __builtin_ctzll(d.bs), has_zp)
+  hipLaunchKernelGGL((k_gemv_mfma<SJ_, NW_, TPW_>), dim3((unsigned)wgs, (unsigned)p.ksplit), \
+                     dim3(NW_ * 64), 0, st, ahl, texp, gs, (int)M, (int)d.c4, (int)d.nb,    \
+                     (int)d.nbh, __builtin_ctzll(d.bs), has_zp, p.kps, part)
 #define MG_DEC_TPW(SJ_, NW_)                  \
   if (tpw == 4) MG_DEC_LAUNCH(SJ_, NW_, 4);  \
   else if (tpw == 2) MG_DEC_LAUNCH(SJ_, NW_, 2); \
@@ -2035,7 +2091,9 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
 #undef MG_DEC_NW
 #undef MG_DEC_TPW
 #undef MG_DEC_LAUNCH
-    return mg_launch_check("k_gemv_mfma");
+    MG_TRY(mg_launch_check("k_gemv_mfma"));
+    if (split) return launch_gemm_reduce(st, part, rs, eend, p.ksplit);
+    return MG_OK;
   }
   if (p.path == 1) return prefill_run(ctx, n, w, a_dev, M, y_dev, ws, p);
   if (p.path == 4)
