@@ -400,13 +400,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 //   * accumulates O, lane = output dim (DL dims per lane), reading V rows
 //     and p from LDS.
 // It writes y, or with several key splits the partials k_attn_combine merges.
+// DMAX: the largest head size (Q/K and V) the LDS tiles hold, 128 or 256
+// (Gemma-style heads; 150 KB of LDS, one workgroup per CU).
 constexpr int DEC_S = 16;
-template <int DL>
+template <int DL, int DMAX>
 __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
-  constexpr int KB = 64, KP = 129;  // keys per block, K row pitch
-  __shared__ float qs[DEC_S * 128];
+  constexpr int KB = 64, KP = DMAX + 1;  // keys per block, K row pitch
+  __shared__ float qs[DEC_S * DMAX];
   __shared__ float ks[KB * KP];
-  __shared__ float vs[KB * 128];
+  __shared__ float vs[KB * DMAX];
   __shared__ float pls[DEC_S * KB];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -430,7 +432,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
   const int t_end = p.kc > 0 ? min(p.T, t_begin + p.kc) : p.T;
   for (int e = tid; e < S * D; e += 256) {
     const int q = e / D, d = e % D;
-    qs[q * 128 + d] = p.q[oq + (int64_t)q * p.q_rs + (int64_t)d * p.q_cs];
+    qs[q * DMAX + d] = p.q[oq + (int64_t)q * p.q_rs + (int64_t)d * p.q_cs];
   }
   // Staging order: consecutive threads take consecutive addresses of
   // whichever index is contiguous in memory.
@@ -456,7 +458,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
     const int nk = min(KB, t_end - tb);
     __syncthreads();  // the previous block's readers are done
     if (rows4) {
-      constexpr int C4 = KB * 128 / 4 / 256;  // float4 per thread at 128 dims
+      constexpr int C4 = KB * DMAX / 4 / 256;  // float4 per thread at DMAX dims
       const int d4 = D / 4, dv4 = DV / 4;
       float4 kx[C4], vx[C4];
 #pragma unroll
@@ -479,7 +481,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
         if (c < KB * dv4) {
           const int key = c / dv4, d = (c % dv4) * 4;
           const float4 x = key < nk ? vx[u] : make_float4(0.f, 0.f, 0.f, 0.f);
-          *reinterpret_cast<float4 *>(vs + key * 128 + d) = x;
+          *reinterpret_cast<float4 *>(vs + key * DMAX + d) = x;
         }
       }
     } else {
@@ -490,7 +492,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
     }
     for (int e = tid; e < KB * DV; e += 256) {
       const int key = v_key_fast ? e % KB : e / DV, d = v_key_fast ? e / KB : e % DV;
-      vs[key * 128 + d] =
+      vs[key * DMAX + d] =
           key < nk ? p.v[ov + (int64_t)(tb + key) * p.v_ts + (int64_t)d * p.v_ds] : 0.f;
     }
     }
@@ -504,7 +506,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
     for (int d = 0; d < D; d++) {
       const float kv = ks[lane * KP + d];
 #pragma unroll
-      for (int i = 0; i < QW; i++) sc[i] = fmaf(qs[(wave + 4 * i) * 128 + d], kv, sc[i]);
+      for (int i = 0; i < QW; i++) sc[i] = fmaf(qs[(wave + 4 * i) * DMAX + d], kv, sc[i]);
     }
 #pragma unroll
     for (int i = 0; i < QW; i++) {
@@ -537,7 +539,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
     for (int j = 0; j < nk; j++) {
       float vv[DL];
 #pragma unroll
-      for (int k = 0; k < DL; k++) vv[k] = vs[j * 128 + lane + 64 * k];
+      for (int k = 0; k < DL; k++) vv[k] = vs[j * DMAX + lane + 64 * k];
 #pragma unroll
       for (int i = 0; i < QW; i++) {
         const int q = wave + 4 * i;
@@ -637,19 +639,23 @@ void launch_attn(const mg_attn_problem &p, dim3 grid, hipStream_t st) {
 
 template <int DS>
 void launch_dvt(const mg_attn_problem &p, dim3 grid, hipStream_t st) {
-  if (p.DV <= 32)
+  if (p.DV <= 32) {
     launch_attn<DS, 1>(p, grid, st);
-  else if (p.DV <= 64)
+  } else if constexpr (DS > 64) {  // value chunks of 64 (mg_attn_run)
     launch_attn<DS, 2>(p, grid, st);
-  else
-    launch_attn<DS, 4>(p, grid, st);
+  } else {
+    if (p.DV <= 64)
+      launch_attn<DS, 2>(p, grid, st);
+    else
+      launch_attn<DS, 4>(p, grid, st);
+  }
 }
 
 }  // namespace
 
 mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
-  if (p.D > 128 || p.DV > 128)
-    return mg_fail(MG_UNSUPPORTED, "attention: head sizes above 128 are not supported");
+  if (p.D > 256 || p.DV > 256)
+    return mg_fail(MG_UNSUPPORTED, "attention: head sizes above 256 are not supported");
   if (p.nbd > MG_ATTN_MAX_BATCH_DIMS)
     return mg_fail(MG_UNSUPPORTED, "attention: more than 4 batch dimensions");
   int64_t nbatch = 1;
@@ -662,10 +668,12 @@ mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
   if (p.kc > 0 && !p.part) return mg_fail(MG_INVALID_ARGUMENT, "attention: no partial buffer");
   const dim3 grid((unsigned)wgs, (unsigned)nsplit);
   if (dec) {
-    if (p.DV <= 64)
-      hipLaunchKernelGGL((k_attn_dec<1>), grid, dim3(256), 0, ctx->stream, p);
+    if (p.D > 128 || p.DV > 128)
+      hipLaunchKernelGGL((k_attn_dec<4, 256>), grid, dim3(256), 0, ctx->stream, p);
+    else if (p.DV <= 64)
+      hipLaunchKernelGGL((k_attn_dec<1, 128>), grid, dim3(256), 0, ctx->stream, p);
     else
-      hipLaunchKernelGGL((k_attn_dec<2>), grid, dim3(256), 0, ctx->stream, p);
+      hipLaunchKernelGGL((k_attn_dec<2, 128>), grid, dim3(256), 0, ctx->stream, p);
     MG_TRY(mg_launch_check("k_attn_dec"));
     if (p.kc > 0) {
       const int64_t n = nbatch * p.S * p.DV;
@@ -675,24 +683,37 @@ mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
     }
     return MG_OK;
   }
-  mg_attn_problem pp = p;
-  if (p.D == 0) {  // no products: the kernel's (masked-off) Q and K loads read V instead
-    pp.q = pp.k = p.v;
-    pp.q_rs = pp.q_cs = pp.k_ts = pp.k_ds = 0;
-    for (int d = 0; d < MG_ATTN_MAX_BATCH_DIMS; d++) pp.q_bs[d] = pp.k_bs[d] = 0;
-  }
-  if (p.D <= 32)
-    launch_dvt<16>(pp, grid, ctx->stream);
-  else if (p.D <= 64)
-    launch_dvt<32>(pp, grid, ctx->stream);
-  else
-    launch_dvt<64>(pp, grid, ctx->stream);
-  MG_TRY(mg_launch_check("k_attn"));
-  if (p.kc > 0) {
-    const int64_t n = nbatch * p.S * p.DV;
-    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                       ctx->stream, pp, nsplit, nbatch);
-    MG_TRY(mg_launch_check("k_attn_combine"));
+  // Value heads above 128 (above 64 with query/key heads above 128, whose
+  // 128 Q values per lane leave no registers for a fourth accumulator tile)
+  // run as column chunks: each chunk computes the same scores in the same
+  // order, so its softmax weights are bitwise those of the others.  A chunk's
+  // partials use the front of the buffer planned for the whole head.
+  const int chunk = p.D > 128 ? 64 : 128;
+  for (int c0 = 0; c0 < p.DV; c0 += chunk) {
+    mg_attn_problem pp = p;
+    pp.v = p.v + (int64_t)c0 * p.v_ds;
+    pp.y = p.y + c0;
+    pp.DV = std::min(chunk, p.DV - c0);
+    if (p.D == 0) {  // no products: the kernel's (masked-off) Q and K loads read V instead
+      pp.q = pp.k = pp.v;
+      pp.q_rs = pp.q_cs = pp.k_ts = pp.k_ds = 0;
+      for (int d = 0; d < MG_ATTN_MAX_BATCH_DIMS; d++) pp.q_bs[d] = pp.k_bs[d] = 0;
+    }
+    if (p.D <= 32)
+      launch_dvt<16>(pp, grid, ctx->stream);
+    else if (p.D <= 64)
+      launch_dvt<32>(pp, grid, ctx->stream);
+    else if (p.D <= 128)
+      launch_dvt<64>(pp, grid, ctx->stream);
+    else
+      launch_dvt<128>(pp, grid, ctx->stream);
+    MG_TRY(mg_launch_check("k_attn"));
+    if (p.kc > 0) {
+      const int64_t n = nbatch * p.S * pp.DV;
+      hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                         ctx->stream, pp, nsplit, nbatch);
+      MG_TRY(mg_launch_check("k_attn_combine"));
+    }
   }
   return MG_OK;
 }

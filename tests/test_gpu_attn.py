@@ -46,6 +46,13 @@ SDPA = [
     ((1, 2, 150, 48), (1, 2, 48, 200), (1, 2, 200, 100), (1, 1, 150, 200)),  # D 48, DV 100
     ((1, 2, 150, 128), (1, 2, 128, 200), (1, 2, 200, 20), ()),               # D 128, DV 20
     ((1, 2, 150, 96), (1, 2, 96, 200), (1, 2, 200, 64), (1, 1, 1, 200)),     # D 96, DV 64
+    # heads above 128 (Gemma-style 256): the tiled kernel's 128-dim halves,
+    # value heads in column chunks; the decode kernel's 256-dim tiles
+    ((1, 2, 150, 256), (1, 2, 256, 200), (1, 2, 200, 256), (1, 1, 150, 200)),  # D = DV = 256
+    ((2, 1, 130, 200), (2, 1, 200, 90), (2, 1, 90, 160), ()),                  # D 200, DV 160
+    ((1, 2, 140, 64), (1, 2, 64, 100), (1, 2, 100, 256), (1, 1, 1, 100)),      # D 64, DV 256
+    ((1, 4, 9, 256), (1, 4, 256, 300), (1, 4, 300, 256), (1, 1, 9, 300)),      # 9 queries: decode kernel
+    ((2, 2, 1, 144), (2, 2, 144, 77), (2, 2, 77, 200), ()),                    # one query, D 144, DV 200
 ]
 
 
@@ -85,7 +92,8 @@ def test_fused_sdpa_masked_rows_and_empty_keys(ops):
 
 @pytest.mark.parametrize("batch,seq,kv,hidden,heads,bias_heads,scale", [
     (2, 9, 9, 24, 4, 4, 0.35), (1, 130, 70, 64, 2, 1, None), (3, 1, 200, 256, 4, 0, None),
-    (32, 128, 128, 384, 12, 0, None)])   # MiniLM self-attention
+    (32, 128, 128, 384, 12, 0, None),    # MiniLM self-attention
+    (1, 150, 150, 1024, 4, 4, None)])    # head 256
 def test_mha_against_oracle(ops, batch, seq, kv, hidden, heads, bias_heads, scale):
     rng = np.random.default_rng(batch * seq + kv)
     q = rng.standard_normal((batch, seq, hidden)).astype(np.float32)
@@ -131,8 +139,10 @@ def test_attention_errors(ops):
         ops.op_fused_sdpa(z((2, 4, 8)), z((2, 7, 5)), z((2, 5, 3)), z((5,)), 1.0)
     with pytest.raises(ArgumentError):  # mask does not broadcast
         ops.op_fused_sdpa(z((2, 4, 8)), z((2, 8, 5)), z((2, 5, 3)), z((3, 5)), 1.0)
-    with pytest.raises(UnsupportedError):  # head size above 128
-        ops.op_fused_sdpa(z((1, 2, 200)), z((1, 200, 3)), z((1, 3, 4)), z(()), 1.0)
+    with pytest.raises(UnsupportedError):  # head size above 256
+        ops.op_fused_sdpa(z((1, 2, 300)), z((1, 300, 3)), z((1, 3, 4)), z(()), 1.0)
+    with pytest.raises(UnsupportedError):  # value head size above 256
+        ops.op_fused_sdpa(z((1, 2, 8)), z((1, 8, 3)), z((1, 3, 260)), z(()), 1.0)
     with pytest.raises(ArgumentError):  # hidden not a multiple of heads
         ops.op_multi_head_attention(z((1, 2, 10)), z((1, 2, 10)), z((1, 2, 10)), num_heads=4)
     with pytest.raises(UnsupportedError):  # bias heads neither 1 nor num_heads
@@ -172,6 +182,11 @@ GQA = [
     (1, 1, 32, 8, 64, 1000, True, False, 32, 0),    # decode: packed heads, key splits
     (2, 1, 14, 2, 64, 700, False, False, 0, 14),    # decode with per-head bias, splits
     (1, 3, 8, 8, 32, 500, True, True, 16, 1),       # short chunk over a long cache, splits
+    # Gemma-3-style heads of 256 (rotary over the whole head)
+    (1, 1, 8, 4, 256, 600, True, False, 128, 0),    # 4B-style decode: 2 q heads per kv head
+    (2, 1, 4, 1, 256, 300, True, False, 128, 0),    # 1B-style decode: one kv head (4:1)
+    (1, 150, 8, 2, 256, 0, True, False, 128, 0),    # causal prefill, 4:1 groups
+    (1, 40, 4, 1, 256, 25, True, True, 64, 4),      # chunk over a cache, partial rotary, bias
 ]
 
 
@@ -242,10 +257,10 @@ def test_gqa_errors(ops):
         ops.op_group_query_attention(q, k, k, num_heads=4, kv_num_heads=2, do_rotary=True,
                                      cos_cache=np.ones((2, 4), np.float32),
                                      sin_cache=np.zeros((2, 4), np.float32))
-    with pytest.raises(UnsupportedError):  # head size 256
-        ops.op_group_query_attention(np.zeros((1, 2, 512), np.float32),
-                                     np.zeros((1, 2, 256), np.float32),
-                                     np.zeros((1, 2, 256), np.float32), num_heads=2,
+    with pytest.raises(UnsupportedError):  # head size above 256
+        ops.op_group_query_attention(np.zeros((1, 2, 640), np.float32),
+                                     np.zeros((1, 2, 320), np.float32),
+                                     np.zeros((1, 2, 320), np.float32), num_heads=2,
                                      kv_num_heads=1)
 
 
