@@ -587,9 +587,96 @@ def decode_sweep(torch, ops, ctx, T, randn, dev, args, stream):
                         "lm_head_us": round(ms_head * 1e3, 2),
                         "lm_head_GB/s": round(hb / (ms_head / 1e3) / 1e9, 1)}
         print(f"# decode M={m}: {out[f'M{m}']}", file=sys.stderr, flush=True)
+    out["layer_with_producers"] = decode_layers_with_producers(torch, ops, ctx, T, randn, dev,
+                                                               args, stream, ws, shapes)
     for w in ws:
         w.release()
     return out
+
+
+def decode_layers_with_producers(torch, ops, ctx, T, randn, dev, args, stream, ws, shapes):
+    """The decode step with the ops that produce each projection's input, as a
+    layer runs them (lib/src/onnx_graph.dart:1227-1309; attention itself is
+    left out: its output is a synthetic buffer): per layer SkipSimplified-
+    LayerNormalization -> q/k/v, o on the attention output, the residual add
+    fused into the next SkipSimplifiedLayerNormalization -> gate/up, SiLU
+    gating (Sigmoid, Mul, Mul) -> down.  Timed twice: every GEMV converting
+    its fp32 input in a prepass launch, and the two norms also writing the
+    split activations their GEMVs read (no prepass launch for q/k/v and
+    gate/up: 12 launches per layer instead of 14)."""
+    H, I = LLAMA_LAYER[0][1], LLAMA_LAYER[4][2]
+    nl = len(LLAMA_LAYER)
+    rng = np.random.default_rng(0x5EED0005)
+    gam = [torch.from_numpy(rng.uniform(0.5, 1.5, H).astype(np.float32)).to(dev)
+           for _ in range(2 * LLAMA_LAYERS)]
+    res = {}
+    for m in (4, 16):
+        x, resid, att = randn(m, H), randn(m, H), randn(m, H)
+        h, ssum, q, o = (torch.empty((m, H), device=dev) for _ in range(4))
+        kk = torch.empty((m, LLAMA_LAYER[1][2]), device=dev)
+        vv = torch.empty((m, LLAMA_LAYER[2][2]), device=dev)
+        g, u, sg, act = (torch.empty((m, I), device=dev) for _ in range(4))
+        dn = torch.empty((m, H), device=dev)
+        sp_h = torch.empty(ops.nbits_split_bytes(H, LLAMA_BLOCK), device=dev, dtype=torch.uint8)
+        P = lambda t: t.data_ptr()  # noqa: E731
+
+        def step(split):
+            xin, rin = x, resid
+            for li in range(LLAMA_LAYERS):
+                lw = ws[li * nl:(li + 1) * nl]
+                if split:
+                    ops.skip_rms_norm_f32_split_dev(P(xin), P(rin), (m, H), P(gam[2 * li]), H, None,
+                                                    1e-5, P(h), P(ssum), LLAMA_BLOCK, P(sp_h),
+                                                    ctx=ctx)
+                    ops.matmul_nbits_group_split_dev(lw[0:3], P(h), P(sp_h), m,
+                                                     [P(q), P(kk), P(vv)], ctx=ctx)
+                else:
+                    ops.skip_rms_norm_f32_dev(P(xin), P(rin), (m, H), P(gam[2 * li]), H, None,
+                                              1e-5, P(h), P(ssum), ctx=ctx)
+                    ops.matmul_nbits_group_dev(lw[0:3], P(h), m, [P(q), P(kk), P(vv)], ctx=ctx)
+                lw[3].run_dev(P(att), m, P(o))
+                if split:
+                    ops.skip_rms_norm_f32_split_dev(P(o), P(ssum), (m, H), P(gam[2 * li + 1]), H,
+                                                    None, 1e-5, P(h), P(ssum), LLAMA_BLOCK,
+                                                    P(sp_h), ctx=ctx)
+                    ops.matmul_nbits_group_split_dev(lw[4:6], P(h), P(sp_h), m, [P(g), P(u)],
+                                                     ctx=ctx)
+                else:
+                    ops.skip_rms_norm_f32_dev(P(o), P(ssum), (m, H), P(gam[2 * li + 1]), H, None,
+                                              1e-5, P(h), P(ssum), ctx=ctx)
+                    ops.matmul_nbits_group_dev(lw[4:6], P(h), m, [P(g), P(u)], ctx=ctx)
+                ops.sigmoid_f32_dev(P(g), m * I, P(sg), ctx=ctx)
+                ops.binary_f32_dev("mul", P(g), (m, I), P(sg), (m, I), P(sg), ctx=ctx)
+                ops.binary_f32_dev("mul", P(sg), (m, I), P(u), (m, I), P(act), ctx=ctx)
+                lw[6].run_dev(P(act), m, P(dn))
+                xin, rin = dn, ssum
+            ws[-1].run_dev(P(dn), m, P(y_head))
+
+        y_head = torch.empty((m, LLAMA_HEAD[2]), device=dev)
+        steps = max(args.steps // 2, 5)
+        r = {}
+        for tag, split in (("prepass", False), ("split", True)):
+            ms = T.loop(lambda: step(split), steps, 2)
+            timing = "host-issued launches"
+            try:
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr, stream=stream):
+                    step(split)
+                ms = T.loop(gr.replay, steps, 2)
+                timing = "HIP graph replay"
+                del gr
+            except Exception as e:
+                print(f"# decode layer M={m} graph capture failed: {e}", file=sys.stderr,
+                      flush=True)
+            r[f"{tag}_ms_per_step"] = round(ms, 4)
+            r["timing"] = timing
+        r["launches_per_layer"] = {"prepass": 14, "split": 12}
+        res[f"M{m}"] = r
+        print(f"# decode layers with producers M={m}: {r}", file=sys.stderr, flush=True)
+    res["workload"] = ("16 Llama-style layers (SkipSimplifiedLayerNormalization, q/k/v, o, "
+                       "SkipSimplifiedLayerNormalization, gate/up, Sigmoid, Mul, Mul, down) + "
+                       "lm_head; attention output synthetic")
+    return res
 
 
 def nbits_float_zp(torch, ops, ctx, T, randn, dev, args):

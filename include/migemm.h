@@ -212,6 +212,28 @@ mg_status mg_matmul_nbits_group_dev(mg_ctx *ctx, int32_t n,
                                     const mg_weight *const *w,
                                     const float *a_dev, int64_t M,
                                     float *const *y_dev);
+/* Split activations for the decode GEMV (3 to 16 rows, integer zero
+ * points, block_size >= 32).  That GEMV takes each activation as an fp16
+ * hi/lo pair with a power-of-two row exponent; without help it converts its
+ * fp32 input in a prepass launch of its own.  The norm producer
+ * (mg_skip_rms_norm_f32_split_dev) also writes that split of the rows it
+ * computes into a device buffer of
+ * mg_nbits_split_bytes bytes, and this entry reads it instead of running the
+ * prepass: the results are bitwise those of mg_matmul_nbits_group_dev on
+ * a_dev.  a_dev is still required (plans other than the 3..16-row GEMV read
+ * it); split_dev may be NULL.  The split must come from a_dev's producer for
+ * the weights' K and block size.  No counterpart in the reference, whose ops
+ * exchange fp32 tensors only (lib/src/onnx_graph.dart:1227-1309); it saves
+ * one launch per decode GEMV whose input comes from a norm (q/k/v and
+ * gate/up of a decoder layer). */
+mg_status mg_matmul_nbits_group_split_dev(mg_ctx *ctx, int32_t n,
+                                          const mg_weight *const *w,
+                                          const float *a_dev,
+                                          const void *split_dev, int64_t M,
+                                          float *const *y_dev);
+/* Bytes of a split activation buffer for rows of K elements read by
+ * MatMulNBits weights of this block_size. */
+mg_status mg_nbits_split_bytes(int64_t K, int64_t block_size, size_t *bytes);
 
 /* ------------------------------------------- MatMulInteger / QLinearMatMul */
 
@@ -601,7 +623,17 @@ mg_status mg_skip_rms_norm_f32_dev(mg_ctx *ctx, const float *x_dev, const float 
                                    const int64_t *shape, int32_t rank, const float *gamma_dev,
                                    int64_t gamma_len, const float *bias_dev, double epsilon,
                                    float *y_dev, float *sum_dev);
-
+/* mg_skip_rms_norm_f32_dev (skip_dev not NULL) or mg_rms_norm_f32_dev over
+ * the last axis (skip_dev NULL: sum_dev is ignored), with y and the sum
+ * bitwise as there, also writing the decode GEMV's split of y into
+ * split_dev (mg_nbits_split_bytes(last dim, block_size) bytes), for at most
+ * 16 rows of at most 8192 elements (MG_INVALID_ARGUMENT otherwise). */
+mg_status mg_skip_rms_norm_f32_split_dev(mg_ctx *ctx, const float *x_dev,
+                                         const float *skip_dev, const int64_t *shape,
+                                         int32_t rank, const float *gamma_dev,
+                                         int64_t gamma_len, const float *bias_dev,
+                                         double epsilon, float *y_dev, float *sum_dev,
+                                         int64_t block_size, void *split_dev);
 /* ----------------------------------------------------------------- weights */
 
 mg_status mg_weight_release(mg_weight *w);

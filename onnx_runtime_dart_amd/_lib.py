@@ -47,6 +47,10 @@ SIGNATURES = {
     "mg_matmul_nbits_dev": [_P, _P, _P, _I64, _P],
     "mg_matmul_nbits_dev_noalloc": [_P, _P, _P, _I64, _P],
     "mg_matmul_nbits_group_dev": [_P, _I32, _P, _P, _I64, _P],
+    "mg_matmul_nbits_group_split_dev": [_P, _I32, _P, _P, _P, _I64, _P],
+    "mg_nbits_split_bytes": [_I64, _I64, _P],
+    "mg_skip_rms_norm_f32_split_dev": [_P, _P, _P, _P, _I32, _P, _I64, _P, C.c_double, _P, _P,
+                                       _I64, _P],
     "mg_weight_int8_create": [_P, _P, _I32, _I64, _I64, _P, _I64, _PP],
     "mg_matmul_integer": [_P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I64, _P, _I64, _P],
     "mg_matmul_integer_i64": [_P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I64, _P, _I64,

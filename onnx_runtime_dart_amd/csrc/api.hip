@@ -621,30 +621,51 @@ mg_status mg_matmul_nbits_dev_noalloc(mg_ctx *ctx, const mg_weight *w, const flo
   return mg_nbits_run(ctx, w, a_dev, M, y_dev, s);
 }
 
-mg_status mg_matmul_nbits_group_dev(mg_ctx *ctx, int32_t n, const mg_weight *const *w,
-                                    const float *a_dev, int64_t M, float *const *y_dev) {
+namespace {
+mg_status nbits_group(mg_ctx *ctx, const std::string &what, int32_t n, const mg_weight *const *w,
+                      const float *a_dev, const void *split_dev, int64_t M,
+                      float *const *y_dev) {
   ProfScope prof_(ctx, "MatMulNBits");
   g_last_error.clear();
   if (!ctx || !w || !y_dev || n < 1 || n > 4)
-    return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits_group_dev: 1 to 4 weights expected");
+    return mg_fail(MG_INVALID_ARGUMENT, what + ": 1 to 4 weights expected");
   for (int32_t i = 0; i < n; i++) {
     if (!w[i] || w[i]->kind != MG_W_NBITS)
-      return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits_group_dev: not a MatMulNBits weight");
+      return mg_fail(MG_INVALID_ARGUMENT, what + ": not a MatMulNBits weight");
     if (w[i]->K != w[0]->K || w[i]->nbits.bs != w[0]->nbits.bs ||
         w[i]->nbits.zp_kind != w[0]->nbits.zp_kind || w[i]->device != w[0]->device)
       return mg_fail(MG_INVALID_ARGUMENT,
-                     "mg_matmul_nbits_group_dev: weights must share K, block_size, zero-point "
-                     "form and device");
-    if (!y_dev[i]) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits_group_dev: null output");
+                     what + ": weights must share K, block_size, zero-point form and device");
+    if (!y_dev[i]) return mg_fail(MG_INVALID_ARGUMENT, what + ": null output");
   }
   if (M < 0) return mg_fail(MG_INVALID_ARGUMENT, "MatMulNBits: invalid K, N, block_size or input shape");
   if (M == 0) return MG_OK;
-  if (!a_dev) return mg_fail(MG_INVALID_ARGUMENT, "mg_matmul_nbits_group_dev: null input");
+  if (!a_dev) return mg_fail(MG_INVALID_ARGUMENT, what + ": null input");
   MG_TRY(mg_use_device(ctx));
   const size_t ws = mg_nbits_group_ws_bytes(ctx, n, w, M);
   MG_TRY(mg_check_control(ctx, (int64_t)ws));
   MG_TRY(mg_ws_reserve(ctx, ws));
-  return mg_nbits_run_group(ctx, n, w, a_dev, M, y_dev, ctx->ws);
+  return mg_nbits_run_group(ctx, n, w, a_dev, M, y_dev, ctx->ws, split_dev);
+}
+}  // namespace
+
+mg_status mg_matmul_nbits_group_dev(mg_ctx *ctx, int32_t n, const mg_weight *const *w,
+                                    const float *a_dev, int64_t M, float *const *y_dev) {
+  return nbits_group(ctx, "mg_matmul_nbits_group_dev", n, w, a_dev, nullptr, M, y_dev);
+}
+
+mg_status mg_matmul_nbits_group_split_dev(mg_ctx *ctx, int32_t n, const mg_weight *const *w,
+                                          const float *a_dev, const void *split_dev, int64_t M,
+                                          float *const *y_dev) {
+  return nbits_group(ctx, "mg_matmul_nbits_group_split_dev", n, w, a_dev, split_dev, M, y_dev);
+}
+
+mg_status mg_nbits_split_bytes(int64_t K, int64_t block_size, size_t *bytes) {
+  g_last_error.clear();
+  if (!bytes || K < 1 || block_size < 16 || (block_size & (block_size - 1)))
+    return mg_fail(MG_INVALID_ARGUMENT, "mg_nbits_split_bytes: invalid K or block_size");
+  *bytes = mg_nbits_split_size(mg_nbits_kpad(K, block_size));
+  return MG_OK;
 }
 
 mg_status mg_matmul_nbits(mg_ctx *ctx, const mg_weight *w, const float *a, int64_t M, float *y) {
@@ -2479,6 +2500,46 @@ mg_status mg_skip_rms_norm_f32_dev(mg_ctx *ctx, const float *x_dev, const float 
   MG_TRY(mg_check_control(ctx, 0));
   return mg_elem_rms_norm(ctx, x_dev, skip_dev, gamma_dev, bias_dev, epsilon, outer, dim, 1,
                           dim, y_dev, sum_dev);
+}
+
+// The producer of a decode GEMV's input that also writes its split
+// activations (at most 16 rows of at most 8192 elements; block_size: that of
+// the MatMulNBits weights that will read the split).
+namespace {
+mg_status split_rows(const char *what, const int64_t *shape, int32_t rank, int64_t block_size,
+                     void *split, int64_t *rows, int64_t *d, int64_t *kpad) {
+  if (!shape_ok(shape, rank) || rank < 1 || !split || block_size < 16 ||
+      (block_size & (block_size - 1)))
+    return mg_fail(MG_INVALID_ARGUMENT, std::string(what) + ": invalid argument");
+  *d = shape[rank - 1];
+  *rows = prod(shape, 0, rank - 1);
+  if (*rows > 16 || *d > 8192)
+    return mg_fail(MG_INVALID_ARGUMENT, std::string(what) +
+                                            ": split activations need at most 16 rows of at "
+                                            "most 8192 elements");
+  *kpad = mg_nbits_kpad(std::max<int64_t>(*d, 1), block_size);
+  return MG_OK;
+}
+}  // namespace
+
+mg_status mg_skip_rms_norm_f32_split_dev(mg_ctx *ctx, const float *x_dev, const float *skip_dev,
+                                         const int64_t *shape, int32_t rank,
+                                         const float *gamma_dev, int64_t gamma_len,
+                                         const float *bias_dev, double epsilon, float *y_dev,
+                                         float *sum_dev, int64_t block_size, void *split_dev) {
+  ProfScope prof_(ctx, skip_dev ? "SkipSimplifiedLayerNormalization" : "RMSNorm");
+  g_last_error.clear();
+  int64_t outer, dim, inner, rows, d, kpad;
+  MG_TRY(rms_common(ctx, "mg_skip_rms_norm_f32_split_dev", x_dev, shape, rank, gamma_dev,
+                    gamma_len, -1, &outer, &dim, &inner));
+  MG_TRY(split_rows("mg_skip_rms_norm_f32_split_dev", shape, rank, block_size, split_dev, &rows,
+                    &d, &kpad));
+  if (outer * dim == 0) return MG_OK;
+  if (!y_dev) return mg_fail(MG_INVALID_ARGUMENT, "mg_skip_rms_norm_f32_split_dev: null buffer");
+  MG_TRY(mg_use_device(ctx));
+  MG_TRY(mg_check_control(ctx, 0));
+  return mg_elem_rms_norm_split(ctx, x_dev, skip_dev, gamma_dev, bias_dev, epsilon, rows, d,
+                                y_dev, skip_dev ? sum_dev : nullptr, kpad, split_dev);
 }
 
 }  // extern "C"

@@ -87,36 +87,87 @@ __device__ inline double block_sum(double v, double *red) {
 // RMSNorm over the last axis: one workgroup per row of d elements.  With a
 // skip input the row is s = x + skip (f32), written to sum when asked; with
 // a bias, out = normed + bias (f32), as the reference's Add after the norm.
-// Any of x, skip, sum and y may be the same buffer (an in-place residual):
-// each element is read and written by one thread only, and once sum holds
-// s the second pass reads s back from it instead of re-adding x and skip.
+// Thread t owns elements t, t + 256, ...: with P > 0 (d <= 256 P) it keeps
+// them in registers between the sum of squares and the output, so the row
+// is read once; P = 0 walks the row twice.  Any of x, skip, sum and y may be
+// the same buffer (an in-place residual): each element is read and written
+// by one thread only, and with P = 0, once sum holds s the second pass reads
+// s back from it instead of re-adding x and skip.  With ybuf, y is also
+// staged there (the split producer) and *mx receives the largest finite |y|
+// of the thread's elements.
+template <int P>
+__device__ inline void rms_row(const float *x, const float *skip,
+                               const float *__restrict__ gamma, const float *__restrict__ bias,
+                               double eps, int64_t d, float *y, float *sum, double *red,
+                               float *ybuf, float *mx) {
+  const int64_t base = (int64_t)blockIdx.x * d;
+  const int t = threadIdx.x;
+  double ss = 0;
+  float v[P > 0 ? P : 1];
+  if constexpr (P > 0) {
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+      const int64_t j = t + 256 * i;
+      v[i] = 0.f;
+      if (j < d) {
+        v[i] = x[base + j];
+        if (skip) v[i] = v[i] + skip[base + j];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+      const int64_t j = t + 256 * i;
+      if (j < d) {
+        if (skip && sum) sum[base + j] = v[i];
+        ss += (double)v[i] * (double)v[i];
+      }
+    }
+  } else {
+    for (int64_t j = t; j < d; j += 256) {
+      float w = x[base + j];
+      if (skip) {
+        w = w + skip[base + j];
+        if (sum) sum[base + j] = w;
+      }
+      ss += (double)w * (double)w;
+    }
+  }
+  ss = block_sum(ss, red);
+  const double inv = 1.0 / sqrt(ss / (double)d + eps);
+  float m = 0.f;
+  auto out = [&](int64_t j, float w) __attribute__((always_inline)) {
+    float o = (float)((double)w * inv * (double)gamma[j]);
+    if (bias) o = o + bias[j];
+    y[base + j] = o;
+    if (ybuf) {
+      ybuf[j] = o;
+      const float f = fabsf(o);
+      m = f < INFINITY ? fmaxf(m, f) : m;  // finite values only
+    }
+  };
+  if constexpr (P > 0) {
+#pragma unroll
+    for (int i = 0; i < P; i++)
+      if (t + 256 * i < d) out(t + 256 * i, v[i]);
+  } else {
+    for (int64_t j = t; j < d; j += 256) {
+      float w;
+      if (skip && sum) w = sum[base + j];
+      else if (skip) w = x[base + j] + skip[base + j];
+      else w = x[base + j];
+      out(j, w);
+    }
+  }
+  if (mx) *mx = m;
+}
+
+template <int P>
 __global__ __launch_bounds__(256) void k_rms_last(const float *x, const float *skip,
                                                   const float *__restrict__ gamma,
                                                   const float *__restrict__ bias, double eps,
                                                   int64_t d, float *y, float *sum) {
   __shared__ double red[4];
-  const int64_t base = (int64_t)blockIdx.x * d;
-  const int t = threadIdx.x;
-  double ss = 0;
-  for (int64_t j = t; j < d; j += 256) {
-    float v = x[base + j];
-    if (skip) {
-      v = v + skip[base + j];
-      if (sum) sum[base + j] = v;
-    }
-    ss += (double)v * (double)v;
-  }
-  ss = block_sum(ss, red);
-  const double inv = 1.0 / sqrt(ss / (double)d + eps);
-  for (int64_t j = t; j < d; j += 256) {
-    float v;
-    if (skip && sum) v = sum[base + j];
-    else if (skip) v = x[base + j] + skip[base + j];
-    else v = x[base + j];
-    float o = (float)((double)v * inv * (double)gamma[j]);
-    if (bias) o = o + bias[j];
-    y[base + j] = o;
-  }
+  rms_row<P>(x, skip, gamma, bias, eps, d, y, sum, red, nullptr, nullptr);
 }
 
 // RMSNorm over another axis: one thread per (outer, inner) slice, walking the
@@ -141,7 +192,94 @@ __global__ __launch_bounds__(256) void k_rms_axis(const float *x,
   }
 }
 
+// ---------------------------------------------- split activations for the GEMV
+//
+// The MatMulNBits decode GEMV (3 to 16 rows) takes its activations as an
+// fp16 hi/lo pair per element with a power-of-two row exponent, in its MFMA
+// A-operand order; its own prepass builds them from the fp32 rows.  The
+// RMSNorm / SkipSimplifiedLayerNormalization kernel over the last axis can
+// also write that split of the row it produces (a norm owns whole rows, so
+// the row maximum costs it one more reduction), and the GEMV that consumes
+// it then needs no prepass launch.  It computes y exactly as without the
+// split, stages the row in LDS, and converts
+// it exactly as the prepass would convert the stored y (same row maximum,
+// exponent and rounding): the GEMV's results are bitwise those of the
+// prepass path.
+//
+// Layout (mg_nbits_split_bytes): uint4 at ((kg * 4 + j) * 2 + part) * 64 +
+// 16 g + row holds the 8 halves of k = 128 kg + 32 j + 8 g + 0..7 (part 0
+// hi, 1 lo), for rows 0..15 and k up to kpad (zeros past the row); the int32
+// row exponents follow at byte mg_align(16 * kpad * 4).
+
+typedef _Float16 half8e __attribute__((ext_vector_type(8)));
+constexpr int SPLIT_MAXD = 8192;  // longest row the producers stage in LDS
+
+// Block-wide maximum (every thread gets it); red holds 4 floats.
+__device__ inline float block_max(float v, float *red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  const int t = threadIdx.x;
+  __syncthreads();
+  if ((t & 63) == 0) red[t >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Row `row` of the split from the d values staged in ybuf (mx: the largest
+// finite |y| of this thread's elements).  256 threads; octets up to kpad / 8.
+__device__ inline void write_split_row(const float *ybuf, int64_t d, int64_t kpad, float mx,
+                                       int row, uint4 *__restrict__ ahl, int *__restrict__ texp,
+                                       float *red) {
+  mx = block_max(mx, red);
+  int e = 0;
+  if (mx > 0.f) {
+    int ex;
+    frexpf(mx, &ex);
+    e = 14 - ex;
+  }
+  const int t = threadIdx.x;
+  if (t == 0) texp[row] = e;
+  for (int64_t o = t; o < kpad / 8; o += 256) {
+    half8e hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int64_t k = o * 8 + i;
+      const float x = ldexpf(k < d ? ybuf[k] : 0.f, (i & 2) ? e - 4 : e);
+      const _Float16 hh = (_Float16)x;
+      float res = x - (float)hh;
+      if (!isfinite(res)) res = 0.f;
+      hi[i] = hh;
+      lo[i] = (_Float16)res;
+    }
+    const int64_t kg = o >> 4, j = (o >> 2) & 3, g = o & 3;
+    uint4 *dst = ahl + ((kg * 4 + j) * 2) * 64 + 16 * g + row;
+    dst[0] = __builtin_bit_cast(uint4, hi);
+    dst[64] = __builtin_bit_cast(uint4, lo);
+  }
+}
+
+// RMSNorm over the last axis (k_rms_last's arithmetic, element for element)
+// writing y, the optional sum, and the split of y.  One workgroup per row,
+// rows < 16, d <= SPLIT_MAXD.
+template <int P>
+__global__ __launch_bounds__(256) void k_rms_last_split(
+    const float *x, const float *skip, const float *__restrict__ gamma,
+    const float *__restrict__ bias, double eps, int64_t d, float *y, float *sum, int64_t kpad,
+    uint4 *__restrict__ ahl, int *__restrict__ texp) {
+  __shared__ double red[4];
+  __shared__ float redf[4];
+  __shared__ float ybuf[SPLIT_MAXD];
+  float mx;
+  rms_row<P>(x, skip, gamma, bias, eps, d, y, sum, red, ybuf, &mx);
+  write_split_row(ybuf, d, kpad, mx, (int)blockIdx.x, ahl, texp, redf);
+}
+
 inline unsigned blocks(int64_t n, int64_t per) { return (unsigned)((n + per - 1) / per); }
+
+// Elements per thread kept in registers for a row of d (0: two passes).
+inline int rms_regs(int64_t d) {
+  return d <= 256 ? 1 : d <= 1024 ? 4 : d <= 2048 ? 8 : d <= 4096 ? 16 : 0;
+}
 
 }  // namespace
 
@@ -189,11 +327,40 @@ mg_status mg_elem_rms_norm(mg_ctx *ctx, const float *x, const float *skip, const
                            int64_t inner, int64_t last, float *y, float *sum) {
   if (outer * dim * inner == 0) return MG_OK;
   if (inner == 1) {  // the caller keeps rows (outer) below 2^31
-    hipLaunchKernelGGL(k_rms_last, dim3((unsigned)outer), dim3(256), 0, ctx->stream, x, skip,
-                       gamma, bias, eps, dim, y, sum);
+#define MG_RMS(P_)                                                                           \
+  hipLaunchKernelGGL((k_rms_last<P_>), dim3((unsigned)outer), dim3(256), 0, ctx->stream, x, \
+                     skip, gamma, bias, eps, dim, y, sum)
+    switch (rms_regs(dim)) {
+      case 1: MG_RMS(1); break;
+      case 4: MG_RMS(4); break;
+      case 8: MG_RMS(8); break;
+      case 16: MG_RMS(16); break;
+      default: MG_RMS(0); break;
+    }
+#undef MG_RMS
     return mg_launch_check("k_rms_last");
   }
   hipLaunchKernelGGL(k_rms_axis, dim3(blocks(outer * inner, 256)), dim3(256), 0, ctx->stream, x,
                      gamma, eps, outer, dim, inner, last, y);
   return mg_launch_check("k_rms_axis");
+}
+
+mg_status mg_elem_rms_norm_split(mg_ctx *ctx, const float *x, const float *skip,
+                                 const float *gamma, const float *bias, double eps, int64_t rows,
+                                 int64_t d, float *y, float *sum, int64_t kpad, void *split) {
+  if (rows == 0 || d == 0) return MG_OK;
+  uint4 *ahl = static_cast<uint4 *>(split);
+  int *texp = reinterpret_cast<int *>(static_cast<char *>(split) + mg_align((size_t)16 * kpad * 4));
+#define MG_RMS(P_)                                                                        \
+  hipLaunchKernelGGL((k_rms_last_split<P_>), dim3((unsigned)rows), dim3(256), 0, ctx->stream, \
+                     x, skip, gamma, bias, eps, d, y, sum, kpad, ahl, texp)
+  switch (rms_regs(d)) {
+    case 1: MG_RMS(1); break;
+    case 4: MG_RMS(4); break;
+    case 8: MG_RMS(8); break;
+    case 16: MG_RMS(16); break;
+    default: MG_RMS(0); break;
+  }
+#undef MG_RMS
+  return mg_launch_check("k_rms_last_split");
 }

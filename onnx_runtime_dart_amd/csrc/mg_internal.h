@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <string>
@@ -192,8 +193,21 @@ mg_status mg_nbits_run(mg_ctx *ctx, const mg_weight *w, const float *a_dev,
 // launch; ws holds mg_nbits_group_ws_bytes bytes.
 size_t mg_nbits_group_ws_bytes(const mg_ctx *ctx, int n, const mg_weight *const *w,
                                int64_t M);
+// split (may be null): the activations already split for the decode GEMV
+// (mg_nbits_split_bytes layout, written by a producer op); when the plan is
+// the 3..16-row GEMV it replaces the activation prepass.
 mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
-                             const float *a_dev, int64_t M, float *const *y_dev, void *ws);
+                             const float *a_dev, int64_t M, float *const *y_dev, void *ws,
+                             const void *split = nullptr);
+// K padded as a MatMulNBits weight of this block size pads it (the split
+// activation buffer covers k < kpad).
+inline int64_t mg_nbits_kpad(int64_t K, int64_t bs) {
+  const int64_t nb = (K + bs - 1) / bs;
+  return std::max<int64_t>((nb * bs + 127) / 128 * 128, 128);
+}
+// Bytes of a split activation buffer for rows of K (16 rows, fp16 hi and lo
+// per element up to kpad, then 16 int32 row exponents).
+inline size_t mg_nbits_split_size(int64_t kpad) { return mg_align((size_t)16 * kpad * 4) + 64; }
 
 // ------------------------------------------------------------ int8 entry
 
@@ -302,6 +316,11 @@ mg_status mg_elem_sigmoid(mg_ctx *ctx, const float *x, float *y, int64_t n);
 mg_status mg_elem_rms_norm(mg_ctx *ctx, const float *x, const float *skip, const float *gamma,
                            const float *bias, double eps, int64_t outer, int64_t dim,
                            int64_t inner, int64_t last, float *y, float *sum);
+// The last-axis RMSNorm over at most 16 rows of d <= 8192, also writing the
+// decode GEMV's split of y into split (kpad: its padded K).
+mg_status mg_elem_rms_norm_split(mg_ctx *ctx, const float *x, const float *skip,
+                                 const float *gamma, const float *bias, double eps, int64_t rows,
+                                 int64_t d, float *y, float *sum, int64_t kpad, void *split);
 
 // --------------------------------------------------------------- conv entry
 

@@ -1980,7 +1980,8 @@ mg_status prefill_run(mg_ctx *ctx, int n, const mg_weight *const *w, const float
 }  // namespace
 
 mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
-                             const float *a_dev, int64_t M, float *const *y_dev, void *ws) {
+                             const float *a_dev, int64_t M, float *const *y_dev, void *ws,
+                             const void *split) {
   if (M == 0 || n == 0) return MG_OK;
   int64_t ng = 0;
   for (int i = 0; i < n; i++) ng += w[i]->nbits.ng;
@@ -2039,7 +2040,11 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
     uint4 *ahl = reinterpret_cast<uint4 *>(base + p.off_a);
     int *texp = reinterpret_cast<int *>(base + p.off_b);
     const int vec = (w0->K % 4 == 0) && (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0);
-    {
+    if (split) {  // written by the producer of a (same layout as the prepass's)
+      ahl = static_cast<uint4 *>(const_cast<void *>(split));
+      texp = reinterpret_cast<int *>(static_cast<char *>(const_cast<void *>(split)) +
+                                     mg_align((size_t)16 * d.kpad * 4));
+    } else {
       const int per = (int)((d.c4 * 16 + 255) / 256);  // octets per thread
 #define MG_SPLIT16(P_)                                                                          \
   hipLaunchKernelGGL((k_af16split16<P_>), dim3(16), dim3(256), 0, st, a_dev, M, w0->K,        \
@@ -2049,8 +2054,8 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
       else if (per <= 4) MG_SPLIT16(4);
       else MG_SPLIT16(0);
 #undef MG_SPLIT16
+      MG_TRY(mg_launch_check("k_af16split16"));
     }
-    MG_TRY(mg_launch_check("k_af16split16"));
     const int has_zp = d.zp_kind == MG_ZP_UINT4;
     const int segj = (int)(std::min<int64_t>(d.bs, KGRP) / 32);
     // Waves per workgroup: 4 for wide weights; narrow ones (fewer than two
@@ -2067,12 +2072,12 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
 #define MG_GEMV16_WG_PER_CU 1
 #endif
     const int64_t cus = std::max(ctx->num_cus, 1) * (int64_t)MG_GEMV16_WG_PER_CU;
-    const bool split = p.ksplit > 1;
-    const int tpw = split || ng >= cus ? 4 : (2 * ng >= cus ? 2 : 1);
+    const bool ksplit = p.ksplit > 1;
+    const int tpw = ksplit || ng >= cus ? 4 : (2 * ng >= cus ? 2 : 1);
     const int64_t wgs = ng * (4 / tpw);
     int nw = 4;
-    if (split ? p.kps >= 8 : (wgs < 2 * cus && d.c4 >= 8)) nw = 8;
-    if (!split && wgs >= 4 * cus && tpw == 4) nw = 1;
+    if (ksplit ? p.kps >= 8 : (wgs < 2 * cus && d.c4 >= 8)) nw = 8;
+    if (!ksplit && wgs >= 4 * cus && tpw == 4) nw = 1;
 #define MG_DEC_LAUNCH(SJ_, NW_, TPW_)                                                      \
   hipLaunchKernelGGL((k_gemv_mfma<SJ_, NW_, TPW_>), dim3((unsigned)wgs, (unsigned)p.ksplit), \
                      dim3(NW_ * 64), 0, st, ahl, texp, gs, (int)M, (int)d.c4, (int)d.nb,    \
@@ -2092,7 +2097,7 @@ mg_status mg_nbits_run_group(mg_ctx *ctx, int n, const mg_weight *const *w,
 #undef MG_DEC_TPW
 #undef MG_DEC_LAUNCH
     MG_TRY(mg_launch_check("k_gemv_mfma"));
-    if (split) return launch_gemm_reduce(st, part, rs, eend, p.ksplit);
+    if (ksplit) return launch_gemm_reduce(st, part, rs, eend, p.ksplit);
     return MG_OK;
   }
   if (p.path == 1) return prefill_run(ctx, n, w, a_dev, M, y_dev, ws, p);

@@ -332,6 +332,28 @@ def matmul_nbits_group_dev(weights, a_ptr: int, m: int, y_ptrs, ctx: Context | N
     check(lib.mg_matmul_nbits_group_dev(ctx.handle, n, ws, C.c_void_p(a_ptr), m, ys))
 
 
+def matmul_nbits_group_split_dev(weights, a_ptr: int, split_ptr: int | None, m: int, y_ptrs,
+                                 ctx: Context | None = None):
+    """matmul_nbits_group_dev with the decode GEMV's split activations written
+    by a_ptr's producer (skip_rms_norm_f32_split_dev): the GEMV's own
+    prepass is skipped; results are bitwise the same."""
+    ctx = ctx or weights[0].ctx
+    n = len(weights)
+    ws = (C.c_void_p * n)(*[w.handle.value if isinstance(w.handle, C.c_void_p) else w.handle
+                            for w in weights])
+    ys = (C.c_void_p * n)(*[C.c_void_p(p).value for p in y_ptrs])
+    check(lib.mg_matmul_nbits_group_split_dev(ctx.handle, n, ws, C.c_void_p(a_ptr),
+                                              C.c_void_p(split_ptr) if split_ptr else None, m,
+                                              ys))
+
+
+def nbits_split_bytes(k: int, block_size: int) -> int:
+    """Bytes of a split activation buffer for rows of k elements."""
+    out = C.c_size_t(0)
+    check(lib.mg_nbits_split_bytes(int(k), int(block_size), C.byref(out)))
+    return out.value
+
+
 def _zp_arg(z):
     if z is None:
         return None, 0
@@ -529,6 +551,22 @@ def rms_norm_f32_dev(x_ptr: int, shape, gamma_ptr: int, gamma_len: int, axis: in
     check(lib.mg_rms_norm_f32_dev(ctx.handle, C.c_void_p(x_ptr), _ptr(sh), sh.size,
                                   C.c_void_p(gamma_ptr), int(gamma_len), int(axis), float(eps),
                                   C.c_void_p(y_ptr)))
+
+
+def skip_rms_norm_f32_split_dev(x_ptr: int, skip_ptr: int | None, shape, gamma_ptr: int,
+                                gamma_len: int, bias_ptr: int | None, eps: float, y_ptr: int,
+                                sum_ptr: int | None, block_size: int, split_ptr: int,
+                                ctx: Context | None = None):
+    """SkipSimplifiedLayerNormalization (or RMSNorm over the last axis when
+    skip_ptr is None) that also writes the decode GEMV's split activations of
+    y (rows <= 16, last dim <= 8192)."""
+    ctx = ctx or default_context()
+    sh = np.ascontiguousarray(np.array(shape, np.int64))
+    check(lib.mg_skip_rms_norm_f32_split_dev(
+        ctx.handle, C.c_void_p(x_ptr), C.c_void_p(skip_ptr) if skip_ptr else None, _ptr(sh),
+        sh.size, C.c_void_p(gamma_ptr), int(gamma_len),
+        C.c_void_p(bias_ptr) if bias_ptr else None, float(eps), C.c_void_p(y_ptr),
+        C.c_void_p(sum_ptr) if sum_ptr else None, int(block_size), C.c_void_p(split_ptr)))
 
 
 def skip_rms_norm_f32_dev(x_ptr: int, skip_ptr: int, shape, gamma_ptr: int, gamma_len: int,
