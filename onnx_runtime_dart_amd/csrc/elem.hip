@@ -17,6 +17,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <initializer_list>
 
 #include "mg_internal.h"
 
@@ -72,8 +73,9 @@ __global__ __launch_bounds__(256) void k_sigmoid(const float *x, float *y, int64
   y[i] = (float)(1.0 / (1.0 + exp(-(double)x[i])));
 }
 
-// Fixed-order double sum over the 256 threads of a workgroup (shuffles within
-// each wave, then the four wave sums in wave order).  Every thread gets it.
+// Fixed-order double sum over the NT threads of a workgroup (shuffles within
+// each wave, then the wave sums in wave order).  Every thread gets it.
+template <int NT>
 __device__ inline double block_sum(double v, double *red) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
@@ -81,21 +83,42 @@ __device__ inline double block_sum(double v, double *red) {
   __syncthreads();  // red may still be read from a previous call
   if ((t & 63) == 0) red[t >> 6] = v;
   __syncthreads();
-  return ((red[0] + red[1]) + red[2]) + red[3];
+  double r = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; w++) r += red[w];
+  return r;
 }
 
-// RMSNorm over the last axis: one workgroup per row of d elements.  With a
-// skip input the row is s = x + skip (f32), written to sum when asked; with
-// a bias, out = normed + bias (f32), as the reference's Add after the norm.
-// Thread t owns elements t, t + 256, ...: with P > 0 (d <= 256 P) it keeps
-// them in registers between the sum of squares and the output, so the row
-// is read once; P = 0 walks the row twice.  Any of x, skip, sum and y may be
-// the same buffer (an in-place residual): each element is read and written
-// by one thread only, and with P = 0, once sum holds s the second pass reads
-// s back from it instead of re-adding x and skip.  With ybuf, y is also
-// staged there (the split producer) and *mx receives the largest finite |y|
-// of the thread's elements.
-template <int P>
+// W consecutive floats (W = 4: one 16-byte access).
+template <int W>
+__device__ inline void ld_w(const float *p, float (&v)[W]) {
+  if constexpr (W == 4) {
+    const float4 q = *reinterpret_cast<const float4 *>(p);
+    v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
+  } else {
+    v[0] = p[0];
+  }
+}
+template <int W>
+__device__ inline void st_w(float *p, const float (&v)[W]) {
+  if constexpr (W == 4) *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  else p[0] = v[0];
+}
+
+// RMSNorm over the last axis: one workgroup of NT threads per row of d
+// elements.  With a skip input the row is s = x + skip (f32), written to sum
+// when asked; with a bias, out = normed + bias (f32), as the reference's Add
+// after the norm.  With P > 0 thread t owns P slots of W elements, slot i at
+// W (t + NT i) (W = 4: float4 accesses; the host takes it when d % 4 == 0
+// and every buffer is 16-byte aligned), and keeps them, with their gamma and
+// bias, in registers between the sum of squares and the output: the row is
+// read once.  P = 0 walks the row twice, one element per thread per step.
+// Any of x, skip, sum and y may be the same buffer (an in-place residual):
+// each element is read and written by one thread only, and with P = 0, once
+// sum holds s the second pass reads s back from it instead of re-adding x
+// and skip.  With ybuf, y is also staged there (the split producer) and *mx
+// receives the largest finite |y| of the thread's elements.
+template <int NT, int P, int W>
 __device__ inline void rms_row(const float *x, const float *skip,
                                const float *__restrict__ gamma, const float *__restrict__ bias,
                                double eps, int64_t d, float *y, float *sum, double *red,
@@ -103,27 +126,59 @@ __device__ inline void rms_row(const float *x, const float *skip,
   const int64_t base = (int64_t)blockIdx.x * d;
   const int t = threadIdx.x;
   double ss = 0;
-  float v[P > 0 ? P : 1];
+  float m = 0.f;
+  auto keep = [&](int64_t j, const auto &o) __attribute__((always_inline)) {
+    if (ybuf) {
+      st_w(ybuf + j, o);
+      for (float f : o) m = fabsf(f) < INFINITY ? fmaxf(m, fabsf(f)) : m;  // finite values only
+    }
+  };
   if constexpr (P > 0) {
+    float v[P][W], g[P][W], b[P][W];
 #pragma unroll
     for (int i = 0; i < P; i++) {
-      const int64_t j = t + 256 * i;
-      v[i] = 0.f;
-      if (j < d) {
-        v[i] = x[base + j];
-        if (skip) v[i] = v[i] + skip[base + j];
+      const int64_t j = (int64_t)W * (t + NT * i);
+#pragma unroll
+      for (int c = 0; c < W; c++) v[i][c] = g[i][c] = b[i][c] = 0.f;
+      if (j < d) {  // d % W == 0: the whole slot is in the row
+        ld_w<W>(x + base + j, v[i]);
+        ld_w<W>(gamma + j, g[i]);
+        if (bias) ld_w<W>(bias + j, b[i]);
+        if (skip) {
+          float k[W];
+          ld_w<W>(skip + base + j, k);
+#pragma unroll
+          for (int c = 0; c < W; c++) v[i][c] = v[i][c] + k[c];
+        }
       }
     }
 #pragma unroll
     for (int i = 0; i < P; i++) {
-      const int64_t j = t + 256 * i;
+      const int64_t j = (int64_t)W * (t + NT * i);
       if (j < d) {
-        if (skip && sum) sum[base + j] = v[i];
-        ss += (double)v[i] * (double)v[i];
+        if (skip && sum) st_w<W>(sum + base + j, v[i]);
+#pragma unroll
+        for (int c = 0; c < W; c++) ss += (double)v[i][c] * (double)v[i][c];
+      }
+    }
+    ss = block_sum<NT>(ss, red);
+    const double inv = 1.0 / sqrt(ss / (double)d + eps);
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+      const int64_t j = (int64_t)W * (t + NT * i);
+      if (j < d) {
+        float o[W];
+#pragma unroll
+        for (int c = 0; c < W; c++) {
+          o[c] = (float)((double)v[i][c] * inv * (double)g[i][c]);
+          if (bias) o[c] = o[c] + b[i][c];
+        }
+        st_w<W>(y + base + j, o);
+        keep(j, o);
       }
     }
   } else {
-    for (int64_t j = t; j < d; j += 256) {
+    for (int64_t j = t; j < d; j += NT) {
       float w = x[base + j];
       if (skip) {
         w = w + skip[base + j];
@@ -131,43 +186,29 @@ __device__ inline void rms_row(const float *x, const float *skip,
       }
       ss += (double)w * (double)w;
     }
-  }
-  ss = block_sum(ss, red);
-  const double inv = 1.0 / sqrt(ss / (double)d + eps);
-  float m = 0.f;
-  auto out = [&](int64_t j, float w) __attribute__((always_inline)) {
-    float o = (float)((double)w * inv * (double)gamma[j]);
-    if (bias) o = o + bias[j];
-    y[base + j] = o;
-    if (ybuf) {
-      ybuf[j] = o;
-      const float f = fabsf(o);
-      m = f < INFINITY ? fmaxf(m, f) : m;  // finite values only
-    }
-  };
-  if constexpr (P > 0) {
-#pragma unroll
-    for (int i = 0; i < P; i++)
-      if (t + 256 * i < d) out(t + 256 * i, v[i]);
-  } else {
-    for (int64_t j = t; j < d; j += 256) {
+    ss = block_sum<NT>(ss, red);
+    const double inv = 1.0 / sqrt(ss / (double)d + eps);
+    for (int64_t j = t; j < d; j += NT) {
       float w;
       if (skip && sum) w = sum[base + j];
       else if (skip) w = x[base + j] + skip[base + j];
       else w = x[base + j];
-      out(j, w);
+      float o[1] = {(float)((double)w * inv * (double)gamma[j])};
+      if (bias) o[0] = o[0] + bias[j];
+      y[base + j] = o[0];
+      keep(j, o);
     }
   }
   if (mx) *mx = m;
 }
 
-template <int P>
-__global__ __launch_bounds__(256) void k_rms_last(const float *x, const float *skip,
-                                                  const float *__restrict__ gamma,
-                                                  const float *__restrict__ bias, double eps,
-                                                  int64_t d, float *y, float *sum) {
-  __shared__ double red[4];
-  rms_row<P>(x, skip, gamma, bias, eps, d, y, sum, red, nullptr, nullptr);
+template <int NT, int P, int W>
+__global__ __launch_bounds__(NT) void k_rms_last(const float *x, const float *skip,
+                                                 const float *__restrict__ gamma,
+                                                 const float *__restrict__ bias, double eps,
+                                                 int64_t d, float *y, float *sum) {
+  __shared__ double red[NT / 64];
+  rms_row<NT, P, W>(x, skip, gamma, bias, eps, d, y, sum, red, nullptr, nullptr);
 }
 
 // RMSNorm over another axis: one thread per (outer, inner) slice, walking the
@@ -214,7 +255,8 @@ __global__ __launch_bounds__(256) void k_rms_axis(const float *x,
 typedef _Float16 half8e __attribute__((ext_vector_type(8)));
 constexpr int SPLIT_MAXD = 8192;  // longest row the producers stage in LDS
 
-// Block-wide maximum (every thread gets it); red holds 4 floats.
+// Block-wide maximum over NT threads (every thread gets it); red holds NT / 64.
+template <int NT>
 __device__ inline float block_max(float v, float *red) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
@@ -222,15 +264,20 @@ __device__ inline float block_max(float v, float *red) {
   __syncthreads();
   if ((t & 63) == 0) red[t >> 6] = v;
   __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; w++) r = fmaxf(r, red[w]);
+  return r;
 }
 
 // Row `row` of the split from the d values staged in ybuf (mx: the largest
-// finite |y| of this thread's elements).  256 threads; octets up to kpad / 8.
+// finite |y| of this thread's elements; the barrier in block_max makes every
+// thread's ybuf stores visible).  NT threads; octets up to kpad / 8.
+template <int NT>
 __device__ inline void write_split_row(const float *ybuf, int64_t d, int64_t kpad, float mx,
                                        int row, uint4 *__restrict__ ahl, int *__restrict__ texp,
                                        float *red) {
-  mx = block_max(mx, red);
+  mx = block_max<NT>(mx, red);
   int e = 0;
   if (mx > 0.f) {
     int ex;
@@ -239,7 +286,7 @@ __device__ inline void write_split_row(const float *ybuf, int64_t d, int64_t kpa
   }
   const int t = threadIdx.x;
   if (t == 0) texp[row] = e;
-  for (int64_t o = t; o < kpad / 8; o += 256) {
+  for (int64_t o = t; o < kpad / 8; o += NT) {
     half8e hi, lo;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -258,27 +305,55 @@ __device__ inline void write_split_row(const float *ybuf, int64_t d, int64_t kpa
   }
 }
 
-// RMSNorm over the last axis (k_rms_last's arithmetic, element for element)
-// writing y, the optional sum, and the split of y.  One workgroup per row,
-// rows < 16, d <= SPLIT_MAXD.
-template <int P>
-__global__ __launch_bounds__(256) void k_rms_last_split(
+// RMSNorm over the last axis (k_rms_last's arithmetic and plan, element for
+// element) writing y, the optional sum, and the split of y.  One workgroup
+// per row, at most 16 rows, d <= SPLIT_MAXD.
+template <int NT, int P, int W>
+__global__ __launch_bounds__(NT) void k_rms_last_split(
     const float *x, const float *skip, const float *__restrict__ gamma,
     const float *__restrict__ bias, double eps, int64_t d, float *y, float *sum, int64_t kpad,
     uint4 *__restrict__ ahl, int *__restrict__ texp) {
-  __shared__ double red[4];
-  __shared__ float redf[4];
+  __shared__ double red[NT / 64];
+  __shared__ float redf[NT / 64];
   __shared__ float ybuf[SPLIT_MAXD];
   float mx;
-  rms_row<P>(x, skip, gamma, bias, eps, d, y, sum, red, ybuf, &mx);
-  write_split_row(ybuf, d, kpad, mx, (int)blockIdx.x, ahl, texp, redf);
+  rms_row<NT, P, W>(x, skip, gamma, bias, eps, d, y, sum, red, ybuf, &mx);
+  write_split_row<NT>(ybuf, d, kpad, mx, (int)blockIdx.x, ahl, texp, redf);
 }
 
 inline unsigned blocks(int64_t n, int64_t per) { return (unsigned)((n + per - 1) / per); }
 
-// Elements per thread kept in registers for a row of d (0: two passes).
-inline int rms_regs(int64_t d) {
-  return d <= 256 ? 1 : d <= 1024 ? 4 : d <= 2048 ? 8 : d <= 4096 ? 16 : 0;
+template <int NT_, int P_, int W_>
+struct RmsPlan {
+  static constexpr int NT = NT_, P = P_, W = W_;
+};
+
+// The row norm's plan for rows of d: float4 slots when d % 4 == 0 and every
+// buffer is 16-byte aligned (vec), with enough threads for one or a few
+// slots each; else one element per slot; rows too long for registers walk
+// twice.  The plain and the split kernel take the same plan, so their y
+// are bitwise equal.
+template <class F>
+void rms_dispatch(int64_t d, bool vec, F &&f) {
+  if (vec && d % 4 == 0) {
+    const int64_t q = d / 4;
+    if (q <= 256) return f(RmsPlan<256, 1, 4>{});
+    if (q <= 512) return f(RmsPlan<512, 1, 4>{});
+    if (q <= 1024) return f(RmsPlan<1024, 1, 4>{});
+    if (q <= 2048) return f(RmsPlan<1024, 2, 4>{});
+    if (q <= 4096) return f(RmsPlan<1024, 4, 4>{});
+  }
+  if (d <= 256) return f(RmsPlan<256, 1, 1>{});
+  if (d <= 1024) return f(RmsPlan<256, 4, 1>{});
+  if (d <= 2048) return f(RmsPlan<256, 8, 1>{});
+  if (d <= 4096) return f(RmsPlan<256, 16, 1>{});
+  f(RmsPlan<256, 0, 1>{});
+}
+
+bool aligned16(std::initializer_list<const void *> ps) {
+  for (const void *p : ps)
+    if (reinterpret_cast<uintptr_t>(p) % 16) return false;  // null passes
+  return true;
 }
 
 }  // namespace
@@ -327,17 +402,11 @@ mg_status mg_elem_rms_norm(mg_ctx *ctx, const float *x, const float *skip, const
                            int64_t inner, int64_t last, float *y, float *sum) {
   if (outer * dim * inner == 0) return MG_OK;
   if (inner == 1) {  // the caller keeps rows (outer) below 2^31
-#define MG_RMS(P_)                                                                           \
-  hipLaunchKernelGGL((k_rms_last<P_>), dim3((unsigned)outer), dim3(256), 0, ctx->stream, x, \
-                     skip, gamma, bias, eps, dim, y, sum)
-    switch (rms_regs(dim)) {
-      case 1: MG_RMS(1); break;
-      case 4: MG_RMS(4); break;
-      case 8: MG_RMS(8); break;
-      case 16: MG_RMS(16); break;
-      default: MG_RMS(0); break;
-    }
-#undef MG_RMS
+    rms_dispatch(dim, aligned16({x, skip, gamma, bias, y, sum}), [&](auto plan) {
+      using C = decltype(plan);
+      hipLaunchKernelGGL((k_rms_last<C::NT, C::P, C::W>), dim3((unsigned)outer), dim3(C::NT), 0,
+                         ctx->stream, x, skip, gamma, bias, eps, dim, y, sum);
+    });
     return mg_launch_check("k_rms_last");
   }
   hipLaunchKernelGGL(k_rms_axis, dim3(blocks(outer * inner, 256)), dim3(256), 0, ctx->stream, x,
@@ -351,16 +420,10 @@ mg_status mg_elem_rms_norm_split(mg_ctx *ctx, const float *x, const float *skip,
   if (rows == 0 || d == 0) return MG_OK;
   uint4 *ahl = static_cast<uint4 *>(split);
   int *texp = reinterpret_cast<int *>(static_cast<char *>(split) + mg_align((size_t)16 * kpad * 4));
-#define MG_RMS(P_)                                                                        \
-  hipLaunchKernelGGL((k_rms_last_split<P_>), dim3((unsigned)rows), dim3(256), 0, ctx->stream, \
-                     x, skip, gamma, bias, eps, d, y, sum, kpad, ahl, texp)
-  switch (rms_regs(d)) {
-    case 1: MG_RMS(1); break;
-    case 4: MG_RMS(4); break;
-    case 8: MG_RMS(8); break;
-    case 16: MG_RMS(16); break;
-    default: MG_RMS(0); break;
-  }
-#undef MG_RMS
+  rms_dispatch(d, aligned16({x, skip, gamma, bias, y, sum}), [&](auto plan) {
+    using C = decltype(plan);
+    hipLaunchKernelGGL((k_rms_last_split<C::NT, C::P, C::W>), dim3((unsigned)rows), dim3(C::NT),
+                       0, ctx->stream, x, skip, gamma, bias, eps, d, y, sum, kpad, ahl, texp);
+  });
   return mg_launch_check("k_rms_last_split");
 }

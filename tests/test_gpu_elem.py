@@ -145,6 +145,42 @@ def test_skip_rms_norm(ops, rows, d, with_bias):
     assert ulps(y, y_ref) <= 1
 
 
+@pytest.mark.parametrize("d", [1022, 2046, 4094, 5001, 12000, 20000, 2048])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_skip_rms_norm_row_plans(ops, d, offset):
+    # The row kernel's plans: float4 slots for rows of d % 4 == 0 on 16-byte
+    # aligned buffers (1 to 4 slots per thread), one element per slot for
+    # other rows or buffers one float off alignment (4 to 16 per thread), and
+    # two passes over rows too long for registers (5001 unaligned, 20000).
+    rng = np.random.default_rng(8 + d + offset)
+    rows = 3
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    skip = rng.standard_normal((rows, d)).astype(np.float32)
+    g = rng.uniform(0.5, 2.0, d).astype(np.float32)
+    bias = rng.standard_normal(d).astype(np.float32)
+    D = ops.DeviceBuffer
+    n = rows * d
+
+    def placed(a):  # a's elements from float `offset` of a buffer of n + 1
+        buf = np.zeros(n + 1, np.float32)
+        buf[offset:offset + n] = a.ravel()
+        return D.from_array(buf)
+
+    bufs = [placed(x), placed(skip), placed(np.zeros(n, np.float32)),
+            placed(np.zeros(n, np.float32))]
+    px, pskip, py, psum = (b.ptr + 4 * offset for b in bufs)
+    bg, bb = D.from_array(g), D.from_array(bias)
+    ops.skip_rms_norm_f32_dev(px, pskip, (rows, d), bg.ptr, d, bb.ptr, 1e-5, py, psum)
+    y, s = (b.to_array(n + 1, np.float32)[offset:offset + n].reshape(rows, d)
+            for b in bufs[2:])
+    s_ref = oracle.binary_f32("add", x, skip)
+    np.testing.assert_array_equal(s, s_ref)
+    y_ref = oracle.binary_f32("add", oracle.rms_norm_f32(s_ref, g, -1, 1e-5), bias)
+    assert ulps(y, y_ref) <= 1
+    for b in (*bufs, bg, bb):
+        b.free()
+
+
 @pytest.mark.parametrize("alias", ["sum=x", "sum=skip", "y=x", "y=skip", "y=sum",
                                    "sum=x,y=skip", "y=x,no-sum"])
 def test_skip_rms_norm_in_place(ops, alias):
