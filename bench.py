@@ -224,12 +224,12 @@ def main():
                     help="headline and lm_head measurements only")
     ap.add_argument("--only", default=None,
                     choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1", "llama16",
-                             "attn", "conv", "pass512", "dec1", "dec4", "dec16"],
+                             "attn", "conv", "qconv", "pass512", "dec1", "dec4", "dec16"],
                     help="profiling mode: launch one workload --steps times and exit "
                          "(lm512 / lm1: Qwen3 lm_head MatMulNBits at M=512 / M=1; i8lm512: "
                          "the lm_head as MatMulInteger at M=512; f32ffn: the MiniLM FFN1 "
                          "Gemm; llama1 / llama16: the Llama lm_head at M=1 / M=16; attn: the MiniLM "
-                         "fused attention; conv: the ResNet-50 3x3 conv; pass512: the headline "
+                         "fused attention; conv / qconv: the ResNet-50 3x3 conv as Conv / QLinearConv; pass512: the headline "
                          "M=512 pass of eight Qwen3 projections, grouped as timed; dec1 / dec4 / "
                          "dec16: the grouped Llama-style decode step at M=1 / 4 / 16; copy: 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
@@ -905,8 +905,8 @@ def conv_family(torch, ops, ctx, T, randn, dev, args):
     tf = conv_flops(xs, ws, ys) / (ms / 1e3) / 1e12
     out["qlinear_conv_resnet50_3x3_256"] = {
         "us": round(ms * 1e3, 2), "TOP/s": round(tf, 2),
-        "note": "integer operands on fp32 MFMA (exact); includes the per-call upload of the "
-                "per-channel requant table and its stream wait"}
+        "note": "int8 MFMA GEMM over a byte im2col (exact int32 sums); includes the per-call "
+                "filter prepack and the upload of the per-channel requant table"}
     print(f"# conv: {out}", file=sys.stderr, flush=True)
     return out
 
@@ -1077,6 +1077,17 @@ def run_only(args, torch, ops, ctx, stream, dev, randn):
             w = None
             for _ in range(args.steps):
                 ops.conv_f32_dev(x.data_ptr(), xs, wt.data_ptr(), ws, y.data_ptr(), ctx=ctx, **at)
+        elif args.only == "qconv":
+            xs, ws, at = RESNET_3X3
+            x = torch.randint(0, 256, xs, device=dev, dtype=torch.uint8)
+            wt = torch.randint(-128, 128, ws, device=dev, dtype=torch.int8)
+            y = torch.empty(ops.conv_output_shape(xs, ws, **at), device=dev, dtype=torch.uint8)
+            wsc = rng.uniform(0.002, 0.02, ws[0]).astype(np.float32)
+            wz = np.zeros(ws[0], np.int8)
+            w = None
+            for _ in range(args.steps):
+                ops.qlinear_conv_dev(x.data_ptr(), False, xs, 0.05, 128, wt.data_ptr(), True, ws,
+                                     wsc, wz, 4.0, 128, y.data_ptr(), lo=0, hi=255, ctx=ctx, **at)
         elif args.only == "attn":
             dh = MINILM_H // MINILM_HEADS
             q = randn(MINILM_B, MINILM_HEADS, MINILM_S, dh)

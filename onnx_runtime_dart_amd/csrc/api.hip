@@ -1863,7 +1863,7 @@ mg_status conv_launch(mg_ctx *ctx, mg_conv_problem p, const std::vector<float> &
                       const std::vector<double> &mult, size_t wz_off, size_t mult_off,
                       size_t phase_off) {
   char *base = static_cast<char *>(ctx->ws);
-  if (!wz.empty()) {
+  if (!wz.empty() && !mg_conv_int8_route(p)) {
     MG_TRY(mg_h2d_table(ctx, base + wz_off, wz.data(), wz.size() * 4));
     p.w_zp = reinterpret_cast<const float *>(base + wz_off);
   }
@@ -2027,6 +2027,8 @@ mg_status mg_conv_integer(mg_ctx *ctx, const void *x, int32_t x_signed, const in
   int64_t ys[5];
   MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, 0, &p, ys));
   conv_int_kinds(&p, x_signed, w_signed);
+  p.w_zp_host = w_zp;
+  p.w_zp_len = w_zp ? w_zp_len : 0;
   p.mode = MG_CONV_OUT_I32;
   p.x_zp = x_zp;
   std::vector<float> wz;
@@ -2049,6 +2051,8 @@ mg_status mg_conv_integer_dev(mg_ctx *ctx, const void *x_dev, int32_t x_signed,
   int64_t ys[5];
   MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, 0, &p, ys));
   conv_int_kinds(&p, x_signed, w_signed);
+  p.w_zp_host = w_zp;
+  p.w_zp_len = w_zp ? w_zp_len : 0;
   p.mode = MG_CONV_OUT_I32;
   p.x_zp = x_zp;
   std::vector<float> wz;
@@ -2073,6 +2077,8 @@ mg_status mg_qlinear_conv(mg_ctx *ctx, const void *x, int32_t x_signed, const in
   int64_t ys[5];
   MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, 0, &p, ys));
   conv_int_kinds(&p, x_signed, w_signed);
+  p.w_zp_host = w_zp;
+  p.w_zp_len = w_zp ? w_zp_len : 0;
   p.mode = MG_CONV_OUT_Q8;
   p.x_zp = x_zp;
   p.y_zp = y_zp;
@@ -2101,6 +2107,8 @@ mg_status mg_qlinear_conv_dev(mg_ctx *ctx, const void *x_dev, int32_t x_signed,
   int64_t ys[5];
   MG_TRY(plan_conv(x_shape, x_rank, w_shape, x_rank, strides, pads, dilations, group, 0, &p, ys));
   conv_int_kinds(&p, x_signed, w_signed);
+  p.w_zp_host = w_zp;
+  p.w_zp_len = w_zp ? w_zp_len : 0;
   p.mode = MG_CONV_OUT_Q8;
   p.x_zp = x_zp;
   p.y_zp = y_zp;

@@ -1,6 +1,8 @@
 // Convolution family on gfx950 fp32 MFMA (v_mfma_f32_32x32x2_f32) as an
 // implicit GEMM: no im2col buffer is written; the workgroup gathers its
-// operand tiles straight from the NC* tensors into LDS.
+// operand tiles straight from the NC* tensors into LDS.  ConvInteger and
+// QLinearConv with one group take the int8 MFMA GEMM over a byte im2col
+// instead (below); grouped integer convolutions stay on this kernel.
 //
 // Reference semantics:
 //   Conv          lib/src/onnx_nn_ops.dart:179-817 (pads resolved by
@@ -46,6 +48,7 @@ namespace {
 
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef int int16v __attribute__((ext_vector_type(16)));
+typedef int int4v __attribute__((ext_vector_type(4)));
 
 // Element e of a byte tensor as an integer (u8 or i8 by a uniform kind).
 __device__ inline int load_int(const uint8_t *p, int64_t i, int kind) {
@@ -432,9 +435,296 @@ void launch_conv(const mg_conv_problem &p, bool big, int64_t out_sp, hipStream_t
   hipLaunchKernelGGL((k_conv<1, 32, TR, INT>), grid, dim3(256), 0, st, p, (int)pix_tiles, tb);
 }
 
+// ------------------------------------- integer convolution on int8 MFMA
+//
+// ConvInteger / QLinearConv with one group (forward) run as MatMulInteger's
+// int8 MFMA GEMM (int8.hip, exact int32 sums with the zero points taken out
+// as row / column sum terms) over an im2col of the input, gathered straight
+// into the GEMM's operand fragments:
+//   A[b * O + o][k] = x[b][c][position of tap r at output o]  (k = c * taps + r)
+//                     or the byte x_zp where the tap falls in the padding,
+//   B[k][m]         = w[m][k]  (prepacked per call from the filter as laid out),
+//   C[b * O + o][m] = sum_k (A - x_zp)(B - w_zp[m])   (int32),
+// so a padded tap contributes (x_zp - x_zp) (w - w_zp) = 0, as in the
+// reference's loop, which skips it.  The epilogue transposes C into
+// y[b][m][o] through LDS and, for QLinearConv, requantises each sum as the
+// fp32-MFMA kernel does (bias, double multiplier, round half to even).
+
+// The GEMM's A operand gathered straight from the input, in the layout
+// MatMulInteger's prepass (k_i8_prep_a) writes: per 32-row tile m32 and
+// 32-k fragment q, lane l (row 32 m32 + l % 32) holds the 16 bytes at k =
+// 128 (q / 4) + 64 (l / 32) + 16 (q % 4), re-centred to signed (u8 ^ 0x80),
+// zero for k >= K or rows past the last; plus the row sums of those bytes
+// over k < K and ca = (x signed ? 0 : 128) - x_zp.  A row is an output
+// position (b, o); byte k = (channel c, tap r) is the input at the tap's
+// position, or x_zp where that lies in the padding.
+// Workgroup = 64 rows (two row tiles) and one of CONV_FRAG_GROUPS groups of
+// 16-k chunks, 4 waves; thread = one row, and wave w of group g takes the
+// chunks ch = 4 g + w (mod 4 CONV_FRAG_GROUPS), so the chunk's channel and
+// tap offsets (from tab, built by k_conv_tab_i8) are the same for the
+// whole wave (scalar loads); each thread stores
+// its 16 bytes into its fragment's lane.  The row sums meet in LDS, then in
+// rowsum by integer atomics (exact in any order; rowsum zeroed first by
+// k_conv_tab_i8).  32-bit index arithmetic: the plan keeps every index
+// below 2^31.
+constexpr int CONV_FRAG_WAVES = 4, CONV_FRAG_GROUPS = 16;
+__global__ __launch_bounds__(64 * CONV_FRAG_WAVES) void k_conv_frag_i8(
+    const mg_conv_problem p, int K, int O, int rows, int rows_pad, int kqp,
+    const int2 *__restrict__ tab, int4v *__restrict__ afrag, int32_t *__restrict__ rowsum,
+    int32_t *__restrict__ ca) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int grp = blockIdx.y;
+  constexpr int STRIDE = CONV_FRAG_WAVES * CONV_FRAG_GROUPS;  // between a wave's chunks
+  const int row = blockIdx.x * 64 + lane;
+  const bool live = row < rows;
+  const int b = live ? row / O : 0, o = live ? row - b * O : 0;
+  const int out1 = (int)p.out[1], out2 = (int)p.out[2];
+  const int oz = o / (out1 * out2), oy = (o / out2) % out1, ox = o % out2;
+  const int in0 = (int)p.in[0], in1 = (int)p.in[1], in2 = (int)p.in[2];
+  const int bz = oz * (int)p.str[0] - (int)p.pad[0], by0 = oy * (int)p.str[1] - (int)p.pad[1],
+            bx = ox * (int)p.str[2] - (int)p.pad[2];
+  const int in_sp = in0 * in1 * in2;
+  // Taps whose input position lies inside this row's window (bit r of inw).
+  const int kd = (int)p.ker[0], kh = (int)p.ker[1], kw = (int)p.ker[2];
+  uint64_t inw = 0;
+  for (int r = 0, kz = 0; kz < kd; kz++)
+    for (int ky = 0; ky < kh; ky++)
+      for (int kx = 0; kx < kw; kx++, r++) {
+        const int iz = bz + kz * (int)p.dil[0], iy = by0 + ky * (int)p.dil[1],
+                  ix = bx + kx * (int)p.dil[2];
+        if ((unsigned)iz < (unsigned)in0 && (unsigned)iy < (unsigned)in1 &&
+            (unsigned)ix < (unsigned)in2)
+          inw |= 1ull << r;
+      }
+  if (!live) inw = 0;
+  // Byte loads through a buffer resource over x: an offset past its end reads
+  // 0 without a memory access (taps outside the window).
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void *>(p.x), (short)0, (int)(p.n * p.c * in_sp), 0x00020000);
+  const int org = b * (int)p.c * in_sp + (bz * in1 + by0) * in2 + bx;  // may lie outside
+  const uint32_t flip = p.xk == MG_CONV_I8 ? 0u : 0x80u;
+  const uint8_t zb = (uint8_t)((p.x_zp & 0xFF) ^ flip);
+  const int nchunk = kqp * 2;  // 16-k chunks up to kpad
+  int s = 0;
+  // Two chunks per pass, all 32 byte loads issued before any is used.
+  for (int ch0 = grp * CONV_FRAG_WAVES + wave; ch0 < nchunk; ch0 += 2 * STRIDE) {
+    uint8_t raw[2][16];
+    uint32_t okm[2] = {0u, 0u};
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int k0 = min((ch0 + u * STRIDE) * 16, nchunk * 16 - 16);  // wave-uniform
+      int4 te[8];  // entries k0 .. k0 + 15 (the table runs to kpad)
+#pragma unroll
+      for (int j2 = 0; j2 < 8; j2++) te[j2] = reinterpret_cast<const int4 *>(tab + k0)[j2];
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int toff = (e & 1) ? te[e >> 1].z : te[e >> 1].x;
+        const int tr = (e & 1) ? te[e >> 1].w : te[e >> 1].y;  // tap; 64 past K
+        const bool ok = tr < 64 && ((inw >> (tr & 63)) & 1ull);
+        raw[u][e] = (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(
+            rx, ok ? (unsigned)(org + toff) : 0x7ffffff0u, 0, 0);
+        okm[u] |= (uint32_t)ok << e;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int ch = ch0 + u * STRIDE;
+      if (ch >= nchunk) break;
+      const int k0 = ch * 16;
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        // in the window: the byte; in the padding (k < K): x_zp; k >= K or a dead row: 0
+        const uint8_t v = ((okm[u] >> e) & 1u) ? (uint8_t)(raw[u][e] ^ flip)
+                          : (live && k0 + e < K) ? zb : (uint8_t)0;
+        w[e >> 2] |= (uint32_t)v << (8 * (e & 3));
+      }
+      const int4v v = (int4v){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      s = __builtin_amdgcn_sdot4(v.x, 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(v.y, 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(v.z, 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
+      if (row < rows_pad) {
+        const int q = (k0 >> 7) * 4 + ((k0 >> 4) & 3), fl = (row & 31) + 32 * ((k0 >> 6) & 1);
+        afrag[((int64_t)(row >> 5) * kqp + q) * 64 + fl] = v;
+      }
+    }
+  }
+  __shared__ int red[CONV_FRAG_WAVES][64];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (t < 64 && row < rows_pad) {
+    int tot = 0;
+#pragma unroll
+    for (int wv = 0; wv < CONV_FRAG_WAVES; wv++) tot += red[wv][t];
+    atomicAdd(&rowsum[row], tot);
+    if (grp == 0) ca[row] = (p.xk == MG_CONV_I8 ? 0 : 128) - p.x_zp;
+  }
+}
+
+// Tap table of the gather: tab[k] = {c * in_sp + (dz * in1 + dy) * in2 + dx,
+// r} for k = (channel c, tap r = (kz, ky, kx)) < K, d* = k* * dilation, and
+// {0, 64} for K <= k < kpad; and rowsum zeroed for the gather's atomics.
+__global__ __launch_bounds__(256) void k_conv_tab_i8(const mg_conv_problem p, int K, int kpad,
+                                                     int2 *__restrict__ tab,
+                                                     int32_t *__restrict__ rowsum, int rows_pad) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < rows_pad) rowsum[i] = 0;
+  if (i >= kpad) return;
+  if (i >= K) {
+    tab[i] = make_int2(0, 64);
+    return;
+  }
+  const int kh = (int)p.ker[1], kw = (int)p.ker[2], k12 = kh * kw;
+  const int taps = (int)p.ker[0] * k12;
+  const int c = i / taps, r = i - c * taps;
+  const int dz = (r / k12) * (int)p.dil[0], dy = ((r / kw) % kh) * (int)p.dil[1],
+            dx = (r % kw) * (int)p.dil[2];
+  const int in1 = (int)p.in[1], in2 = (int)p.in[2];
+  const int in_sp = (int)p.in[0] * in1 * in2;
+  tab[i] = make_int2(c * in_sp + (dz * in1 + dy) * in2 + dx, r);
+}
+
+// C [rows][M] int32 -> y [n][M][O] through a 64 x 64 LDS tile: reads along
+// m, writes along o.  REQ: QLinearConv's requantisation, else the int32 sums.
+template <bool REQ>
+__global__ __launch_bounds__(256) void k_conv_i8_epi(const int32_t *__restrict__ c,
+                                                     const mg_conv_problem p, int64_t O,
+                                                     int64_t rows) {
+  __shared__ int32_t tile[64][65];
+  __shared__ double smult[64];
+  __shared__ int64_t sbias[64];
+  const int t = threadIdx.x, tx = t & 63, ty = t >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, m0 = (int64_t)blockIdx.y * 64;
+  const int64_t M = p.m;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int64_t r = r0 + 4 * i + ty, m = m0 + tx;
+    tile[4 * i + ty][tx] = (r < rows && m < M) ? c[r * M + m] : 0;
+  }
+  if constexpr (REQ) {  // the tile's channel constants, loaded once
+    if (t < 64 && m0 + t < M) {
+      smult[t] = p.mult[m0 + t];
+      sbias[t] = p.bias ? (int64_t) static_cast<const int32_t *>(p.bias)[m0 + t] : 0;
+    }
+  }
+  __syncthreads();
+  const int64_t r = r0 + tx;
+  if (r >= rows) return;
+  const int64_t b = r / O, o = r - b * O;  // once per thread: the tile row is fixed
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int64_t m = m0 + 4 * i + ty;
+    if (m >= M) continue;
+    const int32_t acc = tile[tx][4 * i + ty];
+    const int64_t oi = (b * M + m) * O + o;
+    if constexpr (REQ) {
+      const int64_t sum = (int64_t)acc + sbias[m - m0];
+      const double q = rint((double)sum * smult[m - m0]) + (double)p.y_zp;  // half to even
+      const double cl = fmin(fmax(q, (double)p.lo), (double)p.hi);
+      static_cast<uint8_t *>(p.y)[oi] = (uint8_t)(int)cl;
+    } else {
+      static_cast<int32_t *>(p.y)[oi] = acc;
+    }
+  }
+}
+
+// Sums of up to this many k stay exact in the int8 GEMM's int32 terms.
+constexpr int64_t CONV_I8_MAX_K = 33025;
+// Cap on the GEMM's K split (0: the int8 planner's choice).
+#ifndef MG_CONV_I8_MAX_KS
+#define MG_CONV_I8_MAX_KS 1
+#endif
+
+// 128-row GEMM tiles (the convolutions' C x taps x M products are narrow:
+// the 256-row tiles leave most CUs idle), and no K split: measured on the
+// ResNet-50 3 x 3 layer (6272 x 2304 x 256), the three-way split and its
+// reduction cost 30 + 11.4 us against 22.9 us unsplit with 256-row tiles.
+#ifndef MG_CONV_I8_SMALL_TILES
+#define MG_CONV_I8_SMALL_TILES 1
+#endif
+
+struct ConvI8Plan {
+  bool ok = false;
+  int64_t K = 0, O = 0, rows = 0;
+  mg_i8_a_layout a;
+  size_t off_w = 0, off_c = 0, off_tab = 0, off_g = 0, total = 0;
+};
+
+ConvI8Plan conv_i8_plan(const mg_conv_problem &p) {
+  ConvI8Plan q;
+  if (p.xk == MG_CONV_F32 || p.trans || p.phased || p.group != 1) return q;
+  const bool zp_byte = p.xk == MG_CONV_U8 ? (p.x_zp >= 0 && p.x_zp <= 255)
+                                          : (p.x_zp >= -128 && p.x_zp <= 127);
+  q.K = p.cg * p.ker[0] * p.ker[1] * p.ker[2];
+  q.O = p.out[0] * p.out[1] * p.out[2];
+  q.rows = p.n * q.O;
+  const int64_t lim = (int64_t)1 << 31;
+  // At most 64 taps (the gather's window mask), and x addressed with 32-bit offsets.
+  const bool taps_ok = p.ker[0] * p.ker[1] * p.ker[2] <= 64;
+  if (p.n * p.c * p.in[0] * p.in[1] * p.in[2] >= lim || !zp_byte || !taps_ok || q.K == 0 || q.K > CONV_I8_MAX_K || q.rows * q.K >= lim || q.K * p.m >= lim ||
+      q.rows * p.m >= lim || (q.rows + 63) / 64 > 0x7fffffff || (p.m + 63) / 64 > 65535)
+    return q;
+  q.a = mg_int8_a_layout(q.rows, q.K, p.m, MG_CONV_I8_MAX_KS, MG_CONV_I8_SMALL_TILES);
+  if ((int64_t)q.a.m32n * 32 * ((q.K + 255) / 256 * 256) >= lim) return q;
+  q.off_w = 0;
+  q.off_c = q.off_w + mg_align(mg_int8_weight_ws_bytes(q.K, p.m));
+  q.off_tab = q.off_c + mg_align((size_t)(q.rows * p.m) * 4);
+  q.off_g = q.off_tab + mg_align((size_t)((q.K + 255) / 256 * 256) * 8);
+  q.total = q.off_g + mg_align(q.a.total);
+  q.ok = true;
+  return q;
+}
+
+mg_status conv_i8_run(mg_ctx *ctx, const mg_conv_problem &p, const ConvI8Plan &q, void *ws) {
+  char *base = static_cast<char *>(ws);
+  int32_t *c = reinterpret_cast<int32_t *>(base + q.off_c);
+  char *g = base + q.off_g;
+  hipStream_t st = ctx->stream;
+  const int rows_pad = q.a.m32n * 32;
+  int32_t *rowsum = reinterpret_cast<int32_t *>(g + q.a.off_rs);
+  int2 *tab = reinterpret_cast<int2 *>(base + q.off_tab);
+  const int kpad = q.a.kqp * 32;
+  const int ntab = std::max(rows_pad, kpad);
+  hipLaunchKernelGGL(k_conv_tab_i8, dim3((unsigned)((ntab + 255) / 256)), dim3(256), 0, st, p,
+                     (int)q.K, kpad, tab, rowsum, rows_pad);
+  MG_TRY(mg_launch_check("k_conv_tab_i8"));
+  hipLaunchKernelGGL(k_conv_frag_i8, dim3((unsigned)((rows_pad + 63) / 64), CONV_FRAG_GROUPS),
+                     dim3(64 * CONV_FRAG_WAVES), 0, st, p, (int)q.K, (int)q.O, (int)q.rows,
+                     rows_pad, q.a.kqp, tab, reinterpret_cast<int4v *>(g + q.a.off_a),
+                     reinterpret_cast<int32_t *>(g + q.a.off_rs),
+                     reinterpret_cast<int32_t *>(g + q.a.off_ca));
+  MG_TRY(mg_launch_check("k_conv_frag_i8"));
+  // The filter [M][C taps] is B transposed: prepacked from it directly.
+  mg_weight tw{};
+  tw.kind = MG_W_INT8;
+  tw.K = q.K;
+  tw.N = p.m;
+  // Per-channel zero points that are all equal go as one scalar (no table).
+  int64_t zlen = p.w_zp_len;
+  for (int64_t i = 1; i < zlen; i++)
+    if (p.w_zp_host[i] != p.w_zp_host[0]) break;
+    else if (i == zlen - 1) zlen = 1;
+  MG_TRY(mg_int8_prepack_t_dev(ctx, &tw, p.w, p.wk == MG_CONV_I8, p.w_zp_host, zlen,
+                               base + q.off_w));
+  MG_TRY(mg_int8_run_a_ready(ctx, &tw, q.rows, nullptr, c, g, MG_CONV_I8_MAX_KS,
+                             MG_CONV_I8_SMALL_TILES));
+  const dim3 grid((unsigned)((q.rows + 63) / 64), (unsigned)((p.m + 63) / 64));
+  if (p.mode == MG_CONV_OUT_I32)
+    hipLaunchKernelGGL(k_conv_i8_epi<false>, grid, dim3(256), 0, st, c, p, q.O, q.rows);
+  else
+    hipLaunchKernelGGL(k_conv_i8_epi<true>, grid, dim3(256), 0, st, c, p, q.O, q.rows);
+  return mg_launch_check("k_conv_i8_epi");
+}
+
 }  // namespace
 
+bool mg_conv_int8_route(const mg_conv_problem &p) { return conv_i8_plan(p).ok; }
+
 size_t mg_conv_ws_bytes(const mg_conv_problem &p) {
+  const ConvI8Plan q = conv_i8_plan(p);
+  if (q.ok) return q.total;
   if (!use_phases(p)) return 0;
   return mg_align((size_t)(p.group * p.mg * p.cg * p.ker[0] * p.ker[1] * p.ker[2]) * 4);
 }
@@ -489,6 +779,8 @@ mg_status conv_run_phases(mg_ctx *ctx, const mg_conv_problem &p, float *wph) {
 mg_status mg_conv_run(mg_ctx *ctx, const mg_conv_problem &p, void *ws) {
   const int64_t out_sp = p.out[0] * p.out[1] * p.out[2];
   if (p.n == 0 || p.m == 0 || out_sp == 0) return MG_OK;
+  const ConvI8Plan q = conv_i8_plan(p);
+  if (q.ok) return conv_i8_run(ctx, p, q, ws);
   if (use_phases(p)) return conv_run_phases(ctx, p, static_cast<float *>(ws));
   return conv_launch_all(ctx, p, out_sp, ConvPhases{});
 }

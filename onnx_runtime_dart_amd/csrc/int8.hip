@@ -145,6 +145,81 @@ __global__ __launch_bounds__(256) void k_i8_colsum(
   cb[bi * npad + col] = (b_signed ? 0 : 128) - z;
 }
 
+// B given transposed, bt [N, K] row-major (a convolution filter [M][C taps])
+// -> the fragments of k_i8_prep_b: lane l of fragment q of column tile n32
+// reads the 16 bytes of row 32 n32 + l % 32 at k = 128 (q / 4) + 64 (l / 32)
+// + 16 (q % 4), one 16-byte load where the piece is whole and aligned.  One
+// thread per fragment lane.
+__global__ __launch_bounds__(256) void k_i8_prep_bt(const uint8_t *__restrict__ bt, int b_signed,
+                                                    int64_t K, int64_t N, int n32n, int kqp,
+                                                    int4v *__restrict__ frag) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)n32n * kqp * 64) return;
+  const int lane = (int)(idx & 63);
+  const int64_t fq = idx >> 6;
+  const int q = (int)(fq % kqp), n32 = (int)(fq / kqp);
+  const int64_t n = (int64_t)n32 * 32 + (lane & 31);
+  const int64_t k0 = (int64_t)(q / 4) * 128 + 64 * (lane >> 5) + 16 * (q % 4);
+  const uint32_t flip = b_signed ? 0u : 0x80u;
+  uint32_t w[4];
+  const uint8_t *src = bt + (n < N ? n : 0) * K + k0;
+  if (n < N && k0 + 16 <= K && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    const uint4 x = *reinterpret_cast<const uint4 *>(src);
+    w[0] = x.x, w[1] = x.y, w[2] = x.z, w[3] = x.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int64_t k = k0 + 4 * j + e;
+        const uint32_t by = (n < N && k < K) ? src[4 * j + e] : flip;
+        word |= by << (8 * e);
+      }
+      w[j] = word;
+    }
+  }
+  const uint32_t fl4 = flip * 0x01010101u;
+  frag[idx] = (int4v){(int)(w[0] ^ fl4), (int)(w[1] ^ fl4), (int)(w[2] ^ fl4), (int)(w[3] ^ fl4)};
+}
+
+// Column sums of B' from bt [N, K] (rows contiguous): one wave per column,
+// 16-byte loads where the row allows, and cb per column as k_i8_colsum.
+__global__ __launch_bounds__(256) void k_i8_colsum_t(
+    const uint8_t *__restrict__ bt, int b_signed, int64_t K, int64_t N, int64_t npad,
+    int zb_scalar, const int32_t *__restrict__ zb, int zb_len, int32_t *__restrict__ colsum,
+    int32_t *__restrict__ cb) {
+  const int lane = threadIdx.x & 63;
+  const int64_t col = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (col >= npad) return;
+  const bool live = col < N;
+  int s = 0;
+  if (live) {
+    const uint8_t *row = bt + col * K;
+    const bool vec = K % 16 == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0;
+    const int flip = b_signed ? 0 : 0x80;
+    if (vec) {
+      for (int64_t k = 16 * lane; k < K; k += 1024) {
+        const uint4 x = *reinterpret_cast<const uint4 *>(row + k);
+        const uint32_t wv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) s += (int8_t)(((wv[j] >> (8 * e)) & 0xFFu) ^ flip);
+      }
+    } else {
+      for (int64_t k = lane; k < K; k += 64) s += (int8_t)(row[k] ^ flip);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  if (lane != 0) return;
+  colsum[col] = s;
+  int z = zb_scalar;
+  if (zb && zb_len > 0 && live) z = zb[col % zb_len];
+  cb[col] = (b_signed ? 0 : 128) - z;
+}
+
 // 16 bytes per lane global -> LDS (gfx950 global_load_lds_dwordx4): lane i's
 // data lands at LDS byte address lds + 16 i (lds wave-uniform).  Issued as
 // asm so that the compiler's own waits do not treat it as a write to every
@@ -464,11 +539,12 @@ struct I8Plan {
 };
 
 // a_batch: batches of A; batch: output batches (grid z).
-I8Plan plan_i8(int64_t a_batch, int64_t batch, int64_t M, int64_t K, int64_t N) {
+I8Plan plan_i8(int64_t a_batch, int64_t batch, int64_t M, int64_t K, int64_t N,
+               int max_ks = 0, bool small_tiles = false) {
   I8Plan p;
   p.kpad = (K + 255) / 256 * 256;
   p.nstage = (int)(p.kpad / 256);
-  p.wm = M > 128 ? 2 : 1;
+  p.wm = M > 128 && !small_tiles ? 2 : 1;
   p.mtiles = (int)((M + 128 * p.wm - 1) / (128 * p.wm));
   p.m32n = p.mtiles * 4 * p.wm;
   p.mpad = (int64_t)p.m32n * 32;
@@ -476,7 +552,8 @@ I8Plan plan_i8(int64_t a_batch, int64_t batch, int64_t M, int64_t K, int64_t N) 
   // Split K until ~2 workgroups per CU, keeping >= 2 stages per split.
   const int64_t tiles = (int64_t)p.mtiles * p.ntiles * batch;
   int ks = 1;
-  while (tiles * ks * 2 <= 512 && p.nstage / (ks * 2) >= 2) ks *= 2;
+  while (tiles * ks * 2 <= 512 && p.nstage / (ks * 2) >= 2 && (max_ks <= 0 || ks * 2 <= max_ks))
+    ks *= 2;
   p.sps = (p.nstage + ks - 1) / ks;
   p.ks = (p.nstage + p.sps - 1) / p.sps;
   p.off_a = 0;
@@ -540,6 +617,35 @@ mg_status mg_int8_prepack_dev(mg_ctx *ctx, mg_weight *w, const void *b_dev,
   return mg_launch_check("k_i8_colsum");
 }
 
+mg_status mg_int8_prepack_t_dev(mg_ctx *ctx, mg_weight *w, const void *bt_dev,
+                                int32_t b_signed, const int32_t *b_zp, int64_t b_zp_len,
+                                void *ws_weight) {
+  int8_carve(w, ws_weight);
+  w->i8.b_signed = b_signed;
+  const int64_t K = w->K, N = w->N;
+  const int kqp = (int)(w->i8.kpad / 32), n32 = (int)(w->i8.npad / 32);
+  hipStream_t st = ctx->stream;
+  int zb_scalar = 0;
+  const int32_t *zb_dev = nullptr;
+  int zb_len = 0;
+  if (b_zp && b_zp_len == 1) {
+    zb_scalar = b_zp[0];
+  } else if (b_zp && b_zp_len > 1) {  // through the cb array, as mg_int8_prepack_dev
+    MG_TRY(mg_h2d_table(ctx, w->i8.cb, b_zp, (size_t)b_zp_len * 4));
+    zb_dev = w->i8.cb;
+    zb_len = (int)b_zp_len;
+  }
+  const int64_t slots = (int64_t)n32 * kqp * 64;
+  hipLaunchKernelGGL(k_i8_prep_bt, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st,
+                     static_cast<const uint8_t *>(bt_dev), b_signed, K, N, n32, kqp,
+                     reinterpret_cast<int4v *>(w->i8.bq));
+  MG_TRY(mg_launch_check("k_i8_prep_bt"));
+  hipLaunchKernelGGL(k_i8_colsum_t, dim3((unsigned)((w->i8.npad + 3) / 4)), dim3(256), 0, st,
+                     static_cast<const uint8_t *>(bt_dev), b_signed, K, N, w->i8.npad, zb_scalar,
+                     zb_dev, zb_len, w->i8.colsum, w->i8.cb);
+  return mg_launch_check("k_i8_colsum_t");
+}
+
 mg_status mg_int8_upload(mg_ctx *ctx, mg_weight *w, const void *b,
                          int32_t b_signed, const int32_t *b_zp,
                          int64_t b_zp_len) {
@@ -570,8 +676,21 @@ void mg_int8_free(mg_weight *w) {
   w->i8 = mg_int8_dev{};
 }
 
-size_t mg_int8_ws_bytes(const mg_weight *w, int64_t rows) {
-  return plan_i8(1, 1, rows, w->K, w->N).total;
+size_t mg_int8_ws_bytes(const mg_weight *w, int64_t rows, int max_ks) {
+  return plan_i8(1, 1, rows, w->K, w->N, max_ks).total;
+}
+
+mg_i8_a_layout mg_int8_a_layout(int64_t rows, int64_t K, int64_t N, int max_ks,
+                                bool small_tiles) {
+  const I8Plan p = plan_i8(1, 1, rows, K, N, max_ks, small_tiles);
+  mg_i8_a_layout l;
+  l.off_a = p.off_a;
+  l.off_rs = p.off_rs;
+  l.off_ca = p.off_ca;
+  l.m32n = p.m32n;
+  l.kqp = p.nstage * QS;
+  l.total = p.total;
+  return l;
 }
 
 // Shared launcher.  a_batch/b_batch: 1 or batch; rows per batch = M.  bq,
@@ -581,10 +700,11 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
                              const void *a_dev, int32_t a_signed, int64_t a_batch,
                              int64_t M, int64_t N, int64_t K, const int32_t *a_zp,
                              int64_t a_zp_len, const mg_requant *rq, void *y_dev,
-                             void *ws) {
+                             void *ws, int max_ks = 0, bool a_ready = false,
+                             bool small_tiles = false) {
   if (M == 0 || N == 0) return MG_OK;
   const int64_t batch = a_batch > b_batch ? a_batch : b_batch;
-  const I8Plan p = plan_i8(a_batch, batch, M, K, N);
+  const I8Plan p = plan_i8(a_batch, batch, M, K, N, max_ks, small_tiles);
   hipStream_t st = ctx->stream;
   char *base = static_cast<char *>(ws);
   int4v *afrag = reinterpret_cast<int4v *>(base + p.off_a);
@@ -604,12 +724,14 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
     za_len = (int)a_zp_len;
   }
   const int kqp = p.nstage * QS;
-  const int vec = (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 && K % 16 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(k_i8_prep_a, dim3((unsigned)p.m32n, (unsigned)a_batch),
-                     dim3(64 * PREP_A_WAVES), 0, st,
-                     static_cast<const uint8_t *>(a_dev), K, M * K, a_signed, vec, M, K, kqp,
-                     p.m32n, za_scalar, za, za_len, afrag, rowsum, ca);
-  MG_TRY(mg_launch_check("k_i8_prep_a"));
+  if (!a_ready) {  // else the caller wrote afrag, rowsum and ca (mg_int8_a_layout)
+    const int vec = (reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 && K % 16 == 0) ? 1 : 0;
+    hipLaunchKernelGGL(k_i8_prep_a, dim3((unsigned)p.m32n, (unsigned)a_batch),
+                       dim3(64 * PREP_A_WAVES), 0, st,
+                       static_cast<const uint8_t *>(a_dev), K, M * K, a_signed, vec, M, K, kqp,
+                       p.m32n, za_scalar, za, za_len, afrag, rowsum, ca);
+    MG_TRY(mg_launch_check("k_i8_prep_a"));
+  }
   I8Epi e{};
   e.colsum = colsum;
   e.cb = cb;
@@ -673,9 +795,16 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
 mg_status mg_int8_run(mg_ctx *ctx, const mg_weight *w, const void *a_dev,
                       int32_t a_signed, int64_t rows, const int32_t *a_zp,
                       int64_t a_zp_len, const mg_requant *rq, void *y_dev,
-                      void *ws) {
+                      void *ws, int max_ks) {
   return int8_launch(ctx, w->i8.bq, w->i8.colsum, w->i8.cb, w->i8.npad, 1, a_dev, a_signed, 1,
-                     rows, w->N, w->K, a_zp, a_zp_len, rq, y_dev, ws);
+                     rows, w->N, w->K, a_zp, a_zp_len, rq, y_dev, ws, max_ks);
+}
+
+mg_status mg_int8_run_a_ready(mg_ctx *ctx, const mg_weight *w, int64_t rows,
+                              const mg_requant *rq, void *y_dev, void *ws, int max_ks,
+                              bool small_tiles) {
+  return int8_launch(ctx, w->i8.bq, w->i8.colsum, w->i8.cb, w->i8.npad, 1, nullptr, 0, 1, rows,
+                     w->N, w->K, nullptr, 0, rq, y_dev, ws, max_ks, true, small_tiles);
 }
 
 // Runtime (non-weight) batched form: B is prepacked per batch into the

@@ -215,7 +215,8 @@ mg_status mg_int8_upload(mg_ctx *ctx, mg_weight *w, const void *b,
                          int32_t b_signed, const int32_t *b_zp,
                          int64_t b_zp_len);
 void mg_int8_free(mg_weight *w);
-size_t mg_int8_ws_bytes(const mg_weight *w, int64_t rows);
+// max_ks > 0 caps the GEMM's K split (the workspace then holds fewer partials).
+size_t mg_int8_ws_bytes(const mg_weight *w, int64_t rows, int max_ks = 0);
 // Requant parameters for QLinearMatMul; null => plain int32 output.
 // a_zp_dev, when set, is the A zero point (one int32) in device memory and
 // replaces the host one; quantized_out = 0 then keeps the int32 output of
@@ -236,13 +237,34 @@ inline bool mg_requant_out(const mg_requant *rq) { return rq && rq->quantized_ou
 mg_status mg_int8_run(mg_ctx *ctx, const mg_weight *w, const void *a_dev,
                       int32_t a_signed, int64_t rows, const int32_t *a_zp,
                       int64_t a_zp_len, const mg_requant *rq, void *y_dev,
-                      void *ws);
+                      void *ws, int max_ks = 0);
 // Device-side prepack of a runtime B [K, N] into a temporary weight whose
 // arrays live in `ws_weight` (mg_int8_weight_ws_bytes bytes).
 size_t mg_int8_weight_ws_bytes(int64_t K, int64_t N);
 mg_status mg_int8_prepack_dev(mg_ctx *ctx, mg_weight *w, const void *b_dev,
                               int32_t b_signed, const int32_t *b_zp,
                               int64_t b_zp_len, void *ws_weight);
+
+// Where the GEMM of mg_int8_run keeps its A operand in `ws` for `rows` rows
+// (one batch): afrag [m32n][kqp][64] int4 fragments of A' = A - (a_signed ? 0
+// : 128), rowsum [m32n * 32] of A' over k < K, ca [m32n * 32] = (a_signed ? 0
+// : 128) - aZp, all as k_i8_prep_a writes them; total: the workspace bytes.
+// small_tiles: 128-row workgroup tiles even for rows > 128 (more tiles).
+struct mg_i8_a_layout {
+  size_t off_a = 0, off_rs = 0, off_ca = 0, total = 0;
+  int m32n = 0, kqp = 0;
+};
+mg_i8_a_layout mg_int8_a_layout(int64_t rows, int64_t K, int64_t N, int max_ks = 0,
+                                bool small_tiles = false);
+// mg_int8_run on an A operand its caller already wrote in that layout.
+mg_status mg_int8_run_a_ready(mg_ctx *ctx, const mg_weight *w, int64_t rows,
+                              const mg_requant *rq, void *y_dev, void *ws, int max_ks = 0,
+                              bool small_tiles = false);
+// The same from B given transposed, bt_dev [N, K] row-major (a convolution
+// filter), without a transposed copy.
+mg_status mg_int8_prepack_t_dev(mg_ctx *ctx, mg_weight *w, const void *bt_dev,
+                                int32_t b_signed, const int32_t *b_zp, int64_t b_zp_len,
+                                void *ws_weight);
 
 // ------------------------------------------------------------- fp32 entry
 
@@ -349,6 +371,10 @@ struct mg_conv_problem {
   int64_t w_gs = 0, w_ms = 0, w_cs = 0;
   int32_t x_zp = 0;
   const float *w_zp = nullptr;   // device [M] (integer kinds)
+  // The caller's weight zero points (host, len 0, 1 or M; integer kinds): the
+  // int8 MFMA route prepacks the weights with them.
+  const int32_t *w_zp_host = nullptr;
+  int64_t w_zp_len = 0;
   const double *mult = nullptr;  // device [M] requant multipliers
   int32_t y_zp = 0, lo = 0, hi = 255;
   // Output placement of a sub-pixel phase (set by the phase split of a
@@ -360,6 +386,9 @@ struct mg_conv_problem {
 // Workspace a call needs (the sub-pixel phase weights of a strided fp32
 // ConvTranspose; 0 otherwise), and the launch.
 size_t mg_conv_ws_bytes(const mg_conv_problem &p);
+// Whether p runs on the int8 MFMA route (ConvInteger / QLinearConv, one
+// group), which takes the weight zero points from w_zp_host, not w_zp.
+bool mg_conv_int8_route(const mg_conv_problem &p);
 mg_status mg_conv_run(mg_ctx *ctx, const mg_conv_problem &p, void *ws);
 
 // ---------------------------------------------------------- attention entry

@@ -117,6 +117,14 @@ INTCONV = [
     ((1, 40, 13), (6, 40, 7), True, False, dict(pads=[3, 3])),                   # 1-D, u8 weights
     ((1, 300, 6, 6), (5, 300, 1, 1), False, False, {}),                          # K = 300 > 256
     ((1, 128, 12, 12), (64, 128, 3, 3), False, True, dict(pads=[1, 1, 1, 1])),   # K = 1152
+    # One group: the int8 MFMA GEMM over a byte im2col.  K = 45 (not a
+    # multiple of 4), 3-D with strides and dilations, batches with a 5 x 5
+    # kernel at stride 2.
+    ((1, 5, 9, 9), (4, 5, 3, 3), False, False, dict(pads=[1, 1, 1, 1])),
+    ((2, 7, 4, 5, 6), (3, 7, 2, 3, 3), True, True,
+     dict(pads=[1, 0, 1, 1, 1, 0], strides=[1, 2, 1], dilations=[2, 1, 1])),
+    ((3, 16, 11, 11), (9, 16, 5, 5), False, True,
+     dict(pads=[2, 2, 2, 2], strides=[2, 2], dilations=[1, 2])),
 ]
 
 
@@ -138,6 +146,19 @@ def test_conv_integer_bit_exact(ops, xs, ws, xsg, wsg, at, per_channel):
     np.testing.assert_array_equal(y, ref)
 
 
+@pytest.mark.parametrize("wz_value", [0, -5])
+def test_conv_integer_uniform_per_channel_zero_points(ops, wz_value):
+    # A per-channel zero-point array whose entries are all equal goes to the
+    # GEMM as one scalar; the sums must not change.
+    rng = np.random.default_rng(0x5EED00D0 + wz_value)
+    x = _rand_int(rng, (2, 24, 9, 9), False)
+    w = _rand_int(rng, (12, 24, 3, 3), True)
+    wz = np.full(12, wz_value, np.int8)
+    y = ops.op_conv_integer(x, w, np.uint8(131), wz, pads=[1, 1, 1, 1])
+    np.testing.assert_array_equal(y, oracle.conv_integer(x, w, np.uint8(131), wz,
+                                                         pads=[1, 1, 1, 1]))
+
+
 def test_conv_integer_extreme_values_k_2304(ops):
     """Every product at +-255^2 over K = 256 * 9: the largest magnitudes the
     exact fp32 segments and the int32 accumulators have to carry."""
@@ -152,7 +173,13 @@ def test_conv_integer_extreme_values_k_2304(ops):
     assert ref.min() == -255 * 255 * 256 * 9
 
 
-@pytest.mark.parametrize("xs,ws,xsg,wsg,at", INTCONV[:4])
+QLCONV = INTCONV[:4] + INTCONV[6:] + [
+    # The ResNet-50 3 x 3 layer the bench times, at two images.
+    ((2, 256, 14, 14), (256, 256, 3, 3), False, True, dict(pads=[1, 1, 1, 1])),
+]
+
+
+@pytest.mark.parametrize("xs,ws,xsg,wsg,at", QLCONV)
 @pytest.mark.parametrize("signed_out", [False, True])
 def test_qlinear_conv_bit_exact(ops, xs, ws, xsg, wsg, at, signed_out):
     rng = np.random.default_rng(int(np.prod(ws)) % 9973 + signed_out)
