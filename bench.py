@@ -224,12 +224,15 @@ def main():
                     help="headline and lm_head measurements only")
     ap.add_argument("--only", default=None,
                     choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1", "llama16",
-                             "attn", "conv", "qconv", "pass512", "dec1", "dec4", "dec16"],
+                             "attn", "conv", "qconv", "gqa512", "pass512", "dec1", "dec4",
+                             "dec16"],
                     help="profiling mode: launch one workload --steps times and exit "
                          "(lm512 / lm1: Qwen3 lm_head MatMulNBits at M=512 / M=1; i8lm512: "
                          "the lm_head as MatMulInteger at M=512; f32ffn: the MiniLM FFN1 "
                          "Gemm; llama1 / llama16: the Llama lm_head at M=1 / M=16; attn: the MiniLM "
-                         "fused attention; conv / qconv: the ResNet-50 3x3 conv as Conv / QLinearConv; pass512: the headline "
+                         "fused attention; conv / qconv: the ResNet-50 3x3 conv as Conv / "
+                         "QLinearConv; gqa512: the 512-token causal GroupQueryAttention "
+                         "prefill; pass512: the headline "
                          "M=512 pass of eight Qwen3 projections, grouped as timed; dec1 / dec4 / "
                          "dec16: the grouped Llama-style decode step at M=1 / 4 / 16; copy: 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
@@ -1077,6 +1080,20 @@ def run_only(args, torch, ops, ctx, stream, dev, randn):
             w = None
             for _ in range(args.steps):
                 ops.conv_f32_dev(x.data_ptr(), xs, wt.data_ptr(), ws, y.data_ptr(), ctx=ctx, **at)
+        elif args.only == "gqa512":
+            h, kv, hs, s_ = 32, 8, 64, 512
+            q, k, v = randn(1, s_, h * hs), randn(1, s_, kv * hs), randn(1, s_, kv * hs)
+            cos, sin = randn(s_, hs // 2), randn(s_, hs // 2)
+            y = torch.empty_like(q)
+            prk = torch.empty((1, kv, s_, hs), device=dev)
+            prv = torch.empty_like(prk)
+            w = None
+            for _ in range(args.steps):
+                ops.group_query_attention_dev(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), 1, s_, h * hs, h, kv, y.data_ptr(),
+                    prk.data_ptr(), prv.data_ptr(), cos_ptr=cos.data_ptr(),
+                    sin_ptr=sin.data_ptr(), max_pos=s_, half_rot=hs // 2, do_rotary=True,
+                    ctx=ctx)
         elif args.only == "qconv":
             xs, ws, at = RESNET_3X3
             x = torch.randint(0, 256, xs, device=dev, dtype=torch.uint8)

@@ -573,53 +573,88 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
   }
 }
 
+// More than eight splits: eight per step with independent loads (a loop of
+// one load per split would wait out the memory latency once per split), a
+// pass for the maximum, then the ordered sum.
+template <class Add>
+__device__ inline void combine_many(const float *p0, int64_t cs, int nsplit, int dv, int DV,
+                                    float &M, Add &add) {
+  int c = 0;
+  for (; c + 8 <= nsplit; c += 8) {
+    float mm[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) mm[u] = p0[(c + u) * cs + DV];
+#pragma unroll
+    for (int u = 0; u < 8; u++) M = fmaxf(M, mm[u]);
+  }
+  for (; c < nsplit; c++) M = fmaxf(M, p0[c * cs + DV]);
+  if (M == -INFINITY) return;
+  c = 0;
+  for (; c + 8 <= nsplit; c += 8) {
+    float mm[8], oo[8], ll[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const float *pr = p0 + (c + u) * cs;
+      mm[u] = pr[DV], oo[u] = pr[dv], ll[u] = pr[DV + 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) add(mm[u], oo[u], ll[u]);
+  }
+  for (; c < nsplit; c++) {
+    const float *pr = p0 + c * cs;
+    add(pr[DV], pr[dv], pr[DV + 1]);
+  }
+}
+
 // Merges the key splits of each (batch index, query): with M the largest
 // split max, y = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c; every score
 // -inf gives NaN, as without splits.  One thread per output element.
 __global__ __launch_bounds__(256) void k_attn_combine(const mg_attn_problem p, int nsplit,
                                                       int64_t nbatch) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= nbatch * p.S * p.DV) return;
-  const int dv = (int)(idx % p.DV);
-  const int64_t row = idx / p.DV;  // bi * S + q
-  const int q = (int)(row % p.S);
-  const int64_t bi = row / p.S;
-  // Eight splits per step with independent loads (a loop of one load per
-  // split would wait out the memory latency once per split).
+  const int64_t n = nbatch * p.S * p.DV;
+  if (idx >= n) return;
+  int dv, q;
+  int64_t row, bi;  // row = bi * S + q
+  if (n < ((int64_t)1 << 31)) {  // 32-bit divisions where the indices allow
+    const unsigned i32 = (unsigned)idx, r32 = i32 / (unsigned)p.DV;
+    dv = (int)(i32 - r32 * (unsigned)p.DV);
+    q = (int)(r32 % (unsigned)p.S);
+    row = r32;
+    bi = r32 / (unsigned)p.S;
+  } else {
+    dv = (int)(idx % p.DV);
+    row = idx / p.DV;
+    q = (int)(row % p.S);
+    bi = row / p.S;
+  }
   const float *p0 = p.part + row * (p.DV + 2);
   const int64_t cs = nbatch * p.S * (p.DV + 2);  // stride between splits
-  float M = -INFINITY;
-  int c = 0;
-  for (; c + 8 <= nsplit; c += 8) {
-    float mm[8];
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  auto add = [&](float m, float o, float l) {
+    const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    num = fmaf(w, o, num);
+    den = fmaf(w, l, den);
+  };
+  if (nsplit <= 8) {
+    // Every split's max, value and sum loaded at once (one memory round
+    // trip); the same maximum and ordered sum as combine_many.
+    float mm[8], oo[8], ll[8];
 #pragma unroll
-    for (int u = 0; u < 8; u++) mm[u] = p0[(c + u) * cs + p.DV];
-#pragma unroll
-    for (int u = 0; u < 8; u++) M = fmaxf(M, mm[u]);
-  }
-  for (; c < nsplit; c++) M = fmaxf(M, p0[c * cs + p.DV]);
-  float num = 0.f, den = 0.f;
-  if (M != -INFINITY) {
-    auto add = [&](float m, float o, float l) {
-      const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
-      num = fmaf(w, o, num);
-      den = fmaf(w, l, den);
-    };
-    c = 0;
-    for (; c + 8 <= nsplit; c += 8) {
-      float mm[8], oo[8], ll[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const float *pr = p0 + (c + u) * cs;
-        mm[u] = pr[p.DV], oo[u] = pr[dv], ll[u] = pr[p.DV + 1];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; u++) add(mm[u], oo[u], ll[u]);
+    for (int u = 0; u < 8; u++) {
+      const float *pr = p0 + (u < nsplit ? u : 0) * cs;
+      mm[u] = pr[p.DV], oo[u] = pr[dv], ll[u] = pr[p.DV + 1];
     }
-    for (; c < nsplit; c++) {
-      const float *pr = p0 + c * cs;
-      add(pr[p.DV], pr[dv], pr[p.DV + 1]);
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (u < nsplit) M = fmaxf(M, mm[u]);
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (u < nsplit) add(mm[u], oo[u], ll[u]);
     }
+  } else {
+    combine_many(p0, cs, nsplit, dv, (int)p.DV, M, add);
   }
   int64_t oy = 0, rem = bi;
   for (int d = p.nbd - 1; d >= 0; d--) {
@@ -771,16 +806,18 @@ __device__ inline float rope(const float *x, int64_t d, int64_t half_rot, const 
 // K/V (both written) and, when rotary, of the rotated Q.  Groups [0, nkv)
 // are the caches, [nkv, nkv + nq) Q.  VEC = 4 needs head_size % 4 == 0 and
 // 16-byte aligned tensors (checked by the host): the cache copies are then
-// 16-byte loads and stores.
-template <int VEC>
+// 16-byte loads and stores.  IX: the index type (32-bit where every element
+// index fits, as divisions by the runtime sizes then cost a fraction of the
+// 64-bit ones).
+template <int VEC, class IX>
 __global__ __launch_bounds__(256) void k_gqa_prep(const mg_gqa_prep g, int64_t nkv, int64_t nq) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= nkv + nq) return;
-  const int64_t total = g.past + g.seq;
+  const IX total = (IX)(g.past + g.seq), hs = (IX)g.hs;
   if (idx < nkv) {
-    const int64_t e = idx * VEC;
-    const int64_t d = e % g.hs, j = (e / g.hs) % total, bh = e / (g.hs * total);
-    const int64_t kvh = bh % g.kv_heads, b = bh / g.kv_heads;
+    const IX e = (IX)(idx * VEC);
+    const IX d = e % hs, j = (e / hs) % total, bh = e / (hs * total);
+    const IX kvh = bh % (IX)g.kv_heads, b = bh / (IX)g.kv_heads;
     if (j < g.past) {
       const int64_t src = (bh * g.past + j) * g.hs + d;
       if (VEC == 4) {
@@ -803,9 +840,9 @@ __global__ __launch_bounds__(256) void k_gqa_prep(const mg_gqa_prep g, int64_t n
     }
     return;
   }
-  const int64_t e = (idx - nkv) * VEC;  // rotated Q, [batch][seq][heads * hs]
-  const int64_t d = e % g.hs, row = e - d;
-  const int64_t s = (e / (g.heads * g.hs)) % g.seq;
+  const IX e = (IX)((idx - nkv) * VEC);  // rotated Q, [batch][seq][heads * hs]
+  const IX d = e % hs, row = e - d;
+  const IX s = (e / ((IX)g.heads * hs)) % (IX)g.seq;
 #pragma unroll
   for (int u = 0; u < VEC; u++)
     g.q_rot[e + u] = rope(g.q + row, d + u, g.half_rot, g.cos + (g.past + s) * g.half_rot,
@@ -824,9 +861,15 @@ mg_status mg_gqa_prep_run(mg_ctx *ctx, const mg_gqa_prep &g) {
   if (nkv + nq == 0) return MG_OK;
   const int64_t blocks = (nkv + nq + 255) / 256;
   if (blocks > 0x7fffffff) return mg_fail(MG_UNSUPPORTED, "GroupQueryAttention: too large");
-  if (v4)
-    hipLaunchKernelGGL(k_gqa_prep<4>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, g, nkv, nq);
+  const bool i32 = std::max(nkv, nq) * vec < ((int64_t)1 << 31);
+  const dim3 grid((unsigned)blocks);
+  if (v4 && i32)
+    hipLaunchKernelGGL((k_gqa_prep<4, uint32_t>), grid, dim3(256), 0, ctx->stream, g, nkv, nq);
+  else if (v4)
+    hipLaunchKernelGGL((k_gqa_prep<4, int64_t>), grid, dim3(256), 0, ctx->stream, g, nkv, nq);
+  else if (i32)
+    hipLaunchKernelGGL((k_gqa_prep<1, uint32_t>), grid, dim3(256), 0, ctx->stream, g, nkv, nq);
   else
-    hipLaunchKernelGGL(k_gqa_prep<1>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, g, nkv, nq);
+    hipLaunchKernelGGL((k_gqa_prep<1, int64_t>), grid, dim3(256), 0, ctx->stream, g, nkv, nq);
   return mg_launch_check("k_gqa_prep");
 }

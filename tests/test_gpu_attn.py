@@ -90,6 +90,31 @@ def test_fused_sdpa_masked_rows_and_empty_keys(ops):
     assert y0.shape == (2, 40, 8) and not y0.any()
 
 
+def test_fused_sdpa_non_finite_operands(ops):
+    # Inf / NaN inside Q, K or V follow the reference's IEEE products and
+    # softmax: the Inf / NaN pattern and the finite values.  Batch 0 is
+    # clean; in batch 1 a -Inf element of key 7 drops that key for the
+    # queries with a positive value in its dim and makes the others' scores
+    # +Inf (NaN rows); batch 2 holds a NaN query value (a NaN row) and an Inf
+    # value element (+Inf in that output column).
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal((3, 150, 32)).astype(np.float32)
+    b = rng.standard_normal((3, 32, 90)).astype(np.float32)
+    v = rng.standard_normal((3, 90, 24)).astype(np.float32)
+    m = np.zeros((150, 90), np.float32)
+    b[1, 4, 7] = -np.inf
+    a[2, 130, 3] = np.nan
+    v[2, 20, 5] = np.inf
+    y = ops.op_fused_sdpa(a, b, v, m, 0.2)
+    ref = oracle.fused_sdpa(a, b, v, m, 0.2)
+    assert np.isnan(ref[1]).any() and np.isfinite(ref[1]).any() and np.isinf(ref[2]).any()
+    for f in (np.isnan, np.isposinf, np.isneginf):
+        np.testing.assert_array_equal(f(y), f(ref))
+    fin = np.isfinite(ref)
+    assert fin[0].all() and G.rms_error(y[0], ref[0]) <= TOL
+    assert G.rms_error(y[fin], ref[fin]) <= TOL
+
+
 @pytest.mark.parametrize("batch,seq,kv,hidden,heads,bias_heads,scale", [
     (2, 9, 9, 24, 4, 4, 0.35), (1, 130, 70, 64, 2, 1, None), (3, 1, 200, 256, 4, 0, None),
     (32, 128, 128, 384, 12, 0, None),    # MiniLM self-attention
