@@ -656,10 +656,12 @@ __global__ __launch_bounds__(256) void k_attn_combine(const mg_attn_problem p, i
   } else {
     combine_many(p0, cs, nsplit, dv, (int)p.DV, M, add);
   }
-  int64_t oy = 0, rem = bi;
+  int64_t oy = 0;
+  unsigned rem = (unsigned)bi;  // batch indices: below 2^31 (the host's grid bound)
   for (int d = p.nbd - 1; d >= 0; d--) {
-    oy += (rem % p.bdim[d]) * p.y_bs[d];
-    rem /= p.bdim[d];
+    const unsigned bd = (unsigned)p.bdim[d];
+    oy += (int64_t)(rem % bd) * p.y_bs[d];
+    rem /= bd;
   }
   p.y[oy + (int64_t)q * p.y_rs + dv] = M == -INFINITY ? __builtin_nanf("") : num / den;
 }
