@@ -634,6 +634,7 @@ mg_status mg_skip_rms_norm_f32_split_dev(mg_ctx *ctx, const float *x_dev,
                                          int64_t gamma_len, const float *bias_dev,
                                          double epsilon, float *y_dev, float *sum_dev,
                                          int64_t block_size, void *split_dev);
+
 /* ----------------------------------------------------------------- weights */
 
 mg_status mg_weight_release(mg_weight *w);
