@@ -44,6 +44,11 @@ namespace {
 
 typedef float float16v __attribute__((ext_vector_type(16)));
 
+// Floats per query row of a key split's partials: the DV unnormalised
+// outputs, the running max and the sum, padded to a multiple of four so
+// that rows start 16-byte aligned (the merge reads four outputs at a time).
+__host__ __device__ constexpr int64_t attn_part_row(int64_t dv) { return (dv + 5) & ~int64_t(3); }
+
 template <int DS, int DVT>
 __device__ __attribute__((always_inline)) void attn_tiles(const mg_attn_problem &p) {
   // Tiles prefetched ahead in registers: two for head size <= 32, one for the
@@ -339,9 +344,9 @@ __device__ __attribute__((always_inline)) void attn_tiles(const mg_attn_problem 
   if (!active || !qok) return;
   if (p.part) {
     // Partial of this key split: unnormalised O, the running max (log2
-    // domain) and the sum, [split][batch index][query][DV + 2].
+    // domain) and the sum, [split][batch index][query][attn_part_row(DV)].
     float *pr = p.part + (((int64_t)blockIdx.y * (gridDim.x / qtiles) + bi) * p.S + q) *
-                             (p.DV + 2);
+                             attn_part_row(p.DV);
 #pragma unroll
     for (int j = 0; j < DVT; j++)
 #pragma unroll
@@ -558,7 +563,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const mg_attn_problem p) {
 #pragma unroll
     for (int w = 32; w >= 1; w >>= 1) ls += __shfl_xor(ls, w);
     if (p.part) {
-      float *pr = p.part + (((int64_t)blockIdx.y * gridDim.x + bi) * S + q) * (DV + 2);
+      float *pr = p.part + (((int64_t)blockIdx.y * gridDim.x + bi) * S + q) * attn_part_row(DV);
 #pragma unroll
       for (int k = 0; k < DL; k++)
         if (lane + 64 * k < DV) pr[lane + 64 * k] = o[i][k];
@@ -628,8 +633,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(const mg_attn_problem p, i
     q = (int)(row % p.S);
     bi = row / p.S;
   }
-  const float *p0 = p.part + row * (p.DV + 2);
-  const int64_t cs = nbatch * p.S * (p.DV + 2);  // stride between splits
+  const float *p0 = p.part + row * attn_part_row(p.DV);
+  const int64_t cs = nbatch * p.S * attn_part_row(p.DV);  // stride between splits
   float M = -INFINITY, num = 0.f, den = 0.f;
   auto add = [&](float m, float o, float l) {
     const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
@@ -664,6 +669,98 @@ __global__ __launch_bounds__(256) void k_attn_combine(const mg_attn_problem p, i
     rem /= bd;
   }
   p.y[oy + (int64_t)q * p.y_rs + dv] = M == -INFINITY ? __builtin_nanf("") : num / den;
+}
+
+// k_attn_combine for four outputs of a row per thread (DV % 4 == 0 and
+// 16-byte aligned output rows): each split's four values in one 16-byte
+// load and its max and sum once for the four; per output the same maximum
+// and ordered sum.
+__global__ __launch_bounds__(256) void k_attn_combine4(const mg_attn_problem p, int nsplit,
+                                                       int64_t nbatch) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n = nbatch * p.S * (p.DV / 4);
+  if (idx >= n) return;
+  const int dq = (int)p.DV / 4;
+  int dv, q;
+  int64_t row, bi;
+  if (n < ((int64_t)1 << 31)) {
+    const unsigned i32 = (unsigned)idx, r32 = i32 / (unsigned)dq;
+    dv = 4 * (int)(i32 - r32 * (unsigned)dq);
+    q = (int)(r32 % (unsigned)p.S);
+    row = r32;
+    bi = r32 / (unsigned)p.S;
+  } else {
+    dv = 4 * (int)(idx % dq);
+    row = idx / dq;
+    q = (int)(row % p.S);
+    bi = row / p.S;
+  }
+  const float *p0 = p.part + row * attn_part_row(p.DV);
+  const int64_t cs = nbatch * p.S * attn_part_row(p.DV);
+  float M = -INFINITY;
+  float num[4] = {0.f, 0.f, 0.f, 0.f}, den = 0.f;
+  auto add = [&](float m, const float4 &o, float l) {
+    const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    num[0] = fmaf(w, o.x, num[0]);
+    num[1] = fmaf(w, o.y, num[1]);
+    num[2] = fmaf(w, o.z, num[2]);
+    num[3] = fmaf(w, o.w, num[3]);
+    den = fmaf(w, l, den);
+  };
+  for (int c0 = 0; c0 < nsplit; c0 += 8) {  // the maximum, eight splits' loads at once
+    float mm[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) mm[u] = p0[(c0 + u < nsplit ? c0 + u : c0) * cs + p.DV];
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (c0 + u < nsplit) M = fmaxf(M, mm[u]);
+  }
+  if (M != -INFINITY) {
+    for (int c0 = 0; c0 < nsplit; c0 += 8) {
+      float mm[8], ll[8];
+      float4 oo[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const float *pr = p0 + (c0 + u < nsplit ? c0 + u : c0) * cs;
+        mm[u] = pr[p.DV], ll[u] = pr[p.DV + 1];
+        oo[u] = *reinterpret_cast<const float4 *>(pr + dv);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (c0 + u < nsplit) add(mm[u], oo[u], ll[u]);
+    }
+  }
+  int64_t oy = 0;
+  unsigned rem = (unsigned)bi;
+  for (int d = p.nbd - 1; d >= 0; d--) {
+    const unsigned bd = (unsigned)p.bdim[d];
+    oy += (int64_t)(rem % bd) * p.y_bs[d];
+    rem /= bd;
+  }
+  float4 out;
+  if (M == -INFINITY) {
+    out = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
+                      __builtin_nanf(""));
+  } else {
+    out = make_float4(num[0] / den, num[1] / den, num[2] / den, num[3] / den);
+  }
+  *reinterpret_cast<float4 *>(p.y + oy + (int64_t)q * p.y_rs + dv) = out;
+}
+
+// Launches the merge of nsplit key splits of the outputs of p.
+mg_status launch_combine(const mg_attn_problem &p, int nsplit, int64_t nbatch, hipStream_t st) {
+  bool v4 = p.DV % 4 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0 && p.y_rs % 4 == 0;
+  for (int d = 0; d < p.nbd; d++) v4 = v4 && p.y_bs[d] % 4 == 0;
+  if (v4) {
+    const int64_t n = nbatch * p.S * (p.DV / 4);
+    hipLaunchKernelGGL(k_attn_combine4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p,
+                       nsplit, nbatch);
+  } else {
+    const int64_t n = nbatch * p.S * p.DV;
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p,
+                       nsplit, nbatch);
+  }
+  return mg_launch_check("k_attn_combine");
 }
 
 template <int DS, int DVT>
@@ -712,12 +809,7 @@ mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
     else
       hipLaunchKernelGGL((k_attn_dec<2, 128>), grid, dim3(256), 0, ctx->stream, p);
     MG_TRY(mg_launch_check("k_attn_dec"));
-    if (p.kc > 0) {
-      const int64_t n = nbatch * p.S * p.DV;
-      hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                         ctx->stream, p, nsplit, nbatch);
-      MG_TRY(mg_launch_check("k_attn_combine"));
-    }
+    if (p.kc > 0) return launch_combine(p, nsplit, nbatch, ctx->stream);
     return MG_OK;
   }
   // Value heads above 128 (above 64 with query/key heads above 128, whose
@@ -745,12 +837,7 @@ mg_status mg_attn_run(mg_ctx *ctx, const mg_attn_problem &p) {
     else
       launch_dvt<128>(pp, grid, ctx->stream);
     MG_TRY(mg_launch_check("k_attn"));
-    if (p.kc > 0) {
-      const int64_t n = nbatch * p.S * pp.DV;
-      hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                         ctx->stream, pp, nsplit, nbatch);
-      MG_TRY(mg_launch_check("k_attn_combine"));
-    }
+    if (p.kc > 0) MG_TRY(launch_combine(pp, nsplit, nbatch, ctx->stream));
   }
   return MG_OK;
 }
@@ -776,7 +863,7 @@ size_t mg_attn_plan_split(const mg_ctx *ctx, mg_attn_problem *p) {
   const int64_t nsplit = (p->T + kc - 1) / kc;
   if (nsplit < 2) return 0;
   p->kc = (int)kc;
-  return (size_t)(nsplit * nbatch * p->S * (p->DV + 2)) * 4;
+  return (size_t)(nsplit * nbatch * p->S * attn_part_row(p->DV)) * 4;
 }
 
 // ------------------------------------------------------ GroupQueryAttention
@@ -804,14 +891,49 @@ __device__ inline float rope(const float *x, int64_t d, int64_t half_rot, const 
   return (float)((double)x[d] * cc + (double)x[i] * ss);
 }
 
+// rope() for the four elements d .. d + 3 (d % 4 == 0) of one head row with
+// 16-byte loads of the row, its rotation partner and the cos / sin row
+// (8-byte ones interleaved): half_rot % 4 == 0 (interleaved: % 2 == 0), so
+// the four lie on one side of every boundary.  Per element the arithmetic
+// of rope().
+__device__ inline float4 rope4(const float *x, int64_t d, int64_t half_rot, const float *c,
+                               const float *sn, int interleaved) {
+  auto ld4 = [](const float *ptr) { return *reinterpret_cast<const float4 *>(ptr); };
+  const float4 X = ld4(x + d);
+  if (d >= 2 * half_rot) return X;
+  if (interleaved) {
+    const int64_t i = d >> 1;
+    const float2 C = *reinterpret_cast<const float2 *>(c + i);
+    const float2 S = *reinterpret_cast<const float2 *>(sn + i);
+    return make_float4((float)((double)X.x * (double)C.x - (double)X.y * (double)S.x),
+                       (float)((double)X.y * (double)C.x + (double)X.x * (double)S.x),
+                       (float)((double)X.z * (double)C.y - (double)X.w * (double)S.y),
+                       (float)((double)X.w * (double)C.y + (double)X.z * (double)S.y));
+  }
+  if (d < half_rot) {
+    const float4 Y = ld4(x + d + half_rot), C = ld4(c + d), S = ld4(sn + d);
+    return make_float4((float)((double)X.x * (double)C.x - (double)Y.x * (double)S.x),
+                       (float)((double)X.y * (double)C.y - (double)Y.y * (double)S.y),
+                       (float)((double)X.z * (double)C.z - (double)Y.z * (double)S.z),
+                       (float)((double)X.w * (double)C.w - (double)Y.w * (double)S.w));
+  }
+  const int64_t i = d - half_rot;
+  const float4 Y = ld4(x + i), C = ld4(c + i), S = ld4(sn + i);
+  return make_float4((float)((double)X.x * (double)C.x + (double)Y.x * (double)S.x),
+                     (float)((double)X.y * (double)C.y + (double)Y.y * (double)S.y),
+                     (float)((double)X.z * (double)C.z + (double)Y.z * (double)S.z),
+                     (float)((double)X.w * (double)C.w + (double)Y.w * (double)S.w));
+}
+
 // One thread per VEC consecutive elements (along the head dim) of present
 // K/V (both written) and, when rotary, of the rotated Q.  Groups [0, nkv)
 // are the caches, [nkv, nkv + nq) Q.  VEC = 4 needs head_size % 4 == 0 and
 // 16-byte aligned tensors (checked by the host): the cache copies are then
 // 16-byte loads and stores.  IX: the index type (32-bit where every element
 // index fits, as divisions by the runtime sizes then cost a fraction of the
-// 64-bit ones).
-template <int VEC, class IX>
+// 64-bit ones).  RQ (VEC = 4): the rotations and the new V rows by whole
+// quads (rope4), with every operand 16-byte aligned.
+template <int VEC, class IX, bool RQ>
 __global__ __launch_bounds__(256) void k_gqa_prep(const mg_gqa_prep g, int64_t nkv, int64_t nq) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= nkv + nq) return;
@@ -833,6 +955,14 @@ __global__ __launch_bounds__(256) void k_gqa_prep(const mg_gqa_prep g, int64_t n
       const int64_t s = j - g.past;
       const int64_t row = (b * g.seq + s) * g.kv_heads * g.hs + kvh * g.hs;
       const float *c = g.cos + (g.past + s) * g.half_rot, *sn = g.sin + (g.past + s) * g.half_rot;
+      if constexpr (RQ) {
+        *reinterpret_cast<float4 *>(g.present_k + e) =
+            g.rotary ? rope4(g.k + row, d, g.half_rot, c, sn, g.interleaved)
+                     : *reinterpret_cast<const float4 *>(g.k + row + d);
+        *reinterpret_cast<float4 *>(g.present_v + e) =
+            *reinterpret_cast<const float4 *>(g.v + row + d);
+        return;
+      }
 #pragma unroll
       for (int u = 0; u < VEC; u++) {
         g.present_k[e + u] = g.rotary ? rope(g.k + row, d + u, g.half_rot, c, sn, g.interleaved)
@@ -845,6 +975,12 @@ __global__ __launch_bounds__(256) void k_gqa_prep(const mg_gqa_prep g, int64_t n
   const IX e = (IX)((idx - nkv) * VEC);  // rotated Q, [batch][seq][heads * hs]
   const IX d = e % hs, row = e - d;
   const IX s = (e / ((IX)g.heads * hs)) % (IX)g.seq;
+  if constexpr (RQ) {
+    *reinterpret_cast<float4 *>(g.q_rot + e) =
+        rope4(g.q + row, d, g.half_rot, g.cos + (g.past + s) * g.half_rot,
+              g.sin + (g.past + s) * g.half_rot, g.interleaved);
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < VEC; u++)
     g.q_rot[e + u] = rope(g.q + row, d + u, g.half_rot, g.cos + (g.past + s) * g.half_rot,
@@ -864,14 +1000,33 @@ mg_status mg_gqa_prep_run(mg_ctx *ctx, const mg_gqa_prep &g) {
   const int64_t blocks = (nkv + nq + 255) / 256;
   if (blocks > 0x7fffffff) return mg_fail(MG_UNSUPPORTED, "GroupQueryAttention: too large");
   const bool i32 = std::max(nkv, nq) * vec < ((int64_t)1 << 31);
+  // Quads of the rotation: the rotated halves (interleaved: pairs) hold
+  // whole quads, and the inputs, Q's output and the cos / sin rows are
+  // aligned for 16-byte (interleaved cos / sin: 8-byte) loads.
+  const bool rq =
+      v4 && al(g.k) && al(g.v) && (!g.rotary || ((g.interleaved ? g.half_rot % 2 == 0
+                                                                 : g.half_rot % 4 == 0) &&
+                                                 al(g.q) && al(g.q_rot) &&
+                                                 reinterpret_cast<uintptr_t>(g.cos) % 16 == 0 &&
+                                                 reinterpret_cast<uintptr_t>(g.sin) % 16 == 0));
   const dim3 grid((unsigned)blocks);
-  if (v4 && i32)
-    hipLaunchKernelGGL((k_gqa_prep<4, uint32_t>), grid, dim3(256), 0, ctx->stream, g, nkv, nq);
+  if (rq && i32)
+    hipLaunchKernelGGL((k_gqa_prep<4, uint32_t, true>), grid, dim3(256), 0, ctx->stream, g, nkv,
+                       nq);
+  else if (rq)
+    hipLaunchKernelGGL((k_gqa_prep<4, int64_t, true>), grid, dim3(256), 0, ctx->stream, g, nkv,
+                       nq);
+  else if (v4 && i32)
+    hipLaunchKernelGGL((k_gqa_prep<4, uint32_t, false>), grid, dim3(256), 0, ctx->stream, g, nkv,
+                       nq);
   else if (v4)
-    hipLaunchKernelGGL((k_gqa_prep<4, int64_t>), grid, dim3(256), 0, ctx->stream, g, nkv, nq);
+    hipLaunchKernelGGL((k_gqa_prep<4, int64_t, false>), grid, dim3(256), 0, ctx->stream, g, nkv,
+                       nq);
   else if (i32)
-    hipLaunchKernelGGL((k_gqa_prep<1, uint32_t>), grid, dim3(256), 0, ctx->stream, g, nkv, nq);
+    hipLaunchKernelGGL((k_gqa_prep<1, uint32_t, false>), grid, dim3(256), 0, ctx->stream, g, nkv,
+                       nq);
   else
-    hipLaunchKernelGGL((k_gqa_prep<1, int64_t>), grid, dim3(256), 0, ctx->stream, g, nkv, nq);
+    hipLaunchKernelGGL((k_gqa_prep<1, int64_t, false>), grid, dim3(256), 0, ctx->stream, g, nkv,
+                       nq);
   return mg_launch_check("k_gqa_prep");
 }

@@ -627,3 +627,81 @@ def test_profiling_records_each_op(ops):
     fw.release()
     w.release()
     ctx.close()
+
+
+def _hip_runtime():
+    """The HIP runtime the library is linked against (found in this process's
+    mappings once the library is loaded), for stream capture in tests."""
+    import ctypes
+    from onnx_runtime_dart_amd import _lib  # noqa: F401  (loads the library)
+    with open("/proc/self/maps") as f:
+        paths = {ln.split()[-1] for ln in f if "libamdhip64" in ln}
+    assert paths, "HIP runtime not mapped"
+    return ctypes.CDLL(sorted(paths)[0])
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_split_k_sum_in_launch_graph_replays(ops, m):
+    """Decode GEMVs with K split over workgroups and the ordered sum of the
+    splits (Llama down shapes at M = 1 and 4): two split launches of different
+    grids in a row, eager and as a captured graph replayed three times with
+    eager split launches between the replays; every replay bitwise the eager
+    result, which matches the oracle."""
+    import ctypes
+    from onnx_runtime_dart_amd._lib import lib as L
+    hip = _hip_runtime()
+    vp = ctypes.c_void_p
+    stream, graph, gexec = vp(), vp(), vp()
+    assert hip.hipStreamCreateWithFlags(ctypes.byref(stream), 1) == 0  # non-blocking
+    ctx = ops.Context(0)
+    ctx.set_stream(stream.value)
+    rng = np.random.default_rng(0x5EED0070 + m)
+    k, bs = 8192, 32
+    ns = (2048, 1024)
+    hw = [make_nbits(rng, n, k, bs, "packed") for n in ns]
+    ws = [ops.NBitsWeight(*h, k=k, n=n, block_size=bs, ctx=ctx) for h, n in zip(hw, ns)]
+    a_np = rng.standard_normal((m, k)).astype(np.float32)
+    D = ops.DeviceBuffer
+    a = D.from_array(a_np, ctx=ctx)
+    ys = [D(m * n * 4, ctx=ctx) for n in ns]
+    other = D(m * ns[1] * 4, ctx=ctx)
+    zeros = [np.zeros((m, n), np.float32) for n in ns]
+
+    def launch():
+        for w, y in zip(ws, ys):
+            w.run_dev(a.ptr, m, y.ptr)
+
+    launch()
+    ctx.synchronize()
+    eager = [y.to_array((m, n), np.float32) for y, n in zip(ys, ns)]
+    assert hip.hipStreamBeginCapture(stream, 0) == 0
+    launch()
+    assert hip.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+    assert hip.hipGraphInstantiate(ctypes.byref(gexec), graph, None, None, 0) == 0
+    try:
+        for rep in range(3):
+            for y, z in zip(ys, zeros):
+                assert L.mg_buffer_upload(ctx.handle, y.ptr, z.ctypes.data, z.nbytes) == 0
+            ws[1].run_dev(a.ptr, m, other.ptr)  # an eager split launch between replays
+            ctx.synchronize()
+            np.testing.assert_array_equal(other.to_array((m, ns[1]), np.float32), eager[1])
+            assert hip.hipGraphLaunch(gexec, stream) == 0
+            assert hip.hipStreamSynchronize(stream) == 0
+            for y, n, e in zip(ys, ns, eager):
+                np.testing.assert_array_equal(y.to_array((m, n), np.float32), e,
+                                              err_msg=f"replay {rep}")
+    finally:
+        hip.hipGraphExecDestroy(gexec)
+        hip.hipGraphDestroy(graph)
+    for (b, s, zp), n, e in zip(hw, ns, eager):
+        cols = np.unique(np.concatenate([np.arange(64), np.arange(n - 64, n),
+                                         rng.integers(0, n, 128)]))
+        bb, ss, zz, _ = slice_cols(b, s, zp, None, cols)
+        ref = oracle.matmul_nbits(a_np, bb, ss, zz, k=k, n=len(cols), block_size=bs)
+        assert G.rms_error(e[:, cols], ref) <= TOL
+    for w in ws:
+        w.release()
+    for buf in [a, other] + ys:
+        buf.free()
+    ctx.close()
+    hip.hipStreamDestroy(stream)
