@@ -90,6 +90,35 @@ __device__ __attribute__((always_inline)) void attn_tiles(const mg_attn_problem 
   const int q = q0 + r32;  // this lane's query (B-operand column / result column)
   const bool qok = q < p.S;
 
+  // Keys the workgroup visits: all T, or with causal masking only up to the
+  // last key its last query sees (keys past it are -inf for every query).
+  // With a key split (p.kc > 0) the workgroup takes keys [t_begin,
+  // t_begin + kc) of split blockIdx.y and writes partial results.
+  const int t_begin = p.kc > 0 ? (int)blockIdx.y * p.kc : 0;
+  // (min() by value: a reference to a field of p would put p in scratch memory)
+  int t_loop = p.kc > 0 ? min(p.T, t_begin + p.kc) : p.T;
+  if (p.causal) {
+    const int64_t q_last = (int64_t)(blockIdx.x % qtiles) * 128 + 127;
+    t_loop = (int)std::min<int64_t>(t_loop, std::max<int64_t>(0, q_last + p.causal_off + 1));
+  }
+  if (p.part && t_loop <= t_begin) {
+    // A split past the causal limit of every query of the tile: its partial
+    // is that of no keys (zero O, max -inf, sum 0), written without loading
+    // anything (the whole workgroup leaves here).
+    if (!active || !qok) return;
+    float *pr = p.part + (((int64_t)blockIdx.y * (gridDim.x / qtiles) + bi) * p.S + q) *
+                             attn_part_row(p.DV);
+#pragma unroll
+    for (int j = 0; j < DVT; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int dv = 32 * j + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (dv < p.DV) pr[dv] = 0.f;
+      }
+    if (h == 0) pr[p.DV] = -INFINITY, pr[p.DV + 1] = 0.f;
+    return;
+  }
+
   // Cooperative staging of key tile t0: element e of the thread's share is
   // (key, dim) chosen so that consecutive threads read consecutive addresses
   // of whichever index is contiguous in memory.  Loads are raw buffer loads:
@@ -202,12 +231,27 @@ __device__ __attribute__((always_inline)) void attn_tiles(const mg_attn_problem 
   float qf[DS];
   {
     const float *qr = p.q + oq + (int64_t)(qok ? q : 0) * p.q_rs;
+    // Contiguous, 16-byte aligned query rows with D % 4 == 0: 16-byte loads
+    // (a quad of dims is wholly inside D or past it).
+    const bool qvec = p.q_cs == 1 && (p.q_rs & 3) == 0 && (p.D & 3) == 0 &&
+                      (reinterpret_cast<uintptr_t>(p.q + oq) & 15) == 0;
+    if (qvec) {
 #pragma unroll
-    for (int s = 0; s < DS; s++) {
-      const int d = DS * h + s;
-      const bool in = qok && d < p.D;
-      const float x = qr[in ? d * (int)p.q_cs : 0];
-      qf[s] = in ? x : 0.f;
+      for (int i = 0; i < DS / 4; i++) {
+        const int d = DS * h + 4 * i;
+        const bool in = qok && d < p.D;
+        const float4 x = *reinterpret_cast<const float4 *>(qr + (in ? d : 0));
+        qf[4 * i] = in ? x.x : 0.f, qf[4 * i + 1] = in ? x.y : 0.f;
+        qf[4 * i + 2] = in ? x.z : 0.f, qf[4 * i + 3] = in ? x.w : 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < DS; s++) {
+        const int d = DS * h + s;
+        const bool in = qok && d < p.D;
+        const float x = qr[in ? d * (int)p.q_cs : 0];
+        qf[s] = in ? x : 0.f;
+      }
     }
   }
   float16v o[DVT];
@@ -216,17 +260,6 @@ __device__ __attribute__((always_inline)) void attn_tiles(const mg_attn_problem 
   float m_run = -INFINITY, l_run = 0.f;
   float mcur[16];
 
-  // Keys the workgroup visits: all T, or with causal masking only up to the
-  // last key its last query sees (keys past it are -inf for every query).
-  // With a key split (p.kc > 0) the workgroup takes keys [t_begin,
-  // t_begin + kc) of split blockIdx.y and writes partial results.
-  const int t_begin = p.kc > 0 ? (int)blockIdx.y * p.kc : 0;
-  // (min() by value: a reference to a field of p would put p in scratch memory)
-  int t_loop = p.kc > 0 ? min(p.T, t_begin + p.kc) : p.T;
-  if (p.causal) {
-    const int64_t q_last = (int64_t)(blockIdx.x % qtiles) * 128 + 127;
-    t_loop = (int)std::min<int64_t>(t_loop, std::max<int64_t>(0, q_last + p.causal_off + 1));
-  }
   if (t_loop > t_begin) {
     fetch_any(t_begin, I0{});
     if constexpr (PD == 2) {

@@ -641,7 +641,7 @@ def _hip_runtime():
 
 
 @pytest.mark.parametrize("m", [1, 4])
-def test_split_k_sum_in_launch_graph_replays(ops, m):
+def test_split_k_decode_graph_replays(ops, m):
     """Decode GEMVs with K split over workgroups and the ordered sum of the
     splits (Llama down shapes at M = 1 and 4): two split launches of different
     grids in a row, eager and as a captured graph replayed three times with
