@@ -224,7 +224,7 @@ def main():
                     help="headline and lm_head measurements only")
     ap.add_argument("--only", default=None,
                     choices=["lm512", "lm1", "copy", "i8lm512", "f32ffn", "llama1", "llama16",
-                             "attn", "conv", "qconv", "gqa512", "pass512", "dec1", "dec4",
+                             "attn", "conv", "qconv", "gqa512", "gqadec", "pass512", "dec1", "dec4",
                              "dec16"],
                     help="profiling mode: launch one workload --steps times and exit "
                          "(lm512 / lm1: Qwen3 lm_head MatMulNBits at M=512 / M=1; i8lm512: "
@@ -232,7 +232,7 @@ def main():
                          "Gemm; llama1 / llama16: the Llama lm_head at M=1 / M=16; attn: the MiniLM "
                          "fused attention; conv / qconv: the ResNet-50 3x3 conv as Conv / "
                          "QLinearConv; gqa512: the 512-token causal GroupQueryAttention "
-                         "prefill; pass512: the headline "
+                         "prefill; gqadec: its decode step over a 4096-token cache; pass512: the headline "
                          "M=512 pass of eight Qwen3 projections, grouped as timed; dec1 / dec4 / "
                          "dec16: the grouped Llama-style decode step at M=1 / 4 / 16; copy: 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
@@ -1093,6 +1093,22 @@ def run_only(args, torch, ops, ctx, stream, dev, randn):
                     q.data_ptr(), k.data_ptr(), v.data_ptr(), 1, s_, h * hs, h, kv, y.data_ptr(),
                     prk.data_ptr(), prv.data_ptr(), cos_ptr=cos.data_ptr(),
                     sin_ptr=sin.data_ptr(), max_pos=s_, half_rot=hs // 2, do_rotary=True,
+                    ctx=ctx)
+        elif args.only == "gqadec":
+            h, kv, hs, past = 32, 8, 64, 4096
+            q, k, v = randn(1, 1, h * hs), randn(1, 1, kv * hs), randn(1, 1, kv * hs)
+            pk, pv = randn(1, kv, past, hs), randn(1, kv, past, hs)
+            cos, sin = randn(past + 1, hs // 2), randn(past + 1, hs // 2)
+            y = torch.empty_like(q)
+            prk = torch.empty((1, kv, past + 1, hs), device=dev)
+            prv = torch.empty_like(prk)
+            w = None
+            for _ in range(args.steps):
+                ops.group_query_attention_dev(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), 1, 1, h * hs, h, kv, y.data_ptr(),
+                    prk.data_ptr(), prv.data_ptr(), past_key_ptr=pk.data_ptr(),
+                    past_value_ptr=pv.data_ptr(), past_len=past, cos_ptr=cos.data_ptr(),
+                    sin_ptr=sin.data_ptr(), max_pos=past + 1, half_rot=hs // 2, do_rotary=True,
                     ctx=ctx)
         elif args.only == "qconv":
             xs, ws, at = RESNET_3X3

@@ -780,11 +780,83 @@ __global__ __launch_bounds__(256) void k_attn_combine4(const mg_attn_problem p, 
   *reinterpret_cast<float4 *>(p.y + oy + (int64_t)q * p.y_rs + dv) = out;
 }
 
+// The merge for many splits (9 .. 64) and value heads up to 128: one wave
+// per query row, every load of the row in flight at once (split c's max and
+// sum in lane c, its outputs in lane dv's registers), then the maximum and
+// the ordered sum over splits read lane by lane: per output the same
+// arithmetic in the same order as k_attn_combine, in one memory round trip
+// instead of one per eight splits.
+template <int DPL>
+__global__ __launch_bounds__(256) void k_attn_combine_w(const mg_attn_problem p, int nsplit,
+                                                        int64_t nbatch) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= nbatch * p.S) return;  // whole waves
+  const int64_t bi = row / p.S;
+  const int q = (int)(row % p.S);
+  const float *p0 = p.part + row * attn_part_row(p.DV);
+  const int64_t cs = nbatch * p.S * attn_part_row(p.DV);
+  const int DV = (int)p.DV;
+  const float mc = lane < nsplit ? p0[lane * cs + DV] : -INFINITY;
+  const float lc = lane < nsplit ? p0[lane * cs + DV + 1] : 0.f;
+  float o[DPL][64];
+#pragma unroll
+  for (int c = 0; c < 64; c++)
+#pragma unroll
+    for (int e = 0; e < DPL; e++) {
+      const int dv = lane + 64 * e;
+      o[e][c] = c < nsplit && dv < DV ? p0[c * cs + dv] : 0.f;
+    }
+  float M = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < 64; c++)
+    if (c < nsplit)
+      M = fmaxf(M, __builtin_bit_cast(float,
+                                      __builtin_amdgcn_readlane(__builtin_bit_cast(int, mc), c)));
+  float num[DPL], den = 0.f;
+#pragma unroll
+  for (int e = 0; e < DPL; e++) num[e] = 0.f;
+  if (M != -INFINITY) {
+    const float w = mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - M);
+#pragma unroll
+    for (int c = 0; c < 64; c++) {
+      if (c < nsplit) {
+        const float wc = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), c));
+        const float lcc = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lc), c));
+#pragma unroll
+        for (int e = 0; e < DPL; e++) num[e] = fmaf(wc, o[e][c], num[e]);
+        den = fmaf(wc, lcc, den);
+      }
+    }
+  }
+  int64_t oy = 0;
+  unsigned rem = (unsigned)bi;
+  for (int d = p.nbd - 1; d >= 0; d--) {
+    const unsigned bd = (unsigned)p.bdim[d];
+    oy += (int64_t)(rem % bd) * p.y_bs[d];
+    rem /= bd;
+  }
+  float *yr = p.y + oy + (int64_t)q * p.y_rs;
+#pragma unroll
+  for (int e = 0; e < DPL; e++) {
+    const int dv = lane + 64 * e;
+    if (dv < DV) yr[dv] = M == -INFINITY ? __builtin_nanf("") : num[e] / den;
+  }
+}
+
 // Launches the merge of nsplit key splits of the outputs of p.
 mg_status launch_combine(const mg_attn_problem &p, int nsplit, int64_t nbatch, hipStream_t st) {
   bool v4 = p.DV % 4 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0 && p.y_rs % 4 == 0;
   for (int d = 0; d < p.nbd; d++) v4 = v4 && p.y_bs[d] % 4 == 0;
-  if (v4) {
+  if (nsplit > 8 && nsplit <= 64 && p.DV <= 128) {
+    const unsigned g = (unsigned)((nbatch * p.S + 3) / 4);
+    if (p.DV <= 64)
+      hipLaunchKernelGGL(k_attn_combine_w<1>, dim3(g), dim3(256), 0, st, p, nsplit, nbatch);
+    else
+      hipLaunchKernelGGL(k_attn_combine_w<2>, dim3(g), dim3(256), 0, st, p, nsplit, nbatch);
+  } else if (v4) {
     const int64_t n = nbatch * p.S * (p.DV / 4);
     hipLaunchKernelGGL(k_attn_combine4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p,
                        nsplit, nbatch);

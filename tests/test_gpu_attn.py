@@ -207,6 +207,8 @@ GQA = [
     (1, 1, 32, 8, 64, 1000, True, False, 32, 0),    # decode: packed heads, key splits
     (2, 1, 14, 2, 64, 700, False, False, 0, 14),    # decode with per-head bias, splits
     (1, 3, 8, 8, 32, 500, True, True, 16, 1),       # short chunk over a long cache, splits
+    (1, 1, 8, 2, 128, 3000, True, False, 64, 0),    # decode: 47 key splits merged a wave per row
+    (1, 1, 4, 1, 64, 5000, True, False, 32, 0),     # decode: 79 key splits (merged per thread)
     # Gemma-3-style heads of 256 (rotary over the whole head)
     (1, 1, 8, 4, 256, 600, True, False, 128, 0),    # 4B-style decode: 2 q heads per kv head
     (2, 1, 4, 1, 256, 300, True, False, 128, 0),    # 1B-style decode: one kv head (4:1)
