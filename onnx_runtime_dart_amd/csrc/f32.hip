@@ -8,15 +8,21 @@
 //
 // Workgroup tile 128 x 128 (four waves as 2 x 2 of 64 x 64, i.e. 2 x 2 MFMA
 // tiles of 32 x 32 each) with stages of 16 k or, when that grid would not
-// fill the chip, 64 x 64 (one MFMA tile per wave) with stages of 32 k.  Each
-// stage is double-buffered in LDS as Xs[row][k] (k contiguous, rows padded by
-// 4 floats so 16-byte reads do not collide on banks) for both operands.
-// Within a stage of KS k, MFMA step s gives lane l the k = (KS / 2)(l / 32) + s
-// (not 2 s + l / 32): the sum over the stage is the same, and each lane reads
-// its KS / 2 k of a row with 16-byte LDS loads.
+// fill the chip, 64 x 64 (one MFMA tile per wave) with stages of 32 k (16 k
+// for grids beyond four workgroups per CU).  Each stage is double-buffered in
+// LDS as Xs[row][k] (k contiguous, rows padded by 4 floats so 16-byte reads
+// do not collide on banks) for both operands.
+// Within a stage, MFMA step s gives lane l the k = 2 s + l / 32: LDS rows
+// hold their even k, then their odd k, so each lane still reads its KS / 2
+// k of a row with 16-byte LDS loads, and every output adds the k pairs in
+// order whatever the stage size and tile (plans agree bit for bit).
 // Operands may be stored k-contiguous ("RK": A [M][K], B^T [N][K]) or
 // row-contiguous ("KR": A^T [K][M], B [K][N]); the stage loader reads 32
 // bytes per thread either way and transposes KR tiles on their way into LDS.
+// Where rows are 16-byte aligned and the contiguous extent is a multiple of
+// 4 it uses raw buffer loads with out-of-range quads reading as zeros (no
+// branches, so the loads of the next stage stay in flight across the current
+// stage's products; the branchy form waited for them at once).
 // Batches run on grid.z; each workgroup decodes its batch's operand offsets
 // from the broadcast strides it receives as an argument (numpy broadcasting,
 // lib/src/onnx_ops.dart:1742-1764).
@@ -67,15 +73,53 @@ struct Stage {
     }
   }
 
+  // Branch-free form (raw buffer loads): 16-byte quads of E / 4 consecutive
+  // elements along the contiguous index; a quad past the tensor (row >= R or
+  // k >= K) gets an offset past the resource and reads as zeros in hardware.
+  // Needs 16-byte aligned rows and the contiguous extent (K, or R for KR) a
+  // multiple of 4, so that a quad is wholly inside or outside, and byte
+  // offsets below 2^31 (all checked by the host).
+  __device__ inline void load_b(__amdgpu_buffer_rsrc_t rs, int64_t ld, int64_t R, int64_t K,
+                                int64_t r0, int64_t k0, int t) {
+    const int64_t r = KR ? r0 + (t % (T / E)) * E : r0 + t / (KS / E);
+    const int64_t k = KR ? k0 + t / (T / E) : k0 + (t % (KS / E)) * E;
+#pragma unroll
+    for (int q = 0; q < E / 4; q++) {
+      const bool ok = KR ? (k < K && r + 4 * q < R) : (r < R && k + 4 * q < K);
+      const int64_t off = KR ? k * ld + r + 4 * q : r * ld + k + 4 * q;
+      const unsigned bo = ok ? (unsigned)(off * 4) : 0x80000000u;
+      const float4 x = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, bo, 0, 0));
+      v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+    }
+  }
+
+  // In LDS a row holds its even k first, then its odd k (element k at
+  // (k % 2) * KS / 2 + k / 2): MFMA step s then pairs k = 2 s (lane half 0)
+  // with 2 s + 1 (half 1), so every output adds the pairs (0, 1), (2, 3), ...
+  // in k order whatever the stage size and tile, and any tile plan (and any
+  // column slice of a weight) gives bitwise the same results.
   __device__ inline void store(float *__restrict__ xs, int t) const {
     if (!KR) {
-      float *d = xs + (t / (KS / E)) * LDX + (t % (KS / E)) * E;
+      // E consecutive k from a multiple of E: evens and odds are each E / 2
+      // consecutive slots.
+      const int k = (t % (KS / E)) * E;
+      float *d0 = xs + (t / (KS / E)) * LDX + k / 2;
+      float *d1 = d0 + KS / 2;
+      if constexpr (E % 8 == 0) {
 #pragma unroll
-      for (int q = 0; q < E / 4; q++)
-        *reinterpret_cast<float4 *>(d + 4 * q) =
-            make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        for (int q = 0; q < E / 8; q++) {
+          *reinterpret_cast<float4 *>(d0 + 4 * q) =
+              make_float4(v[8 * q], v[8 * q + 2], v[8 * q + 4], v[8 * q + 6]);
+          *reinterpret_cast<float4 *>(d1 + 4 * q) =
+              make_float4(v[8 * q + 1], v[8 * q + 3], v[8 * q + 5], v[8 * q + 7]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; e += 2) d0[e / 2] = v[e], d1[e / 2] = v[e + 1];
+      }
     } else {
-      float *d = xs + (t % (T / E)) * E * LDX + t / (T / E);
+      const int k = t / (T / E);
+      float *d = xs + (t % (T / E)) * E * LDX + (k & 1) * (KS / 2) + (k >> 1);
 #pragma unroll
       for (int e = 0; e < E; e++) d[e * LDX] = v[e];
     }
@@ -87,7 +131,7 @@ struct Stage {
 // the chip with the larger tile).  KS = k per LDS stage; a stage is
 // KS / 2 MFMA steps per tile.  AKR / BKR: operand layouts (A transposed, B
 // not transposed).
-template <int WT, int KS, bool AKR, bool BKR>
+template <int WT, int KS, bool AKR, bool BKR, bool BV>
 __global__ __launch_bounds__(256) void k_f32_gemm(
     const float *__restrict__ A, const float *__restrict__ B,
     float *__restrict__ Y, int64_t M, int64_t N, int64_t K, int64_t lda,
@@ -136,11 +180,22 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
   const int nst = (int)((K + KS - 1) / KS);
   Stage<WT, KS, AKR> sa;
   Stage<WT, KS, BKR> sb;
+  // BV: every stage through the branch-free buffer loads.
+  auto rsrc = [](const float *base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, 0x7ffffff0,
+                                             0x00020000);
+  };
+  const __amdgpu_buffer_rsrc_t ra = rsrc(Ab), rb = rsrc(Bb);
   auto load = [&](int st) {
     const int64_t k0 = (int64_t)st * KS;
-    const bool kin = k0 + KS <= K;
-    sa.load(Ab, a_in && kin, lda, M, K, r0, k0, t);
-    sb.load(Bb, b_in && kin, ldb, N, K, c0, k0, t);
+    if constexpr (BV) {
+      sa.load_b(ra, lda, M, K, r0, k0, t);
+      sb.load_b(rb, ldb, N, K, c0, k0, t);
+    } else {
+      const bool kin = k0 + KS <= K;
+      sa.load(Ab, a_in && kin, lda, M, K, r0, k0, t);
+      sb.load(Bb, b_in && kin, ldb, N, K, c0, k0, t);
+    }
   };
   load(0);
   sa.store(As[0], t);
@@ -184,7 +239,9 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
   }
 
   // Lane l holds column l % 32 and rows 8 (v / 4) + 4 (l / 32) + v % 4 of
-  // each 32 x 32 tile; 32 lanes write 128 contiguous bytes per store.
+  // each 32 x 32 tile; 32 lanes write 128 contiguous bytes per store.  The
+  // tile's C values are all loaded before the first store (one memory round
+  // trip, not one per row).
   float *Yb = Y + (int64_t)bz * M * ldy;
 #pragma unroll
   for (int i = 0; i < WT; i++)
@@ -192,39 +249,74 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
     for (int j = 0; j < WT; j++) {
       const int64_t col = c0 + wn * 32 * WT + j * 32 + l32;
       if (col >= N) continue;
+      const int64_t rw = r0 + wm * 32 * WT + i * 32 + 4 * h;
+      float cv[16];
+      if (C) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int64_t row = rw + 8 * (v >> 2) + (v & 3);
+          cv[v] = row < M ? C[row * c_rs + col * c_cs] : 0.f;
+        }
+      }
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        const int64_t row = r0 + wm * 32 * WT + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int64_t row = rw + 8 * (v >> 2) + (v & 3);
         if (row >= M) continue;
         float y = acc[i][j][v];
         if (alpha != 1.f) y = alpha * y;
         if (C) {
-          float cv = C[row * c_rs + col * c_cs];
-          if (beta != 1.f) cv = beta * cv;
-          y = y + cv;
+          float c = cv[v];
+          if (beta != 1.f) c = beta * c;
+          y = y + c;
         }
         Yb[row * ldy + col] = y;
       }
     }
 }
 
-template <int WT, int KS>
-void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float *a,
-                const float *b, float *y, int vec_a, int vec_b, uint32_t z0, int nx, int pr,
-                int pc) {
+#ifndef MG_F32_BUFFER_LOADS
+#define MG_F32_BUFFER_LOADS 1
+#endif
+template <int WT, int KS, bool BV>
+void launch_f32_bv(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float *a,
+                   const float *b, float *y, int vec_a, int vec_b, uint32_t z0, int nx, int pr,
+                   int pc) {
 #define MG_F32_ARGS                                                                         \
   a, b, y, p.M, p.N, p.K, p.lda, p.ldb, vec_a, vec_b, p.bc, z0, nx, pr, pc, p.alpha, p.beta, \
       p.c, p.c_rs, p.c_cs, p.ldy ? p.ldy : p.N
   const bool akr = p.trans_a != 0, bkr = p.trans_b == 0;
   if (!akr && !bkr)
-    hipLaunchKernelGGL((k_f32_gemm<WT, KS, false, false>), grid, dim3(256), 0, st, MG_F32_ARGS);
+    hipLaunchKernelGGL((k_f32_gemm<WT, KS, false, false, BV>), grid, dim3(256), 0, st,
+                       MG_F32_ARGS);
   else if (!akr && bkr)
-    hipLaunchKernelGGL((k_f32_gemm<WT, KS, false, true>), grid, dim3(256), 0, st, MG_F32_ARGS);
+    hipLaunchKernelGGL((k_f32_gemm<WT, KS, false, true, BV>), grid, dim3(256), 0, st,
+                       MG_F32_ARGS);
   else if (akr && !bkr)
-    hipLaunchKernelGGL((k_f32_gemm<WT, KS, true, false>), grid, dim3(256), 0, st, MG_F32_ARGS);
+    hipLaunchKernelGGL((k_f32_gemm<WT, KS, true, false, BV>), grid, dim3(256), 0, st,
+                       MG_F32_ARGS);
   else
-    hipLaunchKernelGGL((k_f32_gemm<WT, KS, true, true>), grid, dim3(256), 0, st, MG_F32_ARGS);
+    hipLaunchKernelGGL((k_f32_gemm<WT, KS, true, true, BV>), grid, dim3(256), 0, st,
+                       MG_F32_ARGS);
 #undef MG_F32_ARGS
+}
+
+// The branch-free loads need aligned rows, quads that never straddle the
+// contiguous extent, and every in-range byte offset of both operands (within
+// one batch) below 2^31.
+template <int WT, int KS>
+void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float *a,
+                const float *b, float *y, int vec_a, int vec_b, uint32_t z0, int nx, int pr,
+                int pc) {
+  const bool akr = p.trans_a != 0, bkr = p.trans_b == 0;
+  const int64_t lim = ((int64_t)1 << 31) - 16;
+  const bool bv =
+      MG_F32_BUFFER_LOADS && vec_a && vec_b && (akr ? p.M % 4 == 0 : p.K % 4 == 0) &&
+      (bkr ? p.N % 4 == 0 : p.K % 4 == 0) &&
+      (akr ? p.K * p.lda : p.M * p.lda) * 4 < lim && (bkr ? p.K * p.ldb : p.N * p.ldb) * 4 < lim;
+  if (bv)
+    launch_f32_bv<WT, KS, true>(p, grid, st, a, b, y, vec_a, vec_b, z0, nx, pr, pc);
+  else
+    launch_f32_bv<WT, KS, false>(p, grid, st, a, b, y, vec_a, vec_b, z0, nx, pr, pc);
 }
 
 }  // namespace
@@ -283,12 +375,20 @@ mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
 #ifndef MG_F32_KS_SMALL
 #define MG_F32_KS_SMALL 32
 #endif
+  // 64 x 64 tiles beyond four workgroups per CU take stages of 16 k: their
+  // LDS (20 KB a workgroup against 36 KB) then holds every workgroup of the
+  // grid at once instead of one and a half rounds (MiniLM FFN1 4096 x 384 x
+  // 1536: 64.4 -> 59.6 us; with fewer tiles 32-k stages are faster).
+  const bool small_ks16 = !use_big && nx * ny * p.batch > 4 * (int64_t)ctx->num_cus;
   // Batches in chunks of at most 65535 per launch (grid z).
   for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
     const dim3 grid(gx, 1, (unsigned)std::min<int64_t>(65535, p.batch - z0));
     if (use_big)
       launch_f32<2, MG_F32_KS_BIG>(p, grid, ctx->stream, a_dev, b_dev, y_dev, vec_a, vec_b,
                                    (uint32_t)z0, (int)nx, pr, pc);
+    else if (small_ks16)
+      launch_f32<1, 16>(p, grid, ctx->stream, a_dev, b_dev, y_dev, vec_a, vec_b, (uint32_t)z0,
+                        (int)nx, pr, pc);
     else
       launch_f32<1, MG_F32_KS_SMALL>(p, grid, ctx->stream, a_dev, b_dev, y_dev, vec_a, vec_b,
                                      (uint32_t)z0, (int)nx, pr, pc);
