@@ -103,7 +103,14 @@ ConvPhases phase_table(const mg_conv_problem &p) {
   return t;
 }
 
-template <int WT, int KS, bool TR, bool INT>
+// BUF (float kinds, every element offset of x, w and y below 2^29): the
+// gathered input taps and the bounds-checked weight runs are raw buffer
+// loads, an element outside the tensor or in the padding getting an offset
+// past the resource (read as zero in hardware), and the outputs raw buffer
+// stores.  With a select on the
+// loaded value instead, the compiler waits for the next stage's loads right
+// after issuing them, and no stage overlaps its successor's loads.
+template <int WT, int KS, bool TR, bool INT, bool BUF>
 __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p0, int pix_tiles,
                                               const ConvPhases ph) {
   constexpr int T = 64 * WT, LDX = KS + 4, NS = KS / 2;
@@ -199,6 +206,15 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p0, int pix_
   }
 
   float va[E], vb[E];
+  auto rsrc = [](const void *base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7ffffff0,
+                                             0x00020000);
+  };
+  const __amdgpu_buffer_rsrc_t rw = rsrc(p.w), rx = rsrc(p.x);
+  constexpr unsigned kOob = 0x80000000u;
+  auto ldb = [](__amdgpu_buffer_rsrc_t r, unsigned off) __attribute__((always_inline)) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  };
   auto load = [&](int st) __attribute__((always_inline)) {
     const int64_t k0 = (int64_t)st * KS;
     // Conv weights: an output channel's k run is contiguous (channel stride
@@ -227,12 +243,16 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p0, int pix_
       for (int e = 0; e < E; e++) {
         const bool ok = row_ok && k + e < K;
         const int64_t off = ok ? wbase + (int64_t)c * p.w_cs + r : 0;
-        float v;
-        if (INT)
-          v = (float)load_int(static_cast<const uint8_t *>(p.w), off, p.wk) - wz;
-        else
-          v = static_cast<const float *>(p.w)[off];
-        va[e] = ok ? v : 0.f;
+        if constexpr (BUF) {
+          va[e] = ldb(rw, ok ? (unsigned)off * 4u : kOob);
+        } else {
+          float v;
+          if (INT)
+            v = (float)load_int(static_cast<const uint8_t *>(p.w), off, p.wk) - wz;
+          else
+            v = static_cast<const float *>(p.w)[off];
+          va[e] = ok ? v : 0.f;
+        }
         if (++r == kk) r = 0, c++;
       }
     }
@@ -252,6 +272,10 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p0, int pix_
           const bool ok = k_ok && nok[e] && (unsigned)iz < (unsigned)p.in[0] &&
                           (unsigned)iy < (unsigned)p.in[1] && (unsigned)ix < (unsigned)p.in[2];
           const int64_t off = ok ? xc + (spe[e] + tap) : 0;
+          if constexpr (BUF) {
+            vb[e] = ldb(rx, ok ? (unsigned)off * 4u : kOob);
+            continue;
+          }
           float v;
           if (INT)
             v = (float)(load_int(static_cast<const uint8_t *>(p.x), off, p.xk) - p.x_zp);
@@ -273,6 +297,10 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p0, int pix_
           const bool ok = k_ok && nok[e] && rem3[e] == kr3 && (unsigned)iz < (unsigned)p.in[0] &&
                           (unsigned)iy < (unsigned)p.in[1] && (unsigned)ix < (unsigned)p.in[2];
           const int64_t off = ok ? xc + (spe[e] - tap) : 0;
+          if constexpr (BUF) {
+            vb[e] = ldb(rx, ok ? (unsigned)off * 4u : kOob);
+            continue;
+          }
           float v;
           if (INT)
             v = (float)(load_int(static_cast<const uint8_t *>(p.x), off, p.xk) - p.x_zp);
@@ -364,11 +392,39 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p0, int pix_
 #pragma unroll
     for (int j = 0; j < WT; j++) {
       int64_t col = c0 + wn * 32 * WT + j * 32 + l32;
-      if (col >= out_sp) continue;
+      const bool col_ok = col < out_sp;
+      if (!BUF && !col_ok) continue;
       if (p.phased) {
         const int64_t oz = col / o12, oy = (col % o12) / o2, ox = col % o2;
         col = ((oz * p.ys[0] + p.yb[0]) * p.yo[1] + (oy * p.ys[1] + p.yb[1])) * p.yo[2] +
               (ox * p.ys[2] + p.yb[2]);
+      }
+      // The tile's biases, all loaded before the first store.
+      float bv[16];
+      if (!INT && p.bias) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int64_t row = r0 + wm * 32 * WT + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          bv[v] = static_cast<const float *>(p.bias)[g * p.mg + (row < p.mg ? row : 0)];
+        }
+      }
+      if constexpr (BUF) {
+        // Raw buffer stores, outputs past the tile's channels or positions
+        // given an offset past the resource (dropped in hardware): no
+        // branches, so the stores issue back to back (behind per-element
+        // branches the compiler waited for each store before the next).
+        const __amdgpu_buffer_rsrc_t ry = rsrc(p.y);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int64_t row = r0 + wm * 32 * WT + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          const bool ok = col_ok && row < p.mg;
+          const int64_t oi = (b * p.m + g * p.mg + row) * y_sp + col;
+          float y = acc[i][j][v];
+          if (p.bias) y += bv[v];
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, y), ry,
+                                                ok ? (unsigned)oi * 4u : kOob, 0, 0);
+        }
+        continue;
       }
 #pragma unroll
       for (int v = 0; v < 16; v++) {
@@ -378,7 +434,7 @@ __global__ __launch_bounds__(256) void k_conv(const mg_conv_problem p0, int pix_
         const int64_t oi = (b * p.m + ch) * y_sp + col;
         if (!INT) {
           float y = acc[i][j][v];
-          if (p.bias) y += static_cast<const float *>(p.bias)[ch];
+          if (p.bias) y += bv[v];
           static_cast<float *>(p.y)[oi] = y;
         } else if (p.mode == MG_CONV_OUT_I32) {
           static_cast<int32_t *>(p.y)[oi] = iacc[i][j][v];
@@ -418,6 +474,9 @@ __global__ __launch_bounds__(256) void k_conv_phase_weights(const mg_conv_proble
       static_cast<const float *>(p.w)[g * p.w_gs + m * p.w_ms + c * p.w_cs + tap];
 }
 
+#ifndef MG_CONV_BUFFER_LOADS
+#define MG_CONV_BUFFER_LOADS 1
+#endif
 template <bool TR, bool INT>
 void launch_conv(const mg_conv_problem &p, bool big, int64_t out_sp, hipStream_t st,
                  const ConvPhases &tb) {
@@ -426,13 +485,30 @@ void launch_conv(const mg_conv_problem &p, bool big, int64_t out_sp, hipStream_t
   const dim3 grid((unsigned)(pix_tiles * p.n * p.group), (unsigned)((p.mg + T - 1) / T),
                   (unsigned)(p.phased ? tb.n : 1));
   if constexpr (!INT) {
-    if (big) {
-      hipLaunchKernelGGL((k_conv<2, 16, TR, INT>), grid, dim3(256), 0, st, p, (int)pix_tiles,
-                         tb);
-      return;
-    }
+    // Buffer loads need every element offset of x and w below 2^29 (bytes
+    // below 2^31); phase weights hold as many elements as the filter.
+    const int64_t taps = p.ker[0] * p.ker[1] * p.ker[2];
+    const int64_t x_el = p.n * p.c * p.in[0] * p.in[1] * p.in[2];
+    const int64_t w_el = p.group * p.mg * p.cg * taps;
+    const int64_t y_el = p.n * p.m * (p.phased ? p.yo[0] * p.yo[1] * p.yo[2] : out_sp);
+    const bool buf = MG_CONV_BUFFER_LOADS && x_el < ((int64_t)1 << 29) &&
+                     w_el < ((int64_t)1 << 29) && y_el < ((int64_t)1 << 29);
+    if (big && buf)
+      hipLaunchKernelGGL((k_conv<2, 16, TR, INT, true>), grid, dim3(256), 0, st, p,
+                         (int)pix_tiles, tb);
+    else if (big)
+      hipLaunchKernelGGL((k_conv<2, 16, TR, INT, false>), grid, dim3(256), 0, st, p,
+                         (int)pix_tiles, tb);
+    else if (buf)
+      hipLaunchKernelGGL((k_conv<1, 32, TR, INT, true>), grid, dim3(256), 0, st, p,
+                         (int)pix_tiles, tb);
+    else
+      hipLaunchKernelGGL((k_conv<1, 32, TR, INT, false>), grid, dim3(256), 0, st, p,
+                         (int)pix_tiles, tb);
+    return;
   }
-  hipLaunchKernelGGL((k_conv<1, 32, TR, INT>), grid, dim3(256), 0, st, p, (int)pix_tiles, tb);
+  hipLaunchKernelGGL((k_conv<1, 32, TR, INT, false>), grid, dim3(256), 0, st, p, (int)pix_tiles,
+                     tb);
 }
 
 // ------------------------------------- integer convolution on int8 MFMA

@@ -241,27 +241,32 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
   // Lane l holds column l % 32 and rows 8 (v / 4) + 4 (l / 32) + v % 4 of
   // each 32 x 32 tile; 32 lanes write 128 contiguous bytes per store.  The
   // tile's C values are all loaded before the first store (one memory round
-  // trip, not one per row).
+  // trip, not one per row).  BV: the stores are raw buffer stores, an output
+  // past M or N getting an offset past the resource (dropped in hardware):
+  // no branches, so the stores issue back to back (behind per-element
+  // branches the compiler waited for each store before the next).
   float *Yb = Y + (int64_t)bz * M * ldy;
+  const __amdgpu_buffer_rsrc_t ry = rsrc(Yb);
 #pragma unroll
   for (int i = 0; i < WT; i++)
 #pragma unroll
     for (int j = 0; j < WT; j++) {
       const int64_t col = c0 + wn * 32 * WT + j * 32 + l32;
-      if (col >= N) continue;
+      if (!BV && col >= N) continue;
       const int64_t rw = r0 + wm * 32 * WT + i * 32 + 4 * h;
       float cv[16];
       if (C) {
 #pragma unroll
         for (int v = 0; v < 16; v++) {
           const int64_t row = rw + 8 * (v >> 2) + (v & 3);
-          cv[v] = row < M ? C[row * c_rs + col * c_cs] : 0.f;
+          const bool ok = row < M && col < N;
+          cv[v] = C[ok ? row * c_rs + col * c_cs : 0];
         }
       }
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int64_t row = rw + 8 * (v >> 2) + (v & 3);
-        if (row >= M) continue;
+        if (!BV && row >= M) continue;
         float y = acc[i][j][v];
         if (alpha != 1.f) y = alpha * y;
         if (C) {
@@ -269,7 +274,14 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
           if (beta != 1.f) c = beta * c;
           y = y + c;
         }
-        Yb[row * ldy + col] = y;
+        if constexpr (BV) {
+          const bool ok = row < M && col < N;
+          __builtin_amdgcn_raw_buffer_store_b32(
+              __builtin_bit_cast(unsigned, y), ry,
+              ok ? (unsigned)(row * ldy + col) * 4u : 0x80000000u, 0, 0);
+        } else {
+          Yb[row * ldy + col] = y;
+        }
       }
     }
 }
@@ -301,8 +313,8 @@ void launch_f32_bv(const mg_f32_problem &p, dim3 grid, hipStream_t st, const flo
 }
 
 // The branch-free loads need aligned rows, quads that never straddle the
-// contiguous extent, and every in-range byte offset of both operands (within
-// one batch) below 2^31.
+// contiguous extent, and every in-range byte offset of both operands and of
+// the output (within one batch) below 2^31.
 template <int WT, int KS>
 void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float *a,
                 const float *b, float *y, int vec_a, int vec_b, uint32_t z0, int nx, int pr,
@@ -312,7 +324,8 @@ void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float 
   const bool bv =
       MG_F32_BUFFER_LOADS && vec_a && vec_b && (akr ? p.M % 4 == 0 : p.K % 4 == 0) &&
       (bkr ? p.N % 4 == 0 : p.K % 4 == 0) &&
-      (akr ? p.K * p.lda : p.M * p.lda) * 4 < lim && (bkr ? p.K * p.ldb : p.N * p.ldb) * 4 < lim;
+      (akr ? p.K * p.lda : p.M * p.lda) * 4 < lim && (bkr ? p.K * p.ldb : p.N * p.ldb) * 4 < lim &&
+      p.M * (p.ldy ? p.ldy : p.N) * 4 < lim;
   if (bv)
     launch_f32_bv<WT, KS, true>(p, grid, st, a, b, y, vec_a, vec_b, z0, nx, pr, pc);
   else
