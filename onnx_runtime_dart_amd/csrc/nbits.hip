@@ -1216,18 +1216,22 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   auto ld16 = [](__amdgpu_buffer_rsrc_t r, unsigned vo, int so) __attribute__((always_inline)) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
   };
-  auto fetch = [&](int kg, Ring &R) {
+  // live == false: a slot that is never read (past the wave's last k
+  // group): every offset past its resource, so the loads touch no memory.
+  auto fetch = [&](int kg, Ring &R, bool live) {
+    const unsigned ob = live ? 0u : 0x80000000u;
 #pragma unroll
-    for (int tl = 0; tl < TPW; tl++) R.w[tl] = ld16(r_w, vo_w, (kg * 256 + (t0 + tl) * 16) * 16);
+    for (int tl = 0; tl < TPW; tl++)
+      R.w[tl] = ld16(r_w, vo_w + ob, (kg * 256 + (t0 + tl) * 16) * 16);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      R.ah[j] = ld16(r_a, vo_a, (kg * 4 + j) * 2048);
-      R.al[j] = ld16(r_a, vo_a, (kg * 4 + j) * 2048 + 1024);
+      R.ah[j] = ld16(r_a, vo_a + ob, (kg * 4 + j) * 2048);
+      R.al[j] = ld16(r_a, vo_a + ob, (kg * 4 + j) * 2048 + 1024);
     }
 #pragma unroll
     for (int q = 0; q < NBK; q++) {
       const int b = (kg * KGRP + q * 32 * SEGJ) >> lbs;  // past nb: k padding, zero scale
-      const unsigned so = vo_s + 4u * (unsigned)t0 + 256u * (unsigned)b;
+      const unsigned so = vo_s + 4u * (unsigned)t0 + 256u * (unsigned)b + ob;
       if constexpr (TPW == 4) {
         const float4 x = __builtin_bit_cast(float4, ld16(r_s, so, 0));
         R.s[q][0] = x.x, R.s[q][1] = x.y, R.s[q][2] = x.z, R.s[q][3] = x.w;
@@ -1237,9 +1241,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
       } else {
         R.s[q][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_s, so, 0, 0));
       }
+      // Loaded whether or not the weight has zero points (the table then
+      // points at the scales): a load under a branch would leave the wait
+      // counts uncertain, and the compiler would then wait for every load
+      // in flight, the next k group's included.  compute() picks the value.
       const int bc = min(b, nb - 1);
-      R.zw[q] = has_zp ? __builtin_amdgcn_raw_buffer_load_b32(r_z, vo_z, (bc >> 1) * 64, 0)
-                       : 0x88888888u;
+      R.zw[q] = __builtin_amdgcn_raw_buffer_load_b32(r_z, vo_z + ob, (bc >> 1) * 64, 0);
     }
   };
   uint32_t v_mlo, v_mhi, v_magic;
@@ -1268,9 +1275,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
         const uint32_t sh = (min(b, nb - 1) & 1) * 4;
 #pragma unroll
         for (int tl = 0; tl < TPW; tl++) sq[tl] = R.s[q][tl];
+        const uint32_t zwq = has_zp ? R.zw[q] : 0x88888888u;
 #pragma unroll
         for (int tl = 0; tl < TPW; tl++) {
-          const uint32_t zv = (R.zw[q] >> (8 * (t0 + tl) + sh)) & 15u;
+          const uint32_t zv = (zwq >> (8 * (t0 + tl) + sh)) & 15u;
           z1[tl] = 0xE400E400u + zv * 0x00010001u;
           z16[tl] = 0xE400E400u + zv * 0x00100010u;
         }
@@ -1309,16 +1317,31 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mfma(
   // a load's latency, so a wave with several k groups needs them in flight.
   const int kbeg = part ? (int)blockIdx.y * kps : 0;
   const int kend = part ? min(c4n, kbeg + kps) : c4n;
+  // The blocks of PD k groups whose every prefetch is in range run first,
+  // with no branch around a fetch: under such a branch the compiler cannot
+  // count the loads issued after a slot's and waits for all of them before
+  // each compute, the prefetch included.  The last block or two (bounded
+  // fetches) follow.
   Ring R[PD];
 #pragma unroll
   for (int j = 0; j < PD - 1; j++)
-    if (kbeg + wave + j * NW < kend) fetch(kbeg + wave + j * NW, R[j]);
-  for (int kb = kbeg + wave; kb < kend; kb += PD * NW) {
+    if (kbeg + wave + j * NW < kend) fetch(kbeg + wave + j * NW, R[j], true);
+  int kb = kbeg + wave;
+  for (; kb + (2 * PD - 2) * NW < kend; kb += PD * NW) {
+#pragma unroll
+    for (int j = 0; j < PD; j++) {
+      const int kg = kb + j * NW;
+      fetch(kg + (PD - 1) * NW, R[(j + PD - 1) % PD], true);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(kg, R[j]);
+    }
+  }
+  for (; kb < kend; kb += PD * NW) {
 #pragma unroll
     for (int j = 0; j < PD; j++) {
       const int kg = kb + j * NW;
       if (kg >= kend) break;
-      if (kg + (PD - 1) * NW < kend) fetch(kg + (PD - 1) * NW, R[(j + PD - 1) % PD]);
+      if (kg + (PD - 1) * NW < kend) fetch(kg + (PD - 1) * NW, R[(j + PD - 1) % PD], true);
       __builtin_amdgcn_sched_barrier(0);
       compute(kg, R[j]);
     }
