@@ -833,27 +833,33 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
         m.im[j] = __builtin_bit_cast(
             uint2, __builtin_amdgcn_raw_buffer_load_b64(r_im, vo_im[j], kg * 3072, 0));
     }
+    // Blocks past the last (k padding) read as zero scales: the offset goes
+    // past the resource (a select on the loaded value would make the
+    // compiler wait for it where it computes the select).
     const int blk = (kg * KGRP) >> lbs;
+    const unsigned vo_b = vo_sc + (blk < nb ? 0u : 0x80000000u);
     m.sc = __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(r_sc, vo_sc, min(blk, nbm1) * 256, 0));
+        float, __builtin_amdgcn_raw_buffer_load_b32(r_sc, vo_b, min(blk, nbm1) * 256, 0));
     if constexpr (FZP) {
       m.zf = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(r_zf, vo_sc, min(blk, nbm1) * 256, 0));
+          float, __builtin_amdgcn_raw_buffer_load_b32(r_zf, vo_b, min(blk, nbm1) * 256, 0));
       m.rs = __builtin_bit_cast(float2,
                                 __builtin_amdgcn_raw_buffer_load_b64(r_rs, vo_rs, kg * 8, 0));
     }
   };
   // Piece j of the images into buffer buf (j < 3); with j == 0 also the
   // block scales.
+  // Every thread stores the block scale (and zero point, row sum) of tile
+  // column tc = t % TC (row t % 128): threads t and t + TC loaded the same
+  // value, so the duplicate stores write what the first writes.  A store
+  // under a branch here let the compiler hoist the piece stores above the
+  // k group's products, waiting there for the loads just issued.
   auto store_piece = [&](int kg, Meta &m, int buf, int j) {
     if (j < 3) reinterpret_cast<piece_t *>(&lds[buf * BU4])[t + 256 * j] = m.im[j];
-    if (j == 0 && t < TC) {
-      const int blk = (kg * KGRP) >> lbs;
-      scl[buf][si(tc >> 5, tc & 31)] = blk < nb ? m.sc : 0.f;
-      if constexpr (FZP) czl[buf][tc & 31][tc >> 5] = blk < nb ? m.zf : 0.f;
-    }
-    if constexpr (FZP) {
-      if (j == 0 && t < 128) rl[buf][t] = m.rs.x + m.rs.y;
+    if (j == 0) {
+      scl[buf][si(tc >> 5, tc & 31)] = m.sc;
+      if constexpr (FZP) czl[buf][tc & 31][tc >> 5] = m.zf;
+      if constexpr (FZP) rl[buf][t & 127] = m.rs.x + m.rs.y;
     }
   };
   // Digit d of step st of k group kg: this lane's six dwords.
