@@ -1052,23 +1052,30 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f6kw(
   const __amdgpu_buffer_rsrc_t r_c = rsrc(ps.scales[mem] + (int64_t)cg * nb * 64);
   const unsigned vo16 = 16u * lane, vo8 = 1024u + 8u * lane, vo4 = 4u * lane;
   const unsigned vo_c0 = 4u * (unsigned)sz_pos(lc), vo_c1 = 4u * (unsigned)sz_pos(32 + lc);
-  auto frag = [&](const __amdgpu_buffer_rsrc_t &r, int off) __attribute__((always_inline)) {
-    const uint4 x0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo16, off, 0));
-    const uint2 x1 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, vo8, off, 0));
+  // ob: added to every lane offset; 0x80000000 puts a load past its
+  // resource, so it touches no memory (the loads after a wave's last k
+  // group are issued that way rather than under a branch: behind one the
+  // compiler waits for every load in flight before the products).
+  auto frag = [&](const __amdgpu_buffer_rsrc_t &r, int off, unsigned ob)
+                  __attribute__((always_inline)) {
+    const uint4 x0 =
+        __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo16 + ob, off, 0));
+    const uint2 x1 =
+        __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, vo8 + ob, off, 0));
     return (int8v){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, 0, 0};
   };
-  auto a_load = [&](int kg, int st, int d) __attribute__((always_inline)) {
-    return frag(r_a, ((kg * 2 + st) * 3 + d) * 1536);
+  auto a_load = [&](int kg, int st, int d, unsigned ob = 0u) __attribute__((always_inline)) {
+    return frag(r_a, ((kg * 2 + st) * 3 + d) * 1536, ob);
   };
-  auto b_load = [&](int kg, int st, int n) __attribute__((always_inline)) {
-    return frag(r_b, (n * c4n + kg) * 3072 + st * 1536);
+  auto b_load = [&](int kg, int st, int n, unsigned ob = 0u) __attribute__((always_inline)) {
+    return frag(r_b, (n * c4n + kg) * 3072 + st * 1536, ob);
   };
-  auto s_load = [&](int kg, int st) __attribute__((always_inline)) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r_s, vo4, (kg * 2 + st) * 256, 0);
+  auto s_load = [&](int kg, int st, unsigned ob = 0u) __attribute__((always_inline)) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r_s, vo4 + ob, (kg * 2 + st) * 256, 0);
   };
-  auto c_load = [&](int kg, unsigned vo) __attribute__((always_inline)) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(r_c, vo, ((kg * KGRP) >> lbs) * 256, 0));
+  auto c_load = [&](int kg, unsigned vo, unsigned ob = 0u) __attribute__((always_inline)) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         r_c, vo + ob, ((kg * KGRP) >> lbs) * 256, 0));
   };
 
   float16v acc[2], D[2];
@@ -1093,7 +1100,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f6kw(
     const float16v zero16 = (float16v){};
     for (int kg = kb; kg < ke; kg++) {
       const bool more = kg + 1 < ke;  // wave-uniform
-      const int kn = kg + 1;
+      const int kn = min(kg + 1, ke - 1);
+      const unsigned ob = more ? 0u : 0x80000000u;
 #pragma unroll
       for (int st = 0; st < 2; st++) {
 #pragma unroll
@@ -1105,19 +1113,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f6kw(
                    : d == 1 ? mfma6_digit<1>(A[st][1], B[st][n], cin, (int)sa[st])
                             : mfma6_digit<2>(A[st][2], B[st][n], cin, (int)sa[st]);
           }
-          if (more) A[st][d] = a_load(kn, st, d);
+          A[st][d] = a_load(kn, st, d, ob);
         }
-        if (more) {
-          B[st][0] = b_load(kn, st, 0);
-          B[st][1] = b_load(kn, st, 1);
-          sa[st] = s_load(kn, st);
-        }
+        B[st][0] = b_load(kn, st, 0, ob);
+        B[st][1] = b_load(kn, st, 1, ob);
+        sa[st] = s_load(kn, st, ob);
       }
       const float s0 = sc[0], s1 = sc[1];
-      if (more) {
-        sc[0] = c_load(kn, vo_c0);
-        sc[1] = c_load(kn, vo_c1);
-      }
+      sc[0] = c_load(kn, vo_c0, ob);
+      sc[1] = c_load(kn, vo_c1, ob);
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         acc[0][v] = fmaf(s0, D[0][v], acc[0][v]);
