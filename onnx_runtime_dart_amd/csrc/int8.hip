@@ -538,12 +538,21 @@ struct I8Plan {
   size_t off_a, off_rs, off_ca, off_za, off_part, total;
 };
 
+#ifndef MG_I8_AUTO_SMALL
+#define MG_I8_AUTO_SMALL 1
+#endif
+
 // a_batch: batches of A; batch: output batches (grid z).
 I8Plan plan_i8(int64_t a_batch, int64_t batch, int64_t M, int64_t K, int64_t N,
                int max_ks = 0, bool small_tiles = false) {
   I8Plan p;
   p.kpad = (K + 255) / 256 * 256;
   p.nstage = (int)(p.kpad / 256);
+  // 128-row tiles also where 256-row ones would leave CUs without a tile:
+  // more workgroups and less K split (fewer partial sums to reduce); the
+  // sums are exact integers, so the plan does not change the result.
+  const int64_t big_tiles = (M + 255) / 256 * ((N + TN - 1) / TN) * batch;
+  if (MG_I8_AUTO_SMALL && big_tiles < 256) small_tiles = true;
   p.wm = M > 128 && !small_tiles ? 2 : 1;
   p.mtiles = (int)((M + 128 * p.wm - 1) / (128 * p.wm));
   p.m32n = p.mtiles * 4 * p.wm;

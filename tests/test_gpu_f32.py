@@ -217,3 +217,19 @@ def test_matmul_non_float_cancellations(ops):
     y = ops.op_matmul(a, b)
     assert y[0, 0] == 0.0 and y[1, 1] == 0.0
     np.testing.assert_array_equal(y, oracle.matmul_f64acc(a, b))
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_buffer_stage_layouts_ragged_tiles(ops, ta, tb):
+    # Rows 16-byte aligned and K, M, N multiples of 4: the stages load through
+    # raw buffer loads in both operand layouts (k-contiguous and transposed),
+    # with quads past M, N and K read as zeros and the stores past M and N
+    # dropped; checked against the oracle, with a bias row and alpha / beta.
+    rng = np.random.default_rng(0x5EED0090 + 2 * ta + tb)
+    m, k, n = 132, 68, 100
+    a = rng.standard_normal((k, m) if ta else (m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k) if tb else (k, n)).astype(np.float32)
+    c = rng.standard_normal((n,)).astype(np.float32)
+    y = ops.op_gemm(a, b, c, alpha=0.75, beta=1.5, trans_a=ta, trans_b=tb)
+    ref = oracle.gemm_f32(a, b, c, alpha=0.75, beta=1.5, trans_a=ta, trans_b=tb)
+    assert G.rms_error(y, ref) <= TOL
