@@ -354,11 +354,57 @@ __device__ inline float nbits_weight(const uint4 *__restrict__ wq, const float *
   return (float)(q - z) * s;
 }
 
+// What the epilogue reads that nothing in the k loop produces, loaded when
+// the workgroup starts so that the latency hides under the loop (read at the
+// end, the bias and the flags were two dependent round trips after the last
+// k group): the bias quad of this lane's output columns (zeros past N,
+// without a bias and for k-split partials) and, for lanes < 32, the
+// non-finite flag words of the wave's row lane for the first 8 k groups of
+// the launch's range (clamped to the last; rows past M read zeros).
+// Buffer loads with out-of-range offsets read zeros and touch no memory,
+// so no load sits under a branch.
+struct EpiPre {
+  float4 bv;
+  uint32_t w[8];
+  int flag;
+};
+template <int NT>
+__device__ inline void epi_prefetch(EpiPre &e, int nt, int m32, int M, int c4n, int kg0,
+                                    int kg1, const uint8_t *__restrict__ nf,
+                                    const float *__restrict__ bias, int N) {
+  constexpr int TC = 32 * NT, PPR = 8 * NT;
+  const int lane = threadIdx.x & 63;
+  const unsigned col = (unsigned)(nt * TC + 4 * (lane % PPR));
+  const bool use_bias = gridDim.y == 1 && bias != nullptr;
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(bias), (short)0, use_bias ? N * 4 : 0, 0x00020000);
+  e.bv.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, 4 * col, 0, 0));
+  e.bv.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, 4 * col + 4, 0, 0));
+  e.bv.z = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, 4 * col + 8, 0, 0));
+  e.bv.w = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, 4 * col + 12, 0, 0));
+  const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(nf), (short)0, 0x7ffffff0, 0x00020000);
+  const int row = m32 * 32 + lane;
+  const unsigned ob = (lane < 32 && row < M) ? 0u : 0x80000000u;
+  const unsigned vo = 4u * (unsigned)((int64_t)(lane < 32 && row < M ? row : 0) * c4n) + ob;
+#pragma unroll
+  for (int j = 0; j < 8; j++)
+    e.w[j] = __builtin_amdgcn_raw_buffer_load_b32(rf, vo, 4 * min(kg0 + j, kg1 - 1), 0);
+}
+// The flag of the prefetched words (after they have landed).
+__device__ inline void epi_flags(EpiPre &e) {
+  int f = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) f |= e.w[j] != 0u;
+  e.flag = f;
+}
+
 // Epilogue of the prefill GEMMs: stages each wave's 32 x 32 NT tile of
 // fp32 sums row-major in LDS (free then: every wave has passed the main
 // loop's last barrier), rebuilds the reference's Inf / NaN pattern on rows
 // with a non-finite activation, and writes 16-byte row pieces of y (with the
-// bias) or of this k split's partials.
+// bias) or of this k split's partials.  pre holds the bias quad and the
+// flags of the first 8 k groups (epi_prefetch).
 template <int NT>
 __device__ inline void prefill_epilogue(
     const float16v (&acc)[NT], uint4 *lds, const PrefillSet &ps, int mem, int nt, int m32, int M,
@@ -366,7 +412,7 @@ __device__ inline void prefill_epilogue(
     const uint8_t *__restrict__ nf, const uint4 *__restrict__ wq,
     const float *__restrict__ scales, const uint8_t *__restrict__ zp4,
     const float *__restrict__ zpf, int nb, int nbh, int lbs, int zpk, int N,
-    const float *__restrict__ bias, float *__restrict__ part, int ks) {
+    const EpiPre &pre, float *__restrict__ part, int ks) {
   constexpr int TC = 32 * NT;
   const int t = threadIdx.x, lane = t & 63, lc = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -383,12 +429,12 @@ __device__ inline void prefill_epilogue(
   // Rows of this wave's tile with a non-finite activation in this launch's
   // k range get the reference's Inf / NaN pattern (rare: a uniform branch).
   {
-    int flag = 0;
+    int flag = pre.flag;
     if (lane < 32 && m32 * 32 + lane < M) {
       const uint32_t *nfw = reinterpret_cast<const uint32_t *>(nf) + (int64_t)(m32 * 32 + lane) * c4n;
-      // Eight flag words in flight at a time (one at a time, each load's
-      // latency would add up over the k groups).
-      for (int kb = kg0; kb < kg1; kb += 8) {
+      // The rest of the range, eight flag words in flight at a time (one at
+      // a time, each load's latency would add up over the k groups).
+      for (int kb = kg0 + 8; kb < kg1; kb += 8) {
         uint32_t w[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) w[j] = nfw[min(kb + j, kg1 - 1)];  // branch-free
@@ -439,16 +485,7 @@ __device__ inline void prefill_epilogue(
   constexpr int PPR = 8 * NT, RPI = 64 / PPR;  // pieces per row, rows per iteration
   const int c4 = lane % PPR, ro = lane / PPR;
   const int col = nt * TC + 4 * c4;
-  float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (!split && bias) {
-    if (col + 3 < N) {
-      bv = make_float4(bias[col], bias[col + 1], bias[col + 2], bias[col + 3]);
-    } else {
-      if (col < N) bv.x = bias[col];
-      if (col + 1 < N) bv.y = bias[col + 1];
-      if (col + 2 < N) bv.z = bias[col + 2];
-    }
-  }
+  const float4 bv = pre.bv;
   const bool vec_ok = (N % 4) == 0 && (split || ps.y_vec[mem]);
 #pragma unroll 4
   for (int it = 0; it < 32 / RPI; it++) {
@@ -700,8 +737,13 @@ __global__ __launch_bounds__(64 * MW, MW == 8 ? 1 : (NT == 4 ? 2 : 3)) void k_ge
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
 
+  // (Here the loads are issued after the loop: held across it they made
+  // this kernel spill.)
+  EpiPre pre;
+  epi_prefetch<NT>(pre, nt, m32, M, c4n, kg0, kg1, nf, bias, N);
+  epi_flags(pre);
   prefill_epilogue<NT>(acc, lds, ps, mem, nt, m32, M, c4n, kg0, kg1, K, a, nf, wq, scales, zp4,
-                       nullptr, nb, nbh, lbs, has_zp ? MG_ZP_UINT4 : MG_ZP_NONE, N, bias, part,
+                       nullptr, nb, nbh, lbs, has_zp ? MG_ZP_UINT4 : MG_ZP_NONE, N, pre, part,
                        ks);
 }
 
@@ -758,11 +800,14 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
   constexpr int LDS_U4 = 2 * BU4 > STAGE_U4 ? 2 * BU4 : STAGE_U4;
   constexpr int PB = NT * 4;           // bytes per image piece (3 per thread)
   typedef typename std::conditional<NT == 4, uint4, uint2>::type piece_t;
-  // LD: the images and block scales go global -> LDS directly (no registers,
-  // no LDS stores to schedule), and the activations run in a two-step ring:
-  // every load issued in k group kg is for kg + 1, so the in-order return of
-  // vector loads never makes a step wait for the images behind its own A.
-  constexpr bool LD = NT == 4 && !FZP;
+  // LD (integer zero points, both tile widths): the images and block scales
+  // go global -> LDS directly (no registers, no LDS stores to schedule), and
+  // the activations run in a two-step ring: every load issued in k group kg
+  // is for kg + 1, so the in-order return of vector loads never makes a step
+  // wait for the images behind its own A, and a step's activations have a
+  // whole k group to arrive (with one step of lead, as in the register-staged
+  // form, 64-column launches that fill the chip once waited ~0.6 us a step).
+  constexpr bool LD = !FZP;
   constexpr int AR = LD ? 2 : 1;
   __shared__ uint4 lds[LDS_U4];
   __shared__ float scl[2][32 * NT];  // [buf][n32][col % 32] (LD), else [buf][col % 32][n32]
@@ -800,7 +845,7 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
   unsigned vo_im[3];
 #pragma unroll
   for (int j = 0; j < 3; j++) {
-    const int pb = (t + 256 * j) * PB;
+    const int pb = (t + 256 * j) * (LD ? 16 : PB);
     vo_im[j] = (unsigned)((pb / 3072) * c4n * 3072 + pb % 3072);
   }
   // Block scale of tile column tc = t % TC (threads t < TC stage it).
@@ -890,13 +935,17 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
   for (int n = 0; n < NT; n++) s_pend[n] = 0.f;
   const float16v zero16 = (float16v){};
 
-  // LD: the image pieces p = t + 256 j of k group kg and the block scales of
-  // tile column tc = t (threads t < TC, whole waves) straight into buffer buf.
+  // LD: the image pieces p = t + 256 j of k group kg (16 bytes each: three
+  // per thread at NT = 4, one and a half at NT = 2, where waves 2 and 3 skip
+  // the second) and the block scales of tile column tc = t (threads t < TC,
+  // whole waves) straight into buffer buf.
   auto issue_lds = [&](int kg, int buf) {
     const uint8_t *ib = img + ((int64_t)NT * nt * c4n + kg) * 3072;
     const uint32_t lb = (uint32_t)reinterpret_cast<uintptr_t>(&lds[buf * BU4]);
 #pragma unroll
-    for (int j = 0; j < 3; j++) lds_load16(ib + vo_im[j], lb + (64 * wave + 256 * j) * 16);
+    for (int j = 0; j < 3; j++)
+      if ((64 * wave + 256 * j) * 16 < NT * 3072)
+        lds_load16(ib + vo_im[j], lb + (64 * wave + 256 * j) * 16);
     if (t < TC) {
       const int blk = min((kg * KGRP) >> lbs, nbm1);  // < nb here: bs >= 128 and kpad = nb bs
       lds_load4(scales + ((int64_t)(PH * nt + tcg) * nb + blk) * 64 + sz_pos(tc & 63),
@@ -904,6 +953,8 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
     }
   };
 
+  EpiPre pre;
+  epi_prefetch<NT>(pre, nt, m32, M, c4n, kg0, kg1, nf, bias, N);
   // Activation ring: AR steps of the three digits and their scale word.
   int8v A[AR][3];
   uint32_t sa[AR];
@@ -929,6 +980,7 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
     for (int j = 0; j < 4; j++) store_piece(kg0, m0, 0, j);
   }
   __syncthreads();
+  epi_flags(pre);
 
   for (int kg = kg0; kg < kg1; kg++) {
     const int buf = (kg - kg0) & 1;
@@ -1009,7 +1061,7 @@ __global__ __launch_bounds__(256, NT == 4 || FZP ? 2 : 3) void k_gemm_f6x3(
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[n][v] = fmaf(s_pend[n], D[n][v], acc[n][v]);
   prefill_epilogue<NT>(acc, lds, ps, mem, nt, m32, M, c4n, kg0, kg1, K, a, nf, wq, scales, zp4,
-                       zpf, nb, nbh, lbs, zpk, N, bias, part, ks);
+                       zpf, nb, nbh, lbs, zpk, N, pre, part, ks);
 }
 
 // The fp6 prefill GEMM for small launches (weights with prefill images,
