@@ -1082,6 +1082,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f6kw(
     const PrefillSet ps, int M, int c4n, int nb, int nbh, int lbs, int zpk, int mt32,
     int ntiles) {
   __shared__ __align__(16) float part[4][32 * 64];
+  __shared__ int sflag[4][32];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int L = blockIdx.x;
@@ -1129,6 +1130,38 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f6kw(
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                          r_c, vo + ob, ((kg * KGRP) >> lbs) * 256, 0));
   };
+
+  // What the epilogue reads that the k loop does not produce, loaded now so
+  // that its latency hides under the loop (read at the end, the flag words
+  // and the bias were up to four dependent round trips): the non-finite flag
+  // words of row lane (lanes < 32) for k groups 8 w .. 8 w + 7 of wave w, and
+  // the bias of this thread's eight output columns.  Offsets past the
+  // resources (words past c4n, rows past M, columns past N, no bias) read
+  // zeros and touch no memory.
+  uint32_t fw[8];
+  {
+    const __amdgpu_buffer_rsrc_t r_f = rsrc(nf);
+    const int frow = mt * 32 + lane;
+    const bool frow_ok = lane < 32 && frow < M;
+    const unsigned vo_f = 4u * (unsigned)((int64_t)(frow_ok ? frow : 0) * c4n);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int wd = 8 * wave + i;
+      fw[i] = __builtin_amdgcn_raw_buffer_load_b32(
+          r_f, vo_f + 4u * (unsigned)wd + (frow_ok && wd < c4n ? 0u : 0x80000000u), 0, 0);
+    }
+  }
+  float bv[8];
+  {
+    const float *bias = ps.bias[mem];
+    const __amdgpu_buffer_rsrc_t r_bias = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(bias), (short)0, bias ? N * 4 : 0, 0x00020000);
+    const unsigned vo_bias = 4u * (unsigned)(cg * 64 + 8 * (t & 7));
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      bv[i] = __builtin_bit_cast(float,
+                                 __builtin_amdgcn_raw_buffer_load_b32(r_bias, vo_bias + 4u * i, 0, 0));
+  }
 
   float16v acc[2], D[2];
 #pragma unroll
@@ -1190,6 +1223,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f6kw(
 #pragma unroll
       for (int v = 0; v < 16; v++)
         pw[(8 * (v >> 2) + 4 * lh + (v & 3)) * 64 + n * 32 + lc] = acc[n][v];
+    int f = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) f |= fw[i] != 0u;
+    if (lane < 32) sflag[wave][lane] = f;
   }
   __syncthreads();
   const int r = t >> 3, c0 = 8 * (t & 7);
@@ -1202,15 +1239,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f6kw(
   }
   // Rows of the tile with a non-finite activation (rare; every wave computes
   // the same mask, so the branch is uniform over the workgroup).
-  int flag = 0;
+  int flag = lane < 32 ? (sflag[0][lane] | sflag[1][lane] | sflag[2][lane] | sflag[3][lane]) : 0;
   if (lane < 32 && mt * 32 + lane < M) {
     const uint32_t *nfw = reinterpret_cast<const uint32_t *>(nf) + (int64_t)(mt * 32 + lane) * c4n;
-    for (int kq = 0; kq < c4n; kq += 8) {
-      uint32_t fw[8];
+    // Words past the 32 prefetched (K > 4096).
+    for (int kq = 32; kq < c4n; kq += 8) {
+      uint32_t fr[8];
 #pragma unroll
-      for (int j = 0; j < 8; j++) fw[j] = nfw[min(kq + j, c4n - 1)];
+      for (int j = 0; j < 8; j++) fr[j] = nfw[min(kq + j, c4n - 1)];
 #pragma unroll
-      for (int j = 0; j < 8; j++) flag |= fw[j] != 0u;
+      for (int j = 0; j < 8; j++) flag |= fr[j] != 0u;
     }
   }
   uint64_t rows = __ballot(flag);
@@ -1252,13 +1290,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_f6kw(
   const int row = mt * 32 + r;
   if (row >= M) return;
   const int col = cg * 64 + c0;
-  const float *__restrict__ bias = ps.bias[mem];
   float yv[8] = {y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
-  if (bias) {
 #pragma unroll
-    for (int j = 0; j < 8; j++)
-      if (col + j < N) yv[j] += bias[col + j];
-  }
+  for (int j = 0; j < 8; j++) yv[j] += bv[j];
   float *p = ps.y[mem] + (int64_t)row * N + col;
   if (ps.y_vec[mem] && (N % 4) == 0 && col + 7 < N) {
     __builtin_nontemporal_store((float4v){yv[0], yv[1], yv[2], yv[3]},

@@ -89,6 +89,35 @@ def test_images_and_dequantising_gemm_against_oracle(ops, m, k, n, bs, zp_mode, 
     w_deq.release()
 
 
+def test_wave_split_flags_beyond_the_first_32_k_groups(ops):
+    # k_gemm_f6kw loads the non-finite flags of the first 32 k groups when a
+    # workgroup starts and reads the rest after its loop: non-finite
+    # activations in k groups 0, 32 (the first one read late) and the last
+    # must all give the reference's pattern on their rows, as the
+    # dequantising GEMM (no images) does, with the other rows on the oracle.
+    m, k, n, bs = 40, 8256, 200, 128  # 65 k groups, one 32 x 64 tile row
+    rng = np.random.default_rng(0x5EED0092)
+    b, s, zp = make_nbits(rng, n, k, bs, "packed")
+    bias = rng.standard_normal(n).astype(np.float32)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    bad = {3: (100, np.inf), 9: (4100, -np.inf), 17: (k - 7, np.nan)}
+    for r, (kk, v) in bad.items():
+        a[r, kk] = v
+    w_img = weight(ops, True, b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    w_deq = weight(ops, False, b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    y_img, y_deq = w_img(a), w_deq(a)
+    for r in bad:
+        assert not np.isfinite(y_img[r]).any()
+        for f in (np.isnan, np.isposinf, np.isneginf):
+            np.testing.assert_array_equal(f(y_img[r]), f(y_deq[r]))
+    rows = [r for r in range(m) if r not in bad]
+    assert np.isfinite(y_img[rows]).all()
+    ref = oracle.matmul_nbits(a[rows], b, s, zp, k=k, n=n, block_size=bs, bias=bias)
+    assert G.rms_error(y_img[rows], ref) <= TOL
+    w_img.release()
+    w_deq.release()
+
+
 def test_small_blocks_have_no_images(ops):
     # Blocks below 128 run the fp16 prefill GEMM: no images, same footprint.
     rng = np.random.default_rng(0x5EED0091)
