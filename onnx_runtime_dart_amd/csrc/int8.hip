@@ -515,6 +515,149 @@ __global__ __launch_bounds__(256, 2) void k_i8_gemm(
   }
 }
 
+// The int8 GEMM for small grids (where the tile plan would split K over
+// workgroups and finish with a reduction launch): a workgroup takes 32 rows x
+// TN columns and its four waves take a quarter of the 32-k steps each,
+// streaming A and B fragments straight into registers (no LDS stage, no
+// barrier per step) with RA steps of loads in flight; the four partial tiles
+// meet in LDS and are added (int32 wrap-around, so in any order the exact
+// result), then the epilogue of k_i8_gemm: v = acc + cb*(rowsum + K*ca) +
+// ca*colsum, stored as int32 (MODE 0) or requantised bytes (MODE 1).  Loads
+// past a wave's last step go past their resources (zeros, no memory
+// touched) instead of sitting under a branch.
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void k_i8_gemm_kw(
+    const int4v *__restrict__ afrag, int64_t a_bs, const int4v *__restrict__ bfrag,
+    int64_t b_bs, void *__restrict__ y, I8Epi e, int M, int N, int kqp, int mt32, int ntiles) {
+  __shared__ __align__(16) int32_t part[4][32 * TN];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int L = blockIdx.x;
+  const int xcd = L & 7, qq = L >> 3;
+  const int mt = qq % mt32;  // 32-row tile
+  const int nt = (qq / mt32) * 8 + xcd;
+  if (nt >= ntiles) return;
+  const int64_t bz = blockIdx.z;
+  const int lc = lane & 31, lh = lane >> 5;
+  auto rsrc = [](const void *base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7ffffff0,
+                                             0x00020000);
+  };
+  // A fragments of row tile mt, step j: 1 KB at j; B of column tile nt,
+  // n32 block n, step j: 1 KB at (n kqp + j).
+  const __amdgpu_buffer_rsrc_t r_a = rsrc(afrag + bz * a_bs + (int64_t)mt * kqp * 64);
+  const __amdgpu_buffer_rsrc_t r_b = rsrc(bfrag + bz * b_bs + (int64_t)nt * 4 * kqp * 64);
+  // A resource with no records: loads of steps past the wave's last read
+  // zeros through it and touch no memory (chosen with a scalar select, so
+  // the lane offsets stay fixed registers).
+  const __amdgpu_buffer_rsrc_t r_0 =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int4v *>(afrag), (short)0, 0, 0x00020000);
+  const unsigned vo = 16u * (unsigned)lane;
+  const int kpw = (kqp + 3) >> 2;
+  const int kb = min(kqp, wave * kpw), ke = min(kqp, kb + kpw);
+  struct Step {
+    int4v a, b[4];
+  };
+  auto load = [&](int j, Step &sp) __attribute__((always_inline)) {
+    const bool live = j < ke;
+    sp.a = __builtin_bit_cast(
+        int4v, __builtin_amdgcn_raw_buffer_load_b128(live ? r_a : r_0, vo, j * 1024, 0));
+#pragma unroll
+    for (int n = 0; n < 4; n++)
+      sp.b[n] = __builtin_bit_cast(int4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                              live ? r_b : r_0, vo, (n * kqp + j) * 1024, 0));
+  };
+  int16v acc[4];
+#pragma unroll
+  for (int n = 0; n < 4; n++) acc[n] = (int16v){};
+  if (kb < ke) {
+    Step ring[RA];
+#pragma unroll
+    for (int r = 0; r < RA; r++) load(kb + r, ring[r]);
+    // Steps past ke (to a multiple of RA) multiply zeros.
+    for (int j0 = kb; j0 < ke; j0 += RA) {
+#pragma unroll
+      for (int r = 0; r < RA; r++) {
+        // The slot is reloaded after its products are issued (a reload
+        // before them would need a copy of the slot, whose wait would take
+        // the loads in flight with it).
+#pragma unroll
+        for (int n = 0; n < 4; n++)
+          acc[n] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[r].b[n], ring[r].a, acc[n], 0, 0, 0);
+        load(j0 + r + RA, ring[r]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  // Partial tiles row-major [32 rows][TN] (lane: row lc, columns
+  // 32 n + 8 g + 4 lh + i), then the sum over the waves.
+  {
+    int32_t *pw = part[wave];
+#pragma unroll
+    for (int n = 0; n < 4; n++)
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        *reinterpret_cast<int4v *>(&pw[lc * TN + n * 32 + 8 * g + 4 * lh]) =
+            (int4v){acc[n][4 * g], acc[n][4 * g + 1], acc[n][4 * g + 2], acc[n][4 * g + 3]};
+  }
+  __syncthreads();
+  // Thread: row r = t / 8, columns c0 .. c0 + 15 (four quads).
+  const int r = t >> 3, c0 = 16 * (t & 7);
+  const int row = mt * 32 + r;
+  if (row >= M) return;
+  const int64_t yb = (int64_t)bz * M;
+  const int32_t rs = e.rowsum[bz * e.rs_bs + row];
+  const uint32_t cav = (uint32_t)e.ca[bz * e.rs_bs + row];
+  const uint32_t rk = (uint32_t)rs + (uint32_t)e.K * cav;
+  const float mult = MODE == 1 ? i8_mult(e) : 0.f;
+  const bool vec_ok = (N % 4) == 0 && e.y_vec;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; q4++) {
+    const int cl = c0 + 4 * q4;
+    const int col = nt * TN + cl;  // < npad: the tables are in bounds
+    int4v v = *reinterpret_cast<const int4v *>(&part[0][r * TN + cl]);
+#pragma unroll
+    for (int w = 1; w < 4; w++) {
+      const int4v x = *reinterpret_cast<const int4v *>(&part[w][r * TN + cl]);
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = (int32_t)((uint32_t)v[i] + (uint32_t)x[i]);
+    }
+    const int4v cbv = *reinterpret_cast<const int4v *>(&e.cb[bz * e.cs_bs + col]);
+    const int4v csv = *reinterpret_cast<const int4v *>(&e.colsum[bz * e.cs_bs + col]);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      v[i] = (int32_t)((uint32_t)v[i] + (uint32_t)cbv[i] * rk + cav * (uint32_t)csv[i]);
+    if (col >= N) continue;
+    if (MODE == 1) {
+      uint32_t pk = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float pf = (float)((double)v[i] * (double)mult);
+        int qv = (int)__builtin_amdgcn_fmed3f(rintf(pf), -65536.f, 65536.f) + e.y_zp;
+        qv = qv < e.lo ? e.lo : (qv > e.hi ? e.hi : qv);
+        pk |= (uint32_t)(qv & 255) << (8 * i);
+      }
+      uint8_t *yp = static_cast<uint8_t *>(y) + (yb + row) * N + col;
+      if (vec_ok && col + 3 < N) {
+        *reinterpret_cast<uint32_t *>(yp) = pk;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (col + i < N) yp[i] = (uint8_t)(pk >> (8 * i));
+      }
+    } else {
+      int32_t *yp = static_cast<int32_t *>(y) + (yb + row) * N + col;
+      if (vec_ok && col + 3 < N) {
+        __builtin_nontemporal_store(v, reinterpret_cast<int4v *>(yp));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (col + i < N) yp[i] = v[i];
+      }
+    }
+  }
+}
+
 // Split-K finish (and the K = 0 case, ks = 0): sums the partials of every
 // split and applies the epilogue; one thread per output element.
 template <int REQ>
@@ -540,6 +683,9 @@ struct I8Plan {
 
 #ifndef MG_I8_AUTO_SMALL
 #define MG_I8_AUTO_SMALL 1
+#endif
+#ifndef MG_I8_KWAVE
+#define MG_I8_KWAVE 1
 #endif
 
 // a_batch: batches of A; batch: output batches (grid z).
@@ -761,6 +907,22 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
   }
   int32_t *part = reinterpret_cast<int32_t *>(base + p.off_part);
   const int mode = K == 0 ? 3 : (p.ks > 1 ? 2 : (req ? 1 : 0));
+  // Where the plan splits K: 32-row tiles whose waves split K
+  // (k_i8_gemm_kw, no reduction launch) when they give at least as many
+  // workgroups as the split.
+  const int64_t mt32 = (M + 31) / 32;
+  const int64_t kw_grid = mt32 * ((p.ntiles + 7) / 8) * 8 * batch;
+  if (MG_I8_KWAVE && mode == 2 && kw_grid >= (int64_t)p.mtiles * p.ntiles * p.ks * batch) {
+    e.y_vec = reinterpret_cast<uintptr_t>(y_dev) % 16 == 0 ? 1 : 0;
+    const int64_t a_bs = a_batch > 1 ? (int64_t)p.m32n * kqp * 64 : 0;
+    const int64_t b_bs = b_batch > 1 ? (npad / 32) * kqp * 64 : 0;
+    const dim3 grid((unsigned)(((p.ntiles + 7) / 8) * 8 * mt32), 1, (unsigned)batch);
+#define MG_I8_KW_ARGS                                                                          afrag, a_bs, reinterpret_cast<const int4v *>(bq), b_bs, y_dev, e, (int)M, (int)N, kqp,         (int)mt32, p.ntiles
+    if (req) hipLaunchKernelGGL(k_i8_gemm_kw<1>, grid, dim3(256), 0, st, MG_I8_KW_ARGS);
+    else hipLaunchKernelGGL(k_i8_gemm_kw<0>, grid, dim3(256), 0, st, MG_I8_KW_ARGS);
+#undef MG_I8_KW_ARGS
+    return mg_launch_check("k_i8_gemm_kw");
+  }
   e.y_vec = (mode == 2 || reinterpret_cast<uintptr_t>(y_dev) % 16 == 0) ? 1 : 0;
   if (mode != 3) {
     const int64_t a_bs = a_batch > 1 ? (int64_t)p.m32n * kqp * 64 : 0;
