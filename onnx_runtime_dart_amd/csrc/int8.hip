@@ -46,6 +46,9 @@ typedef int int16v __attribute__((ext_vector_type(16)));
 constexpr int TN = 128;  // workgroup tile columns
 constexpr int QS = 8;    // 32-k MFMA steps per LDS stage (256 k)
 constexpr int RA = 4;    // A register ring: steps loaded ahead of use
+#ifndef KW_RA
+#define KW_RA 4  // k_i8_gemm_kw: steps of loads in flight per wave
+#endif
 
 // B (u8 or i8, [K, N] per batch) -> fragments bfrag[batch][n32][q][lane]
 // (lane l of fragment q holds column 32 n32 + l % 32, k = 128 (q / 4) +
@@ -571,20 +574,20 @@ __global__ __launch_bounds__(256, 2) void k_i8_gemm_kw(
 #pragma unroll
   for (int n = 0; n < 4; n++) acc[n] = (int16v){};
   if (kb < ke) {
-    Step ring[RA];
+    Step ring[KW_RA];
 #pragma unroll
-    for (int r = 0; r < RA; r++) load(kb + r, ring[r]);
-    // Steps past ke (to a multiple of RA) multiply zeros.
-    for (int j0 = kb; j0 < ke; j0 += RA) {
+    for (int r = 0; r < KW_RA; r++) load(kb + r, ring[r]);
+    // Steps past ke (to a multiple of KW_RA) multiply zeros.
+    for (int j0 = kb; j0 < ke; j0 += KW_RA) {
 #pragma unroll
-      for (int r = 0; r < RA; r++) {
+      for (int r = 0; r < KW_RA; r++) {
         // The slot is reloaded after its products are issued (a reload
         // before them would need a copy of the slot, whose wait would take
         // the loads in flight with it).
 #pragma unroll
         for (int n = 0; n < 4; n++)
           acc[n] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[r].b[n], ring[r].a, acc[n], 0, 0, 0);
-        load(j0 + r + RA, ring[r]);
+        load(j0 + r + KW_RA, ring[r]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -687,6 +690,7 @@ struct I8Plan {
 #ifndef MG_I8_KWAVE
 #define MG_I8_KWAVE 1
 #endif
+
 
 // a_batch: batches of A; batch: output batches (grid z).
 I8Plan plan_i8(int64_t a_batch, int64_t batch, int64_t M, int64_t K, int64_t N,
