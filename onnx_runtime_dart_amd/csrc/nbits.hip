@@ -46,6 +46,7 @@
 #include <cmath>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "mg_internal.h"
@@ -1816,22 +1817,57 @@ __global__ __launch_bounds__(256) void k_nbits_repack_tables(
 }
 
 // Reads bytes [off, off + len) of a source into dst.
-mg_status read_source(const mg_byte_source &s, int fd, int64_t off, int64_t len, uint8_t *dst) {
-  if (len == 0) return MG_OK;
+// Bytes [off, off + len) of one source into dst; returns false on a failed
+// read (the caller reports it).
+bool read_part(const mg_byte_source &s, int fd, int64_t off, int64_t len, uint8_t *dst) {
   if (s.host) {
     std::memcpy(dst, s.host + off, (size_t)len);
-    return MG_OK;
+    return true;
   }
   int64_t done = 0;
   while (done < len) {
     const ssize_t r = pread(fd, dst + done, (size_t)(len - done), (off_t)(s.offset + off + done));
     if (r < 0 && errno == EINTR) continue;
-    if (r <= 0)
-      return mg_fail(MG_INVALID_ARGUMENT, std::string("MatMulNBits: cannot read ") +
-                                              std::to_string(len) + " bytes of " + s.path +
-                                              " at offset " + std::to_string(s.offset + off));
+    if (r <= 0) return false;
     done += r;
   }
+  return true;
+}
+
+// A large read is split over up to 4 threads in pieces of at least 8 MiB:
+// one thread's memcpy (or page-cache read) into pinned memory ran at about
+// the rate of the whole upload, below what the host-to-device copy takes.
+mg_status read_source(const mg_byte_source &s, int fd, int64_t off, int64_t len, uint8_t *dst) {
+  if (len == 0) return MG_OK;
+  constexpr int64_t kPiece = 8ll << 20;
+  const int parts = (int)std::min<int64_t>(4, std::max<int64_t>(1, len / kPiece));
+  bool ok = true;
+  if (parts == 1) {
+    ok = read_part(s, fd, off, len, dst);
+  } else {
+    const int64_t step = (len + parts - 1) / parts;
+    bool part_ok[4] = {true, true, true, true};
+    std::thread th[3];
+    int started = 0;
+    for (int i = 1; i < parts; i++) {
+      const int64_t o = i * step, l = std::min(len, o + step) - o;
+      try {
+        th[i - 1] = std::thread([&, i, o, l] { part_ok[i] = read_part(s, fd, off + o, l, dst + o); });
+        started = i;
+      } catch (...) {  // no thread: read the piece here
+        part_ok[i] = read_part(s, fd, off + o, l, dst + o);
+      }
+    }
+    part_ok[0] = read_part(s, fd, off, std::min(len, step), dst);
+    for (int i = 0; i < started; i++)
+      if (th[i].joinable()) th[i].join();
+    for (int i = 0; i < parts; i++) ok = ok && part_ok[i];
+  }
+  if (!ok)
+    return mg_fail(MG_INVALID_ARGUMENT, std::string("MatMulNBits: cannot read ") +
+                                            std::to_string(len) + " bytes of " +
+                                            (s.path ? s.path : "host data") + " at offset " +
+                                            std::to_string(s.offset + off));
   return MG_OK;
 }
 
