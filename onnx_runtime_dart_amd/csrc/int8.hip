@@ -913,10 +913,9 @@ static mg_status int8_launch(mg_ctx *ctx, const int8_t *bq, const int32_t *colsu
   const int mode = K == 0 ? 3 : (p.ks > 1 ? 2 : (req ? 1 : 0));
   // Where the plan splits K: 32-row tiles whose waves split K
   // (k_i8_gemm_kw, no reduction launch) when they give at least as many
-  // workgroups as the split.
+  // workgroups with work as the split (row tiles x column tiles x splits).
   const int64_t mt32 = (M + 31) / 32;
-  const int64_t kw_grid = mt32 * ((p.ntiles + 7) / 8) * 8 * batch;
-  if (MG_I8_KWAVE && mode == 2 && kw_grid >= (int64_t)p.mtiles * p.ntiles * p.ks * batch) {
+  if (MG_I8_KWAVE && mode == 2 && mt32 >= (int64_t)p.mtiles * p.ks) {
     e.y_vec = reinterpret_cast<uintptr_t>(y_dev) % 16 == 0 ? 1 : 0;
     const int64_t a_bs = a_batch > 1 ? (int64_t)p.m32n * kqp * 64 : 0;
     const int64_t b_bs = b_batch > 1 ? (npad / 32) * kqp * 64 : 0;

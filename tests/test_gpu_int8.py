@@ -79,6 +79,48 @@ def test_matmul_integer_batched(ops, ab, bb):
     np.testing.assert_array_equal(y, oracle.matmul_integer(a, b, az, np.array(-3)))
 
 
+# Plans that split K over workgroups run k_i8_gemm_kw (32-row tiles whose
+# waves split K) when it has at least as many workgroups with work: M = 512
+# at the Qwen projection shapes, a ragged N, k steps that do not fill the
+# last ring block of a wave (K = 2304: 18 steps per wave), and batches.
+KW_CASES = [(512, 1024, 2048, "scalar"), (512, 3072, 600, "vector"),
+            (96, 2304, 300, "vector"), (512, 2048, 1024, "none")]
+
+
+@pytest.mark.parametrize("m,k,n,zp_mode", KW_CASES)
+def test_wave_split_plans_exact(ops, m, k, n, zp_mode):
+    rng = np.random.default_rng(0x5EED0093 + m + k + n)
+    a = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    b = rng.integers(-128, 128, (k, n)).astype(np.int8)
+    if zp_mode == "none":
+        az = bz = None
+    elif zp_mode == "scalar":
+        az, bz = np.array(131), np.array(-7)
+    else:
+        az, bz = rng.integers(0, 255, m), rng.integers(-100, 100, n)
+    ref = oracle.matmul_integer(a, b, az, bz)
+    np.testing.assert_array_equal(ops.op_matmul_integer(a, b, az, bz), ref)
+    w = ops.Int8Weight(b, bz)
+    np.testing.assert_array_equal(w.matmul_integer(a, az), ref)
+    w.release()
+
+
+def test_wave_split_requant_and_batches(ops):
+    rng = np.random.default_rng(0x5EED0094)
+    a = rng.integers(0, 256, (512, 1024)).astype(np.uint8)
+    b = rng.integers(-127, 128, (1024, 512)).astype(np.int8)
+    args = (a, np.float32(0.0123), np.array(118), b, np.float32(2 ** -10), np.array(0),
+            np.float32(0.05), np.array(128))
+    np.testing.assert_array_equal(ops.op_qlinear_matmul(*args, lo=0, hi=255),
+                                  oracle.qlinear_matmul(*args, lo=0, hi=255))
+    for bb in (2, 1):
+        a3 = rng.integers(0, 256, (2, 96, 1024)).astype(np.uint8)
+        b3 = rng.integers(-128, 128, (bb, 1024, 200)).astype(np.int8)
+        az = rng.integers(0, 255, 96)
+        np.testing.assert_array_equal(ops.op_matmul_integer(a3, b3, az, np.array(5)),
+                                      oracle.matmul_integer(a3, b3, az, np.array(5)))
+
+
 @pytest.mark.parametrize("signed_out", [False, True])
 @pytest.mark.parametrize("y_scale", [0.05, 0.5, 8.0])
 def test_qlinear_exact(ops, signed_out, y_scale):
