@@ -1092,6 +1092,47 @@ __global__ __launch_bounds__(256) void k_gqa_prep(const mg_gqa_prep g, int64_t n
                           g.sin + (g.past + s) * g.half_rot, g.interleaved);
 }
 
+// The aligned, whole-quad case (RQ) by cache blocks: workgroup x < nbh * pbb
+// takes block bh = x / pbb (batch x KV head, a scalar division) and 256
+// consecutive quads of its present K and V rows (one per thread).  The past
+// part of a block is one contiguous run, present[bh][0 .. past hs) =
+// past[bh][0 .. past hs), so it needs no per-element index division; the
+// new rows (RoPE'd K, raw V) follow.  Workgroups past nbh * pbb rotate Q,
+// one quad per thread, as k_gqa_prep.
+__global__ __launch_bounds__(256) void k_gqa_prep_blk(const mg_gqa_prep g, int nbh, int pbb,
+                                                      int nq4) {
+  const int xb = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int hs4 = (int)g.hs / 4, past4 = (int)g.past * hs4, tot4 = (int)(g.past + g.seq) * hs4;
+  if (xb < nbh * pbb) {
+    const int bh = xb / pbb;
+    const int x = (xb - bh * pbb) * 256 + tid;
+    float4 *ok = reinterpret_cast<float4 *>(g.present_k) + (int64_t)bh * tot4;
+    float4 *ov = reinterpret_cast<float4 *>(g.present_v) + (int64_t)bh * tot4;
+    if (x < past4) {
+      ok[x] = reinterpret_cast<const float4 *>(g.past_k)[(int64_t)bh * past4 + x];
+      ov[x] = reinterpret_cast<const float4 *>(g.past_v)[(int64_t)bh * past4 + x];
+    } else if (x < tot4) {
+      const int r = x - past4, s = r / hs4, d = (r - s * hs4) * 4;
+      const int b = bh / (int)g.kv_heads, kvh = bh - b * (int)g.kv_heads;
+      const int64_t row = ((int64_t)b * g.seq + s) * g.kv_heads * g.hs + (int64_t)kvh * g.hs;
+      const float *c = g.cos + (g.past + s) * g.half_rot, *sn = g.sin + (g.past + s) * g.half_rot;
+      ok[x] = g.rotary ? rope4(g.k + row, d, g.half_rot, c, sn, g.interleaved)
+                       : *reinterpret_cast<const float4 *>(g.k + row + d);
+      ov[x] = *reinterpret_cast<const float4 *>(g.v + row + d);
+    }
+    return;
+  }
+  const int i4 = (xb - nbh * pbb) * 256 + tid;
+  if (i4 >= nq4) return;
+  const int64_t e = (int64_t)i4 * 4;  // rotated Q, [batch][seq][heads * hs]
+  const int64_t d = e % g.hs, row = e - d;
+  const int64_t s = (e / (g.heads * g.hs)) % g.seq;
+  *reinterpret_cast<float4 *>(g.q_rot + e) =
+      rope4(g.q + row, d, g.half_rot, g.cos + (g.past + s) * g.half_rot,
+            g.sin + (g.past + s) * g.half_rot, g.interleaved);
+}
+
 }  // namespace
 
 mg_status mg_gqa_prep_run(mg_ctx *ctx, const mg_gqa_prep &g) {
@@ -1114,6 +1155,19 @@ mg_status mg_gqa_prep_run(mg_ctx *ctx, const mg_gqa_prep &g) {
                                                  al(g.q) && al(g.q_rot) &&
                                                  reinterpret_cast<uintptr_t>(g.cos) % 16 == 0 &&
                                                  reinterpret_cast<uintptr_t>(g.sin) % 16 == 0));
+#ifndef MG_GQA_PREP_BLK
+#define MG_GQA_PREP_BLK 1
+#endif
+  // (32-bit block indices: every block and the grid below 2^31.)
+  const int64_t nbh = g.batch * g.kv_heads, tot4 = (g.past + g.seq) * g.hs / 4;
+  const int64_t pbb = (tot4 + 255) / 256;
+  const int64_t nq4 = g.rotary ? g.batch * g.seq * g.heads * g.hs / 4 : 0;
+  const int64_t nblk = nbh * pbb + (nq4 + 255) / 256;
+  if (MG_GQA_PREP_BLK && rq && nblk < 0x7fffffff && tot4 < 0x7fffffff && nq4 < 0x7fffffff) {
+    hipLaunchKernelGGL(k_gqa_prep_blk, dim3((unsigned)nblk), dim3(256), 0, ctx->stream, g,
+                       (int)nbh, (int)pbb, (int)nq4);
+    return mg_launch_check("k_gqa_prep_blk");
+  }
   const dim3 grid((unsigned)blocks);
   if (rq && i32)
     hipLaunchKernelGGL((k_gqa_prep<4, uint32_t, true>), grid, dim3(256), 0, ctx->stream, g, nkv,
