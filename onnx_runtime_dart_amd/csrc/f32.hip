@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
     float *__restrict__ Y, int64_t M, int64_t N, int64_t K, int64_t lda,
     int64_t ldb, int vec_a, int vec_b,
     const mg_f32_bcast bc, uint32_t z0, int nx, int pr, int pc, float alpha, float beta,
-    const float *__restrict__ C, int64_t c_rs, int64_t c_cs, int64_t ldy) {
+    const float *__restrict__ C, int64_t c_rs, int64_t c_cs, int64_t ldy, int sps) {
   constexpr int T = 64 * WT, LDX = KS + 4, NS = KS / 2;
   __shared__ float As[2][T * LDX];
   __shared__ float Bs[2][T * LDX];
@@ -178,6 +178,10 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
     for (int j = 0; j < WT; j++) acc[i][j] = (float16v){};
 
   const int nst = (int)((K + KS - 1) / KS);
+  // K split (sps > 0): stages [s0, s1) of split blockIdx.y, whose raw sums
+  // go to its own M x ldy block of Y (the partials).
+  const int s0 = sps > 0 ? (int)blockIdx.y * sps : 0;
+  const int s1 = sps > 0 ? min(nst, s0 + sps) : nst;
   Stage<WT, KS, AKR> sa;
   Stage<WT, KS, BKR> sb;
   // BV: every stage through the branch-free buffer loads.
@@ -197,13 +201,13 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
       sb.load(Bb, b_in && kin, ldb, N, K, c0, k0, t);
     }
   };
-  load(0);
+  load(s0);
   sa.store(As[0], t);
   sb.store(Bs[0], t);
   __syncthreads();
-  for (int st = 0; st < nst; st++) {
-    const int buf = st & 1;
-    const bool more = st + 1 < nst;
+  for (int st = s0; st < s1; st++) {
+    const int buf = (st - s0) & 1;
+    const bool more = st + 1 < s1;
     if (more) load(st + 1);
     float a[WT][NS], b[WT][NS];
 #pragma unroll
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
   // past M or N getting an offset past the resource (dropped in hardware):
   // no branches, so the stores issue back to back (behind per-element
   // branches the compiler waited for each store before the next).
-  float *Yb = Y + (int64_t)bz * M * ldy;
+  float *Yb = Y + ((int64_t)bz + blockIdx.y) * M * ldy;  // blockIdx.y > 0 only for K splits
   const __amdgpu_buffer_rsrc_t ry = rsrc(Yb);
 #pragma unroll
   for (int i = 0; i < WT; i++)
@@ -292,10 +296,10 @@ __global__ __launch_bounds__(256) void k_f32_gemm(
 template <int WT, int KS, bool BV>
 void launch_f32_bv(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float *a,
                    const float *b, float *y, int vec_a, int vec_b, uint32_t z0, int nx, int pr,
-                   int pc) {
+                   int pc, int sps) {
 #define MG_F32_ARGS                                                                         \
   a, b, y, p.M, p.N, p.K, p.lda, p.ldb, vec_a, vec_b, p.bc, z0, nx, pr, pc, p.alpha, p.beta, \
-      p.c, p.c_rs, p.c_cs, p.ldy ? p.ldy : p.N
+      p.c, p.c_rs, p.c_cs, p.ldy ? p.ldy : p.N, sps
   const bool akr = p.trans_a != 0, bkr = p.trans_b == 0;
   if (!akr && !bkr)
     hipLaunchKernelGGL((k_f32_gemm<WT, KS, false, false, BV>), grid, dim3(256), 0, st,
@@ -318,7 +322,8 @@ void launch_f32_bv(const mg_f32_problem &p, dim3 grid, hipStream_t st, const flo
 template <int WT, int KS>
 void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float *a,
                 const float *b, float *y, int vec_a, int vec_b, uint32_t z0, int nx, int pr,
-                int pc) {
+                int pc, int kspl = 1) {
+  const int sps = kspl > 1 ? (int)(((p.K + KS - 1) / KS + kspl - 1) / kspl) : 0;
   const bool akr = p.trans_a != 0, bkr = p.trans_b == 0;
   const int64_t lim = ((int64_t)1 << 31) - 16;
   const bool bv =
@@ -327,12 +332,40 @@ void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float 
       (akr ? p.K * p.lda : p.M * p.lda) * 4 < lim && (bkr ? p.K * p.ldb : p.N * p.ldb) * 4 < lim &&
       p.M * (p.ldy ? p.ldy : p.N) * 4 < lim;
   if (bv)
-    launch_f32_bv<WT, KS, true>(p, grid, st, a, b, y, vec_a, vec_b, z0, nx, pr, pc);
+    launch_f32_bv<WT, KS, true>(p, grid, st, a, b, y, vec_a, vec_b, z0, nx, pr, pc, sps);
   else
-    launch_f32_bv<WT, KS, false>(p, grid, st, a, b, y, vec_a, vec_b, z0, nx, pr, pc);
+    launch_f32_bv<WT, KS, false>(p, grid, st, a, b, y, vec_a, vec_b, z0, nx, pr, pc, sps);
+}
+
+// Sum of the kspl partials of one batch in split order, then the epilogue of
+// k_f32_gemm (alpha, then beta C): one thread per output element.
+__global__ __launch_bounds__(256) void k_f32_ksum(const float *__restrict__ part, int kspl,
+                                                  int64_t M, int64_t N, float alpha, float beta,
+                                                  const float *__restrict__ C, int64_t c_rs,
+                                                  int64_t c_cs, float *__restrict__ Y,
+                                                  int64_t ldy) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= M * N) return;
+  const int64_t row = e / N, col = e - row * N;
+  float y = part[e];
+  for (int s = 1; s < kspl; s++) y += part[s * M * N + e];
+  if (alpha != 1.f) y = alpha * y;
+  if (C) {
+    float c = C[row * c_rs + col * c_cs];
+    if (beta != 1.f) c = beta * c;
+    y = y + c;
+  }
+  Y[row * ldy + col] = y;
 }
 
 }  // namespace
+
+int mg_f32_ksplit(int64_t M, int64_t K, int64_t batch) {
+#ifndef MG_F32_KSPLIT
+#define MG_F32_KSPLIT 2
+#endif
+  return batch == 1 && K >= 1024 && M <= 8192 ? MG_F32_KSPLIT : 1;
+}
 
 // The XCD cut of an ny x nx tile grid: pr row bands x pc column bands with
 // pr * pc = 8, at least one tile per band, minimising the tiles fetched
@@ -393,6 +426,29 @@ mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
   // grid at once instead of one and a half rounds (MiniLM FFN1 4096 x 384 x
   // 1536: 64.4 -> 59.6 us; with fewer tiles 32-k stages are faster).
   const bool small_ks16 = !use_big && nx * ny * p.batch > 4 * (int64_t)ctx->num_cus;
+  if (p.kspl > 1 && p.part && p.batch == 1) {
+    // Raw sums of each K split into part, then k_f32_ksum.
+    mg_f32_problem q = p;
+    q.alpha = 1.f;
+    q.c = nullptr;
+    q.ldy = p.N;
+    const dim3 grid(gx, (unsigned)p.kspl, 1);
+    if (use_big)
+      launch_f32<2, MG_F32_KS_BIG>(q, grid, ctx->stream, a_dev, b_dev, p.part, vec_a, vec_b, 0,
+                                   (int)nx, pr, pc, p.kspl);
+    else if (small_ks16)
+      launch_f32<1, 16>(q, grid, ctx->stream, a_dev, b_dev, p.part, vec_a, vec_b, 0, (int)nx,
+                        pr, pc, p.kspl);
+    else
+      launch_f32<1, MG_F32_KS_SMALL>(q, grid, ctx->stream, a_dev, b_dev, p.part, vec_a, vec_b, 0,
+                                     (int)nx, pr, pc, p.kspl);
+    MG_TRY(mg_launch_check("k_f32_gemm"));
+    const int64_t tot = p.M * p.N;
+    hipLaunchKernelGGL(k_f32_ksum, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0,
+                       ctx->stream, p.part, p.kspl, p.M, p.N, p.alpha, p.beta, p.c, p.c_rs,
+                       p.c_cs, y_dev, p.ldy ? p.ldy : p.N);
+    return mg_launch_check("k_f32_ksum");
+  }
   // Batches in chunks of at most 65535 per launch (grid z).
   for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
     const dim3 grid(gx, 1, (unsigned)std::min<int64_t>(65535, p.batch - z0));

@@ -310,9 +310,18 @@ struct mg_f32_problem {
   const float *c;        // null or device C
   int64_t c_rs, c_cs;    // element strides of C over rows / cols (0 = bcast)
   int64_t ldy = 0;       // row stride of Y (0: N; batches then lie M * ldy apart)
+  // K split over workgroups (one batch): kspl partial sums of M x N floats
+  // in part, added by a second launch (mg_f32_ksplit picks kspl).
+  int kspl = 1;
+  float *part = nullptr;
 };
 mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
                      const float *b_dev, float *y_dev);
+// The K split for one batch of M x K by K x N: 2 where K >= 1024 and M <= 8192
+// (few row tiles, long chains of k stages), else 1.  It depends on M and K
+// only, so column slices of a weight take the same split (bitwise equal
+// columns).
+int mg_f32_ksplit(int64_t M, int64_t K, int64_t batch);
 // MatMul on operands given as doubles (the reference's non-float fallback):
 // double products summed in k order, one rounding to f32.  Uses p.M, K, N,
 // batch and bc (row-major A [M, K] and B [K, N] per batch).

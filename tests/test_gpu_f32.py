@@ -233,3 +233,21 @@ def test_gemm_buffer_stage_layouts_ragged_tiles(ops, ta, tb):
     y = ops.op_gemm(a, b, c, alpha=0.75, beta=1.5, trans_a=ta, trans_b=tb)
     ref = oracle.gemm_f32(a, b, c, alpha=0.75, beta=1.5, trans_a=ta, trans_b=tb)
     assert G.rms_error(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("m,k,n,c_shape", [(100, 1100, 70, (70,)), (300, 1536, 384, (300, 384)),
+                                           (8200, 1024, 40, None)])
+def test_weight_gemm_k_split(ops, m, k, n, c_shape):
+    # Weight Gemms with K >= 1024 and M <= 8192 split K over two workgroup
+    # sets and add the partials in a second launch (alpha, then beta C, as
+    # the one-launch epilogue); M = 8200 stays in one launch.  Ragged M, N
+    # and a K that ends inside a stage, against the oracle.
+    rng = np.random.default_rng(0x5EED0095 + m + k + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    c = None if c_shape is None else rng.standard_normal(c_shape).astype(np.float32)
+    fw = ops.F32Weight(w, trans_b=True)
+    y = fw.gemm(a, c, alpha=0.5, beta=2.0)
+    ref = oracle.gemm_f32(a, w, c, alpha=0.5, beta=2.0, trans_a=0, trans_b=1)
+    assert G.rms_error(y, ref) <= TOL
+    fw.release()
