@@ -364,7 +364,10 @@ int mg_f32_ksplit(int64_t M, int64_t K, int64_t batch) {
 #ifndef MG_F32_KSPLIT
 #define MG_F32_KSPLIT 2
 #endif
-  return batch == 1 && K >= 1024 && M <= 8192 ? MG_F32_KSPLIT : 1;
+#ifndef MG_F32_KSPLIT_MIN_K
+#define MG_F32_KSPLIT_MIN_K 1024
+#endif
+  return batch == 1 && K >= MG_F32_KSPLIT_MIN_K && M <= 8192 ? MG_F32_KSPLIT : 1;
 }
 
 // The XCD cut of an ny x nx tile grid: pr row bands x pc column bands with
