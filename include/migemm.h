@@ -393,9 +393,9 @@ mg_status mg_weight_f32_create(mg_ctx *ctx, const float *b, int64_t rows,
  * NULL).  With alpha = 1, beta = 0, C = NULL this is MatMul against an
  * initializer, including the shared-weight batch collapse
  * (lib/src/onnx_ops.dart:1728-1735).  With K >= 1024 and rows <= 8192 the
- * product is split over K: the call then takes 2 * rows * N floats of the
- * context's workspace for the partial sums (counted against the byte
- * budget), also with device pointers. */
+ * product is split over K: the call then takes up to 64 MiB of the
+ * context's workspace for the partial sums (wider weights run in column
+ * chunks; counted against the byte budget), also with device pointers. */
 mg_status mg_gemm_f32_w(mg_ctx *ctx, const float *a, int64_t rows, int64_t K,
                         const mg_weight *w, float alpha, float beta,
                         const float *c, const int64_t *c_shape, int32_t c_rank,

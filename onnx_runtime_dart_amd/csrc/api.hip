@@ -1342,7 +1342,11 @@ mg_status gemm_w(mg_ctx *ctx, const float *a, bool a_dev_ptr, int64_t rows, int6
   const size_t oc = (c && !c_dev_ptr) ? s.take((size_t)nc * 4) : 0;
   const size_t oy = y_dev_ptr ? 0 : s.take((size_t)(rows * w->N) * 4);
   q.kspl = mg_f32_ksplit(rows, K, 1);
-  const size_t op = q.kspl > 1 ? s.take((size_t)q.kspl * rows * w->N * 4) : 0;
+  // Partials of at most 64 MiB: wider weights run in column chunks.
+  if (q.kspl > 1)
+    q.part_cols = std::min<int64_t>(
+        w->N, std::max<int64_t>(64, ((64ll << 20) / ((int64_t)q.kspl * rows * 4)) / 64 * 64));
+  const size_t op = q.kspl > 1 ? s.take((size_t)q.kspl * rows * q.part_cols * 4) : 0;
   MG_TRY(mg_check_control(ctx, (int64_t)s.off));
   MG_TRY(mg_ws_reserve(ctx, s.off));
   char *base = static_cast<char *>(ctx->ws);

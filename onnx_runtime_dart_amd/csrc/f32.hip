@@ -323,7 +323,9 @@ template <int WT, int KS>
 void launch_f32(const mg_f32_problem &p, dim3 grid, hipStream_t st, const float *a,
                 const float *b, float *y, int vec_a, int vec_b, uint32_t z0, int nx, int pr,
                 int pc, int kspl = 1) {
-  const int sps = kspl > 1 ? (int)(((p.K + KS - 1) / KS + kspl - 1) / kspl) : 0;
+  // Stages per split: a split covers a multiple of 32 k whatever the stage
+  // size, so every tile plan splits K at the same k (bitwise equal sums).
+  const int sps = kspl > 1 ? (int)(((p.K + kspl - 1) / kspl + 31) / 32 * (32 / KS)) : 0;
   const bool akr = p.trans_a != 0, bkr = p.trans_b == 0;
   const int64_t lim = ((int64_t)1 << 31) - 16;
   const bool bv =
@@ -429,6 +431,20 @@ mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
   // grid at once instead of one and a half rounds (MiniLM FFN1 4096 x 384 x
   // 1536: 64.4 -> 59.6 us; with fewer tiles 32-k stages are faster).
   const bool small_ks16 = !use_big && nx * ny * p.batch > 4 * (int64_t)ctx->num_cus;
+  if (p.kspl > 1 && p.part && p.batch == 1 && p.part_cols > 0 && p.N > p.part_cols) {
+    // The partial buffer holds part_cols columns: column chunks, each the
+    // same per-output arithmetic as the whole.
+    const int64_t ldy = p.ldy ? p.ldy : p.N;
+    for (int64_t n0 = 0; n0 < p.N; n0 += p.part_cols) {
+      mg_f32_problem q = p;
+      q.N = std::min(p.part_cols, p.N - n0);
+      q.ldy = ldy;
+      if (p.c) q.c = p.c + n0 * p.c_cs;
+      const float *bq = p.trans_b ? b_dev + n0 * p.ldb : b_dev + n0;
+      MG_TRY(mg_f32_run(ctx, q, a_dev, bq, y_dev + n0));
+    }
+    return MG_OK;
+  }
   if (p.kspl > 1 && p.part && p.batch == 1) {
     // Raw sums of each K split into part, then k_f32_ksum.
     mg_f32_problem q = p;

@@ -314,6 +314,7 @@ struct mg_f32_problem {
   // in part, added by a second launch (mg_f32_ksplit picks kspl).
   int kspl = 1;
   float *part = nullptr;
+  int64_t part_cols = 0;  // columns part holds (0: N); wider problems run in column chunks
 };
 mg_status mg_f32_run(mg_ctx *ctx, const mg_f32_problem &p, const float *a_dev,
                      const float *b_dev, float *y_dev);

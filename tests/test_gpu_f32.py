@@ -251,3 +251,26 @@ def test_weight_gemm_k_split(ops, m, k, n, c_shape):
     ref = oracle.gemm_f32(a, w, c, alpha=0.5, beta=2.0, trans_a=0, trans_b=1)
     assert G.rms_error(y, ref) <= TOL
     fw.release()
+
+
+def test_weight_gemm_k_split_column_chunks_and_slices(ops):
+    # rows = 4096, K = 1100, N = 2200: the two partials of the whole weight
+    # exceed 64 MiB, so it runs in column chunks (2048 + 152), while a weight
+    # of its last 152 columns alone takes another tile plan (stages of 32 k
+    # instead of 16).  The split falls on the same k either way, so those
+    # columns are bitwise equal; a row subset is checked against the oracle.
+    rng = np.random.default_rng(0x5EED0096)
+    m, k, n = 4096, 1100, 2200
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    c = rng.standard_normal((n,)).astype(np.float32)
+    fw = ops.F32Weight(w, trans_b=True)
+    y = fw.gemm(a, c)
+    fw.release()
+    fs = ops.F32Weight(np.ascontiguousarray(w[2048:]), trans_b=True)
+    ys = fs.gemm(a, c[2048:])
+    fs.release()
+    np.testing.assert_array_equal(y[:, 2048:], ys)
+    rows = np.arange(0, m, 97)
+    ref = oracle.gemm_f32(a[rows], w, c, alpha=1.0, beta=1.0, trans_a=0, trans_b=1)
+    assert G.rms_error(y[rows], ref) <= TOL
